@@ -1,0 +1,230 @@
+/*
+ * nanokv.h -- C ABI of libnanokv_hip.so, the MI355X (gfx950) implementation
+ * of NanoKV's codec-native historical attention.
+ *
+ * Conventions (all entry points):
+ *  - `stream` is a hipStream_t passed as void* (NULL = the null stream).
+ *    Work is enqueued asynchronously; the library never synchronises.
+ *  - Every pointer is device memory owned and allocated by the caller.  The
+ *    library allocates no device memory; kernels that need scratch take a
+ *    caller-provided workspace whose size is queried first.
+ *  - Return 0 (NKV_OK) or a negative NKV_ERR_* code.  The message for the
+ *    last failure on the calling thread is returned by nkv_last_error().
+ *  - bf16 and fp16 values travel as uint16_t bit patterns.
+ *  - Shapes are validated on the host before any launch; invalid shapes are
+ *    rejected with NKV_ERR_INVALID and launch nothing.
+ *
+ * Reference interfaces replaced (paths relative to the NanoKV tree;
+ * MG = models/Matrix-Game-3.5/fast/diffsynth/models/nanokv_codec.py,
+ * CN = models/Matrix-Game-3.5/fast/codec_native):
+ *  nkv_quant_pack  <- MG:349-351 + _pack_int4 MG:282-292; HY Triton
+ *                     int4_quant_pack_per_row (kv_codec_triton.py:60-81)
+ *  nkv_unpack      <- unpack_int4_scaled (nanokv_codec_kernels.py:30-61),
+ *                     latent_kernel.read (CN/latent_kernel.py:18-23)
+ *  nkv_assign      <- the argmin step of semantic_residual MG:315-321;
+ *                     HY _joint_euclid_assign_kernel (kv_codec_triton.py:238-273)
+ *  nkv_encode      <- encode_tensor MG:333-365 with given shared centers
+ *  nkv_decode      <- _decode_method_segments MG:393-455, decode_tensor
+ *                     MG:368-390, decode_pair_selected MG:801-861
+ *  nkv_attend      <- decode_pair_values (MG:542) followed by the history
+ *                     attention of causal_self_attention_kv
+ *                     (wan_video_dit.py:488-627) / attention_lse
+ *                     (CN/core.py:45-72), fused into one kernel
+ *  nkv_lse_merge   <- merge (CN/core.py:33-42), fast_kernels._merge
+ *                     (CN/fast_kernels.py:30-54)
+ *  nkv_fast_attend <- hybrid_attention (CN/core.py:278-310) and the partition
+ *                     reads of maybe_attention (CN/mg35.py:100-357)
+ */
+#ifndef NANOKV_H
+#define NANOKV_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define NKV_ABI_VERSION 1
+
+enum nkv_status {
+    NKV_OK = 0,
+    NKV_ERR_INVALID = -1,     /* bad shape, pointer or parameter */
+    NKV_ERR_UNSUPPORTED = -2, /* valid request this build does not implement */
+    NKV_ERR_HIP = -3,         /* a HIP runtime call failed */
+    NKV_ERR_WORKSPACE = -4    /* workspace missing or too small */
+};
+
+enum nkv_scale_dtype { NKV_DTYPE_BF16 = 0, NKV_DTYPE_FP16 = 1 };
+
+/* Arithmetic of the quantiser (see nkv_quant_pack). */
+enum nkv_quant_mode { NKV_QUANT_FP32 = 0, NKV_QUANT_BF16 = 1 };
+
+/* ABI version of the loaded library (NKV_ABI_VERSION at build time). */
+int nkv_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). */
+const char* nkv_last_error(void);
+
+/*
+ * INT4 symmetric quantisation of fp32 coefficients, packed two per byte.
+ *   coeff  [rows, r] fp32        packed [rows, r/2] uint8
+ *   scales [rows, r/group] bf16 or fp16 bits (scale_dtype)
+ * Per (row, group): s = max(amax|x|, FLT_EPSILON) / 7 (IEEE division);
+ * code = clamp(round_half_even(x / s), -7, 7); byte j of a row holds codes
+ * 2j (low nibble) and 2j+1 (high nibble) as code + 7; scales store cast(s).
+ * quant_mode NKV_QUANT_BF16 reproduces MG's bf16 tensor arithmetic: the
+ * input, amax, s and x/s are each rounded to bf16 (MG:138-153, 349-351).
+ * group must divide r; r must be even.  group == r is the reference's
+ * one-scale-per-row layout.
+ */
+int nkv_quant_pack(void* stream, const float* coeff, int64_t rows, int r, int group,
+                   int scale_dtype, int quant_mode, uint8_t* packed, uint16_t* scales);
+
+/*
+ * Unpack INT4 codes and apply their group scale:
+ *   latent[i, j] = bf16( float(code[src, j]) * float(scale[src, j / group]) )
+ * with src = row_index ? row_index[i] : i.  latent is [rows, r] bf16 bits.
+ */
+int nkv_unpack(void* stream, const uint8_t* packed, const uint16_t* scales, int scale_dtype,
+               const int32_t* row_index, int64_t rows, int r, int group, uint16_t* latent);
+
+/*
+ * Nearest-center assignment: ids[n] = argmin_c ||x_n - c||^2 over the bf16
+ * table (first index on ties), decided in fp64 from the fp32/bf16 inputs.
+ *   x [rows, HD] fp32, centers [C, HD] bf16, ids [rows] of id_bytes
+ *   (1 = uint8 for C <= 256, 2 = uint16 for C <= 65536, 4 = int32).
+ */
+int nkv_assign(void* stream, const float* x, const uint16_t* centers, int64_t rows, int C,
+               int HD, void* ids, int id_bytes);
+
+/* One K or V codec as stored in the cache (one segment or a concatenation of
+ * segments that share one center table; per-segment tables are concatenated
+ * by the caller with ids offset accordingly). */
+typedef struct nkv_codec {
+    const uint8_t* packed;        /* [B, N, r/2] */
+    const uint16_t* scales;       /* [B, N, r/group] */
+    const void* ids;              /* [B, N] of id_bytes, or NULL when centers == NULL */
+    const uint16_t* centers;      /* [B or 1, C, HD] bf16, or NULL (no center add) */
+    const uint16_t* w_dec;        /* [HD, r] bf16 decoder weight (F.linear layout) */
+    const float* mean;            /* [HD] fp32 bias (applied as bf16), or NULL */
+    int r;
+    int group;
+    int scale_dtype;
+    int id_bytes;
+    int num_centers;
+    int _pad;
+    int64_t centers_batch_stride; /* elements between batch tables; 0 = shared */
+} nkv_codec;
+
+/*
+ * Encode a chunk with given shared centers (assign -> residual -> encoder
+ * projection -> quantise/pack), following encode_tensor MG:333-365:
+ *   residual = x - fp32(center[id]) - mean, cast to bf16 (MG:326-330, 346)
+ *   coeff    = residual @ w_enc^T, fp32 accumulate (MG:134-153)
+ *   packed, scales = nkv_quant_pack(coeff)
+ * `coeff` is an output the caller allocates ([rows, r] fp32); it is also the
+ * exact input the quantiser saw.  With centers == NULL no center is
+ * subtracted and ids is not written (the reference's pca rung).
+ */
+typedef struct nkv_encode_args {
+    int64_t rows;                 /* tokens in this batch item */
+    int HD;
+    int r;
+    int group;
+    int scale_dtype;
+    int quant_mode;
+    int num_centers;
+    int id_bytes;
+    int _pad;
+    const float* x;               /* [rows, HD] fp32 */
+    const uint16_t* centers;      /* [C, HD] bf16 or NULL */
+    const float* mean;            /* [HD] fp32 or NULL */
+    const uint16_t* w_enc;        /* [r, HD] bf16 */
+    void* ids;                    /* out [rows] */
+    float* coeff;                 /* out [rows, r] fp32 */
+    uint8_t* packed;              /* out [rows, r/2] */
+    uint16_t* scales;             /* out [rows, r/group] */
+} nkv_encode_args;
+
+int nkv_encode(void* stream, const nkv_encode_args* args);
+
+/*
+ * Full-width decode of all or selected rows to bf16 (the reference's decode
+ * path, used for decode_value / decode_pair_selected):
+ *   rows = bf16(latent @ w_dec^T + bf16(mean))                  MG:438-443
+ *   rows = bf16(float(rows) + float(center[id]))                MG:445-454
+ * out [B, rows, HD] bf16.  row_index (NULL = all N) selects rows of every
+ * batch item.
+ */
+typedef struct nkv_decode_args {
+    int B;
+    int HD;
+    int64_t N;                    /* tokens per batch item in the codec */
+    int64_t rows;                 /* output rows per batch item */
+    const int32_t* row_index;     /* [rows] or NULL (rows == N) */
+    nkv_codec codec;
+    uint16_t* out;
+} nkv_decode_args;
+
+int nkv_decode(void* stream, const nkv_decode_args* args);
+
+/*
+ * Fused decode-and-attend: softmax(q k^T * softmax_scale) v over the keys
+ * [decoded history (N tokens); current chunk (Nc tokens)], non-causal,
+ * without materialising decoded K/V in global memory.  History K/V rows are
+ * decoded tile by tile inside the kernel with the nkv_decode arithmetic.
+ *   q       [B, Q, H, D] addressed as q[b*q_sb + t*q_st + h*q_sh + d]
+ *   k_cur   [B, Nc, H, D] (k_sb/k_st/k_sh), v_cur likewise (v_*)
+ *   out     [B, Q, H, D] bf16 (o_sb/o_st/o_sh)
+ *   lse     [B, H, Q] fp32 natural-log row log-sum-exp, or NULL
+ * key/value codecs decode to HD = H * D columns; head h reads columns
+ * [h*D, (h+1)*D).  An empty key set gives out = 0 and lse = -inf
+ * (attention_lse, CN/core.py:48-49).  D must be 128.
+ */
+typedef struct nkv_attend_args {
+    int B;
+    int H;
+    int D;
+    int splits;                   /* history splits; 0 = choose automatically */
+    int64_t Q;
+    int64_t N;
+    int64_t Nc;
+    float softmax_scale;
+    int _pad;
+    const uint16_t* q;
+    int64_t q_sb, q_st, q_sh;
+    const uint16_t* k_cur;
+    int64_t k_sb, k_st, k_sh;
+    const uint16_t* v_cur;
+    int64_t v_sb, v_st, v_sh;
+    nkv_codec key;
+    nkv_codec value;
+    uint16_t* out;
+    int64_t o_sb, o_st, o_sh;
+    float* lse;
+} nkv_attend_args;
+
+/* Bytes of workspace nkv_attend needs for these arguments (0 if none). */
+size_t nkv_attend_workspace_size(const nkv_attend_args* args);
+
+int nkv_attend(void* stream, const nkv_attend_args* args, void* workspace,
+               size_t workspace_bytes);
+
+/*
+ * Log-sum-exp merge of two attention partitions (CN/core.py:33-42):
+ *   lse = logaddexp(lse_a, lse_b); origin = lse if finite else 0
+ *   out = a * exp(lse_a - origin) + b * exp(lse_b - origin)   (fp32, -> bf16)
+ * a, b, out: [rows, D] bf16 with row strides (elements); lse_*: [rows] fp32.
+ * out may alias a or b.
+ */
+int nkv_lse_merge(void* stream, int64_t rows, int D,
+                  const uint16_t* a, int64_t a_stride, const float* lse_a,
+                  const uint16_t* b, int64_t b_stride, const float* lse_b,
+                  uint16_t* out, int64_t out_stride, float* lse_out);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* NANOKV_H */

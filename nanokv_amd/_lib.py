@@ -1,0 +1,138 @@
+"""ctypes binding of libnanokv_hip.so (the C ABI declared in include/nanokv.h).
+
+The library is loaded lazily on first use.  There is no fallback: if the
+shared library is missing or fails to load, every product call raises.
+"""
+from __future__ import annotations
+
+import ctypes
+import threading
+from ctypes import (POINTER, Structure, c_char_p, c_float, c_int, c_int64, c_size_t,
+                    c_uint8, c_uint16, c_void_p)
+from pathlib import Path
+
+LIB_PATH = Path(__file__).resolve().parent / "libnanokv_hip.so"
+
+NKV_ABI_VERSION = 1
+NKV_OK = 0
+NKV_ERR_INVALID = -1
+NKV_ERR_UNSUPPORTED = -2
+NKV_ERR_HIP = -3
+NKV_ERR_WORKSPACE = -4
+
+NKV_DTYPE_BF16 = 0
+NKV_DTYPE_FP16 = 1
+NKV_QUANT_FP32 = 0
+NKV_QUANT_BF16 = 1
+
+# Every symbol include/nanokv.h declares (checked by tests/test_abi.py).
+EXPORTED = (
+    "nkv_abi_version", "nkv_last_error", "nkv_quant_pack", "nkv_unpack", "nkv_assign",
+    "nkv_encode", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
+)
+
+
+class NkvCodec(Structure):
+    _fields_ = [
+        ("packed", c_void_p), ("scales", c_void_p), ("ids", c_void_p), ("centers", c_void_p),
+        ("w_dec", c_void_p), ("mean", c_void_p),
+        ("r", c_int), ("group", c_int), ("scale_dtype", c_int), ("id_bytes", c_int),
+        ("num_centers", c_int), ("_pad", c_int),
+        ("centers_batch_stride", c_int64),
+    ]
+
+
+class NkvEncodeArgs(Structure):
+    _fields_ = [
+        ("rows", c_int64), ("HD", c_int), ("r", c_int), ("group", c_int),
+        ("scale_dtype", c_int), ("quant_mode", c_int), ("num_centers", c_int),
+        ("id_bytes", c_int), ("_pad", c_int),
+        ("x", c_void_p), ("centers", c_void_p), ("mean", c_void_p), ("w_enc", c_void_p),
+        ("ids", c_void_p), ("coeff", c_void_p), ("packed", c_void_p), ("scales", c_void_p),
+    ]
+
+
+class NkvDecodeArgs(Structure):
+    _fields_ = [
+        ("B", c_int), ("HD", c_int), ("N", c_int64), ("rows", c_int64),
+        ("row_index", c_void_p), ("codec", NkvCodec), ("out", c_void_p),
+    ]
+
+
+class NkvAttendArgs(Structure):
+    _fields_ = [
+        ("B", c_int), ("H", c_int), ("D", c_int), ("splits", c_int),
+        ("Q", c_int64), ("N", c_int64), ("Nc", c_int64),
+        ("softmax_scale", c_float), ("_pad", c_int),
+        ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
+        ("k_cur", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
+        ("v_cur", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),
+        ("key", NkvCodec), ("value", NkvCodec),
+        ("out", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64),
+        ("lse", c_void_p),
+    ]
+
+
+class NanoKVError(RuntimeError):
+    """A libnanokv_hip.so call returned an error code."""
+
+    def __init__(self, func: str, code: int, message: str):
+        super().__init__(f"{func} failed with code {code}: {message}")
+        self.code = code
+
+
+_lock = threading.Lock()
+_lib = None
+
+
+def _declare(lib: ctypes.CDLL) -> None:
+    lib.nkv_abi_version.restype = c_int
+    lib.nkv_abi_version.argtypes = []
+    lib.nkv_last_error.restype = c_char_p
+    lib.nkv_last_error.argtypes = []
+    lib.nkv_quant_pack.restype = c_int
+    lib.nkv_quant_pack.argtypes = [c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int,
+                                   c_void_p, c_void_p]
+    lib.nkv_unpack.restype = c_int
+    lib.nkv_unpack.argtypes = [c_void_p, c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int,
+                               c_int, c_void_p]
+    lib.nkv_assign.restype = c_int
+    lib.nkv_assign.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p,
+                               c_int]
+    lib.nkv_encode.restype = c_int
+    lib.nkv_encode.argtypes = [c_void_p, POINTER(NkvEncodeArgs)]
+    lib.nkv_decode.restype = c_int
+    lib.nkv_decode.argtypes = [c_void_p, POINTER(NkvDecodeArgs)]
+    lib.nkv_attend_workspace_size.restype = c_size_t
+    lib.nkv_attend_workspace_size.argtypes = [POINTER(NkvAttendArgs)]
+    lib.nkv_attend.restype = c_int
+    lib.nkv_attend.argtypes = [c_void_p, POINTER(NkvAttendArgs), c_void_p, c_size_t]
+    lib.nkv_lse_merge.restype = c_int
+    lib.nkv_lse_merge.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int64, c_void_p,
+                                  c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p]
+
+
+def lib() -> ctypes.CDLL:
+    """Load libnanokv_hip.so once; raise if it is absent or incompatible."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lock:
+        if _lib is None:
+            if not LIB_PATH.exists():
+                raise RuntimeError(
+                    f"{LIB_PATH} is not built; run `python -m nanokv_amd.build` "
+                    "(there is no CPU fallback for the NanoKV HIP path)")
+            handle = ctypes.CDLL(str(LIB_PATH))
+            _declare(handle)
+            version = handle.nkv_abi_version()
+            if version != NKV_ABI_VERSION:
+                raise RuntimeError(f"libnanokv_hip ABI {version} != expected {NKV_ABI_VERSION}")
+            _lib = handle
+    return _lib
+
+
+def check(func: str, code: int) -> None:
+    if code != NKV_OK:
+        message = lib().nkv_last_error().decode(errors="replace")
+        raise NanoKVError(func, code, message)

@@ -1,0 +1,560 @@
+// nkv_codec.hip -- NanoKV chunk codec on gfx950: INT4 quantise/pack, unpack,
+// nearest-center assignment, encoder projection and full-width decode.
+//
+// This translation unit is compiled with -ffp-contract=off: the quantiser and
+// the decode epilogue are bit-exact restatements whose rounding points must
+// not be fused away.
+#include "nkv_common.h"
+
+namespace nkv {
+
+// ============================================================ quantiser
+// One thread per (row, group).  Each thread reads its group with 16-byte
+// loads, computes the exact amax (order-free), the IEEE-divided scale, and
+// writes group/2 packed bytes plus one scale.  Reference: MG:349-351 (fp32
+// arithmetic as in HY kv_codecs.py:244-255; bf16 arithmetic as MG deploys
+// it) and _pack_int4 MG:282-292.
+template <int QUANT_MODE>
+__global__ void __launch_bounds__(256) quant_pack_kernel(const float* __restrict__ coeff,
+                                                         int64_t rows, int r, int group,
+                                                         int scale_dtype,
+                                                         uint8_t* __restrict__ packed,
+                                                         uint16_t* __restrict__ scales) {
+    const int ngroups = r / group;
+    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gid >= rows * ngroups) return;
+    const int64_t row = gid / ngroups;
+    const int g = (int)(gid - row * ngroups);
+    const float* x = coeff + row * r + (int64_t)g * group;
+
+    float amax = 0.0f;
+    for (int j = 0; j < group; j += 4) {
+        f32x4 v = *reinterpret_cast<const f32x4*>(x + j);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            float a = QUANT_MODE == NKV_QUANT_BF16 ? bf16_round(v[e]) : v[e];
+            a = fabsf(a);
+            amax = (a > amax || a != a) ? a : amax;  // NaN propagates like torch.amax
+        }
+    }
+    float s;
+    const float eps = 1.1920928955078125e-07f;  // torch.finfo(torch.float32).eps
+    float clamped = (amax > eps || amax != amax) ? amax : eps;
+    if (QUANT_MODE == NKV_QUANT_BF16) {
+        s = bf16_round(__fdiv_rn(bf16_round(clamped), 7.0f));
+    } else {
+        s = __fdiv_rn(clamped, 7.0f);
+    }
+    scales[row * ngroups + g] =
+        scale_dtype == NKV_DTYPE_FP16 ? f32_to_f16_bits(s) : f32_to_bf16_bits(s);
+
+    uint8_t* out = packed + row * (r / 2) + (int64_t)g * (group / 2);
+    for (int j = 0; j < group; j += 8) {
+        f32x4 v0 = *reinterpret_cast<const f32x4*>(x + j);
+        f32x4 v1 = *reinterpret_cast<const f32x4*>(x + j + 4);
+        uint32_t word = 0;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            float v = e < 4 ? v0[e] : v1[e - 4];
+            if (QUANT_MODE == NKV_QUANT_BF16) v = bf16_round(v);
+            float q = __fdiv_rn(v, s);
+            if (QUANT_MODE == NKV_QUANT_BF16) q = bf16_round(q);
+            float rq = rintf(q);  // round half to even, as torch.round
+            int c = rq != rq ? 0 : (int)fminf(fmaxf(rq, -7.0f), 7.0f);
+            word |= (uint32_t)(c + 7) << (4 * e);
+        }
+        *reinterpret_cast<uint32_t*>(out + j / 2) = word;
+    }
+}
+
+// ============================================================ unpack
+// One thread per 8 consecutive codes (4 packed bytes) of one row.
+__global__ void __launch_bounds__(256) unpack_kernel(const uint8_t* __restrict__ packed,
+                                                     const uint16_t* __restrict__ scales,
+                                                     int scale_dtype,
+                                                     const int32_t* __restrict__ row_index,
+                                                     int64_t rows, int r, int group,
+                                                     uint16_t* __restrict__ out) {
+    const int per_row = r / 8;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= rows * per_row) return;
+    const int64_t i = tid / per_row;
+    const int j0 = (int)(tid - i * per_row) * 8;
+    const int64_t src = row_index ? (int64_t)row_index[i] : i;
+    const uint32_t word = *reinterpret_cast<const uint32_t*>(packed + src * (r / 2) + j0 / 2);
+    const float s = scale_bits_to_f32(scales[src * (r / group) + j0 / group], scale_dtype);
+    u32x4 o;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        float lo = (float)((int)((word >> (8 * e)) & 15u) - 7) * s;
+        float hi = (float)((int)((word >> (8 * e + 4)) & 15u) - 7) * s;
+        o[e] = pack_bf16x2(lo, hi);
+    }
+    *reinterpret_cast<u32x4*>(out + i * r + j0) = o;
+}
+
+// ============================================================ assignment
+// fp64 nearest-center search.  A 256-thread block owns 32 rows and walks the
+// center table in chunks of 64; each thread keeps a 2-row x 4-center fp64
+// register tile.  Per chunk the block stages x[32 x 64] (fp32) and
+// c[64 x 64] (bf16) in LDS along HD.  ||c||^2 is accumulated by the same
+// threads (only the thread column that owns row 0 keeps it).  Distances are
+// ||c||^2 - 2 x.c (||x||^2 is constant per row); ties keep the lowest index.
+constexpr int AS_ROWS = 32, AS_CENT = 64, AS_K = 64;
+
+template <int ID_BYTES>
+__device__ __forceinline__ void store_id(void* ids, int64_t i, int v) {
+    if (ID_BYTES == 1) reinterpret_cast<uint8_t*>(ids)[i] = (uint8_t)v;
+    else if (ID_BYTES == 2) reinterpret_cast<uint16_t*>(ids)[i] = (uint16_t)v;
+    else reinterpret_cast<int32_t*>(ids)[i] = v;
+}
+
+template <int ID_BYTES>
+__global__ void __launch_bounds__(256) assign_kernel(const float* __restrict__ x,
+                                                     const uint16_t* __restrict__ centers,
+                                                     int64_t rows, int C, int HD,
+                                                     void* __restrict__ ids) {
+    __shared__ float xs[AS_ROWS][AS_K + 1];
+    __shared__ float cs[AS_CENT][AS_K + 1];
+    __shared__ double red_d[AS_ROWS][16];
+    __shared__ int red_c[AS_ROWS][16];
+
+    const int t = threadIdx.x;
+    const int tr = t / 16;          // rows tr and tr + 16
+    const int tc = t % 16;          // centers tc + 16*j, j = 0..3
+    const int64_t row0 = (int64_t)blockIdx.x * AS_ROWS;
+
+    double best[2] = {0.0, 0.0};
+    int best_c[2] = {-1, -1};
+
+    for (int c0 = 0; c0 < C; c0 += AS_CENT) {
+        double dot[2][4] = {{0, 0, 0, 0}, {0, 0, 0, 0}};
+        double cc[4] = {0, 0, 0, 0};
+        for (int k0 = 0; k0 < HD; k0 += AS_K) {
+            __syncthreads();
+            // stage x: 32 x 64 fp32 = 2048 values, 8 per thread
+            for (int e = t; e < AS_ROWS * AS_K; e += 256) {
+                int rr = e / AS_K, kk = e % AS_K;
+                int64_t gr = row0 + rr;
+                xs[rr][kk] = (gr < rows && k0 + kk < HD) ? x[gr * HD + k0 + kk] : 0.0f;
+            }
+            for (int e = t; e < AS_CENT * AS_K; e += 256) {
+                int cr = e / AS_K, kk = e % AS_K;
+                int gc = c0 + cr;
+                cs[cr][kk] = (gc < C && k0 + kk < HD)
+                                 ? bf16_bits_to_f32(centers[(int64_t)gc * HD + k0 + kk])
+                                 : 0.0f;
+            }
+            __syncthreads();
+            for (int kk = 0; kk < AS_K; ++kk) {
+                double xv0 = (double)xs[tr][kk];
+                double xv1 = (double)xs[tr + 16][kk];
+#pragma unroll
+                for (int j = 0; j < 4; ++j) {
+                    double cv = (double)cs[tc + 16 * j][kk];
+                    dot[0][j] += xv0 * cv;
+                    dot[1][j] += xv1 * cv;
+                    cc[j] += cv * cv;
+                }
+            }
+        }
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            int c = c0 + tc + 16 * j;
+            if (c >= C) continue;
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                double d = cc[j] - 2.0 * dot[i][j];
+                if (best_c[i] < 0 || d < best[i] || (d == best[i] && c < best_c[i])) {
+                    best[i] = d;
+                    best_c[i] = c;
+                }
+            }
+        }
+    }
+    // reduce over the 16 center lanes of each row (fixed order: lowest index wins ties)
+    red_d[tr][tc] = best[0];
+    red_c[tr][tc] = best_c[0];
+    red_d[tr + 16][tc] = best[1];
+    red_c[tr + 16][tc] = best_c[1];
+    __syncthreads();
+    if (t < AS_ROWS) {
+        double bd = red_d[t][0];
+        int bc = red_c[t][0];
+        for (int j = 1; j < 16; ++j) {
+            int c = red_c[t][j];
+            double d = red_d[t][j];
+            if (c >= 0 && (bc < 0 || d < bd || (d == bd && c < bc))) {
+                bd = d;
+                bc = c;
+            }
+        }
+        int64_t gr = row0 + t;
+        if (gr < rows) store_id<ID_BYTES>(ids, gr, bc);
+    }
+}
+
+// ============================================================ MFMA GEMM core
+// C[M, N] = A[M, K] * B[N, K]^T on v_mfma_f32_32x32x16_bf16.  A 256-thread
+// block computes a 64 x 64 tile: wave w owns the 32 x 32 sub-tile
+// (w / 2, w % 2).  K advances in steps of 32 through LDS.
+//
+// 32x32x16 operand layout (wave64): lane l supplies row (l % 32) of A and
+// column (l % 32) of B, with k = 8 * (l / 32) + [0, 8) inside the 16-wide
+// step.  The 16 accumulator values of lane l belong to column (l % 32) and
+// rows 8 * (i / 4) + 4 * (l / 32) + (i % 4).
+constexpr int GT_M = 64, GT_N = 64, GT_K = 32, GT_PAD = 8;
+
+struct GemmSmem {
+    uint16_t a[GT_M][GT_K + GT_PAD];
+    uint16_t b[GT_N][GT_K + GT_PAD];
+};
+
+__device__ __forceinline__ bf16x8 lds_bf16x8(const uint16_t* p) {
+    return *reinterpret_cast<const bf16x8*>(p);
+}
+
+// Encoder A-tile loader: A[m, k] = bf16(x[m, k] - center[id[m], k] - mean[k]).
+struct EncodeA {
+    const float* x;
+    const uint16_t* centers;
+    const void* ids;
+    int id_bytes;
+    int num_centers;
+    const float* mean;
+    int64_t M;
+    int K;
+    __device__ __forceinline__ int id_of(int64_t m) const {
+        int v;
+        if (id_bytes == 1) v = reinterpret_cast<const uint8_t*>(ids)[m];
+        else if (id_bytes == 2) v = reinterpret_cast<const uint16_t*>(ids)[m];
+        else v = reinterpret_cast<const int32_t*>(ids)[m];
+        return min(max(v, 0), num_centers - 1);
+    }
+    // thread t fills row t/4, k-columns (t%4)*8 .. +8 of the 64 x 32 tile
+    __device__ __forceinline__ void load(GemmSmem& s, int64_t m0, int k0, int t) const {
+        const int rr = t / 4, kc = (t % 4) * 8;
+        const int64_t m = m0 + rr;
+        u32x4 packedv = {0, 0, 0, 0};
+        if (m < M) {
+            const float* xp = x + m * K + k0 + kc;
+            f32x4 x0 = *reinterpret_cast<const f32x4*>(xp);
+            f32x4 x1 = *reinterpret_cast<const f32x4*>(xp + 4);
+            float v[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+            if (centers) {
+                const uint16_t* cp = centers + (int64_t)id_of(m) * K + k0 + kc;
+                u32x4 cw = *reinterpret_cast<const u32x4*>(cp);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[2 * e] = v[2 * e] - __uint_as_float(cw[e] << 16);
+                    v[2 * e + 1] = v[2 * e + 1] - __uint_as_float(cw[e] & 0xffff0000u);
+                }
+            }
+            if (mean) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = v[e] - mean[k0 + kc + e];
+            }
+#pragma unroll
+            for (int e = 0; e < 4; ++e) packedv[e] = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+        }
+        *reinterpret_cast<u32x4*>(&s.a[rr][kc]) = packedv;
+    }
+};
+
+// Decoder A-tile loader: A[m, k] = bf16(code * scale) of row src(m).
+struct DecodeA {
+    const uint8_t* packed;
+    const uint16_t* scales;
+    const int32_t* row_index;
+    int scale_dtype;
+    int group;
+    int64_t M;   // output rows
+    int K;       // r
+    __device__ __forceinline__ void load(GemmSmem& s, int64_t m0, int k0, int t) const {
+        const int rr = t / 4, kc = (t % 4) * 8;
+        const int64_t m = m0 + rr;
+        u32x4 o = {0, 0, 0, 0};
+        if (m < M) {
+            const int64_t src = row_index ? (int64_t)row_index[m] : m;
+            const uint32_t word =
+                *reinterpret_cast<const uint32_t*>(packed + src * (K / 2) + (k0 + kc) / 2);
+            const float sc =
+                scale_bits_to_f32(scales[src * (K / group) + (k0 + kc) / group], scale_dtype);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                float lo = (float)((int)((word >> (8 * e)) & 15u) - 7) * sc;
+                float hi = (float)((int)((word >> (8 * e + 4)) & 15u) - 7) * sc;
+                o[e] = pack_bf16x2(lo, hi);
+            }
+        }
+        *reinterpret_cast<u32x4*>(&s.a[rr][kc]) = o;
+    }
+};
+
+// B tile [64 rows (n) x 32 k] of a bf16 row-major [N, K] matrix.
+__device__ __forceinline__ void load_b_tile(GemmSmem& s, const uint16_t* __restrict__ B,
+                                            int64_t N, int K, int64_t n0, int k0, int t) {
+    const int rr = t / 4, kc = (t % 4) * 8;
+    const int64_t n = n0 + rr;
+    u32x4 v = {0, 0, 0, 0};
+    if (n < N) v = *reinterpret_cast<const u32x4*>(B + n * K + k0 + kc);
+    *reinterpret_cast<u32x4*>(&s.b[rr][kc]) = v;
+}
+
+template <class ALoader>
+__device__ __forceinline__ f32x16 gemm_tile(GemmSmem& s, const ALoader& al,
+                                            const uint16_t* __restrict__ B, int64_t N, int K,
+                                            int64_t m0, int64_t n0) {
+    const int t = threadIdx.x;
+    const int lane = t & 63, wave = t >> 6;
+    const int wm = (wave >> 1) * 32, wn = (wave & 1) * 32;
+    const int hf = lane >> 5, l32 = lane & 31;
+    f32x16 acc = {};
+    for (int k0 = 0; k0 < K; k0 += GT_K) {
+        __syncthreads();
+        al.load(s, m0, k0, t);
+        load_b_tile(s, B, N, K, n0, k0, t);
+        __syncthreads();
+#pragma unroll
+        for (int kk = 0; kk < GT_K; kk += 16) {
+            bf16x8 a = lds_bf16x8(&s.a[wm + l32][kk + 8 * hf]);
+            bf16x8 b = lds_bf16x8(&s.b[wn + l32][kk + 8 * hf]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, acc, 0, 0, 0);
+        }
+    }
+    return acc;
+}
+
+__global__ void __launch_bounds__(256) encode_gemm_kernel(EncodeA al,
+                                                          const uint16_t* __restrict__ w_enc,
+                                                          int r, float* __restrict__ coeff) {
+    __shared__ GemmSmem s;
+    const int64_t m0 = (int64_t)blockIdx.x * GT_M, n0 = (int64_t)blockIdx.y * GT_N;
+    f32x16 acc = gemm_tile(s, al, w_enc, r, al.K, m0, n0);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hf = lane >> 5, l32 = lane & 31;
+    const int64_t n = n0 + (wave & 1) * 32 + l32;
+    if (n >= r) return;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int64_t m = m0 + (wave >> 1) * 32 + 8 * (i / 4) + 4 * hf + (i % 4);
+        if (m < al.M) coeff[m * r + n] = acc[i];
+    }
+}
+
+struct DecodeEpi {
+    const uint16_t* centers;   // [C, HD] for this batch item, or NULL
+    const void* ids;           // [N] of this batch item
+    int id_bytes;
+    int num_centers;
+    const int32_t* row_index;
+    const float* mean;
+    // ids outside the table are clamped (a corrupt payload must not read out of bounds)
+    __device__ __forceinline__ int id_of(int64_t src) const {
+        int v;
+        if (id_bytes == 1) v = reinterpret_cast<const uint8_t*>(ids)[src];
+        else if (id_bytes == 2) v = reinterpret_cast<const uint16_t*>(ids)[src];
+        else v = reinterpret_cast<const int32_t*>(ids)[src];
+        return min(max(v, 0), num_centers - 1);
+    }
+};
+
+// out[m, n] = bf16(bf16(acc + bf16(mean[n])) + center[id[src(m)], n])   (MG:438-454)
+__global__ void __launch_bounds__(256) decode_gemm_kernel(DecodeA al, DecodeEpi ep,
+                                                          const uint16_t* __restrict__ w_dec,
+                                                          int HD, uint16_t* __restrict__ out) {
+    __shared__ GemmSmem s;
+    const int64_t m0 = (int64_t)blockIdx.x * GT_M, n0 = (int64_t)blockIdx.y * GT_N;
+    f32x16 acc = gemm_tile(s, al, w_dec, HD, al.K, m0, n0);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hf = lane >> 5, l32 = lane & 31;
+    const int64_t n = n0 + (wave & 1) * 32 + l32;
+    if (n >= HD) return;
+    const float bias = ep.mean ? bf16_round(ep.mean[n]) : 0.0f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int64_t m = m0 + (wave >> 1) * 32 + 8 * (i / 4) + 4 * hf + (i % 4);
+        if (m >= al.M) continue;
+        float v = bf16_round(acc[i] + bias);
+        if (ep.centers) {
+            const int64_t src = ep.row_index ? (int64_t)ep.row_index[m] : m;
+            v = bf16_round(v + bf16_bits_to_f32(ep.centers[(int64_t)ep.id_of(src) * HD + n]));
+        }
+        out[m * HD + n] = f32_to_bf16_bits(v);
+    }
+}
+
+}  // namespace nkv
+
+using namespace nkv;
+
+// ============================================================ C ABI
+static int check_codec_layout(int r, int group, int scale_dtype) {
+    NKV_REQUIRE(r > 0 && r % 32 == 0, NKV_ERR_INVALID, "r must be a positive multiple of 32");
+    NKV_REQUIRE(group > 0 && r % group == 0 && group % 8 == 0, NKV_ERR_INVALID,
+                "group must divide r and be a multiple of 8");
+    NKV_REQUIRE(scale_dtype == NKV_DTYPE_BF16 || scale_dtype == NKV_DTYPE_FP16,
+                NKV_ERR_INVALID, "scale_dtype must be NKV_DTYPE_BF16 or NKV_DTYPE_FP16");
+    return NKV_OK;
+}
+
+extern "C" int nkv_quant_pack(void* stream, const float* coeff, int64_t rows, int r, int group,
+                              int scale_dtype, int quant_mode, uint8_t* packed,
+                              uint16_t* scales) {
+    clear_error();
+    NKV_REQUIRE(rows >= 0, NKV_ERR_INVALID, "rows must be >= 0");
+    NKV_REQUIRE(r > 0 && r % 8 == 0, NKV_ERR_INVALID, "r must be a positive multiple of 8");
+    NKV_REQUIRE(group > 0 && r % group == 0 && group % 8 == 0, NKV_ERR_INVALID,
+                "group must divide r and be a multiple of 8");
+    NKV_REQUIRE(scale_dtype == NKV_DTYPE_BF16 || scale_dtype == NKV_DTYPE_FP16,
+                NKV_ERR_INVALID, "bad scale_dtype");
+    NKV_REQUIRE(quant_mode == NKV_QUANT_FP32 || quant_mode == NKV_QUANT_BF16, NKV_ERR_INVALID,
+                "bad quant_mode");
+    if (rows == 0) return NKV_OK;
+    NKV_REQUIRE(coeff && packed && scales, NKV_ERR_INVALID, "null pointer");
+    const int64_t threads = rows * (r / group);
+    dim3 grid((unsigned)cdiv(threads, 256));
+    hipStream_t s = (hipStream_t)stream;
+    if (quant_mode == NKV_QUANT_BF16)
+        quant_pack_kernel<NKV_QUANT_BF16><<<grid, 256, 0, s>>>(coeff, rows, r, group, scale_dtype,
+                                                                packed, scales);
+    else
+        quant_pack_kernel<NKV_QUANT_FP32><<<grid, 256, 0, s>>>(coeff, rows, r, group, scale_dtype,
+                                                                packed, scales);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+extern "C" int nkv_unpack(void* stream, const uint8_t* packed, const uint16_t* scales,
+                          int scale_dtype, const int32_t* row_index, int64_t rows, int r,
+                          int group, uint16_t* latent) {
+    clear_error();
+    NKV_REQUIRE(rows >= 0, NKV_ERR_INVALID, "rows must be >= 0");
+    NKV_REQUIRE(r > 0 && r % 8 == 0, NKV_ERR_INVALID, "r must be a positive multiple of 8");
+    NKV_REQUIRE(group > 0 && r % group == 0 && group % 8 == 0, NKV_ERR_INVALID,
+                "group must divide r and be a multiple of 8");
+    NKV_REQUIRE(scale_dtype == NKV_DTYPE_BF16 || scale_dtype == NKV_DTYPE_FP16,
+                NKV_ERR_INVALID, "bad scale_dtype");
+    if (rows == 0) return NKV_OK;
+    NKV_REQUIRE(packed && scales && latent, NKV_ERR_INVALID, "null pointer");
+    const int64_t threads = rows * (r / 8);
+    unpack_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, (hipStream_t)stream>>>(
+        packed, scales, scale_dtype, row_index, rows, r, group, latent);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+static int launch_assign(hipStream_t s, const float* x, const uint16_t* centers, int64_t rows,
+                         int C, int HD, void* ids, int id_bytes) {
+    dim3 grid((unsigned)cdiv(rows, AS_ROWS));
+    if (id_bytes == 1)
+        assign_kernel<1><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
+    else if (id_bytes == 2)
+        assign_kernel<2><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
+    else
+        assign_kernel<4><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+static int check_ids(int C, int id_bytes) {
+    NKV_REQUIRE(id_bytes == 1 || id_bytes == 2 || id_bytes == 4, NKV_ERR_INVALID,
+                "id_bytes must be 1, 2 or 4");
+    NKV_REQUIRE(C > 0, NKV_ERR_INVALID, "need at least one center");
+    NKV_REQUIRE(!(id_bytes == 1 && C > 256), NKV_ERR_INVALID, "uint8 ids need C <= 256");
+    NKV_REQUIRE(!(id_bytes == 2 && C > 65536), NKV_ERR_INVALID, "uint16 ids need C <= 65536");
+    return NKV_OK;
+}
+
+extern "C" int nkv_assign(void* stream, const float* x, const uint16_t* centers, int64_t rows,
+                          int C, int HD, void* ids, int id_bytes) {
+    clear_error();
+    NKV_REQUIRE(rows >= 0 && HD > 0, NKV_ERR_INVALID, "rows must be >= 0 and HD > 0");
+    int rc = check_ids(C, id_bytes);
+    if (rc) return rc;
+    if (rows == 0) return NKV_OK;
+    NKV_REQUIRE(x && centers && ids, NKV_ERR_INVALID, "null pointer");
+    return launch_assign((hipStream_t)stream, x, centers, rows, C, HD, ids, id_bytes);
+}
+
+extern "C" int nkv_encode(void* stream, const nkv_encode_args* a) {
+    clear_error();
+    NKV_REQUIRE(a, NKV_ERR_INVALID, "null args");
+    NKV_REQUIRE(a->rows >= 0, NKV_ERR_INVALID, "rows must be >= 0");
+    NKV_REQUIRE(a->HD > 0 && a->HD % 32 == 0, NKV_ERR_INVALID, "HD must be a multiple of 32");
+    int rc = check_codec_layout(a->r, a->group, a->scale_dtype);
+    if (rc) return rc;
+    NKV_REQUIRE(a->quant_mode == NKV_QUANT_FP32 || a->quant_mode == NKV_QUANT_BF16,
+                NKV_ERR_INVALID, "bad quant_mode");
+    if (a->centers) {
+        rc = check_ids(a->num_centers, a->id_bytes);
+        if (rc) return rc;
+        NKV_REQUIRE(a->ids, NKV_ERR_INVALID, "ids output required with centers");
+    }
+    if (a->rows == 0) return NKV_OK;
+    NKV_REQUIRE(a->x && a->w_enc && a->coeff && a->packed && a->scales, NKV_ERR_INVALID,
+                "null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    if (a->centers) {
+        rc = launch_assign(s, a->x, a->centers, a->rows, a->num_centers, a->HD, a->ids,
+                           a->id_bytes);
+        if (rc) return rc;
+    }
+    EncodeA al;
+    al.x = a->x;
+    al.centers = a->centers;
+    al.ids = a->ids;
+    al.id_bytes = a->id_bytes;
+    al.num_centers = a->num_centers;
+    al.mean = a->mean;
+    al.M = a->rows;
+    al.K = a->HD;
+    dim3 grid((unsigned)cdiv(a->rows, GT_M), (unsigned)cdiv(a->r, GT_N));
+    encode_gemm_kernel<<<grid, 256, 0, s>>>(al, a->w_enc, a->r, a->coeff);
+    NKV_LAUNCH_CHECK();
+    return nkv_quant_pack(stream, a->coeff, a->rows, a->r, a->group, a->scale_dtype,
+                          a->quant_mode, a->packed, a->scales);
+}
+
+extern "C" int nkv_decode(void* stream, const nkv_decode_args* a) {
+    clear_error();
+    NKV_REQUIRE(a, NKV_ERR_INVALID, "null args");
+    const nkv_codec& c = a->codec;
+    NKV_REQUIRE(a->B >= 1 && a->N >= 0 && a->rows >= 0, NKV_ERR_INVALID, "bad B/N/rows");
+    NKV_REQUIRE(a->HD > 0 && a->HD % 32 == 0, NKV_ERR_INVALID, "HD must be a multiple of 32");
+    int rc = check_codec_layout(c.r, c.group, c.scale_dtype);
+    if (rc) return rc;
+    NKV_REQUIRE(a->row_index || a->rows == a->N, NKV_ERR_INVALID,
+                "rows must equal N without row_index");
+    if (c.centers) {
+        rc = check_ids(c.num_centers, c.id_bytes);
+        if (rc) return rc;
+        NKV_REQUIRE(c.ids, NKV_ERR_INVALID, "ids required with centers");
+    }
+    if (a->rows == 0) return NKV_OK;
+    NKV_REQUIRE(c.packed && c.scales && c.w_dec && a->out, NKV_ERR_INVALID, "null pointer");
+    hipStream_t s = (hipStream_t)stream;
+    dim3 grid((unsigned)cdiv(a->rows, GT_M), (unsigned)cdiv(a->HD, GT_N));
+    for (int b = 0; b < a->B; ++b) {
+        DecodeA al;
+        al.packed = c.packed + (int64_t)b * a->N * (c.r / 2);
+        al.scales = c.scales + (int64_t)b * a->N * (c.r / c.group);
+        al.row_index = a->row_index;
+        al.scale_dtype = c.scale_dtype;
+        al.group = c.group;
+        al.M = a->rows;
+        al.K = c.r;
+        DecodeEpi ep;
+        ep.centers = c.centers ? c.centers + (int64_t)b * c.centers_batch_stride : nullptr;
+        ep.ids = c.ids ? (const void*)((const uint8_t*)c.ids + (int64_t)b * a->N * c.id_bytes)
+                       : nullptr;
+        ep.id_bytes = c.id_bytes;
+        ep.num_centers = c.num_centers;
+        ep.row_index = a->row_index;
+        ep.mean = c.mean;
+        decode_gemm_kernel<<<grid, 256, 0, s>>>(al, ep, c.w_dec, a->HD,
+                                                a->out + (int64_t)b * a->rows * a->HD);
+        NKV_LAUNCH_CHECK();
+    }
+    return NKV_OK;
+}

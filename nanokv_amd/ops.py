@@ -1,0 +1,340 @@
+"""Torch-facing wrappers of the NanoKV HIP kernels.
+
+Each function validates shapes, dtypes and devices on the host, allocates its
+outputs with torch on the input's device, and enqueues the kernel on the
+current HIP stream through the C ABI (include/nanokv.h).  There is no CPU
+path: tensors must live on the GPU and the HIP library must be built.
+"""
+from __future__ import annotations
+
+import math
+from ctypes import byref
+from dataclasses import dataclass
+from typing import Optional
+
+import torch
+
+from . import _lib
+from ._lib import (NKV_DTYPE_BF16, NKV_DTYPE_FP16, NKV_QUANT_BF16, NKV_QUANT_FP32, NkvAttendArgs,
+                   NkvCodec, NkvDecodeArgs, NkvEncodeArgs, check, lib)
+
+_SCALE_CODES = {torch.bfloat16: NKV_DTYPE_BF16, torch.float16: NKV_DTYPE_FP16}
+_QUANT_CODES = {"fp32": NKV_QUANT_FP32, "bf16": NKV_QUANT_BF16}
+_ID_BYTES = {torch.uint8: 1, torch.int16: 2, torch.int32: 4}
+if hasattr(torch, "uint16"):
+    _ID_BYTES[torch.uint16] = 2
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None else t.data_ptr()
+
+
+def _require_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
+    device = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("NanoKV HIP ops require GPU tensors (no CPU fallback)")
+        if device is None:
+            device = t.device
+        elif t.device != device:
+            raise ValueError(f"tensors on different devices: {device} vs {t.device}")
+    if device is None:
+        raise ValueError("no tensor given")
+    return device
+
+
+def _contig(t: torch.Tensor, dtype: torch.dtype, name: str) -> torch.Tensor:
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+    return t
+
+
+def id_dtype_for(num_centers: int) -> torch.dtype:
+    """uint8 ids up to 256 centers (the reference's layout), else 16-bit."""
+    if num_centers <= 256:
+        return torch.uint8
+    if num_centers <= 65536:
+        return torch.int16
+    return torch.int32
+
+
+# ---------------------------------------------------------------- quantiser
+def quant_pack(coeff: torch.Tensor, group: int, scale_dtype: torch.dtype = torch.bfloat16,
+               quant_mode: str = "fp32") -> tuple[torch.Tensor, torch.Tensor]:
+    """INT4 quantise + pack fp32 coefficients [..., r] (see nkv_quant_pack).
+
+    Returns (packed uint8 [..., r/2], scales [..., r/group] of scale_dtype).
+    """
+    device = _require_gpu(coeff)
+    _contig(coeff, torch.float32, "coeff")
+    r = int(coeff.shape[-1])
+    rows = coeff.numel() // r if r else 0
+    if r % 2:
+        raise ValueError("INT4 packing needs an even coefficient width")
+    if group <= 0 or r % group:
+        raise ValueError(f"group {group} must divide r={r}")
+    packed = torch.empty((*coeff.shape[:-1], r // 2), device=device, dtype=torch.uint8)
+    scales = torch.empty((*coeff.shape[:-1], r // group), device=device, dtype=scale_dtype)
+    check("nkv_quant_pack", lib().nkv_quant_pack(
+        _stream(device), coeff.data_ptr(), rows, r, group, _SCALE_CODES[scale_dtype],
+        _QUANT_CODES[quant_mode], packed.data_ptr(), scales.data_ptr()))
+    return packed, scales
+
+
+def unpack(packed: torch.Tensor, scales: torch.Tensor, r: int, group: int,
+           row_index: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """bf16(code * scale) for all rows or the rows in row_index: [rows, r]."""
+    device = _require_gpu(packed, scales, row_index)
+    _contig(packed, torch.uint8, "packed")
+    if scales.dtype not in _SCALE_CODES or not scales.is_contiguous():
+        raise TypeError("scales must be a contiguous bf16 or fp16 tensor")
+    src_rows = packed.numel() // (r // 2)
+    if packed.numel() != src_rows * (r // 2) or scales.numel() != src_rows * (r // group):
+        raise ValueError("invalid packed INT4 payload")
+    if row_index is not None:
+        _contig(row_index, torch.int32, "row_index")
+        rows = row_index.numel()
+    else:
+        rows = src_rows
+    out = torch.empty((rows, r), device=device, dtype=torch.bfloat16)
+    check("nkv_unpack", lib().nkv_unpack(
+        _stream(device), packed.data_ptr(), scales.data_ptr(), _SCALE_CODES[scales.dtype],
+        _ptr(row_index), rows, r, group, out.data_ptr()))
+    return out
+
+
+def assign(x: torch.Tensor, centers: torch.Tensor,
+           id_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """Nearest bf16 center per fp32 row (fp64 decision, first index on ties)."""
+    device = _require_gpu(x, centers)
+    _contig(x, torch.float32, "x")
+    _contig(centers, torch.bfloat16, "centers")
+    hd = int(x.shape[-1])
+    if centers.dim() != 2 or centers.shape[1] != hd:
+        raise ValueError("centers must be [C, HD] with the rows' HD")
+    C = int(centers.shape[0])
+    id_dtype = id_dtype or id_dtype_for(C)
+    rows = x.numel() // hd
+    ids = torch.empty(x.shape[:-1], device=device, dtype=id_dtype)
+    check("nkv_assign", lib().nkv_assign(_stream(device), x.data_ptr(), centers.data_ptr(), rows,
+                                         C, hd, ids.data_ptr(), _ID_BYTES[id_dtype]))
+    return ids
+
+
+def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tensor] = None,
+           mean: Optional[torch.Tensor] = None, group: int = 32,
+           scale_dtype: torch.dtype = torch.bfloat16, quant_mode: str = "fp32",
+           id_dtype: Optional[torch.dtype] = None) -> dict:
+    """Encode fp32 rows [rows, HD] with given centers (see nkv_encode)."""
+    device = _require_gpu(x, w_enc, centers, mean)
+    _contig(x, torch.float32, "x")
+    _contig(w_enc, torch.bfloat16, "w_enc")
+    hd = int(x.shape[-1])
+    rows = x.numel() // hd
+    r = int(w_enc.shape[0])
+    if w_enc.shape[1] != hd:
+        raise ValueError("w_enc must be [r, HD]")
+    args = NkvEncodeArgs()
+    args.rows, args.HD, args.r, args.group = rows, hd, r, group
+    args.scale_dtype = _SCALE_CODES[scale_dtype]
+    args.quant_mode = _QUANT_CODES[quant_mode]
+    ids = None
+    if centers is not None:
+        _contig(centers, torch.bfloat16, "centers")
+        C = int(centers.shape[0])
+        id_dtype = id_dtype or id_dtype_for(C)
+        ids = torch.empty(x.shape[:-1], device=device, dtype=id_dtype)
+        args.num_centers, args.id_bytes = C, _ID_BYTES[id_dtype]
+        args.centers, args.ids = centers.data_ptr(), ids.data_ptr()
+    if mean is not None:
+        _contig(mean, torch.float32, "mean")
+        args.mean = mean.data_ptr()
+    coeff = torch.empty((*x.shape[:-1], r), device=device, dtype=torch.float32)
+    packed = torch.empty((*x.shape[:-1], r // 2), device=device, dtype=torch.uint8)
+    scales = torch.empty((*x.shape[:-1], r // group), device=device, dtype=scale_dtype)
+    args.x, args.w_enc = x.data_ptr(), w_enc.data_ptr()
+    args.coeff, args.packed, args.scales = coeff.data_ptr(), packed.data_ptr(), scales.data_ptr()
+    check("nkv_encode", lib().nkv_encode(_stream(device), byref(args)))
+    return {"packed": packed, "scales": scales, "ids": ids, "coeff": coeff}
+
+
+# ---------------------------------------------------------------- codec view
+@dataclass
+class Codec:
+    """Device tensors of one K or V history codec.
+
+    packed [B, N, r/2] uint8, scales [B, N, r/group] bf16/fp16, ids [B, N]
+    (uint8/int16/int32) or None, centers [B or 1, C, HD] bf16 or None,
+    w_dec [HD, r] bf16, mean [HD] fp32 or None.
+    """
+    packed: torch.Tensor
+    scales: torch.Tensor
+    w_dec: torch.Tensor
+    group: int
+    ids: Optional[torch.Tensor] = None
+    centers: Optional[torch.Tensor] = None
+    mean: Optional[torch.Tensor] = None
+
+    @property
+    def r(self) -> int:
+        return int(self.w_dec.shape[1])
+
+    @property
+    def batch(self) -> int:
+        return int(self.packed.shape[0])
+
+    @property
+    def tokens(self) -> int:
+        return int(self.packed.shape[1])
+
+    def validate(self, hd: int) -> None:
+        r = self.r
+        _contig(self.packed, torch.uint8, "packed")
+        _contig(self.w_dec, torch.bfloat16, "w_dec")
+        if self.scales.dtype not in _SCALE_CODES or not self.scales.is_contiguous():
+            raise TypeError("scales must be a contiguous bf16 or fp16 tensor")
+        B, N = self.batch, self.tokens
+        if tuple(self.packed.shape) != (B, N, r // 2):
+            raise ValueError(f"packed must be [B, N, r/2], got {tuple(self.packed.shape)}")
+        if self.group <= 0 or r % self.group or tuple(self.scales.shape) != (B, N, r // self.group):
+            raise ValueError("scales must be [B, N, r/group]")
+        if tuple(self.w_dec.shape) != (hd, r):
+            raise ValueError(f"w_dec must be [HD={hd}, r={r}]")
+        if self.centers is not None:
+            _contig(self.centers, torch.bfloat16, "centers")
+            if self.ids is None or self.ids.dtype not in _ID_BYTES or not self.ids.is_contiguous():
+                raise TypeError("ids must be a contiguous uint8/int16/int32 tensor with centers")
+            if tuple(self.ids.shape) != (B, N):
+                raise ValueError("ids must be [B, N]")
+            if self.centers.dim() != 3 or self.centers.shape[0] not in (1, B) or \
+                    self.centers.shape[2] != hd:
+                raise ValueError("centers must be [B or 1, C, HD]")
+        if self.mean is not None:
+            _contig(self.mean, torch.float32, "mean")
+            if self.mean.numel() != hd:
+                raise ValueError("mean must have HD elements")
+
+    def struct(self) -> NkvCodec:
+        c = NkvCodec()
+        c.packed, c.scales, c.w_dec = (self.packed.data_ptr(), self.scales.data_ptr(),
+                                       self.w_dec.data_ptr())
+        c.r, c.group, c.scale_dtype = self.r, self.group, _SCALE_CODES[self.scales.dtype]
+        if self.centers is not None:
+            c.centers, c.ids = self.centers.data_ptr(), self.ids.data_ptr()
+            c.id_bytes = _ID_BYTES[self.ids.dtype]
+            c.num_centers = int(self.centers.shape[1])
+            c.centers_batch_stride = (0 if self.centers.shape[0] == 1
+                                      else int(self.centers.stride(0)))
+        if self.mean is not None:
+            c.mean = self.mean.data_ptr()
+        return c
+
+
+def decode(codec: Codec, hd: int, row_index: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Full-width bf16 decode [B, rows, HD] of all or selected rows."""
+    device = _require_gpu(codec.packed, row_index)
+    codec.validate(hd)
+    args = NkvDecodeArgs()
+    args.B, args.HD, args.N = codec.batch, hd, codec.tokens
+    if row_index is not None:
+        _contig(row_index, torch.int32, "row_index")
+        args.rows, args.row_index = row_index.numel(), row_index.data_ptr()
+    else:
+        args.rows = codec.tokens
+    args.codec = codec.struct()
+    out = torch.empty((codec.batch, int(args.rows), hd), device=device, dtype=torch.bfloat16)
+    args.out = out.data_ptr()
+    check("nkv_decode", lib().nkv_decode(_stream(device), byref(args)))
+    return out
+
+
+def _strides_bthd(t: torch.Tensor, name: str) -> tuple[int, int, int]:
+    if t.dim() != 4 or t.stride(3) != 1:
+        raise ValueError(f"{name} must be [B, T, H, D] with contiguous D")
+    if t.data_ptr() % 16 or any(s % 8 for s in t.stride()[:3]):
+        raise ValueError(f"{name} must be 16-byte aligned with strides divisible by 8")
+    return t.stride(0), t.stride(1), t.stride(2)
+
+
+def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
+           key: Optional[Codec] = None, value: Optional[Codec] = None, *,
+           softmax_scale: Optional[float] = None, return_lse: bool = True,
+           splits: int = 0, out: Optional[torch.Tensor] = None):
+    """Fused decode+attention (see nkv_attend).
+
+    q [B, Q, H, D] bf16; k_cur/v_cur [B, Nc, H, D] bf16 or None; key/value
+    history codecs (both or neither).  Returns (out [B, Q, H, D] bf16,
+    lse [B, H, Q] fp32 or None).
+    """
+    device = _require_gpu(q, k_cur, v_cur)
+    if q.dtype != torch.bfloat16:
+        raise TypeError("q must be bf16")
+    B, Qn, H, D = (int(v) for v in q.shape)
+    hd = H * D
+    args = NkvAttendArgs()
+    args.B, args.H, args.D, args.splits, args.Q = B, H, D, int(splits), Qn
+    args.softmax_scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    args.q = q.data_ptr()
+    args.q_sb, args.q_st, args.q_sh = _strides_bthd(q, "q")
+    if (key is None) != (value is None):
+        raise ValueError("key and value codecs must be given together")
+    if key is not None:
+        key.validate(hd)
+        value.validate(hd)
+        if key.tokens != value.tokens or key.batch != B or value.batch != B:
+            raise ValueError("key/value codec token counts or batch differ from q")
+        args.N = key.tokens
+        args.key, args.value = key.struct(), value.struct()
+    if (k_cur is None) != (v_cur is None):
+        raise ValueError("k_cur and v_cur must be given together")
+    if k_cur is not None:
+        for name, t in (("k_cur", k_cur), ("v_cur", v_cur)):
+            if t.dtype != torch.bfloat16 or t.shape[0] != B or t.shape[2] != H or t.shape[3] != D:
+                raise ValueError(f"{name} must be bf16 [B, Nc, H, D]")
+        if k_cur.shape[1] != v_cur.shape[1]:
+            raise ValueError("k_cur and v_cur lengths differ")
+        args.Nc = int(k_cur.shape[1])
+        args.k_cur, args.v_cur = k_cur.data_ptr(), v_cur.data_ptr()
+        args.k_sb, args.k_st, args.k_sh = _strides_bthd(k_cur, "k_cur")
+        args.v_sb, args.v_st, args.v_sh = _strides_bthd(v_cur, "v_cur")
+    if out is None:
+        out = torch.empty((B, Qn, H, D), device=device, dtype=torch.bfloat16)
+    args.out = out.data_ptr()
+    args.o_sb, args.o_st, args.o_sh = _strides_bthd(out, "out")
+    lse = torch.empty((B, H, Qn), device=device, dtype=torch.float32) if return_lse else None
+    args.lse = _ptr(lse)
+    need = lib().nkv_attend_workspace_size(byref(args))
+    err = lib().nkv_last_error().decode()
+    if need == 0 and err:
+        raise _lib.NanoKVError("nkv_attend_workspace_size", _lib.NKV_ERR_INVALID, err)
+    ws = torch.empty(need, device=device, dtype=torch.uint8) if need else None
+    check("nkv_attend", lib().nkv_attend(_stream(device), byref(args), _ptr(ws), need))
+    return out, lse
+
+
+def lse_merge(a: torch.Tensor, lse_a: torch.Tensor, b: torch.Tensor, lse_b: torch.Tensor,
+              out: Optional[torch.Tensor] = None):
+    """Merge two attention partitions [..., D] with their LSE [...] (nkv_lse_merge)."""
+    device = _require_gpu(a, lse_a, b, lse_b)
+    for name, t in (("a", a), ("b", b)):
+        _contig(t, torch.bfloat16, name)
+    for name, t in (("lse_a", lse_a), ("lse_b", lse_b)):
+        _contig(t, torch.float32, name)
+    D = int(a.shape[-1])
+    rows = a.numel() // D
+    if b.shape != a.shape or lse_a.numel() != rows or lse_b.numel() != rows:
+        raise ValueError("merge operands have mismatched shapes")
+    out = torch.empty_like(a) if out is None else out
+    lse = torch.empty_like(lse_a)
+    check("nkv_lse_merge", lib().nkv_lse_merge(
+        _stream(device), rows, D, a.data_ptr(), D, lse_a.data_ptr(), b.data_ptr(), D,
+        lse_b.data_ptr(), out.data_ptr(), D, lse.data_ptr()))
+    return out, lse

@@ -1,0 +1,151 @@
+"""Seeded synthetic inputs for the benchmark configurations.
+
+The benchmark shapes have no public checkpoint or dataset behind them, so
+history K/V rows are generated with the structure NanoKV's codec exploits:
+token i = center[u_i] + G_i diag(1/sqrt(k)) U + eps_i with u_i uniform over
+the shared centers, G ~ N(0,1) [N, 64], U an orthonormal [64, HD] basis and
+eps ~ N(0, 0.05^2).  Rows are rounded to bf16 (the dtype a backbone's K/V
+projection produces) and handed to the encoder as fp32.
+
+Everything is generated with torch.Generator objects seeded explicitly, on
+the device requested, so the GPU path and the CPU oracle see the same bits.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass, field
+from typing import Optional
+
+import torch
+
+
+@dataclass(frozen=True)
+class Shape:
+    """One attention layer call: H heads of width D, N history tokens (compressed),
+    Q query tokens, Nc uncompressed current-chunk tokens, ranks rK/rV, scale group
+    G, C shared centers."""
+    name: str
+    H: int
+    D: int
+    N: int
+    Q: int
+    Nc: int
+    rK: int
+    rV: int
+    G: int
+    C: int
+    scale_dtype: torch.dtype = torch.float16
+    B: int = 1
+
+    @property
+    def HD(self) -> int:
+        return self.H * self.D
+
+    def flops(self) -> dict:
+        """Algorithmic flops: attention 4*Q*(N+Nc)*HD and a decode GEMM counted
+        once per history token 2*N*(rK+rV)*HD."""
+        att_hist = 4.0 * self.B * self.Q * self.N * self.HD
+        att_cur = 4.0 * self.B * self.Q * self.Nc * self.HD
+        dec = 2.0 * self.B * self.N * (self.rK + self.rV) * self.HD
+        return {"attention_history": att_hist, "attention_current": att_cur, "decode": dec,
+                "total": att_hist + att_cur + dec}
+
+    def coeff_stream_bytes(self) -> float:
+        """Unique bytes of the compressed history read by one call: packed codes,
+        group scales and center ids of K and V."""
+        id_bytes = 1 if self.C <= 256 else 2
+        # packed codes (r/2 bytes) + 2-byte group scales, for K and V, + one id each
+        per_tok = self.rK // 2 + self.rV // 2 + 2 * (self.rK // self.G) + 2 * (self.rV // self.G)
+        return float(self.B * self.N * (per_tok + 2 * id_bytes))
+
+
+# BASELINE.json configurations (index = position in its "configs" list).
+CONFIGS = {
+    0: Shape("cfg0_cpu_h8_d64", H=8, D=64, N=2048, Q=256, Nc=256, rK=64, rV=64, G=64, C=16,
+             scale_dtype=torch.bfloat16),
+    1: Shape("cfg1_h24_d128_n12480_q1560", H=24, D=128, N=12480, Q=1560, Nc=1560, rK=384,
+             rV=384, G=32, C=256),
+    2: Shape("cfg2_h24_d128_n49920_q780", H=24, D=128, N=49920, Q=780, Nc=780, rK=384, rV=256,
+             G=32, C=1024),
+}
+
+
+def _gen(seed: int, device) -> torch.Generator:
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    return g
+
+
+def orthonormal(rows: int, cols: int, seed: int, device="cpu") -> torch.Tensor:
+    """Orthonormal [rows, cols] (rows <= cols) from the QR of a Gaussian, fp32."""
+    g = _gen(seed, "cpu")
+    a = torch.randn(cols, rows, generator=g, dtype=torch.float64)
+    qm, rm = torch.linalg.qr(a)
+    qm = qm * torch.sign(torch.diagonal(rm))[None, :]
+    return qm.T.contiguous().to(device=device, dtype=torch.float32)
+
+
+@dataclass
+class Layer:
+    """Codec operators and shared centers of one layer (K and V)."""
+    centers_k: torch.Tensor   # [C, HD] bf16
+    centers_v: torch.Tensor
+    w_enc_k: torch.Tensor     # [rK, HD] bf16
+    w_dec_k: torch.Tensor     # [HD, rK] bf16
+    w_enc_v: torch.Tensor
+    w_dec_v: torch.Tensor
+    mean_k: Optional[torch.Tensor] = None   # [HD] fp32
+    mean_v: Optional[torch.Tensor] = None
+
+
+def make_layer(shape: Shape, seed: int = 0, device="cpu", orthonormal_codec: bool = False,
+               with_mean: bool = False) -> Layer:
+    """Random codec operators for one layer.
+
+    Decoders are random N(0,1)/sqrt(r) bf16 [HD, r] (independent for K and V)
+    and encoders their least-squares inverse bf16(W^T * r / HD); with
+    orthonormal_codec the encoder is a fixed orthonormal [r, HD] projection
+    and the decoder its transpose (config 0).  Centers are N(0,1) in bf16.
+    """
+    g = _gen(seed * 1000 + 17, "cpu")
+    HD = shape.HD
+
+    def codec(r, sub):
+        if orthonormal_codec:
+            enc = orthonormal(r, HD, seed * 1000 + sub)
+            dec = enc.T.contiguous()
+        else:
+            dec = torch.randn(HD, r, generator=g) / r ** 0.5
+            enc = dec.T * (r / HD)
+        return (enc.to(torch.bfloat16).contiguous().to(device),
+                dec.to(torch.bfloat16).contiguous().to(device))
+
+    ck = torch.randn(shape.C, HD, generator=g).to(torch.bfloat16).to(device)
+    cv = torch.randn(shape.C, HD, generator=g).to(torch.bfloat16).to(device)
+    ek, dk = codec(shape.rK, 1)
+    ev, dv = codec(shape.rV, 2)
+    mk = mv = None
+    if with_mean:
+        mk = (0.1 * torch.randn(HD, generator=g)).to(device)
+        mv = (0.1 * torch.randn(HD, generator=g)).to(device)
+    return Layer(ck, cv, ek, dk, ev, dv, mk, mv)
+
+
+def history_rows(shape: Shape, centers: torch.Tensor, n: int, seed: int,
+                 device="cpu") -> torch.Tensor:
+    """n structured K or V rows [n, HD] (bf16 values as fp32)."""
+    g = _gen(seed, device)
+    HD = shape.HD
+    basis = orthonormal(64, HD, seed + 7, device)
+    u = torch.randint(0, centers.shape[0], (n,), generator=g, device=device)
+    gcoef = torch.randn(n, 64, generator=g, device=device)
+    decay = torch.arange(1, 65, device=device, dtype=torch.float32).rsqrt()
+    eps = 0.05 * torch.randn(n, HD, generator=g, device=device)
+    rows = centers.to(device).float()[u] + (gcoef * decay) @ basis + eps
+    return rows.to(torch.bfloat16).float()
+
+
+def queries(shape: Shape, seed: int, device="cpu") -> torch.Tensor:
+    """q [B, Q, H, D] bf16 ~ N(0,1)/sqrt(D)."""
+    g = _gen(seed, device)
+    q = torch.randn(shape.B, shape.Q, shape.H, shape.D, generator=g, device=device)
+    return (q / shape.D ** 0.5).to(torch.bfloat16)

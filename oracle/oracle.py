@@ -1,0 +1,353 @@
+"""CPU oracle for NanoKV's codec-native historical attention.
+
+TEST INFRASTRUCTURE ONLY.  This module is the checker the HIP product path is
+compared against.  Only tests/, __graft_entry__.smoke() and the cpu_baseline
+leg of bench.py import it; the product package never imports it and has no
+CPU fallback.
+
+It restates the reference algorithm (paths relative to the NanoKV tree;
+MG = models/Matrix-Game-3.5/fast/diffsynth/models/nanokv_codec.py,
+CN = models/Matrix-Game-3.5/fast/codec_native) in plain C (nkv_oracle.c, for
+the integer/byte and rounding-sensitive steps) and numpy float64 (GEMMs and
+softmax attention).
+
+Pinning (the independent check that fixes each function; see tests/):
+  f32<->bf16/fp16 conversion  exhaustive comparison against torch's own
+                               .to(bfloat16/float16) and numpy float16 over
+                               all bf16 bit patterns and random/edge floats
+                               (tests/test_oracle.py::test_conversions_*)
+  quant_pack                  hand-computed known answers incl. RNE half
+                               ties, zero rows, fp16 overflow/underflow;
+                               brute-force search of the nearest code
+                               (argmin over all 15 codes, ties to even) on
+                               random data; committed golden fixtures
+  pack / unpack_codes         hand-computed bytes; round trip over all codes
+  unpack_latent               torch: codes.float() * scale.float() -> bf16
+                               (MG:429-434) computed by torch, not by the oracle
+  assign                      brute force with exact rational arithmetic
+                               (fractions.Fraction) on small inputs; exact
+                               tie cases; golden fixtures
+  residual_bf16 / project     torch float64 reference of x - c - mean and
+                               the matmul (independent library routine)
+  decode (epilogue)           torch bf16 tensor ops reproducing MG:438-454
+                               (F.linear with bf16 bias, add_ of fp32 gather)
+  attention                   torch.nn.functional.scaled_dot_product_attention
+                               in float64 (library routine), plus the LSE
+                               closed form on tiny inputs
+  merge                       invariant merge(attend(K1), attend(K2)) ==
+                               attend(K1 u K2); closed forms for empty (-inf)
+                               partitions (CN/core.py:33-42)
+  protected_frames            hand-computed policy tables and an exhaustive
+                               comparison with an independent set-based
+                               statement (CN/metadata_cache.py:48-72) for all
+                               small (count, recent, stride, sink)
+  hybrid_attention            identity readers reduce it exactly to the full
+                               decode-then-attend path (CN/reader_tools.py:7-35)
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+import subprocess
+from ctypes import c_int, c_int64, c_void_p
+from pathlib import Path
+from typing import Optional, Sequence
+
+import numpy as np
+
+HERE = Path(__file__).resolve().parent
+LIB_PATH = HERE / "libnkv_oracle.so"
+
+_lib = None
+
+
+def build() -> Path:
+    """Compile nkv_oracle.c with the Makefile next to this file."""
+    subprocess.run(["make", "-s", "-C", str(HERE)], check=True)
+    return LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not LIB_PATH.exists():
+            build()
+        l = ctypes.CDLL(str(LIB_PATH))
+        l.nkvo_quant_pack.argtypes = [c_void_p, c_int64, c_int, c_int, c_int, c_int, c_void_p,
+                                      c_void_p, c_void_p]
+        l.nkvo_unpack_codes.argtypes = [c_void_p, c_int64, c_void_p]
+        l.nkvo_unpack_latent.argtypes = [c_void_p, c_void_p, c_int, c_void_p, c_int64, c_int,
+                                         c_int, c_void_p]
+        l.nkvo_assign.argtypes = [c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p]
+        l.nkvo_residual_bf16.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int,
+                                         c_void_p]
+        l.nkvo_decode_epilogue.argtypes = [c_void_p, c_void_p, c_void_p, c_void_p, c_int64,
+                                           c_int, c_void_p]
+        for name in ("nkvo_round_bf16", "nkvo_round_f16"):
+            getattr(l, name).argtypes = [c_void_p, c_int64, c_void_p]
+        for name in ("nkvo_widen_bf16", "nkvo_widen_f16"):
+            getattr(l, name).argtypes = [c_void_p, c_int64, c_void_p]
+        _lib = l
+    return _lib
+
+
+def _p(a: Optional[np.ndarray]) -> Optional[int]:
+    return None if a is None else a.ctypes.data
+
+
+def _c(a, dtype) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=dtype)
+
+
+SCALE_DTYPES = {"bf16": 0, "fp16": 1}
+QUANT_MODES = {"fp32": 0, "bf16": 1}
+
+
+# ----------------------------------------------------------------- numbers
+def f32_to_bf16(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().nkvo_round_bf16(_p(x), x.size, _p(out))
+    return out
+
+
+def bf16_to_f32(b) -> np.ndarray:
+    b = _c(b, np.uint16)
+    return (b.astype(np.uint32) << 16).view(np.float32)
+
+
+def f32_to_f16(x) -> np.ndarray:
+    x = _c(x, np.float32)
+    out = np.empty(x.shape, np.uint16)
+    lib().nkvo_round_f16(_p(x), x.size, _p(out))
+    return out
+
+
+def f16_to_f32(b) -> np.ndarray:
+    b = _c(b, np.uint16)
+    out = np.empty(b.shape, np.float32)
+    lib().nkvo_widen_f16(_p(b), b.size, _p(out))
+    return out
+
+
+def scale_to_f32(bits, scale_dtype: str) -> np.ndarray:
+    return f16_to_f32(bits) if scale_dtype == "fp16" else bf16_to_f32(bits)
+
+
+# ----------------------------------------------------------------- a4/a5
+def quant_pack(coeff, group: int, scale_dtype: str = "bf16", quant_mode: str = "fp32"):
+    """INT4 quantise + pack (MG:349-351, 282-292; HY kv_codecs.py:237-255).
+
+    Returns (packed uint8 [rows, r/2], scales uint16 bits [rows, r/group],
+    codes int8 [rows, r]).
+    """
+    coeff = _c(coeff, np.float32)
+    r = coeff.shape[-1]
+    rows = coeff.size // r
+    if r % 2 or r % group:
+        raise ValueError("r must be even and divisible by group")
+    packed = np.zeros((rows, r // 2), np.uint8)
+    scales = np.zeros((rows, r // group), np.uint16)
+    codes = np.zeros((rows, r), np.int8)
+    lib().nkvo_quant_pack(_p(coeff), rows, r, group, SCALE_DTYPES[scale_dtype],
+                          QUANT_MODES[quant_mode], _p(packed), _p(scales), _p(codes))
+    lead = coeff.shape[:-1]
+    return (packed.reshape(*lead, r // 2), scales.reshape(*lead, r // group),
+            codes.reshape(*lead, r))
+
+
+def pack_codes(codes) -> np.ndarray:
+    """_pack_int4 (MG:282-292): (c[2j]+7) | (c[2j+1]+7) << 4 over the flat codes."""
+    flat = _c(codes, np.int8).reshape(-1).astype(np.int16) + 7
+    if flat.min(initial=0) < 0 or flat.max(initial=0) >= 16:
+        raise RuntimeError("INT4 codes outside frozen symmetric range [-7,7]")
+    if flat.size % 2:
+        flat = np.concatenate([flat, np.zeros(1, np.int16)])
+    pairs = flat.reshape(-1, 2)
+    return (pairs[:, 0] | (pairs[:, 1] << 4)).astype(np.uint8)
+
+
+def unpack_codes(packed, count: int) -> np.ndarray:
+    """_unpack_int4 (MG:295-298)."""
+    packed = _c(packed, np.uint8).reshape(-1)
+    out = np.empty(count, np.int8)
+    lib().nkvo_unpack_codes(_p(packed), count, _p(out))
+    return out
+
+
+def unpack_latent(packed, scales, r: int, group: int, scale_dtype: str = "bf16",
+                  row_index=None) -> np.ndarray:
+    """bf16(code * stored scale) (MG:426-434; nanokv_codec_kernels.py:11-27)."""
+    packed = _c(packed, np.uint8)
+    scales = _c(scales, np.uint16)
+    idx = None if row_index is None else _c(row_index, np.int32)
+    rows = (packed.size // (r // 2)) if idx is None else idx.size
+    out = np.empty((rows, r), np.uint16)
+    lib().nkvo_unpack_latent(_p(packed), _p(scales), SCALE_DTYPES[scale_dtype], _p(idx), rows,
+                             r, group, _p(out))
+    return out
+
+
+# ----------------------------------------------------------------- a1
+def assign(x, centers_bf16) -> np.ndarray:
+    """argmin_c ||x - c||^2 decided in fp64, first index on ties (MG:315-321)."""
+    x = _c(x, np.float32)
+    centers_bf16 = _c(centers_bf16, np.uint16)
+    hd = x.shape[-1]
+    rows = x.size // hd
+    C = centers_bf16.shape[0]
+    ids = np.empty(rows, np.int32)
+    lib().nkvo_assign(_p(x), _p(centers_bf16), rows, C, hd, _p(ids))
+    return ids.reshape(x.shape[:-1])
+
+
+def residual_bf16(x, centers_bf16, ids, mean) -> np.ndarray:
+    """bf16(x - fp32(center[id]) - mean) (MG:326-330, 346, 138-141)."""
+    x = _c(x, np.float32)
+    hd = x.shape[-1]
+    rows = x.size // hd
+    out = np.empty(x.shape, np.uint16)
+    c = None if centers_bf16 is None else _c(centers_bf16, np.uint16)
+    i = None if ids is None else _c(ids, np.int32)
+    m = None if mean is None else _c(mean, np.float32)
+    lib().nkvo_residual_bf16(_p(x), _p(c), _p(i), _p(m), rows, hd, _p(out))
+    return out
+
+
+def project(rows_bf16, w_bf16) -> np.ndarray:
+    """rows @ w^T with bf16 operands, accumulated in fp64, rounded once to fp32."""
+    a = bf16_to_f32(rows_bf16).astype(np.float64)
+    w = bf16_to_f32(w_bf16).astype(np.float64)
+    return (a @ w.T).astype(np.float32)
+
+
+def encode(x, w_enc_bf16, centers_bf16=None, mean=None, group: int = 32,
+           scale_dtype: str = "bf16", quant_mode: str = "fp32") -> dict:
+    """encode_tensor (MG:333-365) with given shared centers."""
+    x = _c(x, np.float32)
+    ids = None if centers_bf16 is None else assign(x, centers_bf16)
+    res = residual_bf16(x, centers_bf16, ids, mean)
+    coeff = project(res, w_enc_bf16)
+    packed, scales, codes = quant_pack(coeff, group, scale_dtype, quant_mode)
+    return {"packed": packed, "scales": scales, "codes": codes, "ids": ids, "coeff": coeff}
+
+
+# ----------------------------------------------------------------- a7/a8
+def decode(packed, scales, w_dec_bf16, group: int, scale_dtype: str = "bf16", ids=None,
+           centers_bf16=None, mean=None, row_index=None, columns=None) -> np.ndarray:
+    """Full-width decode of one batch item's rows (MG:393-455) -> bf16 bits.
+
+    rows = bf16(bf16(latent @ W^T + bf16(mean)) + center[id]).  The GEMM is
+    accumulated in fp64 and rounded once to fp32.  `columns` (optional index
+    array) restricts the output to those HD columns.
+    """
+    w = _c(w_dec_bf16, np.uint16)
+    r = w.shape[1]
+    latent = unpack_latent(packed, scales, r, group, scale_dtype, row_index)
+    if columns is not None:
+        w = w[np.asarray(columns)]
+    acc = project(latent, w)
+    hd = w.shape[0]
+    cent = None
+    if centers_bf16 is not None:
+        cent = _c(centers_bf16, np.uint16)
+        if columns is not None:
+            cent = np.ascontiguousarray(cent[:, np.asarray(columns)])
+    src_ids = None
+    if ids is not None:
+        src_ids = np.asarray(ids, np.int64)
+        if row_index is not None:
+            src_ids = src_ids[np.asarray(row_index)]
+        src_ids = _c(src_ids, np.int32)
+    m = None
+    if mean is not None:
+        m = _c(mean, np.float32)
+        if columns is not None:
+            m = np.ascontiguousarray(m[np.asarray(columns)])
+    out = np.empty((acc.shape[0], hd), np.uint16)
+    lib().nkvo_decode_epilogue(_p(acc), _p(m), _p(cent), _p(src_ids), acc.shape[0], hd, _p(out))
+    return out
+
+
+# ----------------------------------------------------------------- a10-a12
+def attention(q, k, v, scale: float):
+    """softmax(q k^T * scale) v per head in float64 (wan_video_dit.py:42-82).
+
+    q [H, Q, D], k/v [H, N, D] (float arrays).  Returns (out [H, Q, D] f64,
+    lse [H, Q] natural log).  An empty key set gives (0, -inf) as
+    attention_lse does (CN/core.py:48-49).
+    """
+    q = np.asarray(q, np.float64)
+    k = np.asarray(k, np.float64)
+    v = np.asarray(v, np.float64)
+    H, Qn, _ = q.shape
+    if k.shape[1] == 0:
+        return np.zeros((H, Qn, v.shape[2])), np.full((H, Qn), -np.inf)
+    s = np.einsum("hqd,hkd->hqk", q, k) * scale
+    m = s.max(-1, keepdims=True)
+    e = np.exp(s - m)
+    l = e.sum(-1, keepdims=True)
+    out = np.einsum("hqk,hkd->hqd", e / l, v)
+    return out, (m + np.log(l))[..., 0]
+
+
+def merge(out_a, lse_a, out_b, lse_b):
+    """LSE merge (CN/core.py:33-42)."""
+    lse_a = np.asarray(lse_a, np.float64)
+    lse_b = np.asarray(lse_b, np.float64)
+    lse = np.logaddexp(lse_a, lse_b)
+    origin = np.where(np.isfinite(lse), lse, 0.0)
+    wa = np.exp(lse_a - origin)
+    wb = np.exp(lse_b - origin)
+    out = np.asarray(out_a, np.float64) * wa[..., None] + np.asarray(out_b, np.float64) * wb[..., None]
+    return out, lse
+
+
+def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Optional[dict],
+                  scale: float, heads: Optional[Sequence[int]] = None, D: int = 128):
+    """Reference decode-then-SDPA path for one batch item.
+
+    q [Q, H, D] bf16 bits; k_cur/v_cur [Nc, H, D] bf16 bits or None; key/value
+    are dicts with the decode() keyword arguments (packed, scales, w_dec_bf16,
+    group, scale_dtype, ids, centers_bf16, mean) or None.  Returns
+    (out [Q, H', D] f64, lse [H', Q]) for the selected heads.
+    """
+    q = bf16_to_f32(q_bf16)
+    Qn, H = q.shape[0], q.shape[1]
+    heads = list(range(H)) if heads is None else list(heads)
+    cols = np.concatenate([np.arange(h * D, (h + 1) * D) for h in heads])
+    ks, vs = [], []
+    if key is not None:
+        kd = bf16_to_f32(decode(**key, columns=cols))
+        vd = bf16_to_f32(decode(**value, columns=cols))
+        ks.append(kd.reshape(-1, len(heads), D))
+        vs.append(vd.reshape(-1, len(heads), D))
+    if k_cur_bf16 is not None:
+        ks.append(bf16_to_f32(k_cur_bf16)[:, heads])
+        vs.append(bf16_to_f32(v_cur_bf16)[:, heads])
+    if ks:
+        k = np.concatenate(ks, 0).transpose(1, 0, 2)
+        v = np.concatenate(vs, 0).transpose(1, 0, 2)
+    else:
+        k = np.zeros((len(heads), 0, D))
+        v = np.zeros((len(heads), 0, D))
+    out, lse = attention(q[:, heads].transpose(1, 0, 2), k, v, scale)
+    return out.transpose(1, 0, 2), lse
+
+
+# ----------------------------------------------------------------- a13
+def protected_frames(count: int, recent: int, stride: int, sink: int = 0) -> np.ndarray:
+    """Frame-level protection mask (CN/core.py:140-152, metadata_cache.py:64-68).
+
+    Last `recent` frames, the first `sink` frames and every `stride`-th frame
+    counting back from the newest unprotected one are kept at full width.
+    """
+    if min(recent, stride, sink) < 0:
+        raise ValueError("Negative protection policy")
+    keep = np.zeros(count, bool)
+    old = max(0, count - recent)
+    keep[old:] = True
+    keep[:min(sink, count)] = True
+    if stride and old:
+        keep[np.arange(old - 1, -1, -stride)] = True
+    return keep

@@ -1,0 +1,108 @@
+"""Shared builders for the parity tests: one seeded scenario, two views of it
+(device tensors for the HIP path, numpy arrays for the CPU oracle)."""
+from __future__ import annotations
+
+import numpy as np
+import torch
+
+from nanokv_amd import synth
+
+
+def u16(t: torch.Tensor) -> np.ndarray:
+    """bf16/fp16 tensor -> numpy uint16 bit patterns (host copy)."""
+    return t.detach().contiguous().cpu().view(torch.int16).numpy().view(np.uint16)
+
+
+def from_u16(a: np.ndarray, dtype=torch.bfloat16, device="cpu") -> torch.Tensor:
+    return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(dtype).to(device)
+
+
+def scale_name(dtype: torch.dtype) -> str:
+    return "fp16" if dtype == torch.float16 else "bf16"
+
+
+def max_abs_cos(a, b):
+    a = np.asarray(a, np.float64).ravel()
+    b = np.asarray(b, np.float64).ravel()
+    diff = float(np.abs(a - b).max()) if a.size else 0.0
+    na, nb = np.linalg.norm(a), np.linalg.norm(b)
+    cos = float(a @ b / (na * nb)) if na > 0 and nb > 0 else (1.0 if na == nb else 0.0)
+    return diff, cos
+
+
+class Scenario:
+    """A seeded decode+attend problem encoded by the oracle (so the history
+    payload is identical for both sides)."""
+
+    def __init__(self, *, B=1, H=2, D=128, N=200, Q=100, Nc=64, rK=384, rV=256, G=32, C=16,
+                 scale_dtype=torch.float16, with_mean=False, id_dtype=torch.uint8,
+                 centers=True, seed=0):
+        import oracle.oracle as orc
+        self.shape = synth.Shape("test", H=H, D=D, N=N, Q=Q, Nc=Nc, rK=rK, rV=rV, G=G, C=max(C, 1),
+                                 scale_dtype=scale_dtype, B=B)
+        sh = self.shape
+        layer = synth.make_layer(sh, seed=seed, with_mean=with_mean)
+        self.layer = layer
+        self.B, self.H, self.D, self.N, self.Q, self.Nc = B, H, D, N, Q, Nc
+        self.G, self.scale_dtype, self.id_dtype = G, scale_dtype, id_dtype
+        sname = scale_name(scale_dtype)
+        self.hist = []
+        for b in range(B):
+            item = {}
+            for kind, cent, enc, dec, mean in (
+                    ("k", layer.centers_k, layer.w_enc_k, layer.w_dec_k, layer.mean_k),
+                    ("v", layer.centers_v, layer.w_enc_v, layer.w_dec_v, layer.mean_v)):
+                rows = synth.history_rows(sh, cent, N, seed=seed * 100 + b * 10 + (kind == "v"))
+                e = orc.encode(rows.numpy(), u16(layer.w_enc_k if kind == "k" else layer.w_enc_v),
+                               u16(cent) if centers else None,
+                               None if mean is None else mean.numpy(), G, sname, "fp32")
+                item[kind] = {
+                    "packed": e["packed"], "scales": e["scales"],
+                    "w_dec_bf16": u16(dec), "group": G, "scale_dtype": sname,
+                    "ids": e["ids"] if centers else None,
+                    "centers_bf16": u16(cent) if centers else None,
+                    "mean": None if mean is None else mean.numpy(),
+                }
+            self.hist.append(item)
+        g = torch.Generator().manual_seed(seed + 12345)
+        self.q = (torch.randn(B, Q, H, D, generator=g) / D ** 0.5).to(torch.bfloat16)
+        if Nc:
+            kc = [synth.history_rows(sh, layer.centers_k, Nc, seed=seed * 7 + 1000 + b) for b in range(B)]
+            vc = [synth.history_rows(sh, layer.centers_v, Nc, seed=seed * 7 + 2000 + b) for b in range(B)]
+            self.k_cur = torch.stack(kc).reshape(B, Nc, H, D).to(torch.bfloat16)
+            self.v_cur = torch.stack(vc).reshape(B, Nc, H, D).to(torch.bfloat16)
+        else:
+            self.k_cur = self.v_cur = None
+        self.scale = D ** -0.5
+
+    # ---- device side
+    def codecs(self, device):
+        from nanokv_amd import ops
+        if self.N == 0:
+            return None, None
+        out = []
+        for kind in ("k", "v"):
+            items = [self.hist[b][kind] for b in range(self.B)]
+            packed = torch.from_numpy(np.stack([it["packed"] for it in items])).to(device)
+            scales = from_u16(np.stack([it["scales"] for it in items]), self.scale_dtype, device)
+            w_dec = from_u16(items[0]["w_dec_bf16"], torch.bfloat16, device)
+            ids = centers = mean = None
+            if items[0]["ids"] is not None:
+                ids = torch.from_numpy(np.stack([it["ids"] for it in items]).astype(np.int64))
+                ids = ids.to(self.id_dtype).to(device)
+                centers = from_u16(items[0]["centers_bf16"], torch.bfloat16, device)[None]
+            if items[0]["mean"] is not None:
+                mean = torch.from_numpy(items[0]["mean"]).to(device)
+            out.append(ops.Codec(packed=packed, scales=scales, w_dec=w_dec, group=self.G,
+                                 ids=ids, centers=centers, mean=mean))
+        return out[0], out[1]
+
+    # ---- oracle side
+    def reference(self, b, heads=None):
+        import oracle.oracle as orc
+        key = self.hist[b]["k"] if self.N else None
+        val = self.hist[b]["v"] if self.N else None
+        kc = u16(self.k_cur[b]) if self.Nc else None
+        vc = u16(self.v_cur[b]) if self.Nc else None
+        return orc.decode_attend(u16(self.q[b]), kc, vc, key, val, self.scale, heads=heads,
+                                 D=self.D)

@@ -1,0 +1,148 @@
+"""GPU parity of the codec kernels against the CPU oracle (bit-exact where the
+contract is integer/byte work: INT4 codes, scales, center ids, unpacked
+latents)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle.oracle as orc
+from nanokv_amd import ops, synth
+from tests._helpers import from_u16, scale_name, u16
+
+pytestmark = pytest.mark.gpu
+
+
+def _coeff(rows, r, seed, kind="normal"):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(rows, r, generator=g)
+    if kind == "mixed":
+        x = x * torch.exp(2 * torch.randn(rows, 1, generator=g))
+        x[::7] = 0.0                      # all-zero rows: scale = eps / 7
+        x[1::11] *= 1e-30                 # fp16 scale underflow
+        x[2::13] *= 1e6                   # fp16 scale overflow (inf)
+    return x.float().contiguous()
+
+
+@pytest.mark.parametrize("r,group", [(384, 32), (384, 384), (256, 64), (64, 32), (40, 8)])
+@pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("quant_mode", ["fp32", "bf16"])
+def test_quant_pack_bit_exact(dev, r, group, scale_dtype, quant_mode):
+    for seed, kind in ((1, "normal"), (2, "mixed")):
+        x = _coeff(333, r, seed, kind)
+        packed, scales = ops.quant_pack(x.to(dev), group, scale_dtype, quant_mode)
+        rp, rs, _ = orc.quant_pack(x.numpy(), group, scale_name(scale_dtype), quant_mode)
+        assert np.array_equal(packed.cpu().numpy(), rp), (seed, kind)
+        assert np.array_equal(u16(scales), rs), (seed, kind)
+
+
+def test_quant_pack_half_ties(dev):
+    # x / s lands exactly on k + 0.5: s = 7/7 = 1 when the row amax is 7.
+    vals = np.array([7.0, 0.5, 1.5, 2.5, -0.5, -1.5, -2.5, 6.5, -6.5, 3.5, 4.5, 5.5, -7.0, 0.0,
+                     0.49999997, 1.0000001] + [0.0] * 16, np.float32)[None]
+    x = torch.from_numpy(vals)
+    packed, scales = ops.quant_pack(x.to(dev), 32, torch.bfloat16, "fp32")
+    rp, rs, codes = orc.quant_pack(vals, 32, "bf16", "fp32")
+    assert np.array_equal(packed.cpu().numpy(), rp)
+    assert np.array_equal(u16(scales), rs)
+    assert list(codes[0, :14]) == [7, 0, 2, 2, 0, -2, -2, 6, -6, 4, 4, 6, -7, 0]
+
+
+def test_quant_pack_empty(dev):
+    x = torch.zeros(0, 64, device=dev)
+    packed, scales = ops.quant_pack(x, 32)
+    assert packed.shape == (0, 32) and scales.shape == (0, 2)
+
+
+@pytest.mark.parametrize("scale_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("r,group", [(384, 32), (384, 384), (256, 32)])
+def test_unpack_bit_exact(dev, scale_dtype, r, group):
+    g = torch.Generator().manual_seed(5)
+    rows = 517
+    packed = torch.randint(0, 256, (rows, r // 2), generator=g, dtype=torch.uint8)
+    scales = (torch.rand(rows, r // group, generator=g) * 3).to(scale_dtype)
+    out = ops.unpack(packed.to(dev), scales.to(dev), r, group)
+    ref = orc.unpack_latent(packed.numpy(), u16(scales), r, group, scale_name(scale_dtype))
+    assert np.array_equal(u16(out), ref)
+    idx = torch.tensor([0, 5, 516, 5, 100], dtype=torch.int32)
+    out = ops.unpack(packed.to(dev), scales.to(dev), r, group, row_index=idx.to(dev))
+    ref = orc.unpack_latent(packed.numpy(), u16(scales), r, group, scale_name(scale_dtype),
+                            row_index=idx.numpy())
+    assert np.array_equal(u16(out), ref)
+
+
+@pytest.mark.parametrize("C,id_dtype", [(16, torch.uint8), (256, torch.uint8),
+                                         (300, torch.int16), (70, torch.int32)])
+def test_assign_bit_exact(dev, C, id_dtype):
+    shape = synth.Shape("t", H=4, D=128, N=0, Q=0, Nc=0, rK=64, rV=64, G=32, C=C)
+    layer = synth.make_layer(shape, seed=3)
+    x = synth.history_rows(shape, layer.centers_k, 777, seed=9)
+    ids = ops.assign(x.to(dev), layer.centers_k.to(dev), id_dtype)
+    ref = orc.assign(x.numpy(), u16(layer.centers_k))
+    got = ids.cpu().to(torch.int64).numpy()
+    if id_dtype == torch.int16:
+        got = got & 0xFFFF
+    assert np.array_equal(got, ref)
+
+
+def test_assign_exact_ties(dev):
+    # duplicated centers and rows exactly midway between two centers: the
+    # first index must win (torch.argmin semantics, MG:320).
+    HD = 64
+    c = np.zeros((6, HD), np.float32)
+    c[0, 0], c[1, 0], c[2, 0] = 1.0, 1.0, -1.0   # 0 and 1 duplicate
+    c[3, 1], c[4, 1], c[5, 2] = 2.0, -2.0, 4.0
+    centers = torch.from_numpy(c).to(torch.bfloat16)
+    x = np.zeros((5, HD), np.float32)
+    x[1, 0] = 0.5          # nearer 0/1 (tie -> 0)
+    x[2, 1] = 0.0          # equidistant from 0,1,2 (all at distance 1) -> 0
+    x[3, 1], x[3, 0] = 0.0, -0.5   # nearest 2
+    x[4, 2] = 2.0          # equidistant from 5 (dist 4) and ... check oracle decides
+    ids = ops.assign(torch.from_numpy(x).to(dev), centers.to(dev), torch.int32)
+    ref = orc.assign(x, u16(centers))
+    assert np.array_equal(ids.cpu().numpy(), ref)
+    assert ref[1] == 0 and ref[2] == 0 and ref[3] == 2
+
+
+@pytest.mark.parametrize("group,scale_dtype,quant_mode,with_mean",
+                         [(32, torch.float16, "fp32", False), (384, torch.bfloat16, "fp32", True),
+                          (32, torch.bfloat16, "bf16", True)])
+def test_encode_parity(dev, group, scale_dtype, quant_mode, with_mean):
+    shape = synth.Shape("t", H=4, D=128, N=0, Q=0, Nc=0, rK=384, rV=384, G=group, C=64)
+    layer = synth.make_layer(shape, seed=4, with_mean=with_mean)
+    x = synth.history_rows(shape, layer.centers_k, 300, seed=11)
+    mean = layer.mean_k
+    got = ops.encode(x.to(dev), layer.w_enc_k.to(dev), centers=layer.centers_k.to(dev),
+                     mean=None if mean is None else mean.to(dev), group=group,
+                     scale_dtype=scale_dtype, quant_mode=quant_mode)
+    ref = orc.encode(x.numpy(), u16(layer.w_enc_k), u16(layer.centers_k),
+                     None if mean is None else mean.numpy(), group, scale_name(scale_dtype),
+                     quant_mode)
+    # center ids: bit-exact
+    assert np.array_equal(got["ids"].cpu().numpy().astype(np.int64), ref["ids"])
+    # projection: fp32 GEMM vs fp64-accumulated oracle
+    coeff = got["coeff"].cpu().numpy()
+    np.testing.assert_allclose(coeff, ref["coeff"], rtol=2e-5, atol=2e-5)
+    # codes and scales are bit-exact given the identical fp32 projected input
+    rp, rs, _ = orc.quant_pack(coeff, group, scale_name(scale_dtype), quant_mode)
+    assert np.array_equal(got["packed"].cpu().numpy(), rp)
+    assert np.array_equal(u16(got["scales"]), rs)
+
+
+@pytest.mark.parametrize("with_mean,id_dtype", [(False, torch.uint8), (True, torch.int16)])
+def test_decode_parity(dev, with_mean, id_dtype):
+    from tests._helpers import Scenario
+    sc = Scenario(B=2, H=2, N=150, Q=1, Nc=0, rK=384, rV=256, G=32, C=20, with_mean=with_mean,
+                  id_dtype=id_dtype)
+    key, value = sc.codecs(dev)
+    for codec, kind in ((key, "k"), (value, "v")):
+        out = ops.decode(codec, sc.H * sc.D)
+        for b in range(sc.B):
+            ref = orc.bf16_to_f32(orc.decode(**sc.hist[b][kind]))
+            got = out[b].float().cpu().numpy()
+            # fp32 accumulation order differs from the oracle; each of the two bf16
+            # roundings (GEMM+bias, +center) may land one ulp apart.  The first ulp is
+            # relative to the pre-center value (O(1) here), hence the absolute term.
+            np.testing.assert_allclose(got, ref, rtol=2 ** -7, atol=2 ** -7)
+        idx = torch.tensor([3, 0, 149, 77], dtype=torch.int32, device=dev)
+        sel = ops.decode(codec, sc.H * sc.D, row_index=idx)
+        np.testing.assert_array_equal(u16(sel), u16(out[:, idx.long().cpu()]))
