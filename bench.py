@@ -1,0 +1,216 @@
+#!/usr/bin/env python3
+"""Benchmark of NanoKV's fused codec attention on one MI355X.
+
+One step = one fused decode+attention call (nkv_attend) of BASELINE config 1:
+H=24, D=128, 12,480 INT4-compressed history tokens (r=384, group-32 fp16
+scales, 256 shared centers), 1,560 queries and 1,560 uncompressed current
+K/V tokens, bf16, non-causal.  Inputs are synthetic (nanokv_amd.synth) and
+resident in HBM before the timed region starts.
+
+Prints ONE JSON line:
+  value         algorithmic TFLOP/s over the timed steps (decode GEMM
+                counted once per history token)
+  roofline      the fused kernel's achieved TFLOP/s from HIP events recorded
+                around each launch, against the 2.5 PFLOP/s dense bf16 peak
+  cpu_baseline  the CPU oracle's decode-then-attend (fp32 numpy/BLAS) on a
+                bounded head sample of the same workload, scaled to TFLOP/s
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+if str(ROOT) not in sys.path:
+    sys.path.insert(0, str(ROOT))
+
+PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0
+TRAFFIC_FILE = ROOT / "profiles" / "attend_kernel_traffic.json"
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2))
+    ap.add_argument("--splits", type=int, default=0, help="history splits (0 = automatic)")
+    ap.add_argument("--cpu-seconds", type=float, default=15.0,
+                    help="time budget of the CPU-baseline head sample")
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--profile-kernel", action="store_true",
+                    help="no timing: run a known-size copy and a few fused calls (for rocprofv3 --pmc)")
+    return ap.parse_args()
+
+
+def build_inputs(shape, device, seed=0):
+    """Synthetic config inputs, encoded on the GPU by the product encoder."""
+    import torch
+    from nanokv_amd import ops, synth
+    layer = synth.make_layer(shape, seed=seed, device=device)
+    codecs = []
+    for kind, cent, enc, dec in (("k", layer.centers_k, layer.w_enc_k, layer.w_dec_k),
+                                 ("v", layer.centers_v, layer.w_enc_v, layer.w_dec_v)):
+        rows = synth.history_rows(shape, cent, shape.N, seed=seed * 10 + 1 + (kind == "v"),
+                                  device=device)
+        e = ops.encode(rows, enc, centers=cent, group=shape.G, scale_dtype=shape.scale_dtype)
+        del rows
+        codecs.append(ops.Codec(packed=e["packed"][None], scales=e["scales"][None], w_dec=dec,
+                                group=shape.G, ids=e["ids"][None], centers=cent[None]))
+    q = synth.queries(shape, seed=seed * 10 + 3, device=device)
+    kc = synth.history_rows(shape, layer.centers_k, shape.Nc, seed=seed * 10 + 4, device=device)
+    vc = synth.history_rows(shape, layer.centers_v, shape.Nc, seed=seed * 10 + 5, device=device)
+    kc = kc.reshape(1, shape.Nc, shape.H, shape.D).to(torch.bfloat16)
+    vc = vc.reshape(1, shape.Nc, shape.H, shape.D).to(torch.bfloat16)
+    torch.cuda.synchronize()
+    return layer, codecs, q, kc, vc
+
+
+def cpu_baseline(shape, layer, codecs, q, kc, vc, budget_s: float) -> dict:
+    """Time the CPU oracle (decode-then-attend, fp32 BLAS) on a head sample."""
+    import numpy as np
+    import oracle.oracle as orc
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+
+    def u16(t):
+        return t.detach().contiguous().cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+
+    key = {"packed": codecs[0].packed[0].cpu().numpy(), "scales": u16(codecs[0].scales[0]),
+           "w_dec_bf16": u16(layer.w_dec_k), "group": shape.G, "scale_dtype": "fp16",
+           "ids": codecs[0].ids[0].cpu().numpy().astype(np.int64),
+           "centers_bf16": u16(layer.centers_k)}
+    val = {"packed": codecs[1].packed[0].cpu().numpy(), "scales": u16(codecs[1].scales[0]),
+           "w_dec_bf16": u16(layer.w_dec_v), "group": shape.G, "scale_dtype": "fp16",
+           "ids": codecs[1].ids[0].cpu().numpy().astype(np.int64),
+           "centers_bf16": u16(layer.centers_v)}
+    qn, kn, vn = u16(q[0]), u16(kc[0]), u16(vc[0])
+    orc.decode_attend(qn, kn, vn, key, val, shape.D ** -0.5, heads=[0], D=shape.D,
+                      dtype=np.float32)  # warm-up (BLAS threads, page-in)
+    heads_done, elapsed = 0, 0.0
+    while heads_done < shape.H and elapsed < budget_s:
+        h = heads_done
+        t0 = time.perf_counter()
+        orc.decode_attend(qn, kn, vn, key, val, shape.D ** -0.5, heads=[h], D=shape.D,
+                          dtype=np.float32)
+        elapsed += time.perf_counter() - t0
+        heads_done += 1
+    per_head = elapsed / heads_done
+    full_s = per_head * shape.H
+    flops = shape.flops()["total"]
+    return {"value": round(flops / full_s / 1e12, 4), "unit": "TFLOP/s", "cores": int(threads),
+            "kind": "port",
+            "sample": (f"oracle decode-then-attend (fp32 numpy/BLAS) of {heads_done} of {shape.H} "
+                       f"heads at the full config shape, {elapsed:.1f} s, scaled by "
+                       f"{shape.H}/{heads_done} heads; ms_per_layer={full_s * 1e3:.1f}")}
+
+
+def main():
+    args = parse()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; --gpus must be 1",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+
+    import torch
+    from nanokv_amd import ops, synth
+    device = torch.device("cuda:0")
+    shape = synth.CONFIGS[args.config]
+    layer, codecs, q, kc, vc = build_inputs(shape, device)
+    out = torch.empty_like(q)
+    ws_bytes = ops.attend_workspace_size(q, shape.N, shape.Nc, codecs[0], codecs[1], args.splits)
+    ws = torch.empty(max(ws_bytes, 1), device=device, dtype=torch.uint8)
+
+    def step(events=None):
+        return ops.attend(q, kc, vc, codecs[0], codecs[1], out=out, splits=args.splits,
+                          return_lse=False, workspace=ws, kernel_events=events)
+
+    if args.profile_kernel:
+        # A plain copy of known size (for FETCH_SIZE/WRITE_SIZE calibration), then the kernel.
+        src = torch.empty(256 * 2 ** 20, device=device, dtype=torch.uint8).fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        for _ in range(3):
+            step()
+        torch.cuda.synchronize()
+        print(json.dumps({"profile_kernel": True, "copy_bytes": src.numel(),
+                          "config": shape.name}), flush=True)
+        return
+
+    # per-step HIP events around the fused kernel, recorded by the library on
+    # the stream it launches on (torch's current stream)
+    evs = []
+    for _ in range(args.steps):
+        b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        b.record()
+        e.record()  # materialise the underlying hipEvent_t
+        evs.append((b, e))
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(args.steps):
+        step((evs[i][0].cuda_event, evs[i][1].cuda_event))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    kernel_ms = [b.elapsed_time(e) for b, e in evs]
+    kavg_ms = sum(kernel_ms) / len(kernel_ms)
+
+    fl = shape.flops()
+    ms_per_step = wall * 1e3 / args.steps
+    value = fl["total"] / (ms_per_step * 1e-3) / 1e12
+    achieved = fl["total"] / (kavg_ms * 1e-3) / 1e12
+    traffic = None
+    if TRAFFIC_FILE.exists():
+        try:
+            tr = json.loads(TRAFFIC_FILE.read_text())
+            if tr.get("config") == shape.name:
+                traffic = tr.get("hbm_bytes_per_launch")
+        except Exception:
+            traffic = None
+    from nanokv_amd import _lib
+    result = {
+        "metric": "fused codec-attention TFLOP/s + history tokens/ms (bf16, 12.5k-token history)",
+        "value": round(value, 3),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_per_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (seeded structured history, random-init codec operators)",
+        "config": {"workload": shape.name, "config_index": args.config, "H": shape.H,
+                   "D": shape.D, "history_tokens": shape.N, "query_tokens": shape.Q,
+                   "current_tokens": shape.Nc, "rank_k": shape.rK, "rank_v": shape.rV,
+                   "scale_group": shape.G, "scale_dtype": "fp16", "centers": shape.C,
+                   "parallelism": "single-gpu"},
+        "history_tokens_per_ms": round(shape.N / ms_per_step, 1),
+        "coeff_stream_GBps": round(shape.coeff_stream_bytes() / (kavg_ms * 1e-3) / 1e9, 2),
+        "algorithmic_flops": fl,
+        "roofline": {"bound": "mfma", "kernel": "nkv::attend_kernel",
+                     "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
+                     "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
+                     "traffic": traffic, "kernel_ms_avg": round(kavg_ms, 4)},
+    }
+    if not args.no_cpu_baseline:
+        result["cpu_baseline"] = cpu_baseline(shape, layer, codecs, q, kc, vc, args.cpu_seconds)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -203,6 +203,11 @@ typedef struct nkv_attend_args {
     uint16_t* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
+    /* Optional instrumentation: hipEvent_t handles (as void*) recorded on
+     * `stream` immediately before and after the main fused kernel (not the
+     * split-combine kernel), for per-kernel timing.  NULL = not recorded. */
+    void* ev_kernel_begin;
+    void* ev_kernel_end;
 } nkv_attend_args;
 
 /* Bytes of workspace nkv_attend needs for these arguments (0 if none). */

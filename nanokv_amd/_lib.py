@@ -69,7 +69,7 @@ class NkvAttendArgs(Structure):
         ("v_cur", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),
         ("key", NkvCodec), ("value", NkvCodec),
         ("out", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64),
-        ("lse", c_void_p),
+        ("lse", c_void_p), ("ev_kernel_begin", c_void_p), ("ev_kernel_end", c_void_p),
     ]
 
 

@@ -25,7 +25,9 @@ ARCH = "gfx950"
 SOURCES = {
     "nkv_abi.hip": [],
     "nkv_codec.hip": ["-ffp-contract=off"],
-    "nkv_attend.hip": [],
+    # MFMA accumulators in VGPRs: the fused kernel's softmax/rescale VALU work
+    # runs on them every tile, and its read-only decoder fragments fill AGPRs
+    "nkv_attend.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 COMMON = [

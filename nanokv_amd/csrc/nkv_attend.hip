@@ -1,19 +1,30 @@
 // nkv_attend.hip -- fused INT4-codec decode + flash attention for gfx950.
 //
-// One 256-thread block (4 waves, one per SIMD) owns one (batch, head) pair,
-// a tile of 256 queries (64 per wave) and a contiguous range of 64-token key
-// tiles (a "split").  Per history tile it
-//   1. streams the packed INT4 K and V coefficients with 16-byte loads and
-//      unpacks them (code * scale -> bf16) into LDS,
-//   2. decodes the tile on MFMA: K^T = W_K,h * Z_K^T and V = Z_V * W_V,h^T
-//      (v_mfma_f32_32x32x16_bf16, fp32 accumulate), applies the reference
-//      epilogue bf16(bf16(acc + bf16(mean)) + center[id]) and writes the
-//      bf16 K and V^T tiles to LDS,
-//   3. runs one online-softmax step: S^T = K * Q^T, P = exp2(S*c - m),
-//      O^T += V^T * P^T, all on MFMA.
-// Current-chunk tiles (uncompressed bf16) skip steps 1-2.  Decoded K/V only
-// ever exist in LDS.  With more than one split the per-split partials
-// (O, m, l) go to the caller's workspace and a combine kernel merges them.
+// One 256-thread block (4 waves, one per SIMD, each with the full 512-entry
+// VGPR+AGPR budget) owns one (batch, head) pair, a tile of up to 256 queries
+// (64 per wave) and a contiguous range of 32-token key tiles (a "split").
+//
+// Decoder weights are register-stationary: wave w keeps 64 rows of its
+// codec's decoder slice, W[h*128 + 64*(w&1) + [0,64), 0:r) of the K codec
+// (waves 0-1) or the V codec (waves 2-3), as MFMA operand fragments for the
+// whole kernel (192 registers at r = 384; gfx950 MFMAs read A/B from AGPRs).
+// Per history tile p two barrier-separated phases run:
+//   A: decode -- K^T = W_K * Z_K^T and V^T = W_V * Z_V^T on MFMA
+//      (v_mfma_f32_32x32x16_bf16, fp32 accumulate) from the unpacked codes
+//      in LDS, then the reference epilogue bf16(bf16(acc + bf16(mean)) +
+//      center[id]) into the bf16 K[token][d] and V^T[d][token] tiles in LDS
+//      (the center rows are loaded at the start of the phase, behind the
+//      MFMAs);
+//   B: attention -- S^T = K * Q^T, P = exp2(S*c - m), O^T += V^T * P^T on
+//      MFMA -- with the 16-byte global loads of tile p+1's packed codes
+//      issued first and their unpack (code * scale -> bf16) into LDS last.
+// Accumulators are kept in VGPRs (-mllvm -amdgpu-mfma-vgpr-form) so the
+// softmax and rescale work on them directly; the read-only decoder
+// fragments then live in AGPRs.
+// Current-chunk tiles (uncompressed bf16) are copied into the K/V tiles
+// instead, prefetched a tile ahead.  Decoded K/V never leave LDS.  With more
+// than one split the per-split partials (O, m, l) go to the caller's
+// workspace and a combine kernel merges them.
 //
 // MFMA 32x32x16 bf16 operand layout (wave64): lane l supplies row (l % 32)
 // of A and column (l % 32) of B with k = 8 * (l / 32) + [0, 8); accumulator
@@ -25,29 +36,29 @@
 namespace nkv {
 
 constexpr int AT_D = 128;                     // head dim
-constexpr int AT_BN = 64;                     // keys per tile
-constexpr int AT_WAVES = 4;
+constexpr int AT_BN = 32;                     // keys per tile
+constexpr int AT_THREADS = 256;
 constexpr int AT_QB = 2;                      // 32-query blocks per wave
-constexpr int AT_BM = AT_WAVES * AT_QB * 32;  // 256 queries per block
+constexpr int AT_BM = 4 * AT_QB * 32;         // at most 256 queries per block
 constexpr int AT_RMAX = 384;
+constexpr int AT_KSTEPS = AT_RMAX / 16;       // MFMA k-steps of the decode
 constexpr int AT_ZPAD = 8;
 constexpr int AT_KPAD = 8;
 constexpr int AT_VPAD = 4;
+constexpr int AT_ITEMS = 3;  // unpack items per thread: (rK + rV) / 256 <= 3
+constexpr int AT_CITEMS = AT_BN * (AT_D / 8) * 2 / AT_THREADS;  // current-tile 16B chunks
 
 struct AttendSmem {
-    uint16_t zk[AT_BN][AT_RMAX + AT_ZPAD];  // unpacked K coefficients
-    uint16_t zv[AT_BN][AT_RMAX + AT_ZPAD];  // unpacked V coefficients
-    uint16_t ks[AT_BN][AT_D + AT_KPAD];     // decoded K tile [token][d]
-    uint16_t vt[AT_D][AT_BN + AT_VPAD];     // decoded V tile, transposed [d][token]
-    int ids_k[AT_BN];
-    int ids_v[AT_BN];
-    float bias_k[AT_D];
-    float bias_v[AT_D];
+    uint16_t z[2][AT_BN][AT_RMAX + AT_ZPAD];  // unpacked K (0) and V (1) coefficients
+    uint16_t ks[AT_BN][AT_D + AT_KPAD];       // K tile [token][d]
+    uint16_t vt[AT_D][AT_BN + AT_VPAD];       // V tile, transposed [d][token]
+    uint16_t qs[AT_BM][AT_D + AT_KPAD];       // this block's queries [q][d]
+    float bias[2][AT_D];
 };
 
 struct AttendParams {
     int B, H, S;          // S = splits
-    int q_tiles;
+    int q_tiles, q_per_tile;
     int64_t Q, N, Nc;
     int t_hist, t_total;  // key tiles (history, all)
     float scale_log2;     // softmax_scale * log2(e)
@@ -58,7 +69,7 @@ struct AttendParams {
     int64_t k_sb, k_st, k_sh;
     const uint16_t* v_cur;
     int64_t v_sb, v_st, v_sh;
-    nkv_codec key, value;
+    nkv_codec codec[2];   // K, V
     uint16_t* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
@@ -90,167 +101,342 @@ __device__ __forceinline__ bf16x8 lds_2x64(const uint16_t* p) {
     return as_bf16x8(v);
 }
 
-// Unpack AT_BN rows of one codec (batch-item base pointers) into LDS; rows
-// >= valid become zero.  One work item = 32 codes = 16 packed bytes and one
-// scale (the fused kernel requires group % 32 == 0).  Also stages center ids.
-__device__ __forceinline__ void unpack_tile(uint16_t (*z)[AT_RMAX + AT_ZPAD], int* ids_s,
-                                            const uint8_t* packed, const uint16_t* scales,
-                                            const void* ids, const nkv_codec& c, int64_t tok0,
-                                            int valid, int t) {
-    const int per_row = c.r / 32;
-    const int items = AT_BN * per_row;
-    const int ngroups = c.r / c.group;
-    for (int it = t; it < items; it += 256) {
-        const int row = it / per_row;
-        const int j = it - row * per_row;
-        u32x4 o[4] = {{0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}, {0, 0, 0, 0}};
-        if (row < valid) {
-            const int64_t tok = tok0 + row;
-            const u32x4 w = *reinterpret_cast<const u32x4*>(packed + tok * (c.r / 2) + j * 16);
-            const float s = scale_bits_to_f32(scales[tok * ngroups + (j * 32) / c.group],
-                                              c.scale_dtype);
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Packed-code streaming.  Thread t owns the work items it = t + 256*e
+// (e < AT_ITEMS) of every tile: item it < rK covers 32 K codes (16 bytes,
+// one scale) of row it / (rK/32); items rK .. rK+rV-1 cover V.  The item ->
+// (codec, row, j) map does not depend on the tile, so it is computed once
+// and packed into one register per item; per-codec values are
+// kernel-uniform scalars selected per lane (no runtime indexing of the
+// argument struct).
+struct Streamer {
+    const uint8_t* packed0;
+    const uint8_t* packed1;
+    const uint16_t* scales0;
+    const uint16_t* scales1;
+    int rowb0, rowb1;    // packed bytes per token (r / 2)
+    int ng0, ng1;        // scale groups per token
+    int grp0, grp1;      // scale group width
+    int fp16_0, fp16_1;  // scale dtype is fp16
+    int item[AT_ITEMS];  // row | j << 5 | codec << 9, or -1
+};
+
+__device__ __forceinline__ Streamer make_streamer(const nkv_codec& k, const nkv_codec& v,
+                                                  const uint8_t* pk, const uint16_t* sk,
+                                                  const uint8_t* pv, const uint16_t* sv, int t) {
+    Streamer st;
+    st.packed0 = pk;
+    st.packed1 = pv;
+    st.scales0 = sk;
+    st.scales1 = sv;
+    st.rowb0 = k.r / 2;
+    st.rowb1 = v.r / 2;
+    st.ng0 = k.r / k.group;
+    st.ng1 = v.r / v.group;
+    st.grp0 = k.group;
+    st.grp1 = v.group;
+    st.fp16_0 = k.scale_dtype == NKV_DTYPE_FP16;
+    st.fp16_1 = v.scale_dtype == NKV_DTYPE_FP16;
+    const int rk = k.r, rv = v.r;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-#pragma unroll
-                for (int b = 0; b < 4; ++b) {
-                    float lo = (float)((int)((w[e] >> (8 * b)) & 15u) - 7) * s;
-                    float hi = (float)((int)((w[e] >> (8 * b + 4)) & 15u) - 7) * s;
-                    o[e][b] = pack_bf16x2(lo, hi);
-                }
-            }
+    for (int e = 0; e < AT_ITEMS; ++e) {
+        int it = t + AT_THREADS * e;
+        if (it >= rk + rv) {
+            st.item[e] = -1;
+        } else if (it < rk) {
+            const int row = it / (rk / 32);
+            st.item[e] = row | ((it - row * (rk / 32)) << 5);
+        } else {
+            it -= rk;
+            const int row = it / (rv / 32);
+            st.item[e] = row | ((it - row * (rv / 32)) << 5) | (1 << 9);
         }
-        u32x4* dst = reinterpret_cast<u32x4*>(&z[row][j * 32]);
+    }
+    return st;
+}
+
+// Registers carrying one tile from its global loads to its LDS stores.
+struct ZPrefetch {
+    u32x4 w[AT_ITEMS];  // packed codes
+    float s[AT_ITEMS];  // group scales
+    int id;             // center id of token l32 in this wave's codec
+};
+
+__device__ __forceinline__ void prefetch_tile(ZPrefetch& pf, const Streamer& st,
+                                              const void* my_ids, int id_bytes, int ncent,
+                                              int64_t tok0, int valid, int t) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) dst[e] = o[e];
+    for (int e = 0; e < AT_ITEMS; ++e) {
+        const int item = st.item[e];
+        const int row = item & 31, j = (item >> 5) & 15, c = (item >> 9) & 1;
+        pf.w[e] = u32x4{0, 0, 0, 0};
+        pf.s[e] = 0.0f;
+        if (item >= 0 && row < valid) {
+            const int64_t tok = tok0 + row;
+            const uint8_t* src = c ? st.packed1 + tok * st.rowb1 : st.packed0 + tok * st.rowb0;
+            pf.w[e] = *reinterpret_cast<const u32x4*>(src + j * 16);
+            const uint16_t sb = c ? st.scales1[tok * st.ng1 + (j * 32) / st.grp1]
+                                  : st.scales0[tok * st.ng0 + (j * 32) / st.grp0];
+            pf.s[e] = (c ? st.fp16_1 : st.fp16_0) ? f16_bits_to_f32(sb) : bf16_bits_to_f32(sb);
+        }
     }
     // ids outside the table are clamped so that a corrupt payload cannot read
     // out of bounds (valid payloads never contain them)
-    if (t < AT_BN)
-        ids_s[t] = (c.centers && t < valid)
-                       ? min(max(read_id(ids, c.id_bytes, tok0 + t), 0), c.num_centers - 1)
-                       : 0;
+    const int tok = t & 31;
+    pf.id = (my_ids && tok < valid) ? min(max(read_id(my_ids, id_bytes, tok0 + tok), 0), ncent - 1)
+                                    : 0;
 }
 
-// K^T tile for d rows [32*wave, +32) and tokens [0, 64): A = W_K rows from
-// global memory (16-byte loads), B = unpacked Z_K rows from LDS.  Epilogue
-// writes bf16 K[token][d] (four consecutive d per 8-byte store).
-__device__ __forceinline__ void decode_k(AttendSmem& sm, const nkv_codec& c,
-                                         const uint16_t* centers, int HD, int h, int wave,
-                                         int lane) {
-    const int hf = lane >> 5, l32 = lane & 31;
-    const int d0 = 32 * wave;
-    const uint16_t* wrow = c.w_dec + (int64_t)(h * AT_D + d0 + l32) * c.r + 8 * hf;
-    f32x16 acc0 = {}, acc1 = {};
-    for (int k0 = 0; k0 < c.r; k0 += 64) {
-        u32x4 wa[4];
+__device__ __forceinline__ void store_tile(AttendSmem& sm, const ZPrefetch& pf,
+                                           const Streamer& st) {
 #pragma unroll
-        for (int u = 0; u < 4; ++u) wa[u] = *reinterpret_cast<const u32x4*>(wrow + k0 + 16 * u);
+    for (int e = 0; e < AT_ITEMS; ++e) {
+        const int item = st.item[e];
+        if (item < 0) continue;
+        const int row = item & 31, j = (item >> 5) & 15, c = (item >> 9) & 1;
+        // (nibble - 7) * s = fma(nibble, s, -7 s): both products are exact in
+        // fp32 (<= 15 significant bits), so the fma returns the exact value and
+        // the bf16 conversion rounds it once, as the reference does.
+        const float s = pf.s[e];
+        const float ns7 = -7.0f * s;
+        u32x4* dst = reinterpret_cast<u32x4*>(&sm.z[c][row][j * 32]);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int kk = k0 + 16 * u + 8 * hf;
-            const bf16x8 b0 = lds_b128(&sm.zk[l32][kk]);
-            const bf16x8 b1 = lds_b128(&sm.zk[32 + l32][kk]);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wa[u]), b0, acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(wa[u]), b1, acc1, 0, 0, 0);
+        for (int q = 0; q < 4; ++q) {
+            const uint32_t w = pf.w[e][q];
+            const uint32_t ev = w & 0x0f0f0f0fu;          // codes 0, 2, 4, 6 (byte lanes)
+            const uint32_t od = (w >> 4) & 0x0f0f0f0fu;   // codes 1, 3, 5, 7
+            u32x4 o;
+#pragma unroll
+            for (int b = 0; b < 4; ++b) {
+                const float lo = fmaf((float)((ev >> (8 * b)) & 0xffu), s, ns7);
+                const float hi = fmaf((float)((od >> (8 * b)) & 0xffu), s, ns7);
+                o[b] = pack_bf16x2(lo, hi);
+            }
+            dst[q] = o;
         }
     }
+}
+
+// Center values the epilogue of this lane adds: token l32 of the tile,
+// d = 64*dh + 32*jb + 8*g + 4*hf + [0, 4), as packed bf16 pairs.
+__device__ __forceinline__ void load_centers(u32x2 (&cen)[2][4], const uint16_t* centers, int id,
+                                             int HD, int h, int dh, int hf) {
+    const uint16_t* crow = centers + (int64_t)id * HD + h * AT_D + 64 * dh + 4 * hf;
 #pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-        const int tok = 32 * tb + l32;
-        const uint16_t* crow = centers ? centers + (int64_t)sm.ids_k[tok] * HD + h * AT_D : nullptr;
+    for (int jb = 0; jb < 2; ++jb)
+#pragma unroll
+        for (int g = 0; g < 4; ++g)
+            cen[jb][g] = centers ? *reinterpret_cast<const u32x2*>(crow + 32 * jb + 8 * g)
+                                 : u32x2{0, 0};
+}
+
+// Decode this wave's 64 columns of K (CODEC 0) or V (CODEC 1) for the tile in
+// LDS: acc_jb = W[64*dh + 32*jb + .., :] * Z^T (rows d, columns tokens), then
+// bf16(bf16(acc + bias) + center) stored as K[token][d] or V^T[d][token].
+template <int CODEC, int NKS, int KSMAX>
+__device__ __forceinline__ void decode_tile(AttendSmem& sm, const bf16x8 (&wreg)[2][KSMAX],
+                                            const u32x2 (&cen)[2][4], bool has_bias, int dh,
+                                            int lane) {
+    const int hf = lane >> 5, l32 = lane & 31;
+    const uint16_t* zrow = &sm.z[CODEC][l32][8 * hf];
+    f32x16 acc0 = {}, acc1 = {};
+    bf16x8 zn = lds_b128(zrow);
+#pragma unroll
+    for (int ks = 0; ks < NKS; ++ks) {
+        const bf16x8 zf = zn;
+        if (ks + 1 < NKS) zn = lds_b128(zrow + 16 * (ks + 1));
+        acc0 = mfma32(wreg[0][ks], zf, acc0);
+        acc1 = mfma32(wreg[1][ks], zf, acc1);
+    }
+    const int tok = l32;
+#pragma unroll
+    for (int jb = 0; jb < 2; ++jb) {
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
-            const int d = d0 + 8 * g + 4 * hf;
-            float v[4];
+            const int d = 64 * dh + 32 * jb + 8 * g + 4 * hf;
+            const f32x16& acc = jb ? acc1 : acc0;
+            float a[4] = {acc[4 * g], acc[4 * g + 1], acc[4 * g + 2], acc[4 * g + 3]};
+            if (has_bias) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                v[e] = bf16_round((tb ? acc1[4 * g + e] : acc0[4 * g + e]) + sm.bias_k[d + e]);
-            if (crow) {
-                const u32x2 cw = *reinterpret_cast<const u32x2*>(crow + d);
-                v[0] = bf16_round(v[0] + __uint_as_float(cw[0] << 16));
-                v[1] = bf16_round(v[1] + __uint_as_float(cw[0] & 0xffff0000u));
-                v[2] = bf16_round(v[2] + __uint_as_float(cw[1] << 16));
-                v[3] = bf16_round(v[3] + __uint_as_float(cw[1] & 0xffff0000u));
+                for (int e = 0; e < 4; ++e) a[e] += sm.bias[CODEC][d + e];
             }
-            u32x2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-            *reinterpret_cast<u32x2*>(&sm.ks[tok][d]) = pk;
+            // first rounding (decoder output), widen, add the bf16 center, round again
+            const u32x2 cw = cen[jb][g];
+            u32x2 r;
+#pragma unroll
+            for (int h2 = 0; h2 < 2; ++h2) {
+                const uint32_t pr = pack_bf16x2(a[2 * h2], a[2 * h2 + 1]);
+                const float lo = __uint_as_float(pr << 16) + __uint_as_float(cw[h2] << 16);
+                const float hi = __uint_as_float(pr & 0xffff0000u) +
+                                 __uint_as_float(cw[h2] & 0xffff0000u);
+                r[h2] = pack_bf16x2(lo, hi);
+            }
+            if (CODEC == 0) {
+                *reinterpret_cast<u32x2*>(&sm.ks[tok][d]) = r;
+            } else {
+                sm.vt[d][tok] = (uint16_t)(r[0] & 0xffffu);
+                sm.vt[d + 1][tok] = (uint16_t)(r[0] >> 16);
+                sm.vt[d + 2][tok] = (uint16_t)(r[1] & 0xffffu);
+                sm.vt[d + 3][tok] = (uint16_t)(r[1] >> 16);
+            }
         }
     }
 }
 
-// V tile for tokens [0, 64) and d columns [32*wave, +32): A = Z_V rows from
-// LDS, B = W_V rows from global memory.  Epilogue writes bf16 V^T[d][token]
-// (four consecutive tokens per 8-byte store).
-__device__ __forceinline__ void decode_v(AttendSmem& sm, const nkv_codec& c,
-                                         const uint16_t* centers, int HD, int h, int wave,
-                                         int lane) {
-    const int hf = lane >> 5, l32 = lane & 31;
-    const int d = 32 * wave + l32;
-    const uint16_t* wrow = c.w_dec + (int64_t)(h * AT_D + d) * c.r + 8 * hf;
-    f32x16 acc0 = {}, acc1 = {};
-    for (int k0 = 0; k0 < c.r; k0 += 64) {
-        u32x4 wb[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) wb[u] = *reinterpret_cast<const u32x4*>(wrow + k0 + 16 * u);
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            const int kk = k0 + 16 * u + 8 * hf;
-            const bf16x8 a0 = lds_b128(&sm.zv[l32][kk]);
-            const bf16x8 a1 = lds_b128(&sm.zv[32 + l32][kk]);
-            acc0 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a0, as_bf16x8(wb[u]), acc0, 0, 0, 0);
-            acc1 = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a1, as_bf16x8(wb[u]), acc1, 0, 0, 0);
-        }
-    }
-    const float bias = sm.bias_v[d];
-#pragma unroll
-    for (int tb = 0; tb < 2; ++tb) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-            const int tok = 32 * tb + 8 * g + 4 * hf;
-            float v[4];
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                v[e] = bf16_round((tb ? acc1[4 * g + e] : acc0[4 * g + e]) + bias);
-                if (centers) {
-                    const uint16_t cb =
-                        centers[(int64_t)sm.ids_v[tok + e] * HD + h * AT_D + d];
-                    v[e] = bf16_round(v[e] + bf16_bits_to_f32(cb));
-                }
-            }
-            u32x2 pk = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-            *reinterpret_cast<u32x2*>(&sm.vt[d][tok]) = pk;
-        }
-    }
-}
+// Current-chunk tile chunks: thread t owns 16-byte chunks it = t + 256*e of
+// the 32 x 128 K tile (it < 512) and V tile (it >= 512).
+struct CurPrefetch {
+    u32x4 w[AT_CITEMS];
+};
 
-// Copy an uncompressed current-chunk tile (rows >= valid are zero).
-__device__ __forceinline__ void load_current(AttendSmem& sm, const AttendParams& p, int b,
-                                             int h, int64_t tok0, int valid, int t) {
-    for (int it = t; it < AT_BN * (AT_D / 8); it += 256) {
-        const int row = it / (AT_D / 8);
-        const int d = (it % (AT_D / 8)) * 8;
-        u32x4 kv = {0, 0, 0, 0}, vv = {0, 0, 0, 0};
+__device__ __forceinline__ void prefetch_current(CurPrefetch& cf, const AttendParams& p, int b,
+                                                 int h, int64_t tok0, int valid, int t) {
+#pragma unroll
+    for (int e = 0; e < AT_CITEMS; ++e) {
+        const int it = t + AT_THREADS * e;
+        const int kvsel = it / (AT_BN * (AT_D / 8));
+        const int rem = it % (AT_BN * (AT_D / 8));
+        const int row = rem / (AT_D / 8), d = (rem % (AT_D / 8)) * 8;
+        cf.w[e] = u32x4{0, 0, 0, 0};
         if (row < valid) {
             const int64_t tok = tok0 + row;
-            kv = *reinterpret_cast<const u32x4*>(p.k_cur + b * p.k_sb + tok * p.k_st +
-                                                 h * p.k_sh + d);
-            vv = *reinterpret_cast<const u32x4*>(p.v_cur + b * p.v_sb + tok * p.v_st +
-                                                 h * p.v_sh + d);
-        }
-        *reinterpret_cast<u32x4*>(&sm.ks[row][d]) = kv;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            sm.vt[d + 2 * e][row] = (uint16_t)(vv[e] & 0xffffu);
-            sm.vt[d + 2 * e + 1][row] = (uint16_t)(vv[e] >> 16);
+            const uint16_t* src = kvsel ? p.v_cur + b * p.v_sb + tok * p.v_st + h * p.v_sh + d
+                                        : p.k_cur + b * p.k_sb + tok * p.k_st + h * p.k_sh + d;
+            cf.w[e] = *reinterpret_cast<const u32x4*>(src);
         }
     }
 }
 
-__global__ void __launch_bounds__(256, 1) attend_kernel(AttendParams p) {
+__device__ __forceinline__ void store_current(AttendSmem& sm, const CurPrefetch& cf, int t) {
+#pragma unroll
+    for (int e = 0; e < AT_CITEMS; ++e) {
+        const int it = t + AT_THREADS * e;
+        const int kvsel = it / (AT_BN * (AT_D / 8));
+        const int rem = it % (AT_BN * (AT_D / 8));
+        const int row = rem / (AT_D / 8), d = (rem % (AT_D / 8)) * 8;
+        if (!kvsel) {
+            *reinterpret_cast<u32x4*>(&sm.ks[row][d]) = cf.w[e];
+        } else {
+#pragma unroll
+            for (int q = 0; q < 4; ++q) {
+                sm.vt[d + 2 * q][row] = (uint16_t)(cf.w[e][q] & 0xffffu);
+                sm.vt[d + 2 * q + 1][row] = (uint16_t)(cf.w[e][q] >> 16);
+            }
+        }
+    }
+}
+
+// One online-softmax step of this wave's two query blocks over the tile in
+// LDS.  Blocks past the end of the query tile read zero Q rows; their
+// results are never stored.
+__device__ __forceinline__ void attend_tile(const AttendSmem& sm, int qrow0,
+                                            f32x16 (&o)[AT_QB][AT_D / 32], float (&m_run)[AT_QB],
+                                            float (&l_run)[AT_QB], float scale_log2, int valid,
+                                            int lane) {
+    const int hf = lane >> 5, l32 = lane & 31;
+    f32x16 s[AT_QB];
+#pragma unroll
+    for (int qb = 0; qb < AT_QB; ++qb) s[qb] = f32x16{};
+    // S^T = K Q^T: fragments of k-step kk+1 are loaded before the MFMAs of kk
+    const uint16_t* krow = &sm.ks[l32][8 * hf];
+    const uint16_t* q0row = &sm.qs[qrow0 + l32][8 * hf];
+    const uint16_t* q1row = &sm.qs[qrow0 + 32 + l32][8 * hf];
+    bf16x8 ka = lds_b128(krow), qa = lds_b128(q0row), qb1 = lds_b128(q1row);
+#pragma unroll
+    for (int kk = 0; kk < AT_D / 16; ++kk) {
+        const bf16x8 a = ka, b0 = qa, b1 = qb1;
+        if (kk + 1 < AT_D / 16) {
+            ka = lds_b128(krow + 16 * (kk + 1));
+            qa = lds_b128(q0row + 16 * (kk + 1));
+            qb1 = lds_b128(q1row + 16 * (kk + 1));
+        }
+        s[0] = mfma32(a, b0, s[0]);
+        s[1] = mfma32(a, b1, s[1]);
+    }
+    bf16x8 pb[AT_QB][2];
+    float alpha[AT_QB];
+    bool rescale = false;
+    if (valid < AT_BN) {  // partial tile: keys past the end get -inf
+#pragma unroll
+        for (int qb = 0; qb < AT_QB; ++qb)
+#pragma unroll
+            for (int i = 0; i < 16; ++i)
+                if (8 * (i / 4) + 4 * hf + (i % 4) >= valid) s[qb][i] = -INFINITY;
+    }
+#pragma unroll
+    for (int qb = 0; qb < AT_QB; ++qb) {
+        // the max is taken on raw scores (scale_log2 > 0 preserves order)
+        float tmax = s[qb][0];
+#pragma unroll
+        for (int i = 1; i < 16; ++i) tmax = fmaxf(tmax, s[qb][i]);
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * scale_log2;
+        const float m_new = fmaxf(m_run[qb], tmax);
+        const float m_use = m_new == -INFINITY ? 0.0f : m_new;
+        alpha[qb] = __builtin_amdgcn_exp2f(m_run[qb] - m_use);
+        rescale |= m_new > m_run[qb];
+        m_run[qb] = m_new;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            // v_exp_f32: exp2 of arguments <= 0; results below 2^-126 flush to 0
+            const float e = __builtin_amdgcn_exp2f(fmaf(s[qb][i], scale_log2, -m_use));
+            s[qb][i] = e;
+            lsum += e;
+        }
+        l_run[qb] = l_run[qb] * alpha[qb] + lsum;
+        // P^T operand of k-step ts: accumulator elements [8*ts, +8), i.e.
+        // keys 16*ts + 8*(j/4) + 4*hf + j%4 for slot j
+#pragma unroll
+        for (int ts = 0; ts < 2; ++ts) {
+            u32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+                v[e] = pack_bf16x2(s[qb][8 * ts + 2 * e], s[qb][8 * ts + 2 * e + 1]);
+            pb[qb][ts] = as_bf16x8(v);
+        }
+    }
+    // O is rescaled only when some running max of this wave moved (alpha is
+    // exactly 1 otherwise); first tiles always move it.
+    if (__any(rescale)) {
+#pragma unroll
+        for (int qb = 0; qb < AT_QB; ++qb)
+#pragma unroll
+            for (int db = 0; db < AT_D / 32; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[qb][db][i] *= alpha[qb];
+    }
+    // O^T += V^T P^T: V fragment of step n+1 loaded before the MFMAs of step n
+    bf16x8 va = lds_2x64(&sm.vt[l32][4 * hf]);
+#pragma unroll
+    for (int n = 0; n < 2 * (AT_D / 32); ++n) {
+        const int ts = n / (AT_D / 32), db = n % (AT_D / 32);
+        const bf16x8 a = va;
+        if (n + 1 < 2 * (AT_D / 32)) {
+            const int ts1 = (n + 1) / (AT_D / 32), db1 = (n + 1) % (AT_D / 32);
+            va = lds_2x64(&sm.vt[32 * db1 + l32][16 * ts1 + 4 * hf]);
+        }
+        o[0][db] = mfma32(a, pb[0][ts], o[0][db]);
+        o[1][db] = mfma32(a, pb[1][ts], o[1][db]);
+    }
+}
+
+// RK, RV: ranks of the K and V codecs (compile-time, so each decode wave
+// runs a branch-free unrolled MFMA chain over its rank).
+template <int RK, int RV>
+__global__ void __launch_bounds__(AT_THREADS, 1) attend_kernel(AttendParams p) {
+    constexpr int KSK = RK / 16, KSV = RV / 16;
+    constexpr int KSMAX = KSK > KSV ? KSK : KSV;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     AttendSmem& sm = *reinterpret_cast<AttendSmem*>(smem_raw);
 
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int t = threadIdx.x, lane = t & 63;
+    // the wave index is uniform; readfirstlane lets the compiler keep every
+    // role-dependent value (codec, rank, pointers, loop bounds) in SGPRs and
+    // branch on them with scalar branches instead of exec masks
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int hf = lane >> 5, l32 = lane & 31;
 
     // block -> (bh, q tile, split); bh varies fastest so that with B*H a
@@ -267,37 +453,66 @@ __global__ void __launch_bounds__(256, 1) attend_kernel(AttendParams p) {
 
     const int tile_begin = (int)((int64_t)split * p.t_total / p.S);
     const int tile_end = (int)((int64_t)(split + 1) * p.t_total / p.S);
+    const int hist_end = min(tile_end, p.t_hist);
 
-    // codec base pointers for batch item b
-    const nkv_codec& ck = p.key;
-    const nkv_codec& cv = p.value;
-    const uint8_t* kpacked = ck.packed ? ck.packed + (int64_t)b * p.N * (ck.r / 2) : nullptr;
-    const uint16_t* kscales = ck.scales ? ck.scales + (int64_t)b * p.N * (ck.r / ck.group) : nullptr;
-    const void* kids = ck.ids ? (const void*)((const uint8_t*)ck.ids + (int64_t)b * p.N * ck.id_bytes) : nullptr;
-    const uint16_t* kcent = ck.centers ? ck.centers + (int64_t)b * ck.centers_batch_stride : nullptr;
-    const uint8_t* vpacked = cv.packed ? cv.packed + (int64_t)b * p.N * (cv.r / 2) : nullptr;
-    const uint16_t* vscales = cv.scales ? cv.scales + (int64_t)b * p.N * (cv.r / cv.group) : nullptr;
-    const void* vids = cv.ids ? (const void*)((const uint8_t*)cv.ids + (int64_t)b * p.N * cv.id_bytes) : nullptr;
-    const uint16_t* vcent = cv.centers ? cv.centers + (int64_t)b * cv.centers_batch_stride : nullptr;
+    const nkv_codec& ck = p.codec[0];
+    const nkv_codec& cv = p.codec[1];
+    const int64_t N = p.N;
+    const uint8_t* kpacked = ck.packed ? ck.packed + (int64_t)b * N * (ck.r / 2) : nullptr;
+    const uint16_t* kscales = ck.scales ? ck.scales + (int64_t)b * N * (ck.r / ck.group) : nullptr;
+    const uint8_t* vpacked = cv.packed ? cv.packed + (int64_t)b * N * (cv.r / 2) : nullptr;
+    const uint16_t* vscales = cv.scales ? cv.scales + (int64_t)b * N * (cv.r / cv.group) : nullptr;
+
+    // this wave's decode role: codec (0 = K, 1 = V) and 64-row half dh
+    const int codec = wave >> 1, dh = wave & 1;
+    const bool has_c = codec ? cv.centers != nullptr : ck.centers != nullptr;
+    const uint16_t* my_centers =
+        has_c ? (codec ? cv.centers + (int64_t)b * cv.centers_batch_stride
+                       : ck.centers + (int64_t)b * ck.centers_batch_stride)
+              : nullptr;
+    const void* my_ids =
+        has_c ? (const void*)((const uint8_t*)(codec ? cv.ids : ck.ids) +
+                              (int64_t)b * N * (codec ? cv.id_bytes : ck.id_bytes))
+              : nullptr;
+    const int my_id_bytes = codec ? cv.id_bytes : ck.id_bytes;
+    const int my_ncent = codec ? cv.num_centers : ck.num_centers;
+    const int my_r = codec ? cv.r : ck.r;
+    const uint16_t* my_wdec = codec ? cv.w_dec : ck.w_dec;
+    const bool has_bias = (codec ? cv.mean : ck.mean) != nullptr;
 
     if (t < AT_D) {
-        sm.bias_k[t] = ck.mean ? bf16_round(ck.mean[h * AT_D + t]) : 0.0f;
-        sm.bias_v[t] = cv.mean ? bf16_round(cv.mean[h * AT_D + t]) : 0.0f;
+        sm.bias[0][t] = ck.mean ? bf16_round(ck.mean[h * AT_D + t]) : 0.0f;
+        sm.bias[1][t] = cv.mean ? bf16_round(cv.mean[h * AT_D + t]) : 0.0f;
     }
 
-    // Q^T operands: query column (l32) of block qb, d = 16*kk + 8*hf + [0, 8)
-    const int64_t qbase = (int64_t)qt * AT_BM + wave * (AT_QB * 32);
-    bf16x8 qr[AT_QB][AT_D / 16];
+    // Q tile -> LDS (rows past the tile end are zero)
+    const int64_t tile_q0 = (int64_t)qt * p.q_per_tile;
+    const int64_t tile_q1 = min(p.Q, tile_q0 + p.q_per_tile);
+    for (int it = t; it < AT_BM * (AT_D / 8); it += AT_THREADS) {
+        const int row = it / (AT_D / 8), d = (it % (AT_D / 8)) * 8;
+        const int64_t qi = tile_q0 + row;
+        u32x4 v = {0, 0, 0, 0};
+        if (qi < tile_q1)
+            v = *reinterpret_cast<const u32x4*>(p.q + b * p.q_sb + qi * p.q_st + h * p.q_sh + d);
+        *reinterpret_cast<u32x4*>(&sm.qs[row][d]) = v;
+    }
+    const int qrow0 = wave * (AT_QB * 32);
+    const int64_t q0 = tile_q0 + qrow0;
+    const int nqb = q0 >= tile_q1 ? 0 : (int)min((int64_t)AT_QB, cdiv(tile_q1 - q0, 32));
+
+    // register-stationary decoder fragments: rows 64*dh + 32*jb + l32 of this
+    // wave's codec slice, k = 16*ks + 8*hf + [0, 8)
+    const bool decodes = hist_end > tile_begin;
+    bf16x8 wreg[2][KSMAX];
 #pragma unroll
-    for (int qb = 0; qb < AT_QB; ++qb) {
-        const int64_t qi = qbase + 32 * qb + l32;
+    for (int jb = 0; jb < 2; ++jb) {
+        const uint16_t* wrow =
+            my_wdec + (int64_t)(h * AT_D + 64 * dh + 32 * jb + l32) * my_r + 8 * hf;
 #pragma unroll
-        for (int kk = 0; kk < AT_D / 16; ++kk) {
+        for (int ks = 0; ks < KSMAX; ++ks) {
             u32x4 v = {0, 0, 0, 0};
-            if (qi < p.Q)
-                v = *reinterpret_cast<const u32x4*>(p.q + b * p.q_sb + qi * p.q_st + h * p.q_sh +
-                                                    16 * kk + 8 * hf);
-            qr[qb][kk] = as_bf16x8(v);
+            if (decodes && 16 * ks < my_r) v = *reinterpret_cast<const u32x4*>(wrow + 16 * ks);
+            wreg[jb][ks] = as_bf16x8(v);
         }
     }
 
@@ -313,112 +528,78 @@ __global__ void __launch_bounds__(256, 1) attend_kernel(AttendParams p) {
         l_run[qb] = 0.0f;
     }
 
-    for (int tile = tile_begin; tile < tile_end; ++tile) {
-        const bool hist = tile < p.t_hist;
-        const int64_t tok0 = hist ? (int64_t)tile * AT_BN : (int64_t)(tile - p.t_hist) * AT_BN;
-        const int64_t len = hist ? p.N : p.Nc;
-        const int valid = (int)min((int64_t)AT_BN, len - tok0);
+    auto tile_valid = [&](int tile) {
+        return (int)min((int64_t)AT_BN, N - (int64_t)tile * AT_BN);
+    };
 
-        __syncthreads();  // previous tile fully consumed
-        if (hist) {
-            unpack_tile(sm.zk, sm.ids_k, kpacked, kscales, kids, ck, tok0, valid, t);
-            unpack_tile(sm.zv, sm.ids_v, vpacked, vscales, vids, cv, tok0, valid, t);
+    // ---- history tiles
+    if (tile_begin < hist_end) {
+        const Streamer st = make_streamer(ck, cv, kpacked, kscales, vpacked, vscales, t);
+        // the center ids of the tile in LDS, for this lane's token (l32)
+        int cur_id;
+        {
+            ZPrefetch pf;
+            prefetch_tile(pf, st, my_ids, my_id_bytes, my_ncent, (int64_t)tile_begin * AT_BN,
+                          tile_valid(tile_begin), t);
+            store_tile(sm, pf, st);
+            cur_id = pf.id;
+        }
+        __syncthreads();  // Q, bias and the first unpacked tile are in LDS
+        for (int tile = tile_begin; tile < hist_end; ++tile) {
+            // phase A: decode this tile into the K/V tile buffers; the center
+            // loads are issued first and land while the decode MFMAs run
+            {
+                u32x2 cen[2][4];
+                load_centers(cen, my_centers, cur_id, p.HD, h, dh, hf);
+                if (codec == 0) decode_tile<0, KSK>(sm, wreg, cen, has_bias, dh, lane);
+                else decode_tile<1, KSV>(sm, wreg, cen, has_bias, dh, lane);
+            }
             __syncthreads();
-            decode_k(sm, ck, kcent, p.HD, h, wave, lane);
-            decode_v(sm, cv, vcent, p.HD, h, wave, lane);
-        } else {
-            load_current(sm, p, b, h, tok0, valid, t);
+            // phase B: load the next tile's codes, attend this tile while they
+            // arrive, then unpack them into the (now free) coefficient buffers
+            ZPrefetch pf;
+            const bool next = tile + 1 < hist_end;
+            if (next)
+                prefetch_tile(pf, st, my_ids, my_id_bytes, my_ncent, (int64_t)(tile + 1) * AT_BN,
+                              tile_valid(tile + 1), t);
+            attend_tile(sm, qrow0, o, m_run, l_run, p.scale_log2, tile_valid(tile), lane);
+            if (next) {
+                store_tile(sm, pf, st);
+                cur_id = pf.id;
+            }
+            __syncthreads();
         }
-        __syncthreads();
+    } else {
+        __syncthreads();  // Q and bias are in LDS
+    }
 
-        // ---- S^T = K * Q^T: rows = keys (32*kb + ...), cols = queries
-        f32x16 s[2][AT_QB];
-#pragma unroll
-        for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-            for (int qb = 0; qb < AT_QB; ++qb) s[kb][qb] = f32x16{};
-#pragma unroll
-        for (int kk = 0; kk < AT_D / 16; ++kk) {
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-                const bf16x8 a = lds_b128(&sm.ks[32 * kb + l32][16 * kk + 8 * hf]);
-#pragma unroll
-                for (int qb = 0; qb < AT_QB; ++qb)
-                    s[kb][qb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, qr[qb][kk], s[kb][qb],
-                                                                        0, 0, 0);
-            }
-        }
-
-        // ---- online softmax over the 64 keys of this tile (per query column)
-        bf16x8 pb[AT_QB][4];
-#pragma unroll
-        for (int qb = 0; qb < AT_QB; ++qb) {
-            float tmax = -INFINITY;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const int key = 32 * kb + 8 * (i / 4) + 4 * hf + (i % 4);
-                    float x = s[kb][qb][i] * p.scale_log2;
-                    x = key < valid ? x : -INFINITY;
-                    s[kb][qb][i] = x;
-                    tmax = fmaxf(tmax, x);
-                }
-            }
-            tmax = fmaxf(tmax, __shfl_xor(tmax, 32));
-            const float m_new = fmaxf(m_run[qb], tmax);
-            const float m_use = m_new == -INFINITY ? 0.0f : m_new;
-            const float alpha = exp2f(m_run[qb] - m_use);
-            m_run[qb] = m_new;
-            float lsum = 0.0f;
-#pragma unroll
-            for (int kb = 0; kb < 2; ++kb) {
-#pragma unroll
-                for (int i = 0; i < 16; ++i) {
-                    const float e = exp2f(s[kb][qb][i] - m_use);
-                    s[kb][qb][i] = e;
-                    lsum += e;
-                }
-            }
-            l_run[qb] = l_run[qb] * alpha + lsum;
-#pragma unroll
-            for (int db = 0; db < AT_D / 32; ++db)
-#pragma unroll
-                for (int i = 0; i < 16; ++i) o[qb][db][i] *= alpha;
-            // P^T operands for k-steps of 16 keys: step ts uses accumulator
-            // elements [8*(ts%2), +8) of key block ts/2, i.e. keys
-            // 16*ts + 8*(j/4) + 4*hf + j%4 for slot j.
-#pragma unroll
-            for (int ts = 0; ts < 4; ++ts) {
-                u32x4 v;
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    v[e] = pack_bf16x2(s[ts / 2][qb][8 * (ts % 2) + 2 * e],
-                                       s[ts / 2][qb][8 * (ts % 2) + 2 * e + 1]);
-                pb[qb][ts] = as_bf16x8(v);
-            }
-        }
-
-        // ---- O^T += V^T * P^T
-#pragma unroll
-        for (int ts = 0; ts < 4; ++ts) {
-#pragma unroll
-            for (int db = 0; db < AT_D / 32; ++db) {
-                const bf16x8 a = lds_2x64(&sm.vt[32 * db + l32][16 * ts + 4 * hf]);
-#pragma unroll
-                for (int qb = 0; qb < AT_QB; ++qb)
-                    o[qb][db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, pb[qb][ts], o[qb][db],
-                                                                        0, 0, 0);
-            }
+    // ---- current-chunk tiles (uncompressed), prefetched a tile ahead
+    const int cur_begin = max(tile_begin, p.t_hist);
+    if (cur_begin < tile_end) {
+        auto cur_valid = [&](int tile) {
+            return (int)min((int64_t)AT_BN, p.Nc - (int64_t)(tile - p.t_hist) * AT_BN);
+        };
+        CurPrefetch cf;
+        prefetch_current(cf, p, b, h, (int64_t)(cur_begin - p.t_hist) * AT_BN,
+                         cur_valid(cur_begin), t);
+        for (int tile = cur_begin; tile < tile_end; ++tile) {
+            store_current(sm, cf, t);
+            if (tile + 1 < tile_end)
+                prefetch_current(cf, p, b, h, (int64_t)(tile + 1 - p.t_hist) * AT_BN,
+                                 cur_valid(tile + 1), t);
+            __syncthreads();
+            attend_tile(sm, qrow0, o, m_run, l_run, p.scale_log2, cur_valid(tile), lane);
+            __syncthreads();
         }
     }
 
     // ---- epilogue
 #pragma unroll
     for (int qb = 0; qb < AT_QB; ++qb) {
+        if (qb >= nqb) continue;
         const float l_tot = l_run[qb] + __shfl_xor(l_run[qb], 32);
-        const int64_t qi = qbase + 32 * qb + l32;
-        if (qi >= p.Q) continue;
+        const int64_t qi = q0 + 32 * qb + l32;
+        if (qi >= tile_q1) continue;
         if (p.S == 1) {
             const float inv = l_tot > 0.0f ? 1.0f / l_tot : 0.0f;
             uint16_t* orow = p.out + b * p.o_sb + qi * p.o_st + h * p.o_sh;
@@ -532,16 +713,15 @@ int device_cu_count() {
 }
 
 struct AttendPlan {
-    int q_tiles, t_hist, t_total, splits;
+    int q_tiles, q_per_tile, t_hist, t_total, splits;
 };
 
 int check_attend_codec(const nkv_codec& c, int64_t N, int HD, const char* which) {
     (void)which;
     NKV_REQUIRE(c.packed && c.scales && c.w_dec, NKV_ERR_INVALID,
                 "history codec needs packed, scales and w_dec");
-    NKV_REQUIRE(c.r > 0 && c.r % 64 == 0, NKV_ERR_UNSUPPORTED,
-                "fused attend needs r to be a multiple of 64");
-    NKV_REQUIRE(c.r <= AT_RMAX, NKV_ERR_UNSUPPORTED, "fused attend supports r <= 384");
+    NKV_REQUIRE(c.r == 64 || c.r == 128 || c.r == 256 || c.r == 384, NKV_ERR_UNSUPPORTED,
+                "fused attend supports codec ranks 64, 128, 256 and 384");
     NKV_REQUIRE(c.group > 0 && c.r % c.group == 0 && c.group % 32 == 0, NKV_ERR_UNSUPPORTED,
                 "fused attend needs group to divide r and be a multiple of 32");
     NKV_REQUIRE(c.scale_dtype == NKV_DTYPE_BF16 || c.scale_dtype == NKV_DTYPE_FP16,
@@ -573,6 +753,9 @@ int plan_attend(const nkv_attend_args* a, AttendPlan* plan) {
     if (a->Nc > 0) NKV_REQUIRE(a->k_cur && a->v_cur, NKV_ERR_INVALID, "current K/V missing");
     if (a->Q > 0) NKV_REQUIRE(a->q && a->out, NKV_ERR_INVALID, "q and out required");
     plan->q_tiles = (int)cdiv(a->Q, AT_BM);
+    // spread the queries evenly over the tiles, in whole 32-query blocks
+    plan->q_per_tile =
+        plan->q_tiles ? (int)(cdiv(cdiv(a->Q, plan->q_tiles), 32) * 32) : AT_BM;
     plan->t_hist = (int)cdiv(a->N, AT_BN);
     plan->t_total = plan->t_hist + (int)cdiv(a->Nc, AT_BN);
     int S = a->splits;
@@ -601,6 +784,29 @@ size_t workspace_bytes_for(const nkv_attend_args* a, const AttendPlan& pl) {
     return rows * AT_D * sizeof(float) + rows * 2 * sizeof(float);
 }
 
+typedef void (*AttendKernel)(AttendParams);
+
+template <int RK>
+AttendKernel attend_instance_rv(int rv) {
+    switch (rv) {
+        case 64: return attend_kernel<RK, 64>;
+        case 128: return attend_kernel<RK, 128>;
+        case 256: return attend_kernel<RK, 256>;
+        case 384: return attend_kernel<RK, 384>;
+        default: return nullptr;
+    }
+}
+
+AttendKernel attend_instance(int rk, int rv) {
+    switch (rk) {
+        case 64: return attend_instance_rv<64>(rv);
+        case 128: return attend_instance_rv<128>(rv);
+        case 256: return attend_instance_rv<256>(rv);
+        case 384: return attend_instance_rv<384>(rv);
+        default: return nullptr;
+    }
+}
+
 }  // namespace
 
 extern "C" size_t nkv_attend_workspace_size(const nkv_attend_args* a) {
@@ -627,6 +833,7 @@ extern "C" int nkv_attend(void* stream, const nkv_attend_args* a, void* workspac
     p.H = a->H;
     p.S = pl.splits;
     p.q_tiles = pl.q_tiles;
+    p.q_per_tile = pl.q_per_tile;
     p.Q = a->Q;
     p.N = a->N;
     p.Nc = a->Nc;
@@ -646,8 +853,8 @@ extern "C" int nkv_attend(void* stream, const nkv_attend_args* a, void* workspac
     p.v_sb = a->v_sb;
     p.v_st = a->v_st;
     p.v_sh = a->v_sh;
-    p.key = a->key;
-    p.value = a->value;
+    p.codec[0] = a->key;
+    p.codec[1] = a->value;
     p.out = a->out;
     p.o_sb = a->o_sb;
     p.o_st = a->o_st;
@@ -665,15 +872,19 @@ extern "C" int nkv_attend(void* stream, const nkv_attend_args* a, void* workspac
         p.S = 1;
     }
     const size_t smem = sizeof(AttendSmem);
-    static bool attr_set = false;
-    if (!attr_set) {
-        NKV_HIP_CHECK(hipFuncSetAttribute((const void*)attend_kernel,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        attr_set = true;
-    }
     const int64_t blocks = (int64_t)a->B * a->H * pl.q_tiles * p.S;
-    attend_kernel<<<dim3((unsigned)blocks), 256, smem, s>>>(p);
+    // ranks of the history codecs select the kernel instance (with no history
+    // any instance works: the decode path is never entered)
+    const int rk = a->N > 0 ? a->key.r : 384, rv = a->N > 0 ? a->value.r : 384;
+    auto kernel = attend_instance(rk, rv);
+    NKV_REQUIRE(kernel, NKV_ERR_UNSUPPORTED,
+                "fused attend supports codec ranks 64, 128, 256 and 384");
+    NKV_HIP_CHECK(hipFuncSetAttribute((const void*)kernel,
+                                      hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+    if (a->ev_kernel_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)a->ev_kernel_begin, s));
+    kernel<<<dim3((unsigned)blocks), AT_THREADS, smem, s>>>(p);
     NKV_LAUNCH_CHECK();
+    if (a->ev_kernel_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)a->ev_kernel_end, s));
     if (p.S > 1) {
         const int64_t threads = (int64_t)a->B * a->H * a->Q * (AT_D / 4);
         combine_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(p);

@@ -267,12 +267,16 @@ def _strides_bthd(t: torch.Tensor, name: str) -> tuple[int, int, int]:
 def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
            key: Optional[Codec] = None, value: Optional[Codec] = None, *,
            softmax_scale: Optional[float] = None, return_lse: bool = True,
-           splits: int = 0, out: Optional[torch.Tensor] = None):
+           splits: int = 0, out: Optional[torch.Tensor] = None,
+           kernel_events: Optional[tuple[int, int]] = None,
+           workspace: Optional[torch.Tensor] = None):
     """Fused decode+attention (see nkv_attend).
 
     q [B, Q, H, D] bf16; k_cur/v_cur [B, Nc, H, D] bf16 or None; key/value
     history codecs (both or neither).  Returns (out [B, Q, H, D] bf16,
-    lse [B, H, Q] fp32 or None).
+    lse [B, H, Q] fp32 or None).  kernel_events: optional (begin, end) raw
+    hipEvent_t handles recorded around the fused kernel.  workspace: optional
+    preallocated uint8 buffer of at least nkv_attend_workspace_size bytes.
     """
     device = _require_gpu(q, k_cur, v_cur)
     if q.dtype != torch.bfloat16:
@@ -311,13 +315,30 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
     args.o_sb, args.o_st, args.o_sh = _strides_bthd(out, "out")
     lse = torch.empty((B, H, Qn), device=device, dtype=torch.float32) if return_lse else None
     args.lse = _ptr(lse)
+    if kernel_events is not None:
+        args.ev_kernel_begin, args.ev_kernel_end = kernel_events
     need = lib().nkv_attend_workspace_size(byref(args))
     err = lib().nkv_last_error().decode()
     if need == 0 and err:
         raise _lib.NanoKVError("nkv_attend_workspace_size", _lib.NKV_ERR_INVALID, err)
-    ws = torch.empty(need, device=device, dtype=torch.uint8) if need else None
-    check("nkv_attend", lib().nkv_attend(_stream(device), byref(args), _ptr(ws), need))
+    if need and (workspace is None or workspace.numel() < need):
+        workspace = torch.empty(need, device=device, dtype=torch.uint8)
+    check("nkv_attend", lib().nkv_attend(_stream(device), byref(args),
+                                         _ptr(workspace) if need else None, need))
     return out, lse
+
+
+def attend_workspace_size(q: torch.Tensor, n_hist: int, n_cur: int, key: Optional[Codec],
+                          value: Optional[Codec], splits: int = 0) -> int:
+    """Workspace bytes nkv_attend needs for this problem (0 if none)."""
+    B, Qn, H, D = (int(v) for v in q.shape)
+    args = NkvAttendArgs()
+    args.B, args.H, args.D, args.splits, args.Q, args.N, args.Nc = B, H, D, splits, Qn, n_hist, n_cur
+    if key is not None:
+        args.key, args.value = key.struct(), value.struct()
+    args.q, args.out = q.data_ptr(), q.data_ptr()
+    args.k_cur = args.v_cur = q.data_ptr()
+    return int(lib().nkv_attend_workspace_size(byref(args)))
 
 
 def lse_merge(a: torch.Tensor, lse_a: torch.Tensor, b: torch.Tensor, lse_b: torch.Tensor,

@@ -214,11 +214,12 @@ def residual_bf16(x, centers_bf16, ids, mean) -> np.ndarray:
     return out
 
 
-def project(rows_bf16, w_bf16) -> np.ndarray:
-    """rows @ w^T with bf16 operands, accumulated in fp64, rounded once to fp32."""
-    a = bf16_to_f32(rows_bf16).astype(np.float64)
-    w = bf16_to_f32(w_bf16).astype(np.float64)
-    return (a @ w.T).astype(np.float32)
+def project(rows_bf16, w_bf16, dtype=np.float64) -> np.ndarray:
+    """rows @ w^T with bf16 operands, accumulated in `dtype` (fp64 by default),
+    returned as fp32."""
+    a = bf16_to_f32(rows_bf16).astype(dtype, copy=False)
+    w = bf16_to_f32(w_bf16).astype(dtype, copy=False)
+    return np.matmul(a, w.T).astype(np.float32, copy=False)
 
 
 def encode(x, w_enc_bf16, centers_bf16=None, mean=None, group: int = 32,
@@ -234,19 +235,20 @@ def encode(x, w_enc_bf16, centers_bf16=None, mean=None, group: int = 32,
 
 # ----------------------------------------------------------------- a7/a8
 def decode(packed, scales, w_dec_bf16, group: int, scale_dtype: str = "bf16", ids=None,
-           centers_bf16=None, mean=None, row_index=None, columns=None) -> np.ndarray:
+           centers_bf16=None, mean=None, row_index=None, columns=None,
+           dtype=np.float64) -> np.ndarray:
     """Full-width decode of one batch item's rows (MG:393-455) -> bf16 bits.
 
     rows = bf16(bf16(latent @ W^T + bf16(mean)) + center[id]).  The GEMM is
-    accumulated in fp64 and rounded once to fp32.  `columns` (optional index
-    array) restricts the output to those HD columns.
+    accumulated in `dtype` (fp64 by default) and rounded once to fp32.
+    `columns` (optional index array) restricts the output to those HD columns.
     """
     w = _c(w_dec_bf16, np.uint16)
     r = w.shape[1]
     latent = unpack_latent(packed, scales, r, group, scale_dtype, row_index)
     if columns is not None:
         w = w[np.asarray(columns)]
-    acc = project(latent, w)
+    acc = np.ascontiguousarray(project(latent, w, dtype))
     hd = w.shape[0]
     cent = None
     if centers_bf16 is not None:
@@ -270,24 +272,28 @@ def decode(packed, scales, w_dec_bf16, group: int, scale_dtype: str = "bf16", id
 
 
 # ----------------------------------------------------------------- a10-a12
-def attention(q, k, v, scale: float):
-    """softmax(q k^T * scale) v per head in float64 (wan_video_dit.py:42-82).
+def attention(q, k, v, scale: float, dtype=np.float64):
+    """softmax(q k^T * scale) v per head (wan_video_dit.py:42-82), computed in
+    `dtype` (float64 by default).
 
-    q [H, Q, D], k/v [H, N, D] (float arrays).  Returns (out [H, Q, D] f64,
+    q [H, Q, D], k/v [H, N, D] (float arrays).  Returns (out [H, Q, D],
     lse [H, Q] natural log).  An empty key set gives (0, -inf) as
     attention_lse does (CN/core.py:48-49).
     """
-    q = np.asarray(q, np.float64)
-    k = np.asarray(k, np.float64)
-    v = np.asarray(v, np.float64)
+    q = np.asarray(q, dtype)
+    k = np.asarray(k, dtype)
+    v = np.asarray(v, dtype)
     H, Qn, _ = q.shape
     if k.shape[1] == 0:
-        return np.zeros((H, Qn, v.shape[2])), np.full((H, Qn), -np.inf)
-    s = np.einsum("hqd,hkd->hqk", q, k) * scale
+        return np.zeros((H, Qn, v.shape[2]), dtype), np.full((H, Qn), -np.inf, dtype)
+    s = np.matmul(q, k.transpose(0, 2, 1))
+    s *= dtype(scale)
     m = s.max(-1, keepdims=True)
-    e = np.exp(s - m)
-    l = e.sum(-1, keepdims=True)
-    out = np.einsum("hqk,hkd->hqd", e / l, v)
+    s -= m
+    np.exp(s, out=s)
+    l = s.sum(-1, keepdims=True)
+    s /= l
+    out = np.matmul(s, v)
     return out, (m + np.log(l))[..., 0]
 
 
@@ -304,13 +310,15 @@ def merge(out_a, lse_a, out_b, lse_b):
 
 
 def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Optional[dict],
-                  scale: float, heads: Optional[Sequence[int]] = None, D: int = 128):
+                  scale: float, heads: Optional[Sequence[int]] = None, D: int = 128,
+                  dtype=np.float64):
     """Reference decode-then-SDPA path for one batch item.
 
     q [Q, H, D] bf16 bits; k_cur/v_cur [Nc, H, D] bf16 bits or None; key/value
     are dicts with the decode() keyword arguments (packed, scales, w_dec_bf16,
     group, scale_dtype, ids, centers_bf16, mean) or None.  Returns
-    (out [Q, H', D] f64, lse [H', Q]) for the selected heads.
+    (out [Q, H', D], lse [H', Q]) for the selected heads, computed in `dtype`
+    (float64 for parity checks; float32 is the reference's CPU arithmetic).
     """
     q = bf16_to_f32(q_bf16)
     Qn, H = q.shape[0], q.shape[1]
@@ -318,8 +326,8 @@ def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Op
     cols = np.concatenate([np.arange(h * D, (h + 1) * D) for h in heads])
     ks, vs = [], []
     if key is not None:
-        kd = bf16_to_f32(decode(**key, columns=cols))
-        vd = bf16_to_f32(decode(**value, columns=cols))
+        kd = bf16_to_f32(decode(**key, columns=cols, dtype=dtype))
+        vd = bf16_to_f32(decode(**value, columns=cols, dtype=dtype))
         ks.append(kd.reshape(-1, len(heads), D))
         vs.append(vd.reshape(-1, len(heads), D))
     if k_cur_bf16 is not None:
@@ -331,7 +339,7 @@ def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Op
     else:
         k = np.zeros((len(heads), 0, D))
         v = np.zeros((len(heads), 0, D))
-    out, lse = attention(q[:, heads].transpose(1, 0, 2), k, v, scale)
+    out, lse = attention(q[:, heads].transpose(1, 0, 2), k, v, scale, dtype)
     return out.transpose(1, 0, 2), lse
 
 
