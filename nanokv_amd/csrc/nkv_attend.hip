@@ -41,7 +41,6 @@ constexpr int AT_THREADS = 256;
 constexpr int AT_QB = 2;                      // 32-query blocks per wave
 constexpr int AT_BM = 4 * AT_QB * 32;         // at most 256 queries per block
 constexpr int AT_RMAX = 384;
-constexpr int AT_KSTEPS = AT_RMAX / 16;       // MFMA k-steps of the decode
 constexpr int AT_ZPAD = 8;
 constexpr int AT_KPAD = 8;
 constexpr int AT_VPAD = 4;

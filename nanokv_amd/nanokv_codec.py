@@ -1,0 +1,510 @@
+"""NanoKV codec API on the gfx950 kernels.
+
+Mirrors the function names, payload dicts and error behaviour of the
+reference codec module models/Matrix-Game-3.5/fast/diffsynth/models/
+nanokv_codec.py (cited below as MG:line), so a caller of encode_tensor /
+decode_value / concat_values / select_value / decode_pair_selected /
+direct_latent_pair_segments can switch to this module unchanged.
+
+Differences from the reference, all additive:
+  * payload keys "scale_group", "scale_dtype" and "id_dtype" record the scale
+    layout (group width, bf16/fp16) and the id width; "scale" is
+    [B, S, r/group] (group == r is the reference's one-scale-per-row [B,S,1]);
+  * shared center tables can be registered per (kind, layer) with
+    register_centers(); encode_tensor then assigns rows to them (nkv_assign)
+    instead of fitting per-chunk C64 centers.
+
+Operators (encoder [r, HD], decoder [HD, r], mean [HD]) are registered with
+register_operator() or loaded from the reference's prepacked operator file
+with preload_operator_weights().  All compute goes through libnanokv_hip.so
+(nanokv_amd.ops); there is no CPU path.
+"""
+from __future__ import annotations
+
+import os
+from typing import Any, Optional
+
+import torch
+
+from . import ops
+
+CODEC = "worldplay_c64_pca_int4_v1"
+RAW = "worldplay_raw_v1"
+SEGMENTS = "worldplay_segments_v1"
+PREPACKED_FORMAT = "mg35_worldplay_operator_int8_v1"
+
+_OPERATORS: dict = {}
+_CENTERS: dict = {}
+
+
+# ---------------------------------------------------------------- settings
+def enabled() -> bool:
+    """MG:17-18."""
+    return os.environ.get("MG35_KVCODEC_MODE", "").strip().lower() == "worldplay_method"
+
+
+def _target_enabled(kind: str) -> bool:
+    """MG:28-32."""
+    target = os.environ.get("MG35_KVCODEC_TARGET", "both").strip().lower()
+    if target not in {"k", "v", "both"}:
+        raise ValueError(f"unsupported MG35_KVCODEC_TARGET={target!r}")
+    return target == "both" or target == kind
+
+
+def _scale_group(r: int) -> int:
+    """NANOKV_SCALE_GROUP: 0 (default) = one scale per row as the reference."""
+    g = int(os.environ.get("NANOKV_SCALE_GROUP", "0") or 0)
+    return r if g <= 0 else g
+
+
+def _scale_dtype() -> torch.dtype:
+    v = os.environ.get("NANOKV_SCALE_DTYPE", "bf16").strip().lower()
+    if v in {"bf16", "bfloat16"}:
+        return torch.bfloat16
+    if v in {"fp16", "float16", "half"}:
+        return torch.float16
+    raise ValueError(f"unsupported NANOKV_SCALE_DTYPE={v!r}")
+
+
+def _quant_mode() -> str:
+    """bf16 (default) reproduces MG's bf16 quantiser arithmetic (MG:349-351);
+    fp32 is HY's (kv_codecs.py:244-255)."""
+    v = os.environ.get("NANOKV_QUANT_MODE", "bf16").strip().lower()
+    if v not in {"bf16", "fp32"}:
+        raise ValueError(f"unsupported NANOKV_QUANT_MODE={v!r}")
+    return v
+
+
+# ---------------------------------------------------------------- operators
+def register_operator(kind: str, layer: int, *, encoder: torch.Tensor, decoder: torch.Tensor,
+                      mean: Optional[torch.Tensor] = None) -> None:
+    """Register the codec operator of (kind, layer): encoder [r, HD] and decoder
+    [HD, r] as bf16 (F.linear weight layouts, MG:134-153), mean [HD] fp32."""
+    if kind not in {"k", "v"}:
+        raise ValueError(kind)
+    enc = encoder.detach().to(torch.bfloat16).contiguous()
+    dec = decoder.detach().to(torch.bfloat16).contiguous()
+    if enc.dim() != 2 or dec.dim() != 2 or enc.shape[0] != dec.shape[1] or enc.shape[1] != dec.shape[0]:
+        raise ValueError("encoder must be [r, HD] and decoder [HD, r]")
+    m = None if mean is None else mean.detach().float().reshape(-1).contiguous()
+    _OPERATORS[(kind, int(layer))] = {"encoder": enc, "decoder": dec, "mean": m}
+
+
+def register_centers(kind: str, layer: int, centers: Optional[torch.Tensor]) -> None:
+    """Shared center table [C, HD] (bf16) for (kind, layer); None removes it."""
+    if centers is None:
+        _CENTERS.pop((kind, int(layer)), None)
+        return
+    _CENTERS[(kind, int(layer))] = centers.detach().to(torch.bfloat16).contiguous()
+
+
+def _dequant_int8(packed: dict) -> torch.Tensor:
+    """bf16(int8 weight) * bf16 group scale -> bf16, as _operator_linear (MG:145-152)."""
+    q = packed["qweight"]
+    g = int(packed["group_size"])
+    w = q.reshape(q.shape[0], -1, g).to(torch.bfloat16) * packed["scale"][:, :, None].to(torch.bfloat16)
+    return w.reshape(q.shape)
+
+
+def preload_operator_weights(device: torch.device, path: Optional[str] = None) -> None:
+    """Load every operator of the reference's prepacked file (format
+    mg35_worldplay_operator_int8_v1, MG:257-279) onto `device`."""
+    path = path or os.environ.get("MG35_KVCODEC_PREPACKED_OPERATOR_PATH", "").strip()
+    if not path:
+        raise RuntimeError("formal worldplay_method requires MG35_KVCODEC_PREPACKED_OPERATOR_PATH")
+    payload = torch.load(path, map_location="cpu", weights_only=True)
+    if payload.get("format") != PREPACKED_FORMAT:
+        raise RuntimeError(f"bad prepacked WorldPlay operator: {path}")
+    for name in sorted(payload["entries"]):
+        kind, layer = name.split(":", 1)
+        entry = payload["entries"][name]
+        register_operator(kind, int(layer), encoder=_dequant_int8(entry["encoder"]).to(device),
+                          decoder=_dequant_int8(entry["decoder"]).to(device),
+                          mean=entry["mean"].float().to(device))
+
+
+def _operator(kind: str, layer: int, device: torch.device) -> dict:
+    key = (kind, int(layer))
+    if key not in _OPERATORS:
+        raise RuntimeError(f"no codec operator registered for {kind}:{int(layer):02d}")
+    op = _OPERATORS[key]
+    if op["encoder"].device != device:
+        op = {k: (None if v is None else v.to(device)) for k, v in op.items()}
+        _OPERATORS[key] = op
+    return op
+
+
+# ---------------------------------------------------------------- centers
+@torch.no_grad()
+def semantic_residual_centers(value: torch.Tensor, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-chunk joint-head C64 fit of MG:301-330 (randperm init seeded with
+    20260804 + layer, `iterations` rounds of fp32 distance argmin and mean
+    update).  Returns (bf16 centers [B, C, HD], labels [B, S] int64) where the
+    labels are those of the last assignment round, as in the reference."""
+    batch, sequence, dim = value.shape
+    rows = value.float()
+    clusters = int(os.environ.get("MG35_KVCODEC_C64_CLUSTERS", "64"))
+    iterations = int(os.environ.get("MG35_KVCODEC_C64_ITERS", "2"))
+    if clusters <= 0 or clusters > sequence or clusters > 256:
+        raise ValueError(f"C64 clusters must be in [1,min(S,256)], got {clusters}")
+    generator = torch.Generator(device="cpu").manual_seed(20260804 + int(layer))
+    initial = torch.randperm(sequence, generator=generator)[:clusters].to(rows.device)
+    centers = rows.index_select(1, initial).clone()
+    row_norm = rows.square().sum(-1, keepdim=True)
+    labels = torch.zeros((batch, sequence), dtype=torch.long, device=rows.device)
+    for _ in range(iterations):
+        distances = (row_norm + centers.square().sum(-1).unsqueeze(1)
+                     - 2.0 * torch.bmm(rows, centers.transpose(1, 2)))
+        labels = distances.argmin(-1)
+        assignment = torch.nn.functional.one_hot(labels, num_classes=clusters).transpose(1, 2).float()
+        counts = assignment.sum(-1)
+        updated = torch.bmm(assignment, rows) / counts.clamp_min(1.0).unsqueeze(-1)
+        centers = torch.where((counts > 0).unsqueeze(-1), updated, centers)
+    return centers.to(torch.bfloat16), labels
+
+
+# ---------------------------------------------------------------- encode
+@torch.no_grad()
+def encode_tensor(kind: str, layer: int, value: torch.Tensor) -> dict:
+    """Encode one chunk [B, S, HD] into an immutable payload (MG:333-365).
+
+    With a registered shared center table every row is assigned to its
+    nearest center (nkv_assign); otherwise per-chunk C64 centers are fitted
+    as the reference does.  Projection and INT4 quantisation run in
+    nkv_encode."""
+    if kind not in {"k", "v"}:
+        raise ValueError(kind)
+    if not _target_enabled(kind):
+        return {"codec": RAW, "tensor": value.detach()}
+    if value.dim() != 3:
+        raise ValueError("encode_tensor expects [B, S, HD]")
+    batch, seq, dim = (int(v) for v in value.shape)
+    op = _operator(kind, layer, value.device)
+    r = int(op["encoder"].shape[0])
+    group = _scale_group(r)
+    sdt = _scale_dtype()
+    qmode = _quant_mode()
+    rows = value.detach().float().contiguous()
+    shared = _CENTERS.get((kind, int(layer)))
+    packed, scales, ids_out, tables = [], [], [], []
+    if shared is not None:
+        shared = shared.to(value.device)
+        id_dtype = ops.id_dtype_for(int(shared.shape[0]))
+        for b in range(batch):
+            e = ops.encode(rows[b], op["encoder"], centers=shared, mean=op["mean"], group=group,
+                           scale_dtype=sdt, quant_mode=qmode, id_dtype=id_dtype)
+            packed.append(e["packed"])
+            scales.append(e["scales"])
+            ids_out.append(e["ids"])
+        centers = shared[None]
+        center_batch_shared = True
+    else:
+        fitted, labels = semantic_residual_centers(value, layer)
+        id_dtype = torch.uint8
+        for b in range(batch):
+            # the fit's labels are kept (MG:326-330), so the encoder is given
+            # the rows with their assigned stored center already subtracted
+            resid = rows[b] - fitted[b].float()[labels[b]]
+            e = ops.encode(resid.contiguous(), op["encoder"], centers=None, mean=op["mean"],
+                           group=group, scale_dtype=sdt, quant_mode=qmode)
+            packed.append(e["packed"])
+            scales.append(e["scales"])
+            ids_out.append(labels[b].to(torch.uint8))
+        centers = fitted
+        center_batch_shared = False
+    return {
+        "codec": CODEC,
+        "kind": kind,
+        "layer": int(layer),
+        "shape": (batch, seq, dim),
+        "latent_shape": (batch, seq, r),
+        "latent_numel": batch * seq * r,
+        "packed_codes": torch.stack(packed).reshape(-1),
+        "scale": torch.stack(scales),
+        "centers": centers,
+        "ids": torch.stack(ids_out),
+        "semantic": True,
+        "source_dtype": str(value.dtype).replace("torch.", ""),
+        "scale_group": group,
+        "scale_dtype": "fp16" if sdt == torch.float16 else "bf16",
+        "id_dtype": str(id_dtype).replace("torch.", ""),
+        "shared_centers": center_batch_shared,
+    }
+
+
+def encode_raw_tensor(value: torch.Tensor) -> dict:
+    """Cache-owned bf16 copy of a raw segment (MG:458-469)."""
+    return {"codec": RAW, "tensor": value.detach().clone(memory_format=torch.contiguous_format)}
+
+
+# ---------------------------------------------------------------- views
+def is_payload(value: Any) -> bool:
+    """MG:472-486 (the payload kinds this module produces)."""
+    return isinstance(value, dict) and value.get("codec") in {RAW, CODEC, SEGMENTS}
+
+
+def segments_of(value: Any) -> list:
+    if value is None:
+        return []
+    if isinstance(value, dict) and value.get("codec") == SEGMENTS:
+        return list(value["segments"])
+    return [value]
+
+
+def value_shape(value: Any) -> tuple[int, int, int] | None:
+    """MG:489-513."""
+    if value is None:
+        return None
+    if torch.is_tensor(value):
+        return tuple(int(v) for v in value.shape)
+    codec = value.get("codec")
+    if codec == RAW:
+        return tuple(int(v) for v in value["tensor"].shape)
+    if codec == CODEC:
+        return tuple(int(v) for v in value["shape"])
+    if codec == SEGMENTS:
+        shapes = [value_shape(item) for item in value["segments"]]
+        if not shapes:
+            return None
+        return (shapes[0][0], sum(s[1] for s in shapes), shapes[0][2])
+    raise RuntimeError(f"unsupported cache value {codec}")
+
+
+def payload_bytes(value: Any) -> int:
+    """Resident bytes of a payload tree (MG:697-704)."""
+    if torch.is_tensor(value):
+        return value.numel() * value.element_size()
+    if isinstance(value, dict):
+        return sum(payload_bytes(v) for k, v in value.items() if not str(k).startswith("_"))
+    if isinstance(value, (list, tuple)):
+        return sum(payload_bytes(v) for v in value)
+    return 0
+
+
+def concat_values(left: Any, right: Any) -> Any:
+    """Append immutable segments (MG:600-609)."""
+    if left is None:
+        return right
+    if right is None:
+        return left
+    if not is_payload(left) or not is_payload(right):
+        raise RuntimeError("WorldPlay packed-cache concat received a raw/payload mixture")
+    return {"codec": SEGMENTS, "segments": segments_of(left) + segments_of(right)}
+
+
+def codec_view(part: dict, device: torch.device) -> ops.Codec:
+    """Device tensors of one encoded segment as an ops.Codec."""
+    if part.get("codec") != CODEC:
+        raise RuntimeError(f"unsupported WorldPlay payload {part.get('codec')}")
+    batch, seq, _ = (int(v) for v in part["shape"])
+    r = int(part["latent_shape"][-1])
+    op = _operator(str(part["kind"]), int(part["layer"]), device)
+    group = int(part.get("scale_group", r))
+    scale = part["scale"].to(device)
+    if scale.dtype not in (torch.bfloat16, torch.float16):
+        scale = scale.to(torch.bfloat16)
+    scale = scale.reshape(batch, seq, r // group).contiguous()
+    centers = ids = None
+    if part.get("semantic", True) and part.get("centers") is not None:
+        centers = part["centers"].to(device)
+        if centers.dim() == 2:
+            centers = centers[None]
+        centers = centers.to(torch.bfloat16).contiguous()
+        ids = part["ids"].to(device).reshape(batch, seq)
+        if ids.dtype not in (torch.uint8, torch.int16, torch.int32):
+            ids = ids.to(ops.id_dtype_for(int(centers.shape[1])))
+        ids = ids.contiguous()
+    return ops.Codec(packed=part["packed_codes"].to(device).reshape(batch, seq, r // 2),
+                     scales=scale, w_dec=op["decoder"], group=group, ids=ids,
+                     centers=centers, mean=op["mean"])
+
+
+# ---------------------------------------------------------------- decode
+@torch.no_grad()
+def decode_tensor(payload: dict, *, dtype: torch.dtype, device: torch.device) -> torch.Tensor:
+    """Full-width decode of one payload (MG:368-390) on nkv_decode."""
+    if payload.get("codec") == RAW:
+        return payload["tensor"].to(device=device, dtype=dtype)
+    view = codec_view(payload, torch.device(device))
+    out = ops.decode(view, int(payload["shape"][2]))
+    return out.to(dtype)
+
+
+def decode_value(value: Any, *, dtype: torch.dtype, device: torch.device) -> torch.Tensor | None:
+    """MG:516-539: raw tensors pass through; segment lists decode per segment
+    (each with its own center table) and concatenate along tokens."""
+    if value is None:
+        return None
+    if torch.is_tensor(value):
+        return value.to(device=device, dtype=dtype)
+    if value.get("codec") == SEGMENTS:
+        parts = [decode_value(item, dtype=dtype, device=device) for item in value["segments"]]
+        return torch.cat(parts, dim=1) if parts else None
+    return decode_tensor(value, dtype=dtype, device=device)
+
+
+def decode_pair_values(key: Any, value: Any, *, dtype: torch.dtype, device: torch.device):
+    """MG:542-597."""
+    return (decode_value(key, dtype=dtype, device=device),
+            decode_value(value, dtype=dtype, device=device))
+
+
+def select_value(value: Any, token_idx: torch.Tensor, *, kind: str, layer: int,
+                 dtype: torch.dtype, device: torch.device) -> Any:
+    """Select tokens keeping whole immutable segments (MG:612-694): fully
+    selected segments are reused, a cut segment is decoded, sliced and
+    re-encoded."""
+    if torch.is_tensor(value):
+        return value.index_select(1, token_idx).contiguous()
+    parts = segments_of(value)
+    wanted = token_idx.detach().cpu().tolist()
+    if wanted != sorted(wanted):
+        raise RuntimeError("segmented cache selection expects sorted in-range token indices")
+    out, offset, cursor = [], 0, 0
+    for part in parts:
+        length = int(value_shape(part)[1])
+        local = []
+        while cursor < len(wanted) and wanted[cursor] < offset + length:
+            local.append(wanted[cursor] - offset)
+            cursor += 1
+        if local:
+            if local == list(range(length)):
+                out.append(part)
+            else:
+                tensor = decode_value(part, dtype=dtype, device=device)
+                sel = tensor.index_select(1, torch.as_tensor(local, device=tensor.device))
+                if part.get("codec") == RAW:
+                    out.append(encode_raw_tensor(sel))
+                else:
+                    out.append(encode_tensor(kind, layer, sel.contiguous()))
+        offset += length
+    if cursor != len(wanted):
+        raise RuntimeError("segmented cache selection expects sorted in-range token indices")
+    if not out:
+        return None
+    if len(out) == 1:
+        return out[0]
+    return {"codec": SEGMENTS, "segments": out}
+
+
+def _pairs(key: Any, value: Any) -> list:
+    kp, vp = segments_of(key), segments_of(value)
+    if len(kp) != len(vp):
+        raise ValueError("paired codec segment count mismatch")
+    for k, v in zip(kp, vp):
+        if (k.get("codec") != CODEC or v.get("codec") != CODEC or k.get("kind") != "k"
+                or v.get("kind") != "v" or tuple(k["shape"]) != tuple(v["shape"])
+                or int(k["layer"]) != int(v["layer"])):
+            raise RuntimeError("codec-native attention requires paired formal method payloads")
+    return list(zip(kp, vp))
+
+
+@torch.no_grad()
+def decode_pair_selected(key: Any, value: Any, token_keep: torch.Tensor, *, dtype: torch.dtype,
+                         device: torch.device):
+    """Decode only the kept rows (MG:801-861) with nkv_decode's row index."""
+    pairs = _pairs(key, value)
+    keep = token_keep.to(device="cpu", dtype=torch.bool).reshape(-1)
+    if keep.numel() != sum(int(k["shape"][1]) for k, _ in pairs):
+        raise ValueError("selected decode mask/cache length mismatch")
+    outs = {"k": [], "v": []}
+    offset = 0
+    dev = torch.device(device)
+    for kpart, vpart in pairs:
+        length = int(kpart["shape"][1])
+        local = keep[offset:offset + length]
+        offset += length
+        if not bool(local.any()):
+            continue
+        index = torch.nonzero(local, as_tuple=False).flatten().to(torch.int32).to(dev)
+        for target, part in (("k", kpart), ("v", vpart)):
+            view = codec_view(part, dev)
+            outs[target].append(ops.decode(view, int(part["shape"][2]), row_index=index).to(dtype))
+    if not outs["k"]:
+        shape = value_shape(key)
+        empty = torch.empty((shape[0], 0, shape[2]), device=device, dtype=dtype)
+        return empty, empty.clone()
+    return torch.cat(outs["k"], 1), torch.cat(outs["v"], 1)
+
+
+@torch.no_grad()
+def direct_latent_pair_segments(key: Any, value: Any, *, device: torch.device,
+                                token_keep: Optional[torch.Tensor] = None) -> list:
+    """Expose the bf16 latent rows, center tables/ids and mean of each paired
+    segment without reconstructing K/V (MG:707-798); latents come from
+    nkv_unpack."""
+    pairs = _pairs(key, value)
+    wanted = None
+    if token_keep is not None:
+        wanted = token_keep.to(device="cpu", dtype=torch.bool).reshape(-1)
+        if wanted.numel() != sum(int(k["shape"][1]) for k, _ in pairs):
+            raise ValueError("direct latent token mask/cache length mismatch")
+    dev = torch.device(device)
+    result, offset = [], 0
+    for kpart, vpart in pairs:
+        length = int(kpart["shape"][1])
+        local = None if wanted is None else wanted[offset:offset + length]
+        offset += length
+        if local is not None and not bool(local.any()):
+            continue
+        index = None if local is None else torch.nonzero(local, as_tuple=False).flatten()
+
+        def expose(part):
+            view = codec_view(part, dev)
+            B, S = view.batch, view.tokens
+            r = view.r
+            rows = []
+            for b in range(B):
+                idx = None if index is None else index.to(torch.int32).to(dev)
+                rows.append(ops.unpack(view.packed[b], view.scales[b], r, view.group, idx))
+            latent = torch.stack(rows)
+            ids = None if view.ids is None else view.ids.long()
+            if ids is not None and index is not None:
+                ids = ids.index_select(1, index.to(dev))
+            centers = None if view.centers is None else view.centers.float()
+            return latent, (centers, ids), view.mean
+
+        logical = torch.arange(offset - length, offset, device=dev)
+        if index is not None:
+            logical = logical.index_select(0, index.to(dev))
+        result.append({"k": expose(kpart), "v": expose(vpart), "length": int(logical.numel()),
+                       "logical_indices": logical})
+    return result
+
+
+def history_codecs(key: Any, value: Any, device: torch.device):
+    """One (K, V) ops.Codec pair covering every segment of a paired cache: the
+    packed codes, scales and ids are concatenated along tokens and the
+    per-segment center tables are concatenated with each segment's ids offset
+    into the combined table (int16/int32 ids when it exceeds 256 rows)."""
+    pairs = _pairs(key, value)
+    out = []
+    for which in (0, 1):
+        views = [codec_view(p[which], device) for p in pairs]
+        if len({(v.r, v.group, v.scales.dtype) for v in views}) != 1:
+            raise RuntimeError("history segments must share rank, scale group and scale dtype")
+        packed = torch.cat([v.packed for v in views], 1)
+        scales = torch.cat([v.scales for v in views], 1)
+        ids = centers = None
+        if all(v.centers is not None for v in views):
+            shared = all(v.centers is views[0].centers for v in views) or (
+                len(views) > 0 and all(v.centers.data_ptr() == views[0].centers.data_ptr()
+                                       for v in views))
+            if shared:
+                centers = views[0].centers
+                ids = torch.cat([v.ids for v in views], 1)
+            else:
+                tables, id_parts, base = [], [], 0
+                for v in views:
+                    tables.append(v.centers)
+                    id_parts.append(v.ids.to(torch.int32) + base)
+                    base += int(v.centers.shape[1])
+                centers = torch.cat(tables, 1).contiguous()
+                ids = torch.cat(id_parts, 1)
+                ids = ids.to(ops.id_dtype_for(base)).contiguous() if base <= 65536 else ids
+        elif any(v.centers is not None for v in views):
+            raise RuntimeError("history segments mix semantic and pca payloads")
+        out.append(ops.Codec(packed=packed.contiguous(), scales=scales.contiguous(),
+                             w_dec=views[0].w_dec, group=views[0].group, ids=ids,
+                             centers=centers, mean=views[0].mean))
+    return out[0], out[1]
