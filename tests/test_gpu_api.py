@@ -1,0 +1,99 @@
+"""The reference-compatible API end to end on the GPU: encode_tensor chunks,
+concat_values segment lists, decode_value / decode_pair_selected and the
+fused codec_history_attention, against the oracle's decode-then-attend."""
+import numpy as np
+import pytest
+import torch
+
+import oracle.oracle as orc
+from nanokv_amd import codec_native, nanokv_codec as nc, synth
+from tests._helpers import max_abs_cos, u16
+
+pytestmark = pytest.mark.gpu
+
+H, D = 2, 128
+
+
+def _setup(dev, layer, shared, monkeypatch, r=128, C=16):
+    monkeypatch.setenv("NANOKV_SCALE_GROUP", "32")
+    monkeypatch.setenv("NANOKV_SCALE_DTYPE", "fp16")
+    monkeypatch.setenv("NANOKV_QUANT_MODE", "fp32")
+    monkeypatch.setenv("MG35_KVCODEC_C64_CLUSTERS", "8")
+    sh = synth.Shape("api", H=H, D=D, N=0, Q=0, Nc=0, rK=r, rV=r, G=32, C=C)
+    lay = synth.make_layer(sh, seed=layer, with_mean=True)
+    nc.register_operator("k", layer, encoder=lay.w_enc_k.to(dev), decoder=lay.w_dec_k.to(dev),
+                         mean=lay.mean_k.to(dev))
+    nc.register_operator("v", layer, encoder=lay.w_enc_v.to(dev), decoder=lay.w_dec_v.to(dev),
+                         mean=lay.mean_v.to(dev))
+    nc.register_centers("k", layer, lay.centers_k.to(dev) if shared else None)
+    nc.register_centers("v", layer, lay.centers_v.to(dev) if shared else None)
+    return sh, lay
+
+
+def _oracle_rows(payload, dev):
+    """Oracle decode of one encoded segment (batch item 0) -> float32 [S, HD]."""
+    view = nc.codec_view(payload, dev)
+    return orc.bf16_to_f32(orc.decode(
+        view.packed[0].cpu().numpy(), u16(view.scales[0]), u16(view.w_dec), view.group, "fp16",
+        view.ids[0].cpu().numpy().astype(np.int64), u16(view.centers[0]),
+        view.mean.cpu().numpy()))
+
+
+@pytest.mark.parametrize("shared", [True, False])
+def test_encode_concat_attend(dev, monkeypatch, shared):
+    layer = 3 if shared else 4
+    sh, lay = _setup(dev, layer, shared, monkeypatch)
+    chunks_k, chunks_v = [], []
+    cache_k = cache_v = None
+    for c in range(3):
+        k = synth.history_rows(sh, lay.centers_k, 40, seed=10 + c).to(dev)[None].to(torch.bfloat16)
+        v = synth.history_rows(sh, lay.centers_v, 40, seed=20 + c).to(dev)[None].to(torch.bfloat16)
+        pk, pv = nc.encode_tensor("k", layer, k), nc.encode_tensor("v", layer, v)
+        assert pk["codec"] == nc.CODEC and pk["scale"].shape == (1, 40, 4)
+        chunks_k.append(pk)
+        chunks_v.append(pv)
+        cache_k, cache_v = nc.concat_values(cache_k, pk), nc.concat_values(cache_v, pv)
+    assert nc.value_shape(cache_k) == (1, 120, H * D)
+    # decode_value: per-segment decode, concatenated, vs the oracle
+    dk = nc.decode_value(cache_k, dtype=torch.bfloat16, device=dev)[0].float().cpu().numpy()
+    ref_k = np.concatenate([_oracle_rows(p, dev) for p in chunks_k], 0)
+    np.testing.assert_allclose(dk, ref_k, rtol=2 ** -7, atol=2 ** -7)
+    ref_v = np.concatenate([_oracle_rows(p, dev) for p in chunks_v], 0)
+    # decode_pair_selected returns exactly the decode_value rows
+    keep = torch.zeros(120, dtype=torch.bool)
+    keep[[0, 5, 41, 119]] = True
+    sk, sv = nc.decode_pair_selected(cache_k, cache_v, keep, dtype=torch.bfloat16, device=dev)
+    full_k = nc.decode_value(cache_k, dtype=torch.bfloat16, device=dev)
+    assert torch.equal(sk, full_k[:, keep.to(dev)])
+    # fused history attention vs decode-then-attend
+    g = torch.Generator().manual_seed(7)
+    q = (torch.randn(1, H, 50, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev)
+    kc = torch.randn(1, H, 16, D, generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn(1, H, 16, D, generator=g).to(torch.bfloat16).to(dev)
+    out, lse = codec_native.codec_history_attention(q, cache_k, cache_v, kc, vc, return_lse=True)
+    kk = np.concatenate([ref_k.reshape(120, H, D), orc.bf16_to_f32(u16(kc[0].permute(1, 0, 2)))], 0)
+    vv = np.concatenate([ref_v.reshape(120, H, D), orc.bf16_to_f32(u16(vc[0].permute(1, 0, 2)))], 0)
+    ro, rl = orc.attention(orc.bf16_to_f32(u16(q[0])), kk.transpose(1, 0, 2), vv.transpose(1, 0, 2),
+                           D ** -0.5)
+    diff, cos = max_abs_cos(out[0].float().cpu().numpy(), ro)
+    assert diff <= 2e-2 and cos >= 0.9995, (diff, cos)
+    assert np.abs(lse[0].cpu().numpy() - rl).max() < 2e-3
+
+
+def test_attention_lse_and_merge(dev):
+    g = torch.Generator().manual_seed(9)
+    q = torch.randn(1, H, 30, D, generator=g).to(torch.bfloat16).to(dev)
+    k = torch.randn(1, H, 70, D, generator=g).to(torch.bfloat16).to(dev)
+    v = torch.randn(1, H, 70, D, generator=g).to(torch.bfloat16).to(dev)
+    o1, l1 = codec_native.attention_lse(q, k[:, :, :25], v[:, :, :25])
+    o2, l2 = codec_native.attention_lse(q, k[:, :, 25:], v[:, :, 25:])
+    om, lm = codec_native.merge(o1, l1, o2, l2)
+    oj, lj = codec_native.attention_lse(q, k, v)
+    diff, cos = max_abs_cos(om.float().cpu().numpy(), oj.float().cpu().numpy())
+    assert diff < 1e-2 and cos > 0.9999
+    ref, ref_l = orc.attention(q[0].float().cpu().numpy(), k[0].float().cpu().numpy(),
+                               v[0].float().cpu().numpy(), D ** -0.5)
+    diff, cos = max_abs_cos(oj[0].float().cpu().numpy(), ref)
+    assert diff <= 2e-2 and cos >= 0.9995
+    oe, le = codec_native.attention_lse(q, k[:, :, :0], v[:, :, :0])
+    assert torch.all(oe == 0) and torch.all(torch.isneginf(le))
