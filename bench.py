@@ -41,7 +41,10 @@ def parse():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", type=int, default=1, choices=(1, 2))
-    ap.add_argument("--splits", type=int, default=0, help="history splits (0 = automatic)")
+    ap.add_argument("--splits", type=int, default=0,
+                    help="query_tiles key splits (0 = automatic)")
+    ap.add_argument("--schedule", default="auto", choices=("auto", "query_tiles", "key_chunks"),
+                    help="work decomposition of the fused kernel")
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="time budget of the CPU-baseline head sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
@@ -129,12 +132,14 @@ def main():
     shape = synth.CONFIGS[args.config]
     layer, codecs, q, kc, vc = build_inputs(shape, device)
     out = torch.empty_like(q)
-    ws_bytes = ops.attend_workspace_size(q, shape.N, shape.Nc, codecs[0], codecs[1], args.splits)
+    ws_bytes = ops.attend_workspace_size(q, shape.N, shape.Nc, codecs[0], codecs[1], args.splits,
+                                         args.schedule)
     ws = torch.empty(max(ws_bytes, 1), device=device, dtype=torch.uint8)
 
     def step(events=None):
         return ops.attend(q, kc, vc, codecs[0], codecs[1], out=out, splits=args.splits,
-                          return_lse=False, workspace=ws, kernel_events=events)
+                          return_lse=False, workspace=ws, kernel_events=events,
+                          schedule=args.schedule)
 
     if args.profile_kernel:
         # A plain copy of known size (for FETCH_SIZE/WRITE_SIZE calibration), then the kernel.

@@ -45,7 +45,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 1
+#define NKV_ABI_VERSION 2
 
 enum nkv_status {
     NKV_OK = 0,
@@ -56,6 +56,21 @@ enum nkv_status {
 };
 
 enum nkv_scale_dtype { NKV_DTYPE_BF16 = 0, NKV_DTYPE_FP16 = 1 };
+
+/* Work decomposition of nkv_attend.  Both give the same attention (within
+ * bf16 rounding of the partials); they differ in cost:
+ *  QUERY_TILES  a block owns a 256-query tile and a range of 32-key tiles,
+ *               so every history tile is decoded once per query tile;
+ *               partials only across the `splits` key ranges.
+ *  KEY_CHUNKS   a block owns one 256-key chunk (decoded once, kept in LDS)
+ *               and attends every query to it; each chunk leaves a bf16
+ *               partial output + LSE per query that a combine kernel merges.
+ *  AUTO         KEY_CHUNKS when the queries span more than one query tile. */
+enum nkv_schedule {
+    NKV_SCHEDULE_AUTO = 0,
+    NKV_SCHEDULE_QUERY_TILES = 1,
+    NKV_SCHEDULE_KEY_CHUNKS = 2
+};
 
 /* Arithmetic of the quantiser (see nkv_quant_pack). */
 enum nkv_quant_mode { NKV_QUANT_FP32 = 0, NKV_QUANT_BF16 = 1 };
@@ -186,12 +201,12 @@ typedef struct nkv_attend_args {
     int B;
     int H;
     int D;
-    int splits;                   /* history splits; 0 = choose automatically */
+    int splits;                   /* QUERY_TILES key splits; 0 = choose automatically */
     int64_t Q;
     int64_t N;
     int64_t Nc;
     float softmax_scale;
-    int _pad;
+    int schedule;                 /* NKV_SCHEDULE_*: work decomposition */
     const uint16_t* q;
     int64_t q_sb, q_st, q_sh;
     const uint16_t* k_cur;

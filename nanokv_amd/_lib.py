@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libnanokv_hip.so"
 
-NKV_ABI_VERSION = 1
+NKV_ABI_VERSION = 2
 NKV_OK = 0
 NKV_ERR_INVALID = -1
 NKV_ERR_UNSUPPORTED = -2
@@ -24,6 +24,9 @@ NKV_DTYPE_BF16 = 0
 NKV_DTYPE_FP16 = 1
 NKV_QUANT_FP32 = 0
 NKV_QUANT_BF16 = 1
+NKV_SCHEDULE_AUTO = 0
+NKV_SCHEDULE_QUERY_TILES = 1
+NKV_SCHEDULE_KEY_CHUNKS = 2
 
 # Every symbol include/nanokv.h declares (checked by tests/test_abi.py).
 EXPORTED = (
@@ -63,7 +66,7 @@ class NkvAttendArgs(Structure):
     _fields_ = [
         ("B", c_int), ("H", c_int), ("D", c_int), ("splits", c_int),
         ("Q", c_int64), ("N", c_int64), ("Nc", c_int64),
-        ("softmax_scale", c_float), ("_pad", c_int),
+        ("softmax_scale", c_float), ("schedule", c_int),
         ("q", c_void_p), ("q_sb", c_int64), ("q_st", c_int64), ("q_sh", c_int64),
         ("k_cur", c_void_p), ("k_sb", c_int64), ("k_st", c_int64), ("k_sh", c_int64),
         ("v_cur", c_void_p), ("v_sb", c_int64), ("v_st", c_int64), ("v_sh", c_int64),

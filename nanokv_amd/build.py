@@ -28,6 +28,7 @@ SOURCES = {
     # MFMA accumulators in VGPRs: the fused kernel's softmax/rescale VALU work
     # runs on them every tile, and its read-only decoder fragments fill AGPRs
     "nkv_attend.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "nkv_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 COMMON = [

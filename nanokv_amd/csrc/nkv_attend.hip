@@ -32,6 +32,7 @@
 // Keeping queries on the MFMA column axis (S^T, O^T) makes every softmax
 // statistic lane-local except one exchange between the two half-waves.
 #include "nkv_common.h"
+#include "nkv_internal.h"
 
 namespace nkv {
 
@@ -75,34 +76,6 @@ struct AttendParams {
     float* ws_o;   // [S, B, H, Q, D]   (S > 1)
     float* ws_ml;  // [S, B, H, Q, 2]
 };
-
-__device__ __forceinline__ int read_id(const void* ids, int id_bytes, int64_t i) {
-    if (id_bytes == 1) return reinterpret_cast<const uint8_t*>(ids)[i];
-    if (id_bytes == 2) return reinterpret_cast<const uint16_t*>(ids)[i];
-    return reinterpret_cast<const int32_t*>(ids)[i];
-}
-
-__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
-    bf16x8 r;
-    __builtin_memcpy(&r, &v, 16);
-    return r;
-}
-
-__device__ __forceinline__ bf16x8 lds_b128(const uint16_t* p) {
-    return *reinterpret_cast<const bf16x8*>(p);
-}
-
-// Two 8-byte LDS reads forming one bf16x8 operand: p[0..3] and p[8..11].
-__device__ __forceinline__ bf16x8 lds_2x64(const uint16_t* p) {
-    u32x2 a = *reinterpret_cast<const u32x2*>(p);
-    u32x2 b = *reinterpret_cast<const u32x2*>(p + 8);
-    u32x4 v = {a[0], a[1], b[0], b[1]};
-    return as_bf16x8(v);
-}
-
-__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-}
 
 // Packed-code streaming.  Thread t owns the work items it = t + 256*e
 // (e < AT_ITEMS) of every tile: item it < rK covers 32 K codes (16 bytes,
@@ -808,10 +781,34 @@ AttendKernel attend_instance(int rk, int rv) {
 
 }  // namespace
 
+namespace {
+
+// Resolve NKV_SCHEDULE_AUTO: key chunks once the queries span more than one
+// query tile (each history tile would otherwise be decoded once per tile)
+// and the codecs fit the chunk kernel; query tiles otherwise.
+int resolve_schedule(const nkv_attend_args* a, int* schedule) {
+    NKV_REQUIRE(a->schedule >= NKV_SCHEDULE_AUTO && a->schedule <= NKV_SCHEDULE_KEY_CHUNKS,
+                NKV_ERR_INVALID, "unknown schedule");
+    int sch = a->schedule;
+    if (sch == NKV_SCHEDULE_AUTO) {
+        const bool fits = a->D == 128 &&
+                          (a->N == 0 || (a->key.r % 64 == 0 && a->value.r % 64 == 0 &&
+                                         a->key.group % 32 == 0 && a->value.group % 32 == 0));
+        sch = (fits && a->Q > AT_BM) ? NKV_SCHEDULE_KEY_CHUNKS : NKV_SCHEDULE_QUERY_TILES;
+    }
+    *schedule = sch;
+    return NKV_OK;
+}
+
+}  // namespace
+
 extern "C" size_t nkv_attend_workspace_size(const nkv_attend_args* a) {
     clear_error();
     AttendPlan pl;
     if (plan_attend(a, &pl)) return 0;
+    int sch;
+    if (resolve_schedule(a, &sch)) return 0;
+    if (sch == NKV_SCHEDULE_KEY_CHUNKS) return chunk_check(a) ? 0 : chunk_workspace_bytes(a);
     return workspace_bytes_for(a, pl);
 }
 
@@ -821,8 +818,12 @@ extern "C" int nkv_attend(void* stream, const nkv_attend_args* a, void* workspac
     AttendPlan pl;
     int rc = plan_attend(a, &pl);
     if (rc) return rc;
+    int sch;
+    rc = resolve_schedule(a, &sch);
+    if (rc) return rc;
     if (a->Q == 0) return NKV_OK;
     hipStream_t s = (hipStream_t)stream;
+    if (sch == NKV_SCHEDULE_KEY_CHUNKS) return chunk_attend_launch(s, a, workspace, workspace_bytes);
     const size_t need = workspace_bytes_for(a, pl);
     NKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), NKV_ERR_WORKSPACE,
                 "workspace missing or smaller than nkv_attend_workspace_size()");

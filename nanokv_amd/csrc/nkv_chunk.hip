@@ -1,0 +1,625 @@
+// nkv_chunk.hip -- key-chunk-major fused decode + attention for gfx950
+// (NKV_SCHEDULE_KEY_CHUNKS of nkv_attend).
+//
+// A 256-thread block (4 waves, one per SIMD) owns one (batch, head, chunk)
+// of 256 keys.  It decodes the chunk's K and V once into LDS -- K[key][d]
+// and V^T[d][key], bf16, 136 KB -- and then every wave attends its share of
+// ALL query tiles (64 queries each) to those keys.  Each (query, chunk)
+// leaves a partial: the chunk-local softmax output O / l as bf16 and its
+// log2-sum-exp m + log2(l) as fp32.  A combine kernel merges the partials of
+// every query by log-sum-exp (CN/core.py:33-42 applied over all chunks).
+// Decoding each history key once per head, instead of once per query tile,
+// removes the decode GEMM's re-execution; the price is the partial traffic
+// (256 + 4 bytes per query and chunk).
+//
+// Decode (per wave: 64 keys of the chunk, both codecs; MFMA 32x32x16 bf16):
+//   K^T = W_K[h*128 + d, :] . Z^T   (A = decoder rows, B = unpacked codes)
+//   V   = Z . W_V[h*128 + d, :]^T   (A = unpacked codes, B = decoder rows)
+// The k (rank) axis is walked in blocks of 64: lane half hf supplies
+// k = 64*kq + 32*hf + 8*j + [0, 8) at step j of block kq.  That permutation of
+// the summation index is applied to both operands, so one 16-byte load per
+// lane fetches the packed codes of four MFMA steps, and they share one scale
+// group (group % 32 == 0).  Decoder rows come straight from global memory
+// (L2-resident per head).  The epilogue is the reference decode arithmetic
+// bf16(bf16(acc + bf16(mean)) + center[id]) (MG:438-454); the accumulator
+// orientation puts four consecutive d (K) or four consecutive keys (V) in
+// one lane, so both tiles are written with 8-byte LDS stores.
+// Current-chunk keys (uncompressed bf16) are copied instead of decoded.
+//
+// Attention (per wave and 64-query tile; queries on the MFMA column axis):
+//   S^T = K Q^T, P = exp2(S * c - m), O^T += V^T P^T
+// over eight 32-key steps, software-pipelined: step j's softmax (VALU) runs
+// between the MFMAs of step j+1's scores and step j-1's PV product, which
+// do not depend on it.  The running max is raised only when a score exceeds
+// it by more than 2^8 (P <= 256 otherwise), so O is rarely rescaled.
+#include "nkv_common.h"
+#include "nkv_internal.h"
+
+namespace nkv {
+
+constexpr int CK_T = 256;        // keys per chunk
+constexpr int CK_D = 128;        // head dim
+constexpr int CK_THREADS = 256;  // 4 waves
+constexpr int CK_KROW = CK_D + 8;   // K row: 68 dwords (b128 reads conflict-free)
+constexpr int CK_VROW = CK_T + 4;   // V^T row: 130 dwords (b64 reads conflict-free)
+constexpr int CK_QT = 64;        // queries per wave tile
+constexpr float CK_TAU = 8.0f;   // lazy-rescale threshold (log2 units)
+
+struct ChunkSmem {
+    uint16_t k[CK_T][CK_KROW];    // K[key][d]
+    uint16_t vt[CK_D][CK_VROW];   // V^T[d][key]
+    int ids[2][CK_T];             // center ids of the chunk's keys (K, V)
+    float bias[2][CK_D];          // bf16(mean) of this head (K, V)
+};
+
+struct ChunkParams {
+    int B, H, HD;
+    int nch_hist, nch_total;
+    int64_t Q, N, Nc;
+    float scale_log2;
+    const uint16_t* q;
+    int64_t q_sb, q_st, q_sh;
+    const uint16_t* k_cur;
+    int64_t k_sb, k_st, k_sh;
+    const uint16_t* v_cur;
+    int64_t v_sb, v_st, v_sh;
+    nkv_codec codec[2];
+    uint16_t* part_o;   // [B*H, Q, nch_total, 128] bf16
+    float* part_lse;    // [B*H, Q, nch_total] log2 domain
+    uint16_t* out;
+    int64_t o_sb, o_st, o_sh;
+    float* lse;
+};
+
+// ------------------------------------------------------------------ decode
+// This wave's 64 keys (64*wave + [0, 64) of the chunk) of codec CODEC.
+template <int CODEC>
+__device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, int b, int h,
+                                             int HD, int64_t N, int64_t tok0, int valid,
+                                             int wave, int lane) {
+    const int hf = lane >> 5, l32 = lane & 31;
+    const int R = c.r, KQ = R >> 6, G = c.group, NG = R / G;
+    const bool f16 = c.scale_dtype == NKV_DTYPE_FP16;
+    const uint8_t* prow[2];
+    const uint16_t* srow[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int tl = 64 * wave + 32 * tt + l32;
+        // keys past the chunk end decode key 0's codes (finite, never attended)
+        const int64_t tok = (int64_t)b * N + tok0 + (tl < valid ? tl : 0);
+        prow[tt] = c.packed + tok * (R / 2) + 16 * hf;
+        srow[tt] = c.scales + tok * NG;
+    }
+    const uint16_t* wrow[4];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+        wrow[dt] = c.w_dec + (int64_t)(h * CK_D + 32 * dt + l32) * R + 32 * hf;
+
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[dt][tt] = f32x16{};
+
+    auto load = [&](int kq, u32x4 (&pk)[2], float (&sc)[2], u32x4 (&wf)[4][4]) {
+        const int gi = (64 * kq + 32 * hf) / G;
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            pk[tt] = *reinterpret_cast<const u32x4*>(prow[tt] + 32 * kq);
+            const uint16_t sb = srow[tt][gi];
+            sc[tt] = f16 ? f16_bits_to_f32(sb) : bf16_bits_to_f32(sb);
+        }
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int j = 0; j < 4; ++j)
+                wf[dt][j] = *reinterpret_cast<const u32x4*>(wrow[dt] + 64 * kq + 8 * j);
+    };
+
+    u32x4 pk[2], wf[4][4];
+    float sc[2];
+    load(0, pk, sc, wf);
+    for (int kq = 0; kq < KQ; ++kq) {
+        u32x4 pkn[2], wfn[4][4];
+        float scn[2];
+        if (kq + 1 < KQ) load(kq + 1, pkn, scn, wfn);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+            bf16x8 z[2];
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) z[tt] = unpack8(pk[tt][j], sc[tt], -7.0f * sc[tt]);
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt)
+                    acc[dt][tt] = CODEC == 0 ? mfma32(as_bf16x8(wf[dt][j]), z[tt], acc[dt][tt])
+                                             : mfma32(z[tt], as_bf16x8(wf[dt][j]), acc[dt][tt]);
+        }
+        if (kq + 1 < KQ) {
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                pk[tt] = pkn[tt];
+                sc[tt] = scn[tt];
+            }
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) wf[dt][j] = wfn[dt][j];
+        }
+    }
+
+    const bool has_c = c.centers != nullptr;
+    const uint16_t* cent =
+        has_c ? c.centers + (int64_t)b * c.centers_batch_stride + h * CK_D : nullptr;
+    const bool has_bias = c.mean != nullptr;
+    if (CODEC == 0) {
+        // acc[dt][tt] element i: d = 32*dt + 8*(i/4) + 4*hf + i%4, key 64*wave + 32*tt + l32
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int t = 64 * wave + 32 * tt + l32;
+            const uint16_t* crow = has_c ? cent + (int64_t)sm.ids[0][t] * HD + 4 * hf : nullptr;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = 32 * dt + 8 * g + 4 * hf;
+                    float a[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        a[e] = acc[dt][tt][4 * g + e] + (has_bias ? sm.bias[0][d + e] : 0.0f);
+                    const u32x2 cw = has_c ? *reinterpret_cast<const u32x2*>(crow + 32 * dt + 8 * g)
+                                           : u32x2{0, 0};
+                    u32x2 r;
+#pragma unroll
+                    for (int h2 = 0; h2 < 2; ++h2) {
+                        const uint32_t pr = pack_bf16x2(a[2 * h2], a[2 * h2 + 1]);
+                        r[h2] = pack_bf16x2(
+                            __uint_as_float(pr << 16) + __uint_as_float(cw[h2] << 16),
+                            __uint_as_float(pr & 0xffff0000u) +
+                                __uint_as_float(cw[h2] & 0xffff0000u));
+                    }
+                    *reinterpret_cast<u32x2*>(&sm.k[t][d]) = r;
+                }
+        }
+    } else {
+        // acc[dt][tt] element i: key 64*wave + 32*tt + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int t0 = 64 * wave + 32 * tt + 8 * g + 4 * hf;
+                const uint16_t* crow[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e)
+                    crow[e] = has_c ? cent + (int64_t)sm.ids[1][t0 + e] * HD + l32 : nullptr;
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const int d = 32 * dt + l32;
+                    const float bias = has_bias ? sm.bias[1][d] : 0.0f;
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float a = bf16_round(acc[dt][tt][4 * g + e] + bias);
+                        const float cv = has_c ? bf16_bits_to_f32(crow[e][32 * dt]) : 0.0f;
+                        v[e] = a + cv;
+                    }
+                    const u32x2 r = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    *reinterpret_cast<u32x2*>(&sm.vt[d][t0]) = r;
+                }
+            }
+    }
+}
+
+// Current-chunk keys: copy K rows, transpose V into V^T (rows past the end
+// are zero).
+__device__ __forceinline__ void load_current_chunk(ChunkSmem& sm, const ChunkParams& p, int b,
+                                                   int h, int64_t tok0, int valid, int t) {
+    const bool ok = t < valid;
+    const uint16_t* ks = p.k_cur + (int64_t)b * p.k_sb + (tok0 + (ok ? t : 0)) * p.k_st +
+                         (int64_t)h * p.k_sh;
+    const uint16_t* vs = p.v_cur + (int64_t)b * p.v_sb + (tok0 + (ok ? t : 0)) * p.v_st +
+                         (int64_t)h * p.v_sh;
+#pragma unroll 4
+    for (int e = 0; e < CK_D / 8; ++e) {
+        u32x4 kv = *reinterpret_cast<const u32x4*>(ks + 8 * e);
+        u32x4 vv = *reinterpret_cast<const u32x4*>(vs + 8 * e);
+        if (!ok) kv = vv = u32x4{0, 0, 0, 0};
+        *reinterpret_cast<u32x4*>(&sm.k[t][8 * e]) = kv;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            sm.vt[8 * e + 2 * i][t] = (uint16_t)(vv[i] & 0xffffu);
+            sm.vt[8 * e + 2 * i + 1][t] = (uint16_t)(vv[i] >> 16);
+        }
+    }
+}
+
+// --------------------------------------------------------------- attention
+// One wave attends queries [q0, q0 + 32*NQB) to the chunk in LDS.  FULL: the
+// chunk has all 256 keys (eight pipelined steps); otherwise nsub steps with
+// the last one masked to `valid` keys.
+template <int NQB, bool FULL>
+__device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkParams& p, int b,
+                                             int h, int bh, int chunk, int64_t q0, int nsub,
+                                             int valid, int lane) {
+    const int hf = lane >> 5, l32 = lane & 31;
+    const float c = p.scale_log2;
+
+    // Q^T operand fragments, with the same permuted d walk as the K reads;
+    // columns past the last query repeat query q0 (finite, never stored)
+    bf16x8 qf[NQB][8];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        const int64_t qi = q0 + 32 * qb + l32;
+        const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (qi < p.Q ? qi : q0) * p.q_st +
+                               (int64_t)h * p.q_sh + 32 * hf;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk)
+            qf[qb][kk] = as_bf16x8(
+                *reinterpret_cast<const u32x4*>(qrow + 64 * (kk >> 2) + 8 * (kk & 3)));
+    }
+
+    f32x16 o[NQB][4];
+    float m[NQB], l[NQB];
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        m[qb] = -INFINITY;
+        l[qb] = 0.0f;
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[qb][db] = f32x16{};
+    }
+
+    // K fragments of step j (shared by both query blocks)
+    // Fragment addresses are an opaque per-tile base plus compile-time
+    // offsets (< 64 KiB, folded into the ds_read instructions); without the
+    // opaque step the compiler hoists one address register per unrolled
+    // fragment out of the query-tile loop and spills.
+    uint32_t koff = l32 * CK_KROW + 32 * hf, voff = l32 * CK_VROW + 4 * hf;
+    asm volatile("" : "+v"(koff));
+    asm volatile("" : "+v"(voff));
+    const uint16_t* kbase = &sm.k[0][0] + koff;
+    const uint16_t* vbase = &sm.vt[0][0] + voff;
+    auto load_k = [&](int j, bf16x8 (&kf)[8]) {
+        const uint16_t* kr = kbase + 32 * j * CK_KROW;
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) kf[kk] = lds_b128(kr + 64 * (kk >> 2) + 8 * (kk & 3));
+    };
+    // V^T fragments of step j: P^T operand slot jj of half-step ts holds key
+    // 16*ts + 8*(jj/4) + 4*hf + jj%4 (accumulator element 8*ts + jj of S^T),
+    // and V^T is read with the same key permutation.
+    auto load_v = [&](int j, bf16x8 (&vf)[2][4]) {
+#pragma unroll
+        for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+                vf[ts][db] = lds_2x64(vbase + 32 * db * CK_VROW + 32 * j + 16 * ts);
+    };
+    auto qk = [&](int qb, const bf16x8 (&kf)[8], f32x16& s) {
+        s = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < 8; ++kk) s = mfma32(kf[kk], qf[qb][kk], s);
+    };
+    auto pv = [&](int qb, const bf16x8 (&vf)[2][4], const bf16x8 (&pb)[2]) {
+#pragma unroll
+        for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[qb][db] = mfma32(vf[ts][db], pb[ts], o[qb][db]);
+    };
+    // online softmax of one 32-key x 32-query score tile; returns whether
+    // this lane raised its running max (then O must be scaled by alpha)
+    auto softmax = [&](int qb, f32x16& s, bf16x8 (&pb)[2], float& alpha) {
+        float tmax = fmaxf(s[0], s[1]);
+#pragma unroll
+        for (int i = 2; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
+        // the max is taken on raw scores (c > 0 preserves order)
+        tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * c;
+        const bool up = tmax > m[qb] + CK_TAU;
+        const float m_new = up ? tmax : m[qb];
+        alpha = up ? __builtin_amdgcn_exp2f(m[qb] - m_new) : 1.0f;
+        m[qb] = m_new;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            // v_exp_f32 of arguments <= 8; results below 2^-126 flush to 0
+            const float e = __builtin_amdgcn_exp2f(fmaf(s[i], c, -m_new));
+            s[i] = e;
+            lsum += e;
+        }
+        l[qb] = l[qb] * alpha + lsum;
+#pragma unroll
+        for (int ts = 0; ts < 2; ++ts) {
+            u32x4 v;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = pack_bf16x2(s[8 * ts + 2 * e], s[8 * ts + 2 * e + 1]);
+            pb[ts] = as_bf16x8(v);
+        }
+        return up;
+    };
+    auto rescale = [&](int qb, float alpha) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[qb][db][i] *= alpha;
+    };
+
+    constexpr int NSTEP = CK_T / 32;
+    if (FULL && NQB == 2) {
+        // Two query blocks staggered by half a step: block 0's softmax runs
+        // under block 1's MFMAs and vice versa.  Per step j:
+        //   X: S1 = QK(j), O1 += PV(j-1)      | softmax(S0 of step j)
+        //   Y: S0 = QK(j+1), O0 += PV(j)      | softmax(S1 of step j)
+        f32x16 s0, s1;
+        bf16x8 p0[2], p1[2];
+        bf16x8 kf[8], vprev[2][4];
+        float a0, a1;
+        load_k(0, kf);
+        qk(0, kf, s0);
+#pragma unroll
+        for (int j = 0; j < NSTEP; ++j) {
+            bf16x8 vf[2][4], kn[8];
+            qk(NQB - 1, kf, s1);
+            if (j > 0) pv(NQB - 1, vprev, p1);
+            load_v(j, vf);
+            if (j + 1 < NSTEP) load_k(j + 1, kn);
+            const bool up0 = softmax(0, s0, p0, a0);
+            if (j > 0 && __any(up0)) rescale(0, a0);
+            if (j + 1 < NSTEP) qk(0, kn, s0);
+            pv(0, vf, p0);
+            const bool up1 = softmax(NQB - 1, s1, p1, a1);
+            if (j > 0 && __any(up1)) rescale(NQB - 1, a1);
+#pragma unroll
+            for (int kk = 0; kk < 8; ++kk) kf[kk] = kn[kk];
+#pragma unroll
+            for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) vprev[ts][db] = vf[ts][db];
+        }
+        pv(NQB - 1, vprev, p1);
+    } else if (FULL) {
+        // one query block: step j+1's scores and step j-1's PV under step j's softmax
+        f32x16 s[2];
+        bf16x8 pp[2][2], kf[8], vprev[2][4];
+        float a0;
+        load_k(0, kf);
+        qk(0, kf, s[0]);
+#pragma unroll
+        for (int j = 0; j < NSTEP; ++j) {
+            const int cur = j & 1, nxt = cur ^ 1;
+            bf16x8 vf[2][4];
+            if (j + 1 < NSTEP) {
+                load_k(j + 1, kf);
+                qk(0, kf, s[nxt]);
+            }
+            if (j > 0) pv(0, vprev, pp[nxt]);
+            load_v(j, vf);
+            const bool up = softmax(0, s[cur], pp[cur], a0);
+            if (j > 0 && __any(up)) rescale(0, a0);
+#pragma unroll
+            for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+                for (int db = 0; db < 4; ++db) vprev[ts][db] = vf[ts][db];
+        }
+        pv(0, vprev, pp[(NSTEP - 1) & 1]);
+    } else {
+        for (int j = 0; j < nsub; ++j) {
+            bf16x8 kf[8], vf[2][4];
+            load_k(j, kf);
+            load_v(j, vf);
+            const int vj = valid - 32 * j;
+            int hfo = hf;  // opaque: keeps the mask constants out of the outer loop
+            asm volatile("" : "+v"(hfo));
+#pragma unroll
+            for (int qb = 0; qb < NQB; ++qb) {
+                f32x16 s;
+                bf16x8 pb[2];
+                float a;
+                qk(qb, kf, s);
+                if (vj < 32) {
+#pragma unroll
+                    for (int i = 0; i < 16; ++i)
+                        if (8 * (i >> 2) + 4 * hfo + (i & 3) >= vj) s[i] = -INFINITY;
+                }
+                const bool up = softmax(qb, s, pb, a);
+                if (j > 0 && __any(up)) rescale(qb, a);
+                pv(qb, vf, pb);
+            }
+        }
+    }
+
+    // partial of this chunk: O / l (bf16) and m + log2(l)
+    const int64_t row0 = (int64_t)bh * p.Q;
+#pragma unroll
+    for (int qb = 0; qb < NQB; ++qb) {
+        const float lt = l[qb] + __shfl_xor(l[qb], 32);
+        const int64_t qi = q0 + 32 * qb + l32;
+        if (qi < p.Q) {
+            const float inv = 1.0f / lt;
+            const int64_t prow = (row0 + qi) * p.nch_total + chunk;
+            uint16_t* dst = p.part_o + prow * CK_D + 4 * hf;
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const f32x16& a = o[qb][db];
+                    const u32x2 pk = {pack_bf16x2(a[4 * g] * inv, a[4 * g + 1] * inv),
+                                      pack_bf16x2(a[4 * g + 2] * inv, a[4 * g + 3] * inv)};
+                    *reinterpret_cast<u32x2*>(dst + 32 * db + 8 * g) = pk;
+                }
+            if (hf == 0) p.part_lse[prow] = m[qb] + log2f(lt);
+        }
+    }
+}
+
+__global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    ChunkSmem& sm = *reinterpret_cast<ChunkSmem*>(smem_raw);
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+
+    // block -> (bh, chunk) with bh fastest: with B*H a multiple of 8 all
+    // chunks of one head run on one XCD (blocks go to the 8 XCDs
+    // round-robin), sharing that head's decoder rows, centers and queries in
+    // one L2.  History chunks come first; the cheaper current-chunk blocks
+    // fill the tail.
+    const int BH = p.B * p.H;
+    const int bh = blockIdx.x % BH;
+    const int chunk = blockIdx.x / BH;
+    const int b = bh / p.H, h = bh % p.H;
+    const bool hist = chunk < p.nch_hist;
+    const int64_t tok0 = (int64_t)(hist ? chunk : chunk - p.nch_hist) * CK_T;
+    const int valid = (int)min((int64_t)CK_T, (hist ? p.N : p.Nc) - tok0);
+
+    if (hist) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+            const nkv_codec& cd = p.codec[cc];
+            int id = 0;
+            if (cd.centers && t < valid) {
+                // ids outside the table are clamped so that a corrupt payload
+                // cannot read out of bounds (valid payloads never hold them)
+                id = read_id(cd.ids, cd.id_bytes, (int64_t)b * p.N + tok0 + t);
+                id = min(max(id, 0), cd.num_centers - 1);
+            }
+            sm.ids[cc][t] = id;
+            if (t < CK_D) sm.bias[cc][t] = cd.mean ? bf16_round(cd.mean[h * CK_D + t]) : 0.0f;
+        }
+        __syncthreads();
+        decode_codec<0>(sm, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave, lane);
+        decode_codec<1>(sm, p.codec[1], b, h, p.HD, p.N, tok0, valid, wave, lane);
+    } else {
+        load_current_chunk(sm, p, b, h, tok0, valid, t);
+    }
+    __syncthreads();
+
+    const int nsub = (valid + 31) / 32;
+    const int nqt = (int)cdiv(p.Q, CK_QT);
+    for (int qt = wave; qt < nqt; qt += CK_THREADS / 64) {
+        const int64_t q0 = (int64_t)qt * CK_QT;
+        const bool one = q0 + 32 >= p.Q;
+        if (valid == CK_T) {
+            if (one) attend_qtile<1, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane);
+            else attend_qtile<2, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane);
+        } else {
+            if (one) attend_qtile<1, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane);
+            else attend_qtile<2, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane);
+        }
+    }
+}
+
+// Merge the chunk partials of every (b, h, q) row: 16 threads per row, 8 d
+// each.  out = sum_c 2^(lse_c - M) O_c / sum_c 2^(lse_c - M); no chunks give
+// out = 0 and lse = -inf (CN/core.py:48-49).
+__global__ void __launch_bounds__(256) chunk_combine_kernel(ChunkParams p) {
+    const int64_t rows = (int64_t)p.B * p.H * p.Q;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t row = tid >> 4;
+    const int dg = (int)(tid & 15);
+    if (row >= rows) return;
+    const int NC = p.nch_total;
+    const float* lr = p.part_lse + row * NC;
+    float M = -INFINITY;
+    for (int cc = 0; cc < NC; ++cc) M = fmaxf(M, lr[cc]);
+    const float Mu = M == -INFINITY ? 0.0f : M;
+    float L = 0.0f, acc[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
+    const uint16_t* po = p.part_o + row * NC * CK_D + 8 * dg;
+#pragma unroll 4
+    for (int cc = 0; cc < NC; ++cc) {
+        const float w = exp2f(lr[cc] - Mu);
+        L += w;
+        const u32x4 v = *reinterpret_cast<const u32x4*>(po + (int64_t)cc * CK_D);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            acc[2 * e] += w * __uint_as_float(v[e] << 16);
+            acc[2 * e + 1] += w * __uint_as_float(v[e] & 0xffff0000u);
+        }
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    const int64_t qi = row % p.Q, bhi = row / p.Q;
+    const int h = (int)(bhi % p.H), b = (int)(bhi / p.H);
+    uint16_t* orow = p.out + b * p.o_sb + qi * p.o_st + h * p.o_sh + 8 * dg;
+    u32x4 pk;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) pk[e] = pack_bf16x2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
+    *reinterpret_cast<u32x4*>(orow) = pk;
+    if (p.lse && dg == 0) p.lse[row] = L > 0.0f ? (M + log2f(L)) * 0.69314718055994531f : -INFINITY;
+}
+
+// ------------------------------------------------------------------ host
+size_t chunk_workspace_bytes(const nkv_attend_args* a) {
+    const int64_t nc = cdiv(a->N, CK_T) + cdiv(a->Nc, CK_T);
+    const size_t rows = (size_t)a->B * a->H * a->Q * nc;
+    return rows * CK_D * sizeof(uint16_t) + rows * sizeof(float);
+}
+
+int chunk_check(const nkv_attend_args* a) {
+    NKV_REQUIRE(a->D == CK_D, NKV_ERR_UNSUPPORTED, "key-chunk attend supports D == 128");
+    if (a->N > 0) {
+        for (const nkv_codec* c : {&a->key, &a->value}) {
+            NKV_REQUIRE(c->r > 0 && c->r % 64 == 0 && c->r <= 4096, NKV_ERR_UNSUPPORTED,
+                        "key-chunk attend needs codec ranks that are multiples of 64");
+            NKV_REQUIRE(c->group % 32 == 0, NKV_ERR_UNSUPPORTED,
+                        "key-chunk attend needs scale groups that are multiples of 32");
+        }
+    }
+    return NKV_OK;
+}
+
+int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace,
+                        size_t workspace_bytes) {
+    int rc = chunk_check(a);
+    if (rc) return rc;
+    const size_t need = chunk_workspace_bytes(a);
+    NKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), NKV_ERR_WORKSPACE,
+                "workspace missing or smaller than nkv_attend_workspace_size()");
+    ChunkParams p;
+    p.B = a->B;
+    p.H = a->H;
+    p.HD = a->H * a->D;
+    p.nch_hist = (int)cdiv(a->N, CK_T);
+    p.nch_total = p.nch_hist + (int)cdiv(a->Nc, CK_T);
+    p.Q = a->Q;
+    p.N = a->N;
+    p.Nc = a->Nc;
+    p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
+    p.q = a->q;
+    p.q_sb = a->q_sb;
+    p.q_st = a->q_st;
+    p.q_sh = a->q_sh;
+    p.k_cur = a->k_cur;
+    p.k_sb = a->k_sb;
+    p.k_st = a->k_st;
+    p.k_sh = a->k_sh;
+    p.v_cur = a->v_cur;
+    p.v_sb = a->v_sb;
+    p.v_st = a->v_st;
+    p.v_sh = a->v_sh;
+    p.codec[0] = a->key;
+    p.codec[1] = a->value;
+    const size_t rows = (size_t)a->B * a->H * a->Q * p.nch_total;
+    p.part_o = reinterpret_cast<uint16_t*>(workspace);
+    p.part_lse = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
+                                          rows * CK_D * sizeof(uint16_t));
+    p.out = a->out;
+    p.o_sb = a->o_sb;
+    p.o_st = a->o_st;
+    p.o_sh = a->o_sh;
+    p.lse = a->lse;
+
+    const int64_t blocks = (int64_t)a->B * a->H * p.nch_total;
+    if (a->ev_kernel_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)a->ev_kernel_begin, s));
+    if (blocks > 0) {
+        const size_t smem = sizeof(ChunkSmem);
+        NKV_HIP_CHECK(hipFuncSetAttribute((const void*)chunk_kernel,
+                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
+        chunk_kernel<<<dim3((unsigned)blocks), CK_THREADS, smem, s>>>(p);
+        NKV_LAUNCH_CHECK();
+    }
+    if (a->ev_kernel_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)a->ev_kernel_end, s));
+    const int64_t threads = (int64_t)a->B * a->H * a->Q * 16;
+    chunk_combine_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(p);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+}  // namespace nkv

@@ -94,4 +94,52 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---------------------------------------------------------------- MFMA / LDS helpers
+__device__ __forceinline__ int read_id(const void* ids, int id_bytes, int64_t i) {
+    if (id_bytes == 1) return reinterpret_cast<const uint8_t*>(ids)[i];
+    if (id_bytes == 2) return reinterpret_cast<const uint16_t*>(ids)[i];
+    return reinterpret_cast<const int32_t*>(ids)[i];
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
+    bf16x8 r;
+    __builtin_memcpy(&r, &v, 16);
+    return r;
+}
+
+__device__ __forceinline__ bf16x8 lds_b128(const uint16_t* p) {
+    return *reinterpret_cast<const bf16x8*>(p);
+}
+
+// Two 8-byte LDS reads forming one bf16x8 operand: p[0..3] and p[8..11].
+__device__ __forceinline__ bf16x8 lds_2x64(const uint16_t* p) {
+    u32x2 a = *reinterpret_cast<const u32x2*>(p);
+    u32x2 b = *reinterpret_cast<const u32x2*>(p + 8);
+    u32x4 v = {a[0], a[1], b[0], b[1]};
+    return as_bf16x8(v);
+}
+
+// v_mfma_f32_32x32x16_bf16.  Lane l supplies row l % 32 of A and column
+// l % 32 of B with k = 8 * (l / 32) + [0, 8); accumulator element i of lane l
+// is (row 8*(i/4) + 4*(l/32) + i%4, column l % 32).
+__device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+// Eight INT4 codes of one dword (byte j: code 2j low nibble, 2j+1 high
+// nibble, stored as code + 7) times their group scale s, as the bf16x8 MFMA
+// operand in k order.  (nibble - 7) * s = fma(nibble, s, -7 s): both products
+// are exact in fp32 (<= 15 significant bits), so the fma returns the exact
+// value and the bf16 conversion rounds it once, as the reference does.
+__device__ __forceinline__ bf16x8 unpack8(uint32_t w, float s, float ns7) {
+    const uint32_t ev = w & 0x0f0f0f0fu;         // codes 0, 2, 4, 6 (byte lanes)
+    const uint32_t od = (w >> 4) & 0x0f0f0f0fu;  // codes 1, 3, 5, 7
+    u32x4 o;
+#pragma unroll
+    for (int b = 0; b < 4; ++b)
+        o[b] = pack_bf16x2(fmaf((float)((ev >> (8 * b)) & 0xffu), s, ns7),
+                           fmaf((float)((od >> (8 * b)) & 0xffu), s, ns7));
+    return as_bf16x8(o);
+}
+
 }  // namespace nkv

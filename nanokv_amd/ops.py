@@ -15,12 +15,15 @@ from typing import Optional
 import torch
 
 from . import _lib
-from ._lib import (NKV_DTYPE_BF16, NKV_DTYPE_FP16, NKV_QUANT_BF16, NKV_QUANT_FP32, NkvAttendArgs,
-                   NkvCodec, NkvDecodeArgs, NkvEncodeArgs, check, lib)
+from ._lib import (NKV_DTYPE_BF16, NKV_DTYPE_FP16, NKV_QUANT_BF16, NKV_QUANT_FP32,
+                   NKV_SCHEDULE_AUTO, NKV_SCHEDULE_KEY_CHUNKS, NKV_SCHEDULE_QUERY_TILES,
+                   NkvAttendArgs, NkvCodec, NkvDecodeArgs, NkvEncodeArgs, check, lib)
 
 _SCALE_CODES = {torch.bfloat16: NKV_DTYPE_BF16, torch.float16: NKV_DTYPE_FP16}
 _QUANT_CODES = {"fp32": NKV_QUANT_FP32, "bf16": NKV_QUANT_BF16}
 _ID_BYTES = {torch.uint8: 1, torch.int16: 2, torch.int32: 4}
+SCHEDULES = {"auto": NKV_SCHEDULE_AUTO, "query_tiles": NKV_SCHEDULE_QUERY_TILES,
+             "key_chunks": NKV_SCHEDULE_KEY_CHUNKS}
 if hasattr(torch, "uint16"):
     _ID_BYTES[torch.uint16] = 2
 
@@ -269,7 +272,7 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
            softmax_scale: Optional[float] = None, return_lse: bool = True,
            splits: int = 0, out: Optional[torch.Tensor] = None,
            kernel_events: Optional[tuple[int, int]] = None,
-           workspace: Optional[torch.Tensor] = None):
+           workspace: Optional[torch.Tensor] = None, schedule: str = "auto"):
     """Fused decode+attention (see nkv_attend).
 
     q [B, Q, H, D] bf16; k_cur/v_cur [B, Nc, H, D] bf16 or None; key/value
@@ -277,7 +280,10 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
     lse [B, H, Q] fp32 or None).  kernel_events: optional (begin, end) raw
     hipEvent_t handles recorded around the fused kernel.  workspace: optional
     preallocated uint8 buffer of at least nkv_attend_workspace_size bytes.
+    schedule: "auto", "query_tiles" or "key_chunks" (nkv_schedule).
     """
+    if schedule not in SCHEDULES:
+        raise ValueError(f"schedule must be one of {sorted(SCHEDULES)}")
     device = _require_gpu(q, k_cur, v_cur)
     if q.dtype != torch.bfloat16:
         raise TypeError("q must be bf16")
@@ -286,6 +292,7 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
     args = NkvAttendArgs()
     args.B, args.H, args.D, args.splits, args.Q = B, H, D, int(splits), Qn
     args.softmax_scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
+    args.schedule = SCHEDULES[schedule]
     args.q = q.data_ptr()
     args.q_sb, args.q_st, args.q_sh = _strides_bthd(q, "q")
     if (key is None) != (value is None):
@@ -329,11 +336,12 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
 
 
 def attend_workspace_size(q: torch.Tensor, n_hist: int, n_cur: int, key: Optional[Codec],
-                          value: Optional[Codec], splits: int = 0) -> int:
+                          value: Optional[Codec], splits: int = 0, schedule: str = "auto") -> int:
     """Workspace bytes nkv_attend needs for this problem (0 if none)."""
     B, Qn, H, D = (int(v) for v in q.shape)
     args = NkvAttendArgs()
     args.B, args.H, args.D, args.splits, args.Q, args.N, args.Nc = B, H, D, splits, Qn, n_hist, n_cur
+    args.schedule = SCHEDULES[schedule]
     if key is not None:
         args.key, args.value = key.struct(), value.struct()
     args.q, args.out = q.data_ptr(), q.data_ptr()

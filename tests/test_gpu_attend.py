@@ -14,11 +14,11 @@ MAX_ABS = 2e-2
 MIN_COS = 0.9995
 
 
-def _check(sc, dev, splits=0, heads=None):
+def _check(sc, dev, splits=0, heads=None, schedule="auto"):
     key, value = sc.codecs(dev)
     kc = None if sc.k_cur is None else sc.k_cur.to(dev)
     vc = None if sc.v_cur is None else sc.v_cur.to(dev)
-    out, lse = ops.attend(sc.q.to(dev), kc, vc, key, value, splits=splits)
+    out, lse = ops.attend(sc.q.to(dev), kc, vc, key, value, splits=splits, schedule=schedule)
     out = out.float().cpu().numpy()
     lse = lse.cpu().numpy()
     for b in range(sc.B):
@@ -33,10 +33,22 @@ def _check(sc, dev, splits=0, heads=None):
     return out, lse
 
 
+SCHEDULES = ["query_tiles", "key_chunks"]
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
 @pytest.mark.parametrize("N,Nc,Q", [(200, 64, 100), (257, 37, 300), (64, 0, 1), (0, 100, 33),
                                     (1000, 130, 513)])
-def test_attend_shapes(dev, N, Nc, Q):
-    _check(Scenario(H=2, N=N, Q=Q, Nc=Nc, rK=384, rV=256, G=32, C=16), dev)
+def test_attend_shapes(dev, N, Nc, Q, schedule):
+    _check(Scenario(H=2, N=N, Q=Q, Nc=Nc, rK=384, rV=256, G=32, C=16), dev, schedule=schedule)
+
+
+# key-chunk edges: exact/partial chunks (256 keys), partial 32-key steps,
+# query tiles of 64 with a 1..32-query remainder (single query block)
+@pytest.mark.parametrize("N,Nc,Q", [(256, 0, 64), (512, 256, 128), (255, 1, 65), (1, 31, 96),
+                                    (300, 513, 200), (767, 0, 31), (0, 257, 97)])
+def test_attend_key_chunk_edges(dev, N, Nc, Q):
+    _check(Scenario(H=2, N=N, Q=Q, Nc=Nc, rK=256, rV=384, G=32, C=16), dev, schedule="key_chunks")
 
 
 @pytest.mark.parametrize("splits", [1, 2, 5, 0])
@@ -50,18 +62,38 @@ def test_attend_splits(dev, splits):
     (64, torch.bfloat16, True, torch.int32, True),
     (32, torch.float16, False, torch.uint8, False),
 ])
-def test_attend_codec_variants(dev, G, scale_dtype, with_mean, id_dtype, centers):
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_attend_codec_variants(dev, G, scale_dtype, with_mean, id_dtype, centers, schedule):
     _check(Scenario(H=2, N=300, Q=70, Nc=40, rK=384, rV=384, G=G, C=40, scale_dtype=scale_dtype,
-                    with_mean=with_mean, id_dtype=id_dtype, centers=centers), dev)
+                    with_mean=with_mean, id_dtype=id_dtype, centers=centers), dev,
+           schedule=schedule)
 
 
-def test_attend_batch(dev):
-    _check(Scenario(B=2, H=3, N=150, Q=90, Nc=20, rK=256, rV=256, G=32, C=12), dev)
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_attend_batch(dev, schedule):
+    _check(Scenario(B=2, H=3, N=150, Q=90, Nc=20, rK=256, rV=256, G=32, C=12), dev,
+           schedule=schedule)
 
 
-def test_attend_empty_keys(dev):
+def test_attend_schedules_agree(dev):
+    # the two decompositions compute the same attention; key chunks is AUTO's
+    # choice above one query tile (256 queries)
+    sc = Scenario(H=2, N=900, Q=400, Nc=120, rK=384, rV=384, G=32, C=16)
+    key, value = sc.codecs(dev)
+    q, kc, vc = sc.q.to(dev), sc.k_cur.to(dev), sc.v_cur.to(dev)
+    oa, la = ops.attend(q, kc, vc, key, value, schedule="query_tiles")
+    ob, lb = ops.attend(q, kc, vc, key, value, schedule="key_chunks")
+    oc, lc = ops.attend(q, kc, vc, key, value)
+    diff, cos = max_abs_cos(oa.float().cpu().numpy(), ob.float().cpu().numpy())
+    assert diff < 1e-2 and cos > 0.9999, (diff, cos)
+    assert torch.allclose(la, lb, atol=1e-4)
+    assert torch.equal(oc, ob) and torch.equal(lc, lb)
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_attend_empty_keys(dev, schedule):
     q = torch.randn(1, 5, 2, 128, device=dev).to(torch.bfloat16)
-    out, lse = ops.attend(q, None, None)
+    out, lse = ops.attend(q, None, None, schedule=schedule)
     assert torch.all(out == 0) and torch.all(torch.isneginf(lse))
 
 
@@ -96,7 +128,8 @@ def test_attend_merge_equals_joint(dev):
     assert torch.allclose(lm, lj, atol=1e-4)
 
 
-def test_attend_cfg1_shape_subset_heads(dev):
+@pytest.mark.parametrize("schedule", SCHEDULES)
+def test_attend_cfg1_shape_subset_heads(dev, schedule):
     """Full config-1 call (H=24, D=128, N=12480, Q=Nc=1560, r=384, G=32 fp16,
     C=256), encoded on the GPU; the oracle checks heads 0, 11 and 23."""
     from nanokv_amd import synth
@@ -114,7 +147,7 @@ def test_attend_cfg1_shape_subset_heads(dev):
     vc = synth.history_rows(sh, layer.centers_v, sh.Nc, seed=5, device=dev)
     kc = kc.reshape(1, sh.Nc, sh.H, sh.D).to(torch.bfloat16)
     vc = vc.reshape(1, sh.Nc, sh.H, sh.D).to(torch.bfloat16)
-    out, lse = ops.attend(q, kc, vc, codecs[0], codecs[1])
+    out, lse = ops.attend(q, kc, vc, codecs[0], codecs[1], schedule=schedule)
     heads = [0, 11, 23]
     key = {"packed": codecs[0].packed[0].cpu().numpy(), "scales": u16(codecs[0].scales[0]),
            "w_dec_bf16": u16(layer.w_dec_k), "group": sh.G, "scale_dtype": "fp16",
