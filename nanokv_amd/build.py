@@ -28,7 +28,8 @@ SOURCES = {
     # MFMA accumulators in VGPRs: the fused kernel's softmax/rescale VALU work
     # runs on them every tile, and its read-only decoder fragments fill AGPRs
     "nkv_attend.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
-    "nkv_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    # scores are never NaN (-inf masks are kept): fmaxf needs no NaN quieting
+    "nkv_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"],
 }
 
 COMMON = [

@@ -73,7 +73,9 @@ struct ChunkParams {
 
 // ------------------------------------------------------------------ decode
 // This wave's 64 keys (64*wave + [0, 64) of the chunk) of codec CODEC.
-template <int CODEC>
+// HAS_C: the codec has centers (staged in the wave's K rows); a template
+// argument so that the epilogue is straight-line code.
+template <int CODEC, bool HAS_C>
 __device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, int b, int h,
                                              int HD, int64_t N, int64_t tok0, int valid,
                                              int wave, int lane) {
@@ -148,27 +150,26 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, 
         }
     }
 
-    const bool has_c = c.centers != nullptr;
-    const uint16_t* cent =
-        has_c ? c.centers + (int64_t)b * c.centers_batch_stride + h * CK_D : nullptr;
-    const bool has_bias = c.mean != nullptr;
+    // Epilogue.  The center rows of this wave's keys were staged into its own
+    // K rows of LDS (stage_centers) before the MFMAs, so every center value
+    // is an LDS read.  sm.bias holds bf16(mean) or zeros, so the bias add is
+    // unconditional.
     if (CODEC == 0) {
-        // acc[dt][tt] element i: d = 32*dt + 8*(i/4) + 4*hf + i%4, key 64*wave + 32*tt + l32
+        // acc[dt][tt] element i: d = 32*dt + 8*(i/4) + 4*hf + i%4, key 64*wave + 32*tt + l32;
+        // the result overwrites the staged center it was added to
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int t = 64 * wave + 32 * tt + l32;
-            const uint16_t* crow = has_c ? cent + (int64_t)sm.ids[0][t] * HD + 4 * hf : nullptr;
 #pragma unroll
             for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int d = 32 * dt + 8 * g + 4 * hf;
+                    u32x2* slot = reinterpret_cast<u32x2*>(&sm.k[t][d]);
                     float a[4];
 #pragma unroll
-                    for (int e = 0; e < 4; ++e)
-                        a[e] = acc[dt][tt][4 * g + e] + (has_bias ? sm.bias[0][d + e] : 0.0f);
-                    const u32x2 cw = has_c ? *reinterpret_cast<const u32x2*>(crow + 32 * dt + 8 * g)
-                                           : u32x2{0, 0};
+                    for (int e = 0; e < 4; ++e) a[e] = acc[dt][tt][4 * g + e] + sm.bias[0][d + e];
+                    const u32x2 cw = HAS_C ? *slot : u32x2{0, 0};
                     u32x2 r;
 #pragma unroll
                     for (int h2 = 0; h2 < 2; ++h2) {
@@ -178,7 +179,7 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, 
                             __uint_as_float(pr & 0xffff0000u) +
                                 __uint_as_float(cw[h2] & 0xffff0000u));
                     }
-                    *reinterpret_cast<u32x2*>(&sm.k[t][d]) = r;
+                    *slot = r;
                 }
         }
     } else {
@@ -188,26 +189,39 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, 
 #pragma unroll
             for (int g = 0; g < 4; ++g) {
                 const int t0 = 64 * wave + 32 * tt + 8 * g + 4 * hf;
-                const uint16_t* crow[4];
-#pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    crow[e] = has_c ? cent + (int64_t)sm.ids[1][t0 + e] * HD + l32 : nullptr;
 #pragma unroll
                 for (int dt = 0; dt < 4; ++dt) {
                     const int d = 32 * dt + l32;
-                    const float bias = has_bias ? sm.bias[1][d] : 0.0f;
+                    const float bias = sm.bias[1][d];
                     float v[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float a = bf16_round(acc[dt][tt][4 * g + e] + bias);
-                        const float cv = has_c ? bf16_bits_to_f32(crow[e][32 * dt]) : 0.0f;
-                        v[e] = a + cv;
+                        v[e] = HAS_C ? a + bf16_bits_to_f32(sm.k[t0 + e][d]) : a;
                     }
                     const u32x2 r = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                     *reinterpret_cast<u32x2*>(&sm.vt[d][t0]) = r;
                 }
             }
     }
+}
+
+// Copy this head's center columns for the wave's 64 keys, cent[id[t]][h*128
+// + 0..127], into the wave's own K rows of LDS (coalesced 16-byte loads, one
+// 256-byte row per 16 lanes).  Rows of other waves are not touched.
+__device__ __forceinline__ void stage_centers(ChunkSmem& sm, const nkv_codec& c, int codec, int b,
+                                              int h, int HD, int wave, int lane) {
+    const uint16_t* cent = c.centers + (int64_t)b * c.centers_batch_stride + h * CK_D;
+    u32x4 v[16];
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int t = 64 * wave + 4 * e + (lane >> 4);
+        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[codec][t] * HD +
+                                               8 * (lane & 15));
+    }
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+        *reinterpret_cast<u32x4*>(&sm.k[64 * wave + 4 * e + (lane >> 4)][8 * (lane & 15)]) = v[e];
 }
 
 // Current-chunk keys: copy K rows, transpose V into V^T (rows past the end
@@ -311,7 +325,7 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
 #pragma unroll
         for (int i = 2; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
         // the max is taken on raw scores (c > 0 preserves order)
-        tmax = fmaxf(tmax, __shfl_xor(tmax, 32)) * c;
+        tmax = halfwave_max(tmax) * c;
         const bool up = tmax > m[qb] + CK_TAU;
         const float m_new = up ? tmax : m[qb];
         alpha = up ? __builtin_amdgcn_exp2f(m[qb] - m_new) : 1.0f;
@@ -429,10 +443,10 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
     const int64_t row0 = (int64_t)bh * p.Q;
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
-        const float lt = l[qb] + __shfl_xor(l[qb], 32);
+        const float lt = halfwave_sum(l[qb]);
         const int64_t qi = q0 + 32 * qb + l32;
         if (qi < p.Q) {
-            const float inv = 1.0f / lt;
+            const float inv = __builtin_amdgcn_rcpf(lt);  // the partial is rounded to bf16
             const int64_t prow = (row0 + qi) * p.nch_total + chunk;
             uint16_t* dst = p.part_o + prow * CK_D + 4 * hf;
 #pragma unroll
@@ -483,8 +497,20 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
             if (t < CK_D) sm.bias[cc][t] = cd.mean ? bf16_round(cd.mean[h * CK_D + t]) : 0.0f;
         }
         __syncthreads();
-        decode_codec<0>(sm, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave, lane);
-        decode_codec<1>(sm, p.codec[1], b, h, p.HD, p.N, tok0, valid, wave, lane);
+        // V first: its epilogue reads the staged V centers from the K rows
+        // that the K pass then fills (each wave only touches its own rows)
+        if (p.codec[1].centers) {
+            stage_centers(sm, p.codec[1], 1, b, h, p.HD, wave, lane);
+            decode_codec<1, true>(sm, p.codec[1], b, h, p.HD, p.N, tok0, valid, wave, lane);
+        } else {
+            decode_codec<1, false>(sm, p.codec[1], b, h, p.HD, p.N, tok0, valid, wave, lane);
+        }
+        if (p.codec[0].centers) {
+            stage_centers(sm, p.codec[0], 0, b, h, p.HD, wave, lane);
+            decode_codec<0, true>(sm, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave, lane);
+        } else {
+            decode_codec<0, false>(sm, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave, lane);
+        }
     } else {
         load_current_chunk(sm, p, b, h, tok0, valid, t);
     }

@@ -126,6 +126,21 @@ __device__ __forceinline__ f32x16 mfma32(bf16x8 a, bf16x8 b, f32x16 c) {
     return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
 }
 
+// max / sum of x over lanes l and l ^ 32 (v_permlane32_swap exchanges the
+// two half-waves of two copies of x; the pair holds both values in either
+// order, so the result is symmetric).
+__device__ __forceinline__ float halfwave_max(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+
+__device__ __forceinline__ float halfwave_sum(float x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false,
+                                                    false);
+    return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
 // Eight INT4 codes of one dword (byte j: code 2j low nibble, 2j+1 high
 // nibble, stored as code + 7) times their group scale s, as the bf16x8 MFMA
 // operand in k order.  (nibble - 7) * s = fma(nibble, s, -7 s): both products
