@@ -7,7 +7,10 @@
 // ALL query tiles (64 queries each) to those keys.  Each (query, chunk)
 // leaves a partial: the chunk-local softmax output O / l as bf16 and its
 // log2-sum-exp m + log2(l) as fp32.  A combine kernel merges the partials of
-// every query by log-sum-exp (CN/core.py:33-42 applied over all chunks).
+// every query by log-sum-exp (CN/core.py:33-42 applied over all chunks).  A
+// 32-query block's partial is stored in the MFMA accumulator's lane order
+// (8 KB: eight 1 KB rows of 16 bytes per lane), so the stores here and the
+// combine's loads are contiguous.
 // Decoding each history key once per head, instead of once per query tile,
 // removes the decode GEMM's re-execution; the price is the partial traffic
 // (256 + 4 bytes per query and chunk).
@@ -55,6 +58,7 @@ struct ChunkSmem {
 struct ChunkParams {
     int B, H, HD;
     int nch_hist, nch_total;
+    int qblocks;        // 32-query blocks per (b, h): cdiv(Q, 32)
     int64_t Q, N, Nc;
     float scale_log2;
     const uint16_t* q;
@@ -64,8 +68,8 @@ struct ChunkParams {
     const uint16_t* v_cur;
     int64_t v_sb, v_st, v_sh;
     nkv_codec codec[2];
-    uint16_t* part_o;   // [B*H, Q, nch_total, 128] bf16
-    float* part_lse;    // [B*H, Q, nch_total] log2 domain
+    uint16_t* part_o;   // [B*H, nch_total, qblocks, 8, 64 lanes, 8] bf16 (lane order)
+    float* part_lse;    // [B*H, nch_total, qblocks * 32] log2 domain
     uint16_t* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
@@ -254,7 +258,13 @@ __device__ __forceinline__ void load_current_chunk(ChunkSmem& sm, const ChunkPar
 template <int NQB, bool FULL>
 __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkParams& p, int b,
                                              int h, int bh, int chunk, int64_t q0, int nsub,
-                                             int valid, int lane) {
+                                             int valid, int lane_in) {
+    // Opaque per-tile copy of the lane index: every lane-dependent address
+    // below is recomputed per tile instead of being hoisted out of the
+    // query-tile loop (where it would be spilled: the loop body needs
+    // nearly all 256 VGPRs).
+    int lane = lane_in;
+    asm volatile("" : "+v"(lane));
     const int hf = lane >> 5, l32 = lane & 31;
     const float c = p.scale_log2;
 
@@ -339,6 +349,9 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
             lsum += e;
         }
         l[qb] = l[qb] * alpha + lsum;
+        // materialise the row sum here: left alone, the compiler defers these
+        // adds to the end of the tile and keeps every exp value alive (spills)
+        asm volatile("" : "+v"(l[qb]));
 #pragma unroll
         for (int ts = 0; ts < 2; ++ts) {
             u32x4 v;
@@ -439,27 +452,29 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
         }
     }
 
-    // partial of this chunk: O / l (bf16) and m + log2(l)
-    const int64_t row0 = (int64_t)bh * p.Q;
+    // partial of this chunk: O / l (bf16) and m + log2(l).  Lane dword k of
+    // a block holds o[db = k/8][2*(k%8) + {0, 1}] and is stored at
+    // 1 KB * (k/4) + 16 B * lane + 4 B * (k%4): every store instruction
+    // writes 1 KB contiguous.  Query columns past Q hold finite values
+    // that the combine ignores.
 #pragma unroll
     for (int qb = 0; qb < NQB; ++qb) {
         const float lt = halfwave_sum(l[qb]);
-        const int64_t qi = q0 + 32 * qb + l32;
-        if (qi < p.Q) {
-            const float inv = __builtin_amdgcn_rcpf(lt);  // the partial is rounded to bf16
-            const int64_t prow = (row0 + qi) * p.nch_total + chunk;
-            uint16_t* dst = p.part_o + prow * CK_D + 4 * hf;
+        const float inv = __builtin_amdgcn_rcpf(lt);  // the partial is rounded to bf16
+        const int64_t blk = ((int64_t)bh * p.nch_total + chunk) * p.qblocks + (q0 >> 5) + qb;
+        uint16_t* dst = p.part_o + blk * 4096 + lane * 8;
 #pragma unroll
-            for (int db = 0; db < 4; ++db)
+        for (int st = 0; st < 8; ++st) {
+            const int db = st >> 1, i0 = 8 * (st & 1);
+            u32x4 w;
 #pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const f32x16& a = o[qb][db];
-                    const u32x2 pk = {pack_bf16x2(a[4 * g] * inv, a[4 * g + 1] * inv),
-                                      pack_bf16x2(a[4 * g + 2] * inv, a[4 * g + 3] * inv)};
-                    *reinterpret_cast<u32x2*>(dst + 32 * db + 8 * g) = pk;
-                }
-            if (hf == 0) p.part_lse[prow] = m[qb] + log2f(lt);
+            for (int e = 0; e < 4; ++e)
+                w[e] = pack_bf16x2(o[qb][db][i0 + 2 * e] * inv, o[qb][db][i0 + 2 * e + 1] * inv);
+            *reinterpret_cast<u32x4*>(dst + 512 * st) = w;
         }
+        if (hf == 0)
+            p.part_lse[((int64_t)bh * p.nch_total + chunk) * ((int64_t)p.qblocks * 32) + q0 +
+                       32 * qb + l32] = m[qb] + log2f(lt);
     }
 }
 
@@ -531,51 +546,93 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
     }
 }
 
-// Merge the chunk partials of every (b, h, q) row: 16 threads per row, 8 d
-// each.  out = sum_c 2^(lse_c - M) O_c / sum_c 2^(lse_c - M); no chunks give
+// Merge the chunk partials of every (b, h, q).  A 256-thread block owns one
+// 32-query block; its four waves take every fourth chunk, each lane reading
+// the lane-order payload the attention wave stored, and sum through LDS.
+// out = sum_c 2^(lse_c - M) O_c / sum_c 2^(lse_c - M); no chunks give
 // out = 0 and lse = -inf (CN/core.py:48-49).
-__global__ void __launch_bounds__(256) chunk_combine_kernel(ChunkParams p) {
-    const int64_t rows = (int64_t)p.B * p.H * p.Q;
-    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    const int64_t row = tid >> 4;
-    const int dg = (int)(tid & 15);
-    if (row >= rows) return;
+constexpr int CB_WAVES = 4;
+__global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParams p) {
+    __shared__ float red[CB_WAVES - 1][64][65];  // [wave-1][element][lane] (+1 pad)
+    __shared__ float redl[CB_WAVES - 1][64];
+    const int lane = threadIdx.x & 63, hf = lane >> 5, l32 = lane & 31;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t bh = blockIdx.x / p.qblocks;
+    const int qblk = (int)(blockIdx.x % p.qblocks);
+    const int64_t qi = (int64_t)qblk * 32 + l32;
     const int NC = p.nch_total;
-    const float* lr = p.part_lse + row * NC;
-    float M = -INFINITY;
-    for (int cc = 0; cc < NC; ++cc) M = fmaxf(M, lr[cc]);
+    const int64_t lse_stride = (int64_t)p.qblocks * 32;
+    const float* lr = p.part_lse + bh * NC * lse_stride + qi;
+    // eight independent maxima keep eight loads in flight
+    float mx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx[e] = -INFINITY;
+    int cc0 = 0;
+    for (; cc0 + 8 <= NC; cc0 += 8) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx[e] = fmaxf(mx[e], lr[(cc0 + e) * lse_stride]);
+    }
+    for (; cc0 < NC; ++cc0) mx[0] = fmaxf(mx[0], lr[cc0 * lse_stride]);
+    float M = mx[0];
+#pragma unroll
+    for (int e = 1; e < 8; ++e) M = fmaxf(M, mx[e]);
     const float Mu = M == -INFINITY ? 0.0f : M;
-    float L = 0.0f, acc[8];
+    float L = 0.0f, acc[64];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) acc[e] = 0.0f;
-    const uint16_t* po = p.part_o + row * NC * CK_D + 8 * dg;
-#pragma unroll 4
-    for (int cc = 0; cc < NC; ++cc) {
-        const float w = exp2f(lr[cc] - Mu);
-        L += w;
-        const u32x4 v = *reinterpret_cast<const u32x4*>(po + (int64_t)cc * CK_D);
+    for (int e = 0; e < 64; ++e) acc[e] = 0.0f;
+    const uint16_t* src = p.part_o + (bh * NC * p.qblocks + qblk) * 4096 + lane * 8;
+    const int64_t cstride = (int64_t)p.qblocks * 4096;
+#pragma unroll 2
+    for (int cc = wave; cc < NC; cc += CB_WAVES) {
+        const float wt = exp2f(lr[cc * lse_stride] - Mu);
+        L += wt;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            acc[2 * e] += w * __uint_as_float(v[e] << 16);
-            acc[2 * e + 1] += w * __uint_as_float(v[e] & 0xffff0000u);
+        for (int st = 0; st < 8; ++st) {
+            const u32x4 v = *reinterpret_cast<const u32x4*>(src + cc * cstride + 512 * st);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                acc[8 * st + 2 * e] += wt * __uint_as_float(v[e] << 16);
+                acc[8 * st + 2 * e + 1] += wt * __uint_as_float(v[e] & 0xffff0000u);
+            }
         }
     }
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    const int64_t qi = row % p.Q, bhi = row / p.Q;
-    const int h = (int)(bhi % p.H), b = (int)(bhi / p.H);
-    uint16_t* orow = p.out + b * p.o_sb + qi * p.o_st + h * p.o_sh + 8 * dg;
-    u32x4 pk;
+    if (wave > 0) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e) pk[e] = pack_bf16x2(acc[2 * e] * inv, acc[2 * e + 1] * inv);
-    *reinterpret_cast<u32x4*>(orow) = pk;
-    if (p.lse && dg == 0) p.lse[row] = L > 0.0f ? (M + log2f(L)) * 0.69314718055994531f : -INFINITY;
+        for (int e = 0; e < 64; ++e) red[wave - 1][e][lane] = acc[e];
+        redl[wave - 1][lane] = L;
+    }
+    __syncthreads();
+    if (wave > 0 || qi >= p.Q) return;
+#pragma unroll
+    for (int w = 0; w < CB_WAVES - 1; ++w) {
+#pragma unroll
+        for (int e = 0; e < 64; ++e) acc[e] += red[w][e][lane];
+        L += redl[w][lane];
+    }
+    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
+    const int b = (int)(bh / p.H), h = (int)(bh % p.H);
+    uint16_t* orow = p.out + b * p.o_sb + qi * p.o_st + h * p.o_sh + 4 * hf;
+    // acc[8*st + 2*e + {0,1}] = o[db = st/2][i = 8*(st&1) + 2*e + {0,1}] with
+    // d = 32*db + 8*(i/4) + 4*hf + i%4: acc[4n .. 4n+3] are four consecutive
+    // d of this lane's query
+#pragma unroll
+    for (int n = 0; n < 16; ++n) {
+        const int st = n >> 1;
+        const int db = st >> 1, i = 8 * (st & 1) + 4 * (n & 1);
+        const int d = 32 * db + 8 * (i >> 2);
+        const u32x2 pk = {pack_bf16x2(acc[4 * n] * inv, acc[4 * n + 1] * inv),
+                          pack_bf16x2(acc[4 * n + 2] * inv, acc[4 * n + 3] * inv)};
+        *reinterpret_cast<u32x2*>(orow + d) = pk;
+    }
+    if (p.lse && hf == 0)
+        p.lse[bh * p.Q + qi] = L > 0.0f ? (M + log2f(L)) * 0.69314718055994531f : -INFINITY;
 }
 
 // ------------------------------------------------------------------ host
 size_t chunk_workspace_bytes(const nkv_attend_args* a) {
     const int64_t nc = cdiv(a->N, CK_T) + cdiv(a->Nc, CK_T);
-    const size_t rows = (size_t)a->B * a->H * a->Q * nc;
-    return rows * CK_D * sizeof(uint16_t) + rows * sizeof(float);
+    const size_t blocks = (size_t)a->B * a->H * nc * cdiv(a->Q, 32);
+    return blocks * 32 * CK_D * sizeof(uint16_t) + blocks * 32 * sizeof(float);
 }
 
 int chunk_check(const nkv_attend_args* a) {
@@ -622,10 +679,11 @@ int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace
     p.v_sh = a->v_sh;
     p.codec[0] = a->key;
     p.codec[1] = a->value;
-    const size_t rows = (size_t)a->B * a->H * a->Q * p.nch_total;
+    p.qblocks = (int)cdiv(a->Q, 32);
+    const size_t qrows = (size_t)a->B * a->H * p.nch_total * p.qblocks * 32;
     p.part_o = reinterpret_cast<uint16_t*>(workspace);
     p.part_lse = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
-                                          rows * CK_D * sizeof(uint16_t));
+                                          qrows * CK_D * sizeof(uint16_t));
     p.out = a->out;
     p.o_sb = a->o_sb;
     p.o_st = a->o_st;
@@ -642,9 +700,11 @@ int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace
         NKV_LAUNCH_CHECK();
     }
     if (a->ev_kernel_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)a->ev_kernel_end, s));
-    const int64_t threads = (int64_t)a->B * a->H * a->Q * 16;
-    chunk_combine_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(p);
-    NKV_LAUNCH_CHECK();
+    const int64_t qblocks_total = (int64_t)a->B * a->H * p.qblocks;
+    if (qblocks_total > 0) {
+        chunk_combine_kernel<<<dim3((unsigned)qblocks_total), 64 * CB_WAVES, 0, s>>>(p);
+        NKV_LAUNCH_CHECK();
+    }
     return NKV_OK;
 }
 
