@@ -40,6 +40,12 @@
 
 namespace nkv {
 
+#ifdef NKV_PLAIN_STORES
+#define NT_STORE(v, ptr) (*(ptr) = (v))
+#else
+#define NT_STORE(v, ptr) __builtin_nontemporal_store((v), (ptr))
+#endif
+
 constexpr int CK_T = 256;        // keys per chunk
 constexpr int CK_D = 128;        // head dim
 constexpr int CK_THREADS = 256;  // 4 waves
@@ -77,12 +83,67 @@ struct ChunkParams {
 
 // ------------------------------------------------------------------ decode
 // This wave's 64 keys (64*wave + [0, 64) of the chunk) of codec CODEC.
-// HAS_C: the codec has centers (staged in the wave's K rows); a template
-// argument so that the epilogue is straight-line code.
+// Decoder-slice staging: the block copies W[h*128 + d][64*kq, +64) (16 KB)
+// into LDS with coalesced 16-byte loads (8 threads per 128-byte row), double
+// buffered, so each decoder element is fetched from L2 once per block and
+// every wave reads its MFMA fragments from LDS.  Rows are padded to 72 bf16
+// (36 dwords): the b128 fragment reads of 8 consecutive rows hit distinct
+// banks.
+constexpr int WS_ROW = 72;
+constexpr int WS_BUF = CK_D * WS_ROW;  // bf16 elements per buffer
+static_assert(2 * WS_BUF <= CK_D * CK_VROW && 2 * WS_BUF <= CK_T * CK_KROW,
+              "decoder staging must fit in the V^T and K regions");
+
+// Center columns of head h for the wave's 64 keys, cent[id[t]][h*128 + d],
+// with coalesced 16-byte loads (one 256-byte row per 16 lanes) ...
+__device__ __forceinline__ void load_center_rows(u32x4 (&v)[16], const ChunkSmem& sm,
+                                                 const nkv_codec& c, int codec, int b, int h,
+                                                 int HD, int wave, int lane) {
+    const uint16_t* cent = c.centers + (int64_t)b * c.centers_batch_stride + h * CK_D;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        const int t = 64 * wave + 4 * e + (lane >> 4);
+        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[codec][t] * HD +
+                                               8 * (lane & 15));
+    }
+}
+
+// ... stored into the wave's own K rows of LDS (other waves' rows are not
+// touched).
+__device__ __forceinline__ void store_center_rows(const u32x4 (&v)[16], ChunkSmem& sm, int wave,
+                                                  int lane) {
+#pragma unroll
+    for (int e = 0; e < 16; ++e)
+        *reinterpret_cast<u32x4*>(&sm.k[64 * wave + 4 * e + (lane >> 4)][8 * (lane & 15)]) = v[e];
+}
+
+// K center values in the K^T accumulator layout: key 64*wave + 32*tt + l32,
+// d = 32*dt + 8*g + 4*hf + [0, 4).
+__device__ __forceinline__ void load_k_centers(u32x2 (&cen)[2][4][4], const ChunkSmem& sm,
+                                               const nkv_codec& c, int b, int h, int HD,
+                                               int wave, int lane) {
+    const int hf = lane >> 5, l32 = lane & 31;
+    const uint16_t* cent = c.centers + (int64_t)b * c.centers_batch_stride + h * CK_D + 4 * hf;
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const uint16_t* crow = cent + (int64_t)sm.ids[0][64 * wave + 32 * tt + l32] * HD;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+                cen[tt][dt][g] = *reinterpret_cast<const u32x2*>(crow + 32 * dt + 8 * g);
+    }
+}
+
+// Decode this wave's 64 keys of codec CODEC.  wst: 2 * WS_BUF bf16 of LDS
+// that no other data uses during the call.  HAS_C: the codec has centers (a
+// template argument so that the epilogue is straight-line code); for V they
+// were staged into the wave's K rows, for K they are loaded in the epilogue.
+// Ends with a block barrier after the last read of wst.
 template <int CODEC, bool HAS_C>
-__device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, int b, int h,
-                                             int HD, int64_t N, int64_t tok0, int valid,
-                                             int wave, int lane) {
+__device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const nkv_codec& c,
+                                             int b, int h, int HD, int64_t N, int64_t tok0,
+                                             int valid, int wave, int lane) {
     const int hf = lane >> 5, l32 = lane & 31;
     const int R = c.r, KQ = R >> 6, G = c.group, NG = R / G;
     const bool f16 = c.scale_dtype == NKV_DTYPE_FP16;
@@ -96,18 +157,20 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, 
         prow[tt] = c.packed + tok * (R / 2) + 16 * hf;
         srow[tt] = c.scales + tok * NG;
     }
-    const uint16_t* wrow[4];
+    const int t = 64 * wave + lane;
+    const uint16_t* wsrc = c.w_dec + (int64_t)(h * CK_D + (t >> 3)) * R + 8 * (t & 7);
+    uint16_t* wdst = wst + (t >> 3) * WS_ROW + 8 * (t & 7);
+    auto wload = [&](int kq, u32x4 (&r)[4]) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-        wrow[dt] = c.w_dec + (int64_t)(h * CK_D + 32 * dt + l32) * R + 32 * hf;
-
-    f32x16 acc[4][2];
+        for (int e = 0; e < 4; ++e)
+            r[e] = *reinterpret_cast<const u32x4*>(wsrc + (int64_t)32 * e * R + 64 * kq);
+    };
+    auto wstore = [&](int buf, const u32x4 (&r)[4]) {
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) acc[dt][tt] = f32x16{};
-
-    auto load = [&](int kq, u32x4 (&pk)[2], float (&sc)[2], u32x4 (&wf)[4][4]) {
+        for (int e = 0; e < 4; ++e)
+            *reinterpret_cast<u32x4*>(wdst + buf * WS_BUF + 32 * e * WS_ROW) = r[e];
+    };
+    auto cload = [&](int kq, u32x4 (&pk)[2], float (&sc)[2]) {
         const int gi = (64 * kq + 32 * hf) / G;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
@@ -115,52 +178,74 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, 
             const uint16_t sb = srow[tt][gi];
             sc[tt] = f16 ? f16_bits_to_f32(sb) : bf16_bits_to_f32(sb);
         }
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-            for (int j = 0; j < 4; ++j)
-                wf[dt][j] = *reinterpret_cast<const u32x4*>(wrow[dt] + 64 * kq + 8 * j);
     };
 
-    u32x4 pk[2], wf[4][4];
+    f32x16 acc[4][2];
+#pragma unroll
+    for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) acc[dt][tt] = f32x16{};
+
+    // V: this wave's center rows go to its own K rows (store_center_rows);
+    // their loads are issued first so that they overlap the prologue.
+    u32x4 cst[16];
+    if (CODEC == 1 && HAS_C) load_center_rows(cst, sm, c, 1, b, h, HD, wave, lane);
+
+    // One slice ahead: codes (HBM) and decoder rows for slice kq+1 are
+    // requested while slice kq is multiplied; the rows go to the other LDS
+    // buffer at the end of the iteration.
+    u32x4 wr[4], pk[2];
     float sc[2];
-    load(0, pk, sc, wf);
+    wload(0, wr);
+    cload(0, pk, sc);
+    if (CODEC == 1 && HAS_C) store_center_rows(cst, sm, wave, lane);
+    wstore(0, wr);
+    __syncthreads();
+    // fragment rows 32*dt + l32, k = 32*hf + 8*j within the slice
+    const uint16_t* wfrag = wst + l32 * WS_ROW + 32 * hf;
+    u32x2 cen[2][4][4];  // K epilogue center values, requested during the last slice
     for (int kq = 0; kq < KQ; ++kq) {
-        u32x4 pkn[2], wfn[4][4];
+        u32x4 pkn[2];
         float scn[2];
-        if (kq + 1 < KQ) load(kq + 1, pkn, scn, wfn);
+        const bool more = kq + 1 < KQ;
+        if (more) {
+            wload(kq + 1, wr);
+            cload(kq + 1, pkn, scn);
+        }
+        if (CODEC == 0 && HAS_C && !more) load_k_centers(cen, sm, c, b, h, HD, wave, lane);
+        const uint16_t* wb = wfrag + (kq & 1) * WS_BUF;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
             bf16x8 z[2];
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) z[tt] = unpack8(pk[tt][j], sc[tt], -7.0f * sc[tt]);
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+            for (int dt = 0; dt < 4; ++dt) {
+                const bf16x8 w = lds_b128(wb + 32 * dt * WS_ROW + 8 * j);
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt)
-                    acc[dt][tt] = CODEC == 0 ? mfma32(as_bf16x8(wf[dt][j]), z[tt], acc[dt][tt])
-                                             : mfma32(z[tt], as_bf16x8(wf[dt][j]), acc[dt][tt]);
+                    acc[dt][tt] = CODEC == 0 ? mfma32(w, z[tt], acc[dt][tt])
+                                             : mfma32(z[tt], w, acc[dt][tt]);
+            }
         }
-        if (kq + 1 < KQ) {
+        if (more) {
+            // the other buffer was last read before the previous barrier
+            wstore((kq + 1) & 1, wr);
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
                 pk[tt] = pkn[tt];
                 sc[tt] = scn[tt];
             }
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-                for (int j = 0; j < 4; ++j) wf[dt][j] = wfn[dt][j];
         }
+        __syncthreads();
     }
 
-    // Epilogue.  The center rows of this wave's keys were staged into its own
-    // K rows of LDS (stage_centers) before the MFMAs, so every center value
-    // is an LDS read.  sm.bias holds bf16(mean) or zeros, so the bias add is
+    // Epilogue.  sm.bias holds bf16(mean) or zeros, so the bias add is
     // unconditional.
     if (CODEC == 0) {
-        // acc[dt][tt] element i: d = 32*dt + 8*(i/4) + 4*hf + i%4, key 64*wave + 32*tt + l32;
-        // the result overwrites the staged center it was added to
+        // acc[dt][tt] element i: d = 32*dt + 8*(i/4) + 4*hf + i%4, key
+        // 64*wave + 32*tt + l32; cen holds the center values (4 consecutive d
+        // per group).
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int t = 64 * wave + 32 * tt + l32;
@@ -173,7 +258,7 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, 
                     float a[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) a[e] = acc[dt][tt][4 * g + e] + sm.bias[0][d + e];
-                    const u32x2 cw = HAS_C ? *slot : u32x2{0, 0};
+                    const u32x2 cw = HAS_C ? cen[tt][dt][g] : u32x2{0, 0};
                     u32x2 r;
 #pragma unroll
                     for (int h2 = 0; h2 < 2; ++h2) {
@@ -187,7 +272,8 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, 
                 }
         }
     } else {
-        // acc[dt][tt] element i: key 64*wave + 32*tt + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32
+        // acc[dt][tt] element i: key 64*wave + 32*tt + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32;
+        // the center rows of the wave's keys were staged into its K rows
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -208,24 +294,6 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, const nkv_codec& c, 
                 }
             }
     }
-}
-
-// Copy this head's center columns for the wave's 64 keys, cent[id[t]][h*128
-// + 0..127], into the wave's own K rows of LDS (coalesced 16-byte loads, one
-// 256-byte row per 16 lanes).  Rows of other waves are not touched.
-__device__ __forceinline__ void stage_centers(ChunkSmem& sm, const nkv_codec& c, int codec, int b,
-                                              int h, int HD, int wave, int lane) {
-    const uint16_t* cent = c.centers + (int64_t)b * c.centers_batch_stride + h * CK_D;
-    u32x4 v[16];
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int t = 64 * wave + 4 * e + (lane >> 4);
-        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[codec][t] * HD +
-                                               8 * (lane & 15));
-    }
-#pragma unroll
-    for (int e = 0; e < 16; ++e)
-        *reinterpret_cast<u32x4*>(&sm.k[64 * wave + 4 * e + (lane >> 4)][8 * (lane & 15)]) = v[e];
 }
 
 // Current-chunk keys: copy K rows, transpose V into V^T (rows past the end
@@ -252,13 +320,31 @@ __device__ __forceinline__ void load_current_chunk(ChunkSmem& sm, const ChunkPar
 }
 
 // --------------------------------------------------------------- attention
+// Q^T operand fragments of 32 queries [q_blk, q_blk + 32), with the same
+// permuted d walk as the K reads; rows past the last query read row q_safe
+// (finite, never stored).
+__device__ __forceinline__ void load_q_block(bf16x8 (&qf)[8], const ChunkParams& p, int b, int h,
+                                             int64_t q_blk, int64_t q_safe, int lane) {
+    const int hf = lane >> 5, l32 = lane & 31;
+    const int64_t qi = q_blk + l32;
+    const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (qi < p.Q ? qi : q_safe) * p.q_st +
+                           (int64_t)h * p.q_sh + 32 * hf;
+#pragma unroll
+    for (int kk = 0; kk < 8; ++kk)
+        qf[kk] = as_bf16x8(*reinterpret_cast<const u32x4*>(qrow + 64 * (kk >> 2) + 8 * (kk & 3)));
+}
+
 // One wave attends queries [q0, q0 + 32*NQB) to the chunk in LDS.  FULL: the
 // chunk has all 256 keys (eight pipelined steps); otherwise nsub steps with
-// the last one masked to `valid` keys.
+// the last one masked to `valid` keys.  qf holds this tile's query
+// fragments on entry; as soon as a query block's last score product is
+// issued, its registers are refilled with the wave's next tile (first query
+// q_next), so that tile's loads overlap this tile's remaining work.
 template <int NQB, bool FULL>
 __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkParams& p, int b,
                                              int h, int bh, int chunk, int64_t q0, int nsub,
-                                             int valid, int lane_in) {
+                                             int valid, int lane_in, bf16x8 (&qf)[2][8],
+                                             int64_t q_next) {
     // Opaque per-tile copy of the lane index: every lane-dependent address
     // below is recomputed per tile instead of being hoisted out of the
     // query-tile loop (where it would be spilled: the loop body needs
@@ -267,20 +353,6 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
     asm volatile("" : "+v"(lane));
     const int hf = lane >> 5, l32 = lane & 31;
     const float c = p.scale_log2;
-
-    // Q^T operand fragments, with the same permuted d walk as the K reads;
-    // columns past the last query repeat query q0 (finite, never stored)
-    bf16x8 qf[NQB][8];
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-        const int64_t qi = q0 + 32 * qb + l32;
-        const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (qi < p.Q ? qi : q0) * p.q_st +
-                               (int64_t)h * p.q_sh + 32 * hf;
-#pragma unroll
-        for (int kk = 0; kk < 8; ++kk)
-            qf[qb][kk] = as_bf16x8(
-                *reinterpret_cast<const u32x4*>(qrow + 64 * (kk >> 2) + 8 * (kk & 3)));
-    }
 
     f32x16 o[NQB][4];
     float m[NQB], l[NQB];
@@ -384,12 +456,14 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
         for (int j = 0; j < NSTEP; ++j) {
             bf16x8 vf[2][4], kn[8];
             qk(NQB - 1, kf, s1);
+            if (j == NSTEP - 1) load_q_block(qf[1], p, b, h, q_next + 32, q_next, lane);
             if (j > 0) pv(NQB - 1, vprev, p1);
             load_v(j, vf);
             if (j + 1 < NSTEP) load_k(j + 1, kn);
             const bool up0 = softmax(0, s0, p0, a0);
             if (j > 0 && __any(up0)) rescale(0, a0);
             if (j + 1 < NSTEP) qk(0, kn, s0);
+            if (j == NSTEP - 2) load_q_block(qf[0], p, b, h, q_next, q_next, lane);
             pv(0, vf, p0);
             const bool up1 = softmax(NQB - 1, s1, p1, a1);
             if (j > 0 && __any(up1)) rescale(NQB - 1, a1);
@@ -415,6 +489,10 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
             if (j + 1 < NSTEP) {
                 load_k(j + 1, kf);
                 qk(0, kf, s[nxt]);
+            }
+            if (j == NSTEP - 2) {
+                load_q_block(qf[0], p, b, h, q_next, q_next, lane);
+                load_q_block(qf[1], p, b, h, q_next + 32, q_next, lane);
             }
             if (j > 0) pv(0, vprev, pp[nxt]);
             load_v(j, vf);
@@ -450,6 +528,8 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
                 pv(qb, vf, pb);
             }
         }
+        load_q_block(qf[0], p, b, h, q_next, q_next, lane);
+        load_q_block(qf[1], p, b, h, q_next + 32, q_next, lane);
     }
 
     // partial of this chunk: O / l (bf16) and m + log2(l).  Lane dword k of
@@ -470,11 +550,12 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
 #pragma unroll
             for (int e = 0; e < 4; ++e)
                 w[e] = pack_bf16x2(o[qb][db][i0 + 2 * e] * inv, o[qb][db][i0 + 2 * e + 1] * inv);
-            *reinterpret_cast<u32x4*>(dst + 512 * st) = w;
+            NT_STORE(w, reinterpret_cast<u32x4*>(dst + 512 * st));
         }
         if (hf == 0)
-            p.part_lse[((int64_t)bh * p.nch_total + chunk) * ((int64_t)p.qblocks * 32) + q0 +
-                       32 * qb + l32] = m[qb] + log2f(lt);
+            NT_STORE(m[qb] + log2f(lt),
+                     p.part_lse + ((int64_t)bh * p.nch_total + chunk) * ((int64_t)p.qblocks * 32) +
+                         q0 + 32 * qb + l32);
     }
 }
 
@@ -512,20 +593,26 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
             if (t < CK_D) sm.bias[cc][t] = cd.mean ? bf16_round(cd.mean[h * CK_D + t]) : 0.0f;
         }
         __syncthreads();
-        // V first: its epilogue reads the staged V centers from the K rows
-        // that the K pass then fills (each wave only touches its own rows)
+        // V first: its decoder slices are staged in the (not yet written)
+        // V^T region and its centers in the wave's own K rows; then K, with
+        // its slices staged in the K region once every wave has read its V
+        // centers.
+        uint16_t* vt_scratch = &sm.vt[0][0];
+        uint16_t* k_scratch = &sm.k[0][0];
         if (p.codec[1].centers) {
-            stage_centers(sm, p.codec[1], 1, b, h, p.HD, wave, lane);
-            decode_codec<1, true>(sm, p.codec[1], b, h, p.HD, p.N, tok0, valid, wave, lane);
+            decode_codec<1, true>(sm, vt_scratch, p.codec[1], b, h, p.HD, p.N, tok0, valid, wave,
+                                  lane);
         } else {
-            decode_codec<1, false>(sm, p.codec[1], b, h, p.HD, p.N, tok0, valid, wave, lane);
+            decode_codec<1, false>(sm, vt_scratch, p.codec[1], b, h, p.HD, p.N, tok0, valid,
+                                   wave, lane);
         }
-        if (p.codec[0].centers) {
-            stage_centers(sm, p.codec[0], 0, b, h, p.HD, wave, lane);
-            decode_codec<0, true>(sm, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave, lane);
-        } else {
-            decode_codec<0, false>(sm, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave, lane);
-        }
+        __syncthreads();
+        if (p.codec[0].centers)
+            decode_codec<0, true>(sm, k_scratch, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave,
+                                  lane);
+        else
+            decode_codec<0, false>(sm, k_scratch, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave,
+                                   lane);
     } else {
         load_current_chunk(sm, p, b, h, tok0, valid, t);
     }
@@ -533,15 +620,23 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
 
     const int nsub = (valid + 31) / 32;
     const int nqt = (int)cdiv(p.Q, CK_QT);
-    for (int qt = wave; qt < nqt; qt += CK_THREADS / 64) {
+    constexpr int WAVES = CK_THREADS / 64;
+    bf16x8 qf[2][8];
+    if (wave < nqt) {
+        load_q_block(qf[0], p, b, h, (int64_t)wave * CK_QT, (int64_t)wave * CK_QT, lane);
+        load_q_block(qf[1], p, b, h, (int64_t)wave * CK_QT + 32, (int64_t)wave * CK_QT, lane);
+    }
+    for (int qt = wave; qt < nqt; qt += WAVES) {
         const int64_t q0 = (int64_t)qt * CK_QT;
+        // the wave's next tile, or this one again (a harmless in-bounds reload)
+        const int64_t q_next = qt + WAVES < nqt ? q0 + WAVES * CK_QT : q0;
         const bool one = q0 + 32 >= p.Q;
         if (valid == CK_T) {
-            if (one) attend_qtile<1, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane);
-            else attend_qtile<2, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane);
+            if (one) attend_qtile<1, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
+            else attend_qtile<2, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
         } else {
-            if (one) attend_qtile<1, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane);
-            else attend_qtile<2, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane);
+            if (one) attend_qtile<1, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
+            else attend_qtile<2, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
         }
     }
 }
