@@ -32,7 +32,7 @@ if str(ROOT) not in sys.path:
 
 PEAK_BF16_TFLOPS = 2500.0   # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0
-TRAFFIC_FILE = ROOT / "profiles" / "attend_kernel_traffic.json"
+TRAFFIC_FILE = ROOT / "profiles" / "hbm_traffic.json"
 
 
 def parse():
@@ -177,12 +177,17 @@ def main():
     ms_per_step = wall * 1e3 / args.steps
     value = fl["total"] / (ms_per_step * 1e-3) / 1e12
     achieved = fl["total"] / (kavg_ms * 1e-3) / 1e12
+    # the schedule nkv_attend resolves AUTO to (key chunks above one 256-query tile)
+    schedule = args.schedule
+    if schedule == "auto":
+        schedule = "key_chunks" if shape.Q > 256 else "query_tiles"
+    kernel = "nkv::chunk_kernel" if schedule == "key_chunks" else "nkv::attend_kernel"
     traffic = None
     if TRAFFIC_FILE.exists():
         try:
-            tr = json.loads(TRAFFIC_FILE.read_text())
-            if tr.get("config") == shape.name:
-                traffic = tr.get("hbm_bytes_per_launch")
+            for tr in json.loads(TRAFFIC_FILE.read_text()):
+                if tr.get("config") == shape.name and tr.get("kernel") == kernel:
+                    traffic = tr.get("hbm_bytes_per_launch")
         except Exception:
             traffic = None
     from nanokv_amd import _lib
@@ -207,7 +212,7 @@ def main():
         "history_tokens_per_ms": round(shape.N / ms_per_step, 1),
         "coeff_stream_GBps": round(shape.coeff_stream_bytes() / (kavg_ms * 1e-3) / 1e9, 2),
         "algorithmic_flops": fl,
-        "roofline": {"bound": "mfma", "kernel": "nkv::attend_kernel",
+        "roofline": {"bound": "mfma", "kernel": kernel, "schedule": schedule,
                      "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic, "kernel_ms_avg": round(kavg_ms, 4)},

@@ -232,6 +232,61 @@ int nkv_attend(void* stream, const nkv_attend_args* args, void* workspace,
                size_t workspace_bytes);
 
 /*
+ * One reader group of NanoKV-Fast (ReaderGroup, CN/core.py:155-204): its
+ * heads read the low (unprotected) history rows through learned projections
+ *   q_low = bf16(q_h . q_reduce[i])                         [Q, d]
+ *   k_low = bf16(bf16(latent_K . k_read[i]^T + kbias[i]) + kcent[i][id])
+ *   v_low = bf16(bf16(latent_V . v_read[i]^T + vbias[i]) + vcent[i][id])
+ * with kcent[i] = bf16(center columns of head h . k_affine[i]) and
+ * kbias[i] = bf16(bf16(mean_h) . k_affine[i]) (V likewise with v_affine);
+ * latent = the unpacked INT4 codes (nkv_unpack).  A NULL q_reduce / k_affine
+ * / v_affine is the identity (the reference's identity flags).  The value
+ * width and the lift are D (identity lift).  All pointers are device memory.
+ */
+typedef struct nkv_reader_group {
+    int num_heads;
+    int d;                        /* K/Q reader width: 32, 64 or 128 (== D for identity) */
+    const int32_t* heads;         /* [num_heads] layer head indices */
+    const uint16_t* q_reduce;     /* [num_heads, D, d] bf16 or NULL */
+    const uint16_t* k_read;       /* [num_heads, d, rK] bf16 */
+    const uint16_t* v_read;       /* [num_heads, D, rV] bf16 */
+    const uint16_t* k_affine;     /* [num_heads, D, d] bf16 or NULL */
+    const uint16_t* v_affine;     /* [num_heads, D, D] bf16 or NULL */
+} nkv_reader_group;
+
+/*
+ * NanoKV-Fast mixed-dimensional history attention (hybrid_attention
+ * CN/core.py:278-310 with maybe_attention's partitions CN/mg35.py:192-348):
+ *   native partition: every head attends to the history rows protect_rows
+ *     (decoded at full width, as nkv_attend) and the current keys;
+ *   low partition: the heads of each reader group attend to the history
+ *     rows low_rows through the group's readers;
+ *   out = merge of the two by log-sum-exp (CN/core.py:33-42), per head.
+ * attend carries q, the current K/V, the key/value codecs (decoders for the
+ * native partition), out and lse, as for nkv_attend (its N is the codec's
+ * token count; splits and schedule are ignored).  Every head should belong
+ * to exactly one group (CN/core.py:213-215); a head in no group keeps the
+ * native partition alone.  No RoPE/PRoPE is applied (positions are outside
+ * this build).  Returns NKV_ERR_UNSUPPORTED for D != 128.
+ */
+typedef struct nkv_fast_args {
+    nkv_attend_args attend;
+    const int32_t* protect_rows;  /* [n_protect] codec rows, device memory */
+    int64_t n_protect;
+    const int32_t* low_rows;      /* [n_low] codec rows, device memory */
+    int64_t n_low;
+    int num_groups;
+    int _pad;
+    const nkv_reader_group* groups;  /* host array of num_groups */
+} nkv_fast_args;
+
+/* Bytes of workspace nkv_fast_attend needs for these arguments. */
+size_t nkv_fast_attend_workspace_size(const nkv_fast_args* args);
+
+int nkv_fast_attend(void* stream, const nkv_fast_args* args, void* workspace,
+                    size_t workspace_bytes);
+
+/*
  * Log-sum-exp merge of two attention partitions (CN/core.py:33-42):
  *   lse = logaddexp(lse_a, lse_b); origin = lse if finite else 0
  *   out = a * exp(lse_a - origin) + b * exp(lse_b - origin)   (fp32, -> bf16)

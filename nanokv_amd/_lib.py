@@ -32,6 +32,7 @@ NKV_SCHEDULE_KEY_CHUNKS = 2
 EXPORTED = (
     "nkv_abi_version", "nkv_last_error", "nkv_quant_pack", "nkv_unpack", "nkv_assign",
     "nkv_encode", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
+    "nkv_fast_attend_workspace_size", "nkv_fast_attend",
 )
 
 
@@ -76,6 +77,22 @@ class NkvAttendArgs(Structure):
     ]
 
 
+class NkvReaderGroup(Structure):
+    _fields_ = [
+        ("num_heads", c_int), ("d", c_int), ("heads", c_void_p), ("q_reduce", c_void_p),
+        ("k_read", c_void_p), ("v_read", c_void_p), ("k_affine", c_void_p),
+        ("v_affine", c_void_p),
+    ]
+
+
+class NkvFastArgs(Structure):
+    _fields_ = [
+        ("attend", NkvAttendArgs), ("protect_rows", c_void_p), ("n_protect", c_int64),
+        ("low_rows", c_void_p), ("n_low", c_int64), ("num_groups", c_int), ("_pad", c_int),
+        ("groups", POINTER(NkvReaderGroup)),
+    ]
+
+
 class NanoKVError(RuntimeError):
     """A libnanokv_hip.so call returned an error code."""
 
@@ -110,6 +127,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nkv_attend_workspace_size.argtypes = [POINTER(NkvAttendArgs)]
     lib.nkv_attend.restype = c_int
     lib.nkv_attend.argtypes = [c_void_p, POINTER(NkvAttendArgs), c_void_p, c_size_t]
+    lib.nkv_fast_attend_workspace_size.restype = c_size_t
+    lib.nkv_fast_attend_workspace_size.argtypes = [POINTER(NkvFastArgs)]
+    lib.nkv_fast_attend.restype = c_int
+    lib.nkv_fast_attend.argtypes = [c_void_p, POINTER(NkvFastArgs), c_void_p, c_size_t]
     lib.nkv_lse_merge.restype = c_int
     lib.nkv_lse_merge.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int64, c_void_p,
                                   c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p]

@@ -30,6 +30,7 @@ SOURCES = {
     "nkv_attend.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     # scores are never NaN (-inf masks are kept): fmaxf needs no NaN quieting
     "nkv_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"],
+    "nkv_fast.hip": [],
 }
 
 COMMON = [

@@ -12,6 +12,13 @@ followed by attention), with the decode fused into the attention kernel:
                                    decode-then-attend of a paired K/V codec
                                    cache plus the current chunk, fused
                                    (nkv_attend); K/V are never materialised
+  ReaderGroup / ReaderLayer        CN:155-224 reader parameters, bound to
+                                   the kernels (identity flags CN:256-262)
+  fast_history_attention(q, cache, k_cur, v_cur, reader, protect)
+                                   NanoKV-Fast: maybe_attention's native /
+                                   low partitions (mg35.py:192-348) and
+                                   hybrid_attention's merge (CN:278-310),
+                                   fused (nkv_fast_attend)
 
 Tensors follow the reference's [B, H, S, D] layout; nothing here runs on the
 CPU.
@@ -87,5 +94,102 @@ def codec_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     out, lse = ops.attend(qq, kc, vc, key, value,
                           softmax_scale=D ** -0.5 if scale is None else scale,
                           return_lse=return_lse)
+    out = out.permute(0, 2, 1, 3)
+    return (out, lse) if return_lse else out
+
+
+def _is_identity(w: torch.Tensor) -> bool:
+    """The reference's identity test for reader matrices (CN:259-262)."""
+    return w.shape[-2] == w.shape[-1] and torch.equal(
+        w.float().cpu(), torch.eye(w.shape[-1]).expand_as(w))
+
+
+class ReaderGroup:
+    """One reader group (CN:155-204) on the device: heads that read the low
+    history rows through q_reduce / k_read / v_read / k_affine / v_affine.
+    Matrices equal to the identity are flagged as such (CN:256-262) and
+    skipped, as the reference's fast runtime does.  The value lift must be
+    the identity (vd == native dim); other lifts are not supported."""
+
+    def __init__(self, state: dict, device=None):
+        self.heads = state["heads"].long()
+        self.indices = state["indices"].long()
+        self.v_indices = state.get("v_indices", state["indices"]).long()
+        h, d = len(self.heads), int(self.indices.shape[1])
+        native = int(state["q_reduce"].shape[1])
+        rank = int(state["k_read"].shape[2])
+        vd = int(self.v_indices.shape[1])
+        expected = {"q_reduce": (h, native, d), "k_read": (h, d, rank),
+                    "v_read": (h, vd, int(state["v_read"].shape[2])),
+                    "k_affine": (h, native, d), "v_affine": (h, native, vd),
+                    "lift": (h, vd, native)}
+        for name, shape in expected.items():
+            if tuple(state[name].shape) != shape:
+                raise ValueError(f"Bad {name} shape; expected {shape}")
+        if vd != native or not _is_identity(state["lift"]):
+            raise NotImplementedError("only identity value lifts (vd == D) are supported")
+        self.native_dim, self.d = native, d
+        self.identity_query = _is_identity(state["q_reduce"])
+        self.identity_k = _is_identity(state["k_affine"])
+        self.identity_v = _is_identity(state["v_affine"])
+        device = device if device is not None else state["k_read"].device
+
+        def dev(t):
+            return t.to(device=device, dtype=torch.bfloat16).contiguous()
+
+        self.q_reduce = None if self.identity_query else dev(state["q_reduce"])
+        self.k_affine = None if self.identity_k else dev(state["k_affine"])
+        self.v_affine = None if self.identity_v else dev(state["v_affine"])
+        self.k_read = dev(state["k_read"])
+        self.v_read = dev(state["v_read"])
+        self.heads_dev = self.heads.to(device=device, dtype=torch.int32).contiguous()
+
+    def tensors(self) -> ops.ReaderTensors:
+        return ops.ReaderTensors(heads=self.heads_dev, d=self.d, k_read=self.k_read,
+                                 v_read=self.v_read, q_reduce=self.q_reduce,
+                                 k_affine=self.k_affine, v_affine=self.v_affine)
+
+
+class ReaderLayer:
+    """The reader groups of one layer (CN:207-224); they must partition the
+    heads exactly once (CN:213-215)."""
+
+    def __init__(self, payload: dict, device=None):
+        self.groups = [ReaderGroup(g, device) for g in payload["groups"]]
+        self.heads = int(payload["heads"])
+        self.native_dim = int(payload["native_dim"])
+        self.rank = int(payload["rank"])
+        all_heads = torch.cat([g.heads for g in self.groups]).tolist()
+        if sorted(all_heads) != list(range(self.heads)):
+            raise ValueError("Reader groups must partition heads exactly once")
+
+
+def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
+                           k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
+                           reader: ReaderLayer, protect: torch.Tensor, *,
+                           scale: Optional[float] = None, return_lse: bool = False):
+    """NanoKV-Fast history attention of q [B, H, Q, D]: the protected history
+    tokens (bool mask [N] over the cache) and the current chunk are attended
+    at full width by every head (mg35.py:192-303), the other history tokens
+    through each head's reader group (mg35.py:315-347), and the two are
+    merged by LSE (CN:33-42, 308).  Everything is fused in nkv_fast_attend;
+    no K/V row is materialised.  Scale: native_dim ** -0.5 (CN:287)."""
+    device = q.device
+    B, H, Qn, D = (int(x) for x in q.shape)
+    if H != reader.heads or D != reader.native_dim:
+        raise ValueError("Reader head/shard layout mismatch")
+    key, value = nanokv_codec.history_codecs(cache_k, cache_v, device)
+    protect = protect.to(device=device, dtype=torch.bool)
+    if protect.numel() != key.tokens:
+        raise ValueError("protect must have one entry per history token")
+    protect_rows = torch.nonzero(protect).flatten().to(torch.int32).contiguous()
+    low_rows = torch.nonzero(~protect).flatten().to(torch.int32).contiguous()
+    qq = q.to(torch.bfloat16).permute(0, 2, 1, 3)
+    kc = None if k_cur is None else k_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
+    vc = None if v_cur is None else v_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
+    out, lse = ops.fast_attend(qq, kc, vc, key, value, protect_rows, low_rows,
+                               [g.tensors() for g in reader.groups],
+                               softmax_scale=D ** -0.5 if scale is None else scale,
+                               return_lse=return_lse)
     out = out.permute(0, 2, 1, 3)
     return (out, lse) if return_lse else out

@@ -55,31 +55,50 @@ constexpr int CK_QT = 64;        // queries per wave tile
 constexpr float CK_TAU = 8.0f;   // lazy-rescale threshold (log2 units)
 
 struct ChunkSmem {
-    uint16_t k[CK_T][CK_KROW];    // K[key][d]
+    // K tile [key][DK + 8] (for DK < 128 only the front of the region is the
+    // tile); also decoder-slice and center staging during the decode
+    uint16_t k[CK_T][CK_KROW];
     uint16_t vt[CK_D][CK_VROW];   // V^T[d][key]
     int ids[2][CK_T];             // center ids of the chunk's keys (K, V)
-    float bias[2][CK_D];          // bf16(mean) of this head (K, V)
+    float bias[2][CK_D];          // bf16 bias of this head (K, V)
+};
+
+// K tile row pitch for a K/Q width DK (b128 reads of 8 rows hit distinct banks)
+template <int DK>
+struct KTile {
+    static constexpr int ROW = DK + 8;
 };
 
 struct ChunkParams {
-    int B, H, HD;
+    int B, H;           // H: heads of this launch (launch head i)
     int nch_hist, nch_total;
-    int qblocks;        // 32-query blocks per (b, h): cdiv(Q, 32)
-    int64_t Q, N, Nc;
+    int qblocks;        // 32-query blocks per (b, i): cdiv(Q, 32)
+    int64_t Q;
+    int64_t N;          // history tokens per batch item in the codec arrays
+    int64_t n_rows;     // history keys attended
+    const int32_t* rows;  // [n_rows] codec rows of those keys, or null: rows 0 .. n_rows-1
+    int64_t Nc;
     float scale_log2;
-    const uint16_t* q;
+    const uint16_t* q;  // [B, Q, H, DK] (strides)
     int64_t q_sb, q_st, q_sh;
     const uint16_t* k_cur;
     int64_t k_sb, k_st, k_sh;
     const uint16_t* v_cur;
     int64_t v_sb, v_st, v_sh;
-    nkv_codec codec[2];
+    ChunkCodec codec[2];
     uint16_t* part_o;   // [B*H, nch_total, qblocks, 8, 64 lanes, 8] bf16 (lane order)
     float* part_lse;    // [B*H, nch_total, qblocks * 32] log2 domain
     uint16_t* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
 };
+
+// Codec row of attended history key `key`; rows outside the codec are
+// clamped so that a bad row list cannot read out of bounds.
+__device__ __forceinline__ int64_t history_row(const ChunkParams& p, int64_t key) {
+    if (!p.rows) return key;
+    return min(max((int64_t)p.rows[key], (int64_t)0), p.N - 1);
+}
 
 // ------------------------------------------------------------------ decode
 // This wave's 64 keys (64*wave + [0, 64) of the chunk) of codec CODEC.
@@ -94,16 +113,16 @@ constexpr int WS_BUF = CK_D * WS_ROW;  // bf16 elements per buffer
 static_assert(2 * WS_BUF <= CK_D * CK_VROW && 2 * WS_BUF <= CK_T * CK_KROW,
               "decoder staging must fit in the V^T and K regions");
 
-// Center columns of head h for the wave's 64 keys, cent[id[t]][h*128 + d],
+// The 128 center values of launch head h for the wave's 64 keys (V),
 // with coalesced 16-byte loads (one 256-byte row per 16 lanes) ...
 __device__ __forceinline__ void load_center_rows(u32x4 (&v)[16], const ChunkSmem& sm,
-                                                 const nkv_codec& c, int codec, int b, int h,
-                                                 int HD, int wave, int lane) {
-    const uint16_t* cent = c.centers + (int64_t)b * c.centers_batch_stride + h * CK_D;
+                                                 const ChunkCodec& c, int codec, int b, int h,
+                                                 int wave, int lane) {
+    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         const int t = 64 * wave + 4 * e + (lane >> 4);
-        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[codec][t] * HD +
+        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[codec][t] * c.c_rs +
                                                8 * (lane & 15));
     }
 }
@@ -118,32 +137,36 @@ __device__ __forceinline__ void store_center_rows(const u32x4 (&v)[16], ChunkSme
 }
 
 // K center values in the K^T accumulator layout: key 64*wave + 32*tt + l32,
-// d = 32*dt + 8*g + 4*hf + [0, 4).
-__device__ __forceinline__ void load_k_centers(u32x2 (&cen)[2][4][4], const ChunkSmem& sm,
-                                               const nkv_codec& c, int b, int h, int HD,
-                                               int wave, int lane) {
+// d = 32*dt + 8*g + 4*hf + [0, 4), dt < NDT.
+template <int NDT>
+__device__ __forceinline__ void load_k_centers(u32x2 (&cen)[2][NDT][4], const ChunkSmem& sm,
+                                               const ChunkCodec& c, int b, int h, int wave,
+                                               int lane) {
     const int hf = lane >> 5, l32 = lane & 31;
-    const uint16_t* cent = c.centers + (int64_t)b * c.centers_batch_stride + h * CK_D + 4 * hf;
+    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs + 4 * hf;
 #pragma unroll
     for (int tt = 0; tt < 2; ++tt) {
-        const uint16_t* crow = cent + (int64_t)sm.ids[0][64 * wave + 32 * tt + l32] * HD;
+        const uint16_t* crow = cent + (int64_t)sm.ids[0][64 * wave + 32 * tt + l32] * c.c_rs;
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt)
+        for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
             for (int g = 0; g < 4; ++g)
                 cen[tt][dt][g] = *reinterpret_cast<const u32x2*>(crow + 32 * dt + 8 * g);
     }
 }
 
-// Decode this wave's 64 keys of codec CODEC.  wst: 2 * WS_BUF bf16 of LDS
-// that no other data uses during the call.  HAS_C: the codec has centers (a
-// template argument so that the epilogue is straight-line code); for V they
-// were staged into the wave's K rows, for K they are loaded in the epilogue.
-// Ends with a block barrier after the last read of wst.
-template <int CODEC, bool HAS_C>
-__device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const nkv_codec& c,
-                                             int b, int h, int HD, int64_t N, int64_t tok0,
+// Decode this wave's 64 keys of codec CODEC to WIDTH columns (V: 128; K:
+// the launch's DK, written to the K tile with row pitch KROW).  wst: 2 *
+// WS_BUF bf16 of LDS that no other data uses during the call.  HAS_C: the
+// codec has centers (a template argument so that the epilogue is
+// straight-line code); V's are staged in the wave's K-region rows, K's are
+// loaded during the last slice.  Ends with a block barrier after the last
+// read of wst.
+template <int CODEC, bool HAS_C, int WIDTH, int KROW>
+__device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const ChunkCodec& c,
+                                             const ChunkParams& p, int b, int h, int64_t tok0,
                                              int valid, int wave, int lane) {
+    constexpr int NDT = WIDTH / 32;
     const int hf = lane >> 5, l32 = lane & 31;
     const int R = c.r, KQ = R >> 6, G = c.group, NG = R / G;
     const bool f16 = c.scale_dtype == NKV_DTYPE_FP16;
@@ -153,21 +176,22 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
     for (int tt = 0; tt < 2; ++tt) {
         const int tl = 64 * wave + 32 * tt + l32;
         // keys past the chunk end decode key 0's codes (finite, never attended)
-        const int64_t tok = (int64_t)b * N + tok0 + (tl < valid ? tl : 0);
+        const int64_t key = tok0 + (tl < valid ? tl : 0);
+        const int64_t tok = (int64_t)b * p.N + history_row(p, key);
         prow[tt] = c.packed + tok * (R / 2) + 16 * hf;
         srow[tt] = c.scales + tok * NG;
     }
     const int t = 64 * wave + lane;
-    const uint16_t* wsrc = c.w_dec + (int64_t)(h * CK_D + (t >> 3)) * R + 8 * (t & 7);
+    const uint16_t* wsrc = c.w + (int64_t)h * c.w_hs + (int64_t)(t >> 3) * R + 8 * (t & 7);
     uint16_t* wdst = wst + (t >> 3) * WS_ROW + 8 * (t & 7);
-    auto wload = [&](int kq, u32x4 (&r)[4]) {
+    auto wload = [&](int kq, u32x4 (&r)[NDT]) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
+        for (int e = 0; e < NDT; ++e)
             r[e] = *reinterpret_cast<const u32x4*>(wsrc + (int64_t)32 * e * R + 64 * kq);
     };
-    auto wstore = [&](int buf, const u32x4 (&r)[4]) {
+    auto wstore = [&](int buf, const u32x4 (&r)[NDT]) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e)
+        for (int e = 0; e < NDT; ++e)
             *reinterpret_cast<u32x4*>(wdst + buf * WS_BUF + 32 * e * WS_ROW) = r[e];
     };
     auto cload = [&](int kq, u32x4 (&pk)[2], float (&sc)[2]) {
@@ -180,21 +204,21 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
         }
     };
 
-    f32x16 acc[4][2];
+    f32x16 acc[NDT][2];
 #pragma unroll
-    for (int dt = 0; dt < 4; ++dt)
+    for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) acc[dt][tt] = f32x16{};
 
     // V: this wave's center rows go to its own K rows (store_center_rows);
     // their loads are issued first so that they overlap the prologue.
     u32x4 cst[16];
-    if (CODEC == 1 && HAS_C) load_center_rows(cst, sm, c, 1, b, h, HD, wave, lane);
+    if (CODEC == 1 && HAS_C) load_center_rows(cst, sm, c, 1, b, h, wave, lane);
 
     // One slice ahead: codes (HBM) and decoder rows for slice kq+1 are
     // requested while slice kq is multiplied; the rows go to the other LDS
     // buffer at the end of the iteration.
-    u32x4 wr[4], pk[2];
+    u32x4 wr[NDT], pk[2];
     float sc[2];
     wload(0, wr);
     cload(0, pk, sc);
@@ -203,7 +227,7 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
     __syncthreads();
     // fragment rows 32*dt + l32, k = 32*hf + 8*j within the slice
     const uint16_t* wfrag = wst + l32 * WS_ROW + 32 * hf;
-    u32x2 cen[2][4][4];  // K epilogue center values, requested during the last slice
+    u32x2 cen[2][NDT][4];  // K epilogue center values, requested during the last slice
     for (int kq = 0; kq < KQ; ++kq) {
         u32x4 pkn[2];
         float scn[2];
@@ -212,7 +236,7 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
             wload(kq + 1, wr);
             cload(kq + 1, pkn, scn);
         }
-        if (CODEC == 0 && HAS_C && !more) load_k_centers(cen, sm, c, b, h, HD, wave, lane);
+        if (CODEC == 0 && HAS_C && !more) load_k_centers<NDT>(cen, sm, c, b, h, wave, lane);
         const uint16_t* wb = wfrag + (kq & 1) * WS_BUF;
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
@@ -220,7 +244,7 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) z[tt] = unpack8(pk[tt][j], sc[tt], -7.0f * sc[tt]);
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt) {
+            for (int dt = 0; dt < NDT; ++dt) {
                 const bf16x8 w = lds_b128(wb + 32 * dt * WS_ROW + 8 * j);
 #pragma unroll
                 for (int tt = 0; tt < 2; ++tt)
@@ -246,15 +270,16 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
         // acc[dt][tt] element i: d = 32*dt + 8*(i/4) + 4*hf + i%4, key
         // 64*wave + 32*tt + l32; cen holds the center values (4 consecutive d
         // per group).
+        uint16_t* ktile = &sm.k[0][0];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
             const int t = 64 * wave + 32 * tt + l32;
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int d = 32 * dt + 8 * g + 4 * hf;
-                    u32x2* slot = reinterpret_cast<u32x2*>(&sm.k[t][d]);
+                    u32x2* slot = reinterpret_cast<u32x2*>(ktile + t * KROW + d);
                     float a[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) a[e] = acc[dt][tt][4 * g + e] + sm.bias[0][d + e];
@@ -298,6 +323,7 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
 
 // Current-chunk keys: copy K rows, transpose V into V^T (rows past the end
 // are zero).
+// (Current keys are native: the launch's DK is 128.)
 __device__ __forceinline__ void load_current_chunk(ChunkSmem& sm, const ChunkParams& p, int b,
                                                    int h, int64_t tok0, int valid, int t) {
     const bool ok = t < valid;
@@ -320,18 +346,33 @@ __device__ __forceinline__ void load_current_chunk(ChunkSmem& sm, const ChunkPar
 }
 
 // --------------------------------------------------------------- attention
-// Q^T operand fragments of 32 queries [q_blk, q_blk + 32), with the same
-// permuted d walk as the K reads; rows past the last query read row q_safe
-// (finite, never stored).
+// The d walk of the score product S^T = K Q^T over a K/Q width DK: at
+// k-step kk lane half hf supplies d = dwalk_block(kk) + dwalk_half * hf +
+// [0, 8).  The d axis is cut into blocks of 2 * HALF (HALF = min(DK, 64) / 2)
+// and each lane half walks 16-byte runs of its half-block, so a lane's
+// fragments of consecutive steps are contiguous.  K reads and Q loads use
+// the same walk.
+template <int DK>
+struct DWalk {
+    static constexpr int HALF = (DK < 64 ? DK : 64) / 2;
+    static constexpr int PER = HALF / 8;  // k-steps per half-block
+    static constexpr int KSTEPS = DK / 16;
+    static constexpr int block(int kk) { return (kk / PER) * 2 * HALF + 8 * (kk % PER); }
+};
+
+// Q^T operand fragments of 32 queries [q_blk, q_blk + 32) (width DK); rows
+// past the last query read row q_safe (finite, never stored).
+template <int DK>
 __device__ __forceinline__ void load_q_block(bf16x8 (&qf)[8], const ChunkParams& p, int b, int h,
                                              int64_t q_blk, int64_t q_safe, int lane) {
+    using W = DWalk<DK>;
     const int hf = lane >> 5, l32 = lane & 31;
     const int64_t qi = q_blk + l32;
     const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (qi < p.Q ? qi : q_safe) * p.q_st +
-                           (int64_t)h * p.q_sh + 32 * hf;
+                           (int64_t)h * p.q_sh + W::HALF * hf;
 #pragma unroll
-    for (int kk = 0; kk < 8; ++kk)
-        qf[kk] = as_bf16x8(*reinterpret_cast<const u32x4*>(qrow + 64 * (kk >> 2) + 8 * (kk & 3)));
+    for (int kk = 0; kk < W::KSTEPS; ++kk)
+        qf[kk] = as_bf16x8(*reinterpret_cast<const u32x4*>(qrow + W::block(kk)));
 }
 
 // One wave attends queries [q0, q0 + 32*NQB) to the chunk in LDS.  FULL: the
@@ -340,7 +381,7 @@ __device__ __forceinline__ void load_q_block(bf16x8 (&qf)[8], const ChunkParams&
 // fragments on entry; as soon as a query block's last score product is
 // issued, its registers are refilled with the wave's next tile (first query
 // q_next), so that tile's loads overlap this tile's remaining work.
-template <int NQB, bool FULL>
+template <int DK, int NQB, bool FULL>
 __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkParams& p, int b,
                                              int h, int bh, int chunk, int64_t q0, int nsub,
                                              int valid, int lane_in, bf16x8 (&qf)[2][8],
@@ -369,15 +410,18 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
     // offsets (< 64 KiB, folded into the ds_read instructions); without the
     // opaque step the compiler hoists one address register per unrolled
     // fragment out of the query-tile loop and spills.
-    uint32_t koff = l32 * CK_KROW + 32 * hf, voff = l32 * CK_VROW + 4 * hf;
+    using W = DWalk<DK>;
+    constexpr int KROW = KTile<DK>::ROW;
+    constexpr int KS = W::KSTEPS;
+    uint32_t koff = l32 * KROW + W::HALF * hf, voff = l32 * CK_VROW + 4 * hf;
     asm volatile("" : "+v"(koff));
     asm volatile("" : "+v"(voff));
     const uint16_t* kbase = &sm.k[0][0] + koff;
     const uint16_t* vbase = &sm.vt[0][0] + voff;
-    auto load_k = [&](int j, bf16x8 (&kf)[8]) {
-        const uint16_t* kr = kbase + 32 * j * CK_KROW;
+    auto load_k = [&](int j, bf16x8 (&kf)[KS]) {
+        const uint16_t* kr = kbase + 32 * j * KROW;
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) kf[kk] = lds_b128(kr + 64 * (kk >> 2) + 8 * (kk & 3));
+        for (int kk = 0; kk < KS; ++kk) kf[kk] = lds_b128(kr + W::block(kk));
     };
     // V^T fragments of step j: P^T operand slot jj of half-step ts holds key
     // 16*ts + 8*(jj/4) + 4*hf + jj%4 (accumulator element 8*ts + jj of S^T),
@@ -389,10 +433,10 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
             for (int db = 0; db < 4; ++db)
                 vf[ts][db] = lds_2x64(vbase + 32 * db * CK_VROW + 32 * j + 16 * ts);
     };
-    auto qk = [&](int qb, const bf16x8 (&kf)[8], f32x16& s) {
+    auto qk = [&](int qb, const bf16x8 (&kf)[KS], f32x16& s) {
         s = f32x16{};
 #pragma unroll
-        for (int kk = 0; kk < 8; ++kk) s = mfma32(kf[kk], qf[qb][kk], s);
+        for (int kk = 0; kk < KS; ++kk) s = mfma32(kf[kk], qf[qb][kk], s);
     };
     auto pv = [&](int qb, const bf16x8 (&vf)[2][4], const bf16x8 (&pb)[2]) {
 #pragma unroll
@@ -448,27 +492,27 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
         //   Y: S0 = QK(j+1), O0 += PV(j)      | softmax(S1 of step j)
         f32x16 s0, s1;
         bf16x8 p0[2], p1[2];
-        bf16x8 kf[8], vprev[2][4];
+        bf16x8 kf[KS], vprev[2][4];
         float a0, a1;
         load_k(0, kf);
         qk(0, kf, s0);
 #pragma unroll
         for (int j = 0; j < NSTEP; ++j) {
-            bf16x8 vf[2][4], kn[8];
+            bf16x8 vf[2][4], kn[KS];
             qk(NQB - 1, kf, s1);
-            if (j == NSTEP - 1) load_q_block(qf[1], p, b, h, q_next + 32, q_next, lane);
+            if (j == NSTEP - 1) load_q_block<DK>(qf[1], p, b, h, q_next + 32, q_next, lane);
             if (j > 0) pv(NQB - 1, vprev, p1);
             load_v(j, vf);
             if (j + 1 < NSTEP) load_k(j + 1, kn);
             const bool up0 = softmax(0, s0, p0, a0);
             if (j > 0 && __any(up0)) rescale(0, a0);
             if (j + 1 < NSTEP) qk(0, kn, s0);
-            if (j == NSTEP - 2) load_q_block(qf[0], p, b, h, q_next, q_next, lane);
+            if (j == NSTEP - 2) load_q_block<DK>(qf[0], p, b, h, q_next, q_next, lane);
             pv(0, vf, p0);
             const bool up1 = softmax(NQB - 1, s1, p1, a1);
             if (j > 0 && __any(up1)) rescale(NQB - 1, a1);
 #pragma unroll
-            for (int kk = 0; kk < 8; ++kk) kf[kk] = kn[kk];
+            for (int kk = 0; kk < KS; ++kk) kf[kk] = kn[kk];
 #pragma unroll
             for (int ts = 0; ts < 2; ++ts)
 #pragma unroll
@@ -478,7 +522,7 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
     } else if (FULL) {
         // one query block: step j+1's scores and step j-1's PV under step j's softmax
         f32x16 s[2];
-        bf16x8 pp[2][2], kf[8], vprev[2][4];
+        bf16x8 pp[2][2], kf[KS], vprev[2][4];
         float a0;
         load_k(0, kf);
         qk(0, kf, s[0]);
@@ -491,8 +535,8 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
                 qk(0, kf, s[nxt]);
             }
             if (j == NSTEP - 2) {
-                load_q_block(qf[0], p, b, h, q_next, q_next, lane);
-                load_q_block(qf[1], p, b, h, q_next + 32, q_next, lane);
+                load_q_block<DK>(qf[0], p, b, h, q_next, q_next, lane);
+                load_q_block<DK>(qf[1], p, b, h, q_next + 32, q_next, lane);
             }
             if (j > 0) pv(0, vprev, pp[nxt]);
             load_v(j, vf);
@@ -506,7 +550,7 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
         pv(0, vprev, pp[(NSTEP - 1) & 1]);
     } else {
         for (int j = 0; j < nsub; ++j) {
-            bf16x8 kf[8], vf[2][4];
+            bf16x8 kf[KS], vf[2][4];
             load_k(j, kf);
             load_v(j, vf);
             const int vj = valid - 32 * j;
@@ -528,8 +572,8 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
                 pv(qb, vf, pb);
             }
         }
-        load_q_block(qf[0], p, b, h, q_next, q_next, lane);
-        load_q_block(qf[1], p, b, h, q_next + 32, q_next, lane);
+        load_q_block<DK>(qf[0], p, b, h, q_next, q_next, lane);
+        load_q_block<DK>(qf[1], p, b, h, q_next + 32, q_next, lane);
     }
 
     // partial of this chunk: O / l (bf16) and m + log2(l).  Lane dword k of
@@ -559,7 +603,9 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
     }
 }
 
+template <int DK>
 __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
+    constexpr int KROW = KTile<DK>::ROW;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     ChunkSmem& sm = *reinterpret_cast<ChunkSmem*>(smem_raw);
     const int t = threadIdx.x, lane = t & 63;
@@ -576,21 +622,24 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
     const int b = bh / p.H, h = bh % p.H;
     const bool hist = chunk < p.nch_hist;
     const int64_t tok0 = (int64_t)(hist ? chunk : chunk - p.nch_hist) * CK_T;
-    const int valid = (int)min((int64_t)CK_T, (hist ? p.N : p.Nc) - tok0);
+    const int valid = (int)min((int64_t)CK_T, (hist ? p.n_rows : p.Nc) - tok0);
 
     if (hist) {
 #pragma unroll
         for (int cc = 0; cc < 2; ++cc) {
-            const nkv_codec& cd = p.codec[cc];
+            const ChunkCodec& cd = p.codec[cc];
             int id = 0;
             if (cd.centers && t < valid) {
                 // ids outside the table are clamped so that a corrupt payload
                 // cannot read out of bounds (valid payloads never hold them)
-                id = read_id(cd.ids, cd.id_bytes, (int64_t)b * p.N + tok0 + t);
+                const int64_t key = tok0 + t;
+                id = read_id(cd.ids, cd.id_bytes, (int64_t)b * p.N + history_row(p, key));
                 id = min(max(id, 0), cd.num_centers - 1);
             }
             sm.ids[cc][t] = id;
-            if (t < CK_D) sm.bias[cc][t] = cd.mean ? bf16_round(cd.mean[h * CK_D + t]) : 0.0f;
+            const int width = cc == 0 ? DK : CK_D;
+            if (t < width)
+                sm.bias[cc][t] = cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
         }
         __syncthreads();
         // V first: its decoder slices are staged in the (not yet written)
@@ -599,21 +648,20 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
         // centers.
         uint16_t* vt_scratch = &sm.vt[0][0];
         uint16_t* k_scratch = &sm.k[0][0];
-        if (p.codec[1].centers) {
-            decode_codec<1, true>(sm, vt_scratch, p.codec[1], b, h, p.HD, p.N, tok0, valid, wave,
-                                  lane);
-        } else {
-            decode_codec<1, false>(sm, vt_scratch, p.codec[1], b, h, p.HD, p.N, tok0, valid,
-                                   wave, lane);
-        }
+        if (p.codec[1].centers)
+            decode_codec<1, true, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
+                                              wave, lane);
+        else
+            decode_codec<1, false, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
+                                               wave, lane);
         __syncthreads();
         if (p.codec[0].centers)
-            decode_codec<0, true>(sm, k_scratch, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave,
-                                  lane);
+            decode_codec<0, true, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid, wave,
+                                            lane);
         else
-            decode_codec<0, false>(sm, k_scratch, p.codec[0], b, h, p.HD, p.N, tok0, valid, wave,
-                                   lane);
-    } else {
+            decode_codec<0, false, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
+                                             wave, lane);
+    } else if (DK == CK_D) {
         load_current_chunk(sm, p, b, h, tok0, valid, t);
     }
     __syncthreads();
@@ -623,8 +671,8 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
     constexpr int WAVES = CK_THREADS / 64;
     bf16x8 qf[2][8];
     if (wave < nqt) {
-        load_q_block(qf[0], p, b, h, (int64_t)wave * CK_QT, (int64_t)wave * CK_QT, lane);
-        load_q_block(qf[1], p, b, h, (int64_t)wave * CK_QT + 32, (int64_t)wave * CK_QT, lane);
+        load_q_block<DK>(qf[0], p, b, h, (int64_t)wave * CK_QT, (int64_t)wave * CK_QT, lane);
+        load_q_block<DK>(qf[1], p, b, h, (int64_t)wave * CK_QT + 32, (int64_t)wave * CK_QT, lane);
     }
     for (int qt = wave; qt < nqt; qt += WAVES) {
         const int64_t q0 = (int64_t)qt * CK_QT;
@@ -632,11 +680,11 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
         const int64_t q_next = qt + WAVES < nqt ? q0 + WAVES * CK_QT : q0;
         const bool one = q0 + 32 >= p.Q;
         if (valid == CK_T) {
-            if (one) attend_qtile<1, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
-            else attend_qtile<2, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
+            if (one) attend_qtile<DK, 1, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
+            else attend_qtile<DK, 2, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
         } else {
-            if (one) attend_qtile<1, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
-            else attend_qtile<2, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
+            if (one) attend_qtile<DK, 1, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
+            else attend_qtile<DK, 2, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
         }
     }
 }
@@ -724,11 +772,186 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
 }
 
 // ------------------------------------------------------------------ host
-size_t chunk_workspace_bytes(const nkv_attend_args* a) {
-    const int64_t nc = cdiv(a->N, CK_T) + cdiv(a->Nc, CK_T);
-    const size_t blocks = (size_t)a->B * a->H * nc * cdiv(a->Q, 32);
+ChunkCodec chunk_codec_from(const nkv_codec& c, int D, int HD) {
+    ChunkCodec v{};
+    v.packed = c.packed;
+    v.scales = c.scales;
+    v.ids = c.centers ? c.ids : nullptr;
+    v.r = c.r;
+    v.group = c.group;
+    v.scale_dtype = c.scale_dtype;
+    v.id_bytes = c.id_bytes;
+    v.num_centers = c.num_centers;
+    v.w = c.w_dec;
+    v.w_hs = (int64_t)D * c.r;
+    v.centers = c.centers;
+    v.c_bs = c.centers_batch_stride;
+    v.c_rs = HD;
+    v.c_hs = D;
+    v.bias = c.mean;
+    v.bias_hs = D;
+    return v;
+}
+
+namespace {
+
+int64_t chunk_count(int64_t keys) { return cdiv(keys, CK_T); }
+
+int check_chunk_codec(const ChunkCodec& c) {
+    NKV_REQUIRE(c.packed && c.scales && c.w, NKV_ERR_INVALID,
+                "history codec needs packed codes, scales and decode rows");
+    NKV_REQUIRE(c.r > 0 && c.r % 64 == 0 && c.r <= 4096, NKV_ERR_UNSUPPORTED,
+                "key-chunk attend needs codec ranks that are multiples of 64");
+    NKV_REQUIRE(c.group > 0 && c.group % 32 == 0 && c.r % c.group == 0, NKV_ERR_UNSUPPORTED,
+                "key-chunk attend needs scale groups that are multiples of 32 dividing r");
+    NKV_REQUIRE(c.scale_dtype == NKV_DTYPE_BF16 || c.scale_dtype == NKV_DTYPE_FP16,
+                NKV_ERR_INVALID, "bad scale_dtype");
+    if (c.centers) {
+        NKV_REQUIRE(c.ids && (c.id_bytes == 1 || c.id_bytes == 2 || c.id_bytes == 4),
+                    NKV_ERR_INVALID, "centers need ids of 1, 2 or 4 bytes");
+        NKV_REQUIRE(c.num_centers > 0, NKV_ERR_INVALID, "num_centers must be > 0");
+    }
+    return NKV_OK;
+}
+
+template <int DK>
+void launch_dk(const ChunkParams& p, int64_t blocks, hipStream_t s, int* rc) {
+    const size_t smem = sizeof(ChunkSmem);
+    hipError_t e = hipFuncSetAttribute((const void*)chunk_kernel<DK>,
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess) {
+        set_error(std::string("chunk_launch: hipFuncSetAttribute failed: ") + hipGetErrorString(e));
+        *rc = NKV_ERR_HIP;
+        return;
+    }
+    chunk_kernel<DK><<<dim3((unsigned)blocks), CK_THREADS, smem, s>>>(p);
+    e = hipGetLastError();
+    if (e != hipSuccess) {
+        set_error(std::string("chunk_launch: launch failed: ") + hipGetErrorString(e));
+        *rc = NKV_ERR_HIP;
+    }
+}
+
+}  // namespace
+
+size_t chunk_launch_workspace(const ChunkLaunchDesc& d) {
+    const int64_t nc = chunk_count(d.n_rows) + chunk_count(d.Nc);
+    const size_t blocks = (size_t)d.B * d.H * nc * cdiv(d.Q, 32);
     return blocks * 32 * CK_D * sizeof(uint16_t) + blocks * 32 * sizeof(float);
 }
+
+int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_t workspace_bytes) {
+    NKV_REQUIRE(d.dk == 32 || d.dk == 64 || d.dk == 128, NKV_ERR_UNSUPPORTED,
+                "key-chunk attend supports K/Q widths 32, 64 and 128");
+    NKV_REQUIRE(d.B >= 1 && d.H >= 1 && d.Q >= 0 && d.n_rows >= 0 && d.Nc >= 0, NKV_ERR_INVALID,
+                "bad launch shape");
+    NKV_REQUIRE(d.Nc == 0 || (d.dk == CK_D && d.k_cur && d.v_cur), NKV_ERR_INVALID,
+                "current keys need k_cur/v_cur and a 128-wide launch");
+    if (d.n_rows > 0) {
+        int rc = check_chunk_codec(d.key);
+        if (rc) return rc;
+        rc = check_chunk_codec(d.value);
+        if (rc) return rc;
+    }
+    if (d.Q == 0) return NKV_OK;
+    NKV_REQUIRE(d.q && d.out, NKV_ERR_INVALID, "q and out required");
+    const size_t need = chunk_launch_workspace(d);
+    NKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), NKV_ERR_WORKSPACE,
+                "workspace missing or smaller than the size query returned");
+    ChunkParams p;
+    p.B = d.B;
+    p.H = d.H;
+    p.nch_hist = (int)chunk_count(d.n_rows);
+    p.nch_total = p.nch_hist + (int)chunk_count(d.Nc);
+    p.qblocks = (int)cdiv(d.Q, 32);
+    p.Q = d.Q;
+    p.N = d.N;
+    p.n_rows = d.n_rows;
+    p.rows = d.rows;
+    p.Nc = d.Nc;
+    p.scale_log2 = d.softmax_scale * 1.4426950408889634f;
+    p.q = d.q;
+    p.q_sb = d.q_sb;
+    p.q_st = d.q_st;
+    p.q_sh = d.q_sh;
+    p.k_cur = d.k_cur;
+    p.k_sb = d.k_sb;
+    p.k_st = d.k_st;
+    p.k_sh = d.k_sh;
+    p.v_cur = d.v_cur;
+    p.v_sb = d.v_sb;
+    p.v_st = d.v_st;
+    p.v_sh = d.v_sh;
+    p.codec[0] = d.key;
+    p.codec[1] = d.value;
+    const size_t qrows = (size_t)d.B * d.H * p.nch_total * p.qblocks * 32;
+    p.part_o = reinterpret_cast<uint16_t*>(workspace);
+    p.part_lse = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
+                                          qrows * CK_D * sizeof(uint16_t));
+    p.out = d.out;
+    p.o_sb = d.o_sb;
+    p.o_st = d.o_st;
+    p.o_sh = d.o_sh;
+    p.lse = d.lse;
+
+    const int64_t blocks = (int64_t)d.B * d.H * p.nch_total;
+    if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
+    if (blocks > 0) {
+        int rc = NKV_OK;
+        if (d.dk == 128) launch_dk<128>(p, blocks, s, &rc);
+        else if (d.dk == 64) launch_dk<64>(p, blocks, s, &rc);
+        else launch_dk<32>(p, blocks, s, &rc);
+        if (rc) return rc;
+    }
+    if (d.ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_end, s));
+    const int64_t qblocks_total = (int64_t)d.B * d.H * p.qblocks;
+    if (qblocks_total > 0) {
+        chunk_combine_kernel<<<dim3((unsigned)qblocks_total), 64 * CB_WAVES, 0, s>>>(p);
+        NKV_LAUNCH_CHECK();
+    }
+    return NKV_OK;
+}
+
+// nkv_attend's key-chunk path: every head, all history rows, decoder tables.
+namespace {
+ChunkLaunchDesc desc_from(const nkv_attend_args* a) {
+    ChunkLaunchDesc d{};
+    d.B = a->B;
+    d.H = a->H;
+    d.dk = a->D;
+    d.Q = a->Q;
+    d.N = a->N;
+    d.n_rows = a->N;
+    d.rows = nullptr;
+    d.Nc = a->Nc;
+    d.softmax_scale = a->softmax_scale;
+    d.q = a->q;
+    d.q_sb = a->q_sb;
+    d.q_st = a->q_st;
+    d.q_sh = a->q_sh;
+    d.k_cur = a->k_cur;
+    d.k_sb = a->k_sb;
+    d.k_st = a->k_st;
+    d.k_sh = a->k_sh;
+    d.v_cur = a->v_cur;
+    d.v_sb = a->v_sb;
+    d.v_st = a->v_st;
+    d.v_sh = a->v_sh;
+    const int HD = a->H * a->D;
+    d.key = chunk_codec_from(a->key, a->D, HD);
+    d.value = chunk_codec_from(a->value, a->D, HD);
+    d.out = a->out;
+    d.o_sb = a->o_sb;
+    d.o_st = a->o_st;
+    d.o_sh = a->o_sh;
+    d.lse = a->lse;
+    d.ev_begin = a->ev_kernel_begin;
+    d.ev_end = a->ev_kernel_end;
+    return d;
+}
+}  // namespace
+
+size_t chunk_workspace_bytes(const nkv_attend_args* a) { return chunk_launch_workspace(desc_from(a)); }
 
 int chunk_check(const nkv_attend_args* a) {
     NKV_REQUIRE(a->D == CK_D, NKV_ERR_UNSUPPORTED, "key-chunk attend supports D == 128");
@@ -747,60 +970,7 @@ int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace
                         size_t workspace_bytes) {
     int rc = chunk_check(a);
     if (rc) return rc;
-    const size_t need = chunk_workspace_bytes(a);
-    NKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), NKV_ERR_WORKSPACE,
-                "workspace missing or smaller than nkv_attend_workspace_size()");
-    ChunkParams p;
-    p.B = a->B;
-    p.H = a->H;
-    p.HD = a->H * a->D;
-    p.nch_hist = (int)cdiv(a->N, CK_T);
-    p.nch_total = p.nch_hist + (int)cdiv(a->Nc, CK_T);
-    p.Q = a->Q;
-    p.N = a->N;
-    p.Nc = a->Nc;
-    p.scale_log2 = a->softmax_scale * 1.4426950408889634f;
-    p.q = a->q;
-    p.q_sb = a->q_sb;
-    p.q_st = a->q_st;
-    p.q_sh = a->q_sh;
-    p.k_cur = a->k_cur;
-    p.k_sb = a->k_sb;
-    p.k_st = a->k_st;
-    p.k_sh = a->k_sh;
-    p.v_cur = a->v_cur;
-    p.v_sb = a->v_sb;
-    p.v_st = a->v_st;
-    p.v_sh = a->v_sh;
-    p.codec[0] = a->key;
-    p.codec[1] = a->value;
-    p.qblocks = (int)cdiv(a->Q, 32);
-    const size_t qrows = (size_t)a->B * a->H * p.nch_total * p.qblocks * 32;
-    p.part_o = reinterpret_cast<uint16_t*>(workspace);
-    p.part_lse = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
-                                          qrows * CK_D * sizeof(uint16_t));
-    p.out = a->out;
-    p.o_sb = a->o_sb;
-    p.o_st = a->o_st;
-    p.o_sh = a->o_sh;
-    p.lse = a->lse;
-
-    const int64_t blocks = (int64_t)a->B * a->H * p.nch_total;
-    if (a->ev_kernel_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)a->ev_kernel_begin, s));
-    if (blocks > 0) {
-        const size_t smem = sizeof(ChunkSmem);
-        NKV_HIP_CHECK(hipFuncSetAttribute((const void*)chunk_kernel,
-                                          hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem));
-        chunk_kernel<<<dim3((unsigned)blocks), CK_THREADS, smem, s>>>(p);
-        NKV_LAUNCH_CHECK();
-    }
-    if (a->ev_kernel_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)a->ev_kernel_end, s));
-    const int64_t qblocks_total = (int64_t)a->B * a->H * p.qblocks;
-    if (qblocks_total > 0) {
-        chunk_combine_kernel<<<dim3((unsigned)qblocks_total), 64 * CB_WAVES, 0, s>>>(p);
-        NKV_LAUNCH_CHECK();
-    }
-    return NKV_OK;
+    return chunk_launch(s, desc_from(a), workspace, workspace_bytes);
 }
 
 }  // namespace nkv

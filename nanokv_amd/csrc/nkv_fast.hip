@@ -1,0 +1,356 @@
+// nkv_fast.hip -- NanoKV-Fast mixed-dimensional history attention for gfx950
+// (nkv_fast_attend): hybrid_attention (CN/core.py:278-310) with the partition
+// reads of maybe_attention (CN/mg35.py:100-357), fused per partition.
+//
+// Per layer call:
+//  1. native partition: every head attends its queries to the protected
+//     history rows (decoded in-kernel at full width, as nkv_attend does) and
+//     the current keys -> out (bf16) and lse_n (CN/mg35.py:192-303);
+//  2. per reader group (CN/core.py:155-204), for its heads:
+//       q_low   = bf16(q . q_reduce)                          (query, :164-166)
+//       centers = bf16(center columns . affine), bias = bf16(bf16(mean) . affine)
+//       k_low   = bf16(bf16(latent . k_read^T + bias) + centers[id])  (read, :168-200)
+//       v_low   likewise with v_read / v_affine (width D)
+//     the low rows are attended by the same key-chunk kernel at K/Q width d,
+//     decoding k_low / v_low in-kernel -> out_l, lse_l;
+//  3. merge(out, lse_n, out_l, lse_l) per group head (CN/core.py:33-42), the
+//     lift being the identity (vd == D).
+// The projected tables are small (C x d per head); they are recomputed per
+// call, as the reference's read does.
+#include "nkv_common.h"
+#include "nkv_internal.h"
+
+#include <vector>
+
+namespace nkv {
+
+// out[b][i][m][e] = bf16(sum_d x(b, m, heads[i], d) * w[i][d][e]) with
+// x(b, m, h, d) = x[b*x_b + m*x_m + h*x_h + d] (bf16 bits, or fp32 rounded to
+// bf16 first when X_F32), w == null meaning the identity (E == D).  The
+// output element is stored at out[b*o_b + i*o_i + m*o_m + e]; OUT_F32 stores
+// the bf16-rounded value as fp32.  One thread per output element, fp32
+// accumulation.
+template <bool X_F32, bool OUT_F32>
+__global__ void __launch_bounds__(256) project_kernel(const void* x, int64_t x_b, int64_t x_m,
+                                                      int64_t x_h, const int32_t* heads, int H,
+                                                      const uint16_t* w, int D, int E, int nb,
+                                                      int nh, int64_t M, void* out, int64_t o_b,
+                                                      int64_t o_i, int64_t o_m) {
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t total = (int64_t)nb * nh * M * E;
+    if (tid >= total) return;
+    const int e = (int)(tid % E);
+    int64_t r = tid / E;
+    const int64_t m = r % M;
+    r /= M;
+    const int i = (int)(r % nh);
+    const int b = (int)(r / nh);
+    // head indices outside the layer are clamped (no out-of-bounds reads)
+    const int64_t base = (int64_t)b * x_b + m * x_m + (int64_t)min(max(heads[i], 0), H - 1) * x_h;
+    float acc;
+    if (w == nullptr) {
+        acc = X_F32 ? bf16_round(reinterpret_cast<const float*>(x)[base + e])
+                    : bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[base + e]);
+    } else {
+        acc = 0.0f;
+        const uint16_t* wi = w + (int64_t)i * D * E + e;
+        for (int d = 0; d < D; ++d) {
+            const float xv = X_F32 ? bf16_round(reinterpret_cast<const float*>(x)[base + d])
+                                   : bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[base + d]);
+            acc = fmaf(xv, bf16_bits_to_f32(wi[(int64_t)d * E]), acc);
+        }
+    }
+    const int64_t o = (int64_t)b * o_b + (int64_t)i * o_i + m * o_m + e;
+    if (OUT_F32) reinterpret_cast<float*>(out)[o] = bf16_round(acc);
+    else reinterpret_cast<uint16_t*>(out)[o] = f32_to_bf16_bits(acc);
+}
+
+// Merge of each group head's native and low partitions, in place in out
+// (CN/core.py:33-42): lse = logaddexp(la, lb); origin = lse if finite else
+// 0; out = a e^(la - origin) + b e^(lb - origin) in fp32, rounded to bf16.
+// One thread per (b, q, i) row of D values.
+__global__ void __launch_bounds__(256) group_merge_kernel(
+    int B, int64_t Q, int nh, int D, const int32_t* heads, uint16_t* out, int64_t o_sb,
+    int64_t o_st, int64_t o_sh, const float* lse_n, int H, const uint16_t* low, const float* lse_l,
+    float* lse_out) {
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= (int64_t)B * Q * nh) return;
+    const int i = (int)(tid % nh);
+    const int64_t q = (tid / nh) % Q;
+    const int b = (int)(tid / ((int64_t)nh * Q));
+    const int h = min(max(heads[i], 0), H - 1);
+    const float x = lse_n[((int64_t)b * H + h) * Q + q];
+    const float y = lse_l[((int64_t)b * nh + i) * Q + q];
+    // logaddexp: max + log1p(exp(-|x - y|)); equal inputs (including -inf) give x + ln 2
+    const float l = x == y ? x + 0.69314718055994531f : fmaxf(x, y) + log1pf(expf(-fabsf(x - y)));
+    const float origin = isfinite(l) ? l : 0.0f;
+    const float wa = expf(x - origin), wb = expf(y - origin);
+    uint16_t* orow = out + (int64_t)b * o_sb + q * o_st + (int64_t)h * o_sh;
+    const uint16_t* lrow = low + (((int64_t)b * Q + q) * nh + i) * D;
+    for (int d = 0; d < D; ++d)
+        orow[d] = f32_to_bf16_bits(bf16_bits_to_f32(orow[d]) * wa + bf16_bits_to_f32(lrow[d]) * wb);
+    if (lse_out) lse_out[((int64_t)b * H + h) * Q + q] = l;
+}
+
+namespace {
+
+constexpr size_t WS_ALIGN = 256;
+size_t align_up(size_t n) { return (n + WS_ALIGN - 1) / WS_ALIGN * WS_ALIGN; }
+
+// Workspace of one call: fixed buffers, then one partial area reused by
+// every chunk launch (they run in stream order).
+struct FastLayout {
+    size_t lse_n;                  // [B, H, Q] f32
+    std::vector<size_t> q_low, kc, vc, kb, vb, out_l, lse_l;  // per group
+    size_t partials;
+    size_t total;
+};
+
+int validate(const nkv_fast_args* f) {
+    NKV_REQUIRE(f, NKV_ERR_INVALID, "null args");
+    const nkv_attend_args& a = f->attend;
+    NKV_REQUIRE(a.B >= 1 && a.H >= 1 && a.D == 128, NKV_ERR_UNSUPPORTED,
+                "fast attend supports D == 128");
+    NKV_REQUIRE(a.Q >= 0 && a.N >= 0 && a.Nc >= 0, NKV_ERR_INVALID, "negative length");
+    NKV_REQUIRE(f->n_protect >= 0 && f->n_low >= 0 && f->n_protect <= a.N && f->n_low <= a.N,
+                NKV_ERR_INVALID, "protected/low row counts out of range");
+    NKV_REQUIRE(f->n_protect == 0 || f->protect_rows, NKV_ERR_INVALID, "protect_rows missing");
+    NKV_REQUIRE(f->n_low == 0 || f->low_rows, NKV_ERR_INVALID, "low_rows missing");
+    NKV_REQUIRE(f->num_groups >= 0 && (f->num_groups == 0 || f->groups), NKV_ERR_INVALID,
+                "groups missing");
+    if (a.Q > 0) NKV_REQUIRE(a.q && a.out, NKV_ERR_INVALID, "q and out required");
+    if (a.Nc > 0) NKV_REQUIRE(a.k_cur && a.v_cur, NKV_ERR_INVALID, "current K/V missing");
+    if (f->n_low > 0 || f->n_protect > 0)
+        NKV_REQUIRE(a.key.packed && a.value.packed, NKV_ERR_INVALID, "history codecs missing");
+    for (int g = 0; g < f->num_groups; ++g) {
+        const nkv_reader_group& G = f->groups[g];
+        NKV_REQUIRE(G.num_heads >= 1 && G.num_heads <= a.H && G.heads, NKV_ERR_INVALID,
+                    "reader group needs 1..H heads");
+        NKV_REQUIRE(G.d == 32 || G.d == 64 || G.d == 128, NKV_ERR_UNSUPPORTED,
+                    "reader width d must be 32, 64 or 128");
+        NKV_REQUIRE(G.q_reduce || G.d == a.D, NKV_ERR_INVALID, "identity q_reduce needs d == D");
+        NKV_REQUIRE(G.k_affine || G.d == a.D, NKV_ERR_INVALID, "identity k_affine needs d == D");
+        NKV_REQUIRE(G.k_read && G.v_read, NKV_ERR_INVALID, "reader group needs k_read and v_read");
+    }
+    return NKV_OK;
+}
+
+ChunkLaunchDesc native_desc(const nkv_fast_args* f, float* lse_n) {
+    const nkv_attend_args& a = f->attend;
+    ChunkLaunchDesc d{};
+    d.B = a.B;
+    d.H = a.H;
+    d.dk = a.D;
+    d.Q = a.Q;
+    d.N = a.N;
+    d.n_rows = f->n_protect;
+    d.rows = f->protect_rows;
+    d.Nc = a.Nc;
+    d.softmax_scale = a.softmax_scale;
+    d.q = a.q;
+    d.q_sb = a.q_sb;
+    d.q_st = a.q_st;
+    d.q_sh = a.q_sh;
+    d.k_cur = a.k_cur;
+    d.k_sb = a.k_sb;
+    d.k_st = a.k_st;
+    d.k_sh = a.k_sh;
+    d.v_cur = a.v_cur;
+    d.v_sb = a.v_sb;
+    d.v_st = a.v_st;
+    d.v_sh = a.v_sh;
+    const int HD = a.H * a.D;
+    d.key = chunk_codec_from(a.key, a.D, HD);
+    d.value = chunk_codec_from(a.value, a.D, HD);
+    d.out = a.out;
+    d.o_sb = a.o_sb;
+    d.o_st = a.o_st;
+    d.o_sh = a.o_sh;
+    d.lse = lse_n;
+    d.ev_begin = a.ev_kernel_begin;
+    d.ev_end = a.ev_kernel_end;
+    return d;
+}
+
+// Batch items that have their own center table (0: one shared table).
+int table_batches(const nkv_codec& c, int B) { return c.centers_batch_stride ? B : 1; }
+
+// Low-partition launch of group g over the workspace tables.
+ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const FastLayout& L) {
+    const nkv_attend_args& a = f->attend;
+    const nkv_reader_group& G = f->groups[g];
+    const int nh = G.num_heads, dd = G.d, D = a.D;
+    ChunkLaunchDesc d{};
+    d.B = a.B;
+    d.H = nh;
+    d.dk = dd;
+    d.Q = a.Q;
+    d.N = a.N;
+    d.n_rows = f->n_low;
+    d.rows = f->low_rows;
+    d.Nc = 0;
+    d.softmax_scale = a.softmax_scale;
+    d.q = reinterpret_cast<const uint16_t*>(ws + L.q_low[g]);  // [B, Q, nh, d]
+    d.q_sb = a.Q * nh * dd;
+    d.q_st = (int64_t)nh * dd;
+    d.q_sh = dd;
+    for (int cc = 0; cc < 2; ++cc) {
+        const nkv_codec& c = cc ? a.value : a.key;
+        ChunkCodec v{};
+        v.packed = c.packed;
+        v.scales = c.scales;
+        v.ids = c.centers ? c.ids : nullptr;
+        v.r = c.r;
+        v.group = c.group;
+        v.scale_dtype = c.scale_dtype;
+        v.id_bytes = c.id_bytes;
+        v.num_centers = c.num_centers;
+        const int width = cc ? D : dd;
+        v.w = cc ? G.v_read : G.k_read;
+        v.w_hs = (int64_t)width * c.r;
+        if (c.centers) {
+            // projected table [tables][nh][C][width]
+            v.centers = reinterpret_cast<const uint16_t*>(ws + (cc ? L.vc[g] : L.kc[g]));
+            v.c_rs = width;
+            v.c_hs = (int64_t)c.num_centers * width;
+            v.c_bs = c.centers_batch_stride ? (int64_t)nh * c.num_centers * width : 0;
+        }
+        if (c.mean) {
+            v.bias = reinterpret_cast<const float*>(ws + (cc ? L.vb[g] : L.kb[g]));
+            v.bias_hs = width;
+        }
+        (cc ? d.value : d.key) = v;
+    }
+    d.out = reinterpret_cast<uint16_t*>(ws + L.out_l[g]);  // [B, Q, nh, D]
+    d.o_sb = a.Q * nh * D;
+    d.o_st = (int64_t)nh * D;
+    d.o_sh = D;
+    d.lse = reinterpret_cast<float*>(ws + L.lse_l[g]);
+    return d;
+}
+
+FastLayout layout(const nkv_fast_args* f) {
+    const nkv_attend_args& a = f->attend;
+    FastLayout L;
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off += align_up(bytes);
+        return o;
+    };
+    L.lse_n = take(a.lse ? 0 : (size_t)a.B * a.H * a.Q * sizeof(float));
+    size_t part = chunk_launch_workspace(native_desc(f, nullptr));
+    for (int g = 0; g < f->num_groups; ++g) {
+        const nkv_reader_group& G = f->groups[g];
+        const size_t nh = G.num_heads, dd = G.d, D = a.D;
+        L.q_low.push_back(take((size_t)a.B * a.Q * nh * dd * 2));
+        const size_t kt = a.key.centers ? (size_t)table_batches(a.key, a.B) : 0;
+        const size_t vt = a.value.centers ? (size_t)table_batches(a.value, a.B) : 0;
+        L.kc.push_back(take(kt * nh * a.key.num_centers * dd * 2));
+        L.vc.push_back(take(vt * nh * a.value.num_centers * D * 2));
+        L.kb.push_back(take(nh * dd * sizeof(float)));
+        L.vb.push_back(take(nh * D * sizeof(float)));
+        L.out_l.push_back(take((size_t)a.B * a.Q * nh * D * 2));
+        L.lse_l.push_back(take((size_t)a.B * nh * a.Q * sizeof(float)));
+    }
+    for (int g = 0; g < f->num_groups; ++g) {
+        ChunkLaunchDesc shape{};
+        shape.B = a.B;
+        shape.H = f->groups[g].num_heads;
+        shape.Q = a.Q;
+        shape.n_rows = f->n_low;
+        part = std::max(part, chunk_launch_workspace(shape));
+    }
+    L.partials = take(part);
+    L.total = off;
+    return L;
+}
+
+template <bool XF, bool OF>
+int project(hipStream_t s, const void* x, int64_t x_b, int64_t x_m, int64_t x_h,
+            const int32_t* heads, int H, const uint16_t* w, int D, int E, int nb, int nh,
+            int64_t M, void* out, int64_t o_b, int64_t o_i, int64_t o_m) {
+    const int64_t total = (int64_t)nb * nh * M * E;
+    if (total == 0) return NKV_OK;
+    project_kernel<XF, OF><<<dim3((unsigned)cdiv(total, 256)), 256, 0, s>>>(
+        x, x_b, x_m, x_h, heads, H, w, D, E, nb, nh, M, out, o_b, o_i, o_m);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+}  // namespace
+
+}  // namespace nkv
+
+using namespace nkv;
+
+extern "C" size_t nkv_fast_attend_workspace_size(const nkv_fast_args* f) {
+    clear_error();
+    if (validate(f)) return 0;
+    return layout(f).total;
+}
+
+extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* workspace,
+                               size_t workspace_bytes) {
+    clear_error();
+    int rc = validate(f);
+    if (rc) return rc;
+    const nkv_attend_args& a = f->attend;
+    if (a.Q == 0) return NKV_OK;
+    hipStream_t s = (hipStream_t)stream;
+    const FastLayout L = layout(f);
+    NKV_REQUIRE(workspace && workspace_bytes >= L.total, NKV_ERR_WORKSPACE,
+                "workspace missing or smaller than nkv_fast_attend_workspace_size()");
+    unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
+    const size_t part_bytes = L.total - L.partials;
+    // the native partition's LSE goes to the caller's lse when it asked for
+    // one; the merges then update it in place
+    float* lse_n = a.lse ? a.lse : reinterpret_cast<float*>(ws + L.lse_n);
+
+    // 1. native partition -> out, lse_n
+    rc = chunk_launch(s, native_desc(f, lse_n), ws + L.partials, part_bytes);
+    if (rc) return rc;
+    // no low rows: the native partition is the whole attention
+    if (f->n_low == 0) return NKV_OK;
+
+    // 2-3. reader groups
+    const int D = a.D, HD = a.H * a.D;
+    for (int g = 0; g < f->num_groups; ++g) {
+        const nkv_reader_group& G = f->groups[g];
+        const int nh = G.num_heads, dd = G.d;
+        // q_low [B, Q, nh, d]
+        rc = project<false, false>(s, a.q, a.q_sb, a.q_st, a.q_sh, G.heads, a.H, G.q_reduce, D, dd, a.B,
+                                   nh, a.Q, ws + L.q_low[g], a.Q * nh * dd, dd, (int64_t)nh * dd);
+        if (rc) return rc;
+        for (int cc = 0; cc < 2 && f->n_low > 0; ++cc) {
+            const nkv_codec& c = cc ? a.value : a.key;
+            const int width = cc ? D : dd;
+            const uint16_t* aff = cc ? G.v_affine : G.k_affine;
+            if (c.centers) {
+                // [tables][nh][C][width] = center columns of each head . affine
+                const int nb = table_batches(c, a.B);
+                rc = project<false, false>(s, c.centers, c.centers_batch_stride, HD, D, G.heads, a.H, aff,
+                                           D, width, nb, nh, c.num_centers,
+                                           ws + (cc ? L.vc[g] : L.kc[g]),
+                                           (int64_t)nh * c.num_centers * width,
+                                           (int64_t)c.num_centers * width, width);
+                if (rc) return rc;
+            }
+            if (c.mean) {
+                // [nh][width] = bf16(mean of each head) . affine
+                rc = project<true, true>(s, c.mean, 0, 0, D, G.heads, a.H, aff, D, width, 1, nh, 1,
+                                         ws + (cc ? L.vb[g] : L.kb[g]), 0, width, 0);
+                if (rc) return rc;
+            }
+        }
+        rc = chunk_launch(s, low_desc(f, g, ws, L), ws + L.partials, part_bytes);
+        if (rc) return rc;
+        const int64_t rows = (int64_t)a.B * a.Q * nh;
+        group_merge_kernel<<<dim3((unsigned)cdiv(rows, 256)), 256, 0, s>>>(
+            a.B, a.Q, nh, D, G.heads, a.out, a.o_sb, a.o_st, a.o_sh, lse_n, a.H,
+            reinterpret_cast<const uint16_t*>(ws + L.out_l[g]),
+            reinterpret_cast<const float*>(ws + L.lse_l[g]), a.lse);
+        NKV_LAUNCH_CHECK();
+    }
+    return NKV_OK;
+}

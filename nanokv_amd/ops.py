@@ -17,7 +17,8 @@ import torch
 from . import _lib
 from ._lib import (NKV_DTYPE_BF16, NKV_DTYPE_FP16, NKV_QUANT_BF16, NKV_QUANT_FP32,
                    NKV_SCHEDULE_AUTO, NKV_SCHEDULE_KEY_CHUNKS, NKV_SCHEDULE_QUERY_TILES,
-                   NkvAttendArgs, NkvCodec, NkvDecodeArgs, NkvEncodeArgs, check, lib)
+                   NkvAttendArgs, NkvCodec, NkvDecodeArgs, NkvEncodeArgs, NkvFastArgs,
+                   NkvReaderGroup, check, lib)
 
 _SCALE_CODES = {torch.bfloat16: NKV_DTYPE_BF16, torch.float16: NKV_DTYPE_FP16}
 _QUANT_CODES = {"fp32": NKV_QUANT_FP32, "bf16": NKV_QUANT_BF16}
@@ -267,32 +268,19 @@ def _strides_bthd(t: torch.Tensor, name: str) -> tuple[int, int, int]:
     return t.stride(0), t.stride(1), t.stride(2)
 
 
-def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
-           key: Optional[Codec] = None, value: Optional[Codec] = None, *,
-           softmax_scale: Optional[float] = None, return_lse: bool = True,
-           splits: int = 0, out: Optional[torch.Tensor] = None,
-           kernel_events: Optional[tuple[int, int]] = None,
-           workspace: Optional[torch.Tensor] = None, schedule: str = "auto"):
-    """Fused decode+attention (see nkv_attend).
-
-    q [B, Q, H, D] bf16; k_cur/v_cur [B, Nc, H, D] bf16 or None; key/value
-    history codecs (both or neither).  Returns (out [B, Q, H, D] bf16,
-    lse [B, H, Q] fp32 or None).  kernel_events: optional (begin, end) raw
-    hipEvent_t handles recorded around the fused kernel.  workspace: optional
-    preallocated uint8 buffer of at least nkv_attend_workspace_size bytes.
-    schedule: "auto", "query_tiles" or "key_chunks" (nkv_schedule).
-    """
-    if schedule not in SCHEDULES:
-        raise ValueError(f"schedule must be one of {sorted(SCHEDULES)}")
+def _attend_args(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
+                 key: Optional[Codec], value: Optional[Codec], softmax_scale: Optional[float],
+                 out: Optional[torch.Tensor], return_lse: bool):
+    """Validated nkv_attend_args for [B, Q, H, D] q and [B, Nc, H, D] current K/V;
+    allocates out / lse when not given."""
     device = _require_gpu(q, k_cur, v_cur)
     if q.dtype != torch.bfloat16:
         raise TypeError("q must be bf16")
     B, Qn, H, D = (int(v) for v in q.shape)
     hd = H * D
     args = NkvAttendArgs()
-    args.B, args.H, args.D, args.splits, args.Q = B, H, D, int(splits), Qn
+    args.B, args.H, args.D, args.Q = B, H, D, Qn
     args.softmax_scale = D ** -0.5 if softmax_scale is None else float(softmax_scale)
-    args.schedule = SCHEDULES[schedule]
     args.q = q.data_ptr()
     args.q_sb, args.q_st, args.q_sh = _strides_bthd(q, "q")
     if (key is None) != (value is None):
@@ -322,6 +310,30 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
     args.o_sb, args.o_st, args.o_sh = _strides_bthd(out, "out")
     lse = torch.empty((B, H, Qn), device=device, dtype=torch.float32) if return_lse else None
     args.lse = _ptr(lse)
+    return args, out, lse, device
+
+
+def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
+           key: Optional[Codec] = None, value: Optional[Codec] = None, *,
+           softmax_scale: Optional[float] = None, return_lse: bool = True,
+           splits: int = 0, out: Optional[torch.Tensor] = None,
+           kernel_events: Optional[tuple[int, int]] = None,
+           workspace: Optional[torch.Tensor] = None, schedule: str = "auto"):
+    """Fused decode+attention (see nkv_attend).
+
+    q [B, Q, H, D] bf16; k_cur/v_cur [B, Nc, H, D] bf16 or None; key/value
+    history codecs (both or neither).  Returns (out [B, Q, H, D] bf16,
+    lse [B, H, Q] fp32 or None).  kernel_events: optional (begin, end) raw
+    hipEvent_t handles recorded around the fused kernel.  workspace: optional
+    preallocated uint8 buffer of at least nkv_attend_workspace_size bytes.
+    schedule: "auto", "query_tiles" or "key_chunks" (nkv_schedule).
+    """
+    if schedule not in SCHEDULES:
+        raise ValueError(f"schedule must be one of {sorted(SCHEDULES)}")
+    args, out, lse, device = _attend_args(q, k_cur, v_cur, key, value, softmax_scale, out,
+                                          return_lse)
+    args.splits = int(splits)
+    args.schedule = SCHEDULES[schedule]
     if kernel_events is not None:
         args.ev_kernel_begin, args.ev_kernel_end = kernel_events
     need = lib().nkv_attend_workspace_size(byref(args))
@@ -332,6 +344,82 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
         workspace = torch.empty(need, device=device, dtype=torch.uint8)
     check("nkv_attend", lib().nkv_attend(_stream(device), byref(args),
                                          _ptr(workspace) if need else None, need))
+    return out, lse
+
+
+@dataclass
+class ReaderTensors:
+    """Device tensors of one NanoKV-Fast reader group (nkv_reader_group):
+    heads int32 [nh]; k_read bf16 [nh, d, rK]; v_read bf16 [nh, D, rV];
+    q_reduce / k_affine bf16 [nh, D, d] and v_affine bf16 [nh, D, D], each
+    None for the identity."""
+    heads: torch.Tensor
+    d: int
+    k_read: torch.Tensor
+    v_read: torch.Tensor
+    q_reduce: Optional[torch.Tensor] = None
+    k_affine: Optional[torch.Tensor] = None
+    v_affine: Optional[torch.Tensor] = None
+
+    def struct(self, D: int, rK: int, rV: int) -> NkvReaderGroup:
+        nh, d = int(self.heads.numel()), int(self.d)
+        _contig(self.heads, torch.int32, "heads")
+        expect = {"k_read": (nh, d, rK), "v_read": (nh, D, rV), "q_reduce": (nh, D, d),
+                  "k_affine": (nh, D, d), "v_affine": (nh, D, D)}
+        for name, shape in expect.items():
+            t = getattr(self, name)
+            if t is None:
+                if name in ("k_read", "v_read"):
+                    raise ValueError(f"{name} is required")
+                continue
+            _contig(t, torch.bfloat16, name)
+            if tuple(t.shape) != shape:
+                raise ValueError(f"bad {name} shape {tuple(t.shape)}; expected {shape}")
+        g = NkvReaderGroup()
+        g.num_heads, g.d, g.heads = nh, d, self.heads.data_ptr()
+        g.k_read, g.v_read = self.k_read.data_ptr(), self.v_read.data_ptr()
+        g.q_reduce, g.k_affine, g.v_affine = (_ptr(self.q_reduce), _ptr(self.k_affine),
+                                              _ptr(self.v_affine))
+        return g
+
+
+def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
+                key: Codec, value: Codec, protect_rows: torch.Tensor, low_rows: torch.Tensor,
+                groups: list, *, softmax_scale: Optional[float] = None,
+                return_lse: bool = True, out: Optional[torch.Tensor] = None,
+                kernel_events: Optional[tuple[int, int]] = None,
+                workspace: Optional[torch.Tensor] = None):
+    """NanoKV-Fast mixed-dimensional attention (see nkv_fast_attend).
+
+    protect_rows / low_rows: int32 codec rows of the native and low
+    partitions; groups: ReaderTensors covering every head once.  Returns
+    (out [B, Q, H, D] bf16, lse [B, H, Q] fp32 or None).
+    """
+    args, out, lse, device = _attend_args(q, k_cur, v_cur, key, value, softmax_scale, out,
+                                          return_lse)
+    if kernel_events is not None:
+        args.ev_kernel_begin, args.ev_kernel_end = kernel_events
+    _require_gpu(protect_rows, low_rows, *[g.heads for g in groups])
+    _contig(protect_rows, torch.int32, "protect_rows")
+    _contig(low_rows, torch.int32, "low_rows")
+    f = NkvFastArgs()
+    f.attend = args
+    f.protect_rows, f.n_protect = protect_rows.data_ptr(), protect_rows.numel()
+    f.low_rows, f.n_low = low_rows.data_ptr(), low_rows.numel()
+    D = int(q.shape[3])
+    structs = (NkvReaderGroup * max(1, len(groups)))()
+    for i, g in enumerate(groups):
+        structs[i] = g.struct(D, key.r, value.r)
+    f.num_groups = len(groups)
+    f.groups = structs
+    need = lib().nkv_fast_attend_workspace_size(byref(f))
+    err = lib().nkv_last_error().decode()
+    if need == 0 and err:
+        raise _lib.NanoKVError("nkv_fast_attend_workspace_size", _lib.NKV_ERR_INVALID, err)
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), device=device, dtype=torch.uint8)
+    check("nkv_fast_attend", lib().nkv_fast_attend(_stream(device), byref(f), _ptr(workspace),
+                                                   need))
     return out, lse
 
 

@@ -66,7 +66,18 @@ CONFIGS = {
              rV=384, G=32, C=256),
     2: Shape("cfg2_h24_d128_n49920_q780", H=24, D=128, N=49920, Q=780, Nc=780, rK=384, rV=256,
              G=32, C=1024),
+    # NanoKV-Fast on the config-1 shapes (reader layout in make_readers)
+    3: Shape("cfg3_fast_h24_d128_n12480_q1560", H=24, D=128, N=12480, Q=1560, Nc=1560, rK=384,
+             rV=384, G=32, C=256),
 }
+
+# Config 3: 6 of 24 heads keep full-width reads (identity readers), the rest
+# read K and Q through random 384->32 / 128->32 projections with V at full
+# width; the last 2 frames of 1,560 tokens are protected for every head.
+FAST_FULL_HEADS = (0, 4, 8, 12, 16, 20)
+FAST_READER_D = 32
+FAST_FRAME_TOKENS = 1560
+FAST_RECENT_FRAMES = 2
 
 
 def _gen(seed: int, device) -> torch.Generator:
@@ -149,3 +160,55 @@ def queries(shape: Shape, seed: int, device="cpu") -> torch.Tensor:
     g = _gen(seed, device)
     q = torch.randn(shape.B, shape.Q, shape.H, shape.D, generator=g, device=device)
     return (q / shape.D ** 0.5).to(torch.bfloat16)
+
+
+def make_readers(shape: Shape, layer: Layer, seed: int = 0, full_heads=FAST_FULL_HEADS,
+                 d: int = FAST_READER_D) -> dict:
+    """A NanoKV-Fast reader payload (the layout CN/core.py:207-224 loads) for
+    config 3: one identity group over full_heads (q_reduce = k_affine =
+    v_affine = lift = I, k_read / v_read = the head's decoder rows, so its
+    low read equals the full decode) and one group over the other heads with
+    random N(0,1)/sqrt(fan-in) bf16 q_reduce [D, d], k_read [d, rK] and
+    k_affine [D, d], v_read = the head's V decoder rows and identity
+    v_affine / lift.  Tensors are fp32 on the CPU (bf16-representable), as
+    reader checkpoints store them."""
+    g = _gen(seed * 1000 + 29, "cpu")
+    H, D = shape.H, shape.D
+    full = [h for h in range(H) if h in set(full_heads)]
+    low = [h for h in range(H) if h not in set(full_heads)]
+    wk = layer.w_dec_k.float().cpu().reshape(H, D, shape.rK)
+    wv = layer.w_dec_v.float().cpu().reshape(H, D, shape.rV)
+    eye = torch.eye(D)
+
+    def bf(t):
+        return t.to(torch.bfloat16).float()
+
+    def group(heads, dd, identity):
+        n = len(heads)
+        hs = torch.tensor(heads, dtype=torch.long)
+        if identity:
+            qr = eye.expand(n, D, D).clone()
+            kr = wk[hs].clone()
+            ka = eye.expand(n, D, D).clone()
+        else:
+            qr = bf(torch.randn(n, D, dd, generator=g) / D ** 0.5)
+            kr = bf(torch.randn(n, dd, shape.rK, generator=g) / shape.rK ** 0.5)
+            ka = bf(torch.randn(n, D, dd, generator=g) / D ** 0.5)
+        return {"heads": hs, "indices": torch.arange(dd).expand(n, dd).clone(),
+                "v_indices": torch.arange(D).expand(n, D).clone(),
+                "q_reduce": qr, "k_read": kr, "v_read": wv[hs].clone(),
+                "k_affine": ka, "v_affine": eye.expand(n, D, D).clone(),
+                "lift": eye.expand(n, D, D).clone()}
+
+    groups = [group(full, D, True)]
+    if low:
+        groups.append(group(low, d, False))
+    return {"groups": groups, "heads": H, "native_dim": D, "rank": shape.rK}
+
+
+def fast_protect_mask(shape: Shape, frame_tokens: int = FAST_FRAME_TOKENS,
+                      recent: int = FAST_RECENT_FRAMES, device="cpu") -> torch.Tensor:
+    """bool [N]: history tokens of the last `recent` frames (protected)."""
+    frames = (shape.N + frame_tokens - 1) // frame_tokens
+    frame_of = torch.arange(shape.N, device=device) // frame_tokens
+    return frame_of >= frames - recent

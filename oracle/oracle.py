@@ -359,3 +359,96 @@ def protected_frames(count: int, recent: int, stride: int, sink: int = 0) -> np.
     if stride and old:
         keep[np.arange(old - 1, -1, -stride)] = True
     return keep
+
+
+# ----------------------------------------------------------------- a14-a16
+def reader_tables(centers_bf16, mean, h: int, affine_bf16, D: int = 128, dtype=np.float64):
+    """Projected center rows and bias of one reader head (CN/core.py:179-199):
+    table = bf16(C_h . affine), bias = bf16(bf16(mean_h) . affine); an affine
+    of None is the identity (table = C_h, bias = bf16(mean_h)).  Returns
+    (table [C, e] bf16 bits or None, bias [e] float32 or None)."""
+    table = bias = None
+    if centers_bf16 is not None:
+        ch = _c(centers_bf16, np.uint16)[:, h * D:(h + 1) * D]
+        if affine_bf16 is None:
+            table = np.ascontiguousarray(ch)
+        else:
+            a = bf16_to_f32(affine_bf16).astype(dtype)
+            table = f32_to_bf16((bf16_to_f32(ch).astype(dtype) @ a).astype(np.float32))
+    if mean is not None:
+        mh = bf16_to_f32(f32_to_bf16(np.asarray(mean, np.float32)[h * D:(h + 1) * D]))
+        if affine_bf16 is None:
+            bias = mh.astype(np.float32)
+        else:
+            a = bf16_to_f32(affine_bf16).astype(dtype)
+            bias = bf16_to_f32(f32_to_bf16((mh.astype(dtype) @ a).astype(np.float32)))
+    return table, bias
+
+
+def reader_read(codec: dict, rows, read_bf16, table_bf16, bias, dtype=np.float64):
+    """ReaderGroup.read for one head (CN/core.py:168-200): the latent rows
+    (unpacked codes of `rows`) through F.linear with the bias before the
+    bf16 rounding, plus the projected center of each row:
+      out = bf16(bf16(latent . read^T + bias) + table[id]).
+    codec: decode() keyword dict; read_bf16 [e, r].  Returns [rows, e] bf16
+    bits (nkvo_decode_epilogue does both roundings)."""
+    return decode(codec["packed"], codec["scales"], read_bf16, codec["group"],
+                  codec.get("scale_dtype", "bf16"),
+                  codec.get("ids") if table_bf16 is not None else None,
+                  table_bf16, bias, row_index=np.asarray(rows), dtype=dtype)
+
+
+def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_rows, low_rows,
+                groups: Sequence[dict], scale: float, heads: Optional[Sequence[int]] = None,
+                D: int = 128, dtype=np.float64):
+    """NanoKV-Fast for one batch item: hybrid_attention (CN/core.py:278-310)
+    with maybe_attention's partitions (CN/mg35.py:192-348), identity lift.
+
+    native partition per head: [full decode of protect_rows; current chunk]
+    with q (bf16 output, CN/core.py:45-72); low partition for the head's
+    group: q_low = bf16(q_h . q_reduce) (CN:164-166), k_low / v_low =
+    reader_read of low_rows; merged by LSE (CN:33-42) into bf16.
+    groups: dicts with heads, q_reduce, k_read, v_read, k_affine, v_affine
+    (bf16 bits per head, None = identity).  Returns (out [Q, H', D] float32
+    of the bf16 result, lse [H', Q])."""
+    q = bf16_to_f32(q_bf16)
+    Qn, H = q.shape[0], q.shape[1]
+    heads = list(range(H)) if heads is None else list(heads)
+    prot = np.asarray(protect_rows, np.int64)
+    low = np.asarray(low_rows, np.int64)
+    outs, lses = [], []
+    for h in heads:
+        cols = np.arange(h * D, (h + 1) * D)
+        ks, vs = [], []
+        if prot.size:
+            kd = decode(**key, row_index=prot, columns=cols, dtype=dtype)
+            vd = decode(**value, row_index=prot, columns=cols, dtype=dtype)
+            ks.append(bf16_to_f32(kd))
+            vs.append(bf16_to_f32(vd))
+        if k_cur_bf16 is not None:
+            ks.append(bf16_to_f32(k_cur_bf16)[:, h])
+            vs.append(bf16_to_f32(v_cur_bf16)[:, h])
+        k = np.concatenate(ks, 0) if ks else np.zeros((0, D))
+        v = np.concatenate(vs, 0) if vs else np.zeros((0, D))
+        on, ln = attention(q[None, :, h], k[None], v[None], scale, dtype)
+        on, ln = bf16_to_f32(f32_to_bf16(on[0].astype(np.float32))), ln[0]
+        grp = [(g, list(g["heads"]).index(h)) for g in groups if h in list(g["heads"])]
+        if grp and low.size:
+            g, i = grp[0]
+            qh = q[:, h]
+            if g.get("q_reduce") is not None:
+                qr = bf16_to_f32(g["q_reduce"][i]).astype(dtype)
+                qh = bf16_to_f32(f32_to_bf16((qh.astype(dtype) @ qr).astype(np.float32)))
+            kt, kb = reader_tables(key.get("centers_bf16"), key.get("mean"), h,
+                                   None if g.get("k_affine") is None else g["k_affine"][i], D, dtype)
+            vt, vb = reader_tables(value.get("centers_bf16"), value.get("mean"), h,
+                                   None if g.get("v_affine") is None else g["v_affine"][i], D, dtype)
+            kl = bf16_to_f32(reader_read(key, low, g["k_read"][i], kt, kb, dtype))
+            vl = bf16_to_f32(reader_read(value, low, g["v_read"][i], vt, vb, dtype))
+            ol, ll = attention(qh[None], kl[None], vl[None], scale, dtype)
+            ol = bf16_to_f32(f32_to_bf16(ol[0].astype(np.float32)))
+            mo, ml = merge(on, ln, ol, ll[0])
+            on, ln = bf16_to_f32(f32_to_bf16(np.asarray(mo, np.float32))), ml
+        outs.append(on)
+        lses.append(ln)
+    return np.stack(outs, 1), np.stack(lses, 0)

@@ -106,3 +106,24 @@ class Scenario:
         vc = u16(self.v_cur[b]) if self.Nc else None
         return orc.decode_attend(u16(self.q[b]), kc, vc, key, val, self.scale, heads=heads,
                                  D=self.D)
+
+
+def oracle_groups(payload: dict) -> list:
+    """A reader payload (synth.make_readers layout) as the oracle's group
+    dicts: bf16 bits per head, None where the matrix is the identity."""
+    import torch as _t
+
+    def ident(w):
+        return w.shape[-2] == w.shape[-1] and _t.equal(w.float(), _t.eye(w.shape[-1]).expand_as(w))
+
+    out = []
+    for g in payload["groups"]:
+        out.append({
+            "heads": [int(h) for h in g["heads"]],
+            "q_reduce": None if ident(g["q_reduce"]) else u16(g["q_reduce"].to(_t.bfloat16)),
+            "k_read": u16(g["k_read"].to(_t.bfloat16)),
+            "v_read": u16(g["v_read"].to(_t.bfloat16)),
+            "k_affine": None if ident(g["k_affine"]) else u16(g["k_affine"].to(_t.bfloat16)),
+            "v_affine": None if ident(g["v_affine"]) else u16(g["v_affine"].to(_t.bfloat16)),
+        })
+    return out

@@ -1,0 +1,182 @@
+"""GPU parity of NanoKV-Fast (nkv_fast_attend) against the oracle's
+restatement of hybrid_attention (oracle.fast_attend): max-abs <= 2e-2 and
+cosine >= 0.9995 in bf16, for reader widths 32 / 64 / 128, contiguous and
+scattered protected rows, with and without centers / mean, and the full
+config-3 shape on a subset of heads."""
+import numpy as np
+import pytest
+import torch
+
+import oracle.oracle as orc
+from nanokv_amd import codec_native, ops, synth
+from tests._helpers import Scenario, max_abs_cos, oracle_groups, u16
+
+pytestmark = pytest.mark.gpu
+
+MAX_ABS = 2e-2
+MIN_COS = 0.9995
+
+
+def _run(sc, dev, payload, prot, heads=None):
+    key, value = sc.codecs(dev)
+    reader = codec_native.ReaderLayer(payload, dev)
+    N = sc.N
+    low = np.setdiff1d(np.arange(N), prot)
+    pr = torch.from_numpy(prot.astype(np.int32)).to(dev)
+    lr = torch.from_numpy(low.astype(np.int32)).to(dev)
+    kc = None if sc.k_cur is None else sc.k_cur.to(dev)
+    vc = None if sc.v_cur is None else sc.v_cur.to(dev)
+    out, lse = ops.fast_attend(sc.q.to(dev), kc, vc, key, value, pr, lr,
+                               [g.tensors() for g in reader.groups])
+    out = out.float().cpu().numpy()
+    lse = lse.cpu().numpy()
+    groups = oracle_groups(payload)
+    for b in range(sc.B):
+        kcb = None if sc.k_cur is None else u16(sc.k_cur[b])
+        vcb = None if sc.v_cur is None else u16(sc.v_cur[b])
+        ref, ref_lse = orc.fast_attend(u16(sc.q[b]), kcb, vcb, sc.hist[b]["k"], sc.hist[b]["v"],
+                                       prot, low, groups, sc.scale, heads=heads, D=sc.D)
+        hs = list(range(sc.H)) if heads is None else heads
+        diff, cos = max_abs_cos(out[b][:, hs], ref)
+        assert diff <= MAX_ABS and cos >= MIN_COS, (b, diff, cos)
+        assert np.abs(lse[b][hs] - ref_lse).max() < 2e-3
+    return out, lse
+
+
+def _payload(sc, full_heads, d, seed=0):
+    return synth.make_readers(sc.shape, sc.layer, seed=seed, full_heads=full_heads, d=d)
+
+
+@pytest.mark.parametrize("d", [32, 64, 128])
+def test_fast_reader_widths(dev, d):
+    sc = Scenario(H=4, N=700, Q=150, Nc=64, rK=384, rV=256, G=32, C=16)
+    _run(sc, dev, _payload(sc, (1,), d), np.arange(500, 700))
+
+
+@pytest.mark.parametrize("prot", ["recent", "scattered", "none", "all"])
+def test_fast_partitions(dev, prot):
+    sc = Scenario(H=2, N=600, Q=100, Nc=40, rK=256, rV=256, G=32, C=8, with_mean=True)
+    N = sc.N
+    rows = {"recent": np.arange(400, N),
+            "scattered": np.concatenate([np.arange(0, 30), np.arange(250, 260), np.arange(590, N)]),
+            "none": np.array([], np.int64), "all": np.arange(N)}[prot]
+    _run(sc, dev, _payload(sc, (0,), 32), rows)
+
+
+@pytest.mark.parametrize("G,scale_dtype,centers", [(384, torch.bfloat16, True),
+                                                   (32, torch.float16, False)])
+def test_fast_codec_variants(dev, G, scale_dtype, centers):
+    sc = Scenario(H=2, N=420, Q=70, Nc=33, rK=384, rV=384, G=G, C=12, scale_dtype=scale_dtype,
+                  centers=centers)
+    _run(sc, dev, _payload(sc, (1,), 32), np.arange(300, 420))
+
+
+def test_fast_batch_and_no_current(dev):
+    sc = Scenario(B=2, H=3, N=300, Q=90, Nc=0, rK=128, rV=128, G=32, C=10)
+    _run(sc, dev, _payload(sc, (0, 2), 64), np.arange(200, 300))
+
+
+def test_fast_identity_readers_equal_full_attention(dev):
+    # identity readers: the hybrid result is full attention (CN/core.py:258-262)
+    sc = Scenario(H=2, N=512, Q=130, Nc=50, rK=256, rV=256, G=32, C=16)
+    key, value = sc.codecs(dev)
+    q, kc, vc = sc.q.to(dev), sc.k_cur.to(dev), sc.v_cur.to(dev)
+    reader = codec_native.ReaderLayer(_payload(sc, (0, 1), 128), dev)
+    pr = torch.arange(300, 512, dtype=torch.int32, device=dev)
+    lr = torch.arange(0, 300, dtype=torch.int32, device=dev)
+    of, lf = ops.fast_attend(q, kc, vc, key, value, pr, lr, [g.tensors() for g in reader.groups])
+    oa, la = ops.attend(q, kc, vc, key, value)
+    diff, cos = max_abs_cos(of.float().cpu().numpy(), oa.float().cpu().numpy())
+    assert diff < 1.5e-2 and cos > 0.9999, (diff, cos)
+    assert torch.allclose(lf, la, atol=2e-4)
+
+
+def test_fast_history_attention_api(dev, monkeypatch):
+    # the reference-shaped entry: payload caches, a frame protection mask and a ReaderLayer
+    from nanokv_amd import nanokv_codec as nc
+    monkeypatch.setenv("NANOKV_SCALE_GROUP", "32")
+    monkeypatch.setenv("NANOKV_SCALE_DTYPE", "fp16")
+    monkeypatch.setenv("NANOKV_QUANT_MODE", "fp32")
+    H, D, layer = 2, 128, 7
+    sh = synth.Shape("api", H=H, D=D, N=0, Q=0, Nc=0, rK=128, rV=128, G=32, C=8)
+    lay = synth.make_layer(sh, seed=layer)
+    nc.register_operator("k", layer, encoder=lay.w_enc_k.to(dev), decoder=lay.w_dec_k.to(dev))
+    nc.register_operator("v", layer, encoder=lay.w_enc_v.to(dev), decoder=lay.w_dec_v.to(dev))
+    nc.register_centers("k", layer, lay.centers_k.to(dev))
+    nc.register_centers("v", layer, lay.centers_v.to(dev))
+    cache_k = cache_v = None
+    for c in range(4):  # four frames of 50 tokens
+        k = synth.history_rows(sh, lay.centers_k, 50, seed=30 + c).to(dev)[None].to(torch.bfloat16)
+        v = synth.history_rows(sh, lay.centers_v, 50, seed=40 + c).to(dev)[None].to(torch.bfloat16)
+        cache_k = nc.concat_values(cache_k, nc.encode_tensor("k", layer, k))
+        cache_v = nc.concat_values(cache_v, nc.encode_tensor("v", layer, v))
+    frames = torch.arange(200, device=dev) // 50
+    protect = codec_native.protected_tokens(frames, recent=1, stride=2)
+    # frame 3 (recent) plus frames 2 and 0 (every 2nd run back from the newest old one)
+    assert protect.view(4, 50).all(1).tolist() == [True, False, True, True]
+    payload = synth.make_readers(sh, lay, full_heads=(1,), d=32)
+    reader = codec_native.ReaderLayer(payload, dev)
+    g = torch.Generator().manual_seed(11)
+    q = (torch.randn(1, H, 40, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev)
+    kc = torch.randn(1, H, 20, D, generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn(1, H, 20, D, generator=g).to(torch.bfloat16).to(dev)
+    out, lse = codec_native.fast_history_attention(q, cache_k, cache_v, kc, vc, reader, protect,
+                                                   return_lse=True)
+    assert out.shape == (1, H, 40, D) and lse.shape == (1, H, 40)
+    # oracle over the same payload bits
+    key, value = nc.history_codecs(cache_k, cache_v, dev)
+
+    def od(cd):
+        return {"packed": cd.packed[0].cpu().numpy(), "scales": u16(cd.scales[0]),
+                "w_dec_bf16": u16(cd.w_dec), "group": cd.group, "scale_dtype": "fp16",
+                "ids": cd.ids[0].cpu().numpy().astype(np.int64),
+                "centers_bf16": u16(cd.centers[0])}
+    prot = torch.nonzero(protect).flatten().cpu().numpy()
+    low = torch.nonzero(~protect).flatten().cpu().numpy()
+    ref, ref_lse = orc.fast_attend(u16(q[0].permute(1, 0, 2)), u16(kc[0].permute(1, 0, 2)),
+                                   u16(vc[0].permute(1, 0, 2)), od(key), od(value), prot, low,
+                                   oracle_groups(payload), D ** -0.5, D=D)
+    diff, cos = max_abs_cos(out[0].permute(1, 0, 2).float().cpu().numpy(), ref)
+    assert diff <= MAX_ABS and cos >= MIN_COS, (diff, cos)
+
+
+def test_fast_cfg3_shape_subset_heads(dev):
+    """Config-3 call (H=24, D=128, N=12480, Q=Nc=1560, 6 identity heads, 18
+    heads at d=32, last 2 frames protected), encoded on the GPU; the oracle
+    checks one identity head and two reader heads."""
+    sh = synth.CONFIGS[3]
+    layer = synth.make_layer(sh, seed=0, device=dev)
+    codecs = []
+    for kind, cent, enc, dec in (("k", layer.centers_k, layer.w_enc_k, layer.w_dec_k),
+                                 ("v", layer.centers_v, layer.w_enc_v, layer.w_dec_v)):
+        rows = synth.history_rows(sh, cent, sh.N, seed=1 + (kind == "v"), device=dev)
+        e = ops.encode(rows, enc, centers=cent, group=sh.G, scale_dtype=sh.scale_dtype)
+        codecs.append(ops.Codec(packed=e["packed"][None], scales=e["scales"][None], w_dec=dec,
+                                group=sh.G, ids=e["ids"][None], centers=cent[None]))
+    q = synth.queries(sh, seed=3, device=dev)
+    kc = synth.history_rows(sh, layer.centers_k, sh.Nc, seed=4, device=dev)
+    vc = synth.history_rows(sh, layer.centers_v, sh.Nc, seed=5, device=dev)
+    kc = kc.reshape(1, sh.Nc, sh.H, sh.D).to(torch.bfloat16)
+    vc = vc.reshape(1, sh.Nc, sh.H, sh.D).to(torch.bfloat16)
+    payload = synth.make_readers(sh, layer)
+    reader = codec_native.ReaderLayer(payload, dev)
+    protect = synth.fast_protect_mask(sh, device=dev)
+    pr = torch.nonzero(protect).flatten().to(torch.int32)
+    lr = torch.nonzero(~protect).flatten().to(torch.int32)
+    out, lse = ops.fast_attend(q, kc, vc, codecs[0], codecs[1], pr, lr,
+                               [g.tensors() for g in reader.groups])
+    heads = [0, 5, 23]
+    key = {"packed": codecs[0].packed[0].cpu().numpy(), "scales": u16(codecs[0].scales[0]),
+           "w_dec_bf16": u16(layer.w_dec_k), "group": sh.G, "scale_dtype": "fp16",
+           "ids": codecs[0].ids[0].cpu().numpy().astype(np.int64),
+           "centers_bf16": u16(layer.centers_k)}
+    val = {"packed": codecs[1].packed[0].cpu().numpy(), "scales": u16(codecs[1].scales[0]),
+           "w_dec_bf16": u16(layer.w_dec_v), "group": sh.G, "scale_dtype": "fp16",
+           "ids": codecs[1].ids[0].cpu().numpy().astype(np.int64),
+           "centers_bf16": u16(layer.centers_v)}
+    ref, ref_lse = orc.fast_attend(u16(q[0]), u16(kc[0]), u16(vc[0]), key, val,
+                                   pr.cpu().numpy(), lr.cpu().numpy(), oracle_groups(payload),
+                                   sh.D ** -0.5, heads=heads, D=sh.D)
+    diff, cos = max_abs_cos(out[0][:, heads].float().cpu().numpy(), ref)
+    assert diff <= MAX_ABS and cos >= MIN_COS, (diff, cos)
+    assert np.abs(lse[0][heads].cpu().numpy() - ref_lse).max() < 2e-3
