@@ -38,6 +38,8 @@
 #include "nkv_common.h"
 #include "nkv_internal.h"
 
+#include <type_traits>
+
 namespace nkv {
 
 #ifdef NKV_PLAIN_STORES
@@ -102,71 +104,90 @@ __device__ __forceinline__ int64_t history_row(const ChunkParams& p, int64_t key
 
 // ------------------------------------------------------------------ decode
 // This wave's 64 keys (64*wave + [0, 64) of the chunk) of codec CODEC.
-// Decoder-slice staging: the block copies W[h*128 + d][64*kq, +64) (16 KB)
-// into LDS with coalesced 16-byte loads (8 threads per 128-byte row), double
-// buffered, so each decoder element is fetched from L2 once per block and
-// every wave reads its MFMA fragments from LDS.  Rows are padded to 72 bf16
-// (36 dwords): the b128 fragment reads of 8 consecutive rows hit distinct
-// banks.
-constexpr int WS_ROW = 72;
-constexpr int WS_BUF = CK_D * WS_ROW;  // bf16 elements per buffer
-static_assert(2 * WS_BUF <= CK_D * CK_VROW && 2 * WS_BUF <= CK_T * CK_KROW,
+//
+// Decoder slices W[row d of the launch head][64*s, +64) (WIDTH rows of 128
+// bytes) stream into a ring of DS_NBUF LDS buffers by direct-to-LDS loads
+// (global_load_lds_dwordx4: no register staging), DS_AHEAD slices ahead of
+// the MFMAs.  The block's four waves each copy WIDTH/32 KB of a slice, so
+// every decoder element is fetched from L2 once per block.  Rows are stored
+// unpadded with their 16-byte chunks XOR-swizzled by (row & 7): chunk c of
+// row r sits at chunk c ^ (r & 7), so the MFMA operand reads of eight
+// consecutive rows hit eight distinct chunks (conflict-free), while every
+// load instruction still fills one contiguous 1 KB of LDS.
+//
+// A stage (slice s) = its decoder rows plus this wave's codes and scales of
+// slice s, which go to a register ring of DS_AHEAD entries.  Loads complete
+// in issue order, so waiting for stage s is one vmcnt bound: the stages
+// issued after it may stay in flight.
+constexpr int DS_NBUF = 4;
+constexpr int DS_AHEAD = 3;
+// The rings fit in the regions that hold no live data while they are used:
+// V's decode stages in the V^T region, K's in the K region.
+static_assert(DS_NBUF * CK_D * 64 <= CK_D * CK_VROW && DS_NBUF * CK_D * 64 <= CK_T * CK_KROW,
               "decoder staging must fit in the V^T and K regions");
+static_assert(CK_T * CK_D <= CK_T * CK_KROW, "V centers are staged in the K region");
 
-// The 128 center values of launch head h for the wave's 64 keys (V),
-// with coalesced 16-byte loads (one 256-byte row per 16 lanes) ...
-__device__ __forceinline__ void load_center_rows(u32x4 (&v)[16], const ChunkSmem& sm,
-                                                 const ChunkCodec& c, int codec, int b, int h,
-                                                 int wave, int lane) {
-    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs;
+#define NKV_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits [3:0] and [15:14]; the
+// other counters at their maxima, i.e. not waited on)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// The 128 center values of launch head h for the wave's 64 keys (V), copied
+// into LDS rows [key][128] (unpadded, key 64*wave + ... of the chunk) by
+// 16 direct-to-LDS loads, each filling 4 rows (1 KB).
+__device__ __forceinline__ void dma_v_centers(uint16_t* vcen, const ChunkSmem& sm,
+                                              const ChunkCodec& c, int b, int h, int wave,
+                                              int lane) {
+    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs + 8 * (lane & 15);
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         const int t = 64 * wave + 4 * e + (lane >> 4);
-        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[codec][t] * c.c_rs +
-                                               8 * (lane & 15));
+        __builtin_amdgcn_global_load_lds(cent + (int64_t)sm.ids[1][t] * c.c_rs,
+                                         NKV_LDS(vcen + (64 * wave + 4 * e) * CK_D), 16, 0, 0);
     }
 }
 
-// ... stored into the wave's own K rows of LDS (other waves' rows are not
-// touched).
-__device__ __forceinline__ void store_center_rows(const u32x4 (&v)[16], ChunkSmem& sm, int wave,
-                                                  int lane) {
+// The DK center values of launch head h for the wave's 64 keys (K), as
+// coalesced 16-byte row pieces: entry e of lane L is piece q = 64*e + L of
+// the wave's rows, i.e. key 64*wave + q / (DK/8) of the chunk, columns
+// 8 * (q % (DK/8)).
+template <int DK>
+__device__ __forceinline__ void load_k_center_rows(u32x4 (&v)[DK / 8], const ChunkSmem& sm,
+                                                   const ChunkCodec& c, int b, int h, int wave,
+                                                   int lane) {
+    constexpr int PR = DK / 8;  // 16-byte pieces per row
+    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs;
 #pragma unroll
-    for (int e = 0; e < 16; ++e)
-        *reinterpret_cast<u32x4*>(&sm.k[64 * wave + 4 * e + (lane >> 4)][8 * (lane & 15)]) = v[e];
-}
-
-// K center values in the K^T accumulator layout: key 64*wave + 32*tt + l32,
-// d = 32*dt + 8*g + 4*hf + [0, 4), dt < NDT.
-template <int NDT>
-__device__ __forceinline__ void load_k_centers(u32x2 (&cen)[2][NDT][4], const ChunkSmem& sm,
-                                               const ChunkCodec& c, int b, int h, int wave,
-                                               int lane) {
-    const int hf = lane >> 5, l32 = lane & 31;
-    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs + 4 * hf;
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const uint16_t* crow = cent + (int64_t)sm.ids[0][64 * wave + 32 * tt + l32] * c.c_rs;
-#pragma unroll
-        for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-            for (int g = 0; g < 4; ++g)
-                cen[tt][dt][g] = *reinterpret_cast<const u32x2*>(crow + 32 * dt + 8 * g);
+    for (int e = 0; e < DK / 8; ++e) {
+        const int q = 64 * e + lane;  // piece index within the wave's 64 rows
+        const int t = 64 * wave + q / PR;
+        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[0][t] * c.c_rs +
+                                               8 * (q % PR));
     }
 }
 
-// Decode this wave's 64 keys of codec CODEC to WIDTH columns (V: 128; K:
-// the launch's DK, written to the K tile with row pitch KROW).  wst: 2 *
-// WS_BUF bf16 of LDS that no other data uses during the call.  HAS_C: the
-// codec has centers (a template argument so that the epilogue is
-// straight-line code); V's are staged in the wave's K-region rows, K's are
-// loaded during the last slice.  Ends with a block barrier after the last
-// read of wst.
-template <int CODEC, bool HAS_C, int WIDTH, int KROW>
+// Decode this wave's 64 keys of codec CODEC to WIDTH columns (V: 128, into
+// V^T; K: the launch's DK, into the K tile with row pitch KROW).  wst: the
+// LDS ring (DS_NBUF * WIDTH * 64 bf16) that holds no live data during the
+// call.  HAS_C: the codec has centers (a template argument so that the
+// epilogue is straight-line code); V's are copied into the K region
+// (unpadded rows) after `pre`, K's are loaded into registers before the
+// slices.  pre() runs once the first stages are in flight (V: it publishes
+// the chunk's ids and biases, ending with a block barrier).  Ends with a
+// block barrier.
+template <int CODEC, bool HAS_C, int WIDTH, int KROW, typename Pre>
 __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const ChunkCodec& c,
                                              const ChunkParams& p, int b, int h, int64_t tok0,
-                                             int valid, int wave, int lane) {
+                                             int valid, int wave, int lane, Pre&& pre) {
     constexpr int NDT = WIDTH / 32;
+    constexpr int LPW = WIDTH / 32;           // 1 KB slice loads per wave
+    constexpr int STAGE = LPW + 4;            // vm instructions per stage
+    constexpr int SLICE = WIDTH * 64;         // bf16 per ring buffer
     const int hf = lane >> 5, l32 = lane & 31;
     const int R = c.r, KQ = R >> 6, G = c.group, NG = R / G;
     const bool f16 = c.scale_dtype == NKV_DTYPE_FP16;
@@ -181,26 +202,27 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
         prow[tt] = c.packed + tok * (R / 2) + 16 * hf;
         srow[tt] = c.scales + tok * NG;
     }
-    const int t = 64 * wave + lane;
-    const uint16_t* wsrc = c.w + (int64_t)h * c.w_hs + (int64_t)(t >> 3) * R + 8 * (t & 7);
-    uint16_t* wdst = wst + (t >> 3) * WS_ROW + 8 * (t & 7);
-    auto wload = [&](int kq, u32x4 (&r)[NDT]) {
+    // slice loads: this wave fills 1 KB pieces 4*wave*.. of each slice; lane
+    // L brings logical chunk (L%8) ^ (L/8) of row 8*piece + L/8
+    const int piece_row = lane >> 3, piece_chunk = (lane & 7) ^ (lane >> 3);
+    const uint16_t* wsrc = c.w + (int64_t)h * c.w_hs + (int64_t)piece_row * R + 8 * piece_chunk;
+    auto issue_slice = [&](int s) {
+        uint16_t* dst = wst + (s % DS_NBUF) * SLICE;
 #pragma unroll
-        for (int e = 0; e < NDT; ++e)
-            r[e] = *reinterpret_cast<const u32x4*>(wsrc + (int64_t)32 * e * R + 64 * kq);
+        for (int e = 0; e < LPW; ++e) {
+            const int piece = LPW * wave + e;  // rows 8*piece .. +8
+            __builtin_amdgcn_global_load_lds(wsrc + (int64_t)8 * piece * R + 64 * s,
+                                             NKV_LDS(dst + piece * 512), 16, 0, 0);
+        }
     };
-    auto wstore = [&](int buf, const u32x4 (&r)[NDT]) {
-#pragma unroll
-        for (int e = 0; e < NDT; ++e)
-            *reinterpret_cast<u32x4*>(wdst + buf * WS_BUF + 32 * e * WS_ROW) = r[e];
-    };
-    auto cload = [&](int kq, u32x4 (&pk)[2], float (&sc)[2]) {
-        const int gi = (64 * kq + 32 * hf) / G;
+    // codes and raw scale bits (converted at use: converting here would make
+    // the issue wait for the load)
+    auto issue_codes = [&](int s, u32x4 (&pk)[2], uint16_t (&sb)[2]) {
+        const int gi = (64 * s + 32 * hf) / G;
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
-            pk[tt] = *reinterpret_cast<const u32x4*>(prow[tt] + 32 * kq);
-            const uint16_t sb = srow[tt][gi];
-            sc[tt] = f16 ? f16_bits_to_f32(sb) : bf16_bits_to_f32(sb);
+            pk[tt] = *reinterpret_cast<const u32x4*>(prow[tt] + 32 * s);
+            sb[tt] = srow[tt][gi];
         }
     };
 
@@ -210,66 +232,147 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) acc[dt][tt] = f32x16{};
 
-    // V: this wave's center rows go to its own K rows (store_center_rows);
-    // their loads are issued first so that they overlap the prologue.
-    u32x4 cst[16];
-    if (CODEC == 1 && HAS_C) load_center_rows(cst, sm, c, 1, b, h, wave, lane);
+    // K: center rows, issued before stage 0 (so complete before it)
+    uint16_t* vcen = &sm.k[0][0];
+    u32x4 kcen[WIDTH / 8];
+    if (CODEC == 0 && HAS_C) load_k_center_rows<WIDTH>(kcen, sm, c, b, h, wave, lane);
 
-    // One slice ahead: codes (HBM) and decoder rows for slice kq+1 are
-    // requested while slice kq is multiplied; the rows go to the other LDS
-    // buffer at the end of the iteration.
-    u32x4 wr[NDT], pk[2];
-    float sc[2];
-    wload(0, wr);
-    cload(0, pk, sc);
-    if (CODEC == 1 && HAS_C) store_center_rows(cst, sm, wave, lane);
-    wstore(0, wr);
-    __syncthreads();
-    // fragment rows 32*dt + l32, k = 32*hf + 8*j within the slice
-    const uint16_t* wfrag = wst + l32 * WS_ROW + 32 * hf;
-    u32x2 cen[2][NDT][4];  // K epilogue center values, requested during the last slice
-    for (int kq = 0; kq < KQ; ++kq) {
-        u32x4 pkn[2];
-        float scn[2];
-        const bool more = kq + 1 < KQ;
-        if (more) {
-            wload(kq + 1, wr);
-            cload(kq + 1, pkn, scn);
+    u32x4 pk[DS_AHEAD][2];
+    uint16_t sc[DS_AHEAD][2];
+    // (sched_barrier: the stages must leave in this order, since the vmcnt
+    // bounds below count whole stages)
+#pragma unroll
+    for (int i = 0; i < DS_AHEAD; ++i)
+        if (i < KQ) {
+            issue_slice(i);
+            issue_codes(i, pk[i], sc[i]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        if (CODEC == 0 && HAS_C && !more) load_k_centers<NDT>(cen, sm, c, b, h, wave, lane);
-        const uint16_t* wb = wfrag + (kq & 1) * WS_BUF;
+    pre();
+    // V: center rows into the K region, issued after stages 0 .. DS_AHEAD-1
+    // and before stage DS_AHEAD: NVC more instructions may be in flight while
+    // waiting for the first DS_AHEAD stages
+    constexpr int NVC = CODEC == 1 && HAS_C ? 16 : 0;
+    if (CODEC == 1 && HAS_C) dma_v_centers(vcen, sm, c, b, h, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);
+
+    // per-lane swizzled chunk offsets of the operand reads: row 32*dt + l32,
+    // logical chunk 4*hf + j
+    int wofs[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-            bf16x8 z[2];
+    for (int j = 0; j < 4; ++j) wofs[j] = l32 * 64 + 8 * ((4 * hf + j) ^ (l32 & 7));
+
+    // operand of the current sub-step (carried across slices), and its scales
+    u32x4 zc[2];
+    float scl[2], ns7[2];
+    if (KQ > 0) {
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) z[tt] = unpack8(pk[tt][j], sc[tt], -7.0f * sc[tt]);
+        for (int tt = 0; tt < 2; ++tt) {
+            scl[tt] = f16 ? f16_bits_to_f32(sc[0][tt]) : bf16_bits_to_f32(sc[0][tt]);
+            ns7[tt] = -7.0f * scl[tt];
+            Unpack8 u;
+            u.split(pk[0][tt][0]);
 #pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) {
-                const bf16x8 w = lds_b128(wb + 32 * dt * WS_ROW + 8 * j);
+            for (int e = 0; e < 4; ++e) zc[tt][e] = u.pair(e, scl[tt], ns7[tt]);
+        }
+    }
+    for (int s0 = 0; s0 < KQ; s0 += DS_AHEAD) {
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt)
-                    acc[dt][tt] = CODEC == 0 ? mfma32(w, z[tt], acc[dt][tt])
-                                             : mfma32(z[tt], w, acc[dt][tt]);
+        for (int i = 0; i < DS_AHEAD; ++i) {
+            const int s = s0 + i;
+            if (s >= KQ) break;
+            // stage s landed (for this wave) once at most the later issued
+            // stages are in flight; the barrier makes every wave's part visible
+            // and retires the reads of the buffer the next slice goes to
+            static_assert(DS_AHEAD == 3, "the wait bounds below assume three stages ahead");
+            const int later = min(KQ - 1 - s, DS_AHEAD - 1);
+            if (s < DS_AHEAD) {
+                if (later >= 2) wait_vmcnt<2 * STAGE + NVC>();
+                else if (later == 1) wait_vmcnt<STAGE + NVC>();
+                else wait_vmcnt<NVC>();
+            } else {
+                if (later >= 2) wait_vmcnt<2 * STAGE>();
+                else if (later == 1) wait_vmcnt<STAGE>();
+                else wait_vmcnt<0>();
             }
-        }
-        if (more) {
-            // the other buffer was last read before the previous barrier
-            wstore((kq + 1) & 1, wr);
+            __builtin_amdgcn_s_barrier();
+            if (s + DS_AHEAD < KQ) issue_slice(s + DS_AHEAD);
+            __builtin_amdgcn_sched_barrier(0);
+            const uint16_t* wb = wst + (s % DS_NBUF) * SLICE;
+            // Software pipeline in explicit slots: each MFMA of sub-step j is
+            // followed by one eighth of the next sub-step's unpack (for the
+            // last sub-step: the next slice's first, whose codes are already
+            // in the ring) and, every other slot, one of the next sub-step's
+            // decoder-operand reads (not across slices: those need the
+            // barrier); sched_barrier keeps the slots in order so that the
+            // unpack runs under the MFMAs.
+            // (after the last slice the ring entry holds stale codes: the
+            // unpack is then wasted work, kept branch-free)
+            const int inx = (i + 1) % DS_AHEAD;
+            float scn[2], nsn[2];
 #pragma unroll
             for (int tt = 0; tt < 2; ++tt) {
-                pk[tt] = pkn[tt];
-                sc[tt] = scn[tt];
+                scn[tt] = f16 ? f16_bits_to_f32(sc[inx][tt]) : bf16_bits_to_f32(sc[inx][tt]);
+                nsn[tt] = -7.0f * scn[tt];
             }
+            u32x4 zn[2];
+            bf16x8 wc[NDT], wn[NDT];
+#pragma unroll
+            for (int dt = 0; dt < NDT; ++dt) wc[dt] = lds_b128(wb + 32 * dt * 64 + wofs[0]);
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                Unpack8 u[2];
+                constexpr int SLOTS = 2 * NDT;  // MFMAs per sub-step
+#pragma unroll
+                for (int m = 0; m < SLOTS; ++m) {
+                    const int dt = m >> 1, tt = m & 1;
+                    acc[dt][tt] = CODEC == 0 ? mfma32(wc[dt], as_bf16x8(zc[tt]), acc[dt][tt])
+                                             : mfma32(as_bf16x8(zc[tt]), wc[dt], acc[dt][tt]);
+                    // unpack pieces: 8 dwords (2 tt x 4) over the SLOTS slots
+#pragma unroll
+                    for (int q = (8 * m) / SLOTS; q < (8 * (m + 1)) / SLOTS; ++q) {
+                        const int qt = q >> 2, qe = q & 3;
+                        if (j + 1 < 4) {
+                            if (qe == 0) u[qt].split(pk[i][qt][j + 1]);
+                            zn[qt][qe] = u[qt].pair(qe, scl[qt], ns7[qt]);
+                        } else {
+                            if (qe == 0) u[qt].split(pk[inx][qt][0]);
+                            zn[qt][qe] = u[qt].pair(qe, scn[qt], nsn[qt]);
+                            // computed here, under this slice's MFMAs (the
+                            // compiler would otherwise sink it past the barrier)
+                            asm volatile("" : "+v"(zn[qt][qe]));
+                        }
+                    }
+                    if (j + 1 < 4 && (m & 1) == 0)
+                        wn[dt] = lds_b128(wb + 32 * dt * 64 + wofs[j + 1]);
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) zc[tt] = zn[tt];
+                if (j + 1 < 4) {
+#pragma unroll
+                    for (int dt = 0; dt < NDT; ++dt) wc[dt] = wn[dt];
+                }
+            }
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                scl[tt] = scn[tt];
+                ns7[tt] = nsn[tt];
+            }
+            // this ring entry is consumed: refill it with stage s + DS_AHEAD
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + DS_AHEAD < KQ) issue_codes(s + DS_AHEAD, pk[i], sc[i]);
+            __builtin_amdgcn_sched_barrier(0);
         }
-        __syncthreads();
     }
+    // every wave's slice reads are done before the epilogue writes over the ring
+    __syncthreads();
 
     // Epilogue.  sm.bias holds bf16(mean) or zeros, so the bias add is
     // unconditional.
     if (CODEC == 0) {
         // acc[dt][tt] element i: d = 32*dt + 8*(i/4) + 4*hf + i%4, key
-        // 64*wave + 32*tt + l32; cen holds the center values (4 consecutive d
-        // per group).
+        // 64*wave + 32*tt + l32.  Pass 1 stores bf16(acc + bias) ...
         uint16_t* ktile = &sm.k[0][0];
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt) {
@@ -279,26 +382,36 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const int d = 32 * dt + 8 * g + 4 * hf;
-                    u32x2* slot = reinterpret_cast<u32x2*>(ktile + t * KROW + d);
                     float a[4];
 #pragma unroll
                     for (int e = 0; e < 4; ++e) a[e] = acc[dt][tt][4 * g + e] + sm.bias[0][d + e];
-                    const u32x2 cw = HAS_C ? cen[tt][dt][g] : u32x2{0, 0};
-                    u32x2 r;
-#pragma unroll
-                    for (int h2 = 0; h2 < 2; ++h2) {
-                        const uint32_t pr = pack_bf16x2(a[2 * h2], a[2 * h2 + 1]);
-                        r[h2] = pack_bf16x2(
-                            __uint_as_float(pr << 16) + __uint_as_float(cw[h2] << 16),
-                            __uint_as_float(pr & 0xffff0000u) +
-                                __uint_as_float(cw[h2] & 0xffff0000u));
-                    }
-                    *slot = r;
+                    const u32x2 r = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+                    *reinterpret_cast<u32x2*>(ktile + t * KROW + d) = r;
                 }
+        }
+        if (HAS_C) {
+            // ... pass 2 adds the center rows piece by piece (the wave's own
+            // rows: its LDS operations stay in order, no barrier needed)
+            constexpr int PR = WIDTH / 8;
+#pragma unroll
+            for (int e = 0; e < WIDTH / 8; ++e) {
+                const int q = 64 * e + lane;
+                u32x4* slot = reinterpret_cast<u32x4*>(ktile + (64 * wave + q / PR) * KROW +
+                                                       8 * (q % PR));
+                const u32x4 kv = *slot;
+                u32x4 r;
+#pragma unroll
+                for (int h2 = 0; h2 < 4; ++h2)
+                    r[h2] = pack_bf16x2(
+                        __uint_as_float(kv[h2] << 16) + __uint_as_float(kcen[e][h2] << 16),
+                        __uint_as_float(kv[h2] & 0xffff0000u) +
+                            __uint_as_float(kcen[e][h2] & 0xffff0000u));
+                *slot = r;
+            }
         }
     } else {
         // acc[dt][tt] element i: key 64*wave + 32*tt + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32;
-        // the center rows of the wave's keys were staged into its K rows
+        // the center rows of the wave's keys are in vcen
 #pragma unroll
         for (int tt = 0; tt < 2; ++tt)
 #pragma unroll
@@ -312,7 +425,7 @@ __device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const
 #pragma unroll
                     for (int e = 0; e < 4; ++e) {
                         const float a = bf16_round(acc[dt][tt][4 * g + e] + bias);
-                        v[e] = HAS_C ? a + bf16_bits_to_f32(sm.k[t0 + e][d]) : a;
+                        v[e] = HAS_C ? a + bf16_bits_to_f32(vcen[(t0 + e) * CK_D + d]) : a;
                     }
                     const u32x2 r = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                     *reinterpret_cast<u32x2*>(&sm.vt[d][t0]) = r;
@@ -486,39 +599,117 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
 
     constexpr int NSTEP = CK_T / 32;
     if (FULL && NQB == 2) {
-        // Two query blocks staggered by half a step: block 0's softmax runs
-        // under block 1's MFMAs and vice versa.  Per step j:
-        //   X: S1 = QK(j), O1 += PV(j-1)      | softmax(S0 of step j)
-        //   Y: S0 = QK(j+1), O0 += PV(j)      | softmax(S1 of step j)
+        // Two query blocks staggered by half a step.  Every phase issues up
+        // to 16 MFMAs that do not depend on its softmax (one block's scores
+        // of the next step, the other block's PV) and spreads that softmax
+        // between them, one slice per MFMA, with the next operands' LDS
+        // loads riding along; sched_barrier fences keep this order, so one
+        // wave keeps the matrix core busy while it runs the softmax.
+        //   X(j): S1 = QK(K_j), O1 += PV(V_{j-1}, P1) | softmax(S0) | load K_{j+1}
+        //   Y(j): S0 = QK(K_{j+1}), O0 += PV(V_j, P0) | softmax(S1) | load V_{j+1}
         f32x16 s0, s1;
         bf16x8 p0[2], p1[2];
-        bf16x8 kf[KS], vprev[2][4];
-        float a0, a1;
-        load_k(0, kf);
-        qk(0, kf, s0);
+        bf16x8 kb[2][KS], vb[2][2][4];
+        float a0 = 1.0f, a1 = 1.0f;
+        load_k(0, kb[0]);
+        load_v(0, vb[0]);
+        qk(0, kb[0], s0);
+        // one phase; NQK / NPV = MFMAs of the score / PV product (0 = none)
+        auto phase = [&](auto nqk_c, auto npv_c, const bf16x8 (&kq)[KS], int qa, f32x16& s_out,
+                         const bf16x8 (&vv)[2][4], int qv, const bf16x8 (&pin)[2], int qs,
+                         f32x16& s_in, bf16x8 (&pout)[2], float& alpha, auto&& ld) -> bool {
+            constexpr int NQK = decltype(nqk_c)::value, NPV = decltype(npv_c)::value;
+            constexpr int BOTH = NQK < NPV ? NQK : NPV;
+            const float mq = m[qs];
+            float tm = 0.0f, mn = 0.0f, lsum = 0.0f;
+            bool up = false;
+            uint32_t pw[8];
+#pragma unroll
+            for (int t = 0; t < 16; ++t) {
+                // MFMA t: score and PV products alternate, then the longer one's tail
+                int kind = -1, idx = 0;  // 0: score step idx, 1: PV step idx
+                if (t < 2 * BOTH) {
+                    kind = t & 1;
+                    idx = t >> 1;
+                } else if (t - BOTH < NQK && NQK > BOTH) {
+                    kind = 0;
+                    idx = t - BOTH;
+                } else if (t - BOTH < NPV && NPV > BOTH) {
+                    kind = 1;
+                    idx = t - BOTH;
+                }
+                if (kind == 0) {
+                    s_out = mfma32(kq[idx], qf[qa][idx], idx == 0 ? f32x16{} : s_out);
+                } else if (kind == 1) {
+                    const int ts = idx >> 2, db = idx & 3;
+                    o[qv][db] = mfma32(vv[ts][db], pin[ts], o[qv][db]);
+                }
+                // softmax slice t (the max is taken on raw scores: c > 0 preserves order)
+                if (t < 4) {
+                    const float a = fmaxf(s_in[4 * t], s_in[4 * t + 1]);
+                    const float b2 = fmaxf(s_in[4 * t + 2], s_in[4 * t + 3]);
+                    tm = t == 0 ? fmaxf(a, b2) : fmaxf(tm, fmaxf(a, b2));
+                } else if (t == 4) {
+                    tm = halfwave_max(tm) * c;
+                    up = tm > mq + CK_TAU;
+                    mn = up ? tm : mq;
+                    alpha = up ? __builtin_amdgcn_exp2f(mq - mn) : 1.0f;
+                    m[qs] = mn;
+                } else if (t < 13) {
+                    // v_exp_f32 of arguments <= 8; results below 2^-126 flush to 0
+                    const int k = t - 5;
+                    const float e0 = __builtin_amdgcn_exp2f(fmaf(s_in[2 * k], c, -mn));
+                    const float e1 = __builtin_amdgcn_exp2f(fmaf(s_in[2 * k + 1], c, -mn));
+                    pw[k] = pack_bf16x2(e0, e1);
+                } else if (t < 15) {
+                    // row sum of the bf16 weights the PV product uses
+#pragma unroll
+                    for (int k = 4 * (t - 13); k < 4 * (t - 13) + 4; ++k)
+                        lsum = __builtin_amdgcn_fdot2_f32_bf16(
+                            __builtin_bit_cast(bf16x2, pw[k]),
+                            __builtin_bit_cast(bf16x2, 0x3F803F80u), lsum, false);
+                } else {
+                    l[qs] = l[qs] * alpha + lsum;
+                    asm volatile("" : "+v"(l[qs]));
+                    pout[0] = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
+                    pout[1] = as_bf16x8(u32x4{pw[4], pw[5], pw[6], pw[7]});
+                }
+                ld(t);
+                __builtin_amdgcn_sched_barrier(0);
+            }
+            return up;
+        };
+        using I0 = std::integral_constant<int, 0>;
+        using IK = std::integral_constant<int, KS>;
+        using I8 = std::integral_constant<int, 8>;
+        auto no_load = [](int) {};
 #pragma unroll
         for (int j = 0; j < NSTEP; ++j) {
-            bf16x8 vf[2][4], kn[KS];
-            qk(NQB - 1, kf, s1);
+            const int cj = j & 1, nj = cj ^ 1;
+            auto ld_k = [&](int t) {
+                if (j + 1 < NSTEP && t < KS) kb[nj][t] = lds_b128(kbase + 32 * (j + 1) * KROW + W::block(t));
+            };
+            auto ld_v = [&](int t) {
+                if (j + 1 < NSTEP && t < 8)
+                    vb[nj][t >> 2][t & 3] =
+                        lds_2x64(vbase + 32 * (t & 3) * CK_VROW + 32 * (j + 1) + 16 * (t >> 2));
+            };
+            bool up0;
+            if (j == 0)
+                up0 = phase(IK{}, I0{}, kb[cj], 1, s1, vb[nj], 1, p1, 0, s0, p0, a0, ld_k);
+            else
+                up0 = phase(IK{}, I8{}, kb[cj], 1, s1, vb[nj], 1, p1, 0, s0, p0, a0, ld_k);
             if (j == NSTEP - 1) load_q_block<DK>(qf[1], p, b, h, q_next + 32, q_next, lane);
-            if (j > 0) pv(NQB - 1, vprev, p1);
-            load_v(j, vf);
-            if (j + 1 < NSTEP) load_k(j + 1, kn);
-            const bool up0 = softmax(0, s0, p0, a0);
             if (j > 0 && __any(up0)) rescale(0, a0);
-            if (j + 1 < NSTEP) qk(0, kn, s0);
+            bool up1;
+            if (j + 1 < NSTEP)
+                up1 = phase(IK{}, I8{}, kb[nj], 0, s0, vb[cj], 0, p0, 1, s1, p1, a1, ld_v);
+            else
+                up1 = phase(I0{}, I8{}, kb[nj], 0, s0, vb[cj], 0, p0, 1, s1, p1, a1, no_load);
             if (j == NSTEP - 2) load_q_block<DK>(qf[0], p, b, h, q_next, q_next, lane);
-            pv(0, vf, p0);
-            const bool up1 = softmax(NQB - 1, s1, p1, a1);
-            if (j > 0 && __any(up1)) rescale(NQB - 1, a1);
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk) kf[kk] = kn[kk];
-#pragma unroll
-            for (int ts = 0; ts < 2; ++ts)
-#pragma unroll
-                for (int db = 0; db < 4; ++db) vprev[ts][db] = vf[ts][db];
+            if (j > 0 && __any(up1)) rescale(1, a1);
         }
-        pv(NQB - 1, vprev, p1);
+        pv(1, vb[(NSTEP - 1) & 1], p1);
     } else if (FULL) {
         // one query block: step j+1's scores and step j-1's PV under step j's softmax
         f32x16 s[2];
@@ -625,42 +816,49 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
     const int valid = (int)min((int64_t)CK_T, (hist ? p.n_rows : p.Nc) - tok0);
 
     if (hist) {
+        // The chunk's center ids and this head's biases are loaded and
+        // published to LDS once V's first decode stages are in flight, so
+        // that the latencies of both overlap.
+        auto publish = [&]() {
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc) {
-            const ChunkCodec& cd = p.codec[cc];
-            int id = 0;
-            if (cd.centers && t < valid) {
-                // ids outside the table are clamped so that a corrupt payload
-                // cannot read out of bounds (valid payloads never hold them)
-                const int64_t key = tok0 + t;
-                id = read_id(cd.ids, cd.id_bytes, (int64_t)b * p.N + history_row(p, key));
-                id = min(max(id, 0), cd.num_centers - 1);
+            for (int cc = 0; cc < 2; ++cc) {
+                const ChunkCodec& cd = p.codec[cc];
+                int id = 0;
+                if (cd.centers && t < valid) {
+                    // ids outside the table are clamped so that a corrupt
+                    // payload cannot read out of bounds (valid payloads never
+                    // hold them)
+                    const int64_t key = tok0 + t;
+                    id = read_id(cd.ids, cd.id_bytes, (int64_t)b * p.N + history_row(p, key));
+                    id = min(max(id, 0), cd.num_centers - 1);
+                }
+                sm.ids[cc][t] = id;
+                const int width = cc == 0 ? DK : CK_D;
+                if (t < width)
+                    sm.bias[cc][t] =
+                        cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
             }
-            sm.ids[cc][t] = id;
-            const int width = cc == 0 ? DK : CK_D;
-            if (t < width)
-                sm.bias[cc][t] = cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
-        }
-        __syncthreads();
+            __syncthreads();
+        };
+        auto nothing = []() {};
         // V first: its decoder slices are staged in the (not yet written)
-        // V^T region and its centers in the wave's own K rows; then K, with
-        // its slices staged in the K region once every wave has read its V
-        // centers.
+        // V^T region and its centers in the K region; then K, with its
+        // slices staged in the K region once V's epilogue is done.
         uint16_t* vt_scratch = &sm.vt[0][0];
         uint16_t* k_scratch = &sm.k[0][0];
         if (p.codec[1].centers)
             decode_codec<1, true, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
-                                              wave, lane);
+                                              wave, lane, publish);
         else
             decode_codec<1, false, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
-                                               wave, lane);
+                                               wave, lane, publish);
         __syncthreads();
         if (p.codec[0].centers)
             decode_codec<0, true, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid, wave,
-                                            lane);
+                                            lane, nothing);
         else
             decode_codec<0, false, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
-                                             wave, lane);
+                                             wave, lane, nothing);
     } else if (DK == CK_D) {
         load_current_chunk(sm, p, b, h, tok0, valid, t);
     }

@@ -146,9 +146,31 @@ __device__ __forceinline__ float halfwave_sum(float x) {
 // operand in k order.  (nibble - 7) * s = fma(nibble, s, -7 s): both products
 // are exact in fp32 (<= 15 significant bits), so the fma returns the exact
 // value and the bf16 conversion rounds it once, as the reference does.
+// unpack8 in pieces: split() prepares the two masked words of w (opaque, so
+// that v_cvt_f32_ubyte{0..3} converts each byte in one instruction), and
+// pair(b) is operand dword b (codes 2b and 2b+1).
+struct Unpack8 {
+    uint32_t ev, od;
+    __device__ __forceinline__ void split(uint32_t w) {
+        ev = w & 0x0f0f0f0fu;
+        od = (w >> 4) & 0x0f0f0f0fu;
+        asm("" : "+v"(ev));
+        asm("" : "+v"(od));
+    }
+    __device__ __forceinline__ uint32_t pair(int b, float s, float ns7) const {
+        return pack_bf16x2(fmaf((float)((ev >> (8 * b)) & 0xffu), s, ns7),
+                           fmaf((float)((od >> (8 * b)) & 0xffu), s, ns7));
+    }
+};
+
 __device__ __forceinline__ bf16x8 unpack8(uint32_t w, float s, float ns7) {
-    const uint32_t ev = w & 0x0f0f0f0fu;         // codes 0, 2, 4, 6 (byte lanes)
-    const uint32_t od = (w >> 4) & 0x0f0f0f0fu;  // codes 1, 3, 5, 7
+    uint32_t ev = w & 0x0f0f0f0fu;         // codes 0, 2, 4, 6 (byte lanes)
+    uint32_t od = (w >> 4) & 0x0f0f0f0fu;  // codes 1, 3, 5, 7
+    // opaque: otherwise the known 4-bit range turns each byte conversion
+    // into a bit-field extract plus a conversion, where v_cvt_f32_ubyte{0..3}
+    // converts byte b of the masked word in one instruction
+    asm("" : "+v"(ev));
+    asm("" : "+v"(od));
     u32x4 o;
 #pragma unroll
     for (int b = 0; b < 4; ++b)
