@@ -89,7 +89,7 @@ struct ChunkParams {
     int64_t v_sb, v_st, v_sh;
     ChunkCodec codec[2];
     uint16_t* part_o;   // [B*H, nch_total, qblocks, 8, 64 lanes, 8] bf16 (lane order)
-    float* part_lse;    // [B*H, nch_total, qblocks * 32] log2 domain
+    float* part_ml;     // [B*H, nch_total, qblocks * 32, 2]: running max (log2 units), row sum
     uint16_t* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
@@ -475,10 +475,11 @@ struct DWalk {
 
 // Q^T operand fragments of 32 queries [q_blk, q_blk + 32) (width DK); rows
 // past the last query read row q_safe (finite, never stored).
-template <int DK>
-__device__ __forceinline__ void load_q_block(bf16x8 (&qf)[8], const ChunkParams& p, int b, int h,
+template <int DK, int NF>
+__device__ __forceinline__ void load_q_block(bf16x8 (&qf)[NF], const ChunkParams& p, int b, int h,
                                              int64_t q_blk, int64_t q_safe, int lane) {
     using W = DWalk<DK>;
+    static_assert(NF >= W::KSTEPS, "fragment array too small");
     const int hf = lane >> 5, l32 = lane & 31;
     const int64_t qi = q_blk + l32;
     const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (qi < p.Q ? qi : q_safe) * p.q_st +
@@ -494,6 +495,39 @@ __device__ __forceinline__ void load_q_block(bf16x8 (&qf)[8], const ChunkParams&
 // fragments on entry; as soon as a query block's last score product is
 // issued, its registers are refilled with the wave's next tile (first query
 // q_next), so that tile's loads overlap this tile's remaining work.
+// The partial of one 32-query block for this chunk: its O (unnormalised,
+// bf16) and per query the running max m (log2 units) and row sum l, so that
+// the combine forms sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  Lane
+// dword k of the block holds o[db = k/8][2*(k%8) + {0, 1}] and is stored at
+// 1 KB * (k/4) + 16 B * lane + 4 B * (k%4): every store instruction writes
+// 1 KB contiguous.  Query columns past Q hold finite values that the combine
+// ignores; both half-waves store the same (m, l) of their query.
+__device__ __forceinline__ void store_partial_piece(const ChunkParams& p, int64_t blk,
+                                                    const f32x16 (&o)[4], int st, int lane) {
+    uint16_t* dst = p.part_o + blk * 4096 + lane * 8;
+    const int db = st >> 1, i0 = 8 * (st & 1);
+    u32x4 w;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(o[db][i0 + 2 * e], o[db][i0 + 2 * e + 1]);
+    NT_STORE(w, reinterpret_cast<u32x4*>(dst + 512 * st));
+}
+
+__device__ __forceinline__ void store_partial_ml(const ChunkParams& p, int64_t bh, int chunk,
+                                                 int64_t qcol, float m, float lt) {
+    const int64_t idx = (bh * p.nch_total + chunk) * ((int64_t)p.qblocks * 32) + qcol;
+    NT_STORE((u32x2{__float_as_uint(m), __float_as_uint(lt)}),
+             reinterpret_cast<u32x2*>(p.part_ml + 2 * idx));
+}
+
+__device__ __forceinline__ void store_partial(const ChunkParams& p, int64_t bh, int chunk,
+                                              int64_t qblk0, const f32x16 (&o)[4], float m,
+                                              float lt, int lane) {
+    const int64_t blk = ((int64_t)bh * p.nch_total + chunk) * p.qblocks + (qblk0 >> 5);
+#pragma unroll
+    for (int st = 0; st < 8; ++st) store_partial_piece(p, blk, o, st, lane);
+    store_partial_ml(p, bh, chunk, qblk0 + (lane & 31), m, lt);
+}
+
 template <int DK, int NQB, bool FULL>
 __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkParams& p, int b,
                                              int h, int bh, int chunk, int64_t q0, int nsub,
@@ -767,31 +801,241 @@ __device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkPar
         load_q_block<DK>(qf[1], p, b, h, q_next + 32, q_next, lane);
     }
 
-    // partial of this chunk: O / l (bf16) and m + log2(l).  Lane dword k of
-    // a block holds o[db = k/8][2*(k%8) + {0, 1}] and is stored at
-    // 1 KB * (k/4) + 16 B * lane + 4 B * (k%4): every store instruction
-    // writes 1 KB contiguous.  Query columns past Q hold finite values
-    // that the combine ignores.
+    // partial of this chunk
 #pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-        const float lt = halfwave_sum(l[qb]);
-        const float inv = __builtin_amdgcn_rcpf(lt);  // the partial is rounded to bf16
-        const int64_t blk = ((int64_t)bh * p.nch_total + chunk) * p.qblocks + (q0 >> 5) + qb;
-        uint16_t* dst = p.part_o + blk * 4096 + lane * 8;
+    for (int qb = 0; qb < NQB; ++qb)
+        store_partial(p, bh, chunk, q0 + 32 * qb, o[qb], m[qb], halfwave_sum(l[qb]), lane);
+}
+
+// All of a wave's two-block query tiles of a full chunk as one pipeline.
+// Within a tile the 16 phases are those of attend_qtile's two-block path
+// (X(j): S1 = QK(K_j), O1 += PV(V_{j-1}), softmax(S0); Y(j): S0 =
+// QK(K_{j+1}), O0 += PV(V_j), softmax(S1)).  Across tiles there is no
+// seam: Y(7) computes the next tile's first scores (K_0 with the next
+// queries), X(0) adds the previous tile's last PV, and the previous tile's
+// partials are stored from X(0) (block 0) and Y(0) (block 1), spread over
+// their MFMA slots.  Each phase issues up to 16 MFMAs that do not depend on
+// its softmax, with the softmax, the LDS loads of the next operands and any
+// store work in between, one slice per MFMA (sched_barrier keeps the order),
+// so that one wave keeps the matrix core busy.
+//
+// Tile i covers queries (wave + 4 i) * 64 + [0, 64); every tile must have
+// both blocks (q0 + 32 < Q).  The first tile's "previous partials" are
+// stored into its own slots, which its real partials overwrite later (same
+// wave, same addresses, program order).
+template <int DK>
+__device__ __forceinline__ void attend_stream(const ChunkSmem& sm, const ChunkParams& p, int b,
+                                              int h, int bh, int chunk, int wave, int lane_in,
+                                              int ntiles) {
+    int lane = lane_in;
+    asm volatile("" : "+v"(lane));
+    const int hf = lane >> 5, l32 = lane & 31;
+    const float c = p.scale_log2;
+    using W = DWalk<DK>;
+    constexpr int KROW = KTile<DK>::ROW;
+    constexpr int KS = W::KSTEPS;
+    constexpr int NSTEP = CK_T / 32;
+    uint32_t koff = l32 * KROW + W::HALF * hf, voff = l32 * CK_VROW + 4 * hf;
+    asm volatile("" : "+v"(koff));
+    asm volatile("" : "+v"(voff));
+    const uint16_t* kbase = &sm.k[0][0] + koff;
+    const uint16_t* vbase = &sm.vt[0][0] + voff;
+    const int64_t part_blk = ((int64_t)bh * p.nch_total + chunk) * p.qblocks;
+    auto tile_q0 = [&](int i) { return (int64_t)(wave + 4 * i) * CK_QT; };
+
+    f32x16 o[2][4];
+    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
 #pragma unroll
-        for (int st = 0; st < 8; ++st) {
-            const int db = st >> 1, i0 = 8 * (st & 1);
-            u32x4 w;
+    for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-                w[e] = pack_bf16x2(o[qb][db][i0 + 2 * e] * inv, o[qb][db][i0 + 2 * e + 1] * inv);
-            NT_STORE(w, reinterpret_cast<u32x4*>(dst + 512 * st));
-        }
-        if (hf == 0)
-            NT_STORE(m[qb] + log2f(lt),
-                     p.part_lse + ((int64_t)bh * p.nch_total + chunk) * ((int64_t)p.qblocks * 32) +
-                         q0 + 32 * qb + l32);
+        for (int db = 0; db < 4; ++db) o[qb][db] = f32x16{};
+    f32x16 s0, s1;
+    bf16x8 p0[2], p1[2];
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts) p0[ts] = p1[ts] = bf16x8{};
+    bf16x8 kb[2][KS], vb[2][2][4];
+    bf16x8 qf[2][KS], qn[2][KS];  // this tile's and the next tile's query fragments
+
+    auto lds_k = [&](int j, int kk) { return lds_b128(kbase + 32 * j * KROW + W::block(kk)); };
+    auto lds_v = [&](int j, int t) {
+        return lds_2x64(vbase + 32 * (t & 3) * CK_VROW + 32 * j + 16 * (t >> 2));
+    };
+    {
+        const int64_t q0 = tile_q0(0);
+        load_q_block<DK>(qf[0], p, b, h, q0, q0, lane);
+        load_q_block<DK>(qf[1], p, b, h, q0 + 32, q0, lane);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) kb[0][kk] = lds_k(0, kk);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) vb[0][t >> 2][t & 3] = lds_v(0, t);
+        s0 = f32x16{};
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) s0 = mfma32(kb[0][kk], qf[0][kk], s0);
     }
+
+    // One phase.  NQK / NPV: MFMAs of the score / PV product (0 = none); ZPV:
+    // the PV product starts a new O (zero accumulator); FRESH: the softmax
+    // starts a new row state.  ld(t) / ext(t) add slot t's loads / extra work.
+    auto phase = [&](auto nqk_c, auto npv_c, auto zpv_c, auto fresh_c,
+                     const bf16x8 (&kq)[KS], const bf16x8 (&qsrc)[KS], f32x16& s_out,
+                     const bf16x8 (&vv)[2][4], int qv, const bf16x8 (&pin)[2], int qs,
+                     f32x16& s_in, bf16x8 (&pout)[2], float& alpha, auto&& ld,
+                     auto&& ext) -> bool {
+        constexpr int NQK = decltype(nqk_c)::value, NPV = decltype(npv_c)::value;
+        constexpr bool ZPV = decltype(zpv_c)::value, FRESH = decltype(fresh_c)::value;
+        constexpr int BOTH = NQK < NPV ? NQK : NPV;
+        const float mq = FRESH ? -INFINITY : m[qs];
+        float tm = 0.0f, mn = 0.0f, lsum = 0.0f;
+        bool up = false;
+        uint32_t pw[8];
+#pragma unroll
+        for (int t = 0; t < 16; ++t) {
+            int kind = -1, idx = 0;  // 0: score step idx, 1: PV step idx
+            if (t < 2 * BOTH) {
+                kind = t & 1;
+                idx = t >> 1;
+            } else if (t - BOTH < NQK && NQK > BOTH) {
+                kind = 0;
+                idx = t - BOTH;
+            } else if (t - BOTH < NPV && NPV > BOTH) {
+                kind = 1;
+                idx = t - BOTH;
+            }
+            if (kind == 0) {
+                s_out = mfma32(kq[idx], qsrc[idx], idx == 0 ? f32x16{} : s_out);
+            } else if (kind == 1) {
+                const int ts = idx >> 2, db = idx & 3;
+                o[qv][db] = mfma32(vv[ts][db], pin[ts], ZPV && ts == 0 ? f32x16{} : o[qv][db]);
+            }
+            // softmax slice t (the max is taken on raw scores: c > 0 preserves order)
+            if (t < 4) {
+                const float a = fmaxf(s_in[4 * t], s_in[4 * t + 1]);
+                const float b2 = fmaxf(s_in[4 * t + 2], s_in[4 * t + 3]);
+                tm = t == 0 ? fmaxf(a, b2) : fmaxf(tm, fmaxf(a, b2));
+            } else if (t == 4) {
+                tm = halfwave_max(tm) * c;
+                up = tm > mq + CK_TAU;
+                mn = up ? tm : mq;
+                alpha = up ? __builtin_amdgcn_exp2f(mq - mn) : 1.0f;
+                m[qs] = mn;
+            } else if (t < 13) {
+                // v_exp_f32 of arguments <= 8; results below 2^-126 flush to 0
+                const int k = t - 5;
+                const float e0 = __builtin_amdgcn_exp2f(fmaf(s_in[2 * k], c, -mn));
+                const float e1 = __builtin_amdgcn_exp2f(fmaf(s_in[2 * k + 1], c, -mn));
+                pw[k] = pack_bf16x2(e0, e1);
+            } else if (t < 15) {
+                // row sum of the bf16 weights the PV product uses
+#pragma unroll
+                for (int k = 4 * (t - 13); k < 4 * (t - 13) + 4; ++k)
+                    lsum = __builtin_amdgcn_fdot2_f32_bf16(
+                        __builtin_bit_cast(bf16x2, pw[k]),
+                        __builtin_bit_cast(bf16x2, 0x3F803F80u), lsum, false);
+            } else {
+                l[qs] = FRESH ? lsum : l[qs] * alpha + lsum;
+                asm volatile("" : "+v"(l[qs]));
+                pout[0] = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
+                pout[1] = as_bf16x8(u32x4{pw[4], pw[5], pw[6], pw[7]});
+            }
+            ld(t);
+            ext(t);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        return up;
+    };
+    auto rescale = [&](int qb, float alpha) {
+#pragma unroll
+        for (int db = 0; db < 4; ++db)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) o[qb][db][i] *= alpha;
+    };
+    using I0 = std::integral_constant<int, 0>;
+    using IK = std::integral_constant<int, KS>;
+    using I8 = std::integral_constant<int, 8>;
+    using BT = std::true_type;
+    using BF = std::false_type;
+    auto none = [](int) {};
+    // store work of the previous tile's block qb: its O pieces and (m, l)
+    // over slots 0 .. 8 of a phase
+    auto store_ext = [&](int qb, int64_t q0p, float mp, float lp) {
+        return [&, qb, q0p, mp, lp](int t) {
+            const int64_t blk = part_blk + (q0p >> 5) + qb;
+            if (t < 8) store_partial_piece(p, blk, o[qb], t, lane);
+            if (t == 8) store_partial_ml(p, bh, chunk, q0p + 32 * qb + l32, mp, halfwave_sum(lp));
+        };
+    };
+
+    for (int i = 0; i < ntiles; ++i) {
+        const int64_t q0 = tile_q0(i);
+        const int64_t q0p = i > 0 ? tile_q0(i - 1) : q0;
+        const int64_t qnx = tile_q0(i + 1);  // rows past Q are clamped to q0
+        float a0 = 1.0f, a1 = 1.0f;
+        // X(0): previous tile's O1 += PV(V_7); store its block 0
+        {
+            const float mp = m[0], lp = l[0];
+            auto ld = [&](int t) { if (t < KS) kb[1][t] = lds_k(1, t); };
+            phase(IK{}, I8{}, BF{}, BT{}, kb[0], qf[1], s1, vb[1], 1, p1, 0, s0, p0, a0, ld,
+                  store_ext(0, q0p, mp, lp));
+        }
+        // Y(0): O0 = PV(V_0) from zero; store the previous tile's block 1
+        {
+            const float mp = m[1], lp = l[1];
+            auto ld = [&](int t) { if (t < 8) vb[1][t >> 2][t & 3] = lds_v(1, t); };
+            phase(IK{}, I8{}, BT{}, BT{}, kb[1], qf[0], s0, vb[0], 0, p0, 1, s1, p1, a1, ld,
+                  store_ext(1, q0p, mp, lp));
+        }
+        // X(1): O1 = PV(V_0) from zero
+        {
+            auto ld = [&](int t) { if (t < KS) kb[0][t] = lds_k(2, t); };
+            const bool up = phase(IK{}, I8{}, BT{}, BF{}, kb[1], qf[1], s1, vb[0], 1, p1, 0, s0,
+                                  p0, a0, ld, none);
+            if (__any(up)) rescale(0, a0);
+        }
+        // Y(1)
+        {
+            auto ld = [&](int t) { if (t < 8) vb[0][t >> 2][t & 3] = lds_v(2, t); };
+            const bool up = phase(IK{}, I8{}, BF{}, BF{}, kb[0], qf[0], s0, vb[1], 0, p0, 1, s1,
+                                  p1, a1, ld, none);
+            if (__any(up)) rescale(1, a1);
+        }
+#pragma unroll
+        for (int j = 2; j < NSTEP; ++j) {
+            const int cj = j & 1, nj = cj ^ 1;
+            const int jn = (j + 1) % NSTEP;  // next step (the next tile's first after the last)
+            // X(j); the next tile's queries are requested during X(4) / X(5)
+            {
+                auto ld = [&](int t) { if (t < KS) kb[nj][t] = lds_k(jn, t); };
+                auto ext = [&](int t) {
+                    if (j == 4 && t == 0) load_q_block<DK>(qn[0], p, b, h, qnx, q0, lane);
+                    if (j == 5 && t == 0) load_q_block<DK>(qn[1], p, b, h, qnx + 32, q0, lane);
+                };
+                const bool up = phase(IK{}, I8{}, BF{}, BF{}, kb[cj], qf[1], s1, vb[nj], 1, p1,
+                                      0, s0, p0, a0, ld, ext);
+                if (__any(up)) rescale(0, a0);
+            }
+            // Y(j); Y(7) scores the next tile's first step with its block-0 queries
+            {
+                auto ld = [&](int t) { if (t < 8) vb[nj][t >> 2][t & 3] = lds_v(jn, t); };
+                const bool up = phase(IK{}, I8{}, BF{}, BF{}, kb[nj], j + 1 < NSTEP ? qf[0] : qn[0],
+                                      s0, vb[cj], 0, p0, 1, s1, p1, a1, ld, none);
+                if (__any(up)) rescale(1, a1);
+            }
+        }
+        // the next tile's queries become this tile's
+#pragma unroll
+        for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) qf[qb][kk] = qn[qb][kk];
+    }
+    // the last tile: O1 += PV(V_7), then both partials
+#pragma unroll
+    for (int ts = 0; ts < 2; ++ts)
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[1][db] = mfma32(vb[1][ts][db], p1[ts], o[1][db]);
+    const int64_t q0l = tile_q0(ntiles - 1);
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+        store_partial(p, bh, chunk, q0l + 32 * qb, o[qb], m[qb], halfwave_sum(l[qb]), lane);
 }
 
 template <int DK>
@@ -867,6 +1111,22 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
     const int nsub = (valid + 31) / 32;
     const int nqt = (int)cdiv(p.Q, CK_QT);
     constexpr int WAVES = CK_THREADS / 64;
+    if (valid == CK_T) {
+        // full chunk: the wave's two-block tiles (wave + 4 i, those with
+        // q0 + 32 < Q: a prefix of its tiles) as one pipeline, then at most
+        // one single-block tile
+        const int t2 = p.Q > 32 ? (int)((p.Q + 31) / CK_QT) : 0;
+        const int n2 = t2 > wave ? (t2 - wave + WAVES - 1) / WAVES : 0;
+        if (n2 > 0) attend_stream<DK>(sm, p, b, h, bh, chunk, wave, lane, n2);
+        const int qt = wave + WAVES * n2;
+        if (qt < nqt) {
+            const int64_t q0 = (int64_t)qt * CK_QT;
+            bf16x8 qf[2][8];
+            load_q_block<DK>(qf[0], p, b, h, q0, q0, lane);
+            attend_qtile<DK, 1, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q0);
+        }
+        return;
+    }
     bf16x8 qf[2][8];
     if (wave < nqt) {
         load_q_block<DK>(qf[0], p, b, h, (int64_t)wave * CK_QT, (int64_t)wave * CK_QT, lane);
@@ -876,21 +1136,17 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
         const int64_t q0 = (int64_t)qt * CK_QT;
         // the wave's next tile, or this one again (a harmless in-bounds reload)
         const int64_t q_next = qt + WAVES < nqt ? q0 + WAVES * CK_QT : q0;
-        const bool one = q0 + 32 >= p.Q;
-        if (valid == CK_T) {
-            if (one) attend_qtile<DK, 1, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
-            else attend_qtile<DK, 2, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
-        } else {
-            if (one) attend_qtile<DK, 1, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
-            else attend_qtile<DK, 2, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
-        }
+        if (q0 + 32 >= p.Q)
+            attend_qtile<DK, 1, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
+        else
+            attend_qtile<DK, 2, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
     }
 }
 
 // Merge the chunk partials of every (b, h, q).  A 256-thread block owns one
 // 32-query block; its four waves take every fourth chunk, each lane reading
 // the lane-order payload the attention wave stored, and sum through LDS.
-// out = sum_c 2^(lse_c - M) O_c / sum_c 2^(lse_c - M); no chunks give
+// out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c (O_c unnormalised); no chunks give
 // out = 0 and lse = -inf (CN/core.py:48-49).
 constexpr int CB_WAVES = 4;
 __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParams p) {
@@ -903,21 +1159,23 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
     const int64_t qi = (int64_t)qblk * 32 + l32;
     const int NC = p.nch_total;
     const int64_t lse_stride = (int64_t)p.qblocks * 32;
-    const float* lr = p.part_lse + bh * NC * lse_stride + qi;
-    // eight independent maxima keep eight loads in flight
+    const u32x2* ml = reinterpret_cast<const u32x2*>(p.part_ml) + bh * NC * lse_stride + qi;
+    // the largest running max; eight independent maxima keep eight loads in flight
     float mx[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) mx[e] = -INFINITY;
     int cc0 = 0;
     for (; cc0 + 8 <= NC; cc0 += 8) {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) mx[e] = fmaxf(mx[e], lr[(cc0 + e) * lse_stride]);
+        for (int e = 0; e < 8; ++e)
+            mx[e] = fmaxf(mx[e], __uint_as_float(ml[(cc0 + e) * lse_stride][0]));
     }
-    for (; cc0 < NC; ++cc0) mx[0] = fmaxf(mx[0], lr[cc0 * lse_stride]);
+    for (; cc0 < NC; ++cc0) mx[0] = fmaxf(mx[0], __uint_as_float(ml[cc0 * lse_stride][0]));
     float M = mx[0];
 #pragma unroll
     for (int e = 1; e < 8; ++e) M = fmaxf(M, mx[e]);
     const float Mu = M == -INFINITY ? 0.0f : M;
+    // out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c (O_c unnormalised)
     float L = 0.0f, acc[64];
 #pragma unroll
     for (int e = 0; e < 64; ++e) acc[e] = 0.0f;
@@ -925,8 +1183,9 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
     const int64_t cstride = (int64_t)p.qblocks * 4096;
 #pragma unroll 2
     for (int cc = wave; cc < NC; cc += CB_WAVES) {
-        const float wt = exp2f(lr[cc * lse_stride] - Mu);
-        L += wt;
+        const u32x2 mlc = ml[cc * lse_stride];
+        const float wt = exp2f(__uint_as_float(mlc[0]) - Mu);
+        L += wt * __uint_as_float(mlc[1]);
 #pragma unroll
         for (int st = 0; st < 8; ++st) {
             const u32x4 v = *reinterpret_cast<const u32x4*>(src + cc * cstride + 512 * st);
@@ -1035,7 +1294,7 @@ void launch_dk(const ChunkParams& p, int64_t blocks, hipStream_t s, int* rc) {
 size_t chunk_launch_workspace(const ChunkLaunchDesc& d) {
     const int64_t nc = chunk_count(d.n_rows) + chunk_count(d.Nc);
     const size_t blocks = (size_t)d.B * d.H * nc * cdiv(d.Q, 32);
-    return blocks * 32 * CK_D * sizeof(uint16_t) + blocks * 32 * sizeof(float);
+    return blocks * 32 * CK_D * sizeof(uint16_t) + blocks * 32 * 2 * sizeof(float);
 }
 
 int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_t workspace_bytes) {
@@ -1084,8 +1343,8 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.codec[1] = d.value;
     const size_t qrows = (size_t)d.B * d.H * p.nch_total * p.qblocks * 32;
     p.part_o = reinterpret_cast<uint16_t*>(workspace);
-    p.part_lse = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
-                                          qrows * CK_D * sizeof(uint16_t));
+    p.part_ml = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
+                                         qrows * CK_D * sizeof(uint16_t));
     p.out = d.out;
     p.o_sb = d.o_sb;
     p.o_st = d.o_st;
