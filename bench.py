@@ -40,7 +40,8 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=1, choices=(1, 2))
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3),
+                    help="1: headline config; 2: long history; 3: NanoKV-Fast on the config-1 shape")
     ap.add_argument("--splits", type=int, default=0,
                     help="query_tiles key splits (0 = automatic)")
     ap.add_argument("--schedule", default="auto", choices=("auto", "query_tiles", "key_chunks"),
@@ -132,11 +133,28 @@ def main():
     shape = synth.CONFIGS[args.config]
     layer, codecs, q, kc, vc = build_inputs(shape, device)
     out = torch.empty_like(q)
-    ws_bytes = ops.attend_workspace_size(q, shape.N, shape.Nc, codecs[0], codecs[1], args.splits,
-                                         args.schedule)
-    ws = torch.empty(max(ws_bytes, 1), device=device, dtype=torch.uint8)
+    fast = args.config == 3
+    if fast:
+        # NanoKV-Fast: every head attends the protected rows and the current
+        # keys at full width, the other rows through its reader group
+        from nanokv_amd import codec_native
+        reader = codec_native.ReaderLayer(synth.make_readers(shape, layer), device)
+        groups = [g.tensors() for g in reader.groups]
+        protect = synth.fast_protect_mask(shape, device=device)
+        prot_rows = torch.nonzero(protect).flatten().to(torch.int32)
+        low_rows = torch.nonzero(~protect).flatten().to(torch.int32)
+        ws_bytes = ops.fast_attend_workspace_size(q, kc, vc, codecs[0], codecs[1], prot_rows,
+                                                  low_rows, groups)
+        ws = torch.empty(max(ws_bytes, 1), device=device, dtype=torch.uint8)
+    else:
+        ws_bytes = ops.attend_workspace_size(q, shape.N, shape.Nc, codecs[0], codecs[1],
+                                             args.splits, args.schedule)
+        ws = torch.empty(max(ws_bytes, 1), device=device, dtype=torch.uint8)
 
     def step(events=None):
+        if fast:
+            return ops.fast_attend(q, kc, vc, codecs[0], codecs[1], prot_rows, low_rows, groups,
+                                   out=out, return_lse=False, workspace=ws)
         return ops.attend(q, kc, vc, codecs[0], codecs[1], out=out, splits=args.splits,
                           return_lse=False, workspace=ws, kernel_events=events,
                           schedule=args.schedule)
@@ -167,13 +185,19 @@ def main():
     torch.cuda.synchronize()
     t0 = time.perf_counter()
     for i in range(args.steps):
-        step((evs[i][0].cuda_event, evs[i][1].cuda_event))
+        if fast:
+            # several launches: the events bracket the whole call
+            evs[i][0].record()
+            step()
+            evs[i][1].record()
+        else:
+            step((evs[i][0].cuda_event, evs[i][1].cuda_event))
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
     kernel_ms = [b.elapsed_time(e) for b, e in evs]
     kavg_ms = sum(kernel_ms) / len(kernel_ms)
 
-    fl = shape.flops()
+    fl = shape.fast_flops(int(prot_rows.numel())) if fast else shape.flops()
     ms_per_step = wall * 1e3 / args.steps
     value = fl["total"] / (ms_per_step * 1e-3) / 1e12
     achieved = fl["total"] / (kavg_ms * 1e-3) / 1e12
@@ -182,6 +206,8 @@ def main():
     if schedule == "auto":
         schedule = "key_chunks" if shape.Q > 256 else "query_tiles"
     kernel = "nkv::chunk_kernel" if schedule == "key_chunks" else "nkv::attend_kernel"
+    if fast:
+        schedule, kernel = "key_chunks", "nkv_fast_attend (every launch of the call)"
     traffic = None
     if TRAFFIC_FILE.exists():
         try:
@@ -208,7 +234,9 @@ def main():
                    "D": shape.D, "history_tokens": shape.N, "query_tokens": shape.Q,
                    "current_tokens": shape.Nc, "rank_k": shape.rK, "rank_v": shape.rV,
                    "scale_group": shape.G, "scale_dtype": "fp16", "centers": shape.C,
-                   "parallelism": "single-gpu"},
+                   "parallelism": "single-gpu"}
+        | ({"protected_rows": int(prot_rows.numel()), "full_heads": list(synth.FAST_FULL_HEADS),
+            "reader_width": synth.FAST_READER_D} if fast else {}),
         "history_tokens_per_ms": round(shape.N / ms_per_step, 1),
         "coeff_stream_GBps": round(shape.coeff_stream_bytes() / (kavg_ms * 1e-3) / 1e9, 2),
         "algorithmic_flops": fl,
@@ -217,7 +245,7 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic, "kernel_ms_avg": round(kavg_ms, 4)},
     }
-    if not args.no_cpu_baseline:
+    if not args.no_cpu_baseline and not fast:
         result["cpu_baseline"] = cpu_baseline(shape, layer, codecs, q, kc, vc, args.cpu_seconds)
     print(json.dumps(result), flush=True)
 

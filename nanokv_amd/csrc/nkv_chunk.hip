@@ -1,40 +1,38 @@
 // nkv_chunk.hip -- key-chunk-major fused decode + attention for gfx950
 // (NKV_SCHEDULE_KEY_CHUNKS of nkv_attend).
 //
-// A 256-thread block (4 waves, one per SIMD) owns one (batch, head, chunk)
+// A 512-thread block (8 waves, two per SIMD) owns one (batch, head, chunk)
 // of 256 keys.  It decodes the chunk's K and V once into LDS -- K[key][d]
-// and V^T[d][key], bf16, 136 KB -- and then every wave attends its share of
-// ALL query tiles (64 queries each) to those keys.  Each (query, chunk)
-// leaves a partial: the chunk-local softmax output O / l as bf16 and its
-// log2-sum-exp m + log2(l) as fp32.  A combine kernel merges the partials of
-// every query by log-sum-exp (CN/core.py:33-42 applied over all chunks).  A
-// 32-query block's partial is stored in the MFMA accumulator's lane order
-// (8 KB: eight 1 KB rows of 16 bytes per lane), so the stores here and the
+// and V^T[d][key], bf16, 137 KB -- and then every wave attends its share of
+// ALL the head's 32-query blocks to those keys.  Each (query, chunk) leaves
+// a partial: the chunk-local O (bf16, unnormalised) with its running max and
+// row sum.  A combine kernel merges the partials of every query by
+// log-sum-exp (CN/core.py:33-42 applied over all chunks).  A 32-query
+// block's partial is stored in the MFMA accumulator's lane order (8 KB:
+// eight 1 KB rows of 16 bytes per lane), so the stores here and the
 // combine's loads are contiguous.
 // Decoding each history key once per head, instead of once per query tile,
 // removes the decode GEMM's re-execution; the price is the partial traffic
-// (256 + 4 bytes per query and chunk).
+// (256 + 8 bytes per query and chunk).
 //
-// Decode (per wave: 64 keys of the chunk, both codecs; MFMA 32x32x16 bf16):
+// Decode (per wave: 32 keys of the chunk, both codecs; MFMA 32x32x16 bf16):
 //   K^T = W_K[h*128 + d, :] . Z^T   (A = decoder rows, B = unpacked codes)
 //   V   = Z . W_V[h*128 + d, :]^T   (A = unpacked codes, B = decoder rows)
 // The k (rank) axis is walked in blocks of 64: lane half hf supplies
 // k = 64*kq + 32*hf + 8*j + [0, 8) at step j of block kq.  That permutation of
 // the summation index is applied to both operands, so one 16-byte load per
 // lane fetches the packed codes of four MFMA steps, and they share one scale
-// group (group % 32 == 0).  Decoder rows come straight from global memory
-// (L2-resident per head).  The epilogue is the reference decode arithmetic
+// group (group % 32 == 0).  Decoder rows stream through an LDS ring (see
+// below).  The epilogue is the reference decode arithmetic
 // bf16(bf16(acc + bf16(mean)) + center[id]) (MG:438-454); the accumulator
 // orientation puts four consecutive d (K) or four consecutive keys (V) in
 // one lane, so both tiles are written with 8-byte LDS stores.
 // Current-chunk keys (uncompressed bf16) are copied instead of decoded.
 //
-// Attention (per wave and 64-query tile; queries on the MFMA column axis):
+// Attention (per wave and 32-query block; queries on the MFMA column axis):
 //   S^T = K Q^T, P = exp2(S * c - m), O^T += V^T P^T
-// over eight 32-key steps, software-pipelined: step j's softmax (VALU) runs
-// between the MFMAs of step j+1's scores and step j-1's PV product, which
-// do not depend on it.  The running max is raised only when a score exceeds
-// it by more than 2^8 (P <= 256 otherwise), so O is rarely rescaled.
+// over eight 32-key steps.  The running max is raised only when a score
+// exceeds it by more than 2^8 (P <= 256 otherwise), so O is rarely rescaled.
 #include "nkv_common.h"
 #include "nkv_internal.h"
 
@@ -50,20 +48,8 @@ namespace nkv {
 
 constexpr int CK_T = 256;        // keys per chunk
 constexpr int CK_D = 128;        // head dim
-constexpr int CK_THREADS = 256;  // 4 waves
 constexpr int CK_KROW = CK_D + 8;   // K row: 68 dwords (b128 reads conflict-free)
-constexpr int CK_VROW = CK_T + 4;   // V^T row: 130 dwords (b64 reads conflict-free)
-constexpr int CK_QT = 64;        // queries per wave tile
 constexpr float CK_TAU = 8.0f;   // lazy-rescale threshold (log2 units)
-
-struct ChunkSmem {
-    // K tile [key][DK + 8] (for DK < 128 only the front of the region is the
-    // tile); also decoder-slice and center staging during the decode
-    uint16_t k[CK_T][CK_KROW];
-    uint16_t vt[CK_D][CK_VROW];   // V^T[d][key]
-    int ids[2][CK_T];             // center ids of the chunk's keys (K, V)
-    float bias[2][CK_D];          // bf16 bias of this head (K, V)
-};
 
 // K tile row pitch for a K/Q width DK (b128 reads of 8 rows hit distinct banks)
 template <int DK>
@@ -103,17 +89,17 @@ __device__ __forceinline__ int64_t history_row(const ChunkParams& p, int64_t key
 }
 
 // ------------------------------------------------------------------ decode
-// This wave's 64 keys (64*wave + [0, 64) of the chunk) of codec CODEC.
-//
 // Decoder slices W[row d of the launch head][64*s, +64) (WIDTH rows of 128
 // bytes) stream into a ring of DS_NBUF LDS buffers by direct-to-LDS loads
 // (global_load_lds_dwordx4: no register staging), DS_AHEAD slices ahead of
-// the MFMAs.  The block's four waves each copy WIDTH/32 KB of a slice, so
-// every decoder element is fetched from L2 once per block.  Rows are stored
-// unpadded with their 16-byte chunks XOR-swizzled by (row & 7): chunk c of
-// row r sits at chunk c ^ (r & 7), so the MFMA operand reads of eight
-// consecutive rows hit eight distinct chunks (conflict-free), while every
-// load instruction still fills one contiguous 1 KB of LDS.
+// the MFMAs.  The block's waves each copy a share of every slice, so every
+// decoder element is fetched from L2 once per block.  Rows are stored
+// unpadded with their 16-byte chunks XOR-swizzled: chunk c of row r sits at
+// chunk c ^ ((r >> 1) & 7).  gfx950 serves 16-byte LDS reads 16 lanes at a
+// time over 64 banks; with 128-byte rows, rows r and r + 1 share a bank half
+// only if their chunks differ, so the MFMA operand reads of 16 consecutive
+// rows are conflict-free, while every load instruction still fills one
+// contiguous 1 KB of LDS.
 //
 // A stage (slice s) = its decoder rows plus this wave's codes and scales of
 // slice s, which go to a register ring of DS_AHEAD entries.  Loads complete
@@ -122,9 +108,9 @@ __device__ __forceinline__ int64_t history_row(const ChunkParams& p, int64_t key
 constexpr int DS_NBUF = 4;
 constexpr int DS_AHEAD = 3;
 // The rings fit in the regions that hold no live data while they are used:
-// V's decode stages in the V^T region, K's in the K region.
-static_assert(DS_NBUF * CK_D * 64 <= CK_D * CK_VROW && DS_NBUF * CK_D * 64 <= CK_T * CK_KROW,
-              "decoder staging must fit in the V^T and K regions");
+// V's decode stages in the V^T region, K's in the K region; V's centers are
+// staged in the K region.
+static_assert(DS_NBUF * CK_D * 64 <= CK_T * CK_KROW, "decoder staging must fit in the K region");
 static_assert(CK_T * CK_D <= CK_T * CK_KROW, "V centers are staged in the K region");
 
 #define NKV_LDS(p) ((__attribute__((address_space(3))) void*)(p))
@@ -135,327 +121,6 @@ template <int N>
 __device__ __forceinline__ void wait_vmcnt() {
     static_assert(N >= 0 && N < 64, "vmcnt out of range");
     __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
-
-// The 128 center values of launch head h for the wave's 64 keys (V), copied
-// into LDS rows [key][128] (unpadded, key 64*wave + ... of the chunk) by
-// 16 direct-to-LDS loads, each filling 4 rows (1 KB).
-__device__ __forceinline__ void dma_v_centers(uint16_t* vcen, const ChunkSmem& sm,
-                                              const ChunkCodec& c, int b, int h, int wave,
-                                              int lane) {
-    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs + 8 * (lane & 15);
-#pragma unroll
-    for (int e = 0; e < 16; ++e) {
-        const int t = 64 * wave + 4 * e + (lane >> 4);
-        __builtin_amdgcn_global_load_lds(cent + (int64_t)sm.ids[1][t] * c.c_rs,
-                                         NKV_LDS(vcen + (64 * wave + 4 * e) * CK_D), 16, 0, 0);
-    }
-}
-
-// The DK center values of launch head h for the wave's 64 keys (K), as
-// coalesced 16-byte row pieces: entry e of lane L is piece q = 64*e + L of
-// the wave's rows, i.e. key 64*wave + q / (DK/8) of the chunk, columns
-// 8 * (q % (DK/8)).
-template <int DK>
-__device__ __forceinline__ void load_k_center_rows(u32x4 (&v)[DK / 8], const ChunkSmem& sm,
-                                                   const ChunkCodec& c, int b, int h, int wave,
-                                                   int lane) {
-    constexpr int PR = DK / 8;  // 16-byte pieces per row
-    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs;
-#pragma unroll
-    for (int e = 0; e < DK / 8; ++e) {
-        const int q = 64 * e + lane;  // piece index within the wave's 64 rows
-        const int t = 64 * wave + q / PR;
-        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[0][t] * c.c_rs +
-                                               8 * (q % PR));
-    }
-}
-
-// Decode this wave's 64 keys of codec CODEC to WIDTH columns (V: 128, into
-// V^T; K: the launch's DK, into the K tile with row pitch KROW).  wst: the
-// LDS ring (DS_NBUF * WIDTH * 64 bf16) that holds no live data during the
-// call.  HAS_C: the codec has centers (a template argument so that the
-// epilogue is straight-line code); V's are copied into the K region
-// (unpadded rows) after `pre`, K's are loaded into registers before the
-// slices.  pre() runs once the first stages are in flight (V: it publishes
-// the chunk's ids and biases, ending with a block barrier).  Ends with a
-// block barrier.
-template <int CODEC, bool HAS_C, int WIDTH, int KROW, typename Pre>
-__device__ __forceinline__ void decode_codec(ChunkSmem& sm, uint16_t* wst, const ChunkCodec& c,
-                                             const ChunkParams& p, int b, int h, int64_t tok0,
-                                             int valid, int wave, int lane, Pre&& pre) {
-    constexpr int NDT = WIDTH / 32;
-    constexpr int LPW = WIDTH / 32;           // 1 KB slice loads per wave
-    constexpr int STAGE = LPW + 4;            // vm instructions per stage
-    constexpr int SLICE = WIDTH * 64;         // bf16 per ring buffer
-    const int hf = lane >> 5, l32 = lane & 31;
-    const int R = c.r, KQ = R >> 6, G = c.group, NG = R / G;
-    const bool f16 = c.scale_dtype == NKV_DTYPE_FP16;
-    const uint8_t* prow[2];
-    const uint16_t* srow[2];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const int tl = 64 * wave + 32 * tt + l32;
-        // keys past the chunk end decode key 0's codes (finite, never attended)
-        const int64_t key = tok0 + (tl < valid ? tl : 0);
-        const int64_t tok = (int64_t)b * p.N + history_row(p, key);
-        prow[tt] = c.packed + tok * (R / 2) + 16 * hf;
-        srow[tt] = c.scales + tok * NG;
-    }
-    // slice loads: this wave fills 1 KB pieces 4*wave*.. of each slice; lane
-    // L brings logical chunk (L%8) ^ (L/8) of row 8*piece + L/8
-    const int piece_row = lane >> 3, piece_chunk = (lane & 7) ^ (lane >> 3);
-    const uint16_t* wsrc = c.w + (int64_t)h * c.w_hs + (int64_t)piece_row * R + 8 * piece_chunk;
-    auto issue_slice = [&](int s) {
-        uint16_t* dst = wst + (s % DS_NBUF) * SLICE;
-#pragma unroll
-        for (int e = 0; e < LPW; ++e) {
-            const int piece = LPW * wave + e;  // rows 8*piece .. +8
-            __builtin_amdgcn_global_load_lds(wsrc + (int64_t)8 * piece * R + 64 * s,
-                                             NKV_LDS(dst + piece * 512), 16, 0, 0);
-        }
-    };
-    // codes and raw scale bits (converted at use: converting here would make
-    // the issue wait for the load)
-    auto issue_codes = [&](int s, u32x4 (&pk)[2], uint16_t (&sb)[2]) {
-        const int gi = (64 * s + 32 * hf) / G;
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            pk[tt] = *reinterpret_cast<const u32x4*>(prow[tt] + 32 * s);
-            sb[tt] = srow[tt][gi];
-        }
-    };
-
-    f32x16 acc[NDT][2];
-#pragma unroll
-    for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) acc[dt][tt] = f32x16{};
-
-    // K: center rows, issued before stage 0 (so complete before it)
-    uint16_t* vcen = &sm.k[0][0];
-    u32x4 kcen[WIDTH / 8];
-    if (CODEC == 0 && HAS_C) load_k_center_rows<WIDTH>(kcen, sm, c, b, h, wave, lane);
-
-    u32x4 pk[DS_AHEAD][2];
-    uint16_t sc[DS_AHEAD][2];
-    // (sched_barrier: the stages must leave in this order, since the vmcnt
-    // bounds below count whole stages)
-#pragma unroll
-    for (int i = 0; i < DS_AHEAD; ++i)
-        if (i < KQ) {
-            issue_slice(i);
-            issue_codes(i, pk[i], sc[i]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    pre();
-    // V: center rows into the K region, issued after stages 0 .. DS_AHEAD-1
-    // and before stage DS_AHEAD: NVC more instructions may be in flight while
-    // waiting for the first DS_AHEAD stages
-    constexpr int NVC = CODEC == 1 && HAS_C ? 16 : 0;
-    if (CODEC == 1 && HAS_C) dma_v_centers(vcen, sm, c, b, h, wave, lane);
-    __builtin_amdgcn_sched_barrier(0);
-
-    // per-lane swizzled chunk offsets of the operand reads: row 32*dt + l32,
-    // logical chunk 4*hf + j
-    int wofs[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) wofs[j] = l32 * 64 + 8 * ((4 * hf + j) ^ (l32 & 7));
-
-    // operand of the current sub-step (carried across slices), and its scales
-    u32x4 zc[2];
-    float scl[2], ns7[2];
-    if (KQ > 0) {
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            scl[tt] = f16 ? f16_bits_to_f32(sc[0][tt]) : bf16_bits_to_f32(sc[0][tt]);
-            ns7[tt] = -7.0f * scl[tt];
-            Unpack8 u;
-            u.split(pk[0][tt][0]);
-#pragma unroll
-            for (int e = 0; e < 4; ++e) zc[tt][e] = u.pair(e, scl[tt], ns7[tt]);
-        }
-    }
-    for (int s0 = 0; s0 < KQ; s0 += DS_AHEAD) {
-#pragma unroll
-        for (int i = 0; i < DS_AHEAD; ++i) {
-            const int s = s0 + i;
-            if (s >= KQ) break;
-            // stage s landed (for this wave) once at most the later issued
-            // stages are in flight; the barrier makes every wave's part visible
-            // and retires the reads of the buffer the next slice goes to
-            static_assert(DS_AHEAD == 3, "the wait bounds below assume three stages ahead");
-            const int later = min(KQ - 1 - s, DS_AHEAD - 1);
-            if (s < DS_AHEAD) {
-                if (later >= 2) wait_vmcnt<2 * STAGE + NVC>();
-                else if (later == 1) wait_vmcnt<STAGE + NVC>();
-                else wait_vmcnt<NVC>();
-            } else {
-                if (later >= 2) wait_vmcnt<2 * STAGE>();
-                else if (later == 1) wait_vmcnt<STAGE>();
-                else wait_vmcnt<0>();
-            }
-            __builtin_amdgcn_s_barrier();
-            if (s + DS_AHEAD < KQ) issue_slice(s + DS_AHEAD);
-            __builtin_amdgcn_sched_barrier(0);
-            const uint16_t* wb = wst + (s % DS_NBUF) * SLICE;
-            // Software pipeline in explicit slots: each MFMA of sub-step j is
-            // followed by one eighth of the next sub-step's unpack (for the
-            // last sub-step: the next slice's first, whose codes are already
-            // in the ring) and, every other slot, one of the next sub-step's
-            // decoder-operand reads (not across slices: those need the
-            // barrier); sched_barrier keeps the slots in order so that the
-            // unpack runs under the MFMAs.
-            // (after the last slice the ring entry holds stale codes: the
-            // unpack is then wasted work, kept branch-free)
-            const int inx = (i + 1) % DS_AHEAD;
-            float scn[2], nsn[2];
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                scn[tt] = f16 ? f16_bits_to_f32(sc[inx][tt]) : bf16_bits_to_f32(sc[inx][tt]);
-                nsn[tt] = -7.0f * scn[tt];
-            }
-            u32x4 zn[2];
-            bf16x8 wc[NDT], wn[NDT];
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt) wc[dt] = lds_b128(wb + 32 * dt * 64 + wofs[0]);
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                Unpack8 u[2];
-                constexpr int SLOTS = 2 * NDT;  // MFMAs per sub-step
-#pragma unroll
-                for (int m = 0; m < SLOTS; ++m) {
-                    const int dt = m >> 1, tt = m & 1;
-                    acc[dt][tt] = CODEC == 0 ? mfma32(wc[dt], as_bf16x8(zc[tt]), acc[dt][tt])
-                                             : mfma32(as_bf16x8(zc[tt]), wc[dt], acc[dt][tt]);
-                    // unpack pieces: 8 dwords (2 tt x 4) over the SLOTS slots
-#pragma unroll
-                    for (int q = (8 * m) / SLOTS; q < (8 * (m + 1)) / SLOTS; ++q) {
-                        const int qt = q >> 2, qe = q & 3;
-                        if (j + 1 < 4) {
-                            if (qe == 0) u[qt].split(pk[i][qt][j + 1]);
-                            zn[qt][qe] = u[qt].pair(qe, scl[qt], ns7[qt]);
-                        } else {
-                            if (qe == 0) u[qt].split(pk[inx][qt][0]);
-                            zn[qt][qe] = u[qt].pair(qe, scn[qt], nsn[qt]);
-                            // computed here, under this slice's MFMAs (the
-                            // compiler would otherwise sink it past the barrier)
-                            asm volatile("" : "+v"(zn[qt][qe]));
-                        }
-                    }
-                    if (j + 1 < 4 && (m & 1) == 0)
-                        wn[dt] = lds_b128(wb + 32 * dt * 64 + wofs[j + 1]);
-                    __builtin_amdgcn_sched_barrier(0);
-                }
-#pragma unroll
-                for (int tt = 0; tt < 2; ++tt) zc[tt] = zn[tt];
-                if (j + 1 < 4) {
-#pragma unroll
-                    for (int dt = 0; dt < NDT; ++dt) wc[dt] = wn[dt];
-                }
-            }
-#pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                scl[tt] = scn[tt];
-                ns7[tt] = nsn[tt];
-            }
-            // this ring entry is consumed: refill it with stage s + DS_AHEAD
-            __builtin_amdgcn_sched_barrier(0);
-            if (s + DS_AHEAD < KQ) issue_codes(s + DS_AHEAD, pk[i], sc[i]);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-    // every wave's slice reads are done before the epilogue writes over the ring
-    __syncthreads();
-
-    // Epilogue.  sm.bias holds bf16(mean) or zeros, so the bias add is
-    // unconditional.
-    if (CODEC == 0) {
-        // acc[dt][tt] element i: d = 32*dt + 8*(i/4) + 4*hf + i%4, key
-        // 64*wave + 32*tt + l32.  Pass 1 stores bf16(acc + bias) ...
-        uint16_t* ktile = &sm.k[0][0];
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            const int t = 64 * wave + 32 * tt + l32;
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int d = 32 * dt + 8 * g + 4 * hf;
-                    float a[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) a[e] = acc[dt][tt][4 * g + e] + sm.bias[0][d + e];
-                    const u32x2 r = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
-                    *reinterpret_cast<u32x2*>(ktile + t * KROW + d) = r;
-                }
-        }
-        if (HAS_C) {
-            // ... pass 2 adds the center rows piece by piece (the wave's own
-            // rows: its LDS operations stay in order, no barrier needed)
-            constexpr int PR = WIDTH / 8;
-#pragma unroll
-            for (int e = 0; e < WIDTH / 8; ++e) {
-                const int q = 64 * e + lane;
-                u32x4* slot = reinterpret_cast<u32x4*>(ktile + (64 * wave + q / PR) * KROW +
-                                                       8 * (q % PR));
-                const u32x4 kv = *slot;
-                u32x4 r;
-#pragma unroll
-                for (int h2 = 0; h2 < 4; ++h2)
-                    r[h2] = pack_bf16x2(
-                        __uint_as_float(kv[h2] << 16) + __uint_as_float(kcen[e][h2] << 16),
-                        __uint_as_float(kv[h2] & 0xffff0000u) +
-                            __uint_as_float(kcen[e][h2] & 0xffff0000u));
-                *slot = r;
-            }
-        }
-    } else {
-        // acc[dt][tt] element i: key 64*wave + 32*tt + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32;
-        // the center rows of the wave's keys are in vcen
-#pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int t0 = 64 * wave + 32 * tt + 8 * g + 4 * hf;
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) {
-                    const int d = 32 * dt + l32;
-                    const float bias = sm.bias[1][d];
-                    float v[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float a = bf16_round(acc[dt][tt][4 * g + e] + bias);
-                        v[e] = HAS_C ? a + bf16_bits_to_f32(vcen[(t0 + e) * CK_D + d]) : a;
-                    }
-                    const u32x2 r = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-                    *reinterpret_cast<u32x2*>(&sm.vt[d][t0]) = r;
-                }
-            }
-    }
-}
-
-// Current-chunk keys: copy K rows, transpose V into V^T (rows past the end
-// are zero).
-// (Current keys are native: the launch's DK is 128.)
-__device__ __forceinline__ void load_current_chunk(ChunkSmem& sm, const ChunkParams& p, int b,
-                                                   int h, int64_t tok0, int valid, int t) {
-    const bool ok = t < valid;
-    const uint16_t* ks = p.k_cur + (int64_t)b * p.k_sb + (tok0 + (ok ? t : 0)) * p.k_st +
-                         (int64_t)h * p.k_sh;
-    const uint16_t* vs = p.v_cur + (int64_t)b * p.v_sb + (tok0 + (ok ? t : 0)) * p.v_st +
-                         (int64_t)h * p.v_sh;
-#pragma unroll 4
-    for (int e = 0; e < CK_D / 8; ++e) {
-        u32x4 kv = *reinterpret_cast<const u32x4*>(ks + 8 * e);
-        u32x4 vv = *reinterpret_cast<const u32x4*>(vs + 8 * e);
-        if (!ok) kv = vv = u32x4{0, 0, 0, 0};
-        *reinterpret_cast<u32x4*>(&sm.k[t][8 * e]) = kv;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            sm.vt[8 * e + 2 * i][t] = (uint16_t)(vv[i] & 0xffffu);
-            sm.vt[8 * e + 2 * i + 1][t] = (uint16_t)(vv[i] >> 16);
-        }
-    }
 }
 
 // --------------------------------------------------------------- attention
@@ -489,12 +154,6 @@ __device__ __forceinline__ void load_q_block(bf16x8 (&qf)[NF], const ChunkParams
         qf[kk] = as_bf16x8(*reinterpret_cast<const u32x4*>(qrow + W::block(kk)));
 }
 
-// One wave attends queries [q0, q0 + 32*NQB) to the chunk in LDS.  FULL: the
-// chunk has all 256 keys (eight pipelined steps); otherwise nsub steps with
-// the last one masked to `valid` keys.  qf holds this tile's query
-// fragments on entry; as soon as a query block's last score product is
-// issued, its registers are refilled with the wave's next tile (first query
-// q_next), so that tile's loads overlap this tile's remaining work.
 // The partial of one 32-query block for this chunk: its O (unnormalised,
 // bf16) and per query the running max m (log2 units) and row sum l, so that
 // the combine forms sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c.  Lane
@@ -528,529 +187,403 @@ __device__ __forceinline__ void store_partial(const ChunkParams& p, int64_t bh, 
     store_partial_ml(p, bh, chunk, qblk0 + (lane & 31), m, lt);
 }
 
-template <int DK, int NQB, bool FULL>
-__device__ __forceinline__ void attend_qtile(const ChunkSmem& sm, const ChunkParams& p, int b,
-                                             int h, int bh, int chunk, int64_t q0, int nsub,
-                                             int valid, int lane_in, bf16x8 (&qf)[2][8],
-                                             int64_t q_next) {
-    // Opaque per-tile copy of the lane index: every lane-dependent address
-    // below is recomputed per tile instead of being hoisted out of the
-    // query-tile loop (where it would be spilled: the loop body needs
-    // nearly all 256 VGPRs).
-    int lane = lane_in;
-    asm volatile("" : "+v"(lane));
-    const int hf = lane >> 5, l32 = lane & 31;
-    const float c = p.scale_log2;
+// ======================================================= 8-wave key-chunk kernel
+// The same key-chunk schedule with eight waves per block, two per SIMD: while
+// one wave runs VALU work (INT4 unpack, decode epilogue, softmax) the other's
+// MFMAs keep the matrix core busy, so each wave's own code can stay serial.
+// Each wave decodes 32 of the chunk's keys and attends 32-query blocks.
+// Every attention operand is one 16-byte LDS read (gfx950 serves those at
+// up to ~190 B/clk per CU with several waves per SIMD, against ~125 for
+// 8-byte reads).
+constexpr int C8_THREADS = 512;
+constexpr int C8_WAVES = C8_THREADS / 64;
+constexpr int C8_VROW = CK_T + 8;  // V^T row: 132 dwords, 16 rows of b128 reads hit distinct banks
 
-    f32x16 o[NQB][4];
-    float m[NQB], l[NQB];
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb) {
-        m[qb] = -INFINITY;
-        l[qb] = 0.0f;
-#pragma unroll
-        for (int db = 0; db < 4; ++db) o[qb][db] = f32x16{};
-    }
+struct Chunk8Smem {
+    uint16_t k[CK_T][CK_KROW];  // K tile (also decoder-slice and center staging)
+    uint16_t vt[CK_D][C8_VROW];  // V^T[d][vt_col(key)]
+    int ids[2][CK_T];
+    float bias[2][CK_D];
+};
+static_assert(sizeof(Chunk8Smem) <= 160 * 1024, "LDS budget");
+static_assert(DS_NBUF * CK_D * 64 <= CK_D * C8_VROW, "decoder staging must fit in the V^T region");
 
-    // K fragments of step j (shared by both query blocks)
-    // Fragment addresses are an opaque per-tile base plus compile-time
-    // offsets (< 64 KiB, folded into the ds_read instructions); without the
-    // opaque step the compiler hoists one address register per unrolled
-    // fragment out of the query-tile loop and spills.
-    using W = DWalk<DK>;
-    constexpr int KROW = KTile<DK>::ROW;
-    constexpr int KS = W::KSTEPS;
-    uint32_t koff = l32 * KROW + W::HALF * hf, voff = l32 * CK_VROW + 4 * hf;
-    asm volatile("" : "+v"(koff));
-    asm volatile("" : "+v"(voff));
-    const uint16_t* kbase = &sm.k[0][0] + koff;
-    const uint16_t* vbase = &sm.vt[0][0] + voff;
-    auto load_k = [&](int j, bf16x8 (&kf)[KS]) {
-        const uint16_t* kr = kbase + 32 * j * KROW;
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) kf[kk] = lds_b128(kr + W::block(kk));
-    };
-    // V^T fragments of step j: P^T operand slot jj of half-step ts holds key
-    // 16*ts + 8*(jj/4) + 4*hf + jj%4 (accumulator element 8*ts + jj of S^T),
-    // and V^T is read with the same key permutation.
-    auto load_v = [&](int j, bf16x8 (&vf)[2][4]) {
-#pragma unroll
-        for (int ts = 0; ts < 2; ++ts)
-#pragma unroll
-            for (int db = 0; db < 4; ++db)
-                vf[ts][db] = lds_2x64(vbase + 32 * db * CK_VROW + 32 * j + 16 * ts);
-    };
-    auto qk = [&](int qb, const bf16x8 (&kf)[KS], f32x16& s) {
-        s = f32x16{};
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) s = mfma32(kf[kk], qf[qb][kk], s);
-    };
-    auto pv = [&](int qb, const bf16x8 (&vf)[2][4], const bf16x8 (&pb)[2]) {
-#pragma unroll
-        for (int ts = 0; ts < 2; ++ts)
-#pragma unroll
-            for (int db = 0; db < 4; ++db) o[qb][db] = mfma32(vf[ts][db], pb[ts], o[qb][db]);
-    };
-    // online softmax of one 32-key x 32-query score tile; returns whether
-    // this lane raised its running max (then O must be scaled by alpha)
-    auto softmax = [&](int qb, f32x16& s, bf16x8 (&pb)[2], float& alpha) {
-        float tmax = fmaxf(s[0], s[1]);
-#pragma unroll
-        for (int i = 2; i < 16; ++i) tmax = fmaxf(tmax, s[i]);
-        // the max is taken on raw scores (c > 0 preserves order)
-        tmax = halfwave_max(tmax) * c;
-        const bool up = tmax > m[qb] + CK_TAU;
-        const float m_new = up ? tmax : m[qb];
-        alpha = up ? __builtin_amdgcn_exp2f(m[qb] - m_new) : 1.0f;
-        m[qb] = m_new;
-        float lsum = 0.0f;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            // v_exp_f32 of arguments <= 8; results below 2^-126 flush to 0
-            const float e = __builtin_amdgcn_exp2f(fmaf(s[i], c, -m_new));
-            s[i] = e;
-            lsum += e;
-        }
-        l[qb] = l[qb] * alpha + lsum;
-        // materialise the row sum here: left alone, the compiler defers these
-        // adds to the end of the tile and keeps every exp value alive (spills)
-        asm volatile("" : "+v"(l[qb]));
-#pragma unroll
-        for (int ts = 0; ts < 2; ++ts) {
-            u32x4 v;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) v[e] = pack_bf16x2(s[8 * ts + 2 * e], s[8 * ts + 2 * e + 1]);
-            pb[ts] = as_bf16x8(v);
-        }
-        return up;
-    };
-    auto rescale = [&](int qb, float alpha) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[qb][db][i] *= alpha;
-    };
-
-    constexpr int NSTEP = CK_T / 32;
-    if (FULL && NQB == 2) {
-        // Two query blocks staggered by half a step.  Every phase issues up
-        // to 16 MFMAs that do not depend on its softmax (one block's scores
-        // of the next step, the other block's PV) and spreads that softmax
-        // between them, one slice per MFMA, with the next operands' LDS
-        // loads riding along; sched_barrier fences keep this order, so one
-        // wave keeps the matrix core busy while it runs the softmax.
-        //   X(j): S1 = QK(K_j), O1 += PV(V_{j-1}, P1) | softmax(S0) | load K_{j+1}
-        //   Y(j): S0 = QK(K_{j+1}), O0 += PV(V_j, P0) | softmax(S1) | load V_{j+1}
-        f32x16 s0, s1;
-        bf16x8 p0[2], p1[2];
-        bf16x8 kb[2][KS], vb[2][2][4];
-        float a0 = 1.0f, a1 = 1.0f;
-        load_k(0, kb[0]);
-        load_v(0, vb[0]);
-        qk(0, kb[0], s0);
-        // one phase; NQK / NPV = MFMAs of the score / PV product (0 = none)
-        auto phase = [&](auto nqk_c, auto npv_c, const bf16x8 (&kq)[KS], int qa, f32x16& s_out,
-                         const bf16x8 (&vv)[2][4], int qv, const bf16x8 (&pin)[2], int qs,
-                         f32x16& s_in, bf16x8 (&pout)[2], float& alpha, auto&& ld) -> bool {
-            constexpr int NQK = decltype(nqk_c)::value, NPV = decltype(npv_c)::value;
-            constexpr int BOTH = NQK < NPV ? NQK : NPV;
-            const float mq = m[qs];
-            float tm = 0.0f, mn = 0.0f, lsum = 0.0f;
-            bool up = false;
-            uint32_t pw[8];
-#pragma unroll
-            for (int t = 0; t < 16; ++t) {
-                // MFMA t: score and PV products alternate, then the longer one's tail
-                int kind = -1, idx = 0;  // 0: score step idx, 1: PV step idx
-                if (t < 2 * BOTH) {
-                    kind = t & 1;
-                    idx = t >> 1;
-                } else if (t - BOTH < NQK && NQK > BOTH) {
-                    kind = 0;
-                    idx = t - BOTH;
-                } else if (t - BOTH < NPV && NPV > BOTH) {
-                    kind = 1;
-                    idx = t - BOTH;
-                }
-                if (kind == 0) {
-                    s_out = mfma32(kq[idx], qf[qa][idx], idx == 0 ? f32x16{} : s_out);
-                } else if (kind == 1) {
-                    const int ts = idx >> 2, db = idx & 3;
-                    o[qv][db] = mfma32(vv[ts][db], pin[ts], o[qv][db]);
-                }
-                // softmax slice t (the max is taken on raw scores: c > 0 preserves order)
-                if (t < 4) {
-                    const float a = fmaxf(s_in[4 * t], s_in[4 * t + 1]);
-                    const float b2 = fmaxf(s_in[4 * t + 2], s_in[4 * t + 3]);
-                    tm = t == 0 ? fmaxf(a, b2) : fmaxf(tm, fmaxf(a, b2));
-                } else if (t == 4) {
-                    tm = halfwave_max(tm) * c;
-                    up = tm > mq + CK_TAU;
-                    mn = up ? tm : mq;
-                    alpha = up ? __builtin_amdgcn_exp2f(mq - mn) : 1.0f;
-                    m[qs] = mn;
-                } else if (t < 13) {
-                    // v_exp_f32 of arguments <= 8; results below 2^-126 flush to 0
-                    const int k = t - 5;
-                    const float e0 = __builtin_amdgcn_exp2f(fmaf(s_in[2 * k], c, -mn));
-                    const float e1 = __builtin_amdgcn_exp2f(fmaf(s_in[2 * k + 1], c, -mn));
-                    pw[k] = pack_bf16x2(e0, e1);
-                } else if (t < 15) {
-                    // row sum of the bf16 weights the PV product uses
-#pragma unroll
-                    for (int k = 4 * (t - 13); k < 4 * (t - 13) + 4; ++k)
-                        lsum = __builtin_amdgcn_fdot2_f32_bf16(
-                            __builtin_bit_cast(bf16x2, pw[k]),
-                            __builtin_bit_cast(bf16x2, 0x3F803F80u), lsum, false);
-                } else {
-                    l[qs] = l[qs] * alpha + lsum;
-                    asm volatile("" : "+v"(l[qs]));
-                    pout[0] = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
-                    pout[1] = as_bf16x8(u32x4{pw[4], pw[5], pw[6], pw[7]});
-                }
-                ld(t);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-            return up;
-        };
-        using I0 = std::integral_constant<int, 0>;
-        using IK = std::integral_constant<int, KS>;
-        using I8 = std::integral_constant<int, 8>;
-        auto no_load = [](int) {};
-#pragma unroll
-        for (int j = 0; j < NSTEP; ++j) {
-            const int cj = j & 1, nj = cj ^ 1;
-            auto ld_k = [&](int t) {
-                if (j + 1 < NSTEP && t < KS) kb[nj][t] = lds_b128(kbase + 32 * (j + 1) * KROW + W::block(t));
-            };
-            auto ld_v = [&](int t) {
-                if (j + 1 < NSTEP && t < 8)
-                    vb[nj][t >> 2][t & 3] =
-                        lds_2x64(vbase + 32 * (t & 3) * CK_VROW + 32 * (j + 1) + 16 * (t >> 2));
-            };
-            bool up0;
-            if (j == 0)
-                up0 = phase(IK{}, I0{}, kb[cj], 1, s1, vb[nj], 1, p1, 0, s0, p0, a0, ld_k);
-            else
-                up0 = phase(IK{}, I8{}, kb[cj], 1, s1, vb[nj], 1, p1, 0, s0, p0, a0, ld_k);
-            if (j == NSTEP - 1) load_q_block<DK>(qf[1], p, b, h, q_next + 32, q_next, lane);
-            if (j > 0 && __any(up0)) rescale(0, a0);
-            bool up1;
-            if (j + 1 < NSTEP)
-                up1 = phase(IK{}, I8{}, kb[nj], 0, s0, vb[cj], 0, p0, 1, s1, p1, a1, ld_v);
-            else
-                up1 = phase(I0{}, I8{}, kb[nj], 0, s0, vb[cj], 0, p0, 1, s1, p1, a1, no_load);
-            if (j == NSTEP - 2) load_q_block<DK>(qf[0], p, b, h, q_next, q_next, lane);
-            if (j > 0 && __any(up1)) rescale(1, a1);
-        }
-        pv(1, vb[(NSTEP - 1) & 1], p1);
-    } else if (FULL) {
-        // one query block: step j+1's scores and step j-1's PV under step j's softmax
-        f32x16 s[2];
-        bf16x8 pp[2][2], kf[KS], vprev[2][4];
-        float a0;
-        load_k(0, kf);
-        qk(0, kf, s[0]);
-#pragma unroll
-        for (int j = 0; j < NSTEP; ++j) {
-            const int cur = j & 1, nxt = cur ^ 1;
-            bf16x8 vf[2][4];
-            if (j + 1 < NSTEP) {
-                load_k(j + 1, kf);
-                qk(0, kf, s[nxt]);
-            }
-            if (j == NSTEP - 2) {
-                load_q_block<DK>(qf[0], p, b, h, q_next, q_next, lane);
-                load_q_block<DK>(qf[1], p, b, h, q_next + 32, q_next, lane);
-            }
-            if (j > 0) pv(0, vprev, pp[nxt]);
-            load_v(j, vf);
-            const bool up = softmax(0, s[cur], pp[cur], a0);
-            if (j > 0 && __any(up)) rescale(0, a0);
-#pragma unroll
-            for (int ts = 0; ts < 2; ++ts)
-#pragma unroll
-                for (int db = 0; db < 4; ++db) vprev[ts][db] = vf[ts][db];
-        }
-        pv(0, vprev, pp[(NSTEP - 1) & 1]);
-    } else {
-        for (int j = 0; j < nsub; ++j) {
-            bf16x8 kf[KS], vf[2][4];
-            load_k(j, kf);
-            load_v(j, vf);
-            const int vj = valid - 32 * j;
-            int hfo = hf;  // opaque: keeps the mask constants out of the outer loop
-            asm volatile("" : "+v"(hfo));
-#pragma unroll
-            for (int qb = 0; qb < NQB; ++qb) {
-                f32x16 s;
-                bf16x8 pb[2];
-                float a;
-                qk(qb, kf, s);
-                if (vj < 32) {
-#pragma unroll
-                    for (int i = 0; i < 16; ++i)
-                        if (8 * (i >> 2) + 4 * hfo + (i & 3) >= vj) s[i] = -INFINITY;
-                }
-                const bool up = softmax(qb, s, pb, a);
-                if (j > 0 && __any(up)) rescale(qb, a);
-                pv(qb, vf, pb);
-            }
-        }
-        load_q_block<DK>(qf[0], p, b, h, q_next, q_next, lane);
-        load_q_block<DK>(qf[1], p, b, h, q_next + 32, q_next, lane);
-    }
-
-    // partial of this chunk
-#pragma unroll
-    for (int qb = 0; qb < NQB; ++qb)
-        store_partial(p, bh, chunk, q0 + 32 * qb, o[qb], m[qb], halfwave_sum(l[qb]), lane);
+// V^T column of a key: inside each group of 16 keys the middle two quarters
+// swap (0 1 2 3 -> 0 2 1 3), so the eight keys one lane half supplies to a
+// PV MFMA step (quarters hf and hf + 2 of the group) are one contiguous
+// 16-byte run.
+__device__ __forceinline__ int vt_col(int key) {
+    const int q = (key >> 2) & 3;
+    const int pq = (q == 1 || q == 2) ? 3 - q : q;
+    return (key & ~15) | (pq << 2) | (key & 3);
 }
 
-// All of a wave's two-block query tiles of a full chunk as one pipeline.
-// Within a tile the 16 phases are those of attend_qtile's two-block path
-// (X(j): S1 = QK(K_j), O1 += PV(V_{j-1}), softmax(S0); Y(j): S0 =
-// QK(K_{j+1}), O0 += PV(V_j), softmax(S1)).  Across tiles there is no
-// seam: Y(7) computes the next tile's first scores (K_0 with the next
-// queries), X(0) adds the previous tile's last PV, and the previous tile's
-// partials are stored from X(0) (block 0) and Y(0) (block 1), spread over
-// their MFMA slots.  Each phase issues up to 16 MFMAs that do not depend on
-// its softmax, with the softmax, the LDS loads of the next operands and any
-// store work in between, one slice per MFMA (sched_barrier keeps the order),
-// so that one wave keeps the matrix core busy.
-//
-// Tile i covers queries (wave + 4 i) * 64 + [0, 64); every tile must have
-// both blocks (q0 + 32 < Q).  The first tile's "previous partials" are
-// stored into its own slots, which its real partials overwrite later (same
-// wave, same addresses, program order).
-template <int DK>
-__device__ __forceinline__ void attend_stream(const ChunkSmem& sm, const ChunkParams& p, int b,
-                                              int h, int bh, int chunk, int wave, int lane_in,
-                                              int ntiles) {
-    int lane = lane_in;
-    asm volatile("" : "+v"(lane));
-    const int hf = lane >> 5, l32 = lane & 31;
-    const float c = p.scale_log2;
-    using W = DWalk<DK>;
-    constexpr int KROW = KTile<DK>::ROW;
-    constexpr int KS = W::KSTEPS;
-    constexpr int NSTEP = CK_T / 32;
-    uint32_t koff = l32 * KROW + W::HALF * hf, voff = l32 * CK_VROW + 4 * hf;
-    asm volatile("" : "+v"(koff));
-    asm volatile("" : "+v"(voff));
-    const uint16_t* kbase = &sm.k[0][0] + koff;
-    const uint16_t* vbase = &sm.vt[0][0] + voff;
-    const int64_t part_blk = ((int64_t)bh * p.nch_total + chunk) * p.qblocks;
-    auto tile_q0 = [&](int i) { return (int64_t)(wave + 4 * i) * CK_QT; };
-
-    f32x16 o[2][4];
-    float m[2] = {-INFINITY, -INFINITY}, l[2] = {0.0f, 0.0f};
+// The V center rows of the wave's 32 keys, copied into LDS rows [key][128]
+// (unpadded) by 8 direct-to-LDS loads of 4 rows each.
+__device__ __forceinline__ void dma_v_centers8(uint16_t* vcen, const Chunk8Smem& sm,
+                                               const ChunkCodec& c, int b, int h, int wave,
+                                               int lane) {
+    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs + 8 * (lane & 15);
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-        for (int db = 0; db < 4; ++db) o[qb][db] = f32x16{};
-    f32x16 s0, s1;
-    bf16x8 p0[2], p1[2];
-#pragma unroll
-    for (int ts = 0; ts < 2; ++ts) p0[ts] = p1[ts] = bf16x8{};
-    bf16x8 kb[2][KS], vb[2][2][4];
-    bf16x8 qf[2][KS], qn[2][KS];  // this tile's and the next tile's query fragments
-
-    auto lds_k = [&](int j, int kk) { return lds_b128(kbase + 32 * j * KROW + W::block(kk)); };
-    auto lds_v = [&](int j, int t) {
-        return lds_2x64(vbase + 32 * (t & 3) * CK_VROW + 32 * j + 16 * (t >> 2));
-    };
-    {
-        const int64_t q0 = tile_q0(0);
-        load_q_block<DK>(qf[0], p, b, h, q0, q0, lane);
-        load_q_block<DK>(qf[1], p, b, h, q0 + 32, q0, lane);
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) kb[0][kk] = lds_k(0, kk);
-#pragma unroll
-        for (int t = 0; t < 8; ++t) vb[0][t >> 2][t & 3] = lds_v(0, t);
-        s0 = f32x16{};
-#pragma unroll
-        for (int kk = 0; kk < KS; ++kk) s0 = mfma32(kb[0][kk], qf[0][kk], s0);
+    for (int e = 0; e < 8; ++e) {
+        const int t = 32 * wave + 4 * e + (lane >> 4);
+        __builtin_amdgcn_global_load_lds(cent + (int64_t)sm.ids[1][t] * c.c_rs,
+                                         NKV_LDS(vcen + (32 * wave + 4 * e) * CK_D), 16, 0, 0);
     }
+}
 
-    // One phase.  NQK / NPV: MFMAs of the score / PV product (0 = none); ZPV:
-    // the PV product starts a new O (zero accumulator); FRESH: the softmax
-    // starts a new row state.  ld(t) / ext(t) add slot t's loads / extra work.
-    auto phase = [&](auto nqk_c, auto npv_c, auto zpv_c, auto fresh_c,
-                     const bf16x8 (&kq)[KS], const bf16x8 (&qsrc)[KS], f32x16& s_out,
-                     const bf16x8 (&vv)[2][4], int qv, const bf16x8 (&pin)[2], int qs,
-                     f32x16& s_in, bf16x8 (&pout)[2], float& alpha, auto&& ld,
-                     auto&& ext) -> bool {
-        constexpr int NQK = decltype(nqk_c)::value, NPV = decltype(npv_c)::value;
-        constexpr bool ZPV = decltype(zpv_c)::value, FRESH = decltype(fresh_c)::value;
-        constexpr int BOTH = NQK < NPV ? NQK : NPV;
-        const float mq = FRESH ? -INFINITY : m[qs];
-        float tm = 0.0f, mn = 0.0f, lsum = 0.0f;
-        bool up = false;
-        uint32_t pw[8];
+// The DK K-center values of the wave's 32 keys as coalesced 16-byte pieces:
+// entry e of lane L is piece q = 64*e + L, key 32*wave + q / (DK/8), columns
+// 8 * (q % (DK/8)).
+template <int DK>
+__device__ __forceinline__ void load_k_center_rows8(u32x4 (&v)[DK / 16], const Chunk8Smem& sm,
+                                                    const ChunkCodec& c, int b, int h, int wave,
+                                                    int lane) {
+    constexpr int PR = DK / 8;
+    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs;
 #pragma unroll
-        for (int t = 0; t < 16; ++t) {
-            int kind = -1, idx = 0;  // 0: score step idx, 1: PV step idx
-            if (t < 2 * BOTH) {
-                kind = t & 1;
-                idx = t >> 1;
-            } else if (t - BOTH < NQK && NQK > BOTH) {
-                kind = 0;
-                idx = t - BOTH;
-            } else if (t - BOTH < NPV && NPV > BOTH) {
-                kind = 1;
-                idx = t - BOTH;
-            }
-            if (kind == 0) {
-                s_out = mfma32(kq[idx], qsrc[idx], idx == 0 ? f32x16{} : s_out);
-            } else if (kind == 1) {
-                const int ts = idx >> 2, db = idx & 3;
-                o[qv][db] = mfma32(vv[ts][db], pin[ts], ZPV && ts == 0 ? f32x16{} : o[qv][db]);
-            }
-            // softmax slice t (the max is taken on raw scores: c > 0 preserves order)
-            if (t < 4) {
-                const float a = fmaxf(s_in[4 * t], s_in[4 * t + 1]);
-                const float b2 = fmaxf(s_in[4 * t + 2], s_in[4 * t + 3]);
-                tm = t == 0 ? fmaxf(a, b2) : fmaxf(tm, fmaxf(a, b2));
-            } else if (t == 4) {
-                tm = halfwave_max(tm) * c;
-                up = tm > mq + CK_TAU;
-                mn = up ? tm : mq;
-                alpha = up ? __builtin_amdgcn_exp2f(mq - mn) : 1.0f;
-                m[qs] = mn;
-            } else if (t < 13) {
-                // v_exp_f32 of arguments <= 8; results below 2^-126 flush to 0
-                const int k = t - 5;
-                const float e0 = __builtin_amdgcn_exp2f(fmaf(s_in[2 * k], c, -mn));
-                const float e1 = __builtin_amdgcn_exp2f(fmaf(s_in[2 * k + 1], c, -mn));
-                pw[k] = pack_bf16x2(e0, e1);
-            } else if (t < 15) {
-                // row sum of the bf16 weights the PV product uses
+    for (int e = 0; e < DK / 16; ++e) {
+        const int q = 64 * e + lane;
+        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[0][32 * wave + q / PR] * c.c_rs +
+                                               8 * (q % PR));
+    }
+}
+
+// Decode this wave's 32 keys (32*wave + [0, 32) of the chunk) of codec CODEC
+// to WIDTH columns: V into V^T (permuted columns), K into the K tile.  The
+// decoder-slice ring and code/scale ring are those of decode_codec; each of
+// the eight waves copies WIDTH/64 KB of every slice (for WIDTH = 32 waves
+// 4-7 repeat waves 0-3's pieces: the same bytes to the same place).
+template <int CODEC, bool HAS_C, int WIDTH, int KROW, typename Pre>
+__device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, const ChunkCodec& c,
+                                              const ChunkParams& p, int b, int h, int64_t tok0,
+                                              int valid, int wave, int lane, Pre&& pre) {
+    constexpr int NDT = WIDTH / 32;
+    constexpr int PIECES = WIDTH / 8;                        // 1 KB pieces per slice
+    constexpr int LPW = PIECES >= C8_WAVES ? PIECES / C8_WAVES : 1;
+    constexpr int STAGE = LPW + 2;                           // vm instructions per stage
+    constexpr int SLICE = WIDTH * 64;
+    const int hf = lane >> 5, l32 = lane & 31;
+    const int R = c.r, KQ = R >> 6, G = c.group, NG = R / G;
+    const bool f16 = c.scale_dtype == NKV_DTYPE_FP16;
+    const int tl = 32 * wave + l32;
+    // keys past the chunk end decode key 0's codes (finite, never attended)
+    const int64_t tok = (int64_t)b * p.N + history_row(p, tok0 + (tl < valid ? tl : 0));
+    const uint8_t* prow = c.packed + tok * (R / 2) + 16 * hf;
+    const uint16_t* srow = c.scales + tok * NG;
+    // slice pieces: lane L of piece q brings logical chunk
+    // (L % 8) ^ ((row >> 1) & 7) of row 8 q + L / 8
+    const int piece_row = lane >> 3;
+    const uint16_t* wsrc = c.w + (int64_t)h * c.w_hs + (int64_t)piece_row * R;
+    auto issue_slice = [&](int s) {
+        uint16_t* dst = wst + (s % DS_NBUF) * SLICE;
 #pragma unroll
-                for (int k = 4 * (t - 13); k < 4 * (t - 13) + 4; ++k)
-                    lsum = __builtin_amdgcn_fdot2_f32_bf16(
-                        __builtin_bit_cast(bf16x2, pw[k]),
-                        __builtin_bit_cast(bf16x2, 0x3F803F80u), lsum, false);
-            } else {
-                l[qs] = FRESH ? lsum : l[qs] * alpha + lsum;
-                asm volatile("" : "+v"(l[qs]));
-                pout[0] = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
-                pout[1] = as_bf16x8(u32x4{pw[4], pw[5], pw[6], pw[7]});
-            }
-            ld(t);
-            ext(t);
+        for (int e = 0; e < LPW; ++e) {
+            const int piece = (LPW * wave + e) % PIECES;
+            const int chunk = (lane & 7) ^ ((4 * (piece & 1) + (piece_row >> 1)) & 7);
+            __builtin_amdgcn_global_load_lds(wsrc + (int64_t)8 * piece * R + 64 * s + 8 * chunk,
+                                             NKV_LDS(dst + piece * 512), 16, 0, 0);
+        }
+    };
+    auto issue_codes = [&](int s, u32x4& pk, uint16_t& sb) {
+        pk = *reinterpret_cast<const u32x4*>(prow + 32 * s);
+        sb = srow[(64 * s + 32 * hf) / G];
+    };
+
+    f32x16 acc[NDT];
+#pragma unroll
+    for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16{};
+
+    uint16_t* vcen = &sm.k[0][0];
+    u32x4 kcen[WIDTH / 16];
+    if (CODEC == 0 && HAS_C) load_k_center_rows8<WIDTH>(kcen, sm, c, b, h, wave, lane);
+    u32x4 pk[DS_AHEAD];
+    uint16_t sc[DS_AHEAD];
+#pragma unroll
+    for (int i = 0; i < DS_AHEAD; ++i)
+        if (i < KQ) {
+            issue_slice(i);
+            issue_codes(i, pk[i], sc[i]);
             __builtin_amdgcn_sched_barrier(0);
         }
-        return up;
-    };
-    auto rescale = [&](int qb, float alpha) {
-#pragma unroll
-        for (int db = 0; db < 4; ++db)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) o[qb][db][i] *= alpha;
-    };
-    using I0 = std::integral_constant<int, 0>;
-    using IK = std::integral_constant<int, KS>;
-    using I8 = std::integral_constant<int, 8>;
-    using BT = std::true_type;
-    using BF = std::false_type;
-    auto none = [](int) {};
-    // store work of the previous tile's block qb: its O pieces and (m, l)
-    // over slots 0 .. 8 of a phase
-    auto store_ext = [&](int qb, int64_t q0p, float mp, float lp) {
-        return [&, qb, q0p, mp, lp](int t) {
-            const int64_t blk = part_blk + (q0p >> 5) + qb;
-            if (t < 8) store_partial_piece(p, blk, o[qb], t, lane);
-            if (t == 8) store_partial_ml(p, bh, chunk, q0p + 32 * qb + l32, mp, halfwave_sum(lp));
-        };
-    };
+    pre();
+    constexpr int NVC = CODEC == 1 && HAS_C ? 8 : 0;
+    if (CODEC == 1 && HAS_C) dma_v_centers8(vcen, sm, c, b, h, wave, lane);
+    __builtin_amdgcn_sched_barrier(0);
 
-    for (int i = 0; i < ntiles; ++i) {
-        const int64_t q0 = tile_q0(i);
-        const int64_t q0p = i > 0 ? tile_q0(i - 1) : q0;
-        const int64_t qnx = tile_q0(i + 1);  // rows past Q are clamped to q0
-        float a0 = 1.0f, a1 = 1.0f;
-        // X(0): previous tile's O1 += PV(V_7); store its block 0
-        {
-            const float mp = m[0], lp = l[0];
-            auto ld = [&](int t) { if (t < KS) kb[1][t] = lds_k(1, t); };
-            phase(IK{}, I8{}, BF{}, BT{}, kb[0], qf[1], s1, vb[1], 1, p1, 0, s0, p0, a0, ld,
-                  store_ext(0, q0p, mp, lp));
-        }
-        // Y(0): O0 = PV(V_0) from zero; store the previous tile's block 1
-        {
-            const float mp = m[1], lp = l[1];
-            auto ld = [&](int t) { if (t < 8) vb[1][t >> 2][t & 3] = lds_v(1, t); };
-            phase(IK{}, I8{}, BT{}, BT{}, kb[1], qf[0], s0, vb[0], 0, p0, 1, s1, p1, a1, ld,
-                  store_ext(1, q0p, mp, lp));
-        }
-        // X(1): O1 = PV(V_0) from zero
-        {
-            auto ld = [&](int t) { if (t < KS) kb[0][t] = lds_k(2, t); };
-            const bool up = phase(IK{}, I8{}, BT{}, BF{}, kb[1], qf[1], s1, vb[0], 1, p1, 0, s0,
-                                  p0, a0, ld, none);
-            if (__any(up)) rescale(0, a0);
-        }
-        // Y(1)
-        {
-            auto ld = [&](int t) { if (t < 8) vb[0][t >> 2][t & 3] = lds_v(2, t); };
-            const bool up = phase(IK{}, I8{}, BF{}, BF{}, kb[0], qf[0], s0, vb[1], 0, p0, 1, s1,
-                                  p1, a1, ld, none);
-            if (__any(up)) rescale(1, a1);
-        }
+    int wofs[4];
 #pragma unroll
-        for (int j = 2; j < NSTEP; ++j) {
-            const int cj = j & 1, nj = cj ^ 1;
-            const int jn = (j + 1) % NSTEP;  // next step (the next tile's first after the last)
-            // X(j); the next tile's queries are requested during X(4) / X(5)
-            {
-                auto ld = [&](int t) { if (t < KS) kb[nj][t] = lds_k(jn, t); };
-                auto ext = [&](int t) {
-                    if (j == 4 && t == 0) load_q_block<DK>(qn[0], p, b, h, qnx, q0, lane);
-                    if (j == 5 && t == 0) load_q_block<DK>(qn[1], p, b, h, qnx + 32, q0, lane);
-                };
-                const bool up = phase(IK{}, I8{}, BF{}, BF{}, kb[cj], qf[1], s1, vb[nj], 1, p1,
-                                      0, s0, p0, a0, ld, ext);
-                if (__any(up)) rescale(0, a0);
-            }
-            // Y(j); Y(7) scores the next tile's first step with its block-0 queries
-            {
-                auto ld = [&](int t) { if (t < 8) vb[nj][t >> 2][t & 3] = lds_v(jn, t); };
-                const bool up = phase(IK{}, I8{}, BF{}, BF{}, kb[nj], j + 1 < NSTEP ? qf[0] : qn[0],
-                                      s0, vb[cj], 0, p0, 1, s1, p1, a1, ld, none);
-                if (__any(up)) rescale(1, a1);
-            }
-        }
-        // the next tile's queries become this tile's
+    for (int j = 0; j < 4; ++j) wofs[j] = l32 * 64 + 8 * ((4 * hf + j) ^ ((l32 >> 1) & 7));
+
+    u32x4 zc;
+    float scl = 0.0f, ns7 = 0.0f;
+    if (KQ > 0) {
+        scl = f16 ? f16_bits_to_f32(sc[0]) : bf16_bits_to_f32(sc[0]);
+        ns7 = -7.0f * scl;
+        Unpack8 u;
+        u.split(pk[0][0]);
 #pragma unroll
-        for (int qb = 0; qb < 2; ++qb)
-#pragma unroll
-            for (int kk = 0; kk < KS; ++kk) qf[qb][kk] = qn[qb][kk];
+        for (int e = 0; e < 4; ++e) zc[e] = u.pair(e, scl, ns7);
     }
-    // the last tile: O1 += PV(V_7), then both partials
+    for (int s0 = 0; s0 < KQ; s0 += DS_AHEAD) {
 #pragma unroll
-    for (int ts = 0; ts < 2; ++ts)
+        for (int i = 0; i < DS_AHEAD; ++i) {
+            const int s = s0 + i;
+            if (s >= KQ) break;
+            static_assert(DS_AHEAD == 3, "the wait bounds below assume three stages ahead");
+            const int later = min(KQ - 1 - s, DS_AHEAD - 1);
+            if (s < DS_AHEAD) {
+                if (later >= 2) wait_vmcnt<2 * STAGE + NVC>();
+                else if (later == 1) wait_vmcnt<STAGE + NVC>();
+                else wait_vmcnt<NVC>();
+            } else {
+                if (later >= 2) wait_vmcnt<2 * STAGE>();
+                else if (later == 1) wait_vmcnt<STAGE>();
+                else wait_vmcnt<0>();
+            }
+            __builtin_amdgcn_s_barrier();
+            if (s + DS_AHEAD < KQ) issue_slice(s + DS_AHEAD);
+            __builtin_amdgcn_sched_barrier(0);
+            const uint16_t* wb = wst + (s % DS_NBUF) * SLICE;
+            // sub-step j+1's codes (for the last, the next slice's first) are
+            // unpacked under sub-step j's MFMAs, a pair of codes per slot
+            const int inx = (i + 1) % DS_AHEAD;
+            const float scn = f16 ? f16_bits_to_f32(sc[inx]) : bf16_bits_to_f32(sc[inx]);
+            const float nsn = -7.0f * scn;
+            u32x4 zn;
 #pragma unroll
-        for (int db = 0; db < 4; ++db) o[1][db] = mfma32(vb[1][ts][db], p1[ts], o[1][db]);
-    const int64_t q0l = tile_q0(ntiles - 1);
+            for (int j = 0; j < 4; ++j) {
+                bf16x8 w[NDT];
 #pragma unroll
-    for (int qb = 0; qb < 2; ++qb)
-        store_partial(p, bh, chunk, q0l + 32 * qb, o[qb], m[qb], halfwave_sum(l[qb]), lane);
+                for (int dt = 0; dt < NDT; ++dt) w[dt] = lds_b128(wb + 32 * dt * 64 + wofs[j]);
+                Unpack8 u;
+                u.split(j + 1 < 4 ? pk[i][j + 1] : pk[inx][0]);
+#pragma unroll
+                for (int m = 0; m < NDT; ++m) {
+                    acc[m] = CODEC == 0 ? mfma32(w[m], as_bf16x8(zc), acc[m])
+                                        : mfma32(as_bf16x8(zc), w[m], acc[m]);
+#pragma unroll
+                    for (int q = (4 * m) / NDT; q < (4 * (m + 1)) / NDT; ++q) {
+                        zn[q] = j + 1 < 4 ? u.pair(q, scl, ns7) : u.pair(q, scn, nsn);
+                        if (j + 1 == 4) asm volatile("" : "+v"(zn[q]));
+                    }
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                zc = zn;
+            }
+            scl = scn;
+            ns7 = nsn;
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + DS_AHEAD < KQ) issue_codes(s + DS_AHEAD, pk[i], sc[i]);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    __syncthreads();
+
+    if (CODEC == 0) {
+        // acc[dt] element i: d = 32*dt + 8*(i/4) + 4*hf + i%4, key 32*wave + l32
+        uint16_t* ktile = &sm.k[0][0];
+        const int t = 32 * wave + l32;
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int d = 32 * dt + 8 * g + 4 * hf;
+                float a[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) a[e] = acc[dt][4 * g + e] + sm.bias[0][d + e];
+                const u32x2 r = {pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+                *reinterpret_cast<u32x2*>(ktile + t * KROW + d) = r;
+            }
+        if (HAS_C) {
+            // the wave's own rows: its LDS operations stay in order
+            constexpr int PR = WIDTH / 8;
+#pragma unroll
+            for (int e = 0; e < WIDTH / 16; ++e) {
+                const int q = 64 * e + lane;
+                u32x4* slot = reinterpret_cast<u32x4*>(ktile + (32 * wave + q / PR) * KROW +
+                                                       8 * (q % PR));
+                const u32x4 kv = *slot;
+                u32x4 r;
+#pragma unroll
+                for (int h2 = 0; h2 < 4; ++h2)
+                    r[h2] = pack_bf16x2(
+                        __uint_as_float(kv[h2] << 16) + __uint_as_float(kcen[e][h2] << 16),
+                        __uint_as_float(kv[h2] & 0xffff0000u) +
+                            __uint_as_float(kcen[e][h2] & 0xffff0000u));
+                *slot = r;
+            }
+        }
+    } else {
+        // acc[dt] element i: key 32*wave + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+            const int t0 = 32 * wave + 8 * g + 4 * hf;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) {
+                const int d = 32 * dt + l32;
+                const float bias = sm.bias[1][d];
+                float v[4];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const float a = bf16_round(acc[dt][4 * g + e] + bias);
+                    v[e] = HAS_C ? a + bf16_bits_to_f32(vcen[(t0 + e) * CK_D + d]) : a;
+                }
+                const u32x2 r = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                *reinterpret_cast<u32x2*>(&sm.vt[d][vt_col(t0)]) = r;
+            }
+        }
+    }
+}
+
+// Current (uncompressed) keys of this chunk into the K tile and V^T (DK =
+// 128).  Thread t handles keys 4*(t % 64) .. +4 and d = 16*(t / 64) .. +16:
+// K rows go out as 16-byte stores, V^T as one 8-byte store (four keys) per
+// d.  Keys past `valid` are zero.
+__device__ __forceinline__ void load_current_chunk8(Chunk8Smem& sm, const ChunkParams& p, int b,
+                                                    int h, int64_t tok0, int valid, int t) {
+    const int k0 = 4 * (t & 63), d0 = 16 * (t >> 6);
+    u32x4 kv[4][2], vv[4][2];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const int key = k0 + e;
+        const bool ok = key < valid;
+        const int64_t tok = tok0 + (ok ? key : 0);
+        const uint16_t* ks = p.k_cur + (int64_t)b * p.k_sb + tok * p.k_st + (int64_t)h * p.k_sh + d0;
+        const uint16_t* vs = p.v_cur + (int64_t)b * p.v_sb + tok * p.v_st + (int64_t)h * p.v_sh + d0;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            kv[e][x] = ok ? *reinterpret_cast<const u32x4*>(ks + 8 * x) : u32x4{0, 0, 0, 0};
+            vv[e][x] = ok ? *reinterpret_cast<const u32x4*>(vs + 8 * x) : u32x4{0, 0, 0, 0};
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+            *reinterpret_cast<u32x4*>(&sm.k[k0 + e][d0 + 8 * x]) = kv[e][x];
+    const int col = vt_col(k0);
+#pragma unroll
+    for (int dd = 0; dd < 16; ++dd) {
+        const int x = dd >> 3, w = (dd & 7) >> 1, sh = 16 * (dd & 1);
+        auto val = [&](int e) { return (vv[e][x][w] >> sh) & 0xffffu; };
+        *reinterpret_cast<u32x2*>(&sm.vt[d0 + dd][col]) =
+            u32x2{val(0) | (val(1) << 16), val(2) | (val(3) << 16)};
+    }
+}
+
+// One wave attends its 32-query blocks (wave + 8 i) to the chunk in LDS,
+// key step by key step: S^T = K Q^T (KS MFMAs), online softmax, O^T += V^T
+// P^T (8 MFMAs).  The next step's K and V fragments are read as soon as the
+// current ones have been issued to the matrix core, and the next block's
+// queries are requested during its predecessor.
+template <int DK>
+__device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams& p, int b, int h,
+                                        int bh, int chunk, int wave, int lane_in, int nsub,
+                                        int valid) {
+    int lane = lane_in;
+    asm volatile("" : "+v"(lane));
+    const int hf = lane >> 5, l32 = lane & 31;
+    const float c = p.scale_log2;
+    using W = DWalk<DK>;
+    constexpr int KROW = KTile<DK>::ROW;
+    constexpr int KS = W::KSTEPS;
+    uint32_t koff = l32 * KROW + W::HALF * hf, voff = l32 * C8_VROW + 8 * hf;
+    asm volatile("" : "+v"(koff));
+    asm volatile("" : "+v"(voff));
+    const uint16_t* kbase = &sm.k[0][0] + koff;
+    const uint16_t* vbase = &sm.vt[0][0] + voff;
+    auto lds_k = [&](int j, int kk) { return lds_b128(kbase + 32 * j * KROW + W::block(kk)); };
+    // V^T fragment (ts, db) of step j: rows 32*db + l32, the 8 keys of half-step ts
+    auto lds_v = [&](int j, int t) {
+        return lds_b128(vbase + 32 * (t & 3) * C8_VROW + 32 * j + 16 * (t >> 2));
+    };
+    const int nqb = p.qblocks;
+    if (wave >= nqb) return;
+    bf16x8 qf[KS], qn[KS], kf[KS], vf[8];
+    {
+        const int64_t q0 = (int64_t)wave * 32;
+        load_q_block<DK>(qf, p, b, h, q0, q0, lane);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) kf[kk] = lds_k(0, kk);
+#pragma unroll
+    for (int t = 0; t < 8; ++t) vf[t] = lds_v(0, t);
+    const bool full = valid == CK_T;
+    for (int qb = wave; qb < nqb; qb += C8_WAVES) {
+        const int64_t q0 = (int64_t)qb * 32;
+        // the next block's queries (rows past Q are clamped to q0)
+        load_q_block<DK>(qn, p, b, h, q0 + 32 * C8_WAVES, q0, lane);
+        f32x16 o[4];
+        float m = -INFINITY, l = 0.0f;
+        for (int j = 0; j < nsub; ++j) {
+            f32x16 s = mfma32(kf[0], qf[0], f32x16{});
+#pragma unroll
+            for (int kk = 1; kk < KS; ++kk) s = mfma32(kf[kk], qf[kk], s);
+            // next step's K fragments (the block's first after the last step)
+            const int jn = j + 1 < nsub ? j + 1 : 0;
+#pragma unroll
+            for (int kk = 0; kk < KS; ++kk) kf[kk] = lds_k(jn, kk);
+            if (!full && 32 * j + 32 > valid) {
+                const int vj = valid - 32 * j;
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (8 * (i >> 2) + 4 * hf + (i & 3) >= vj) s[i] = -INFINITY;
+            }
+            // online softmax of the 32-key x 32-query tile
+            float tm = fmaxf(s[0], s[1]);
+#pragma unroll
+            for (int i = 2; i < 16; ++i) tm = fmaxf(tm, s[i]);
+            tm = halfwave_max(tm) * c;
+            const bool up = tm > m + CK_TAU;
+            const float mn = up ? tm : m;
+            const float alpha = up ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+            m = mn;
+            uint32_t pw[8];
+            float lsum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                // v_exp_f32 of arguments <= 8; results below 2^-126 flush to 0
+                pw[k] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(s[2 * k], c, -mn)),
+                                    __builtin_amdgcn_exp2f(fmaf(s[2 * k + 1], c, -mn)));
+                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[k]),
+                                                       __builtin_bit_cast(bf16x2, 0x3F803F80u),
+                                                       lsum, false);
+            }
+            l = j == 0 ? lsum : l * alpha + lsum;
+            const bf16x8 p0 = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
+            const bf16x8 p1 = as_bf16x8(u32x4{pw[4], pw[5], pw[6], pw[7]});
+            if (j == 0) {
+#pragma unroll
+                for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[db], p0, f32x16{});
+            } else {
+                if (__any(up)) {
+#pragma unroll
+                    for (int db = 0; db < 4; ++db)
+#pragma unroll
+                        for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+                }
+#pragma unroll
+                for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[db], p0, o[db]);
+            }
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[4 + db], p1, o[db]);
+#pragma unroll
+            for (int t = 0; t < 8; ++t) vf[t] = lds_v(jn, t);
+        }
+        store_partial(p, bh, chunk, q0, o, m, halfwave_sum(l), lane);
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) qf[kk] = qn[kk];
+    }
 }
 
 template <int DK>
-__global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
+__global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
     constexpr int KROW = KTile<DK>::ROW;
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    ChunkSmem& sm = *reinterpret_cast<ChunkSmem*>(smem_raw);
+    Chunk8Smem& sm = *reinterpret_cast<Chunk8Smem*>(smem_raw);
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-
-    // block -> (bh, chunk) with bh fastest: with B*H a multiple of 8 all
-    // chunks of one head run on one XCD (blocks go to the 8 XCDs
-    // round-robin), sharing that head's decoder rows, centers and queries in
-    // one L2.  History chunks come first; the cheaper current-chunk blocks
-    // fill the tail.
     const int BH = p.B * p.H;
     const int bh = blockIdx.x % BH;
     const int chunk = blockIdx.x / BH;
@@ -1060,102 +593,65 @@ __global__ void __launch_bounds__(CK_THREADS, 1) chunk_kernel(ChunkParams p) {
     const int valid = (int)min((int64_t)CK_T, (hist ? p.n_rows : p.Nc) - tok0);
 
     if (hist) {
-        // The chunk's center ids and this head's biases are loaded and
-        // published to LDS once V's first decode stages are in flight, so
-        // that the latencies of both overlap.
         auto publish = [&]() {
+            if (t < CK_T) {
 #pragma unroll
-            for (int cc = 0; cc < 2; ++cc) {
-                const ChunkCodec& cd = p.codec[cc];
-                int id = 0;
-                if (cd.centers && t < valid) {
-                    // ids outside the table are clamped so that a corrupt
-                    // payload cannot read out of bounds (valid payloads never
-                    // hold them)
-                    const int64_t key = tok0 + t;
-                    id = read_id(cd.ids, cd.id_bytes, (int64_t)b * p.N + history_row(p, key));
-                    id = min(max(id, 0), cd.num_centers - 1);
+                for (int cc = 0; cc < 2; ++cc) {
+                    const ChunkCodec& cd = p.codec[cc];
+                    int id = 0;
+                    if (cd.centers && t < valid) {
+                        // ids outside the table are clamped so that a corrupt
+                        // payload cannot read out of bounds
+                        id = read_id(cd.ids, cd.id_bytes,
+                                     (int64_t)b * p.N + history_row(p, tok0 + t));
+                        id = min(max(id, 0), cd.num_centers - 1);
+                    }
+                    sm.ids[cc][t] = id;
+                    if (t < (cc == 0 ? DK : CK_D))
+                        sm.bias[cc][t] =
+                            cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
                 }
-                sm.ids[cc][t] = id;
-                const int width = cc == 0 ? DK : CK_D;
-                if (t < width)
-                    sm.bias[cc][t] =
-                        cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
             }
             __syncthreads();
         };
         auto nothing = []() {};
-        // V first: its decoder slices are staged in the (not yet written)
-        // V^T region and its centers in the K region; then K, with its
-        // slices staged in the K region once V's epilogue is done.
         uint16_t* vt_scratch = &sm.vt[0][0];
         uint16_t* k_scratch = &sm.k[0][0];
         if (p.codec[1].centers)
-            decode_codec<1, true, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
-                                              wave, lane, publish);
-        else
-            decode_codec<1, false, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
+            decode_codec8<1, true, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
                                                wave, lane, publish);
+        else
+            decode_codec8<1, false, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
+                                                wave, lane, publish);
         __syncthreads();
         if (p.codec[0].centers)
-            decode_codec<0, true, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid, wave,
-                                            lane, nothing);
-        else
-            decode_codec<0, false, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
+            decode_codec8<0, true, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
                                              wave, lane, nothing);
+        else
+            decode_codec8<0, false, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
+                                              wave, lane, nothing);
     } else if (DK == CK_D) {
-        load_current_chunk(sm, p, b, h, tok0, valid, t);
+        load_current_chunk8(sm, p, b, h, tok0, valid, t);
     }
     __syncthreads();
-
-    const int nsub = (valid + 31) / 32;
-    const int nqt = (int)cdiv(p.Q, CK_QT);
-    constexpr int WAVES = CK_THREADS / 64;
-    if (valid == CK_T) {
-        // full chunk: the wave's two-block tiles (wave + 4 i, those with
-        // q0 + 32 < Q: a prefix of its tiles) as one pipeline, then at most
-        // one single-block tile
-        const int t2 = p.Q > 32 ? (int)((p.Q + 31) / CK_QT) : 0;
-        const int n2 = t2 > wave ? (t2 - wave + WAVES - 1) / WAVES : 0;
-        if (n2 > 0) attend_stream<DK>(sm, p, b, h, bh, chunk, wave, lane, n2);
-        const int qt = wave + WAVES * n2;
-        if (qt < nqt) {
-            const int64_t q0 = (int64_t)qt * CK_QT;
-            bf16x8 qf[2][8];
-            load_q_block<DK>(qf[0], p, b, h, q0, q0, lane);
-            attend_qtile<DK, 1, true>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q0);
-        }
-        return;
-    }
-    bf16x8 qf[2][8];
-    if (wave < nqt) {
-        load_q_block<DK>(qf[0], p, b, h, (int64_t)wave * CK_QT, (int64_t)wave * CK_QT, lane);
-        load_q_block<DK>(qf[1], p, b, h, (int64_t)wave * CK_QT + 32, (int64_t)wave * CK_QT, lane);
-    }
-    for (int qt = wave; qt < nqt; qt += WAVES) {
-        const int64_t q0 = (int64_t)qt * CK_QT;
-        // the wave's next tile, or this one again (a harmless in-bounds reload)
-        const int64_t q_next = qt + WAVES < nqt ? q0 + WAVES * CK_QT : q0;
-        if (q0 + 32 >= p.Q)
-            attend_qtile<DK, 1, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
-        else
-            attend_qtile<DK, 2, false>(sm, p, b, h, bh, chunk, q0, nsub, valid, lane, qf, q_next);
-    }
+    attend8<DK>(sm, p, b, h, bh, chunk, wave, lane, (valid + 31) / 32, valid);
 }
 
-// Merge the chunk partials of every (b, h, q).  A 256-thread block owns one
-// 32-query block; its four waves take every fourth chunk, each lane reading
-// the lane-order payload the attention wave stored, and sum through LDS.
+// Merge the chunk partials of every (b, h, q).  One wave owns one 32-query
+// block and walks all its chunks, each lane reading the lane-order payload
+// the attention wave stored (1 KB per load instruction, four chunks in
+// flight); no cross-wave reduction, so blocks need no LDS and fill the GPU
+// in one round.
 // out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c (O_c unnormalised); no chunks give
 // out = 0 and lse = -inf (CN/core.py:48-49).
-constexpr int CB_WAVES = 4;
+constexpr int CB_WAVES = 4;  // query blocks per 256-thread block
 __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParams p) {
-    __shared__ float red[CB_WAVES - 1][64][65];  // [wave-1][element][lane] (+1 pad)
-    __shared__ float redl[CB_WAVES - 1][64];
     const int lane = threadIdx.x & 63, hf = lane >> 5, l32 = lane & 31;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t bh = blockIdx.x / p.qblocks;
-    const int qblk = (int)(blockIdx.x % p.qblocks);
+    const int64_t gq = (int64_t)blockIdx.x * CB_WAVES + wave;
+    if (gq >= (int64_t)p.B * p.H * p.qblocks) return;
+    const int64_t bh = gq / p.qblocks;
+    const int qblk = (int)(gq % p.qblocks);
     const int64_t qi = (int64_t)qblk * 32 + l32;
     const int NC = p.nch_total;
     const int64_t lse_stride = (int64_t)p.qblocks * 32;
@@ -1175,40 +671,42 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
 #pragma unroll
     for (int e = 1; e < 8; ++e) M = fmaxf(M, mx[e]);
     const float Mu = M == -INFINITY ? 0.0f : M;
-    // out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c (O_c unnormalised)
     float L = 0.0f, acc[64];
 #pragma unroll
     for (int e = 0; e < 64; ++e) acc[e] = 0.0f;
     const uint16_t* src = p.part_o + (bh * NC * p.qblocks + qblk) * 4096 + lane * 8;
     const int64_t cstride = (int64_t)p.qblocks * 4096;
-#pragma unroll 2
-    for (int cc = wave; cc < NC; cc += CB_WAVES) {
-        const u32x2 mlc = ml[cc * lse_stride];
-        const float wt = exp2f(__uint_as_float(mlc[0]) - Mu);
-        L += wt * __uint_as_float(mlc[1]);
+    // a ring of CB_AHEAD chunks in flight (prefetches past the last chunk
+    // reload it and are never used)
+    constexpr int CB_AHEAD = 4;
+    u32x4 buf[CB_AHEAD][8];
+    u32x2 mlb[CB_AHEAD];
+    auto issue = [&](int cc, int i) {
+        cc = min(cc, NC - 1);
+        mlb[i] = ml[cc * lse_stride];
 #pragma unroll
-        for (int st = 0; st < 8; ++st) {
-            const u32x4 v = *reinterpret_cast<const u32x4*>(src + cc * cstride + 512 * st);
+        for (int st = 0; st < 8; ++st)
+            buf[i][st] = *reinterpret_cast<const u32x4*>(src + cc * cstride + 512 * st);
+    };
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                acc[8 * st + 2 * e] += wt * __uint_as_float(v[e] << 16);
-                acc[8 * st + 2 * e + 1] += wt * __uint_as_float(v[e] & 0xffff0000u);
-            }
+    for (int i = 0; i < CB_AHEAD; ++i) issue(i, i);
+    for (int cc0 = 0; cc0 < NC; cc0 += CB_AHEAD) {
+#pragma unroll
+        for (int i = 0; i < CB_AHEAD; ++i) {
+            if (cc0 + i >= NC) break;
+            const float wt = exp2f(__uint_as_float(mlb[i][0]) - Mu);
+            L += wt * __uint_as_float(mlb[i][1]);
+#pragma unroll
+            for (int st = 0; st < 8; ++st)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    acc[8 * st + 2 * e] += wt * __uint_as_float(buf[i][st][e] << 16);
+                    acc[8 * st + 2 * e + 1] += wt * __uint_as_float(buf[i][st][e] & 0xffff0000u);
+                }
+            issue(cc0 + i + CB_AHEAD, i);
         }
     }
-    if (wave > 0) {
-#pragma unroll
-        for (int e = 0; e < 64; ++e) red[wave - 1][e][lane] = acc[e];
-        redl[wave - 1][lane] = L;
-    }
-    __syncthreads();
-    if (wave > 0 || qi >= p.Q) return;
-#pragma unroll
-    for (int w = 0; w < CB_WAVES - 1; ++w) {
-#pragma unroll
-        for (int e = 0; e < 64; ++e) acc[e] += red[w][e][lane];
-        L += redl[w][lane];
-    }
+    if (qi >= p.Q) return;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
     const int b = (int)(bh / p.H), h = (int)(bh % p.H);
     uint16_t* orow = p.out + b * p.o_sb + qi * p.o_st + h * p.o_sh + 4 * hf;
@@ -1273,15 +771,15 @@ int check_chunk_codec(const ChunkCodec& c) {
 
 template <int DK>
 void launch_dk(const ChunkParams& p, int64_t blocks, hipStream_t s, int* rc) {
-    const size_t smem = sizeof(ChunkSmem);
-    hipError_t e = hipFuncSetAttribute((const void*)chunk_kernel<DK>,
+    const size_t smem = sizeof(Chunk8Smem);
+    hipError_t e = hipFuncSetAttribute((const void*)chunk8_kernel<DK>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) {
         set_error(std::string("chunk_launch: hipFuncSetAttribute failed: ") + hipGetErrorString(e));
         *rc = NKV_ERR_HIP;
         return;
     }
-    chunk_kernel<DK><<<dim3((unsigned)blocks), CK_THREADS, smem, s>>>(p);
+    chunk8_kernel<DK><<<dim3((unsigned)blocks), C8_THREADS, smem, s>>>(p);
     e = hipGetLastError();
     if (e != hipSuccess) {
         set_error(std::string("chunk_launch: launch failed: ") + hipGetErrorString(e));
@@ -1363,7 +861,8 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     if (d.ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_end, s));
     const int64_t qblocks_total = (int64_t)d.B * d.H * p.qblocks;
     if (qblocks_total > 0) {
-        chunk_combine_kernel<<<dim3((unsigned)qblocks_total), 64 * CB_WAVES, 0, s>>>(p);
+        chunk_combine_kernel<<<dim3((unsigned)cdiv(qblocks_total, CB_WAVES)), 64 * CB_WAVES, 0,
+                               s>>>(p);
         NKV_LAUNCH_CHECK();
     }
     return NKV_OK;

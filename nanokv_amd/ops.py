@@ -383,22 +383,10 @@ class ReaderTensors:
         return g
 
 
-def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
-                key: Codec, value: Codec, protect_rows: torch.Tensor, low_rows: torch.Tensor,
-                groups: list, *, softmax_scale: Optional[float] = None,
-                return_lse: bool = True, out: Optional[torch.Tensor] = None,
-                kernel_events: Optional[tuple[int, int]] = None,
-                workspace: Optional[torch.Tensor] = None):
-    """NanoKV-Fast mixed-dimensional attention (see nkv_fast_attend).
-
-    protect_rows / low_rows: int32 codec rows of the native and low
-    partitions; groups: ReaderTensors covering every head once.  Returns
-    (out [B, Q, H, D] bf16, lse [B, H, Q] fp32 or None).
-    """
+def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, softmax_scale, out,
+               return_lse):
     args, out, lse, device = _attend_args(q, k_cur, v_cur, key, value, softmax_scale, out,
                                           return_lse)
-    if kernel_events is not None:
-        args.ev_kernel_begin, args.ev_kernel_end = kernel_events
     _require_gpu(protect_rows, low_rows, *[g.heads for g in groups])
     _contig(protect_rows, torch.int32, "protect_rows")
     _contig(low_rows, torch.int32, "low_rows")
@@ -416,6 +404,37 @@ def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[
     err = lib().nkv_last_error().decode()
     if need == 0 and err:
         raise _lib.NanoKVError("nkv_fast_attend_workspace_size", _lib.NKV_ERR_INVALID, err)
+    # structs must stay alive while f points at them
+    return f, structs, need, out, lse, device
+
+
+def fast_attend_workspace_size(q: torch.Tensor, k_cur: Optional[torch.Tensor],
+                               v_cur: Optional[torch.Tensor], key: Codec, value: Codec,
+                               protect_rows: torch.Tensor, low_rows: torch.Tensor,
+                               groups: list) -> int:
+    """Workspace bytes nkv_fast_attend needs for this problem."""
+    return int(_fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, None,
+                          None, False)[2])
+
+
+def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
+                key: Codec, value: Codec, protect_rows: torch.Tensor, low_rows: torch.Tensor,
+                groups: list, *, softmax_scale: Optional[float] = None,
+                return_lse: bool = True, out: Optional[torch.Tensor] = None,
+                kernel_events: Optional[tuple[int, int]] = None,
+                workspace: Optional[torch.Tensor] = None):
+    """NanoKV-Fast mixed-dimensional attention (see nkv_fast_attend).
+
+    protect_rows / low_rows: int32 codec rows of the native and low
+    partitions; groups: ReaderTensors covering every head once.  Returns
+    (out [B, Q, H, D] bf16, lse [B, H, Q] fp32 or None).  kernel_events
+    bracket the native partition's attention kernel.
+    """
+    f, structs, need, out, lse, device = _fast_args(q, k_cur, v_cur, key, value, protect_rows,
+                                                    low_rows, groups, softmax_scale, out,
+                                                    return_lse)
+    if kernel_events is not None:
+        f.attend.ev_kernel_begin, f.attend.ev_kernel_end = kernel_events
     if workspace is None or workspace.numel() < need:
         workspace = torch.empty(max(need, 1), device=device, dtype=torch.uint8)
     check("nkv_fast_attend", lib().nkv_fast_attend(_stream(device), byref(f), _ptr(workspace),

@@ -49,6 +49,26 @@ class Shape:
         return {"attention_history": att_hist, "attention_current": att_cur, "decode": dec,
                 "total": att_hist + att_cur + dec}
 
+    def fast_flops(self, n_protect: int, full_heads=None, d: int = None) -> dict:
+        """Algorithmic flops of a NanoKV-Fast call: the native partition (the
+        n_protect protected rows and the current keys, every head, full
+        width), the low partition (identity-reader heads at full width, the
+        other heads with K/Q width d and V width D), the full decode of the
+        protected rows (all heads) and of the low rows of identity heads, and
+        the reader reads of the low rows for the other heads."""
+        full_heads = FAST_FULL_HEADS if full_heads is None else full_heads
+        d = FAST_READER_D if d is None else d
+        nf, nr = len(full_heads), self.H - len(full_heads)
+        low = self.N - n_protect
+        att_native = 4.0 * self.B * self.Q * (n_protect + self.Nc) * self.HD
+        att_low = (4.0 * self.B * self.Q * low * self.D * nf
+                   + 2.0 * self.B * self.Q * low * (d + self.D) * nr)
+        dec_full = (2.0 * self.B * n_protect * (self.rK + self.rV) * self.HD
+                    + 2.0 * self.B * low * (self.rK + self.rV) * self.D * nf)
+        reads = 2.0 * self.B * low * (self.rK * d + self.rV * self.D) * nr
+        return {"attention_native": att_native, "attention_low": att_low, "decode_full": dec_full,
+                "reader_reads": reads, "total": att_native + att_low + dec_full + reads}
+
     def coeff_stream_bytes(self) -> float:
         """Unique bytes of the compressed history read by one call: packed codes,
         group scales and center ids of K and V."""
