@@ -517,9 +517,14 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
         f32x16 o[4];
         float m = -INFINITY, l = 0.0f;
         for (int j = 0; j < nsub; ++j) {
+            // wave priority is raised around each MFMA cluster: the two waves
+            // of a SIMD then settle into alternation, one issuing MFMAs while
+            // the other runs its softmax
+            __builtin_amdgcn_s_setprio(1);
             f32x16 s = mfma32(kf[0], qf[0], f32x16{});
 #pragma unroll
             for (int kk = 1; kk < KS; ++kk) s = mfma32(kf[kk], qf[kk], s);
+            __builtin_amdgcn_s_setprio(0);
             // next step's K fragments (the block's first after the last step)
             const int jn = j + 1 < nsub ? j + 1 : 0;
 #pragma unroll
@@ -553,6 +558,7 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
             l = j == 0 ? lsum : l * alpha + lsum;
             const bf16x8 p0 = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
             const bf16x8 p1 = as_bf16x8(u32x4{pw[4], pw[5], pw[6], pw[7]});
+            __builtin_amdgcn_s_setprio(1);
             if (j == 0) {
 #pragma unroll
                 for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[db], p0, f32x16{});
@@ -568,6 +574,7 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
             }
 #pragma unroll
             for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[4 + db], p1, o[db]);
+            __builtin_amdgcn_s_setprio(0);
 #pragma unroll
             for (int t = 0; t < 8; ++t) vf[t] = lds_v(jn, t);
         }
