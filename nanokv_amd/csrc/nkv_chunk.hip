@@ -663,22 +663,10 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
     const int NC = p.nch_total;
     const int64_t lse_stride = (int64_t)p.qblocks * 32;
     const u32x2* ml = reinterpret_cast<const u32x2*>(p.part_ml) + bh * NC * lse_stride + qi;
-    // the largest running max; eight independent maxima keep eight loads in flight
-    float mx[8];
-#pragma unroll
-    for (int e = 0; e < 8; ++e) mx[e] = -INFINITY;
-    int cc0 = 0;
-    for (; cc0 + 8 <= NC; cc0 += 8) {
-#pragma unroll
-        for (int e = 0; e < 8; ++e)
-            mx[e] = fmaxf(mx[e], __uint_as_float(ml[(cc0 + e) * lse_stride][0]));
-    }
-    for (; cc0 < NC; ++cc0) mx[0] = fmaxf(mx[0], __uint_as_float(ml[cc0 * lse_stride][0]));
-    float M = mx[0];
-#pragma unroll
-    for (int e = 1; e < 8; ++e) M = fmaxf(M, mx[e]);
-    const float Mu = M == -INFINITY ? 0.0f : M;
-    float L = 0.0f, acc[64];
+    // online merge: M is the largest chunk max seen so far; a chunk whose max
+    // exceeds it rescales the running sums (per lane), so no separate pass
+    // over the maxima delays the first partial loads
+    float M = -INFINITY, L = 0.0f, acc[64];
 #pragma unroll
     for (int e = 0; e < 64; ++e) acc[e] = 0.0f;
     const uint16_t* src = p.part_o + (bh * NC * p.qblocks + qblk) * 4096 + lane * 8;
@@ -701,7 +689,17 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
 #pragma unroll
         for (int i = 0; i < CB_AHEAD; ++i) {
             if (cc0 + i >= NC) break;
-            const float wt = exp2f(__uint_as_float(mlb[i][0]) - Mu);
+            const float mc = __uint_as_float(mlb[i][0]);
+            // a chunk with no valid key for this query has m = -inf and O = 0
+            const bool up = mc > M;
+            if (__any(up)) {
+                const float f = up ? exp2f(M - mc) : 1.0f;  // M = -inf gives 0
+                L *= f;
+#pragma unroll
+                for (int e = 0; e < 64; ++e) acc[e] *= f;
+            }
+            M = up ? mc : M;
+            const float wt = mc == -INFINITY ? 0.0f : exp2f(mc - M);
             L += wt * __uint_as_float(mlb[i][1]);
 #pragma unroll
             for (int st = 0; st < 8; ++st)
