@@ -194,6 +194,120 @@ __global__ void __launch_bounds__(256) assign_kernel(const float* __restrict__ x
     }
 }
 
+// fp64 MFMA nearest-center search (v_mfma_f64_16x16x4_f64).  A 256-thread
+// block owns 16 rows; wave w takes centers 64*w + [0, 64) of every group of
+// 256 as four 16 x 16 output tiles.  Operands come straight from L2: at each
+// 16-wide k block lane l supplies x row (l % 16) and center column (l % 16)
+// at k = k0 + 4*(l / 16) + [0, 4), one 16-byte x piece and one 8-byte
+// center piece per tile for four MFMA steps (any k order is valid for the
+// reduction, and A and B use the same one).  Every product of an fp32 x and
+// a bf16 center is exact in fp64, so only the order of the fp64 sums differs
+// from the fp64 VALU search (relative 1e-16).  ||c||^2 comes from the same
+// center pieces.  Output layout: lane l, element e holds row 4e + l/16,
+// column l % 16.  Needs HD % 16 == 0, x 16-byte and centers 8-byte aligned.
+constexpr int AM_ROWS = 16;
+typedef double f64x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ bool better(double d, int c, double bd, int bc) {
+    return bc < 0 || (c >= 0 && (d < bd || (d == bd && c < bc)));
+}
+
+template <int ID_BYTES>
+__global__ void __launch_bounds__(256) assign_mfma_kernel(const float* __restrict__ x,
+                                                          const uint16_t* __restrict__ centers,
+                                                          int64_t rows, int C, int HD,
+                                                          void* __restrict__ ids) {
+    __shared__ double red_d[4][AM_ROWS];
+    __shared__ int red_c[4][AM_ROWS];
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, col = lane & 15;
+    const int64_t row0 = (int64_t)blockIdx.x * AM_ROWS;
+    const int64_t xr = min(row0 + col, rows - 1);  // rows past the end read the last row
+    const float* xp = x + xr * HD + 4 * g;
+    double bd[4];
+    int bc[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) { bd[e] = 0.0; bc[e] = -1; }
+
+    for (int cg = 0; cg < C; cg += 256) {
+        const uint16_t* cp[4];
+        int cid[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            cid[t] = cg + 64 * wave + 16 * t + col;
+            cp[t] = centers + (int64_t)min(cid[t], C - 1) * HD + 4 * g;
+        }
+        f64x4 acc[4];
+        double cc[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) { acc[t] = f64x4{0.0, 0.0, 0.0, 0.0}; cc[t] = 0.0; }
+        u32x4 xa = *reinterpret_cast<const u32x4*>(xp);
+        u32x2 cb[4];
+#pragma unroll
+        for (int t = 0; t < 4; ++t) cb[t] = *reinterpret_cast<const u32x2*>(cp[t]);
+        for (int k0 = 0; k0 < HD; k0 += 16) {
+            // next k block's operands (the last block reloads itself)
+            const int kn = k0 + 16 < HD ? k0 + 16 : k0;
+            const u32x4 xn = *reinterpret_cast<const u32x4*>(xp + kn);
+            u32x2 cn[4];
+#pragma unroll
+            for (int t = 0; t < 4; ++t) cn[t] = *reinterpret_cast<const u32x2*>(cp[t] + kn);
+#pragma unroll
+            for (int st = 0; st < 4; ++st) {
+                const double a = (double)__uint_as_float(xa[st]);
+#pragma unroll
+                for (int t = 0; t < 4; ++t) {
+                    const uint32_t w = cb[t][st >> 1];
+                    const double b = (double)__uint_as_float((st & 1) ? (w & 0xffff0000u) : (w << 16));
+                    acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[t], 0, 0, 0);
+                    cc[t] = fma(b, b, cc[t]);
+                }
+            }
+            xa = xn;
+#pragma unroll
+            for (int t = 0; t < 4; ++t) cb[t] = cn[t];
+        }
+#pragma unroll
+        for (int t = 0; t < 4; ++t) {
+            // ||c||^2 over the four k subsets of this column
+            cc[t] += __shfl_xor(cc[t], 16);
+            cc[t] += __shfl_xor(cc[t], 32);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const double d = cc[t] - 2.0 * acc[t][e];
+                const int c = cid[t] < C ? cid[t] : -1;
+                if (better(d, c, bd[e], bc[e])) { bd[e] = d; bc[e] = c; }
+            }
+        }
+    }
+    // lanes of one row group (same g) hold rows 4e + g: reduce over columns
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int off = 1; off < 16; off <<= 1) {
+            const double od = __shfl_xor(bd[e], off);
+            const int oc = __shfl_xor(bc[e], off);
+            if (better(od, oc, bd[e], bc[e])) { bd[e] = od; bc[e] = oc; }
+        }
+    if (col == 0) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            red_d[wave][4 * e + g] = bd[e];
+            red_c[wave][4 * e + g] = bc[e];
+        }
+    }
+    __syncthreads();
+    if (threadIdx.x < AM_ROWS) {
+        const int r = threadIdx.x;
+        double d = red_d[0][r];
+        int c = red_c[0][r];
+        for (int w = 1; w < 4; ++w)
+            if (better(red_d[w][r], red_c[w][r], d, c)) { d = red_d[w][r]; c = red_c[w][r]; }
+        const int64_t gr = row0 + r;
+        if (gr < rows) store_id<ID_BYTES>(ids, gr, c);
+    }
+}
+
 // ============================================================ MFMA GEMM core
 // C[M, N] = A[M, K] * B[N, K]^T on v_mfma_f32_32x32x16_bf16.  A 256-thread
 // block computes a 64 x 64 tile: wave w owns the 32 x 32 sub-tile
@@ -446,6 +560,19 @@ extern "C" int nkv_unpack(void* stream, const uint8_t* packed, const uint16_t* s
 
 static int launch_assign(hipStream_t s, const float* x, const uint16_t* centers, int64_t rows,
                          int C, int HD, void* ids, int id_bytes) {
+    if (rows <= 0) return NKV_OK;
+    if (HD > 0 && HD % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(centers) % 8 == 0) {
+        dim3 grid((unsigned)cdiv(rows, AM_ROWS));
+        if (id_bytes == 1)
+            assign_mfma_kernel<1><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
+        else if (id_bytes == 2)
+            assign_mfma_kernel<2><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
+        else
+            assign_mfma_kernel<4><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
+        NKV_LAUNCH_CHECK();
+        return NKV_OK;
+    }
     dim3 grid((unsigned)cdiv(rows, AS_ROWS));
     if (id_bytes == 1)
         assign_kernel<1><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
