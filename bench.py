@@ -15,7 +15,9 @@ Prints ONE JSON line:
   cpu_baseline  the CPU oracle's decode-then-attend (fp32 numpy/BLAS) on a
                 bounded head sample of the same workload, scaled to TFLOP/s
 
-Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2]
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4]
+(config 4 prints its own line: rollout step latency and peak HBM, compressed
+versus uncompressed KV)
 """
 from __future__ import annotations
 
@@ -40,8 +42,11 @@ def parse():
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
-    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3),
-                    help="1: headline config; 2: long history; 3: NanoKV-Fast on the config-1 shape")
+    ap.add_argument("--config", type=int, default=1, choices=(1, 2, 3, 4),
+                    help="1: headline config; 2: long history; 3: NanoKV-Fast on the config-1 "
+                         "shape; 4: 30-layer rollout step, compressed vs uncompressed KV")
+    ap.add_argument("--no-sdpa", action="store_true",
+                    help="config 4: skip the torch flash-attention comparator")
     ap.add_argument("--splits", type=int, default=0,
                     help="query_tiles key splits (0 = automatic)")
     ap.add_argument("--schedule", default="auto", choices=("auto", "query_tiles", "key_chunks"),
@@ -119,6 +124,211 @@ def cpu_baseline(shape, layer, codecs, q, kc, vc, budget_s: float) -> dict:
                        f"{shape.H}/{heads_done} heads; ms_per_layer={full_s * 1e3:.1f}")}
 
 
+ROLLOUT_LAYERS, ROLLOUT_FRAMES, ROLLOUT_CHUNK = 30, 16, 1560
+
+
+def rollout(args, device) -> dict:
+    """one rollout step of a 30-layer random-init attention
+    stack (H=24, D=128, bf16) with 16 frames of 1,560 tokens of history per
+    layer.  Per layer: QKV projection of the chunk's hidden state, attention
+    of the chunk's queries over the history and the chunk itself, output
+    projection with a residual, and the commit of the chunk's K and V to the
+    layer's cache.  Compressed: history in the INT4 codec (config-1 codec:
+    r=384, group-32 fp16 scales, 256 centers), fused nkv_attend, commit =
+    nkv_encode of the chunk into a ring slot.  Uncompressed: bf16 K/V ring of
+    17 frames (history plus the chunk), nkv_attend over uncompressed keys, and
+    (unless --no-sdpa) torch's flash attention over the same ring."""
+    import torch
+    from nanokv_amd import ops, synth
+    sh = synth.CONFIGS[1]
+    L, F, T, H, D = ROLLOUT_LAYERS, ROLLOUT_FRAMES, ROLLOUT_CHUNK, sh.H, sh.D
+    HD, N = H * D, F * T
+    bf16 = torch.bfloat16
+    g = torch.Generator(device=device).manual_seed(4)
+    torch.cuda.reset_peak_memory_stats()
+    # projection weights, shared by both KV modes
+    w_qkv = [(torch.randn(3 * HD, HD, generator=g, device=device) / HD ** 0.5).to(bf16)
+             for _ in range(L)]
+    w_o = [(torch.randn(HD, HD, generator=g, device=device) / HD ** 0.5).to(bf16)
+           for _ in range(L)]
+    h0 = torch.randn(T, HD, generator=g, device=device).to(bf16)
+    torch.cuda.synchronize()
+    base_bytes = torch.cuda.memory_allocated()
+
+    def time_steps(step, n_warm, n_steps):
+        for i in range(n_warm):
+            step(i)
+        torch.cuda.synchronize()
+        torch.cuda.reset_peak_memory_stats()
+        t0 = time.perf_counter()
+        for i in range(n_steps):
+            step(n_warm + i)
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / n_steps, torch.cuda.max_memory_allocated()
+
+    def breakdown(step_parts):
+        """ms of each part over one step, from events around every call."""
+        torch.cuda.synchronize()
+        acc = {}
+        marks = step_parts()
+        torch.cuda.synchronize()
+        for name, b, e in marks:
+            acc[name] = acc.get(name, 0.0) + b.elapsed_time(e)
+        return {k: round(v, 3) for k, v in acc.items()}
+
+    def ev():
+        e = torch.cuda.Event(enable_timing=True)
+        e.record()
+        return e
+
+    # ---------------------------------------------------------------- compressed
+    comp = []
+    for li in range(L):
+        lay = synth.make_layer(sh, seed=100 + li, device=device)
+        rings = []
+        for kind, cent, enc, dec in (("k", lay.centers_k, lay.w_enc_k, lay.w_dec_k),
+                                     ("v", lay.centers_v, lay.w_enc_v, lay.w_dec_v)):
+            rows = synth.history_rows(sh, cent, N, seed=1000 + 2 * li + (kind == "v"),
+                                      device=device)
+            e = ops.encode(rows, enc, centers=cent, group=sh.G, scale_dtype=sh.scale_dtype)
+            del rows
+            codec = ops.Codec(packed=e["packed"][None], scales=e["scales"][None], w_dec=dec,
+                              group=sh.G, ids=e["ids"][None], centers=cent[None])
+            rings.append((e, enc, cent, codec))
+        comp.append(rings)
+    coeff = torch.empty(T, sh.rK, device=device, dtype=torch.float32)
+    obuf = torch.empty(1, T, H, D, device=device, dtype=bf16)
+    q0 = h0.view(1, T, H, D)
+    ws = torch.empty(max(ops.attend_workspace_size(q0, N, T, comp[0][0][3], comp[0][1][3]), 1),
+                     device=device, dtype=torch.uint8)
+    torch.cuda.synchronize()
+    comp_cache = sum(t.numel() * t.element_size()
+                     for rings in comp for (e, enc, cent, codec) in rings
+                     for t in (e["packed"], e["scales"], e["ids"], codec.w_dec, cent))
+
+    def comp_layer(li, h, slot, marks=None):
+        qkv = h @ w_qkv[li].T
+        q, k, v = (qkv[:, i * HD:(i + 1) * HD].view(1, T, H, D) for i in range(3))
+        rk, rv = comp[li]
+        b = ev() if marks is not None else None
+        ops.attend(q, k, v, rk[3], rv[3], out=obuf, return_lse=False, workspace=ws)
+        if marks is not None:
+            marks.append(("attend", b, ev()))
+            b = ev()
+        sl = slice(slot * T, (slot + 1) * T)
+        for (e, enc, cent, codec), x in ((rk, k), (rv, v)):
+            ops.encode(x.reshape(T, HD).float(), enc, centers=cent, group=sh.G,
+                       scale_dtype=sh.scale_dtype,
+                       out={"packed": e["packed"][sl], "scales": e["scales"][sl],
+                            "ids": e["ids"][sl], "coeff": coeff})
+        if marks is not None:
+            marks.append(("encode", b, ev()))
+        return h + obuf.view(T, HD) @ w_o[li].T
+
+    def comp_step(i):
+        h = h0
+        for li in range(L):
+            h = comp_layer(li, h, i % F)
+        return h
+
+    def comp_parts():
+        marks, h = [], h0
+        b = ev()
+        for li in range(L):
+            h = comp_layer(li, h, 0, marks)
+        marks.append(("step", b, ev()))
+        return marks
+
+    c_ms, c_peak = time_steps(comp_step, args.warmup, args.steps)
+    c_parts = breakdown(comp_parts)
+    del comp, ws
+    torch.cuda.empty_cache()
+
+    # -------------------------------------------------------------- uncompressed
+    S = F + 1
+    kc = [torch.randn(S * T, HD, generator=g, device=device).to(bf16) for _ in range(L)]
+    vc = [torch.randn(S * T, HD, generator=g, device=device).to(bf16) for _ in range(L)]
+    qd = h0.view(1, T, H, D)
+    ws2 = torch.empty(max(ops.attend_workspace_size(qd, 0, S * T, None, None), 1),
+                      device=device, dtype=torch.uint8)
+    torch.cuda.synchronize()
+    raw_cache = sum(t.numel() * t.element_size() for t in kc + vc)
+    use_sdpa = [False]
+
+    def raw_layer(li, h, slot, marks=None):
+        qkv = h @ w_qkv[li].T
+        q, k, v = (qkv[:, i * HD:(i + 1) * HD] for i in range(3))
+        sl = slice(slot * T, (slot + 1) * T)
+        kc[li][sl].copy_(k)
+        vc[li][sl].copy_(v)
+        b = ev() if marks is not None else None
+        if use_sdpa[0]:
+            from torch.nn.attention import SDPBackend, sdpa_kernel
+            with sdpa_kernel([SDPBackend.FLASH_ATTENTION]):
+                o = torch.nn.functional.scaled_dot_product_attention(
+                    q.view(1, T, H, D).transpose(1, 2), kc[li].view(1, S * T, H, D).transpose(1, 2),
+                    vc[li].view(1, S * T, H, D).transpose(1, 2))
+            obuf.copy_(o.transpose(1, 2))
+        else:
+            ops.attend(q.view(1, T, H, D), kc[li].view(1, S * T, H, D),
+                       vc[li].view(1, S * T, H, D), None, None, out=obuf, return_lse=False,
+                       workspace=ws2)
+        if marks is not None:
+            marks.append(("attend", b, ev()))
+        return h + obuf.view(T, HD) @ w_o[li].T
+
+    def raw_step(i):
+        h = h0
+        for li in range(L):
+            h = raw_layer(li, h, i % S)
+        return h
+
+    def raw_parts():
+        marks, h = [], h0
+        b = ev()
+        for li in range(L):
+            h = raw_layer(li, h, 0, marks)
+        marks.append(("step", b, ev()))
+        return marks
+
+    r_ms, r_peak = time_steps(raw_step, args.warmup, args.steps)
+    r_parts = breakdown(raw_parts)
+    sdpa = None
+    if not args.no_sdpa:
+        use_sdpa[0] = True
+        try:
+            s_ms, s_peak = time_steps(raw_step, args.warmup, args.steps)
+            sdpa = {"ms_per_step": round(s_ms, 3), "peak_hbm_GB": round(s_peak / 1e9, 3),
+                    "parts_ms": breakdown(raw_parts)}
+        except RuntimeError as exc:   # flash attention unavailable: no fallback path
+            sdpa = {"unavailable": str(exc).splitlines()[0][:200]}
+        use_sdpa[0] = False
+    return {
+        "metric": "rollout step latency (30-layer attention stack, INT4 codec KV)",
+        "value": round(c_ms, 3),
+        "unit": "ms/step",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(c_ms, 3),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic (random-init projections and codec operators, structured history)",
+        "config": {"workload": "cfg4_rollout_30l_h24_d128_16x1560", "config_index": 4,
+                   "layers": L, "history_frames": F, "chunk_tokens": T, "H": H, "D": D,
+                   "rank": sh.rK, "scale_group": sh.G, "centers": sh.C,
+                   "parallelism": "single-gpu"},
+        "compressed": {"ms_per_step": round(c_ms, 3), "peak_hbm_GB": round(c_peak / 1e9, 3),
+                       "kv_cache_GB": round(comp_cache / 1e9, 4), "parts_ms": c_parts},
+        "uncompressed_nkv": {"ms_per_step": round(r_ms, 3), "peak_hbm_GB": round(r_peak / 1e9, 3),
+                             "kv_cache_GB": round(raw_cache / 1e9, 4), "parts_ms": r_parts},
+        "uncompressed_torch_flash": sdpa,
+        "projection_weights_GB": round(base_bytes / 1e9, 3),
+    }
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -130,6 +340,9 @@ def main():
     import torch
     from nanokv_amd import ops, synth
     device = torch.device("cuda:0")
+    if args.config == 4:
+        print(json.dumps(rollout(args, device)), flush=True)
+        return
     shape = synth.CONFIGS[args.config]
     layer, codecs, q, kc, vc = build_inputs(shape, device)
     out = torch.empty_like(q)

@@ -205,7 +205,7 @@ __global__ void __launch_bounds__(256) assign_kernel(const float* __restrict__ x
 // from the fp64 VALU search (relative 1e-16).  ||c||^2 comes from the same
 // center pieces.  Output layout: lane l, element e holds row 4e + l/16,
 // column l % 16.  Needs HD % 16 == 0, x 16-byte and centers 8-byte aligned.
-constexpr int AM_ROWS = 16;
+constexpr int AM_ROWS = 16, AM_AHEAD = 4;
 typedef double f64x4 __attribute__((ext_vector_type(4)));
 
 __device__ __forceinline__ bool better(double d, int c, double bd, int bc) {
@@ -241,31 +241,42 @@ __global__ void __launch_bounds__(256) assign_mfma_kernel(const float* __restric
         double cc[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) { acc[t] = f64x4{0.0, 0.0, 0.0, 0.0}; cc[t] = 0.0; }
-        u32x4 xa = *reinterpret_cast<const u32x4*>(xp);
-        u32x2 cb[4];
+        // a ring of AM_AHEAD k blocks of operands in flight (one k block =
+        // 16 k: four MFMA steps per tile); block kb lives in slot kb % AM_AHEAD
+        const int NB = HD / 16;
+        u32x4 xa[AM_AHEAD];
+        u32x2 cb[AM_AHEAD][4];
+        auto issue = [&](int kb, int slot) {
+            xa[slot] = *reinterpret_cast<const u32x4*>(xp + 16 * kb);
 #pragma unroll
-        for (int t = 0; t < 4; ++t) cb[t] = *reinterpret_cast<const u32x2*>(cp[t]);
-        for (int k0 = 0; k0 < HD; k0 += 16) {
-            // next k block's operands (the last block reloads itself)
-            const int kn = k0 + 16 < HD ? k0 + 16 : k0;
-            const u32x4 xn = *reinterpret_cast<const u32x4*>(xp + kn);
-            u32x2 cn[4];
+            for (int t = 0; t < 4; ++t) cb[slot][t] = *reinterpret_cast<const u32x2*>(cp[t] + 16 * kb);
+        };
 #pragma unroll
-            for (int t = 0; t < 4; ++t) cn[t] = *reinterpret_cast<const u32x2*>(cp[t] + kn);
+        for (int i = 0; i < AM_AHEAD; ++i)
+            if (i < NB) issue(i, i);
+        for (int kb0 = 0; kb0 < NB; kb0 += AM_AHEAD) {
 #pragma unroll
-            for (int st = 0; st < 4; ++st) {
-                const double a = (double)__uint_as_float(xa[st]);
+            for (int i = 0; i < AM_AHEAD; ++i) {
+                const int kb = kb0 + i;
+                if (kb >= NB) break;
+                const u32x4 xv = xa[i];
+                u32x2 cv[4];
 #pragma unroll
-                for (int t = 0; t < 4; ++t) {
-                    const uint32_t w = cb[t][st >> 1];
-                    const double b = (double)__uint_as_float((st & 1) ? (w & 0xffff0000u) : (w << 16));
-                    acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[t], 0, 0, 0);
-                    cc[t] = fma(b, b, cc[t]);
+                for (int t = 0; t < 4; ++t) cv[t] = cb[i][t];
+                if (kb + AM_AHEAD < NB) issue(kb + AM_AHEAD, i);
+#pragma unroll
+                for (int st = 0; st < 4; ++st) {
+                    const double a = (double)__uint_as_float(xv[st]);
+#pragma unroll
+                    for (int t = 0; t < 4; ++t) {
+                        const uint32_t w = cv[t][st >> 1];
+                        const double b =
+                            (double)__uint_as_float((st & 1) ? (w & 0xffff0000u) : (w << 16));
+                        acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[t], 0, 0, 0);
+                        cc[t] = fma(b, b, cc[t]);
+                    }
                 }
             }
-            xa = xn;
-#pragma unroll
-            for (int t = 0; t < 4; ++t) cb[t] = cn[t];
         }
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -456,6 +467,113 @@ __global__ void __launch_bounds__(256) encode_gemm_kernel(EncodeA al,
     }
 }
 
+// Encoder projection coeff[M, r] = bf16(x - center[id] - mean) W_enc^T, fp32
+// accumulation.  The chain of dependent k steps, not the MFMA work, bounds a
+// projection of a few thousand rows (each step waits on L2/HBM), so a block
+// owns 32 rows x 96 coefficient columns (three 32-wide tiles) and its four
+// waves split K in quarters: every wave builds its own residual A fragments
+// in registers (x and the center row from L2, the mean from LDS) and reads
+// its W_enc fragments, one 64-wide k step ahead of the MFMAs, with no block
+// barrier in the loop.  The four partial sums are added through LDS in wave
+// order (deterministic).  Needs HD % 256 == 0 and HD <= EP_MAXK.
+constexpr int EP_ROWS = 32, EP_TILES = 3, EP_SPLIT = 4, EP_MAXK = 8192;
+
+__global__ void __launch_bounds__(256) encode_proj_kernel(EncodeA al,
+                                                          const uint16_t* __restrict__ w_enc,
+                                                          int r, float* __restrict__ coeff) {
+    __shared__ float mean_s[EP_MAXK];
+    __shared__ float part[EP_SPLIT - 1][EP_TILES][16][64];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int hf = lane >> 5, l32 = lane & 31;
+    const int64_t m0 = (int64_t)blockIdx.x * EP_ROWS;
+    const int n0 = blockIdx.y * (EP_TILES * 32);
+    const int K = al.K, KW = K / EP_SPLIT, kbeg = wave * KW;
+    if (al.mean) {
+        for (int k = t; k < K; k += 256) mean_s[k] = al.mean[k];
+        __syncthreads();
+    }
+    const int64_t m = m0 + l32;
+    const bool row_ok = m < al.M;
+    const float* xrow = al.x + (row_ok ? m : 0) * (int64_t)K + kbeg + 8 * hf;
+    const uint16_t* crow =
+        al.centers ? al.centers + (int64_t)(row_ok ? al.id_of(m) : 0) * K + kbeg + 8 * hf : nullptr;
+    const uint16_t* wrow[EP_TILES];
+#pragma unroll
+    for (int j = 0; j < EP_TILES; ++j)
+        wrow[j] = w_enc + (int64_t)min(n0 + 32 * j + l32, r - 1) * K + kbeg + 8 * hf;
+    // raw operands of one 64-wide k step: four 16-wide MFMA sub-steps
+    struct Raw {
+        f32x4 x[4][2];
+        u32x4 c[4];
+        u32x4 w[EP_TILES][4];
+    };
+    auto fetch = [&](int k0, Raw& rw) {
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+            rw.x[sub][0] = *reinterpret_cast<const f32x4*>(xrow + k0 + 16 * sub);
+            rw.x[sub][1] = *reinterpret_cast<const f32x4*>(xrow + k0 + 16 * sub + 4);
+            if (crow) rw.c[sub] = *reinterpret_cast<const u32x4*>(crow + k0 + 16 * sub);
+#pragma unroll
+            for (int j = 0; j < EP_TILES; ++j)
+                rw.w[j][sub] = *reinterpret_cast<const u32x4*>(wrow[j] + k0 + 16 * sub);
+        }
+    };
+    f32x16 acc[EP_TILES];
+#pragma unroll
+    for (int j = 0; j < EP_TILES; ++j) acc[j] = f32x16{};
+    Raw cur, nxt;
+    fetch(0, cur);
+    for (int k0 = 0; k0 < KW; k0 += 64) {
+        if (k0 + 64 < KW) fetch(k0 + 64, nxt);
+#pragma unroll
+        for (int sub = 0; sub < 4; ++sub) {
+            float v[8] = {cur.x[sub][0][0], cur.x[sub][0][1], cur.x[sub][0][2], cur.x[sub][0][3],
+                          cur.x[sub][1][0], cur.x[sub][1][1], cur.x[sub][1][2], cur.x[sub][1][3]};
+            if (crow) {
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    v[2 * e] = v[2 * e] - __uint_as_float(cur.c[sub][e] << 16);
+                    v[2 * e + 1] = v[2 * e + 1] - __uint_as_float(cur.c[sub][e] & 0xffff0000u);
+                }
+            }
+            if (al.mean) {
+                const int kk = kbeg + k0 + 16 * sub + 8 * hf;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) v[e] = v[e] - mean_s[kk + e];
+            }
+            u32x4 a;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) a[e] = row_ok ? pack_bf16x2(v[2 * e], v[2 * e + 1]) : 0u;
+#pragma unroll
+            for (int j = 0; j < EP_TILES; ++j)
+                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(cur.w[j][sub]),
+                                                                 acc[j], 0, 0, 0);
+        }
+        if (k0 + 64 < KW) cur = nxt;
+    }
+    // sum the K quarters in wave order
+    if (wave > 0) {
+#pragma unroll
+        for (int j = 0; j < EP_TILES; ++j)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) part[wave - 1][j][i][lane] = acc[j][i];
+    }
+    __syncthreads();
+    if (wave > 0) return;
+#pragma unroll
+    for (int j = 0; j < EP_TILES; ++j) {
+        const int n = n0 + 32 * j + l32;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            float sum = acc[j][i];
+#pragma unroll
+            for (int w = 0; w < EP_SPLIT - 1; ++w) sum += part[w][j][i][lane];
+            const int64_t mm = m0 + 8 * (i / 4) + 4 * hf + (i % 4);
+            if (n < r && mm < al.M) coeff[mm * r + n] = sum;
+        }
+    }
+}
+
 struct DecodeEpi {
     const uint16_t* centers;   // [C, HD] for this batch item, or NULL
     const void* ids;           // [N] of this batch item
@@ -636,8 +754,13 @@ extern "C" int nkv_encode(void* stream, const nkv_encode_args* a) {
     al.mean = a->mean;
     al.M = a->rows;
     al.K = a->HD;
-    dim3 grid((unsigned)cdiv(a->rows, GT_M), (unsigned)cdiv(a->r, GT_N));
-    encode_gemm_kernel<<<grid, 256, 0, s>>>(al, a->w_enc, a->r, a->coeff);
+    if (a->HD % (EP_SPLIT * 64) == 0 && a->HD <= EP_MAXK) {
+        dim3 grid((unsigned)cdiv(a->rows, EP_ROWS), (unsigned)cdiv(a->r, EP_TILES * 32));
+        encode_proj_kernel<<<grid, 256, 0, s>>>(al, a->w_enc, a->r, a->coeff);
+    } else {
+        dim3 grid((unsigned)cdiv(a->rows, GT_M), (unsigned)cdiv(a->r, GT_N));
+        encode_gemm_kernel<<<grid, 256, 0, s>>>(al, a->w_enc, a->r, a->coeff);
+    }
     NKV_LAUNCH_CHECK();
     return nkv_quant_pack(stream, a->coeff, a->rows, a->r, a->group, a->scale_dtype,
                           a->quant_mode, a->packed, a->scales);

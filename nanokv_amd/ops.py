@@ -136,8 +136,12 @@ def assign(x: torch.Tensor, centers: torch.Tensor,
 def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tensor] = None,
            mean: Optional[torch.Tensor] = None, group: int = 32,
            scale_dtype: torch.dtype = torch.bfloat16, quant_mode: str = "fp32",
-           id_dtype: Optional[torch.dtype] = None) -> dict:
-    """Encode fp32 rows [rows, HD] with given centers (see nkv_encode)."""
+           id_dtype: Optional[torch.dtype] = None, out: Optional[dict] = None) -> dict:
+    """Encode fp32 rows [rows, HD] with given centers (see nkv_encode).
+
+    out: optional preallocated outputs {"packed", "scales", "ids", "coeff"}
+    (contiguous, shaped like the returned ones; "ids" only with centers), so
+    that a chunk can be encoded straight into a slot of a larger cache."""
     device = _require_gpu(x, w_enc, centers, mean)
     _contig(x, torch.float32, "x")
     _contig(w_enc, torch.bfloat16, "w_enc")
@@ -150,20 +154,31 @@ def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tens
     args.rows, args.HD, args.r, args.group = rows, hd, r, group
     args.scale_dtype = _SCALE_CODES[scale_dtype]
     args.quant_mode = _QUANT_CODES[quant_mode]
+    lead = tuple(x.shape[:-1])
+
+    def _out(name, shape, dtype):
+        if out is None or out.get(name) is None:
+            return torch.empty(shape, device=device, dtype=dtype)
+        t = out[name]
+        _contig(t, dtype, f"out[{name!r}]")
+        if t.numel() != math.prod(shape) or t.device != device:
+            raise ValueError(f"out[{name!r}] must hold {tuple(shape)} on {device}")
+        return t
+
     ids = None
     if centers is not None:
         _contig(centers, torch.bfloat16, "centers")
         C = int(centers.shape[0])
         id_dtype = id_dtype or id_dtype_for(C)
-        ids = torch.empty(x.shape[:-1], device=device, dtype=id_dtype)
+        ids = _out("ids", lead, id_dtype)
         args.num_centers, args.id_bytes = C, _ID_BYTES[id_dtype]
         args.centers, args.ids = centers.data_ptr(), ids.data_ptr()
     if mean is not None:
         _contig(mean, torch.float32, "mean")
         args.mean = mean.data_ptr()
-    coeff = torch.empty((*x.shape[:-1], r), device=device, dtype=torch.float32)
-    packed = torch.empty((*x.shape[:-1], r // 2), device=device, dtype=torch.uint8)
-    scales = torch.empty((*x.shape[:-1], r // group), device=device, dtype=scale_dtype)
+    coeff = _out("coeff", (*lead, r), torch.float32)
+    packed = _out("packed", (*lead, r // 2), torch.uint8)
+    scales = _out("scales", (*lead, r // group), scale_dtype)
     args.x, args.w_enc = x.data_ptr(), w_enc.data_ptr()
     args.coeff, args.packed, args.scales = coeff.data_ptr(), packed.data_ptr(), scales.data_ptr()
     check("nkv_encode", lib().nkv_encode(_stream(device), byref(args)))
