@@ -47,6 +47,7 @@ namespace nkv {
 #endif
 
 constexpr int CK_T = 256;        // keys per chunk
+constexpr int CK_CUR_SPLITS = 3; // most blocks per current-key chunk (query shares)
 constexpr int CK_D = 128;        // head dim
 constexpr int CK_KROW = CK_D + 8;   // K row: 68 dwords (b128 reads conflict-free)
 constexpr float CK_TAU = 8.0f;   // lazy-rescale threshold (log2 units)
@@ -61,6 +62,7 @@ struct ChunkParams {
     int B, H;           // H: heads of this launch (launch head i)
     int nch_hist, nch_total;
     int qblocks;        // 32-query blocks per (b, i): cdiv(Q, 32)
+    int cur_splits;     // blocks per current-key chunk, each attending a share of the query blocks
     int64_t Q;
     int64_t N;          // history tokens per batch item in the codec arrays
     int64_t n_rows;     // history keys attended
@@ -480,7 +482,7 @@ __device__ __forceinline__ void load_current_chunk8(Chunk8Smem& sm, const ChunkP
 template <int DK>
 __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams& p, int b, int h,
                                         int bh, int chunk, int wave, int lane_in, int nsub,
-                                        int valid) {
+                                        int valid, int qb_lo, int qb_hi) {
     int lane = lane_in;
     asm volatile("" : "+v"(lane));
     const int hf = lane >> 5, l32 = lane & 31;
@@ -498,11 +500,10 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
     auto lds_v = [&](int j, int t) {
         return lds_b128(vbase + 32 * (t & 3) * C8_VROW + 32 * j + 16 * (t >> 2));
     };
-    const int nqb = p.qblocks;
-    if (wave >= nqb) return;
+    if (qb_lo + wave >= qb_hi) return;
     bf16x8 qf[KS], qn[KS], kf[KS], vf[8];
     {
-        const int64_t q0 = (int64_t)wave * 32;
+        const int64_t q0 = (int64_t)(qb_lo + wave) * 32;
         load_q_block<DK>(qf, p, b, h, q0, q0, lane);
     }
 #pragma unroll
@@ -510,7 +511,7 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
 #pragma unroll
     for (int t = 0; t < 8; ++t) vf[t] = lds_v(0, t);
     const bool full = valid == CK_T;
-    for (int qb = wave; qb < nqb; qb += C8_WAVES) {
+    for (int qb = qb_lo + wave; qb < qb_hi; qb += C8_WAVES) {
         const int64_t q0 = (int64_t)qb * 32;
         // the next block's queries (rows past Q are clamped to q0)
         load_q_block<DK>(qn, p, b, h, q0 + 32 * C8_WAVES, q0, lane);
@@ -591,9 +592,24 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
     Chunk8Smem& sm = *reinterpret_cast<Chunk8Smem*>(smem_raw);
     const int t = threadIdx.x, lane = t & 63;
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    // history chunks first, (batch, head) fastest; then every current-key
+    // chunk as cur_splits blocks over consecutive shares of the query blocks
+    // (smaller work items where the grid drains)
     const int BH = p.B * p.H;
-    const int bh = blockIdx.x % BH;
-    const int chunk = blockIdx.x / BH;
+    const int64_t nh = (int64_t)p.nch_hist * BH;
+    int bh, chunk, qb_lo = 0, qb_hi = p.qblocks;
+    if ((int64_t)blockIdx.x < nh) {
+        bh = blockIdx.x % BH;
+        chunk = blockIdx.x / BH;
+    } else {
+        const int c = (int)(blockIdx.x - nh), ncur = p.nch_total - p.nch_hist;
+        bh = c % BH;
+        const int rest = c / BH;
+        chunk = p.nch_hist + rest % ncur;
+        const int qs = rest / ncur;
+        qb_lo = (int)((int64_t)qs * p.qblocks / p.cur_splits);
+        qb_hi = (int)((int64_t)(qs + 1) * p.qblocks / p.cur_splits);
+    }
     const int b = bh / p.H, h = bh % p.H;
     const bool hist = chunk < p.nch_hist;
     const int64_t tok0 = (int64_t)(hist ? chunk : chunk - p.nch_hist) * CK_T;
@@ -641,7 +657,7 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
         load_current_chunk8(sm, p, b, h, tok0, valid, t);
     }
     __syncthreads();
-    attend8<DK>(sm, p, b, h, bh, chunk, wave, lane, (valid + 31) / 32, valid);
+    attend8<DK>(sm, p, b, h, bh, chunk, wave, lane, (valid + 31) / 32, valid, qb_lo, qb_hi);
 }
 
 // Merge the chunk partials of every (b, h, q).  One wave owns one 32-query
@@ -824,6 +840,10 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.nch_hist = (int)chunk_count(d.n_rows);
     p.nch_total = p.nch_hist + (int)chunk_count(d.Nc);
     p.qblocks = (int)cdiv(d.Q, 32);
+    // current-key chunks carry no decode: split their query blocks so that
+    // the work items at the end of the grid are short (at least 16 query
+    // blocks, two waves' worth, per split)
+    p.cur_splits = (int)std::max<int64_t>(1, std::min<int64_t>(CK_CUR_SPLITS, p.qblocks / 16));
     p.Q = d.Q;
     p.N = d.N;
     p.n_rows = d.n_rows;
@@ -854,7 +874,8 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.o_sh = d.o_sh;
     p.lse = d.lse;
 
-    const int64_t blocks = (int64_t)d.B * d.H * p.nch_total;
+    const int64_t blocks = (int64_t)d.B * d.H *
+                           (p.nch_hist + (int64_t)(p.nch_total - p.nch_hist) * p.cur_splits);
     if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
     if (blocks > 0) {
         int rc = NKV_OK;
