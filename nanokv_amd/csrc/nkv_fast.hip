@@ -65,19 +65,85 @@ __global__ void __launch_bounds__(256) project_kernel(const void* x, int64_t x_b
     else reinterpret_cast<uint16_t*>(out)[o] = f32_to_bf16_bits(acc);
 }
 
+// The same projection on MFMA for a non-identity w (D <= 128, E in {32, 64,
+// 128}): a block owns 128 rows m of one (b, i) and all E columns; w[i] is
+// staged transposed in LDS ([e][d], 16-byte operand reads) and each wave
+// computes 32 rows x E with v_mfma_f32_32x32x16_bf16.  The bf16 rounding of
+// the inputs and of the fp32 sum is that of project_kernel; only the order
+// of the fp32 sum differs.
+constexpr int PJ_ROWS = 128, PJ_MAXE = 128, PJ_MAXD = 128, PJ_PAD = 8;
+
+template <bool X_F32, bool OUT_F32>
+__global__ void __launch_bounds__(256) project_mfma_kernel(const void* x, int64_t x_b, int64_t x_m,
+                                                           int64_t x_h, const int32_t* heads, int H,
+                                                           const uint16_t* w, int D, int E,
+                                                           int64_t M, void* out, int64_t o_b,
+                                                           int64_t o_i, int64_t o_m) {
+    __shared__ __align__(16) uint16_t wt[PJ_MAXE][PJ_MAXD + PJ_PAD];
+    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+    const int hf = lane >> 5, l32 = lane & 31;
+    const int i = blockIdx.y, b = blockIdx.z;
+    const uint16_t* wi = w + (int64_t)i * D * E;
+    for (int idx = t; idx < D * E; idx += 256) wt[idx % E][idx / E] = wi[idx];
+    __syncthreads();
+    const int64_t m = (int64_t)blockIdx.x * PJ_ROWS + 32 * wave + l32;
+    const int64_t ml = m < M ? m : M - 1;  // rows past the end read the last row (not stored)
+    const int64_t base = (int64_t)b * x_b + ml * x_m + (int64_t)min(max(heads[i], 0), H - 1) * x_h;
+    const int ntile = E / 32;
+    f32x16 acc[PJ_MAXE / 32];
+#pragma unroll
+    for (int tt = 0; tt < PJ_MAXE / 32; ++tt) acc[tt] = f32x16{};
+    for (int k0 = 0; k0 < D; k0 += 16) {
+        u32x4 a;
+        if (X_F32) {
+            const float* xp = reinterpret_cast<const float*>(x) + base + k0 + 8 * hf;
+            const f32x4 x0 = *reinterpret_cast<const f32x4*>(xp);
+            const f32x4 x1 = *reinterpret_cast<const f32x4*>(xp + 4);
+            a = u32x4{pack_bf16x2(x0[0], x0[1]), pack_bf16x2(x0[2], x0[3]),
+                      pack_bf16x2(x1[0], x1[1]), pack_bf16x2(x1[2], x1[3])};
+        } else {
+            a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(x) + base + k0 +
+                                                8 * hf);
+        }
+#pragma unroll
+        for (int tt = 0; tt < PJ_MAXE / 32; ++tt)
+            if (tt < ntile)
+                acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(
+                    as_bf16x8(a), *reinterpret_cast<const bf16x8*>(&wt[32 * tt + l32][k0 + 8 * hf]),
+                    acc[tt], 0, 0, 0);
+    }
+#pragma unroll
+    for (int tt = 0; tt < PJ_MAXE / 32; ++tt) {
+        if (tt >= ntile) continue;
+        const int e = 32 * tt + l32;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            const int64_t mr = (int64_t)blockIdx.x * PJ_ROWS + 32 * wave + 8 * (r / 4) + 4 * hf + (r % 4);
+            if (mr >= M) continue;
+            const int64_t o = (int64_t)b * o_b + (int64_t)i * o_i + mr * o_m + e;
+            if (OUT_F32) reinterpret_cast<float*>(out)[o] = bf16_round(acc[tt][r]);
+            else reinterpret_cast<uint16_t*>(out)[o] = f32_to_bf16_bits(acc[tt][r]);
+        }
+    }
+}
+
 // Merge of each group head's native and low partitions, in place in out
 // (CN/core.py:33-42): lse = logaddexp(la, lb); origin = lse if finite else
 // 0; out = a e^(la - origin) + b e^(lb - origin) in fp32, rounded to bf16.
-// One thread per (b, q, i) row of D values.
+// Sixteen threads per (b, q, i) row of D = 128 values, 8 values (16 bytes)
+// each.
 __global__ void __launch_bounds__(256) group_merge_kernel(
     int B, int64_t Q, int nh, int D, const int32_t* heads, uint16_t* out, int64_t o_sb,
     int64_t o_st, int64_t o_sh, const float* lse_n, int H, const uint16_t* low, const float* lse_l,
     float* lse_out) {
+    const int per_row = D / 8;
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (tid >= (int64_t)B * Q * nh) return;
-    const int i = (int)(tid % nh);
-    const int64_t q = (tid / nh) % Q;
-    const int b = (int)(tid / ((int64_t)nh * Q));
+    if (tid >= (int64_t)B * Q * nh * per_row) return;
+    const int part = (int)(tid % per_row);
+    const int64_t row = tid / per_row;
+    const int i = (int)(row % nh);
+    const int64_t q = (row / nh) % Q;
+    const int b = (int)(row / ((int64_t)nh * Q));
     const int h = min(max(heads[i], 0), H - 1);
     const float x = lse_n[((int64_t)b * H + h) * Q + q];
     const float y = lse_l[((int64_t)b * nh + i) * Q + q];
@@ -85,11 +151,17 @@ __global__ void __launch_bounds__(256) group_merge_kernel(
     const float l = x == y ? x + 0.69314718055994531f : fmaxf(x, y) + log1pf(expf(-fabsf(x - y)));
     const float origin = isfinite(l) ? l : 0.0f;
     const float wa = expf(x - origin), wb = expf(y - origin);
-    uint16_t* orow = out + (int64_t)b * o_sb + q * o_st + (int64_t)h * o_sh;
-    const uint16_t* lrow = low + (((int64_t)b * Q + q) * nh + i) * D;
-    for (int d = 0; d < D; ++d)
-        orow[d] = f32_to_bf16_bits(bf16_bits_to_f32(orow[d]) * wa + bf16_bits_to_f32(lrow[d]) * wb);
-    if (lse_out) lse_out[((int64_t)b * H + h) * Q + q] = l;
+    u32x4* op = reinterpret_cast<u32x4*>(out + (int64_t)b * o_sb + q * o_st + (int64_t)h * o_sh + 8 * part);
+    const u32x4 lv = *reinterpret_cast<const u32x4*>(low + (((int64_t)b * Q + q) * nh + i) * D + 8 * part);
+    const u32x4 ov = *op;
+    u32x4 r;
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+        r[e] = pack_bf16x2(__uint_as_float(ov[e] << 16) * wa + __uint_as_float(lv[e] << 16) * wb,
+                           __uint_as_float(ov[e] & 0xffff0000u) * wa +
+                               __uint_as_float(lv[e] & 0xffff0000u) * wb);
+    *op = r;
+    if (lse_out && part == 0) lse_out[((int64_t)b * H + h) * Q + q] = l;
 }
 
 namespace {
@@ -119,6 +191,10 @@ int validate(const nkv_fast_args* f) {
     NKV_REQUIRE(f->num_groups >= 0 && (f->num_groups == 0 || f->groups), NKV_ERR_INVALID,
                 "groups missing");
     if (a.Q > 0) NKV_REQUIRE(a.q && a.out, NKV_ERR_INVALID, "q and out required");
+    if (a.Q > 0)
+        NKV_REQUIRE(reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && a.o_sb % 8 == 0 &&
+                        a.o_st % 8 == 0 && a.o_sh % 8 == 0,
+                    NKV_ERR_INVALID, "out must be 16-byte aligned with strides divisible by 8");
     if (a.Nc > 0) NKV_REQUIRE(a.k_cur && a.v_cur, NKV_ERR_INVALID, "current K/V missing");
     if (f->n_low > 0 || f->n_protect > 0)
         NKV_REQUIRE(a.key.packed && a.value.packed, NKV_ERR_INVALID, "history codecs missing");
@@ -272,8 +348,18 @@ int project(hipStream_t s, const void* x, int64_t x_b, int64_t x_m, int64_t x_h,
             int64_t M, void* out, int64_t o_b, int64_t o_i, int64_t o_m) {
     const int64_t total = (int64_t)nb * nh * M * E;
     if (total == 0) return NKV_OK;
-    project_kernel<XF, OF><<<dim3((unsigned)cdiv(total, 256)), 256, 0, s>>>(
-        x, x_b, x_m, x_h, heads, H, w, D, E, nb, nh, M, out, o_b, o_i, o_m);
+    // 16-byte operand loads need aligned rows (8 bf16 or 4 fp32 elements)
+    const int64_t el = XF ? 4 : 8;
+    const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && x_b % el == 0 &&
+                         x_m % el == 0 && x_h % el == 0;
+    if (w && aligned && D <= PJ_MAXD && D % 16 == 0 && E % 32 == 0 && E <= PJ_MAXE) {
+        project_mfma_kernel<XF, OF><<<dim3((unsigned)cdiv(M, PJ_ROWS), (unsigned)nh, (unsigned)nb),
+                                      256, 0, s>>>(x, x_b, x_m, x_h, heads, H, w, D, E, M, out, o_b,
+                                                   o_i, o_m);
+    } else {
+        project_kernel<XF, OF><<<dim3((unsigned)cdiv(total, 256)), 256, 0, s>>>(
+            x, x_b, x_m, x_h, heads, H, w, D, E, nb, nh, M, out, o_b, o_i, o_m);
+    }
     NKV_LAUNCH_CHECK();
     return NKV_OK;
 }
@@ -345,8 +431,8 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
         }
         rc = chunk_launch(s, low_desc(f, g, ws, L), ws + L.partials, part_bytes);
         if (rc) return rc;
-        const int64_t rows = (int64_t)a.B * a.Q * nh;
-        group_merge_kernel<<<dim3((unsigned)cdiv(rows, 256)), 256, 0, s>>>(
+        const int64_t threads = (int64_t)a.B * a.Q * nh * (D / 8);
+        group_merge_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(
             a.B, a.Q, nh, D, G.heads, a.out, a.o_sb, a.o_st, a.o_sh, lse_n, a.H,
             reinterpret_cast<const uint16_t*>(ws + L.out_l[g]),
             reinterpret_cast<const float*>(ws + L.lse_l[g]), a.lse);
