@@ -201,6 +201,8 @@ constexpr int C8_THREADS = 512;
 constexpr int C8_WAVES = C8_THREADS / 64;
 constexpr int C8_VROW = CK_T + 8;  // V^T row: 132 dwords, 16 rows of b128 reads hit distinct banks
 
+typedef short short4v __attribute__((ext_vector_type(4)));
+
 struct Chunk8Smem {
     uint16_t k[CK_T][CK_KROW];  // K tile (also decoder-slice and center staging)
     uint16_t vt[CK_D][C8_VROW];  // V^T[d][vt_col(key)]
@@ -417,7 +419,15 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
             }
         }
     } else {
-        // acc[dt] element i: key 32*wave + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32
+        // acc[dt] element i: key 32*wave + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32.
+        // The centers of keys t0 .. t0+3 at column d come from one LDS
+        // transpose read (ds_read_b64_tr_b16): within a group of 16 lanes,
+        // lane j receives element j % 4 of the 8-byte rows that lanes
+        // j / 4, j / 4 + 4, j / 4 + 8, j / 4 + 12 address, so lane x = a + 4k
+        // addresses key t0 + k at columns dbase + 4a .. +4 and lane j gets
+        // the four keys at column dbase + j.
+        const int tr_x = lane & 15;
+        const int tr_off = (tr_x >> 2) * CK_D + 4 * (tr_x & 3) + 16 * ((lane >> 4) & 1);
 #pragma unroll
         for (int g = 0; g < 4; ++g) {
             const int t0 = 32 * wave + 8 * g + 4 * hf;
@@ -425,11 +435,15 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
             for (int dt = 0; dt < 4; ++dt) {
                 const int d = 32 * dt + l32;
                 const float bias = sm.bias[1][d];
+                short4v cen = {};
+                if (HAS_C)
+                    cen = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                        (__attribute__((address_space(3))) short4v*)(vcen + t0 * CK_D + 32 * dt + tr_off));
                 float v[4];
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     const float a = bf16_round(acc[dt][4 * g + e] + bias);
-                    v[e] = HAS_C ? a + bf16_bits_to_f32(vcen[(t0 + e) * CK_D + d]) : a;
+                    v[e] = HAS_C ? a + __uint_as_float((uint32_t)(uint16_t)cen[e] << 16) : a;
                 }
                 const u32x2 r = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                 *reinterpret_cast<u32x2*>(&sm.vt[d][vt_col(t0)]) = r;
