@@ -51,6 +51,14 @@ def test_attend_key_chunk_edges(dev, N, Nc, Q):
     _check(Scenario(H=2, N=N, Q=Q, Nc=Nc, rK=256, rV=384, G=32, C=16), dev, schedule="key_chunks")
 
 
+# current-key chunks run as several blocks over shares of the query blocks
+# (two shares from 32..47 query blocks, three from 48 or more): uneven
+# shares, partial current chunks, a partial last query block
+@pytest.mark.parametrize("N,Nc,Q", [(300, 600, 1100), (0, 300, 1530), (256, 1, 1024)])
+def test_attend_current_chunk_query_shares(dev, N, Nc, Q):
+    _check(Scenario(H=2, N=N, Q=Q, Nc=Nc, rK=128, rV=128, G=32, C=8), dev, schedule="key_chunks")
+
+
 @pytest.mark.parametrize("splits", [1, 2, 5, 0])
 def test_attend_splits(dev, splits):
     _check(Scenario(H=2, N=700, Q=260, Nc=100, rK=128, rV=64, G=32, C=8), dev, splits=splits)

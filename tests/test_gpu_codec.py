@@ -128,6 +128,57 @@ def test_encode_parity(dev, group, scale_dtype, quant_mode, with_mean):
     assert np.array_equal(u16(got["scales"]), rs)
 
 
+@pytest.mark.parametrize("H,D", [(3, 32), (2, 64)])
+def test_encode_parity_narrow_rows(dev, H, D):
+    # row widths of 96 and 128 (not multiples of 256): the projection takes the
+    # general GEMM kernel instead of the split-K one
+    shape = synth.Shape("t", H=H, D=D, N=0, Q=0, Nc=0, rK=64, rV=64, G=32, C=20)
+    layer = synth.make_layer(shape, seed=8)
+    x = synth.history_rows(shape, layer.centers_k, 150, seed=12)
+    got = ops.encode(x.to(dev), layer.w_enc_k.to(dev), centers=layer.centers_k.to(dev), group=32,
+                     scale_dtype=torch.float16)
+    ref = orc.encode(x.numpy(), u16(layer.w_enc_k), u16(layer.centers_k), None, 32, "fp16", "fp32")
+    assert np.array_equal(got["ids"].cpu().numpy().astype(np.int64), ref["ids"])
+    coeff = got["coeff"].cpu().numpy()
+    np.testing.assert_allclose(coeff, ref["coeff"], rtol=2e-5, atol=2e-5)
+    rp, rs, _ = orc.quant_pack(coeff, 32, "fp16", "fp32")
+    assert np.array_equal(got["packed"].cpu().numpy(), rp)
+    assert np.array_equal(u16(got["scales"]), rs)
+
+
+def test_assign_rows_not_multiple_of_16(dev):
+    # HD = 72: the fp64 VALU search (the MFMA search needs HD % 16 == 0)
+    g = torch.Generator().manual_seed(21)
+    centers = torch.randn(40, 72, generator=g).to(torch.bfloat16)
+    x = (centers.float()[torch.randint(0, 40, (90,), generator=g)]
+         + 0.3 * torch.randn(90, 72, generator=g))
+    ids = ops.assign(x.to(dev), centers.to(dev), torch.int32)
+    assert np.array_equal(ids.cpu().numpy(), orc.assign(x.numpy(), u16(centers)))
+
+
+def test_encode_into_cache_slot(dev):
+    # ops.encode(out=...) writes a chunk straight into a slot of a larger cache
+    shape = synth.Shape("t", H=4, D=128, N=0, Q=0, Nc=0, rK=384, rV=384, G=32, C=64)
+    layer = synth.make_layer(shape, seed=5)
+    x = synth.history_rows(shape, layer.centers_k, 200, seed=6).to(dev)
+    kw = dict(centers=layer.centers_k.to(dev), group=32, scale_dtype=torch.float16)
+    ref = ops.encode(x, layer.w_enc_k.to(dev), **kw)
+    cache = {"packed": torch.zeros(600, 192, dtype=torch.uint8, device=dev),
+             "scales": torch.zeros(600, 12, dtype=torch.float16, device=dev),
+             "ids": torch.zeros(600, dtype=torch.uint8, device=dev)}
+    sl = slice(200, 400)
+    got = ops.encode(x, layer.w_enc_k.to(dev), **kw,
+                     out={"packed": cache["packed"][sl], "scales": cache["scales"][sl],
+                          "ids": cache["ids"][sl],
+                          "coeff": torch.empty(200, 384, device=dev)})
+    assert got["packed"].data_ptr() == cache["packed"][sl].data_ptr()
+    for k in ("packed", "scales", "ids"):
+        assert torch.equal(cache[k][sl], ref[k])
+        assert not cache[k][:200].bool().any() and not cache[k][400:].bool().any()
+    with pytest.raises(ValueError):
+        ops.encode(x, layer.w_enc_k.to(dev), **kw, out={"packed": cache["packed"][:100]})
+
+
 @pytest.mark.parametrize("with_mean,id_dtype", [(False, torch.uint8), (True, torch.int16)])
 def test_decode_parity(dev, with_mean, id_dtype):
     from tests._helpers import Scenario
