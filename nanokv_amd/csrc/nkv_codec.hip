@@ -426,11 +426,15 @@ __global__ void __launch_bounds__(256) assign_bf16_kernel(const float* __restric
                 const bf16x8 b = as_bf16x8(bcur[tt][ks]);
                 acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b, acc[tt], 0, 0, 0);
                 acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b, acc[tt], 0, 0, 0);
+                // (the words go through named scalars: indexing the vector
+                // inside the bit_cast was lowered to word 0 four times)
+                const uint32_t w4[4] = {bcur[tt][ks].x, bcur[tt][ks].y, bcur[tt][ks].z,
+                                        bcur[tt][ks].w};
 #pragma unroll
-                for (int e = 0; e < 4; ++e)
-                    cn[tt] = __builtin_amdgcn_fdot2_f32_bf16(
-                        __builtin_bit_cast(bf16x2, bcur[tt][ks][e]),
-                        __builtin_bit_cast(bf16x2, bcur[tt][ks][e]), cn[tt], false);
+                for (int e = 0; e < 4; ++e) {
+                    const bf16x2 wv = __builtin_bit_cast(bf16x2, w4[e]);
+                    cn[tt] = __builtin_amdgcn_fdot2_f32_bf16(wv, wv, cn[tt], false);
+                }
             }
         }
         __syncthreads();

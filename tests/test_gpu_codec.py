@@ -146,6 +146,30 @@ def test_encode_parity_narrow_rows(dev, H, D):
     assert np.array_equal(u16(got["scales"]), rs)
 
 
+@pytest.mark.parametrize("id_dtype", [torch.uint8, torch.int32])
+def test_assign_near_ties_exact(dev, id_dtype):
+    # HD = 256, C <= 256: the bf16 MFMA search.  Rows on the exact midpoint of
+    # two centers tie (the first index must win); rows moved a hair off a
+    # midpoint differ by far less than the search's error bound, so both
+    # kinds go through the exact fp64 re-evaluation of their candidates.
+    # small-integer centers: every product and sum below is exact in fp64, so
+    # the ties are exact whatever the summation order
+    g = torch.Generator().manual_seed(31)
+    C, HD = 24, 256
+    centers = torch.randint(-8, 9, (C, HD), generator=g).to(torch.bfloat16)
+    cf = centers.float()
+    a = torch.randint(0, C, (64,), generator=g)
+    b = (a + 1 + torch.randint(0, C - 1, (64,), generator=g)) % C
+    mid = 0.5 * (cf[a] + cf[b])                      # exact in fp32
+    nudge = (cf[b] - cf[a]) * 2.0 ** -20              # toward b: b wins by a hair
+    x = torch.cat([mid, mid + nudge, mid - nudge, cf[a] + torch.randint(-1, 2, (64, HD), generator=g)])
+    ids = ops.assign(x.to(dev), centers.to(dev), id_dtype)
+    got = ids.cpu().to(torch.int64).numpy()
+    ref = orc.assign(x.numpy(), u16(centers))
+    assert np.array_equal(got, ref)
+    assert np.array_equal(ref[:64], np.minimum(a, b).numpy())
+
+
 def test_assign_rows_not_multiple_of_16(dev):
     # HD = 72: the fp64 VALU search (the MFMA search needs HD % 16 == 0)
     g = torch.Generator().manual_seed(21)
