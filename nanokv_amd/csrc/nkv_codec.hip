@@ -322,151 +322,140 @@ __global__ void __launch_bounds__(256) assign_mfma_kernel(const float* __restric
 // bf16 MFMA nearest-center search with an exact decision (C <= 256).
 // x = hi + lo + r with hi = bf16(x), lo = bf16(x - hi), |r| <= 2^-16 |x|;
 // the centers are exact bf16, so the two MFMA passes hi.c and lo.c have
-// exact products and only fp32 sums.  Even with one fp32 rounding per
-// addition (2 HD of them) the dot product is within 3.9e-4 ||x|| ||c|| of
-// x.c, and ||c||^2 (fp32 from the same center pieces) within 1.8e-4 ||c||^2,
-// so every approximate distance dt_c = ||c||^2 - 2 x.c is within
-//   E_c = AB_KAPPA (||x|| ||c|| + ||c||^2),   AB_KAPPA = 2e-3 (> 2.5x that),
-// of the exact one.  With U = min_c (dt_c + E_c) the exact argmin is among
-// the candidates {c : dt_c - E_c <= U}; a row with one candidate is decided,
-// a row with several re-evaluates just those in fp64 (exact products, first
-// index on ties), the arithmetic of assign_kernel.
-// A 256-thread block owns 32 rows; wave w takes centers 64w + [0, 64) as two
-// 32 x 32 tiles.  x is split into hi/lo bf16 tiles in LDS per 128-wide k
-// chunk (shared by the four waves); center fragments come from L2 one chunk
-// ahead.  Needs HD % 128 == 0, C <= 256, x 16-byte and centers 16-byte
-// aligned rows.
-constexpr int AB_ROWS = 32, AB_KC = 128, AB_MAXC = 256;
-constexpr float AB_KAPPA = 2e-3f;
+// exact products and only fp32 sums.  The MFMA accumulator restarts every
+// AB_SEG k values and the segment sums are added in a second fp32
+// accumulator, so even with one fp32 rounding per addition the dot product
+// is within (g_2SEG + g_nseg)(1 + 2^-7) + 2^-16 < 5e-5 of sum |x||c| <=
+// ||x|| ||c|| (g_n = n 2^-24 / (1 - n 2^-24), nseg = HD / SEG <= 64);
+// ||c||^2 is summed the same way (fp32 per segment, fp64 across: < 1e-5
+// ||c||^2).  With the final fp32 subtraction every approximate distance
+// dt_c = ||c||^2 - 2 x.c is within 1.1e-4 (||x|| ||c|| + ||c||^2) of the
+// exact one (2e-4 if the matrix core truncated instead of rounding); the
+// search uses
+//   E_c = AB_KAPPA (||x|| ||c|| + ||c||^2),   AB_KAPPA = 2.5e-4,
+// With U = min_c (dt_c + E_c) the exact argmin is among the candidates
+// {c : dt_c - E_c <= U}; a row with one candidate is decided, a row with
+// several re-evaluates just those in fp64 (exact products, first index on
+// ties), the arithmetic of assign_kernel.
+// A 512-thread block owns 32 rows; wave w takes centers 32w + [0, 32) as one
+// 32 x 32 tile.  x is split into hi/lo bf16 tiles in LDS per 128-wide k
+// chunk (shared by the eight waves); center fragments come from L2 one chunk
+// ahead.  Needs HD % AB_SEG == 0, HD <= AB_MAXK, C <= 256, x and centers
+// 16-byte aligned.
+constexpr int AB_ROWS = 32, AB_KC = 128, AB_SEG = 256, AB_MAXC = 256, AB_WAVES = 8, AB_MAXK = 16384;
+constexpr float AB_KAPPA = 2.5e-4f;
 
 template <int ID_BYTES>
-__global__ void __launch_bounds__(256) assign_bf16_kernel(const float* __restrict__ x,
-                                                          const uint16_t* __restrict__ centers,
-                                                          int64_t rows, int C, int HD,
-                                                          void* __restrict__ ids) {
+__global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(
+    const float* __restrict__ x, const uint16_t* __restrict__ centers, int64_t rows, int C, int HD,
+    void* __restrict__ ids) {
     __shared__ __align__(16) uint16_t xs[2][AB_ROWS][AB_KC + 8];
     __shared__ float xn[AB_ROWS];
-    __shared__ float red[4][AB_ROWS];
+    __shared__ float red[AB_WAVES][AB_ROWS];
     __shared__ int cnt[AB_ROWS], first[AB_ROWS];
     __shared__ uint32_t cand[AB_ROWS][AB_MAXC / 32];
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hf = lane >> 5, l32 = lane & 31;
     const int64_t row0 = (int64_t)blockIdx.x * AB_ROWS;
     if (t < AB_ROWS) { xn[t] = 0.0f; cnt[t] = 0; first[t] = 0x7fffffff; }
-    for (int e = t; e < AB_ROWS * AB_MAXC / 32; e += 256) (&cand[0][0])[e] = 0u;
-    // fill: thread t splits row t/8, k columns 16*(t%8) .. +16 of each chunk
-    const int frow = t >> 3, fk = 16 * (t & 7);
+    for (int e = t; e < AB_ROWS * AB_MAXC / 32; e += 64 * AB_WAVES) (&cand[0][0])[e] = 0u;
+    // fill: thread t splits row t/16, k columns 8*(t%16) .. +8 of each chunk
+    const int frow = t >> 4, fk = 8 * (t & 15);
     const int64_t fr = min(row0 + frow, rows - 1);
     const float* xrow = x + fr * HD + fk;
     const bool frow_ok = row0 + frow < rows;
-    // this lane's two center columns
-    int col[2];
-    const uint16_t* crow[2];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        col[tt] = 64 * wave + 32 * tt + l32;
-        crow[tt] = centers + (int64_t)min(col[tt], C - 1) * HD + 8 * hf;
-    }
-    f32x16 acc[2] = {f32x16{}, f32x16{}};
-    float cn[2] = {0.0f, 0.0f};
+    // this lane's center column
+    const int col = 32 * wave + l32;
+    const uint16_t* crow = centers + (int64_t)min(col, C - 1) * HD + 8 * hf;
+    f32x16 acc = {}, tot = {};
+    float cseg = 0.0f;
+    double cn = 0.0;
     float xsq = 0.0f;
-    u32x4 bcur[2][8], bnxt[2][8];
-    auto fetch_b = [&](int kc, u32x4 (&b)[2][8]) {
+    u32x4 bcur[8], bnxt[8];
+    f32x4 xcur[2], xnxt[2];
+    auto fetch = [&](int kc, u32x4 (&b)[8], f32x4 (&xv)[2]) {
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks)
-                b[tt][ks] = *reinterpret_cast<const u32x4*>(crow[tt] + kc + 16 * ks);
+        for (int ks = 0; ks < 8; ++ks) b[ks] = *reinterpret_cast<const u32x4*>(crow + kc + 16 * ks);
+        xv[0] = *reinterpret_cast<const f32x4*>(xrow + kc);
+        xv[1] = *reinterpret_cast<const f32x4*>(xrow + kc + 4);
     };
-    f32x4 xcur[4], xnxt[4];
-    auto fetch_x = [&](int kc, f32x4 (&xv)[4]) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xv[e] = *reinterpret_cast<const f32x4*>(xrow + kc + 4 * e);
-    };
-    fetch_b(0, bcur);
-    fetch_x(0, xcur);
+    fetch(0, bcur, xcur);
     __syncthreads();
     for (int kc = 0; kc < HD; kc += AB_KC) {
         // the next chunk's operands (the last chunk reloads itself), issued
         // before this chunk's work and kept there (the fence stops the
         // scheduler from sinking the loads next to their use)
         const int kn = kc + AB_KC < HD ? kc + AB_KC : kc;
-        fetch_b(kn, bnxt);
-        fetch_x(kn, xnxt);
+        fetch(kn, bnxt, xnxt);
         __builtin_amdgcn_sched_barrier(0);
         {
-            // split 16 values of this thread's row into hi / lo bf16
-            u32x4 hi[2], lo[2];
+            // split this thread's 8 values into hi / lo bf16
+            const float v[8] = {xcur[0][0], xcur[0][1], xcur[0][2], xcur[0][3],
+                                xcur[1][0], xcur[1][1], xcur[1][2], xcur[1][3]};
+            u32x4 hi, lo;
 #pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                const f32x4 v0 = xcur[2 * h2], v1 = xcur[2 * h2 + 1];
-                const float v[8] = {v0[0], v0[1], v0[2], v0[3], v1[0], v1[1], v1[2], v1[3]};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const uint32_t hp = pack_bf16x2(v[2 * e], v[2 * e + 1]);
-                    hi[h2][e] = hp;
-                    lo[h2][e] = pack_bf16x2(v[2 * e] - __uint_as_float(hp << 16),
-                                            v[2 * e + 1] - __uint_as_float(hp & 0xffff0000u));
-                    xsq = fmaf(v[2 * e], v[2 * e], fmaf(v[2 * e + 1], v[2 * e + 1], xsq));
-                }
+            for (int e = 0; e < 4; ++e) {
+                const uint32_t hp = pack_bf16x2(v[2 * e], v[2 * e + 1]);
+                hi[e] = hp;
+                lo[e] = pack_bf16x2(v[2 * e] - __uint_as_float(hp << 16),
+                                    v[2 * e + 1] - __uint_as_float(hp & 0xffff0000u));
+                xsq = fmaf(v[2 * e], v[2 * e], fmaf(v[2 * e + 1], v[2 * e + 1], xsq));
             }
-#pragma unroll
-            for (int h2 = 0; h2 < 2; ++h2) {
-                *reinterpret_cast<u32x4*>(&xs[0][frow][fk + 8 * h2]) = hi[h2];
-                *reinterpret_cast<u32x4*>(&xs[1][frow][fk + 8 * h2]) = lo[h2];
-            }
+            *reinterpret_cast<u32x4*>(&xs[0][frow][fk]) = hi;
+            *reinterpret_cast<u32x4*>(&xs[1][frow][fk]) = lo;
         }
         __syncthreads();
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) {
             const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&xs[0][l32][16 * ks + 8 * hf]);
             const bf16x8 al = *reinterpret_cast<const bf16x8*>(&xs[1][l32][16 * ks + 8 * hf]);
+            const bf16x8 b = as_bf16x8(bcur[ks]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b, acc, 0, 0, 0);
+            // (the words go through named scalars: indexing the vector inside
+            // the bit_cast was lowered to word 0 four times)
+            const uint32_t w4[4] = {bcur[ks].x, bcur[ks].y, bcur[ks].z, bcur[ks].w};
 #pragma unroll
-            for (int tt = 0; tt < 2; ++tt) {
-                const bf16x8 b = as_bf16x8(bcur[tt][ks]);
-                acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b, acc[tt], 0, 0, 0);
-                acc[tt] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b, acc[tt], 0, 0, 0);
-                // (the words go through named scalars: indexing the vector
-                // inside the bit_cast was lowered to word 0 four times)
-                const uint32_t w4[4] = {bcur[tt][ks].x, bcur[tt][ks].y, bcur[tt][ks].z,
-                                        bcur[tt][ks].w};
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    const bf16x2 wv = __builtin_bit_cast(bf16x2, w4[e]);
-                    cn[tt] = __builtin_amdgcn_fdot2_f32_bf16(wv, wv, cn[tt], false);
-                }
+            for (int e = 0; e < 4; ++e) {
+                const bf16x2 wv = __builtin_bit_cast(bf16x2, w4[e]);
+                cseg = __builtin_amdgcn_fdot2_f32_bf16(wv, wv, cseg, false);
             }
+        }
+        if ((kc + AB_KC) % AB_SEG == 0) {
+            // end of a segment: fold it into the second accumulators
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tot[i] += acc[i];
+            acc = f32x16{};
+            cn += (double)cseg;
+            cseg = 0.0f;
         }
         __syncthreads();
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt)
-#pragma unroll
-            for (int ks = 0; ks < 8; ++ks) bcur[tt][ks] = bnxt[tt][ks];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) xcur[e] = xnxt[e];
+        for (int ks = 0; ks < 8; ++ks) bcur[ks] = bnxt[ks];
+        xcur[0] = xnxt[0];
+        xcur[1] = xnxt[1];
     }
-    // ||x||^2 per row (8 threads per row), ||c||^2 per column (two k halves)
+    // ||x||^2 per row (16 threads per row), ||c||^2 per column (two k halves)
     atomicAdd(&xn[frow], frow_ok ? xsq : 0.0f);
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) cn[tt] += __shfl_xor(cn[tt], 32);
+    cn += __shfl_xor(cn, 32);
+    const float cnf = (float)cn;
     __syncthreads();
-    // acc[tt] element i: row 8(i/4) + 4hf + i%4, column col[tt]
-    float dt[2][16], ee[2][16];
-#pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const float cnorm = sqrtf(cn[tt]) * 1.001f;
+    // tot element i: row 8(i/4) + 4hf + i%4, column col
+    float dt[16], ee[16];
+    {
+        const float cnorm = sqrtf(cnf) * 1.001f;
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
             const int r = 8 * (i / 4) + 4 * hf + (i % 4);
             const float xnorm = sqrtf(xn[r]) * 1.001f;
-            dt[tt][i] = col[tt] < C ? cn[tt] - 2.0f * acc[tt][i] : INFINITY;
-            ee[tt][i] = AB_KAPPA * (xnorm * cnorm + cn[tt] * 1.001f);
+            dt[i] = col < C ? cnf - 2.0f * tot[i] : INFINITY;
+            ee[i] = AB_KAPPA * (xnorm * cnorm + cnf * 1.001f);
         }
     }
-    // U = min over the row's columns of dt + E: lanes of one half-wave hold a row's 32 columns
+    // U = min over the row's columns of dt + E: a half-wave holds a row's 32 columns
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
-        float u = fminf(dt[0][i] + ee[0][i], dt[1][i] + ee[1][i]);
+        float u = dt[i] + ee[i];
 #pragma unroll
         for (int off = 1; off < 32; off <<= 1) u = fminf(u, __shfl_xor(u, off));
         if (l32 == 0) red[wave][8 * (i / 4) + 4 * hf + (i % 4)] = u;
@@ -476,20 +465,19 @@ __global__ void __launch_bounds__(256) assign_bf16_kernel(const float* __restric
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
         const int r = 8 * (i / 4) + 4 * hf + (i % 4);
-        const float U = fminf(fminf(red[0][r], red[1][r]), fminf(red[2][r], red[3][r]));
+        float U = red[0][r];
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            if (col[tt] < C && dt[tt][i] - ee[tt][i] <= U) {
-                atomicAdd(&cnt[r], 1);
-                atomicMin(&first[r], col[tt]);
-                atomicOr(&cand[r][col[tt] >> 5], 1u << (col[tt] & 31));
-            }
+        for (int w = 1; w < AB_WAVES; ++w) U = fminf(U, red[w][r]);
+        if (col < C && dt[i] - ee[i] <= U) {
+            atomicAdd(&cnt[r], 1);
+            atomicMin(&first[r], col);
+            atomicOr(&cand[r][col >> 5], 1u << (col & 31));
         }
     }
     __syncthreads();
     // rows with one candidate are decided; the others compare their
     // candidates exactly in fp64 (one wave per row, lanes split HD)
-    for (int r = wave; r < AB_ROWS; r += 4) {
+    for (int r = wave; r < AB_ROWS; r += AB_WAVES) {
         const int64_t gr = row0 + r;
         if (gr >= rows) continue;
         // (no candidate only for non-finite rows: index 0 then)
@@ -505,10 +493,20 @@ __global__ void __launch_bounds__(256) assign_bf16_kernel(const float* __restric
                     bits &= bits - 1;
                     const uint16_t* cr = centers + (int64_t)c * HD;
                     double cc = 0.0, xc = 0.0;
-                    for (int k = lane; k < HD; k += 64) {
-                        const double cv = (double)bf16_bits_to_f32(cr[k]);
-                        cc = fma(cv, cv, cc);
-                        xc = fma((double)xr[k], cv, xc);
+                    // 8 consecutive values per lane and step (HD % 256 == 0)
+                    for (int k = 8 * lane; k < HD; k += 512) {
+                        const u32x4 cw = *reinterpret_cast<const u32x4*>(cr + k);
+                        const f32x4 x0 = *reinterpret_cast<const f32x4*>(xr + k);
+                        const f32x4 x1 = *reinterpret_cast<const f32x4*>(xr + k + 4);
+                        const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+                        const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+#pragma unroll
+                        for (int e = 0; e < 8; ++e) {
+                            const uint32_t hb = (e & 1) ? (w4[e >> 1] & 0xffff0000u) : (w4[e >> 1] << 16);
+                            const double cv = (double)__uint_as_float(hb);
+                            cc = fma(cv, cv, cc);
+                            xc = fma((double)xv[e], cv, xc);
+                        }
                     }
 #pragma unroll
                     for (int off = 1; off < 64; off <<= 1) {
@@ -884,15 +882,16 @@ extern "C" int nkv_unpack(void* stream, const uint8_t* packed, const uint16_t* s
 static int launch_assign(hipStream_t s, const float* x, const uint16_t* centers, int64_t rows,
                          int C, int HD, void* ids, int id_bytes) {
     if (rows <= 0) return NKV_OK;
-    if (C <= AB_MAXC && HD > 0 && HD % AB_KC == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+    if (C <= AB_MAXC && HD > 0 && HD % AB_SEG == 0 && HD <= AB_MAXK && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(centers) % 16 == 0) {
         dim3 grid((unsigned)cdiv(rows, AB_ROWS));
+        const unsigned threads = 64 * AB_WAVES;
         if (id_bytes == 1)
-            assign_bf16_kernel<1><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
+            assign_bf16_kernel<1><<<grid, threads, 0, s>>>(x, centers, rows, C, HD, ids);
         else if (id_bytes == 2)
-            assign_bf16_kernel<2><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
+            assign_bf16_kernel<2><<<grid, threads, 0, s>>>(x, centers, rows, C, HD, ids);
         else
-            assign_bf16_kernel<4><<<grid, 256, 0, s>>>(x, centers, rows, C, HD, ids);
+            assign_bf16_kernel<4><<<grid, threads, 0, s>>>(x, centers, rows, C, HD, ids);
         NKV_LAUNCH_CHECK();
         return NKV_OK;
     }
