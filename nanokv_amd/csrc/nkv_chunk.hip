@@ -707,21 +707,30 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
     u32x4 buf[CB_AHEAD][8];
     u32x2 mlb[CB_AHEAD];
     auto issue = [&](int cc, int i) {
-        cc = min(cc, NC - 1);
+        cc = max(min(cc, NC - 1), 0);
         mlb[i] = ml[cc * lse_stride];
 #pragma unroll
         for (int st = 0; st < 8; ++st)
             buf[i][st] = *reinterpret_cast<const u32x4*>(src + cc * cstride + 512 * st);
+        // chunks are issued in ring order, so waiting for slot i leaves the
+        // slots issued after it in flight
+        __builtin_amdgcn_sched_barrier(0);
     };
+    // no chunks (no keys at all): nothing to read, and the workspace may be
+    // null; the loads must not be issued ahead of this test
+    if (NC > 0) {
 #pragma unroll
     for (int i = 0; i < CB_AHEAD; ++i) issue(i, i);
     for (int cc0 = 0; cc0 < NC; cc0 += CB_AHEAD) {
 #pragma unroll
         for (int i = 0; i < CB_AHEAD; ++i) {
-            if (cc0 + i >= NC) break;
+            // Slots past the last chunk hold a reloaded copy of it and get
+            // weight 0.  No branch skips them, so the compiler's wait for
+            // slot i leaves the other slots' loads in flight.
+            const bool live = cc0 + i < NC;
             const float mc = __uint_as_float(mlb[i][0]);
             // a chunk with no valid key for this query has m = -inf and O = 0
-            const bool up = mc > M;
+            const bool up = live && mc > M;
             if (__any(up)) {
                 const float f = up ? exp2f(M - mc) : 1.0f;  // M = -inf gives 0
                 L *= f;
@@ -729,7 +738,7 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
                 for (int e = 0; e < 64; ++e) acc[e] *= f;
             }
             M = up ? mc : M;
-            const float wt = mc == -INFINITY ? 0.0f : exp2f(mc - M);
+            const float wt = !live || mc == -INFINITY ? 0.0f : exp2f(mc - M);
             L += wt * __uint_as_float(mlb[i][1]);
 #pragma unroll
             for (int st = 0; st < 8; ++st)
@@ -740,6 +749,7 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
                 }
             issue(cc0 + i + CB_AHEAD, i);
         }
+    }
     }
     if (qi >= p.Q) return;
     const float inv = L > 0.0f ? 1.0f / L : 0.0f;
