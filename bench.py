@@ -54,6 +54,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=15.0,
                     help="time budget of the CPU-baseline head sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--rope", action="store_true",
+                    help="configs 1-2: read-time RoPE of the history keys (frames of "
+                         "30 x 52 tokens at temporal positions 0, 1, ...)")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="no timing: run a known-size copy and a few fused calls (for rocprofv3 --pmc)")
     return ap.parse_args()
@@ -363,6 +366,12 @@ def main():
         ws_bytes = ops.attend_workspace_size(q, shape.N, shape.Nc, codecs[0], codecs[1],
                                              args.splits, args.schedule)
         ws = torch.empty(max(ws_bytes, 1), device=device, dtype=torch.uint8)
+    rope = None
+    if args.rope and not fast:
+        grid_h, grid_w = 30, 52  # 1,560 tokens per frame
+        frames = -(-shape.N // (grid_h * grid_w))
+        rope = ops.Rope.from_bands(ops.rope_bands(shape.D), range(frames), grid_h, grid_w,
+                                   device)
 
     def step(events=None):
         if fast:
@@ -370,7 +379,7 @@ def main():
                                    out=out, return_lse=False, workspace=ws)
         return ops.attend(q, kc, vc, codecs[0], codecs[1], out=out, splits=args.splits,
                           return_lse=False, workspace=ws, kernel_events=events,
-                          schedule=args.schedule)
+                          schedule=args.schedule, rope=rope)
 
     if args.profile_kernel:
         # A plain copy of known size (for FETCH_SIZE/WRITE_SIZE calibration), then the kernel.
@@ -449,7 +458,8 @@ def main():
                    "scale_group": shape.G, "scale_dtype": "fp16", "centers": shape.C,
                    "parallelism": "single-gpu"}
         | ({"protected_rows": int(prot_rows.numel()), "full_heads": list(synth.FAST_FULL_HEADS),
-            "reader_width": synth.FAST_READER_D} if fast else {}),
+            "reader_width": synth.FAST_READER_D} if fast else {})
+        | ({"rope": "history keys rotated at read, frames of 30x52 tokens"} if rope else {}),
         "history_tokens_per_ms": round(shape.N / ms_per_step, 1),
         "coeff_stream_GBps": round(shape.coeff_stream_bytes() / (kavg_ms * 1e-3) / 1e9, 2),
         "algorithmic_flops": fl,

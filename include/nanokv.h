@@ -34,6 +34,11 @@
  *                     (CN/fast_kernels.py:30-54)
  *  nkv_fast_attend <- hybrid_attention (CN/core.py:278-310) and the partition
  *                     reads of maybe_attention (CN/mg35.py:100-357)
+ *  nkv_rope_apply  <- rope_apply (wan_video_dit.py:185-192) with the 3-D
+ *                     frequencies of _kv_freqs (pipelines/wan_video.py:3322-3341);
+ *                     nkv_attend_args.rope fuses the same rotation into the
+ *                     decode (the read-time RoPE of cached keys,
+ *                     wan_video_dit.py:538-546)
  */
 #ifndef NANOKV_H
 #define NANOKV_H
@@ -45,7 +50,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 2
+#define NKV_ABI_VERSION 3
 
 enum nkv_status {
     NKV_OK = 0,
@@ -77,6 +82,44 @@ enum nkv_quant_mode { NKV_QUANT_FP32 = 0, NKV_QUANT_BF16 = 1 };
 
 /* ABI version of the loaded library (NKV_ABI_VERSION at build time). */
 int nkv_abi_version(void);
+
+/*
+ * Rotary position embedding of cached keys, applied at read time
+ * (rope_apply, wan_video_dit.py:185-192, over the per-token frequencies
+ * that _kv_freqs builds from precompute_freqs_cis_3d, wan_video_dit.py:168-182).
+ * The positions follow the codec row n of a key: frame f = n / (grid_h*grid_w)
+ * at temporal position frame_pos[f], row (n % (grid_h*grid_w)) / grid_w and
+ * column n % grid_w.  Complex pair p (dims 2p, 2p+1) of a head rotates by
+ *   p < pt            cs_t[frame_pos[f]][p]
+ *   pt <= p < pt+ph   cs_h[row][p - pt]
+ *   otherwise         cs_w[col][p - pt - ph]
+ * where every entry is an fp64 (cos, sin) pair (the reference's complex128
+ * polar(1, angle) tables; a (1, 0) band is no rotation, as the reference's
+ * prope_disable_t_rope).  In fp64 with each product rounded:
+ *   y[2p] = x[2p] c - x[2p+1] s,  y[2p+1] = x[2p] s + x[2p+1] c,
+ * rounded to fp32 and then to bf16 (torch's float64 -> bfloat16).
+ * pt + ph + pw must be D / 2.  Table pointers are device memory.
+ */
+typedef struct nkv_rope {
+    const double* cs_t;           /* [n_t, pt, 2] temporal band */
+    const double* cs_h;           /* [grid_h, ph, 2] row band */
+    const double* cs_w;           /* [grid_w, pw, 2] column band */
+    const int32_t* frame_pos;     /* [n_frames] cs_t row of each frame */
+    int64_t n_frames;
+    int n_t;
+    int pt, ph, pw;
+    int grid_h, grid_w;
+} nkv_rope;
+
+/*
+ * out[b, s, h, :] = RoPE of x[b, s, h, :] at the position of row rows[s]
+ * (rows NULL: row s), x and out [B, S, H, D] bf16 addressed as
+ * x[b*x_sb + s*x_st + h*x_sh + d] (out likewise; out may be x).  D even.
+ */
+int nkv_rope_apply(void* stream, const nkv_rope* rope, int B, int64_t S, int H, int D,
+                   const uint16_t* x, int64_t x_sb, int64_t x_st, int64_t x_sh,
+                   const int32_t* rows, uint16_t* out, int64_t o_sb, int64_t o_st,
+                   int64_t o_sh);
 
 /* Message of the last failed call on this thread ("" if none). */
 const char* nkv_last_error(void);
@@ -196,6 +239,9 @@ int nkv_decode(void* stream, const nkv_decode_args* args);
  * key/value codecs decode to HD = H * D columns; head h reads columns
  * [h*D, (h+1)*D).  An empty key set gives out = 0 and lse = -inf
  * (attention_lse, CN/core.py:48-49).  D must be 128.
+ * rope (host pointer, NULL = none): history keys are rotated after decode at
+ * the positions of their codec rows (see nkv_rope); q and k_cur are taken as
+ * already rotated.  RoPE runs on the KEY_CHUNKS schedule (AUTO picks it).
  */
 typedef struct nkv_attend_args {
     int B;
@@ -223,6 +269,7 @@ typedef struct nkv_attend_args {
      * split-combine kernel), for per-kernel timing.  NULL = not recorded. */
     void* ev_kernel_begin;
     void* ev_kernel_end;
+    const nkv_rope* rope;
 } nkv_attend_args;
 
 /* Bytes of workspace nkv_attend needs for these arguments (0 if none). */
@@ -266,8 +313,8 @@ typedef struct nkv_reader_group {
  * native partition), out and lse, as for nkv_attend (its N is the codec's
  * token count; splits and schedule are ignored).  Every head should belong
  * to exactly one group (CN/core.py:213-215); a head in no group keeps the
- * native partition alone.  No RoPE/PRoPE is applied (positions are outside
- * this build).  Returns NKV_ERR_UNSUPPORTED for D != 128.
+ * native partition alone.  attend.rope must be NULL (RoPE of the reader
+ * partitions is not built).  Returns NKV_ERR_UNSUPPORTED for D != 128.
  */
 typedef struct nkv_fast_args {
     nkv_attend_args attend;

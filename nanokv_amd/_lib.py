@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libnanokv_hip.so"
 
-NKV_ABI_VERSION = 2
+NKV_ABI_VERSION = 3
 NKV_OK = 0
 NKV_ERR_INVALID = -1
 NKV_ERR_UNSUPPORTED = -2
@@ -32,7 +32,7 @@ NKV_SCHEDULE_KEY_CHUNKS = 2
 EXPORTED = (
     "nkv_abi_version", "nkv_last_error", "nkv_quant_pack", "nkv_unpack", "nkv_assign",
     "nkv_encode", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
-    "nkv_fast_attend_workspace_size", "nkv_fast_attend",
+    "nkv_fast_attend_workspace_size", "nkv_fast_attend", "nkv_rope_apply",
 )
 
 
@@ -63,6 +63,14 @@ class NkvDecodeArgs(Structure):
     ]
 
 
+class NkvRope(Structure):
+    _fields_ = [
+        ("cs_t", c_void_p), ("cs_h", c_void_p), ("cs_w", c_void_p), ("frame_pos", c_void_p),
+        ("n_frames", c_int64), ("n_t", c_int), ("pt", c_int), ("ph", c_int), ("pw", c_int),
+        ("grid_h", c_int), ("grid_w", c_int),
+    ]
+
+
 class NkvAttendArgs(Structure):
     _fields_ = [
         ("B", c_int), ("H", c_int), ("D", c_int), ("splits", c_int),
@@ -74,6 +82,7 @@ class NkvAttendArgs(Structure):
         ("key", NkvCodec), ("value", NkvCodec),
         ("out", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64),
         ("lse", c_void_p), ("ev_kernel_begin", c_void_p), ("ev_kernel_end", c_void_p),
+        ("rope", POINTER(NkvRope)),
     ]
 
 
@@ -131,6 +140,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nkv_fast_attend_workspace_size.argtypes = [POINTER(NkvFastArgs)]
     lib.nkv_fast_attend.restype = c_int
     lib.nkv_fast_attend.argtypes = [c_void_p, POINTER(NkvFastArgs), c_void_p, c_size_t]
+    lib.nkv_rope_apply.restype = c_int
+    lib.nkv_rope_apply.argtypes = [c_void_p, POINTER(NkvRope), c_int, c_int64, c_int, c_int,
+                                   c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+                                   c_int64, c_int64, c_int64]
     lib.nkv_lse_merge.restype = c_int
     lib.nkv_lse_merge.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int64, c_void_p,
                                   c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p]

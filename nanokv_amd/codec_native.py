@@ -8,10 +8,15 @@ followed by attention), with the decode fused into the attention kernel:
   attention_lse(q, k, v)           CN:45-72   uncompressed partition, (O, lse)
   merge(out_a, lse_a, out_b, lse_b) CN:33-42  exact LSE merge of partitions
   protected_tokens(frame_ids, ...) CN:140-152 frame-level protection policy
-  codec_history_attention(q, cache, k_cur, v_cur)
+  codec_history_attention(q, cache, k_cur, v_cur, rope=None)
                                    decode-then-attend of a paired K/V codec
                                    cache plus the current chunk, fused
-                                   (nkv_attend); K/V are never materialised
+                                   (nkv_attend); K/V are never materialised;
+                                   rope: read-time RoPE of the cached keys
+                                   (wan_video_dit.py:538-546)
+  kv_rope(freqs, positions, h, w)  the positions of cached frames, as
+                                   _kv_freqs (pipelines/wan_video.py:3322-3341)
+                                   builds them, for the fused kernel
   ReaderGroup / ReaderLayer        CN:155-224 reader parameters, bound to
                                    the kernels (identity flags CN:256-262)
   fast_history_attention(q, cache, k_cur, v_cur, reader, protect)
@@ -73,15 +78,36 @@ def protected_tokens(frame_ids: torch.Tensor, recent: int, stride: int, sink: in
     return keep[inverse]
 
 
+def kv_rope(freqs, temporal_positions, h: int, w: int, device, *,
+            disable_t: bool = False) -> ops.Rope:
+    """Read-time RoPE positions of cached frames: `freqs` is the model's
+    frequency tuple (precompute_freqs_cis_3d: temporal, row, column bands
+    first), one temporal position per cached frame, frames of h x w tokens.
+    The same arguments as _kv_freqs (pipelines/wan_video.py:3322-3341), which
+    returns the per-token complex table instead.  disable_t: identity
+    temporal band (prope_disable_t_rope, wan_video_dit.py:542-545)."""
+    bands = tuple(torch.as_tensor(b) for b in freqs[:3])
+    for b in bands:
+        if not torch.is_complex(b) or b.dim() != 2:
+            raise ValueError("freqs bands must be complex [positions, pairs] tensors")
+    bands = tuple(b.to(torch.complex128).cpu() for b in bands)
+    return ops.Rope.from_bands(bands, temporal_positions, h, w, torch.device(device),
+                               disable_t=disable_t)
+
+
 def codec_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
                             k_cur: Optional[torch.Tensor] = None,
                             v_cur: Optional[torch.Tensor] = None, *,
-                            scale: Optional[float] = None, return_lse: bool = False):
+                            scale: Optional[float] = None, return_lse: bool = False,
+                            rope: Optional[ops.Rope] = None):
     """Attention of q [B, H, Q, D] over [decoded history; current chunk] where
     the history is the paired codec cache (nanokv_codec payloads or segment
     lists) and k_cur/v_cur [B, H, Nc, D] are uncompressed.  Equivalent to the
     reference's decode_pair_values + attention (wan_video_dit.py:497-627)
-    with the decode fused into nkv_attend."""
+    with the decode fused into nkv_attend.  rope (kv_rope): the cached keys
+    are rotated after decode at their positions, as the reference's
+    rope_apply(cache_k_pre, cache_freqs) (wan_video_dit.py:538-546); q and
+    k_cur are taken as already rotated."""
     device = q.device
     B, H, Qn, D = (int(x) for x in q.shape)
     key = value = None
@@ -93,7 +119,7 @@ def codec_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     vc = None if v_cur is None else v_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
     out, lse = ops.attend(qq, kc, vc, key, value,
                           softmax_scale=D ** -0.5 if scale is None else scale,
-                          return_lse=return_lse)
+                          return_lse=return_lse, rope=rope if key is not None else None)
     out = out.permute(0, 2, 1, 3)
     return (out, lse) if return_lse else out
 

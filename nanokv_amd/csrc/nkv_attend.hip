@@ -785,7 +785,8 @@ namespace {
 
 // Resolve NKV_SCHEDULE_AUTO: key chunks once the queries span more than one
 // query tile (each history tile would otherwise be decoded once per tile)
-// and the codecs fit the chunk kernel; query tiles otherwise.
+// and the codecs fit the chunk kernel; query tiles otherwise.  Read-time RoPE
+// is built into the key-chunk kernel only, so it always takes key chunks.
 int resolve_schedule(const nkv_attend_args* a, int* schedule) {
     NKV_REQUIRE(a->schedule >= NKV_SCHEDULE_AUTO && a->schedule <= NKV_SCHEDULE_KEY_CHUNKS,
                 NKV_ERR_INVALID, "unknown schedule");
@@ -794,8 +795,12 @@ int resolve_schedule(const nkv_attend_args* a, int* schedule) {
         const bool fits = a->D == 128 &&
                           (a->N == 0 || (a->key.r % 64 == 0 && a->value.r % 64 == 0 &&
                                          a->key.group % 32 == 0 && a->value.group % 32 == 0));
-        sch = (fits && a->Q > AT_BM) ? NKV_SCHEDULE_KEY_CHUNKS : NKV_SCHEDULE_QUERY_TILES;
+        sch = (fits && (a->Q > AT_BM || a->rope)) ? NKV_SCHEDULE_KEY_CHUNKS
+                                                  : NKV_SCHEDULE_QUERY_TILES;
     }
+    NKV_REQUIRE(!a->rope || sch == NKV_SCHEDULE_KEY_CHUNKS, NKV_ERR_UNSUPPORTED,
+                "read-time RoPE needs the key-chunk schedule (D = 128, ranks that are "
+                "multiples of 64, scale groups that are multiples of 32)");
     *schedule = sch;
     return NKV_OK;
 }

@@ -81,6 +81,7 @@ struct ChunkParams {
     uint16_t* out;
     int64_t o_sb, o_st, o_sh;
     float* lse;
+    RopeDev rope;       // RoPE of the history keys (cs_t null: none)
 };
 
 // Codec row of attended history key `key`; rows outside the codec are
@@ -258,6 +259,37 @@ __device__ __forceinline__ void load_k_center_rows8(u32x4 (&v)[DK / 16], const C
 // decoder-slice ring and code/scale ring are those of decode_codec; each of
 // the eight waves copies WIDTH/64 KB of every slice (for WIDTH = 32 waves
 // 4-7 repeat waves 0-3's pieces: the same bytes to the same place).
+// Read-time RoPE of the wave's 32 decoded keys in the K tile (after their
+// bias and centers): lane half hf rotates pairs [WIDTH/4 * hf, +WIDTH/4) of key
+// 32 * wave + l32 at the position of its codec row.  The wave's LDS
+// operations stay in order, so no barrier separates this from the epilogue.
+template <int WIDTH, int KROW>
+__device__ __forceinline__ void rope_k_rows(uint16_t* ktile, const ChunkParams& p, int h,
+                                            int64_t tok0, int valid, int wave, int lane) {
+    constexpr int HP = WIDTH / 4;  // pairs per lane
+    const int hf = lane >> 5, kt = 32 * wave + (lane & 31);
+    const RopeRows rr = rope_rows(p.rope, history_row(p, tok0 + (kt < valid ? kt : 0)));
+    uint16_t* krow = ktile + kt * KROW + 2 * HP * hf;
+    const int32_t* pmap = p.rope.pairs ? p.rope.pairs + (int64_t)h * (WIDTH / 2) + HP * hf
+                                       : nullptr;
+    // every table load of the lane is issued before the first rotation (the
+    // decode's accumulators are dead here), so their latencies overlap
+    double2 cs[HP];
+#pragma unroll
+    for (int e = 0; e < HP; ++e) {
+        const int pj = pmap ? pmap[e] : HP * hf + e;
+        cs[e] = *reinterpret_cast<const double2*>(rope_entry(p.rope, rr, pj));
+    }
+#pragma unroll
+    for (int q = 0; q < HP / 4; ++q) {
+        const u32x4 kv = *reinterpret_cast<const u32x4*>(krow + 8 * q);
+        u32x4 y;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) y[e] = rope_pair(kv[e], cs[4 * q + e].x, cs[4 * q + e].y);
+        *reinterpret_cast<u32x4*>(krow + 8 * q) = y;
+    }
+}
+
 template <int CODEC, bool HAS_C, int WIDTH, int KROW, typename Pre>
 __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, const ChunkCodec& c,
                                               const ChunkParams& p, int b, int h, int64_t tok0,
@@ -418,6 +450,8 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
                 *slot = r;
             }
         }
+        if (p.rope.cs_t || p.rope.cs_h || p.rope.cs_w)
+            rope_k_rows<WIDTH, KROW>(ktile, p, h, tok0, valid, wave, lane);
     } else {
         // acc[dt] element i: key 32*wave + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32.
         // The centers of keys t0 .. t0+3 at column d come from one LDS
@@ -897,6 +931,7 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.o_st = d.o_st;
     p.o_sh = d.o_sh;
     p.lse = d.lse;
+    p.rope = d.rope;
 
     const int64_t blocks = (int64_t)d.B * d.H *
                            (p.nch_hist + (int64_t)(p.nch_total - p.nch_hist) * p.cur_splits);
@@ -976,7 +1011,14 @@ int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace
                         size_t workspace_bytes) {
     int rc = chunk_check(a);
     if (rc) return rc;
-    return chunk_launch(s, desc_from(a), workspace, workspace_bytes);
+    ChunkLaunchDesc d = desc_from(a);
+    if (a->rope) {
+        rc = rope_from_abi(a->rope, a->D, &d.rope);
+        if (rc) return rc;
+        NKV_REQUIRE(a->N <= a->rope->n_frames * (int64_t)a->rope->grid_h * a->rope->grid_w,
+                    NKV_ERR_INVALID, "more history tokens than the RoPE frames cover");
+    }
+    return chunk_launch(s, d, workspace, workspace_bytes);
 }
 
 }  // namespace nkv

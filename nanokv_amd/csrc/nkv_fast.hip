@@ -184,6 +184,7 @@ int validate(const nkv_fast_args* f) {
     NKV_REQUIRE(a.B >= 1 && a.H >= 1 && a.D == 128, NKV_ERR_UNSUPPORTED,
                 "fast attend supports D == 128");
     NKV_REQUIRE(a.Q >= 0 && a.N >= 0 && a.Nc >= 0, NKV_ERR_INVALID, "negative length");
+    NKV_REQUIRE(!a.rope, NKV_ERR_UNSUPPORTED, "fast attend does not apply RoPE");
     NKV_REQUIRE(f->n_protect >= 0 && f->n_low >= 0 && f->n_protect <= a.N && f->n_low <= a.N,
                 NKV_ERR_INVALID, "protected/low row counts out of range");
     NKV_REQUIRE(f->n_protect == 0 || f->protect_rows, NKV_ERR_INVALID, "protect_rows missing");

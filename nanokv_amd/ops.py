@@ -7,6 +7,7 @@ path: tensors must live on the GPU and the HIP library must be built.
 """
 from __future__ import annotations
 
+import ctypes
 import math
 from ctypes import byref
 from dataclasses import dataclass
@@ -18,7 +19,7 @@ from . import _lib
 from ._lib import (NKV_DTYPE_BF16, NKV_DTYPE_FP16, NKV_QUANT_BF16, NKV_QUANT_FP32,
                    NKV_SCHEDULE_AUTO, NKV_SCHEDULE_KEY_CHUNKS, NKV_SCHEDULE_QUERY_TILES,
                    NkvAttendArgs, NkvCodec, NkvDecodeArgs, NkvEncodeArgs, NkvFastArgs,
-                   NkvReaderGroup, check, lib)
+                   NkvReaderGroup, NkvRope, check, lib)
 
 _SCALE_CODES = {torch.bfloat16: NKV_DTYPE_BF16, torch.float16: NKV_DTYPE_FP16}
 _QUANT_CODES = {"fp32": NKV_QUANT_FP32, "bf16": NKV_QUANT_BF16}
@@ -328,12 +329,120 @@ def _attend_args(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional
     return args, out, lse, device
 
 
+def rope_bands(D: int, end: int = 1024, theta: float = 10000.0):
+    """The temporal, row and column RoPE frequency bands of a D-wide head,
+    complex128 on the CPU: t [end, pt], h [end, ph], w [end, pw] with
+    ph = pw = (D // 3) // 2 and pt = D / 2 - ph - pw.  Entry [n, i] is
+    exp(1j * n * theta^(-2i / dim)) for the band's width dim (the tables of
+    precompute_freqs_cis_3d, wan_video_dit.py:168-182; the angles are formed
+    and rounded as there, so the rotations agree to the last bit)."""
+    def band(dim: int) -> torch.Tensor:
+        inv = 1.0 / (theta ** (torch.arange(0, dim, 2)[: dim // 2].double() / dim))
+        angle = torch.outer(torch.arange(end), inv)
+        return torch.polar(torch.ones_like(angle), angle)
+    third = D // 3
+    return band(D - 2 * third), band(third), band(third)
+
+
+@dataclass
+class Rope:
+    """Read-time RoPE positions (nkv_rope) on the device: fp64 (cos, sin)
+    bands cs_t [n_t, pt, 2], cs_h [grid_h, ph, 2], cs_w [grid_w, pw, 2], and
+    frame_pos int32 [n_frames], the cs_t row of each frame of codec rows
+    (frame f holds rows f*grid_h*grid_w .. +grid_h*grid_w, row-major)."""
+    cs_t: torch.Tensor
+    cs_h: torch.Tensor
+    cs_w: torch.Tensor
+    frame_pos: torch.Tensor
+    grid_h: int
+    grid_w: int
+
+    @classmethod
+    def from_bands(cls, bands, temporal_positions, grid_h: int, grid_w: int,
+                   device: torch.device, disable_t: bool = False) -> "Rope":
+        """Positions of frames at the given temporal positions (one per frame)
+        on a grid_h x grid_w token grid, as _kv_freqs builds them
+        (pipelines/wan_video.py:3322-3341).  disable_t: identity temporal band
+        (prope_disable_t_rope, wan_video_dit.py:276-283)."""
+        t, h, w = bands
+        pos = torch.as_tensor(list(temporal_positions), dtype=torch.int64)
+        if pos.numel() == 0:
+            raise ValueError("RoPE needs at least one frame")
+        if int(pos.min()) < 0 or int(pos.max()) >= t.shape[0]:
+            raise ValueError("temporal position outside the frequency table")
+        if grid_h > h.shape[0] or grid_w > w.shape[0]:
+            raise ValueError("token grid larger than the frequency tables")
+        used, frame_pos = torch.unique(pos, return_inverse=True)
+        cs_t = torch.view_as_real(t[used]).contiguous()
+        if disable_t:
+            cs_t = torch.zeros_like(cs_t)
+            cs_t[..., 0] = 1.0
+        return cls(cs_t=cs_t.to(device), cs_h=torch.view_as_real(h[:grid_h]).contiguous().to(device),
+                   cs_w=torch.view_as_real(w[:grid_w]).contiguous().to(device),
+                   frame_pos=frame_pos.to(torch.int32).to(device), grid_h=int(grid_h),
+                   grid_w=int(grid_w))
+
+    @property
+    def pairs(self) -> int:
+        return int(self.cs_t.shape[1] + self.cs_h.shape[1] + self.cs_w.shape[1])
+
+    @property
+    def rows(self) -> int:
+        """Codec rows the frames cover."""
+        return int(self.frame_pos.numel()) * self.grid_h * self.grid_w
+
+    def struct(self) -> NkvRope:
+        for name in ("cs_t", "cs_h", "cs_w"):
+            t = getattr(self, name)
+            _contig(t, torch.float64, name)
+            if t.dim() != 3 or t.shape[2] != 2:
+                raise ValueError(f"{name} must be [n, pairs, 2] float64")
+        _contig(self.frame_pos, torch.int32, "frame_pos")
+        _require_gpu(self.cs_t, self.cs_h, self.cs_w, self.frame_pos)
+        if self.cs_h.shape[0] < self.grid_h or self.cs_w.shape[0] < self.grid_w:
+            raise ValueError("cs_h / cs_w have fewer rows than the token grid")
+        r = NkvRope()
+        r.cs_t, r.cs_h, r.cs_w = (self.cs_t.data_ptr(), self.cs_h.data_ptr(),
+                                  self.cs_w.data_ptr())
+        r.frame_pos, r.n_frames = self.frame_pos.data_ptr(), int(self.frame_pos.numel())
+        r.n_t = int(self.cs_t.shape[0])
+        r.pt, r.ph, r.pw = (int(self.cs_t.shape[1]), int(self.cs_h.shape[1]),
+                            int(self.cs_w.shape[1]))
+        r.grid_h, r.grid_w = self.grid_h, self.grid_w
+        return r
+
+
+def rope_apply(x: torch.Tensor, rope: Rope, rows: Optional[torch.Tensor] = None,
+               out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """RoPE of x [B, S, H, D] bf16 at the positions of codec rows rows[s]
+    (int32 [S]; None: row s), as rope_apply (wan_video_dit.py:185-192) with
+    the frequencies of rope (nkv_rope_apply).  out may be x."""
+    device = _require_gpu(x, rows, out)
+    if x.dtype != torch.bfloat16 or x.dim() != 4 or x.stride(3) != 1:
+        raise ValueError("x must be bf16 [B, S, H, D] with contiguous D")
+    B, S, H, D = (int(v) for v in x.shape)
+    if rows is not None:
+        _contig(rows, torch.int32, "rows")
+        if rows.numel() != S:
+            raise ValueError("rows must hold one codec row per position s")
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != torch.bfloat16 or out.stride(3) != 1:
+        raise ValueError("out must match x")
+    r = rope.struct()
+    check("nkv_rope_apply", lib().nkv_rope_apply(
+        _stream(device), byref(r), B, S, H, D, x.data_ptr(), x.stride(0), x.stride(1),
+        x.stride(2), _ptr(rows), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)))
+    return out
+
+
 def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
            key: Optional[Codec] = None, value: Optional[Codec] = None, *,
            softmax_scale: Optional[float] = None, return_lse: bool = True,
            splits: int = 0, out: Optional[torch.Tensor] = None,
            kernel_events: Optional[tuple[int, int]] = None,
-           workspace: Optional[torch.Tensor] = None, schedule: str = "auto"):
+           workspace: Optional[torch.Tensor] = None, schedule: str = "auto",
+           rope: Optional[Rope] = None):
     """Fused decode+attention (see nkv_attend).
 
     q [B, Q, H, D] bf16; k_cur/v_cur [B, Nc, H, D] bf16 or None; key/value
@@ -342,6 +451,8 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
     hipEvent_t handles recorded around the fused kernel.  workspace: optional
     preallocated uint8 buffer of at least nkv_attend_workspace_size bytes.
     schedule: "auto", "query_tiles" or "key_chunks" (nkv_schedule).
+    rope: read-time RoPE of the history keys at their codec rows (q and
+    k_cur are taken as already rotated); runs on the key-chunk schedule.
     """
     if schedule not in SCHEDULES:
         raise ValueError(f"schedule must be one of {sorted(SCHEDULES)}")
@@ -349,6 +460,10 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
                                           return_lse)
     args.splits = int(splits)
     args.schedule = SCHEDULES[schedule]
+    rope_struct = None
+    if rope is not None:
+        rope_struct = rope.struct()
+        args.rope = ctypes.pointer(rope_struct)
     if kernel_events is not None:
         args.ev_kernel_begin, args.ev_kernel_end = kernel_events
     need = lib().nkv_attend_workspace_size(byref(args))

@@ -43,6 +43,15 @@ Pinning (the independent check that fixes each function; see tests/):
                                small (count, recent, stride, sink)
   hybrid_attention            identity readers reduce it exactly to the full
                                decode-then-attend path (CN/reader_tools.py:7-35)
+  rope_bands / kv_freqs       the closed form exp(1j * n * theta^(-2i/dim))
+                               element by element against torch.polar; band
+                               widths for several D; position 0 = identity;
+                               the layout against a hand-built token
+  rope_apply                  the RoPE identities in fp64: every pair keeps its
+                               norm, rotations compose (angle addition), the
+                               score q(m) . k(n) depends only on n - m; torch's
+                               view_as_complex product (the reference's form)
+                               agrees after rounding to bf16
 """
 from __future__ import annotations
 
@@ -311,7 +320,7 @@ def merge(out_a, lse_a, out_b, lse_b):
 
 def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Optional[dict],
                   scale: float, heads: Optional[Sequence[int]] = None, D: int = 128,
-                  dtype=np.float64):
+                  dtype=np.float64, key_freqs: Optional[np.ndarray] = None):
     """Reference decode-then-SDPA path for one batch item.
 
     q [Q, H, D] bf16 bits; k_cur/v_cur [Nc, H, D] bf16 bits or None; key/value
@@ -319,6 +328,8 @@ def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Op
     group, scale_dtype, ids, centers_bf16, mean) or None.  Returns
     (out [Q, H', D], lse [H', Q]) for the selected heads, computed in `dtype`
     (float64 for parity checks; float32 is the reference's CPU arithmetic).
+    key_freqs [N, D/2] complex128: read-time RoPE of the decoded history keys
+    (wan_video_dit.py:538-546), applied before attention.
     """
     q = bf16_to_f32(q_bf16)
     Qn, H = q.shape[0], q.shape[1]
@@ -326,7 +337,10 @@ def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Op
     cols = np.concatenate([np.arange(h * D, (h + 1) * D) for h in heads])
     ks, vs = [], []
     if key is not None:
-        kd = bf16_to_f32(decode(**key, columns=cols, dtype=dtype))
+        kbits = decode(**key, columns=cols, dtype=dtype)
+        if key_freqs is not None:
+            kbits = rope_apply(kbits.reshape(-1, len(heads), D), key_freqs)
+        kd = bf16_to_f32(kbits)
         vd = bf16_to_f32(decode(**value, columns=cols, dtype=dtype))
         ks.append(kd.reshape(-1, len(heads), D))
         vs.append(vd.reshape(-1, len(heads), D))
@@ -341,6 +355,55 @@ def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Op
         v = np.zeros((len(heads), 0, D))
     out, lse = attention(q[:, heads].transpose(1, 0, 2), k, v, scale, dtype)
     return out.transpose(1, 0, 2), lse
+
+
+# ------------------------------------------------------------------- RoPE
+def rope_bands(D: int, end: int, theta: float = 10000.0):
+    """precompute_freqs_cis_3d (wan_video_dit.py:168-182): the temporal, row
+    and column bands of a D-wide head as complex128 [end, pairs]; row n of a
+    band of width dim is exp(1j * n * theta^(-2i/dim)), i < dim / 2
+    (precompute_freqs_cis, wan_video_dit.py:177-182)."""
+    def band(dim):
+        inv = 1.0 / (theta ** (np.arange(0, dim, 2)[: dim // 2].astype(np.float64) / dim))
+        ang = np.outer(np.arange(end, dtype=np.float64), inv)
+        return np.cos(ang) + 1j * np.sin(ang)
+    third = D // 3
+    return band(D - 2 * third), band(third), band(third)
+
+
+def kv_freqs(bands, temporal_positions, grid_h: int, grid_w: int) -> np.ndarray:
+    """_kv_freqs (pipelines/wan_video.py:3322-3341): per-token frequencies
+    [frames * grid_h * grid_w, pairs] complex128, frame-major, then row, then
+    column: [t[p], h[row], w[col]] concatenated over the pair axis."""
+    t, h, w = bands
+    parts = []
+    for p in temporal_positions:
+        tt = np.broadcast_to(t[int(p)], (grid_h, grid_w, t.shape[1]))
+        hh = np.broadcast_to(h[:grid_h, None, :], (grid_h, grid_w, h.shape[1]))
+        ww = np.broadcast_to(w[None, :grid_w, :], (grid_h, grid_w, w.shape[1]))
+        parts.append(np.concatenate([tt, hh, ww], axis=-1).reshape(grid_h * grid_w, -1))
+    return np.concatenate(parts, 0)
+
+
+def rope_rotate(x, freqs) -> np.ndarray:
+    """The fp64 rotation of rope_apply (wan_video_dit.py:185-192) before the
+    cast: x [S, H, D] (bf16 bits or float) times freqs [S, D/2] per complex
+    pair (2i, 2i+1), each product and sum rounded separately."""
+    x = np.asarray(x)
+    xf = bf16_to_f32(x).astype(np.float64) if x.dtype == np.uint16 else x.astype(np.float64)
+    a, b = xf[..., 0::2], xf[..., 1::2]
+    c = np.real(freqs)[:, None, :]
+    s = np.imag(freqs)[:, None, :]
+    y = np.empty_like(xf)
+    y[..., 0::2] = a * c - b * s
+    y[..., 1::2] = a * s + b * c
+    return y
+
+
+def rope_apply(x_bf16, freqs) -> np.ndarray:
+    """rope_apply (wan_video_dit.py:185-192): bf16 bits [S, H, D] rotated in
+    fp64 and cast back (float64 -> float32 -> bfloat16, torch's cast)."""
+    return f32_to_bf16(rope_rotate(x_bf16, freqs).astype(np.float32))
 
 
 # ----------------------------------------------------------------- a13

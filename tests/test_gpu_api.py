@@ -97,3 +97,41 @@ def test_attention_lse_and_merge(dev):
     assert diff <= 2e-2 and cos >= 0.9995
     oe, le = codec_native.attention_lse(q, k[:, :, :0], v[:, :, :0])
     assert torch.all(oe == 0) and torch.all(torch.isneginf(le))
+
+
+def test_history_attention_with_read_time_rope(dev, monkeypatch):
+    """codec_history_attention(rope=kv_rope(...)) against the reference's order
+    of operations: decode_pair_values, rope_apply(cache_k_pre, cache_freqs),
+    attention (wan_video_dit.py:497-627)."""
+    layer = 5
+    sh, lay = _setup(dev, layer, True, monkeypatch)
+    cache_k = cache_v = None
+    chunks_k, chunks_v = [], []
+    for c in range(3):
+        k = synth.history_rows(sh, lay.centers_k, 40, seed=30 + c).to(dev)[None].to(torch.bfloat16)
+        v = synth.history_rows(sh, lay.centers_v, 40, seed=40 + c).to(dev)[None].to(torch.bfloat16)
+        pk, pv = nc.encode_tensor("k", layer, k), nc.encode_tensor("v", layer, v)
+        chunks_k.append(pk)
+        chunks_v.append(pv)
+        cache_k, cache_v = nc.concat_values(cache_k, pk), nc.concat_values(cache_v, pv)
+    from nanokv_amd import ops
+    freqs = ops.rope_bands(D, 64)  # the model's (temporal, row, column) bands
+    positions, gh, gw = [9, 4, 12], 5, 8  # three cached frames of 5 x 8 tokens
+    rope = codec_native.kv_rope(freqs, positions, gh, gw, dev)
+    g = torch.Generator().manual_seed(11)
+    q = (torch.randn(1, H, 37, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev)
+    kc = torch.randn(1, H, 9, D, generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn(1, H, 9, D, generator=g).to(torch.bfloat16).to(dev)
+    out, lse = codec_native.codec_history_attention(q, cache_k, cache_v, kc, vc,
+                                                    return_lse=True, rope=rope)
+    ref_k = np.concatenate([_oracle_rows(p, dev) for p in chunks_k], 0)
+    ref_v = np.concatenate([_oracle_rows(p, dev) for p in chunks_v], 0)
+    table = orc.kv_freqs(tuple(b.numpy() for b in freqs), positions, gh, gw)
+    k_rot = orc.bf16_to_f32(orc.rope_apply(orc.f32_to_bf16(ref_k.reshape(120, H, D)), table))
+    kk = np.concatenate([k_rot, orc.bf16_to_f32(u16(kc[0].permute(1, 0, 2)))], 0)
+    vv = np.concatenate([ref_v.reshape(120, H, D), orc.bf16_to_f32(u16(vc[0].permute(1, 0, 2)))], 0)
+    ro, rl = orc.attention(orc.bf16_to_f32(u16(q[0])), kk.transpose(1, 0, 2),
+                           vv.transpose(1, 0, 2), D ** -0.5)
+    diff, cos = max_abs_cos(out[0].float().cpu().numpy(), ro)
+    assert diff <= 2e-2 and cos >= 0.9995, (diff, cos)
+    assert np.abs(lse[0].cpu().numpy() - rl).max() < 2e-3
