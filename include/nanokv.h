@@ -299,6 +299,11 @@ typedef struct nkv_reader_group {
     const uint16_t* v_read;       /* [num_heads, D, rV] bf16 */
     const uint16_t* k_affine;     /* [num_heads, D, d] bf16 or NULL */
     const uint16_t* v_affine;     /* [num_heads, D, D] bf16 or NULL */
+    /* RoPE of the reader keys and queries (rope_selected, CN/core.py:75-91):
+     * [num_heads, d/2] int32, the original pair (indices[:, 0::2] / 2) of each
+     * pair of the d-wide key/query; NULL = pair j (d == D).  Used only when
+     * the call applies RoPE. */
+    const int32_t* rope_pairs;
 } nkv_reader_group;
 
 /*
@@ -313,8 +318,13 @@ typedef struct nkv_reader_group {
  * native partition), out and lse, as for nkv_attend (its N is the codec's
  * token count; splits and schedule are ignored).  Every head should belong
  * to exactly one group (CN/core.py:213-215); a head in no group keeps the
- * native partition alone.  attend.rope must be NULL (RoPE of the reader
- * partitions is not built).  Returns NKV_ERR_UNSUPPORTED for D != 128.
+ * native partition alone.  Returns NKV_ERR_UNSUPPORTED for D != 128.
+ * RoPE (attend.rope != NULL, CN/mg35.py:207-214, 305-336): the native
+ * partition's history keys are rotated at their codec rows and attend.q is
+ * taken as already rotated; each reader group forms its queries from the
+ * pre-RoPE queries q_pre, q_low = bf16(q_pre . q_reduce), and rotates the
+ * pairs rope_pairs of q_low at the query positions q_rope (query t at row t)
+ * and of k_low at the codec rows' positions (attend.rope).
  */
 typedef struct nkv_fast_args {
     nkv_attend_args attend;
@@ -325,6 +335,9 @@ typedef struct nkv_fast_args {
     int num_groups;
     int _pad;
     const nkv_reader_group* groups;  /* host array of num_groups */
+    const uint16_t* q_pre;        /* [B, Q, H, D] bf16 pre-RoPE queries (with RoPE) */
+    int64_t qp_sb, qp_st, qp_sh;
+    const nkv_rope* q_rope;       /* query positions (with RoPE), host pointer */
 } nkv_fast_args;
 
 /* Bytes of workspace nkv_fast_attend needs for these arguments. */

@@ -90,7 +90,7 @@ class NkvReaderGroup(Structure):
     _fields_ = [
         ("num_heads", c_int), ("d", c_int), ("heads", c_void_p), ("q_reduce", c_void_p),
         ("k_read", c_void_p), ("v_read", c_void_p), ("k_affine", c_void_p),
-        ("v_affine", c_void_p),
+        ("v_affine", c_void_p), ("rope_pairs", c_void_p),
     ]
 
 
@@ -99,6 +99,8 @@ class NkvFastArgs(Structure):
         ("attend", NkvAttendArgs), ("protect_rows", c_void_p), ("n_protect", c_int64),
         ("low_rows", c_void_p), ("n_low", c_int64), ("num_groups", c_int), ("_pad", c_int),
         ("groups", POINTER(NkvReaderGroup)),
+        ("q_pre", c_void_p), ("qp_sb", c_int64), ("qp_st", c_int64), ("qp_sh", c_int64),
+        ("q_rope", POINTER(NkvRope)),
     ]
 
 

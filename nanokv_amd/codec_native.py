@@ -169,11 +169,22 @@ class ReaderGroup:
         self.k_read = dev(state["k_read"])
         self.v_read = dev(state["v_read"])
         self.heads_dev = self.heads.to(device=device, dtype=torch.int32).contiguous()
+        # RoPE acts on complete original pairs only (rope_selected, CN:75-91):
+        # reader dims (2j, 2j+1) must be original dims (2p, 2p+1); pair j then
+        # rotates with original pair p
+        ind = self.indices
+        self.rope_complete = bool(torch.equal(ind[:, 1::2], ind[:, ::2] + 1)
+                                  and not bool((ind[:, ::2] % 2).any()))
+        self.rope_pairs = (ind[:, ::2] // 2).to(device=device, dtype=torch.int32).contiguous() \
+            if self.rope_complete else None
 
-    def tensors(self) -> ops.ReaderTensors:
+    def tensors(self, rope: bool = False) -> ops.ReaderTensors:
+        if rope and not self.rope_complete:
+            raise ValueError("RoPE mapping must retain complete original pairs")
         return ops.ReaderTensors(heads=self.heads_dev, d=self.d, k_read=self.k_read,
                                  v_read=self.v_read, q_reduce=self.q_reduce,
-                                 k_affine=self.k_affine, v_affine=self.v_affine)
+                                 k_affine=self.k_affine, v_affine=self.v_affine,
+                                 rope_pairs=self.rope_pairs if rope else None)
 
 
 class ReaderLayer:
@@ -193,13 +204,20 @@ class ReaderLayer:
 def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
                            k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
                            reader: ReaderLayer, protect: torch.Tensor, *,
-                           scale: Optional[float] = None, return_lse: bool = False):
+                           scale: Optional[float] = None, return_lse: bool = False,
+                           rope: Optional[ops.Rope] = None,
+                           q_pre: Optional[torch.Tensor] = None,
+                           q_rope: Optional[ops.Rope] = None):
     """NanoKV-Fast history attention of q [B, H, Q, D]: the protected history
     tokens (bool mask [N] over the cache) and the current chunk are attended
     at full width by every head (mg35.py:192-303), the other history tokens
     through each head's reader group (mg35.py:315-347), and the two are
     merged by LSE (CN:33-42, 308).  Everything is fused in nkv_fast_attend;
-    no K/V row is materialised.  Scale: native_dim ** -0.5 (CN:287)."""
+    no K/V row is materialised.  Scale: native_dim ** -0.5 (CN:287).
+    RoPE (mg35.py:207-214, 305-336): rope = kv_rope(...) of the cached
+    frames; q is then the rotated query, q_pre [B, H, Q, D] the pre-RoPE
+    query that the reader groups project, and q_rope the positions of the
+    current chunk's queries (query t at row t)."""
     device = q.device
     B, H, Qn, D = (int(x) for x in q.shape)
     if H != reader.heads or D != reader.native_dim:
@@ -213,9 +231,14 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     qq = q.to(torch.bfloat16).permute(0, 2, 1, 3)
     kc = None if k_cur is None else k_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
     vc = None if v_cur is None else v_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
+    qp = None
+    if rope is not None:
+        if q_pre is None or q_rope is None:
+            raise ValueError("RoPE needs q_pre and q_rope for the reader groups")
+        qp = q_pre.to(torch.bfloat16).permute(0, 2, 1, 3)
     out, lse = ops.fast_attend(qq, kc, vc, key, value, protect_rows, low_rows,
-                               [g.tensors() for g in reader.groups],
+                               [g.tensors(rope=rope is not None) for g in reader.groups],
                                softmax_scale=D ** -0.5 if scale is None else scale,
-                               return_lse=return_lse)
+                               return_lse=return_lse, rope=rope, q_pre=qp, q_rope=q_rope)
     out = out.permute(0, 2, 1, 3)
     return (out, lse) if return_lse else out

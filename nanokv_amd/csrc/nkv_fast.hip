@@ -1,6 +1,10 @@
 // nkv_fast.hip -- NanoKV-Fast mixed-dimensional history attention for gfx950
 // (nkv_fast_attend): hybrid_attention (CN/core.py:278-310) with the partition
 // reads of maybe_attention (CN/mg35.py:100-357), fused per partition.
+// With RoPE, the history keys of both partitions are rotated in-kernel after
+// decode (the low partition on the reader's retained pairs) and the reader
+// queries are formed from the pre-RoPE queries and rotated likewise
+// (CN/mg35.py:207-214, 305-336).
 //
 // Per layer call:
 //  1. native partition: every head attends its queries to the protected
@@ -164,6 +168,25 @@ __global__ void __launch_bounds__(256) group_merge_kernel(
     if (lse_out && part == 0) lse_out[((int64_t)b * H + h) * Q + q] = l;
 }
 
+// RoPE of the reader queries in place (rope_selected, CN/core.py:75-91):
+// q_low [B, Q, nh, d] bf16, pair j of head i rotated by original pair
+// pairs[i * d/2 + j] (null: j) at the position of query t (row t of the
+// query positions).  One thread per pair.
+__global__ void __launch_bounds__(256) rope_low_kernel(uint16_t* q_low, int B, int64_t Q, int nh,
+                                                       int d, RopeDev pos) {
+    const int hp = d / 2;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= (int64_t)B * Q * nh * hp) return;
+    const int j = (int)(tid % hp);
+    const int64_t row = tid / hp;  // (b, t, i)
+    const int i = (int)(row % nh);
+    const int64_t t = (row / nh) % Q;
+    const int pj = pos.pairs ? pos.pairs[(int64_t)i * hp + j] : j;
+    const double* cs = rope_entry(pos, rope_rows(pos, t), pj);
+    uint32_t* w = reinterpret_cast<uint32_t*>(q_low) + tid;
+    *w = rope_pair(*w, cs[0], cs[1]);
+}
+
 namespace {
 
 constexpr size_t WS_ALIGN = 256;
@@ -184,7 +207,26 @@ int validate(const nkv_fast_args* f) {
     NKV_REQUIRE(a.B >= 1 && a.H >= 1 && a.D == 128, NKV_ERR_UNSUPPORTED,
                 "fast attend supports D == 128");
     NKV_REQUIRE(a.Q >= 0 && a.N >= 0 && a.Nc >= 0, NKV_ERR_INVALID, "negative length");
-    NKV_REQUIRE(!a.rope, NKV_ERR_UNSUPPORTED, "fast attend does not apply RoPE");
+    if (a.rope) {
+        RopeDev chk;
+        int rc = rope_from_abi(a.rope, a.D, &chk);
+        if (rc) return rc;
+        NKV_REQUIRE(a.N <= a.rope->n_frames * (int64_t)a.rope->grid_h * a.rope->grid_w,
+                    NKV_ERR_INVALID, "more history tokens than the RoPE frames cover");
+        if (f->n_low > 0 && f->num_groups > 0) {
+            NKV_REQUIRE(f->q_pre && f->q_rope, NKV_ERR_INVALID,
+                        "RoPE of the reader groups needs q_pre and q_rope");
+            NKV_REQUIRE(reinterpret_cast<uintptr_t>(f->q_pre) % 16 == 0 && f->qp_sb % 8 == 0 &&
+                            f->qp_st % 8 == 0 && f->qp_sh % 8 == 0,
+                        NKV_ERR_INVALID,
+                        "q_pre must be 16-byte aligned with strides divisible by 8");
+            rc = rope_from_abi(f->q_rope, a.D, &chk);
+            if (rc) return rc;
+            NKV_REQUIRE(a.Q <= f->q_rope->n_frames * (int64_t)f->q_rope->grid_h *
+                                   f->q_rope->grid_w,
+                        NKV_ERR_INVALID, "more queries than the query RoPE frames cover");
+        }
+    }
     NKV_REQUIRE(f->n_protect >= 0 && f->n_low >= 0 && f->n_protect <= a.N && f->n_low <= a.N,
                 NKV_ERR_INVALID, "protected/low row counts out of range");
     NKV_REQUIRE(f->n_protect == 0 || f->protect_rows, NKV_ERR_INVALID, "protect_rows missing");
@@ -208,6 +250,8 @@ int validate(const nkv_fast_args* f) {
         NKV_REQUIRE(G.q_reduce || G.d == a.D, NKV_ERR_INVALID, "identity q_reduce needs d == D");
         NKV_REQUIRE(G.k_affine || G.d == a.D, NKV_ERR_INVALID, "identity k_affine needs d == D");
         NKV_REQUIRE(G.k_read && G.v_read, NKV_ERR_INVALID, "reader group needs k_read and v_read");
+        NKV_REQUIRE(!a.rope || G.rope_pairs || G.d == a.D, NKV_ERR_INVALID,
+                    "RoPE of a reader group narrower than D needs rope_pairs");
     }
     return NKV_OK;
 }
@@ -394,8 +438,16 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
     // one; the merges then update it in place
     float* lse_n = a.lse ? a.lse : reinterpret_cast<float*>(ws + L.lse_n);
 
+    RopeDev krope{}, qrope{};
+    if (a.rope) {
+        rope_from_abi(a.rope, a.D, &krope);
+        if (f->q_rope) rope_from_abi(f->q_rope, a.D, &qrope);
+    }
+
     // 1. native partition -> out, lse_n
-    rc = chunk_launch(s, native_desc(f, lse_n), ws + L.partials, part_bytes);
+    ChunkLaunchDesc nd = native_desc(f, lse_n);
+    nd.rope = krope;
+    rc = chunk_launch(s, nd, ws + L.partials, part_bytes);
     if (rc) return rc;
     // no low rows: the native partition is the whole attention
     if (f->n_low == 0) return NKV_OK;
@@ -405,10 +457,26 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
     for (int g = 0; g < f->num_groups; ++g) {
         const nkv_reader_group& G = f->groups[g];
         const int nh = G.num_heads, dd = G.d;
-        // q_low [B, Q, nh, d]
-        rc = project<false, false>(s, a.q, a.q_sb, a.q_st, a.q_sh, G.heads, a.H, G.q_reduce, D, dd, a.B,
-                                   nh, a.Q, ws + L.q_low[g], a.Q * nh * dd, dd, (int64_t)nh * dd);
+        // q_low [B, Q, nh, d]: from the pre-RoPE queries when RoPE is applied
+        // (then rotated on its retained pairs), else from q
+        uint16_t* q_low = reinterpret_cast<uint16_t*>(ws + L.q_low[g]);
+        if (a.rope)
+            rc = project<false, false>(s, f->q_pre, f->qp_sb, f->qp_st, f->qp_sh, G.heads, a.H,
+                                       G.q_reduce, D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
+                                       (int64_t)nh * dd);
+        else
+            rc = project<false, false>(s, a.q, a.q_sb, a.q_st, a.q_sh, G.heads, a.H, G.q_reduce,
+                                       D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
+                                       (int64_t)nh * dd);
         if (rc) return rc;
+        if (a.rope) {
+            RopeDev qp = qrope;
+            qp.pairs = G.rope_pairs;
+            const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 2);
+            rope_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(q_low, a.B, a.Q, nh,
+                                                                              dd, qp);
+            NKV_LAUNCH_CHECK();
+        }
         for (int cc = 0; cc < 2 && f->n_low > 0; ++cc) {
             const nkv_codec& c = cc ? a.value : a.key;
             const int width = cc ? D : dd;
@@ -430,7 +498,12 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
                 if (rc) return rc;
             }
         }
-        rc = chunk_launch(s, low_desc(f, g, ws, L), ws + L.partials, part_bytes);
+        ChunkLaunchDesc ld = low_desc(f, g, ws, L);
+        if (a.rope) {
+            ld.rope = krope;
+            ld.rope.pairs = G.rope_pairs;
+        }
+        rc = chunk_launch(s, ld, ws + L.partials, part_bytes);
         if (rc) return rc;
         const int64_t threads = (int64_t)a.B * a.Q * nh * (D / 8);
         group_merge_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(

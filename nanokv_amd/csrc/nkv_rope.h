@@ -50,8 +50,9 @@ __device__ __forceinline__ RopeRows rope_rows(const RopeDev& r, int64_t row64) {
     return rr;
 }
 
-// (cos, sin) of pair p (0 <= p < pt + ph + pw) of a row
+// (cos, sin) of pair p of a row (p is clamped into [0, pt + ph + pw))
 __device__ __forceinline__ const double* rope_entry(const RopeDev& r, const RopeRows& rr, int p) {
+    p = min(max(p, 0), r.pt + r.ph + r.pw - 1);
     return p < r.pt ? rr.t + 2 * p
                     : (p < r.pt + r.ph ? rr.h + 2 * (p - r.pt) : rr.w + 2 * (p - r.pt - r.ph));
 }

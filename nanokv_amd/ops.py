@@ -482,7 +482,8 @@ class ReaderTensors:
     """Device tensors of one NanoKV-Fast reader group (nkv_reader_group):
     heads int32 [nh]; k_read bf16 [nh, d, rK]; v_read bf16 [nh, D, rV];
     q_reduce / k_affine bf16 [nh, D, d] and v_affine bf16 [nh, D, D], each
-    None for the identity."""
+    None for the identity; rope_pairs int32 [nh, d/2], the original RoPE
+    pair of each reader pair (None: pair j, d == D)."""
     heads: torch.Tensor
     d: int
     k_read: torch.Tensor
@@ -490,6 +491,7 @@ class ReaderTensors:
     q_reduce: Optional[torch.Tensor] = None
     k_affine: Optional[torch.Tensor] = None
     v_affine: Optional[torch.Tensor] = None
+    rope_pairs: Optional[torch.Tensor] = None
 
     def struct(self, D: int, rK: int, rV: int) -> NkvReaderGroup:
         nh, d = int(self.heads.numel()), int(self.d)
@@ -510,13 +512,23 @@ class ReaderTensors:
         g.k_read, g.v_read = self.k_read.data_ptr(), self.v_read.data_ptr()
         g.q_reduce, g.k_affine, g.v_affine = (_ptr(self.q_reduce), _ptr(self.k_affine),
                                               _ptr(self.v_affine))
+        if self.rope_pairs is not None:
+            _contig(self.rope_pairs, torch.int32, "rope_pairs")
+            if tuple(self.rope_pairs.shape) != (nh, d // 2):
+                raise ValueError(f"rope_pairs must be [{nh}, {d // 2}]")
+            g.rope_pairs = self.rope_pairs.data_ptr()
         return g
 
 
 def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, softmax_scale, out,
-               return_lse):
+               return_lse, rope=None, q_pre=None, q_rope=None):
     args, out, lse, device = _attend_args(q, k_cur, v_cur, key, value, softmax_scale, out,
                                           return_lse)
+    keep = []  # ctypes structs the call points to
+    if rope is not None:
+        r = rope.struct()
+        keep.append(r)
+        args.rope = ctypes.pointer(r)
     _require_gpu(protect_rows, low_rows, *[g.heads for g in groups])
     _contig(protect_rows, torch.int32, "protect_rows")
     _contig(low_rows, torch.int32, "low_rows")
@@ -530,12 +542,23 @@ def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, soft
         structs[i] = g.struct(D, key.r, value.r)
     f.num_groups = len(groups)
     f.groups = structs
+    if rope is not None:
+        if q_pre is not None:
+            _require_gpu(q_pre)
+            if q_pre.dtype != torch.bfloat16 or tuple(q_pre.shape) != tuple(q.shape):
+                raise ValueError("q_pre must be bf16 with q's shape [B, Q, H, D]")
+            f.q_pre = q_pre.data_ptr()
+            f.qp_sb, f.qp_st, f.qp_sh = _strides_bthd(q_pre, "q_pre")
+        if q_rope is not None:
+            qr = q_rope.struct()
+            keep.append(qr)
+            f.q_rope = ctypes.pointer(qr)
     need = lib().nkv_fast_attend_workspace_size(byref(f))
     err = lib().nkv_last_error().decode()
     if need == 0 and err:
         raise _lib.NanoKVError("nkv_fast_attend_workspace_size", _lib.NKV_ERR_INVALID, err)
     # structs must stay alive while f points at them
-    return f, structs, need, out, lse, device
+    return f, (structs, keep), need, out, lse, device
 
 
 def fast_attend_workspace_size(q: torch.Tensor, k_cur: Optional[torch.Tensor],
@@ -552,17 +575,21 @@ def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[
                 groups: list, *, softmax_scale: Optional[float] = None,
                 return_lse: bool = True, out: Optional[torch.Tensor] = None,
                 kernel_events: Optional[tuple[int, int]] = None,
-                workspace: Optional[torch.Tensor] = None):
+                workspace: Optional[torch.Tensor] = None, rope: Optional[Rope] = None,
+                q_pre: Optional[torch.Tensor] = None, q_rope: Optional[Rope] = None):
     """NanoKV-Fast mixed-dimensional attention (see nkv_fast_attend).
 
     protect_rows / low_rows: int32 codec rows of the native and low
     partitions; groups: ReaderTensors covering every head once.  Returns
     (out [B, Q, H, D] bf16, lse [B, H, Q] fp32 or None).  kernel_events
-    bracket the native partition's attention kernel.
+    bracket the native partition's attention kernel.  rope: positions of the
+    codec rows (history keys rotated at read); then q is the rotated query,
+    q_pre [B, Q, H, D] the pre-RoPE query the reader groups project and
+    q_rope the queries' positions (query t at row t).
     """
     f, structs, need, out, lse, device = _fast_args(q, k_cur, v_cur, key, value, protect_rows,
                                                     low_rows, groups, softmax_scale, out,
-                                                    return_lse)
+                                                    return_lse, rope, q_pre, q_rope)
     if kernel_events is not None:
         f.attend.ev_kernel_begin, f.attend.ev_kernel_end = kernel_events
     if workspace is None or workspace.numel() < need:

@@ -463,7 +463,8 @@ def reader_read(codec: dict, rows, read_bf16, table_bf16, bias, dtype=np.float64
 
 def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_rows, low_rows,
                 groups: Sequence[dict], scale: float, heads: Optional[Sequence[int]] = None,
-                D: int = 128, dtype=np.float64):
+                D: int = 128, dtype=np.float64, key_freqs: Optional[np.ndarray] = None,
+                q_pre_bf16=None, q_freqs: Optional[np.ndarray] = None):
     """NanoKV-Fast for one batch item: hybrid_attention (CN/core.py:278-310)
     with maybe_attention's partitions (CN/mg35.py:192-348), identity lift.
 
@@ -473,7 +474,14 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
     reader_read of low_rows; merged by LSE (CN:33-42) into bf16.
     groups: dicts with heads, q_reduce, k_read, v_read, k_affine, v_affine
     (bf16 bits per head, None = identity).  Returns (out [Q, H', D] float32
-    of the bf16 result, lse [H', Q])."""
+    of the bf16 result, lse [H', Q]).
+
+    RoPE (key_freqs [N, D/2] of the codec rows, CN/mg35.py:207-214, 305-336):
+    the protected keys are rotated after decode (rope_apply); a group's
+    query is q_pre_bf16 [Q, H, D] projected, and it and k_low are rotated on
+    the retained pairs (rope_selected, CN/core.py:75-91) with original pair
+    rope_pairs[i][j] (group key; None: pair j), the query at q_freqs [Q, D/2].
+    q_bf16 is then the already rotated query of the native partition."""
     q = bf16_to_f32(q_bf16)
     Qn, H = q.shape[0], q.shape[1]
     heads = list(range(H)) if heads is None else list(heads)
@@ -486,6 +494,8 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
         if prot.size:
             kd = decode(**key, row_index=prot, columns=cols, dtype=dtype)
             vd = decode(**value, row_index=prot, columns=cols, dtype=dtype)
+            if key_freqs is not None:
+                kd = rope_apply(kd[:, None, :], key_freqs[prot])[:, 0]
             ks.append(bf16_to_f32(kd))
             vs.append(bf16_to_f32(vd))
         if k_cur_bf16 is not None:
@@ -498,15 +508,22 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
         grp = [(g, list(g["heads"]).index(h)) for g in groups if h in list(g["heads"])]
         if grp and low.size:
             g, i = grp[0]
-            qh = q[:, h]
+            qh = q[:, h] if key_freqs is None else bf16_to_f32(q_pre_bf16)[:, h]
             if g.get("q_reduce") is not None:
                 qr = bf16_to_f32(g["q_reduce"][i]).astype(dtype)
                 qh = bf16_to_f32(f32_to_bf16((qh.astype(dtype) @ qr).astype(np.float32)))
+            if key_freqs is not None:
+                rp = g.get("rope_pairs")
+                pairs = np.arange(qh.shape[1] // 2) if rp is None else np.asarray(rp[i])
+                qh = bf16_to_f32(rope_apply(f32_to_bf16(qh)[:, None, :], q_freqs[:, pairs])[:, 0])
             kt, kb = reader_tables(key.get("centers_bf16"), key.get("mean"), h,
                                    None if g.get("k_affine") is None else g["k_affine"][i], D, dtype)
             vt, vb = reader_tables(value.get("centers_bf16"), value.get("mean"), h,
                                    None if g.get("v_affine") is None else g["v_affine"][i], D, dtype)
-            kl = bf16_to_f32(reader_read(key, low, g["k_read"][i], kt, kb, dtype))
+            kl = reader_read(key, low, g["k_read"][i], kt, kb, dtype)
+            if key_freqs is not None:
+                kl = rope_apply(kl[:, None, :], key_freqs[low][:, pairs])[:, 0]
+            kl = bf16_to_f32(kl)
             vl = bf16_to_f32(reader_read(value, low, g["v_read"][i], vt, vb, dtype))
             ol, ll = attention(qh[None], kl[None], vl[None], scale, dtype)
             ol = bf16_to_f32(f32_to_bf16(ol[0].astype(np.float32)))

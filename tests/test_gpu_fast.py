@@ -180,3 +180,69 @@ def test_fast_cfg3_shape_subset_heads(dev):
     diff, cos = max_abs_cos(out[0][:, heads].float().cpu().numpy(), ref)
     assert diff <= MAX_ABS and cos >= MIN_COS, (diff, cos)
     assert np.abs(lse[0][heads].cpu().numpy() - ref_lse).max() < 2e-3
+
+
+@pytest.mark.parametrize("d", [32, 64])
+def test_fast_rope_matches_oracle(dev, d):
+    """RoPE through every partition (CN/mg35.py:207-214, 305-336): protected
+    keys rotated at their rows, reader queries from q_pre rotated on the
+    group's retained pairs, reader keys likewise; readers keep a random set
+    of complete original pairs."""
+    sc = Scenario(H=4, N=700, Q=150, Nc=64, rK=384, rV=256, G=32, C=16, with_mean=True, seed=d)
+    payload = _payload(sc, (1,), d)
+    rng = np.random.default_rng(d)
+    for g in payload["groups"]:
+        n, dd = g["indices"].shape
+        if dd == sc.D:
+            continue
+        pairs = np.stack([np.sort(rng.choice(sc.D // 2, dd // 2, replace=False)) for _ in range(n)])
+        g["indices"] = torch.from_numpy(np.stack([2 * pairs, 2 * pairs + 1], 2).reshape(n, dd))
+    reader = codec_native.ReaderLayer(payload, dev)
+    key, value = sc.codecs(dev)
+    bands = ops.rope_bands(sc.D, 64)
+    rope = ops.Rope.from_bands(bands, [3, 8], 10, 35, dev)          # 2 frames of 350 rows
+    q_rope = ops.Rope.from_bands(bands, [12], 10, 15, dev)          # the 150 queries
+    q_pre = sc.q.to(dev)
+    q = ops.rope_apply(q_pre, q_rope)
+    prot = np.arange(500, 700)
+    low = np.setdiff1d(np.arange(sc.N), prot)
+    pr = torch.from_numpy(prot.astype(np.int32)).to(dev)
+    lr = torch.from_numpy(low.astype(np.int32)).to(dev)
+    out, lse = ops.fast_attend(q, sc.k_cur.to(dev), sc.v_cur.to(dev), key, value, pr, lr,
+                               [g.tensors(rope=True) for g in reader.groups], rope=rope,
+                               q_pre=q_pre, q_rope=q_rope)
+    torch.cuda.synchronize()
+    t = torch.view_as_complex(rope.cs_t.cpu()).numpy()
+    h = torch.view_as_complex(rope.cs_h.cpu()).numpy()
+    w = torch.view_as_complex(rope.cs_w.cpu()).numpy()
+    key_freqs = orc.kv_freqs((t, h, w), rope.frame_pos.cpu().numpy(), 10, 35)
+    q_freqs = orc.kv_freqs(tuple(torch.view_as_complex(b.cpu()).numpy()
+                                 for b in (q_rope.cs_t, q_rope.cs_h, q_rope.cs_w)),
+                           q_rope.frame_pos.cpu().numpy(), 10, 15)
+    groups = oracle_groups(payload)
+    for g, pg in zip(groups, payload["groups"]):
+        ind = pg["indices"].numpy()
+        g["rope_pairs"] = ind[:, ::2] // 2
+    ref, ref_lse = orc.fast_attend(u16(q[0]), u16(sc.k_cur[0]), u16(sc.v_cur[0]), sc.hist[0]["k"],
+                                   sc.hist[0]["v"], prot, low, groups, sc.scale, D=sc.D,
+                                   key_freqs=key_freqs, q_pre_bf16=u16(sc.q[0]), q_freqs=q_freqs)
+    diff, cos = max_abs_cos(out[0].float().cpu().numpy(), ref)
+    assert diff <= MAX_ABS and cos >= MIN_COS, (diff, cos)
+    assert np.abs(lse[0].cpu().numpy() - ref_lse).max() < 2e-3
+
+
+def test_fast_rope_requires_pairs_and_query_positions(dev):
+    sc = Scenario(H=2, N=200, Q=40, Nc=0, rK=128, rV=128, G=32, C=8)
+    payload = _payload(sc, (0,), 32)
+    payload["groups"][1]["indices"] = torch.arange(32).flip(0).expand(1, 32).clone()  # not pairs
+    reader = codec_native.ReaderLayer(payload, dev)
+    with pytest.raises(ValueError, match="complete original pairs"):
+        reader.groups[1].tensors(rope=True)
+    key, value = sc.codecs(dev)
+    rope = ops.Rope.from_bands(ops.rope_bands(128, 16), [0, 1], 10, 10, dev)
+    pr = torch.arange(100, 200, dtype=torch.int32, device=dev)
+    lr = torch.arange(0, 100, dtype=torch.int32, device=dev)
+    from nanokv_amd import _lib
+    with pytest.raises(_lib.NanoKVError, match="q_pre and q_rope"):
+        ops.fast_attend(sc.q.to(dev), None, None, key, value, pr, lr,
+                        [reader.groups[0].tensors(rope=True)], rope=rope)

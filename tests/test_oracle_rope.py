@@ -136,3 +136,78 @@ def test_decode_attend_with_rope_rotates_history_keys():
     c, lc = orc.decode_attend(q, None, None, key, val, 128 ** -0.5, key_freqs=f)
     assert np.abs(c - a).max() > 1e-3
     assert math.isfinite(float(lc.max()))
+
+
+# ---------------------------------------------------------------- NanoKV-Fast
+def _fast_rope_problem(D=32, N=90, Q=12, Nc=10):
+    from tests._helpers import Scenario, u16
+    sc = Scenario(H=2, D=D, N=N, Q=Q, Nc=Nc, rK=64, rV=64, G=32, C=6, with_mean=True)
+    bands = orc.rope_bands(D, 16)
+    key_freqs = orc.kv_freqs(bands, [2, 9, 4], 5, 6)[:N]           # 3 frames of 30 rows
+    q_freqs = orc.kv_freqs(bands, [11], 3, 4)[:Q]                   # the current frame
+    q_pre = u16(sc.q[0])
+    q = orc.rope_apply(q_pre, q_freqs)                              # the hook's rotated query
+    return sc, bands, key_freqs, q_freqs, q_pre, q
+
+
+@pytest.mark.parametrize("split", ["recent", "anchors", "none", "all"])
+def test_fast_rope_identity_readers_equal_full_decode(split):
+    """Identity readers (CN/core.py:258-262) reduce NanoKV-Fast with RoPE to the
+    full decode -> rope_apply -> attention of every history row, whatever the
+    split: the low partition's q_low is rope(q_pre) = q and its keys are the
+    rotated full decode."""
+    from nanokv_amd import synth
+    from tests._helpers import max_abs_cos, oracle_groups, u16
+    sc, _, key_freqs, q_freqs, q_pre, q = _fast_rope_problem()
+    N = sc.N
+    prot = {"recent": np.arange(60, N), "anchors": np.array([0, 1, 2, 30, 31, 50, 88, 89]),
+            "none": np.array([], np.int64), "all": np.arange(N)}[split]
+    low = np.setdiff1d(np.arange(N), prot)
+    payload = synth.make_readers(sc.shape, sc.layer, full_heads=tuple(range(sc.H)))
+    groups = oracle_groups(payload)
+    key, val = sc.hist[0]["k"], sc.hist[0]["v"]
+    out, lse = orc.fast_attend(q, u16(sc.k_cur[0]), u16(sc.v_cur[0]), key, val, prot, low,
+                               groups, sc.scale, D=sc.D, key_freqs=key_freqs, q_pre_bf16=q_pre,
+                               q_freqs=q_freqs)
+    ref, ref_lse = orc.decode_attend(q, u16(sc.k_cur[0]), u16(sc.v_cur[0]), key, val, sc.scale,
+                                     D=sc.D, key_freqs=key_freqs)
+    diff, cos = max_abs_cos(out, ref)
+    assert diff < 2e-2 and cos > 0.9999, (split, diff, cos)
+    np.testing.assert_allclose(lse, ref_lse, atol=1e-4)
+
+
+def test_fast_rope_selection_reader_pins_pair_map():
+    """A reader that keeps original pairs P (q_reduce = k_affine = the 0/1
+    selection of dims 2p, 2p+1; k_read = the head's decoder rows of those
+    dims) makes the low partition attention over exactly those dims of the
+    rotated full keys and queries: a wrong pair index or band breaks it."""
+    from tests._helpers import max_abs_cos, u16
+    sc, _, key_freqs, q_freqs, q_pre, q = _fast_rope_problem(N=80, Nc=0)
+    D, H = sc.D, sc.H
+    pairs = np.array([[0, 3, 7, 15], [14, 6, 9, 2]])                # 4 pairs -> d = 8 per head
+    d = 2 * pairs.shape[1]
+    dims = np.stack([np.stack([2 * p, 2 * p + 1], 1).reshape(-1) for p in pairs])  # [H, d]
+    sel = np.zeros((H, D, d), np.float32)
+    for h in range(H):
+        sel[h, dims[h], np.arange(d)] = 1.0
+    wk = orc.bf16_to_f32(sc.hist[0]["k"]["w_dec_bf16"]).reshape(H, D, -1)
+    group = {"heads": [0, 1], "q_reduce": orc.f32_to_bf16(sel),
+             "k_read": orc.f32_to_bf16(np.stack([wk[h][dims[h]] for h in range(H)])),
+             "v_read": sc.hist[0]["v"]["w_dec_bf16"].reshape(H, D, -1),
+             "k_affine": orc.f32_to_bf16(sel), "v_affine": None, "rope_pairs": pairs}
+    key, val = sc.hist[0]["k"], sc.hist[0]["v"]
+    low = np.arange(sc.N)
+    out, lse = orc.fast_attend(q, None, None, key, val, np.array([], np.int64), low, [group],
+                               sc.scale, D=D, key_freqs=key_freqs, q_pre_bf16=q_pre,
+                               q_freqs=q_freqs)
+    # the same attention from the full, rotated decode restricted to the dims
+    kfull = orc.rope_apply(orc.decode(**key).reshape(sc.N, H, D), key_freqs)
+    vfull = orc.bf16_to_f32(orc.decode(**val).reshape(sc.N, H, D))
+    qf = orc.bf16_to_f32(q)
+    kf = orc.bf16_to_f32(kfull)
+    for h in range(H):
+        ro, rl = orc.attention(qf[None, :, h, dims[h]], kf[None, :, h, dims[h]], vfull[None, :, h],
+                               sc.scale)
+        diff, cos = max_abs_cos(out[:, h], ro[0])
+        assert diff < 1e-2 and cos > 0.9999, (h, diff, cos)
+        np.testing.assert_allclose(lse[h], rl[0], atol=1e-4)
