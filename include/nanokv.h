@@ -34,6 +34,9 @@
  *                     (CN/fast_kernels.py:30-54)
  *  nkv_fast_attend <- hybrid_attention (CN/core.py:278-310) and the partition
  *                     reads of maybe_attention (CN/mg35.py:100-357)
+ *  nkv_int8_pack   <- _pack_operator MG:108-131 (INT8 operator storage)
+ *  nkv_int8_dequant <- unpack_int8_weight (nanokv_codec_kernels.py:64-82),
+ *                     the INT8 branch of _operator_linear MG:145-152
  *  nkv_rope_apply  <- rope_apply (wan_video_dit.py:185-192) with the 3-D
  *                     frequencies of _kv_freqs (pipelines/wan_video.py:3322-3341);
  *                     nkv_attend_args.rope fuses the same rotation into the
@@ -82,6 +85,19 @@ enum nkv_quant_mode { NKV_QUANT_FP32 = 0, NKV_QUANT_BF16 = 1 };
 
 /* ABI version of the loaded library (NKV_ABI_VERSION at build time). */
 int nkv_abi_version(void);
+
+/*
+ * INT8 codec operators (the mg35_worldplay_operator_int8_v1 storage).
+ * nkv_int8_pack (_pack_operator, MG:108-131): w [rows, cols] fp32 in groups
+ * of `group` columns; per (row, group) s = max(amax|w|, 1e-12) / 127 (fp32),
+ * q = clamp(rint(w / s), -127, 127), scale[row, g] = bf16(s).
+ * nkv_int8_dequant (unpack_int8_weight, nanokv_codec_kernels.py:64-82):
+ * out [rows, cols] = bf16(q * scale[row, col / group]).
+ */
+int nkv_int8_pack(void* stream, const float* w, int64_t rows, int cols, int group, int8_t* q,
+                  uint16_t* scale);
+int nkv_int8_dequant(void* stream, const int8_t* q, const uint16_t* scale, int64_t rows, int cols,
+                     int group, uint16_t* out);
 
 /*
  * Rotary position embedding of cached keys, applied at read time

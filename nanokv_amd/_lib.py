@@ -32,7 +32,8 @@ NKV_SCHEDULE_KEY_CHUNKS = 2
 EXPORTED = (
     "nkv_abi_version", "nkv_last_error", "nkv_quant_pack", "nkv_unpack", "nkv_assign",
     "nkv_encode", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
-    "nkv_fast_attend_workspace_size", "nkv_fast_attend", "nkv_rope_apply",
+    "nkv_fast_attend_workspace_size", "nkv_fast_attend", "nkv_rope_apply", "nkv_int8_pack",
+    "nkv_int8_dequant",
 )
 
 
@@ -142,6 +143,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nkv_fast_attend_workspace_size.argtypes = [POINTER(NkvFastArgs)]
     lib.nkv_fast_attend.restype = c_int
     lib.nkv_fast_attend.argtypes = [c_void_p, POINTER(NkvFastArgs), c_void_p, c_size_t]
+    lib.nkv_int8_pack.restype = c_int
+    lib.nkv_int8_pack.argtypes = [c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p]
+    lib.nkv_int8_dequant.restype = c_int
+    lib.nkv_int8_dequant.argtypes = [c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int,
+                                     c_void_p]
     lib.nkv_rope_apply.restype = c_int
     lib.nkv_rope_apply.argtypes = [c_void_p, POINTER(NkvRope), c_int, c_int64, c_int, c_int,
                                    c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,

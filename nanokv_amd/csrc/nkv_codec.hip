@@ -833,6 +833,61 @@ static int check_codec_layout(int r, int group, int scale_dtype) {
     return NKV_OK;
 }
 
+namespace nkv {
+
+// ------------------------------------------------------- INT8 operator weights
+// _pack_operator (MG:108-131): per (row, group) s = max(amax|w|, 1e-12) / 127
+// in fp32, q = clamp(rint(w / s), -127, 127), stored scale = bf16(s) (the codes
+// use the unrounded s).  One wave per (row, group): a wave-wide amax, then
+// every lane codes elements lane, lane + 64, ...
+__global__ void __launch_bounds__(256) int8_pack_kernel(const float* __restrict__ w, int64_t rows,
+                                                        int cols, int group,
+                                                        int8_t* __restrict__ q,
+                                                        uint16_t* __restrict__ scale) {
+    const int lane = threadIdx.x & 63;
+    const int ngroups = cols / group;
+    const int64_t gid = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+    if (gid >= rows * ngroups) return;  // uniform per wave
+    const int64_t row = gid / ngroups;
+    const int64_t base = row * cols + (gid - row * ngroups) * (int64_t)group;
+    float amax = 0.0f;
+    for (int j = lane; j < group; j += 64) {
+        const float a = fabsf(w[base + j]);
+        amax = (a > amax || a != a) ? a : amax;  // NaN propagates like torch.amax
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+        const float b = __shfl_xor(amax, o);
+        amax = (b > amax || b != b) ? b : amax;
+    }
+    const float s = __fdiv_rn((amax > 1e-12f || amax != amax) ? amax : 1e-12f, 127.0f);
+    if (lane == 0) scale[gid] = f32_to_bf16_bits(s);
+    for (int j = lane; j < group; j += 64) {
+        const float r = rintf(__fdiv_rn(w[base + j], s));  // round half to even (torch.round)
+        q[base + j] = (int8_t)(int)fminf(fmaxf(r, -127.0f), 127.0f);
+    }
+}
+
+// unpack_int8_weight (nanokv_codec_kernels.py:64-82), _operator_linear
+// (MG:145-152): out = bf16(q * scale); the product of an 8-bit integer and a
+// bf16 scale is exact in fp32, so out is rounded once.  Eight weights per
+// thread when the row length allows 8-byte loads.
+__global__ void __launch_bounds__(256) int8_dequant_kernel(const int8_t* __restrict__ q,
+                                                           const uint16_t* __restrict__ scale,
+                                                           int64_t count, int group,
+                                                           uint16_t* __restrict__ out) {
+    const int64_t i0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 8;
+    if (i0 >= count) return;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+        const int64_t i = i0 + e;
+        if (i < count)
+            out[i] = f32_to_bf16_bits((float)q[i] * bf16_bits_to_f32(scale[i / group]));
+    }
+}
+
+}  // namespace nkv
+
 extern "C" int nkv_quant_pack(void* stream, const float* coeff, int64_t rows, int r, int group,
                               int scale_dtype, int quant_mode, uint8_t* packed,
                               uint16_t* scales) {
@@ -856,6 +911,34 @@ extern "C" int nkv_quant_pack(void* stream, const float* coeff, int64_t rows, in
     else
         quant_pack_kernel<NKV_QUANT_FP32><<<grid, 256, 0, s>>>(coeff, rows, r, group, scale_dtype,
                                                                 packed, scales);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+extern "C" int nkv_int8_pack(void* stream, const float* w, int64_t rows, int cols, int group,
+                             int8_t* q, uint16_t* scale) {
+    clear_error();
+    NKV_REQUIRE(rows >= 0 && cols > 0, NKV_ERR_INVALID, "bad weight shape");
+    NKV_REQUIRE(group > 0 && cols % group == 0, NKV_ERR_INVALID, "group must divide cols");
+    if (rows == 0) return NKV_OK;
+    NKV_REQUIRE(w && q && scale, NKV_ERR_INVALID, "null pointer");
+    const int64_t waves = rows * (cols / group);
+    nkv::int8_pack_kernel<<<dim3((unsigned)cdiv(waves, 4)), 256, 0, (hipStream_t)stream>>>(
+        w, rows, cols, group, q, scale);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+extern "C" int nkv_int8_dequant(void* stream, const int8_t* q, const uint16_t* scale, int64_t rows,
+                                int cols, int group, uint16_t* out) {
+    clear_error();
+    NKV_REQUIRE(rows >= 0 && cols > 0, NKV_ERR_INVALID, "bad weight shape");
+    NKV_REQUIRE(group > 0 && cols % group == 0, NKV_ERR_INVALID, "group must divide cols");
+    if (rows == 0) return NKV_OK;
+    NKV_REQUIRE(q && scale && out, NKV_ERR_INVALID, "null pointer");
+    const int64_t count = rows * cols;
+    nkv::int8_dequant_kernel<<<dim3((unsigned)cdiv(cdiv(count, 8), 256)), 256, 0,
+                               (hipStream_t)stream>>>(q, scale, count, group, out);
     NKV_LAUNCH_CHECK();
     return NKV_OK;
 }

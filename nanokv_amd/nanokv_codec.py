@@ -76,14 +76,36 @@ def _quant_mode() -> str:
 
 
 # ---------------------------------------------------------------- operators
-def register_operator(kind: str, layer: int, *, encoder: torch.Tensor, decoder: torch.Tensor,
+def pack_operator(weight: torch.Tensor, device: torch.device,
+                  group_size: Optional[int] = None) -> dict:
+    """The int8 operator storage of _pack_operator (MG:108-131) on `device`
+    (nkv_int8_pack): {"storage": "int8", "qweight", "scale", "group_size"};
+    group_size defaults to MG35_KVCODEC_INT8_WEIGHT_GROUP_SIZE (0: whole row)."""
+    if group_size is None:
+        group_size = int(os.environ.get("MG35_KVCODEC_INT8_WEIGHT_GROUP_SIZE", "0") or 0)
+    return ops.int8_pack(weight.detach().float().to(device), group_size)
+
+
+def _operator_weight(w) -> torch.Tensor:
+    """bf16 weight of a registered operator: a tensor, or an int8 operator dict
+    dequantized on its device (nkv_int8_dequant) as _operator_linear does
+    per call (MG:145-152); the operator weights are static, so once here."""
+    if isinstance(w, dict):
+        if w.get("storage", "int8") != "int8":
+            return w["weight"].detach().to(torch.bfloat16).contiguous()
+        return ops.int8_dequant(w)
+    return w.detach().to(torch.bfloat16).contiguous()
+
+
+def register_operator(kind: str, layer: int, *, encoder, decoder,
                       mean: Optional[torch.Tensor] = None) -> None:
     """Register the codec operator of (kind, layer): encoder [r, HD] and decoder
-    [HD, r] as bf16 (F.linear weight layouts, MG:134-153), mean [HD] fp32."""
+    [HD, r] (F.linear weight layouts, MG:134-153) as bf16 tensors or int8
+    operator dicts (pack_operator / the prepacked file), mean [HD] fp32."""
     if kind not in {"k", "v"}:
         raise ValueError(kind)
-    enc = encoder.detach().to(torch.bfloat16).contiguous()
-    dec = decoder.detach().to(torch.bfloat16).contiguous()
+    enc = _operator_weight(encoder)
+    dec = _operator_weight(decoder)
     if enc.dim() != 2 or dec.dim() != 2 or enc.shape[0] != dec.shape[1] or enc.shape[1] != dec.shape[0]:
         raise ValueError("encoder must be [r, HD] and decoder [HD, r]")
     m = None if mean is None else mean.detach().float().reshape(-1).contiguous()
@@ -98,14 +120,6 @@ def register_centers(kind: str, layer: int, centers: Optional[torch.Tensor]) -> 
     _CENTERS[(kind, int(layer))] = centers.detach().to(torch.bfloat16).contiguous()
 
 
-def _dequant_int8(packed: dict) -> torch.Tensor:
-    """bf16(int8 weight) * bf16 group scale -> bf16, as _operator_linear (MG:145-152)."""
-    q = packed["qweight"]
-    g = int(packed["group_size"])
-    w = q.reshape(q.shape[0], -1, g).to(torch.bfloat16) * packed["scale"][:, :, None].to(torch.bfloat16)
-    return w.reshape(q.shape)
-
-
 def preload_operator_weights(device: torch.device, path: Optional[str] = None) -> None:
     """Load every operator of the reference's prepacked file (format
     mg35_worldplay_operator_int8_v1, MG:257-279) onto `device`."""
@@ -115,12 +129,16 @@ def preload_operator_weights(device: torch.device, path: Optional[str] = None) -
     payload = torch.load(path, map_location="cpu", weights_only=True)
     if payload.get("format") != PREPACKED_FORMAT:
         raise RuntimeError(f"bad prepacked WorldPlay operator: {path}")
+    def move(packed):
+        return {"storage": "int8", "group_size": int(packed["group_size"]),
+                "qweight": packed["qweight"].to(device=device, dtype=torch.int8).contiguous(),
+                "scale": packed["scale"].to(device=device, dtype=torch.bfloat16).contiguous()}
+
     for name in sorted(payload["entries"]):
         kind, layer = name.split(":", 1)
         entry = payload["entries"][name]
-        register_operator(kind, int(layer), encoder=_dequant_int8(entry["encoder"]).to(device),
-                          decoder=_dequant_int8(entry["decoder"]).to(device),
-                          mean=entry["mean"].float().to(device))
+        register_operator(kind, int(layer), encoder=move(entry["encoder"]),
+                          decoder=move(entry["decoder"]), mean=entry["mean"].float().to(device))
 
 
 def _operator(kind: str, layer: int, device: torch.device) -> dict:

@@ -329,6 +329,44 @@ def _attend_args(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional
     return args, out, lse, device
 
 
+def int8_pack(weight: torch.Tensor, group_size: int = 0) -> dict:
+    """INT8 operator storage of a weight [rows, cols] (_pack_operator's int8
+    mode, MG:108-131, nkv_int8_pack): per row and group of `group_size`
+    columns (0: the whole row) s = max(amax, 1e-12) / 127, qweight =
+    clamp(round(w / s), -127, 127) int8, scale = bf16(s) [rows, cols/group]."""
+    device = _require_gpu(weight)
+    if weight.dim() != 2:
+        raise ValueError("weight must be [rows, cols]")
+    rows, cols = (int(v) for v in weight.shape)
+    group = int(group_size) or cols
+    if group > cols or cols % group:
+        raise ValueError(f"INT8 group size {group} must divide {cols}")
+    w = weight.detach().to(torch.float32).contiguous()
+    q = torch.empty((rows, cols), device=device, dtype=torch.int8)
+    scale = torch.empty((rows, cols // group), device=device, dtype=torch.bfloat16)
+    check("nkv_int8_pack", lib().nkv_int8_pack(_stream(device), w.data_ptr(), rows, cols, group,
+                                               q.data_ptr(), scale.data_ptr()))
+    return {"storage": "int8", "qweight": q, "scale": scale, "group_size": group}
+
+
+def int8_dequant(packed: dict) -> torch.Tensor:
+    """bf16 weight of an INT8 operator dict (qweight, scale, group_size):
+    bf16(q * scale), as unpack_int8_weight (nanokv_codec_kernels.py:64-82)."""
+    q, scale = packed["qweight"], packed["scale"]
+    device = _require_gpu(q, scale)
+    _contig(q, torch.int8, "qweight")
+    _contig(scale, torch.bfloat16, "scale")
+    rows, cols = (int(v) for v in q.shape)
+    group = int(packed["group_size"])
+    if group <= 0 or cols % group or tuple(scale.shape) != (rows, cols // group):
+        raise ValueError("scale must be [rows, cols / group_size]")
+    out = torch.empty((rows, cols), device=device, dtype=torch.bfloat16)
+    check("nkv_int8_dequant", lib().nkv_int8_dequant(_stream(device), q.data_ptr(),
+                                                     scale.data_ptr(), rows, cols, group,
+                                                     out.data_ptr()))
+    return out
+
+
 def rope_bands(D: int, end: int = 1024, theta: float = 10000.0):
     """The temporal, row and column RoPE frequency bands of a D-wide head,
     complex128 on the CPU: t [end, pt], h [end, ph], w [end, pw] with

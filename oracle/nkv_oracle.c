@@ -294,3 +294,39 @@ void nkvo_widen_bf16(const uint16_t* x, int64_t n, float* out) {
 void nkvo_widen_f16(const uint16_t* x, int64_t n, float* out) {
     for (int64_t i = 0; i < n; ++i) out[i] = nkvo_f16_to_f32(x[i]);
 }
+
+
+/* INT8 operator storage, _pack_operator (MG:108-131): per (row, group)
+ * s = max(amax|w|, 1e-12) / 127 in fp32, q = clamp(rint(w / s), -127, 127),
+ * scale = bf16(s). */
+void nkvo_int8_pack(const float* w, int64_t rows, int cols, int group, int8_t* q,
+                    uint16_t* scale) {
+    int ngroups = cols / group;
+    for (int64_t row = 0; row < rows; ++row) {
+        for (int g = 0; g < ngroups; ++g) {
+            const float* wg = w + row * (int64_t)cols + (int64_t)g * group;
+            float amax = 0.0f;
+            for (int j = 0; j < group; ++j) {
+                float a = fabsf(wg[j]);
+                if (a > amax || isnan(a)) amax = a;
+            }
+            float s = (amax > 1e-12f || isnan(amax) ? amax : 1e-12f) / 127.0f;
+            scale[row * ngroups + g] = nkvo_f32_to_bf16(s);
+            for (int j = 0; j < group; ++j) {
+                float r = rintf(wg[j] / s);
+                if (isnan(r)) r = -127.0f;             /* as fmax(NaN, -127) */
+                if (r > 127.0f) r = 127.0f;
+                if (r < -127.0f) r = -127.0f;
+                q[row * (int64_t)cols + (int64_t)g * group + j] = (int8_t)(int)r;
+            }
+        }
+    }
+}
+
+/* bf16(q * scale) of every weight (unpack_int8_weight,
+ * nanokv_codec_kernels.py:64-82). */
+void nkvo_int8_dequant(const int8_t* q, const uint16_t* scale, int64_t rows, int cols, int group,
+                       uint16_t* out) {
+    for (int64_t i = 0; i < rows * (int64_t)cols; ++i)
+        out[i] = nkvo_f32_to_bf16((float)q[i] * nkvo_bf16_to_f32(scale[i / group]));
+}

@@ -22,6 +22,10 @@ Pinning (the independent check that fixes each function; see tests/):
                                (argmin over all 15 codes, ties to even) on
                                random data; committed golden fixtures
   pack / unpack_codes         hand-computed bytes; round trip over all codes
+  int8_pack / int8_dequant    brute-force nearest code per weight (ties to
+                               even); hand KATs (zero rows, exact multiples,
+                               the 1e-12 floor); torch's tensor ops of
+                               _pack_operator and of the bf16 dequant product
   unpack_latent               torch: codes.float() * scale.float() -> bf16
                                (MG:429-434) computed by torch, not by the oracle
   assign                      brute force with exact rational arithmetic
@@ -96,6 +100,8 @@ def lib() -> ctypes.CDLL:
             getattr(l, name).argtypes = [c_void_p, c_int64, c_void_p]
         for name in ("nkvo_widen_bf16", "nkvo_widen_f16"):
             getattr(l, name).argtypes = [c_void_p, c_int64, c_void_p]
+        l.nkvo_int8_pack.argtypes = [c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p]
+        l.nkvo_int8_dequant.argtypes = [c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p]
         _lib = l
     return _lib
 
@@ -144,6 +150,31 @@ def scale_to_f32(bits, scale_dtype: str) -> np.ndarray:
 
 
 # ----------------------------------------------------------------- a4/a5
+def int8_pack(w, group: int = 0):
+    """INT8 operator storage (_pack_operator, MG:108-131): w [rows, cols]
+    float32 in groups of `group` columns (0: the whole row).  Returns
+    (qweight int8 [rows, cols], scale uint16 bf16 bits [rows, cols/group])."""
+    w = _c(w, np.float32)
+    rows, cols = w.shape
+    group = group or cols
+    if cols % group:
+        raise ValueError("group must divide cols")
+    q = np.zeros((rows, cols), np.int8)
+    scale = np.zeros((rows, cols // group), np.uint16)
+    lib().nkvo_int8_pack(_p(w), rows, cols, group, _p(q), _p(scale))
+    return q, scale
+
+
+def int8_dequant(q, scale, group: int) -> np.ndarray:
+    """bf16(q * scale) (unpack_int8_weight, nanokv_codec_kernels.py:64-82) ->
+    bf16 bits [rows, cols]."""
+    q = _c(q, np.int8)
+    scale = _c(scale, np.uint16)
+    out = np.zeros(q.shape, np.uint16)
+    lib().nkvo_int8_dequant(_p(q), _p(scale), q.shape[0], q.shape[1], group, _p(out))
+    return out
+
+
 def quant_pack(coeff, group: int, scale_dtype: str = "bf16", quant_mode: str = "fp32"):
     """INT4 quantise + pack (MG:349-351, 282-292; HY kv_codecs.py:237-255).
 
