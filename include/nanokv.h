@@ -24,6 +24,7 @@
  *  nkv_assign      <- the argmin step of semantic_residual MG:315-321;
  *                     HY _joint_euclid_assign_kernel (kv_codec_triton.py:238-273)
  *  nkv_encode      <- encode_tensor MG:333-365 with given shared centers
+ *  nkv_c64_fit     <- the C64 center fit of semantic_residual MG:301-330
  *  nkv_decode      <- _decode_method_segments MG:393-455, decode_tensor
  *                     MG:368-390, decode_pair_selected MG:801-861
  *  nkv_attend      <- decode_pair_values (MG:542) followed by the history
@@ -210,7 +211,7 @@ typedef struct nkv_encode_args {
     int quant_mode;
     int num_centers;
     int id_bytes;
-    int _pad;
+    int ids_in;                   /* 1: ids hold each row's center on input (no search) */
     const float* x;               /* [rows, HD] fp32 */
     const uint16_t* centers;      /* [C, HD] bf16 or NULL */
     const float* mean;            /* [HD] fp32 or NULL */
@@ -222,6 +223,23 @@ typedef struct nkv_encode_args {
 } nkv_encode_args;
 
 int nkv_encode(void* stream, const nkv_encode_args* args);
+
+/*
+ * Per-chunk C64 center fit (semantic_residual, MG:301-330), per batch item:
+ * the centers start as the rows init_rows[0 .. C) (the reference draws them
+ * with randperm(S, Generator(cpu).manual_seed(20260804 + layer))[:C]); each
+ * of `iterations` rounds labels every row with its nearest center (exact
+ * fp64 decision, first index on ties, as nkv_assign) and replaces every
+ * center that has rows by their mean, fp32(fp64 sum in row order) / count in
+ * fp32 (the reference sums in fp32 in library order); a center without rows
+ * keeps its value.  labels are the last round's (zero for 0 rounds).
+ *   x [B, S, HD] fp32; centers out [B, C, HD] fp32; labels out [B, S] int32;
+ *   1 <= C <= min(S, 256).
+ */
+size_t nkv_c64_fit_workspace_size(int B, int64_t S, int C);
+int nkv_c64_fit(void* stream, const float* x, int B, int64_t S, int HD, int C, int iterations,
+                const int32_t* init_rows, float* centers, int32_t* labels, void* workspace,
+                size_t workspace_bytes);
 
 /*
  * Full-width decode of all or selected rows to bf16 (the reference's decode

@@ -33,7 +33,7 @@ EXPORTED = (
     "nkv_abi_version", "nkv_last_error", "nkv_quant_pack", "nkv_unpack", "nkv_assign",
     "nkv_encode", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
     "nkv_fast_attend_workspace_size", "nkv_fast_attend", "nkv_rope_apply", "nkv_int8_pack",
-    "nkv_int8_dequant",
+    "nkv_int8_dequant", "nkv_c64_fit_workspace_size", "nkv_c64_fit",
 )
 
 
@@ -51,7 +51,7 @@ class NkvEncodeArgs(Structure):
     _fields_ = [
         ("rows", c_int64), ("HD", c_int), ("r", c_int), ("group", c_int),
         ("scale_dtype", c_int), ("quant_mode", c_int), ("num_centers", c_int),
-        ("id_bytes", c_int), ("_pad", c_int),
+        ("id_bytes", c_int), ("ids_in", c_int),
         ("x", c_void_p), ("centers", c_void_p), ("mean", c_void_p), ("w_enc", c_void_p),
         ("ids", c_void_p), ("coeff", c_void_p), ("packed", c_void_p), ("scales", c_void_p),
     ]
@@ -143,6 +143,11 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nkv_fast_attend_workspace_size.argtypes = [POINTER(NkvFastArgs)]
     lib.nkv_fast_attend.restype = c_int
     lib.nkv_fast_attend.argtypes = [c_void_p, POINTER(NkvFastArgs), c_void_p, c_size_t]
+    lib.nkv_c64_fit_workspace_size.restype = c_size_t
+    lib.nkv_c64_fit_workspace_size.argtypes = [c_int, c_int64, c_int]
+    lib.nkv_c64_fit.restype = c_int
+    lib.nkv_c64_fit.argtypes = [c_void_p, c_void_p, c_int, c_int64, c_int, c_int, c_int, c_void_p,
+                                c_void_p, c_void_p, c_void_p, c_size_t]
     lib.nkv_int8_pack.restype = c_int
     lib.nkv_int8_pack.argtypes = [c_void_p, c_void_p, c_int64, c_int, c_int, c_void_p, c_void_p]
     lib.nkv_int8_dequant.restype = c_int

@@ -109,9 +109,15 @@ __device__ __forceinline__ void store_id(void* ids, int64_t i, int v) {
     else reinterpret_cast<int32_t*>(ids)[i] = v;
 }
 
-template <int ID_BYTES>
+// A center element as fp32: bf16 bits or fp32 (both exact in fp64).
+__device__ __forceinline__ float center_value(const uint16_t* c, int64_t i) {
+    return bf16_bits_to_f32(c[i]);
+}
+__device__ __forceinline__ float center_value(const float* c, int64_t i) { return c[i]; }
+
+template <int ID_BYTES, typename CT = uint16_t>
 __global__ void __launch_bounds__(256) assign_kernel(const float* __restrict__ x,
-                                                     const uint16_t* __restrict__ centers,
+                                                     const CT* __restrict__ centers,
                                                      int64_t rows, int C, int HD,
                                                      void* __restrict__ ids) {
     __shared__ float xs[AS_ROWS][AS_K + 1];
@@ -142,7 +148,7 @@ __global__ void __launch_bounds__(256) assign_kernel(const float* __restrict__ x
                 int cr = e / AS_K, kk = e % AS_K;
                 int gc = c0 + cr;
                 cs[cr][kk] = (gc < C && k0 + kk < HD)
-                                 ? bf16_bits_to_f32(centers[(int64_t)gc * HD + k0 + kk])
+                                 ? center_value(centers, (int64_t)gc * HD + k0 + kk)
                                  : 0.0f;
             }
             __syncthreads();
@@ -212,11 +218,32 @@ __device__ __forceinline__ bool better(double d, int c, double bd, int bc) {
     return bc < 0 || (c >= 0 && (d < bd || (d == bd && c < bc)));
 }
 
-template <int ID_BYTES>
+// Four consecutive center elements of one lane's k block: 8 bytes of bf16
+// or 16 bytes of fp32; element st as an exact fp64.
+template <typename CT>
+struct CenterPiece;
+template <>
+struct CenterPiece<uint16_t> {
+    using V = u32x2;
+    static __device__ __forceinline__ double get(const V& v, int st) {
+        const uint32_t w = v[st >> 1];
+        return (double)__uint_as_float((st & 1) ? (w & 0xffff0000u) : (w << 16));
+    }
+};
+template <>
+struct CenterPiece<float> {
+    using V = u32x4;
+    static __device__ __forceinline__ double get(const V& v, int st) {
+        return (double)__uint_as_float(v[st]);
+    }
+};
+
+template <int ID_BYTES, typename CT = uint16_t>
 __global__ void __launch_bounds__(256) assign_mfma_kernel(const float* __restrict__ x,
-                                                          const uint16_t* __restrict__ centers,
+                                                          const CT* __restrict__ centers,
                                                           int64_t rows, int C, int HD,
                                                           void* __restrict__ ids) {
+    using CP = CenterPiece<CT>;
     __shared__ double red_d[4][AM_ROWS];
     __shared__ int red_c[4][AM_ROWS];
     const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -230,7 +257,7 @@ __global__ void __launch_bounds__(256) assign_mfma_kernel(const float* __restric
     for (int e = 0; e < 4; ++e) { bd[e] = 0.0; bc[e] = -1; }
 
     for (int cg = 0; cg < C; cg += 256) {
-        const uint16_t* cp[4];
+        const CT* cp[4];
         int cid[4];
 #pragma unroll
         for (int t = 0; t < 4; ++t) {
@@ -245,11 +272,12 @@ __global__ void __launch_bounds__(256) assign_mfma_kernel(const float* __restric
         // 16 k: four MFMA steps per tile); block kb lives in slot kb % AM_AHEAD
         const int NB = HD / 16;
         u32x4 xa[AM_AHEAD];
-        u32x2 cb[AM_AHEAD][4];
+        typename CP::V cb[AM_AHEAD][4];
         auto issue = [&](int kb, int slot) {
             xa[slot] = *reinterpret_cast<const u32x4*>(xp + 16 * kb);
 #pragma unroll
-            for (int t = 0; t < 4; ++t) cb[slot][t] = *reinterpret_cast<const u32x2*>(cp[t] + 16 * kb);
+            for (int t = 0; t < 4; ++t)
+                cb[slot][t] = *reinterpret_cast<const typename CP::V*>(cp[t] + 16 * kb);
         };
 #pragma unroll
         for (int i = 0; i < AM_AHEAD; ++i)
@@ -260,7 +288,7 @@ __global__ void __launch_bounds__(256) assign_mfma_kernel(const float* __restric
                 const int kb = kb0 + i;
                 if (kb >= NB) break;
                 const u32x4 xv = xa[i];
-                u32x2 cv[4];
+                typename CP::V cv[4];
 #pragma unroll
                 for (int t = 0; t < 4; ++t) cv[t] = cb[i][t];
                 if (kb + AM_AHEAD < NB) issue(kb + AM_AHEAD, i);
@@ -269,9 +297,7 @@ __global__ void __launch_bounds__(256) assign_mfma_kernel(const float* __restric
                     const double a = (double)__uint_as_float(xv[st]);
 #pragma unroll
                     for (int t = 0; t < 4; ++t) {
-                        const uint32_t w = cv[t][st >> 1];
-                        const double b =
-                            (double)__uint_as_float((st & 1) ? (w & 0xffff0000u) : (w << 16));
+                        const double b = CP::get(cv[t], st);
                         acc[t] = __builtin_amdgcn_mfma_f64_16x16x4f64(a, b, acc[t], 0, 0, 0);
                         cc[t] = fma(b, b, cc[t]);
                     }
@@ -962,6 +988,123 @@ extern "C" int nkv_unpack(void* stream, const uint8_t* packed, const uint16_t* s
     return NKV_OK;
 }
 
+namespace nkv {
+
+// ------------------------------------------------------------ C64 fit
+// The per-chunk joint-head center fit of semantic_residual (MG:301-330):
+// centers start as the rows init_rows (the caller's seeded permutation),
+// then each round labels every row with its nearest center (the exact fp64
+// search, first index on ties) and moves every center that has rows to their
+// mean.  The mean is deterministic: the rows of each cluster are listed in
+// row order (a stable counting sort), summed in fp64 in that order, rounded
+// to fp32 and divided by the count in fp32.
+
+__global__ void __launch_bounds__(256) c64_init_kernel(const float* __restrict__ x, int B, int64_t S,
+                                                       int HD, int C,
+                                                       const int32_t* __restrict__ init_rows,
+                                                       float* __restrict__ centers) {
+    const int64_t total = (int64_t)B * C * HD;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < total;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        const int d = (int)(i % HD);
+        const int c = (int)((i / HD) % C);
+        const int64_t b = i / ((int64_t)HD * C);
+        const int64_t row = min(max((int64_t)init_rows[c], (int64_t)0), S - 1);
+        centers[i] = x[(b * S + row) * HD + d];
+    }
+}
+
+constexpr int FIT_THREADS = 256, FIT_MAXC = 256;
+
+// One block per batch item: cluster sizes, their exclusive offsets, and the
+// rows of each cluster in row order (order[offset[c] + k] = k-th row of c).
+__global__ void __launch_bounds__(FIT_THREADS) c64_sort_kernel(const int32_t* __restrict__ labels,
+                                                                int64_t S, int C,
+                                                                int32_t* __restrict__ counts,
+                                                                int32_t* __restrict__ offsets,
+                                                                int32_t* __restrict__ order) {
+    __shared__ int cnt[FIT_MAXC], cur[FIT_MAXC], lab[FIT_THREADS];
+    const int t = threadIdx.x;
+    const int64_t b = blockIdx.x;
+    const int32_t* lb = labels + b * S;
+    for (int c = t; c < C; c += FIT_THREADS) cnt[c] = 0;
+    __syncthreads();
+    for (int64_t i = t; i < S; i += FIT_THREADS) atomicAdd(&cnt[min(max(lb[i], 0), C - 1)], 1);
+    __syncthreads();
+    if (t == 0) {
+        int run = 0;
+        for (int c = 0; c < C; ++c) {
+            cur[c] = run;
+            run += cnt[c];
+        }
+    }
+    __syncthreads();
+    for (int c = t; c < C; c += FIT_THREADS) {
+        counts[b * C + c] = cnt[c];
+        offsets[b * C + c] = cur[c];
+    }
+    for (int64_t i0 = 0; i0 < S; i0 += FIT_THREADS) {
+        const int64_t i = i0 + t;
+        const int L = i < S ? min(max(lb[i], 0), C - 1) : -1;
+        lab[t] = L;
+        __syncthreads();
+        if (L >= 0) {
+            // rows of this cluster earlier in the chunk come first
+            int rank = 0;
+            for (int u = 0; u < t; ++u) rank += lab[u] == L;
+            order[b * S + cur[L] + rank] = (int32_t)i;
+        }
+        __syncthreads();
+        if (L >= 0) atomicAdd(&cur[L], 1);
+        __syncthreads();
+    }
+}
+
+// grid (cdiv(HD, 256), C, B): one thread per center element.
+__global__ void __launch_bounds__(256) c64_update_kernel(const float* __restrict__ x, int64_t S,
+                                                         int HD, int C,
+                                                         const int32_t* __restrict__ counts,
+                                                         const int32_t* __restrict__ offsets,
+                                                         const int32_t* __restrict__ order,
+                                                         float* __restrict__ centers) {
+    const int d = blockIdx.x * 256 + threadIdx.x;
+    const int c = blockIdx.y;
+    const int64_t b = blockIdx.z;
+    if (d >= HD) return;
+    const int n = counts[b * C + c];
+    if (n == 0) return;  // an empty cluster keeps its center
+    const int32_t* ord = order + b * S + offsets[b * C + c];
+    const float* xb = x + b * S * HD + d;
+    double sum = 0.0;
+    for (int k = 0; k < n; ++k) sum += (double)xb[(int64_t)ord[k] * HD];
+    centers[(b * C + c) * HD + d] = __fdiv_rn((float)sum, (float)n);
+}
+
+__global__ void zero_i32_kernel(int32_t* p, int64_t n) {
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x)
+        p[i] = 0;
+}
+
+}  // namespace nkv
+
+// Nearest fp32 center of every row (int32 labels): the fp64 MFMA search, or
+// the fp64 VALU search for unaligned operands.
+static int launch_assign_f32(hipStream_t s, const float* x, const float* centers, int64_t rows,
+                             int C, int HD, int32_t* ids) {
+    if (rows <= 0) return NKV_OK;
+    if (HD % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
+        reinterpret_cast<uintptr_t>(centers) % 16 == 0) {
+        assign_mfma_kernel<4, float><<<dim3((unsigned)cdiv(rows, AM_ROWS)), 256, 0, s>>>(
+            x, centers, rows, C, HD, ids);
+    } else {
+        assign_kernel<4, float><<<dim3((unsigned)cdiv(rows, AS_ROWS)), 256, 0, s>>>(
+            x, centers, rows, C, HD, ids);
+    }
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
 static int launch_assign(hipStream_t s, const float* x, const uint16_t* centers, int64_t rows,
                          int C, int HD, void* ids, int id_bytes) {
     if (rows <= 0) return NKV_OK;
@@ -1010,6 +1153,62 @@ static int check_ids(int C, int id_bytes) {
     return NKV_OK;
 }
 
+namespace {
+size_t fit_ws_align(size_t n) { return (n + 255) / 256 * 256; }
+}  // namespace
+
+extern "C" size_t nkv_c64_fit_workspace_size(int B, int64_t S, int C) {
+    if (B <= 0 || S <= 0 || C <= 0) return 0;
+    return 2 * fit_ws_align((size_t)B * C * sizeof(int32_t)) +
+           fit_ws_align((size_t)B * S * sizeof(int32_t));
+}
+
+extern "C" int nkv_c64_fit(void* stream, const float* x, int B, int64_t S, int HD, int C,
+                           int iterations, const int32_t* init_rows, float* centers,
+                           int32_t* labels, void* workspace, size_t workspace_bytes) {
+    clear_error();
+    NKV_REQUIRE(B >= 0 && S >= 0 && HD > 0, NKV_ERR_INVALID, "bad shape");
+    NKV_REQUIRE(iterations >= 0, NKV_ERR_INVALID, "iterations must be >= 0");
+    if (B == 0 || S == 0) return NKV_OK;
+    NKV_REQUIRE(C >= 1 && C <= S && C <= FIT_MAXC, NKV_ERR_INVALID,
+                "C64 clusters must be in [1, min(S, 256)]");
+    NKV_REQUIRE(S < INT32_MAX, NKV_ERR_INVALID, "rows must fit in 32 bits");
+    NKV_REQUIRE(x && init_rows && centers && labels, NKV_ERR_INVALID, "null pointer");
+    const size_t need = nkv_c64_fit_workspace_size(B, S, C);
+    NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_ERR_WORKSPACE,
+                "workspace missing or smaller than nkv_c64_fit_workspace_size()");
+    unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
+    int32_t* counts = reinterpret_cast<int32_t*>(ws);
+    int32_t* offsets = reinterpret_cast<int32_t*>(ws + fit_ws_align((size_t)B * C * 4));
+    int32_t* order = reinterpret_cast<int32_t*>(ws + 2 * fit_ws_align((size_t)B * C * 4));
+    hipStream_t s = (hipStream_t)stream;
+    const int64_t elems = (int64_t)B * C * HD;
+    c64_init_kernel<<<dim3((unsigned)std::min<int64_t>(cdiv(elems, 256), 4096)), 256, 0, s>>>(
+        x, B, S, HD, C, init_rows, centers);
+    NKV_LAUNCH_CHECK();
+    if (iterations == 0) {
+        // no round: the labels stay zero, as the reference initialises them
+        zero_i32_kernel<<<dim3((unsigned)std::min<int64_t>(cdiv((int64_t)B * S, 256), 4096)), 256,
+                          0, s>>>(labels, (int64_t)B * S);
+        NKV_LAUNCH_CHECK();
+        return NKV_OK;
+    }
+    for (int it = 0; it < iterations; ++it) {
+        for (int b = 0; b < B; ++b) {
+            int rc = launch_assign_f32(s, x + (int64_t)b * S * HD, centers + (int64_t)b * C * HD,
+                                       S, C, HD, labels + (int64_t)b * S);
+            if (rc) return rc;
+        }
+        c64_sort_kernel<<<dim3((unsigned)B), FIT_THREADS, 0, s>>>(labels, S, C, counts, offsets,
+                                                                  order);
+        NKV_LAUNCH_CHECK();
+        c64_update_kernel<<<dim3((unsigned)cdiv(HD, 256), (unsigned)C, (unsigned)B), 256, 0, s>>>(
+            x, S, HD, C, counts, offsets, order, centers);
+        NKV_LAUNCH_CHECK();
+    }
+    return NKV_OK;
+}
+
 extern "C" int nkv_assign(void* stream, const float* x, const uint16_t* centers, int64_t rows,
                           int C, int HD, void* ids, int id_bytes) {
     clear_error();
@@ -1033,13 +1232,13 @@ extern "C" int nkv_encode(void* stream, const nkv_encode_args* a) {
     if (a->centers) {
         rc = check_ids(a->num_centers, a->id_bytes);
         if (rc) return rc;
-        NKV_REQUIRE(a->ids, NKV_ERR_INVALID, "ids output required with centers");
+        NKV_REQUIRE(a->ids, NKV_ERR_INVALID, "ids required with centers");
     }
     if (a->rows == 0) return NKV_OK;
     NKV_REQUIRE(a->x && a->w_enc && a->coeff && a->packed && a->scales, NKV_ERR_INVALID,
                 "null pointer");
     hipStream_t s = (hipStream_t)stream;
-    if (a->centers) {
+    if (a->centers && !a->ids_in) {
         rc = launch_assign(s, a->x, a->centers, a->rows, a->num_centers, a->HD, a->ids,
                            a->id_bytes);
         if (rc) return rc;

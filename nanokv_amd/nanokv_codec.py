@@ -155,29 +155,21 @@ def _operator(kind: str, layer: int, device: torch.device) -> dict:
 # ---------------------------------------------------------------- centers
 @torch.no_grad()
 def semantic_residual_centers(value: torch.Tensor, layer: int) -> tuple[torch.Tensor, torch.Tensor]:
-    """Per-chunk joint-head C64 fit of MG:301-330 (randperm init seeded with
-    20260804 + layer, `iterations` rounds of fp32 distance argmin and mean
-    update).  Returns (bf16 centers [B, C, HD], labels [B, S] int64) where the
-    labels are those of the last assignment round, as in the reference."""
+    """Per-chunk joint-head C64 centers (MG:301-330) on the GPU (nkv_c64_fit):
+    the initial centers are the rows randperm(S) draws from a CPU generator
+    seeded with 20260804 + layer (so they match the reference's draw), then
+    MG35_KVCODEC_C64_ITERS rounds of nearest-center labels and mean updates.
+    Returns (bf16 centers [B, C, HD], labels [B, S] int32 of the last round),
+    the stored centers of store_centers (MG:69-90)."""
     batch, sequence, dim = value.shape
-    rows = value.float()
     clusters = int(os.environ.get("MG35_KVCODEC_C64_CLUSTERS", "64"))
     iterations = int(os.environ.get("MG35_KVCODEC_C64_ITERS", "2"))
     if clusters <= 0 or clusters > sequence or clusters > 256:
         raise ValueError(f"C64 clusters must be in [1,min(S,256)], got {clusters}")
-    generator = torch.Generator(device="cpu").manual_seed(20260804 + int(layer))
-    initial = torch.randperm(sequence, generator=generator)[:clusters].to(rows.device)
-    centers = rows.index_select(1, initial).clone()
-    row_norm = rows.square().sum(-1, keepdim=True)
-    labels = torch.zeros((batch, sequence), dtype=torch.long, device=rows.device)
-    for _ in range(iterations):
-        distances = (row_norm + centers.square().sum(-1).unsqueeze(1)
-                     - 2.0 * torch.bmm(rows, centers.transpose(1, 2)))
-        labels = distances.argmin(-1)
-        assignment = torch.nn.functional.one_hot(labels, num_classes=clusters).transpose(1, 2).float()
-        counts = assignment.sum(-1)
-        updated = torch.bmm(assignment, rows) / counts.clamp_min(1.0).unsqueeze(-1)
-        centers = torch.where((counts > 0).unsqueeze(-1), updated, centers)
+    draw = torch.Generator(device="cpu").manual_seed(20260804 + int(layer))
+    init = torch.randperm(sequence, generator=draw)[:clusters].to(torch.int32)
+    centers, labels = ops.c64_fit(value.detach().float().contiguous(),
+                                  init.to(value.device), iterations)
     return centers.to(torch.bfloat16), labels
 
 
@@ -220,14 +212,14 @@ def encode_tensor(kind: str, layer: int, value: torch.Tensor) -> dict:
         fitted, labels = semantic_residual_centers(value, layer)
         id_dtype = torch.uint8
         for b in range(batch):
-            # the fit's labels are kept (MG:326-330), so the encoder is given
-            # the rows with their assigned stored center already subtracted
-            resid = rows[b] - fitted[b].float()[labels[b]]
-            e = ops.encode(resid.contiguous(), op["encoder"], centers=None, mean=op["mean"],
-                           group=group, scale_dtype=sdt, quant_mode=qmode)
+            # the fit's labels are kept (MG:326-330): the encoder subtracts each
+            # row's stored center without searching again
+            ids = labels[b].to(torch.uint8)
+            e = ops.encode(rows[b], op["encoder"], centers=fitted[b], mean=op["mean"],
+                           group=group, scale_dtype=sdt, quant_mode=qmode, ids=ids)
             packed.append(e["packed"])
             scales.append(e["scales"])
-            ids_out.append(labels[b].to(torch.uint8))
+            ids_out.append(ids)
         centers = fitted
         center_batch_shared = False
     return {

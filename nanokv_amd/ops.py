@@ -137,12 +137,15 @@ def assign(x: torch.Tensor, centers: torch.Tensor,
 def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tensor] = None,
            mean: Optional[torch.Tensor] = None, group: int = 32,
            scale_dtype: torch.dtype = torch.bfloat16, quant_mode: str = "fp32",
-           id_dtype: Optional[torch.dtype] = None, out: Optional[dict] = None) -> dict:
+           id_dtype: Optional[torch.dtype] = None, out: Optional[dict] = None,
+           ids: Optional[torch.Tensor] = None) -> dict:
     """Encode fp32 rows [rows, HD] with given centers (see nkv_encode).
 
     out: optional preallocated outputs {"packed", "scales", "ids", "coeff"}
     (contiguous, shaped like the returned ones; "ids" only with centers), so
-    that a chunk can be encoded straight into a slot of a larger cache."""
+    that a chunk can be encoded straight into a slot of a larger cache.
+    ids: each row's center, given (no nearest-center search), e.g. the
+    labels of a C64 fit; returned as the payload's ids."""
     device = _require_gpu(x, w_enc, centers, mean)
     _contig(x, torch.float32, "x")
     _contig(w_enc, torch.bfloat16, "w_enc")
@@ -166,12 +169,23 @@ def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tens
             raise ValueError(f"out[{name!r}] must hold {tuple(shape)} on {device}")
         return t
 
+    given = ids
     ids = None
+    if given is not None and centers is None:
+        raise ValueError("ids need centers")
     if centers is not None:
         _contig(centers, torch.bfloat16, "centers")
         C = int(centers.shape[0])
-        id_dtype = id_dtype or id_dtype_for(C)
-        ids = _out("ids", lead, id_dtype)
+        if given is not None:
+            _require_gpu(given)
+            if given.dtype not in _ID_BYTES or not given.is_contiguous() \
+                    or given.numel() != rows:
+                raise ValueError("ids must be a contiguous integer tensor of one id per row")
+            ids, id_dtype = given, given.dtype
+            args.ids_in = 1
+        else:
+            id_dtype = id_dtype or id_dtype_for(C)
+            ids = _out("ids", lead, id_dtype)
         args.num_centers, args.id_bytes = C, _ID_BYTES[id_dtype]
         args.centers, args.ids = centers.data_ptr(), ids.data_ptr()
     if mean is not None:
@@ -327,6 +341,30 @@ def _attend_args(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional
     lse = torch.empty((B, H, Qn), device=device, dtype=torch.float32) if return_lse else None
     args.lse = _ptr(lse)
     return args, out, lse, device
+
+
+def c64_fit(x: torch.Tensor, init_rows: torch.Tensor, iterations: int = 2,
+            workspace: Optional[torch.Tensor] = None):
+    """Per-chunk C64 center fit (nkv_c64_fit): x [B, S, HD] fp32, init_rows
+    int32 [C] (the seeded permutation's first C rows).  Returns (centers
+    [B, C, HD] fp32, labels [B, S] int32 of the last round)."""
+    device = _require_gpu(x, init_rows)
+    _contig(x, torch.float32, "x")
+    _contig(init_rows, torch.int32, "init_rows")
+    if x.dim() != 3:
+        raise ValueError("x must be [B, S, HD]")
+    B, S, HD = (int(v) for v in x.shape)
+    C = int(init_rows.numel())
+    centers = torch.empty((B, C, HD), device=device, dtype=torch.float32)
+    labels = torch.empty((B, S), device=device, dtype=torch.int32)
+    need = int(lib().nkv_c64_fit_workspace_size(B, S, C))
+    if workspace is None or workspace.numel() < need:
+        workspace = torch.empty(max(need, 1), device=device, dtype=torch.uint8)
+    check("nkv_c64_fit", lib().nkv_c64_fit(_stream(device), x.data_ptr(), B, S, HD, C,
+                                           int(iterations), init_rows.data_ptr(),
+                                           centers.data_ptr(), labels.data_ptr(),
+                                           workspace.data_ptr(), need))
+    return centers, labels
 
 
 def int8_pack(weight: torch.Tensor, group_size: int = 0) -> dict:

@@ -22,6 +22,12 @@ Pinning (the independent check that fixes each function; see tests/):
                                (argmin over all 15 codes, ties to even) on
                                random data; committed golden fixtures
   pack / unpack_codes         hand-computed bytes; round trip over all codes
+  c64_fit                     labels against exact rational distances on
+                               small inputs; the update against the closed-form
+                               mean of each cluster; 0 rounds = the drawn rows;
+                               the reference's torch loop (fp32 bmm, one-hot
+                               mean) on the CPU agrees (labels equal, centers
+                               to fp32 rounding)
   int8_pack / int8_dequant    brute-force nearest code per weight (ties to
                                even); hand KATs (zero rows, exact multiples,
                                the 1e-12 floor); torch's tensor ops of
@@ -150,6 +156,35 @@ def scale_to_f32(bits, scale_dtype: str) -> np.ndarray:
 
 
 # ----------------------------------------------------------------- a4/a5
+def c64_fit(x, init_rows, iterations: int = 2):
+    """The C64 center fit of semantic_residual (MG:301-330): centers start as
+    rows init_rows of each batch item; each round labels every row with the
+    center minimising ||c||^2 - 2 x.c in fp64 (first index on ties) and sets
+    every center that has rows to fp32(fp64 sum in row order) / count
+    (fp32); a center without rows keeps its value.  x [B, S, HD] float32.
+    Returns (centers [B, C, HD] float32, labels [B, S] int64 of the last
+    round; zeros for 0 rounds)."""
+    x = _c(x, np.float32)
+    B, S, HD = x.shape
+    init = np.asarray(init_rows, np.int64)
+    centers = x[:, init].copy()
+    C = centers.shape[1]
+    labels = np.zeros((B, S), np.int64)
+    x64 = x.astype(np.float64)
+    for _ in range(iterations):
+        for b in range(B):
+            c64 = centers[b].astype(np.float64)
+            d = (c64 * c64).sum(1)[None, :] - 2.0 * (x64[b] @ c64.T)
+            labels[b] = np.argmin(d, axis=1)
+        for b in range(B):
+            for c in range(C):
+                rows = np.nonzero(labels[b] == c)[0]
+                if rows.size:
+                    total = np.cumsum(x64[b][rows], axis=0)[-1].astype(np.float32)
+                    centers[b, c] = total / np.float32(rows.size)
+    return centers, labels
+
+
 def int8_pack(w, group: int = 0):
     """INT8 operator storage (_pack_operator, MG:108-131): w [rows, cols]
     float32 in groups of `group` columns (0: the whole row).  Returns
