@@ -19,6 +19,9 @@ followed by attention), with the decode fused into the attention kernel:
                                    builds them, for the fused kernel
   ReaderGroup / ReaderLayer        CN:155-224 reader parameters, bound to
                                    the kernels (identity flags CN:256-262)
+  enabled(prefix), file_sha256(path), get_layer(prefix, model, layer, ...)
+                                   CN:20-30, 229-275: reader checkpoints bound
+                                   by a manifest to the deployed codec operator
   fast_history_attention(q, cache, k_cur, v_cur, reader, protect)
                                    NanoKV-Fast: maybe_attention's native /
                                    low partitions (mg35.py:192-348) and
@@ -30,7 +33,11 @@ CPU.
 """
 from __future__ import annotations
 
+import hashlib
+import json
 import math
+import os
+from pathlib import Path
 from typing import Any, Optional
 
 import torch
@@ -185,6 +192,75 @@ class ReaderGroup:
                                  v_read=self.v_read, q_reduce=self.q_reduce,
                                  k_affine=self.k_affine, v_affine=self.v_affine,
                                  rope_pairs=self.rope_pairs if rope else None)
+
+
+def enabled(prefix: str) -> bool:
+    """Whether the codec-native path of `prefix` is switched on (CN:20-21)."""
+    return os.environ.get(prefix + "_ENABLE", "0").lower() in {"1", "true", "yes"}
+
+
+_DIGESTS: dict = {}
+
+
+def file_sha256(path: str) -> str:
+    """SHA-256 hex digest of a file, streamed in 8 MiB blocks and remembered
+    per (path, size, mtime) (CN:24-30)."""
+    st = os.stat(path)
+    key = (str(path), st.st_size, st.st_mtime_ns)
+    if key not in _DIGESTS:
+        h = hashlib.sha256()
+        with open(path, "rb") as f:
+            while True:
+                block = f.read(8 << 20)
+                if not block:
+                    break
+                h.update(block)
+        _DIGESTS[key] = h.hexdigest()
+    return _DIGESTS[key]
+
+
+_READER_BANKS: dict = {}
+
+
+def get_layer(prefix: str, model: str, layer: int, *, device, heads: int, native_dim: int,
+              operator_path: str, sp_rank: int = 0):
+    """The reader layer of (sp_rank, layer) from the manifest named by
+    `<prefix>_MANIFEST` (format codec_native_manifest_v1, CN:229-275): the
+    manifest must be for `model` and bound to the deployed codec operator
+    file by SHA-256; each reader checkpoint is checked against its recorded
+    SHA-256 and loaded with weights_only=True; uncalibrated readers are
+    refused unless `<prefix>_ALLOW_UNCALIBRATED=1`.  Returns (ReaderLayer or
+    None for a layer the manifest does not list, manifest); (None, None) when
+    the prefix is not enabled."""
+    if not enabled(prefix):
+        return None, None
+    path = Path(os.environ[prefix + "_MANIFEST"]).resolve()
+    op_path = str(Path(operator_path).resolve())
+    bank_key = (str(path), model, str(device), op_path)
+    if bank_key not in _READER_BANKS:
+        manifest = json.loads(path.read_text())
+        if manifest.get("format") != "codec_native_manifest_v1" or manifest.get("model") != model:
+            raise ValueError("Wrong codec-native manifest/model")
+        if manifest.get("codec_operator_sha256") != file_sha256(op_path):
+            raise ValueError("Reader is not bound to the deployed frozen codec operator")
+        _READER_BANKS[bank_key] = (manifest, {})
+    manifest, loaded = _READER_BANKS[bank_key]
+    entry = manifest["layers"].get(f"{int(sp_rank)}:{int(layer)}")
+    if entry is None:
+        return None, manifest
+    if not entry.get("calibrated", False) and os.environ.get(prefix + "_ALLOW_UNCALIBRATED") != "1":
+        raise RuntimeError("Reader is initialization-only; fit and validate before deployment")
+    ident = (int(sp_rank), int(layer))
+    if ident not in loaded:
+        artifact = (path.parent / entry["path"]).resolve()
+        if file_sha256(str(artifact)) != entry["sha256"]:
+            raise ValueError("Reader checkpoint checksum mismatch")
+        payload = torch.load(artifact, map_location="cpu", weights_only=True)
+        loaded[ident] = ReaderLayer(payload, device)
+    reader = loaded[ident]
+    if reader.heads != heads or reader.native_dim != native_dim:
+        raise ValueError("Reader head/shard layout mismatch")
+    return reader, manifest
 
 
 class ReaderLayer:
