@@ -141,8 +141,12 @@ class ReaderGroup:
     """One reader group (CN:155-204) on the device: heads that read the low
     history rows through q_reduce / k_read / v_read / k_affine / v_affine.
     Matrices equal to the identity are flagged as such (CN:256-262) and
-    skipped, as the reference's fast runtime does.  The value lift must be
-    the identity (vd == native dim); other lifts are not supported."""
+    skipped, as the reference's fast runtime does.  A value lift [vd, D]
+    other than the identity is folded into the value reader once: attention
+    is linear in V, so lifting each low partition's output (CN:202-204,
+    mg35.py:347) equals reading V' = v_low . lift, i.e. v_read' = lift^T .
+    v_read [D, r] and v_affine' = v_affine . lift [D, D] (composed in fp32,
+    rounded to bf16 once); only where the bf16 roundings fall differs."""
 
     def __init__(self, state: dict, device=None):
         self.heads = state["heads"].long()
@@ -159,22 +163,28 @@ class ReaderGroup:
         for name, shape in expected.items():
             if tuple(state[name].shape) != shape:
                 raise ValueError(f"Bad {name} shape; expected {shape}")
-        if vd != native or not _is_identity(state["lift"]):
-            raise NotImplementedError("only identity value lifts (vd == D) are supported")
         self.native_dim, self.d = native, d
         self.identity_query = _is_identity(state["q_reduce"])
         self.identity_k = _is_identity(state["k_affine"])
-        self.identity_v = _is_identity(state["v_affine"])
+        self.identity_lift = vd == native and _is_identity(state["lift"])
         device = device if device is not None else state["k_read"].device
 
         def dev(t):
             return t.to(device=device, dtype=torch.bfloat16).contiguous()
 
+        v_read, v_affine = state["v_read"], state["v_affine"]
+        if not self.identity_lift:
+            lift = state["lift"].to(device=device, dtype=torch.float32)       # [h, vd, D]
+            v_read = torch.matmul(lift.transpose(1, 2),
+                                  v_read.to(device=device, dtype=torch.float32))   # [h, D, r]
+            v_affine = torch.matmul(v_affine.to(device=device, dtype=torch.float32),
+                                    lift)                                      # [h, D, D]
+        self.identity_v = _is_identity(v_affine)
         self.q_reduce = None if self.identity_query else dev(state["q_reduce"])
         self.k_affine = None if self.identity_k else dev(state["k_affine"])
-        self.v_affine = None if self.identity_v else dev(state["v_affine"])
+        self.v_affine = None if self.identity_v else dev(v_affine)
         self.k_read = dev(state["k_read"])
-        self.v_read = dev(state["v_read"])
+        self.v_read = dev(v_read)
         self.heads_dev = self.heads.to(device=device, dtype=torch.int32).contiguous()
         # RoPE acts on complete original pairs only (rope_selected, CN:75-91):
         # reader dims (2j, 2j+1) must be original dims (2p, 2p+1); pair j then

@@ -539,7 +539,8 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
     group: q_low = bf16(q_h . q_reduce) (CN:164-166), k_low / v_low =
     reader_read of low_rows; merged by LSE (CN:33-42) into bf16.
     groups: dicts with heads, q_reduce, k_read, v_read, k_affine, v_affine
-    (bf16 bits per head, None = identity).  Returns (out [Q, H', D] float32
+    and lift (bf16 bits per head, None = identity; v_read [vd, r], v_affine
+    [D, vd], lift [vd, D]).  Returns (out [Q, H', D] float32
     of the bf16 result, lse [H', Q]).
 
     RoPE (key_freqs [N, D/2] of the codec rows, CN/mg35.py:207-214, 305-336):
@@ -593,6 +594,10 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
             vl = bf16_to_f32(reader_read(value, low, g["v_read"][i], vt, vb, dtype))
             ol, ll = attention(qh[None], kl[None], vl[None], scale, dtype)
             ol = bf16_to_f32(f32_to_bf16(ol[0].astype(np.float32)))
+            if g.get("lift") is not None:
+                # lift_output (CN/core.py:202-204), applied before the merge (mg35.py:347)
+                lf = bf16_to_f32(g["lift"][i]).astype(dtype)
+                ol = bf16_to_f32(f32_to_bf16((ol.astype(dtype) @ lf).astype(np.float32)))
             mo, ml = merge(on, ln, ol, ll[0])
             on, ln = bf16_to_f32(f32_to_bf16(np.asarray(mo, np.float32))), ml
         outs.append(on)

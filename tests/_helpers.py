@@ -125,5 +125,6 @@ def oracle_groups(payload: dict) -> list:
             "v_read": u16(g["v_read"].to(_t.bfloat16)),
             "k_affine": None if ident(g["k_affine"]) else u16(g["k_affine"].to(_t.bfloat16)),
             "v_affine": None if ident(g["v_affine"]) else u16(g["v_affine"].to(_t.bfloat16)),
+            "lift": None if ident(g["lift"]) else u16(g["lift"].to(_t.bfloat16)),
         })
     return out

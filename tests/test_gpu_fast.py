@@ -246,3 +246,24 @@ def test_fast_rope_requires_pairs_and_query_positions(dev):
     with pytest.raises(_lib.NanoKVError, match="q_pre and q_rope"):
         ops.fast_attend(sc.q.to(dev), None, None, key, value, pr, lr,
                         [reader.groups[0].tensors(rope=True)], rope=rope)
+
+
+@pytest.mark.parametrize("vd", [64, 128])
+def test_fast_value_lift(dev, vd):
+    """A reader group with a learned value lift [vd, D] (CN/core.py:202-204):
+    the oracle lifts each low partition's bf16 output before the merge, as the
+    reference does; the kernels read V through the folded matrices."""
+    sc = Scenario(H=4, N=600, Q=120, Nc=40, rK=256, rV=256, G=32, C=12, with_mean=True, seed=vd)
+    payload = _payload(sc, (0,), 32)
+    g = torch.Generator().manual_seed(vd)
+    low = payload["groups"][1]
+    n, D = len(low["heads"]), sc.D
+
+    def bf(t):
+        return t.to(torch.bfloat16).float()
+
+    low["v_read"] = bf(torch.randn(n, vd, sc.shape.rV, generator=g) / sc.shape.rV ** 0.5)
+    low["v_affine"] = bf(torch.randn(n, D, vd, generator=g) / D ** 0.5)
+    low["lift"] = bf(torch.randn(n, vd, D, generator=g) / vd ** 0.5)
+    low["v_indices"] = torch.arange(vd).expand(n, vd).clone()
+    _run(sc, dev, payload, np.arange(400, 600))

@@ -81,3 +81,26 @@ def test_reader_read_against_torch_linear():
     ids = torch.from_numpy(np.asarray(key["ids"], np.int64)[rows])
     ref = (lin.float() + table[ids].float()).to(torch.bfloat16).float()
     np.testing.assert_array_equal(got, ref.numpy())
+
+
+def test_lift_applies_to_the_low_output():
+    """With no native rows the hybrid result is the low partition alone; a lift
+    L then gives bf16(out_without_lift . L) up to the bf16 rounding of the
+    unlifted output (a transposed or misplaced lift fails this)."""
+    sc = Scenario(H=2, D=32, N=70, Q=9, Nc=0, rK=64, rV=64, G=32, C=5, with_mean=True)
+    payload = _identity_payload(sc)
+    groups = oracle_groups(payload)
+    key, val = sc.hist[0]["k"], sc.hist[0]["v"]
+    low = np.arange(sc.N)
+    none = np.array([], np.int64)
+    base, _ = orc.fast_attend(u16(sc.q[0]), None, None, key, val, none, low, groups, sc.scale, D=sc.D)
+    g = torch.Generator().manual_seed(4)
+    L = (torch.randn(2, 32, 32, generator=g) / 32 ** 0.5).to(torch.bfloat16)
+    lifted_groups = [dict(gr, lift=u16(L[[h for h in gr["heads"]]])) for gr in groups]
+    out, _ = orc.fast_attend(u16(sc.q[0]), None, None, key, val, none, low, lifted_groups,
+                             sc.scale, D=sc.D)
+    for h in range(2):
+        ref = base[:, h] @ L[h].float().numpy()
+        np.testing.assert_allclose(out[:, h], ref, rtol=2e-2, atol=2e-2)
+        # not the transpose
+        assert np.abs(out[:, h] - base[:, h] @ L[h].float().numpy().T).max() > 5e-2
