@@ -57,6 +57,9 @@ def parse():
     ap.add_argument("--rope", action="store_true",
                     help="configs 1-2: read-time RoPE of the history keys (frames of "
                          "30 x 52 tokens at temporal positions 0, 1, ...)")
+    ap.add_argument("--camera", action="store_true",
+                    help="configs 1-2: camera P^-1 of the history keys and values (frames "
+                         "of 1,560 tokens, four camera matrix sets)")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="no timing: run a known-size copy and a few fused calls (for rocprofv3 --pmc)")
     return ap.parse_args()
@@ -372,6 +375,13 @@ def main():
         frames = -(-shape.N // (grid_h * grid_w))
         rope = ops.Rope.from_bands(ops.rope_bands(shape.D), range(frames), grid_h, grid_w,
                                    device)
+    camera = None
+    if args.camera and not fast:
+        frames = -(-shape.N // 1560)
+        g = torch.Generator().manual_seed(7)
+        mats = torch.eye(4).expand(1, 4, 4, 4, 4) + 0.3 * torch.randn(1, 4, 4, 4, 4, generator=g)
+        camera = ops.Camera(mats.contiguous().to(device),
+                            torch.arange(frames, dtype=torch.int32).remainder(4).to(device), 1560)
 
     def step(events=None):
         if fast:
@@ -379,7 +389,7 @@ def main():
                                    out=out, return_lse=False, workspace=ws)
         return ops.attend(q, kc, vc, codecs[0], codecs[1], out=out, splits=args.splits,
                           return_lse=False, workspace=ws, kernel_events=events,
-                          schedule=args.schedule, rope=rope)
+                          schedule=args.schedule, rope=rope, camera=camera)
 
     if args.profile_kernel:
         # A plain copy of known size (for FETCH_SIZE/WRITE_SIZE calibration), then the kernel.
@@ -459,7 +469,9 @@ def main():
                    "parallelism": "single-gpu"}
         | ({"protected_rows": int(prot_rows.numel()), "full_heads": list(synth.FAST_FULL_HEADS),
             "reader_width": synth.FAST_READER_D} if fast else {})
-        | ({"rope": "history keys rotated at read, frames of 30x52 tokens"} if rope else {}),
+        | ({"rope": "history keys rotated at read, frames of 30x52 tokens"} if rope else {})
+        | ({"camera": "history keys and values times P^-1 at read, frames of 1560 tokens"}
+           if camera else {}),
         "history_tokens_per_ms": round(shape.N / ms_per_step, 1),
         "coeff_stream_GBps": round(shape.coeff_stream_bytes() / (kavg_ms * 1e-3) / 1e9, 2),
         "algorithmic_flops": fl,

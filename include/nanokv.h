@@ -38,6 +38,9 @@
  *  nkv_int8_pack   <- _pack_operator MG:108-131 (INT8 operator storage)
  *  nkv_int8_dequant <- unpack_int8_weight (nanokv_codec_kernels.py:64-82),
  *                     the INT8 branch of _operator_linear MG:145-152
+ *  nkv_camera_apply, nkv_attend_args.camera <- the camera PRoPE transforms of
+ *                     prope_attention_by_frame_indices (wan_video_dit.py:85-128)
+ *                     and the fused camera kernel (CN/camera_kernel.py:8-36)
  *  nkv_rope_apply  <- rope_apply (wan_video_dit.py:185-192) with the 3-D
  *                     frequencies of _kv_freqs (pipelines/wan_video.py:3322-3341);
  *                     nkv_attend_args.rope fuses the same rotation into the
@@ -127,6 +130,41 @@ typedef struct nkv_rope {
     int pt, ph, pw;
     int grid_h, grid_w;
 } nkv_rope;
+
+/*
+ * Camera PRoPE (prope_attention_by_frame_indices, wan_video_dit.py:85-128;
+ * layouts of prope_attention.py:9-24, 120-176): each frame of rows has a set
+ * of four sub-frame 4x4 matrices (P^-1 for keys and values, P^T for queries,
+ * P for outputs); 4-vectors of each head are multiplied by their sub-frame's
+ * matrix, y = M x, with the matrix entries rounded to bf16, the products
+ * summed exactly, and the result rounded fp32 -> bf16 (camera_kernel.py:8-36,
+ * fp64 accumulation).  Layouts: FULL tiles all D dims (D % 64 == 0): dim
+ * d = ((p*4 + c)*4 + j)*(D/64) + r, vector over j, sub-frame c; SF13 puts
+ * sub-frame 1 on dims [0, 16) and 3 on [16, 32) as contiguous 4-vectors and
+ * leaves the rest.  Row n of batch item b uses matrix set
+ * frame_mat[n / tokens_per_frame] of mats + b * mats_bs (frame and set
+ * indices clamped to range).  mats must be 16-byte aligned and mats_bs a
+ * multiple of 4.
+ */
+enum nkv_camera_layout { NKV_CAMERA_FULL = 0, NKV_CAMERA_SF13 = 1 };
+
+typedef struct nkv_camera {
+    const float* mats;            /* [batches, n_mats, 4, 4, 4] fp32, device */
+    int64_t mats_bs;              /* floats between batch items (0: shared) */
+    int n_mats;
+    int layout;                   /* nkv_camera_layout */
+    const int32_t* frame_mat;     /* [n_frames] matrix set of each frame, device */
+    int64_t n_frames;
+    int tokens_per_frame;
+    int _pad;
+} nkv_camera;
+
+/* out[b, s, h, :] = the camera transform of x[b, s, h, :] at row rows[s]
+ * (rows NULL: row s); layout as nkv_rope_apply.  out may be x. */
+int nkv_camera_apply(void* stream, const nkv_camera* camera, int B, int64_t S, int H, int D,
+                     const uint16_t* x, int64_t x_sb, int64_t x_st, int64_t x_sh,
+                     const int32_t* rows, uint16_t* out, int64_t o_sb, int64_t o_st,
+                     int64_t o_sh);
 
 /*
  * out[b, s, h, :] = RoPE of x[b, s, h, :] at the position of row rows[s]
@@ -276,6 +314,10 @@ int nkv_decode(void* stream, const nkv_decode_args* args);
  * rope (host pointer, NULL = none): history keys are rotated after decode at
  * the positions of their codec rows (see nkv_rope); q and k_cur are taken as
  * already rotated.  RoPE runs on the KEY_CHUNKS schedule (AUTO picks it).
+ * camera (host pointer, NULL = none): history keys (after RoPE) and values are
+ * multiplied by their frame's P^-1 after decode (see nkv_camera); q, k_cur and
+ * v_cur are taken as already transformed and the caller applies P to out.
+ * The camera also runs on the KEY_CHUNKS schedule.
  */
 typedef struct nkv_attend_args {
     int B;
@@ -304,6 +346,7 @@ typedef struct nkv_attend_args {
     void* ev_kernel_begin;
     void* ev_kernel_end;
     const nkv_rope* rope;
+    const nkv_camera* camera;
 } nkv_attend_args;
 
 /* Bytes of workspace nkv_attend needs for these arguments (0 if none). */

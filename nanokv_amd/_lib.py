@@ -33,7 +33,7 @@ EXPORTED = (
     "nkv_abi_version", "nkv_last_error", "nkv_quant_pack", "nkv_unpack", "nkv_assign",
     "nkv_encode", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
     "nkv_fast_attend_workspace_size", "nkv_fast_attend", "nkv_rope_apply", "nkv_int8_pack",
-    "nkv_int8_dequant", "nkv_c64_fit_workspace_size", "nkv_c64_fit",
+    "nkv_int8_dequant", "nkv_c64_fit_workspace_size", "nkv_c64_fit", "nkv_camera_apply",
 )
 
 
@@ -72,6 +72,18 @@ class NkvRope(Structure):
     ]
 
 
+NKV_CAMERA_FULL = 0
+NKV_CAMERA_SF13 = 1
+
+
+class NkvCamera(Structure):
+    _fields_ = [
+        ("mats", c_void_p), ("mats_bs", c_int64), ("n_mats", c_int), ("layout", c_int),
+        ("frame_mat", c_void_p), ("n_frames", c_int64), ("tokens_per_frame", c_int),
+        ("_pad", c_int),
+    ]
+
+
 class NkvAttendArgs(Structure):
     _fields_ = [
         ("B", c_int), ("H", c_int), ("D", c_int), ("splits", c_int),
@@ -83,7 +95,7 @@ class NkvAttendArgs(Structure):
         ("key", NkvCodec), ("value", NkvCodec),
         ("out", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64),
         ("lse", c_void_p), ("ev_kernel_begin", c_void_p), ("ev_kernel_end", c_void_p),
-        ("rope", POINTER(NkvRope)),
+        ("rope", POINTER(NkvRope)), ("camera", POINTER(NkvCamera)),
     ]
 
 
@@ -157,6 +169,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nkv_rope_apply.argtypes = [c_void_p, POINTER(NkvRope), c_int, c_int64, c_int, c_int,
                                    c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
                                    c_int64, c_int64, c_int64]
+    lib.nkv_camera_apply.restype = c_int
+    lib.nkv_camera_apply.argtypes = [c_void_p, POINTER(NkvCamera), c_int, c_int64, c_int, c_int,
+                                     c_void_p, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+                                     c_int64, c_int64, c_int64]
     lib.nkv_lse_merge.restype = c_int
     lib.nkv_lse_merge.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int64, c_void_p,
                                   c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p]

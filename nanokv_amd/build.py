@@ -33,6 +33,7 @@ SOURCES = {
     "nkv_fast.hip": [],
     # RoPE rounds every fp64 product and sum separately, as the oracle does
     "nkv_rope.hip": ["-ffp-contract=off"],
+    "nkv_camera.hip": ["-ffp-contract=off"],
 }
 
 COMMON = [

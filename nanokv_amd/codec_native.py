@@ -85,6 +85,21 @@ def protected_tokens(frame_ids: torch.Tensor, recent: int, stride: int, sink: in
     return keep[inverse]
 
 
+def kv_camera(P_inv: torch.Tensor, frames, tokens_per_frame: int, device, *,
+              layout: str = "full") -> ops.Camera:
+    """Camera of cached frames for the history keys and values: P_inv
+    [batches, cameras, 4, 4, 4] (camera_info[1][2]), frames the camera index
+    of each cached frame (the runs _viewmats collapses, CN/mg35.py:38-51),
+    each frame tokens_per_frame codec rows; layout "full" or "sf13"."""
+    mats = P_inv.to(device=device, dtype=torch.float32).contiguous()
+    frame_mat = torch.as_tensor(list(frames), dtype=torch.int32)
+    if frame_mat.numel() == 0:
+        raise ValueError("camera needs at least one frame")
+    if int(frame_mat.min()) < 0 or int(frame_mat.max()) >= mats.shape[1]:
+        raise ValueError("frame camera index outside P_inv")
+    return ops.Camera(mats, frame_mat.to(device), int(tokens_per_frame), layout)
+
+
 def kv_rope(freqs, temporal_positions, h: int, w: int, device, *,
             disable_t: bool = False) -> ops.Rope:
     """Read-time RoPE positions of cached frames: `freqs` is the model's
@@ -106,7 +121,8 @@ def codec_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
                             k_cur: Optional[torch.Tensor] = None,
                             v_cur: Optional[torch.Tensor] = None, *,
                             scale: Optional[float] = None, return_lse: bool = False,
-                            rope: Optional[ops.Rope] = None):
+                            rope: Optional[ops.Rope] = None,
+                            camera: Optional[ops.Camera] = None):
     """Attention of q [B, H, Q, D] over [decoded history; current chunk] where
     the history is the paired codec cache (nanokv_codec payloads or segment
     lists) and k_cur/v_cur [B, H, Nc, D] are uncompressed.  Equivalent to the
@@ -114,7 +130,11 @@ def codec_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     with the decode fused into nkv_attend.  rope (kv_rope): the cached keys
     are rotated after decode at their positions, as the reference's
     rope_apply(cache_k_pre, cache_freqs) (wan_video_dit.py:538-546); q and
-    k_cur are taken as already rotated."""
+    k_cur are taken as already rotated.  camera (kv_camera): the cached keys
+    (after RoPE) and values are multiplied by their frames' P^-1 inside the
+    kernel, as _native_prope does to the decoded history (CN/mg35.py:54-71);
+    q, k_cur and v_cur are taken as already transformed and the caller
+    applies P to the output."""
     device = q.device
     B, H, Qn, D = (int(x) for x in q.shape)
     key = value = None
@@ -126,7 +146,8 @@ def codec_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     vc = None if v_cur is None else v_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
     out, lse = ops.attend(qq, kc, vc, key, value,
                           softmax_scale=D ** -0.5 if scale is None else scale,
-                          return_lse=return_lse, rope=rope if key is not None else None)
+                          return_lse=return_lse, rope=rope if key is not None else None,
+                          camera=camera if key is not None else None)
     out = out.permute(0, 2, 1, 3)
     return (out, lse) if return_lse else out
 

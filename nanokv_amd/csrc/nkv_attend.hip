@@ -795,12 +795,12 @@ int resolve_schedule(const nkv_attend_args* a, int* schedule) {
         const bool fits = a->D == 128 &&
                           (a->N == 0 || (a->key.r % 64 == 0 && a->value.r % 64 == 0 &&
                                          a->key.group % 32 == 0 && a->value.group % 32 == 0));
-        sch = (fits && (a->Q > AT_BM || a->rope)) ? NKV_SCHEDULE_KEY_CHUNKS
-                                                  : NKV_SCHEDULE_QUERY_TILES;
+        sch = (fits && (a->Q > AT_BM || a->rope || a->camera)) ? NKV_SCHEDULE_KEY_CHUNKS
+                                                               : NKV_SCHEDULE_QUERY_TILES;
     }
-    NKV_REQUIRE(!a->rope || sch == NKV_SCHEDULE_KEY_CHUNKS, NKV_ERR_UNSUPPORTED,
-                "read-time RoPE needs the key-chunk schedule (D = 128, ranks that are "
-                "multiples of 64, scale groups that are multiples of 32)");
+    NKV_REQUIRE((!a->rope && !a->camera) || sch == NKV_SCHEDULE_KEY_CHUNKS, NKV_ERR_UNSUPPORTED,
+                "read-time RoPE and camera need the key-chunk schedule (D = 128, ranks that "
+                "are multiples of 64, scale groups that are multiples of 32)");
     *schedule = sch;
     return NKV_OK;
 }

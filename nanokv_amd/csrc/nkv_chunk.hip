@@ -33,6 +33,7 @@
 //   S^T = K Q^T, P = exp2(S * c - m), O^T += V^T P^T
 // over eight 32-key steps.  The running max is raised only when a score
 // exceeds it by more than 2^8 (P <= 256 otherwise), so O is rarely rescaled.
+#include "nkv_camera.h"
 #include "nkv_common.h"
 #include "nkv_internal.h"
 
@@ -82,6 +83,7 @@ struct ChunkParams {
     int64_t o_sb, o_st, o_sh;
     float* lse;
     RopeDev rope;       // RoPE of the history keys (cs_t null: none)
+    CameraDev cam;      // camera P^-1 of the history keys and values (mats null: none)
 };
 
 // Codec row of attended history key `key`; rows outside the codec are
@@ -290,6 +292,19 @@ __device__ __forceinline__ void rope_k_rows(uint16_t* ktile, const ChunkParams& 
     }
 }
 
+// Camera P^-1 of the wave's 32 decoded keys (after RoPE) in the K tile: the
+// two lane halves share key 32 * wave + l32.  Full-width keys only.
+template <int KROW>
+__device__ __forceinline__ void camera_k_rows(uint16_t* ktile, const ChunkParams& p, int b,
+                                              int64_t tok0, int valid, int wave, int lane) {
+    const int hf = lane >> 5, kt = 32 * wave + (lane & 31);
+    const float* M = camera_mats(p.cam, b, history_row(p, tok0 + (kt < valid ? kt : 0)));
+    uint16_t* krow = ktile + kt * KROW;
+    camera_row<CK_D>(
+        M, p.cam.layout, hf, [&](int d) { return bf16_bits_to_f32(krow[d]); },
+        [&](int d, float y) { krow[d] = f32_to_bf16_bits(y); });
+}
+
 template <int CODEC, bool HAS_C, int WIDTH, int KROW, typename Pre>
 __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, const ChunkCodec& c,
                                               const ChunkParams& p, int b, int h, int64_t tok0,
@@ -452,6 +467,7 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
         }
         if (p.rope.cs_t || p.rope.cs_h || p.rope.cs_w)
             rope_k_rows<WIDTH, KROW>(ktile, p, h, tok0, valid, wave, lane);
+        if (WIDTH == CK_D && p.cam.mats) camera_k_rows<KROW>(ktile, p, b, tok0, valid, wave, lane);
     } else {
         // acc[dt] element i: key 32*wave + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32.
         // The centers of keys t0 .. t0+3 at column d come from one LDS
@@ -482,6 +498,16 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
                 const u32x2 r = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                 *reinterpret_cast<u32x2*>(&sm.vt[d][vt_col(t0)]) = r;
             }
+        }
+        if (p.cam.mats) {
+            // camera P^-1 of the wave's 32 value columns of V^T: the two lane
+            // halves share key 32 * wave + l32
+            const int kt = 32 * wave + l32;
+            const float* M = camera_mats(p.cam, b, history_row(p, tok0 + (kt < valid ? kt : 0)));
+            const int col = vt_col(kt);
+            camera_row<CK_D>(
+                M, p.cam.layout, hf, [&](int d) { return bf16_bits_to_f32(sm.vt[d][col]); },
+                [&](int d, float y) { sm.vt[d][col] = f32_to_bf16_bits(y); });
         }
     }
 }
@@ -932,6 +958,7 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.o_sh = d.o_sh;
     p.lse = d.lse;
     p.rope = d.rope;
+    p.cam = d.cam;
 
     const int64_t blocks = (int64_t)d.B * d.H *
                            (p.nch_hist + (int64_t)(p.nch_total - p.nch_hist) * p.cur_splits);
@@ -1012,6 +1039,10 @@ int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace
     int rc = chunk_check(a);
     if (rc) return rc;
     ChunkLaunchDesc d = desc_from(a);
+    if (a->camera) {
+        rc = camera_from_abi(a->camera, a->D, &d.cam);
+        if (rc) return rc;
+    }
     if (a->rope) {
         rc = rope_from_abi(a->rope, a->D, &d.rope);
         if (rc) return rc;

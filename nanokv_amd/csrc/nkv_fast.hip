@@ -207,6 +207,8 @@ int validate(const nkv_fast_args* f) {
     NKV_REQUIRE(a.B >= 1 && a.H >= 1 && a.D == 128, NKV_ERR_UNSUPPORTED,
                 "fast attend supports D == 128");
     NKV_REQUIRE(a.Q >= 0 && a.N >= 0 && a.Nc >= 0, NKV_ERR_INVALID, "negative length");
+    NKV_REQUIRE(!a.camera, NKV_ERR_UNSUPPORTED,
+                "fast attend does not apply the camera transform (reader partitions)");
     if (a.rope) {
         RopeDev chk;
         int rc = rope_from_abi(a.rope, a.D, &chk);

@@ -3,6 +3,7 @@
 #pragma once
 
 #include "nkv_common.h"
+#include "nkv_camera.h"
 #include "nkv_rope.h"
 
 namespace nkv {
@@ -46,6 +47,7 @@ struct ChunkLaunchDesc {
     void* ev_begin;  // optional hipEvent_t recorded around the attention kernel
     void* ev_end;
     RopeDev rope;    // RoPE of the history keys at their codec rows (cs_t null: none)
+    CameraDev cam;   // camera P^-1 of the history keys and values (mats null: none)
 };
 
 // The decoder view of an nkv_codec for head dim D: head h reads decoder rows

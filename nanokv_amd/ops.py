@@ -19,7 +19,7 @@ from . import _lib
 from ._lib import (NKV_DTYPE_BF16, NKV_DTYPE_FP16, NKV_QUANT_BF16, NKV_QUANT_FP32,
                    NKV_SCHEDULE_AUTO, NKV_SCHEDULE_KEY_CHUNKS, NKV_SCHEDULE_QUERY_TILES,
                    NkvAttendArgs, NkvCodec, NkvDecodeArgs, NkvEncodeArgs, NkvFastArgs,
-                   NkvReaderGroup, NkvRope, check, lib)
+                   NkvCamera, NkvReaderGroup, NkvRope, check, lib)
 
 _SCALE_CODES = {torch.bfloat16: NKV_DTYPE_BF16, torch.float16: NKV_DTYPE_FP16}
 _QUANT_CODES = {"fp32": NKV_QUANT_FP32, "bf16": NKV_QUANT_BF16}
@@ -512,13 +512,73 @@ def rope_apply(x: torch.Tensor, rope: Rope, rows: Optional[torch.Tensor] = None,
     return out
 
 
+CAMERA_LAYOUTS = {"full": _lib.NKV_CAMERA_FULL, "sf13": _lib.NKV_CAMERA_SF13}
+
+
+@dataclass
+class Camera:
+    """Camera PRoPE matrices (nkv_camera) on the device: mats fp32
+    [batches, n_mats, 4 sub-frames, 4, 4] (one of P, P_T, P_inv, as the role
+    needs: keys and values take P_inv), frame_mat int32 [n_frames], the
+    matrix set of each frame of codec rows, tokens_per_frame codec rows per
+    frame; layout "full" or "sf13" (PROPE_CAMERA_LAYOUTS,
+    prope_attention.py:21-24)."""
+    mats: torch.Tensor
+    frame_mat: torch.Tensor
+    tokens_per_frame: int
+    layout: str = "full"
+
+    def struct(self) -> NkvCamera:
+        _contig(self.mats, torch.float32, "mats")
+        _contig(self.frame_mat, torch.int32, "frame_mat")
+        _require_gpu(self.mats, self.frame_mat)
+        if self.mats.dim() != 5 or tuple(self.mats.shape[2:]) != (4, 4, 4):
+            raise ValueError("mats must be [batches, n_mats, 4, 4, 4] float32")
+        if self.layout not in CAMERA_LAYOUTS:
+            raise ValueError(f"camera layout must be one of {sorted(CAMERA_LAYOUTS)}")
+        c = NkvCamera()
+        c.mats = self.mats.data_ptr()
+        c.mats_bs = self.mats.stride(0) if self.mats.shape[0] > 1 else 0
+        c.n_mats, c.layout = int(self.mats.shape[1]), CAMERA_LAYOUTS[self.layout]
+        c.frame_mat, c.n_frames = self.frame_mat.data_ptr(), int(self.frame_mat.numel())
+        c.tokens_per_frame = int(self.tokens_per_frame)
+        return c
+
+
+def camera_apply(x: torch.Tensor, camera: Camera, rows: Optional[torch.Tensor] = None,
+                 out: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Camera transform of x [B, S, H, D] bf16 at codec rows rows[s] (int32
+    [S]; None: row s) by the frame matrices of camera (nkv_camera_apply), the
+    per-frame 4x4 products of _apply_tiled_projmat / _apply_contiguous_projmat
+    (prope_attention.py:120-176).  out may be x."""
+    device = _require_gpu(x, rows, out)
+    if x.dtype != torch.bfloat16 or x.dim() != 4 or x.stride(3) != 1:
+        raise ValueError("x must be bf16 [B, S, H, D] with contiguous D")
+    B, S, H, D = (int(v) for v in x.shape)
+    if camera.mats.shape[0] not in (1, B):
+        raise ValueError("camera batch must match x or broadcast")
+    if rows is not None:
+        _contig(rows, torch.int32, "rows")
+        if rows.numel() != S:
+            raise ValueError("rows must hold one codec row per position s")
+    if out is None:
+        out = torch.empty_like(x)
+    elif out.shape != x.shape or out.dtype != torch.bfloat16 or out.stride(3) != 1:
+        raise ValueError("out must match x")
+    c = camera.struct()
+    check("nkv_camera_apply", lib().nkv_camera_apply(
+        _stream(device), byref(c), B, S, H, D, x.data_ptr(), x.stride(0), x.stride(1),
+        x.stride(2), _ptr(rows), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)))
+    return out
+
+
 def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
            key: Optional[Codec] = None, value: Optional[Codec] = None, *,
            softmax_scale: Optional[float] = None, return_lse: bool = True,
            splits: int = 0, out: Optional[torch.Tensor] = None,
            kernel_events: Optional[tuple[int, int]] = None,
            workspace: Optional[torch.Tensor] = None, schedule: str = "auto",
-           rope: Optional[Rope] = None):
+           rope: Optional[Rope] = None, camera: Optional[Camera] = None):
     """Fused decode+attention (see nkv_attend).
 
     q [B, Q, H, D] bf16; k_cur/v_cur [B, Nc, H, D] bf16 or None; key/value
@@ -529,6 +589,9 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
     schedule: "auto", "query_tiles" or "key_chunks" (nkv_schedule).
     rope: read-time RoPE of the history keys at their codec rows (q and
     k_cur are taken as already rotated); runs on the key-chunk schedule.
+    camera: camera P^-1 of the decoded history keys (after rope) and values
+    at their codec rows (q, k_cur and v_cur are taken as already
+    transformed; the caller applies P to the output); key-chunk schedule.
     """
     if schedule not in SCHEDULES:
         raise ValueError(f"schedule must be one of {sorted(SCHEDULES)}")
@@ -540,6 +603,12 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
     if rope is not None:
         rope_struct = rope.struct()
         args.rope = ctypes.pointer(rope_struct)
+    cam_struct = None
+    if camera is not None:
+        if camera.mats.shape[0] not in (1, q.shape[0]):
+            raise ValueError("camera batch must match q or broadcast")
+        cam_struct = camera.struct()
+        args.camera = ctypes.pointer(cam_struct)
     if kernel_events is not None:
         args.ev_kernel_begin, args.ev_kernel_end = kernel_events
     need = lib().nkv_attend_workspace_size(byref(args))

@@ -62,6 +62,12 @@ Pinning (the independent check that fixes each function; see tests/):
                                score q(m) . k(n) depends only on n - m; torch's
                                view_as_complex product (the reference's form)
                                agrees after rounding to bf16
+  camera_vectors / camera_apply  the reference's rearrange + einsum of both
+                               layouts (prope_attention.py:120-176) in fp64
+                               on bf16-rounded matrices, element for element;
+                               identity matrices leave x unchanged; a
+                               permutation matrix moves dims exactly; P then
+                               P^-1 returns x to bf16 rounding
 """
 from __future__ import annotations
 
@@ -386,7 +392,8 @@ def merge(out_a, lse_a, out_b, lse_b):
 
 def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Optional[dict],
                   scale: float, heads: Optional[Sequence[int]] = None, D: int = 128,
-                  dtype=np.float64, key_freqs: Optional[np.ndarray] = None):
+                  dtype=np.float64, key_freqs: Optional[np.ndarray] = None,
+                  key_cam: Optional[tuple] = None):
     """Reference decode-then-SDPA path for one batch item.
 
     q [Q, H, D] bf16 bits; k_cur/v_cur [Nc, H, D] bf16 bits or None; key/value
@@ -396,6 +403,8 @@ def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Op
     (float64 for parity checks; float32 is the reference's CPU arithmetic).
     key_freqs [N, D/2] complex128: read-time RoPE of the decoded history keys
     (wan_video_dit.py:538-546), applied before attention.
+    key_cam (mats [N, 4, 4, 4] fp32, layout): camera P^-1 of the decoded
+    history keys (after RoPE) and values at their rows (camera_apply).
     """
     q = bf16_to_f32(q_bf16)
     Qn, H = q.shape[0], q.shape[1]
@@ -406,8 +415,12 @@ def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Op
         kbits = decode(**key, columns=cols, dtype=dtype)
         if key_freqs is not None:
             kbits = rope_apply(kbits.reshape(-1, len(heads), D), key_freqs)
+        vbits = decode(**value, columns=cols, dtype=dtype)
+        if key_cam is not None:
+            kbits = camera_apply(kbits.reshape(-1, len(heads), D), *key_cam)
+            vbits = camera_apply(vbits.reshape(-1, len(heads), D), *key_cam)
         kd = bf16_to_f32(kbits)
-        vd = bf16_to_f32(decode(**value, columns=cols, dtype=dtype))
+        vd = bf16_to_f32(vbits)
         ks.append(kd.reshape(-1, len(heads), D))
         vs.append(vd.reshape(-1, len(heads), D))
     if k_cur_bf16 is not None:
@@ -470,6 +483,47 @@ def rope_apply(x_bf16, freqs) -> np.ndarray:
     """rope_apply (wan_video_dit.py:185-192): bf16 bits [S, H, D] rotated in
     fp64 and cast back (float64 -> float32 -> bfloat16, torch's cast)."""
     return f32_to_bf16(rope_rotate(x_bf16, freqs).astype(np.float32))
+
+
+# ------------------------------------------------------------ camera PRoPE
+def camera_vectors(layout: str, D: int):
+    """(dims [4], sub-frame) of every 4-vector of a D-dim head the camera
+    transforms.  "full" (_apply_tiled_projmat, prope_attention.py:120-130):
+    dims ((p*4 + c)*4 + j)*(D/64) + r over j, sub-frame c; "sf13"
+    (_apply_contiguous_projmat :133-176, PROPE_CAMERA_LAYOUTS :21-24):
+    sub-frame 1 on dims [0, 16), 3 on [16, 32), contiguous 4-vectors."""
+    out = []
+    if layout == "full":
+        if D % 64:
+            raise ValueError("full camera layout needs D % 64 == 0")
+        rn = D // 64
+        for p in range(4):
+            for c in range(4):
+                for r in range(rn):
+                    out.append(([((p * 4 + c) * 4 + j) * rn + r for j in range(4)], c))
+    elif layout == "sf13":
+        if D < 32:
+            raise ValueError("sf13 camera layout needs D >= 32")
+        for k, sub in enumerate((1, 3)):
+            for f in range(4):
+                out.append(([16 * k + 4 * f + j for j in range(4)], sub))
+    else:
+        raise ValueError(layout)
+    return out
+
+
+def camera_apply(x_bf16, mats, layout: str = "full") -> np.ndarray:
+    """Camera transform of bf16 bits x [S, H, D] by the 4x4 sub-frame
+    matrices of each row, mats [S, 4, 4, 4] fp32: the matrix entries rounded
+    to bf16 (camera_kernel.py:21-24, 34), y_i = sum_j M_ij x_j summed in fp64
+    (exact for four bf16 x bf16 products), then fp64 -> fp32 -> bf16; dims
+    the layout leaves alone are copied."""
+    x = bf16_to_f32(np.asarray(x_bf16)).astype(np.float64)
+    m = bf16_to_f32(f32_to_bf16(np.asarray(mats, np.float32))).astype(np.float64)
+    y = x.copy()
+    for dims, sub in camera_vectors(layout, x.shape[-1]):
+        y[:, :, dims] = np.einsum("sij,shj->shi", m[:, sub], x[:, :, dims])
+    return f32_to_bf16(y.astype(np.float32))
 
 
 # ----------------------------------------------------------------- a13

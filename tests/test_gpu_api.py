@@ -135,3 +135,47 @@ def test_history_attention_with_read_time_rope(dev, monkeypatch):
     diff, cos = max_abs_cos(out[0].float().cpu().numpy(), ro)
     assert diff <= 2e-2 and cos >= 0.9995, (diff, cos)
     assert np.abs(lse[0].cpu().numpy() - rl).max() < 2e-3
+
+
+def test_history_attention_with_rope_and_camera(dev, monkeypatch):
+    """codec_history_attention(rope=..., camera=kv_camera(...)) against the
+    reference's order for the decoded history: rope_apply, then P^-1 of each
+    frame on keys and values (CN/mg35.py:54-71), then attention."""
+    layer = 6
+    sh, lay = _setup(dev, layer, True, monkeypatch)
+    cache_k = cache_v = None
+    chunks_k, chunks_v = [], []
+    for c in range(3):
+        k = synth.history_rows(sh, lay.centers_k, 40, seed=50 + c).to(dev)[None].to(torch.bfloat16)
+        v = synth.history_rows(sh, lay.centers_v, 40, seed=60 + c).to(dev)[None].to(torch.bfloat16)
+        pk, pv = nc.encode_tensor("k", layer, k), nc.encode_tensor("v", layer, v)
+        chunks_k.append(pk)
+        chunks_v.append(pv)
+        cache_k, cache_v = nc.concat_values(cache_k, pk), nc.concat_values(cache_v, pv)
+    from nanokv_amd import ops
+    freqs = ops.rope_bands(D, 64)
+    positions, gh, gw = [2, 7, 3], 5, 8
+    rope = codec_native.kv_rope(freqs, positions, gh, gw, dev)
+    g = torch.Generator().manual_seed(12)
+    P_inv = torch.eye(4).expand(1, 2, 4, 4, 4) + 0.3 * torch.randn(1, 2, 4, 4, 4, generator=g)
+    frames = [1, 0, 1]
+    camera = codec_native.kv_camera(P_inv, frames, gh * gw, dev)
+    q = (torch.randn(1, H, 37, D, generator=g) / D ** 0.5).to(torch.bfloat16).to(dev)
+    kc = torch.randn(1, H, 9, D, generator=g).to(torch.bfloat16).to(dev)
+    vc = torch.randn(1, H, 9, D, generator=g).to(torch.bfloat16).to(dev)
+    out, lse = codec_native.codec_history_attention(q, cache_k, cache_v, kc, vc,
+                                                    return_lse=True, rope=rope, camera=camera)
+    ref_k = np.concatenate([_oracle_rows(p, dev) for p in chunks_k], 0)
+    ref_v = np.concatenate([_oracle_rows(p, dev) for p in chunks_v], 0)
+    table = orc.kv_freqs(tuple(b.numpy() for b in freqs), positions, gh, gw)
+    row_mats = P_inv[0].numpy()[np.repeat(frames, gh * gw)]
+    k_rot = orc.rope_apply(orc.f32_to_bf16(ref_k.reshape(120, H, D)), table)
+    k_cam = orc.bf16_to_f32(orc.camera_apply(k_rot, row_mats))
+    v_cam = orc.bf16_to_f32(orc.camera_apply(orc.f32_to_bf16(ref_v.reshape(120, H, D)), row_mats))
+    kk = np.concatenate([k_cam, orc.bf16_to_f32(u16(kc[0].permute(1, 0, 2)))], 0)
+    vv = np.concatenate([v_cam, orc.bf16_to_f32(u16(vc[0].permute(1, 0, 2)))], 0)
+    ro, rl = orc.attention(orc.bf16_to_f32(u16(q[0])), kk.transpose(1, 0, 2),
+                           vv.transpose(1, 0, 2), D ** -0.5)
+    diff, cos = max_abs_cos(out[0].float().cpu().numpy(), ro)
+    assert diff <= 2e-2 and cos >= 0.9995, (diff, cos)
+    assert np.abs(lse[0].cpu().numpy() - rl).max() < 2e-3
