@@ -57,7 +57,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 3
+#define NKV_ABI_VERSION 4
 
 enum nkv_status {
     NKV_OK = 0,
@@ -119,6 +119,10 @@ int nkv_int8_dequant(void* stream, const int8_t* q, const uint16_t* scale, int64
  *   y[2p] = x[2p] c - x[2p+1] s,  y[2p+1] = x[2p] s + x[2p+1] c,
  * rounded to fp32 and then to bf16 (torch's float64 -> bfloat16).
  * pt + ph + pw must be D / 2.  Table pointers are device memory.
+ * Per-row table (cs_rows != NULL, the reference's own per-token cache_freqs
+ * layout [n, 1, D/2] complex128 viewed as real): pair p of row n rotates by
+ * cs_rows[n][p] (n clamped to [0, n_rows)); the bands, frame_pos and the
+ * grid are then ignored.
  */
 typedef struct nkv_rope {
     const double* cs_t;           /* [n_t, pt, 2] temporal band */
@@ -129,6 +133,9 @@ typedef struct nkv_rope {
     int n_t;
     int pt, ph, pw;
     int grid_h, grid_w;
+    int _pad;
+    const double* cs_rows;        /* [n_rows, D/2, 2] per-row table, or NULL */
+    int64_t n_rows;
 } nkv_rope;
 
 /*
@@ -144,7 +151,9 @@ typedef struct nkv_rope {
  * leaves the rest.  Row n of batch item b uses matrix set
  * frame_mat[n / tokens_per_frame] of mats + b * mats_bs (frame and set
  * indices clamped to range).  mats must be 16-byte aligned and mats_bs a
- * multiple of 4.
+ * multiple of 4.  n_batches is the number of matrix batches mats holds; a
+ * call over B batch items needs mats_bs == 0 (one set shared by every item)
+ * or B <= n_batches.
  */
 enum nkv_camera_layout { NKV_CAMERA_FULL = 0, NKV_CAMERA_SF13 = 1 };
 
@@ -156,7 +165,7 @@ typedef struct nkv_camera {
     const int32_t* frame_mat;     /* [n_frames] matrix set of each frame, device */
     int64_t n_frames;
     int tokens_per_frame;
-    int _pad;
+    int n_batches;                /* matrix batches in mats (>= B unless mats_bs == 0) */
 } nkv_camera;
 
 /* out[b, s, h, :] = the camera transform of x[b, s, h, :] at row rows[s]
@@ -211,9 +220,38 @@ int nkv_unpack(void* stream, const uint8_t* packed, const uint16_t* scales, int 
 int nkv_assign(void* stream, const float* x, const uint16_t* centers, int64_t rows, int C,
                int HD, void* ids, int id_bytes);
 
-/* One K or V codec as stored in the cache (one segment or a concatenation of
- * segments that share one center table; per-segment tables are concatenated
- * by the caller with ids offset accordingly). */
+/*
+ * One immutable segment of a codec cache (a payload of the reference's
+ * worldplay_segments_v1 list, nanokv_codec.py:600-609): its own packed
+ * codes, scales, center ids and center table.  Segment s holds codec rows
+ * [row_start, row_start + rows); the segments of a codec are in row order and
+ * contiguous from row 0 (row_start of segment s = the sum of the rows before
+ * it).  center_base = the sum of num_centers of the segments before it (the
+ * row of this segment's table in the concatenation of all tables, used when
+ * the library projects the tables of every segment at once).  Every segment
+ * of a codec has centers, or none does.
+ */
+typedef struct nkv_segment {
+    const uint8_t* packed;        /* [B, rows, r/2] */
+    const uint16_t* scales;       /* [B, rows, r/group] */
+    const void* ids;              /* [B, rows] of id_bytes, or NULL (no centers) */
+    const uint16_t* centers;      /* [B or 1, num_centers, HD] bf16, or NULL */
+    int64_t row_start;
+    int64_t rows;
+    int64_t centers_batch_stride; /* elements between batch tables; 0 = shared */
+    int64_t center_base;
+    int num_centers;
+    int id_bytes;
+} nkv_segment;
+
+/* One K or V codec as stored in the cache: either one flat array of all rows
+ * (packed, scales, ids, centers below) or, with n_segments > 0, the segment
+ * table (the reference's segment list, decoded segment by segment with each
+ * segment's own center table, nanokv_codec.py:393-455), given twice: as a host
+ * array the library validates and plans from, and as the same table in device
+ * memory that the kernels read.  With segments, packed/scales/ids/centers,
+ * id_bytes, num_centers and centers_batch_stride of the codec are ignored;
+ * r, group, scale_dtype, w_dec and mean apply to every segment. */
 typedef struct nkv_codec {
     const uint8_t* packed;        /* [B, N, r/2] */
     const uint16_t* scales;       /* [B, N, r/group] */
@@ -226,8 +264,10 @@ typedef struct nkv_codec {
     int scale_dtype;
     int id_bytes;
     int num_centers;
-    int _pad;
+    int n_segments;               /* 0: the flat arrays above */
     int64_t centers_batch_stride; /* elements between batch tables; 0 = shared */
+    const nkv_segment* segments;      /* host array of n_segments */
+    const nkv_segment* segments_dev;  /* the same table in device memory */
 } nkv_codec;
 
 /*
@@ -285,7 +325,8 @@ int nkv_c64_fit(void* stream, const float* x, int B, int64_t S, int HD, int C, i
  *   rows = bf16(latent @ w_dec^T + bf16(mean))                  MG:438-443
  *   rows = bf16(float(rows) + float(center[id]))                MG:445-454
  * out [B, rows, HD] bf16.  row_index (NULL = all N) selects rows of every
- * batch item.
+ * batch item.  The codec must be flat (n_segments == 0): each segment of a
+ * segment list is decoded by its own call, as the reference decodes them.
  */
 typedef struct nkv_decode_args {
     int B;
@@ -318,6 +359,20 @@ int nkv_decode(void* stream, const nkv_decode_args* args);
  * multiplied by their frame's P^-1 after decode (see nkv_camera); q, k_cur and
  * v_cur are taken as already transformed and the caller applies P to out.
  * The camera also runs on the KEY_CHUNKS schedule.
+ * hist_rows (device, NULL = rows 0 .. N-1 in order): the codec rows attended,
+ * n_hist of them (rows outside [0, N) are clamped; an empty list is a
+ * non-NULL pointer with n_hist = 0); the reference's frame selection by
+ * cache chunk id (wan_video_dit.py:509-530).
+ * cur_mask (device, NULL = every current key visible): visibility bits of the
+ * current keys per query group, bit k % 32 of word cur_mask[g*cur_mask_words
+ * + k/32] for current key k seen by the queries of group g; q_group[t] (device,
+ * NULL = group 0) is the group of query t (groups clamped to [0, n_groups)).
+ * Query groups with identical visibility are attention_grouped_mask's
+ * (CN/core.py:94-103); the bits carry any boolean mask of attention_lse
+ * (CN/core.py:45-72) and the hook's hole/chunk-id keep masks
+ * (CN/mg35.py:258-283).  A query that sees no key gets out = 0, lse = -inf.
+ * rope, camera, hist_rows, cur_mask and codec segments run on the
+ * KEY_CHUNKS schedule (AUTO picks it when any is given).
  */
 typedef struct nkv_attend_args {
     int B;
@@ -347,6 +402,12 @@ typedef struct nkv_attend_args {
     void* ev_kernel_end;
     const nkv_rope* rope;
     const nkv_camera* camera;
+    const int32_t* hist_rows;     /* [n_hist] codec rows attended, or NULL (all N) */
+    int64_t n_hist;
+    const uint32_t* cur_mask;     /* [n_groups, cur_mask_words] or NULL */
+    const int32_t* q_group;       /* [Q] mask group of each query, or NULL */
+    int n_groups;
+    int cur_mask_words;           /* >= ceil(Nc / 32) */
 } nkv_attend_args;
 
 /* Bytes of workspace nkv_attend needs for these arguments (0 if none). */
@@ -381,6 +442,13 @@ typedef struct nkv_reader_group {
      * pair of the d-wide key/query; NULL = pair j (d == D).  Used only when
      * the call applies RoPE. */
     const int32_t* rope_pairs;
+    /* Camera of the reader keys and queries (camera_selected, CN/core.py:
+     * 110-137): [num_heads, d/8] int32, the camera sub-frame of each 8-dim
+     * block of the d-wide key/query (the original block's (indices[8j] / 8) % 4);
+     * NULL = block j uses sub-frame j % 4 (d == D).  Within a block the two
+     * 4-vectors are dims {0, 2, 4, 6} and {1, 3, 5, 7}, as in the full
+     * layout.  Used only when the call applies a camera. */
+    const int32_t* cam_blocks;
 } nkv_reader_group;
 
 /*
@@ -402,6 +470,14 @@ typedef struct nkv_reader_group {
  * pre-RoPE queries q_pre, q_low = bf16(q_pre . q_reduce), and rotates the
  * pairs rope_pairs of q_low at the query positions q_rope (query t at row t)
  * and of k_low at the codec rows' positions (attend.rope).
+ * Camera (attend.camera != NULL, the FULL layout, CN/mg35.py:253-257,
+ * 310-346): attend.camera holds P^-1 of the history rows; the native
+ * partition's history keys and values are transformed in-kernel and attend.q,
+ * k_cur and v_cur are taken as already transformed; each reader group's q_low
+ * is transformed by P^T of the query rows (q_camera, query t at row t) and
+ * k_low / v_low by P^-1 on their blocks (cam_blocks).  The caller applies P
+ * to out, as for nkv_attend: with a value lift folded into the value reader
+ * (block-selection or identity lifts) P commutes with the lift.
  */
 typedef struct nkv_fast_args {
     nkv_attend_args attend;
@@ -415,6 +491,7 @@ typedef struct nkv_fast_args {
     const uint16_t* q_pre;        /* [B, Q, H, D] bf16 pre-RoPE queries (with RoPE) */
     int64_t qp_sb, qp_st, qp_sh;
     const nkv_rope* q_rope;       /* query positions (with RoPE), host pointer */
+    const nkv_camera* q_camera;   /* P^T of the query rows (with a camera), host pointer */
 } nkv_fast_args;
 
 /* Bytes of workspace nkv_fast_attend needs for these arguments. */

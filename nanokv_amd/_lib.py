@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libnanokv_hip.so"
 
-NKV_ABI_VERSION = 3
+NKV_ABI_VERSION = 4
 NKV_OK = 0
 NKV_ERR_INVALID = -1
 NKV_ERR_UNSUPPORTED = -2
@@ -37,13 +37,22 @@ EXPORTED = (
 )
 
 
+class NkvSegment(Structure):
+    _fields_ = [
+        ("packed", c_void_p), ("scales", c_void_p), ("ids", c_void_p), ("centers", c_void_p),
+        ("row_start", c_int64), ("rows", c_int64), ("centers_batch_stride", c_int64),
+        ("center_base", c_int64), ("num_centers", c_int), ("id_bytes", c_int),
+    ]
+
+
 class NkvCodec(Structure):
     _fields_ = [
         ("packed", c_void_p), ("scales", c_void_p), ("ids", c_void_p), ("centers", c_void_p),
         ("w_dec", c_void_p), ("mean", c_void_p),
         ("r", c_int), ("group", c_int), ("scale_dtype", c_int), ("id_bytes", c_int),
-        ("num_centers", c_int), ("_pad", c_int),
+        ("num_centers", c_int), ("n_segments", c_int),
         ("centers_batch_stride", c_int64),
+        ("segments", POINTER(NkvSegment)), ("segments_dev", c_void_p),
     ]
 
 
@@ -68,7 +77,8 @@ class NkvRope(Structure):
     _fields_ = [
         ("cs_t", c_void_p), ("cs_h", c_void_p), ("cs_w", c_void_p), ("frame_pos", c_void_p),
         ("n_frames", c_int64), ("n_t", c_int), ("pt", c_int), ("ph", c_int), ("pw", c_int),
-        ("grid_h", c_int), ("grid_w", c_int),
+        ("grid_h", c_int), ("grid_w", c_int), ("_pad", c_int),
+        ("cs_rows", c_void_p), ("n_rows", c_int64),
     ]
 
 
@@ -80,7 +90,7 @@ class NkvCamera(Structure):
     _fields_ = [
         ("mats", c_void_p), ("mats_bs", c_int64), ("n_mats", c_int), ("layout", c_int),
         ("frame_mat", c_void_p), ("n_frames", c_int64), ("tokens_per_frame", c_int),
-        ("_pad", c_int),
+        ("n_batches", c_int),
     ]
 
 
@@ -96,6 +106,8 @@ class NkvAttendArgs(Structure):
         ("out", c_void_p), ("o_sb", c_int64), ("o_st", c_int64), ("o_sh", c_int64),
         ("lse", c_void_p), ("ev_kernel_begin", c_void_p), ("ev_kernel_end", c_void_p),
         ("rope", POINTER(NkvRope)), ("camera", POINTER(NkvCamera)),
+        ("hist_rows", c_void_p), ("n_hist", c_int64), ("cur_mask", c_void_p),
+        ("q_group", c_void_p), ("n_groups", c_int), ("cur_mask_words", c_int),
     ]
 
 
@@ -103,7 +115,7 @@ class NkvReaderGroup(Structure):
     _fields_ = [
         ("num_heads", c_int), ("d", c_int), ("heads", c_void_p), ("q_reduce", c_void_p),
         ("k_read", c_void_p), ("v_read", c_void_p), ("k_affine", c_void_p),
-        ("v_affine", c_void_p), ("rope_pairs", c_void_p),
+        ("v_affine", c_void_p), ("rope_pairs", c_void_p), ("cam_blocks", c_void_p),
     ]
 
 
@@ -113,7 +125,7 @@ class NkvFastArgs(Structure):
         ("low_rows", c_void_p), ("n_low", c_int64), ("num_groups", c_int), ("_pad", c_int),
         ("groups", POINTER(NkvReaderGroup)),
         ("q_pre", c_void_p), ("qp_sb", c_int64), ("qp_st", c_int64), ("qp_sh", c_int64),
-        ("q_rope", POINTER(NkvRope)),
+        ("q_rope", POINTER(NkvRope)), ("q_camera", POINTER(NkvCamera)),
     ]
 
 

@@ -45,21 +45,68 @@ import torch
 from . import nanokv_codec, ops
 
 
-def attention_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
-                  mask: Optional[torch.Tensor] = None, *, scale: Optional[float] = None):
-    """softmax(q k^T * scale) v with its natural-log LSE for [B, H, S, D]
-    inputs (CN:45-72).  An empty key set gives (0, -inf) (CN:48-49).
-    Boolean visibility masks are not supported by the fused kernel."""
-    if mask is not None:
-        raise NotImplementedError("attention masks are not supported by nkv_attend")
-    scale = q.shape[-1] ** -0.5 if scale is None else scale
+def _attend_bhsd(q, k, v, scale, visibility=None):
+    """nkv_attend of [B, H, S, D] tensors with k/v as uncompressed keys."""
     qq = q.to(torch.bfloat16).permute(0, 2, 1, 3)
     if k.shape[-2] == 0:
         out, lse = ops.attend(qq.contiguous(), None, None, softmax_scale=scale)
     else:
         out, lse = ops.attend(qq.contiguous(), k.to(torch.bfloat16).permute(0, 2, 1, 3),
-                              v.to(torch.bfloat16).permute(0, 2, 1, 3), softmax_scale=scale)
+                              v.to(torch.bfloat16).permute(0, 2, 1, 3), softmax_scale=scale,
+                              visibility=visibility)
     return out.permute(0, 2, 1, 3).to(q.dtype), lse
+
+
+def attention_lse(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                  mask: Optional[torch.Tensor] = None, *, scale: Optional[float] = None):
+    """softmax(q k^T * scale) v with its natural-log LSE for [B, H, S, D]
+    inputs (CN:45-72).  An empty key set gives (0, -inf) (CN:48-49).
+    mask (True = visible) broadcasts as [..., Q or 1, N] over [B, H]; the
+    kernel takes one visibility per query group (rows of equal visibility), so
+    a mask that differs across batch items or heads runs one call per
+    (b, h).  A query that sees no key gets (0, -inf)."""
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    if mask is None or k.shape[-2] == 0:
+        return _attend_bhsd(q, k, v, scale)
+    if mask.dtype != torch.bool:
+        raise ValueError("Only boolean visibility masks are supported")
+    B, H, Qn, _ = q.shape
+    N = int(k.shape[-2])
+    if mask.dim() < 2 or mask.shape[-1] != N or mask.shape[-2] not in (1, Qn):
+        raise ValueError("mask must broadcast as [..., Q or 1, N]")
+    lead = mask.reshape(-1, *mask.shape[-2:]) if mask.dim() > 2 else mask[None]
+    if lead.shape[0] == 1:
+        vis = ops.Visibility.from_bool(lead[0].expand(Qn, N), q.device)
+        return _attend_bhsd(q, k, v, scale, vis)
+    full = mask.expand(B, H, Qn, N)
+    out = torch.empty((B, H, Qn, v.shape[-1]), device=q.device, dtype=q.dtype)
+    lse = torch.empty((B, H, Qn), device=q.device, dtype=torch.float32)
+    for b in range(B):
+        for h in range(H):
+            vis = ops.Visibility.from_bool(full[b, h], q.device)
+            o, l = _attend_bhsd(q[b:b + 1, h:h + 1], k[b:b + 1, h:h + 1], v[b:b + 1, h:h + 1],
+                                scale, vis)
+            out[b, h], lse[b, h] = o[0, 0], l[0, 0]
+    return out, lse
+
+
+def attention_grouped_mask(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor,
+                           mask: torch.Tensor, query_groups: torch.Tensor, *, scale: float):
+    """Attention where the queries of each group share one visibility row,
+    mask[0, 0, first query of the group] (CN:94-103), in one fused call: the
+    groups become the kernel's query groups."""
+    if k.shape[-2] == 0:
+        return _attend_bhsd(q, k, v, scale)
+    groups, inverse = torch.unique(query_groups.to(q.device), return_inverse=True)
+    first = torch.full((groups.numel(),), query_groups.numel(), device=q.device, dtype=torch.long)
+    first.scatter_reduce_(0, inverse, torch.arange(query_groups.numel(), device=q.device),
+                          reduce="amin")
+    rows = mask[0, 0].index_select(0, first)
+    vis = ops.Visibility.from_bool(rows, q.device)
+    # from_bool regroups equal rows; map each query's group through it
+    vis = ops.Visibility(vis.bits, vis.q_group.long().index_select(0, inverse).to(torch.int32)
+                         .contiguous())
+    return _attend_bhsd(q, k, v, scale, vis)
 
 
 def merge(out_a: torch.Tensor, lse_a: torch.Tensor, out_b: torch.Tensor, lse_b: torch.Tensor):
@@ -121,8 +168,9 @@ def codec_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
                             k_cur: Optional[torch.Tensor] = None,
                             v_cur: Optional[torch.Tensor] = None, *,
                             scale: Optional[float] = None, return_lse: bool = False,
-                            rope: Optional[ops.Rope] = None,
-                            camera: Optional[ops.Camera] = None):
+                            rope=None, camera: Optional[ops.Camera] = None,
+                            hist_rows: Optional[torch.Tensor] = None,
+                            visibility: Optional[ops.Visibility] = None):
     """Attention of q [B, H, Q, D] over [decoded history; current chunk] where
     the history is the paired codec cache (nanokv_codec payloads or segment
     lists) and k_cur/v_cur [B, H, Nc, D] are uncompressed.  Equivalent to the
@@ -134,22 +182,52 @@ def codec_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     (after RoPE) and values are multiplied by their frames' P^-1 inside the
     kernel, as _native_prope does to the decoded history (CN/mg35.py:54-71);
     q, k_cur and v_cur are taken as already transformed and the caller
-    applies P to the output."""
+    applies P to the output.  hist_rows: int32 cache rows attended (the
+    frames a chunk id selects, wan_video_dit.py:509-530); visibility: which
+    current keys each query sees (the hole and chunk-id keep masks,
+    wan_video_dit.py:454-520)."""
     device = q.device
     B, H, Qn, D = (int(x) for x in q.shape)
     key = value = None
-    if cache_k is not None and nanokv_codec.value_shape(cache_k) is not None \
-            and nanokv_codec.value_shape(cache_k)[1] > 0:
+    shape = None if cache_k is None else nanokv_codec.value_shape(cache_k)
+    if shape is not None and shape[1] > 0:
+        if camera is not None and camera.frame_mat.numel() * camera.tokens_per_frame != shape[1]:
+            raise ValueError("the camera's frames must cover exactly the cached rows "
+                             "(complete equal-sized frames)")
         key, value = nanokv_codec.history_codecs(cache_k, cache_v, device)
     qq = q.to(torch.bfloat16).permute(0, 2, 1, 3)
     kc = None if k_cur is None else k_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
     vc = None if v_cur is None else v_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
+    if key is None:
+        hist_rows = None
+    elif hist_rows is not None:
+        hist_rows = hist_rows.to(device=device, dtype=torch.int32).contiguous()
     out, lse = ops.attend(qq, kc, vc, key, value,
                           softmax_scale=D ** -0.5 if scale is None else scale,
                           return_lse=return_lse, rope=rope if key is not None else None,
-                          camera=camera if key is not None else None)
+                          camera=camera if key is not None else None, hist_rows=hist_rows,
+                          visibility=visibility if kc is not None else None)
     out = out.permute(0, 2, 1, 3)
     return (out, lse) if return_lse else out
+
+
+def _whole_blocks(indices: torch.Tensor) -> bool:
+    """Reader dims made of whole, aligned 8-dim original blocks (CN:118-123)."""
+    ind = indices.long().cpu()
+    if ind.shape[-1] % 8:
+        return False
+    blocks = ind.reshape(ind.shape[0], -1, 8)
+    return bool(torch.equal(blocks, blocks[..., :1] + torch.arange(8))) and \
+        not bool((blocks[..., 0] % 8).any())
+
+
+def _is_selection(lift: torch.Tensor, v_indices: torch.Tensor) -> bool:
+    """lift[h] [vd, D] scatters reader dim e to original dim v_indices[h, e]
+    (reader_tools.initialize_reader_state's lift) and nothing else."""
+    lf = lift.float().cpu()
+    sel = torch.zeros_like(lf)
+    sel.scatter_(2, v_indices.long().cpu()[..., None], 1.0)
+    return bool(torch.equal(lf, sel))
 
 
 def _is_identity(w: torch.Tensor) -> bool:
@@ -215,14 +293,30 @@ class ReaderGroup:
                                   and not bool((ind[:, ::2] % 2).any()))
         self.rope_pairs = (ind[:, ::2] // 2).to(device=device, dtype=torch.int32).contiguous() \
             if self.rope_complete else None
+        # camera_selected keeps whole 8-dim blocks (CN:117-127): reader block
+        # j is original block indices[8j] / 8, whose camera sub-frame is that
+        # block's index mod 4
+        self.camera_blocks = _whole_blocks(ind) and (d % 8 == 0)
+        self.cam_blocks = ((ind[:, ::8] // 8) % 4).to(device=device, dtype=torch.int32) \
+            .contiguous() if self.camera_blocks else None
+        # the camera of the values and output commutes with the value lift
+        # folded into v_read only for an identity or block-selection lift
+        self.camera_lift = self.identity_lift or (
+            _whole_blocks(self.v_indices) and _is_selection(state["lift"], self.v_indices))
 
-    def tensors(self, rope: bool = False) -> ops.ReaderTensors:
+    def tensors(self, rope: bool = False, camera: bool = False) -> ops.ReaderTensors:
         if rope and not self.rope_complete:
             raise ValueError("RoPE mapping must retain complete original pairs")
+        if camera and not self.camera_blocks:
+            raise ValueError("Invalid MG camera blocks")
+        if camera and not self.camera_lift:
+            raise ValueError("the camera of a reader group needs an identity or block-selection "
+                             "value lift (a learned lift does not commute with P)")
         return ops.ReaderTensors(heads=self.heads_dev, d=self.d, k_read=self.k_read,
                                  v_read=self.v_read, q_reduce=self.q_reduce,
                                  k_affine=self.k_affine, v_affine=self.v_affine,
-                                 rope_pairs=self.rope_pairs if rope else None)
+                                 rope_pairs=self.rope_pairs if rope else None,
+                                 cam_blocks=self.cam_blocks if camera else None)
 
 
 def enabled(prefix: str) -> bool:
@@ -312,19 +406,26 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
                            k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
                            reader: ReaderLayer, protect: torch.Tensor, *,
                            scale: Optional[float] = None, return_lse: bool = False,
-                           rope: Optional[ops.Rope] = None,
-                           q_pre: Optional[torch.Tensor] = None,
-                           q_rope: Optional[ops.Rope] = None):
+                           rope=None, q_pre: Optional[torch.Tensor] = None, q_rope=None,
+                           low: Optional[torch.Tensor] = None,
+                           camera: Optional[ops.Camera] = None,
+                           q_camera: Optional[ops.Camera] = None,
+                           visibility: Optional[ops.Visibility] = None):
     """NanoKV-Fast history attention of q [B, H, Q, D]: the protected history
     tokens (bool mask [N] over the cache) and the current chunk are attended
-    at full width by every head (mg35.py:192-303), the other history tokens
-    through each head's reader group (mg35.py:315-347), and the two are
-    merged by LSE (CN:33-42, 308).  Everything is fused in nkv_fast_attend;
-    no K/V row is materialised.  Scale: native_dim ** -0.5 (CN:287).
-    RoPE (mg35.py:207-214, 305-336): rope = kv_rope(...) of the cached
-    frames; q is then the rotated query, q_pre [B, H, Q, D] the pre-RoPE
-    query that the reader groups project, and q_rope the positions of the
-    current chunk's queries (query t at row t)."""
+    at full width by every head (mg35.py:192-303), the low history tokens
+    (bool mask [N], default: the unprotected ones) through each head's reader
+    group (mg35.py:315-347), and the two are merged by LSE (CN:33-42, 308).
+    Everything is fused in nkv_fast_attend; no K/V row is materialised.
+    Scale: native_dim ** -0.5 (CN:287).
+    RoPE (mg35.py:207-214, 305-336): rope = kv_rope(...) or an ops.RopeTable
+    of the cached rows; q is then the rotated query, q_pre [B, H, Q, D] the
+    pre-RoPE query that the reader groups project, and q_rope the positions of
+    the current chunk's queries (query t at row t).
+    Camera (mg35.py:253-257, 310-346): camera = kv_camera(P_inv, ...) of the
+    cached rows and q_camera the P^T of the query rows; q, k_cur and v_cur are
+    then already transformed, q_pre is not, and the caller applies P to the
+    output.  visibility: which current keys each query sees."""
     device = q.device
     B, H, Qn, D = (int(x) for x in q.shape)
     if H != reader.heads or D != reader.native_dim:
@@ -333,19 +434,29 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     protect = protect.to(device=device, dtype=torch.bool)
     if protect.numel() != key.tokens:
         raise ValueError("protect must have one entry per history token")
+    low = ~protect if low is None else low.to(device=device, dtype=torch.bool)
+    if low.numel() != key.tokens or bool((low & protect).any()):
+        raise ValueError("low must be a mask over the history disjoint from protect")
+    if camera is not None and camera.frame_mat.numel() * camera.tokens_per_frame != key.tokens:
+        raise ValueError("the camera's frames must cover exactly the cached rows "
+                         "(complete equal-sized frames)")
     protect_rows = torch.nonzero(protect).flatten().to(torch.int32).contiguous()
-    low_rows = torch.nonzero(~protect).flatten().to(torch.int32).contiguous()
+    low_rows = torch.nonzero(low).flatten().to(torch.int32).contiguous()
     qq = q.to(torch.bfloat16).permute(0, 2, 1, 3)
     kc = None if k_cur is None else k_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
     vc = None if v_cur is None else v_cur.to(torch.bfloat16).permute(0, 2, 1, 3)
     qp = None
-    if rope is not None:
-        if q_pre is None or q_rope is None:
-            raise ValueError("RoPE needs q_pre and q_rope for the reader groups")
+    if rope is not None and (q_pre is None or q_rope is None):
+        raise ValueError("RoPE needs q_pre and q_rope for the reader groups")
+    if camera is not None and (q_pre is None or q_camera is None):
+        raise ValueError("the camera needs q_pre and q_camera for the reader groups")
+    if q_pre is not None:
         qp = q_pre.to(torch.bfloat16).permute(0, 2, 1, 3)
-    out, lse = ops.fast_attend(qq, kc, vc, key, value, protect_rows, low_rows,
-                               [g.tensors(rope=rope is not None) for g in reader.groups],
+    groups = [g.tensors(rope=rope is not None, camera=camera is not None) for g in reader.groups]
+    out, lse = ops.fast_attend(qq, kc, vc, key, value, protect_rows, low_rows, groups,
                                softmax_scale=D ** -0.5 if scale is None else scale,
-                               return_lse=return_lse, rope=rope, q_pre=qp, q_rope=q_rope)
+                               return_lse=return_lse, rope=rope, q_pre=qp, q_rope=q_rope,
+                               camera=camera, q_camera=q_camera,
+                               visibility=visibility if kc is not None else None)
     out = out.permute(0, 2, 1, 3)
     return (out, lse) if return_lse else out

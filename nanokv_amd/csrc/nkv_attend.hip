@@ -690,7 +690,7 @@ struct AttendPlan {
 
 int check_attend_codec(const nkv_codec& c, int64_t N, int HD, const char* which) {
     (void)which;
-    NKV_REQUIRE(c.packed && c.scales && c.w_dec, NKV_ERR_INVALID,
+    NKV_REQUIRE(((c.packed && c.scales) || c.n_segments > 0) && c.w_dec, NKV_ERR_INVALID,
                 "history codec needs packed, scales and w_dec");
     NKV_REQUIRE(c.r == 64 || c.r == 128 || c.r == 256 || c.r == 384, NKV_ERR_UNSUPPORTED,
                 "fused attend supports codec ranks 64, 128, 256 and 384");
@@ -698,7 +698,7 @@ int check_attend_codec(const nkv_codec& c, int64_t N, int HD, const char* which)
                 "fused attend needs group to divide r and be a multiple of 32");
     NKV_REQUIRE(c.scale_dtype == NKV_DTYPE_BF16 || c.scale_dtype == NKV_DTYPE_FP16,
                 NKV_ERR_INVALID, "bad scale_dtype");
-    if (c.centers) {
+    if (c.centers && c.n_segments == 0) {
         NKV_REQUIRE(c.ids, NKV_ERR_INVALID, "ids required with centers");
         NKV_REQUIRE(c.id_bytes == 1 || c.id_bytes == 2 || c.id_bytes == 4, NKV_ERR_INVALID,
                     "id_bytes must be 1, 2 or 4");
@@ -787,6 +787,11 @@ namespace {
 // query tile (each history tile would otherwise be decoded once per tile)
 // and the codecs fit the chunk kernel; query tiles otherwise.  Read-time RoPE
 // is built into the key-chunk kernel only, so it always takes key chunks.
+bool key_chunks_only(const nkv_attend_args* a) {
+    return a->rope || a->camera || a->hist_rows || a->cur_mask ||
+           (a->N > 0 && (a->key.n_segments > 0 || a->value.n_segments > 0));
+}
+
 int resolve_schedule(const nkv_attend_args* a, int* schedule) {
     NKV_REQUIRE(a->schedule >= NKV_SCHEDULE_AUTO && a->schedule <= NKV_SCHEDULE_KEY_CHUNKS,
                 NKV_ERR_INVALID, "unknown schedule");
@@ -795,12 +800,13 @@ int resolve_schedule(const nkv_attend_args* a, int* schedule) {
         const bool fits = a->D == 128 &&
                           (a->N == 0 || (a->key.r % 64 == 0 && a->value.r % 64 == 0 &&
                                          a->key.group % 32 == 0 && a->value.group % 32 == 0));
-        sch = (fits && (a->Q > AT_BM || a->rope || a->camera)) ? NKV_SCHEDULE_KEY_CHUNKS
-                                                               : NKV_SCHEDULE_QUERY_TILES;
+        sch = (fits && (a->Q > AT_BM || key_chunks_only(a))) ? NKV_SCHEDULE_KEY_CHUNKS
+                                                              : NKV_SCHEDULE_QUERY_TILES;
     }
-    NKV_REQUIRE((!a->rope && !a->camera) || sch == NKV_SCHEDULE_KEY_CHUNKS, NKV_ERR_UNSUPPORTED,
-                "read-time RoPE and camera need the key-chunk schedule (D = 128, ranks that "
-                "are multiples of 64, scale groups that are multiples of 32)");
+    NKV_REQUIRE(!key_chunks_only(a) || sch == NKV_SCHEDULE_KEY_CHUNKS, NKV_ERR_UNSUPPORTED,
+                "read-time RoPE, the camera, history row lists, current-key masks and "
+                "segmented codecs need the key-chunk schedule (D = 128, ranks that are "
+                "multiples of 64, scale groups that are multiples of 32)");
     *schedule = sch;
     return NKV_OK;
 }

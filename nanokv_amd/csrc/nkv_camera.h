@@ -21,6 +21,9 @@ struct CameraDev {
     const int32_t* frame_mat = nullptr;
     int64_t n_frames = 0;
     int tokens_per_frame = 1;
+    // [launch heads, width / 8] sub-frame of each 8-dim block of a reader key
+    // (camera_selected, CN/core.py:110-137), or null: the FULL/SF13 layout
+    const int32_t* blocks = nullptr;
 };
 
 // Sub-frame matrices of codec row `row` of batch item b (indices clamped).
@@ -115,7 +118,37 @@ __device__ __forceinline__ void camera_vector_dims(int layout, int D, int v, int
     }
 }
 
-// Host: validate an nkv_camera for heads of D dims and fill dev.
-int camera_from_abi(const nkv_camera* c, int D, CameraDev* dev);
+// The camera transform of one reader row of W dims (W % 8 == 0) whose 8-dim
+// block j uses sub-frame cams[j]: within a block the 4-vectors are dims
+// {0, 2, 4, 6} and {1, 3, 5, 7} (the full layout's (j, r) order), so lane
+// half hf takes vector hf of every block.  Each sub-frame's entries are
+// loaded and rounded once per block.
+template <int W, typename Get, typename Put>
+__device__ __forceinline__ void camera_row_blocks(const float* M, const int32_t* cams, int hf,
+                                                  Get get, Put put) {
+#pragma unroll
+    for (int j = 0; j < W / 8; ++j) {
+        const int c = cams[j] & 3;
+        float m[16];
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const float4 f = reinterpret_cast<const float4*>(M + 16 * c)[q];
+            m[4 * q] = bf16_round(f.x);
+            m[4 * q + 1] = bf16_round(f.y);
+            m[4 * q + 2] = bf16_round(f.z);
+            m[4 * q + 3] = bf16_round(f.w);
+        }
+        float x[4], y[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) x[e] = get(8 * j + 2 * e + hf);
+        camera_vec4_rounded(m, x, y);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) put(8 * j + 2 * e + hf, y[e]);
+    }
+}
+
+// Host: validate an nkv_camera for heads of D dims and a call over B batch
+// items, and fill dev (blocks stays null).
+int camera_from_abi(const nkv_camera* c, int D, int B, CameraDev* dev);
 
 }  // namespace nkv

@@ -9,7 +9,7 @@
 
 namespace nkv {
 
-int camera_from_abi(const nkv_camera* c, int D, CameraDev* dev) {
+int camera_from_abi(const nkv_camera* c, int D, int B, CameraDev* dev) {
     NKV_REQUIRE(c, NKV_ERR_INVALID, "camera is null");
     NKV_REQUIRE(c->mats && c->frame_mat, NKV_ERR_INVALID, "camera needs mats and frame_mat");
     NKV_REQUIRE(c->n_mats >= 1 && c->n_frames >= 1 && c->tokens_per_frame >= 1 && c->mats_bs >= 0,
@@ -22,6 +22,8 @@ int camera_from_abi(const nkv_camera* c, int D, CameraDev* dev) {
                 "the FULL camera layout needs D % 64 == 0");
     NKV_REQUIRE(c->layout != NKV_CAMERA_SF13 || D >= 32, NKV_ERR_INVALID,
                 "the SF13 camera layout needs D >= 32");
+    NKV_REQUIRE(c->mats_bs == 0 || B <= c->n_batches, NKV_ERR_INVALID,
+                "camera mats hold fewer matrix batches than the call's batch items");
     dev->mats = c->mats;
     dev->mats_bs = c->mats_bs;
     dev->n_mats = c->n_mats;
@@ -29,6 +31,7 @@ int camera_from_abi(const nkv_camera* c, int D, CameraDev* dev) {
     dev->frame_mat = c->frame_mat;
     dev->n_frames = c->n_frames;
     dev->tokens_per_frame = c->tokens_per_frame;
+    dev->blocks = nullptr;
     return NKV_OK;
 }
 
@@ -86,7 +89,7 @@ extern "C" int nkv_camera_apply(void* stream, const nkv_camera* camera, int B, i
                                 int64_t o_st, int64_t o_sh) {
     clear_error();
     CameraApplyParams p;
-    int rc = camera_from_abi(camera, D, &p.cam);
+    int rc = camera_from_abi(camera, D, B, &p.cam);
     if (rc) return rc;
     NKV_REQUIRE(B >= 0 && S >= 0 && H >= 0, NKV_ERR_INVALID, "negative shape");
     if ((int64_t)B * S * H == 0) return NKV_OK;

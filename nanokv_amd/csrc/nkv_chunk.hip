@@ -84,6 +84,10 @@ struct ChunkParams {
     float* lse;
     RopeDev rope;       // RoPE of the history keys (cs_t null: none)
     CameraDev cam;      // camera P^-1 of the history keys and values (mats null: none)
+    const uint32_t* cur_mask;  // visibility of the current keys per query group, or null
+    const int32_t* q_group;
+    int n_groups, mask_words;
+    int64_t blk_base;   // first work item of this launch (blockIdx.x + blk_base)
 };
 
 // Codec row of attended history key `key`; rows outside the codec are
@@ -209,7 +213,7 @@ typedef short short4v __attribute__((ext_vector_type(4)));
 struct Chunk8Smem {
     uint16_t k[CK_T][CK_KROW];  // K tile (also decoder-slice and center staging)
     uint16_t vt[CK_D][C8_VROW];  // V^T[d][vt_col(key)]
-    int ids[2][CK_T];
+    const uint16_t* crow[2][CK_T];  // center row of each key (the launch head's columns)
     float bias[2][CK_D];
 };
 static_assert(sizeof(Chunk8Smem) <= 160 * 1024, "LDS budget");
@@ -227,14 +231,12 @@ __device__ __forceinline__ int vt_col(int key) {
 
 // The V center rows of the wave's 32 keys, copied into LDS rows [key][128]
 // (unpadded) by 8 direct-to-LDS loads of 4 rows each.
-__device__ __forceinline__ void dma_v_centers8(uint16_t* vcen, const Chunk8Smem& sm,
-                                               const ChunkCodec& c, int b, int h, int wave,
+__device__ __forceinline__ void dma_v_centers8(uint16_t* vcen, const Chunk8Smem& sm, int wave,
                                                int lane) {
-    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs + 8 * (lane & 15);
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
         const int t = 32 * wave + 4 * e + (lane >> 4);
-        __builtin_amdgcn_global_load_lds(cent + (int64_t)sm.ids[1][t] * c.c_rs,
+        __builtin_amdgcn_global_load_lds(sm.crow[1][t] + 8 * (lane & 15),
                                          NKV_LDS(vcen + (32 * wave + 4 * e) * CK_D), 16, 0, 0);
     }
 }
@@ -244,15 +246,12 @@ __device__ __forceinline__ void dma_v_centers8(uint16_t* vcen, const Chunk8Smem&
 // 8 * (q % (DK/8)).
 template <int DK>
 __device__ __forceinline__ void load_k_center_rows8(u32x4 (&v)[DK / 16], const Chunk8Smem& sm,
-                                                    const ChunkCodec& c, int b, int h, int wave,
-                                                    int lane) {
+                                                    int wave, int lane) {
     constexpr int PR = DK / 8;
-    const uint16_t* cent = c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs;
 #pragma unroll
     for (int e = 0; e < DK / 16; ++e) {
         const int q = 64 * e + lane;
-        v[e] = *reinterpret_cast<const u32x4*>(cent + (int64_t)sm.ids[0][32 * wave + q / PR] * c.c_rs +
-                                               8 * (q % PR));
+        v[e] = *reinterpret_cast<const u32x4*>(sm.crow[0][32 * wave + q / PR] + 8 * (q % PR));
     }
 }
 
@@ -293,16 +292,21 @@ __device__ __forceinline__ void rope_k_rows(uint16_t* ktile, const ChunkParams& 
 }
 
 // Camera P^-1 of the wave's 32 decoded keys (after RoPE) in the K tile: the
-// two lane halves share key 32 * wave + l32.  Full-width keys only.
-template <int KROW>
-__device__ __forceinline__ void camera_k_rows(uint16_t* ktile, const ChunkParams& p, int b,
+// two lane halves share key 32 * wave + l32.  Full-width keys use the
+// camera's layout; reader keys (WIDTH < 128, or a block map) the launch
+// head's sub-frame of each 8-dim block.
+template <int WIDTH, int KROW>
+__device__ __forceinline__ void camera_k_rows(uint16_t* ktile, const ChunkParams& p, int b, int h,
                                               int64_t tok0, int valid, int wave, int lane) {
     const int hf = lane >> 5, kt = 32 * wave + (lane & 31);
     const float* M = camera_mats(p.cam, b, history_row(p, tok0 + (kt < valid ? kt : 0)));
     uint16_t* krow = ktile + kt * KROW;
-    camera_row<CK_D>(
-        M, p.cam.layout, hf, [&](int d) { return bf16_bits_to_f32(krow[d]); },
-        [&](int d, float y) { krow[d] = f32_to_bf16_bits(y); });
+    auto get = [&](int d) { return bf16_bits_to_f32(krow[d]); };
+    auto put = [&](int d, float y) { krow[d] = f32_to_bf16_bits(y); };
+    if (p.cam.blocks)
+        camera_row_blocks<WIDTH>(M, p.cam.blocks + (int64_t)h * (WIDTH / 8), hf, get, put);
+    else if (WIDTH == CK_D)
+        camera_row<CK_D>(M, p.cam.layout, hf, get, put);
 }
 
 template <int CODEC, bool HAS_C, int WIDTH, int KROW, typename Pre>
@@ -315,13 +319,14 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
     constexpr int STAGE = LPW + 2;                           // vm instructions per stage
     constexpr int SLICE = WIDTH * 64;
     const int hf = lane >> 5, l32 = lane & 31;
-    const int R = c.r, KQ = R >> 6, G = c.group, NG = R / G;
+    const int R = c.r, KQ = R >> 6, G = c.group;
     const bool f16 = c.scale_dtype == NKV_DTYPE_FP16;
     const int tl = 32 * wave + l32;
     // keys past the chunk end decode key 0's codes (finite, never attended)
-    const int64_t tok = (int64_t)b * p.N + history_row(p, tok0 + (tl < valid ? tl : 0));
-    const uint8_t* prow = c.packed + tok * (R / 2) + 16 * hf;
-    const uint16_t* srow = c.scales + tok * NG;
+    const uint8_t* prow;
+    const uint16_t* srow;
+    codec_row_ptrs(c, b, p.N, history_row(p, tok0 + (tl < valid ? tl : 0)), prow, srow);
+    prow += 16 * hf;
     // slice pieces: lane L of piece q brings logical chunk
     // (L % 8) ^ ((row >> 1) & 7) of row 8 q + L / 8
     const int piece_row = lane >> 3;
@@ -347,7 +352,7 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
 
     uint16_t* vcen = &sm.k[0][0];
     u32x4 kcen[WIDTH / 16];
-    if (CODEC == 0 && HAS_C) load_k_center_rows8<WIDTH>(kcen, sm, c, b, h, wave, lane);
+    if (CODEC == 0 && HAS_C) load_k_center_rows8<WIDTH>(kcen, sm, wave, lane);
     u32x4 pk[DS_AHEAD];
     uint16_t sc[DS_AHEAD];
 #pragma unroll
@@ -359,7 +364,7 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
         }
     pre();
     constexpr int NVC = CODEC == 1 && HAS_C ? 8 : 0;
-    if (CODEC == 1 && HAS_C) dma_v_centers8(vcen, sm, c, b, h, wave, lane);
+    if (CODEC == 1 && HAS_C) dma_v_centers8(vcen, sm, wave, lane);
     __builtin_amdgcn_sched_barrier(0);
 
     int wofs[4];
@@ -465,9 +470,8 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
                 *slot = r;
             }
         }
-        if (p.rope.cs_t || p.rope.cs_h || p.rope.cs_w)
-            rope_k_rows<WIDTH, KROW>(ktile, p, h, tok0, valid, wave, lane);
-        if (WIDTH == CK_D && p.cam.mats) camera_k_rows<KROW>(ktile, p, b, tok0, valid, wave, lane);
+        if (rope_on(p.rope)) rope_k_rows<WIDTH, KROW>(ktile, p, h, tok0, valid, wave, lane);
+        if (p.cam.mats) camera_k_rows<WIDTH, KROW>(ktile, p, b, h, tok0, valid, wave, lane);
     } else {
         // acc[dt] element i: key 32*wave + 8*(i/4) + 4*hf + i%4, d = 32*dt + l32.
         // The centers of keys t0 .. t0+3 at column d come from one LDS
@@ -553,10 +557,14 @@ __device__ __forceinline__ void load_current_chunk8(Chunk8Smem& sm, const ChunkP
 // P^T (8 MFMAs).  The next step's K and V fragments are read as soon as the
 // current ones have been issued to the matrix core, and the next block's
 // queries are requested during its predecessor.
-template <int DK>
+// MASK: the chunk holds current keys tok0 .. (keys of the current chunk) and
+// each query sees only the keys its group's bits of p.cur_mask allow; a
+// query that sees no key of a step keeps m = -inf, and its exponentials use
+// 0 as the reference so that they are 0, not NaN.
+template <int DK, bool MASK>
 __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams& p, int b, int h,
                                         int bh, int chunk, int wave, int lane_in, int nsub,
-                                        int valid, int qb_lo, int qb_hi) {
+                                        int valid, int qb_lo, int qb_hi, int64_t tok0) {
     int lane = lane_in;
     asm volatile("" : "+v"(lane));
     const int hf = lane >> 5, l32 = lane & 31;
@@ -587,8 +595,20 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
     const bool full = valid == CK_T;
     for (int qb = qb_lo + wave; qb < qb_hi; qb += C8_WAVES) {
         const int64_t q0 = (int64_t)qb * 32;
-        // the next block's queries (rows past Q are clamped to q0)
-        load_q_block<DK>(qn, p, b, h, q0 + 32 * C8_WAVES, q0, lane);
+        // the next block's queries (rows past Q are clamped to q0); the
+        // masked instance loads each block's queries when it starts instead,
+        // which leaves the registers its mask needs
+        if (MASK) {
+            if (qb != qb_lo + wave) load_q_block<DK>(qf, p, b, h, q0, q0, lane);
+        } else {
+            load_q_block<DK>(qn, p, b, h, q0 + 32 * C8_WAVES, q0, lane);
+        }
+        const uint32_t* mrow = nullptr;
+        if (MASK) {
+            const int64_t qi = min(q0 + l32, p.Q - 1);
+            const int g = p.q_group ? min(max(p.q_group[qi], 0), p.n_groups - 1) : 0;
+            mrow = p.cur_mask + (int64_t)g * p.mask_words + (tok0 >> 5);
+        }
         f32x16 o[4];
         float m = -INFINITY, l = 0.0f;
         for (int j = 0; j < nsub; ++j) {
@@ -610,6 +630,12 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
                 for (int i = 0; i < 16; ++i)
                     if (8 * (i >> 2) + 4 * hf + (i & 3) >= vj) s[i] = -INFINITY;
             }
+            if (MASK) {
+                const uint32_t bits = mrow[j];
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (!((bits >> (8 * (i >> 2) + 4 * hf + (i & 3))) & 1u)) s[i] = -INFINITY;
+            }
             // online softmax of the 32-key x 32-query tile
             float tm = fmaxf(s[0], s[1]);
 #pragma unroll
@@ -619,13 +645,14 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
             const float mn = up ? tm : m;
             const float alpha = up ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
             m = mn;
+            const float mref = MASK && mn == -INFINITY ? 0.0f : mn;
             uint32_t pw[8];
             float lsum = 0.0f;
 #pragma unroll
             for (int k = 0; k < 8; ++k) {
                 // v_exp_f32 of arguments <= 8; results below 2^-126 flush to 0
-                pw[k] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(s[2 * k], c, -mn)),
-                                    __builtin_amdgcn_exp2f(fmaf(s[2 * k + 1], c, -mn)));
+                pw[k] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(s[2 * k], c, -mref)),
+                                    __builtin_amdgcn_exp2f(fmaf(s[2 * k + 1], c, -mref)));
                 lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[k]),
                                                        __builtin_bit_cast(bf16x2, 0x3F803F80u),
                                                        lsum, false);
@@ -654,12 +681,17 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
             for (int t = 0; t < 8; ++t) vf[t] = lds_v(jn, t);
         }
         store_partial(p, bh, chunk, q0, o, m, halfwave_sum(l), lane);
+        if (!MASK) {
 #pragma unroll
-        for (int kk = 0; kk < KS; ++kk) qf[kk] = qn[kk];
+            for (int kk = 0; kk < KS; ++kk) qf[kk] = qn[kk];
+        }
     }
 }
 
-template <int DK>
+// MASK: the launch covers only the current-key chunks, attended under
+// p.cur_mask (a separate instance, so that the mask's registers do not
+// burden the history chunks' decode and attention).
+template <int DK, bool MASK>
 __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
     constexpr int KROW = KTile<DK>::ROW;
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -671,12 +703,13 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
     // (smaller work items where the grid drains)
     const int BH = p.B * p.H;
     const int64_t nh = (int64_t)p.nch_hist * BH;
+    const int64_t item = (int64_t)blockIdx.x + p.blk_base;
     int bh, chunk, qb_lo = 0, qb_hi = p.qblocks;
-    if ((int64_t)blockIdx.x < nh) {
-        bh = blockIdx.x % BH;
-        chunk = blockIdx.x / BH;
+    if (item < nh) {
+        bh = (int)(item % BH);
+        chunk = (int)(item / BH);
     } else {
-        const int c = (int)(blockIdx.x - nh), ncur = p.nch_total - p.nch_hist;
+        const int c = (int)(item - nh), ncur = p.nch_total - p.nch_hist;
         bh = c % BH;
         const int rest = c / BH;
         chunk = p.nch_hist + rest % ncur;
@@ -689,21 +722,17 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
     const int64_t tok0 = (int64_t)(hist ? chunk : chunk - p.nch_hist) * CK_T;
     const int valid = (int)min((int64_t)CK_T, (hist ? p.n_rows : p.Nc) - tok0);
 
-    if (hist) {
+    if (!MASK && hist) {
         auto publish = [&]() {
             if (t < CK_T) {
 #pragma unroll
                 for (int cc = 0; cc < 2; ++cc) {
                     const ChunkCodec& cd = p.codec[cc];
-                    int id = 0;
-                    if (cd.centers && t < valid) {
-                        // ids outside the table are clamped so that a corrupt
-                        // payload cannot read out of bounds
-                        id = read_id(cd.ids, cd.id_bytes,
-                                     (int64_t)b * p.N + history_row(p, tok0 + t));
-                        id = min(max(id, 0), cd.num_centers - 1);
-                    }
-                    sm.ids[cc][t] = id;
+                    // keys past the chunk end take key 0's center (finite,
+                    // never attended)
+                    if (cd.has_centers)
+                        sm.crow[cc][t] = center_row(cd, b, h, p.N,
+                                                    history_row(p, tok0 + (t < valid ? t : 0)));
                     if (t < (cc == 0 ? DK : CK_D))
                         sm.bias[cc][t] =
                             cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
@@ -714,14 +743,14 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
         auto nothing = []() {};
         uint16_t* vt_scratch = &sm.vt[0][0];
         uint16_t* k_scratch = &sm.k[0][0];
-        if (p.codec[1].centers)
+        if (p.codec[1].has_centers)
             decode_codec8<1, true, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
                                                wave, lane, publish);
         else
             decode_codec8<1, false, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
                                                 wave, lane, publish);
         __syncthreads();
-        if (p.codec[0].centers)
+        if (p.codec[0].has_centers)
             decode_codec8<0, true, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
                                              wave, lane, nothing);
         else
@@ -731,7 +760,8 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
         load_current_chunk8(sm, p, b, h, tok0, valid, t);
     }
     __syncthreads();
-    attend8<DK>(sm, p, b, h, bh, chunk, wave, lane, (valid + 31) / 32, valid, qb_lo, qb_hi);
+    attend8<DK, MASK>(sm, p, b, h, bh, chunk, wave, lane, (valid + 31) / 32, valid, qb_lo, qb_hi,
+                      tok0);
 }
 
 // Merge the chunk partials of every (b, h, q).  One wave owns one 32-query
@@ -834,23 +864,60 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
 // ------------------------------------------------------------------ host
 ChunkCodec chunk_codec_from(const nkv_codec& c, int D, int HD) {
     ChunkCodec v{};
-    v.packed = c.packed;
-    v.scales = c.scales;
-    v.ids = c.centers ? c.ids : nullptr;
     v.r = c.r;
     v.group = c.group;
     v.scale_dtype = c.scale_dtype;
-    v.id_bytes = c.id_bytes;
-    v.num_centers = c.num_centers;
     v.w = c.w_dec;
     v.w_hs = (int64_t)D * c.r;
-    v.centers = c.centers;
-    v.c_bs = c.centers_batch_stride;
     v.c_rs = HD;
     v.c_hs = D;
     v.bias = c.mean;
     v.bias_hs = D;
+    if (c.n_segments > 0) {
+        // each segment's own table (checked on the host: all or none have one)
+        v.seg = c.segments_dev;
+        v.n_seg = c.n_segments;
+        v.seg_flat = 0;
+        v.has_centers = c.segments[0].centers != nullptr;
+        return v;
+    }
+    v.packed = c.packed;
+    v.scales = c.scales;
+    v.ids = c.centers ? c.ids : nullptr;
+    v.id_bytes = c.id_bytes;
+    v.num_centers = c.num_centers;
+    v.centers = c.centers;
+    v.c_bs = c.centers_batch_stride;
+    v.has_centers = c.centers != nullptr;
     return v;
+}
+
+int check_segments(const nkv_codec& c, int64_t N) {
+    if (c.n_segments == 0) return NKV_OK;
+    NKV_REQUIRE(c.n_segments > 0 && c.segments && c.segments_dev, NKV_ERR_INVALID,
+                "a segmented codec needs its host and device segment tables");
+    const bool cent = c.segments[0].centers != nullptr;
+    int64_t row = 0, cbase = 0;
+    for (int i = 0; i < c.n_segments; ++i) {
+        const nkv_segment& s = c.segments[i];
+        NKV_REQUIRE(s.packed && s.scales && s.rows >= 1, NKV_ERR_INVALID,
+                    "every segment needs packed codes, scales and at least one row");
+        NKV_REQUIRE(s.row_start == row, NKV_ERR_INVALID,
+                    "segments must be in row order and contiguous from row 0");
+        NKV_REQUIRE((s.centers != nullptr) == cent, NKV_ERR_INVALID,
+                    "every segment must have a center table, or none");
+        if (cent) {
+            NKV_REQUIRE(s.ids && (s.id_bytes == 1 || s.id_bytes == 2 || s.id_bytes == 4) &&
+                            s.num_centers > 0 && s.centers_batch_stride >= 0,
+                        NKV_ERR_INVALID, "segment centers need ids of 1, 2 or 4 bytes");
+            NKV_REQUIRE(s.center_base == cbase, NKV_ERR_INVALID,
+                        "segment center_base must be the sum of the tables before it");
+            cbase += s.num_centers;
+        }
+        row += s.rows;
+    }
+    NKV_REQUIRE(row == N, NKV_ERR_INVALID, "the segments must hold exactly the codec's N rows");
+    return NKV_OK;
 }
 
 namespace {
@@ -858,7 +925,7 @@ namespace {
 int64_t chunk_count(int64_t keys) { return cdiv(keys, CK_T); }
 
 int check_chunk_codec(const ChunkCodec& c) {
-    NKV_REQUIRE(c.packed && c.scales && c.w, NKV_ERR_INVALID,
+    NKV_REQUIRE((c.seg || (c.packed && c.scales)) && c.w, NKV_ERR_INVALID,
                 "history codec needs packed codes, scales and decode rows");
     NKV_REQUIRE(c.r > 0 && c.r % 64 == 0 && c.r <= 4096, NKV_ERR_UNSUPPORTED,
                 "key-chunk attend needs codec ranks that are multiples of 64");
@@ -866,25 +933,28 @@ int check_chunk_codec(const ChunkCodec& c) {
                 "key-chunk attend needs scale groups that are multiples of 32 dividing r");
     NKV_REQUIRE(c.scale_dtype == NKV_DTYPE_BF16 || c.scale_dtype == NKV_DTYPE_FP16,
                 NKV_ERR_INVALID, "bad scale_dtype");
-    if (c.centers) {
-        NKV_REQUIRE(c.ids && (c.id_bytes == 1 || c.id_bytes == 2 || c.id_bytes == 4),
+    if (c.has_centers && !c.seg) {
+        NKV_REQUIRE(c.centers && c.ids && (c.id_bytes == 1 || c.id_bytes == 2 || c.id_bytes == 4),
                     NKV_ERR_INVALID, "centers need ids of 1, 2 or 4 bytes");
         NKV_REQUIRE(c.num_centers > 0, NKV_ERR_INVALID, "num_centers must be > 0");
     }
+    NKV_REQUIRE(!c.seg || c.n_seg > 0, NKV_ERR_INVALID, "empty segment table");
+    NKV_REQUIRE(!(c.seg && c.has_centers && c.seg_flat) || c.centers, NKV_ERR_INVALID,
+                "a flat center table is missing");
     return NKV_OK;
 }
 
-template <int DK>
+template <int DK, bool MASK>
 void launch_dk(const ChunkParams& p, int64_t blocks, hipStream_t s, int* rc) {
     const size_t smem = sizeof(Chunk8Smem);
-    hipError_t e = hipFuncSetAttribute((const void*)chunk8_kernel<DK>,
+    hipError_t e = hipFuncSetAttribute((const void*)chunk8_kernel<DK, MASK>,
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) {
         set_error(std::string("chunk_launch: hipFuncSetAttribute failed: ") + hipGetErrorString(e));
         *rc = NKV_ERR_HIP;
         return;
     }
-    chunk8_kernel<DK><<<dim3((unsigned)blocks), C8_THREADS, smem, s>>>(p);
+    chunk8_kernel<DK, MASK><<<dim3((unsigned)blocks), C8_THREADS, smem, s>>>(p);
     e = hipGetLastError();
     if (e != hipSuccess) {
         set_error(std::string("chunk_launch: launch failed: ") + hipGetErrorString(e));
@@ -907,6 +977,9 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
                 "bad launch shape");
     NKV_REQUIRE(d.Nc == 0 || (d.dk == CK_D && d.k_cur && d.v_cur), NKV_ERR_INVALID,
                 "current keys need k_cur/v_cur and a 128-wide launch");
+    NKV_REQUIRE(!d.cur_mask || (d.n_groups >= 1 && d.mask_words >= cdiv(d.Nc, 32)),
+                NKV_ERR_INVALID, "the current-key mask needs n_groups >= 1 and "
+                "cur_mask_words >= ceil(Nc / 32)");
     if (d.n_rows > 0) {
         int rc = check_chunk_codec(d.key);
         if (rc) return rc;
@@ -959,15 +1032,34 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.lse = d.lse;
     p.rope = d.rope;
     p.cam = d.cam;
+    p.cur_mask = d.Nc > 0 ? d.cur_mask : nullptr;
+    p.q_group = d.q_group;
+    p.n_groups = d.n_groups;
+    p.mask_words = d.mask_words;
 
-    const int64_t blocks = (int64_t)d.B * d.H *
-                           (p.nch_hist + (int64_t)(p.nch_total - p.nch_hist) * p.cur_splits);
+    const int64_t hist_blocks = (int64_t)d.B * d.H * p.nch_hist;
+    const int64_t cur_blocks = (int64_t)d.B * d.H * (p.nch_total - p.nch_hist) * p.cur_splits;
+    p.blk_base = 0;
     if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
-    if (blocks > 0) {
-        int rc = NKV_OK;
-        if (d.dk == 128) launch_dk<128>(p, blocks, s, &rc);
-        else if (d.dk == 64) launch_dk<64>(p, blocks, s, &rc);
-        else launch_dk<32>(p, blocks, s, &rc);
+    int rc = NKV_OK;
+    if (p.cur_mask) {
+        // history chunks, then the masked current-key chunks (128 wide)
+        if (hist_blocks > 0) {
+            if (d.dk == 128) launch_dk<128, false>(p, hist_blocks, s, &rc);
+            else if (d.dk == 64) launch_dk<64, false>(p, hist_blocks, s, &rc);
+            else launch_dk<32, false>(p, hist_blocks, s, &rc);
+            if (rc) return rc;
+        }
+        if (cur_blocks > 0) {
+            p.blk_base = hist_blocks;
+            launch_dk<128, true>(p, cur_blocks, s, &rc);
+            if (rc) return rc;
+        }
+    } else if (hist_blocks + cur_blocks > 0) {
+        const int64_t blocks = hist_blocks + cur_blocks;
+        if (d.dk == 128) launch_dk<128, false>(p, blocks, s, &rc);
+        else if (d.dk == 64) launch_dk<64, false>(p, blocks, s, &rc);
+        else launch_dk<32, false>(p, blocks, s, &rc);
         if (rc) return rc;
     }
     if (d.ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_end, s));
@@ -989,8 +1081,8 @@ ChunkLaunchDesc desc_from(const nkv_attend_args* a) {
     d.dk = a->D;
     d.Q = a->Q;
     d.N = a->N;
-    d.n_rows = a->N;
-    d.rows = nullptr;
+    d.n_rows = a->hist_rows ? a->n_hist : a->N;
+    d.rows = a->hist_rows;
     d.Nc = a->Nc;
     d.softmax_scale = a->softmax_scale;
     d.q = a->q;
@@ -1015,6 +1107,10 @@ ChunkLaunchDesc desc_from(const nkv_attend_args* a) {
     d.lse = a->lse;
     d.ev_begin = a->ev_kernel_begin;
     d.ev_end = a->ev_kernel_end;
+    d.cur_mask = a->cur_mask;
+    d.q_group = a->q_group;
+    d.n_groups = a->n_groups;
+    d.mask_words = a->cur_mask_words;
     return d;
 }
 }  // namespace
@@ -1023,7 +1119,13 @@ size_t chunk_workspace_bytes(const nkv_attend_args* a) { return chunk_launch_wor
 
 int chunk_check(const nkv_attend_args* a) {
     NKV_REQUIRE(a->D == CK_D, NKV_ERR_UNSUPPORTED, "key-chunk attend supports D == 128");
+    NKV_REQUIRE(!a->hist_rows || (a->n_hist >= 0 && a->n_hist <= INT32_MAX), NKV_ERR_INVALID,
+                "bad n_hist");
     if (a->N > 0) {
+        int rc = check_segments(a->key, a->N);
+        if (rc) return rc;
+        rc = check_segments(a->value, a->N);
+        if (rc) return rc;
         for (const nkv_codec* c : {&a->key, &a->value}) {
             NKV_REQUIRE(c->r > 0 && c->r % 64 == 0 && c->r <= 4096, NKV_ERR_UNSUPPORTED,
                         "key-chunk attend needs codec ranks that are multiples of 64");
@@ -1040,13 +1142,13 @@ int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace
     if (rc) return rc;
     ChunkLaunchDesc d = desc_from(a);
     if (a->camera) {
-        rc = camera_from_abi(a->camera, a->D, &d.cam);
+        rc = camera_from_abi(a->camera, a->D, a->B, &d.cam);
         if (rc) return rc;
     }
     if (a->rope) {
         rc = rope_from_abi(a->rope, a->D, &d.rope);
         if (rc) return rc;
-        NKV_REQUIRE(a->N <= a->rope->n_frames * (int64_t)a->rope->grid_h * a->rope->grid_w,
+        NKV_REQUIRE(a->N <= rope_rows_covered(a->rope),
                     NKV_ERR_INVALID, "more history tokens than the RoPE frames cover");
     }
     return chunk_launch(s, d, workspace, workspace_bytes);

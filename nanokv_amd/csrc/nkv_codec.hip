@@ -1274,6 +1274,8 @@ extern "C" int nkv_decode(void* stream, const nkv_decode_args* a) {
     if (rc) return rc;
     NKV_REQUIRE(a->row_index || a->rows == a->N, NKV_ERR_INVALID,
                 "rows must equal N without row_index");
+    NKV_REQUIRE(c.n_segments == 0, NKV_ERR_UNSUPPORTED,
+                "nkv_decode takes a flat codec; decode segments one at a time");
     if (c.centers) {
         rc = check_ids(c.num_centers, c.id_bytes);
         if (rc) return rc;

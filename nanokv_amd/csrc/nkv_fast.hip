@@ -20,7 +20,14 @@
 //  3. merge(out, lse_n, out_l, lse_l) per group head (CN/core.py:33-42), the
 //     lift being the identity (vd == D).
 // The projected tables are small (C x d per head); they are recomputed per
-// call, as the reference's read does.
+// call, as the reference's read does.  With a segmented codec the tables of
+// every segment are projected into one table (segment s at rows center_base
+// ..) in one launch, and the low launch reads row center_base + id.
+// Camera (CN/mg35.py:253-257, 310-346): the history rows of both partitions
+// are multiplied by P^-1 in-kernel (the reader keys on their own 8-dim
+// blocks, camera_selected CN/core.py:110-137), q_low by P^T of the query
+// rows; the value lift is folded into the value reader, so the values and
+// the output stay in the native layout and the caller applies P to out.
 #include "nkv_common.h"
 #include "nkv_internal.h"
 
@@ -28,15 +35,39 @@
 
 namespace nkv {
 
+// Source row (b, m, head) of a projection: x[b*x_b + m*x_m + head*x_h], or,
+// with a segment table, row m of the concatenation of the segments' center
+// tables (segment s holds rows center_base .. center_base + num_centers).
+template <bool X_F32>
+__device__ __forceinline__ const void* proj_row(const void* x, int64_t x_b, int64_t x_m, int64_t x_h,
+                                                const nkv_segment* seg, int n_seg, int b, int64_t m,
+                                                int head) {
+    if (seg) {
+        int lo = 0, hi = n_seg - 1;
+        while (lo < hi) {
+            const int mid = (lo + hi + 1) >> 1;
+            if (seg[mid].center_base <= m) lo = mid;
+            else hi = mid - 1;
+        }
+        const nkv_segment& sg = seg[lo];
+        const int64_t local = min(max(m - sg.center_base, (int64_t)0), (int64_t)sg.num_centers - 1);
+        return sg.centers + (int64_t)b * sg.centers_batch_stride + local * x_m + (int64_t)head * x_h;
+    }
+    const int64_t off = (int64_t)b * x_b + m * x_m + (int64_t)head * x_h;
+    return X_F32 ? (const void*)(reinterpret_cast<const float*>(x) + off)
+                 : (const void*)(reinterpret_cast<const uint16_t*>(x) + off);
+}
+
 // out[b][i][m][e] = bf16(sum_d x(b, m, heads[i], d) * w[i][d][e]) with
 // x(b, m, h, d) = x[b*x_b + m*x_m + h*x_h + d] (bf16 bits, or fp32 rounded to
 // bf16 first when X_F32), w == null meaning the identity (E == D).  The
 // output element is stored at out[b*o_b + i*o_i + m*o_m + e]; OUT_F32 stores
 // the bf16-rounded value as fp32.  One thread per output element, fp32
-// accumulation.
+// accumulation.  seg: rows come from the segments' center tables (proj_row).
 template <bool X_F32, bool OUT_F32>
 __global__ void __launch_bounds__(256) project_kernel(const void* x, int64_t x_b, int64_t x_m,
-                                                      int64_t x_h, const int32_t* heads, int H,
+                                                      int64_t x_h, const nkv_segment* seg,
+                                                      int n_seg, const int32_t* heads, int H,
                                                       const uint16_t* w, int D, int E, int nb,
                                                       int nh, int64_t M, void* out, int64_t o_b,
                                                       int64_t o_i, int64_t o_m) {
@@ -50,17 +81,17 @@ __global__ void __launch_bounds__(256) project_kernel(const void* x, int64_t x_b
     const int i = (int)(r % nh);
     const int b = (int)(r / nh);
     // head indices outside the layer are clamped (no out-of-bounds reads)
-    const int64_t base = (int64_t)b * x_b + m * x_m + (int64_t)min(max(heads[i], 0), H - 1) * x_h;
+    const void* xr = proj_row<X_F32>(x, x_b, x_m, x_h, seg, n_seg, b, m, min(max(heads[i], 0), H - 1));
     float acc;
     if (w == nullptr) {
-        acc = X_F32 ? bf16_round(reinterpret_cast<const float*>(x)[base + e])
-                    : bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[base + e]);
+        acc = X_F32 ? bf16_round(reinterpret_cast<const float*>(xr)[e])
+                    : bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(xr)[e]);
     } else {
         acc = 0.0f;
         const uint16_t* wi = w + (int64_t)i * D * E + e;
         for (int d = 0; d < D; ++d) {
-            const float xv = X_F32 ? bf16_round(reinterpret_cast<const float*>(x)[base + d])
-                                   : bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(x)[base + d]);
+            const float xv = X_F32 ? bf16_round(reinterpret_cast<const float*>(xr)[d])
+                                   : bf16_bits_to_f32(reinterpret_cast<const uint16_t*>(xr)[d]);
             acc = fmaf(xv, bf16_bits_to_f32(wi[(int64_t)d * E]), acc);
         }
     }
@@ -79,7 +110,8 @@ constexpr int PJ_ROWS = 128, PJ_MAXE = 128, PJ_MAXD = 128, PJ_PAD = 8;
 
 template <bool X_F32, bool OUT_F32>
 __global__ void __launch_bounds__(256) project_mfma_kernel(const void* x, int64_t x_b, int64_t x_m,
-                                                           int64_t x_h, const int32_t* heads, int H,
+                                                           int64_t x_h, const nkv_segment* seg,
+                                                           int n_seg, const int32_t* heads, int H,
                                                            const uint16_t* w, int D, int E,
                                                            int64_t M, void* out, int64_t o_b,
                                                            int64_t o_i, int64_t o_m) {
@@ -92,7 +124,8 @@ __global__ void __launch_bounds__(256) project_mfma_kernel(const void* x, int64_
     __syncthreads();
     const int64_t m = (int64_t)blockIdx.x * PJ_ROWS + 32 * wave + l32;
     const int64_t ml = m < M ? m : M - 1;  // rows past the end read the last row (not stored)
-    const int64_t base = (int64_t)b * x_b + ml * x_m + (int64_t)min(max(heads[i], 0), H - 1) * x_h;
+    const void* xr =
+        proj_row<X_F32>(x, x_b, x_m, x_h, seg, n_seg, b, ml, min(max(heads[i], 0), H - 1));
     const int ntile = E / 32;
     f32x16 acc[PJ_MAXE / 32];
 #pragma unroll
@@ -100,14 +133,13 @@ __global__ void __launch_bounds__(256) project_mfma_kernel(const void* x, int64_
     for (int k0 = 0; k0 < D; k0 += 16) {
         u32x4 a;
         if (X_F32) {
-            const float* xp = reinterpret_cast<const float*>(x) + base + k0 + 8 * hf;
+            const float* xp = reinterpret_cast<const float*>(xr) + k0 + 8 * hf;
             const f32x4 x0 = *reinterpret_cast<const f32x4*>(xp);
             const f32x4 x1 = *reinterpret_cast<const f32x4*>(xp + 4);
             a = u32x4{pack_bf16x2(x0[0], x0[1]), pack_bf16x2(x0[2], x0[3]),
                       pack_bf16x2(x1[0], x1[1]), pack_bf16x2(x1[2], x1[3])};
         } else {
-            a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(x) + base + k0 +
-                                                8 * hf);
+            a = *reinterpret_cast<const u32x4*>(reinterpret_cast<const uint16_t*>(xr) + k0 + 8 * hf);
         }
 #pragma unroll
         for (int tt = 0; tt < PJ_MAXE / 32; ++tt)
@@ -187,6 +219,32 @@ __global__ void __launch_bounds__(256) rope_low_kernel(uint16_t* q_low, int B, i
     *w = rope_pair(*w, cs[0], cs[1]);
 }
 
+// Camera P^T of the reader queries in place (camera_selected, CN/core.py:
+// 110-137): q_low [B, Q, nh, d] bf16; block j of head i uses sub-frame
+// cams[i * d/8 + j] (null: j % 4) of query t's matrices (query t at row t).
+// One thread per (b, t, i, block, vector); a block's 4-vectors are its dims
+// {0, 2, 4, 6} and {1, 3, 5, 7}.
+__global__ void __launch_bounds__(256) camera_low_kernel(uint16_t* q_low, int B, int64_t Q, int nh,
+                                                         int d, CameraDev cam, const int32_t* cams) {
+    const int nbk = d / 8;
+    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (tid >= (int64_t)B * Q * nh * nbk * 2) return;
+    const int r = (int)(tid & 1);
+    const int j = (int)((tid >> 1) % nbk);
+    const int64_t row = (tid >> 1) / nbk;  // (b, t, i)
+    const int i = (int)(row % nh);
+    const int64_t t = (row / nh) % Q;
+    const int b = (int)(row / ((int64_t)nh * Q));
+    const int sub = cams ? (cams[(int64_t)i * nbk + j] & 3) : (j & 3);
+    uint16_t* v = q_low + row * d + 8 * j + r;
+    float x[4], y[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) x[e] = bf16_bits_to_f32(v[2 * e]);
+    camera_vec4(camera_mats(cam, b, t) + 16 * sub, x, y);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[2 * e] = f32_to_bf16_bits(y[e]);
+}
+
 namespace {
 
 constexpr size_t WS_ALIGN = 256;
@@ -201,32 +259,86 @@ struct FastLayout {
     size_t total;
 };
 
+// Batch items that have their own center table (0: one shared table).
+int table_batches(const nkv_codec& c, int B) {
+    if (c.n_segments > 0) return c.segments[0].centers_batch_stride ? B : 1;
+    return c.centers_batch_stride ? B : 1;
+}
+
+bool has_centers(const nkv_codec& c) {
+    return c.n_segments > 0 ? c.segments[0].centers != nullptr : c.centers != nullptr;
+}
+
+// Rows of the (concatenated) center table of a codec.
+int64_t table_rows(const nkv_codec& c) {
+    if (c.n_segments == 0) return c.num_centers;
+    const nkv_segment& last = c.segments[c.n_segments - 1];
+    return last.center_base + last.num_centers;
+}
+
+// The queries the reader groups project: the pre-RoPE / pre-camera queries
+// when given, else attend.q.
+bool reader_q_pre(const nkv_fast_args* f) { return f->q_pre != nullptr; }
+
 int validate(const nkv_fast_args* f) {
     NKV_REQUIRE(f, NKV_ERR_INVALID, "null args");
     const nkv_attend_args& a = f->attend;
     NKV_REQUIRE(a.B >= 1 && a.H >= 1 && a.D == 128, NKV_ERR_UNSUPPORTED,
                 "fast attend supports D == 128");
     NKV_REQUIRE(a.Q >= 0 && a.N >= 0 && a.Nc >= 0, NKV_ERR_INVALID, "negative length");
-    NKV_REQUIRE(!a.camera, NKV_ERR_UNSUPPORTED,
-                "fast attend does not apply the camera transform (reader partitions)");
+    NKV_REQUIRE(!a.hist_rows, NKV_ERR_INVALID,
+                "fast attend selects history rows with protect_rows / low_rows");
+    const bool readers = f->n_low > 0 && f->num_groups > 0;
+    if (a.N > 0) {
+        int rc = check_segments(a.key, a.N);
+        if (rc) return rc;
+        rc = check_segments(a.value, a.N);
+        if (rc) return rc;
+        if (readers)
+            for (const nkv_codec* c : {&a.key, &a.value})
+                if (c->n_segments > 0 && has_centers(*c))
+                    for (int i = 1; i < c->n_segments; ++i)
+                        NKV_REQUIRE((c->segments[i].centers_batch_stride != 0) ==
+                                        (c->segments[0].centers_batch_stride != 0),
+                                    NKV_ERR_UNSUPPORTED,
+                                    "reader groups need segments that all share or all have "
+                                    "per-batch center tables");
+    }
+    if (readers && a.rope)
+        NKV_REQUIRE(f->q_pre && f->q_rope, NKV_ERR_INVALID,
+                    "RoPE of the reader groups needs q_pre and q_rope");
+    if (readers && a.camera)
+        NKV_REQUIRE(f->q_pre && f->q_camera, NKV_ERR_INVALID,
+                    "the camera of the reader groups needs q_pre and q_camera");
+    if (f->q_pre)
+        NKV_REQUIRE(reinterpret_cast<uintptr_t>(f->q_pre) % 16 == 0 && f->qp_sb % 8 == 0 &&
+                        f->qp_st % 8 == 0 && f->qp_sh % 8 == 0,
+                    NKV_ERR_INVALID, "q_pre must be 16-byte aligned with strides divisible by 8");
     if (a.rope) {
         RopeDev chk;
         int rc = rope_from_abi(a.rope, a.D, &chk);
         if (rc) return rc;
-        NKV_REQUIRE(a.N <= a.rope->n_frames * (int64_t)a.rope->grid_h * a.rope->grid_w,
+        NKV_REQUIRE(a.N <= rope_rows_covered(a.rope),
                     NKV_ERR_INVALID, "more history tokens than the RoPE frames cover");
-        if (f->n_low > 0 && f->num_groups > 0) {
-            NKV_REQUIRE(f->q_pre && f->q_rope, NKV_ERR_INVALID,
-                        "RoPE of the reader groups needs q_pre and q_rope");
-            NKV_REQUIRE(reinterpret_cast<uintptr_t>(f->q_pre) % 16 == 0 && f->qp_sb % 8 == 0 &&
-                            f->qp_st % 8 == 0 && f->qp_sh % 8 == 0,
-                        NKV_ERR_INVALID,
-                        "q_pre must be 16-byte aligned with strides divisible by 8");
+        if (readers) {
+            NKV_REQUIRE(f->q_rope, NKV_ERR_INVALID, "RoPE of the reader groups needs q_rope");
             rc = rope_from_abi(f->q_rope, a.D, &chk);
             if (rc) return rc;
-            NKV_REQUIRE(a.Q <= f->q_rope->n_frames * (int64_t)f->q_rope->grid_h *
-                                   f->q_rope->grid_w,
+            NKV_REQUIRE(a.Q <= rope_rows_covered(f->q_rope),
                         NKV_ERR_INVALID, "more queries than the query RoPE frames cover");
+        }
+    }
+    if (a.camera) {
+        CameraDev chk;
+        int rc = camera_from_abi(a.camera, a.D, a.B, &chk);
+        if (rc) return rc;
+        NKV_REQUIRE(a.camera->layout == NKV_CAMERA_FULL, NKV_ERR_UNSUPPORTED,
+                    "fast attend's camera supports the FULL layout (CN/mg35.py:131-132)");
+        if (readers) {
+            NKV_REQUIRE(f->q_camera, NKV_ERR_INVALID,
+                        "the camera of the reader groups needs q_camera (P^T of the queries)");
+            rc = camera_from_abi(f->q_camera, a.D, a.B, &chk);
+            if (rc) return rc;
         }
     }
     NKV_REQUIRE(f->n_protect >= 0 && f->n_low >= 0 && f->n_protect <= a.N && f->n_low <= a.N,
@@ -241,8 +353,13 @@ int validate(const nkv_fast_args* f) {
                         a.o_st % 8 == 0 && a.o_sh % 8 == 0,
                     NKV_ERR_INVALID, "out must be 16-byte aligned with strides divisible by 8");
     if (a.Nc > 0) NKV_REQUIRE(a.k_cur && a.v_cur, NKV_ERR_INVALID, "current K/V missing");
+    NKV_REQUIRE(!a.cur_mask || (a.n_groups >= 1 && a.cur_mask_words >= cdiv(a.Nc, 32)),
+                NKV_ERR_INVALID, "the current-key mask needs n_groups >= 1 and "
+                "cur_mask_words >= ceil(Nc / 32)");
     if (f->n_low > 0 || f->n_protect > 0)
-        NKV_REQUIRE(a.key.packed && a.value.packed, NKV_ERR_INVALID, "history codecs missing");
+        NKV_REQUIRE((a.key.packed || a.key.n_segments > 0) &&
+                        (a.value.packed || a.value.n_segments > 0),
+                    NKV_ERR_INVALID, "history codecs missing");
     for (int g = 0; g < f->num_groups; ++g) {
         const nkv_reader_group& G = f->groups[g];
         NKV_REQUIRE(G.num_heads >= 1 && G.num_heads <= a.H && G.heads, NKV_ERR_INVALID,
@@ -254,6 +371,8 @@ int validate(const nkv_fast_args* f) {
         NKV_REQUIRE(G.k_read && G.v_read, NKV_ERR_INVALID, "reader group needs k_read and v_read");
         NKV_REQUIRE(!a.rope || G.rope_pairs || G.d == a.D, NKV_ERR_INVALID,
                     "RoPE of a reader group narrower than D needs rope_pairs");
+        NKV_REQUIRE(!a.camera || G.cam_blocks || G.d == a.D, NKV_ERR_INVALID,
+                    "the camera of a reader group narrower than D needs cam_blocks");
     }
     return NKV_OK;
 }
@@ -292,11 +411,12 @@ ChunkLaunchDesc native_desc(const nkv_fast_args* f, float* lse_n) {
     d.lse = lse_n;
     d.ev_begin = a.ev_kernel_begin;
     d.ev_end = a.ev_kernel_end;
+    d.cur_mask = a.cur_mask;
+    d.q_group = a.q_group;
+    d.n_groups = a.n_groups;
+    d.mask_words = a.cur_mask_words;
     return d;
 }
-
-// Batch items that have their own center table (0: one shared table).
-int table_batches(const nkv_codec& c, int B) { return c.centers_batch_stride ? B : 1; }
 
 // Low-partition launch of group g over the workspace tables.
 ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const FastLayout& L) {
@@ -320,23 +440,31 @@ ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const
     for (int cc = 0; cc < 2; ++cc) {
         const nkv_codec& c = cc ? a.value : a.key;
         ChunkCodec v{};
-        v.packed = c.packed;
-        v.scales = c.scales;
-        v.ids = c.centers ? c.ids : nullptr;
         v.r = c.r;
         v.group = c.group;
         v.scale_dtype = c.scale_dtype;
-        v.id_bytes = c.id_bytes;
-        v.num_centers = c.num_centers;
+        if (c.n_segments > 0) {
+            v.seg = c.segments_dev;
+            v.n_seg = c.n_segments;
+            v.seg_flat = 1;
+        } else {
+            v.packed = c.packed;
+            v.scales = c.scales;
+            v.ids = c.centers ? c.ids : nullptr;
+            v.id_bytes = c.id_bytes;
+            v.num_centers = c.num_centers;
+        }
         const int width = cc ? D : dd;
         v.w = cc ? G.v_read : G.k_read;
         v.w_hs = (int64_t)width * c.r;
-        if (c.centers) {
+        if (has_centers(c)) {
             // projected table [tables][nh][C][width]
+            const int64_t C = table_rows(c);
+            v.has_centers = 1;
             v.centers = reinterpret_cast<const uint16_t*>(ws + (cc ? L.vc[g] : L.kc[g]));
             v.c_rs = width;
-            v.c_hs = (int64_t)c.num_centers * width;
-            v.c_bs = c.centers_batch_stride ? (int64_t)nh * c.num_centers * width : 0;
+            v.c_hs = C * width;
+            v.c_bs = table_batches(c, a.B) > 1 ? (int64_t)nh * C * width : 0;
         }
         if (c.mean) {
             v.bias = reinterpret_cast<const float*>(ws + (cc ? L.vb[g] : L.kb[g]));
@@ -367,10 +495,10 @@ FastLayout layout(const nkv_fast_args* f) {
         const nkv_reader_group& G = f->groups[g];
         const size_t nh = G.num_heads, dd = G.d, D = a.D;
         L.q_low.push_back(take((size_t)a.B * a.Q * nh * dd * 2));
-        const size_t kt = a.key.centers ? (size_t)table_batches(a.key, a.B) : 0;
-        const size_t vt = a.value.centers ? (size_t)table_batches(a.value, a.B) : 0;
-        L.kc.push_back(take(kt * nh * a.key.num_centers * dd * 2));
-        L.vc.push_back(take(vt * nh * a.value.num_centers * D * 2));
+        const size_t kt = has_centers(a.key) ? (size_t)table_batches(a.key, a.B) : 0;
+        const size_t vt = has_centers(a.value) ? (size_t)table_batches(a.value, a.B) : 0;
+        L.kc.push_back(take(kt * nh * (size_t)table_rows(a.key) * dd * 2));
+        L.vc.push_back(take(vt * nh * (size_t)table_rows(a.value) * D * 2));
         L.kb.push_back(take(nh * dd * sizeof(float)));
         L.vb.push_back(take(nh * D * sizeof(float)));
         L.out_l.push_back(take((size_t)a.B * a.Q * nh * D * 2));
@@ -391,21 +519,24 @@ FastLayout layout(const nkv_fast_args* f) {
 
 template <bool XF, bool OF>
 int project(hipStream_t s, const void* x, int64_t x_b, int64_t x_m, int64_t x_h,
-            const int32_t* heads, int H, const uint16_t* w, int D, int E, int nb, int nh,
-            int64_t M, void* out, int64_t o_b, int64_t o_i, int64_t o_m) {
+            const nkv_segment* seg, int n_seg, const int32_t* heads, int H, const uint16_t* w,
+            int D, int E, int nb, int nh, int64_t M, void* out, int64_t o_b, int64_t o_i,
+            int64_t o_m) {
     const int64_t total = (int64_t)nb * nh * M * E;
     if (total == 0) return NKV_OK;
-    // 16-byte operand loads need aligned rows (8 bf16 or 4 fp32 elements)
+    // 16-byte operand loads need aligned rows (8 bf16 or 4 fp32 elements);
+    // segment tables are [*, C, HD] bf16 tensors (HD a multiple of 8)
     const int64_t el = XF ? 4 : 8;
-    const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && x_b % el == 0 &&
-                         x_m % el == 0 && x_h % el == 0;
+    const bool aligned = seg ? x_m % el == 0 && x_h % el == 0
+                             : reinterpret_cast<uintptr_t>(x) % 16 == 0 && x_b % el == 0 &&
+                                   x_m % el == 0 && x_h % el == 0;
     if (w && aligned && D <= PJ_MAXD && D % 16 == 0 && E % 32 == 0 && E <= PJ_MAXE) {
         project_mfma_kernel<XF, OF><<<dim3((unsigned)cdiv(M, PJ_ROWS), (unsigned)nh, (unsigned)nb),
-                                      256, 0, s>>>(x, x_b, x_m, x_h, heads, H, w, D, E, M, out, o_b,
-                                                   o_i, o_m);
+                                      256, 0, s>>>(x, x_b, x_m, x_h, seg, n_seg, heads, H, w, D, E,
+                                                   M, out, o_b, o_i, o_m);
     } else {
         project_kernel<XF, OF><<<dim3((unsigned)cdiv(total, 256)), 256, 0, s>>>(
-            x, x_b, x_m, x_h, heads, H, w, D, E, nb, nh, M, out, o_b, o_i, o_m);
+            x, x_b, x_m, x_h, seg, n_seg, heads, H, w, D, E, nb, nh, M, out, o_b, o_i, o_m);
     }
     NKV_LAUNCH_CHECK();
     return NKV_OK;
@@ -445,10 +576,16 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
         rope_from_abi(a.rope, a.D, &krope);
         if (f->q_rope) rope_from_abi(f->q_rope, a.D, &qrope);
     }
+    CameraDev kcam{}, qcam{};
+    if (a.camera) {
+        camera_from_abi(a.camera, a.D, a.B, &kcam);
+        if (f->q_camera) camera_from_abi(f->q_camera, a.D, a.B, &qcam);
+    }
 
     // 1. native partition -> out, lse_n
     ChunkLaunchDesc nd = native_desc(f, lse_n);
     nd.rope = krope;
+    nd.cam = kcam;
     rc = chunk_launch(s, nd, ws + L.partials, part_bytes);
     if (rc) return rc;
     // no low rows: the native partition is the whole attention
@@ -459,16 +596,16 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
     for (int g = 0; g < f->num_groups; ++g) {
         const nkv_reader_group& G = f->groups[g];
         const int nh = G.num_heads, dd = G.d;
-        // q_low [B, Q, nh, d]: from the pre-RoPE queries when RoPE is applied
-        // (then rotated on its retained pairs), else from q
+        // q_low [B, Q, nh, d] from the pre-RoPE, pre-camera queries when
+        // given (then rotated / transformed on its retained pairs and blocks)
         uint16_t* q_low = reinterpret_cast<uint16_t*>(ws + L.q_low[g]);
-        if (a.rope)
-            rc = project<false, false>(s, f->q_pre, f->qp_sb, f->qp_st, f->qp_sh, G.heads, a.H,
-                                       G.q_reduce, D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
-                                       (int64_t)nh * dd);
+        if (reader_q_pre(f))
+            rc = project<false, false>(s, f->q_pre, f->qp_sb, f->qp_st, f->qp_sh, nullptr, 0,
+                                       G.heads, a.H, G.q_reduce, D, dd, a.B, nh, a.Q, q_low,
+                                       a.Q * nh * dd, dd, (int64_t)nh * dd);
         else
-            rc = project<false, false>(s, a.q, a.q_sb, a.q_st, a.q_sh, G.heads, a.H, G.q_reduce,
-                                       D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
+            rc = project<false, false>(s, a.q, a.q_sb, a.q_st, a.q_sh, nullptr, 0, G.heads, a.H,
+                                       G.q_reduce, D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
                                        (int64_t)nh * dd);
         if (rc) return rc;
         if (a.rope) {
@@ -479,24 +616,32 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
                                                                               dd, qp);
             NKV_LAUNCH_CHECK();
         }
+        if (a.camera) {
+            const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 8) * 2;
+            camera_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(
+                q_low, a.B, a.Q, nh, dd, qcam, G.cam_blocks);
+            NKV_LAUNCH_CHECK();
+        }
         for (int cc = 0; cc < 2 && f->n_low > 0; ++cc) {
             const nkv_codec& c = cc ? a.value : a.key;
             const int width = cc ? D : dd;
             const uint16_t* aff = cc ? G.v_affine : G.k_affine;
-            if (c.centers) {
+            if (has_centers(c)) {
                 // [tables][nh][C][width] = center columns of each head . affine
                 const int nb = table_batches(c, a.B);
-                rc = project<false, false>(s, c.centers, c.centers_batch_stride, HD, D, G.heads, a.H, aff,
-                                           D, width, nb, nh, c.num_centers,
-                                           ws + (cc ? L.vc[g] : L.kc[g]),
-                                           (int64_t)nh * c.num_centers * width,
-                                           (int64_t)c.num_centers * width, width);
+                const int64_t C = table_rows(c);
+                rc = project<false, false>(
+                    s, c.centers, c.centers_batch_stride, HD, D,
+                    c.n_segments > 0 ? c.segments_dev : nullptr, c.n_segments, G.heads, a.H, aff,
+                    D, width, nb, nh, C, ws + (cc ? L.vc[g] : L.kc[g]), (int64_t)nh * C * width,
+                    C * width, width);
                 if (rc) return rc;
             }
             if (c.mean) {
                 // [nh][width] = bf16(mean of each head) . affine
-                rc = project<true, true>(s, c.mean, 0, 0, D, G.heads, a.H, aff, D, width, 1, nh, 1,
-                                         ws + (cc ? L.vb[g] : L.kb[g]), 0, width, 0);
+                rc = project<true, true>(s, c.mean, 0, 0, D, nullptr, 0, G.heads, a.H, aff, D,
+                                         width, 1, nh, 1, ws + (cc ? L.vb[g] : L.kb[g]), 0, width,
+                                         0);
                 if (rc) return rc;
             }
         }
@@ -504,6 +649,10 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
         if (a.rope) {
             ld.rope = krope;
             ld.rope.pairs = G.rope_pairs;
+        }
+        if (a.camera) {
+            ld.cam = kcam;
+            ld.cam.blocks = G.cam_blocks;
         }
         rc = chunk_launch(s, ld, ws + L.partials, part_bytes);
         if (rc) return rc;

@@ -15,14 +15,73 @@ struct ChunkCodec {
     const uint8_t* packed;    // [B, N, r/2]
     const uint16_t* scales;   // [B, N, r/group]
     const void* ids;          // [B, N] of id_bytes, or null
-    int r, group, scale_dtype, id_bytes, num_centers, _pad;
+    int r, group, scale_dtype, id_bytes, num_centers;
+    int has_centers;          // 1: add each row's center (flat table or the segments' tables)
     const uint16_t* w;        // bf16 row d of head i: w + i*w_hs + d*r
     int64_t w_hs;
-    const uint16_t* centers;  // bf16 value (b, id, i, d): centers[b*c_bs + id*c_rs + i*c_hs + d];
-    int64_t c_bs, c_rs, c_hs;  // null = no center add
+    const uint16_t* centers;  // bf16 value (b, id, i, d): centers[b*c_bs + id*c_rs + i*c_hs + d]
+    int64_t c_bs, c_rs, c_hs;
     const float* bias;        // (i, d): bias[i*bias_hs + d], applied as bf16; null = none
     int64_t bias_hs;
+    // Segment table in device memory (null: the flat arrays above).  Row n of
+    // batch item b lives in segment s = seg_find(n) at local row n - row_start.
+    // seg_flat == 0: its center is (b, id) of the segment's own table
+    // (segment centers + b*centers_batch_stride + id*c_rs + i*c_hs + d);
+    // seg_flat == 1: row center_base + id of the one table `centers` above.
+    const nkv_segment* seg;
+    int n_seg;
+    int seg_flat;
 };
+
+// Segment holding codec row `row` of a table in row order, contiguous from
+// row 0 (binary search; rows outside the table give its first or last).
+__device__ __forceinline__ int seg_find(const nkv_segment* seg, int n, int64_t row) {
+    int lo = 0, hi = n - 1;
+    while (lo < hi) {
+        const int mid = (lo + hi + 1) >> 1;
+        if (seg[mid].row_start <= row) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+// Packed-code and scale rows of codec row `row` of batch item b (N rows per
+// batch item in the flat layout).
+__device__ __forceinline__ void codec_row_ptrs(const ChunkCodec& c, int b, int64_t N, int64_t row,
+                                               const uint8_t*& prow, const uint16_t*& srow) {
+    const int NG = c.r / c.group;
+    if (c.seg) {
+        const nkv_segment& s = c.seg[seg_find(c.seg, c.n_seg, row)];
+        const int64_t local = min(max(row - s.row_start, (int64_t)0), s.rows - 1);
+        const int64_t tok = (int64_t)b * s.rows + local;
+        prow = s.packed + tok * (c.r / 2);
+        srow = s.scales + tok * NG;
+    } else {
+        const int64_t tok = (int64_t)b * N + row;
+        prow = c.packed + tok * (c.r / 2);
+        srow = c.scales + tok * NG;
+    }
+}
+
+// Center row (bf16, the launch head's columns) of codec row `row` of batch
+// item b; ids outside a table are clamped so that a corrupt payload cannot
+// read out of bounds.  Only for codecs with has_centers.
+__device__ __forceinline__ const uint16_t* center_row(const ChunkCodec& c, int b, int h, int64_t N,
+                                                      int64_t row) {
+    if (c.seg) {
+        const nkv_segment& s = c.seg[seg_find(c.seg, c.n_seg, row)];
+        const int64_t local = min(max(row - s.row_start, (int64_t)0), s.rows - 1);
+        int id = read_id(s.ids, s.id_bytes, (int64_t)b * s.rows + local);
+        id = min(max(id, 0), s.num_centers - 1);
+        if (c.seg_flat)
+            return c.centers + (int64_t)b * c.c_bs + (s.center_base + id) * c.c_rs + (int64_t)h * c.c_hs;
+        return s.centers + (int64_t)b * s.centers_batch_stride + (int64_t)id * c.c_rs +
+               (int64_t)h * c.c_hs;
+    }
+    int id = read_id(c.ids, c.id_bytes, (int64_t)b * N + row);
+    id = min(max(id, 0), c.num_centers - 1);
+    return c.centers + (int64_t)b * c.c_bs + (int64_t)id * c.c_rs + (int64_t)h * c.c_hs;
+}
 
 // One key-chunk attention launch: every launch head i attends queries
 // q[b, :, i, :dk] to the history keys rows[0 .. n_rows) (decoded with the
@@ -48,11 +107,20 @@ struct ChunkLaunchDesc {
     void* ev_end;
     RopeDev rope;    // RoPE of the history keys at their codec rows (cs_t null: none)
     CameraDev cam;   // camera P^-1 of the history keys and values (mats null: none)
+    // visibility of the current keys: bit k % 32 of cur_mask[g * mask_words +
+    // k / 32] for the queries of group g = q_group[t] (null: all visible)
+    const uint32_t* cur_mask;
+    const int32_t* q_group;
+    int n_groups, mask_words;
 };
 
 // The decoder view of an nkv_codec for head dim D: head h reads decoder rows
 // h*D .., center columns h*D .. and mean h*D ...
 ChunkCodec chunk_codec_from(const nkv_codec& c, int D, int HD);
+
+// Host check of a codec's segment table against its N rows (NKV_OK when the
+// codec has no segments).
+int check_segments(const nkv_codec& c, int64_t N);
 
 // Key-chunk schedule (nkv_chunk.hip).
 int chunk_check(const nkv_attend_args* a);

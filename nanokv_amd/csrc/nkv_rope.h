@@ -24,7 +24,15 @@ struct RopeDev {
     // [launch heads, width / 2] original pair of each pair of a narrower key
     // (rope_selected, CN/core.py:75-91), or null: pair j is pair j
     const int32_t* pairs = nullptr;
+    // per-row table [n_rows, pt, 2] (pt = D / 2, ph = pw = 0), or null: bands
+    const double* cs_rows = nullptr;
+    int64_t n_rows = 0;
 };
+
+// Whether a RopeDev rotates anything.
+__host__ __device__ __forceinline__ bool rope_on(const RopeDev& r) {
+    return r.cs_t || r.cs_h || r.cs_w || r.cs_rows;
+}
 
 // The three band rows of one codec row (codec rows and the frame geometry
 // are 32-bit, checked on the host); indices are clamped into the tables, so
@@ -36,10 +44,16 @@ struct RopeRows {
 };
 
 __device__ __forceinline__ RopeRows rope_rows(const RopeDev& r, int64_t row64) {
+    RopeRows rr;
+    if (r.cs_rows) {
+        // the whole row is the "temporal" band: pair p reads entry p
+        rr.t = r.cs_rows + 2 * min(max(row64, (int64_t)0), r.n_rows - 1) * r.pt;
+        rr.h = rr.w = rr.t;
+        return rr;
+    }
     const int tpf = r.grid_h * r.grid_w;
     const int row = (int)row64;
     const int f = row / tpf, rem = row - f * tpf, hr = rem / r.grid_w;
-    RopeRows rr;
     rr.t = r.cs_t;
     if (r.pt) {
         const int tp = min(max(r.frame_pos[min(f, (int)r.n_frames - 1)], 0), r.n_t - 1);
@@ -70,5 +84,10 @@ __device__ __forceinline__ uint32_t rope_pair(uint32_t w, double c, double s) {
 // Host: validate an nkv_rope for heads of D dims (D / 2 pairs) and fill dev
 // (pairs stays null).  Returns NKV_OK or an error code with the message set.
 int rope_from_abi(const nkv_rope* r, int D, RopeDev* dev);
+
+// Host: rows an nkv_rope gives positions to (its per-row table, or its frames).
+inline int64_t rope_rows_covered(const nkv_rope* r) {
+    return r->cs_rows ? r->n_rows : r->n_frames * (int64_t)r->grid_h * r->grid_w;
+}
 
 }  // namespace nkv

@@ -14,6 +14,14 @@ namespace nkv {
 int rope_from_abi(const nkv_rope* r, int D, RopeDev* dev) {
     NKV_REQUIRE(r, NKV_ERR_INVALID, "rope is null");
     NKV_REQUIRE(D > 0 && D % 2 == 0, NKV_ERR_INVALID, "RoPE needs an even head dimension");
+    if (r->cs_rows) {
+        NKV_REQUIRE(r->n_rows >= 1, NKV_ERR_INVALID, "a per-row RoPE table needs n_rows >= 1");
+        *dev = RopeDev{};
+        dev->cs_rows = r->cs_rows;
+        dev->n_rows = r->n_rows;
+        dev->pt = D / 2;
+        return NKV_OK;
+    }
     NKV_REQUIRE(r->pt >= 0 && r->ph >= 0 && r->pw >= 0 && r->pt + r->ph + r->pw == D / 2,
                 NKV_ERR_INVALID, "RoPE bands must hold D / 2 pairs (pt + ph + pw)");
     NKV_REQUIRE(r->grid_h >= 1 && r->grid_w >= 1 && r->n_frames >= 1, NKV_ERR_INVALID,
@@ -101,8 +109,7 @@ extern "C" int nkv_rope_apply(void* stream, const nkv_rope* rope, int B, int64_t
     NKV_REQUIRE(B >= 0 && S >= 0 && H >= 0, NKV_ERR_INVALID, "negative shape");
     if ((int64_t)B * S * H == 0) return NKV_OK;
     NKV_REQUIRE(x && out, NKV_ERR_INVALID, "x and out are required");
-    const int64_t tpf = (int64_t)rope->grid_h * rope->grid_w;
-    NKV_REQUIRE(rows || S <= rope->n_frames * tpf, NKV_ERR_INVALID,
+    NKV_REQUIRE(rows || S <= rope_rows_covered(rope), NKV_ERR_INVALID,
                 "more rows than the RoPE frames cover");
     NKV_REQUIRE(S < INT32_MAX, NKV_ERR_INVALID, "RoPE rows must fit in 32 bits");
     const bool vec = D % 8 == 0 && (reinterpret_cast<uintptr_t>(x) | reinterpret_cast<uintptr_t>(out)) % 16 == 0 &&

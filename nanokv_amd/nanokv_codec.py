@@ -22,6 +22,7 @@ with preload_operator_weights().  All compute goes through libnanokv_hip.so
 from __future__ import annotations
 
 import os
+from collections import OrderedDict
 from typing import Any, Optional
 
 import torch
@@ -482,39 +483,42 @@ def direct_latent_pair_segments(key: Any, value: Any, *, device: torch.device,
     return result
 
 
+_HISTORY_TABLES: "OrderedDict[tuple, tuple]" = OrderedDict()
+_HISTORY_TABLES_MAX = 256
+
+
 def history_codecs(key: Any, value: Any, device: torch.device):
-    """One (K, V) ops.Codec pair covering every segment of a paired cache: the
-    packed codes, scales and ids are concatenated along tokens and the
-    per-segment center tables are concatenated with each segment's ids offset
-    into the combined table (int16/int32 ids when it exceeds 256 rows)."""
+    """One (K, V) ops.Codec pair covering every segment of a paired cache.
+
+    A single segment is passed as its own flat arrays.  A segment list is
+    passed as an nkv_segment table over the segments' own tensors (each with
+    its own center table, as the reference decodes them, MG:393-455): no
+    codes, scales, ids or tables are copied.  The tables are remembered per
+    segment list (bounded LRU keyed by the payloads, which are immutable), so
+    the per-layer reads of one denoise step and the next reuse them."""
     pairs = _pairs(key, value)
+    dev = torch.device(device)
+    if len(pairs) == 1:
+        return codec_view(pairs[0][0], dev), codec_view(pairs[0][1], dev)
+    ident = (str(dev),) + tuple((id(k), id(v)) for k, v in pairs)
+    hit = _HISTORY_TABLES.get(ident)
+    if hit is not None:
+        _HISTORY_TABLES.move_to_end(ident)
+        return hit[1]
     out = []
     for which in (0, 1):
-        views = [codec_view(p[which], device) for p in pairs]
-        if len({(v.r, v.group, v.scales.dtype) for v in views}) != 1:
-            raise RuntimeError("history segments must share rank, scale group and scale dtype")
-        packed = torch.cat([v.packed for v in views], 1)
-        scales = torch.cat([v.scales for v in views], 1)
-        ids = centers = None
-        if all(v.centers is not None for v in views):
-            shared = all(v.centers is views[0].centers for v in views) or (
-                len(views) > 0 and all(v.centers.data_ptr() == views[0].centers.data_ptr()
-                                       for v in views))
-            if shared:
-                centers = views[0].centers
-                ids = torch.cat([v.ids for v in views], 1)
-            else:
-                tables, id_parts, base = [], [], 0
-                for v in views:
-                    tables.append(v.centers)
-                    id_parts.append(v.ids.to(torch.int32) + base)
-                    base += int(v.centers.shape[1])
-                centers = torch.cat(tables, 1).contiguous()
-                ids = torch.cat(id_parts, 1)
-                ids = ids.to(ops.id_dtype_for(base)).contiguous() if base <= 65536 else ids
-        elif any(v.centers is not None for v in views):
+        views = [codec_view(p[which], dev) for p in pairs]
+        if len({(v.r, v.group, v.scales.dtype, v.w_dec.data_ptr()) for v in views}) != 1:
+            raise RuntimeError("history segments must share rank, scale group, scale dtype "
+                               "and codec operator")
+        if len({v.centers is None for v in views}) != 1:
             raise RuntimeError("history segments mix semantic and pca payloads")
-        out.append(ops.Codec(packed=packed.contiguous(), scales=scales.contiguous(),
-                             w_dec=views[0].w_dec, group=views[0].group, ids=ids,
-                             centers=centers, mean=views[0].mean))
+        table = ops.SegmentTable([ops.Segment(v.packed, v.scales, v.ids, v.centers)
+                                  for v in views], dev)
+        out.append(ops.Codec(packed=None, scales=None, w_dec=views[0].w_dec,
+                             group=views[0].group, mean=views[0].mean, segments=table))
+    # the payloads are kept with the entry so that their ids stay unique
+    _HISTORY_TABLES[ident] = (pairs, (out[0], out[1]))
+    while len(_HISTORY_TABLES) > _HISTORY_TABLES_MAX:
+        _HISTORY_TABLES.popitem(last=False)
     return out[0], out[1]

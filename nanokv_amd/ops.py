@@ -19,7 +19,7 @@ from . import _lib
 from ._lib import (NKV_DTYPE_BF16, NKV_DTYPE_FP16, NKV_QUANT_BF16, NKV_QUANT_FP32,
                    NKV_SCHEDULE_AUTO, NKV_SCHEDULE_KEY_CHUNKS, NKV_SCHEDULE_QUERY_TILES,
                    NkvAttendArgs, NkvCodec, NkvDecodeArgs, NkvEncodeArgs, NkvFastArgs,
-                   NkvCamera, NkvReaderGroup, NkvRope, check, lib)
+                   NkvCamera, NkvReaderGroup, NkvRope, NkvSegment, check, lib)
 
 _SCALE_CODES = {torch.bfloat16: NKV_DTYPE_BF16, torch.float16: NKV_DTYPE_FP16}
 _QUANT_CODES = {"fp32": NKV_QUANT_FP32, "bf16": NKV_QUANT_BF16}
@@ -202,20 +202,83 @@ def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tens
 
 # ---------------------------------------------------------------- codec view
 @dataclass
-class Codec:
-    """Device tensors of one K or V history codec.
-
-    packed [B, N, r/2] uint8, scales [B, N, r/group] bf16/fp16, ids [B, N]
-    (uint8/int16/int32) or None, centers [B or 1, C, HD] bf16 or None,
-    w_dec [HD, r] bf16, mean [HD] fp32 or None.
-    """
+class Segment:
+    """Device tensors of one immutable segment of a codec cache (one payload of
+    a worldplay_segments_v1 list): packed [B, rows, r/2] uint8, scales
+    [B, rows, r/group] bf16/fp16, ids [B, rows] or None, centers [B or 1, C, HD]
+    bf16 or None (its own table)."""
     packed: torch.Tensor
     scales: torch.Tensor
+    ids: Optional[torch.Tensor] = None
+    centers: Optional[torch.Tensor] = None
+
+
+class SegmentTable:
+    """The nkv_segment table of a list of segments: a host ctypes array (the
+    library validates and plans from it) and the same bytes in device memory
+    (the kernels read it).  Built once per segment list; the segments'
+    tensors are kept alive with it."""
+
+    def __init__(self, segments: list, device: torch.device):
+        if not segments:
+            raise ValueError("a segment table needs at least one segment")
+        self.segments = list(segments)
+        n = len(self.segments)
+        self.host = (NkvSegment * n)()
+        row, cbase = 0, 0
+        with_centers = self.segments[0].centers is not None
+        for i, sg in enumerate(self.segments):
+            _contig(sg.packed, torch.uint8, "segment packed")
+            if sg.scales.dtype not in _SCALE_CODES or not sg.scales.is_contiguous():
+                raise TypeError("segment scales must be contiguous bf16 or fp16")
+            if sg.packed.dim() != 3 or sg.scales.dim() != 3 or \
+                    sg.scales.shape[:2] != sg.packed.shape[:2]:
+                raise ValueError("segment packed/scales must be [B, rows, ...]")
+            if (sg.centers is not None) != with_centers:
+                raise ValueError("every segment must have a center table, or none")
+            e = self.host[i]
+            e.packed, e.scales = sg.packed.data_ptr(), sg.scales.data_ptr()
+            e.row_start, e.rows = row, int(sg.packed.shape[1])
+            if with_centers:
+                _contig(sg.centers, torch.bfloat16, "segment centers")
+                if sg.ids is None or sg.ids.dtype not in _ID_BYTES or not sg.ids.is_contiguous() \
+                        or tuple(sg.ids.shape) != tuple(sg.packed.shape[:2]):
+                    raise ValueError("segment ids must be contiguous [B, rows] integers")
+                if sg.centers.dim() != 3 or sg.centers.shape[0] not in (1, sg.packed.shape[0]):
+                    raise ValueError("segment centers must be [B or 1, C, HD]")
+                e.ids, e.centers = sg.ids.data_ptr(), sg.centers.data_ptr()
+                e.id_bytes = _ID_BYTES[sg.ids.dtype]
+                e.num_centers = int(sg.centers.shape[1])
+                e.centers_batch_stride = 0 if sg.centers.shape[0] == 1 else int(sg.centers.stride(0))
+                e.center_base = cbase
+                cbase += e.num_centers
+            row += e.rows
+        self.rows = row
+        self.batch = int(self.segments[0].packed.shape[0])
+        raw = bytes(memoryview(self.host).cast("B"))
+        self.device = torch.frombuffer(bytearray(raw), dtype=torch.uint8).to(device)
+
+    @property
+    def has_centers(self) -> bool:
+        return self.segments[0].centers is not None
+
+
+@dataclass
+class Codec:
+    """Device tensors of one K or V history codec: either flat arrays of all
+    rows, packed [B, N, r/2] uint8, scales [B, N, r/group] bf16/fp16, ids
+    [B, N] (uint8/int16/int32) or None, centers [B or 1, C, HD] bf16 or None;
+    or a SegmentTable of per-segment arrays (then packed/scales/ids/centers
+    are None).  w_dec [HD, r] bf16, mean [HD] fp32 or None apply to all rows.
+    """
+    packed: Optional[torch.Tensor]
+    scales: Optional[torch.Tensor]
     w_dec: torch.Tensor
     group: int
     ids: Optional[torch.Tensor] = None
     centers: Optional[torch.Tensor] = None
     mean: Optional[torch.Tensor] = None
+    segments: Optional[SegmentTable] = None
 
     @property
     def r(self) -> int:
@@ -223,14 +286,39 @@ class Codec:
 
     @property
     def batch(self) -> int:
-        return int(self.packed.shape[0])
+        return self.segments.batch if self.segments is not None else int(self.packed.shape[0])
 
     @property
     def tokens(self) -> int:
-        return int(self.packed.shape[1])
+        return self.segments.rows if self.segments is not None else int(self.packed.shape[1])
+
+    @property
+    def scale_dtype(self) -> torch.dtype:
+        src = self.segments.segments[0].scales if self.segments is not None else self.scales
+        return src.dtype
 
     def validate(self, hd: int) -> None:
         r = self.r
+        _contig(self.w_dec, torch.bfloat16, "w_dec")
+        if tuple(self.w_dec.shape) != (hd, r):
+            raise ValueError(f"w_dec must be [HD={hd}, r={r}]")
+        if self.mean is not None:
+            _contig(self.mean, torch.float32, "mean")
+            if self.mean.numel() != hd:
+                raise ValueError("mean must have HD elements")
+        if self.segments is not None:
+            if self.group <= 0 or r % self.group:
+                raise ValueError("group must divide r")
+            for sg in self.segments.segments:
+                B, rows = int(sg.packed.shape[0]), int(sg.packed.shape[1])
+                if tuple(sg.packed.shape) != (B, rows, r // 2) or \
+                        tuple(sg.scales.shape) != (B, rows, r // self.group) or \
+                        B != self.batch or sg.scales.dtype != self.scale_dtype:
+                    raise ValueError("every segment must be [B, rows, r/2] codes with "
+                                     "[B, rows, r/group] scales of one dtype")
+                if sg.centers is not None and sg.centers.shape[2] != hd:
+                    raise ValueError("segment centers must have HD columns")
+            return
         _contig(self.packed, torch.uint8, "packed")
         _contig(self.w_dec, torch.bfloat16, "w_dec")
         if self.scales.dtype not in _SCALE_CODES or not self.scales.is_contiguous():
@@ -240,8 +328,6 @@ class Codec:
             raise ValueError(f"packed must be [B, N, r/2], got {tuple(self.packed.shape)}")
         if self.group <= 0 or r % self.group or tuple(self.scales.shape) != (B, N, r // self.group):
             raise ValueError("scales must be [B, N, r/group]")
-        if tuple(self.w_dec.shape) != (hd, r):
-            raise ValueError(f"w_dec must be [HD={hd}, r={r}]")
         if self.centers is not None:
             _contig(self.centers, torch.bfloat16, "centers")
             if self.ids is None or self.ids.dtype not in _ID_BYTES or not self.ids.is_contiguous():
@@ -251,29 +337,33 @@ class Codec:
             if self.centers.dim() != 3 or self.centers.shape[0] not in (1, B) or \
                     self.centers.shape[2] != hd:
                 raise ValueError("centers must be [B or 1, C, HD]")
-        if self.mean is not None:
-            _contig(self.mean, torch.float32, "mean")
-            if self.mean.numel() != hd:
-                raise ValueError("mean must have HD elements")
 
     def struct(self) -> NkvCodec:
         c = NkvCodec()
-        c.packed, c.scales, c.w_dec = (self.packed.data_ptr(), self.scales.data_ptr(),
-                                       self.w_dec.data_ptr())
-        c.r, c.group, c.scale_dtype = self.r, self.group, _SCALE_CODES[self.scales.dtype]
+        c.w_dec = self.w_dec.data_ptr()
+        c.r, c.group, c.scale_dtype = self.r, self.group, _SCALE_CODES[self.scale_dtype]
+        if self.mean is not None:
+            c.mean = self.mean.data_ptr()
+        if self.segments is not None:
+            c.n_segments = len(self.segments.segments)
+            c.segments = ctypes.cast(self.segments.host, ctypes.POINTER(NkvSegment))
+            c.segments_dev = self.segments.device.data_ptr()
+            return c
+        c.packed, c.scales = self.packed.data_ptr(), self.scales.data_ptr()
         if self.centers is not None:
             c.centers, c.ids = self.centers.data_ptr(), self.ids.data_ptr()
             c.id_bytes = _ID_BYTES[self.ids.dtype]
             c.num_centers = int(self.centers.shape[1])
             c.centers_batch_stride = (0 if self.centers.shape[0] == 1
                                       else int(self.centers.stride(0)))
-        if self.mean is not None:
-            c.mean = self.mean.data_ptr()
         return c
 
 
 def decode(codec: Codec, hd: int, row_index: Optional[torch.Tensor] = None) -> torch.Tensor:
-    """Full-width bf16 decode [B, rows, HD] of all or selected rows."""
+    """Full-width bf16 decode [B, rows, HD] of all or selected rows (a flat
+    codec; the segments of a segment list are decoded one by one)."""
+    if codec.segments is not None:
+        raise ValueError("decode takes a flat codec; decode segments one at a time")
     device = _require_gpu(codec.packed, row_index)
     codec.validate(hd)
     args = NkvDecodeArgs()
@@ -341,6 +431,36 @@ def _attend_args(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional
     lse = torch.empty((B, H, Qn), device=device, dtype=torch.float32) if return_lse else None
     args.lse = _ptr(lse)
     return args, out, lse, device
+
+
+def _set_visibility(args: NkvAttendArgs, visibility: Optional[Visibility], Qn: int) -> None:
+    """Point the args at a current-key visibility mask (nkv_attend_args.cur_mask)."""
+    if visibility is None:
+        return
+    _contig(visibility.bits, torch.int32, "visibility bits")
+    _contig(visibility.q_group, torch.int32, "visibility q_group")
+    if visibility.bits.dim() != 2 or visibility.q_group.numel() != Qn:
+        raise ValueError("visibility must be bits [groups, words] and q_group [Q]")
+    if visibility.words * 32 < args.Nc:
+        raise ValueError("visibility bits cover fewer keys than the current chunk holds")
+    args.cur_mask, args.q_group = visibility.bits.data_ptr(), visibility.q_group.data_ptr()
+    args.n_groups, args.cur_mask_words = visibility.groups, visibility.words
+
+
+def _set_hist_rows(args: NkvAttendArgs, hist_rows: Optional[torch.Tensor]):
+    """Point the args at a history row list (nkv_attend_args.hist_rows).  An
+    empty list still needs a non-NULL pointer (NULL means every row), and an
+    empty tensor's data_ptr() is 0, so it gets a one-element stand-in that is
+    never read; the caller keeps the returned tensor alive over the call."""
+    if hist_rows is None:
+        return None
+    _contig(hist_rows, torch.int32, "hist_rows")
+    if hist_rows.numel() == 0:
+        hist_rows = torch.zeros(1, device=hist_rows.device, dtype=torch.int32)
+        args.hist_rows, args.n_hist = hist_rows.data_ptr(), 0
+        return hist_rows
+    args.hist_rows, args.n_hist = hist_rows.data_ptr(), int(hist_rows.numel())
+    return hist_rows
 
 
 def c64_fit(x: torch.Tensor, init_rows: torch.Tensor, iterations: int = 2,
@@ -488,6 +608,88 @@ class Rope:
         return r
 
 
+@dataclass
+class RopeTable:
+    """Read-time RoPE from a per-row frequency table (nkv_rope.cs_rows): the
+    reference's own per-token form, cache_freqs [rows, 1, D/2] or [rows, D/2]
+    complex128 (_kv_freqs, pipelines/wan_video.py:3322-3341), stored on the
+    device as fp64 (cos, sin) pairs [rows, D/2, 2]; row n of the codec (or
+    query t) rotates by entry n."""
+    cs_rows: torch.Tensor
+
+    @classmethod
+    def from_freqs(cls, freqs: torch.Tensor, device: torch.device) -> "RopeTable":
+        f = torch.as_tensor(freqs)
+        if not torch.is_complex(f):
+            raise ValueError("freqs must be a complex per-row table")
+        if f.dim() == 3:
+            if f.shape[1] != 1:
+                raise ValueError("freqs must be [rows, 1, D/2] or [rows, D/2]")
+            f = f[:, 0]
+        if f.dim() != 2 or f.shape[0] == 0:
+            raise ValueError("freqs must be a non-empty [rows, D/2] table")
+        return cls(torch.view_as_real(f.to(torch.complex128)).contiguous().to(device))
+
+    @property
+    def pairs(self) -> int:
+        return int(self.cs_rows.shape[1])
+
+    @property
+    def rows(self) -> int:
+        return int(self.cs_rows.shape[0])
+
+    def struct(self) -> NkvRope:
+        _contig(self.cs_rows, torch.float64, "cs_rows")
+        _require_gpu(self.cs_rows)
+        if self.cs_rows.dim() != 3 or self.cs_rows.shape[2] != 2:
+            raise ValueError("cs_rows must be [rows, D/2, 2] float64")
+        r = NkvRope()
+        r.cs_rows, r.n_rows = self.cs_rows.data_ptr(), self.rows
+        r.pt = self.pairs
+        return r
+
+
+@dataclass
+class Visibility:
+    """Visibility of the current keys per query group (nkv_attend_args.cur_mask):
+    bits [groups, words] int32 (bit k % 32 of word k / 32: current key k is
+    seen), q_group [Q] int32 (each query's group).  from_bool builds it from
+    a boolean mask [Q, Nc] (True = visible, the reference's attention_lse
+    mask convention, CN/core.py:45-72) by grouping identical rows, as
+    attention_grouped_mask groups queries of equal visibility
+    (CN/core.py:94-103)."""
+    bits: torch.Tensor
+    q_group: torch.Tensor
+
+    @classmethod
+    def from_bool(cls, mask: torch.Tensor, device: torch.device) -> "Visibility":
+        m = torch.as_tensor(mask)
+        if m.dtype != torch.bool:
+            raise ValueError("Only boolean visibility masks are supported")
+        if m.dim() != 2:
+            raise ValueError("mask must be [Q, Nc]")
+        rows, inverse = torch.unique(m.to(torch.uint8), dim=0, return_inverse=True)
+        nc = int(m.shape[1])
+        words = max(1, (nc + 31) // 32)
+        padded = torch.zeros((rows.shape[0], words * 32), dtype=torch.int64, device=rows.device)
+        padded[:, :nc] = rows.to(torch.int64)
+        weights = torch.bitwise_left_shift(torch.ones(32, dtype=torch.int64, device=rows.device),
+                                           torch.arange(32, device=rows.device))
+        packed = (padded.view(rows.shape[0], words, 32) * weights).sum(-1)
+        # two's-complement int32 view of the unsigned 32-bit words
+        packed = torch.where(packed >= 2 ** 31, packed - 2 ** 32, packed).to(torch.int32)
+        return cls(packed.contiguous().to(device),
+                   inverse.reshape(-1).to(torch.int32).contiguous().to(device))
+
+    @property
+    def groups(self) -> int:
+        return int(self.bits.shape[0])
+
+    @property
+    def words(self) -> int:
+        return int(self.bits.shape[1])
+
+
 def rope_apply(x: torch.Tensor, rope: Rope, rows: Optional[torch.Tensor] = None,
                out: Optional[torch.Tensor] = None) -> torch.Tensor:
     """RoPE of x [B, S, H, D] bf16 at the positions of codec rows rows[s]
@@ -542,6 +744,7 @@ class Camera:
         c.n_mats, c.layout = int(self.mats.shape[1]), CAMERA_LAYOUTS[self.layout]
         c.frame_mat, c.n_frames = self.frame_mat.data_ptr(), int(self.frame_mat.numel())
         c.tokens_per_frame = int(self.tokens_per_frame)
+        c.n_batches = int(self.mats.shape[0])
         return c
 
 
@@ -578,7 +781,8 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
            splits: int = 0, out: Optional[torch.Tensor] = None,
            kernel_events: Optional[tuple[int, int]] = None,
            workspace: Optional[torch.Tensor] = None, schedule: str = "auto",
-           rope: Optional[Rope] = None, camera: Optional[Camera] = None):
+           rope=None, camera: Optional[Camera] = None,
+           hist_rows: Optional[torch.Tensor] = None, visibility: Optional[Visibility] = None):
     """Fused decode+attention (see nkv_attend).
 
     q [B, Q, H, D] bf16; k_cur/v_cur [B, Nc, H, D] bf16 or None; key/value
@@ -592,11 +796,18 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
     camera: camera P^-1 of the decoded history keys (after rope) and values
     at their codec rows (q, k_cur and v_cur are taken as already
     transformed; the caller applies P to the output); key-chunk schedule.
+    rope may be a Rope (frame bands) or a RopeTable (per-row table).
+    hist_rows: int32 codec rows attended (None: all, in order).
+    visibility: which current keys each query sees (None: all).
     """
     if schedule not in SCHEDULES:
         raise ValueError(f"schedule must be one of {sorted(SCHEDULES)}")
     args, out, lse, device = _attend_args(q, k_cur, v_cur, key, value, softmax_scale, out,
                                           return_lse)
+    if hist_rows is not None or visibility is not None:
+        _require_gpu(q, hist_rows, *(() if visibility is None else (visibility.bits,)))
+    hold = _set_hist_rows(args, hist_rows)
+    _set_visibility(args, visibility, int(q.shape[1]))
     args.splits = int(splits)
     args.schedule = SCHEDULES[schedule]
     rope_struct = None
@@ -619,6 +830,7 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
         workspace = torch.empty(need, device=device, dtype=torch.uint8)
     check("nkv_attend", lib().nkv_attend(_stream(device), byref(args),
                                          _ptr(workspace) if need else None, need))
+    del hold
     return out, lse
 
 
@@ -628,7 +840,9 @@ class ReaderTensors:
     heads int32 [nh]; k_read bf16 [nh, d, rK]; v_read bf16 [nh, D, rV];
     q_reduce / k_affine bf16 [nh, D, d] and v_affine bf16 [nh, D, D], each
     None for the identity; rope_pairs int32 [nh, d/2], the original RoPE
-    pair of each reader pair (None: pair j, d == D)."""
+    pair of each reader pair (None: pair j, d == D); cam_blocks int32
+    [nh, d/8], the camera sub-frame of each 8-dim reader block (None: j % 4,
+    d == D)."""
     heads: torch.Tensor
     d: int
     k_read: torch.Tensor
@@ -637,6 +851,7 @@ class ReaderTensors:
     k_affine: Optional[torch.Tensor] = None
     v_affine: Optional[torch.Tensor] = None
     rope_pairs: Optional[torch.Tensor] = None
+    cam_blocks: Optional[torch.Tensor] = None
 
     def struct(self, D: int, rK: int, rV: int) -> NkvReaderGroup:
         nh, d = int(self.heads.numel()), int(self.d)
@@ -662,11 +877,17 @@ class ReaderTensors:
             if tuple(self.rope_pairs.shape) != (nh, d // 2):
                 raise ValueError(f"rope_pairs must be [{nh}, {d // 2}]")
             g.rope_pairs = self.rope_pairs.data_ptr()
+        if self.cam_blocks is not None:
+            _contig(self.cam_blocks, torch.int32, "cam_blocks")
+            if tuple(self.cam_blocks.shape) != (nh, d // 8):
+                raise ValueError(f"cam_blocks must be [{nh}, {d // 8}]")
+            g.cam_blocks = self.cam_blocks.data_ptr()
         return g
 
 
 def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, softmax_scale, out,
-               return_lse, rope=None, q_pre=None, q_rope=None):
+               return_lse, rope=None, q_pre=None, q_rope=None, camera=None, q_camera=None,
+               visibility=None):
     args, out, lse, device = _attend_args(q, k_cur, v_cur, key, value, softmax_scale, out,
                                           return_lse)
     keep = []  # ctypes structs the call points to
@@ -674,6 +895,15 @@ def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, soft
         r = rope.struct()
         keep.append(r)
         args.rope = ctypes.pointer(r)
+    if camera is not None:
+        if camera.mats.shape[0] not in (1, q.shape[0]):
+            raise ValueError("camera batch must match q or broadcast")
+        c = camera.struct()
+        keep.append(c)
+        args.camera = ctypes.pointer(c)
+    if visibility is not None:
+        _require_gpu(visibility.bits)
+        _set_visibility(args, visibility, int(q.shape[1]))
     _require_gpu(protect_rows, low_rows, *[g.heads for g in groups])
     _contig(protect_rows, torch.int32, "protect_rows")
     _contig(low_rows, torch.int32, "low_rows")
@@ -687,17 +917,20 @@ def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, soft
         structs[i] = g.struct(D, key.r, value.r)
     f.num_groups = len(groups)
     f.groups = structs
-    if rope is not None:
-        if q_pre is not None:
-            _require_gpu(q_pre)
-            if q_pre.dtype != torch.bfloat16 or tuple(q_pre.shape) != tuple(q.shape):
-                raise ValueError("q_pre must be bf16 with q's shape [B, Q, H, D]")
-            f.q_pre = q_pre.data_ptr()
-            f.qp_sb, f.qp_st, f.qp_sh = _strides_bthd(q_pre, "q_pre")
-        if q_rope is not None:
-            qr = q_rope.struct()
-            keep.append(qr)
-            f.q_rope = ctypes.pointer(qr)
+    if q_pre is not None:
+        _require_gpu(q_pre)
+        if q_pre.dtype != torch.bfloat16 or tuple(q_pre.shape) != tuple(q.shape):
+            raise ValueError("q_pre must be bf16 with q's shape [B, Q, H, D]")
+        f.q_pre = q_pre.data_ptr()
+        f.qp_sb, f.qp_st, f.qp_sh = _strides_bthd(q_pre, "q_pre")
+    if rope is not None and q_rope is not None:
+        qr = q_rope.struct()
+        keep.append(qr)
+        f.q_rope = ctypes.pointer(qr)
+    if camera is not None and q_camera is not None:
+        qc = q_camera.struct()
+        keep.append(qc)
+        f.q_camera = ctypes.pointer(qc)
     need = lib().nkv_fast_attend_workspace_size(byref(f))
     err = lib().nkv_last_error().decode()
     if need == 0 and err:
@@ -720,8 +953,10 @@ def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[
                 groups: list, *, softmax_scale: Optional[float] = None,
                 return_lse: bool = True, out: Optional[torch.Tensor] = None,
                 kernel_events: Optional[tuple[int, int]] = None,
-                workspace: Optional[torch.Tensor] = None, rope: Optional[Rope] = None,
-                q_pre: Optional[torch.Tensor] = None, q_rope: Optional[Rope] = None):
+                workspace: Optional[torch.Tensor] = None, rope=None,
+                q_pre: Optional[torch.Tensor] = None, q_rope=None,
+                camera: Optional[Camera] = None, q_camera: Optional[Camera] = None,
+                visibility: Optional[Visibility] = None):
     """NanoKV-Fast mixed-dimensional attention (see nkv_fast_attend).
 
     protect_rows / low_rows: int32 codec rows of the native and low
@@ -730,11 +965,16 @@ def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[
     bracket the native partition's attention kernel.  rope: positions of the
     codec rows (history keys rotated at read); then q is the rotated query,
     q_pre [B, Q, H, D] the pre-RoPE query the reader groups project and
-    q_rope the queries' positions (query t at row t).
+    q_rope the queries' positions (query t at row t).  camera: P^-1 of the
+    history rows (q, k_cur, v_cur already transformed; the caller applies P
+    to out), q_camera: P^T of the query rows for the reader queries (then q_pre
+    is the untransformed query).  visibility: which current keys each query
+    sees in the native partition.
     """
     f, structs, need, out, lse, device = _fast_args(q, k_cur, v_cur, key, value, protect_rows,
                                                     low_rows, groups, softmax_scale, out,
-                                                    return_lse, rope, q_pre, q_rope)
+                                                    return_lse, rope, q_pre, q_rope, camera,
+                                                    q_camera, visibility)
     if kernel_events is not None:
         f.attend.ev_kernel_begin, f.attend.ev_kernel_end = kernel_events
     if workspace is None or workspace.numel() < need:

@@ -80,8 +80,10 @@ class Shape:
 
 # BASELINE.json configurations (index = position in its "configs" list).
 CONFIGS = {
-    0: Shape("cfg0_cpu_h8_d64", H=8, D=64, N=2048, Q=256, Nc=256, rK=64, rV=64, G=64, C=16,
-             scale_dtype=torch.bfloat16),
+    # the CPU reference case: per-32 fp16 scales, fixed orthonormal 512 x 64
+    # encoder / decoder (make_layer(..., orthonormal_codec=True))
+    0: Shape("cfg0_cpu_h8_d64", H=8, D=64, N=2048, Q=256, Nc=256, rK=64, rV=64, G=32, C=16,
+             scale_dtype=torch.float16),
     1: Shape("cfg1_h24_d128_n12480_q1560", H=24, D=128, N=12480, Q=1560, Nc=1560, rK=384,
              rV=384, G=32, C=256),
     2: Shape("cfg2_h24_d128_n49920_q780", H=24, D=128, N=49920, Q=780, Nc=780, rK=384, rV=256,

@@ -68,6 +68,15 @@ Pinning (the independent check that fixes each function; see tests/):
                                identity matrices leave x unchanged; a
                                permutation matrix moves dims exactly; P then
                                P^-1 returns x to bf16 rounding
+  camera_blocks_apply         camera_selected's einsum "bhfgij,bhftgjr->
+                               bhftgir" (CN/core.py:134-137) in fp64 on
+                               bf16-rounded matrices; block sub-frames j % 4
+                               at width 128 equal camera_apply's full layout
+  attention (mask)            torch SDPA with a boolean attn_mask in fp64 for
+                               rows that see a key; the closed form (0, -inf)
+                               of the reference's blockwise path for rows that
+                               see none (CN/core.py:57-72); an all-True mask
+                               equals no mask
 """
 from __future__ import annotations
 
@@ -353,13 +362,16 @@ def decode(packed, scales, w_dec_bf16, group: int, scale_dtype: str = "bf16", id
 
 
 # ----------------------------------------------------------------- a10-a12
-def attention(q, k, v, scale: float, dtype=np.float64):
+def attention(q, k, v, scale: float, dtype=np.float64, mask=None):
     """softmax(q k^T * scale) v per head (wan_video_dit.py:42-82), computed in
     `dtype` (float64 by default).
 
     q [H, Q, D], k/v [H, N, D] (float arrays).  Returns (out [H, Q, D],
     lse [H, Q] natural log).  An empty key set gives (0, -inf) as
-    attention_lse does (CN/core.py:48-49).
+    attention_lse does (CN/core.py:48-49).  mask [Q, N] bool (True =
+    visible, CN/core.py:45-72, shared by the heads): hidden keys get logit
+    -inf; a row that sees no key gives (0, -inf), as the reference's
+    blockwise path does (its origin is 0 and every probability 0).
     """
     q = np.asarray(q, dtype)
     k = np.asarray(k, dtype)
@@ -369,13 +381,19 @@ def attention(q, k, v, scale: float, dtype=np.float64):
         return np.zeros((H, Qn, v.shape[2]), dtype), np.full((H, Qn), -np.inf, dtype)
     s = np.matmul(q, k.transpose(0, 2, 1))
     s *= dtype(scale)
+    if mask is not None:
+        s = np.where(np.asarray(mask, bool)[None], s, -np.inf)
     m = s.max(-1, keepdims=True)
+    empty = ~np.isfinite(m)
+    m = np.where(empty, 0.0, m)
     s -= m
     np.exp(s, out=s)
     l = s.sum(-1, keepdims=True)
-    s /= l
+    s /= np.where(empty, 1.0, l)
     out = np.matmul(s, v)
-    return out, (m + np.log(l))[..., 0]
+    with np.errstate(divide="ignore"):
+        lse = np.where(empty, -np.inf, m + np.log(np.where(empty, 1.0, l)))
+    return out, lse[..., 0]
 
 
 def merge(out_a, lse_a, out_b, lse_b):
@@ -393,7 +411,7 @@ def merge(out_a, lse_a, out_b, lse_b):
 def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Optional[dict],
                   scale: float, heads: Optional[Sequence[int]] = None, D: int = 128,
                   dtype=np.float64, key_freqs: Optional[np.ndarray] = None,
-                  key_cam: Optional[tuple] = None):
+                  key_cam: Optional[tuple] = None, hist_rows=None, cur_mask=None):
     """Reference decode-then-SDPA path for one batch item.
 
     q [Q, H, D] bf16 bits; k_cur/v_cur [Nc, H, D] bf16 bits or None; key/value
@@ -405,34 +423,48 @@ def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Op
     (wan_video_dit.py:538-546), applied before attention.
     key_cam (mats [N, 4, 4, 4] fp32, layout): camera P^-1 of the decoded
     history keys (after RoPE) and values at their rows (camera_apply).
+    hist_rows: the codec rows attended (the history filter of
+    wan_video_dit.py:509-530), in order; key_freqs and key_cam stay indexed
+    by codec row.  cur_mask [Q, Nc] bool: which current keys each query sees
+    (the history is visible to every query).
     """
     q = bf16_to_f32(q_bf16)
     Qn, H = q.shape[0], q.shape[1]
     heads = list(range(H)) if heads is None else list(heads)
     cols = np.concatenate([np.arange(h * D, (h + 1) * D) for h in heads])
     ks, vs = [], []
+    n_hist = 0
     if key is not None:
-        kbits = decode(**key, columns=cols, dtype=dtype)
+        rows = None if hist_rows is None else np.asarray(hist_rows, np.int64)
+        kbits = decode(**key, row_index=rows, columns=cols, dtype=dtype)
         if key_freqs is not None:
-            kbits = rope_apply(kbits.reshape(-1, len(heads), D), key_freqs)
-        vbits = decode(**value, columns=cols, dtype=dtype)
+            kf = key_freqs if rows is None else key_freqs[rows]
+            kbits = rope_apply(kbits.reshape(-1, len(heads), D), kf)
+        vbits = decode(**value, row_index=rows, columns=cols, dtype=dtype)
         if key_cam is not None:
-            kbits = camera_apply(kbits.reshape(-1, len(heads), D), *key_cam)
-            vbits = camera_apply(vbits.reshape(-1, len(heads), D), *key_cam)
+            mats = key_cam[0] if rows is None else np.asarray(key_cam[0])[rows]
+            kbits = camera_apply(kbits.reshape(-1, len(heads), D), mats, *key_cam[1:])
+            vbits = camera_apply(vbits.reshape(-1, len(heads), D), mats, *key_cam[1:])
         kd = bf16_to_f32(kbits)
         vd = bf16_to_f32(vbits)
         ks.append(kd.reshape(-1, len(heads), D))
         vs.append(vd.reshape(-1, len(heads), D))
+        n_hist = ks[0].shape[0]
+    n_cur = 0
     if k_cur_bf16 is not None:
         ks.append(bf16_to_f32(k_cur_bf16)[:, heads])
         vs.append(bf16_to_f32(v_cur_bf16)[:, heads])
+        n_cur = ks[-1].shape[0]
     if ks:
         k = np.concatenate(ks, 0).transpose(1, 0, 2)
         v = np.concatenate(vs, 0).transpose(1, 0, 2)
     else:
         k = np.zeros((len(heads), 0, D))
         v = np.zeros((len(heads), 0, D))
-    out, lse = attention(q[:, heads].transpose(1, 0, 2), k, v, scale, dtype)
+    mask = None
+    if cur_mask is not None and n_cur:
+        mask = np.concatenate([np.ones((Qn, n_hist), bool), np.asarray(cur_mask, bool)], 1)
+    out, lse = attention(q[:, heads].transpose(1, 0, 2), k, v, scale, dtype, mask=mask)
     return out.transpose(1, 0, 2), lse
 
 
@@ -526,6 +558,22 @@ def camera_apply(x_bf16, mats, layout: str = "full") -> np.ndarray:
     return f32_to_bf16(y.astype(np.float32))
 
 
+def camera_blocks_apply(x_bf16, mats, cams) -> np.ndarray:
+    """camera_selected (CN/core.py:110-137) of bf16 bits x [S, W] (one head's
+    W reader dims, whole 8-dim blocks) by mats [S, 4, 4, 4] fp32 of each row:
+    block j uses sub-frame cams[j]; its dims 8j + 2e + r form vector r over
+    e (the (j, r) order of the full layout).  Matrix entries rounded to bf16,
+    sums exact in fp64, then fp64 -> fp32 -> bf16 (as camera_apply)."""
+    x = bf16_to_f32(np.asarray(x_bf16)).astype(np.float64)
+    m = bf16_to_f32(f32_to_bf16(np.asarray(mats, np.float32))).astype(np.float64)
+    y = x.copy()
+    for j, c in enumerate(np.asarray(cams, np.int64).tolist()):
+        for r in range(2):
+            dims = [8 * j + 2 * e + r for e in range(4)]
+            y[:, dims] = np.einsum("sij,sj->si", m[:, c % 4], x[:, dims])
+    return f32_to_bf16(y.astype(np.float32))
+
+
 # ----------------------------------------------------------------- a13
 def protected_frames(count: int, recent: int, stride: int, sink: int = 0) -> np.ndarray:
     """Frame-level protection mask (CN/core.py:140-152, metadata_cache.py:64-68).
@@ -584,7 +632,8 @@ def reader_read(codec: dict, rows, read_bf16, table_bf16, bias, dtype=np.float64
 def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_rows, low_rows,
                 groups: Sequence[dict], scale: float, heads: Optional[Sequence[int]] = None,
                 D: int = 128, dtype=np.float64, key_freqs: Optional[np.ndarray] = None,
-                q_pre_bf16=None, q_freqs: Optional[np.ndarray] = None):
+                q_pre_bf16=None, q_freqs: Optional[np.ndarray] = None, cur_mask=None,
+                key_cam=None, q_cam=None, out_cam=None):
     """NanoKV-Fast for one batch item: hybrid_attention (CN/core.py:278-310)
     with maybe_attention's partitions (CN/mg35.py:192-348), identity lift.
 
@@ -602,7 +651,17 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
     query is q_pre_bf16 [Q, H, D] projected, and it and k_low are rotated on
     the retained pairs (rope_selected, CN/core.py:75-91) with original pair
     rope_pairs[i][j] (group key; None: pair j), the query at q_freqs [Q, D/2].
-    q_bf16 is then the already rotated query of the native partition."""
+    q_bf16 is then the already rotated query of the native partition.
+    cur_mask [Q, Nc] bool: which current keys each query sees (native
+    partition, CN/mg35.py:258-300).
+    Camera (CN/mg35.py:253-257, 310-347), mats [rows, 4, 4, 4] fp32 per row:
+    key_cam (P^-1 of the codec rows) transforms the protected keys (after
+    RoPE) and values in the full layout and the low keys / values on their
+    8-dim blocks (camera_selected, group keys cam_blocks / v_cam_blocks,
+    None: block j % 4); q_cam (P^T of the queries) the group query after its
+    RoPE; out_cam (P of the queries) the native output before the merge and
+    each low output before its lift.  q_bf16, k_cur and v_cur are taken as
+    already transformed; a group's query comes from q_pre_bf16 when given."""
     q = bf16_to_f32(q_bf16)
     Qn, H = q.shape[0], q.shape[1]
     heads = list(range(H)) if heads is None else list(heads)
@@ -612,24 +671,36 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
     for h in heads:
         cols = np.arange(h * D, (h + 1) * D)
         ks, vs = [], []
+        n_prot = 0
         if prot.size:
             kd = decode(**key, row_index=prot, columns=cols, dtype=dtype)
             vd = decode(**value, row_index=prot, columns=cols, dtype=dtype)
             if key_freqs is not None:
                 kd = rope_apply(kd[:, None, :], key_freqs[prot])[:, 0]
+            if key_cam is not None:
+                kd = camera_apply(kd[:, None, :], np.asarray(key_cam)[prot], "full")[:, 0]
+                vd = camera_apply(vd[:, None, :], np.asarray(key_cam)[prot], "full")[:, 0]
             ks.append(bf16_to_f32(kd))
             vs.append(bf16_to_f32(vd))
+            n_prot = prot.size
+        n_cur = 0
         if k_cur_bf16 is not None:
             ks.append(bf16_to_f32(k_cur_bf16)[:, h])
             vs.append(bf16_to_f32(v_cur_bf16)[:, h])
+            n_cur = ks[-1].shape[0]
         k = np.concatenate(ks, 0) if ks else np.zeros((0, D))
         v = np.concatenate(vs, 0) if vs else np.zeros((0, D))
-        on, ln = attention(q[None, :, h], k[None], v[None], scale, dtype)
+        mask = None
+        if cur_mask is not None and n_cur:
+            mask = np.concatenate([np.ones((Qn, n_prot), bool), np.asarray(cur_mask, bool)], 1)
+        on, ln = attention(q[None, :, h], k[None], v[None], scale, dtype, mask=mask)
         on, ln = bf16_to_f32(f32_to_bf16(on[0].astype(np.float32))), ln[0]
+        if out_cam is not None:
+            on = bf16_to_f32(camera_apply(f32_to_bf16(on)[:, None, :], out_cam, "full")[:, 0])
         grp = [(g, list(g["heads"]).index(h)) for g in groups if h in list(g["heads"])]
         if grp and low.size:
             g, i = grp[0]
-            qh = q[:, h] if key_freqs is None else bf16_to_f32(q_pre_bf16)[:, h]
+            qh = q[:, h] if q_pre_bf16 is None else bf16_to_f32(q_pre_bf16)[:, h]
             if g.get("q_reduce") is not None:
                 qr = bf16_to_f32(g["q_reduce"][i]).astype(dtype)
                 qh = bf16_to_f32(f32_to_bf16((qh.astype(dtype) @ qr).astype(np.float32)))
@@ -637,6 +708,11 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
                 rp = g.get("rope_pairs")
                 pairs = np.arange(qh.shape[1] // 2) if rp is None else np.asarray(rp[i])
                 qh = bf16_to_f32(rope_apply(f32_to_bf16(qh)[:, None, :], q_freqs[:, pairs])[:, 0])
+            cb = g.get("cam_blocks")
+            kcams = np.arange(qh.shape[1] // 8) % 4 if cb is None else np.asarray(cb[i])
+            vcb = g.get("v_cam_blocks")
+            if q_cam is not None:
+                qh = bf16_to_f32(camera_blocks_apply(f32_to_bf16(qh), q_cam, kcams))
             kt, kb = reader_tables(key.get("centers_bf16"), key.get("mean"), h,
                                    None if g.get("k_affine") is None else g["k_affine"][i], D, dtype)
             vt, vb = reader_tables(value.get("centers_bf16"), value.get("mean"), h,
@@ -644,10 +720,17 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
             kl = reader_read(key, low, g["k_read"][i], kt, kb, dtype)
             if key_freqs is not None:
                 kl = rope_apply(kl[:, None, :], key_freqs[low][:, pairs])[:, 0]
+            vl = reader_read(value, low, g["v_read"][i], vt, vb, dtype)
+            vcams = np.arange(vl.shape[1] // 8) % 4 if vcb is None else np.asarray(vcb[i])
+            if key_cam is not None:
+                kl = camera_blocks_apply(kl, np.asarray(key_cam)[low], kcams)
+                vl = camera_blocks_apply(vl, np.asarray(key_cam)[low], vcams)
             kl = bf16_to_f32(kl)
-            vl = bf16_to_f32(reader_read(value, low, g["v_read"][i], vt, vb, dtype))
+            vl = bf16_to_f32(vl)
             ol, ll = attention(qh[None], kl[None], vl[None], scale, dtype)
             ol = bf16_to_f32(f32_to_bf16(ol[0].astype(np.float32)))
+            if out_cam is not None:
+                ol = bf16_to_f32(camera_blocks_apply(f32_to_bf16(ol), out_cam, vcams))
             if g.get("lift") is not None:
                 # lift_output (CN/core.py:202-204), applied before the merge (mg35.py:347)
                 lf = bf16_to_f32(g["lift"][i]).astype(dtype)

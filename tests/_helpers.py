@@ -98,14 +98,14 @@ class Scenario:
         return out[0], out[1]
 
     # ---- oracle side
-    def reference(self, b, heads=None):
+    def reference(self, b, heads=None, **kw):
         import oracle.oracle as orc
         key = self.hist[b]["k"] if self.N else None
         val = self.hist[b]["v"] if self.N else None
         kc = u16(self.k_cur[b]) if self.Nc else None
         vc = u16(self.v_cur[b]) if self.Nc else None
         return orc.decode_attend(u16(self.q[b]), kc, vc, key, val, self.scale, heads=heads,
-                                 D=self.D)
+                                 D=self.D, **kw)
 
 
 def oracle_groups(payload: dict) -> list:
@@ -126,5 +126,37 @@ def oracle_groups(payload: dict) -> list:
             "k_affine": None if ident(g["k_affine"]) else u16(g["k_affine"].to(_t.bfloat16)),
             "v_affine": None if ident(g["v_affine"]) else u16(g["v_affine"].to(_t.bfloat16)),
             "lift": None if ident(g["lift"]) else u16(g["lift"].to(_t.bfloat16)),
+            # camera sub-frame of each 8-dim reader block (camera_selected)
+            "cam_blocks": ((g["indices"][:, ::8] // 8) % 4).numpy(),
+            "v_cam_blocks": ((g.get("v_indices", g["indices"])[:, ::8] // 8) % 4).numpy(),
         })
     return out
+
+
+def oracle_codec(cd, b: int = 0, scale_dtype: str = "fp16") -> dict:
+    """One batch item of an ops.Codec (flat or a segment table) as the oracle's
+    codec dict.  A segment table becomes the concatenation of its segments,
+    each segment's ids offset by the rows of the tables before it and the
+    tables concatenated: the same center row for every token, so the same
+    decode."""
+    if cd.segments is None:
+        return {"packed": cd.packed[b].cpu().numpy(), "scales": u16(cd.scales[b]),
+                "w_dec_bf16": u16(cd.w_dec), "group": cd.group, "scale_dtype": scale_dtype,
+                "ids": None if cd.ids is None else cd.ids[b].cpu().numpy().astype(np.int64),
+                "centers_bf16": None if cd.centers is None else
+                u16(cd.centers[b if cd.centers.shape[0] > 1 else 0]),
+                "mean": None if cd.mean is None else cd.mean.cpu().numpy()}
+    segs = cd.segments.segments
+    ids, tables, base = [], [], 0
+    for sg in segs:
+        if sg.centers is not None:
+            ids.append(sg.ids[b].cpu().numpy().astype(np.int64) + base)
+            t = sg.centers[b if sg.centers.shape[0] > 1 else 0]
+            tables.append(u16(t))
+            base += int(t.shape[0])
+    return {"packed": np.concatenate([sg.packed[b].cpu().numpy() for sg in segs]),
+            "scales": np.concatenate([u16(sg.scales[b]) for sg in segs]),
+            "w_dec_bf16": u16(cd.w_dec), "group": cd.group, "scale_dtype": scale_dtype,
+            "ids": np.concatenate(ids) if ids else None,
+            "centers_bf16": np.concatenate(tables) if tables else None,
+            "mean": None if cd.mean is None else cd.mean.cpu().numpy()}

@@ -56,3 +56,41 @@ def test_attend_rejects_unsupported_shapes():
     args.key.packed = args.key.scales = args.key.w_dec = 1
     rc = lib.nkv_attend(None, ctypes.byref(args), None, 0)
     assert rc == _lib.NKV_ERR_UNSUPPORTED and b"ranks" in lib.nkv_last_error()
+
+
+STRUCTS = {
+    "nkv_segment": _lib.NkvSegment, "nkv_codec": _lib.NkvCodec, "nkv_rope": _lib.NkvRope,
+    "nkv_camera": _lib.NkvCamera, "nkv_encode_args": _lib.NkvEncodeArgs,
+    "nkv_decode_args": _lib.NkvDecodeArgs, "nkv_attend_args": _lib.NkvAttendArgs,
+    "nkv_reader_group": _lib.NkvReaderGroup, "nkv_fast_args": _lib.NkvFastArgs,
+}
+
+
+def test_ctypes_structs_match_the_header_layout(tmp_path):
+    """Every ctypes mirror has the size and field offsets gcc gives the C
+    structs of include/nanokv.h (a stale mirror would pass fields at the wrong
+    offsets)."""
+    import shutil
+    import subprocess
+    gcc = shutil.which("gcc") or shutil.which("cc")
+    if gcc is None:
+        pytest.skip("no C compiler")
+    lines = ["#include <stdio.h>", "#include <stddef.h>", f'#include "{HEADER}"', "int main(void){"]
+    for cname, cls in STRUCTS.items():
+        lines.append(f'printf("{cname} size %zu\\n", sizeof({cname}));')
+        for field, _ in cls._fields_:
+            lines.append(f'printf("{cname} {field} %zu\\n", offsetof({cname}, {field}));')
+    lines.append("return 0;}")
+    src = tmp_path / "layout.c"
+    src.write_text("\n".join(lines))
+    exe = tmp_path / "layout"
+    subprocess.run([gcc, "-std=c99", str(src), "-o", str(exe)], check=True)
+    got = {}
+    for line in subprocess.run([str(exe)], check=True, capture_output=True,
+                               text=True).stdout.splitlines():
+        cname, field, value = line.split()
+        got[(cname, field)] = int(value)
+    for cname, cls in STRUCTS.items():
+        assert ctypes.sizeof(cls) == got[(cname, "size")], cname
+        for field, _ in cls._fields_:
+            assert getattr(cls, field).offset == got[(cname, field)], (cname, field)

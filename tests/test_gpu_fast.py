@@ -9,7 +9,7 @@ import torch
 
 import oracle.oracle as orc
 from nanokv_amd import codec_native, ops, synth
-from tests._helpers import Scenario, max_abs_cos, oracle_groups, u16
+from tests._helpers import Scenario, max_abs_cos, oracle_codec, oracle_groups, u16
 
 pytestmark = pytest.mark.gpu
 
@@ -125,12 +125,10 @@ def test_fast_history_attention_api(dev, monkeypatch):
     assert out.shape == (1, H, 40, D) and lse.shape == (1, H, 40)
     # oracle over the same payload bits
     key, value = nc.history_codecs(cache_k, cache_v, dev)
+    assert key.segments is not None and len(key.segments.segments) == 4
 
     def od(cd):
-        return {"packed": cd.packed[0].cpu().numpy(), "scales": u16(cd.scales[0]),
-                "w_dec_bf16": u16(cd.w_dec), "group": cd.group, "scale_dtype": "fp16",
-                "ids": cd.ids[0].cpu().numpy().astype(np.int64),
-                "centers_bf16": u16(cd.centers[0])}
+        return oracle_codec(cd, 0, "bf16" if cd.scale_dtype == torch.bfloat16 else "fp16")
     prot = torch.nonzero(protect).flatten().cpu().numpy()
     low = torch.nonzero(~protect).flatten().cpu().numpy()
     ref, ref_lse = orc.fast_attend(u16(q[0].permute(1, 0, 2)), u16(kc[0].permute(1, 0, 2)),

@@ -286,3 +286,51 @@ def test_protected_frames_exhaustive_small():
                 for sink in range(0, 3):
                     assert list(orc.protected_frames(count, recent, stride, sink)) == \
                         _protected_sets(count, recent, stride, sink)
+
+
+def test_masked_attention_against_torch_sdpa():
+    """oracle.attention with a boolean mask: rows that see a key equal torch's
+    SDPA with the same attn_mask in fp64 (a library routine); rows that see
+    none give (0, -inf) (the reference's blockwise path); an all-True mask is
+    no mask."""
+    g = torch.Generator().manual_seed(3)
+    H, Q, N, D = 2, 9, 13, 16
+    q = torch.randn(H, Q, D, generator=g, dtype=torch.float64)
+    k = torch.randn(H, N, D, generator=g, dtype=torch.float64)
+    v = torch.randn(H, N, D, generator=g, dtype=torch.float64)
+    mask = torch.rand(Q, N, generator=g) > 0.5
+    mask[3] = False
+    mask[5] = True
+    out, lse = orc.attention(q.numpy(), k.numpy(), v.numpy(), 0.25, mask=mask.numpy())
+    seen = mask.any(1)
+    ref = torch.nn.functional.scaled_dot_product_attention(
+        q[:, seen], k, v, attn_mask=mask[seen][None], scale=0.25)
+    np.testing.assert_allclose(out[:, seen.numpy()], ref.numpy(), rtol=1e-12, atol=1e-12)
+    s = (q @ k.transpose(1, 2)) * 0.25
+    ref_lse = torch.logsumexp(s.masked_fill(~mask[None], -np.inf), -1)
+    np.testing.assert_allclose(lse[:, seen.numpy()], ref_lse[:, seen].numpy(), rtol=1e-12)
+    assert np.all(out[:, 3] == 0) and np.all(np.isneginf(lse[:, 3]))
+    full, full_lse = orc.attention(q.numpy(), k.numpy(), v.numpy(), 0.25, mask=np.ones((Q, N), bool))
+    plain, plain_lse = orc.attention(q.numpy(), k.numpy(), v.numpy(), 0.25)
+    np.testing.assert_array_equal(full, plain)
+    np.testing.assert_array_equal(full_lse, plain_lse)
+
+
+def test_decode_attend_row_list_equals_selected_codec():
+    """decode_attend(hist_rows) equals decode_attend over a codec holding only
+    those rows (its packed codes, scales and ids sliced by the same rows)."""
+    from tests._helpers import Scenario, u16
+    sc = Scenario(H=2, D=32, N=70, Q=10, Nc=6, rK=64, rV=64, G=32, C=5)
+    rows = np.array([3, 4, 9, 20, 21, 22, 50, 69])
+    key, val = sc.hist[0]["k"], sc.hist[0]["v"]
+
+    def sliced(c):
+        c = dict(c)
+        c["packed"], c["scales"], c["ids"] = c["packed"][rows], c["scales"][rows], c["ids"][rows]
+        return c
+    a, la = orc.decode_attend(u16(sc.q[0]), u16(sc.k_cur[0]), u16(sc.v_cur[0]), key, val,
+                              sc.scale, D=sc.D, hist_rows=rows)
+    b, lb = orc.decode_attend(u16(sc.q[0]), u16(sc.k_cur[0]), u16(sc.v_cur[0]), sliced(key),
+                              sliced(val), sc.scale, D=sc.D)
+    np.testing.assert_array_equal(a, b)
+    np.testing.assert_array_equal(la, lb)

@@ -99,3 +99,37 @@ def test_camera_rejects_bad_layouts():
         orc.camera_vectors("full", 96)
     with pytest.raises(ValueError):
         orc.camera_vectors("sf13", 16)
+
+
+def _ref_selected(x, matrix, cams):
+    """camera_selected (CN/core.py:125-137) for one head: x [S, W] reader dims
+    in whole 8-dim blocks, matrix [S, 4, 4, 4], block j on sub-frame
+    cams[j]; the reference's einsum "bhfgij,bhftgjr->bhftgir" with one frame
+    per row (f = S, t = 1), in fp64."""
+    S, W = x.shape
+    selected = matrix[:, torch.as_tensor(cams)][None, None]       # b h f g i j
+    values = x.reshape(1, 1, S, 1, W // 8, 4, 2)                   # b h f t g j r
+    out = torch.einsum("bhfgij,bhftgjr->bhftgir", selected, values)
+    return out.reshape(S, W)
+
+
+@pytest.mark.parametrize("W", [32, 64, 128])
+def test_camera_blocks_match_reference_camera_selected(W):
+    g = torch.Generator().manual_seed(W + 1)
+    S = 7
+    mats = torch.eye(4).expand(S, 4, 4, 4) + 0.4 * torch.randn(S, 4, 4, 4, generator=g)
+    x = (torch.randn(S, W, generator=g) * 2).to(torch.bfloat16)
+    cams = torch.randint(0, 4, (W // 8,), generator=g)
+    ref = _ref_selected(x.double(), _bf16(mats), cams)
+    got = orc.camera_blocks_apply(_bits(x), mats.numpy(), cams.numpy())
+    assert np.array_equal(got, _bits(ref))
+
+
+def test_camera_blocks_j_mod_4_is_the_full_layout_at_128():
+    g = torch.Generator().manual_seed(5)
+    S = 6
+    mats = torch.eye(4).expand(S, 4, 4, 4) + 0.3 * torch.randn(S, 4, 4, 4, generator=g)
+    x = torch.randn(S, 128, generator=g).to(torch.bfloat16)
+    a = orc.camera_blocks_apply(_bits(x), mats.numpy(), np.arange(16) % 4)
+    b = orc.camera_apply(_bits(x)[:, None, :], mats.numpy(), "full")[:, 0]
+    assert np.array_equal(a, b)

@@ -104,3 +104,45 @@ def test_lift_applies_to_the_low_output():
         np.testing.assert_allclose(out[:, h], ref, rtol=2e-2, atol=2e-2)
         # not the transpose
         assert np.abs(out[:, h] - base[:, h] @ L[h].float().numpy().T).max() > 5e-2
+
+
+def test_identity_readers_with_camera_equal_full_decode():
+    """With identity readers (block sub-frames j % 4) the camera path of
+    fast_attend is the full decode with P^-1 on the history keys / values and
+    P on the output (CN/mg35.py:253-257, 310-347), for a recent-frames split."""
+    sc = Scenario(H=2, D=128, N=60, Q=12, Nc=10, rK=64, rV=64, G=32, C=6)
+    g = torch.Generator().manual_seed(9)
+    kinv = (torch.eye(4).expand(sc.N, 4, 4, 4) + 0.2 * torch.randn(sc.N, 4, 4, 4, generator=g)).numpy()
+    qt = (torch.eye(4).expand(sc.Q, 4, 4, 4) + 0.2 * torch.randn(sc.Q, 4, 4, 4, generator=g)).numpy()
+    p = (torch.eye(4).expand(sc.Q, 4, 4, 4) + 0.2 * torch.randn(sc.Q, 4, 4, 4, generator=g)).numpy()
+    prot, low = np.arange(40, sc.N), np.arange(40)
+    groups = oracle_groups(_identity_payload(sc))
+    key, val = sc.hist[0]["k"], sc.hist[0]["v"]
+    # the native query is the transformed one; the readers start from q_pre
+    q_native = orc.camera_apply(u16(sc.q[0]), qt, "full")
+    out, lse = orc.fast_attend(q_native, u16(sc.k_cur[0]), u16(sc.v_cur[0]), key, val, prot,
+                               low, groups, sc.scale, D=sc.D, q_pre_bf16=u16(sc.q[0]),
+                               key_cam=kinv, q_cam=qt, out_cam=p)
+    ref, ref_lse = orc.decode_attend(q_native, u16(sc.k_cur[0]), u16(sc.v_cur[0]), key, val,
+                                     sc.scale, D=sc.D, key_cam=(kinv, "full"))
+    ref = orc.bf16_to_f32(orc.camera_apply(orc.f32_to_bf16(ref.astype(np.float32)), p, "full"))
+    diff, cos = max_abs_cos(out, ref)
+    assert diff < 3e-2 and cos > 0.9999, (diff, cos)
+    np.testing.assert_allclose(lse, ref_lse, atol=1e-4)
+
+
+def test_identity_readers_with_mask_equal_full_decode():
+    """A current-key mask reaches only the native partition: with identity
+    readers fast_attend equals decode_attend under the same mask."""
+    sc = Scenario(H=2, D=32, N=50, Q=14, Nc=12, rK=64, rV=64, G=32, C=5)
+    mask = np.random.default_rng(4).random((sc.Q, sc.Nc)) > 0.4
+    prot, low = np.arange(30, sc.N), np.arange(30)
+    groups = oracle_groups(_identity_payload(sc))
+    key, val = sc.hist[0]["k"], sc.hist[0]["v"]
+    out, lse = orc.fast_attend(u16(sc.q[0]), u16(sc.k_cur[0]), u16(sc.v_cur[0]), key, val, prot,
+                               low, groups, sc.scale, D=sc.D, cur_mask=mask)
+    ref, ref_lse = orc.decode_attend(u16(sc.q[0]), u16(sc.k_cur[0]), u16(sc.v_cur[0]), key, val,
+                                     sc.scale, D=sc.D, cur_mask=mask)
+    diff, cos = max_abs_cos(out, ref)
+    assert diff < 2e-2 and cos > 0.9999, (diff, cos)
+    np.testing.assert_allclose(lse, ref_lse, atol=1e-4)
