@@ -417,6 +417,23 @@ int nkv_attend(void* stream, const nkv_attend_args* args, void* workspace,
                size_t workspace_bytes);
 
 /*
+ * Allocation-free nkv_attend.  No counterpart in the reference: it is for
+ * callers that cannot allocate device memory or pass a workspace (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * Same arguments, arithmetic and results as nkv_attend, but the scratch is a
+ * static array of NKV_STATIC_SCRATCH_BYTES per GPU inside the library (held
+ * until the process ends); a call that needs more (nkv_attend_workspace_size)
+ * fails with NKV_ERR_WORKSPACE and launches nothing.  No part of the scratch
+ * needs to start at zero: every byte a call reads it wrote first.  Every call
+ * on one GPU shares that GPU's array, so calls that overlap on one GPU (two
+ * streams, two threads) race; serialise them.  The stream must belong to the
+ * current device.  Allocates nothing (no hipMalloc, no allocating library
+ * routine).
+ */
+#define NKV_STATIC_SCRATCH_BYTES (64u << 20)
+int nkv_attend_static(void* stream, const nkv_attend_args* args);
+
+/*
  * One reader group of NanoKV-Fast (ReaderGroup, CN/core.py:155-204): its
  * heads read the low (unprotected) history rows through learned projections
  *   q_low = bf16(q_h . q_reduce[i])                         [Q, d]

@@ -34,7 +34,9 @@ EXPORTED = (
     "nkv_encode", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
     "nkv_fast_attend_workspace_size", "nkv_fast_attend", "nkv_rope_apply", "nkv_int8_pack",
     "nkv_int8_dequant", "nkv_c64_fit_workspace_size", "nkv_c64_fit", "nkv_camera_apply",
+    "nkv_attend_static",
 )
+NKV_STATIC_SCRATCH_BYTES = 64 << 20
 
 
 class NkvSegment(Structure):
@@ -163,6 +165,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nkv_attend_workspace_size.argtypes = [POINTER(NkvAttendArgs)]
     lib.nkv_attend.restype = c_int
     lib.nkv_attend.argtypes = [c_void_p, POINTER(NkvAttendArgs), c_void_p, c_size_t]
+    lib.nkv_attend_static.restype = c_int
+    lib.nkv_attend_static.argtypes = [c_void_p, POINTER(NkvAttendArgs)]
     lib.nkv_fast_attend_workspace_size.restype = c_size_t
     lib.nkv_fast_attend_workspace_size.argtypes = [POINTER(NkvFastArgs)]
     lib.nkv_fast_attend.restype = c_int

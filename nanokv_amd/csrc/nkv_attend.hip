@@ -34,6 +34,9 @@
 #include "nkv_common.h"
 #include "nkv_internal.h"
 
+#include <mutex>
+#include <string>
+
 namespace nkv {
 
 constexpr int AT_D = 128;                     // head dim
@@ -902,6 +905,75 @@ extern "C" int nkv_attend(void* stream, const nkv_attend_args* a, void* workspac
         NKV_LAUNCH_CHECK();
     }
     return NKV_OK;
+}
+
+// ------------------------------------------------- allocation-free nkv_attend
+// The scratch of nkv_attend_static: one array per GPU in the code object, so
+// a call allocates nothing.  In host code the name `scratch` is only a
+// host-side stand-in for the symbol; the device address of each GPU's copy
+// comes from hipGetSymbolAddress, once per device (with that device current),
+// and only that address is passed to kernels.
+static __device__ __align__(256) unsigned char scratch[NKV_STATIC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kScratchDevices = 64;
+std::once_flag g_scratch_once[kScratchDevices];
+void* g_scratch_ptr[kScratchDevices];
+hipError_t g_scratch_err[kScratchDevices];
+
+// The scratch address of device `dev` (which must be current).
+int scratch_address(int dev, void** ptr) {
+    NKV_REQUIRE(dev >= 0 && dev < kScratchDevices, NKV_ERR_UNSUPPORTED,
+                "device index beyond the static scratch table");
+    std::call_once(g_scratch_once[dev], [dev]() {
+        void* p = nullptr;
+        g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+        g_scratch_ptr[dev] = p;
+    });
+    if (g_scratch_err[dev] != hipSuccess || !g_scratch_ptr[dev]) {
+        set_error(std::string("nkv_attend_static: hipGetSymbolAddress failed: ") +
+                  hipGetErrorString(g_scratch_err[dev]));
+        return NKV_ERR_HIP;
+    }
+    *ptr = g_scratch_ptr[dev];
+    return NKV_OK;
+}
+
+}  // namespace
+
+extern "C" int nkv_attend_static(void* stream, const nkv_attend_args* a) {
+    clear_error();
+    AttendPlan pl;
+    int rc = plan_attend(a, &pl);
+    if (rc) return rc;
+    int sch;
+    rc = resolve_schedule(a, &sch);
+    if (rc) return rc;
+    size_t need;
+    if (sch == NKV_SCHEDULE_KEY_CHUNKS) {
+        rc = chunk_check(a);
+        if (rc) return rc;
+        need = chunk_workspace_bytes(a);
+    } else {
+        need = workspace_bytes_for(a, pl);
+    }
+    NKV_REQUIRE(need <= (size_t)NKV_STATIC_SCRATCH_BYTES, NKV_ERR_WORKSPACE,
+                "the call needs " + std::to_string(need) + " bytes of scratch; "
+                "nkv_attend_static holds " + std::to_string((size_t)NKV_STATIC_SCRATCH_BYTES) +
+                " (use nkv_attend with a caller workspace)");
+    int dev = 0;
+    NKV_HIP_CHECK(hipGetDevice(&dev));
+    if (stream) {
+        hipDevice_t sdev = 0;
+        NKV_HIP_CHECK(hipStreamGetDevice((hipStream_t)stream, &sdev));
+        NKV_REQUIRE((int)sdev == dev, NKV_ERR_INVALID,
+                    "nkv_attend_static: the stream belongs to another device than the current one");
+    }
+    void* ptr = nullptr;
+    rc = scratch_address(dev, &ptr);
+    if (rc) return rc;
+    return nkv_attend(stream, a, need ? ptr : nullptr, need);
 }
 
 extern "C" int nkv_lse_merge(void* stream, int64_t rows, int D, const uint16_t* a,

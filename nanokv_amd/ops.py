@@ -834,6 +834,37 @@ def attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch
     return out, lse
 
 
+def attend_static(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
+                  key: Optional[Codec] = None, value: Optional[Codec] = None, *,
+                  softmax_scale: Optional[float] = None, return_lse: bool = True,
+                  out: Optional[torch.Tensor] = None, lse: Optional[torch.Tensor] = None,
+                  schedule: str = "auto", hist_rows: Optional[torch.Tensor] = None,
+                  visibility: Optional[Visibility] = None):
+    """nkv_attend_static: attend() without any device allocation by the
+    library (its scratch is a static per-GPU array of
+    NKV_STATIC_SCRATCH_BYTES).  Pass out (and lse) to allocate nothing here
+    either, e.g. under graph capture.  Calls that overlap on one GPU race."""
+    if schedule not in SCHEDULES:
+        raise ValueError(f"schedule must be one of {sorted(SCHEDULES)}")
+    args, out, lse_new, device = _attend_args(q, k_cur, v_cur, key, value, softmax_scale, out,
+                                              return_lse and lse is None)
+    if lse is not None:
+        _contig(lse, torch.float32, "lse")
+        if tuple(lse.shape) != (q.shape[0], q.shape[2], q.shape[1]) or lse.device != device:
+            raise ValueError("lse must be float32 [B, H, Q] on q's device")
+        args.lse = lse.data_ptr()
+    else:
+        lse = lse_new
+    args.schedule = SCHEDULES[schedule]
+    if hist_rows is not None and hist_rows.numel() == 0:
+        raise ValueError("an empty history row list needs attend() (it allocates a stand-in)")
+    hold = _set_hist_rows(args, hist_rows)
+    _set_visibility(args, visibility, int(q.shape[1]))
+    check("nkv_attend_static", lib().nkv_attend_static(_stream(device), byref(args)))
+    del hold
+    return out, lse
+
+
 @dataclass
 class ReaderTensors:
     """Device tensors of one NanoKV-Fast reader group (nkv_reader_group):
