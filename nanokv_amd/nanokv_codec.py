@@ -23,6 +23,7 @@ from __future__ import annotations
 
 import os
 from collections import OrderedDict
+from pathlib import Path
 from typing import Any, Optional
 
 import torch
@@ -42,6 +43,94 @@ _CENTERS: dict = {}
 def enabled() -> bool:
     """MG:17-18."""
     return os.environ.get("MG35_KVCODEC_MODE", "").strip().lower() == "worldplay_method"
+
+
+def _rung() -> str:
+    """The operator rung of this deployment, MG35_WORLDPLAY_RUNG (MG:21-25):
+    pca (no centers), c64, c64_vqat or full (semantic C64 centers)."""
+    value = os.environ.get("MG35_WORLDPLAY_RUNG", "full").strip().lower()
+    if value not in {"pca", "c64", "c64_vqat", "full"}:
+        raise ValueError(f"unsupported MG35_WORLDPLAY_RUNG={value!r}")
+    return value
+
+
+def _center_storage_mode() -> str:
+    """Storage of the per-chunk centers, MG35_KVCODEC_CENTER_STORAGE (MG:35-46):
+    bf16 (the WorldPlay method) or int8_block (an MG-only experiment)."""
+    mode = os.environ.get("MG35_KVCODEC_CENTER_STORAGE", "bf16").strip().lower()
+    if mode not in {"bf16", "int8_block"}:
+        raise ValueError(f"unsupported MG35 center storage mode={mode!r}")
+    return mode
+
+
+def _expected_center_provenance() -> tuple[str, int]:
+    """MG:49-54."""
+    if _rung() == "pca":
+        return "none", 0
+    return _center_storage_mode(), int(os.environ.get("MG35_KVCODEC_CENTER_BLOCK_SIZE", "64"))
+
+
+def _check_center_provenance(payload: dict, *, context: str) -> None:
+    """An operator artifact must record the center storage this runtime uses
+    (MG:56-66)."""
+    expected_storage, expected_block = _expected_center_provenance()
+    if payload.get("center_storage") != expected_storage or int(
+            payload.get("center_block_size", -1)) != expected_block:
+        raise RuntimeError(
+            f"{context} center provenance mismatch: "
+            f"artifact={payload.get('center_storage')}/{payload.get('center_block_size')} "
+            f"runtime={expected_storage}/{expected_block}")
+
+
+def _portable_codec_verified(path: str) -> bool:
+    """A prepacked operator vouched for by NANOKV_PORTABLE_CODEC_SHA256 may
+    carry training-machine paths (nanokv/artifacts.py:8-23)."""
+    expected = os.environ.get("NANOKV_PORTABLE_CODEC_SHA256", "").lower()
+    if not expected:
+        return False
+    if len(expected) != 64 or any(c not in "0123456789abcdef" for c in expected):
+        raise ValueError("NANOKV_PORTABLE_CODEC_SHA256 must be a SHA256 digest")
+    from .codec_native import file_sha256
+    if file_sha256(str(Path(path).resolve())) != expected:
+        raise ValueError(f"Packed codec checksum mismatch: {path}")
+    return True
+
+
+def _same_artifact_dir(recorded, expected, portable: bool) -> bool:
+    """MG:191-198: recorded and expected artifact directories agree (after
+    resolving links), or the packed codec is a verified portable one."""
+    if portable:
+        return True
+    recorded, expected = str(recorded or ""), str(expected or "")
+    if not recorded or not expected:
+        return recorded == expected
+    return Path(recorded).resolve() == Path(expected).resolve()
+
+
+def _check_entry_provenance(kind: str, layer: int, entry: dict, portable: bool) -> None:
+    """The basis / decoder / QAT directories an operator entry was built from
+    must be this deployment's (MG:186-212)."""
+    basis = os.environ.get("MG35_KVCODEC_BASIS_DIR")
+    if basis is None and not portable:
+        raise RuntimeError("MG35_KVCODEC_BASIS_DIR is required to check operator provenance")
+    expected_basis = str(Path(basis).resolve()) if basis else ""
+    rung = _rung()
+    if kind == "k":
+        expected = ""
+        if rung == "full":
+            expected = str(Path(os.environ["MG35_KVCODEC_DECODER_DIR_K"]).resolve()) \
+                if not portable else ""
+        if not _same_artifact_dir(entry.get("basis_dir"), expected_basis, portable) or \
+                not _same_artifact_dir(entry.get("decoder_dir"), expected, portable):
+            raise RuntimeError(f"prepacked K operator provenance mismatch L{layer}")
+    else:
+        expected = ""
+        if rung in {"c64_vqat", "full"}:
+            expected = str(Path(os.environ["MG35_KVCODEC_DECODER_DIR_V"]).resolve()) \
+                if not portable else ""
+        if not _same_artifact_dir(entry.get("basis_dir"), expected_basis, portable) or \
+                not _same_artifact_dir(entry.get("qat_dir"), expected, portable):
+            raise RuntimeError(f"prepacked V operator provenance mismatch L{layer}")
 
 
 def _target_enabled(kind: str) -> bool:
@@ -123,13 +212,24 @@ def register_centers(kind: str, layer: int, centers: Optional[torch.Tensor]) -> 
 
 def preload_operator_weights(device: torch.device, path: Optional[str] = None) -> None:
     """Load every operator of the reference's prepacked file (format
-    mg35_worldplay_operator_int8_v1, MG:257-279) onto `device`."""
+    mg35_worldplay_operator_int8_v1, MG:257-279) onto `device`, after its
+    checks: the file's center provenance and rung must be this runtime's
+    (MG:272-274), and every entry's basis / decoder directories
+    (MG:186-212)."""
     path = path or os.environ.get("MG35_KVCODEC_PREPACKED_OPERATOR_PATH", "").strip()
     if not path:
         raise RuntimeError("formal worldplay_method requires MG35_KVCODEC_PREPACKED_OPERATOR_PATH")
     payload = torch.load(path, map_location="cpu", weights_only=True)
     if payload.get("format") != PREPACKED_FORMAT:
         raise RuntimeError(f"bad prepacked WorldPlay operator: {path}")
+    _check_center_provenance(payload, context="prepacked operator")
+    if payload.get("rung") != _rung():
+        raise RuntimeError(f"operator rung={payload.get('rung')} runtime={_rung()}")
+    portable = _portable_codec_verified(path)
+    for name in sorted(payload["entries"]):
+        kind, layer = name.split(":", 1)
+        _check_entry_provenance(kind, int(layer), payload["entries"][name], portable)
+
     def move(packed):
         return {"storage": "int8", "group_size": int(packed["group_size"]),
                 "qweight": packed["qweight"].to(device=device, dtype=torch.int8).contiguous(),
@@ -189,6 +289,10 @@ def encode_tensor(kind: str, layer: int, value: torch.Tensor) -> dict:
         return {"codec": RAW, "tensor": value.detach()}
     if value.dim() != 3:
         raise ValueError("encode_tensor expects [B, S, HD]")
+    semantic = _rung() != "pca"
+    if semantic and _center_storage_mode() != "bf16":
+        raise NotImplementedError("MG35_KVCODEC_CENTER_STORAGE=int8_block (an MG-only "
+                                  "experiment, not WorldPlay parity) is not built")
     batch, seq, dim = (int(v) for v in value.shape)
     op = _operator(kind, layer, value.device)
     r = int(op["encoder"].shape[0])
@@ -198,7 +302,17 @@ def encode_tensor(kind: str, layer: int, value: torch.Tensor) -> dict:
     rows = value.detach().float().contiguous()
     shared = _CENTERS.get((kind, int(layer)))
     packed, scales, ids_out, tables = [], [], [], []
-    if shared is not None:
+    centers = ids_t = None
+    id_dtype = torch.uint8
+    center_batch_shared = False
+    if not semantic:
+        # the pca rung: the rows themselves are projected (MG:338-342)
+        for b in range(batch):
+            e = ops.encode(rows[b], op["encoder"], mean=op["mean"], group=group,
+                           scale_dtype=sdt, quant_mode=qmode)
+            packed.append(e["packed"])
+            scales.append(e["scales"])
+    elif shared is not None:
         shared = shared.to(value.device)
         id_dtype = ops.id_dtype_for(int(shared.shape[0]))
         for b in range(batch):
@@ -223,6 +337,8 @@ def encode_tensor(kind: str, layer: int, value: torch.Tensor) -> dict:
             ids_out.append(ids)
         centers = fitted
         center_batch_shared = False
+    if ids_out:
+        ids_t = torch.stack(ids_out)
     return {
         "codec": CODEC,
         "kind": kind,
@@ -233,8 +349,8 @@ def encode_tensor(kind: str, layer: int, value: torch.Tensor) -> dict:
         "packed_codes": torch.stack(packed).reshape(-1),
         "scale": torch.stack(scales),
         "centers": centers,
-        "ids": torch.stack(ids_out),
-        "semantic": True,
+        "ids": ids_t,
+        "semantic": semantic,
         "source_dtype": str(value.dtype).replace("torch.", ""),
         "scale_group": group,
         "scale_dtype": "fp16" if sdt == torch.float16 else "bf16",

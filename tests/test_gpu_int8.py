@@ -38,6 +38,15 @@ def test_preload_prepacked_operator_file(dev, tmp_path, monkeypatch):
     monkeypatch.setenv("NANOKV_QUANT_MODE", "fp32")
     sh = synth.Shape("int8", H=2, D=128, N=0, Q=0, Nc=0, rK=128, rV=128, G=32, C=8)
     lay = synth.make_layer(sh, seed=6, with_mean=True)
+    # the artifact directories the entries record must be this deployment's
+    for name in ("basis", "dec_k", "qat_v"):
+        (tmp_path / name).mkdir()
+    monkeypatch.setenv("MG35_KVCODEC_BASIS_DIR", str(tmp_path / "basis"))
+    monkeypatch.setenv("MG35_KVCODEC_DECODER_DIR_K", str(tmp_path / "dec_k"))
+    monkeypatch.setenv("MG35_KVCODEC_DECODER_DIR_V", str(tmp_path / "qat_v"))
+    monkeypatch.delenv("MG35_WORLDPLAY_RUNG", raising=False)
+    monkeypatch.delenv("MG35_KVCODEC_CENTER_STORAGE", raising=False)
+    monkeypatch.delenv("NANOKV_PORTABLE_CODEC_SHA256", raising=False)
     entries = {}
     for kind, enc, dec, mean in (("k", lay.w_enc_k, lay.w_dec_k, lay.mean_k),
                                  ("v", lay.w_enc_v, lay.w_dec_v, lay.mean_v)):
@@ -47,9 +56,13 @@ def test_preload_prepacked_operator_file(dev, tmp_path, monkeypatch):
             "mean": mean.cpu(),
             "encoder": {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in pe.items()},
             "decoder": {k: (v.cpu() if torch.is_tensor(v) else v) for k, v in pd.items()},
+            "basis_dir": str(tmp_path / "basis"),
+            "decoder_dir": str(tmp_path / "dec_k") if kind == "k" else "",
+            "qat_dir": str(tmp_path / "qat_v") if kind == "v" else "",
         }
     path = tmp_path / "codec.pt"
-    torch.save({"format": nc.PREPACKED_FORMAT, "entries": entries}, path)
+    torch.save({"format": nc.PREPACKED_FORMAT, "entries": entries, "rung": "full",
+                "center_storage": "bf16", "center_block_size": 64}, path)
     nc.preload_operator_weights(dev, str(path))
     for kind in ("k", "v"):
         e = entries[f"{kind}:07"]

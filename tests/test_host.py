@@ -102,3 +102,16 @@ def test_protected_tokens_matches_oracle_policy():
     # repeated frame ids form one run (CN:142-145)
     frames = torch.tensor([5, 5, 7, 7, 5, 5])
     assert codec_native.protected_tokens(frames, 1, 0).tolist() == [False] * 4 + [True] * 2
+
+
+def test_codec_history_attention_refuses_short_camera_frames():
+    """The camera's frames must cover the cached rows exactly (complete
+    equal-sized frames, as mg35.py _expand_frames and camera_kernel.py:64
+    require); refused before any device work."""
+    import torch
+    from nanokv_amd import codec_native, nanokv_codec, ops
+    payload = {"codec": nanokv_codec.CODEC, "kind": "k", "layer": 0, "shape": (1, 120, 256)}
+    cam = ops.Camera(torch.zeros(1, 2, 4, 4, 4), torch.tensor([0, 1], dtype=torch.int32), 50)
+    q = torch.zeros(1, 2, 4, 128, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="frames must cover exactly"):
+        codec_native.codec_history_attention(q, payload, payload, camera=cam)
