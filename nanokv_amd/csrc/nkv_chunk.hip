@@ -41,11 +41,14 @@
 
 namespace nkv {
 
-#ifdef NKV_PLAIN_STORES
-#define NT_STORE(v, ptr) (*(ptr) = (v))
-#else
+// Partials are written non-temporally: they are read once, by the combine,
+// after the chunk kernel has written all of them (hundreds of MB at long
+// histories), so caching them only evicts the codec tables and decoded tiles
+// that the running blocks re-read.  Plain stores measured 7 % slower over
+// the whole call at 1,560 queries x 14,040 keys (0.580 vs 0.540 ms), and
+// head-group launches sized for the partials to stay in the MALL slower
+// still (0.547-0.573 ms; at 50,700 keys 1.55 vs 1.02 ms).
 #define NT_STORE(v, ptr) __builtin_nontemporal_store((v), (ptr))
-#endif
 
 constexpr int CK_T = 256;        // keys per chunk
 constexpr int CK_CUR_SPLITS = 3; // most blocks per current-key chunk (query shares)
@@ -88,6 +91,11 @@ struct ChunkParams {
     const int32_t* q_group;
     int n_groups, mask_words;
     int64_t blk_base;   // first work item of this launch (blockIdx.x + blk_base)
+    // staged schedule: tile images [B*H, ntiles, K / V^T image] (history
+    // tiles 0 .. ntiles_hist, two per 256-key chunk, then the current keys'),
+    // qpt query blocks per flash block, `splits` key ranges per query block
+    uint16_t* tiles;
+    int ntiles_hist, ntiles, qpt, splits;
 };
 
 // Codec row of attended history key `key`; rows outside the codec are
@@ -552,6 +560,48 @@ __device__ __forceinline__ void load_current_chunk8(Chunk8Smem& sm, const ChunkP
     }
 }
 
+// Decode the chunk's V (into V^T) and K (into the K tile) for (b, h): every
+// thread of the block takes part; the tile is complete after a barrier.
+template <int DK>
+__device__ __forceinline__ void fill_history8(Chunk8Smem& sm, const ChunkParams& p, int b, int h,
+                                              int64_t tok0, int valid, int t, int wave,
+                                              int lane) {
+    constexpr int KROW = KTile<DK>::ROW;
+    auto publish = [&]() {
+        if (t < CK_T) {
+#pragma unroll
+            for (int cc = 0; cc < 2; ++cc) {
+                const ChunkCodec& cd = p.codec[cc];
+                // keys past the chunk end take key 0's center (finite,
+                // never attended)
+                if (cd.has_centers)
+                    sm.crow[cc][t] = center_row(cd, b, h, p.N,
+                                                history_row(p, tok0 + (t < valid ? t : 0)));
+                if (t < (cc == 0 ? DK : CK_D))
+                    sm.bias[cc][t] =
+                        cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
+            }
+        }
+        __syncthreads();
+    };
+    auto nothing = []() {};
+    uint16_t* vt_scratch = &sm.vt[0][0];
+    uint16_t* k_scratch = &sm.k[0][0];
+    if (p.codec[1].has_centers)
+        decode_codec8<1, true, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
+                                           wave, lane, publish);
+    else
+        decode_codec8<1, false, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
+                                            wave, lane, publish);
+    __syncthreads();
+    if (p.codec[0].has_centers)
+        decode_codec8<0, true, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
+                                         wave, lane, nothing);
+    else
+        decode_codec8<0, false, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
+                                          wave, lane, nothing);
+}
+
 // One wave attends its 32-query blocks (wave + 8 i) to the chunk in LDS,
 // key step by key step: S^T = K Q^T (KS MFMAs), online softmax, O^T += V^T
 // P^T (8 MFMAs).  The next step's K and V fragments are read as soon as the
@@ -693,7 +743,6 @@ __device__ __forceinline__ void attend8(const Chunk8Smem& sm, const ChunkParams&
 // burden the history chunks' decode and attention).
 template <int DK, bool MASK>
 __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
-    constexpr int KROW = KTile<DK>::ROW;
     extern __shared__ __align__(16) unsigned char smem_raw[];
     Chunk8Smem& sm = *reinterpret_cast<Chunk8Smem*>(smem_raw);
     const int t = threadIdx.x, lane = t & 63;
@@ -722,46 +771,500 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
     const int64_t tok0 = (int64_t)(hist ? chunk : chunk - p.nch_hist) * CK_T;
     const int valid = (int)min((int64_t)CK_T, (hist ? p.n_rows : p.Nc) - tok0);
 
-    if (!MASK && hist) {
-        auto publish = [&]() {
-            if (t < CK_T) {
-#pragma unroll
-                for (int cc = 0; cc < 2; ++cc) {
-                    const ChunkCodec& cd = p.codec[cc];
-                    // keys past the chunk end take key 0's center (finite,
-                    // never attended)
-                    if (cd.has_centers)
-                        sm.crow[cc][t] = center_row(cd, b, h, p.N,
-                                                    history_row(p, tok0 + (t < valid ? t : 0)));
-                    if (t < (cc == 0 ? DK : CK_D))
-                        sm.bias[cc][t] =
-                            cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
-                }
-            }
-            __syncthreads();
-        };
-        auto nothing = []() {};
-        uint16_t* vt_scratch = &sm.vt[0][0];
-        uint16_t* k_scratch = &sm.k[0][0];
-        if (p.codec[1].has_centers)
-            decode_codec8<1, true, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
-                                               wave, lane, publish);
-        else
-            decode_codec8<1, false, CK_D, KROW>(sm, vt_scratch, p.codec[1], p, b, h, tok0, valid,
-                                                wave, lane, publish);
-        __syncthreads();
-        if (p.codec[0].has_centers)
-            decode_codec8<0, true, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
-                                             wave, lane, nothing);
-        else
-            decode_codec8<0, false, DK, KROW>(sm, k_scratch, p.codec[0], p, b, h, tok0, valid,
-                                              wave, lane, nothing);
-    } else if (DK == CK_D) {
-        load_current_chunk8(sm, p, b, h, tok0, valid, t);
-    }
+    if (!MASK && hist) fill_history8<DK>(sm, p, b, h, tok0, valid, t, wave, lane);
+    else if (DK == CK_D) load_current_chunk8(sm, p, b, h, tok0, valid, t);
     __syncthreads();
     attend8<DK, MASK>(sm, p, b, h, bh, chunk, wave, lane, (valid + 31) / 32, valid, qb_lo, qb_hi,
                       tok0);
+}
+
+// ===================================================== staged schedule
+// Stage: each 256-key chunk of (b, h) is decoded (history) or loaded
+// (current keys) into LDS exactly as for the key-chunk kernel, then written
+// to the workspace as two 128-key tiles.  A tile is two images, the K rows
+// [128 keys][136] and the V^T rows [128 d][136] (keys in V^T column order),
+// each the exact LDS layout that the attention operand reads expect (8
+// padding elements per row), so the flash kernel copies a tile into LDS with
+// plain 1 KB direct-to-LDS loads.
+// Flash: one block of eight waves per (b*h, query tile, key split).  Wave w
+// attends query block qt * qpt + w to the split's tiles, which stream
+// through two LDS buffers, and keeps O, the running max and the row sum in
+// registers across the whole split; the split's partial goes to the combine
+// as a key-chunk partial (chunk index = split).  Next to the key-chunk
+// schedule this trades the per-chunk partials of every query block (3x the
+// decoded K/V) for one write and a few L2/MALL re-reads of the decoded K/V.
+constexpr int FT_T = 128;                      // keys per tile
+constexpr int FT_ROW = CK_KROW;                // row pitch of both images (elements)
+constexpr int FT_IMG = FT_T * FT_ROW;          // elements per image
+constexpr int FT_TILE = 2 * FT_IMG;            // K image, then V^T image
+constexpr int FT_PIECES = FT_TILE * 2 / 1024;  // 1 KB pieces per tile
+static_assert(FT_TILE * 2 % 1024 == 0, "a tile must be whole 1 KB pieces");
+static_assert(CK_T == 2 * FT_T, "two tiles per chunk");
+
+// s_waitcnt vmcnt(0) lgkmcnt(0): the wave's loads have landed and its LDS
+// reads are done
+__device__ __forceinline__ void wait_loads_and_lds() { __builtin_amdgcn_s_waitcnt(7 << 4); }
+
+__global__ void __launch_bounds__(C8_THREADS, 1) stage8_kernel(ChunkParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    Chunk8Smem& sm = *reinterpret_cast<Chunk8Smem*>(smem_raw);
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int BH = p.B * p.H;
+    const int bh = (int)(blockIdx.x % BH), chunk = (int)(blockIdx.x / BH);
+    const int b = bh / p.H, h = bh % p.H;
+    const int nch_hist = p.ntiles_hist / 2;
+    const bool hist = chunk < nch_hist;
+    const int64_t tok0 = (int64_t)(hist ? chunk : chunk - nch_hist) * CK_T;
+    const int valid = (int)min((int64_t)CK_T, (hist ? p.n_rows : p.Nc) - tok0);
+    if (hist) fill_history8<CK_D>(sm, p, b, h, tok0, valid, t, wave, lane);
+    else load_current_chunk8(sm, p, b, h, tok0, valid, t);
+    __syncthreads();
+    uint16_t* dst = p.tiles + ((int64_t)bh * p.ntiles + 2 * chunk) * FT_TILE;
+    // a second half with no valid key is never attended: not written
+    const int halves = valid > FT_T ? 2 : 1;
+    for (int hh = 0; hh < halves; ++hh) {
+        u32x4* kd = reinterpret_cast<u32x4*>(dst + hh * FT_TILE);
+        u32x4* vd = reinterpret_cast<u32x4*>(dst + hh * FT_TILE + FT_IMG);
+        // K rows 128 hh .. +128 (with their padding) are one run of LDS
+        const u32x4* ks = reinterpret_cast<const u32x4*>(&sm.k[FT_T * hh][0]);
+        for (int i = t; i < FT_IMG / 8; i += C8_THREADS) kd[i] = ks[i];
+        // V^T: the 16 pieces of keys 128 hh .. +128 of each d row
+        for (int i = t; i < CK_D * 16; i += C8_THREADS) {
+            const int d = i >> 4, c = i & 15;
+            vd[d * (FT_ROW / 8) + c] = *reinterpret_cast<const u32x4*>(&sm.vt[d][FT_T * hh + 8 * c]);
+        }
+    }
+}
+
+// ------------------------------------------------------------ decode GEMM
+// The history tiles of launches without read-time RoPE or camera come from
+// dtile_kernel instead of stage8_kernel: one codec of one 256-key chunk of
+// one head per block of four waves (two blocks per CU), each wave 64 keys x
+// 128 columns, so that each decoder fragment read from LDS feeds two MFMAs;
+// the tile images are written straight from the accumulators.
+constexpr int DT_THREADS = 256;  // four waves of 64 keys: one chunk of one head
+constexpr int DT_NBUF = 4;       // decoder-slice ring, three slices ahead
+constexpr int DT_AHEAD = 3;
+struct DTileSmem {
+    // decoder slices; after the GEMM the waves' V center rows, or a current
+    // tile's V^T
+    uint16_t ring[DT_NBUF][CK_D * 64];
+    const uint16_t* crow[CK_T];  // center row of each key (the head's columns)
+    float bias[CK_D];
+};
+static_assert(DT_NBUF * CK_D * 64 >= FT_IMG, "a current tile's V^T fits in the ring");
+static_assert(DT_NBUF * CK_D * 64 >= DT_THREADS / 64 * 64 * CK_D, "V center rows fit in the ring");
+
+// One codec of a history chunk of head bh: wave w owns keys 64 w .. +64 (two
+// 32-key groups kg) and all 128 columns.  A stage (slice s: 64 ranks) is the
+// decoder slice (128 rows x 64 ranks, into the XOR-swizzled LDS ring by
+// direct-to-LDS loads, the wave's share 4 KB) plus the wave's codes and
+// scales of the slice (a register ring), DT_AHEAD stages ahead; stages
+// complete in issue order, so waiting for stage s is one vmcnt bound.  Lane
+// half hf unpacks ranks 32 hf .. +32 of each slice: k-step j takes ranks
+// 8 j + 32 hf .. +8, logical chunk 4 hf + j of decoder row 32 dt + l32.
+template <int CODEC>
+__device__ __forceinline__ void dtile_history(DTileSmem& sm, const ChunkParams& p, int bh,
+                                              int chunk, int wave, int lane) {
+    const ChunkCodec& cd = p.codec[CODEC];
+    const int t = threadIdx.x, hf = lane >> 5, l32 = lane & 31;
+    const int b = bh / p.H, h = bh % p.H;
+    const int64_t tok0 = (int64_t)chunk * CK_T;
+    const int valid = (int)min((int64_t)CK_T, p.n_rows - tok0);
+    const int R = cd.r, KQ = R >> 6, G = cd.group;
+    const bool cent = cd.has_centers, f16 = cd.scale_dtype == NKV_DTYPE_FP16;
+    // keys past the chunk end take key 0's codes and center (finite, never
+    // attended)
+    sm.crow[t] = cent ? center_row(cd, b, h, p.N, history_row(p, tok0 + (t < valid ? t : 0)))
+                      : nullptr;
+    if (t < CK_D) sm.bias[t] = cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
+    const uint8_t* prow[2];
+    const uint16_t* srow[2];
+#pragma unroll
+    for (int kg = 0; kg < 2; ++kg) {
+        const int kw = 64 * wave + 32 * kg + l32;
+        codec_row_ptrs(cd, b, p.N, history_row(p, tok0 + (kw < valid ? kw : 0)), prow[kg], srow[kg]);
+        prow[kg] += 16 * hf;
+    }
+    __syncthreads();
+
+    // piece e of a slice: decoder rows 8 (4 wave + e) .. +8; lane L brings
+    // logical 16-byte chunk (L % 8) ^ ((row >> 1) & 7) of row 8 piece + L / 8
+    const int piece_row = lane >> 3;
+    const uint16_t* wsrc = cd.w + (int64_t)h * cd.w_hs + (int64_t)piece_row * R;
+    auto issue_slice = [&](int s) {
+        uint16_t* dst = sm.ring[s % DT_NBUF];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int piece = 4 * wave + e;
+            const int ch = (lane & 7) ^ ((4 * (piece & 1) + (piece_row >> 1)) & 7);
+            __builtin_amdgcn_global_load_lds(wsrc + (int64_t)8 * piece * R + 64 * s + 8 * ch,
+                                             NKV_LDS(dst + piece * 512), 16, 0, 0);
+        }
+    };
+    constexpr int STAGE = 4 + 2 + 2;  // vm instructions per stage: slice, codes, scales
+    u32x4 pk[DT_AHEAD][2];
+    uint16_t sc[DT_AHEAD][2];
+    auto issue_codes = [&](int s, int i) {
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg) {
+            pk[i][kg] = *reinterpret_cast<const u32x4*>(prow[kg] + 32 * s);
+            sc[i][kg] = srow[kg][(64 * s + 32 * hf) / G];
+        }
+    };
+    int wofs[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wofs[j] = l32 * 64 + 8 * ((4 * hf + j) ^ ((l32 >> 1) & 7));
+    f32x16 acc[2][4];
+#pragma unroll
+    for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) acc[kg][dt] = f32x16{};
+
+#pragma unroll
+    for (int i = 0; i < DT_AHEAD; ++i)
+        if (i < KQ) {
+            issue_slice(i);
+            issue_codes(i, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    for (int s0 = 0; s0 < KQ; s0 += DT_AHEAD) {
+#pragma unroll
+        for (int i = 0; i < DT_AHEAD; ++i) {
+            const int s = s0 + i;
+            if (s >= KQ) break;
+            static_assert(DT_AHEAD == 3, "the wait bounds below assume three stages ahead");
+            const int later = min(KQ - 1 - s, DT_AHEAD - 1);
+            if (later >= 2) wait_vmcnt<2 * STAGE>();
+            else if (later == 1) wait_vmcnt<STAGE>();
+            else wait_vmcnt<0>();
+            __builtin_amdgcn_s_barrier();
+            if (s + DT_AHEAD < KQ) issue_slice(s + DT_AHEAD);
+            __builtin_amdgcn_sched_barrier(0);
+            const uint16_t* wb = sm.ring[s % DT_NBUF];
+            float scl[2], ns7[2];
+#pragma unroll
+            for (int kg = 0; kg < 2; ++kg) {
+                scl[kg] = f16 ? f16_bits_to_f32(sc[i][kg]) : bf16_bits_to_f32(sc[i][kg]);
+                ns7[kg] = -7.0f * scl[kg];
+            }
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                bf16x8 w[4], z[2];
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) w[dt] = lds_b128(wb + 32 * dt * 64 + wofs[j]);
+#pragma unroll
+                for (int kg = 0; kg < 2; ++kg) z[kg] = unpack8(pk[i][kg][j], scl[kg], ns7[kg]);
+#pragma unroll
+                for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt)
+                        acc[kg][dt] = CODEC == 0 ? mfma32(w[dt], z[kg], acc[kg][dt])
+                                                 : mfma32(z[kg], w[dt], acc[kg][dt]);
+            }
+            __builtin_amdgcn_sched_barrier(0);
+            if (s + DT_AHEAD < KQ) issue_codes(s + DT_AHEAD, i);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    }
+    uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + 2 * chunk + (wave >> 1)) * FT_TILE;
+    if (CODEC == 0) {
+        // acc[kg][dt] element i: d = 32 dt + 8 (i/4) + 4 hf + i%4 of key
+        // 64 wave + 32 kg + l32; K = bf16(bf16(acc + bias) + center).  Every
+        // center value is requested before the first store (a store may
+        // alias them, so no load would pass it).
+        u32x2 cv[2][16];
+        if (cent) {
+#pragma unroll
+            for (int kg = 0; kg < 2; ++kg) {
+                const uint16_t* cr = sm.crow[64 * wave + 32 * kg + l32];
+#pragma unroll
+                for (int n = 0; n < 16; ++n)
+                    cv[kg][n] = *reinterpret_cast<const u32x2*>(cr + 32 * (n >> 2) + 8 * (n & 3) + 4 * hf);
+            }
+        }
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg) {
+            const int kr = 64 * (wave & 1) + 32 * kg + l32;
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const int d = 32 * dt + 8 * g + 4 * hf;
+                    const f32x4 bs = *reinterpret_cast<const f32x4*>(&sm.bias[d]);
+                    float a[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) a[e] = bf16_round(acc[kg][dt][4 * g + e] + bs[e]);
+                    if (cent) {
+                        const u32x2 c2 = cv[kg][4 * dt + g];
+                        a[0] += __uint_as_float(c2[0] << 16);
+                        a[1] += __uint_as_float(c2[0] & 0xffff0000u);
+                        a[2] += __uint_as_float(c2[1] << 16);
+                        a[3] += __uint_as_float(c2[1] & 0xffff0000u);
+                    }
+                    *reinterpret_cast<u32x2*>(img + kr * FT_ROW + d) =
+                        u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+                }
+        }
+    } else {
+        // acc[kg][dt] element i: key 64 wave + 32 kg + 8 (i/4) + 4 hf + i%4,
+        // d = 32 dt + l32; V = bf16(bf16(acc + bias) + center).  The centers
+        // of keys t0 .. t0+3 at column d come from one transposing LDS read
+        // (ds_read_b64_tr_b16) of the group's center rows: within a group of
+        // 16 lanes, lane j receives element j % 4 of the 8-byte rows that
+        // lanes j / 4, j / 4 + 4, j / 4 + 8, j / 4 + 12 address, so lane
+        // x = a + 4k addresses key t0 + k at columns dbase + 4a .. +4 and
+        // lane j gets the four keys at column dbase + j.  Both groups' rows
+        // are staged (every wave is done with the ring) before any store, so
+        // that waiting for them does not wait for stores.
+        uint16_t* vcen = &sm.ring[0][0] + wave * 64 * CK_D;
+        __syncthreads();
+        if (cent) {
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const int k = 4 * e + (lane >> 4);
+                __builtin_amdgcn_global_load_lds(sm.crow[64 * wave + k] + 8 * (lane & 15),
+                                                 NKV_LDS(vcen + 4 * e * CK_D), 16, 0, 0);
+            }
+            wait_vmcnt<0>();
+        }
+        const int tr_x = lane & 15;
+        const int tr_off = (tr_x >> 2) * CK_D + 4 * (tr_x & 3) + 16 * ((lane >> 4) & 1);
+        float bs[4];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) bs[dt] = sm.bias[32 * dt + l32];
+#pragma unroll
+        for (int kg = 0; kg < 2; ++kg)
+#pragma unroll
+            for (int g = 0; g < 4; ++g) {
+                const int t0 = 32 * kg + 8 * g + 4 * hf;
+                const int col = vt_col(64 * (wave & 1) + t0);
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    short4v cen = {};
+                    if (cent)
+                        cen = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                            (__attribute__((address_space(3))) short4v*)(vcen + t0 * CK_D + 32 * dt + tr_off));
+                    float v[4];
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) {
+                        const float a = bf16_round(acc[kg][dt][4 * g + e] + bs[dt]);
+                        v[e] = cent ? a + __uint_as_float((uint32_t)(uint16_t)cen[e] << 16) : a;
+                    }
+                    *reinterpret_cast<u32x2*>(img + FT_IMG + (32 * dt + l32) * FT_ROW + col) =
+                        u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                }
+            }
+    }
+}
+
+// A current-key tile: thread t brings keys 4 (t % 32) .. +4, columns
+// 16 (t / 32) .. +16 of K and V (every load before any store); K rows go
+// straight into the image, V through LDS into V^T column order (one 8-byte
+// write of four keys per column).  Keys past the end are zero.
+__device__ __forceinline__ void dtile_current(DTileSmem& sm, const ChunkParams& p, int bh, int ct,
+                                              int t) {
+    const int b = bh / p.H, h = bh % p.H;
+    const int64_t key0 = (int64_t)ct * FT_T;
+    const int valid = (int)min((int64_t)FT_T, p.Nc - key0);
+    uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + p.ntiles_hist + ct) * FT_TILE;
+    uint16_t* vt = &sm.ring[0][0];  // [128 d][FT_ROW]
+    const int k0 = 4 * (t & 31), d0 = 16 * (t >> 5);
+    u32x4 kv[4][2], vv[4][2];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+        const bool ok = k0 + e < valid;
+        const int64_t tok = key0 + (ok ? k0 + e : 0);
+        const uint16_t* ks = p.k_cur + (int64_t)b * p.k_sb + tok * p.k_st + (int64_t)h * p.k_sh + d0;
+        const uint16_t* vs = p.v_cur + (int64_t)b * p.v_sb + tok * p.v_st + (int64_t)h * p.v_sh + d0;
+#pragma unroll
+        for (int x = 0; x < 2; ++x) {
+            kv[e][x] = ok ? *reinterpret_cast<const u32x4*>(ks + 8 * x) : u32x4{0, 0, 0, 0};
+            vv[e][x] = ok ? *reinterpret_cast<const u32x4*>(vs + 8 * x) : u32x4{0, 0, 0, 0};
+        }
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+#pragma unroll
+        for (int x = 0; x < 2; ++x)
+            *reinterpret_cast<u32x4*>(img + (k0 + e) * FT_ROW + d0 + 8 * x) = kv[e][x];
+    const int col = vt_col(k0);
+#pragma unroll
+    for (int dd = 0; dd < 16; ++dd) {
+        const int x = dd >> 3, w = (dd & 7) >> 1, sh = 16 * (dd & 1);
+        auto val = [&](int e) { return (vv[e][x][w] >> sh) & 0xffffu; };
+        *reinterpret_cast<u32x2*>(vt + (d0 + dd) * FT_ROW + col) =
+            u32x2{val(0) | (val(1) << 16), val(2) | (val(3) << 16)};
+    }
+    __syncthreads();
+    for (int i = t; i < CK_D * 16; i += DT_THREADS) {
+        const int d = i >> 4, c = i & 15;
+        *reinterpret_cast<u32x4*>(img + FT_IMG + d * FT_ROW + 8 * c) =
+            *reinterpret_cast<const u32x4*>(vt + d * FT_ROW + 8 * c);
+    }
+}
+
+// Work items: (b*h, history chunk, codec) with the codec fastest and b*h
+// next, so that one head's decoder rows and centers of one codec stay on one
+// XCD (blockIdx % 8) when B*H is a multiple of 4; then the current tiles.
+__global__ void __launch_bounds__(DT_THREADS, 2) dtile_kernel(ChunkParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    DTileSmem& sm = *reinterpret_cast<DTileSmem*>(smem_raw);
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int BH = p.B * p.H;
+    const int64_t nh = (int64_t)BH * p.ntiles_hist;  // two codecs per history chunk
+    const int64_t item = blockIdx.x;
+    if (item < nh) {
+        const int64_t r = item >> 1;
+        const int bh = (int)(r % BH), chunk = (int)(r / BH);
+        if (item & 1) dtile_history<1>(sm, p, bh, chunk, wave, lane);
+        else dtile_history<0>(sm, p, bh, chunk, wave, lane);
+    } else {
+        const int64_t c = item - nh;
+        dtile_current(sm, p, (int)(c % BH), (int)(c / BH), t);
+    }
+}
+
+struct FlashSmem {
+    uint16_t buf[2][FT_TILE];
+};
+static_assert(sizeof(FlashSmem) <= 160 * 1024, "LDS budget");
+
+// MASK: the current keys are attended under p.cur_mask (the history tiles
+// never are).
+template <bool MASK>
+__global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    FlashSmem& sm = *reinterpret_cast<FlashSmem*>(smem_raw);
+    int lane = threadIdx.x & 63;
+    asm volatile("" : "+v"(lane));
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    // (batch, head) fastest: with B*H a multiple of 8 every block of a head
+    // runs on one XCD (blockIdx % 8), whose L2 then serves its tiles to the
+    // head's other query tiles
+    const int BH = p.B * p.H;
+    const int bh = (int)(blockIdx.x % BH), rest = (int)(blockIdx.x / BH);
+    const int split = rest % p.splits, qt = rest / p.splits;
+    const int b = bh / p.H, h = bh % p.H;
+    const int t0 = (int)((int64_t)split * p.ntiles / p.splits);
+    const int t1 = (int)((int64_t)(split + 1) * p.ntiles / p.splits);
+    const int qb = qt * p.qpt + wave;
+    const bool active = wave < p.qpt && qb < p.qblocks;
+    const uint16_t* src = p.tiles + (int64_t)bh * p.ntiles * FT_TILE + 8 * lane;
+    auto issue = [&](int tile) {
+        const uint16_t* s = src + (int64_t)tile * FT_TILE;
+        uint16_t* d = sm.buf[tile & 1];
+        for (int e = wave; e < FT_PIECES; e += C8_WAVES)
+            __builtin_amdgcn_global_load_lds(s + 512 * e, NKV_LDS(d + 512 * e), 16, 0, 0);
+    };
+    const int hf = lane >> 5, l32 = lane & 31;
+    const float c = p.scale_log2;
+    using W = DWalk<CK_D>;
+    constexpr int KS = W::KSTEPS;
+    bf16x8 qf[KS], kf[KS], vf[8];
+    const int64_t q0 = (int64_t)qb * 32;
+    if (active) load_q_block<CK_D>(qf, p, b, h, q0, q0, lane);
+    if (t0 < t1) issue(t0);
+    uint32_t koff = l32 * FT_ROW + W::HALF * hf, voff = FT_IMG + l32 * FT_ROW + 8 * hf;
+    asm volatile("" : "+v"(koff));
+    asm volatile("" : "+v"(voff));
+    const uint32_t* mbase = nullptr;
+    if (MASK && active) {
+        const int64_t qi = min(q0 + l32, p.Q - 1);
+        const int g = p.q_group ? min(max(p.q_group[qi], 0), p.n_groups - 1) : 0;
+        mbase = p.cur_mask + (int64_t)g * p.mask_words;
+    }
+    f32x16 o[4];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) o[db] = f32x16{};
+    float m = -INFINITY, l = 0.0f;
+    for (int tile = t0; tile < t1; ++tile) {
+        wait_loads_and_lds();
+        __builtin_amdgcn_s_barrier();
+        // the other buffer's last readers have passed the barrier
+        if (tile + 1 < t1) issue(tile + 1);
+        const bool cur = tile >= p.ntiles_hist;
+        const int64_t key0 = (int64_t)(cur ? tile - p.ntiles_hist : tile) * FT_T;
+        const int valid = (int)min((int64_t)FT_T, (cur ? p.Nc : p.n_rows) - key0);
+        if (!active || valid <= 0) continue;
+        const uint16_t* kbase = sm.buf[tile & 1] + koff;
+        const uint16_t* vbase = sm.buf[tile & 1] + voff;
+        auto lds_k = [&](int j, int kk) { return lds_b128(kbase + 32 * j * FT_ROW + W::block(kk)); };
+        auto lds_v = [&](int j, int t) {
+            return lds_b128(vbase + 32 * (t & 3) * FT_ROW + 32 * j + 16 * (t >> 2));
+        };
+        const uint32_t* mrow = MASK && cur ? mbase + (key0 >> 5) : nullptr;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) kf[kk] = lds_k(0, kk);
+#pragma unroll
+        for (int t = 0; t < 8; ++t) vf[t] = lds_v(0, t);
+        const int nsub = (valid + 31) >> 5;
+        for (int j = 0; j < nsub; ++j) {
+            __builtin_amdgcn_s_setprio(1);
+            f32x16 s = mfma32(kf[0], qf[0], f32x16{});
+#pragma unroll
+            for (int kk = 1; kk < KS; ++kk) s = mfma32(kf[kk], qf[kk], s);
+            __builtin_amdgcn_s_setprio(0);
+            if (j + 1 < nsub) {
+#pragma unroll
+                for (int kk = 0; kk < KS; ++kk) kf[kk] = lds_k(j + 1, kk);
+            }
+            if (32 * j + 32 > valid) {
+                const int vj = valid - 32 * j;
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (8 * (i >> 2) + 4 * hf + (i & 3) >= vj) s[i] = -INFINITY;
+            }
+            if (MASK && cur) {
+                const uint32_t bits = mrow[j];
+#pragma unroll
+                for (int i = 0; i < 16; ++i)
+                    if (!((bits >> (8 * (i >> 2) + 4 * hf + (i & 3))) & 1u)) s[i] = -INFINITY;
+            }
+            float tm = fmaxf(s[0], s[1]);
+#pragma unroll
+            for (int i = 2; i < 16; ++i) tm = fmaxf(tm, s[i]);
+            tm = halfwave_max(tm) * c;
+            const bool up = tm > m + CK_TAU;
+            const float mn = up ? tm : m;
+            // m = -inf (nothing seen yet) gives alpha 0 on zero sums
+            const float alpha = up ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+            m = mn;
+            const float mref = MASK && mn == -INFINITY ? 0.0f : mn;
+            uint32_t pw[8];
+            float lsum = 0.0f;
+#pragma unroll
+            for (int k = 0; k < 8; ++k) {
+                pw[k] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(s[2 * k], c, -mref)),
+                                    __builtin_amdgcn_exp2f(fmaf(s[2 * k + 1], c, -mref)));
+                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[k]),
+                                                       __builtin_bit_cast(bf16x2, 0x3F803F80u),
+                                                       lsum, false);
+            }
+            l = l * alpha + lsum;
+            const bf16x8 p0 = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
+            const bf16x8 p1 = as_bf16x8(u32x4{pw[4], pw[5], pw[6], pw[7]});
+            __builtin_amdgcn_s_setprio(1);
+            if (__any(up)) {
+#pragma unroll
+                for (int db = 0; db < 4; ++db)
+#pragma unroll
+                    for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+            }
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[db], p0, o[db]);
+#pragma unroll
+            for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[4 + db], p1, o[db]);
+            __builtin_amdgcn_s_setprio(0);
+            if (j + 1 < nsub) {
+#pragma unroll
+                for (int t = 0; t < 8; ++t) vf[t] = lds_v(j + 1, t);
+            }
+        }
+    }
+    if (active) store_partial(p, bh, split, q0, o, m, halfwave_sum(l), lane);
 }
 
 // Merge the chunk partials of every (b, h, q).  One wave owns one 32-query
@@ -962,9 +1465,113 @@ void launch_dk(const ChunkParams& p, int64_t blocks, hipStream_t s, int* rc) {
     }
 }
 
+template <typename K>
+int set_smem(K* kernel, size_t smem) {
+    const hipError_t e = hipFuncSetAttribute((const void*)kernel,
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess) {
+        set_error(std::string("chunk_launch: hipFuncSetAttribute failed: ") + hipGetErrorString(e));
+        return NKV_ERR_HIP;
+    }
+    return NKV_OK;
+}
+
+// ---------------------------------------------------------- staged (host)
+constexpr int FT_CUS = 256;          // compute units of an MI355X
+// The staged schedule from 32 query blocks up: below, the key-chunk
+// schedule's per-chunk partials cost less than writing the decoded tiles
+// (measured: 49 blocks, 1,560 queries over 14,040 keys, favour staging; 25
+// blocks, 780 queries over 50,700 keys, do not).
+constexpr int FT_MIN_QBLOCKS = 32;
+
+struct FlashPlan {
+    int qpt, qtiles, splits, ntiles_hist, ntiles;
+};
+
+// Query tiles of at most eight blocks, balanced (49 blocks: 7 tiles of 7);
+// key splits: the fewest that bring the grid closest to whole rounds of the
+// CUs (rounds per unit of work), each split at least 4 tiles.
+FlashPlan flash_plan(const ChunkLaunchDesc& d) {
+    FlashPlan f{};
+    const int64_t qblocks = cdiv(d.Q, 32);
+    f.qtiles = (int)cdiv(qblocks, C8_WAVES);
+    f.qpt = (int)cdiv(qblocks, f.qtiles);
+    f.ntiles_hist = 2 * (int)chunk_count(d.n_rows);
+    f.ntiles = f.ntiles_hist + 2 * (int)chunk_count(d.Nc);
+    const int64_t base = (int64_t)d.B * d.H * f.qtiles;
+    f.splits = 1;
+    double best = 1e30;
+    for (int sp = 1; sp <= 16 && 4 * sp <= std::max(f.ntiles, 4); ++sp) {
+        const double cost = (double)cdiv(base * sp, FT_CUS) / sp;
+        if (cost < best - 1e-9) {
+            best = cost;
+            f.splits = sp;
+        }
+    }
+    return f;
+}
+
+bool use_staged(const ChunkLaunchDesc& d) {
+    return d.dk == CK_D && cdiv(d.Q, 32) >= FT_MIN_QBLOCKS && d.n_rows + d.Nc > 0;
+}
+
+size_t staged_tile_bytes(const ChunkLaunchDesc& d, const FlashPlan& f) {
+    return (size_t)d.B * d.H * f.ntiles * FT_TILE * sizeof(uint16_t);
+}
+
+// History tiles from the decode GEMM (dtile_kernel); with read-time RoPE or
+// camera, from stage8_kernel's in-LDS decode.
+bool staged_gemm(const ChunkLaunchDesc& d) { return d.n_rows > 0 && !rope_on(d.rope) && !d.cam.mats; }
+
+size_t staged_workspace(const ChunkLaunchDesc& d) {
+    const FlashPlan f = flash_plan(d);
+    const size_t rows = (size_t)d.B * d.H * f.splits * cdiv(d.Q, 32) * 32;
+    return staged_tile_bytes(d, f) + rows * CK_D * sizeof(uint16_t) + rows * 2 * sizeof(float);
+}
+
+// Stage, flash, combine; p holds everything but the staged fields.
+int staged_launch(hipStream_t s, const ChunkLaunchDesc& d, ChunkParams p, void* workspace) {
+    const FlashPlan f = flash_plan(d);
+    const int64_t BH = (int64_t)d.B * d.H;
+    p.tiles = reinterpret_cast<uint16_t*>(workspace);
+    p.ntiles_hist = f.ntiles_hist;
+    p.ntiles = f.ntiles;
+    p.qpt = f.qpt;
+    p.splits = f.splits;
+    // the partials of the splits, in the key-chunk layout with chunk = split
+    p.nch_hist = 0;
+    p.nch_total = f.splits;
+    const size_t rows = (size_t)BH * f.splits * p.qblocks * 32;
+    p.part_o = reinterpret_cast<uint16_t*>(reinterpret_cast<unsigned char*>(workspace) +
+                                           staged_tile_bytes(d, f));
+    p.part_ml = reinterpret_cast<float*>(p.part_o + rows * CK_D);
+    const bool gemm = staged_gemm(d);
+    int rc = gemm ? set_smem(dtile_kernel, sizeof(DTileSmem)) : set_smem(stage8_kernel, sizeof(Chunk8Smem));
+    if (!rc) rc = p.cur_mask ? set_smem(flash8_kernel<true>, sizeof(FlashSmem))
+                             : set_smem(flash8_kernel<false>, sizeof(FlashSmem));
+    if (rc) return rc;
+    if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
+    if (gemm) {
+        const int64_t items = BH * f.ntiles_hist + BH * (f.ntiles - f.ntiles_hist);
+        dtile_kernel<<<dim3((unsigned)items), DT_THREADS, sizeof(DTileSmem), s>>>(p);
+    } else {
+        stage8_kernel<<<dim3((unsigned)(BH * f.ntiles / 2)), C8_THREADS, sizeof(Chunk8Smem), s>>>(p);
+    }
+    NKV_LAUNCH_CHECK();
+    const dim3 grid((unsigned)(BH * f.qtiles * f.splits));
+    if (p.cur_mask) flash8_kernel<true><<<grid, C8_THREADS, sizeof(FlashSmem), s>>>(p);
+    else flash8_kernel<false><<<grid, C8_THREADS, sizeof(FlashSmem), s>>>(p);
+    NKV_LAUNCH_CHECK();
+    if (d.ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_end, s));
+    chunk_combine_kernel<<<dim3((unsigned)cdiv(BH * p.qblocks, CB_WAVES)), 64 * CB_WAVES, 0, s>>>(p);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
 }  // namespace
 
 size_t chunk_launch_workspace(const ChunkLaunchDesc& d) {
+    if (use_staged(d)) return staged_workspace(d);
     const int64_t nc = chunk_count(d.n_rows) + chunk_count(d.Nc);
     const size_t blocks = (size_t)d.B * d.H * nc * cdiv(d.Q, 32);
     return blocks * 32 * CK_D * sizeof(uint16_t) + blocks * 32 * 2 * sizeof(float);
@@ -1036,6 +1643,9 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.q_group = d.q_group;
     p.n_groups = d.n_groups;
     p.mask_words = d.mask_words;
+    p.tiles = nullptr;
+    p.ntiles_hist = p.ntiles = p.qpt = p.splits = 0;
+    if (use_staged(d)) return staged_launch(s, d, p, workspace);
 
     const int64_t hist_blocks = (int64_t)d.B * d.H * p.nch_hist;
     const int64_t cur_blocks = (int64_t)d.B * d.H * (p.nch_total - p.nch_hist) * p.cur_splits;
