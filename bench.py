@@ -10,10 +10,14 @@ resident in HBM before the timed region starts.
 Prints ONE JSON line:
   value         algorithmic TFLOP/s over the timed steps (decode GEMM
                 counted once per history token)
-  roofline      the fused kernel's achieved TFLOP/s from HIP events recorded
-                around each launch, against the 2.5 PFLOP/s dense bf16 peak
+  roofline      the attention kernel's achieved TFLOP/s from HIP events
+                recorded around each launch, against the 2.5 PFLOP/s dense
+                bf16 peak: at 1,024+ queries the staged schedule's flash
+                kernel (attention flops; the history decode before it is a
+                kernel of its own), else the fused key-chunk kernel (all flops)
   cpu_baseline  the CPU oracle's decode-then-attend (fp32 numpy/BLAS) on a
-                bounded head sample of the same workload, scaled to TFLOP/s
+                bounded head sample of the same workload, scaled to TFLOP/s,
+                with the host CPU (lscpu) and config 0 run in full
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--config 1|2|3|4]
 (config 4 prints its own line: rollout step latency and peak HBM, compressed
@@ -88,6 +92,71 @@ def build_inputs(shape, device, seed=0):
     return layer, codecs, q, kc, vc
 
 
+def cpu_info() -> dict:
+    """The host CPU as lscpu reports it (model name, logical CPUs, threads per core)."""
+    import subprocess
+    info = {"model": None, "logical_cpus": os.cpu_count(), "threads_per_core": None}
+    try:
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "Model name":
+                info["model"] = val
+            elif key == "CPU(s)" and val.isdigit():
+                info["logical_cpus"] = int(val)
+            elif key == "Thread(s) per core" and val.isdigit():
+                info["threads_per_core"] = int(val)
+    except Exception:
+        pass
+    if info["model"] is None:
+        try:
+            for line in open("/proc/cpuinfo"):
+                if line.startswith("model name"):
+                    info["model"] = line.split(":", 1)[1].strip()
+                    break
+        except OSError:
+            pass
+    return info
+
+
+def _oracle_codecs(shape, layer, codecs):
+    import numpy as np
+
+    def u16(t):
+        return t.detach().contiguous().cpu().view(__import__("torch").int16).numpy().view(np.uint16)
+
+    out = []
+    for cd, dec, cent in ((codecs[0], layer.w_dec_k, layer.centers_k),
+                          (codecs[1], layer.w_dec_v, layer.centers_v)):
+        out.append({"packed": cd.packed[0].cpu().numpy(), "scales": u16(cd.scales[0]),
+                    "w_dec_bf16": u16(dec), "group": shape.G, "scale_dtype": "fp16",
+                    "ids": cd.ids[0].cpu().numpy().astype(np.int64), "centers_bf16": u16(cent)})
+    return out, u16
+
+
+def cpu_config0(device) -> dict:
+    """Config 0 (H=8, D=64, 2,048 history tokens, r=64) in full on the CPU: the
+    oracle's decode-then-attend of every head in fp32, median of 3."""
+    import numpy as np
+    import oracle.oracle as orc
+    from nanokv_amd import synth
+    shape = synth.CONFIGS[0]
+    layer, codecs, q, kc, vc = build_inputs(shape, device)
+    (key, val), u16 = _oracle_codecs(shape, layer, codecs)
+    qn, kn, vn = u16(q[0]), u16(kc[0]), u16(vc[0])
+    times = []
+    for _ in range(4):
+        t0 = time.perf_counter()
+        orc.decode_attend(qn, kn, vn, key, val, shape.D ** -0.5, D=shape.D, dtype=np.float32)
+        times.append(time.perf_counter() - t0)
+    t = sorted(times[1:])[1]
+    flops = shape.flops()["total"]
+    return {"value": round(flops / t / 1e12, 5), "unit": "TFLOP/s", "ms": round(t * 1e3, 2),
+            "sample": f"config 0 in full ({shape.name}), all {shape.H} heads, median of 3 after "
+                      "one warm-up"}
+
+
 def cpu_baseline(shape, layer, codecs, q, kc, vc, budget_s: float) -> dict:
     """Time the CPU oracle (decode-then-attend, fp32 BLAS) on a head sample."""
     import numpy as np
@@ -97,18 +166,7 @@ def cpu_baseline(shape, layer, codecs, q, kc, vc, budget_s: float) -> dict:
         threads = max([p.get("num_threads", 1) for p in threadpool_info()] or [1])
     except Exception:
         threads = os.cpu_count() or 1
-
-    def u16(t):
-        return t.detach().contiguous().cpu().view(__import__("torch").int16).numpy().view(np.uint16)
-
-    key = {"packed": codecs[0].packed[0].cpu().numpy(), "scales": u16(codecs[0].scales[0]),
-           "w_dec_bf16": u16(layer.w_dec_k), "group": shape.G, "scale_dtype": "fp16",
-           "ids": codecs[0].ids[0].cpu().numpy().astype(np.int64),
-           "centers_bf16": u16(layer.centers_k)}
-    val = {"packed": codecs[1].packed[0].cpu().numpy(), "scales": u16(codecs[1].scales[0]),
-           "w_dec_bf16": u16(layer.w_dec_v), "group": shape.G, "scale_dtype": "fp16",
-           "ids": codecs[1].ids[0].cpu().numpy().astype(np.int64),
-           "centers_bf16": u16(layer.centers_v)}
+    (key, val), u16 = _oracle_codecs(shape, layer, codecs)
     qn, kn, vn = u16(q[0]), u16(kc[0]), u16(vc[0])
     orc.decode_attend(qn, kn, vn, key, val, shape.D ** -0.5, heads=[0], D=shape.D,
                       dtype=np.float32)  # warm-up (BLAS threads, page-in)
@@ -124,7 +182,7 @@ def cpu_baseline(shape, layer, codecs, q, kc, vc, budget_s: float) -> dict:
     full_s = per_head * shape.H
     flops = shape.flops()["total"]
     return {"value": round(flops / full_s / 1e12, 4), "unit": "TFLOP/s", "cores": int(threads),
-            "kind": "port",
+            "kind": "port", "cpu": cpu_info(),
             "sample": (f"oracle decode-then-attend (fp32 numpy/BLAS) of {heads_done} of {shape.H} "
                        f"heads at the full config shape, {elapsed:.1f} s, scaled by "
                        f"{shape.H}/{heads_done} heads; ms_per_layer={full_s * 1e3:.1f}")}
@@ -432,14 +490,21 @@ def main():
     fl = shape.fast_flops(int(prot_rows.numel())) if fast else shape.flops()
     ms_per_step = wall * 1e3 / args.steps
     value = fl["total"] / (ms_per_step * 1e-3) / 1e12
-    achieved = fl["total"] / (kavg_ms * 1e-3) / 1e12
     # the schedule nkv_attend resolves AUTO to (key chunks above one 256-query tile)
     schedule = args.schedule
     if schedule == "auto":
         schedule = "key_chunks" if shape.Q > 256 else "query_tiles"
     kernel = "nkv::chunk_kernel" if schedule == "key_chunks" else "nkv::attend_kernel"
+    # the key-chunk path stages from 32 query blocks up: the history is decoded
+    # once into tiles (dtile_kernel), then the flash kernel -- the one the
+    # events bracket -- does the attention flops
+    kflops = fl["total"]
+    if schedule == "key_chunks" and -(-shape.Q // 32) >= 32 and not fast:
+        schedule, kernel = "staged", "nkv::flash8_kernel"
+        kflops = fl["attention_history"] + fl["attention_current"]
     if fast:
         schedule, kernel = "key_chunks", "nkv_fast_attend (every launch of the call)"
+    achieved = kflops / (kavg_ms * 1e-3) / 1e12
     traffic = None
     if TRAFFIC_FILE.exists():
         try:
@@ -473,15 +538,16 @@ def main():
         | ({"camera": "history keys and values times P^-1 at read, frames of 1560 tokens"}
            if camera else {}),
         "history_tokens_per_ms": round(shape.N / ms_per_step, 1),
-        "coeff_stream_GBps": round(shape.coeff_stream_bytes() / (kavg_ms * 1e-3) / 1e9, 2),
         "algorithmic_flops": fl,
         "roofline": {"bound": "mfma", "kernel": kernel, "schedule": schedule,
+                     "kernel_flops": kflops,
                      "achieved": round(achieved, 3), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic, "kernel_ms_avg": round(kavg_ms, 4)},
     }
     if not args.no_cpu_baseline and not fast:
         result["cpu_baseline"] = cpu_baseline(shape, layer, codecs, q, kc, vc, args.cpu_seconds)
+        result["cpu_baseline"]["config0"] = cpu_config0(q.device)
     print(json.dumps(result), flush=True)
 
 

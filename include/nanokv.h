@@ -396,8 +396,10 @@ typedef struct nkv_attend_args {
     int64_t o_sb, o_st, o_sh;
     float* lse;
     /* Optional instrumentation: hipEvent_t handles (as void*) recorded on
-     * `stream` immediately before and after the main fused kernel (not the
-     * split-combine kernel), for per-kernel timing.  NULL = not recorded. */
+     * `stream` immediately before and after the main attention kernel (the
+     * fused kernel; with the staged schedule, the flash kernel after the
+     * history decode; never the split-combine), for per-kernel timing.
+     * NULL = not recorded. */
     void* ev_kernel_begin;
     void* ev_kernel_end;
     const nkv_rope* rope;

@@ -644,13 +644,18 @@ __global__ void __launch_bounds__(256) combine_kernel(AttendParams p) {
 }
 
 // ---- LSE merge of two partitions (CN/core.py:33-42; fast_kernels.py:30-54).
-// One thread per row so that lse_out may alias lse_a or lse_b.
-__global__ void __launch_bounds__(256) lse_merge_kernel(int64_t rows, int D, const uint16_t* a,
-                                                        int64_t as, const float* la,
-                                                        const uint16_t* bb, int64_t bs,
-                                                        const float* lb, uint16_t* out,
-                                                        int64_t os, float* lo) {
-    const int64_t row = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+// One wave per row, its lanes striding over d, so that neighbouring lanes
+// touch neighbouring elements.  Every lane reads the row's two LSEs before
+// lane 0 writes the merged one, so lse_out may alias lse_a or lse_b.
+constexpr int LM_WAVES = 4;
+__global__ void __launch_bounds__(64 * LM_WAVES) lse_merge_kernel(int64_t rows, int D,
+                                                                 const uint16_t* a, int64_t as,
+                                                                 const float* la,
+                                                                 const uint16_t* bb, int64_t bs,
+                                                                 const float* lb, uint16_t* out,
+                                                                 int64_t os, float* lo) {
+    const int lane = threadIdx.x & 63;
+    const int64_t row = (int64_t)blockIdx.x * LM_WAVES + (threadIdx.x >> 6);
     if (row >= rows) return;
     const float x = la[row], y = lb[row];
     // logaddexp: max + log1p(exp(-|x - y|)); equal inputs (including -inf) give x + ln 2
@@ -658,12 +663,12 @@ __global__ void __launch_bounds__(256) lse_merge_kernel(int64_t rows, int D, con
                            : fmaxf(x, y) + log1pf(expf(-fabsf(x - y)));
     const float origin = isfinite(l) ? l : 0.0f;
     const float wa = expf(x - origin), wb = expf(y - origin);
-    for (int d = 0; d < D; ++d) {
+    for (int d = lane; d < D; d += 64) {
         const float va = bf16_bits_to_f32(a[row * as + d]);
         const float vb = bf16_bits_to_f32(bb[row * bs + d]);
         out[row * os + d] = f32_to_bf16_bits(va * wa + vb * wb);
     }
-    if (lo) lo[row] = l;
+    if (lo && lane == 0) lo[row] = l;
 }
 
 }  // namespace nkv
@@ -984,7 +989,7 @@ extern "C" int nkv_lse_merge(void* stream, int64_t rows, int D, const uint16_t* 
     NKV_REQUIRE(rows >= 0 && D > 0, NKV_ERR_INVALID, "rows must be >= 0 and D > 0");
     if (rows == 0) return NKV_OK;
     NKV_REQUIRE(a && b && lse_a && lse_b && out, NKV_ERR_INVALID, "null pointer");
-    lse_merge_kernel<<<dim3((unsigned)cdiv(rows, 256)), 256, 0, (hipStream_t)stream>>>(
+    lse_merge_kernel<<<dim3((unsigned)cdiv(rows, LM_WAVES)), 64 * LM_WAVES, 0, (hipStream_t)stream>>>(
         rows, D, a, a_stride, lse_a, b, b_stride, lse_b, out, out_stride, lse_out);
     NKV_LAUNCH_CHECK();
     return NKV_OK;

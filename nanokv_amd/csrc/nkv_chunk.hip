@@ -1550,7 +1550,6 @@ int staged_launch(hipStream_t s, const ChunkLaunchDesc& d, ChunkParams p, void* 
     if (!rc) rc = p.cur_mask ? set_smem(flash8_kernel<true>, sizeof(FlashSmem))
                              : set_smem(flash8_kernel<false>, sizeof(FlashSmem));
     if (rc) return rc;
-    if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
     if (gemm) {
         const int64_t items = BH * f.ntiles_hist + BH * (f.ntiles - f.ntiles_hist);
         dtile_kernel<<<dim3((unsigned)items), DT_THREADS, sizeof(DTileSmem), s>>>(p);
@@ -1558,6 +1557,8 @@ int staged_launch(hipStream_t s, const ChunkLaunchDesc& d, ChunkParams p, void* 
         stage8_kernel<<<dim3((unsigned)(BH * f.ntiles / 2)), C8_THREADS, sizeof(Chunk8Smem), s>>>(p);
     }
     NKV_LAUNCH_CHECK();
+    // the kernel events bracket the attention (flash) kernel
+    if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
     const dim3 grid((unsigned)(BH * f.qtiles * f.splits));
     if (p.cur_mask) flash8_kernel<true><<<grid, C8_THREADS, sizeof(FlashSmem), s>>>(p);
     else flash8_kernel<false><<<grid, C8_THREADS, sizeof(FlashSmem), s>>>(p);
