@@ -33,6 +33,13 @@
  *                     (CN/core.py:45-72), fused into one kernel
  *  nkv_lse_merge   <- merge (CN/core.py:33-42), fast_kernels._merge
  *                     (CN/fast_kernels.py:30-54)
+ *  nkv_lift_lse_combine <- HY lift_lse_combine (HYP:1807-1867; kernels
+ *                     _main_lift_lse_combine_kernel / _prope_lift_lse_combine_kernel
+ *                     HYP:883-1014), HYP = models/HY-WorldPlay/fast/hyvideo/models/
+ *                     transformers/modules/codec_native_position_triton.py
+ *  nkv_finish      <- LingBot finish (LBF:36-46, kernel _finish LBF:10-34),
+ *                     LBF = models/LingBot-World-2.0/fast/wan/modules/
+ *                     codec_native_finish_triton.py
  *  nkv_fast_attend <- hybrid_attention (CN/core.py:278-310) and the partition
  *                     reads of maybe_attention (CN/mg35.py:100-357)
  *  nkv_int8_pack   <- _pack_operator MG:108-131 (INT8 operator storage)
@@ -530,6 +537,73 @@ int nkv_lse_merge(void* stream, int64_t rows, int D,
                   const uint16_t* a, int64_t a_stride, const float* lse_a,
                   const uint16_t* b, int64_t b_stride, const float* lse_b,
                   uint16_t* out, int64_t out_stride, float* lse_out);
+
+/*
+ * HY's two history branches merged into the native output with their value
+ * lift fused in (HYP:883-1014).  native, low and the LSEs hold 2B batch
+ * items: items 0 .. B are the Main branch, items B .. 2B the PRoPE branch.
+ *   Main  (b < B):  h_o = sum_k low[b,h,q,k] main_lift[h,k,o]            o < 128
+ *   PRoPE (b >= B): h_(4j+c) = sum_k low[b,h,q,4k+c] prope_mix[h,k,j]    j < 32, c < 4
+ *   m = max(native_lse, history_lse); wn = exp(native_lse - m), wh = exp(history_lse - m)
+ *   out[b,h,q,:] = (native wn + h wh) / (wn + wh)          (fp32, -> bf16 once)
+ * low_dim is 32, 64 or 96 (HYP:1834-1835).  All tensors bf16 (uint16_t
+ * bits) except the fp32 LSEs; strides in elements; out is contiguous
+ * [2B, H, Q, 128] and may not alias an input.
+ */
+typedef struct nkv_lift_combine_args {
+    int B, H, Q, low_dim;
+    const uint16_t* native;       /* [2B, H, Q, 128] */
+    int64_t n_sb, n_sh, n_sq, n_sd;
+    const float* native_lse;      /* [2B, H, Q] */
+    int64_t nl_sb, nl_sh, nl_sq;
+    const uint16_t* low;          /* [2B, H, Q, low_dim] */
+    int64_t l_sb, l_sh, l_sq, l_sd;
+    const uint16_t* main_lift;    /* [H, low_dim, 128] */
+    int64_t ml_sh, ml_sk, ml_so;
+    const uint16_t* prope_mix;    /* [H, low_dim / 4, 32] */
+    int64_t pm_sh, pm_sk, pm_so;
+    const float* history_lse;     /* [2B, H, Q] */
+    int64_t hl_sb, hl_sh, hl_sq;
+    uint16_t* out;                /* [2B, H, Q, 128] contiguous */
+} nkv_lift_combine_args;
+
+int nkv_lift_lse_combine(void* stream, const nkv_lift_combine_args* args);
+
+/*
+ * LingBot's finish of one reader group (LBF:10-46): merge the group's lifted
+ * low output into the native output of its heads and scatter the rows to
+ * the native head index heads[g].  For group head g, native head hd = heads[g]:
+ *   x = native_lse[b,hd,s], z = low_lse[b,g,s]
+ *   l = (x == z and |x| = inf) ? x : max(x, z) + log1p(exp(-|x - z|))
+ *   origin = l if finite else 0
+ *   v = lifted[b,g,s,:]  (+ mean[b,hd,:] - projected[b,g,:] with the value-mean
+ *                          correction, LingBot codec_native_attention.py:779-785)
+ *   result[b,hd,s,:] = native[b,hd,s,:] exp(x - origin) + v exp(z - origin)
+ * in fp32 with one bf16 rounding.  native, lifted, result bf16; the LSEs, mean
+ * and projected fp32; mean and projected both set or both NULL.  result may
+ * alias native (each element is read before it is written).  A heads entry
+ * outside [0, H_native) writes nothing for that group head.
+ */
+typedef struct nkv_finish_args {
+    int B, H_native, H_group, S, D;
+    const uint16_t* native;       /* [B, H_native, S, D] */
+    int64_t a_sb, a_sh, a_ss, a_sd;
+    const float* native_lse;      /* [B, H_native, S] */
+    int64_t la_sb, la_sh, la_ss;
+    const uint16_t* lifted;       /* [B, H_group, S, D] */
+    int64_t b_sb, b_sh, b_ss, b_sd;
+    const float* low_lse;         /* [B, H_group, S] */
+    int64_t lb_sb, lb_sh, lb_ss;
+    const int32_t* heads;         /* [H_group] native head of each group head */
+    const float* mean;            /* [B, H_native, D] or NULL */
+    int64_t m_sb, m_sh, m_sd;
+    const float* projected;       /* [B, H_group, D] or NULL */
+    int64_t p_sb, p_sh, p_sd;
+    uint16_t* result;             /* [B, H_native, S, D] */
+    int64_t y_sb, y_sh, y_ss, y_sd;
+} nkv_finish_args;
+
+int nkv_finish(void* stream, const nkv_finish_args* args);
 
 #ifdef __cplusplus
 }

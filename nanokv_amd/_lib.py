@@ -34,7 +34,7 @@ EXPORTED = (
     "nkv_encode", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
     "nkv_fast_attend_workspace_size", "nkv_fast_attend", "nkv_rope_apply", "nkv_int8_pack",
     "nkv_int8_dequant", "nkv_c64_fit_workspace_size", "nkv_c64_fit", "nkv_camera_apply",
-    "nkv_attend_static",
+    "nkv_attend_static", "nkv_lift_lse_combine", "nkv_finish",
 )
 NKV_STATIC_SCRATCH_BYTES = 64 << 20
 
@@ -131,6 +131,38 @@ class NkvFastArgs(Structure):
     ]
 
 
+class NkvLiftCombineArgs(Structure):
+    _fields_ = [
+        ("B", c_int), ("H", c_int), ("Q", c_int), ("low_dim", c_int),
+        ("native", c_void_p), ("n_sb", c_int64), ("n_sh", c_int64), ("n_sq", c_int64),
+        ("n_sd", c_int64),
+        ("native_lse", c_void_p), ("nl_sb", c_int64), ("nl_sh", c_int64), ("nl_sq", c_int64),
+        ("low", c_void_p), ("l_sb", c_int64), ("l_sh", c_int64), ("l_sq", c_int64),
+        ("l_sd", c_int64),
+        ("main_lift", c_void_p), ("ml_sh", c_int64), ("ml_sk", c_int64), ("ml_so", c_int64),
+        ("prope_mix", c_void_p), ("pm_sh", c_int64), ("pm_sk", c_int64), ("pm_so", c_int64),
+        ("history_lse", c_void_p), ("hl_sb", c_int64), ("hl_sh", c_int64), ("hl_sq", c_int64),
+        ("out", c_void_p),
+    ]
+
+
+class NkvFinishArgs(Structure):
+    _fields_ = [
+        ("B", c_int), ("H_native", c_int), ("H_group", c_int), ("S", c_int), ("D", c_int),
+        ("native", c_void_p), ("a_sb", c_int64), ("a_sh", c_int64), ("a_ss", c_int64),
+        ("a_sd", c_int64),
+        ("native_lse", c_void_p), ("la_sb", c_int64), ("la_sh", c_int64), ("la_ss", c_int64),
+        ("lifted", c_void_p), ("b_sb", c_int64), ("b_sh", c_int64), ("b_ss", c_int64),
+        ("b_sd", c_int64),
+        ("low_lse", c_void_p), ("lb_sb", c_int64), ("lb_sh", c_int64), ("lb_ss", c_int64),
+        ("heads", c_void_p),
+        ("mean", c_void_p), ("m_sb", c_int64), ("m_sh", c_int64), ("m_sd", c_int64),
+        ("projected", c_void_p), ("p_sb", c_int64), ("p_sh", c_int64), ("p_sd", c_int64),
+        ("result", c_void_p), ("y_sb", c_int64), ("y_sh", c_int64), ("y_ss", c_int64),
+        ("y_sd", c_int64),
+    ]
+
+
 class NanoKVError(RuntimeError):
     """A libnanokv_hip.so call returned an error code."""
 
@@ -192,6 +224,10 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nkv_lse_merge.restype = c_int
     lib.nkv_lse_merge.argtypes = [c_void_p, c_int64, c_int, c_void_p, c_int64, c_void_p,
                                   c_void_p, c_int64, c_void_p, c_void_p, c_int64, c_void_p]
+    lib.nkv_lift_lse_combine.restype = c_int
+    lib.nkv_lift_lse_combine.argtypes = [c_void_p, POINTER(NkvLiftCombineArgs)]
+    lib.nkv_finish.restype = c_int
+    lib.nkv_finish.argtypes = [c_void_p, POINTER(NkvFinishArgs)]
 
 
 def lib() -> ctypes.CDLL:

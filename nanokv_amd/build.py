@@ -31,6 +31,8 @@ SOURCES = {
     # scores are never NaN (-inf masks are kept): fmaxf needs no NaN quieting
     "nkv_chunk.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1", "-fno-honor-nans"],
     "nkv_fast.hip": [],
+    # the partition merges keep the reference's unfused fp32 products
+    "nkv_merge.hip": ["-ffp-contract=off"],
     # RoPE rounds every fp64 product and sum separately, as the oracle does
     "nkv_rope.hip": ["-ffp-contract=off"],
     "nkv_camera.hip": ["-ffp-contract=off"],

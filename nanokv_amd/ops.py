@@ -19,7 +19,8 @@ from . import _lib
 from ._lib import (NKV_DTYPE_BF16, NKV_DTYPE_FP16, NKV_QUANT_BF16, NKV_QUANT_FP32,
                    NKV_SCHEDULE_AUTO, NKV_SCHEDULE_KEY_CHUNKS, NKV_SCHEDULE_QUERY_TILES,
                    NkvAttendArgs, NkvCodec, NkvDecodeArgs, NkvEncodeArgs, NkvFastArgs,
-                   NkvCamera, NkvReaderGroup, NkvRope, NkvSegment, check, lib)
+                   NkvCamera, NkvFinishArgs, NkvLiftCombineArgs, NkvReaderGroup, NkvRope,
+                   NkvSegment, check, lib)
 
 _SCALE_CODES = {torch.bfloat16: NKV_DTYPE_BF16, torch.float16: NKV_DTYPE_FP16}
 _QUANT_CODES = {"fp32": NKV_QUANT_FP32, "bf16": NKV_QUANT_BF16}
@@ -1047,3 +1048,138 @@ def lse_merge(a: torch.Tensor, lse_a: torch.Tensor, b: torch.Tensor, lse_b: torc
         _stream(device), rows, D, a.data_ptr(), D, lse_a.data_ptr(), b.data_ptr(), D,
         lse_b.data_ptr(), out.data_ptr(), D, lse.data_ptr()))
     return out, lse
+
+
+def lift_lse_combine(native: torch.Tensor, native_lse: torch.Tensor, low: torch.Tensor,
+                     main_lift: torch.Tensor, prope_mix: torch.Tensor,
+                     history_lse: torch.Tensor) -> torch.Tensor:
+    """HY's two history branches lifted to D = 128 and merged into the native
+    output by LSE in one write (nkv_lift_lse_combine; the reference's
+    lift_lse_combine, HYP:1807-1867, with the same arguments and checks).
+    native [2B, H, Q, 128], low [2B, H, Q, Dlow] (Dlow in 32/64/96): items
+    0..B the Main branch (lifted by main_lift [H, Dlow, 128]), items B..2B the
+    PRoPE branch (coordinate c of quartet k mixed by prope_mix [H, Dlow/4, 32]
+    into output dims 4j + c); LSEs [2B, H, Q].  Returns a new contiguous
+    [2B, H, Q, 128] bf16 tensor."""
+    device = _require_gpu(native, native_lse, low, main_lift, prope_mix, history_lse)
+    if native.ndim != 4 or native.shape[0] % 2:
+        raise ValueError("native output must be [2B,H,Q,128]")
+    batch, heads, queries, width = (native.shape[0] // 2, native.shape[1], native.shape[2],
+                                    native.shape[3])
+    if width != 128 or low.ndim != 4 or tuple(low.shape[:3]) != (2 * batch, heads, queries):
+        raise ValueError("fused lift expects [2B,H,Q,Dlow] and D128 native")
+    low_dim = int(low.shape[-1])
+    if low_dim not in (32, 64, 96):
+        raise ValueError("fused lift supports D32/D64/D96")
+    if tuple(main_lift.shape) != (heads, low_dim, 128):
+        raise ValueError("main lift must be [H,Dlow,128]")
+    if tuple(prope_mix.shape) != (heads, low_dim // 4, 32):
+        raise ValueError("PRoPE lift must be [H,Dlow/4,32]")
+    if tuple(native_lse.shape) != tuple(native.shape[:-1]) or \
+            tuple(history_lse.shape) != tuple(native_lse.shape):
+        raise ValueError("segment LSE tensors must match [2B,H,Q]")
+    for name, t in (("native", native), ("low", low)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16")
+    main_lift = main_lift.to(torch.bfloat16)
+    prope_mix = prope_mix.to(torch.bfloat16)
+    native_lse = native_lse.float()
+    history_lse = history_lse.float()
+    out = torch.empty(native.shape, device=device, dtype=torch.bfloat16)
+    a = NkvLiftCombineArgs()
+    a.B, a.H, a.Q, a.low_dim = batch, heads, queries, low_dim
+    a.native = native.data_ptr()
+    a.n_sb, a.n_sh, a.n_sq, a.n_sd = native.stride()
+    a.native_lse = native_lse.data_ptr()
+    a.nl_sb, a.nl_sh, a.nl_sq = native_lse.stride()
+    a.low = low.data_ptr()
+    a.l_sb, a.l_sh, a.l_sq, a.l_sd = low.stride()
+    a.main_lift = main_lift.data_ptr()
+    a.ml_sh, a.ml_sk, a.ml_so = main_lift.stride()
+    a.prope_mix = prope_mix.data_ptr()
+    a.pm_sh, a.pm_sk, a.pm_so = prope_mix.stride()
+    a.history_lse = history_lse.data_ptr()
+    a.hl_sb, a.hl_sh, a.hl_sq = history_lse.stride()
+    a.out = out.data_ptr()
+    check("nkv_lift_lse_combine", lib().nkv_lift_lse_combine(_stream(device), byref(a)))
+    return out
+
+
+def lse_combine_split(native: torch.Tensor, native_lse: torch.Tensor, main: torch.Tensor,
+                      prope: torch.Tensor, history_lse: torch.Tensor) -> torch.Tensor:
+    """HY's merge of already lifted history halves (the reference's
+    lse_combine_split, HYP:1768-1804): items 0..B of native merge with main
+    [B, H, Q, D], items B..2B with prope, by their LSEs [2B, H, Q]
+    (nkv_lse_merge over each half).  Returns a new contiguous tensor."""
+    _require_gpu(native, native_lse, main, prope, history_lse)
+    if native.ndim != 4 or native.shape[0] % 2:
+        raise ValueError("native output must be [2B,H,Q,D]")
+    batch = native.shape[0] // 2
+    expected = (batch, *native.shape[1:])
+    if tuple(main.shape) != expected or tuple(prope.shape) != expected:
+        raise ValueError("split history outputs must each be [B,H,Q,D]")
+    if tuple(native_lse.shape) != tuple(native.shape[:-1]) or \
+            tuple(history_lse.shape) != tuple(native_lse.shape):
+        raise ValueError("segment LSE tensors must match [2B,H,Q]")
+    out = torch.empty(native.shape, device=native.device, dtype=torch.bfloat16)
+    for half, hist in ((slice(0, batch), main), (slice(batch, 2 * batch), prope)):
+        lse_merge(native[half].to(torch.bfloat16).contiguous(),
+                  native_lse[half].float().contiguous(),
+                  hist.to(torch.bfloat16).contiguous(), history_lse[half].float().contiguous(),
+                  out=out[half])
+    return out
+
+
+def finish(native: torch.Tensor, native_lse: torch.Tensor, lifted: torch.Tensor,
+           low_lse: torch.Tensor, heads: torch.Tensor, result: torch.Tensor,
+           mean: Optional[torch.Tensor] = None, projected: Optional[torch.Tensor] = None):
+    """LingBot's finish of one reader group (nkv_finish; the reference's
+    finish, LBF:36-46, with the same arguments): merge lifted [B, h, S, D]
+    (LSE low_lse [B, h, S]) into native [B, Hn, S, D] (native_lse [B, Hn, S])
+    at native heads heads[g] and write the rows to result [B, Hn, S, D]; with
+    mean [B, Hn, 1, D] and projected [B, h, 1, D] (fp32) the lifted values are
+    first corrected by + mean - projected.  Returns result."""
+    device = _require_gpu(native, native_lse, lifted, low_lse, heads, result)
+    correct = mean is not None
+    if correct != (projected is not None):
+        raise ValueError("mean and projected come together")
+    if native.ndim != 4 or lifted.ndim != 4 or result.shape != native.shape:
+        raise ValueError("native, lifted and result must be [B,H,S,D]")
+    b, h, s, d = (int(x) for x in lifted.shape)
+    if native.shape[0] != b or native.shape[2] != s or native.shape[3] != d:
+        raise ValueError("lifted must match native in batch, rows and width")
+    if tuple(low_lse.shape) != (b, h, s) or tuple(native_lse.shape) != tuple(native.shape[:3]):
+        raise ValueError("LSE shapes must be [B,H,S]")
+    if heads.numel() != h:
+        raise ValueError("one native head per group head")
+    for name, t in (("native", native), ("result", result)):
+        if t.dtype != torch.bfloat16:
+            raise TypeError(f"{name} must be bfloat16")
+    lifted = lifted.to(torch.bfloat16)
+    native_lse = native_lse.float()
+    low_lse = low_lse.float()
+    heads32 = heads.to(device=device, dtype=torch.int32).contiguous()
+    a = NkvFinishArgs()
+    a.B, a.H_native, a.H_group, a.S, a.D = b, int(native.shape[1]), h, s, d
+    a.native = native.data_ptr()
+    a.a_sb, a.a_sh, a.a_ss, a.a_sd = native.stride()
+    a.native_lse = native_lse.data_ptr()
+    a.la_sb, a.la_sh, a.la_ss = native_lse.stride()
+    a.lifted = lifted.data_ptr()
+    a.b_sb, a.b_sh, a.b_ss, a.b_sd = lifted.stride()
+    a.low_lse = low_lse.data_ptr()
+    a.lb_sb, a.lb_sh, a.lb_ss = low_lse.stride()
+    a.heads = heads32.data_ptr()
+    if correct:
+        mean = mean.float()
+        projected = projected.float()
+        if mean.ndim != 4 or projected.ndim != 4 or mean.shape[3] != d or projected.shape[3] != d:
+            raise ValueError("mean and projected must be [B,H,1,D]")
+        a.mean = mean.data_ptr()
+        a.m_sb, a.m_sh, a.m_sd = mean.stride(0), mean.stride(1), mean.stride(3)
+        a.projected = projected.data_ptr()
+        a.p_sb, a.p_sh, a.p_sd = projected.stride(0), projected.stride(1), projected.stride(3)
+    a.result = result.data_ptr()
+    a.y_sb, a.y_sh, a.y_ss, a.y_sd = result.stride()
+    check("nkv_finish", lib().nkv_finish(_stream(device), byref(a)))
+    return result

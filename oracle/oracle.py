@@ -77,6 +77,15 @@ Pinning (the independent check that fixes each function; see tests/):
                                of the reference's blockwise path for rows that
                                see none (CN/core.py:57-72); an all-True mask
                                equals no mask
+  lift_lse_combine            the union invariant in fp64: merging the native
+                               partition with a lifted low partition equals one
+                               softmax over both key sets with the low values
+                               lifted (V_low L); the PRoPE mix equals the Main
+                               lift by the matrix L[4k+c, 4j+c] = mix[k, j]
+  finish                      equals merge() of the native and lifted rows at
+                               the group's heads (other heads untouched); the
+                               correction equals merging lifted + mean -
+                               projected; mean = projected changes nothing
 """
 from __future__ import annotations
 
@@ -406,6 +415,55 @@ def merge(out_a, lse_a, out_b, lse_b):
     wb = np.exp(lse_b - origin)
     out = np.asarray(out_a, np.float64) * wa[..., None] + np.asarray(out_b, np.float64) * wb[..., None]
     return out, lse
+
+
+def lift_lse_combine(native, native_lse, low, main_lift, prope_mix, history_lse):
+    """HY's value lift of its two history branches fused with the LSE merge
+    (models/HY-WorldPlay/fast/hyvideo/models/transformers/modules/
+    codec_native_position_triton.py:883-1014, wrapper :1807-1867), in fp64.
+    native [2B, H, Q, 128] and low [2B, H, Q, Dlow] as floats (the bf16
+    values), lifts [H, Dlow, 128] / [H, Dlow/4, 32], LSEs [2B, H, Q].  Items
+    0..B lift by main_lift, items B..2B by the quartet mix (output dim 4j + c
+    takes coordinate c of every quartet k of the low row)."""
+    native = np.asarray(native, np.float64)
+    low = np.asarray(low, np.float64)
+    main_lift = np.asarray(main_lift, np.float64)
+    prope_mix = np.asarray(prope_mix, np.float64)
+    B = native.shape[0] // 2
+    H, Q, K = low.shape[1], low.shape[2], low.shape[3]
+    hist = np.empty(native.shape, np.float64)
+    hist[:B] = np.einsum("bhqk,hko->bhqo", low[:B], main_lift)
+    quart = low[B:].reshape(B, H, Q, K // 4, 4)               # [..., k, c]
+    mixed = np.einsum("bhqkc,hkj->bhqjc", quart, prope_mix)   # [..., j, c]
+    hist[B:] = mixed.reshape(B, H, Q, 128)                    # dim 4j + c
+    a = np.asarray(native_lse, np.float64)
+    b = np.asarray(history_lse, np.float64)
+    m = np.maximum(a, b)
+    wa, wb = np.exp(a - m)[..., None], np.exp(b - m)[..., None]
+    return (native * wa + hist * wb) / (wa + wb)
+
+
+def finish(native, native_lse, lifted, low_lse, heads, result, mean=None, projected=None):
+    """LingBot's finish of one reader group (models/LingBot-World-2.0/fast/wan/
+    modules/codec_native_finish_triton.py:10-46), in fp64: result (a copy, as
+    floats) with the rows of native head heads[g] replaced by the LSE merge of
+    native and lifted[:, g] (+ mean[:, heads[g]] - projected[:, g] when given)."""
+    native = np.asarray(native, np.float64)
+    lifted = np.asarray(lifted, np.float64)
+    out = np.array(result, np.float64)
+    x_all = np.asarray(native_lse, np.float64)
+    z_all = np.asarray(low_lse, np.float64)
+    for g, hd in enumerate(np.asarray(heads).tolist()):
+        x, z = x_all[:, hd], z_all[:, g]
+        with np.errstate(invalid="ignore"):
+            l = np.maximum(x, z) + np.log1p(np.exp(-np.abs(x - z)))
+        l = np.where((x == z) & np.isinf(x), x, l)
+        origin = np.where(np.isinf(l), 0.0, l)
+        v = lifted[:, g]
+        if mean is not None:
+            v = (v + np.asarray(mean, np.float64)[:, hd]) - np.asarray(projected, np.float64)[:, g]
+        out[:, hd] = native[:, hd] * np.exp(x - origin)[..., None] + v * np.exp(z - origin)[..., None]
+    return out
 
 
 def decode_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: Optional[dict], value: Optional[dict],
