@@ -64,7 +64,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 4
+#define NKV_ABI_VERSION 5
 
 enum nkv_status {
     NKV_OK = 0,
@@ -504,6 +504,11 @@ typedef struct nkv_reader_group {
  * k_low / v_low by P^-1 on their blocks (cam_blocks).  The caller applies P
  * to out, as for nkv_attend: with a value lift folded into the value reader
  * (block-selection or identity lifts) P commutes with the lift.
+ * Value-mean correction (low_shift != NULL; LingBot codec_native_attention.py
+ * :779-785 and finish, codec_native_finish_triton.py:31-32): low_shift[b, h]
+ * ([B, H, D] fp32, strides ls_sb, ls_sh, unit d stride) is added to every
+ * low-partition value of head h, i.e. to the low output before the merge;
+ * the reference's mean - projected, where the lift is low-rank.
  */
 typedef struct nkv_fast_args {
     nkv_attend_args attend;
@@ -518,6 +523,8 @@ typedef struct nkv_fast_args {
     int64_t qp_sb, qp_st, qp_sh;
     const nkv_rope* q_rope;       /* query positions (with RoPE), host pointer */
     const nkv_camera* q_camera;   /* P^T of the query rows (with a camera), host pointer */
+    const float* low_shift;       /* [B, H, D] fp32 low value shift, or NULL */
+    int64_t ls_sb, ls_sh;
 } nkv_fast_args;
 
 /* Bytes of workspace nkv_fast_attend needs for these arguments. */

@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libnanokv_hip.so"
 
-NKV_ABI_VERSION = 4
+NKV_ABI_VERSION = 5
 NKV_OK = 0
 NKV_ERR_INVALID = -1
 NKV_ERR_UNSUPPORTED = -2
@@ -128,6 +128,7 @@ class NkvFastArgs(Structure):
         ("groups", POINTER(NkvReaderGroup)),
         ("q_pre", c_void_p), ("qp_sb", c_int64), ("qp_st", c_int64), ("qp_sh", c_int64),
         ("q_rope", POINTER(NkvRope)), ("q_camera", POINTER(NkvCamera)),
+        ("low_shift", c_void_p), ("ls_sb", c_int64), ("ls_sh", c_int64),
     ]
 
 

@@ -262,7 +262,7 @@ class ReaderGroup:
         for name, shape in expected.items():
             if tuple(state[name].shape) != shape:
                 raise ValueError(f"Bad {name} shape; expected {shape}")
-        self.native_dim, self.d = native, d
+        self.native_dim, self.d, self.vd = native, d, vd
         self.identity_query = _is_identity(state["q_reduce"])
         self.identity_k = _is_identity(state["k_affine"])
         self.identity_lift = vd == native and _is_identity(state["lift"])
@@ -402,6 +402,101 @@ class ReaderLayer:
             raise ValueError("Reader groups must partition heads exactly once")
 
 
+def _low_value_sums(cache_k: Any, cache_v: Any, low: torch.Tensor, device: torch.device):
+    """The sufficient statistics of the low value rows (LingBot
+    codec_native_attention.py:478-489): the fp32 sum of their bf16 latents
+    [B, r], the center sum from the center counts [B, HD] (None without
+    centers), the row count and the value operator; None when no row is
+    low."""
+    items = nanokv_codec.direct_latent_pair_segments(cache_k, cache_v, device=device,
+                                                     token_keep=low)
+    if not items:
+        return None
+    latent_sum = center_sum = None
+    count = 0
+    for item in items:
+        latent, (centers, ids), _ = item["v"]
+        ls = latent.float().sum(1)
+        latent_sum = ls if latent_sum is None else latent_sum + ls
+        if centers is not None:
+            counts = torch.zeros(ids.shape[0], centers.shape[1], device=device,
+                                 dtype=torch.float32)
+            counts.scatter_add_(1, ids, torch.ones_like(ids, dtype=torch.float32))
+            cs = torch.einsum("bc,bcd->bd", counts,
+                              centers.float().expand(ids.shape[0], -1, -1))
+            center_sum = cs if center_sum is None else center_sum + cs
+        count += int(latent.shape[1])
+    part = nanokv_codec.segments_of(cache_v)[0]
+    op = nanokv_codec._operator(str(part["kind"]), int(part["layer"]), device)
+    return latent_sum, center_sum, count, op
+
+
+def _mean_bias(op, B: int, HD: int, center_sum, count: int, device) -> torch.Tensor:
+    """bf16(mean) + the mean center per batch item, [B, HD] fp32."""
+    base = torch.zeros(B, HD, device=device)
+    if op["mean"] is not None:
+        base = base + op["mean"].to(torch.bfloat16).float()
+    if center_sum is not None:
+        base = base + center_sum / count
+    return base
+
+
+def compressed_value_mean(cache_k: Any, cache_v: Any, low: torch.Tensor, heads: int,
+                          device: torch.device) -> Optional[torch.Tensor]:
+    """LingBot's first moment of the low history values (LingBot
+    codec_native_attention.py:465-501) from the latent sums and the center
+    counts, never the decoded rows: value = W_dec (sum latent / n) +
+    bf16(mean) + (sum_c count_c center_c) / n in fp32, per batch item and
+    native head, [B, H, 1, D]; None when no row is low."""
+    sums = _low_value_sums(cache_k, cache_v, low, device)
+    if sums is None:
+        return None
+    latent_sum, center_sum, count, op = sums
+    mean = op["mean"]
+    value = torch.nn.functional.linear(latent_sum / count, op["decoder"].float(),
+                                       None if mean is None else mean.to(torch.bfloat16).float())
+    if center_sum is not None:
+        value = value + center_sum / count
+    B, HD = value.shape
+    return value.reshape(B, heads, 1, HD // heads)
+
+
+def value_mean_shift(reader: ReaderLayer, cache_k: Any, cache_v: Any, low: torch.Tensor,
+                     device: torch.device) -> Optional[torch.Tensor]:
+    """The value-mean correction of LingBot's Fast (codec_native_attention.py
+    :779-785) as a per-head shift of the low values, [B, H, D] fp32: for
+    the heads of each group whose value lift is low-rank (reader value width
+    below the native width), mean - projected, where mean is the first moment
+    of the full decode (compressed_value_mean) and projected the mean of the
+    group's low value reads after the lift; 0 for the other heads.  projected
+    is formed from the same latent and center sums through the group's value
+    reader (lift folded in: v_read' = lift^T v_read, v_affine' = v_affine
+    lift), as the reads are affine in the latent and the center."""
+    if not any(g.vd < g.native_dim for g in reader.groups):
+        return None
+    sums = _low_value_sums(cache_k, cache_v, low, device)
+    if sums is None:
+        return None
+    latent_sum, center_sum, count, op = sums
+    H, D = reader.heads, reader.native_dim
+    lat = latent_sum / count                                                  # [B, r]
+    B = lat.shape[0]
+    base = _mean_bias(op, B, H * D, center_sum, count, device)               # [B, HD]
+    value_mean = (torch.nn.functional.linear(lat, op["decoder"].float()) + base).reshape(B, H, D)
+    base = base.reshape(B, H, D)
+    shift = torch.zeros(B, H, D, device=device, dtype=torch.float32)
+    for g in reader.groups:
+        if g.vd >= g.native_dim:
+            continue
+        heads = g.heads.to(device)
+        proj = torch.einsum("br,hdr->bhd", lat, g.v_read.float())
+        aff = base.index_select(1, heads)
+        proj = proj + (aff if g.v_affine is None
+                       else torch.einsum("bhe,hed->bhd", aff, g.v_affine.float()))
+        shift[:, heads] = value_mean.index_select(1, heads) - proj
+    return shift
+
+
 def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
                            k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
                            reader: ReaderLayer, protect: torch.Tensor, *,
@@ -410,7 +505,8 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
                            low: Optional[torch.Tensor] = None,
                            camera: Optional[ops.Camera] = None,
                            q_camera: Optional[ops.Camera] = None,
-                           visibility: Optional[ops.Visibility] = None):
+                           visibility: Optional[ops.Visibility] = None,
+                           value_mean_correction: bool = False):
     """NanoKV-Fast history attention of q [B, H, Q, D]: the protected history
     tokens (bool mask [N] over the cache) and the current chunk are attended
     at full width by every head (mg35.py:192-303), the low history tokens
@@ -425,7 +521,9 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     Camera (mg35.py:253-257, 310-346): camera = kv_camera(P_inv, ...) of the
     cached rows and q_camera the P^T of the query rows; q, k_cur and v_cur are
     then already transformed, q_pre is not, and the caller applies P to the
-    output.  visibility: which current keys each query sees."""
+    output.  visibility: which current keys each query sees.
+    value_mean_correction: LingBot's first-moment correction of the low
+    values of groups with a low-rank value lift (value_mean_shift)."""
     device = q.device
     B, H, Qn, D = (int(x) for x in q.shape)
     if H != reader.heads or D != reader.native_dim:
@@ -453,10 +551,13 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     if q_pre is not None:
         qp = q_pre.to(torch.bfloat16).permute(0, 2, 1, 3)
     groups = [g.tensors(rope=rope is not None, camera=camera is not None) for g in reader.groups]
+    shift = value_mean_shift(reader, cache_k, cache_v, low, device) \
+        if value_mean_correction else None
     out, lse = ops.fast_attend(qq, kc, vc, key, value, protect_rows, low_rows, groups,
                                softmax_scale=D ** -0.5 if scale is None else scale,
                                return_lse=return_lse, rope=rope, q_pre=qp, q_rope=q_rope,
                                camera=camera, q_camera=q_camera,
-                               visibility=visibility if kc is not None else None)
+                               visibility=visibility if kc is not None else None,
+                               low_shift=shift)
     out = out.permute(0, 2, 1, 3)
     return (out, lse) if return_lse else out

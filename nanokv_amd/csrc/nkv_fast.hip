@@ -171,7 +171,7 @@ __global__ void __launch_bounds__(256) project_mfma_kernel(const void* x, int64_
 __global__ void __launch_bounds__(256) group_merge_kernel(
     int B, int64_t Q, int nh, int D, const int32_t* heads, uint16_t* out, int64_t o_sb,
     int64_t o_st, int64_t o_sh, const float* lse_n, int H, const uint16_t* low, const float* lse_l,
-    float* lse_out) {
+    float* lse_out, const float* shift, int64_t sh_sb, int64_t sh_sh) {
     const int per_row = D / 8;
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (tid >= (int64_t)B * Q * nh * per_row) return;
@@ -190,12 +190,20 @@ __global__ void __launch_bounds__(256) group_merge_kernel(
     u32x4* op = reinterpret_cast<u32x4*>(out + (int64_t)b * o_sb + q * o_st + (int64_t)h * o_sh + 8 * part);
     const u32x4 lv = *reinterpret_cast<const u32x4*>(low + (((int64_t)b * Q + q) * nh + i) * D + 8 * part);
     const u32x4 ov = *op;
+    // the value-mean correction shifts the low output of head h
+    float sv[8] = {};
+    if (shift) {
+        const float* sp = shift + (int64_t)b * sh_sb + (int64_t)h * sh_sh + 8 * part;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) sv[e] = sp[e];
+    }
     u32x4 r;
 #pragma unroll
     for (int e = 0; e < 4; ++e)
-        r[e] = pack_bf16x2(__uint_as_float(ov[e] << 16) * wa + __uint_as_float(lv[e] << 16) * wb,
-                           __uint_as_float(ov[e] & 0xffff0000u) * wa +
-                               __uint_as_float(lv[e] & 0xffff0000u) * wb);
+        r[e] = pack_bf16x2(
+            __uint_as_float(ov[e] << 16) * wa + (__uint_as_float(lv[e] << 16) + sv[2 * e]) * wb,
+            __uint_as_float(ov[e] & 0xffff0000u) * wa +
+                (__uint_as_float(lv[e] & 0xffff0000u) + sv[2 * e + 1]) * wb);
     *op = r;
     if (lse_out && part == 0) lse_out[((int64_t)b * H + h) * Q + q] = l;
 }
@@ -660,7 +668,8 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
         group_merge_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(
             a.B, a.Q, nh, D, G.heads, a.out, a.o_sb, a.o_st, a.o_sh, lse_n, a.H,
             reinterpret_cast<const uint16_t*>(ws + L.out_l[g]),
-            reinterpret_cast<const float*>(ws + L.lse_l[g]), a.lse);
+            reinterpret_cast<const float*>(ws + L.lse_l[g]), a.lse, f->low_shift, f->ls_sb,
+            f->ls_sh);
         NKV_LAUNCH_CHECK();
     }
     return NKV_OK;

@@ -919,7 +919,7 @@ class ReaderTensors:
 
 def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, softmax_scale, out,
                return_lse, rope=None, q_pre=None, q_rope=None, camera=None, q_camera=None,
-               visibility=None):
+               visibility=None, low_shift=None):
     args, out, lse, device = _attend_args(q, k_cur, v_cur, key, value, softmax_scale, out,
                                           return_lse)
     keep = []  # ctypes structs the call points to
@@ -963,6 +963,14 @@ def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, soft
         qc = q_camera.struct()
         keep.append(qc)
         f.q_camera = ctypes.pointer(qc)
+    if low_shift is not None:
+        _require_gpu(low_shift)
+        B, _, H, D = (int(x) for x in q.shape)
+        if low_shift.dtype != torch.float32 or tuple(low_shift.shape) != (B, H, D) or \
+                low_shift.stride(2) != 1:
+            raise ValueError("low_shift must be float32 [B, H, D] with unit stride in d")
+        f.low_shift = low_shift.data_ptr()
+        f.ls_sb, f.ls_sh = low_shift.stride(0), low_shift.stride(1)
     need = lib().nkv_fast_attend_workspace_size(byref(f))
     err = lib().nkv_last_error().decode()
     if need == 0 and err:
@@ -988,7 +996,8 @@ def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[
                 workspace: Optional[torch.Tensor] = None, rope=None,
                 q_pre: Optional[torch.Tensor] = None, q_rope=None,
                 camera: Optional[Camera] = None, q_camera: Optional[Camera] = None,
-                visibility: Optional[Visibility] = None):
+                visibility: Optional[Visibility] = None,
+                low_shift: Optional[torch.Tensor] = None):
     """NanoKV-Fast mixed-dimensional attention (see nkv_fast_attend).
 
     protect_rows / low_rows: int32 codec rows of the native and low
@@ -1001,12 +1010,13 @@ def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[
     history rows (q, k_cur, v_cur already transformed; the caller applies P
     to out), q_camera: P^T of the query rows for the reader queries (then q_pre
     is the untransformed query).  visibility: which current keys each query
-    sees in the native partition.
+    sees in the native partition.  low_shift [B, H, D] fp32: the value-mean
+    correction added to each head's low-partition values before the merge.
     """
     f, structs, need, out, lse, device = _fast_args(q, k_cur, v_cur, key, value, protect_rows,
                                                     low_rows, groups, softmax_scale, out,
                                                     return_lse, rope, q_pre, q_rope, camera,
-                                                    q_camera, visibility)
+                                                    q_camera, visibility, low_shift)
     if kernel_events is not None:
         f.attend.ev_kernel_begin, f.attend.ev_kernel_end = kernel_events
     if workspace is None or workspace.numel() < need:

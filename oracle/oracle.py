@@ -691,7 +691,7 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
                 groups: Sequence[dict], scale: float, heads: Optional[Sequence[int]] = None,
                 D: int = 128, dtype=np.float64, key_freqs: Optional[np.ndarray] = None,
                 q_pre_bf16=None, q_freqs: Optional[np.ndarray] = None, cur_mask=None,
-                key_cam=None, q_cam=None, out_cam=None):
+                key_cam=None, q_cam=None, out_cam=None, low_shift=None):
     """NanoKV-Fast for one batch item: hybrid_attention (CN/core.py:278-310)
     with maybe_attention's partitions (CN/mg35.py:192-348), identity lift.
 
@@ -719,7 +719,9 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
     None: block j % 4); q_cam (P^T of the queries) the group query after its
     RoPE; out_cam (P of the queries) the native output before the merge and
     each low output before its lift.  q_bf16, k_cur and v_cur are taken as
-    already transformed; a group's query comes from q_pre_bf16 when given."""
+    already transformed; a group's query comes from q_pre_bf16 when given.
+    low_shift [H, D]: LingBot's value-mean correction (codec_native_attention.py
+    :779-785), added to each head's lifted low output before the merge."""
     q = bf16_to_f32(q_bf16)
     Qn, H = q.shape[0], q.shape[1]
     heads = list(range(H)) if heads is None else list(heads)
@@ -793,6 +795,8 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
                 # lift_output (CN/core.py:202-204), applied before the merge (mg35.py:347)
                 lf = bf16_to_f32(g["lift"][i]).astype(dtype)
                 ol = bf16_to_f32(f32_to_bf16((ol.astype(dtype) @ lf).astype(np.float32)))
+            if low_shift is not None:
+                ol = ol + np.asarray(low_shift, np.float64)[h]
             mo, ml = merge(on, ln, ol, ll[0])
             on, ln = bf16_to_f32(f32_to_bf16(np.asarray(mo, np.float32))), ml
         outs.append(on)

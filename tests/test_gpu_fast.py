@@ -265,3 +265,83 @@ def test_fast_value_lift(dev, vd):
     low["lift"] = bf(torch.randn(n, vd, D, generator=g) / vd ** 0.5)
     low["v_indices"] = torch.arange(vd).expand(n, vd).clone()
     _run(sc, dev, payload, np.arange(400, 600))
+
+
+def test_fast_value_mean_correction(dev, monkeypatch):
+    """LingBot's value-mean correction (codec_native_attention.py:465-501,
+    779-785) in the fused path: for a group with a low-rank value lift
+    (vd = 64 < 128), every low value is shifted by mean - projected, where
+    mean is the first moment of the low rows' full decode and projected the
+    mean of their lifted reader value reads.  Both are formed here in fp64
+    from the oracle's latents and reads, independently of the library's
+    closed form, and the result is checked against the oracle's Fast with
+    that shift."""
+    from nanokv_amd import nanokv_codec as nc
+    monkeypatch.setenv("NANOKV_SCALE_GROUP", "32")
+    monkeypatch.setenv("NANOKV_SCALE_DTYPE", "fp16")
+    monkeypatch.setenv("NANOKV_QUANT_MODE", "fp32")
+    H, D, layer, vd = 3, 128, 9, 64
+    sh = synth.Shape("vmc", H=H, D=D, N=0, Q=0, Nc=0, rK=128, rV=128, G=32, C=8)
+    lay = synth.make_layer(sh, seed=layer, with_mean=True)
+    nc.register_operator("k", layer, encoder=lay.w_enc_k.to(dev), decoder=lay.w_dec_k.to(dev),
+                         mean=lay.mean_k.to(dev))
+    nc.register_operator("v", layer, encoder=lay.w_enc_v.to(dev), decoder=lay.w_dec_v.to(dev),
+                         mean=lay.mean_v.to(dev))
+    nc.register_centers("k", layer, None)  # per-segment C64 tables
+    nc.register_centers("v", layer, None)
+    monkeypatch.setenv("MG35_KVCODEC_C64_CLUSTERS", "8")
+    cache_k = cache_v = None
+    for c in range(3):
+        k = synth.history_rows(sh, lay.centers_k, 64, seed=50 + c).to(dev)[None].to(torch.bfloat16)
+        v = synth.history_rows(sh, lay.centers_v, 64, seed=60 + c).to(dev)[None].to(torch.bfloat16)
+        cache_k = nc.concat_values(cache_k, nc.encode_tensor("k", layer, k))
+        cache_v = nc.concat_values(cache_v, nc.encode_tensor("v", layer, v))
+    protect = torch.zeros(192, dtype=torch.bool, device=dev)
+    protect[128:] = True
+    payload = synth.make_readers(sh, lay, full_heads=(0,), d=32)
+    low_g = payload["groups"][1]
+    n = len(low_g["heads"])
+    gen = torch.Generator().manual_seed(5)
+
+    def bf(t):
+        return t.to(torch.bfloat16).float()
+    low_g["v_read"] = bf(torch.randn(n, vd, sh.rV, generator=gen) / sh.rV ** 0.5)
+    low_g["v_affine"] = bf(torch.randn(n, D, vd, generator=gen) / D ** 0.5)
+    low_g["lift"] = bf(torch.randn(n, vd, D, generator=gen) / vd ** 0.5)
+    low_g["v_indices"] = torch.arange(vd).expand(n, vd).clone()
+    reader = codec_native.ReaderLayer(payload, dev)
+    q = (torch.randn(1, H, 30, D, generator=gen) / D ** 0.5).to(torch.bfloat16).to(dev)
+    kc = torch.randn(1, H, 16, D, generator=gen).to(torch.bfloat16).to(dev)
+    vc = torch.randn(1, H, 16, D, generator=gen).to(torch.bfloat16).to(dev)
+    out = codec_native.fast_history_attention(q, cache_k, cache_v, kc, vc, reader, protect,
+                                              value_mean_correction=True)
+    plain = codec_native.fast_history_attention(q, cache_k, cache_v, kc, vc, reader, protect)
+    # the shift, in fp64 from the oracle's pieces
+    key, value = nc.history_codecs(cache_k, cache_v, dev)
+    sname = "bf16" if value.scale_dtype == torch.bfloat16 else "fp16"
+    ov, ok = oracle_codec(value, 0, sname), oracle_codec(key, 0, sname)
+    low = np.arange(128)
+    lat = orc.bf16_to_f32(orc.unpack_latent(ov["packed"], ov["scales"], sh.rV, ov["group"],
+                                            sname, row_index=low)).astype(np.float64)
+    w = orc.bf16_to_f32(ov["w_dec_bf16"]).astype(np.float64)            # [HD, r]
+    cen = orc.bf16_to_f32(ov["centers_bf16"]).astype(np.float64)[np.asarray(ov["ids"])[low]]
+    mean_bf = orc.bf16_to_f32(orc.f32_to_bf16(np.asarray(ov["mean"], np.float32)))
+    full_mean = (lat @ w.T).mean(0) + mean_bf + cen.mean(0)              # [HD]
+    groups = oracle_groups(payload)
+    shift = np.zeros((H, D))
+    g1 = groups[1]
+    for i, h in enumerate(g1["heads"]):
+        vt, vb = orc.reader_tables(ov.get("centers_bf16"), ov.get("mean"), h, g1["v_affine"][i], D)
+        vl = orc.bf16_to_f32(orc.reader_read(ov, low, g1["v_read"][i], vt, vb)).astype(np.float64)
+        projected = vl.mean(0) @ orc.bf16_to_f32(g1["lift"][i]).astype(np.float64)
+        shift[h] = full_mean[h * D:(h + 1) * D] - projected
+    got_shift = codec_native.value_mean_shift(reader, cache_k, cache_v, ~protect, dev)
+    assert np.abs(got_shift[0].cpu().numpy() - shift).max() < 2e-2 * max(1.0, np.abs(shift).max())
+    assert np.abs(shift).max() > 1e-2  # the correction is not trivial here
+    ref, _ = orc.fast_attend(u16(q[0].permute(1, 0, 2)), u16(kc[0].permute(1, 0, 2)),
+                             u16(vc[0].permute(1, 0, 2)), ok, ov, np.arange(128, 192), low,
+                             groups, D ** -0.5, D=D, low_shift=shift)
+    diff, cos = max_abs_cos(out[0].permute(1, 0, 2).float().cpu().numpy(), ref)
+    assert diff <= MAX_ABS and cos >= MIN_COS, (diff, cos)
+    # heads of the identity group (full width) are not corrected
+    assert torch.equal(out[:, 0].view(torch.int16), plain[:, 0].view(torch.int16))
