@@ -259,7 +259,7 @@ __device__ __forceinline__ void load_k_center_rows8(u32x4 (&v)[DK / 16], const C
 #pragma unroll
     for (int e = 0; e < DK / 16; ++e) {
         const int q = 64 * e + lane;
-        v[e] = *reinterpret_cast<const u32x4*>(sm.crow[0][32 * wave + q / PR] + 8 * (q % PR));
+        v[e] = ldg(reinterpret_cast<const u32x4*>(sm.crow[0][32 * wave + q / PR] + 8 * (q % PR)));
     }
 }
 
@@ -350,8 +350,8 @@ __device__ __forceinline__ void decode_codec8(Chunk8Smem& sm, uint16_t* wst, con
         }
     };
     auto issue_codes = [&](int s, u32x4& pk, uint16_t& sb) {
-        pk = *reinterpret_cast<const u32x4*>(prow + 32 * s);
-        sb = srow[(64 * s + 32 * hf) / G];
+        pk = ldg(reinterpret_cast<const u32x4*>(prow + 32 * s));
+        sb = ldg(srow + (64 * s + 32 * hf) / G);
     };
 
     f32x16 acc[NDT];
@@ -781,11 +781,12 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
 // ===================================================== staged schedule
 // Stage: each 256-key chunk of (b, h) is decoded (history) or loaded
 // (current keys) into LDS exactly as for the key-chunk kernel, then written
-// to the workspace as two 128-key tiles.  A tile is two images, the K rows
-// [128 keys][136] and the V^T rows [128 d][136] (keys in V^T column order),
-// each the exact LDS layout that the attention operand reads expect (8
-// padding elements per row), so the flash kernel copies a tile into LDS with
-// plain 1 KB direct-to-LDS loads.
+// to the workspace as two 128-key tiles.  A tile is two row-major images,
+// the K rows [128 keys][128] and the V^T rows [128 d][128] (keys in V^T
+// column order), unpadded: every 128-byte line of an image is written whole,
+// and the flash kernel copies a tile into LDS with 1 KB direct-to-LDS loads
+// whose sources place 16-byte chunk c of row r at chunk c ^ (r % 16), so that
+// its operand reads of 16 consecutive rows hit distinct banks.
 // Flash: one block of eight waves per (b*h, query tile, key split).  Wave w
 // attends query block qt * qpt + w to the split's tiles, which stream
 // through two LDS buffers, and keeps O, the running max and the row sum in
@@ -794,7 +795,7 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
 // schedule this trades the per-chunk partials of every query block (3x the
 // decoded K/V) for one write and a few L2/MALL re-reads of the decoded K/V.
 constexpr int FT_T = 128;                      // keys per tile
-constexpr int FT_ROW = CK_KROW;                // row pitch of both images (elements)
+constexpr int FT_ROW = CK_D;                   // row pitch of both images (elements)
 constexpr int FT_IMG = FT_T * FT_ROW;          // elements per image
 constexpr int FT_TILE = 2 * FT_IMG;            // K image, then V^T image
 constexpr int FT_PIECES = FT_TILE * 2 / 1024;  // 1 KB pieces per tile
@@ -826,9 +827,9 @@ __global__ void __launch_bounds__(C8_THREADS, 1) stage8_kernel(ChunkParams p) {
     for (int hh = 0; hh < halves; ++hh) {
         u32x4* kd = reinterpret_cast<u32x4*>(dst + hh * FT_TILE);
         u32x4* vd = reinterpret_cast<u32x4*>(dst + hh * FT_TILE + FT_IMG);
-        // K rows 128 hh .. +128 (with their padding) are one run of LDS
-        const u32x4* ks = reinterpret_cast<const u32x4*>(&sm.k[FT_T * hh][0]);
-        for (int i = t; i < FT_IMG / 8; i += C8_THREADS) kd[i] = ks[i];
+        // K rows 128 hh .. +128 without their LDS padding
+        for (int i = t; i < FT_T * (FT_ROW / 8); i += C8_THREADS)
+            kd[i] = *reinterpret_cast<const u32x4*>(&sm.k[FT_T * hh + (i >> 4)][8 * (i & 15)]);
         // V^T: the 16 pieces of keys 128 hh .. +128 of each d row
         for (int i = t; i < CK_D * 16; i += C8_THREADS) {
             const int d = i >> 4, c = i & 15;
@@ -837,239 +838,27 @@ __global__ void __launch_bounds__(C8_THREADS, 1) stage8_kernel(ChunkParams p) {
     }
 }
 
-// ------------------------------------------------------------ decode GEMM
-// The history tiles of launches without read-time RoPE or camera come from
-// dtile_kernel instead of stage8_kernel: one codec of one 256-key chunk of
-// one head per block of four waves (two blocks per CU), each wave 64 keys x
-// 128 columns, so that each decoder fragment read from LDS feeds two MFMAs;
-// the tile images are written straight from the accumulators.
-constexpr int DT_THREADS = 256;  // four waves of 64 keys: one chunk of one head
-constexpr int DT_NBUF = 4;       // decoder-slice ring, three slices ahead
-constexpr int DT_AHEAD = 3;
-struct DTileSmem {
-    // decoder slices; after the GEMM the waves' V center rows, or a current
-    // tile's V^T
-    uint16_t ring[DT_NBUF][CK_D * 64];
-    const uint16_t* crow[CK_T];  // center row of each key (the head's columns)
-    float bias[CK_D];
+// ------------------------------------------------------------ current tiles
+// A current-key tile (the uncompressed keys of the chunk being attended):
+// thread t brings keys 4 (t % 32) .. +4, columns 16 (t / 32) .. +16 of K and
+// V (every load before any store); K rows go straight into the image, V
+// through LDS into V^T column order (one 8-byte write of four keys per
+// column).  Keys past the end are zero.
+constexpr int CT_THREADS = 256;
+struct CTileSmem {
+    uint16_t vt[FT_IMG];  // [128 d][128] in V^T column order
 };
-static_assert(DT_NBUF * CK_D * 64 >= FT_IMG, "a current tile's V^T fits in the ring");
-static_assert(DT_NBUF * CK_D * 64 >= DT_THREADS / 64 * 64 * CK_D, "V center rows fit in the ring");
 
-// One codec of a history chunk of head bh: wave w owns keys 64 w .. +64 (two
-// 32-key groups kg) and all 128 columns.  A stage (slice s: 64 ranks) is the
-// decoder slice (128 rows x 64 ranks, into the XOR-swizzled LDS ring by
-// direct-to-LDS loads, the wave's share 4 KB) plus the wave's codes and
-// scales of the slice (a register ring), DT_AHEAD stages ahead; stages
-// complete in issue order, so waiting for stage s is one vmcnt bound.  Lane
-// half hf unpacks ranks 32 hf .. +32 of each slice: k-step j takes ranks
-// 8 j + 32 hf .. +8, logical chunk 4 hf + j of decoder row 32 dt + l32.
-template <int CODEC>
-__device__ __forceinline__ void dtile_history(DTileSmem& sm, const ChunkParams& p, int bh,
-                                              int chunk, int wave, int lane) {
-    const ChunkCodec& cd = p.codec[CODEC];
-    const int t = threadIdx.x, hf = lane >> 5, l32 = lane & 31;
-    const int b = bh / p.H, h = bh % p.H;
-    const int64_t tok0 = (int64_t)chunk * CK_T;
-    const int valid = (int)min((int64_t)CK_T, p.n_rows - tok0);
-    const int R = cd.r, KQ = R >> 6, G = cd.group;
-    const bool cent = cd.has_centers, f16 = cd.scale_dtype == NKV_DTYPE_FP16;
-    // keys past the chunk end take key 0's codes and center (finite, never
-    // attended)
-    sm.crow[t] = cent ? center_row(cd, b, h, p.N, history_row(p, tok0 + (t < valid ? t : 0)))
-                      : nullptr;
-    if (t < CK_D) sm.bias[t] = cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
-    const uint8_t* prow[2];
-    const uint16_t* srow[2];
-#pragma unroll
-    for (int kg = 0; kg < 2; ++kg) {
-        const int kw = 64 * wave + 32 * kg + l32;
-        codec_row_ptrs(cd, b, p.N, history_row(p, tok0 + (kw < valid ? kw : 0)), prow[kg], srow[kg]);
-        prow[kg] += 16 * hf;
-    }
-    __syncthreads();
-
-    // piece e of a slice: decoder rows 8 (4 wave + e) .. +8; lane L brings
-    // logical 16-byte chunk (L % 8) ^ ((row >> 1) & 7) of row 8 piece + L / 8
-    const int piece_row = lane >> 3;
-    const uint16_t* wsrc = cd.w + (int64_t)h * cd.w_hs + (int64_t)piece_row * R;
-    auto issue_slice = [&](int s) {
-        uint16_t* dst = sm.ring[s % DT_NBUF];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int piece = 4 * wave + e;
-            const int ch = (lane & 7) ^ ((4 * (piece & 1) + (piece_row >> 1)) & 7);
-            __builtin_amdgcn_global_load_lds(wsrc + (int64_t)8 * piece * R + 64 * s + 8 * ch,
-                                             NKV_LDS(dst + piece * 512), 16, 0, 0);
-        }
-    };
-    constexpr int STAGE = 4 + 2 + 2;  // vm instructions per stage: slice, codes, scales
-    u32x4 pk[DT_AHEAD][2];
-    uint16_t sc[DT_AHEAD][2];
-    auto issue_codes = [&](int s, int i) {
-#pragma unroll
-        for (int kg = 0; kg < 2; ++kg) {
-            pk[i][kg] = *reinterpret_cast<const u32x4*>(prow[kg] + 32 * s);
-            sc[i][kg] = srow[kg][(64 * s + 32 * hf) / G];
-        }
-    };
-    int wofs[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) wofs[j] = l32 * 64 + 8 * ((4 * hf + j) ^ ((l32 >> 1) & 7));
-    f32x16 acc[2][4];
-#pragma unroll
-    for (int kg = 0; kg < 2; ++kg)
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) acc[kg][dt] = f32x16{};
-
-#pragma unroll
-    for (int i = 0; i < DT_AHEAD; ++i)
-        if (i < KQ) {
-            issue_slice(i);
-            issue_codes(i, i);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    for (int s0 = 0; s0 < KQ; s0 += DT_AHEAD) {
-#pragma unroll
-        for (int i = 0; i < DT_AHEAD; ++i) {
-            const int s = s0 + i;
-            if (s >= KQ) break;
-            static_assert(DT_AHEAD == 3, "the wait bounds below assume three stages ahead");
-            const int later = min(KQ - 1 - s, DT_AHEAD - 1);
-            if (later >= 2) wait_vmcnt<2 * STAGE>();
-            else if (later == 1) wait_vmcnt<STAGE>();
-            else wait_vmcnt<0>();
-            __builtin_amdgcn_s_barrier();
-            if (s + DT_AHEAD < KQ) issue_slice(s + DT_AHEAD);
-            __builtin_amdgcn_sched_barrier(0);
-            const uint16_t* wb = sm.ring[s % DT_NBUF];
-            float scl[2], ns7[2];
-#pragma unroll
-            for (int kg = 0; kg < 2; ++kg) {
-                scl[kg] = f16 ? f16_bits_to_f32(sc[i][kg]) : bf16_bits_to_f32(sc[i][kg]);
-                ns7[kg] = -7.0f * scl[kg];
-            }
-#pragma unroll
-            for (int j = 0; j < 4; ++j) {
-                bf16x8 w[4], z[2];
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) w[dt] = lds_b128(wb + 32 * dt * 64 + wofs[j]);
-#pragma unroll
-                for (int kg = 0; kg < 2; ++kg) z[kg] = unpack8(pk[i][kg][j], scl[kg], ns7[kg]);
-#pragma unroll
-                for (int kg = 0; kg < 2; ++kg)
-#pragma unroll
-                    for (int dt = 0; dt < 4; ++dt)
-                        acc[kg][dt] = CODEC == 0 ? mfma32(w[dt], z[kg], acc[kg][dt])
-                                                 : mfma32(z[kg], w[dt], acc[kg][dt]);
-            }
-            __builtin_amdgcn_sched_barrier(0);
-            if (s + DT_AHEAD < KQ) issue_codes(s + DT_AHEAD, i);
-            __builtin_amdgcn_sched_barrier(0);
-        }
-    }
-    uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + 2 * chunk + (wave >> 1)) * FT_TILE;
-    if (CODEC == 0) {
-        // acc[kg][dt] element i: d = 32 dt + 8 (i/4) + 4 hf + i%4 of key
-        // 64 wave + 32 kg + l32; K = bf16(bf16(acc + bias) + center).  Every
-        // center value is requested before the first store (a store may
-        // alias them, so no load would pass it).
-        u32x2 cv[2][16];
-        if (cent) {
-#pragma unroll
-            for (int kg = 0; kg < 2; ++kg) {
-                const uint16_t* cr = sm.crow[64 * wave + 32 * kg + l32];
-#pragma unroll
-                for (int n = 0; n < 16; ++n)
-                    cv[kg][n] = *reinterpret_cast<const u32x2*>(cr + 32 * (n >> 2) + 8 * (n & 3) + 4 * hf);
-            }
-        }
-#pragma unroll
-        for (int kg = 0; kg < 2; ++kg) {
-            const int kr = 64 * (wave & 1) + 32 * kg + l32;
-#pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const int d = 32 * dt + 8 * g + 4 * hf;
-                    const f32x4 bs = *reinterpret_cast<const f32x4*>(&sm.bias[d]);
-                    float a[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) a[e] = bf16_round(acc[kg][dt][4 * g + e] + bs[e]);
-                    if (cent) {
-                        const u32x2 c2 = cv[kg][4 * dt + g];
-                        a[0] += __uint_as_float(c2[0] << 16);
-                        a[1] += __uint_as_float(c2[0] & 0xffff0000u);
-                        a[2] += __uint_as_float(c2[1] << 16);
-                        a[3] += __uint_as_float(c2[1] & 0xffff0000u);
-                    }
-                    *reinterpret_cast<u32x2*>(img + kr * FT_ROW + d) =
-                        u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
-                }
-        }
-    } else {
-        // acc[kg][dt] element i: key 64 wave + 32 kg + 8 (i/4) + 4 hf + i%4,
-        // d = 32 dt + l32; V = bf16(bf16(acc + bias) + center).  The centers
-        // of keys t0 .. t0+3 at column d come from one transposing LDS read
-        // (ds_read_b64_tr_b16) of the group's center rows: within a group of
-        // 16 lanes, lane j receives element j % 4 of the 8-byte rows that
-        // lanes j / 4, j / 4 + 4, j / 4 + 8, j / 4 + 12 address, so lane
-        // x = a + 4k addresses key t0 + k at columns dbase + 4a .. +4 and
-        // lane j gets the four keys at column dbase + j.  Both groups' rows
-        // are staged (every wave is done with the ring) before any store, so
-        // that waiting for them does not wait for stores.
-        uint16_t* vcen = &sm.ring[0][0] + wave * 64 * CK_D;
-        __syncthreads();
-        if (cent) {
-#pragma unroll
-            for (int e = 0; e < 16; ++e) {
-                const int k = 4 * e + (lane >> 4);
-                __builtin_amdgcn_global_load_lds(sm.crow[64 * wave + k] + 8 * (lane & 15),
-                                                 NKV_LDS(vcen + 4 * e * CK_D), 16, 0, 0);
-            }
-            wait_vmcnt<0>();
-        }
-        const int tr_x = lane & 15;
-        const int tr_off = (tr_x >> 2) * CK_D + 4 * (tr_x & 3) + 16 * ((lane >> 4) & 1);
-        float bs[4];
-#pragma unroll
-        for (int dt = 0; dt < 4; ++dt) bs[dt] = sm.bias[32 * dt + l32];
-#pragma unroll
-        for (int kg = 0; kg < 2; ++kg)
-#pragma unroll
-            for (int g = 0; g < 4; ++g) {
-                const int t0 = 32 * kg + 8 * g + 4 * hf;
-                const int col = vt_col(64 * (wave & 1) + t0);
-#pragma unroll
-                for (int dt = 0; dt < 4; ++dt) {
-                    short4v cen = {};
-                    if (cent)
-                        cen = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                            (__attribute__((address_space(3))) short4v*)(vcen + t0 * CK_D + 32 * dt + tr_off));
-                    float v[4];
-#pragma unroll
-                    for (int e = 0; e < 4; ++e) {
-                        const float a = bf16_round(acc[kg][dt][4 * g + e] + bs[dt]);
-                        v[e] = cent ? a + __uint_as_float((uint32_t)(uint16_t)cen[e] << 16) : a;
-                    }
-                    *reinterpret_cast<u32x2*>(img + FT_IMG + (32 * dt + l32) * FT_ROW + col) =
-                        u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
-                }
-            }
-    }
-}
-
-// A current-key tile: thread t brings keys 4 (t % 32) .. +4, columns
-// 16 (t / 32) .. +16 of K and V (every load before any store); K rows go
-// straight into the image, V through LDS into V^T column order (one 8-byte
-// write of four keys per column).  Keys past the end are zero.
-__device__ __forceinline__ void dtile_current(DTileSmem& sm, const ChunkParams& p, int bh, int ct,
-                                              int t) {
+__global__ void __launch_bounds__(CT_THREADS) ctile_kernel(ChunkParams p) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    CTileSmem& sm = *reinterpret_cast<CTileSmem*>(smem_raw);
+    const int t = threadIdx.x;
+    const int BH = p.B * p.H;
+    const int bh = (int)(blockIdx.x % BH), ct = (int)(blockIdx.x / BH);
     const int b = bh / p.H, h = bh % p.H;
     const int64_t key0 = (int64_t)ct * FT_T;
     const int valid = (int)min((int64_t)FT_T, p.Nc - key0);
     uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + p.ntiles_hist + ct) * FT_TILE;
-    uint16_t* vt = &sm.ring[0][0];  // [128 d][FT_ROW]
     const int k0 = 4 * (t & 31), d0 = 16 * (t >> 5);
     u32x4 kv[4][2], vv[4][2];
 #pragma unroll
@@ -1094,43 +883,273 @@ __device__ __forceinline__ void dtile_current(DTileSmem& sm, const ChunkParams& 
     for (int dd = 0; dd < 16; ++dd) {
         const int x = dd >> 3, w = (dd & 7) >> 1, sh = 16 * (dd & 1);
         auto val = [&](int e) { return (vv[e][x][w] >> sh) & 0xffffu; };
-        *reinterpret_cast<u32x2*>(vt + (d0 + dd) * FT_ROW + col) =
+        *reinterpret_cast<u32x2*>(sm.vt + (d0 + dd) * FT_ROW + col) =
             u32x2{val(0) | (val(1) << 16), val(2) | (val(3) << 16)};
     }
     __syncthreads();
-    for (int i = t; i < CK_D * 16; i += DT_THREADS) {
-        const int d = i >> 4, c = i & 15;
-        *reinterpret_cast<u32x4*>(img + FT_IMG + d * FT_ROW + 8 * c) =
-            *reinterpret_cast<const u32x4*>(vt + d * FT_ROW + 8 * c);
+    for (int i = t; i < CK_D * (FT_ROW / 8); i += CT_THREADS)
+        *reinterpret_cast<u32x4*>(img + FT_IMG + 8 * i) = *reinterpret_cast<const u32x4*>(sm.vt + 8 * i);
+}
+
+// ------------------------------------------------ decode GEMM, resident decoder
+// For codec ranks up to DR_MAXQ * 64 the history tiles come from drtile_kernel:
+// one block of eight waves per (b*h, codec, range of tiles) loads the head's
+// decoder rows into LDS once and keeps them for the whole range, so each
+// decoder element is read from L2 once per block rather than once per 256-key
+// chunk.  The block decodes two tiles at a time: wave w takes keys
+// 32 (w % 4) .. +32 of tile 2 i + w / 4 at all 128 columns, so each unpacked
+// INT4 code feeds four MFMAs, and stores its part of the image from
+// registers (each 128-byte line of a K row is written by one wave, each line
+// of a V^T row by two).  The center rows of every key of the range are
+// resolved once, into LDS, before the first tile, so the tile loop writes no
+// LDS and needs no barrier: each wave runs its tiles at its own pace, one
+// wave's epilogue overlapping another's GEMM on the same SIMD.  Codes are
+// fetched one pair of tiles ahead; the center values of a pair are requested
+// before its GEMM and used after it.
+constexpr int DR_THREADS = 512;
+constexpr int DR_MAXQ = 6;             // 64-rank decoder slices held: r <= 384
+constexpr int DR_SLICE = CK_D * 64;    // elements per slice
+constexpr int DR_MAXT = 24;            // tiles per block (the center-row table)
+struct DResSmem {
+    uint16_t dec[DR_MAXQ * DR_SLICE];      // slice s at s * DR_SLICE: [128 rows][64], chunks swizzled
+    const uint16_t* crow[DR_MAXT * FT_T];  // center row of key k of tile ta + k / 128
+    float bias[CK_D];
+};
+static_assert(sizeof(DResSmem) <= 160 * 1024, "LDS budget");
+
+// A key's center row as a reference loaded ahead of its use: the row is
+// base + clamp(id, 0, nc - 1) * c_rs (the id is the only value that waits on
+// memory when the reference is formed).
+struct CenterRef {
+    const uint16_t* base;
+    int id, nc;
+};
+
+__device__ __forceinline__ CenterRef center_ref(const ChunkCodec& c, int b, int h, int64_t N,
+                                                int64_t row) {
+    if (c.seg) {
+        const NKV_GLOBAL nkv_segment& s = seg_at(c.seg, seg_find(c.seg, c.n_seg, row));
+        const int64_t local = min(max(row - s.row_start, (int64_t)0), s.rows - 1);
+        const uint16_t* base =
+            c.seg_flat ? c.centers + (int64_t)b * c.c_bs + s.center_base * c.c_rs + (int64_t)h * c.c_hs
+                       : s.centers + (int64_t)b * s.centers_batch_stride + (int64_t)h * c.c_hs;
+        return {base, read_id(s.ids, s.id_bytes, (int64_t)b * s.rows + local), s.num_centers};
+    }
+    return {c.centers + (int64_t)b * c.c_bs + (int64_t)h * c.c_hs,
+            read_id(c.ids, c.id_bytes, (int64_t)b * N + row), c.num_centers};
+}
+
+__device__ __forceinline__ const uint16_t* center_ptr(const CenterRef& r, int64_t c_rs) {
+    return r.base + (int64_t)min(max(r.id, 0), r.nc - 1) * c_rs;
+}
+
+// One codec of tiles [ta, tb) (tb - ta <= DR_MAXT) of head bh, two at a time
+// (pair i: tiles ta + 2 i and ta + 2 i + 1).
+template <int CODEC, int KQ>
+__device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p, int bh, int ta,
+                                             int tb, int wave, int lane) {
+    const ChunkCodec& cd = p.codec[CODEC];
+    const int t = threadIdx.x, hf = lane >> 5, l32 = lane & 31;
+    const int kq = wave & 3, tp = wave >> 2;
+    const int b = bh / p.H, h = bh % p.H;
+    const int R = cd.r, G = cd.group;
+    const bool cent = cd.has_centers, f16 = cd.scale_dtype == NKV_DTYPE_FP16;
+    // the head's decoder rows, KQ slices of 16 pieces (8 rows x 128 B) taken
+    // by the waves in turn: lane L of a piece brings logical chunk
+    // (L % 8) ^ ((row >> 1) & 7) of its row 8 piece + L / 8
+    {
+        const uint16_t* wsrc = cd.w + (int64_t)h * cd.w_hs;
+        for (int e = wave; e < KQ * 16; e += DR_THREADS / 64) {
+            const int s = e >> 4, pc = e & 15, row = 8 * pc + (lane >> 3);
+            const int ch = (lane & 7) ^ ((row >> 1) & 7);
+            __builtin_amdgcn_global_load_lds(wsrc + (int64_t)row * R + 64 * s + 8 * ch,
+                                             NKV_LDS(sm.dec + s * DR_SLICE + pc * 512), 16, 0, 0);
+        }
+    }
+    if (t < CK_D) sm.bias[t] = cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
+    // codec row of key k of tile `tile`; keys past the last row take key 0's
+    // codes and center (finite, never attended)
+    auto key_row = [&](int tile, int k) {
+        const int64_t tok0 = (int64_t)tile * FT_T;
+        const int valid = (int)min((int64_t)FT_T, p.n_rows - tok0);
+        return history_row(p, tok0 + (k < valid ? k : 0));
+    };
+    // this lane's key: 32 kq + l32 of tile 2 i + tp of the pair
+    const int key = 32 * kq + l32;
+    // scale of this lane's ranks 64 s + 32 hf .. +32 (one group: group % 32 == 0)
+    int sidx[KQ];
+#pragma unroll
+    for (int s = 0; s < KQ; ++s) sidx[s] = (64 * s + 32 * hf) / G;
+    auto fetch = [&](int tile, u32x4 (&pk)[KQ], uint16_t (&sc)[KQ]) {
+        const uint8_t* prow;
+        const uint16_t* srow;
+        codec_row_ptrs(cd, b, p.N, key_row(tile < tb ? tile : ta, key), prow, srow);
+        prow += 16 * hf;
+#pragma unroll
+        for (int s = 0; s < KQ; ++s) {
+            pk[s] = ldg(reinterpret_cast<const u32x4*>(prow + 32 * s));
+            sc[s] = ldg(srow + sidx[s]);
+        }
+    };
+    // center values of this lane's tile (table rows from crow): K, the 32
+    // columns 32 dt + 8 g + 4 hf .. +4 of this lane's key; V, column
+    // d = 32 dt + l32 of keys 32 kq + 8 g + 4 hf + e
+    constexpr int NCV = CODEC == 0 ? 32 : 64;
+    auto load_centers = [&](uint32_t (&cv)[NCV], const uint16_t* const* crow) {
+        if (CODEC == 0) {
+            const uint16_t* cr = crow[key];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                for (int g = 0; g < 4; ++g) {
+                    const u32x2 v = ldg(reinterpret_cast<const u32x2*>(cr + 32 * dt + 8 * g + 4 * hf));
+                    cv[2 * (4 * dt + g)] = v[0];
+                    cv[2 * (4 * dt + g) + 1] = v[1];
+                }
+        } else {
+#pragma unroll
+            for (int g = 0; g < 4; ++g)
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const uint16_t* cr = crow[32 * kq + 8 * g + 4 * hf + e];
+#pragma unroll
+                    for (int dt = 0; dt < 4; ++dt) cv[16 * dt + 4 * g + e] = ldg(cr + 32 * dt + l32);
+                }
+        }
+    };
+    int wofs[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) wofs[j] = l32 * 64 + 8 * ((4 * hf + j) ^ ((l32 >> 1) & 7));
+    u32x4 pk[KQ], pn[KQ];
+    uint16_t sc[KQ], sn[KQ];
+    uint32_t cv[NCV];
+    fetch(ta + tp, pk, sc);
+    // the center row of every key of the range: all references are requested
+    // before the first is resolved
+    if (cent) {
+        constexpr int PER = DR_MAXT * FT_T / DR_THREADS;
+        const int nk = (tb - ta) * FT_T;
+        CenterRef r[PER];
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int k = t + e * DR_THREADS;
+            if (k < nk) r[e] = center_ref(cd, b, h, p.N, key_row(ta + (k >> 7), k & 127));
+        }
+#pragma unroll
+        for (int e = 0; e < PER; ++e) {
+            const int k = t + e * DR_THREADS;
+            if (k < nk) sm.crow[k] = center_ptr(r[e], cd.c_rs);
+        }
+    }
+    wait_vmcnt<0>();
+    __syncthreads();
+    const int npairs = (tb - ta + 1) / 2;
+    for (int i = 0; i < npairs; ++i) {
+        const int tile = ta + 2 * i + tp;
+        // the last pair of an odd range has no second tile: its waves are done
+        if (tile >= tb) break;
+        if (cent) load_centers(cv, sm.crow + (tile - ta) * FT_T);
+        if (tile + 2 < tb) fetch(tile + 2, pn, sn);
+        f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
+#pragma unroll
+        for (int s = 0; s < KQ; ++s) {
+            const float scl = f16 ? f16_bits_to_f32(sc[s]) : bf16_bits_to_f32(sc[s]);
+            const float ns7 = -7.0f * scl;
+            const uint16_t* ws = sm.dec + s * DR_SLICE;
+#pragma unroll
+            for (int j = 0; j < 4; ++j) {
+                const bf16x8 z = unpack8(pk[s][j], scl, ns7);
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const bf16x8 w = lds_b128(ws + 32 * dt * 64 + wofs[j]);
+                    acc[dt] = CODEC == 0 ? mfma32(w, z, acc[dt]) : mfma32(z, w, acc[dt]);
+                }
+            }
+        }
+        {
+            uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + tile) * FT_TILE + CODEC * FT_IMG;
+            if (CODEC == 0) {
+                // acc[dt] element i: d = 32 dt + 8 (i/4) + 4 hf + i%4 of this
+                // lane's key; K = bf16(bf16(acc + bias) + center)
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        const int d = 32 * dt + 8 * g + 4 * hf;
+                        const f32x4 bs = *reinterpret_cast<const f32x4*>(&sm.bias[d]);
+                        float a[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) a[e] = bf16_round(acc[dt][4 * g + e] + bs[e]);
+                        if (cent) {
+                            const uint32_t c0 = cv[2 * (4 * dt + g)], c1 = cv[2 * (4 * dt + g) + 1];
+                            a[0] += __uint_as_float(c0 << 16);
+                            a[1] += __uint_as_float(c0 & 0xffff0000u);
+                            a[2] += __uint_as_float(c1 << 16);
+                            a[3] += __uint_as_float(c1 & 0xffff0000u);
+                        }
+                        *reinterpret_cast<u32x2*>(img + key * FT_ROW + d) =
+                            u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+                    }
+            } else {
+                // acc[dt] element i: key 32 kq + 8 (i/4) + 4 hf + i%4, d = 32 dt
+                // + l32; V = bf16(bf16(acc + bias) + center), written to V^T in
+                // the attention's column order
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt) {
+                    const float bs = sm.bias[32 * dt + l32];
+#pragma unroll
+                    for (int g = 0; g < 4; ++g) {
+                        float v[4];
+#pragma unroll
+                        for (int e = 0; e < 4; ++e) {
+                            const float a = bf16_round(acc[dt][4 * g + e] + bs);
+                            v[e] = cent ? a + __uint_as_float((cv[16 * dt + 4 * g + e] & 0xffffu) << 16) : a;
+                        }
+                        *reinterpret_cast<u32x2*>(img + (32 * dt + l32) * FT_ROW +
+                                                   vt_col(32 * kq + 8 * g + 4 * hf)) =
+                            u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
+                    }
+                }
+            }
+        }
+#pragma unroll
+        for (int s = 0; s < KQ; ++s) {
+            pk[s] = pn[s];
+            sc[s] = sn[s];
+        }
     }
 }
 
-// Work items: (b*h, history chunk, codec) with the codec fastest and b*h
-// next, so that one head's decoder rows and centers of one codec stay on one
-// XCD (blockIdx % 8) when B*H is a multiple of 4; then the current tiles.
-__global__ void __launch_bounds__(DT_THREADS, 2) dtile_kernel(ChunkParams p) {
+// Blocks: (codec, b*h) fastest -- with B*H a multiple of 4 every range of one
+// head's codec runs on one XCD (blockIdx % 8) and shares its decoder rows in
+// L2 -- then the `ranges` tile ranges of each.  codecs: 3 = both (K and V
+// have KQ slices), 1 = K only, 2 = V only.
+template <int KQ>
+__global__ void __launch_bounds__(DR_THREADS, 1) drtile_kernel(ChunkParams p, int ranges, int codecs) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    DTileSmem& sm = *reinterpret_cast<DTileSmem*>(smem_raw);
-    const int t = threadIdx.x, lane = t & 63;
-    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
-    const int BH = p.B * p.H;
-    const int64_t nh = (int64_t)BH * p.ntiles_hist;  // two codecs per history chunk
-    const int64_t item = blockIdx.x;
-    if (item < nh) {
-        const int64_t r = item >> 1;
-        const int bh = (int)(r % BH), chunk = (int)(r / BH);
-        if (item & 1) dtile_history<1>(sm, p, bh, chunk, wave, lane);
-        else dtile_history<0>(sm, p, bh, chunk, wave, lane);
-    } else {
-        const int64_t c = item - nh;
-        dtile_current(sm, p, (int)(c % BH), (int)(c / BH), t);
-    }
+    DResSmem& sm = *reinterpret_cast<DResSmem*>(smem_raw);
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int nc = codecs == 3 ? 2 : 1;
+    const int np = nc * p.B * p.H;
+    const int pair = (int)(blockIdx.x % np), rg = (int)(blockIdx.x / np);
+    const int cc = codecs == 3 ? pair % 2 : codecs - 1, bh = pair / nc;
+    const int T = (int)cdiv(p.n_rows, FT_T);
+    const int ta = (int)((int64_t)rg * T / ranges), tb = (int)((int64_t)(rg + 1) * T / ranges);
+    if (ta >= tb) return;
+    if (cc == 0) drtile_range<0, KQ>(sm, p, bh, ta, tb, wave, lane);
+    else drtile_range<1, KQ>(sm, p, bh, ta, tb, wave, lane);
 }
 
+// The two tile buffers as [K0][K1][V0][V1]: a buffer's images sit 32 KB
+// from the other buffer's, so that every operand read is one per-lane
+// register plus an immediate offset (below 64 KB) for both buffers.
 struct FlashSmem {
-    uint16_t buf[2][FT_TILE];
+    uint16_t k[2][FT_IMG];
+    uint16_t v[2][FT_IMG];
 };
 static_assert(sizeof(FlashSmem) <= 160 * 1024, "LDS budget");
+constexpr int FT_IMG_BYTES = FT_IMG * 2;
 
 // MASK: the current keys are attended under p.cur_mask (the history tiles
 // never are).
@@ -1152,12 +1171,17 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
     const int t1 = (int)((int64_t)(split + 1) * p.ntiles / p.splits);
     const int qb = qt * p.qpt + wave;
     const bool active = wave < p.qpt && qb < p.qblocks;
-    const uint16_t* src = p.tiles + (int64_t)bh * p.ntiles * FT_TILE + 8 * lane;
+    // tile i of the split goes to buffer i % 2; piece e (1 KB, 4 rows) of a
+    // tile: lane L brings chunk (L % 16) ^ (row % 16) of row 4 e + L / 16
+    const uint16_t* src = p.tiles + (int64_t)bh * p.ntiles * FT_TILE + (lane >> 4) * FT_ROW;
     auto issue = [&](int tile) {
         const uint16_t* s = src + (int64_t)tile * FT_TILE;
-        uint16_t* d = sm.buf[tile & 1];
-        for (int e = wave; e < FT_PIECES; e += C8_WAVES)
-            __builtin_amdgcn_global_load_lds(s + 512 * e, NKV_LDS(d + 512 * e), 16, 0, 0);
+        const int bi = (tile - t0) & 1;
+        for (int e = wave; e < FT_PIECES; e += C8_WAVES) {
+            const int ch = (lane & 15) ^ ((4 * e + (lane >> 4)) & 15);
+            uint16_t* d = e < FT_PIECES / 2 ? sm.k[bi] + 512 * e : sm.v[bi] + 512 * (e - FT_PIECES / 2);
+            __builtin_amdgcn_global_load_lds(s + 512 * e + 8 * ch, NKV_LDS(d), 16, 0, 0);
+        }
     };
     const int hf = lane >> 5, l32 = lane & 31;
     const float c = p.scale_log2;
@@ -1167,9 +1191,22 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
     const int64_t q0 = (int64_t)qb * 32;
     if (active) load_q_block<CK_D>(qf, p, b, h, q0, q0, lane);
     if (t0 < t1) issue(t0);
-    uint32_t koff = l32 * FT_ROW + W::HALF * hf, voff = FT_IMG + l32 * FT_ROW + 8 * hf;
-    asm volatile("" : "+v"(koff));
-    asm volatile("" : "+v"(voff));
+    // byte offsets in buffer 0 of this lane's operand fragments: K row l32
+    // (+ 32 j), logical chunk 8 (kk / 4) + 4 hf + kk % 4; V^T row l32 (+ 32
+    // (t % 4)), logical chunk 4 j + 2 (t / 4) + hf; each at chunk ^ (l32 % 16)
+    uint32_t kofs[KS], vofs[8];
+#pragma unroll
+    for (int kk = 0; kk < KS; ++kk) {
+        const int chunk = (W::block(kk) + W::HALF * hf) >> 3;
+        kofs[kk] = 2 * (l32 * FT_ROW + 8 * (chunk ^ (l32 & 15)));
+        asm volatile("" : "+v"(kofs[kk]));
+    }
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+        const int chunk = 4 * (i >> 1) + 2 * (i & 1) + hf;
+        vofs[i] = 2 * FT_IMG * 2 + 2 * (l32 * FT_ROW + 8 * (chunk ^ (l32 & 15)));
+        asm volatile("" : "+v"(vofs[i]));
+    }
     const uint32_t* mbase = nullptr;
     if (MASK && active) {
         const int64_t qi = min(q0 + l32, p.Q - 1);
@@ -1180,7 +1217,10 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] = f32x16{};
     float m = -INFINITY, l = 0.0f;
-    for (int tile = t0; tile < t1; ++tile) {
+    // one tile in buffer BI (the tile loop runs two at a time, so that the
+    // buffer's offsets are immediates)
+    auto run_tile = [&](int tile, auto bi_tag) {
+        constexpr int BI = decltype(bi_tag)::value;
         wait_loads_and_lds();
         __builtin_amdgcn_s_barrier();
         // the other buffer's last readers have passed the barrier
@@ -1188,12 +1228,14 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
         const bool cur = tile >= p.ntiles_hist;
         const int64_t key0 = (int64_t)(cur ? tile - p.ntiles_hist : tile) * FT_T;
         const int valid = (int)min((int64_t)FT_T, (cur ? p.Nc : p.n_rows) - key0);
-        if (!active || valid <= 0) continue;
-        const uint16_t* kbase = sm.buf[tile & 1] + koff;
-        const uint16_t* vbase = sm.buf[tile & 1] + voff;
-        auto lds_k = [&](int j, int kk) { return lds_b128(kbase + 32 * j * FT_ROW + W::block(kk)); };
+        if (!active || valid <= 0) return;
+        auto lds_k = [&](int j, int kk) {
+            return lds_b128(reinterpret_cast<const uint16_t*>(
+                smem_raw + kofs[kk] + BI * FT_IMG_BYTES + j * 32 * FT_ROW * 2));
+        };
         auto lds_v = [&](int j, int t) {
-            return lds_b128(vbase + 32 * (t & 3) * FT_ROW + 32 * j + 16 * (t >> 2));
+            return lds_b128(reinterpret_cast<const uint16_t*>(
+                smem_raw + vofs[2 * j + (t >> 2)] + BI * FT_IMG_BYTES + (t & 3) * 32 * FT_ROW * 2));
         };
         const uint32_t* mrow = MASK && cur ? mbase + (key0 >> 5) : nullptr;
 #pragma unroll
@@ -1201,7 +1243,9 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
 #pragma unroll
         for (int t = 0; t < 8; ++t) vf[t] = lds_v(0, t);
         const int nsub = (valid + 31) >> 5;
-        for (int j = 0; j < nsub; ++j) {
+#pragma unroll
+        for (int j = 0; j < FT_T / 32; ++j) {
+            if (j >= nsub) break;
             __builtin_amdgcn_s_setprio(1);
             f32x16 s = mfma32(kf[0], qf[0], f32x16{});
 #pragma unroll
@@ -1263,6 +1307,10 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
                 for (int t = 0; t < 8; ++t) vf[t] = lds_v(j + 1, t);
             }
         }
+    };
+    for (int tile = t0; tile < t1; tile += 2) {
+        run_tile(tile, std::integral_constant<int, 0>{});
+        if (tile + 1 < t1) run_tile(tile + 1, std::integral_constant<int, 1>{});
     }
     if (active) store_partial(p, bh, split, q0, o, m, halfwave_sum(l), lane);
 }
@@ -1519,14 +1567,39 @@ size_t staged_tile_bytes(const ChunkLaunchDesc& d, const FlashPlan& f) {
     return (size_t)d.B * d.H * f.ntiles * FT_TILE * sizeof(uint16_t);
 }
 
-// History tiles from the decode GEMM (dtile_kernel); with read-time RoPE or
-// camera, from stage8_kernel's in-LDS decode.
-bool staged_gemm(const ChunkLaunchDesc& d) { return d.n_rows > 0 && !rope_on(d.rope) && !d.cam.mats; }
+// History tiles from the decode GEMM with the decoder held in LDS
+// (drtile_kernel, current tiles from ctile_kernel); with read-time RoPE or
+// camera, or ranks above what LDS holds, both from stage8_kernel's decode.
+bool staged_gemm(const ChunkLaunchDesc& d) {
+    return d.n_rows > 0 && !rope_on(d.rope) && !d.cam.mats && d.key.r <= 64 * DR_MAXQ &&
+           d.value.r <= 64 * DR_MAXQ;
+}
 
 size_t staged_workspace(const ChunkLaunchDesc& d) {
     const FlashPlan f = flash_plan(d);
     const size_t rows = (size_t)d.B * d.H * f.splits * cdiv(d.Q, 32) * 32;
     return staged_tile_bytes(d, f) + rows * CK_D * sizeof(uint16_t) + rows * 2 * sizeof(float);
+}
+
+template <int KQ>
+int drtile_launch_kq(const ChunkParams& p, int64_t blocks, int ranges, int codecs, hipStream_t s) {
+    const int rc = set_smem(drtile_kernel<KQ>, sizeof(DResSmem));
+    if (rc) return rc;
+    drtile_kernel<KQ><<<dim3((unsigned)blocks), DR_THREADS, sizeof(DResSmem), s>>>(p, ranges, codecs);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+int drtile_launch(int kq, const ChunkParams& p, int64_t blocks, int ranges, int codecs,
+                  hipStream_t s) {
+    switch (kq) {
+        case 1: return drtile_launch_kq<1>(p, blocks, ranges, codecs, s);
+        case 2: return drtile_launch_kq<2>(p, blocks, ranges, codecs, s);
+        case 3: return drtile_launch_kq<3>(p, blocks, ranges, codecs, s);
+        case 4: return drtile_launch_kq<4>(p, blocks, ranges, codecs, s);
+        case 5: return drtile_launch_kq<5>(p, blocks, ranges, codecs, s);
+        default: return drtile_launch_kq<6>(p, blocks, ranges, codecs, s);
+    }
 }
 
 // Stage, flash, combine; p holds everything but the staged fields.
@@ -1546,17 +1619,34 @@ int staged_launch(hipStream_t s, const ChunkLaunchDesc& d, ChunkParams p, void* 
                                            staged_tile_bytes(d, f));
     p.part_ml = reinterpret_cast<float*>(p.part_o + rows * CK_D);
     const bool gemm = staged_gemm(d);
-    int rc = gemm ? set_smem(dtile_kernel, sizeof(DTileSmem)) : set_smem(stage8_kernel, sizeof(Chunk8Smem));
+    int rc = gemm ? set_smem(ctile_kernel, sizeof(CTileSmem)) : set_smem(stage8_kernel, sizeof(Chunk8Smem));
     if (!rc) rc = p.cur_mask ? set_smem(flash8_kernel<true>, sizeof(FlashSmem))
                              : set_smem(flash8_kernel<false>, sizeof(FlashSmem));
     if (rc) return rc;
     if (gemm) {
-        const int64_t items = BH * f.ntiles_hist + BH * (f.ntiles - f.ntiles_hist);
-        dtile_kernel<<<dim3((unsigned)items), DT_THREADS, sizeof(DTileSmem), s>>>(p);
+        // the current tiles, then the history with the decoder held in LDS:
+        // ranges per (head, codec) so that the blocks fill the CUs once
+        const int64_t cur = BH * (f.ntiles - f.ntiles_hist);
+        if (cur > 0) {
+            ctile_kernel<<<dim3((unsigned)cur), CT_THREADS, sizeof(CTileSmem), s>>>(p);
+            NKV_LAUNCH_CHECK();
+        }
+        const int64_t T = cdiv(d.n_rows, FT_T);
+        const int qk = d.key.r >> 6, qv = d.value.r >> 6;
+        // both codecs in one launch when their ranks agree
+        for (int codecs : {qk == qv ? 3 : 1, qk == qv ? 0 : 2}) {
+            if (!codecs) continue;
+            const int64_t np = (codecs == 3 ? 2 : 1) * BH;
+            // enough ranges to fill the CUs once, each at most DR_MAXT tiles
+            const int ranges = (int)std::max<int64_t>(
+                std::max<int64_t>(1, std::min<int64_t>(T, FT_CUS / np)), cdiv(T, DR_MAXT));
+            rc = drtile_launch(codecs == 2 ? qv : qk, p, np * ranges, ranges, codecs, s);
+            if (rc) return rc;
+        }
     } else {
         stage8_kernel<<<dim3((unsigned)(BH * f.ntiles / 2)), C8_THREADS, sizeof(Chunk8Smem), s>>>(p);
+        NKV_LAUNCH_CHECK();
     }
-    NKV_LAUNCH_CHECK();
     // the kernel events bracket the attention (flash) kernel
     if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
     const dim3 grid((unsigned)(BH * f.qtiles * f.splits));

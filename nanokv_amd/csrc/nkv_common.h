@@ -94,11 +94,21 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
 
 __host__ __device__ __forceinline__ int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// A load from device (global) memory through a pointer whose address space
+// the compiler cannot infer (one read from a table in memory or from LDS).
+// Such loads are otherwise flat, and flat loads also count against lgkmcnt:
+// every wait for an LDS read would then wait for them as well.
+#define NKV_GLOBAL __attribute__((address_space(1)))
+template <typename T>
+__device__ __forceinline__ T ldg(const T* p) {
+    return *(const NKV_GLOBAL T*)p;
+}
+
 // ---------------------------------------------------------------- MFMA / LDS helpers
 __device__ __forceinline__ int read_id(const void* ids, int id_bytes, int64_t i) {
-    if (id_bytes == 1) return reinterpret_cast<const uint8_t*>(ids)[i];
-    if (id_bytes == 2) return reinterpret_cast<const uint16_t*>(ids)[i];
-    return reinterpret_cast<const int32_t*>(ids)[i];
+    if (id_bytes == 1) return ldg(reinterpret_cast<const uint8_t*>(ids) + i);
+    if (id_bytes == 2) return ldg(reinterpret_cast<const uint16_t*>(ids) + i);
+    return ldg(reinterpret_cast<const int32_t*>(ids) + i);
 }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {

@@ -36,13 +36,19 @@ struct ChunkCodec {
 // Segment holding codec row `row` of a table in row order, contiguous from
 // row 0 (binary search; rows outside the table give its first or last).
 __device__ __forceinline__ int seg_find(const nkv_segment* seg, int n, int64_t row) {
+    const NKV_GLOBAL nkv_segment* sg = (const NKV_GLOBAL nkv_segment*)seg;
     int lo = 0, hi = n - 1;
     while (lo < hi) {
         const int mid = (lo + hi + 1) >> 1;
-        if (seg[mid].row_start <= row) lo = mid;
+        if (sg[mid].row_start <= row) lo = mid;
         else hi = mid - 1;
     }
     return lo;
+}
+
+// Segment `i` of a device segment table, read as global memory.
+__device__ __forceinline__ const NKV_GLOBAL nkv_segment& seg_at(const nkv_segment* seg, int i) {
+    return ((const NKV_GLOBAL nkv_segment*)seg)[i];
 }
 
 // Packed-code and scale rows of codec row `row` of batch item b (N rows per
@@ -51,7 +57,7 @@ __device__ __forceinline__ void codec_row_ptrs(const ChunkCodec& c, int b, int64
                                                const uint8_t*& prow, const uint16_t*& srow) {
     const int NG = c.r / c.group;
     if (c.seg) {
-        const nkv_segment& s = c.seg[seg_find(c.seg, c.n_seg, row)];
+        const NKV_GLOBAL nkv_segment& s = seg_at(c.seg, seg_find(c.seg, c.n_seg, row));
         const int64_t local = min(max(row - s.row_start, (int64_t)0), s.rows - 1);
         const int64_t tok = (int64_t)b * s.rows + local;
         prow = s.packed + tok * (c.r / 2);
@@ -69,7 +75,7 @@ __device__ __forceinline__ void codec_row_ptrs(const ChunkCodec& c, int b, int64
 __device__ __forceinline__ const uint16_t* center_row(const ChunkCodec& c, int b, int h, int64_t N,
                                                       int64_t row) {
     if (c.seg) {
-        const nkv_segment& s = c.seg[seg_find(c.seg, c.n_seg, row)];
+        const NKV_GLOBAL nkv_segment& s = seg_at(c.seg, seg_find(c.seg, c.n_seg, row));
         const int64_t local = min(max(row - s.row_start, (int64_t)0), s.rows - 1);
         int id = read_id(s.ids, s.id_bytes, (int64_t)b * s.rows + local);
         id = min(max(id, 0), s.num_centers - 1);

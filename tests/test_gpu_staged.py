@@ -64,6 +64,19 @@ def test_staged_ranks(dev):
     _check(Scenario(H=3, N=530, Q=1100, Nc=60, rK=64, rV=256, G=32, C=8, seed=5), dev)
 
 
+def test_staged_ranks_at_resident_limit(dev):
+    """K at the largest rank the decode kernel holds in LDS (384, six
+    slices) and V at one slice, in two launches."""
+    _check(Scenario(H=2, N=600, Q=1030, Nc=50, rK=384, rV=64, G=64, C=8, seed=15), dev)
+
+
+def test_staged_multi_tile_ranges(dev):
+    """Blocks of the resident-decoder kernel that decode several pairs of
+    tiles, with odd tile counts per block (63 tiles over 8 ranges per head
+    and codec), and a ragged last tile."""
+    _check(Scenario(H=16, N=8000, Q=1024, Nc=40, rK=384, rV=384, G=32, C=16, seed=16), dev)
+
+
 @pytest.mark.parametrize("rows", ["scattered", "empty"])
 def test_staged_history_rows(dev, rows):
     sc = Scenario(H=2, N=800, Q=1050, Nc=70, rK=128, rV=128, G=32, C=16, seed=6)
