@@ -132,6 +132,13 @@ static_assert(CK_T * CK_D <= CK_T * CK_KROW, "V centers are staged in the K regi
 
 #define NKV_LDS(p) ((__attribute__((address_space(3))) void*)(p))
 
+// one 16-byte-per-lane global -> LDS DMA (the 64 lanes fill 1 KB at l); a
+// function of its own so that kernel templates name no target builtin in
+// their bodies (the host pass then instantiates them for every width)
+__device__ __forceinline__ void dma16(const void* g, void* l) {
+    __builtin_amdgcn_global_load_lds(g, NKV_LDS(l), 16, 0, 0);
+}
+
 // s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits [3:0] and [15:14]; the
 // other counters at their maxima, i.e. not waited on)
 template <int N>
@@ -796,10 +803,24 @@ __global__ void __launch_bounds__(C8_THREADS, 1) chunk8_kernel(ChunkParams p) {
 // decoded K/V) for one write and a few L2/MALL re-reads of the decoded K/V.
 constexpr int FT_T = 128;                      // keys per tile
 constexpr int FT_ROW = CK_D;                   // row pitch of both images (elements)
-constexpr int FT_IMG = FT_T * FT_ROW;          // elements per image
-constexpr int FT_TILE = 2 * FT_IMG;            // K image, then V^T image
-constexpr int FT_PIECES = FT_TILE * 2 / 1024;  // 1 KB pieces per tile
-static_assert(FT_TILE * 2 % 1024 == 0, "a tile must be whole 1 KB pieces");
+constexpr int FT_IMG = FT_T * FT_ROW;          // elements per V^T image (and K at DK = 128)
+constexpr int FT_TILE = 2 * FT_IMG;            // K image, then V^T image (DK = 128)
+
+// Tile geometry at K/Q width DK: the K image [128 keys][DK], then the V^T
+// image [128 d][128].  K row r keeps logical 16-byte chunk c at chunk
+// c ^ kswz(r), V^T row r at c ^ (r % 16), so that 16 consecutive rows read at
+// one logical chunk hit distinct banks (rows of 16 chunks fill all 64 banks,
+// rows of 8 or 4 chunks repeat every 2 or 4 rows).
+template <int DK>
+struct TileFmt {
+    static constexpr int K_IMG = FT_T * DK;         // elements
+    static constexpr int TILE = K_IMG + FT_IMG;     // elements
+    static constexpr int CPR = DK / 8;              // chunks per K row
+    static constexpr int K_PIECES = K_IMG * 2 / 1024;
+    static constexpr int PIECES = TILE * 2 / 1024;
+    __device__ static int kswz(int r) { return (r / (16 / CPR)) % CPR; }
+};
+static_assert(TileFmt<32>::K_IMG * 2 % 1024 == 0, "a K image must be whole 1 KB pieces");
 static_assert(CK_T == 2 * FT_T, "two tiles per chunk");
 
 // s_waitcnt vmcnt(0) lgkmcnt(0): the wave's loads have landed and its LDS
@@ -944,29 +965,32 @@ __device__ __forceinline__ const uint16_t* center_ptr(const CenterRef& r, int64_
 }
 
 // One codec of tiles [ta, tb) (tb - ta <= DR_MAXT) of head bh, two at a time
-// (pair i: tiles ta + 2 i and ta + 2 i + 1).
-template <int CODEC, int KQ>
+// (pair i: tiles ta + 2 i and ta + 2 i + 1), K at width DK (V at 128).
+template <int CODEC, int KQ, int DK>
 __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p, int bh, int ta,
                                              int tb, int wave, int lane) {
+    using TF = TileFmt<DK>;
+    constexpr int W = CODEC == 0 ? DK : CK_D;  // decoded columns
+    constexpr int NDT = W / 32;                 // 32-column MFMA tiles per wave
     const ChunkCodec& cd = p.codec[CODEC];
     const int t = threadIdx.x, hf = lane >> 5, l32 = lane & 31;
     const int kq = wave & 3, tp = wave >> 2;
     const int b = bh / p.H, h = bh % p.H;
     const int R = cd.r, G = cd.group;
     const bool cent = cd.has_centers, f16 = cd.scale_dtype == NKV_DTYPE_FP16;
-    // the head's decoder rows, KQ slices of 16 pieces (8 rows x 128 B) taken
-    // by the waves in turn: lane L of a piece brings logical chunk
+    // the head's decoder rows, KQ slices of W / 8 pieces (8 rows x 128 B)
+    // taken by the waves in turn: lane L of a piece brings logical chunk
     // (L % 8) ^ ((row >> 1) & 7) of its row 8 piece + L / 8
     {
         const uint16_t* wsrc = cd.w + (int64_t)h * cd.w_hs;
-        for (int e = wave; e < KQ * 16; e += DR_THREADS / 64) {
-            const int s = e >> 4, pc = e & 15, row = 8 * pc + (lane >> 3);
+        for (int e = wave; e < KQ * (W / 8); e += DR_THREADS / 64) {
+            const int s = e / (W / 8), pc = e % (W / 8), row = 8 * pc + (lane >> 3);
             const int ch = (lane & 7) ^ ((row >> 1) & 7);
             __builtin_amdgcn_global_load_lds(wsrc + (int64_t)row * R + 64 * s + 8 * ch,
                                              NKV_LDS(sm.dec + s * DR_SLICE + pc * 512), 16, 0, 0);
         }
     }
-    if (t < CK_D) sm.bias[t] = cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
+    if (t < W) sm.bias[t] = cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
     // codec row of key k of tile `tile`; keys past the last row take key 0's
     // codes and center (finite, never attended)
     auto key_row = [&](int tile, int k) {
@@ -991,15 +1015,15 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
             sc[s] = ldg(srow + sidx[s]);
         }
     };
-    // center values of this lane's tile (table rows from crow): K, the 32
+    // center values of this lane's tile (table rows from crow): K, the
     // columns 32 dt + 8 g + 4 hf .. +4 of this lane's key; V, column
     // d = 32 dt + l32 of keys 32 kq + 8 g + 4 hf + e
-    constexpr int NCV = CODEC == 0 ? 32 : 64;
+    constexpr int NCV = CODEC == 0 ? 8 * NDT : 64;
     auto load_centers = [&](uint32_t (&cv)[NCV], const uint16_t* const* crow) {
         if (CODEC == 0) {
             const uint16_t* cr = crow[key];
 #pragma unroll
-            for (int dt = 0; dt < 4; ++dt)
+            for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
                 for (int g = 0; g < 4; ++g) {
                     const u32x2 v = ldg(reinterpret_cast<const u32x2*>(cr + 32 * dt + 8 * g + 4 * hf));
@@ -1050,7 +1074,9 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
         if (tile >= tb) break;
         if (cent) load_centers(cv, sm.crow + (tile - ta) * FT_T);
         if (tile + 2 < tb) fetch(tile + 2, pn, sn);
-        f32x16 acc[4] = {f32x16{}, f32x16{}, f32x16{}, f32x16{}};
+        f32x16 acc[NDT];
+#pragma unroll
+        for (int dt = 0; dt < NDT; ++dt) acc[dt] = f32x16{};
 #pragma unroll
         for (int s = 0; s < KQ; ++s) {
             const float scl = f16 ? f16_bits_to_f32(sc[s]) : bf16_bits_to_f32(sc[s]);
@@ -1060,19 +1086,19 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
             for (int j = 0; j < 4; ++j) {
                 const bf16x8 z = unpack8(pk[s][j], scl, ns7);
 #pragma unroll
-                for (int dt = 0; dt < 4; ++dt) {
+                for (int dt = 0; dt < NDT; ++dt) {
                     const bf16x8 w = lds_b128(ws + 32 * dt * 64 + wofs[j]);
                     acc[dt] = CODEC == 0 ? mfma32(w, z, acc[dt]) : mfma32(z, w, acc[dt]);
                 }
             }
         }
         {
-            uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + tile) * FT_TILE + CODEC * FT_IMG;
+            uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + tile) * TF::TILE + CODEC * TF::K_IMG;
             if (CODEC == 0) {
                 // acc[dt] element i: d = 32 dt + 8 (i/4) + 4 hf + i%4 of this
                 // lane's key; K = bf16(bf16(acc + bias) + center)
 #pragma unroll
-                for (int dt = 0; dt < 4; ++dt)
+                for (int dt = 0; dt < NDT; ++dt)
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int d = 32 * dt + 8 * g + 4 * hf;
@@ -1087,7 +1113,7 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                             a[2] += __uint_as_float(c1 << 16);
                             a[3] += __uint_as_float(c1 & 0xffff0000u);
                         }
-                        *reinterpret_cast<u32x2*>(img + key * FT_ROW + d) =
+                        *reinterpret_cast<u32x2*>(img + key * DK + d) =
                             u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
                     }
             } else {
@@ -1124,7 +1150,7 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
 // head's codec runs on one XCD (blockIdx % 8) and shares its decoder rows in
 // L2 -- then the `ranges` tile ranges of each.  codecs: 3 = both (K and V
 // have KQ slices), 1 = K only, 2 = V only.
-template <int KQ>
+template <int KQ, int DK>
 __global__ void __launch_bounds__(DR_THREADS, 1) drtile_kernel(ChunkParams p, int ranges, int codecs) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
     DResSmem& sm = *reinterpret_cast<DResSmem*>(smem_raw);
@@ -1137,26 +1163,29 @@ __global__ void __launch_bounds__(DR_THREADS, 1) drtile_kernel(ChunkParams p, in
     const int T = (int)cdiv(p.n_rows, FT_T);
     const int ta = (int)((int64_t)rg * T / ranges), tb = (int)((int64_t)(rg + 1) * T / ranges);
     if (ta >= tb) return;
-    if (cc == 0) drtile_range<0, KQ>(sm, p, bh, ta, tb, wave, lane);
-    else drtile_range<1, KQ>(sm, p, bh, ta, tb, wave, lane);
+    if (cc == 0) drtile_range<0, KQ, DK>(sm, p, bh, ta, tb, wave, lane);
+    else drtile_range<1, KQ, DK>(sm, p, bh, ta, tb, wave, lane);
 }
 
-// The two tile buffers as [K0][K1][V0][V1]: a buffer's images sit 32 KB
-// from the other buffer's, so that every operand read is one per-lane
+// The two tile buffers as [K0][K1][V0][V1]: a buffer's images sit one
+// image from the other buffer's, so that every operand read is one per-lane
 // register plus an immediate offset (below 64 KB) for both buffers.
+template <int DK>
 struct FlashSmem {
-    uint16_t k[2][FT_IMG];
+    uint16_t k[2][TileFmt<DK>::K_IMG];
     uint16_t v[2][FT_IMG];
 };
-static_assert(sizeof(FlashSmem) <= 160 * 1024, "LDS budget");
+static_assert(sizeof(FlashSmem<CK_D>) <= 160 * 1024, "LDS budget");
 constexpr int FT_IMG_BYTES = FT_IMG * 2;
 
-// MASK: the current keys are attended under p.cur_mask (the history tiles
-// never are).
-template <bool MASK>
+// K/Q width DK.  MASK: the current keys are attended under p.cur_mask (the
+// history tiles never are).
+template <int DK, bool MASK>
 __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
+    using TF = TileFmt<DK>;
+    constexpr int K_BYTES = TF::K_IMG * 2;
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    FlashSmem& sm = *reinterpret_cast<FlashSmem*>(smem_raw);
+    FlashSmem<DK>& sm = *reinterpret_cast<FlashSmem<DK>*>(smem_raw);
     int lane = threadIdx.x & 63;
     asm volatile("" : "+v"(lane));
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -1171,40 +1200,49 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
     const int t1 = (int)((int64_t)(split + 1) * p.ntiles / p.splits);
     const int qb = qt * p.qpt + wave;
     const bool active = wave < p.qpt && qb < p.qblocks;
-    // tile i of the split goes to buffer i % 2; piece e (1 KB, 4 rows) of a
-    // tile: lane L brings chunk (L % 16) ^ (row % 16) of row 4 e + L / 16
-    const uint16_t* src = p.tiles + (int64_t)bh * p.ntiles * FT_TILE + (lane >> 4) * FT_ROW;
+    // tile i of the split goes to buffer i % 2; piece e (1 KB) of a tile:
+    // lane L brings chunk (L % CPR) ^ kswz(row) of K row 512 e / DK + L / CPR,
+    // or chunk (L % 16) ^ (row % 16) of V^T row 4 e' + L / 16 (e' = e minus
+    // the K pieces)
+    const uint16_t* src = p.tiles + (int64_t)bh * p.ntiles * TF::TILE;
     auto issue = [&](int tile) {
-        const uint16_t* s = src + (int64_t)tile * FT_TILE;
+        const uint16_t* s = src + (int64_t)tile * TF::TILE;
         const int bi = (tile - t0) & 1;
-        for (int e = wave; e < FT_PIECES; e += C8_WAVES) {
-            const int ch = (lane & 15) ^ ((4 * e + (lane >> 4)) & 15);
-            uint16_t* d = e < FT_PIECES / 2 ? sm.k[bi] + 512 * e : sm.v[bi] + 512 * (e - FT_PIECES / 2);
-            __builtin_amdgcn_global_load_lds(s + 512 * e + 8 * ch, NKV_LDS(d), 16, 0, 0);
+        for (int e = wave; e < TF::PIECES; e += C8_WAVES) {
+            if (e < TF::K_PIECES) {
+                const int row = e * (512 / DK) + lane / TF::CPR;
+                const int ch = (lane % TF::CPR) ^ TF::kswz(row);
+                dma16(s + row * DK + 8 * ch, sm.k[bi] + 512 * e);
+            } else {
+                const int ev = e - TF::K_PIECES, row = 4 * ev + (lane >> 4);
+                const int ch = (lane & 15) ^ (row & 15);
+                dma16(s + TF::K_IMG + row * FT_ROW + 8 * ch, sm.v[bi] + 512 * ev);
+            }
         }
     };
     const int hf = lane >> 5, l32 = lane & 31;
     const float c = p.scale_log2;
-    using W = DWalk<CK_D>;
+    using W = DWalk<DK>;
     constexpr int KS = W::KSTEPS;
     bf16x8 qf[KS], kf[KS], vf[8];
     const int64_t q0 = (int64_t)qb * 32;
-    if (active) load_q_block<CK_D>(qf, p, b, h, q0, q0, lane);
+    if (active) load_q_block<DK>(qf, p, b, h, q0, q0, lane);
     if (t0 < t1) issue(t0);
     // byte offsets in buffer 0 of this lane's operand fragments: K row l32
-    // (+ 32 j), logical chunk 8 (kk / 4) + 4 hf + kk % 4; V^T row l32 (+ 32
-    // (t % 4)), logical chunk 4 j + 2 (t / 4) + hf; each at chunk ^ (l32 % 16)
+    // (+ 32 j) at its logical chunk of k-step kk, at chunk ^ kswz(l32); V^T
+    // row l32 (+ 32 (t % 4)), logical chunk 4 j + 2 (t / 4) + hf, at
+    // chunk ^ (l32 % 16)
     uint32_t kofs[KS], vofs[8];
 #pragma unroll
     for (int kk = 0; kk < KS; ++kk) {
         const int chunk = (W::block(kk) + W::HALF * hf) >> 3;
-        kofs[kk] = 2 * (l32 * FT_ROW + 8 * (chunk ^ (l32 & 15)));
+        kofs[kk] = 2 * (l32 * DK + 8 * (chunk ^ TF::kswz(l32)));
         asm volatile("" : "+v"(kofs[kk]));
     }
 #pragma unroll
     for (int i = 0; i < 8; ++i) {
         const int chunk = 4 * (i >> 1) + 2 * (i & 1) + hf;
-        vofs[i] = 2 * FT_IMG * 2 + 2 * (l32 * FT_ROW + 8 * (chunk ^ (l32 & 15)));
+        vofs[i] = 2 * K_BYTES + 2 * (l32 * FT_ROW + 8 * (chunk ^ (l32 & 15)));
         asm volatile("" : "+v"(vofs[i]));
     }
     const uint32_t* mbase = nullptr;
@@ -1231,7 +1269,7 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
         if (!active || valid <= 0) return;
         auto lds_k = [&](int j, int kk) {
             return lds_b128(reinterpret_cast<const uint16_t*>(
-                smem_raw + kofs[kk] + BI * FT_IMG_BYTES + j * 32 * FT_ROW * 2));
+                smem_raw + kofs[kk] + BI * K_BYTES + j * 32 * DK * 2));
         };
         auto lds_v = [&](int j, int t) {
             return lds_b128(reinterpret_cast<const uint16_t*>(
@@ -1314,6 +1352,15 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
     }
     if (active) store_partial(p, bh, split, q0, o, m, halfwave_sum(l), lane);
 }
+
+// the host launch stubs of every width (the launches sit in an unnamed
+// namespace, which leaves them uninstantiated otherwise)
+template __global__ void flash8_kernel<32, false>(ChunkParams);
+template __global__ void flash8_kernel<32, true>(ChunkParams);
+template __global__ void flash8_kernel<64, false>(ChunkParams);
+template __global__ void flash8_kernel<64, true>(ChunkParams);
+template __global__ void flash8_kernel<128, false>(ChunkParams);
+template __global__ void flash8_kernel<128, true>(ChunkParams);
 
 // Merge the chunk partials of every (b, h, q).  One wave owns one 32-query
 // block and walks all its chunks, each lane reading the lane-order payload
@@ -1559,12 +1606,16 @@ FlashPlan flash_plan(const ChunkLaunchDesc& d) {
     return f;
 }
 
+// Reader widths below 128 are staged only by the decode GEMM (no read-time
+// RoPE or camera: stage8_kernel decodes at full width).
 bool use_staged(const ChunkLaunchDesc& d) {
-    return d.dk == CK_D && cdiv(d.Q, 32) >= FT_MIN_QBLOCKS && d.n_rows + d.Nc > 0;
+    const bool width = d.dk == CK_D || ((d.dk == 32 || d.dk == 64) && !rope_on(d.rope) && !d.cam.mats &&
+                                        d.key.r <= 64 * DR_MAXQ && d.value.r <= 64 * DR_MAXQ);
+    return width && cdiv(d.Q, 32) >= FT_MIN_QBLOCKS && d.n_rows + d.Nc > 0;
 }
 
 size_t staged_tile_bytes(const ChunkLaunchDesc& d, const FlashPlan& f) {
-    return (size_t)d.B * d.H * f.ntiles * FT_TILE * sizeof(uint16_t);
+    return (size_t)d.B * d.H * f.ntiles * (FT_T * d.dk + FT_IMG) * sizeof(uint16_t);
 }
 
 // History tiles from the decode GEMM with the decoder held in LDS
@@ -1581,25 +1632,44 @@ size_t staged_workspace(const ChunkLaunchDesc& d) {
     return staged_tile_bytes(d, f) + rows * CK_D * sizeof(uint16_t) + rows * 2 * sizeof(float);
 }
 
-template <int KQ>
+template <int KQ, int DK>
 int drtile_launch_kq(const ChunkParams& p, int64_t blocks, int ranges, int codecs, hipStream_t s) {
-    const int rc = set_smem(drtile_kernel<KQ>, sizeof(DResSmem));
+    const int rc = set_smem(drtile_kernel<KQ, DK>, sizeof(DResSmem));
     if (rc) return rc;
-    drtile_kernel<KQ><<<dim3((unsigned)blocks), DR_THREADS, sizeof(DResSmem), s>>>(p, ranges, codecs);
+    drtile_kernel<KQ, DK><<<dim3((unsigned)blocks), DR_THREADS, sizeof(DResSmem), s>>>(p, ranges, codecs);
     NKV_LAUNCH_CHECK();
     return NKV_OK;
 }
 
-int drtile_launch(int kq, const ChunkParams& p, int64_t blocks, int ranges, int codecs,
-                  hipStream_t s) {
+template <int DK>
+int drtile_launch_dk(int kq, const ChunkParams& p, int64_t blocks, int ranges, int codecs,
+                     hipStream_t s) {
     switch (kq) {
-        case 1: return drtile_launch_kq<1>(p, blocks, ranges, codecs, s);
-        case 2: return drtile_launch_kq<2>(p, blocks, ranges, codecs, s);
-        case 3: return drtile_launch_kq<3>(p, blocks, ranges, codecs, s);
-        case 4: return drtile_launch_kq<4>(p, blocks, ranges, codecs, s);
-        case 5: return drtile_launch_kq<5>(p, blocks, ranges, codecs, s);
-        default: return drtile_launch_kq<6>(p, blocks, ranges, codecs, s);
+        case 1: return drtile_launch_kq<1, DK>(p, blocks, ranges, codecs, s);
+        case 2: return drtile_launch_kq<2, DK>(p, blocks, ranges, codecs, s);
+        case 3: return drtile_launch_kq<3, DK>(p, blocks, ranges, codecs, s);
+        case 4: return drtile_launch_kq<4, DK>(p, blocks, ranges, codecs, s);
+        case 5: return drtile_launch_kq<5, DK>(p, blocks, ranges, codecs, s);
+        default: return drtile_launch_kq<6, DK>(p, blocks, ranges, codecs, s);
     }
+}
+
+int drtile_launch(int kq, int dk, const ChunkParams& p, int64_t blocks, int ranges, int codecs,
+                  hipStream_t s) {
+    if (dk == 32) return drtile_launch_dk<32>(kq, p, blocks, ranges, codecs, s);
+    if (dk == 64) return drtile_launch_dk<64>(kq, p, blocks, ranges, codecs, s);
+    return drtile_launch_dk<128>(kq, p, blocks, ranges, codecs, s);
+}
+
+template <int DK>
+int flash_launch(const ChunkParams& p, dim3 grid, hipStream_t s) {
+    const size_t smem = sizeof(FlashSmem<DK>);
+    int rc = p.cur_mask ? set_smem(flash8_kernel<DK, true>, smem) : set_smem(flash8_kernel<DK, false>, smem);
+    if (rc) return rc;
+    if (p.cur_mask) flash8_kernel<DK, true><<<grid, C8_THREADS, smem, s>>>(p);
+    else flash8_kernel<DK, false><<<grid, C8_THREADS, smem, s>>>(p);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
 }
 
 // Stage, flash, combine; p holds everything but the staged fields.
@@ -1620,8 +1690,6 @@ int staged_launch(hipStream_t s, const ChunkLaunchDesc& d, ChunkParams p, void* 
     p.part_ml = reinterpret_cast<float*>(p.part_o + rows * CK_D);
     const bool gemm = staged_gemm(d);
     int rc = gemm ? set_smem(ctile_kernel, sizeof(CTileSmem)) : set_smem(stage8_kernel, sizeof(Chunk8Smem));
-    if (!rc) rc = p.cur_mask ? set_smem(flash8_kernel<true>, sizeof(FlashSmem))
-                             : set_smem(flash8_kernel<false>, sizeof(FlashSmem));
     if (rc) return rc;
     if (gemm) {
         // the current tiles, then the history with the decoder held in LDS:
@@ -1640,7 +1708,7 @@ int staged_launch(hipStream_t s, const ChunkLaunchDesc& d, ChunkParams p, void* 
             // enough ranges to fill the CUs once, each at most DR_MAXT tiles
             const int ranges = (int)std::max<int64_t>(
                 std::max<int64_t>(1, std::min<int64_t>(T, FT_CUS / np)), cdiv(T, DR_MAXT));
-            rc = drtile_launch(codecs == 2 ? qv : qk, p, np * ranges, ranges, codecs, s);
+            rc = drtile_launch(codecs == 2 ? qv : qk, d.dk, p, np * ranges, ranges, codecs, s);
             if (rc) return rc;
         }
     } else {
@@ -1650,9 +1718,10 @@ int staged_launch(hipStream_t s, const ChunkLaunchDesc& d, ChunkParams p, void* 
     // the kernel events bracket the attention (flash) kernel
     if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
     const dim3 grid((unsigned)(BH * f.qtiles * f.splits));
-    if (p.cur_mask) flash8_kernel<true><<<grid, C8_THREADS, sizeof(FlashSmem), s>>>(p);
-    else flash8_kernel<false><<<grid, C8_THREADS, sizeof(FlashSmem), s>>>(p);
-    NKV_LAUNCH_CHECK();
+    if (d.dk == 32) rc = flash_launch<32>(p, grid, s);
+    else if (d.dk == 64) rc = flash_launch<64>(p, grid, s);
+    else rc = flash_launch<128>(p, grid, s);
+    if (rc) return rc;
     if (d.ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_end, s));
     chunk_combine_kernel<<<dim3((unsigned)cdiv(BH * p.qblocks, CB_WAVES)), 64 * CB_WAVES, 0, s>>>(p);
     NKV_LAUNCH_CHECK();

@@ -53,6 +53,16 @@ def test_fast_reader_widths(dev, d):
     _run(sc, dev, _payload(sc, (1,), d), np.arange(500, 700))
 
 
+@pytest.mark.parametrize("d", [32, 64])
+def test_fast_reader_widths_staged(dev, d):
+    """From 32 query blocks up the reader groups run the staged schedule at
+    their width (K image [128][d], flash at K/Q width d): a ragged history,
+    means and centers, fp16 group scales."""
+    sc = Scenario(H=4, N=900, Q=1040, Nc=70, rK=384, rV=256, G=32, C=16, with_mean=True,
+                  seed=d)
+    _run(sc, dev, _payload(sc, (2,), d, seed=d), np.arange(700, 900))
+
+
 @pytest.mark.parametrize("prot", ["recent", "scattered", "none", "all"])
 def test_fast_partitions(dev, prot):
     sc = Scenario(H=2, N=600, Q=100, Nc=40, rK=256, rV=256, G=32, C=8, with_mean=True)
