@@ -37,7 +37,12 @@
 #include "nkv_common.h"
 #include "nkv_internal.h"
 
+#include <algorithm>
+#include <cmath>
+#include <cstring>
+#include <map>
 #include <type_traits>
+#include <vector>
 
 namespace nkv {
 
@@ -75,6 +80,8 @@ struct ChunkParams {
     float scale_log2;
     const uint16_t* q;  // [B, Q, H, DK] (strides)
     int64_t q_sb, q_st, q_sh;
+    const int32_t* q_heads;  // query head of launch head i (null: i), clamped to [0, q_heads_n)
+    int q_heads_n;
     const uint16_t* k_cur;
     int64_t k_sb, k_st, k_sh;
     const uint16_t* v_cur;
@@ -97,6 +104,35 @@ struct ChunkParams {
     uint16_t* tiles;
     int ntiles_hist, ntiles, qpt, splits;
 };
+
+// ------------------------------------------------ multi-partition launches
+// One launch of the staged schedule runs the blocks of up to NKV_MAX_PARTS
+// attention partitions (the native partition and the reader groups of a
+// NanoKV-Fast call, or one nkv_attend call), each with its own ChunkParams
+// and K/Q width.  Blocks [seg_first[s], seg_first[s + 1]) run segment s: work
+// seg_kind[s] of partition seg_part[s] (seg_ranges[s]: tile ranges per head
+// of a decode segment).
+constexpr int MP_SEGS = 3 * NKV_MAX_PARTS;
+enum : int { SEG_K = 0, SEG_V = 1, SEG_CUR = 2, SEG_FLASH = 3 };
+struct MultiParams {
+    ChunkParams part[NKV_MAX_PARTS];
+    int dk[NKV_MAX_PARTS];
+    // combine: layer head of head i of partition j >= 1 (partition 0 covers
+    // every head of the layer and holds its output)
+    const int32_t* heads[NKV_MAX_PARTS];
+    int nparts, nseg;
+    int seg_part[MP_SEGS], seg_kind[MP_SEGS], seg_ranges[MP_SEGS];
+    int64_t seg_first[MP_SEGS + 1];
+};
+
+// Segment of block x (a scan over the uniform table).
+__device__ __forceinline__ int multi_segment(const MultiParams& P, int64_t x) {
+    int sg = 0;
+#pragma unroll
+    for (int i = 1; i < MP_SEGS; ++i)
+        if (i < P.nseg && x >= P.seg_first[i]) sg = i;
+    return sg;
+}
 
 // Codec row of attended history key `key`; rows outside the codec are
 // clamped so that a bad row list cannot read out of bounds.
@@ -171,8 +207,9 @@ __device__ __forceinline__ void load_q_block(bf16x8 (&qf)[NF], const ChunkParams
     static_assert(NF >= W::KSTEPS, "fragment array too small");
     const int hf = lane >> 5, l32 = lane & 31;
     const int64_t qi = q_blk + l32;
+    const int hq = p.q_heads ? min(max(ldg(p.q_heads + h), 0), p.q_heads_n - 1) : h;
     const uint16_t* qrow = p.q + (int64_t)b * p.q_sb + (qi < p.Q ? qi : q_safe) * p.q_st +
-                           (int64_t)h * p.q_sh + W::HALF * hf;
+                           (int64_t)hq * p.q_sh + W::HALF * hf;
 #pragma unroll
     for (int kk = 0; kk < W::KSTEPS; ++kk)
         qf[kk] = as_bf16x8(*reinterpret_cast<const u32x4*>(qrow + W::block(kk)));
@@ -860,25 +897,22 @@ __global__ void __launch_bounds__(C8_THREADS, 1) stage8_kernel(ChunkParams p) {
 }
 
 // ------------------------------------------------------------ current tiles
-// A current-key tile (the uncompressed keys of the chunk being attended):
-// thread t brings keys 4 (t % 32) .. +4, columns 16 (t / 32) .. +16 of K and
-// V (every load before any store); K rows go straight into the image, V
-// through LDS into V^T column order (one 8-byte write of four keys per
-// column).  Keys past the end are zero.
+// A current-key tile (the uncompressed keys of the chunk being attended),
+// built by CT_THREADS threads: thread t brings keys 4 (t % 32) .. +4,
+// columns 16 (t / 32) .. +16 of K and V (every load before any store); K
+// rows go straight into the image, V through LDS into V^T column order (one
+// 8-byte write of four keys per column).  Keys past the end are zero.  A
+// thread group with live == false (no such tile) only joins the barrier.
 constexpr int CT_THREADS = 256;
 struct CTileSmem {
     uint16_t vt[FT_IMG];  // [128 d][128] in V^T column order
 };
 
-__global__ void __launch_bounds__(CT_THREADS) ctile_kernel(ChunkParams p) {
-    extern __shared__ __align__(16) unsigned char smem_raw[];
-    CTileSmem& sm = *reinterpret_cast<CTileSmem*>(smem_raw);
-    const int t = threadIdx.x;
-    const int BH = p.B * p.H;
-    const int bh = (int)(blockIdx.x % BH), ct = (int)(blockIdx.x / BH);
+__device__ __forceinline__ void ctile_tile(const ChunkParams& p, int bh, int ct, bool live,
+                                           CTileSmem& sm, int t) {
     const int b = bh / p.H, h = bh % p.H;
     const int64_t key0 = (int64_t)ct * FT_T;
-    const int valid = (int)min((int64_t)FT_T, p.Nc - key0);
+    const int valid = live ? (int)min((int64_t)FT_T, p.Nc - key0) : 0;
     uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + p.ntiles_hist + ct) * FT_TILE;
     const int k0 = 4 * (t & 31), d0 = 16 * (t >> 5);
     u32x4 kv[4][2], vv[4][2];
@@ -894,11 +928,13 @@ __global__ void __launch_bounds__(CT_THREADS) ctile_kernel(ChunkParams p) {
             vv[e][x] = ok ? *reinterpret_cast<const u32x4*>(vs + 8 * x) : u32x4{0, 0, 0, 0};
         }
     }
+    if (live) {
 #pragma unroll
-    for (int e = 0; e < 4; ++e)
+        for (int e = 0; e < 4; ++e)
 #pragma unroll
-        for (int x = 0; x < 2; ++x)
-            *reinterpret_cast<u32x4*>(img + (k0 + e) * FT_ROW + d0 + 8 * x) = kv[e][x];
+            for (int x = 0; x < 2; ++x)
+                *reinterpret_cast<u32x4*>(img + (k0 + e) * FT_ROW + d0 + 8 * x) = kv[e][x];
+    }
     const int col = vt_col(k0);
 #pragma unroll
     for (int dd = 0; dd < 16; ++dd) {
@@ -908,8 +944,9 @@ __global__ void __launch_bounds__(CT_THREADS) ctile_kernel(ChunkParams p) {
             u32x2{val(0) | (val(1) << 16), val(2) | (val(3) << 16)};
     }
     __syncthreads();
-    for (int i = t; i < CK_D * (FT_ROW / 8); i += CT_THREADS)
-        *reinterpret_cast<u32x4*>(img + FT_IMG + 8 * i) = *reinterpret_cast<const u32x4*>(sm.vt + 8 * i);
+    if (live)
+        for (int i = t; i < CK_D * (FT_ROW / 8); i += CT_THREADS)
+            *reinterpret_cast<u32x4*>(img + FT_IMG + 8 * i) = *reinterpret_cast<const u32x4*>(sm.vt + 8 * i);
 }
 
 // ------------------------------------------------ decode GEMM, resident decoder
@@ -976,6 +1013,8 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
     const int t = threadIdx.x, hf = lane >> 5, l32 = lane & 31;
     const int kq = wave & 3, tp = wave >> 2;
     const int b = bh / p.H, h = bh % p.H;
+    // head of the center table and bias
+    const int hc = cd.c_heads ? min(max(ldg(cd.c_heads + h), 0), cd.c_heads_n - 1) : h;
     const int R = cd.r, G = cd.group;
     const bool cent = cd.has_centers, f16 = cd.scale_dtype == NKV_DTYPE_FP16;
     // the head's decoder rows, KQ slices of W / 8 pieces (8 rows x 128 B)
@@ -990,7 +1029,7 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                                              NKV_LDS(sm.dec + s * DR_SLICE + pc * 512), 16, 0, 0);
         }
     }
-    if (t < W) sm.bias[t] = cd.bias ? bf16_round(cd.bias[(int64_t)h * cd.bias_hs + t]) : 0.0f;
+    if (t < W) sm.bias[t] = cd.bias ? bf16_round(cd.bias[(int64_t)hc * cd.bias_hs + t]) : 0.0f;
     // codec row of key k of tile `tile`; keys past the last row take key 0's
     // codes and center (finite, never attended)
     auto key_row = [&](int tile, int k) {
@@ -1057,7 +1096,7 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
             const int k = t + e * DR_THREADS;
-            if (k < nk) r[e] = center_ref(cd, b, h, p.N, key_row(ta + (k >> 7), k & 127));
+            if (k < nk) r[e] = center_ref(cd, b, hc, p.N, key_row(ta + (k >> 7), k & 127));
         }
 #pragma unroll
         for (int e = 0; e < PER; ++e) {
@@ -1146,25 +1185,43 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
     }
 }
 
-// Blocks: (codec, b*h) fastest -- with B*H a multiple of 4 every range of one
-// head's codec runs on one XCD (blockIdx % 8) and shares its decoder rows in
-// L2 -- then the `ranges` tile ranges of each.  codecs: 3 = both (K and V
-// have KQ slices), 1 = K only, 2 = V only.
-template <int KQ, int DK>
-__global__ void __launch_bounds__(DR_THREADS, 1) drtile_kernel(ChunkParams p, int ranges, int codecs) {
+// Blocks of a decode segment: b*h fastest -- with B*H a multiple of 8 every
+// range of one head's codec runs on one XCD (blockIdx % 8) and shares its
+// decoder rows in L2 -- then its seg_ranges tile ranges.  A current-key
+// segment: b*h fastest, then pairs of current tiles, one per 256 threads.
+// KQ: decoder slices of the launch's decode segments.
+static_assert(2 * sizeof(CTileSmem) <= sizeof(DResSmem), "current tiles share the decode LDS");
+template <int KQ>
+__global__ void __launch_bounds__(DR_THREADS, 1) drtile_kernel(MultiParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
-    DResSmem& sm = *reinterpret_cast<DResSmem*>(smem_raw);
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int nc = codecs == 3 ? 2 : 1;
-    const int np = nc * p.B * p.H;
-    const int pair = (int)(blockIdx.x % np), rg = (int)(blockIdx.x / np);
-    const int cc = codecs == 3 ? pair % 2 : codecs - 1, bh = pair / nc;
+    const int sg = multi_segment(P, blockIdx.x);
+    const int pi = P.seg_part[sg], kind = P.seg_kind[sg], dk = P.dk[pi];
+    const ChunkParams& p = P.part[pi];
+    const int64_t local = (int64_t)blockIdx.x - P.seg_first[sg];
+    const int BH = p.B * p.H;
+    const int bh = (int)(local % BH), rg = (int)(local / BH);
+    if (kind == SEG_CUR) {
+        CTileSmem* ct = reinterpret_cast<CTileSmem*>(smem_raw);
+        const int half = threadIdx.x / CT_THREADS, c = 2 * rg + half;
+        ctile_tile(p, bh, c, c < p.ntiles - p.ntiles_hist, ct[half], threadIdx.x % CT_THREADS);
+        return;
+    }
+    DResSmem& sm = *reinterpret_cast<DResSmem*>(smem_raw);
+    const int ranges = P.seg_ranges[sg];
     const int T = (int)cdiv(p.n_rows, FT_T);
     const int ta = (int)((int64_t)rg * T / ranges), tb = (int)((int64_t)(rg + 1) * T / ranges);
     if (ta >= tb) return;
-    if (cc == 0) drtile_range<0, KQ, DK>(sm, p, bh, ta, tb, wave, lane);
-    else drtile_range<1, KQ, DK>(sm, p, bh, ta, tb, wave, lane);
+    if (kind == SEG_K) {
+        if (dk == 32) drtile_range<0, KQ, 32>(sm, p, bh, ta, tb, wave, lane);
+        else if (dk == 64) drtile_range<0, KQ, 64>(sm, p, bh, ta, tb, wave, lane);
+        else drtile_range<0, KQ, 128>(sm, p, bh, ta, tb, wave, lane);
+    } else {
+        if (dk == 32) drtile_range<1, KQ, 32>(sm, p, bh, ta, tb, wave, lane);
+        else if (dk == 64) drtile_range<1, KQ, 64>(sm, p, bh, ta, tb, wave, lane);
+        else drtile_range<1, KQ, 128>(sm, p, bh, ta, tb, wave, lane);
+    }
 }
 
 // The two tile buffers as [K0][K1][V0][V1]: a buffer's images sit one
@@ -1178,13 +1235,12 @@ struct FlashSmem {
 static_assert(sizeof(FlashSmem<CK_D>) <= 160 * 1024, "LDS budget");
 constexpr int FT_IMG_BYTES = FT_IMG * 2;
 
-// K/Q width DK.  MASK: the current keys are attended under p.cur_mask (the
-// history tiles never are).
+// Block blk of one partition at K/Q width DK.  MASK: the current keys are
+// attended under p.cur_mask (the history tiles never are).
 template <int DK, bool MASK>
-__global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
+__device__ __forceinline__ void flash_block(const ChunkParams& p, int64_t blk, unsigned char* smem_raw) {
     using TF = TileFmt<DK>;
     constexpr int K_BYTES = TF::K_IMG * 2;
-    extern __shared__ __align__(16) unsigned char smem_raw[];
     FlashSmem<DK>& sm = *reinterpret_cast<FlashSmem<DK>*>(smem_raw);
     int lane = threadIdx.x & 63;
     asm volatile("" : "+v"(lane));
@@ -1193,7 +1249,7 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
     // runs on one XCD (blockIdx % 8), whose L2 then serves its tiles to the
     // head's other query tiles
     const int BH = p.B * p.H;
-    const int bh = (int)(blockIdx.x % BH), rest = (int)(blockIdx.x / BH);
+    const int bh = (int)(blk % BH), rest = (int)(blk / BH);
     const int split = rest % p.splits, qt = rest / p.splits;
     const int b = bh / p.H, h = bh % p.H;
     const int t0 = (int)((int64_t)split * p.ntiles / p.splits);
@@ -1353,42 +1409,47 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(ChunkParams p) {
     if (active) store_partial(p, bh, split, q0, o, m, halfwave_sum(l), lane);
 }
 
-// the host launch stubs of every width (the launches sit in an unnamed
-// namespace, which leaves them uninstantiated otherwise)
-template __global__ void flash8_kernel<32, false>(ChunkParams);
-template __global__ void flash8_kernel<32, true>(ChunkParams);
-template __global__ void flash8_kernel<64, false>(ChunkParams);
-template __global__ void flash8_kernel<64, true>(ChunkParams);
-template __global__ void flash8_kernel<128, false>(ChunkParams);
-template __global__ void flash8_kernel<128, true>(ChunkParams);
+// The flash segments of a multi-partition launch.  Only a 128-wide
+// partition has current keys, so MASK reaches that width alone.
+template <bool MASK>
+__global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(MultiParams P) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    const int sg = multi_segment(P, blockIdx.x);
+    const int pi = P.seg_part[sg], dk = P.dk[pi];
+    const int64_t blk = (int64_t)blockIdx.x - P.seg_first[sg];
+    if (dk == 32) flash_block<32, false>(P.part[pi], blk, smem_raw);
+    else if (dk == 64) flash_block<64, false>(P.part[pi], blk, smem_raw);
+    else flash_block<128, MASK>(P.part[pi], blk, smem_raw);
+}
 
-// Merge the chunk partials of every (b, h, q).  One wave owns one 32-query
-// block and walks all its chunks, each lane reading the lane-order payload
-// the attention wave stored (1 KB per load instruction, four chunks in
-// flight); no cross-wave reduction, so blocks need no LDS and fill the GPU
-// in one round.
-// out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c (O_c unnormalised); no chunks give
-// out = 0 and lse = -inf (CN/core.py:48-49).
+// Merge of chunk partials.  One wave owns one 32-query block and walks all
+// its chunks, each lane reading the lane-order payload the attention wave
+// stored (1 KB per load instruction, four chunks in flight); no cross-wave
+// reduction, so blocks need no LDS and fill the GPU in one round.
+// out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c (O_c unnormalised); no
+// chunks give out = 0 and lse = -inf (CN/core.py:48-49).
 constexpr int CB_WAVES = 4;  // query blocks per 256-thread block
-__global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParams p) {
-    const int lane = threadIdx.x & 63, hf = lane >> 5, l32 = lane & 31;
-    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t gq = (int64_t)blockIdx.x * CB_WAVES + wave;
-    if (gq >= (int64_t)p.B * p.H * p.qblocks) return;
-    const int64_t bh = gq / p.qblocks;
-    const int qblk = (int)(gq % p.qblocks);
-    const int64_t qi = (int64_t)qblk * 32 + l32;
-    const int NC = p.nch_total;
-    const int64_t lse_stride = (int64_t)p.qblocks * 32;
-    const u32x2* ml = reinterpret_cast<const u32x2*>(p.part_ml) + bh * NC * lse_stride + qi;
-    // online merge: M is the largest chunk max seen so far; a chunk whose max
-    // exceeds it rescales the running sums (per lane), so no separate pass
-    // over the maxima delays the first partial loads
-    float M = -INFINITY, L = 0.0f, acc[64];
-#pragma unroll
-    for (int e = 0; e < 64; ++e) acc[e] = 0.0f;
-    const uint16_t* src = p.part_o + (bh * NC * p.qblocks + qblk) * 4096 + lane * 8;
-    const int64_t cstride = (int64_t)p.qblocks * 4096;
+
+// The running merge of one wave: M the largest chunk max so far, L the
+// weighted row sum, acc the weighted O; Lx the part of L that the tracked
+// source contributed (rescaled with L).
+struct CombineAcc {
+    float M, L, Lx;
+    float acc[64];
+};
+
+// Fold partials 0 .. NC of (bh, query block qblk) in, from a partial area
+// of qblocks query blocks per (bh, chunk).  A chunk whose max exceeds M
+// rescales the running sums (per lane), so no separate pass over the maxima
+// delays the first partial loads.
+__device__ __forceinline__ void combine_partials(CombineAcc& A, const uint16_t* part_o,
+                                                 const float* part_ml, int64_t bh, int NC,
+                                                 int qblocks, int qblk, int lane, bool track) {
+    const int64_t qi = (int64_t)qblk * 32 + (lane & 31);
+    const int64_t lse_stride = (int64_t)qblocks * 32;
+    const u32x2* ml = reinterpret_cast<const u32x2*>(part_ml) + bh * NC * lse_stride + qi;
+    const uint16_t* src = part_o + (bh * NC * qblocks + qblk) * 4096 + lane * 8;
+    const int64_t cstride = (int64_t)qblocks * 4096;
     // a ring of CB_AHEAD chunks in flight (prefetches past the last chunk
     // reload it and are never used)
     constexpr int CB_AHEAD = 4;
@@ -1406,7 +1467,7 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
     };
     // no chunks (no keys at all): nothing to read, and the workspace may be
     // null; the loads must not be issued ahead of this test
-    if (NC > 0) {
+    if (NC <= 0) return;
 #pragma unroll
     for (int i = 0; i < CB_AHEAD; ++i) issue(i, i);
     for (int cc0 = 0; cc0 < NC; cc0 += CB_AHEAD) {
@@ -1418,31 +1479,41 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
             const bool live = cc0 + i < NC;
             const float mc = __uint_as_float(mlb[i][0]);
             // a chunk with no valid key for this query has m = -inf and O = 0
-            const bool up = live && mc > M;
+            const bool up = live && mc > A.M;
             if (__any(up)) {
-                const float f = up ? exp2f(M - mc) : 1.0f;  // M = -inf gives 0
-                L *= f;
+                const float f = up ? exp2f(A.M - mc) : 1.0f;  // M = -inf gives 0
+                A.L *= f;
+                A.Lx *= f;
 #pragma unroll
-                for (int e = 0; e < 64; ++e) acc[e] *= f;
+                for (int e = 0; e < 64; ++e) A.acc[e] *= f;
             }
-            M = up ? mc : M;
-            const float wt = !live || mc == -INFINITY ? 0.0f : exp2f(mc - M);
-            L += wt * __uint_as_float(mlb[i][1]);
+            A.M = up ? mc : A.M;
+            const float wt = !live || mc == -INFINITY ? 0.0f : exp2f(mc - A.M);
+            const float wl = wt * __uint_as_float(mlb[i][1]);
+            A.L += wl;
+            if (track) A.Lx += wl;
 #pragma unroll
             for (int st = 0; st < 8; ++st)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
-                    acc[8 * st + 2 * e] += wt * __uint_as_float(buf[i][st][e] << 16);
-                    acc[8 * st + 2 * e + 1] += wt * __uint_as_float(buf[i][st][e] & 0xffff0000u);
+                    A.acc[8 * st + 2 * e] += wt * __uint_as_float(buf[i][st][e] << 16);
+                    A.acc[8 * st + 2 * e + 1] += wt * __uint_as_float(buf[i][st][e] & 0xffff0000u);
                 }
             issue(cc0 + i + CB_AHEAD, i);
         }
     }
-    }
-    if (qi >= p.Q) return;
-    const float inv = L > 0.0f ? 1.0f / L : 0.0f;
-    const int b = (int)(bh / p.H), h = (int)(bh % p.H);
-    uint16_t* orow = p.out + b * p.o_sb + qi * p.o_st + h * p.o_sh + 4 * hf;
+}
+
+// Normalise and store query qi of (b, h): out = (acc + shift * Lx) / L in
+// bf16 (shift: the row of 128 values added to the tracked source's output,
+// or null), lse = ln(sum) when lse is given.
+__device__ __forceinline__ void combine_store(const CombineAcc& A, uint16_t* out, int64_t o_sb,
+                                              int64_t o_st, int64_t o_sh, float* lse, int64_t Q,
+                                              int H, int b, int h, int64_t qi, int lane,
+                                              const float* shift) {
+    const int hf = lane >> 5;
+    const float inv = A.L > 0.0f ? 1.0f / A.L : 0.0f;
+    uint16_t* orow = out + b * o_sb + qi * o_st + h * o_sh + 4 * hf;
     // acc[8*st + 2*e + {0,1}] = o[db = st/2][i = 8*(st&1) + 2*e + {0,1}] with
     // d = 32*db + 8*(i/4) + 4*hf + i%4: acc[4n .. 4n+3] are four consecutive
     // d of this lane's query
@@ -1451,12 +1522,82 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
         const int st = n >> 1;
         const int db = st >> 1, i = 8 * (st & 1) + 4 * (n & 1);
         const int d = 32 * db + 8 * (i >> 2);
-        const u32x2 pk = {pack_bf16x2(acc[4 * n] * inv, acc[4 * n + 1] * inv),
-                          pack_bf16x2(acc[4 * n + 2] * inv, acc[4 * n + 3] * inv)};
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = A.acc[4 * n + e];
+        if (shift) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) v[e] = fmaf(shift[d + 4 * hf + e], A.Lx, v[e]);
+        }
+        const u32x2 pk = {pack_bf16x2(v[0] * inv, v[1] * inv), pack_bf16x2(v[2] * inv, v[3] * inv)};
         *reinterpret_cast<u32x2*>(orow + d) = pk;
     }
-    if (p.lse && hf == 0)
-        p.lse[bh * p.Q + qi] = L > 0.0f ? (M + log2f(L)) * 0.69314718055994531f : -INFINITY;
+    if (lse && hf == 0)
+        lse[((int64_t)b * H + h) * Q + qi] =
+            A.L > 0.0f ? (A.M + log2f(A.L)) * 0.69314718055994531f : -INFINITY;
+}
+
+__device__ __forceinline__ void combine_init(CombineAcc& A) {
+    A.M = -INFINITY;
+    A.L = A.Lx = 0.0f;
+#pragma unroll
+    for (int e = 0; e < 64; ++e) A.acc[e] = 0.0f;
+}
+
+// The key-chunk schedule's merge: every (b, h, q) of one launch.
+__global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParams p) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int64_t gq = (int64_t)blockIdx.x * CB_WAVES + wave;
+    if (gq >= (int64_t)p.B * p.H * p.qblocks) return;
+    const int64_t bh = gq / p.qblocks;
+    const int qblk = (int)(gq % p.qblocks);
+    CombineAcc A;
+    combine_init(A);
+    combine_partials(A, p.part_o, p.part_ml, bh, p.nch_total, p.qblocks, qblk, lane, false);
+    const int64_t qi = (int64_t)qblk * 32 + (lane & 31);
+    if (qi >= p.Q) return;
+    combine_store(A, p.out, p.o_sb, p.o_st, p.o_sh, p.lse, p.Q, p.H, (int)(bh / p.H),
+                  (int)(bh % p.H), qi, lane, nullptr);
+}
+
+// The staged schedule's merge over every partition (CN/core.py:33-42 for
+// two): one wave per (b, h, query block) of partition 0, which covers every
+// head of the layer, folds in that head's partials of partition 0, then of
+// the first other partition that lists h among its heads, whose output is
+// shifted by shift[b*sh_sb + h*sh_sh + d] (null: none; the value-mean
+// correction) before the merge.
+__global__ void __launch_bounds__(64 * CB_WAVES) staged_combine_kernel(MultiParams P,
+                                                                       const float* shift,
+                                                                       int64_t sh_sb, int64_t sh_sh) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const ChunkParams& n = P.part[0];
+    const int64_t gq = (int64_t)blockIdx.x * CB_WAVES + wave;
+    if (gq >= (int64_t)n.B * n.H * n.qblocks) return;
+    const int64_t bh = gq / n.qblocks;
+    const int qblk = (int)(gq % n.qblocks);
+    const int b = (int)(bh / n.H), h = (int)(bh % n.H);
+    // the partition holding head h besides partition 0 (0: none)
+    int lp = 0, li = 0;
+    for (int pi = 1; pi < NKV_MAX_PARTS && pi < P.nparts && lp == 0; ++pi)
+        for (int i = 0; i < P.part[pi].H; ++i)
+            if (ldg(P.heads[pi] + i) == h) {
+                lp = pi;
+                li = i;
+                break;
+            }
+    CombineAcc A;
+    combine_init(A);
+    for (int src = 0; src < (lp ? 2 : 1); ++src) {
+        const ChunkParams& g = P.part[src ? lp : 0];
+        combine_partials(A, g.part_o, g.part_ml, src ? (int64_t)b * g.H + li : bh, g.nch_total,
+                         g.qblocks, qblk, lane, src == 1);
+    }
+    const int64_t qi = (int64_t)qblk * 32 + (lane & 31);
+    if (qi >= n.Q) return;
+    combine_store(A, n.out, n.o_sb, n.o_st, n.o_sh, n.lse, n.Q, n.H, b, h, qi, lane,
+                  lp && shift ? shift + (int64_t)b * sh_sb + (int64_t)h * sh_sh : nullptr);
 }
 
 // ------------------------------------------------------------------ host
@@ -1539,6 +1680,7 @@ int check_chunk_codec(const ChunkCodec& c) {
     NKV_REQUIRE(!c.seg || c.n_seg > 0, NKV_ERR_INVALID, "empty segment table");
     NKV_REQUIRE(!(c.seg && c.has_centers && c.seg_flat) || c.centers, NKV_ERR_INVALID,
                 "a flat center table is missing");
+    NKV_REQUIRE(!c.c_heads || c.c_heads_n >= 1, NKV_ERR_INVALID, "c_heads needs c_heads_n >= 1");
     return NKV_OK;
 }
 
@@ -1583,26 +1725,15 @@ struct FlashPlan {
     int qpt, qtiles, splits, ntiles_hist, ntiles;
 };
 
-// Query tiles of at most eight blocks, balanced (49 blocks: 7 tiles of 7);
-// key splits: the fewest that bring the grid closest to whole rounds of the
-// CUs (rounds per unit of work), each split at least 4 tiles.
-FlashPlan flash_plan(const ChunkLaunchDesc& d) {
+// Query tiles of at most eight blocks, balanced (49 blocks: 7 tiles of 7).
+FlashPlan flash_shape(const ChunkLaunchDesc& d) {
     FlashPlan f{};
     const int64_t qblocks = cdiv(d.Q, 32);
     f.qtiles = (int)cdiv(qblocks, C8_WAVES);
     f.qpt = (int)cdiv(qblocks, f.qtiles);
     f.ntiles_hist = 2 * (int)chunk_count(d.n_rows);
     f.ntiles = f.ntiles_hist + 2 * (int)chunk_count(d.Nc);
-    const int64_t base = (int64_t)d.B * d.H * f.qtiles;
-    f.splits = 1;
-    double best = 1e30;
-    for (int sp = 1; sp <= 16 && 4 * sp <= std::max(f.ntiles, 4); ++sp) {
-        const double cost = (double)cdiv(base * sp, FT_CUS) / sp;
-        if (cost < best - 1e-9) {
-            best = cost;
-            f.splits = sp;
-        }
-    }
+    f.splits = 0;
     return f;
 }
 
@@ -1614,151 +1745,329 @@ bool use_staged(const ChunkLaunchDesc& d) {
     return width && cdiv(d.Q, 32) >= FT_MIN_QBLOCKS && d.n_rows + d.Nc > 0;
 }
 
-size_t staged_tile_bytes(const ChunkLaunchDesc& d, const FlashPlan& f) {
-    return (size_t)d.B * d.H * f.ntiles * (FT_T * d.dk + FT_IMG) * sizeof(uint16_t);
-}
-
-// History tiles from the decode GEMM with the decoder held in LDS
-// (drtile_kernel, current tiles from ctile_kernel); with read-time RoPE or
-// camera, or ranks above what LDS holds, both from stage8_kernel's decode.
+// History tiles from the decode GEMM with the decoder held in LDS (and the
+// current tiles copied in the same launch); with read-time RoPE or camera,
+// or ranks above what LDS holds, both from stage8_kernel's decode.
 bool staged_gemm(const ChunkLaunchDesc& d) {
-    return d.n_rows > 0 && !rope_on(d.rope) && !d.cam.mats && d.key.r <= 64 * DR_MAXQ &&
-           d.value.r <= 64 * DR_MAXQ;
+    return !rope_on(d.rope) && !d.cam.mats && d.key.r <= 64 * DR_MAXQ && d.value.r <= 64 * DR_MAXQ;
 }
 
-size_t staged_workspace(const ChunkLaunchDesc& d) {
-    const FlashPlan f = flash_plan(d);
-    const size_t rows = (size_t)d.B * d.H * f.splits * cdiv(d.Q, 32) * 32;
-    return staged_tile_bytes(d, f) + rows * CK_D * sizeof(uint16_t) + rows * 2 * sizeof(float);
+// Cost model of the staged kernels for planning their grids, in units of one
+// 128-wide tile of a kernel's steady state (on MI355X the flash kernel takes
+// ~4.4 us per tile and block at 128 wide, ~3.1 us at 32; the decode ~5 us),
+// plus a fixed cost per block (the decode's: the decoder rows and the
+// range's center rows, ~8 us).
+double flash_tile_cost(int dk) { return dk == 32 ? 0.7 : dk == 64 ? 0.82 : 1.0; }
+double decode_tile_cost(int w) { return w == 32 ? 0.5 : w == 64 ? 0.7 : 1.0; }
+constexpr double FLASH_BLOCK_COST = 1.0, DECODE_BLOCK_COST = 1.6, CTILE_BLOCK_COST = 0.5;
+constexpr double FLASH_TILE_US = 4.4;
+// each split's partials are written by the flash kernel and read back by the
+// combine at about 4 TB/s
+constexpr double PARTIAL_BYTES_PER_US = 4.0e6;
+constexpr size_t PARTIAL_ROW_BYTES = CK_D * sizeof(uint16_t) + 2 * sizeof(float);
+
+// Finishing time of greedy list scheduling (largest blocks first, each to
+// the least loaded CU) of groups of equal blocks (cost, count) on FT_CUS
+// CUs.  CUs with equal loads are kept as one entry, so each step places a
+// whole run of blocks.
+double lpt_makespan(std::vector<std::pair<double, int64_t>> groups) {
+    std::sort(groups.begin(), groups.end(),
+              [](const std::pair<double, int64_t>& x, const std::pair<double, int64_t>& y) {
+                  return x.first > y.first;
+              });
+    std::map<double, int64_t> loads{{0.0, FT_CUS}};
+    double span = 0.0;
+    for (const auto& g : groups) {
+        int64_t n = g.second;
+        while (n > 0) {
+            auto it = loads.begin();
+            const double at = it->first;
+            const int64_t take = std::min(n, it->second);
+            if (take == it->second) loads.erase(it);
+            else it->second -= take;
+            loads[at + g.first] += take;
+            span = std::max(span, at + g.first);
+            n -= take;
+        }
+    }
+    return span;
 }
 
-template <int KQ, int DK>
-int drtile_launch_kq(const ChunkParams& p, int64_t blocks, int ranges, int codecs, hipStream_t s) {
-    const int rc = set_smem(drtile_kernel<KQ, DK>, sizeof(DResSmem));
+// The staged plan of partitions d[0 .. n): flash key splits per partition,
+// decode tile ranges per (partition, codec), the workspace layout.
+struct MultiPlan {
+    int n;
+    FlashPlan f[NKV_MAX_PARTS];
+    int ranges[NKV_MAX_PARTS][2];  // decode tile ranges per head of K and V (0: none)
+    size_t tiles_off[NKV_MAX_PARTS], part_off[NKV_MAX_PARTS], total;
+};
+
+size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Key splits: every split count of every partition gives a candidate block
+// cost; each candidate gives each partition the fewest splits whose blocks
+// stay within it, and the plan with the least modelled time (the makespan
+// plus the partials' traffic) wins.  One partition at cfg1 (112 tiles, 168
+// query tiles): 3 splits, 504 blocks in two rounds of the CUs.
+void plan_flash(const ChunkLaunchDesc* d, int n, MultiPlan& P) {
+    std::vector<double> cand;
+    double work[NKV_MAX_PARTS];
+    int smax[NKV_MAX_PARTS];
+    for (int i = 0; i < n; ++i) {
+        P.f[i] = flash_shape(d[i]);
+        work[i] = P.f[i].ntiles * flash_tile_cost(d[i].dk);
+        smax[i] = std::max(1, std::min(16, P.f[i].ntiles / 4));
+        if (P.f[i].ntiles == 0) continue;
+        for (int sp = 1; sp <= smax[i]; ++sp) cand.push_back(work[i] / sp);
+    }
+    double best = 1e300;
+    int64_t best_blocks = 0;
+    int best_sp[NKV_MAX_PARTS] = {};
+    for (const double c : cand) {
+        std::vector<std::pair<double, int64_t>> groups;
+        int sp[NKV_MAX_PARTS] = {};
+        int64_t blocks = 0;
+        double bytes = 0.0;
+        for (int i = 0; i < n; ++i) {
+            if (P.f[i].ntiles == 0) continue;
+            sp[i] = std::min(smax[i], std::max(1, (int)std::ceil(work[i] / c - 1e-9)));
+            const int64_t nb = (int64_t)d[i].B * d[i].H * P.f[i].qtiles * sp[i];
+            groups.push_back({work[i] / sp[i] + FLASH_BLOCK_COST, nb});
+            blocks += nb;
+            bytes += 2.0 * (double)d[i].B * d[i].H * sp[i] * cdiv(d[i].Q, 32) * 32 * PARTIAL_ROW_BYTES;
+        }
+        const double t = lpt_makespan(groups) * FLASH_TILE_US + bytes / PARTIAL_BYTES_PER_US;
+        if (t < best - 1e-6 || (t < best + 1e-6 && blocks < best_blocks)) {
+            best = t;
+            best_blocks = blocks;
+            for (int i = 0; i < n; ++i) best_sp[i] = sp[i];
+        }
+    }
+    for (int i = 0; i < n; ++i) P.f[i].splits = best_sp[i];
+}
+
+// Decode ranges: candidate block costs from 1 .. 32 ranges above the least
+// each (partition, codec) needs (DR_MAXT tiles per range), the current-key
+// blocks placed after the decode blocks.  cfg1 (98 tiles of each codec, 24
+// heads): 5 ranges per head and codec, 240 blocks in one round.
+void plan_decode(const ChunkLaunchDesc* d, int n, MultiPlan& P) {
+    struct Seg {
+        int i, cc;
+        int64_t T, bh;
+        double w;
+    };
+    std::vector<Seg> segs;
+    std::vector<std::pair<double, int64_t>> cur;
+    for (int i = 0; i < n; ++i) {
+        P.ranges[i][0] = P.ranges[i][1] = 0;
+        const int64_t bh = (int64_t)d[i].B * d[i].H;
+        if (d[i].n_rows > 0) {
+            const int64_t T = cdiv(d[i].n_rows, FT_T);
+            for (int cc = 0; cc < 2; ++cc)
+                segs.push_back({i, cc, T, bh, T * decode_tile_cost(cc ? CK_D : d[i].dk)});
+        }
+        const int64_t nct = P.f[i].ntiles - P.f[i].ntiles_hist;
+        if (nct > 0) cur.push_back({CTILE_BLOCK_COST, bh * cdiv(nct, 2)});
+    }
+    if (segs.empty()) return;
+    std::vector<double> cand;
+    for (const Seg& g : segs) {
+        const int64_t rmin = cdiv(g.T, DR_MAXT);
+        for (int64_t r = rmin; r <= std::min(g.T, rmin + 31); ++r) cand.push_back(g.w / r);
+    }
+    double best = 1e300;
+    int64_t best_blocks = 0;
+    std::vector<int64_t> best_r(segs.size());
+    std::vector<int64_t> r(segs.size());
+    for (const double c : cand) {
+        std::vector<std::pair<double, int64_t>> groups = cur;
+        int64_t blocks = 0;
+        for (size_t k = 0; k < segs.size(); ++k) {
+            const Seg& g = segs[k];
+            r[k] = std::min(g.T, std::max(cdiv(g.T, DR_MAXT), (int64_t)std::ceil(g.w / c - 1e-9)));
+            groups.push_back({g.w / r[k] + DECODE_BLOCK_COST, g.bh * r[k]});
+            blocks += g.bh * r[k];
+        }
+        const double t = lpt_makespan(groups);
+        if (t < best - 1e-6 || (t < best + 1e-6 && blocks < best_blocks)) {
+            best = t;
+            best_blocks = blocks;
+            best_r = r;
+        }
+    }
+    for (size_t k = 0; k < segs.size(); ++k) P.ranges[segs[k].i][segs[k].cc] = (int)best_r[k];
+}
+
+// The plan depends on the partitions' shapes alone; the last one is kept
+// (a layer loop repeats the same shapes).
+MultiPlan multi_plan(const ChunkLaunchDesc* d, int n) {
+    std::vector<int64_t> key{n};
+    for (int i = 0; i < n; ++i)
+        for (int64_t v : {(int64_t)d[i].B, (int64_t)d[i].H, (int64_t)d[i].dk, d[i].Q, d[i].n_rows,
+                          d[i].Nc, (int64_t)staged_gemm(d[i])})
+            key.push_back(v);
+    thread_local std::vector<int64_t> last_key;
+    thread_local MultiPlan last;
+    if (key == last_key) return last;
+    MultiPlan P{};
+    P.n = n;
+    plan_flash(d, n, P);
+    plan_decode(d, n, P);
+    size_t off = 0;
+    for (int i = 0; i < n; ++i) {
+        const FlashPlan& f = P.f[i];
+        P.tiles_off[i] = off;
+        off += align256((size_t)d[i].B * d[i].H * f.ntiles * (FT_T * d[i].dk + FT_IMG) * sizeof(uint16_t));
+        P.part_off[i] = off;
+        off += align256((size_t)d[i].B * d[i].H * f.splits * cdiv(d[i].Q, 32) * 32 * PARTIAL_ROW_BYTES);
+    }
+    P.total = off;
+    last_key = key;
+    last = P;
+    return P;
+}
+
+template <int KQ>
+int drtile_launch_kq(const MultiParams& M, int64_t blocks, hipStream_t s) {
+    const int rc = set_smem(drtile_kernel<KQ>, sizeof(DResSmem));
     if (rc) return rc;
-    drtile_kernel<KQ, DK><<<dim3((unsigned)blocks), DR_THREADS, sizeof(DResSmem), s>>>(p, ranges, codecs);
+    drtile_kernel<KQ><<<dim3((unsigned)blocks), DR_THREADS, sizeof(DResSmem), s>>>(M);
     NKV_LAUNCH_CHECK();
     return NKV_OK;
 }
 
-template <int DK>
-int drtile_launch_dk(int kq, const ChunkParams& p, int64_t blocks, int ranges, int codecs,
-                     hipStream_t s) {
+int drtile_launch(int kq, const MultiParams& M, int64_t blocks, hipStream_t s) {
     switch (kq) {
-        case 1: return drtile_launch_kq<1, DK>(p, blocks, ranges, codecs, s);
-        case 2: return drtile_launch_kq<2, DK>(p, blocks, ranges, codecs, s);
-        case 3: return drtile_launch_kq<3, DK>(p, blocks, ranges, codecs, s);
-        case 4: return drtile_launch_kq<4, DK>(p, blocks, ranges, codecs, s);
-        case 5: return drtile_launch_kq<5, DK>(p, blocks, ranges, codecs, s);
-        default: return drtile_launch_kq<6, DK>(p, blocks, ranges, codecs, s);
+        case 1: return drtile_launch_kq<1>(M, blocks, s);
+        case 2: return drtile_launch_kq<2>(M, blocks, s);
+        case 3: return drtile_launch_kq<3>(M, blocks, s);
+        case 4: return drtile_launch_kq<4>(M, blocks, s);
+        case 5: return drtile_launch_kq<5>(M, blocks, s);
+        default: return drtile_launch_kq<6>(M, blocks, s);
     }
 }
 
-int drtile_launch(int kq, int dk, const ChunkParams& p, int64_t blocks, int ranges, int codecs,
-                  hipStream_t s) {
-    if (dk == 32) return drtile_launch_dk<32>(kq, p, blocks, ranges, codecs, s);
-    if (dk == 64) return drtile_launch_dk<64>(kq, p, blocks, ranges, codecs, s);
-    return drtile_launch_dk<128>(kq, p, blocks, ranges, codecs, s);
+// Block cost of a segment for ordering a launch (largest first).
+struct SegOrder {
+    double cost;
+    int part, kind, ranges;
+    int64_t blocks;
+};
+
+void set_segments(MultiParams& M, std::vector<SegOrder> segs) {
+    std::stable_sort(segs.begin(), segs.end(),
+                     [](const SegOrder& x, const SegOrder& y) { return x.cost > y.cost; });
+    M.nseg = (int)segs.size();
+    int64_t first = 0;
+    for (int k = 0; k < M.nseg; ++k) {
+        M.seg_part[k] = segs[k].part;
+        M.seg_kind[k] = segs[k].kind;
+        M.seg_ranges[k] = segs[k].ranges;
+        M.seg_first[k] = first;
+        first += segs[k].blocks;
+    }
+    for (int k = M.nseg; k <= MP_SEGS; ++k) M.seg_first[k] = first;
 }
 
-template <int DK>
-int flash_launch(const ChunkParams& p, dim3 grid, hipStream_t s) {
-    const size_t smem = sizeof(FlashSmem<DK>);
-    int rc = p.cur_mask ? set_smem(flash8_kernel<DK, true>, smem) : set_smem(flash8_kernel<DK, false>, smem);
-    if (rc) return rc;
-    if (p.cur_mask) flash8_kernel<DK, true><<<grid, C8_THREADS, smem, s>>>(p);
-    else flash8_kernel<DK, false><<<grid, C8_THREADS, smem, s>>>(p);
-    NKV_LAUNCH_CHECK();
-    return NKV_OK;
-}
+int64_t seg_blocks(const MultiParams& M) { return M.seg_first[M.nseg]; }
 
-// Stage, flash, combine; p holds everything but the staged fields.
-int staged_launch(hipStream_t s, const ChunkLaunchDesc& d, ChunkParams p, void* workspace) {
-    const FlashPlan f = flash_plan(d);
-    const int64_t BH = (int64_t)d.B * d.H;
-    p.tiles = reinterpret_cast<uint16_t*>(workspace);
-    p.ntiles_hist = f.ntiles_hist;
-    p.ntiles = f.ntiles;
-    p.qpt = f.qpt;
-    p.splits = f.splits;
-    // the partials of the splits, in the key-chunk layout with chunk = split
-    p.nch_hist = 0;
-    p.nch_total = f.splits;
-    const size_t rows = (size_t)BH * f.splits * p.qblocks * 32;
-    p.part_o = reinterpret_cast<uint16_t*>(reinterpret_cast<unsigned char*>(workspace) +
-                                           staged_tile_bytes(d, f));
-    p.part_ml = reinterpret_cast<float*>(p.part_o + rows * CK_D);
-    const bool gemm = staged_gemm(d);
-    int rc = gemm ? set_smem(ctile_kernel, sizeof(CTileSmem)) : set_smem(stage8_kernel, sizeof(Chunk8Smem));
-    if (rc) return rc;
-    if (gemm) {
-        // the current tiles, then the history with the decoder held in LDS:
-        // ranges per (head, codec) so that the blocks fill the CUs once
-        const int64_t cur = BH * (f.ntiles - f.ntiles_hist);
-        if (cur > 0) {
-            ctile_kernel<<<dim3((unsigned)cur), CT_THREADS, sizeof(CTileSmem), s>>>(p);
-            NKV_LAUNCH_CHECK();
-        }
-        const int64_t T = cdiv(d.n_rows, FT_T);
-        const int qk = d.key.r >> 6, qv = d.value.r >> 6;
-        // both codecs in one launch when their ranks agree
-        for (int codecs : {qk == qv ? 3 : 1, qk == qv ? 0 : 2}) {
-            if (!codecs) continue;
-            const int64_t np = (codecs == 3 ? 2 : 1) * BH;
-            // enough ranges to fill the CUs once, each at most DR_MAXT tiles
-            const int ranges = (int)std::max<int64_t>(
-                std::max<int64_t>(1, std::min<int64_t>(T, FT_CUS / np)), cdiv(T, DR_MAXT));
-            rc = drtile_launch(codecs == 2 ? qv : qk, d.dk, p, np * ranges, ranges, codecs, s);
+// Stage, flash, combine of partitions d[0 .. n); ps[i] holds everything of
+// partition i but the staged fields.
+int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, int n,
+               const int32_t* const* heads, const float* shift, int64_t sh_sb, int64_t sh_sh,
+               void* workspace) {
+    const MultiPlan P = multi_plan(d, n);
+    unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
+    MultiParams M;
+    memset(&M, 0, sizeof(M));
+    M.nparts = n;
+    for (int i = 0; i < n; ++i) {
+        const FlashPlan& f = P.f[i];
+        ChunkParams p = ps[i];
+        p.tiles = reinterpret_cast<uint16_t*>(ws + P.tiles_off[i]);
+        p.ntiles_hist = f.ntiles_hist;
+        p.ntiles = f.ntiles;
+        p.qpt = f.qpt;
+        p.splits = std::max(f.splits, 1);
+        // the partials of the splits, in the key-chunk layout with chunk = split
+        p.nch_hist = 0;
+        p.nch_total = f.splits;
+        p.part_o = reinterpret_cast<uint16_t*>(ws + P.part_off[i]);
+        p.part_ml = reinterpret_cast<float*>(
+            p.part_o + (size_t)d[i].B * d[i].H * f.splits * p.qblocks * 32 * CK_D);
+        M.part[i] = p;
+        M.dk[i] = d[i].dk;
+        M.heads[i] = heads ? heads[i] : nullptr;
+    }
+    int rc = NKV_OK;
+    if (!staged_gemm(d[0])) {
+        // one partition (read-time RoPE / camera, or ranks above the resident
+        // decoder's): stage8_kernel decodes its history and current tiles
+        const ChunkParams& p = M.part[0];
+        rc = set_smem(stage8_kernel, sizeof(Chunk8Smem));
+        if (rc) return rc;
+        stage8_kernel<<<dim3((unsigned)((int64_t)d[0].B * d[0].H * P.f[0].ntiles / 2)), C8_THREADS,
+                        sizeof(Chunk8Smem), s>>>(p);
+        NKV_LAUNCH_CHECK();
+    } else {
+        // both codecs in one launch when their ranks agree, the current
+        // tiles with the first
+        const int qk = d[0].key.r >> 6, qv = d[0].value.r >> 6;
+        for (int pass = 0; pass < (qk == qv ? 1 : 2); ++pass) {
+            std::vector<SegOrder> segs;
+            for (int i = 0; i < n; ++i) {
+                const int64_t bh = (int64_t)d[i].B * d[i].H;
+                const int64_t T = cdiv(d[i].n_rows, FT_T);
+                for (int cc = 0; cc < 2; ++cc) {
+                    const int r = P.ranges[i][cc];
+                    if (r == 0 || (qk != qv && cc != pass)) continue;
+                    const double w = decode_tile_cost(cc ? CK_D : d[i].dk);
+                    segs.push_back({(double)T / r * w + DECODE_BLOCK_COST, i, cc ? SEG_V : SEG_K, r,
+                                    bh * r});
+                }
+                const int64_t nct = P.f[i].ntiles - P.f[i].ntiles_hist;
+                if (pass == 0 && nct > 0)
+                    segs.push_back({CTILE_BLOCK_COST, i, SEG_CUR, 0, bh * cdiv(nct, 2)});
+            }
+            set_segments(M, segs);
+            if (seg_blocks(M) == 0) continue;
+            rc = drtile_launch(qk == qv || pass == 0 ? qk : qv, M, seg_blocks(M), s);
             if (rc) return rc;
         }
-    } else {
-        stage8_kernel<<<dim3((unsigned)(BH * f.ntiles / 2)), C8_THREADS, sizeof(Chunk8Smem), s>>>(p);
+    }
+    // flash: the kernel events bracket it
+    {
+        std::vector<SegOrder> segs;
+        for (int i = 0; i < n; ++i) {
+            const FlashPlan& f = P.f[i];
+            if (f.ntiles == 0 || f.splits == 0) continue;
+            segs.push_back({(double)f.ntiles / f.splits * flash_tile_cost(d[i].dk), i, SEG_FLASH, 0,
+                            (int64_t)d[i].B * d[i].H * f.qtiles * f.splits});
+        }
+        set_segments(M, segs);
+    }
+    if (d[0].ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d[0].ev_begin, s));
+    if (seg_blocks(M) > 0) {
+        const size_t smem = sizeof(FlashSmem<CK_D>);
+        const bool mask = M.part[0].cur_mask != nullptr;
+        rc = mask ? set_smem(flash8_kernel<true>, smem) : set_smem(flash8_kernel<false>, smem);
+        if (rc) return rc;
+        if (mask) flash8_kernel<true><<<dim3((unsigned)seg_blocks(M)), C8_THREADS, smem, s>>>(M);
+        else flash8_kernel<false><<<dim3((unsigned)seg_blocks(M)), C8_THREADS, smem, s>>>(M);
         NKV_LAUNCH_CHECK();
     }
-    // the kernel events bracket the attention (flash) kernel
-    if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
-    const dim3 grid((unsigned)(BH * f.qtiles * f.splits));
-    if (d.dk == 32) rc = flash_launch<32>(p, grid, s);
-    else if (d.dk == 64) rc = flash_launch<64>(p, grid, s);
-    else rc = flash_launch<128>(p, grid, s);
-    if (rc) return rc;
-    if (d.ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_end, s));
-    chunk_combine_kernel<<<dim3((unsigned)cdiv(BH * p.qblocks, CB_WAVES)), 64 * CB_WAVES, 0, s>>>(p);
+    if (d[0].ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d[0].ev_end, s));
+    const int64_t waves = (int64_t)d[0].B * d[0].H * M.part[0].qblocks;
+    staged_combine_kernel<<<dim3((unsigned)cdiv(waves, CB_WAVES)), 64 * CB_WAVES, 0, s>>>(
+        M, shift, sh_sb, sh_sh);
     NKV_LAUNCH_CHECK();
     return NKV_OK;
 }
 
-}  // namespace
-
-size_t chunk_launch_workspace(const ChunkLaunchDesc& d) {
-    if (use_staged(d)) return staged_workspace(d);
-    const int64_t nc = chunk_count(d.n_rows) + chunk_count(d.Nc);
-    const size_t blocks = (size_t)d.B * d.H * nc * cdiv(d.Q, 32);
-    return blocks * 32 * CK_D * sizeof(uint16_t) + blocks * 32 * 2 * sizeof(float);
-}
-
-int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_t workspace_bytes) {
-    NKV_REQUIRE(d.dk == 32 || d.dk == 64 || d.dk == 128, NKV_ERR_UNSUPPORTED,
-                "key-chunk attend supports K/Q widths 32, 64 and 128");
-    NKV_REQUIRE(d.B >= 1 && d.H >= 1 && d.Q >= 0 && d.n_rows >= 0 && d.Nc >= 0, NKV_ERR_INVALID,
-                "bad launch shape");
-    NKV_REQUIRE(d.Nc == 0 || (d.dk == CK_D && d.k_cur && d.v_cur), NKV_ERR_INVALID,
-                "current keys need k_cur/v_cur and a 128-wide launch");
-    NKV_REQUIRE(!d.cur_mask || (d.n_groups >= 1 && d.mask_words >= cdiv(d.Nc, 32)),
-                NKV_ERR_INVALID, "the current-key mask needs n_groups >= 1 and "
-                "cur_mask_words >= ceil(Nc / 32)");
-    if (d.n_rows > 0) {
-        int rc = check_chunk_codec(d.key);
-        if (rc) return rc;
-        rc = check_chunk_codec(d.value);
-        if (rc) return rc;
-    }
-    if (d.Q == 0) return NKV_OK;
-    NKV_REQUIRE(d.q && d.out, NKV_ERR_INVALID, "q and out required");
-    const size_t need = chunk_launch_workspace(d);
-    NKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), NKV_ERR_WORKSPACE,
-                "workspace missing or smaller than the size query returned");
+// Everything of a launch's ChunkParams but the workspace areas.
+ChunkParams chunk_params(const ChunkLaunchDesc& d) {
     ChunkParams p;
+    memset(&p, 0, sizeof(p));
     p.B = d.B;
     p.H = d.H;
     p.nch_hist = (int)chunk_count(d.n_rows);
@@ -1778,6 +2087,8 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.q_sb = d.q_sb;
     p.q_st = d.q_st;
     p.q_sh = d.q_sh;
+    p.q_heads = d.q_heads;
+    p.q_heads_n = d.q_heads_n;
     p.k_cur = d.k_cur;
     p.k_sb = d.k_sb;
     p.k_st = d.k_st;
@@ -1788,10 +2099,6 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.v_sh = d.v_sh;
     p.codec[0] = d.key;
     p.codec[1] = d.value;
-    const size_t qrows = (size_t)d.B * d.H * p.nch_total * p.qblocks * 32;
-    p.part_o = reinterpret_cast<uint16_t*>(workspace);
-    p.part_ml = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
-                                         qrows * CK_D * sizeof(uint16_t));
     p.out = d.out;
     p.o_sb = d.o_sb;
     p.o_st = d.o_st;
@@ -1803,15 +2110,94 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.q_group = d.q_group;
     p.n_groups = d.n_groups;
     p.mask_words = d.mask_words;
-    p.tiles = nullptr;
-    p.ntiles_hist = p.ntiles = p.qpt = p.splits = 0;
-    if (use_staged(d)) return staged_launch(s, d, p, workspace);
+    return p;
+}
+
+int check_desc(const ChunkLaunchDesc& d) {
+    NKV_REQUIRE(d.dk == 32 || d.dk == 64 || d.dk == 128, NKV_ERR_UNSUPPORTED,
+                "key-chunk attend supports K/Q widths 32, 64 and 128");
+    NKV_REQUIRE(d.B >= 1 && d.H >= 1 && d.Q >= 0 && d.n_rows >= 0 && d.Nc >= 0, NKV_ERR_INVALID,
+                "bad launch shape");
+    NKV_REQUIRE(d.Nc == 0 || (d.dk == CK_D && d.k_cur && d.v_cur), NKV_ERR_INVALID,
+                "current keys need k_cur/v_cur and a 128-wide launch");
+    NKV_REQUIRE(!d.cur_mask || (d.n_groups >= 1 && d.mask_words >= cdiv(d.Nc, 32)),
+                NKV_ERR_INVALID, "the current-key mask needs n_groups >= 1 and "
+                "cur_mask_words >= ceil(Nc / 32)");
+    NKV_REQUIRE(!d.q_heads || d.q_heads_n >= 1, NKV_ERR_INVALID, "q_heads needs q_heads_n >= 1");
+    if (d.n_rows > 0) {
+        int rc = check_chunk_codec(d.key);
+        if (rc) return rc;
+        rc = check_chunk_codec(d.value);
+        if (rc) return rc;
+    }
+    return NKV_OK;
+}
+
+}  // namespace
+
+size_t chunk_launch_workspace(const ChunkLaunchDesc& d) {
+    if (use_staged(d)) return multi_plan(&d, 1).total;
+    const int64_t nc = chunk_count(d.n_rows) + chunk_count(d.Nc);
+    const size_t blocks = (size_t)d.B * d.H * nc * cdiv(d.Q, 32);
+    return blocks * 32 * CK_D * sizeof(uint16_t) + blocks * 32 * 2 * sizeof(float);
+}
+
+bool staged_multi_supported(const ChunkLaunchDesc* d, int n) {
+    if (n < 1 || n > NKV_MAX_PARTS) return false;
+    for (int i = 0; i < n; ++i) {
+        if (!use_staged(d[i]) && !(i > 0 && d[i].n_rows == 0 && d[i].Nc == 0)) return false;
+        if (!staged_gemm(d[i]) || d[i].Q != d[0].Q || d[i].B != d[0].B) return false;
+        if (d[i].key.r != d[0].key.r || d[i].value.r != d[0].value.r) return false;
+        if (i > 0 && (d[i].Nc > 0 || d[i].cur_mask)) return false;
+    }
+    return d[0].dk == CK_D;
+}
+
+size_t staged_multi_workspace(const ChunkLaunchDesc* d, int n) { return multi_plan(d, n).total; }
+
+int staged_multi_launch(hipStream_t s, const ChunkLaunchDesc* d, int n, const int32_t* const* heads,
+                        const float* shift, int64_t sh_sb, int64_t sh_sh, void* workspace,
+                        size_t workspace_bytes) {
+    NKV_REQUIRE(staged_multi_supported(d, n), NKV_ERR_UNSUPPORTED,
+                "these partitions do not fit one staged launch");
+    ChunkParams ps[NKV_MAX_PARTS];
+    for (int i = 0; i < n; ++i) {
+        int rc = check_desc(d[i]);
+        if (rc) return rc;
+        NKV_REQUIRE(i == 0 || (heads && heads[i]), NKV_ERR_INVALID,
+                    "every partition after the first needs its head list");
+        ps[i] = chunk_params(d[i]);
+    }
+    if (d[0].Q == 0) return NKV_OK;
+    NKV_REQUIRE(d[0].q && d[0].out, NKV_ERR_INVALID, "q and out required");
+    const size_t need = staged_multi_workspace(d, n);
+    NKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), NKV_ERR_WORKSPACE,
+                "workspace missing or smaller than the size query returned");
+    return staged_run(s, d, ps, n, heads, shift, sh_sb, sh_sh, workspace);
+}
+
+int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_t workspace_bytes) {
+    int rc = check_desc(d);
+    if (rc) return rc;
+    // the head maps of the tables are read by the decode GEMM alone
+    NKV_REQUIRE((!d.key.c_heads && !d.value.c_heads) || (use_staged(d) && staged_gemm(d)),
+                NKV_ERR_UNSUPPORTED, "table head maps need the staged decode GEMM");
+    if (d.Q == 0) return NKV_OK;
+    NKV_REQUIRE(d.q && d.out, NKV_ERR_INVALID, "q and out required");
+    const size_t need = chunk_launch_workspace(d);
+    NKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), NKV_ERR_WORKSPACE,
+                "workspace missing or smaller than the size query returned");
+    ChunkParams p = chunk_params(d);
+    if (use_staged(d)) return staged_run(s, &d, &p, 1, nullptr, nullptr, 0, 0, workspace);
+    const size_t qrows = (size_t)d.B * d.H * p.nch_total * p.qblocks * 32;
+    p.part_o = reinterpret_cast<uint16_t*>(workspace);
+    p.part_ml = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
+                                         qrows * CK_D * sizeof(uint16_t));
 
     const int64_t hist_blocks = (int64_t)d.B * d.H * p.nch_hist;
     const int64_t cur_blocks = (int64_t)d.B * d.H * (p.nch_total - p.nch_hist) * p.cur_splits;
     p.blk_base = 0;
     if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
-    int rc = NKV_OK;
     if (p.cur_mask) {
         // history chunks, then the masked current-key chunks (128 wide)
         if (hist_blocks > 0) {

@@ -261,6 +261,7 @@ size_t align_up(size_t n) { return (n + WS_ALIGN - 1) / WS_ALIGN * WS_ALIGN; }
 // Workspace of one call: fixed buffers, then one partial area reused by
 // every chunk launch (they run in stream order).
 struct FastLayout {
+    bool multi;                    // the staged multi-partition launch serves the call
     size_t lse_n;                  // [B, H, Q] f32
     std::vector<size_t> q_low, kc, vc, kb, vb, out_l, lse_l;  // per group
     size_t partials;
@@ -426,8 +427,24 @@ ChunkLaunchDesc native_desc(const nkv_fast_args* f, float* lse_n) {
     return d;
 }
 
+// Identity readers (k_affine / v_affine null): their center tables and
+// means are the layer's own (bf16 columns of head heads[i]; the mean applied
+// as bf16), read through the head map instead of projected copies.
+// Identity q_reduce: the queries are the layer's (pre-RoPE when given).
+// The staged multi-partition launch reads them so; the per-group launches
+// take projected copies.
+struct ReaderIdent {
+    bool q, k, v;
+};
+
+ReaderIdent reader_ident(const nkv_reader_group& G, bool multi) {
+    return multi ? ReaderIdent{!G.q_reduce, !G.k_affine, !G.v_affine} : ReaderIdent{false, false, false};
+}
+
 // Low-partition launch of group g over the workspace tables.
-ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const FastLayout& L) {
+ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const FastLayout& L,
+                         bool multi = false) {
+    const ReaderIdent id = reader_ident(f->groups[g], multi);
     const nkv_attend_args& a = f->attend;
     const nkv_reader_group& G = f->groups[g];
     const int nh = G.num_heads, dd = G.d, D = a.D;
@@ -441,10 +458,22 @@ ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const
     d.rows = f->low_rows;
     d.Nc = 0;
     d.softmax_scale = a.softmax_scale;
-    d.q = reinterpret_cast<const uint16_t*>(ws + L.q_low[g]);  // [B, Q, nh, d]
-    d.q_sb = a.Q * nh * dd;
-    d.q_st = (int64_t)nh * dd;
-    d.q_sh = dd;
+    auto at = [&](size_t off) { return ws ? ws + off : nullptr; };
+    if (id.q) {
+        // the layer's queries of heads G.heads
+        const bool pre = reader_q_pre(f);
+        d.q = reinterpret_cast<const uint16_t*>(pre ? f->q_pre : a.q);
+        d.q_sb = pre ? f->qp_sb : a.q_sb;
+        d.q_st = pre ? f->qp_st : a.q_st;
+        d.q_sh = pre ? f->qp_sh : a.q_sh;
+        d.q_heads = G.heads;
+        d.q_heads_n = a.H;
+    } else {
+        d.q = reinterpret_cast<const uint16_t*>(at(L.q_low[g]));  // [B, Q, nh, d]
+        d.q_sb = a.Q * nh * dd;
+        d.q_st = (int64_t)nh * dd;
+        d.q_sh = dd;
+    }
     for (int cc = 0; cc < 2; ++cc) {
         const nkv_codec& c = cc ? a.value : a.key;
         ChunkCodec v{};
@@ -465,60 +494,111 @@ ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const
         const int width = cc ? D : dd;
         v.w = cc ? G.v_read : G.k_read;
         v.w_hs = (int64_t)width * c.r;
+        if (cc ? id.v : id.k) {
+            // the layer's tables, as the native partition reads them
+            const ChunkCodec own = chunk_codec_from(c, D, a.H * D);
+            v.seg_flat = own.seg_flat;
+            v.has_centers = own.has_centers;
+            v.centers = own.centers;
+            v.c_bs = own.c_bs;
+            v.c_rs = own.c_rs;
+            v.c_hs = own.c_hs;
+            v.bias = own.bias;
+            v.bias_hs = own.bias_hs;
+            v.c_heads = G.heads;
+            v.c_heads_n = a.H;
+            (cc ? d.value : d.key) = v;
+            continue;
+        }
         if (has_centers(c)) {
             // projected table [tables][nh][C][width]
             const int64_t C = table_rows(c);
             v.has_centers = 1;
-            v.centers = reinterpret_cast<const uint16_t*>(ws + (cc ? L.vc[g] : L.kc[g]));
+            v.centers = reinterpret_cast<const uint16_t*>(at(cc ? L.vc[g] : L.kc[g]));
             v.c_rs = width;
             v.c_hs = C * width;
             v.c_bs = table_batches(c, a.B) > 1 ? (int64_t)nh * C * width : 0;
         }
         if (c.mean) {
-            v.bias = reinterpret_cast<const float*>(ws + (cc ? L.vb[g] : L.kb[g]));
+            v.bias = reinterpret_cast<const float*>(at(cc ? L.vb[g] : L.kb[g]));
             v.bias_hs = width;
         }
         (cc ? d.value : d.key) = v;
     }
-    d.out = reinterpret_cast<uint16_t*>(ws + L.out_l[g]);  // [B, Q, nh, D]
+    d.out = reinterpret_cast<uint16_t*>(at(L.out_l[g]));  // [B, Q, nh, D]
     d.o_sb = a.Q * nh * D;
     d.o_st = (int64_t)nh * D;
     d.o_sh = D;
-    d.lse = reinterpret_cast<float*>(ws + L.lse_l[g]);
+    d.lse = reinterpret_cast<float*>(at(L.lse_l[g]));
     return d;
+}
+
+// The partitions of the staged multi-partition launch: the native one, then
+// every reader group (heads[1 + g] = its heads).
+int multi_descs(const nkv_fast_args* f, unsigned char* ws, const FastLayout& L,
+                ChunkLaunchDesc* d, const int32_t** heads) {
+    d[0] = native_desc(f, f->attend.lse);
+    heads[0] = nullptr;
+    for (int g = 0; g < f->num_groups; ++g) {
+        d[1 + g] = low_desc(f, g, ws, L, true);
+        heads[1 + g] = f->groups[g].heads;
+    }
+    return 1 + f->num_groups;
+}
+
+// One decode, one flash and one combine launch serve the whole call (every
+// partition merged in the combine, no per-group merge) when there is no
+// read-time RoPE or camera and the native partition and the reader groups
+// fit one staged launch.
+bool use_multi(const nkv_fast_args* f) {
+    const nkv_attend_args& a = f->attend;
+    if (a.rope || a.camera || f->n_low == 0 || f->num_groups < 1 ||
+        f->num_groups + 1 > NKV_MAX_PARTS)
+        return false;
+    FastLayout L{};
+    for (auto* v : {&L.q_low, &L.kc, &L.vc, &L.kb, &L.vb, &L.out_l, &L.lse_l})
+        v->assign(f->num_groups, 0);
+    ChunkLaunchDesc d[NKV_MAX_PARTS];
+    const int32_t* heads[NKV_MAX_PARTS];
+    const int n = multi_descs(f, nullptr, L, d, heads);
+    return staged_multi_supported(d, n);
 }
 
 FastLayout layout(const nkv_fast_args* f) {
     const nkv_attend_args& a = f->attend;
     FastLayout L;
+    L.multi = use_multi(f);
     size_t off = 0;
     auto take = [&](size_t bytes) {
         const size_t o = off;
         off += align_up(bytes);
         return o;
     };
-    L.lse_n = take(a.lse ? 0 : (size_t)a.B * a.H * a.Q * sizeof(float));
-    size_t part = chunk_launch_workspace(native_desc(f, nullptr));
+    L.lse_n = take(a.lse || L.multi ? 0 : (size_t)a.B * a.H * a.Q * sizeof(float));
     for (int g = 0; g < f->num_groups; ++g) {
         const nkv_reader_group& G = f->groups[g];
+        const ReaderIdent id = reader_ident(G, L.multi);
         const size_t nh = G.num_heads, dd = G.d, D = a.D;
-        L.q_low.push_back(take((size_t)a.B * a.Q * nh * dd * 2));
-        const size_t kt = has_centers(a.key) ? (size_t)table_batches(a.key, a.B) : 0;
-        const size_t vt = has_centers(a.value) ? (size_t)table_batches(a.value, a.B) : 0;
+        L.q_low.push_back(take(id.q ? 0 : (size_t)a.B * a.Q * nh * dd * 2));
+        const size_t kt = has_centers(a.key) && !id.k ? (size_t)table_batches(a.key, a.B) : 0;
+        const size_t vt = has_centers(a.value) && !id.v ? (size_t)table_batches(a.value, a.B) : 0;
         L.kc.push_back(take(kt * nh * (size_t)table_rows(a.key) * dd * 2));
         L.vc.push_back(take(vt * nh * (size_t)table_rows(a.value) * D * 2));
-        L.kb.push_back(take(nh * dd * sizeof(float)));
-        L.vb.push_back(take(nh * D * sizeof(float)));
-        L.out_l.push_back(take((size_t)a.B * a.Q * nh * D * 2));
-        L.lse_l.push_back(take((size_t)a.B * nh * a.Q * sizeof(float)));
+        L.kb.push_back(take(id.k ? 0 : nh * dd * sizeof(float)));
+        L.vb.push_back(take(id.v ? 0 : nh * D * sizeof(float)));
+        L.out_l.push_back(take(L.multi ? 0 : (size_t)a.B * a.Q * nh * D * 2));
+        L.lse_l.push_back(take(L.multi ? 0 : (size_t)a.B * nh * a.Q * sizeof(float)));
     }
-    for (int g = 0; g < f->num_groups; ++g) {
-        ChunkLaunchDesc shape{};
-        shape.B = a.B;
-        shape.H = f->groups[g].num_heads;
-        shape.Q = a.Q;
-        shape.n_rows = f->n_low;
-        part = std::max(part, chunk_launch_workspace(shape));
+    size_t part;
+    if (L.multi) {
+        ChunkLaunchDesc d[NKV_MAX_PARTS];
+        const int32_t* heads[NKV_MAX_PARTS];
+        const int n = multi_descs(f, nullptr, L, d, heads);
+        part = staged_multi_workspace(d, n);
+    } else {
+        part = chunk_launch_workspace(native_desc(f, nullptr));
+        for (int g = 0; g < f->num_groups; ++g)
+            part = std::max(part, chunk_launch_workspace(low_desc(f, g, nullptr, L)));
     }
     L.partials = take(part);
     L.total = off;
@@ -547,6 +627,72 @@ int project(hipStream_t s, const void* x, int64_t x_b, int64_t x_m, int64_t x_h,
             x, x_b, x_m, x_h, seg, n_seg, heads, H, w, D, E, nb, nh, M, out, o_b, o_i, o_m);
     }
     NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+// The tables reader group g reads through (CN/core.py:155-204): q_low, and
+// its projected center tables and means, for the parts that are not the
+// layer's own (identity readers of the multi-partition launch).
+int reader_tables(hipStream_t s, const nkv_fast_args* f, int g, unsigned char* ws,
+                  const FastLayout& L, const RopeDev& qrope, const CameraDev& qcam) {
+    const nkv_attend_args& a = f->attend;
+    const nkv_reader_group& G = f->groups[g];
+    const ReaderIdent id = reader_ident(G, L.multi);
+    const int D = a.D, HD = a.H * a.D;
+    const int nh = G.num_heads, dd = G.d;
+    int rc = NKV_OK;
+    // q_low [B, Q, nh, d] from the pre-RoPE, pre-camera queries when
+    // given (then rotated / transformed on its retained pairs and blocks)
+    uint16_t* q_low = reinterpret_cast<uint16_t*>(ws + L.q_low[g]);
+    if (!id.q) {
+        if (reader_q_pre(f))
+            rc = project<false, false>(s, f->q_pre, f->qp_sb, f->qp_st, f->qp_sh, nullptr, 0,
+                                       G.heads, a.H, G.q_reduce, D, dd, a.B, nh, a.Q, q_low,
+                                       a.Q * nh * dd, dd, (int64_t)nh * dd);
+        else
+            rc = project<false, false>(s, a.q, a.q_sb, a.q_st, a.q_sh, nullptr, 0, G.heads, a.H,
+                                       G.q_reduce, D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
+                                       (int64_t)nh * dd);
+        if (rc) return rc;
+    }
+    if (a.rope) {
+        RopeDev qp = qrope;
+        qp.pairs = G.rope_pairs;
+        const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 2);
+        rope_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(q_low, a.B, a.Q, nh,
+                                                                          dd, qp);
+        NKV_LAUNCH_CHECK();
+    }
+    if (a.camera) {
+        const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 8) * 2;
+        camera_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(
+            q_low, a.B, a.Q, nh, dd, qcam, G.cam_blocks);
+        NKV_LAUNCH_CHECK();
+    }
+    for (int cc = 0; cc < 2 && f->n_low > 0; ++cc) {
+        if (cc ? id.v : id.k) continue;
+        const nkv_codec& c = cc ? a.value : a.key;
+        const int width = cc ? D : dd;
+        const uint16_t* aff = cc ? G.v_affine : G.k_affine;
+        if (has_centers(c)) {
+            // [tables][nh][C][width] = center columns of each head . affine
+            const int nb = table_batches(c, a.B);
+            const int64_t C = table_rows(c);
+            rc = project<false, false>(
+                s, c.centers, c.centers_batch_stride, HD, D,
+                c.n_segments > 0 ? c.segments_dev : nullptr, c.n_segments, G.heads, a.H, aff,
+                D, width, nb, nh, C, ws + (cc ? L.vc[g] : L.kc[g]), (int64_t)nh * C * width,
+                C * width, width);
+            if (rc) return rc;
+        }
+        if (c.mean) {
+            // [nh][width] = bf16(mean of each head) . affine
+            rc = project<true, true>(s, c.mean, 0, 0, D, nullptr, 0, G.heads, a.H, aff, D,
+                                     width, 1, nh, 1, ws + (cc ? L.vb[g] : L.kb[g]), 0, width,
+                                     0);
+            if (rc) return rc;
+        }
+    }
     return NKV_OK;
 }
 
@@ -590,6 +736,20 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
         if (f->q_camera) camera_from_abi(f->q_camera, a.D, a.B, &qcam);
     }
 
+    if (L.multi) {
+        // the reader tables, then every partition in one staged launch whose
+        // combine merges each head's partitions into out / lse
+        for (int g = 0; g < f->num_groups; ++g) {
+            rc = reader_tables(s, f, g, ws, L, qrope, qcam);
+            if (rc) return rc;
+        }
+        ChunkLaunchDesc d[NKV_MAX_PARTS];
+        const int32_t* heads[NKV_MAX_PARTS];
+        const int n = multi_descs(f, ws, L, d, heads);
+        return staged_multi_launch(s, d, n, heads, f->low_shift, f->ls_sb, f->ls_sh,
+                                   ws + L.partials, part_bytes);
+    }
+
     // 1. native partition -> out, lse_n
     ChunkLaunchDesc nd = native_desc(f, lse_n);
     nd.rope = krope;
@@ -600,59 +760,11 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
     if (f->n_low == 0) return NKV_OK;
 
     // 2-3. reader groups
-    const int D = a.D, HD = a.H * a.D;
     for (int g = 0; g < f->num_groups; ++g) {
         const nkv_reader_group& G = f->groups[g];
-        const int nh = G.num_heads, dd = G.d;
-        // q_low [B, Q, nh, d] from the pre-RoPE, pre-camera queries when
-        // given (then rotated / transformed on its retained pairs and blocks)
-        uint16_t* q_low = reinterpret_cast<uint16_t*>(ws + L.q_low[g]);
-        if (reader_q_pre(f))
-            rc = project<false, false>(s, f->q_pre, f->qp_sb, f->qp_st, f->qp_sh, nullptr, 0,
-                                       G.heads, a.H, G.q_reduce, D, dd, a.B, nh, a.Q, q_low,
-                                       a.Q * nh * dd, dd, (int64_t)nh * dd);
-        else
-            rc = project<false, false>(s, a.q, a.q_sb, a.q_st, a.q_sh, nullptr, 0, G.heads, a.H,
-                                       G.q_reduce, D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
-                                       (int64_t)nh * dd);
+        const int nh = G.num_heads, D = a.D;
+        rc = reader_tables(s, f, g, ws, L, qrope, qcam);
         if (rc) return rc;
-        if (a.rope) {
-            RopeDev qp = qrope;
-            qp.pairs = G.rope_pairs;
-            const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 2);
-            rope_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(q_low, a.B, a.Q, nh,
-                                                                              dd, qp);
-            NKV_LAUNCH_CHECK();
-        }
-        if (a.camera) {
-            const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 8) * 2;
-            camera_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(
-                q_low, a.B, a.Q, nh, dd, qcam, G.cam_blocks);
-            NKV_LAUNCH_CHECK();
-        }
-        for (int cc = 0; cc < 2 && f->n_low > 0; ++cc) {
-            const nkv_codec& c = cc ? a.value : a.key;
-            const int width = cc ? D : dd;
-            const uint16_t* aff = cc ? G.v_affine : G.k_affine;
-            if (has_centers(c)) {
-                // [tables][nh][C][width] = center columns of each head . affine
-                const int nb = table_batches(c, a.B);
-                const int64_t C = table_rows(c);
-                rc = project<false, false>(
-                    s, c.centers, c.centers_batch_stride, HD, D,
-                    c.n_segments > 0 ? c.segments_dev : nullptr, c.n_segments, G.heads, a.H, aff,
-                    D, width, nb, nh, C, ws + (cc ? L.vc[g] : L.kc[g]), (int64_t)nh * C * width,
-                    C * width, width);
-                if (rc) return rc;
-            }
-            if (c.mean) {
-                // [nh][width] = bf16(mean of each head) . affine
-                rc = project<true, true>(s, c.mean, 0, 0, D, nullptr, 0, G.heads, a.H, aff, D,
-                                         width, 1, nh, 1, ws + (cc ? L.vb[g] : L.kb[g]), 0, width,
-                                         0);
-                if (rc) return rc;
-            }
-        }
         ChunkLaunchDesc ld = low_desc(f, g, ws, L);
         if (a.rope) {
             ld.rope = krope;

@@ -23,6 +23,12 @@ struct ChunkCodec {
     int64_t c_bs, c_rs, c_hs;
     const float* bias;        // (i, d): bias[i*bias_hs + d], applied as bf16; null = none
     int64_t bias_hs;
+    // Head of the center table and bias of launch head i: c_heads[i] clamped
+    // to [0, c_heads_n) (null: i).  Lets a launch over a subset of a layer's
+    // heads read the layer's own tables; honoured by the resident-decoder
+    // tile kernel only (the staged schedule's decode GEMM).
+    const int32_t* c_heads;
+    int c_heads_n;
     // Segment table in device memory (null: the flat arrays above).  Row n of
     // batch item b lives in segment s = seg_find(n) at local row n - row_start.
     // seg_flat == 0: its center is (b, id) of the segment's own table
@@ -94,6 +100,10 @@ __device__ __forceinline__ const uint16_t* center_row(const ChunkCodec& c, int b
 // codec tables, K to width dk, V to width 128) and the current keys
 // k_cur/v_cur[b, 0 .. Nc, i]; out[b, :, i, :128] bf16, lse[b, i, :] natural
 // log (or null).
+// Partitions of one multi-partition staged launch (a NanoKV-Fast call's
+// native partition and reader groups).
+constexpr int NKV_MAX_PARTS = 4;
+
 struct ChunkLaunchDesc {
     int B, H, dk;
     int64_t Q, N, n_rows, Nc;
@@ -101,6 +111,10 @@ struct ChunkLaunchDesc {
     float softmax_scale;
     const uint16_t* q;
     int64_t q_sb, q_st, q_sh;
+    // query head of launch head i: q_heads[i] clamped to [0, q_heads_n)
+    // (null: i); staged schedule only
+    const int32_t* q_heads;
+    int q_heads_n;
     const uint16_t* k_cur;
     int64_t k_sb, k_st, k_sh;
     const uint16_t* v_cur;
@@ -135,5 +149,21 @@ int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace
                         size_t workspace_bytes);
 size_t chunk_launch_workspace(const ChunkLaunchDesc& d);
 int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_t workspace_bytes);
+
+// Partitions d[0 .. n) of one attention call through the staged schedule in
+// one decode, one flash and one combine launch (the decode in two when the
+// codecs' ranks differ).  Partition 0 (128 wide) covers every head of the
+// layer; the combine writes the merged output and LSE to its out / lse.
+// Partition i >= 1 covers heads heads[i][0 .. d[i].H) of the layer (the first
+// partition listing a head is merged into it; heads outside the layer are
+// never merged), its output shifted by shift[b*sh_sb + h*sh_sh + e] (null:
+// none) before the merge.  Supported: every partition staged by the decode
+// GEMM (no read-time RoPE or camera, ranks <= 384, the same codec ranks, B
+// and Q), current keys in partition 0 only.
+bool staged_multi_supported(const ChunkLaunchDesc* d, int n);
+size_t staged_multi_workspace(const ChunkLaunchDesc* d, int n);
+int staged_multi_launch(hipStream_t s, const ChunkLaunchDesc* d, int n, const int32_t* const* heads,
+                        const float* shift, int64_t sh_sb, int64_t sh_sh, void* workspace,
+                        size_t workspace_bytes);
 
 }  // namespace nkv
