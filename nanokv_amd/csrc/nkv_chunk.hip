@@ -102,7 +102,7 @@ struct ChunkParams {
     // tiles 0 .. ntiles_hist, two per 256-key chunk, then the current keys'),
     // qpt query blocks per flash block, `splits` key ranges per query block
     uint16_t* tiles;
-    int ntiles_hist, ntiles, qpt, splits;
+    int ntiles_hist, ntiles, qpt, splits, qtiles;
 };
 
 // ------------------------------------------------ multi-partition launches
@@ -1245,12 +1245,20 @@ __device__ __forceinline__ void flash_block(const ChunkParams& p, int64_t blk, u
     int lane = threadIdx.x & 63;
     asm volatile("" : "+v"(lane));
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    // (batch, head) fastest: with B*H a multiple of 8 every block of a head
-    // runs on one XCD (blockIdx % 8), whose L2 then serves its tiles to the
-    // head's other query tiles
+    // Work items in group-major order (group g = (head, split) = bh + B*H *
+    // split, then its qtiles query tiles), cut into eight equal runs, one
+    // per XCD: block blk is dispatch slot blk / 8 of XCD blk % 8 (the
+    // segment starts at a multiple of 8) and takes item (blk % 8) * per +
+    // blk / 8.  The query tiles of a group then run on one XCD in
+    // consecutive slots, streaming the same tiles at the same time, so that
+    // XCD's L2 serves all but the first read of each tile; every XCD gets the
+    // same number of items, the last run ending in empty blocks.
     const int BH = p.B * p.H;
-    const int bh = (int)(blk % BH), rest = (int)(blk / BH);
-    const int split = rest % p.splits, qt = rest / p.splits;
+    const int64_t items = (int64_t)BH * p.splits * p.qtiles, per = (items + 7) >> 3;
+    const int64_t item = (blk & 7) * per + (blk >> 3);
+    if (item >= items) return;
+    const int g = (int)(item / p.qtiles), qt = (int)(item % p.qtiles);
+    const int bh = g % BH, split = g / BH;
     const int b = bh / p.H, h = bh % p.H;
     const int t0 = (int)((int64_t)split * p.ntiles / p.splits);
     const int t1 = (int)((int64_t)(split + 1) * p.ntiles / p.splits);
@@ -1988,6 +1996,7 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
         p.ntiles_hist = f.ntiles_hist;
         p.ntiles = f.ntiles;
         p.qpt = f.qpt;
+        p.qtiles = f.qtiles;
         p.splits = std::max(f.splits, 1);
         // the partials of the splits, in the key-chunk layout with chunk = split
         p.nch_hist = 0;
@@ -2041,8 +2050,9 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
         for (int i = 0; i < n; ++i) {
             const FlashPlan& f = P.f[i];
             if (f.ntiles == 0 || f.splits == 0) continue;
+            // eight equal runs of work items, one per XCD (see flash_block)
             segs.push_back({(double)f.ntiles / f.splits * flash_tile_cost(d[i].dk), i, SEG_FLASH, 0,
-                            (int64_t)d[i].B * d[i].H * f.qtiles * f.splits});
+                            8 * cdiv((int64_t)d[i].B * d[i].H * f.splits * f.qtiles, 8)});
         }
         set_segments(M, segs);
     }
