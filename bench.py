@@ -496,7 +496,7 @@ def main():
         schedule = "key_chunks" if shape.Q > 256 else "query_tiles"
     kernel = "nkv::chunk_kernel" if schedule == "key_chunks" else "nkv::attend_kernel"
     # the key-chunk path stages from 32 query blocks up: the history is decoded
-    # once into tiles (dtile_kernel), then the flash kernel -- the one the
+    # once into tiles (drtile_kernel), then the flash kernel -- the one the
     # events bracket -- does the attention flops
     kflops = fl["total"]
     if schedule == "key_chunks" and -(-shape.Q // 32) >= 32 and not fast:

@@ -19,6 +19,15 @@
 //     decoding k_low / v_low in-kernel -> out_l, lse_l;
 //  3. merge(out, lse_n, out_l, lse_l) per group head (CN/core.py:33-42), the
 //     lift being the identity (vd == D).
+// Without read-time RoPE or camera, from 32 query blocks up and with at most
+// NKV_MAX_PARTS - 1 groups, all partitions run as one staged launch
+// (staged_multi_launch): one decode launch for every partition's tiles, one
+// flash launch over all of them, and one combine that folds each head's
+// native and group partials together (the merge of step 3, with the
+// low_shift), so no group output or LSE is written.  Identity readers then
+// read the layer's own queries, center tables and means through head maps
+// instead of projected copies.  Otherwise the partitions run one after
+// another and group_merge_kernel merges each group's output in place.
 // The projected tables are small (C x d per head); they are recomputed per
 // call, as the reference's read does.  With a segmented codec the tables of
 // every segment are projected into one table (segment s at rows center_base

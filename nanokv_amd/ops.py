@@ -1003,7 +1003,8 @@ def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[
     protect_rows / low_rows: int32 codec rows of the native and low
     partitions; groups: ReaderTensors covering every head once.  Returns
     (out [B, Q, H, D] bf16, lse [B, H, Q] fp32 or None).  kernel_events
-    bracket the native partition's attention kernel.  rope: positions of the
+    bracket the native partition's attention kernel (the one attention launch
+    of every partition when they run as one staged launch).  rope: positions of the
     codec rows (history keys rotated at read); then q is the rotated query,
     q_pre [B, Q, H, D] the pre-RoPE query the reader groups project and
     q_rope the queries' positions (query t at row t).  camera: P^-1 of the
