@@ -968,10 +968,12 @@ constexpr int DR_THREADS = 512;
 constexpr int DR_MAXQ = 6;             // 64-rank decoder slices held: r <= 384
 constexpr int DR_SLICE = CK_D * 64;    // elements per slice
 constexpr int DR_MAXT = 24;            // tiles per block (the center-row table)
+constexpr int DR_SROW = 40;            // staging row: 32 values + 8 of padding (80 B)
 struct DResSmem {
     uint16_t dec[DR_MAXQ * DR_SLICE];      // slice s at s * DR_SLICE: [128 rows][64], chunks swizzled
     const uint16_t* crow[DR_MAXT * FT_T];  // center row of key k of tile ta + k / 128
     float bias[CK_D];
+    uint16_t stage[DR_THREADS / 64][32 * DR_SROW];  // per wave: one 32 x 32 slice of its output
 };
 static_assert(sizeof(DResSmem) <= 160 * 1024, "LDS budget");
 
@@ -1133,11 +1135,28 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
         }
         {
             uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + tile) * TF::TILE + CODEC * TF::K_IMG;
+            // Each 32-column slice dt of the wave's output goes through its own
+            // LDS staging rows, then out as 64 contiguous bytes per row (four
+            // lanes of 16 B): K rows are the wave's 32 keys at columns 32 dt ..,
+            // V^T rows 32 dt .. at the wave's 32 key columns.  Scattered 8-byte
+            // stores from the accumulator layout would cost the L2 four times
+            // the write requests.
+            uint16_t* st = sm.stage[wave];
+            auto flush = [&](int dt) {
+#pragma unroll
+                for (int i = 0; i < 2; ++i) {
+                    const int r = (lane >> 2) + 16 * i, c = lane & 3;
+                    const u32x4 x = *reinterpret_cast<const u32x4*>(st + r * DR_SROW + 8 * c);
+                    uint16_t* dst = CODEC == 0 ? img + (32 * kq + r) * DK + 32 * dt + 8 * c
+                                               : img + (32 * dt + r) * FT_ROW + 32 * kq + 8 * c;
+                    *reinterpret_cast<u32x4*>(dst) = x;
+                }
+            };
             if (CODEC == 0) {
                 // acc[dt] element i: d = 32 dt + 8 (i/4) + 4 hf + i%4 of this
                 // lane's key; K = bf16(bf16(acc + bias) + center)
 #pragma unroll
-                for (int dt = 0; dt < NDT; ++dt)
+                for (int dt = 0; dt < NDT; ++dt) {
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int d = 32 * dt + 8 * g + 4 * hf;
@@ -1152,9 +1171,11 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                             a[2] += __uint_as_float(c1 << 16);
                             a[3] += __uint_as_float(c1 & 0xffff0000u);
                         }
-                        *reinterpret_cast<u32x2*>(img + key * DK + d) =
+                        *reinterpret_cast<u32x2*>(st + l32 * DR_SROW + 8 * g + 4 * hf) =
                             u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
                     }
+                    flush(dt);
+                }
             } else {
                 // acc[dt] element i: key 32 kq + 8 (i/4) + 4 hf + i%4, d = 32 dt
                 // + l32; V = bf16(bf16(acc + bias) + center), written to V^T in
@@ -1170,10 +1191,10 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                             const float a = bf16_round(acc[dt][4 * g + e] + bs);
                             v[e] = cent ? a + __uint_as_float((cv[16 * dt + 4 * g + e] & 0xffffu) << 16) : a;
                         }
-                        *reinterpret_cast<u32x2*>(img + (32 * dt + l32) * FT_ROW +
-                                                   vt_col(32 * kq + 8 * g + 4 * hf)) =
+                        *reinterpret_cast<u32x2*>(st + l32 * DR_SROW + vt_col(8 * g + 4 * hf)) =
                             u32x2{pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3])};
                     }
+                    flush(dt);
                 }
             }
         }
