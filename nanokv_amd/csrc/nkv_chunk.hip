@@ -1744,11 +1744,14 @@ int set_smem(K* kernel, size_t smem) {
 
 // ---------------------------------------------------------- staged (host)
 constexpr int FT_CUS = 256;          // compute units of an MI355X
-// The staged schedule from 32 query blocks up: below, the key-chunk
-// schedule's per-chunk partials cost less than writing the decoded tiles
-// (measured: 49 blocks, 1,560 queries over 14,040 keys, favour staging; 25
-// blocks, 780 queries over 50,700 keys, do not).
-constexpr int FT_MIN_QBLOCKS = 32;
+// The staged schedule from 8 query blocks up: below, the key-chunk schedule's
+// per-chunk partials (query blocks x 8.25 KB per 256 keys) cost less than
+// writing and reading the decoded tiles (128 KB per 256 keys).  Measured on
+// MI355X against the key-chunk kernel (cfg1's codec, Q = Nc): 12 blocks over
+// 49,920 history keys 0.747 vs 0.837 ms, over 12,480 keys 0.224 vs 0.254 ms;
+// 16 blocks 0.764 vs 0.918 and 0.245 vs 0.286 ms; cfg2 (25 blocks) 0.950 vs
+// 1.067 ms.
+constexpr int FT_MIN_QBLOCKS = 8;
 
 struct FlashPlan {
     int qpt, qtiles, splits, ntiles_hist, ntiles;

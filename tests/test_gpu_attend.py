@@ -51,9 +51,8 @@ def test_attend_key_chunk_edges(dev, N, Nc, Q):
     _check(Scenario(H=2, N=N, Q=Q, Nc=Nc, rK=256, rV=384, G=32, C=16), dev, schedule="key_chunks")
 
 
-# current-key chunks run as several blocks over shares of the query blocks
-# (two shares from 32..47 query blocks, three from 48 or more): uneven
-# shares, partial current chunks, a partial last query block
+# many query blocks with long current-key runs (the staged schedule at
+# these sizes): partial current chunks and tiles, a partial last query block
 @pytest.mark.parametrize("N,Nc,Q", [(300, 600, 1100), (0, 300, 1530), (256, 1, 1024)])
 def test_attend_current_chunk_query_shares(dev, N, Nc, Q):
     _check(Scenario(H=2, N=N, Q=Q, Nc=Nc, rK=128, rV=128, G=32, C=8), dev, schedule="key_chunks")
