@@ -69,6 +69,49 @@ def parse():
     return ap.parse_args()
 
 
+class HipTimer:
+    """Timing events of the HIP runtime torch has loaded, created without the
+    system-scope fence a default timing event performs when it completes
+    (hipEventDisableSystemFence): that fence writes back and invalidates the
+    caches around every recorded event, which delays the next launch by
+    several microseconds.  Recorded by the library around its kernel
+    (kernel events) or on the current stream (record)."""
+
+    DISABLE_SYSTEM_FENCE = 0x20000000
+
+    def __init__(self):
+        import ctypes
+        self.ct = ctypes
+        self.hip = ctypes.CDLL("libamdhip64.so")
+        self.hip.hipEventCreateWithFlags.argtypes = [ctypes.POINTER(ctypes.c_void_p), ctypes.c_uint]
+        self.hip.hipEventRecord.argtypes = [ctypes.c_void_p, ctypes.c_void_p]
+        self.hip.hipEventElapsedTime.argtypes = [ctypes.POINTER(ctypes.c_float), ctypes.c_void_p,
+                                                 ctypes.c_void_p]
+        self.hip.hipEventDestroy.argtypes = [ctypes.c_void_p]
+
+    def event(self) -> int:
+        h = self.ct.c_void_p()
+        rc = self.hip.hipEventCreateWithFlags(self.ct.byref(h), self.DISABLE_SYSTEM_FENCE)
+        if rc != 0:
+            raise RuntimeError(f"hipEventCreateWithFlags failed ({rc})")
+        return h.value
+
+    def record(self, ev: int, stream: int) -> None:
+        rc = self.hip.hipEventRecord(ev, stream)
+        if rc != 0:
+            raise RuntimeError(f"hipEventRecord failed ({rc})")
+
+    def elapsed_ms(self, begin: int, end: int) -> float:
+        ms = self.ct.c_float()
+        rc = self.hip.hipEventElapsedTime(self.ct.byref(ms), begin, end)
+        if rc != 0:
+            raise RuntimeError(f"hipEventElapsedTime failed ({rc})")
+        return ms.value
+
+    def destroy(self, ev: int) -> None:
+        self.hip.hipEventDestroy(ev)
+
+
 def build_inputs(shape, device, seed=0):
     """Synthetic config inputs, encoded on the GPU by the product encoder."""
     import torch
@@ -464,12 +507,9 @@ def main():
 
     # per-step HIP events around the fused kernel, recorded by the library on
     # the stream it launches on (torch's current stream)
-    evs = []
-    for _ in range(args.steps):
-        b, e = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        b.record()
-        e.record()  # materialise the underlying hipEvent_t
-        evs.append((b, e))
+    timer = HipTimer()
+    evs = [(timer.event(), timer.event()) for _ in range(args.steps)]
+    stream = torch.cuda.current_stream().cuda_stream
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
@@ -477,14 +517,17 @@ def main():
     for i in range(args.steps):
         if fast:
             # several launches: the events bracket the whole call
-            evs[i][0].record()
+            timer.record(evs[i][0], stream)
             step()
-            evs[i][1].record()
+            timer.record(evs[i][1], stream)
         else:
-            step((evs[i][0].cuda_event, evs[i][1].cuda_event))
+            step(evs[i])
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    kernel_ms = [b.elapsed_time(e) for b, e in evs]
+    kernel_ms = [timer.elapsed_ms(b, e) for b, e in evs]
+    for b, e in evs:
+        timer.destroy(b)
+        timer.destroy(e)
     kavg_ms = sum(kernel_ms) / len(kernel_ms)
 
     fl = shape.fast_flops(int(prot_rows.numel())) if fast else shape.flops()

@@ -37,6 +37,8 @@
 #include "nkv_common.h"
 #include "nkv_internal.h"
 
+#include <hip/hip_ext.h>
+
 #include <algorithm>
 #include <cmath>
 #include <cstring>
@@ -2080,17 +2082,30 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
         }
         set_segments(M, segs);
     }
-    if (d[0].ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d[0].ev_begin, s));
+    const bool events = d[0].ev_begin || d[0].ev_end;
     if (seg_blocks(M) > 0) {
         const size_t smem = sizeof(FlashSmem<CK_D>);
         const bool mask = M.part[0].cur_mask != nullptr;
         rc = mask ? set_smem(flash8_kernel<true>, smem) : set_smem(flash8_kernel<false>, smem);
         if (rc) return rc;
-        if (mask) flash8_kernel<true><<<dim3((unsigned)seg_blocks(M)), C8_THREADS, smem, s>>>(M);
-        else flash8_kernel<false><<<dim3((unsigned)seg_blocks(M)), C8_THREADS, smem, s>>>(M);
+        const dim3 grid((unsigned)seg_blocks(M));
+        if (events) {
+            // the dispatch itself stamps the kernel events (no marker packets
+            // between the launches, which would delay the next one)
+            const void* fn = mask ? (const void*)flash8_kernel<true> : (const void*)flash8_kernel<false>;
+            void* args[] = {&M};
+            NKV_HIP_CHECK(hipExtLaunchKernel(fn, grid, dim3(C8_THREADS), args, smem, s,
+                                             (hipEvent_t)d[0].ev_begin, (hipEvent_t)d[0].ev_end, 0));
+        } else if (mask) {
+            flash8_kernel<true><<<grid, C8_THREADS, smem, s>>>(M);
+        } else {
+            flash8_kernel<false><<<grid, C8_THREADS, smem, s>>>(M);
+        }
         NKV_LAUNCH_CHECK();
+    } else if (events) {
+        if (d[0].ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d[0].ev_begin, s));
+        if (d[0].ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d[0].ev_end, s));
     }
-    if (d[0].ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d[0].ev_end, s));
     const int64_t waves = (int64_t)d[0].B * d[0].H * M.part[0].qblocks;
     staged_combine_kernel<<<dim3((unsigned)cdiv(waves, CB_WAVES)), 64 * CB_WAVES, 0, s>>>(
         M, shift, sh_sb, sh_sh);

@@ -177,3 +177,27 @@ def test_staged_workspace_and_repeat(dev):
         torch.cuda.synchronize()
         assert torch.equal(a.view(torch.int16), b_.view(torch.int16))
         assert torch.equal(la, lb)
+
+
+def test_staged_kernel_events(dev):
+    """Kernel events stamped by the flash launch itself: the output is
+    bit-identical to a call without events, and the bracketed time is
+    positive and inside the call's own."""
+    sc = Scenario(H=2, N=900, Q=1100, Nc=100, rK=128, rV=128, G=32, C=8, seed=12)
+    key, value = sc.codecs(dev)
+    args = (sc.q.to(dev), sc.k_cur.to(dev), sc.v_cur.to(dev), key, value)
+    plain, lp = ops.attend(*args)
+    kb, ke = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    cb, ce = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    kb.record()  # torch creates the underlying events on their first record
+    ke.record()
+    torch.cuda.synchronize()
+    assert kb.cuda_event and ke.cuda_event
+    cb.record()
+    timed, lt = ops.attend(*args, kernel_events=(kb.cuda_event, ke.cuda_event))
+    ce.record()
+    torch.cuda.synchronize()
+    assert torch.equal(plain.view(torch.int16), timed.view(torch.int16))
+    assert torch.equal(lp, lt)
+    kms, cms = kb.elapsed_time(ke), cb.elapsed_time(ce)
+    assert 0.0 < kms <= cms, (kms, cms)
