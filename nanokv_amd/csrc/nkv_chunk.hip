@@ -1453,44 +1453,47 @@ __global__ void __launch_bounds__(C8_THREADS, 1) flash8_kernel(MultiParams P) {
     else flash_block<128, MASK>(P.part[pi], blk, smem_raw);
 }
 
-// Merge of chunk partials.  One wave owns one 32-query block and walks all
-// its chunks, each lane reading the lane-order payload the attention wave
-// stored (1 KB per load instruction, four chunks in flight); no cross-wave
-// reduction, so blocks need no LDS and fill the GPU in one round.
+// Merge of chunk partials.  Two waves own one 32-query block, one per half
+// of its 128 columns (lane-order rows 0-3 and 4-7 of the payload the
+// attention wave stored, 1 KB per load instruction, four chunks in flight),
+// and walk all its chunks; no cross-wave reduction, so blocks need no LDS.
+// Both read the block's (m, l).
 // out = sum_c 2^(m_c - M) O_c / sum_c 2^(m_c - M) l_c (O_c unnormalised); no
 // chunks give out = 0 and lse = -inf (CN/core.py:48-49).
-constexpr int CB_WAVES = 4;  // query blocks per 256-thread block
+constexpr int CB_WAVES = 4;  // waves per 256-thread block
+constexpr int CB_ROWS = 4;   // payload rows (of 8) per wave: half of the columns
 
 // The running merge of one wave: M the largest chunk max so far, L the
 // weighted row sum, acc the weighted O; Lx the part of L that the tracked
 // source contributed (rescaled with L).
 struct CombineAcc {
     float M, L, Lx;
-    float acc[64];
+    float acc[8 * CB_ROWS];
 };
 
-// Fold partials 0 .. NC of (bh, query block qblk) in, from a partial area
-// of qblocks query blocks per (bh, chunk).  A chunk whose max exceeds M
-// rescales the running sums (per lane), so no separate pass over the maxima
-// delays the first partial loads.
+// Fold payload rows half * CB_ROWS .. +CB_ROWS of partials 0 .. NC of (bh,
+// query block qblk) in, from a partial area of qblocks query blocks per
+// (bh, chunk).  A chunk whose max exceeds M rescales the running sums (per
+// lane), so no separate pass over the maxima delays the first partial loads.
 __device__ __forceinline__ void combine_partials(CombineAcc& A, const uint16_t* part_o,
                                                  const float* part_ml, int64_t bh, int NC,
-                                                 int qblocks, int qblk, int lane, bool track) {
+                                                 int qblocks, int qblk, int half, int lane,
+                                                 bool track) {
     const int64_t qi = (int64_t)qblk * 32 + (lane & 31);
     const int64_t lse_stride = (int64_t)qblocks * 32;
     const u32x2* ml = reinterpret_cast<const u32x2*>(part_ml) + bh * NC * lse_stride + qi;
-    const uint16_t* src = part_o + (bh * NC * qblocks + qblk) * 4096 + lane * 8;
+    const uint16_t* src = part_o + (bh * NC * qblocks + qblk) * 4096 + 512 * CB_ROWS * half + lane * 8;
     const int64_t cstride = (int64_t)qblocks * 4096;
     // a ring of CB_AHEAD chunks in flight (prefetches past the last chunk
     // reload it and are never used)
     constexpr int CB_AHEAD = 4;
-    u32x4 buf[CB_AHEAD][8];
+    u32x4 buf[CB_AHEAD][CB_ROWS];
     u32x2 mlb[CB_AHEAD];
     auto issue = [&](int cc, int i) {
         cc = max(min(cc, NC - 1), 0);
         mlb[i] = ml[cc * lse_stride];
 #pragma unroll
-        for (int st = 0; st < 8; ++st)
+        for (int st = 0; st < CB_ROWS; ++st)
             buf[i][st] = *reinterpret_cast<const u32x4*>(src + cc * cstride + 512 * st);
         // chunks are issued in ring order, so waiting for slot i leaves the
         // slots issued after it in flight
@@ -1516,7 +1519,7 @@ __device__ __forceinline__ void combine_partials(CombineAcc& A, const uint16_t* 
                 A.L *= f;
                 A.Lx *= f;
 #pragma unroll
-                for (int e = 0; e < 64; ++e) A.acc[e] *= f;
+                for (int e = 0; e < 8 * CB_ROWS; ++e) A.acc[e] *= f;
             }
             A.M = up ? mc : A.M;
             const float wt = !live || mc == -INFINITY ? 0.0f : exp2f(mc - A.M);
@@ -1524,7 +1527,7 @@ __device__ __forceinline__ void combine_partials(CombineAcc& A, const uint16_t* 
             A.L += wl;
             if (track) A.Lx += wl;
 #pragma unroll
-            for (int st = 0; st < 8; ++st)
+            for (int st = 0; st < CB_ROWS; ++st)
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
                     A.acc[8 * st + 2 * e] += wt * __uint_as_float(buf[i][st][e] << 16);
@@ -1535,22 +1538,23 @@ __device__ __forceinline__ void combine_partials(CombineAcc& A, const uint16_t* 
     }
 }
 
-// Normalise and store query qi of (b, h): out = (acc + shift * Lx) / L in
-// bf16 (shift: the row of 128 values added to the tracked source's output,
-// or null), lse = ln(sum) when lse is given.
+// Normalise and store this wave's half of query qi of (b, h): out = (acc +
+// shift * Lx) / L in bf16 (shift: the row of 128 values added to the
+// tracked source's output, or null); half 0 also writes lse = ln(sum) when
+// lse is given.
 __device__ __forceinline__ void combine_store(const CombineAcc& A, uint16_t* out, int64_t o_sb,
                                               int64_t o_st, int64_t o_sh, float* lse, int64_t Q,
-                                              int H, int b, int h, int64_t qi, int lane,
+                                              int H, int b, int h, int64_t qi, int half, int lane,
                                               const float* shift) {
     const int hf = lane >> 5;
     const float inv = A.L > 0.0f ? 1.0f / A.L : 0.0f;
     uint16_t* orow = out + b * o_sb + qi * o_st + h * o_sh + 4 * hf;
-    // acc[8*st + 2*e + {0,1}] = o[db = st/2][i = 8*(st&1) + 2*e + {0,1}] with
-    // d = 32*db + 8*(i/4) + 4*hf + i%4: acc[4n .. 4n+3] are four consecutive
-    // d of this lane's query
+    // acc[8*st + 2*e + {0,1}] (payload row st0 + st, st0 = CB_ROWS * half)
+    // = o[db = st/2][i = 8*(st&1) + 2*e + {0,1}] with d = 32*db + 8*(i/4) +
+    // 4*hf + i%4: acc[4n .. 4n+3] are four consecutive d of this lane's query
 #pragma unroll
-    for (int n = 0; n < 16; ++n) {
-        const int st = n >> 1;
+    for (int n = 0; n < 2 * CB_ROWS; ++n) {
+        const int st = CB_ROWS * half + (n >> 1);
         const int db = st >> 1, i = 8 * (st & 1) + 4 * (n & 1);
         const int d = 32 * db + 8 * (i >> 2);
         float v[4];
@@ -1563,7 +1567,7 @@ __device__ __forceinline__ void combine_store(const CombineAcc& A, uint16_t* out
         const u32x2 pk = {pack_bf16x2(v[0] * inv, v[1] * inv), pack_bf16x2(v[2] * inv, v[3] * inv)};
         *reinterpret_cast<u32x2*>(orow + d) = pk;
     }
-    if (lse && hf == 0)
+    if (lse && hf == 0 && half == 0)
         lse[((int64_t)b * H + h) * Q + qi] =
             A.L > 0.0f ? (A.M + log2f(A.L)) * 0.69314718055994531f : -INFINITY;
 }
@@ -1572,24 +1576,26 @@ __device__ __forceinline__ void combine_init(CombineAcc& A) {
     A.M = -INFINITY;
     A.L = A.Lx = 0.0f;
 #pragma unroll
-    for (int e = 0; e < 64; ++e) A.acc[e] = 0.0f;
+    for (int e = 0; e < 8 * CB_ROWS; ++e) A.acc[e] = 0.0f;
 }
 
 // The key-chunk schedule's merge: every (b, h, q) of one launch.
 __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParams p) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int64_t gq = (int64_t)blockIdx.x * CB_WAVES + wave;
+    const int64_t gw = (int64_t)blockIdx.x * CB_WAVES + wave;
+    const int64_t gq = gw >> 1;
+    const int half = (int)(gw & 1);
     if (gq >= (int64_t)p.B * p.H * p.qblocks) return;
     const int64_t bh = gq / p.qblocks;
     const int qblk = (int)(gq % p.qblocks);
     CombineAcc A;
     combine_init(A);
-    combine_partials(A, p.part_o, p.part_ml, bh, p.nch_total, p.qblocks, qblk, lane, false);
+    combine_partials(A, p.part_o, p.part_ml, bh, p.nch_total, p.qblocks, qblk, half, lane, false);
     const int64_t qi = (int64_t)qblk * 32 + (lane & 31);
     if (qi >= p.Q) return;
     combine_store(A, p.out, p.o_sb, p.o_st, p.o_sh, p.lse, p.Q, p.H, (int)(bh / p.H),
-                  (int)(bh % p.H), qi, lane, nullptr);
+                  (int)(bh % p.H), qi, half, lane, nullptr);
 }
 
 // The staged schedule's merge over every partition (CN/core.py:33-42 for
@@ -1604,7 +1610,9 @@ __global__ void __launch_bounds__(64 * CB_WAVES) staged_combine_kernel(MultiPara
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const ChunkParams& n = P.part[0];
-    const int64_t gq = (int64_t)blockIdx.x * CB_WAVES + wave;
+    const int64_t gw = (int64_t)blockIdx.x * CB_WAVES + wave;
+    const int64_t gq = gw >> 1;
+    const int half = (int)(gw & 1);
     if (gq >= (int64_t)n.B * n.H * n.qblocks) return;
     const int64_t bh = gq / n.qblocks;
     const int qblk = (int)(gq % n.qblocks);
@@ -1623,11 +1631,11 @@ __global__ void __launch_bounds__(64 * CB_WAVES) staged_combine_kernel(MultiPara
     for (int src = 0; src < (lp ? 2 : 1); ++src) {
         const ChunkParams& g = P.part[src ? lp : 0];
         combine_partials(A, g.part_o, g.part_ml, src ? (int64_t)b * g.H + li : bh, g.nch_total,
-                         g.qblocks, qblk, lane, src == 1);
+                         g.qblocks, qblk, half, lane, src == 1);
     }
     const int64_t qi = (int64_t)qblk * 32 + (lane & 31);
     if (qi >= n.Q) return;
-    combine_store(A, n.out, n.o_sb, n.o_st, n.o_sh, n.lse, n.Q, n.H, b, h, qi, lane,
+    combine_store(A, n.out, n.o_sb, n.o_st, n.o_sh, n.lse, n.Q, n.H, b, h, qi, half, lane,
                   lp && shift ? shift + (int64_t)b * sh_sb + (int64_t)h * sh_sh : nullptr);
 }
 
@@ -2106,7 +2114,7 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
         if (d[0].ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d[0].ev_begin, s));
         if (d[0].ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d[0].ev_end, s));
     }
-    const int64_t waves = (int64_t)d[0].B * d[0].H * M.part[0].qblocks;
+    const int64_t waves = 2 * (int64_t)d[0].B * d[0].H * M.part[0].qblocks;
     staged_combine_kernel<<<dim3((unsigned)cdiv(waves, CB_WAVES)), 64 * CB_WAVES, 0, s>>>(
         M, shift, sh_sb, sh_sh);
     NKV_LAUNCH_CHECK();
@@ -2270,7 +2278,7 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     if (d.ev_end) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_end, s));
     const int64_t qblocks_total = (int64_t)d.B * d.H * p.qblocks;
     if (qblocks_total > 0) {
-        chunk_combine_kernel<<<dim3((unsigned)cdiv(qblocks_total, CB_WAVES)), 64 * CB_WAVES, 0,
+        chunk_combine_kernel<<<dim3((unsigned)cdiv(2 * qblocks_total, CB_WAVES)), 64 * CB_WAVES, 0,
                                s>>>(p);
         NKV_LAUNCH_CHECK();
     }
