@@ -84,7 +84,9 @@ enum nkv_scale_dtype { NKV_DTYPE_BF16 = 0, NKV_DTYPE_FP16 = 1 };
  *  KEY_CHUNKS   a block owns one 256-key chunk (decoded once, kept in LDS)
  *               and attends every query to it; each chunk leaves a bf16
  *               partial output + LSE per query that a combine kernel merges.
- *  AUTO         KEY_CHUNKS when the queries span more than one query tile. */
+ *  AUTO         KEY_CHUNKS whenever the codecs fit it (D = 128, ranks that
+ *               are multiples of 64, scale groups that are multiples of 32),
+ *               QUERY_TILES otherwise. */
 enum nkv_schedule {
     NKV_SCHEDULE_AUTO = 0,
     NKV_SCHEDULE_QUERY_TILES = 1,

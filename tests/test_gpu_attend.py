@@ -84,7 +84,7 @@ def test_attend_batch(dev, schedule):
 
 def test_attend_schedules_agree(dev):
     # the two decompositions compute the same attention; key chunks is AUTO's
-    # choice above one query tile (256 queries)
+    # choice whenever the codecs fit it
     sc = Scenario(H=2, N=900, Q=400, Nc=120, rK=384, rV=384, G=32, C=16)
     key, value = sc.codecs(dev)
     q, kc, vc = sc.q.to(dev), sc.k_cur.to(dev), sc.v_cur.to(dev)

@@ -30,7 +30,7 @@ def _both(sc, dev, **kw):
 
 
 def test_static_scratch_matches_nkv_attend_twice(dev):
-    # 1: key-chunk schedule (Q > 256), partials in the static scratch
+    # 1: key-chunk schedule (staged at 10 query blocks), tiles and partials in the static scratch
     big = Scenario(H=2, N=600, Q=300, Nc=64, rK=384, rV=256, G=32, C=16, seed=1)
     need = ops.attend_workspace_size(big.q, big.N, big.Nc, *big.codecs(dev))
     assert 0 < need <= _lib.NKV_STATIC_SCRATCH_BYTES
@@ -51,7 +51,7 @@ def test_static_scratch_matches_nkv_attend_twice(dev):
 
 
 def test_static_scratch_refuses_oversize_calls(dev):
-    """A config-1-sized key-chunk call (556 MB of partials) is refused with
+    """A config-1-sized key-chunk call (206 MB of tiles and partials) is refused with
     NKV_ERR_WORKSPACE before anything is launched (the pointers are never
     read: the size check comes first)."""
     args = _lib.NkvAttendArgs()
