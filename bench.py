@@ -538,11 +538,11 @@ def main():
     if schedule == "auto":
         schedule = "key_chunks"
     kernel = "nkv::chunk_kernel" if schedule == "key_chunks" else "nkv::attend_kernel"
-    # the key-chunk path stages from 8 query blocks up: the history is decoded
+    # the key-chunk path stages the history: it is decoded
     # once into tiles (drtile_kernel), then the flash kernel -- the one the
     # events bracket -- does the attention flops
     kflops = fl["total"]
-    if schedule == "key_chunks" and -(-shape.Q // 32) >= 8 and not fast:
+    if schedule == "key_chunks" and not fast:
         schedule, kernel = "staged", "nkv::flash8_kernel"
         kflops = fl["attention_history"] + fl["attention_current"]
     if fast:

@@ -1754,14 +1754,14 @@ int set_smem(K* kernel, size_t smem) {
 
 // ---------------------------------------------------------- staged (host)
 constexpr int FT_CUS = 256;          // compute units of an MI355X
-// The staged schedule from 8 query blocks up: below, the key-chunk schedule's
-// per-chunk partials (query blocks x 8.25 KB per 256 keys) cost less than
-// writing and reading the decoded tiles (128 KB per 256 keys).  Measured on
-// MI355X against the key-chunk kernel (cfg1's codec, Q = Nc): 12 blocks over
-// 49,920 history keys 0.747 vs 0.837 ms, over 12,480 keys 0.224 vs 0.254 ms;
-// 16 blocks 0.764 vs 0.918 and 0.245 vs 0.286 ms; cfg2 (25 blocks) 0.950 vs
-// 1.067 ms.
-constexpr int FT_MIN_QBLOCKS = 8;
+// The staged schedule from one query block up.  Measured on MI355X against
+// the key-chunk kernel (cfg1's codec, 24 heads, Q = Nc), the staged call was
+// faster at every size tried: 1 block over 49,920 history keys 0.543 vs
+// 0.571 ms, over 12,480 keys 0.161 vs 0.177 ms; 6 blocks 0.590 vs 0.660 and
+// 0.174 vs 0.202 ms; 12 blocks 0.747 vs 0.837 and 0.224 vs 0.254 ms; cfg2 (25
+// blocks) 0.950 vs 1.067 ms.  The key-chunk kernel remains for reader widths
+// 32/64 with read-time RoPE or camera.
+constexpr int FT_MIN_QBLOCKS = 1;
 
 struct FlashPlan {
     int qpt, qtiles, splits, ntiles_hist, ntiles;

@@ -19,7 +19,7 @@
 //     decoding k_low / v_low in-kernel -> out_l, lse_l;
 //  3. merge(out, lse_n, out_l, lse_l) per group head (CN/core.py:33-42), the
 //     lift being the identity (vd == D).
-// Without read-time RoPE or camera, from 8 query blocks up and with at most
+// Without read-time RoPE or camera and with at most
 // NKV_MAX_PARTS - 1 groups, all partitions run as one staged launch
 // (staged_multi_launch): one decode launch for every partition's tiles, one
 // flash launch over all of them, and one combine that folds each head's

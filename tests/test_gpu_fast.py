@@ -55,7 +55,7 @@ def test_fast_reader_widths(dev, d):
 
 @pytest.mark.parametrize("d", [32, 64])
 def test_fast_reader_widths_staged(dev, d):
-    """From 8 query blocks up the reader groups run the staged schedule at
+    """Without read-time RoPE or camera the reader groups run the staged schedule at
     their width (K image [128][d], flash at K/Q width d): a ragged history,
     means and centers, fp16 group scales."""
     sc = Scenario(H=4, N=900, Q=1040, Nc=70, rK=384, rV=256, G=32, C=16, with_mean=True,

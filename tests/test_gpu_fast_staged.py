@@ -1,5 +1,5 @@
-"""GPU parity of NanoKV-Fast's one-launch staged path: from 8 query blocks
-up, with no read-time RoPE or camera and at most three reader groups,
+"""GPU parity of NanoKV-Fast's one-launch staged path: with no read-time
+RoPE or camera and at most three reader groups,
 nkv_fast_attend decodes every partition's tiles in one launch, attends all of
 them in one flash launch and merges each head's native and low partitions in
 one combine (the value-mean shift folded in), with identity readers reading

@@ -1,6 +1,6 @@
 """GPU parity of nkv_attend's staged schedule (decode the history into tile
 images once, then flash attention over them with key splits and the LSE
-combine), which the library takes from 8 query blocks (256 queries) up:
+combine), which the key-chunk decomposition runs at D = 128:
 every decode variant (the decode GEMM's register epilogue: bias, centers of
 1/2/4-byte ids, no centers, scale groups, bf16 scales, segment tables; the
 in-LDS decode for read-time RoPE and camera), history row lists, current-key
