@@ -492,9 +492,8 @@ typedef struct nkv_reader_group {
  * token count; splits and schedule are ignored).  Every head should belong
  * to exactly one group (CN/core.py:213-215); a head in no group keeps the
  * native partition alone (a head listed by several groups is merged with the
- * first of them only when the call runs as one staged launch: no read-time
- * RoPE or camera, at most 3 groups).  Returns
- * NKV_ERR_UNSUPPORTED for D != 128.
+ * first of them only when the call runs as one staged launch: no camera, at
+ * most 3 groups).  Returns NKV_ERR_UNSUPPORTED for D != 128.
  * RoPE (attend.rope != NULL, CN/mg35.py:207-214, 305-336): the native
  * partition's history keys are rotated at their codec rows and attend.q is
  * taken as already rotated; each reader group forms its queries from the

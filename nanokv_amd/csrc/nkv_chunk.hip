@@ -1156,9 +1156,30 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
             };
             if (CODEC == 0) {
                 // acc[dt] element i: d = 32 dt + 8 (i/4) + 4 hf + i%4 of this
-                // lane's key; K = bf16(bf16(acc + bias) + center)
+                // lane's key; K = bf16(bf16(acc + bias) + center), then with
+                // read-time RoPE each bf16 pair (d, d + 1) rotated by its
+                // pair's (cos, sin) at the key's codec row (rope_pair: fp64,
+                // as rope_apply); a narrower reader's pair j is the original
+                // pair p.rope.pairs[h][j]
+                const bool rope = rope_on(p.rope);
+                RopeRows rr{};
+                const int32_t* pmap = nullptr;
+                if (rope) {
+                    rr = rope_rows(p.rope, key_row(tile, key));
+                    if (p.rope.pairs) pmap = p.rope.pairs + (int64_t)h * (DK / 2);
+                }
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) {
+                    // the slice's 8 pairs of this lane: 16 dt + 4 g + 2 hf + {0, 1}
+                    double2 cs[8];
+                    if (rope) {
+#pragma unroll
+                        for (int x = 0; x < 8; ++x) {
+                            const int pj = 16 * dt + 4 * (x >> 1) + 2 * hf + (x & 1);
+                            cs[x] = *reinterpret_cast<const double2*>(
+                                rope_entry(p.rope, rr, pmap ? ldg(pmap + pj) : pj));
+                        }
+                    }
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int d = 32 * dt + 8 * g + 4 * hf;
@@ -1173,8 +1194,12 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                             a[2] += __uint_as_float(c1 << 16);
                             a[3] += __uint_as_float(c1 & 0xffff0000u);
                         }
-                        *reinterpret_cast<u32x2*>(st + l32 * DR_SROW + 8 * g + 4 * hf) =
-                            u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
+                        uint32_t w0 = pack_bf16x2(a[0], a[1]), w1 = pack_bf16x2(a[2], a[3]);
+                        if (rope) {
+                            w0 = rope_pair(w0, cs[2 * g].x, cs[2 * g].y);
+                            w1 = rope_pair(w1, cs[2 * g + 1].x, cs[2 * g + 1].y);
+                        }
+                        *reinterpret_cast<u32x2*>(st + l32 * DR_SROW + 8 * g + 4 * hf) = u32x2{w0, w1};
                     }
                     flush(dt);
                 }
@@ -1779,19 +1804,19 @@ FlashPlan flash_shape(const ChunkLaunchDesc& d) {
     return f;
 }
 
-// Reader widths below 128 are staged only by the decode GEMM (no read-time
-// RoPE or camera: stage8_kernel decodes at full width).
+// Reader widths below 128 are staged only by the decode GEMM (no camera:
+// stage8_kernel decodes at full width).
 bool use_staged(const ChunkLaunchDesc& d) {
-    const bool width = d.dk == CK_D || ((d.dk == 32 || d.dk == 64) && !rope_on(d.rope) && !d.cam.mats &&
+    const bool width = d.dk == CK_D || ((d.dk == 32 || d.dk == 64) && !d.cam.mats &&
                                         d.key.r <= 64 * DR_MAXQ && d.value.r <= 64 * DR_MAXQ);
     return width && cdiv(d.Q, 32) >= FT_MIN_QBLOCKS && d.n_rows + d.Nc > 0;
 }
 
-// History tiles from the decode GEMM with the decoder held in LDS (and the
-// current tiles copied in the same launch); with read-time RoPE or camera,
-// or ranks above what LDS holds, both from stage8_kernel's decode.
+// History tiles from the decode GEMM with the decoder held in LDS (read-time
+// RoPE in its epilogue, the current tiles copied in the same launch); with
+// the camera, or ranks above what LDS holds, both from stage8_kernel's decode.
 bool staged_gemm(const ChunkLaunchDesc& d) {
-    return !rope_on(d.rope) && !d.cam.mats && d.key.r <= 64 * DR_MAXQ && d.value.r <= 64 * DR_MAXQ;
+    return !d.cam.mats && d.key.r <= 64 * DR_MAXQ && d.value.r <= 64 * DR_MAXQ;
 }
 
 // Cost model of the staged kernels for planning their grids, in units of one

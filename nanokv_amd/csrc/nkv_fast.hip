@@ -19,15 +19,15 @@
 //     decoding k_low / v_low in-kernel -> out_l, lse_l;
 //  3. merge(out, lse_n, out_l, lse_l) per group head (CN/core.py:33-42), the
 //     lift being the identity (vd == D).
-// Without read-time RoPE or camera and with at most
-// NKV_MAX_PARTS - 1 groups, all partitions run as one staged launch
-// (staged_multi_launch): one decode launch for every partition's tiles, one
-// flash launch over all of them, and one combine that folds each head's
-// native and group partials together (the merge of step 3, with the
-// low_shift), so no group output or LSE is written.  Identity readers then
-// read the layer's own queries, center tables and means through head maps
-// instead of projected copies.  Otherwise the partitions run one after
-// another and group_merge_kernel merges each group's output in place.
+// Without a camera and with at most NKV_MAX_PARTS - 1 groups, all partitions
+// run as one staged launch (staged_multi_launch): one decode launch for
+// every partition's tiles (RoPE in its epilogue), one flash launch over all
+// of them, and one combine that folds each head's native and group partials
+// together (the merge of step 3, with the low_shift), so no group output or
+// LSE is written.  Identity readers then read the layer's own center tables
+// and means (and, without RoPE, queries) through head maps instead of
+// projected copies.  Otherwise the partitions run one after another and
+// group_merge_kernel merges each group's output in place.
 // The projected tables are small (C x d per head); they are recomputed per
 // call, as the reference's read does.  With a segmented codec the tables of
 // every segment are projected into one table (segment s at rows center_base
@@ -446,14 +446,17 @@ struct ReaderIdent {
     bool q, k, v;
 };
 
-ReaderIdent reader_ident(const nkv_reader_group& G, bool multi) {
-    return multi ? ReaderIdent{!G.q_reduce, !G.k_affine, !G.v_affine} : ReaderIdent{false, false, false};
+// With read-time RoPE the reader queries are always formed from q_pre and
+// rotated at the query positions, as the per-group path does.
+ReaderIdent reader_ident(const nkv_fast_args* f, const nkv_reader_group& G, bool multi) {
+    return multi ? ReaderIdent{!G.q_reduce && !f->attend.rope, !G.k_affine, !G.v_affine}
+                 : ReaderIdent{false, false, false};
 }
 
 // Low-partition launch of group g over the workspace tables.
 ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const FastLayout& L,
                          bool multi = false) {
-    const ReaderIdent id = reader_ident(f->groups[g], multi);
+    const ReaderIdent id = reader_ident(f, f->groups[g], multi);
     const nkv_attend_args& a = f->attend;
     const nkv_reader_group& G = f->groups[g];
     const int nh = G.num_heads, dd = G.d, D = a.D;
@@ -543,13 +546,20 @@ ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const
 }
 
 // The partitions of the staged multi-partition launch: the native one, then
-// every reader group (heads[1 + g] = its heads).
+// every reader group (heads[1 + g] = its heads).  With read-time RoPE every
+// partition rotates its history keys at their codec rows, a reader group on
+// its pair map.
 int multi_descs(const nkv_fast_args* f, unsigned char* ws, const FastLayout& L,
                 ChunkLaunchDesc* d, const int32_t** heads) {
+    RopeDev krope{};
+    if (f->attend.rope) rope_from_abi(f->attend.rope, f->attend.D, &krope);
     d[0] = native_desc(f, f->attend.lse);
+    d[0].rope = krope;
     heads[0] = nullptr;
     for (int g = 0; g < f->num_groups; ++g) {
         d[1 + g] = low_desc(f, g, ws, L, true);
+        d[1 + g].rope = krope;
+        d[1 + g].rope.pairs = f->groups[g].rope_pairs;
         heads[1 + g] = f->groups[g].heads;
     }
     return 1 + f->num_groups;
@@ -557,12 +567,11 @@ int multi_descs(const nkv_fast_args* f, unsigned char* ws, const FastLayout& L,
 
 // One decode, one flash and one combine launch serve the whole call (every
 // partition merged in the combine, no per-group merge) when there is no
-// read-time RoPE or camera and the native partition and the reader groups
-// fit one staged launch.
+// camera and the native partition and the reader groups fit one staged
+// launch.
 bool use_multi(const nkv_fast_args* f) {
     const nkv_attend_args& a = f->attend;
-    if (a.rope || a.camera || f->n_low == 0 || f->num_groups < 1 ||
-        f->num_groups + 1 > NKV_MAX_PARTS)
+    if (a.camera || f->n_low == 0 || f->num_groups < 1 || f->num_groups + 1 > NKV_MAX_PARTS)
         return false;
     FastLayout L{};
     for (auto* v : {&L.q_low, &L.kc, &L.vc, &L.kb, &L.vb, &L.out_l, &L.lse_l})
@@ -586,7 +595,7 @@ FastLayout layout(const nkv_fast_args* f) {
     L.lse_n = take(a.lse || L.multi ? 0 : (size_t)a.B * a.H * a.Q * sizeof(float));
     for (int g = 0; g < f->num_groups; ++g) {
         const nkv_reader_group& G = f->groups[g];
-        const ReaderIdent id = reader_ident(G, L.multi);
+        const ReaderIdent id = reader_ident(f, G, L.multi);
         const size_t nh = G.num_heads, dd = G.d, D = a.D;
         L.q_low.push_back(take(id.q ? 0 : (size_t)a.B * a.Q * nh * dd * 2));
         const size_t kt = has_centers(a.key) && !id.k ? (size_t)table_batches(a.key, a.B) : 0;
@@ -646,7 +655,7 @@ int reader_tables(hipStream_t s, const nkv_fast_args* f, int g, unsigned char* w
                   const FastLayout& L, const RopeDev& qrope, const CameraDev& qcam) {
     const nkv_attend_args& a = f->attend;
     const nkv_reader_group& G = f->groups[g];
-    const ReaderIdent id = reader_ident(G, L.multi);
+    const ReaderIdent id = reader_ident(f, G, L.multi);
     const int D = a.D, HD = a.H * a.D;
     const int nh = G.num_heads, dd = G.d;
     int rc = NKV_OK;
