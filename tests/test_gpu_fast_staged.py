@@ -147,3 +147,31 @@ def test_fast_staged_segments(dev, monkeypatch):
     diff, cos = max_abs_cos(out[0].permute(1, 0, 2).float().cpu().numpy(), ref)
     assert diff <= MAX_ABS and cos >= MIN_COS, (diff, cos)
     assert np.abs(lse[0].cpu().numpy() - ref_lse).max() < 2e-3
+
+
+def _multi_payload(sc, spec, seed=0):
+    """A reader payload with one group per (heads, d) of spec (d None: an
+    identity group), each cut from synth.make_readers over those heads."""
+    groups = []
+    for i, (heads, d) in enumerate(spec):
+        others = tuple(h for h in range(sc.H) if h not in heads)
+        if d is None:
+            pl = synth.make_readers(sc.shape, sc.layer, seed=seed + i, full_heads=tuple(heads), d=32)
+            groups.append(pl["groups"][0])
+        else:
+            pl = synth.make_readers(sc.shape, sc.layer, seed=seed + i, full_heads=others, d=d)
+            groups.append(pl["groups"][1])
+    return {"groups": groups, "heads": sc.H, "native_dim": sc.D, "rank": sc.shape.rK}
+
+
+@pytest.mark.parametrize("spec", [
+    # three groups: the native partition and three readers fill one launch
+    [([0], None), ([1, 2], 32), ([3], 64)],
+    # four groups: more partitions than one launch holds, run group by group
+    [([0], None), ([1, 2], 32), ([3], 64), ([4], 32)],
+])
+def test_fast_staged_group_counts(dev, spec):
+    H = max(max(hs) for hs, _ in spec) + 1
+    sc = Scenario(H=H, N=800, Q=300, Nc=40, rK=256, rV=256, G=32, C=16, with_mean=True,
+                  seed=20 + len(spec))
+    _run(sc, dev, _multi_payload(sc, spec, seed=len(spec)), np.arange(600, 800))
