@@ -1315,21 +1315,37 @@ __device__ __forceinline__ void flash_block(const ChunkParams& p, int64_t blk, u
     // tile i of the split goes to buffer i % 2; piece e (1 KB) of a tile:
     // lane L brings chunk (L % CPR) ^ kswz(row) of K row 512 e / DK + L / CPR,
     // or chunk (L % 16) ^ (row % 16) of V^T row 4 e' + L / 16 (e' = e minus
-    // the K pieces)
-    const uint16_t* src = p.tiles + (int64_t)bh * p.ntiles * TF::TILE;
+    // the K pieces).  This wave's pieces are e = wave + 8 i: K_PIECES is a
+    // multiple of 8 and both swizzles repeat every 16 rows (4 per piece), so
+    // in each of them the lane reads at the piece's first byte (1024 e, the
+    // V^T image starting at piece K_PIECES) plus one per-lane offset, koff in
+    // the K pieces and voff in the V^T pieces.
+    static_assert(TF::K_PIECES % C8_WAVES == 0 && TF::PIECES % C8_WAVES == 0, "piece split");
+    const uint32_t koff = [&] {
+        const int row = wave * (512 / DK) + lane / TF::CPR;
+        return (uint32_t)(2 * ((lane / TF::CPR) * DK + 8 * ((lane % TF::CPR) ^ TF::kswz(row))));
+    }();
+    const uint32_t voff = [&] {
+        const int row = 4 * wave + (lane >> 4);
+        return (uint32_t)(2 * ((lane >> 4) * FT_ROW + 8 * ((lane & 15) ^ (row & 15))));
+    }();
+    const unsigned char* src = reinterpret_cast<const unsigned char*>(
+        p.tiles + (int64_t)bh * p.ntiles * TF::TILE);
     auto issue = [&](int tile) {
-        const uint16_t* s = src + (int64_t)tile * TF::TILE;
+        const unsigned char* s = src + (int64_t)tile * TF::TILE * 2;
         const int bi = (tile - t0) & 1;
-        for (int e = wave; e < TF::PIECES; e += C8_WAVES) {
-            if (e < TF::K_PIECES) {
-                const int row = e * (512 / DK) + lane / TF::CPR;
-                const int ch = (lane % TF::CPR) ^ TF::kswz(row);
-                dma16(s + row * DK + 8 * ch, sm.k[bi] + 512 * e);
-            } else {
-                const int ev = e - TF::K_PIECES, row = 4 * ev + (lane >> 4);
-                const int ch = (lane & 15) ^ (row & 15);
-                dma16(s + TF::K_IMG + row * FT_ROW + 8 * ch, sm.v[bi] + 512 * ev);
-            }
+        // opaque here, so that the per-piece sums are not hoisted out of
+        // the tile loop into 64-bit registers: each load is a uniform base
+        // plus the lane's 32-bit offset
+        uint32_t ko = koff, vo = voff;
+        asm volatile("" : "+v"(ko), "+v"(vo));
+#pragma unroll
+        for (int i = 0; i < TF::PIECES / C8_WAVES; ++i) {
+            const int e = wave + C8_WAVES * i;
+            if (i < TF::K_PIECES / C8_WAVES)
+                dma16(s + 1024 * e + ko, sm.k[bi] + 512 * e);
+            else
+                dma16(s + 1024 * e + vo, sm.v[bi] + 512 * (e - TF::K_PIECES));
         }
     };
     const int hf = lane >> 5, l32 = lane & 31;
@@ -1367,37 +1383,91 @@ __device__ __forceinline__ void flash_block(const ChunkParams& p, int64_t blk, u
 #pragma unroll
     for (int db = 0; db < 4; ++db) o[db] = f32x16{};
     float m = -INFINITY, l = 0.0f;
-    // one tile in buffer BI (the tile loop runs two at a time, so that the
-    // buffer's offsets are immediates)
-    auto run_tile = [&](int tile, auto bi_tag) {
-        constexpr int BI = decltype(bi_tag)::value;
+    // The softmax of one 32-key step's scores s and its P.V products with the
+    // V^T fragments in vf (registers only).
+    auto softmax_pv = [&](const f32x16& s) {
+        float tm = fmaxf(s[0], s[1]);
+#pragma unroll
+        for (int i = 2; i < 16; ++i) tm = fmaxf(tm, s[i]);
+        tm = halfwave_max(tm) * c;
+        const bool up = tm > m + CK_TAU;
+        const float mn = up ? tm : m;
+        // m = -inf (nothing seen yet) gives alpha 0 on zero sums
+        const float alpha = up ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
+        m = mn;
+        const float mref = MASK && mn == -INFINITY ? 0.0f : mn;
+        uint32_t pw[8];
+        float lsum = 0.0f;
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            pw[k] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(s[2 * k], c, -mref)),
+                                __builtin_amdgcn_exp2f(fmaf(s[2 * k + 1], c, -mref)));
+            lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[k]),
+                                                   __builtin_bit_cast(bf16x2, 0x3F803F80u),
+                                                   lsum, false);
+        }
+        l = l * alpha + lsum;
+        const bf16x8 p0 = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
+        const bf16x8 p1 = as_bf16x8(u32x4{pw[4], pw[5], pw[6], pw[7]});
+        __builtin_amdgcn_s_setprio(1);
+        if (__any(up)) {
+#pragma unroll
+            for (int db = 0; db < 4; ++db)
+#pragma unroll
+                for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
+        }
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[db], p0, o[db]);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[4 + db], p1, o[db]);
+        __builtin_amdgcn_s_setprio(0);
+    };
+    // Waves 4-7 run half a step behind waves 0-3 (wave w and w + 4 share a
+    // SIMD): each carries its tile's last step (masked scores in s, V^T
+    // fragments in vf) across the barrier and finishes it first in the next
+    // tile.  On each SIMD one wave's softmax then overlaps the other's MFMA
+    // products, instead of both waves reaching the same phase together after
+    // every barrier.  Every wave still walks its steps in key order.
+    const bool lag = wave >= C8_WAVES / 2;
+    bool pend = false;
+    f32x16 s;
+    // The tiles in turn: kofs / vofs address the current tile's buffer and
+    // move to the other one after each tile (uniform +-image size).
+    for (int tile = t0; tile < t1; ++tile) {
         wait_loads_and_lds();
         __builtin_amdgcn_s_barrier();
-        // the other buffer's last readers have passed the barrier
+        // the other buffer's last readers have passed the barrier (a carried
+        // step holds its operands in registers)
         if (tile + 1 < t1) issue(tile + 1);
         const bool cur = tile >= p.ntiles_hist;
         const int64_t key0 = (int64_t)(cur ? tile - p.ntiles_hist : tile) * FT_T;
         const int valid = (int)min((int64_t)FT_T, (cur ? p.Nc : p.n_rows) - key0);
-        if (!active || valid <= 0) return;
+        const int nsub = active && valid > 0 ? (valid + 31) >> 5 : 0;
         auto lds_k = [&](int j, int kk) {
-            return lds_b128(reinterpret_cast<const uint16_t*>(
-                smem_raw + kofs[kk] + BI * K_BYTES + j * 32 * DK * 2));
+            return lds_b128(reinterpret_cast<const uint16_t*>(smem_raw + kofs[kk] + j * 32 * DK * 2));
         };
         auto lds_v = [&](int j, int t) {
             return lds_b128(reinterpret_cast<const uint16_t*>(
-                smem_raw + vofs[2 * j + (t >> 2)] + BI * FT_IMG_BYTES + (t & 3) * 32 * FT_ROW * 2));
+                smem_raw + vofs[2 * j + (t >> 2)] + (t & 3) * 32 * FT_ROW * 2));
         };
-        const uint32_t* mrow = MASK && cur ? mbase + (key0 >> 5) : nullptr;
+        // (an idle wave's reads of the first step stay inside the buffer)
 #pragma unroll
         for (int kk = 0; kk < KS; ++kk) kf[kk] = lds_k(0, kk);
+        if (pend) {
+            softmax_pv(s);
+            // the new tile's V^T reads wait for the carried products, so
+            // that both fragment sets are never live at once
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        pend = false;
+        const uint32_t* mrow = MASK && cur ? mbase + (key0 >> 5) : nullptr;
 #pragma unroll
         for (int t = 0; t < 8; ++t) vf[t] = lds_v(0, t);
-        const int nsub = (valid + 31) >> 5;
 #pragma unroll
         for (int j = 0; j < FT_T / 32; ++j) {
             if (j >= nsub) break;
             __builtin_amdgcn_s_setprio(1);
-            f32x16 s = mfma32(kf[0], qf[0], f32x16{});
+            s = mfma32(kf[0], qf[0], f32x16{});
 #pragma unroll
             for (int kk = 1; kk < KS; ++kk) s = mfma32(kf[kk], qf[kk], s);
             __builtin_amdgcn_s_setprio(0);
@@ -1417,51 +1487,30 @@ __device__ __forceinline__ void flash_block(const ChunkParams& p, int64_t blk, u
                 for (int i = 0; i < 16; ++i)
                     if (!((bits >> (8 * (i >> 2) + 4 * hf + (i & 3))) & 1u)) s[i] = -INFINITY;
             }
-            float tm = fmaxf(s[0], s[1]);
-#pragma unroll
-            for (int i = 2; i < 16; ++i) tm = fmaxf(tm, s[i]);
-            tm = halfwave_max(tm) * c;
-            const bool up = tm > m + CK_TAU;
-            const float mn = up ? tm : m;
-            // m = -inf (nothing seen yet) gives alpha 0 on zero sums
-            const float alpha = up ? __builtin_amdgcn_exp2f(m - mn) : 1.0f;
-            m = mn;
-            const float mref = MASK && mn == -INFINITY ? 0.0f : mn;
-            uint32_t pw[8];
-            float lsum = 0.0f;
-#pragma unroll
-            for (int k = 0; k < 8; ++k) {
-                pw[k] = pack_bf16x2(__builtin_amdgcn_exp2f(fmaf(s[2 * k], c, -mref)),
-                                    __builtin_amdgcn_exp2f(fmaf(s[2 * k + 1], c, -mref)));
-                lsum = __builtin_amdgcn_fdot2_f32_bf16(__builtin_bit_cast(bf16x2, pw[k]),
-                                                       __builtin_bit_cast(bf16x2, 0x3F803F80u),
-                                                       lsum, false);
+            if (lag && j + 1 == nsub) {
+                pend = true;
+                break;
             }
-            l = l * alpha + lsum;
-            const bf16x8 p0 = as_bf16x8(u32x4{pw[0], pw[1], pw[2], pw[3]});
-            const bf16x8 p1 = as_bf16x8(u32x4{pw[4], pw[5], pw[6], pw[7]});
-            __builtin_amdgcn_s_setprio(1);
-            if (__any(up)) {
-#pragma unroll
-                for (int db = 0; db < 4; ++db)
-#pragma unroll
-                    for (int i = 0; i < 16; ++i) o[db][i] *= alpha;
-            }
-#pragma unroll
-            for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[db], p0, o[db]);
-#pragma unroll
-            for (int db = 0; db < 4; ++db) o[db] = mfma32(vf[4 + db], p1, o[db]);
-            __builtin_amdgcn_s_setprio(0);
+            softmax_pv(s);
             if (j + 1 < nsub) {
 #pragma unroll
                 for (int t = 0; t < 8; ++t) vf[t] = lds_v(j + 1, t);
             }
         }
-    };
-    for (int tile = t0; tile < t1; tile += 2) {
-        run_tile(tile, std::integral_constant<int, 0>{});
-        if (tile + 1 < t1) run_tile(tile + 1, std::integral_constant<int, 1>{});
+        const int kstep = ((tile - t0) & 1) ? -K_BYTES : K_BYTES;
+        const int vstep = ((tile - t0) & 1) ? -FT_IMG_BYTES : FT_IMG_BYTES;
+#pragma unroll
+        for (int kk = 0; kk < KS; ++kk) {
+            kofs[kk] += kstep;
+            asm volatile("" : "+v"(kofs[kk]));
+        }
+#pragma unroll
+        for (int i = 0; i < 8; ++i) {
+            vofs[i] += vstep;
+            asm volatile("" : "+v"(vofs[i]));
+        }
     }
+    if (pend) softmax_pv(s);
     if (active) store_partial(p, bh, split, q0, o, m, halfwave_sum(l), lane);
 }
 
