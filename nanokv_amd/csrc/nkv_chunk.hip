@@ -1062,8 +1062,15 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
     // columns 32 dt + 8 g + 4 hf .. +4 of this lane's key; V, column
     // d = 32 dt + l32 of keys 32 kq + 8 g + 4 hf + e
     constexpr int NCV = CODEC == 0 ? 8 * NDT : 64;
+    // K with read-time RoPE: the lane's own key at columns 32 dt + 8 g + 4 hf
+    // .. +4 (added before the rotation, in the accumulator layout).  K
+    // otherwise: row (lane >> 2) + 16 i of the wave's 32 keys at columns
+    // 32 dt + 8 (lane & 3) .. +8 (added when the staged rows are flushed), so
+    // that each load reads 16 rows x 64 contiguous bytes rather than 32 rows
+    // x 16 bytes.
+    const bool rope = CODEC == 0 && rope_on(p.rope);
     auto load_centers = [&](uint32_t (&cv)[NCV], const uint16_t* const* crow) {
-        if (CODEC == 0) {
+        if (CODEC == 0 && rope) {
             const uint16_t* cr = crow[key];
 #pragma unroll
             for (int dt = 0; dt < NDT; ++dt)
@@ -1073,6 +1080,17 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                     cv[2 * (4 * dt + g)] = v[0];
                     cv[2 * (4 * dt + g) + 1] = v[1];
                 }
+        } else if (CODEC == 0) {
+#pragma unroll
+            for (int i = 0; i < 2; ++i) {
+                const uint16_t* cr = crow[32 * kq + (lane >> 2) + 16 * i];
+#pragma unroll
+                for (int dt = 0; dt < NDT; ++dt) {
+                    const u32x4 v = ldg(reinterpret_cast<const u32x4*>(cr + 32 * dt + 8 * (lane & 3)));
+#pragma unroll
+                    for (int w = 0; w < 4; ++w) cv[4 * (2 * dt + i) + w] = v[w];
+                }
+            }
         } else {
 #pragma unroll
             for (int g = 0; g < 4; ++g)
@@ -1151,17 +1169,30 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                     const u32x4 x = *reinterpret_cast<const u32x4*>(st + r * DR_SROW + 8 * c);
                     uint16_t* dst = CODEC == 0 ? img + (32 * kq + r) * DK + 32 * dt + 8 * c
                                                : img + (32 * dt + r) * FT_ROW + 32 * kq + 8 * c;
-                    *reinterpret_cast<u32x4*>(dst) = x;
+                    if (CODEC == 0 && cent && !rope) {
+                        // K = bf16(bf16(acc + bias) + center) (MG:438-454)
+                        u32x4 y;
+#pragma unroll
+                        for (int w = 0; w < 4; ++w) {
+                            const uint32_t cw = cv[4 * (2 * dt + i) + w];
+                            y[w] = pack_bf16x2(__uint_as_float(x[w] << 16) + __uint_as_float(cw << 16),
+                                               __uint_as_float(x[w] & 0xffff0000u) +
+                                                   __uint_as_float(cw & 0xffff0000u));
+                        }
+                        *reinterpret_cast<u32x4*>(dst) = y;
+                    } else {
+                        *reinterpret_cast<u32x4*>(dst) = x;
+                    }
                 }
             };
             if (CODEC == 0) {
                 // acc[dt] element i: d = 32 dt + 8 (i/4) + 4 hf + i%4 of this
-                // lane's key; K = bf16(bf16(acc + bias) + center), then with
-                // read-time RoPE each bf16 pair (d, d + 1) rotated by its
+                // lane's key; K = bf16(bf16(acc + bias) + center), the center
+                // added in flush() from coalesced rows unless RoPE applies;
+                // with read-time RoPE each bf16 pair (d, d + 1) rotated by its
                 // pair's (cos, sin) at the key's codec row (rope_pair: fp64,
                 // as rope_apply); a narrower reader's pair j is the original
                 // pair p.rope.pairs[h][j]
-                const bool rope = rope_on(p.rope);
                 RopeRows rr{};
                 const int32_t* pmap = nullptr;
                 if (rope) {
@@ -1186,8 +1217,10 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                         const f32x4 bs = *reinterpret_cast<const f32x4*>(&sm.bias[d]);
                         float a[4];
 #pragma unroll
-                        for (int e = 0; e < 4; ++e) a[e] = bf16_round(acc[dt][4 * g + e] + bs[e]);
-                        if (cent) {
+                        for (int e = 0; e < 4; ++e) a[e] = acc[dt][4 * g + e] + bs[e];
+                        if (cent && rope) {
+#pragma unroll
+                            for (int e = 0; e < 4; ++e) a[e] = bf16_round(a[e]);
                             const uint32_t c0 = cv[2 * (4 * dt + g)], c1 = cv[2 * (4 * dt + g) + 1];
                             a[0] += __uint_as_float(c0 << 16);
                             a[1] += __uint_as_float(c0 & 0xffff0000u);
