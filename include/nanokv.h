@@ -78,12 +78,18 @@ enum nkv_scale_dtype { NKV_DTYPE_BF16 = 0, NKV_DTYPE_FP16 = 1 };
 
 /* Work decomposition of nkv_attend.  Both give the same attention (within
  * bf16 rounding of the partials); they differ in cost:
- *  QUERY_TILES  a block owns a 256-query tile and a range of 32-key tiles,
- *               so every history tile is decoded once per query tile;
- *               partials only across the `splits` key ranges.
- *  KEY_CHUNKS   a block owns one 256-key chunk (decoded once, kept in LDS)
- *               and attends every query to it; each chunk leaves a bf16
- *               partial output + LSE per query that a combine kernel merges.
+ *  QUERY_TILES  a block owns a 256-query tile and a range of 32-key tiles and
+ *               decodes each tile into registers and LDS right before
+ *               attending it (decoded K/V never leave the CU), so every
+ *               history tile is decoded once per query tile; partials only
+ *               across the `splits` key ranges.
+ *  KEY_CHUNKS   every history tile is decoded once per head (the staged
+ *               schedule): one launch decodes each 128-key tile into the
+ *               call's workspace in the attention kernel's LDS layout (K and
+ *               V^T images, 64 KiB per tile: 176 MB at 24 heads x 12,480
+ *               keys), a flash launch streams the tiles through LDS with each
+ *               query block's O in registers over a key split, and a combine
+ *               merges the splits' bf16 partials by LSE.
  *  AUTO         KEY_CHUNKS whenever the codecs fit it (D = 128, ranks that
  *               are multiples of 64, scale groups that are multiples of 32),
  *               QUERY_TILES otherwise. */
@@ -350,10 +356,13 @@ typedef struct nkv_decode_args {
 int nkv_decode(void* stream, const nkv_decode_args* args);
 
 /*
- * Fused decode-and-attend: softmax(q k^T * softmax_scale) v over the keys
- * [decoded history (N tokens); current chunk (Nc tokens)], non-causal,
- * without materialising decoded K/V in global memory.  History K/V rows are
- * decoded tile by tile inside the kernel with the nkv_decode arithmetic.
+ * Decode-and-attend in one call: softmax(q k^T * softmax_scale) v over the
+ * keys [decoded history (N tokens); current chunk (Nc tokens)], non-causal.
+ * History K/V rows are decoded tile by tile with the nkv_decode arithmetic:
+ * once per head into the workspace, in the attention kernel's LDS layout
+ * (KEY_CHUNKS, the staged schedule), or once per 256-query tile into
+ * registers and LDS right before they are attended (QUERY_TILES); no
+ * decoded K/V tensor is produced.
  *   q       [B, Q, H, D] addressed as q[b*q_sb + t*q_st + h*q_sh + d]
  *   k_cur   [B, Nc, H, D] (k_sb/k_st/k_sh), v_cur likewise (v_*)
  *   out     [B, Q, H, D] bf16 (o_sb/o_st/o_sh)
@@ -435,7 +444,8 @@ int nkv_attend(void* stream, const nkv_attend_args* args, void* workspace,
  * static array of NKV_STATIC_SCRATCH_BYTES per GPU inside the library (held
  * until the process ends); a call that needs more (nkv_attend_workspace_size)
  * fails with NKV_ERR_WORKSPACE and launches nothing.  No part of the scratch
- * needs to start at zero: every byte a call reads it wrote first.  Every call
+ * needs to start at zero: every byte a call reads it wrote first (the
+ * flash kernel copies no tile the decode left unwritten).  Every call
  * on one GPU shares that GPU's array, so calls that overlap on one GPU (two
  * streams, two threads) race; serialise them.  The stream must belong to the
  * current device.  Allocates nothing (no hipMalloc, no allocating library
@@ -491,9 +501,12 @@ typedef struct nkv_reader_group {
  * native partition), out and lse, as for nkv_attend (its N is the codec's
  * token count; splits and schedule are ignored).  Every head should belong
  * to exactly one group (CN/core.py:213-215); a head in no group keeps the
- * native partition alone (a head listed by several groups is merged with the
- * first of them only when the call runs as one staged launch: no camera, at
- * most 3 groups).  Returns NKV_ERR_UNSUPPORTED for D != 128.
+ * native partition alone.  A head listed by more than one group is invalid
+ * (the reference rejects such groups, CN/core.py:213-215); the heads arrays
+ * are device memory, so the call cannot check it, and such a head's output is
+ * unspecified (one staged launch merges the first group listing it, the
+ * per-group path every one in turn).  The Python layer (ReaderLayer) refuses
+ * such groups before any call.  Returns NKV_ERR_UNSUPPORTED for D != 128.
  * RoPE (attend.rope != NULL, CN/mg35.py:207-214, 305-336): the native
  * partition's history keys are rotated at their codec rows and attend.q is
  * taken as already rotated; each reader group forms its queries from the

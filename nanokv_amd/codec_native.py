@@ -10,8 +10,10 @@ followed by attention), with the decode fused into the attention kernel:
   protected_tokens(frame_ids, ...) CN:140-152 frame-level protection policy
   codec_history_attention(q, cache, k_cur, v_cur, rope=None)
                                    decode-then-attend of a paired K/V codec
-                                   cache plus the current chunk, fused
-                                   (nkv_attend); K/V are never materialised;
+                                   cache plus the current chunk in one library
+                                   call (nkv_attend): each history tile is
+                                   decoded once, into the call's workspace in
+                                   the flash kernel's layout; no K/V tensor;
                                    rope: read-time RoPE of the cached keys
                                    (wan_video_dit.py:538-546)
   kv_rope(freqs, positions, h, w)  the positions of cached frames, as
@@ -512,7 +514,10 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     at full width by every head (mg35.py:192-303), the low history tokens
     (bool mask [N], default: the unprotected ones) through each head's reader
     group (mg35.py:315-347), and the two are merged by LSE (CN:33-42, 308).
-    Everything is fused in nkv_fast_attend; no K/V row is materialised.
+    Everything runs in one nkv_fast_attend call: every partition's history
+    tiles are decoded once into the call's workspace (the staged schedule)
+    or into LDS (the key-chunk kernel, reader groups with the camera); no
+    K/V tensor is produced.
     Scale: native_dim ** -0.5 (CN:287).
     RoPE (mg35.py:207-214, 305-336): rope = kv_rope(...) or an ops.RopeTable
     of the cached rows; q is then the rotated query, q_pre [B, H, Q, D] the

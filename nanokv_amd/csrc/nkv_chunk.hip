@@ -1,7 +1,18 @@
-// nkv_chunk.hip -- key-chunk-major fused decode + attention for gfx950
-// (NKV_SCHEDULE_KEY_CHUNKS of nkv_attend).
+// nkv_chunk.hip -- decode-once schedules of nkv_attend for gfx950
+// (NKV_SCHEDULE_KEY_CHUNKS).
 //
-// A 512-thread block (8 waves, two per SIMD) owns one (batch, head, chunk)
+// Two schedules live here; both decode every history key once per head.
+//  - The staged schedule (the drtile / stage8 decode, flash8_kernel and
+//    staged_combine_kernel, further below) serves every call at K/Q width
+//    128 and the reader widths 32/64 without the camera: the decode writes
+//    each 128-key tile once into the call's workspace, in the flash kernel's
+//    LDS layout, and the flash kernel streams the tiles back with O held in
+//    registers over a whole key split.
+//  - The key-chunk kernel (chunk8_kernel, next) serves reader widths 32/64
+//    with the camera, or with ranks above the resident decoder's 384: the
+//    decoded K/V stay in LDS, and each (chunk, query block) leaves a partial.
+//
+// Key-chunk kernel: a 512-thread block (8 waves, two per SIMD) owns one (batch, head, chunk)
 // of 256 keys.  It decodes the chunk's K and V once into LDS -- K[key][d]
 // and V^T[d][key], bf16, 137 KB -- and then every wave attends its share of
 // ALL the head's 32-query blocks to those keys.  Each (query, chunk) leaves
@@ -860,6 +871,18 @@ struct TileFmt {
     __device__ static int kswz(int r) { return (r / (16 / CPR)) % CPR; }
 };
 static_assert(TileFmt<32>::K_IMG * 2 % 1024 == 0, "a K image must be whole 1 KB pieces");
+static_assert(TileFmt<32>::TILE == FT_T * 32 + FT_IMG && TileFmt<64>::TILE == FT_T * 64 + FT_IMG &&
+                  TileFmt<CK_D>::TILE == FT_TILE,
+              "the tile format and the workspace plan must agree on a tile's size");
+
+// Elements of one tile image pair (K, then V^T) and of its K image at K/Q
+// width dk, from the same TileFmt the kernels address the tiles with.
+size_t tile_elems(int dk) {
+    return dk == 32 ? TileFmt<32>::TILE : dk == 64 ? TileFmt<64>::TILE : TileFmt<CK_D>::TILE;
+}
+size_t k_image_elems(int dk) {
+    return dk == 32 ? TileFmt<32>::K_IMG : dk == 64 ? TileFmt<64>::K_IMG : TileFmt<CK_D>::K_IMG;
+}
 static_assert(CK_T == 2 * FT_T, "two tiles per chunk");
 
 // s_waitcnt vmcnt(0) lgkmcnt(0): the wave's loads have landed and its LDS
@@ -1365,6 +1388,9 @@ __device__ __forceinline__ void flash_block(const ChunkParams& p, int64_t blk, u
     const unsigned char* src = reinterpret_cast<const unsigned char*>(
         p.tiles + (int64_t)bh * p.ntiles * TF::TILE);
     auto issue = [&](int tile) {
+        // the history's last tile holds no keys when n_rows % 256 is in
+        // (0, 128]: the decode never writes it and no step reads it
+        if (tile < p.ntiles_hist && (int64_t)tile * FT_T >= p.n_rows) return;
         const unsigned char* s = src + (int64_t)tile * TF::TILE * 2;
         const int bi = (tile - t0) & 1;
         // opaque here, so that the per-piece sums are not hoisted out of
@@ -1867,7 +1893,8 @@ constexpr int FT_CUS = 256;          // compute units of an MI355X
 // 0.571 ms, over 12,480 keys 0.161 vs 0.177 ms; 6 blocks 0.590 vs 0.660 and
 // 0.174 vs 0.202 ms; 12 blocks 0.747 vs 0.837 and 0.224 vs 0.254 ms; cfg2 (25
 // blocks) 0.950 vs 1.067 ms.  The key-chunk kernel remains for reader widths
-// 32/64 with read-time RoPE or camera.
+// 32/64 with the camera, or with ranks above 384 (read-time RoPE alone is
+// staged: drtile_kernel rotates in its K epilogue).
 constexpr int FT_MIN_QBLOCKS = 1;
 
 struct FlashPlan {
@@ -2047,6 +2074,49 @@ void plan_decode(const ChunkLaunchDesc* d, int n, MultiPlan& P) {
     for (size_t k = 0; k < segs.size(); ++k) P.ranges[segs[k].i][segs[k].cc] = (int)best_r[k];
 }
 
+// The byte extents the staged kernels write in a plan's workspace, checked
+// against each partition's slice [tiles_off, part_off) of tile images and
+// [part_off, next tiles_off) of split partials: the last tile's V^T image as
+// the decode addresses it (tile t of head bh at (bh * ntiles + t) tile
+// images, its V^T image after the K image, both at the partition's width;
+// v_dk != 0 addresses the V^T images at that width instead, to check a
+// layout mismatch), the current tiles' copies (128 wide) and the flash
+// kernel's partials (a 32 x 128 bf16 block per (b*h, split, query block),
+// then (m, l) per query).  On a violation, msg names it.
+bool plan_extents_ok(const MultiPlan& P, const ChunkLaunchDesc* d, int n, int v_dk,
+                     std::string* msg) {
+    for (int i = 0; i < n; ++i) {
+        const FlashPlan& f = P.f[i];
+        const size_t bh = (size_t)d[i].B * d[i].H;
+        const size_t tile = tile_elems(d[i].dk) * sizeof(uint16_t);
+        const size_t slice_end = P.part_off[i];
+        const size_t tiles_end = P.tiles_off[i] + bh * f.ntiles * tile;
+        auto fail = [&](const char* what, size_t end, size_t lim) {
+            if (msg)
+                *msg = "partition " + std::to_string(i) + " (width " + std::to_string(d[i].dk) +
+                       "): " + what + " ends at byte " + std::to_string(end) + ", past " +
+                       std::to_string(lim);
+            return false;
+        };
+        if (tiles_end > slice_end) return fail("tile images", tiles_end, slice_end);
+        const int64_t hist = cdiv(d[i].n_rows, FT_T);
+        if (hist > 0 && bh > 0) {
+            const int vw = v_dk ? v_dk : d[i].dk;
+            const size_t vtile = tile_elems(vw) * sizeof(uint16_t);
+            const size_t v_end = P.tiles_off[i] + ((bh - 1) * f.ntiles + hist - 1) * vtile +
+                                 (k_image_elems(vw) + FT_IMG) * sizeof(uint16_t);
+            if (v_end > tiles_end) return fail("the last V^T image", v_end, tiles_end);
+        }
+        if (f.ntiles > f.ntiles_hist && d[i].dk != CK_D)
+            return fail("current tiles at a width other than 128", tiles_end, tiles_end);
+        const size_t rows = bh * f.splits * cdiv(d[i].Q, 32) * 32;
+        const size_t part_end = P.part_off[i] + rows * PARTIAL_ROW_BYTES;
+        const size_t lim = i + 1 < n ? P.tiles_off[i + 1] : P.total;
+        if (part_end > lim) return fail("the split partials", part_end, lim);
+    }
+    return true;
+}
+
 // The plan depends on the partitions' shapes alone; the last one is kept
 // (a layer loop repeats the same shapes).
 MultiPlan multi_plan(const ChunkLaunchDesc* d, int n) {
@@ -2066,7 +2136,7 @@ MultiPlan multi_plan(const ChunkLaunchDesc* d, int n) {
     for (int i = 0; i < n; ++i) {
         const FlashPlan& f = P.f[i];
         P.tiles_off[i] = off;
-        off += align256((size_t)d[i].B * d[i].H * f.ntiles * (FT_T * d[i].dk + FT_IMG) * sizeof(uint16_t));
+        off += align256((size_t)d[i].B * d[i].H * f.ntiles * tile_elems(d[i].dk) * sizeof(uint16_t));
         P.part_off[i] = off;
         off += align256((size_t)d[i].B * d[i].H * f.splits * cdiv(d[i].Q, 32) * 32 * PARTIAL_ROW_BYTES);
     }
@@ -2126,6 +2196,13 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
                const int32_t* const* heads, const float* shift, int64_t sh_sb, int64_t sh_sh,
                void* workspace) {
     const MultiPlan P = multi_plan(d, n);
+    {
+        std::string why;
+        NKV_REQUIRE(plan_extents_ok(P, d, n, 0, &why), NKV_ERR_INVALID,
+                    "internal: staged workspace plan: " + why);
+    }
+    NKV_REQUIRE(staged_gemm(d[0]) || (n == 1 && d[0].dk == CK_D), NKV_ERR_INVALID,
+                "internal: stage8_kernel decodes one 128-wide partition");
     unsigned char* ws = reinterpret_cast<unsigned char*>(workspace);
     MultiParams M;
     memset(&M, 0, sizeof(M));
@@ -2151,8 +2228,9 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
     }
     int rc = NKV_OK;
     if (!staged_gemm(d[0])) {
-        // one partition (read-time RoPE / camera, or ranks above the resident
-        // decoder's): stage8_kernel decodes its history and current tiles
+        // one partition at width 128 with the camera, or ranks above the
+        // resident decoder's: stage8_kernel decodes its history and current
+        // tiles (read-time RoPE without the camera is drtile_kernel's)
         const ChunkParams& p = M.part[0];
         rc = set_smem(stage8_kernel, sizeof(Chunk8Smem));
         if (rc) return rc;
@@ -2358,27 +2436,18 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.part_ml = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
                                          qrows * CK_D * sizeof(uint16_t));
 
-    const int64_t hist_blocks = (int64_t)d.B * d.H * p.nch_hist;
-    const int64_t cur_blocks = (int64_t)d.B * d.H * (p.nch_total - p.nch_hist) * p.cur_splits;
+    // Only reader widths 32 and 64 reach the key-chunk kernel (with the
+    // camera, or ranks above the resident decoder's): every call at width
+    // 128 with keys to attend is staged, and current keys (the only masked
+    // ones) come with width 128 alone.  A call without keys only runs the
+    // combine (out = 0, lse = -inf).
+    NKV_REQUIRE(d.n_rows + d.Nc == 0 || (d.dk != CK_D && d.Nc == 0), NKV_ERR_INVALID,
+                "internal: a 128-wide or current-key launch reached the key-chunk kernel");
+    const int64_t blocks = (int64_t)d.B * d.H * p.nch_hist;
     p.blk_base = 0;
     if (d.ev_begin) NKV_HIP_CHECK(hipEventRecord((hipEvent_t)d.ev_begin, s));
-    if (p.cur_mask) {
-        // history chunks, then the masked current-key chunks (128 wide)
-        if (hist_blocks > 0) {
-            if (d.dk == 128) launch_dk<128, false>(p, hist_blocks, s, &rc);
-            else if (d.dk == 64) launch_dk<64, false>(p, hist_blocks, s, &rc);
-            else launch_dk<32, false>(p, hist_blocks, s, &rc);
-            if (rc) return rc;
-        }
-        if (cur_blocks > 0) {
-            p.blk_base = hist_blocks;
-            launch_dk<128, true>(p, cur_blocks, s, &rc);
-            if (rc) return rc;
-        }
-    } else if (hist_blocks + cur_blocks > 0) {
-        const int64_t blocks = hist_blocks + cur_blocks;
-        if (d.dk == 128) launch_dk<128, false>(p, blocks, s, &rc);
-        else if (d.dk == 64) launch_dk<64, false>(p, blocks, s, &rc);
+    if (blocks > 0) {
+        if (d.dk == 64) launch_dk<64, false>(p, blocks, s, &rc);
         else launch_dk<32, false>(p, blocks, s, &rc);
         if (rc) return rc;
     }
@@ -2475,3 +2544,43 @@ int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace
 }
 
 }  // namespace nkv
+
+// Test hook, not part of the C ABI header: the staged planner over n <=
+// NKV_MAX_PARTS partitions given as rows of nine int64 (B, H, dk, Q, n_rows,
+// Nc, rK, rV, camera), then the check of every extent the staged kernels
+// write against the plan (v_dk != 0 addresses the V^T images at that width,
+// to show that a layout mismatch is caught).  Host arithmetic only: it runs
+// without a GPU.  Returns NKV_OK, or NKV_ERR_INVALID with the violation in
+// nkv_last_error; *total receives the plan's workspace bytes.
+extern "C" int nkv_plan_check(const int64_t* shapes, int n, int v_dk, size_t* total) {
+    using namespace nkv;
+    clear_error();
+    NKV_REQUIRE(shapes && n >= 1 && n <= NKV_MAX_PARTS, NKV_ERR_INVALID, "1..4 partitions");
+    NKV_REQUIRE(v_dk == 0 || v_dk == 32 || v_dk == 64 || v_dk == 128, NKV_ERR_INVALID,
+                "v_dk must be 0, 32, 64 or 128");
+    static const float fake_mats = 0.0f;  // only its presence is read
+    ChunkLaunchDesc d[NKV_MAX_PARTS];
+    for (int i = 0; i < n; ++i) {
+        const int64_t* r = shapes + 9 * i;
+        memset(&d[i], 0, sizeof(ChunkLaunchDesc));
+        d[i].B = (int)r[0];
+        d[i].H = (int)r[1];
+        d[i].dk = (int)r[2];
+        d[i].Q = r[3];
+        d[i].n_rows = r[4];
+        d[i].N = r[4];
+        d[i].Nc = r[5];
+        d[i].key.r = (int)r[6];
+        d[i].value.r = (int)r[7];
+        d[i].cam.mats = r[8] ? &fake_mats : nullptr;
+        NKV_REQUIRE(d[i].B >= 1 && d[i].H >= 1 && d[i].Q >= 1 && d[i].n_rows >= 0 && d[i].Nc >= 0,
+                    NKV_ERR_INVALID, "bad partition shape");
+        NKV_REQUIRE(use_staged(d[i]), NKV_ERR_INVALID,
+                    "partition " + std::to_string(i) + " is not staged");
+    }
+    const MultiPlan P = multi_plan(d, n);
+    if (total) *total = P.total;
+    std::string why;
+    NKV_REQUIRE(plan_extents_ok(P, d, n, v_dk, &why), NKV_ERR_INVALID, why);
+    return NKV_OK;
+}

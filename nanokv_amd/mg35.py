@@ -22,10 +22,7 @@ does (CN/metadata_cache.py:48-72).
 """
 from __future__ import annotations
 
-import atexit
-import json
 import os
-from pathlib import Path
 from typing import Any, Callable, Optional
 
 import torch
@@ -34,47 +31,6 @@ from . import codec_native, nanokv_codec, ops
 
 MODEL = "matrix-game-3.5"
 PREFIX = "MG35_CODEC_NATIVE"
-
-
-# ---------------------------------------------------------------- accounting
-_ROWS: dict = {}
-
-
-def record(layer, q, k, low, heads, dim, low_dim_sum, write_cache, batch=1, history=0):
-    """Shape-based dense QK+AV MAC accounting of one call, kept only when
-    MG35_CODEC_NATIVE_MAC_JSON names an output file (accounting.py:5-13)."""
-    if not os.environ.get("MG35_CODEC_NATIVE_MAC_JSON"):
-        return
-    key = f'{layer}:{"rebuild" if write_cache else "denoise"}'
-    row = _ROWS.setdefault(key, dict(layer=int(layer), rebuild=bool(write_cache), calls=0,
-                                     baseline=0, candidate=0, history_low_tokens=0,
-                                     history_baseline=0))
-    base = 2 * batch * int(q) * int(k) * heads * dim
-    saved = 2 * batch * int(q) * int(low) * (heads * dim - int(low_dim_sum))
-    row["calls"] += 1
-    row["baseline"] += base
-    row["candidate"] += base - saved
-    row["history_low_tokens"] += int(low)
-    row["history_baseline"] += 2 * batch * int(q) * int(history) * heads * dim
-
-
-@atexit.register
-def _save_accounting():
-    """Write the accounting summary at exit (accounting.py:14-21)."""
-    dest = os.environ.get("MG35_CODEC_NATIVE_MAC_JSON")
-    if not dest or not _ROWS:
-        return
-    rows = list(_ROWS.values())
-    base = sum(r["baseline"] for r in rows)
-    candidate = sum(r["candidate"] for r in rows)
-    history = sum(r["history_baseline"] for r in rows)
-    Path(dest).write_text(json.dumps(dict(
-        scope="all self-attention layers, dense QK+AV, includes current/mosaic/rebuild; "
-              "excludes cross-attention",
-        baseline=base, candidate=candidate, reduction=1 - candidate / base,
-        history_baseline=history, history_fraction=history / base,
-        history_only_reduction_if_no_native_projection=(base - candidate) / history
-        if history else 0, rows=rows), indent=2))
 
 
 # ---------------------------------------------------------------- cache writes
@@ -232,12 +188,6 @@ def maybe_attention(self_attn, q_pre, q_native, k_native, v_raw, cur_k_pre, freq
     frames = list(cache_frames or [])
     chunk_ids = [] if cache is None else list(cache.get("chunk_ids", []))
     if reader is None:
-        n = cache_tokens
-        if n and cache_read_chunk_id is not None and len(chunk_ids) == len(frames) and frames:
-            n = n // len(frames) * sum(int(c) < 0 or int(c) == int(cache_read_chunk_id)
-                                       for c in chunk_ids)
-        record(layer_idx, q_pre.shape[1] - mosaic_tokens, n + k_native.shape[1], 0, num_heads,
-               dim, 0, write_cache, batch=q_pre.shape[0], history=n)
         return None
     use_camera = camera_info is not None
     if self_attn.prope_camera_layout != "full" and use_camera:
@@ -256,11 +206,6 @@ def maybe_attention(self_attn, q_pre, q_native, k_native, v_raw, cur_k_pre, freq
                                   "policy keeps current and mosaic tokens native")
     r = route(frames, chunk_ids, cache_read_chunk_id, cache_tokens, recent, stride, sink,
               bool(policy.get("native_history", False)))
-    record(layer_idx, q_pre.shape[1] - mosaic_tokens, r["active_count"] + k_native.shape[1],
-           r["low_count"], num_heads, reader.native_dim,
-           sum(len(g.heads) * (g.indices.shape[1] + g.v_indices.shape[1]) / 2
-               for g in reader.groups),
-           write_cache, batch=q_pre.shape[0], history=r["active_count"])
     # no old low-dimensional history: the native path is cheaper and
     # numerically authoritative (MG35:187-190)
     if r["low_count"] == 0:

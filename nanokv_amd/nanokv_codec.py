@@ -22,6 +22,7 @@ with preload_operator_weights().  All compute goes through libnanokv_hip.so
 from __future__ import annotations
 
 import os
+import weakref
 from collections import OrderedDict
 from pathlib import Path
 from typing import Any, Optional
@@ -408,6 +409,13 @@ def payload_bytes(value: Any) -> int:
     return 0
 
 
+class SegmentList(dict):
+    """A worldplay_segments_v1 list, {"codec": SEGMENTS, "segments": [...]}:
+    a plain dict to every caller (same keys, same behaviour), which can also be
+    weakly referenced, so that history_codecs can remember its segment tables
+    exactly as long as the caller keeps the list."""
+
+
 def concat_values(left: Any, right: Any) -> Any:
     """Append immutable segments (MG:600-609)."""
     if left is None:
@@ -416,7 +424,7 @@ def concat_values(left: Any, right: Any) -> Any:
         return left
     if not is_payload(left) or not is_payload(right):
         raise RuntimeError("WorldPlay packed-cache concat received a raw/payload mixture")
-    return {"codec": SEGMENTS, "segments": segments_of(left) + segments_of(right)}
+    return SegmentList(codec=SEGMENTS, segments=segments_of(left) + segments_of(right))
 
 
 def codec_view(part: dict, device: torch.device) -> ops.Codec:
@@ -511,7 +519,7 @@ def select_value(value: Any, token_idx: torch.Tensor, *, kind: str, layer: int,
         return None
     if len(out) == 1:
         return out[0]
-    return {"codec": SEGMENTS, "segments": out}
+    return SegmentList(codec=SEGMENTS, segments=out)
 
 
 def _pairs(key: Any, value: Any) -> list:
@@ -603,22 +611,32 @@ _HISTORY_TABLES: "OrderedDict[tuple, tuple]" = OrderedDict()
 _HISTORY_TABLES_MAX = 256
 
 
+def _evict_history_table(ident: tuple, ref: "weakref.ref") -> None:
+    entry = _HISTORY_TABLES.get(ident)
+    if entry is not None and any(r is ref for r in entry[0]):
+        del _HISTORY_TABLES[ident]
+
+
 def history_codecs(key: Any, value: Any, device: torch.device):
     """One (K, V) ops.Codec pair covering every segment of a paired cache.
 
     A single segment is passed as its own flat arrays.  A segment list is
     passed as an nkv_segment table over the segments' own tensors (each with
     its own center table, as the reference decodes them, MG:393-455): no
-    codes, scales, ids or tables are copied.  The tables are remembered per
-    segment list (bounded LRU keyed by the payloads, which are immutable), so
-    the per-layer reads of one denoise step and the next reuse them."""
+    codes, scales, ids or tables are copied.  The tables of a K/V pair of
+    SegmentLists (what concat_values and select_value return) are remembered
+    while both lists live, so the per-layer reads of one denoise step and the
+    next reuse them: an entry holds weak references to the two lists and is
+    dropped with them (select_value evicting frames, a cache reset), and with
+    it the device views it kept.  Other segment lists are not remembered."""
     pairs = _pairs(key, value)
     dev = torch.device(device)
     if len(pairs) == 1:
         return codec_view(pairs[0][0], dev), codec_view(pairs[0][1], dev)
-    ident = (str(dev),) + tuple((id(k), id(v)) for k, v in pairs)
-    hit = _HISTORY_TABLES.get(ident)
-    if hit is not None:
+    remember = isinstance(key, SegmentList) and isinstance(value, SegmentList)
+    ident = (str(dev), id(key), id(value))
+    hit = _HISTORY_TABLES.get(ident) if remember else None
+    if hit is not None and hit[0][0]() is key and hit[0][1]() is value:
         _HISTORY_TABLES.move_to_end(ident)
         return hit[1]
     out = []
@@ -633,8 +651,10 @@ def history_codecs(key: Any, value: Any, device: torch.device):
                                   for v in views], dev)
         out.append(ops.Codec(packed=None, scales=None, w_dec=views[0].w_dec,
                              group=views[0].group, mean=views[0].mean, segments=table))
-    # the payloads are kept with the entry so that their ids stay unique
-    _HISTORY_TABLES[ident] = (pairs, (out[0], out[1]))
-    while len(_HISTORY_TABLES) > _HISTORY_TABLES_MAX:
-        _HISTORY_TABLES.popitem(last=False)
+    if remember:
+        refs = tuple(weakref.ref(x, lambda ref, ident=ident: _evict_history_table(ident, ref))
+                     for x in (key, value))
+        _HISTORY_TABLES[ident] = (refs, (out[0], out[1]))
+        while len(_HISTORY_TABLES) > _HISTORY_TABLES_MAX:
+            _HISTORY_TABLES.popitem(last=False)
     return out[0], out[1]

@@ -14,6 +14,7 @@ import pytest
 import torch
 
 import oracle.oracle as orc
+from tests._mg35_ref import keep_reference, route_reference
 from nanokv_amd import codec_native, mg35, nanokv_codec as nc, ops, synth
 from tests._helpers import max_abs_cos, oracle_codec, oracle_groups, u16
 
@@ -120,11 +121,13 @@ def test_maybe_attention_against_oracle(dev, tmp_path, monkeypatch, camera, disa
     assert out is not None and out.shape == (1, M + S, H * D)
     assert bool((out[:, :M] == 0).all())
     # ---- oracle, in the reference's order
-    r = mg35.route(cache["frames"], cache["chunk_ids"], 0, N, 2, 2, 1, False)
-    prot = torch.nonzero(r["protect"]).flatten().numpy()
-    low = torch.nonzero(r["low"]).flatten().numpy()
+    # routing and visibility from the independent restatements of
+    # MG35:155-170 and MG35:258-283, not from the hook's own helpers
+    r_prot, r_low = route_reference(cache["frames"], cache["chunk_ids"], 0, N, 2, 2, 1, False)
+    prot = torch.nonzero(r_prot).flatten().numpy()
+    low = torch.nonzero(r_low).flatten().numpy()
     assert prot.size and low.size
-    keep = mg35.visibility_keep(S, M, S, cur_frames, hole_keep, [-1, 0]).numpy()
+    keep = keep_reference(S, M, S, len(cur_frames), hole_keep, [-1, 0]).numpy()
     key, value = nc.history_codecs(cache["k"], cache["v"], dev)
     sname = "bf16" if key.scale_dtype == torch.bfloat16 else "fp16"
     qn = q_nat[M:]

@@ -115,3 +115,33 @@ def test_codec_history_attention_refuses_short_camera_frames():
     q = torch.zeros(1, 2, 4, 128, dtype=torch.bfloat16)
     with pytest.raises(ValueError, match="frames must cover exactly"):
         codec_native.codec_history_attention(q, payload, payload, camera=cam)
+
+
+def test_history_codecs_cache_releases_dropped_payloads():
+    """history_codecs remembers the segment table of a paired segment list, but
+    only while the payloads live: dropping them (as select_value or a cache
+    reset does) removes the entry, and the codes' memory is freed."""
+    import gc
+    import weakref
+
+    nc.register_operator("k", 0, encoder=torch.zeros(64, 128), decoder=torch.zeros(128, 64))
+    nc.register_operator("v", 0, encoder=torch.zeros(64, 128), decoder=torch.zeros(128, 64))
+    nc._HISTORY_TABLES.clear()
+    k = nc.concat_values(_fake_payload("k", 10), _fake_payload("k", 6))
+    v = nc.concat_values(_fake_payload("v", 10), _fake_payload("v", 6))
+    first = nc.history_codecs(k, v, torch.device("cpu"))
+    assert len(nc._HISTORY_TABLES) == 1
+    again = nc.history_codecs(k, v, torch.device("cpu"))
+    assert again[0] is first[0] and again[1] is first[1]     # the remembered tables
+    codes = weakref.ref(k["segments"][0]["packed_codes"])
+    storage = weakref.ref(k["segments"][0]["packed_codes"].untyped_storage())
+    del first, again, k, v
+    gc.collect()
+    assert len(nc._HISTORY_TABLES) == 0
+    assert codes() is None
+    # a fresh list of new payloads builds a new entry
+    k2 = nc.concat_values(_fake_payload("k", 4), _fake_payload("k", 4))
+    v2 = nc.concat_values(_fake_payload("v", 4), _fake_payload("v", 4))
+    nc.history_codecs(k2, v2, torch.device("cpu"))
+    assert len(nc._HISTORY_TABLES) == 1
+    del storage

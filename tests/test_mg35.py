@@ -11,6 +11,7 @@ import types
 import pytest
 import torch
 
+from tests._mg35_ref import keep_reference, route_reference
 from nanokv_amd import codec_native, mg35
 
 
@@ -67,25 +68,6 @@ def test_unlisted_layer_returns_none(monkeypatch, tmp_path):
         _call(layer_idx=3)
 
 
-def _reference_routing(frames, chunk_ids, read_chunk, tokens, recent, stride, sink, native):
-    """MG35:155-170 with tensors: token frame ordinals, the active mask from
-    chunk ids, protected_tokens over the frame ordinals (CN/core.py:140-152)."""
-    n = len(frames)
-    ordinal = torch.arange(n).repeat_interleave(tokens // n) if n else torch.empty(0, dtype=torch.long)
-    active = torch.ones(tokens, dtype=torch.bool)
-    if read_chunk is not None and len(chunk_ids) == n:
-        fa = torch.tensor([int(v) < 0 or int(v) == int(read_chunk) for v in chunk_ids],
-                          dtype=torch.bool)
-        active &= fa.index_select(0, ordinal)
-    protect = torch.zeros_like(active)
-    if tokens:
-        fp = codec_native.protected_tokens(torch.arange(n), recent, stride, sink)
-        protect = active & fp.index_select(0, ordinal)
-    if native:
-        protect = active.clone()
-    return protect, active & ~protect
-
-
 def test_route_matches_reference_formulation():
     cases = 0
     for n in range(0, 7):
@@ -96,7 +78,7 @@ def test_route_matches_reference_formulation():
                     tokens = 3 * n
                     r = mg35.route(list(range(10, 10 + n)), chunks, read, tokens, recent,
                                    stride, sink, native)
-                    p, lo = _reference_routing(list(range(n)), chunks, read, tokens, recent,
+                    p, lo = route_reference(list(range(n)), chunks, read, tokens, recent,
                                                stride, sink, native)
                     assert torch.equal(r["protect"], p), (n, recent, stride, sink, chunks, read)
                     assert torch.equal(r["low"], lo)
@@ -126,3 +108,28 @@ def test_visibility_keep():
     assert torch.equal(keep[:, 2:], want) and bool(keep[:, :2].all())
     with pytest.raises(RuntimeError, match="divisible"):
         mg35.visibility_keep(5, 0, 4, [0, 1], None, [0, 1])
+
+
+def test_visibility_keep_matches_per_key_rule():
+    """visibility_keep against the per-(query, key) statement of MG35:258-283
+    over frame counts, chunk-id patterns (anchors, one chunk, mixed) and hole
+    masks."""
+    g = torch.Generator().manual_seed(3)
+    cases = 0
+    for F in (1, 2, 3, 4):
+        for ids in (None, [-1] * F, [0] * F, [(i % 3) - 1 for i in range(F)],
+                    [i for i in range(F)], [-1] + [2] * (F - 1)):
+            for M in (0, 3):
+                for hole in (None, torch.rand(M, generator=g) > 0.4):
+                    if hole is not None and M == 0:
+                        continue
+                    for qpf, kpf in ((1, 1), (2, 3), (4, 2)):
+                        Q, K = qpf * F, kpf * F
+                        got = mg35.visibility_keep(Q, M, K, list(range(F)), hole, ids)
+                        want = keep_reference(Q, M, K, F, hole, ids)
+                        if want is None:
+                            assert got is None, (F, ids, M, qpf, kpf)
+                        else:
+                            assert got is not None and torch.equal(got, want), (F, ids, M, qpf, kpf)
+                        cases += 1
+    assert cases > 200

@@ -52,16 +52,41 @@ def test_static_scratch_matches_nkv_attend_twice(dev):
 
 def test_static_scratch_refuses_oversize_calls(dev):
     """A config-1-sized key-chunk call (206 MB of tiles and partials) is refused with
-    NKV_ERR_WORKSPACE before anything is launched (the pointers are never
-    read: the size check comes first)."""
+    NKV_ERR_WORKSPACE before anything is launched.  The size query (host
+    arithmetic) already exceeds the static array; every pointer of the call is a
+    real device buffer of its declared shape, so no launch could read outside
+    memory even if the refusal came later."""
+    B, H, D, Q, N, Nc, r, G = 1, 24, 128, 1560, 12480, 1560, 384, 32
     args = _lib.NkvAttendArgs()
-    args.B, args.H, args.D, args.Q, args.N, args.Nc = 1, 24, 128, 1560, 12480, 1560
-    args.softmax_scale = 128 ** -0.5
-    fake = 1 << 20
-    args.q = args.out = args.k_cur = args.v_cur = fake
+    args.B, args.H, args.D, args.Q, args.N, args.Nc = B, H, D, Q, N, Nc
+    args.softmax_scale = D ** -0.5
     for c in (args.key, args.value):
-        c.packed = c.scales = c.w_dec = fake
-        c.r, c.group, c.scale_dtype = 384, 32, _lib.NKV_DTYPE_FP16
+        c.r, c.group, c.scale_dtype = r, G, _lib.NKV_DTYPE_FP16
+    bf = dict(dtype=torch.bfloat16, device=dev)
+    q = torch.zeros(B, Q, H, D, **bf)
+    out = torch.empty(B, Q, H, D, **bf)
+    k_cur = torch.zeros(B, Nc, H, D, **bf)
+    v_cur = torch.zeros(B, Nc, H, D, **bf)
+    keep = [q, out, k_cur, v_cur]
+    args.q, args.out = q.data_ptr(), out.data_ptr()
+    args.k_cur, args.v_cur = k_cur.data_ptr(), v_cur.data_ptr()
+    for t in (q, out, k_cur, v_cur):
+        assert t.is_contiguous()
+    args.q_sb, args.q_st, args.q_sh = Q * H * D, H * D, D
+    args.o_sb, args.o_st, args.o_sh = Q * H * D, H * D, D
+    args.k_sb, args.k_st, args.k_sh = Nc * H * D, H * D, D
+    args.v_sb, args.v_st, args.v_sh = Nc * H * D, H * D, D
+    for c in (args.key, args.value):
+        packed = torch.zeros(B, N, r // 2, dtype=torch.uint8, device=dev)
+        scales = torch.zeros(B, N, r // G, dtype=torch.float16, device=dev)
+        w_dec = torch.zeros(H * D, r, **bf)
+        keep += [packed, scales, w_dec]
+        c.packed, c.scales, c.w_dec = packed.data_ptr(), scales.data_ptr(), w_dec.data_ptr()
+    need = _lib.lib().nkv_attend_workspace_size(ctypes.byref(args))
+    assert need > _lib.NKV_STATIC_SCRATCH_BYTES
+    torch.cuda.synchronize()
     rc = _lib.lib().nkv_attend_static(None, ctypes.byref(args))
     assert rc == _lib.NKV_ERR_WORKSPACE
     assert b"nkv_attend_static holds" in _lib.lib().nkv_last_error()
+    torch.cuda.synchronize()
+    del keep
