@@ -436,6 +436,43 @@ def rollout(args, device) -> dict:
     }
 
 
+def fast_vs_full_decode(run_fast, q, kc, vc, codecs) -> dict:
+    """Config 3's comparison of the Fast read with the full decode of the same
+    inputs (nkv_attend: every history row at full width for every head):
+    max-abs difference and cosine over all heads, over the full-width heads
+    (protected everywhere: equal up to the merge's rounding) and over the
+    reader heads (their old rows read through random, unfitted 384 -> 32
+    readers, so their deviation measures the readers, not the kernels).  With
+    BASELINE's queries (scores of standard deviation ~0.1 here) attention is
+    near-uniform and every read agrees closely; with the queries 16 times
+    larger (peaked attention) the readers' effect shows.  run_fast(q) is the
+    Fast call's output for queries q."""
+    from nanokv_amd import ops, synth
+    H = q.shape[2]
+    full_heads = list(synth.FAST_FULL_HEADS)
+    reader_heads = [h for h in range(H) if h not in full_heads]
+
+    def stats(a, b, heads):
+        a = a[:, :, heads].double().flatten()
+        b = b[:, :, heads].double().flatten()
+        cos = float((a @ b) / (a.norm() * b.norm()))
+        return {"max_abs": round(float((a - b).abs().max()), 5), "cos": round(cos, 6)}
+
+    result = {}
+    for name, scale in (("baseline_queries", 1.0), ("queries_x16", 16.0)):
+        qx = q if scale == 1.0 else (q.float() * scale).to(q.dtype)
+        fast = run_fast(qx).clone()
+        full = ops.attend(qx, kc, vc, codecs[0], codecs[1], return_lse=False)
+        if isinstance(full, tuple):
+            full = full[0]
+        result[name] = {"all_heads": stats(fast, full, list(range(H))),
+                        "full_heads": stats(fast, full, full_heads),
+                        "reader_heads": stats(fast, full, reader_heads)}
+    result["note"] = ("Fast against nkv_attend's full decode on the same inputs; reader heads "
+                      "use random (unfitted) 384->32 readers")
+    return result
+
+
 def main():
     args = parse()
     world = int(os.environ.get("WORLD_SIZE", "1"))
@@ -588,6 +625,12 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic, "kernel_ms_avg": round(kavg_ms, 4)},
     }
+    if fast:
+        def run_fast(qx):
+            r = ops.fast_attend(qx, kc, vc, codecs[0], codecs[1], prot_rows, low_rows, groups,
+                                out=out, return_lse=False, workspace=ws)
+            return r[0] if isinstance(r, tuple) else r
+        result["vs_full_decode"] = fast_vs_full_decode(run_fast, q, kc, vc, codecs)
     if not args.no_cpu_baseline and not fast:
         result["cpu_baseline"] = cpu_baseline(shape, layer, codecs, q, kc, vc, args.cpu_seconds)
         result["cpu_baseline"]["config0"] = cpu_config0(q.device)
