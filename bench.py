@@ -59,11 +59,13 @@ def parse():
                     help="time budget of the CPU-baseline head sample")
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--rope", action="store_true",
-                    help="configs 1-2: read-time RoPE of the history keys (frames of "
-                         "30 x 52 tokens at temporal positions 0, 1, ...)")
+                    help="configs 1-3: read-time RoPE of the history keys (frames of "
+                         "30 x 52 tokens at temporal positions 0, 1, ...); config 3 also "
+                         "rotates the reader queries (the chunk's frame)")
     ap.add_argument("--camera", action="store_true",
-                    help="configs 1-2: camera P^-1 of the history keys and values (frames "
-                         "of 1,560 tokens, four camera matrix sets)")
+                    help="configs 1-3: camera P^-1 of the history keys and values (frames "
+                         "of 1,560 tokens, four camera matrix sets); config 3 also takes "
+                         "P^T of the reader queries and applies P to the output")
     ap.add_argument("--profile-kernel", action="store_true",
                     help="no timing: run a known-size copy and a few fused calls (for rocprofv3 --pmc)")
     return ap.parse_args()
@@ -436,7 +438,7 @@ def rollout(args, device) -> dict:
     }
 
 
-def fast_vs_full_decode(run_fast, q, kc, vc, codecs) -> dict:
+def fast_vs_full_decode(run_fast, q, kc, vc, codecs, rope=None, camera=None) -> dict:
     """Config 3's comparison of the Fast read with the full decode of the same
     inputs (nkv_attend: every history row at full width for every head):
     max-abs difference and cosine over all heads, over the full-width heads
@@ -445,8 +447,9 @@ def fast_vs_full_decode(run_fast, q, kc, vc, codecs) -> dict:
     readers, so their deviation measures the readers, not the kernels).  With
     BASELINE's queries (scores of standard deviation ~0.1 here) attention is
     near-uniform and every read agrees closely; with the queries 16 times
-    larger (peaked attention) the readers' effect shows.  run_fast(q) is the
-    Fast call's output for queries q."""
+    larger (peaked attention) the readers' effect shows.  run_fast(scale) is
+    the Fast call's output for the queries times scale (exact in bf16); rope
+    and camera are the history's, applied by the full decode likewise."""
     from nanokv_amd import ops, synth
     H = q.shape[2]
     full_heads = list(synth.FAST_FULL_HEADS)
@@ -461,8 +464,9 @@ def fast_vs_full_decode(run_fast, q, kc, vc, codecs) -> dict:
     result = {}
     for name, scale in (("baseline_queries", 1.0), ("queries_x16", 16.0)):
         qx = q if scale == 1.0 else (q.float() * scale).to(q.dtype)
-        fast = run_fast(qx).clone()
-        full = ops.attend(qx, kc, vc, codecs[0], codecs[1], return_lse=False)
+        fast = run_fast(scale).clone()
+        full = ops.attend(qx, kc, vc, codecs[0], codecs[1], return_lse=False, rope=rope,
+                          camera=camera)
         if isinstance(full, tuple):
             full = full[0]
         result[name] = {"all_heads": stats(fast, full, list(range(H))),
@@ -507,24 +511,64 @@ def main():
         ws_bytes = ops.attend_workspace_size(q, shape.N, shape.Nc, codecs[0], codecs[1],
                                              args.splits, args.schedule)
         ws = torch.empty(max(ws_bytes, 1), device=device, dtype=torch.uint8)
-    rope = None
-    if args.rope and not fast:
-        grid_h, grid_w = 30, 52  # 1,560 tokens per frame
-        frames = -(-shape.N // (grid_h * grid_w))
-        rope = ops.Rope.from_bands(ops.rope_bands(shape.D), range(frames), grid_h, grid_w,
-                                   device)
-    camera = None
-    if args.camera and not fast:
-        frames = -(-shape.N // 1560)
-        g = torch.Generator().manual_seed(7)
-        mats = torch.eye(4).expand(1, 4, 4, 4, 4) + 0.3 * torch.randn(1, 4, 4, 4, 4, generator=g)
-        camera = ops.Camera(mats.contiguous().to(device),
+    rope = q_rope = None
+    grid_h, grid_w = 30, 52  # 1,560 tokens per frame
+    frames = -(-shape.N // (grid_h * grid_w))
+    if args.rope:
+        bands = ops.rope_bands(shape.D)
+        rope = ops.Rope.from_bands(bands, range(frames), grid_h, grid_w, device)
+        # the queries are the chunk after the history: frame `frames`
+        q_rope = ops.Rope.from_bands(bands, [frames], grid_h, grid_w, device) if fast else None
+    camera = q_camera = out_camera = None
+    if args.camera:
+        # PRoPE matrices per (matrix set, sub-frame); the history rows take
+        # P^-1 of their frame's set (frame f: set f % 4), the queries P^T and
+        # the output P of the chunk's frame
+        P, P_T, P_inv = synth.camera_matrices(4, seed=7)
+        camera = ops.Camera(P_inv.to(device),
                             torch.arange(frames, dtype=torch.int32).remainder(4).to(device), 1560)
+        if fast:
+            qf = torch.tensor([frames % 4], dtype=torch.int32, device=device)
+            q_camera = ops.Camera(P_T.to(device), qf, 1560)
+            out_camera = ops.Camera(P.to(device), qf, 1560)
+    q_pre = None
+    if fast and (rope or camera):
+        # the groups project the untransformed queries; the native partition
+        # takes them rotated and transformed (RoPE, then P^T), as are the
+        # current keys (their values by P^-1) -- inputs, outside the step
+        q_pre = q
+        q = ops.rope_apply(q, q_rope) if rope else q
+        q = ops.camera_apply(q, q_camera) if camera else q
+        if rope:
+            kc = ops.rope_apply(kc, q_rope)
+        if camera:
+            cur = ops.Camera(camera.mats, torch.tensor([frames % 4], dtype=torch.int32,
+                                                       device=device), 1560)
+            kc, vc = ops.camera_apply(kc, cur), ops.camera_apply(vc, cur)
+        groups = [g.tensors(rope=rope is not None, camera=camera is not None)
+                  for g in reader.groups]
+        ws_bytes = ops.fast_attend_workspace_size(
+            q, kc, vc, codecs[0], codecs[1], prot_rows, low_rows, groups, rope=rope,
+            q_pre=q_pre, q_rope=q_rope, camera=camera, q_camera=q_camera, out_camera=out_camera)
+        ws = torch.empty(max(ws_bytes, 1), device=device, dtype=torch.uint8)
+        torch.cuda.synchronize()
+
+    def run_fast(scale=1.0):
+        qx, qp = q, q_pre
+        if scale != 1.0:
+            qx = (q.float() * scale).to(q.dtype)
+            qp = (q_pre.float() * scale).to(q.dtype) if q_pre is not None else None
+        # with the camera the call also puts P of its query's frame on the
+        # output (CN/mg35.py:310-347)
+        r = ops.fast_attend(qx, kc, vc, codecs[0], codecs[1], prot_rows, low_rows, groups,
+                            out=out, return_lse=False, workspace=ws, rope=rope, q_pre=qp,
+                            q_rope=q_rope, camera=camera, q_camera=q_camera,
+                            out_camera=out_camera)
+        return r[0] if isinstance(r, tuple) else r
 
     def step(events=None):
         if fast:
-            return ops.fast_attend(q, kc, vc, codecs[0], codecs[1], prot_rows, low_rows, groups,
-                                   out=out, return_lse=False, workspace=ws)
+            return run_fast()
         return ops.attend(q, kc, vc, codecs[0], codecs[1], out=out, splits=args.splits,
                           return_lse=False, workspace=ws, kernel_events=events,
                           schedule=args.schedule, rope=rope, camera=camera)
@@ -614,8 +658,12 @@ def main():
                    "parallelism": "single-gpu"}
         | ({"protected_rows": int(prot_rows.numel()), "full_heads": list(synth.FAST_FULL_HEADS),
             "reader_width": synth.FAST_READER_D} if fast else {})
-        | ({"rope": "history keys rotated at read, frames of 30x52 tokens"} if rope else {})
-        | ({"camera": "history keys and values times P^-1 at read, frames of 1560 tokens"}
+        | ({"rope": "history keys rotated at read, frames of 30x52 tokens"
+                      + ("; reader queries rotated at the chunk's frame" if fast else "")}
+           if rope else {})
+        | ({"camera": "PRoPE: history keys and values times P^-1 at read, frames of 1560 tokens"
+                        + ("; reader queries times P^T, P on the output (in the call)"
+                           if fast else "")}
            if camera else {}),
         "history_tokens_per_ms": round(shape.N / ms_per_step, 1),
         "algorithmic_flops": fl,
@@ -625,12 +673,10 @@ def main():
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
                      "traffic": traffic, "kernel_ms_avg": round(kavg_ms, 4)},
     }
-    if fast:
-        def run_fast(qx):
-            r = ops.fast_attend(qx, kc, vc, codecs[0], codecs[1], prot_rows, low_rows, groups,
-                                out=out, return_lse=False, workspace=ws)
-            return r[0] if isinstance(r, tuple) else r
-        result["vs_full_decode"] = fast_vs_full_decode(run_fast, q, kc, vc, codecs)
+    if fast and out_camera is None:
+        # (with the camera the two reads take different queries: the full
+        # decode's are q, P^T already applied, with no P on its output)
+        result["vs_full_decode"] = fast_vs_full_decode(run_fast, q, kc, vc, codecs, rope, camera)
     if not args.no_cpu_baseline and not fast:
         result["cpu_baseline"] = cpu_baseline(shape, layer, codecs, q, kc, vc, args.cpu_seconds)
         result["cpu_baseline"]["config0"] = cpu_config0(q.device)

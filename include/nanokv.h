@@ -518,9 +518,13 @@ typedef struct nkv_reader_group {
  * partition's history keys and values are transformed in-kernel and attend.q,
  * k_cur and v_cur are taken as already transformed; each reader group's q_low
  * is transformed by P^T of the query rows (q_camera, query t at row t) and
- * k_low / v_low by P^-1 on their blocks (cam_blocks).  The caller applies P
- * to out, as for nkv_attend: with a value lift folded into the value reader
- * (block-selection or identity lifts) P commutes with the lift.
+ * k_low / v_low by P^-1 on their blocks (cam_blocks).  P of the query rows
+ * goes on out after the merge: by the call when o_camera is given, else by
+ * the caller (as for nkv_attend).  With a value lift folded into the value
+ * reader (block-selection or identity lifts) P commutes with the lift, and
+ * it commutes with the merge (one P per query row for both partitions); the
+ * reference applies it to each partition's bf16 output before the merge
+ * (CN/mg35.py:310-347), so only the bf16 rounding points differ.
  * Value-mean correction (low_shift != NULL; LingBot codec_native_attention.py
  * :779-785 and finish, codec_native_finish_triton.py:31-32): low_shift[b, h]
  * ([B, H, D] fp32, strides ls_sb, ls_sh, unit d stride) is added to every
@@ -542,6 +546,11 @@ typedef struct nkv_fast_args {
     const nkv_camera* q_camera;   /* P^T of the query rows (with a camera), host pointer */
     const float* low_shift;       /* [B, H, D] fp32 low value shift, or NULL */
     int64_t ls_sb, ls_sh;
+    /* P of the query rows, applied to out (FULL layout) once the partitions
+     * are merged: out = bf16(P . out) as nkv_camera_apply computes it, the
+     * caller's last step of the camera attention (CN/mg35.py:310-347).
+     * Host pointer, or NULL: out is left in the values' frame. */
+    const nkv_camera* o_camera;
 } nkv_fast_args;
 
 /* Bytes of workspace nkv_fast_attend needs for these arguments. */

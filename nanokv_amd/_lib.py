@@ -129,6 +129,7 @@ class NkvFastArgs(Structure):
         ("q_pre", c_void_p), ("qp_sb", c_int64), ("qp_st", c_int64), ("qp_sh", c_int64),
         ("q_rope", POINTER(NkvRope)), ("q_camera", POINTER(NkvCamera)),
         ("low_shift", c_void_p), ("ls_sb", c_int64), ("ls_sh", c_int64),
+        ("o_camera", POINTER(NkvCamera)),
     ]
 
 

@@ -732,6 +732,15 @@ int plan_attend(const nkv_attend_args* a, AttendPlan* plan) {
     }
     if (a->Nc > 0) NKV_REQUIRE(a->k_cur && a->v_cur, NKV_ERR_INVALID, "current K/V missing");
     if (a->Q > 0) NKV_REQUIRE(a->q && a->out, NKV_ERR_INVALID, "q and out required");
+    if (a->Q > 0)
+        NKV_REQUIRE(rows16(a->q, a->q_sb, a->q_st, a->q_sh) &&
+                        rows16(a->out, a->o_sb, a->o_st, a->o_sh),
+                    NKV_ERR_INVALID, "q and out must be 16-byte aligned with strides divisible by 8");
+    if (a->Nc > 0)
+        NKV_REQUIRE(rows16(a->k_cur, a->k_sb, a->k_st, a->k_sh) &&
+                        rows16(a->v_cur, a->v_sb, a->v_st, a->v_sh),
+                    NKV_ERR_INVALID,
+                    "k_cur and v_cur must be 16-byte aligned with strides divisible by 8");
     plan->q_tiles = (int)cdiv(a->Q, AT_BM);
     // spread the queries evenly over the tiles, in whole 32-query blocks
     plan->q_per_tile =

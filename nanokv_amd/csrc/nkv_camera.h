@@ -24,7 +24,23 @@ struct CameraDev {
     // [launch heads, width / 8] sub-frame of each 8-dim block of a reader key
     // (camera_selected, CN/core.py:110-137), or null: the FULL/SF13 layout
     const int32_t* blocks = nullptr;
+    // the matrices rounded to bf16, held in fp64, [mat batches, n_mats, 64]
+    // (filled per call in the staged schedule's workspace), or null
+    const double* m64 = nullptr;
 };
+
+// Matrix batches an nkv_camera holds for a call over B batch items.
+__host__ __device__ __forceinline__ int camera_batches(const CameraDev& c, int B) {
+    return c.mats_bs ? B : 1;
+}
+
+// Index of the matrix set of codec row `row` of batch item b (indices
+// clamped), in units of one set (4 sub-frames x 16 entries).
+__device__ __forceinline__ int64_t camera_set(const CameraDev& c, int b, int64_t row) {
+    const int64_t f = min(max(row / c.tokens_per_frame, (int64_t)0), c.n_frames - 1);
+    const int m = min(max(c.frame_mat[f], 0), c.n_mats - 1);
+    return (c.mats_bs ? (int64_t)b * c.n_mats : 0) + m;
+}
 
 // Sub-frame matrices of codec row `row` of batch item b (indices clamped).
 __device__ __forceinline__ const float* camera_mats(const CameraDev& c, int b, int64_t row) {
@@ -35,24 +51,36 @@ __device__ __forceinline__ const float* camera_mats(const CameraDev& c, int b, i
 
 // y = bf16(M . x) for one 4-vector, M row-major 4x4 (fp32, used as bf16).
 __device__ __forceinline__ void camera_vec4(const float* M, const float (&x)[4], float (&y)[4]) {
+#pragma clang fp contract(off)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         double acc = 0.0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc += (double)(bf16_round(M[4 * i + j]) * x[j]);
-        y[i] = bf16_round((float)acc);
+        y[i] = bf16_round(f64_to_f32(acc));
     }
+}
+
+// Output r of camera_vec4: bf16(M[r] . x), M row-major 4x4 (fp32, used as
+// bf16).
+__device__ __forceinline__ float camera_vec4_row(const float* M, int r, const float (&x)[4]) {
+#pragma clang fp contract(off)
+    double acc = 0.0;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc += (double)(bf16_round(M[4 * r + j]) * x[j]);
+    return bf16_round(f64_to_f32(acc));
 }
 
 // y = bf16(m . x) for one 4-vector, m row-major 4x4 already rounded to bf16.
 __device__ __forceinline__ void camera_vec4_rounded(const float (&m)[16], const float (&x)[4],
                                                     float (&y)[4]) {
+#pragma clang fp contract(off)
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
         double acc = 0.0;
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc += (double)(m[4 * i + j] * x[j]);
-        y[i] = bf16_round((float)acc);
+        y[i] = bf16_round(f64_to_f32(acc));
     }
 }
 
@@ -150,5 +178,10 @@ __device__ __forceinline__ void camera_row_blocks(const float* M, const int32_t*
 // Host: validate an nkv_camera for heads of D dims and a call over B batch
 // items, and fill dev (blocks stays null).
 int camera_from_abi(const nkv_camera* c, int D, int B, CameraDev* dev);
+
+// Host: x [B, S, H, D] bf16 times the camera in place (row s at codec row s),
+// as nkv_camera_apply.
+int camera_apply_inplace(hipStream_t s, const CameraDev& cam, int B, int64_t S, int H, int D,
+                         uint16_t* x, int64_t sb, int64_t st, int64_t sh);
 
 }  // namespace nkv

@@ -83,6 +83,35 @@ __global__ void __launch_bounds__(256) camera_apply_kernel(CameraApplyParams p) 
 
 using namespace nkv;
 
+namespace nkv {
+
+int camera_apply_inplace(hipStream_t s, const CameraDev& cam, int B, int64_t S, int H, int D,
+                         uint16_t* x, int64_t sb, int64_t st, int64_t sh) {
+    if ((int64_t)B * S * H == 0) return NKV_OK;
+    CameraApplyParams p;
+    p.cam = cam;
+    p.B = B;
+    p.H = H;
+    p.D = D;
+    p.S = S;
+    p.x = x;
+    p.x_sb = sb;
+    p.x_st = st;
+    p.x_sh = sh;
+    p.rows = nullptr;
+    p.out = x;
+    p.o_sb = sb;
+    p.o_st = st;
+    p.o_sh = sh;
+    const int64_t items = (int64_t)B * S * H * camera_vectors(cam.layout, D);
+    const unsigned grid = (unsigned)std::min<int64_t>(cdiv(items, 256), 65536);
+    camera_apply_kernel<<<grid, 256, 0, s>>>(p);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+}  // namespace nkv
+
 extern "C" int nkv_camera_apply(void* stream, const nkv_camera* camera, int B, int64_t S, int H,
                                 int D, const uint16_t* x, int64_t x_sb, int64_t x_st,
                                 int64_t x_sh, const int32_t* rows, uint16_t* out, int64_t o_sb,

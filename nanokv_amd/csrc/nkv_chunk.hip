@@ -2,15 +2,16 @@
 // (NKV_SCHEDULE_KEY_CHUNKS).
 //
 // Two schedules live here; both decode every history key once per head.
-//  - The staged schedule (the drtile / stage8 decode, flash8_kernel and
-//    staged_combine_kernel, further below) serves every call at K/Q width
-//    128 and the reader widths 32/64 without the camera: the decode writes
-//    each 128-key tile once into the call's workspace, in the flash kernel's
-//    LDS layout, and the flash kernel streams the tiles back with O held in
-//    registers over a whole key split.
+//  - The staged schedule (the drtile / stage8 decode, tile_xform_kernel,
+//    flash8_kernel and staged_combine_kernel, further below) serves every
+//    call at K/Q width 128 and the reader widths 32/64 with ranks up to the
+//    resident decoder's 384: the decode writes each 128-key tile once into
+//    the call's workspace, in the flash kernel's LDS layout, and the flash
+//    kernel streams the tiles back with O held in registers over a whole
+//    key split.
 //  - The key-chunk kernel (chunk8_kernel, next) serves reader widths 32/64
-//    with the camera, or with ranks above the resident decoder's 384: the
-//    decoded K/V stay in LDS, and each (chunk, query block) leaves a partial.
+//    with ranks above 384: the decoded K/V stay in LDS, and each (chunk,
+//    query block) leaves a partial.
 //
 // Key-chunk kernel: a 512-thread block (8 waves, two per SIMD) owns one (batch, head, chunk)
 // of 256 keys.  It decodes the chunk's K and V once into LDS -- K[key][d]
@@ -125,8 +126,8 @@ struct ChunkParams {
 // and K/Q width.  Blocks [seg_first[s], seg_first[s + 1]) run segment s: work
 // seg_kind[s] of partition seg_part[s] (seg_ranges[s]: tile ranges per head
 // of a decode segment).
-constexpr int MP_SEGS = 3 * NKV_MAX_PARTS;
-enum : int { SEG_K = 0, SEG_V = 1, SEG_CUR = 2, SEG_FLASH = 3 };
+constexpr int MP_SEGS = 4 * NKV_MAX_PARTS;
+enum : int { SEG_K = 0, SEG_V = 1, SEG_CUR = 2, SEG_FLASH = 3, SEG_XFORM = 4, SEG_TABLE = 5 };
 struct MultiParams {
     ChunkParams part[NKV_MAX_PARTS];
     int dk[NKV_MAX_PARTS];
@@ -344,7 +345,8 @@ __device__ __forceinline__ void rope_k_rows(uint16_t* ktile, const ChunkParams& 
 #pragma unroll
     for (int e = 0; e < HP; ++e) {
         const int pj = pmap ? pmap[e] : HP * hf + e;
-        cs[e] = *reinterpret_cast<const double2*>(rope_entry(p.rope, rr, pj));
+        const f64x2 v = ldg(reinterpret_cast<const f64x2*>(rope_entry(p.rope, rr, pj)));
+        cs[e] = double2{v.x, v.y};
     }
 #pragma unroll
     for (int q = 0; q < HP / 4; ++q) {
@@ -1085,25 +1087,12 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
     // columns 32 dt + 8 g + 4 hf .. +4 of this lane's key; V, column
     // d = 32 dt + l32 of keys 32 kq + 8 g + 4 hf + e
     constexpr int NCV = CODEC == 0 ? 8 * NDT : 64;
-    // K with read-time RoPE: the lane's own key at columns 32 dt + 8 g + 4 hf
-    // .. +4 (added before the rotation, in the accumulator layout).  K
-    // otherwise: row (lane >> 2) + 16 i of the wave's 32 keys at columns
-    // 32 dt + 8 (lane & 3) .. +8 (added when the staged rows are flushed), so
-    // that each load reads 16 rows x 64 contiguous bytes rather than 32 rows
-    // x 16 bytes.
-    const bool rope = CODEC == 0 && rope_on(p.rope);
+    // K: row (lane >> 2) + 16 i of the wave's 32 keys at columns 32 dt +
+    // 8 (lane & 3) .. +8 (added when the staged rows are flushed), so that
+    // each load reads 16 rows x 64 contiguous bytes rather than 32 rows x 16
+    // bytes.
     auto load_centers = [&](uint32_t (&cv)[NCV], const uint16_t* const* crow) {
-        if (CODEC == 0 && rope) {
-            const uint16_t* cr = crow[key];
-#pragma unroll
-            for (int dt = 0; dt < NDT; ++dt)
-#pragma unroll
-                for (int g = 0; g < 4; ++g) {
-                    const u32x2 v = ldg(reinterpret_cast<const u32x2*>(cr + 32 * dt + 8 * g + 4 * hf));
-                    cv[2 * (4 * dt + g)] = v[0];
-                    cv[2 * (4 * dt + g) + 1] = v[1];
-                }
-        } else if (CODEC == 0) {
+        if (CODEC == 0) {
 #pragma unroll
             for (int i = 0; i < 2; ++i) {
                 const uint16_t* cr = crow[32 * kq + (lane >> 2) + 16 * i];
@@ -1192,7 +1181,7 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                     const u32x4 x = *reinterpret_cast<const u32x4*>(st + r * DR_SROW + 8 * c);
                     uint16_t* dst = CODEC == 0 ? img + (32 * kq + r) * DK + 32 * dt + 8 * c
                                                : img + (32 * dt + r) * FT_ROW + 32 * kq + 8 * c;
-                    if (CODEC == 0 && cent && !rope) {
+                    if (CODEC == 0 && cent) {
                         // K = bf16(bf16(acc + bias) + center) (MG:438-454)
                         u32x4 y;
 #pragma unroll
@@ -1211,29 +1200,10 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
             if (CODEC == 0) {
                 // acc[dt] element i: d = 32 dt + 8 (i/4) + 4 hf + i%4 of this
                 // lane's key; K = bf16(bf16(acc + bias) + center), the center
-                // added in flush() from coalesced rows unless RoPE applies;
-                // with read-time RoPE each bf16 pair (d, d + 1) rotated by its
-                // pair's (cos, sin) at the key's codec row (rope_pair: fp64,
-                // as rope_apply); a narrower reader's pair j is the original
-                // pair p.rope.pairs[h][j]
-                RopeRows rr{};
-                const int32_t* pmap = nullptr;
-                if (rope) {
-                    rr = rope_rows(p.rope, key_row(tile, key));
-                    if (p.rope.pairs) pmap = p.rope.pairs + (int64_t)h * (DK / 2);
-                }
+                // added in flush() from coalesced rows (read-time RoPE and the
+                // camera follow in tile_xform_kernel)
 #pragma unroll
                 for (int dt = 0; dt < NDT; ++dt) {
-                    // the slice's 8 pairs of this lane: 16 dt + 4 g + 2 hf + {0, 1}
-                    double2 cs[8];
-                    if (rope) {
-#pragma unroll
-                        for (int x = 0; x < 8; ++x) {
-                            const int pj = 16 * dt + 4 * (x >> 1) + 2 * hf + (x & 1);
-                            cs[x] = *reinterpret_cast<const double2*>(
-                                rope_entry(p.rope, rr, pmap ? ldg(pmap + pj) : pj));
-                        }
-                    }
 #pragma unroll
                     for (int g = 0; g < 4; ++g) {
                         const int d = 32 * dt + 8 * g + 4 * hf;
@@ -1241,21 +1211,8 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
                         float a[4];
 #pragma unroll
                         for (int e = 0; e < 4; ++e) a[e] = acc[dt][4 * g + e] + bs[e];
-                        if (cent && rope) {
-#pragma unroll
-                            for (int e = 0; e < 4; ++e) a[e] = bf16_round(a[e]);
-                            const uint32_t c0 = cv[2 * (4 * dt + g)], c1 = cv[2 * (4 * dt + g) + 1];
-                            a[0] += __uint_as_float(c0 << 16);
-                            a[1] += __uint_as_float(c0 & 0xffff0000u);
-                            a[2] += __uint_as_float(c1 << 16);
-                            a[3] += __uint_as_float(c1 & 0xffff0000u);
-                        }
-                        uint32_t w0 = pack_bf16x2(a[0], a[1]), w1 = pack_bf16x2(a[2], a[3]);
-                        if (rope) {
-                            w0 = rope_pair(w0, cs[2 * g].x, cs[2 * g].y);
-                            w1 = rope_pair(w1, cs[2 * g + 1].x, cs[2 * g + 1].y);
-                        }
-                        *reinterpret_cast<u32x2*>(st + l32 * DR_SROW + 8 * g + 4 * hf) = u32x2{w0, w1};
+                        *reinterpret_cast<u32x2*>(st + l32 * DR_SROW + 8 * g + 4 * hf) =
+                            u32x2{pack_bf16x2(a[0], a[1]), pack_bf16x2(a[2], a[3])};
                     }
                     flush(dt);
                 }
@@ -1289,6 +1246,15 @@ __device__ __forceinline__ void drtile_range(DResSmem& sm, const ChunkParams& p,
     }
 }
 
+// Entry i of a camera's fp64 matrix table (the tile pass reads it): entry e
+// of set s is bf16(mats[batch][m][e]), s = batch * n_mats + m.
+__device__ __forceinline__ void camera_table_entry(const CameraDev& c, int batches, int64_t i) {
+    const int64_t per = (int64_t)c.n_mats * 64;
+    if (i >= batches * per) return;
+    const int64_t b = i / per, r = i - b * per;
+    const_cast<double*>(c.m64)[i] = (double)bf16_round(ldg(c.mats + b * c.mats_bs + r));
+}
+
 // Blocks of a decode segment: b*h fastest -- with B*H a multiple of 8 every
 // range of one head's codec runs on one XCD (blockIdx % 8) and shares its
 // decoder rows in L2 -- then its seg_ranges tile ranges.  A current-key
@@ -1306,6 +1272,10 @@ __global__ void __launch_bounds__(DR_THREADS, 1) drtile_kernel(MultiParams P) {
     const int64_t local = (int64_t)blockIdx.x - P.seg_first[sg];
     const int BH = p.B * p.H;
     const int bh = (int)(local % BH), rg = (int)(local / BH);
+    if (kind == SEG_TABLE) {
+        camera_table_entry(p.cam, camera_batches(p.cam, p.B), local * DR_THREADS + threadIdx.x);
+        return;
+    }
     if (kind == SEG_CUR) {
         CTileSmem* ct = reinterpret_cast<CTileSmem*>(smem_raw);
         const int half = threadIdx.x / CT_THREADS, c = 2 * rg + half;
@@ -1326,6 +1296,197 @@ __global__ void __launch_bounds__(DR_THREADS, 1) drtile_kernel(MultiParams P) {
         else if (dk == 64) drtile_range<1, KQ, 64>(sm, p, bh, ta, tb, wave, lane);
         else drtile_range<1, KQ, 128>(sm, p, bh, ta, tb, wave, lane);
     }
+}
+
+// ---------------------------------------- read-time transforms of the tiles
+// Read-time RoPE and the camera's FULL layout are applied to the decode
+// GEMM's history tiles in place, after the decode launch and before the flash
+// launch (drtile_kernel's epilogue has no registers to spare for them): one
+// block of TX_THREADS threads per history tile.  The block first issues its
+// first tile loads, then resolves each key's tables once into LDS (its RoPE
+// band rows and its camera matrix set), then transforms the tile in groups
+// of TX_GROUP words per thread.  K: each 32-bit word is one pair of a key
+// row; RoPE rotates pair pp (or, for a reader key, its original pair
+// rope.pairs[h][pp], rope_selected CN/core.py:75-91) at the key's codec row
+// (rope_k_rows' arithmetic).  The camera multiplies the two 4-vectors of
+// each 8-dim block j of a key -- the block's even and odd dims, i.e. the low
+// and high halves of its four pair words, which sit in one quad of lanes --
+// by sub-frame j % 4 of P^-1 (a 128-wide key and every value: the FULL
+// layout, prope_attention.py:120-176) or cam.blocks[h][j] (a reader key,
+// camera_selected CN/core.py:110-137); lane w of the quad computes output w
+// of both.  V^T: a lane holds two key columns of the 8 rows of block j.
+// This is the arithmetic of the key-chunk kernel's camera passes
+// (camera_k_rows and the V^T pass of decode_codec8) on the same bf16
+// values, so both schedules write bit-identical K and V.
+constexpr int TX_THREADS = 256;
+constexpr int TX_GROUP = 8;  // K words of a thread in flight at once
+struct TXformSmem {
+    const double* band[3][FT_T];  // RoPE: the t, h and w band rows of each key's codec row
+    const double* mats[FT_T];     // camera: each key's sub-frame matrices in the fp64 table
+};
+
+// m_row . x for one row of a matrix of the fp64 table (entries rounded to
+// bf16) and a 4-vector x of bf16 values: camera_vec4's sum, in order, in
+// fp64.  Every product of two bf16 values is exact in fp64, so a fused
+// multiply-add rounds exactly as the sum of the product does.
+__device__ __forceinline__ float camera_dot64(const double* m_row, const float (&x)[4]) {
+    const f64x2 a = ldg(reinterpret_cast<const f64x2*>(m_row));
+    const f64x2 c = ldg(reinterpret_cast<const f64x2*>(m_row) + 1);
+    double acc = a.x * (double)x[0];
+    acc = __builtin_fma(a.y, (double)x[1], acc);
+    acc = __builtin_fma(c.x, (double)x[2], acc);
+    acc = __builtin_fma(c.y, (double)x[3], acc);
+    return bf16_round(f64_to_f32(acc));
+}
+
+// Lane q of every quad (lanes 4 a .. 4 a + 4) receives v of lane 4 a + Q.
+template <int Q>
+__device__ __forceinline__ uint32_t quad_bcast(uint32_t v) {
+    return (uint32_t)__builtin_amdgcn_mov_dpp((int)v, Q * 0x55, 0xf, 0xf, false);
+}
+
+template <int DK>
+__device__ __forceinline__ void tile_xform(TXformSmem& sm, const ChunkParams& p, int bh, int tile,
+                                           int t) {
+    using TF = TileFmt<DK>;
+    constexpr int PPR = DK / 2;            // pair words per K row
+    constexpr int RPI = TX_THREADS / PPR;  // K rows per pass of the block
+    constexpr int KU = FT_T / RPI;         // K words per thread
+    static_assert(KU % TX_GROUP == 0, "whole groups of K words");
+    const int b = bh / p.H, h = bh % p.H;
+    const int64_t tok0 = (int64_t)tile * FT_T;
+    const int valid = (int)min((int64_t)FT_T, p.n_rows - tok0);
+    const bool rope = rope_on(p.rope), cam = p.cam.mats != nullptr;
+    // a reader key without a block map keeps its values under the camera,
+    // as in camera_k_rows
+    const int32_t* blocks = p.cam.blocks ? p.cam.blocks + (int64_t)h * (DK / 8) : nullptr;
+    const bool kcam = cam && (blocks || DK == CK_D);
+    uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + tile) * TF::TILE;
+    // K: thread t takes pair pp of key rows t / PPR + RPI i (a wave reads
+    // whole rows); keys past the last row keep their K
+    const int pp = t % PPR, r0 = t / PPR;
+    uint32_t* kw = reinterpret_cast<uint32_t*>(img) + pp;
+    auto load_group = [&](int g, uint32_t (&kx)[TX_GROUP]) {
+#pragma unroll
+        for (int i = 0; i < TX_GROUP; ++i) {
+            const int k = r0 + RPI * (g + i);
+            kx[i] = k < valid ? kw[k * PPR] : 0u;
+        }
+    };
+    uint32_t kx[TX_GROUP];
+    if (rope || kcam) load_group(0, kx);
+    // each key's tables, once (keys past the last row take key 0's)
+    if (t < FT_T) {
+        const int64_t row = history_row(p, tok0 + (t < valid ? t : 0));
+        if (rope) {
+            const RopeRows rr = rope_rows(p.rope, row);
+            sm.band[0][t] = rr.t;
+            sm.band[1][t] = rr.h;
+            sm.band[2][t] = rr.w;
+        }
+        if (cam) sm.mats[t] = p.cam.m64 + 64 * camera_set(p.cam, b, row);
+    }
+    __syncthreads();
+    if (rope || kcam) {
+        // this lane's pair: its RoPE band and entry, its block and sub-frame
+        int band = 0, off = 0;
+        if (rope) {
+            int pj = p.rope.pairs ? ldg(p.rope.pairs + (int64_t)h * PPR + pp) : pp;
+            pj = min(max(pj, 0), p.rope.pt + p.rope.ph + p.rope.pw - 1);
+            band = pj < p.rope.pt ? 0 : (pj < p.rope.pt + p.rope.ph ? 1 : 2);
+            off = 2 * (pj - (band == 0 ? 0 : band == 1 ? p.rope.pt : p.rope.pt + p.rope.ph));
+        }
+        const int j = pp >> 2, w = pp & 3;
+        const int sub = kcam ? (blocks ? ldg(blocks + j) & 3 : j & 3) : 0;
+        for (int g = 0; g < KU; g += TX_GROUP) {
+            if (g > 0) load_group(g, kx);
+            if (rope) {
+                // global loads (generic pointers from LDS would make flat
+                // loads, which wait with the LDS reads)
+                f64x2 cs[TX_GROUP];
+#pragma unroll
+                for (int i = 0; i < TX_GROUP; ++i) {
+                    const int k = min(r0 + RPI * (g + i), valid - 1);
+                    cs[i] = ldg(reinterpret_cast<const f64x2*>(sm.band[band][k] + off));
+                }
+#pragma unroll
+                for (int i = 0; i < TX_GROUP; ++i) kx[i] = rope_pair(kx[i], cs[i].x, cs[i].y);
+            }
+            if (kcam) {
+#pragma unroll
+                for (int i = 0; i < TX_GROUP; ++i) {
+                    const int k = min(r0 + RPI * (g + i), valid - 1);
+                    const uint32_t q0 = quad_bcast<0>(kx[i]), q1 = quad_bcast<1>(kx[i]);
+                    const uint32_t q2 = quad_bcast<2>(kx[i]), q3 = quad_bcast<3>(kx[i]);
+                    const float x0[4] = {__uint_as_float(q0 << 16), __uint_as_float(q1 << 16),
+                                         __uint_as_float(q2 << 16), __uint_as_float(q3 << 16)};
+                    const float x1[4] = {__uint_as_float(q0 & 0xffff0000u),
+                                         __uint_as_float(q1 & 0xffff0000u),
+                                         __uint_as_float(q2 & 0xffff0000u),
+                                         __uint_as_float(q3 & 0xffff0000u)};
+                    const double* mr = sm.mats[k] + 16 * sub + 4 * w;
+                    kx[i] = pack_bf16x2(camera_dot64(mr, x0), camera_dot64(mr, x1));
+                }
+            }
+#pragma unroll
+            for (int i = 0; i < TX_GROUP; ++i) {
+                const int k = r0 + RPI * (g + i);
+                if (k < valid) kw[k * PPR] = kx[i];
+            }
+        }
+    }
+    if (cam) {
+        // wave v takes blocks j = 4 v .. 4 v + 4 (sub-frames 0 .. 3) of V^T:
+        // rows 8 j .. 8 j + 8 at key columns 2 lane, 2 lane + 1; the finite
+        // columns of keys past the last row are never attended
+        const int lane = t & 63, v = t >> 6;
+        uint32_t* vw = reinterpret_cast<uint32_t*>(img + TF::K_IMG) + lane;
+        const double* mk[2];
+#pragma unroll
+        for (int c = 0; c < 2; ++c) mk[c] = sm.mats[vt_col(2 * lane + c)];
+#pragma unroll 1
+        for (int jj = 0; jj < 4; ++jj) {
+            const int j = 4 * v + jj;
+            uint32_t vx[8];
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vx[e] = vw[(8 * j + e) * (FT_ROW / 2)];
+#pragma unroll
+            for (int c = 0; c < 2; ++c) {
+                const int sh = 16 * c;
+                float x0[4], x1[4];
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    x0[i] = __uint_as_float(((vx[2 * i] >> sh) & 0xffffu) << 16);
+                    x1[i] = __uint_as_float(((vx[2 * i + 1] >> sh) & 0xffffu) << 16);
+                }
+                const uint32_t keep = ~(0xffffu << sh);
+#pragma unroll
+                for (int i = 0; i < 4; ++i) {
+                    const double* mrow = mk[c] + 16 * jj + 4 * i;
+                    const float y0 = camera_dot64(mrow, x0), y1 = camera_dot64(mrow, x1);
+                    vx[2 * i] = (vx[2 * i] & keep) | ((uint32_t)f32_to_bf16_bits(y0) << sh);
+                    vx[2 * i + 1] = (vx[2 * i + 1] & keep) | ((uint32_t)f32_to_bf16_bits(y1) << sh);
+                }
+            }
+#pragma unroll
+            for (int e = 0; e < 8; ++e) vw[(8 * j + e) * (FT_ROW / 2)] = vx[e];
+        }
+    }
+}
+
+// Blocks of a transform segment: the partition's history tiles, tile
+// fastest within each b*h.
+__global__ void __launch_bounds__(TX_THREADS) tile_xform_kernel(MultiParams P) {
+    __shared__ TXformSmem sm;
+    const int sg = multi_segment(P, blockIdx.x);
+    const int pi = P.seg_part[sg];
+    const ChunkParams& p = P.part[pi];
+    const int64_t local = (int64_t)blockIdx.x - P.seg_first[sg];
+    const int T = (int)cdiv(p.n_rows, FT_T);
+    const int bh = (int)(local / T), tile = (int)(local % T);
+    if (P.dk[pi] == 32) tile_xform<32>(sm, p, bh, tile, threadIdx.x);
+    else if (P.dk[pi] == 64) tile_xform<64>(sm, p, bh, tile, threadIdx.x);
+    else tile_xform<CK_D>(sm, p, bh, tile, threadIdx.x);
 }
 
 // The two tile buffers as [K0][K1][V0][V1]: a buffer's images sit one
@@ -1673,15 +1834,32 @@ __device__ __forceinline__ void combine_partials(CombineAcc& A, const uint16_t* 
 
 // Normalise and store this wave's half of query qi of (b, h): out = (acc +
 // shift * Lx) / L in bf16 (shift: the row of 128 values added to the
-// tracked source's output, or null); half 0 also writes lse = ln(sum) when
-// lse is given.
+// tracked source's output, or null), then, with ocam, bf16(P . out) for P
+// of query row qi in the FULL layout (nkv_camera_apply's arithmetic); half
+// 0 also writes lse = ln(sum) when lse is given.  With ocam both lanes of a
+// query (lane and lane ^ 32, which hold the two halves of every 8-dim
+// block) must reach this call.
 __device__ __forceinline__ void combine_store(const CombineAcc& A, uint16_t* out, int64_t o_sb,
                                               int64_t o_st, int64_t o_sh, float* lse, int64_t Q,
                                               int H, int b, int h, int64_t qi, int half, int lane,
-                                              const float* shift) {
+                                              const float* shift, const CameraDev* ocam = nullptr) {
     const int hf = lane >> 5;
     const float inv = A.L > 0.0f ? 1.0f / A.L : 0.0f;
     uint16_t* orow = out + b * o_sb + qi * o_st + h * o_sh + 4 * hf;
+    // with ocam: rows 2 hf and 2 hf + 1 of P's four sub-frames for query qi,
+    // rounded to bf16 once
+    float pm[4][2][4];
+    if (ocam) {
+        const float* M = camera_mats(*ocam, b, qi);
+#pragma unroll
+        for (int c = 0; c < 4; ++c)
+#pragma unroll
+            for (int r = 0; r < 2; ++r) {
+                const f32x4 m = ldg(reinterpret_cast<const f32x4*>(M + 16 * c + 4 * (2 * hf + r)));
+#pragma unroll
+                for (int e = 0; e < 4; ++e) pm[c][r][e] = bf16_round(m[e]);
+            }
+    }
     // acc[8*st + 2*e + {0,1}] (payload row st0 + st, st0 = CB_ROWS * half)
     // = o[db = st/2][i = 8*(st&1) + 2*e + {0,1}] with d = 32*db + 8*(i/4) +
     // 4*hf + i%4: acc[4n .. 4n+3] are four consecutive d of this lane's query
@@ -1697,7 +1875,33 @@ __device__ __forceinline__ void combine_store(const CombineAcc& A, uint16_t* out
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = fmaf(shift[d + 4 * hf + e], A.Lx, v[e]);
         }
-        const u32x2 pk = {pack_bf16x2(v[0] * inv, v[1] * inv), pack_bf16x2(v[2] * inv, v[3] * inv)};
+        u32x2 pk = {pack_bf16x2(v[0] * inv, v[1] * inv), pack_bf16x2(v[2] * inv, v[3] * inv)};
+        if (ocam) {
+            // block d / 8: this lane holds dims 4 hf .. 4 hf + 4, lane ^ 32 the
+            // other four; its 4-vectors are the block's even and odd dims,
+            // and this lane forms outputs 2 hf, 2 hf + 1 of each
+            const uint32_t o0 = __shfl_xor(pk[0], 32), o1 = __shfl_xor(pk[1], 32);
+            const uint32_t lo0 = hf ? o0 : pk[0], lo1 = hf ? o1 : pk[1];
+            const uint32_t hi0 = hf ? pk[0] : o0, hi1 = hf ? pk[1] : o1;
+            const float x0[4] = {__uint_as_float(lo0 << 16), __uint_as_float(lo1 << 16),
+                                 __uint_as_float(hi0 << 16), __uint_as_float(hi1 << 16)};
+            const float x1[4] = {__uint_as_float(lo0 & 0xffff0000u), __uint_as_float(lo1 & 0xffff0000u),
+                                 __uint_as_float(hi0 & 0xffff0000u), __uint_as_float(hi1 & 0xffff0000u)};
+            const int c = (d >> 3) & 3;
+            float y[2][2];
+#pragma unroll
+            for (int r = 0; r < 2; ++r)
+#pragma unroll
+                for (int v = 0; v < 2; ++v) {
+                    // camera_vec4's sum for one output, the products exact
+#pragma clang fp contract(off)
+                    double acc = 0.0;
+#pragma unroll
+                    for (int e = 0; e < 4; ++e) acc += (double)(pm[c][r][e] * (v ? x1[e] : x0[e]));
+                    y[r][v] = bf16_round(f64_to_f32(acc));
+                }
+            pk = {pack_bf16x2(y[0][0], y[0][1]), pack_bf16x2(y[1][0], y[1][1])};
+        }
         *reinterpret_cast<u32x2*>(orow + d) = pk;
     }
     if (lse && hf == 0 && half == 0)
@@ -1739,7 +1943,8 @@ __global__ void __launch_bounds__(64 * CB_WAVES) chunk_combine_kernel(ChunkParam
 // correction) before the merge.
 __global__ void __launch_bounds__(64 * CB_WAVES) staged_combine_kernel(MultiParams P,
                                                                        const float* shift,
-                                                                       int64_t sh_sb, int64_t sh_sh) {
+                                                                       int64_t sh_sb, int64_t sh_sh,
+                                                                       CameraDev ocam) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const ChunkParams& n = P.part[0];
@@ -1769,7 +1974,8 @@ __global__ void __launch_bounds__(64 * CB_WAVES) staged_combine_kernel(MultiPara
     const int64_t qi = (int64_t)qblk * 32 + (lane & 31);
     if (qi >= n.Q) return;
     combine_store(A, n.out, n.o_sb, n.o_st, n.o_sh, n.lse, n.Q, n.H, b, h, qi, half, lane,
-                  lp && shift ? shift + (int64_t)b * sh_sb + (int64_t)h * sh_sh : nullptr);
+                  lp && shift ? shift + (int64_t)b * sh_sb + (int64_t)h * sh_sh : nullptr,
+                  ocam.mats ? &ocam : nullptr);
 }
 
 // ------------------------------------------------------------------ host
@@ -1893,8 +2099,8 @@ constexpr int FT_CUS = 256;          // compute units of an MI355X
 // 0.571 ms, over 12,480 keys 0.161 vs 0.177 ms; 6 blocks 0.590 vs 0.660 and
 // 0.174 vs 0.202 ms; 12 blocks 0.747 vs 0.837 and 0.224 vs 0.254 ms; cfg2 (25
 // blocks) 0.950 vs 1.067 ms.  The key-chunk kernel remains for reader widths
-// 32/64 with the camera, or with ranks above 384 (read-time RoPE alone is
-// staged: drtile_kernel rotates in its K epilogue).
+// 32/64 with ranks above 384 (read-time RoPE and the FULL camera layout are
+// tile_xform_kernel's pass over the decoded tiles).
 constexpr int FT_MIN_QBLOCKS = 1;
 
 struct FlashPlan {
@@ -1913,19 +2119,20 @@ FlashPlan flash_shape(const ChunkLaunchDesc& d) {
     return f;
 }
 
-// Reader widths below 128 are staged only by the decode GEMM (no camera:
-// stage8_kernel decodes at full width).
-bool use_staged(const ChunkLaunchDesc& d) {
-    const bool width = d.dk == CK_D || ((d.dk == 32 || d.dk == 64) && !d.cam.mats &&
-                                        d.key.r <= 64 * DR_MAXQ && d.value.r <= 64 * DR_MAXQ);
-    return width && cdiv(d.Q, 32) >= FT_MIN_QBLOCKS && d.n_rows + d.Nc > 0;
+// History tiles from the decode GEMM with the decoder held in LDS (the
+// current tiles copied in the same launch; read-time RoPE and the camera's
+// FULL layout applied by tile_xform_kernel); with the SF13 camera layout, or
+// ranks above what LDS holds, both from stage8_kernel's decode.
+bool staged_gemm(const ChunkLaunchDesc& d) {
+    return (!d.cam.mats || d.cam.layout == NKV_CAMERA_FULL) && d.key.r <= 64 * DR_MAXQ &&
+           d.value.r <= 64 * DR_MAXQ;
 }
 
-// History tiles from the decode GEMM with the decoder held in LDS (read-time
-// RoPE in its epilogue, the current tiles copied in the same launch); with
-// the camera, or ranks above what LDS holds, both from stage8_kernel's decode.
-bool staged_gemm(const ChunkLaunchDesc& d) {
-    return !d.cam.mats && d.key.r <= 64 * DR_MAXQ && d.value.r <= 64 * DR_MAXQ;
+// Reader widths below 128 are staged only by the decode GEMM (stage8_kernel
+// decodes at full width).
+bool use_staged(const ChunkLaunchDesc& d) {
+    const bool width = d.dk == CK_D || ((d.dk == 32 || d.dk == 64) && staged_gemm(d));
+    return width && cdiv(d.Q, 32) >= FT_MIN_QBLOCKS && d.n_rows + d.Nc > 0;
 }
 
 // Cost model of the staged kernels for planning their grids, in units of one
@@ -1975,10 +2182,20 @@ struct MultiPlan {
     int n;
     FlashPlan f[NKV_MAX_PARTS];
     int ranges[NKV_MAX_PARTS][2];  // decode tile ranges per head of K and V (0: none)
-    size_t tiles_off[NKV_MAX_PARTS], part_off[NKV_MAX_PARTS], total;
+    size_t tiles_off[NKV_MAX_PARTS], part_off[NKV_MAX_PARTS];
+    // each camera partition's fp64 matrix table (after every tile and
+    // partial area, which end at areas_end)
+    size_t cam_off[NKV_MAX_PARTS], areas_end, total;
 };
 
 size_t align256(size_t n) { return (n + 255) / 256 * 256; }
+
+// Bytes of a partition's fp64 camera table: the staged decode GEMM's tile
+// pass reads the matrices from it (0: no camera on that path).
+int64_t cam_table_bytes(const ChunkLaunchDesc& d) {
+    if (!d.cam.mats || !staged_gemm(d)) return 0;
+    return (int64_t)camera_batches(d.cam, d.B) * d.cam.n_mats * 64 * (int64_t)sizeof(double);
+}
 
 // Key splits: every split count of every partition gives a candidate block
 // cost; each candidate gives each partition the fewest splits whose blocks
@@ -2111,7 +2328,7 @@ bool plan_extents_ok(const MultiPlan& P, const ChunkLaunchDesc* d, int n, int v_
             return fail("current tiles at a width other than 128", tiles_end, tiles_end);
         const size_t rows = bh * f.splits * cdiv(d[i].Q, 32) * 32;
         const size_t part_end = P.part_off[i] + rows * PARTIAL_ROW_BYTES;
-        const size_t lim = i + 1 < n ? P.tiles_off[i + 1] : P.total;
+        const size_t lim = i + 1 < n ? P.tiles_off[i + 1] : P.areas_end;
         if (part_end > lim) return fail("the split partials", part_end, lim);
     }
     return true;
@@ -2123,7 +2340,7 @@ MultiPlan multi_plan(const ChunkLaunchDesc* d, int n) {
     std::vector<int64_t> key{n};
     for (int i = 0; i < n; ++i)
         for (int64_t v : {(int64_t)d[i].B, (int64_t)d[i].H, (int64_t)d[i].dk, d[i].Q, d[i].n_rows,
-                          d[i].Nc, (int64_t)staged_gemm(d[i])})
+                          d[i].Nc, (int64_t)staged_gemm(d[i]), cam_table_bytes(d[i])})
             key.push_back(v);
     thread_local std::vector<int64_t> last_key;
     thread_local MultiPlan last;
@@ -2139,6 +2356,11 @@ MultiPlan multi_plan(const ChunkLaunchDesc* d, int n) {
         off += align256((size_t)d[i].B * d[i].H * f.ntiles * tile_elems(d[i].dk) * sizeof(uint16_t));
         P.part_off[i] = off;
         off += align256((size_t)d[i].B * d[i].H * f.splits * cdiv(d[i].Q, 32) * 32 * PARTIAL_ROW_BYTES);
+    }
+    P.areas_end = off;
+    for (int i = 0; i < n; ++i) {
+        P.cam_off[i] = off;
+        off += align256((size_t)cam_table_bytes(d[i]));
     }
     P.total = off;
     last_key = key;
@@ -2194,7 +2416,7 @@ int64_t seg_blocks(const MultiParams& M) { return M.seg_first[M.nseg]; }
 // partition i but the staged fields.
 int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, int n,
                const int32_t* const* heads, const float* shift, int64_t sh_sb, int64_t sh_sh,
-               void* workspace) {
+               void* workspace, const CameraDev& ocam = CameraDev{}) {
     const MultiPlan P = multi_plan(d, n);
     {
         std::string why;
@@ -2227,10 +2449,26 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
         M.heads[i] = heads ? heads[i] : nullptr;
     }
     int rc = NKV_OK;
+    // the fp64 matrix table of each camera of the tile pass, once per
+    // distinct camera (filled by the decode launch, table[i] set)
+    bool table[NKV_MAX_PARTS] = {};
+    for (int i = 0; i < n; ++i) {
+        if (!cam_table_bytes(d[i])) continue;
+        CameraDev& c = M.part[i].cam;
+        for (int k = 0; k < i && !c.m64; ++k) {
+            const CameraDev& o = M.part[k].cam;
+            if (o.m64 && o.mats == c.mats && o.mats_bs == c.mats_bs && o.n_mats == c.n_mats &&
+                d[k].B == d[i].B)
+                c.m64 = o.m64;
+        }
+        if (c.m64) continue;
+        c.m64 = reinterpret_cast<const double*>(ws + P.cam_off[i]);
+        table[i] = true;
+    }
     if (!staged_gemm(d[0])) {
-        // one partition at width 128 with the camera, or ranks above the
-        // resident decoder's: stage8_kernel decodes its history and current
-        // tiles (read-time RoPE without the camera is drtile_kernel's)
+        // one partition at width 128 with the SF13 camera layout, or ranks
+        // above the resident decoder's: stage8_kernel decodes its history and
+        // current tiles
         const ChunkParams& p = M.part[0];
         rc = set_smem(stage8_kernel, sizeof(Chunk8Smem));
         if (rc) return rc;
@@ -2256,11 +2494,28 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
                 const int64_t nct = P.f[i].ntiles - P.f[i].ntiles_hist;
                 if (pass == 0 && nct > 0)
                     segs.push_back({CTILE_BLOCK_COST, i, SEG_CUR, 0, bh * cdiv(nct, 2)});
+                if (pass == 0 && table[i]) {
+                    const CameraDev& c = M.part[i].cam;
+                    const int64_t elems = (int64_t)camera_batches(c, d[i].B) * c.n_mats * 64;
+                    segs.push_back({0.0, i, SEG_TABLE, 0, cdiv(elems, DR_THREADS)});
+                }
             }
             set_segments(M, segs);
             if (seg_blocks(M) == 0) continue;
             rc = drtile_launch(qk == qv || pass == 0 ? qk : qv, M, seg_blocks(M), s);
             if (rc) return rc;
+        }
+        // read-time RoPE and the camera of every partition's history tiles,
+        // in place
+        std::vector<SegOrder> segs;
+        for (int i = 0; i < n; ++i)
+            if ((rope_on(d[i].rope) || d[i].cam.mats) && d[i].n_rows > 0)
+                segs.push_back({(double)(d[i].cam.mats ? tile_elems(d[i].dk) : k_image_elems(d[i].dk)),
+                                i, SEG_XFORM, 0, (int64_t)d[i].B * d[i].H * cdiv(d[i].n_rows, FT_T)});
+        if (!segs.empty()) {
+            set_segments(M, segs);
+            tile_xform_kernel<<<dim3((unsigned)seg_blocks(M)), TX_THREADS, 0, s>>>(M);
+            NKV_LAUNCH_CHECK();
         }
     }
     // flash: the kernel events bracket it
@@ -2301,7 +2556,7 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
     }
     const int64_t waves = 2 * (int64_t)d[0].B * d[0].H * M.part[0].qblocks;
     staged_combine_kernel<<<dim3((unsigned)cdiv(waves, CB_WAVES)), 64 * CB_WAVES, 0, s>>>(
-        M, shift, sh_sb, sh_sh);
+        M, shift, sh_sb, sh_sh, ocam);
     NKV_LAUNCH_CHECK();
     return NKV_OK;
 }
@@ -2399,7 +2654,7 @@ size_t staged_multi_workspace(const ChunkLaunchDesc* d, int n) { return multi_pl
 
 int staged_multi_launch(hipStream_t s, const ChunkLaunchDesc* d, int n, const int32_t* const* heads,
                         const float* shift, int64_t sh_sb, int64_t sh_sh, void* workspace,
-                        size_t workspace_bytes) {
+                        size_t workspace_bytes, const CameraDev& ocam) {
     NKV_REQUIRE(staged_multi_supported(d, n), NKV_ERR_UNSUPPORTED,
                 "these partitions do not fit one staged launch");
     ChunkParams ps[NKV_MAX_PARTS];
@@ -2415,7 +2670,7 @@ int staged_multi_launch(hipStream_t s, const ChunkLaunchDesc* d, int n, const in
     const size_t need = staged_multi_workspace(d, n);
     NKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), NKV_ERR_WORKSPACE,
                 "workspace missing or smaller than the size query returned");
-    return staged_run(s, d, ps, n, heads, shift, sh_sb, sh_sh, workspace);
+    return staged_run(s, d, ps, n, heads, shift, sh_sb, sh_sh, workspace, ocam);
 }
 
 int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_t workspace_bytes) {
@@ -2436,9 +2691,9 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
     p.part_ml = reinterpret_cast<float*>(reinterpret_cast<unsigned char*>(workspace) +
                                          qrows * CK_D * sizeof(uint16_t));
 
-    // Only reader widths 32 and 64 reach the key-chunk kernel (with the
-    // camera, or ranks above the resident decoder's): every call at width
-    // 128 with keys to attend is staged, and current keys (the only masked
+    // Only reader widths 32 and 64 reach the key-chunk kernel (with ranks
+    // above the resident decoder's): every call at width 128 with keys to
+    // attend is staged, and current keys (the only masked
     // ones) come with width 128 alone.  A call without keys only runs the
     // combine (out = 0, lse = -inf).
     NKV_REQUIRE(d.n_rows + d.Nc == 0 || (d.dk != CK_D && d.Nc == 0), NKV_ERR_INVALID,
@@ -2504,7 +2759,28 @@ ChunkLaunchDesc desc_from(const nkv_attend_args* a) {
 }
 }  // namespace
 
-size_t chunk_workspace_bytes(const nkv_attend_args* a) { return chunk_launch_workspace(desc_from(a)); }
+// The launch description with the call's read-time RoPE and camera (the
+// workspace plan depends on the camera).
+int full_desc(const nkv_attend_args* a, ChunkLaunchDesc* d) {
+    *d = desc_from(a);
+    if (a->camera) {
+        int rc = camera_from_abi(a->camera, a->D, a->B, &d->cam);
+        if (rc) return rc;
+    }
+    if (a->rope) {
+        int rc = rope_from_abi(a->rope, a->D, &d->rope);
+        if (rc) return rc;
+        NKV_REQUIRE(a->N <= rope_rows_covered(a->rope),
+                    NKV_ERR_INVALID, "more history tokens than the RoPE frames cover");
+    }
+    return NKV_OK;
+}
+
+size_t chunk_workspace_bytes(const nkv_attend_args* a) {
+    ChunkLaunchDesc d;
+    if (full_desc(a, &d)) return 0;
+    return chunk_launch_workspace(d);
+}
 
 int chunk_check(const nkv_attend_args* a) {
     NKV_REQUIRE(a->D == CK_D, NKV_ERR_UNSUPPORTED, "key-chunk attend supports D == 128");
@@ -2529,17 +2805,9 @@ int chunk_attend_launch(hipStream_t s, const nkv_attend_args* a, void* workspace
                         size_t workspace_bytes) {
     int rc = chunk_check(a);
     if (rc) return rc;
-    ChunkLaunchDesc d = desc_from(a);
-    if (a->camera) {
-        rc = camera_from_abi(a->camera, a->D, a->B, &d.cam);
-        if (rc) return rc;
-    }
-    if (a->rope) {
-        rc = rope_from_abi(a->rope, a->D, &d.rope);
-        if (rc) return rc;
-        NKV_REQUIRE(a->N <= rope_rows_covered(a->rope),
-                    NKV_ERR_INVALID, "more history tokens than the RoPE frames cover");
-    }
+    ChunkLaunchDesc d;
+    rc = full_desc(a, &d);
+    if (rc) return rc;
     return chunk_launch(s, d, workspace, workspace_bytes);
 }
 

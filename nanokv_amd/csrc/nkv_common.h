@@ -18,6 +18,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef double f64x2 __attribute__((ext_vector_type(2)));
 
 namespace nkv {
 
@@ -77,6 +78,17 @@ __device__ __forceinline__ uint16_t f32_to_f16_bits(float f) {
 
 __device__ __forceinline__ float bf16_round(float f) {
     return bf16_bits_to_f32(f32_to_bf16_bits(f));
+}
+
+// fp64 -> fp32 (round to nearest even), kept as an fp32 value: a later bf16
+// rounding of it is the second of two roundings, as in the reference's
+// fp64 -> fp32 -> bf16.  (Without the barrier the compiler may fold the two
+// truncations into one fp64 -> bf16 rounding, which differs at double-
+// rounding ties.)
+__device__ __forceinline__ float f64_to_f32(double x) {
+    float f = (float)x;
+    __asm__("" : "+v"(f));
+    return f;
 }
 
 __device__ __forceinline__ float scale_bits_to_f32(uint16_t b, int scale_dtype) {

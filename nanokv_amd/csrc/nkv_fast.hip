@@ -19,14 +19,14 @@
 //     decoding k_low / v_low in-kernel -> out_l, lse_l;
 //  3. merge(out, lse_n, out_l, lse_l) per group head (CN/core.py:33-42), the
 //     lift being the identity (vd == D).
-// Without a camera and with at most NKV_MAX_PARTS - 1 groups, all partitions
-// run as one staged launch (staged_multi_launch): one decode launch for
-// every partition's tiles (RoPE in its epilogue), one flash launch over all
-// of them, and one combine that folds each head's native and group partials
-// together (the merge of step 3, with the low_shift), so no group output or
-// LSE is written.  Identity readers then read the layer's own center tables
-// and means (and, without RoPE, queries) through head maps instead of
-// projected copies.  Otherwise the partitions run one after another and
+// With at most NKV_MAX_PARTS - 1 groups, all partitions run as one staged
+// launch (staged_multi_launch): one decode launch for every partition's
+// tiles, with read-time RoPE or the camera one in-place pass over them,
+// one flash launch over all of them, and one combine that folds each head's
+// native and group partials together (the merge of step 3, with the
+// low_shift), so no group output or LSE is written.  Identity readers then
+// read the layer's own center tables and means (and, without RoPE or the
+// camera, queries) through head maps instead of projected copies.  Otherwise the partitions run one after another and
 // group_merge_kernel merges each group's output in place.
 // The projected tables are small (C x d per head); they are recomputed per
 // call, as the reference's read does.  With a segmented codec the tables of
@@ -217,49 +217,59 @@ __global__ void __launch_bounds__(256) group_merge_kernel(
     if (lse_out && part == 0) lse_out[((int64_t)b * H + h) * Q + q] = l;
 }
 
-// RoPE of the reader queries in place (rope_selected, CN/core.py:75-91):
-// q_low [B, Q, nh, d] bf16, pair j of head i rotated by original pair
-// pairs[i * d/2 + j] (null: j) at the position of query t (row t of the
-// query positions).  One thread per pair.
-__global__ void __launch_bounds__(256) rope_low_kernel(uint16_t* q_low, int B, int64_t Q, int nh,
-                                                       int d, RopeDev pos) {
-    const int hp = d / 2;
-    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (tid >= (int64_t)B * Q * nh * hp) return;
-    const int j = (int)(tid % hp);
-    const int64_t row = tid / hp;  // (b, t, i)
-    const int i = (int)(row % nh);
-    const int64_t t = (row / nh) % Q;
-    const int pj = pos.pairs ? pos.pairs[(int64_t)i * hp + j] : j;
-    const double* cs = rope_entry(pos, rope_rows(pos, t), pj);
-    uint32_t* w = reinterpret_cast<uint32_t*>(q_low) + tid;
-    *w = rope_pair(*w, cs[0], cs[1]);
-}
-
-// Camera P^T of the reader queries in place (camera_selected, CN/core.py:
-// 110-137): q_low [B, Q, nh, d] bf16; block j of head i uses sub-frame
-// cams[i * d/8 + j] (null: j % 4) of query t's matrices (query t at row t).
-// One thread per (b, t, i, block, vector); a block's 4-vectors are its dims
-// {0, 2, 4, 6} and {1, 3, 5, 7}.
-__global__ void __launch_bounds__(256) camera_low_kernel(uint16_t* q_low, int B, int64_t Q, int nh,
-                                                         int d, CameraDev cam, const int32_t* cams) {
+// The reader queries' read-time transforms in one pass, q_low [B, Q, nh, d]
+// bf16 written in place, or from the layer's queries src[b, t, heads[i]]
+// (an identity q_reduce, d == D) when src is given: RoPE rotates pair p of
+// head i by original pair pos.pairs[i * d/2 + p] (null: p) at the position of
+// query t (rope_selected, CN/core.py:75-91), then the camera multiplies the
+// two 4-vectors of 8-dim block j -- its dims {0, 2, 4, 6} and {1, 3, 5, 7} --
+// by sub-frame cams[i * d/8 + j] (null: j % 4) of query t's matrices
+// (camera_selected, CN/core.py:110-137).  One thread per (b, t, i, block):
+// one 16-byte load and store.
+__global__ void __launch_bounds__(256) query_low_kernel(uint16_t* q_low, const uint16_t* src,
+                                                        int64_t s_b, int64_t s_t, int64_t s_h,
+                                                        const int32_t* heads, int H, int B,
+                                                        int64_t Q, int nh, int d, RopeDev pos,
+                                                        CameraDev cam, const int32_t* cams) {
     const int nbk = d / 8;
     const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (tid >= (int64_t)B * Q * nh * nbk * 2) return;
-    const int r = (int)(tid & 1);
-    const int j = (int)((tid >> 1) % nbk);
-    const int64_t row = (tid >> 1) / nbk;  // (b, t, i)
+    if (tid >= (int64_t)B * Q * nh * nbk) return;
+    const int j = (int)(tid % nbk);
+    const int64_t row = tid / nbk;  // (b, t, i)
     const int i = (int)(row % nh);
     const int64_t t = (row / nh) % Q;
     const int b = (int)(row / ((int64_t)nh * Q));
-    const int sub = cams ? (cams[(int64_t)i * nbk + j] & 3) : (j & 3);
-    uint16_t* v = q_low + row * d + 8 * j + r;
-    float x[4], y[4];
+    uint16_t* dst = q_low + row * d + 8 * j;
+    const uint16_t* from = dst;
+    if (src) {
+        const int hq = min(max(ldg(heads + i), 0), H - 1);
+        from = src + b * s_b + t * s_t + hq * s_h + 8 * j;
+    }
+    u32x4 v = ldg(reinterpret_cast<const u32x4*>(from));
+    if (rope_on(pos)) {
+        const RopeRows rr = rope_rows(pos, t);
 #pragma unroll
-    for (int e = 0; e < 4; ++e) x[e] = bf16_bits_to_f32(v[2 * e]);
-    camera_vec4(camera_mats(cam, b, t) + 16 * sub, x, y);
+        for (int w = 0; w < 4; ++w) {
+            const int pj = pos.pairs ? ldg(pos.pairs + (int64_t)i * (d / 2) + 4 * j + w) : 4 * j + w;
+            const f64x2 cs = ldg(reinterpret_cast<const f64x2*>(rope_entry(pos, rr, pj)));
+            v[w] = rope_pair(v[w], cs.x, cs.y);
+        }
+    }
+    if (cam.mats) {
+        const int sub = cams ? (ldg(cams + (int64_t)i * nbk + j) & 3) : (j & 3);
+        const float* M = camera_mats(cam, b, t) + 16 * sub;
+        float x0[4], x1[4], y0[4], y1[4];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) v[2 * e] = f32_to_bf16_bits(y[e]);
+        for (int e = 0; e < 4; ++e) {
+            x0[e] = __uint_as_float(v[e] << 16);
+            x1[e] = __uint_as_float(v[e] & 0xffff0000u);
+        }
+        camera_vec4(M, x0, y0);
+        camera_vec4(M, x1, y1);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = pack_bf16x2(y0[e], y1[e]);
+    }
+    *reinterpret_cast<u32x4*>(dst) = v;
 }
 
 namespace {
@@ -359,6 +369,13 @@ int validate(const nkv_fast_args* f) {
             if (rc) return rc;
         }
     }
+    if (f->o_camera) {
+        CameraDev chk;
+        int rc = camera_from_abi(f->o_camera, a.D, a.B, &chk);
+        if (rc) return rc;
+        NKV_REQUIRE(f->o_camera->layout == NKV_CAMERA_FULL, NKV_ERR_UNSUPPORTED,
+                    "o_camera supports the FULL layout (CN/mg35.py:131-132)");
+    }
     NKV_REQUIRE(f->n_protect >= 0 && f->n_low >= 0 && f->n_protect <= a.N && f->n_low <= a.N,
                 NKV_ERR_INVALID, "protected/low row counts out of range");
     NKV_REQUIRE(f->n_protect == 0 || f->protect_rows, NKV_ERR_INVALID, "protect_rows missing");
@@ -367,9 +384,13 @@ int validate(const nkv_fast_args* f) {
                 "groups missing");
     if (a.Q > 0) NKV_REQUIRE(a.q && a.out, NKV_ERR_INVALID, "q and out required");
     if (a.Q > 0)
-        NKV_REQUIRE(reinterpret_cast<uintptr_t>(a.out) % 16 == 0 && a.o_sb % 8 == 0 &&
-                        a.o_st % 8 == 0 && a.o_sh % 8 == 0,
-                    NKV_ERR_INVALID, "out must be 16-byte aligned with strides divisible by 8");
+        NKV_REQUIRE(rows16(a.q, a.q_sb, a.q_st, a.q_sh) && rows16(a.out, a.o_sb, a.o_st, a.o_sh),
+                    NKV_ERR_INVALID, "q and out must be 16-byte aligned with strides divisible by 8");
+    if (a.Nc > 0)
+        NKV_REQUIRE(rows16(a.k_cur, a.k_sb, a.k_st, a.k_sh) &&
+                        rows16(a.v_cur, a.v_sb, a.v_st, a.v_sh),
+                    NKV_ERR_INVALID,
+                    "k_cur and v_cur must be 16-byte aligned with strides divisible by 8");
     if (a.Nc > 0) NKV_REQUIRE(a.k_cur && a.v_cur, NKV_ERR_INVALID, "current K/V missing");
     NKV_REQUIRE(!a.cur_mask || (a.n_groups >= 1 && a.cur_mask_words >= cdiv(a.Nc, 32)),
                 NKV_ERR_INVALID, "the current-key mask needs n_groups >= 1 and "
@@ -449,7 +470,8 @@ struct ReaderIdent {
 // With read-time RoPE the reader queries are always formed from q_pre and
 // rotated at the query positions, as the per-group path does.
 ReaderIdent reader_ident(const nkv_fast_args* f, const nkv_reader_group& G, bool multi) {
-    return multi ? ReaderIdent{!G.q_reduce && !f->attend.rope, !G.k_affine, !G.v_affine}
+    return multi ? ReaderIdent{!G.q_reduce && !f->attend.rope && !f->attend.camera, !G.k_affine,
+                               !G.v_affine}
                  : ReaderIdent{false, false, false};
 }
 
@@ -545,33 +567,46 @@ ChunkLaunchDesc low_desc(const nkv_fast_args* f, int g, unsigned char* ws, const
     return d;
 }
 
+// A partition's read-time transforms as the launches apply them: the
+// history keys' RoPE at their codec rows (a reader group's keys on its pair
+// map) and the camera's P^-1 (a reader group's keys on its block map).  The
+// workspace plan depends on them, so the size query applies them too.
+void add_transforms(const nkv_fast_args* f, const nkv_reader_group* G, ChunkLaunchDesc& d) {
+    const nkv_attend_args& a = f->attend;
+    if (a.rope) {
+        rope_from_abi(a.rope, a.D, &d.rope);
+        if (G) d.rope.pairs = G->rope_pairs;
+    }
+    if (a.camera) {
+        camera_from_abi(a.camera, a.D, a.B, &d.cam);
+        if (G) d.cam.blocks = G->cam_blocks;
+    }
+}
+
 // The partitions of the staged multi-partition launch: the native one, then
 // every reader group (heads[1 + g] = its heads).  With read-time RoPE every
 // partition rotates its history keys at their codec rows, a reader group on
-// its pair map.
+// its pair map; with the camera every partition's history rows take P^-1, a
+// reader group's keys on its block map.
 int multi_descs(const nkv_fast_args* f, unsigned char* ws, const FastLayout& L,
                 ChunkLaunchDesc* d, const int32_t** heads) {
-    RopeDev krope{};
-    if (f->attend.rope) rope_from_abi(f->attend.rope, f->attend.D, &krope);
     d[0] = native_desc(f, f->attend.lse);
-    d[0].rope = krope;
+    add_transforms(f, nullptr, d[0]);
     heads[0] = nullptr;
     for (int g = 0; g < f->num_groups; ++g) {
         d[1 + g] = low_desc(f, g, ws, L, true);
-        d[1 + g].rope = krope;
-        d[1 + g].rope.pairs = f->groups[g].rope_pairs;
+        add_transforms(f, &f->groups[g], d[1 + g]);
         heads[1 + g] = f->groups[g].heads;
     }
     return 1 + f->num_groups;
 }
 
-// One decode, one flash and one combine launch serve the whole call (every
-// partition merged in the combine, no per-group merge) when there is no
-// camera and the native partition and the reader groups fit one staged
-// launch.
+// One decode, one flash and one combine launch (and with the camera one
+// tile pass) serve the whole call (every partition merged in the combine,
+// no per-group merge) when the native partition and the reader groups fit
+// one staged launch.
 bool use_multi(const nkv_fast_args* f) {
-    const nkv_attend_args& a = f->attend;
-    if (a.camera || f->n_low == 0 || f->num_groups < 1 || f->num_groups + 1 > NKV_MAX_PARTS)
+    if (f->n_low == 0 || f->num_groups < 1 || f->num_groups + 1 > NKV_MAX_PARTS)
         return false;
     FastLayout L{};
     for (auto* v : {&L.q_low, &L.kc, &L.vc, &L.kb, &L.vb, &L.out_l, &L.lse_l})
@@ -614,9 +649,14 @@ FastLayout layout(const nkv_fast_args* f) {
         const int n = multi_descs(f, nullptr, L, d, heads);
         part = staged_multi_workspace(d, n);
     } else {
-        part = chunk_launch_workspace(native_desc(f, nullptr));
-        for (int g = 0; g < f->num_groups; ++g)
-            part = std::max(part, chunk_launch_workspace(low_desc(f, g, nullptr, L)));
+        ChunkLaunchDesc nd = native_desc(f, nullptr);
+        add_transforms(f, nullptr, nd);
+        part = chunk_launch_workspace(nd);
+        for (int g = 0; g < f->num_groups; ++g) {
+            ChunkLaunchDesc ld = low_desc(f, g, nullptr, L);
+            add_transforms(f, &f->groups[g], ld);
+            part = std::max(part, chunk_launch_workspace(ld));
+        }
     }
     L.partials = take(part);
     L.total = off;
@@ -660,31 +700,31 @@ int reader_tables(hipStream_t s, const nkv_fast_args* f, int g, unsigned char* w
     const int nh = G.num_heads, dd = G.d;
     int rc = NKV_OK;
     // q_low [B, Q, nh, d] from the pre-RoPE, pre-camera queries when
-    // given (then rotated / transformed on its retained pairs and blocks)
+    // given, then rotated / transformed on its retained pairs and blocks;
+    // an identity q_reduce takes them through the head map in the same pass
     uint16_t* q_low = reinterpret_cast<uint16_t*>(ws + L.q_low[g]);
-    if (!id.q) {
-        if (reader_q_pre(f))
-            rc = project<false, false>(s, f->q_pre, f->qp_sb, f->qp_st, f->qp_sh, nullptr, 0,
-                                       G.heads, a.H, G.q_reduce, D, dd, a.B, nh, a.Q, q_low,
-                                       a.Q * nh * dd, dd, (int64_t)nh * dd);
-        else
-            rc = project<false, false>(s, a.q, a.q_sb, a.q_st, a.q_sh, nullptr, 0, G.heads, a.H,
-                                       G.q_reduce, D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
-                                       (int64_t)nh * dd);
+    const bool pre = reader_q_pre(f);
+    const uint16_t* qsrc = reinterpret_cast<const uint16_t*>(pre ? f->q_pre : a.q);
+    const int64_t qs_b = pre ? f->qp_sb : a.q_sb, qs_t = pre ? f->qp_st : a.q_st,
+                  qs_h = pre ? f->qp_sh : a.q_sh;
+    const bool xform = a.rope || a.camera;
+    if (!id.q && (G.q_reduce || !xform)) {
+        rc = project<false, false>(s, qsrc, qs_b, qs_t, qs_h, nullptr, 0, G.heads, a.H,
+                                   G.q_reduce, D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
+                                   (int64_t)nh * dd);
         if (rc) return rc;
     }
-    if (a.rope) {
-        RopeDev qp = qrope;
-        qp.pairs = G.rope_pairs;
-        const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 2);
-        rope_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(q_low, a.B, a.Q, nh,
-                                                                          dd, qp);
-        NKV_LAUNCH_CHECK();
-    }
-    if (a.camera) {
-        const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 8) * 2;
-        camera_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(
-            q_low, a.B, a.Q, nh, dd, qcam, G.cam_blocks);
+    if (!id.q && xform) {
+        RopeDev qp{};
+        if (a.rope) {
+            qp = qrope;
+            qp.pairs = G.rope_pairs;
+        }
+        const CameraDev qc = a.camera ? qcam : CameraDev{};
+        const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 8);
+        query_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(
+            q_low, G.q_reduce ? nullptr : qsrc, qs_b, qs_t, qs_h, G.heads, a.H, a.B, a.Q, nh, dd,
+            qp, qc, a.camera ? G.cam_blocks : nullptr);
         NKV_LAUNCH_CHECK();
     }
     for (int cc = 0; cc < 2 && f->n_low > 0; ++cc) {
@@ -743,16 +783,12 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
     // one; the merges then update it in place
     float* lse_n = a.lse ? a.lse : reinterpret_cast<float*>(ws + L.lse_n);
 
-    RopeDev krope{}, qrope{};
-    if (a.rope) {
-        rope_from_abi(a.rope, a.D, &krope);
-        if (f->q_rope) rope_from_abi(f->q_rope, a.D, &qrope);
-    }
-    CameraDev kcam{}, qcam{};
-    if (a.camera) {
-        camera_from_abi(a.camera, a.D, a.B, &kcam);
-        if (f->q_camera) camera_from_abi(f->q_camera, a.D, a.B, &qcam);
-    }
+    // the reader queries' positions and camera (the history's are added to
+    // each partition's launch by add_transforms)
+    RopeDev qrope{};
+    if (a.rope && f->q_rope) rope_from_abi(f->q_rope, a.D, &qrope);
+    CameraDev qcam{};
+    if (a.camera && f->q_camera) camera_from_abi(f->q_camera, a.D, a.B, &qcam);
 
     if (L.multi) {
         // the reader tables, then every partition in one staged launch whose
@@ -764,18 +800,27 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
         ChunkLaunchDesc d[NKV_MAX_PARTS];
         const int32_t* heads[NKV_MAX_PARTS];
         const int n = multi_descs(f, ws, L, d, heads);
+        CameraDev ocam{};
+        if (f->o_camera) camera_from_abi(f->o_camera, a.D, a.B, &ocam);
         return staged_multi_launch(s, d, n, heads, f->low_shift, f->ls_sb, f->ls_sh,
-                                   ws + L.partials, part_bytes);
+                                   ws + L.partials, part_bytes, ocam);
     }
+
+    // P of the query rows on the merged output, when the call applies it
+    auto finish = [&]() -> int {
+        if (!f->o_camera) return NKV_OK;
+        CameraDev ocam{};
+        camera_from_abi(f->o_camera, a.D, a.B, &ocam);
+        return camera_apply_inplace(s, ocam, a.B, a.Q, a.H, a.D, a.out, a.o_sb, a.o_st, a.o_sh);
+    };
 
     // 1. native partition -> out, lse_n
     ChunkLaunchDesc nd = native_desc(f, lse_n);
-    nd.rope = krope;
-    nd.cam = kcam;
+    add_transforms(f, nullptr, nd);
     rc = chunk_launch(s, nd, ws + L.partials, part_bytes);
     if (rc) return rc;
     // no low rows: the native partition is the whole attention
-    if (f->n_low == 0) return NKV_OK;
+    if (f->n_low == 0) return finish();
 
     // 2-3. reader groups
     for (int g = 0; g < f->num_groups; ++g) {
@@ -784,14 +829,7 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
         rc = reader_tables(s, f, g, ws, L, qrope, qcam);
         if (rc) return rc;
         ChunkLaunchDesc ld = low_desc(f, g, ws, L);
-        if (a.rope) {
-            ld.rope = krope;
-            ld.rope.pairs = G.rope_pairs;
-        }
-        if (a.camera) {
-            ld.cam = kcam;
-            ld.cam.blocks = G.cam_blocks;
-        }
+        add_transforms(f, &G, ld);
         rc = chunk_launch(s, ld, ws + L.partials, part_bytes);
         if (rc) return rc;
         const int64_t threads = (int64_t)a.B * a.Q * nh * (D / 8);
@@ -802,5 +840,5 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
             f->ls_sh);
         NKV_LAUNCH_CHECK();
     }
-    return NKV_OK;
+    return finish();
 }

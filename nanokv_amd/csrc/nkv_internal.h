@@ -138,6 +138,12 @@ struct ChunkLaunchDesc {
 // h*D .., center columns h*D .. and mean h*D ...
 ChunkCodec chunk_codec_from(const nkv_codec& c, int D, int HD);
 
+// Whether rows of a [B, T, H, D] bf16 tensor can be read and written as
+// 16-byte pieces (the kernels' query, output and current-key accesses).
+inline bool rows16(const void* p, int64_t sb, int64_t st, int64_t sh) {
+    return reinterpret_cast<uintptr_t>(p) % 16 == 0 && sb % 8 == 0 && st % 8 == 0 && sh % 8 == 0;
+}
+
 // Host check of a codec's segment table against its N rows (NKV_OK when the
 // codec has no segments).
 int check_segments(const nkv_codec& c, int64_t N);
@@ -157,13 +163,15 @@ int chunk_launch(hipStream_t s, const ChunkLaunchDesc& d, void* workspace, size_
 // Partition i >= 1 covers heads heads[i][0 .. d[i].H) of the layer (the first
 // partition listing a head is merged into it; heads outside the layer are
 // never merged), its output shifted by shift[b*sh_sb + h*sh_sh + e] (null:
-// none) before the merge.  Supported: every partition staged by the decode
-// GEMM (no read-time RoPE or camera, ranks <= 384, the same codec ranks, B
-// and Q), current keys in partition 0 only.
+// none) before the merge; with ocam.mats set, the merged output is then
+// multiplied by P of its query row (FULL layout).  Supported: every
+// partition staged by the decode GEMM (ranks <= 384, the camera only in the
+// FULL layout, the same codec ranks, B and Q), current keys in partition 0
+// only.
 bool staged_multi_supported(const ChunkLaunchDesc* d, int n);
 size_t staged_multi_workspace(const ChunkLaunchDesc* d, int n);
 int staged_multi_launch(hipStream_t s, const ChunkLaunchDesc* d, int n, const int32_t* const* heads,
                         const float* shift, int64_t sh_sb, int64_t sh_sh, void* workspace,
-                        size_t workspace_bytes);
+                        size_t workspace_bytes, const CameraDev& ocam);
 
 }  // namespace nkv

@@ -72,12 +72,17 @@ __device__ __forceinline__ const double* rope_entry(const RopeDev& r, const Rope
 }
 
 // Rotate the bf16 pair (lo, hi) of `w` by (c, s) in fp64, every product and
-// sum rounded (no fused multiply-add), then fp64 -> fp32 -> bf16.
+// sum rounded (no fused multiply-add, whatever the translation unit's
+// contraction policy), then fp64 -> fp32 -> bf16.
 __device__ __forceinline__ uint32_t rope_pair(uint32_t w, double c, double s) {
+#pragma clang fp contract(off)
     const double a = (double)__uint_as_float(w << 16);
     const double b = (double)__uint_as_float(w & 0xffff0000u);
-    const float y0 = (float)__dsub_rn(__dmul_rn(a, c), __dmul_rn(b, s));
-    const float y1 = (float)__dadd_rn(__dmul_rn(a, s), __dmul_rn(b, c));
+    // (HIP's __dmul_rn is a plain product the translation unit may contract;
+    // the pragma above holds for these operations)
+    const double ac = a * c, bs = b * s, as = a * s, bc = b * c;
+    const float y0 = f64_to_f32(ac - bs);
+    const float y1 = f64_to_f32(as + bc);
     return pack_bf16x2(y0, y1);
 }
 

@@ -14,8 +14,8 @@ only its import.  Underneath, the whole read is one nkv_fast_attend call:
                            blocks in-kernel (MG35:305-347)
   merge                    log-sum-exp of the partitions (CN/core.py:33-42)
 
-and the output camera P is one nkv_camera_apply of the merged output (it
-commutes with the merge and with block-selection lifts).  The frame routing
+and the output camera P goes on the merged output inside the same call
+(o_camera; it commutes with the merge and with block-selection lifts).  The frame routing
 (which history rows are active, protected or low, MG35:146-190) is computed
 on the host from the frame metadata lists, as the reference's metadata cache
 does (CN/metadata_cache.py:48-72).
@@ -260,9 +260,7 @@ def maybe_attention(self_attn, q_pre, q_native, k_native, v_raw, cur_k_pre, freq
                              key, value, protect_rows, low_rows, groups,
                              softmax_scale=reader.native_dim ** -0.5, return_lse=False,
                              rope=kv_rope, q_pre=qp.to(torch.bfloat16), q_rope=q_rope,
-                             camera=kv_cam, q_camera=q_cam, visibility=vis)
-    if out_cam is not None:
-        out = ops.camera_apply(out, out_cam)
+                             camera=kv_cam, q_camera=q_cam, visibility=vis, out_camera=out_cam)
     result = torch.zeros_like(q_native)
     result[:, mosaic_tokens:] = out.reshape(B, Sq, H * D).to(q_native.dtype)
     if write_cache and cache is not None:

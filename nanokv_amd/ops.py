@@ -919,7 +919,7 @@ class ReaderTensors:
 
 def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, softmax_scale, out,
                return_lse, rope=None, q_pre=None, q_rope=None, camera=None, q_camera=None,
-               visibility=None, low_shift=None):
+               visibility=None, low_shift=None, out_camera=None):
     args, out, lse, device = _attend_args(q, k_cur, v_cur, key, value, softmax_scale, out,
                                           return_lse)
     keep = []  # ctypes structs the call points to
@@ -963,6 +963,12 @@ def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, soft
         qc = q_camera.struct()
         keep.append(qc)
         f.q_camera = ctypes.pointer(qc)
+    if out_camera is not None:
+        if out_camera.mats.shape[0] not in (1, q.shape[0]):
+            raise ValueError("out_camera batch must match q or broadcast")
+        oc = out_camera.struct()
+        keep.append(oc)
+        f.o_camera = ctypes.pointer(oc)
     if low_shift is not None:
         _require_gpu(low_shift)
         B, _, H, D = (int(x) for x in q.shape)
@@ -982,10 +988,12 @@ def _fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, soft
 def fast_attend_workspace_size(q: torch.Tensor, k_cur: Optional[torch.Tensor],
                                v_cur: Optional[torch.Tensor], key: Codec, value: Codec,
                                protect_rows: torch.Tensor, low_rows: torch.Tensor,
-                               groups: list) -> int:
-    """Workspace bytes nkv_fast_attend needs for this problem."""
+                               groups: list, **kw) -> int:
+    """Workspace bytes nkv_fast_attend needs for this problem; kw: the
+    transforms fast_attend takes (rope, q_pre, q_rope, camera, q_camera,
+    visibility, low_shift, out_camera), which the workspace depends on."""
     return int(_fast_args(q, k_cur, v_cur, key, value, protect_rows, low_rows, groups, None,
-                          None, False)[2])
+                          None, False, **kw)[2])
 
 
 def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[torch.Tensor],
@@ -997,7 +1005,8 @@ def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[
                 q_pre: Optional[torch.Tensor] = None, q_rope=None,
                 camera: Optional[Camera] = None, q_camera: Optional[Camera] = None,
                 visibility: Optional[Visibility] = None,
-                low_shift: Optional[torch.Tensor] = None):
+                low_shift: Optional[torch.Tensor] = None,
+                out_camera: Optional[Camera] = None):
     """NanoKV-Fast mixed-dimensional attention (see nkv_fast_attend).
 
     protect_rows / low_rows: int32 codec rows of the native and low
@@ -1008,16 +1017,17 @@ def fast_attend(q: torch.Tensor, k_cur: Optional[torch.Tensor], v_cur: Optional[
     codec rows (history keys rotated at read); then q is the rotated query,
     q_pre [B, Q, H, D] the pre-RoPE query the reader groups project and
     q_rope the queries' positions (query t at row t).  camera: P^-1 of the
-    history rows (q, k_cur, v_cur already transformed; the caller applies P
-    to out), q_camera: P^T of the query rows for the reader queries (then q_pre
-    is the untransformed query).  visibility: which current keys each query
+    history rows (q, k_cur, v_cur already transformed), q_camera: P^T of the
+    query rows for the reader queries (then q_pre is the untransformed
+    query), out_camera: P of the query rows, applied to out after the merge
+    (None: the caller applies it).  visibility: which current keys each query
     sees in the native partition.  low_shift [B, H, D] fp32: the value-mean
     correction added to each head's low-partition values before the merge.
     """
     f, structs, need, out, lse, device = _fast_args(q, k_cur, v_cur, key, value, protect_rows,
                                                     low_rows, groups, softmax_scale, out,
                                                     return_lse, rope, q_pre, q_rope, camera,
-                                                    q_camera, visibility, low_shift)
+                                                    q_camera, visibility, low_shift, out_camera)
     if kernel_events is not None:
         f.attend.ev_kernel_begin, f.attend.ev_kernel_end = kernel_events
     if workspace is None or workspace.numel() < need:

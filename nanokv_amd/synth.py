@@ -234,3 +234,34 @@ def fast_protect_mask(shape: Shape, frame_tokens: int = FAST_FRAME_TOKENS,
     frames = (shape.N + frame_tokens - 1) // frame_tokens
     frame_of = torch.arange(shape.N, device=device) // frame_tokens
     return frame_of >= frames - recent
+
+
+def camera_matrices(sets: int, seed: int, sub_frames: int = 4):
+    """PRoPE projection matrices as _prepare_projection_matrices builds them
+    (camera_rope.py:195-222): for each of `sets` matrix sets and each
+    sub-frame a camera with a random rotation, a translation of N(0, 0.3)
+    per axis and normalised focal lengths in [0.8, 1.2]; P = lift(K) . V,
+    P^T, and P^-1 = invert_SE3(V) . lift(K^-1) (camera_rope.py:318-337).
+    Returns (P, P_T, P_inv), fp32 [1, sets, sub_frames, 4, 4] on the CPU."""
+    g = _gen(seed * 1000 + 41, "cpu")
+    n = sets * sub_frames
+    q, r = torch.linalg.qr(torch.randn(n, 3, 3, generator=g, dtype=torch.float64))
+    rot = q * torch.sign(torch.diagonal(r, dim1=-2, dim2=-1))[:, None, :]
+    rot = torch.where(torch.det(rot)[:, None, None] < 0, -rot, rot)      # det +1
+    t = 0.3 * torch.randn(n, 3, generator=g, dtype=torch.float64)
+    f = 0.8 + 0.4 * torch.rand(n, 2, generator=g, dtype=torch.float64)
+    view = torch.zeros(n, 4, 4, dtype=torch.float64)
+    view[:, :3, :3], view[:, :3, 3], view[:, 3, 3] = rot, t, 1.0
+    k = torch.zeros(n, 4, 4, dtype=torch.float64)
+    k[:, 0, 0], k[:, 1, 1], k[:, 2, 2], k[:, 3, 3] = f[:, 0], f[:, 1], 1.0, 1.0
+    k_inv = torch.zeros_like(k)
+    k_inv[:, 0, 0], k_inv[:, 1, 1], k_inv[:, 2, 2], k_inv[:, 3, 3] = 1 / f[:, 0], 1 / f[:, 1], 1.0, 1.0
+    view_inv = torch.zeros_like(view)
+    view_inv[:, :3, :3] = rot.transpose(-1, -2)
+    view_inv[:, :3, 3] = -(rot.transpose(-1, -2) @ t[:, :, None])[:, :, 0]
+    view_inv[:, 3, 3] = 1.0
+    P = (k @ view).float()
+    P_inv = (view_inv @ k_inv).float()
+    shape = (1, sets, sub_frames, 4, 4)
+    return (P.reshape(shape).contiguous(), P.transpose(-1, -2).reshape(shape).contiguous(),
+            P_inv.reshape(shape).contiguous())

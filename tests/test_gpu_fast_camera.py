@@ -125,3 +125,48 @@ def test_fast_over_segments_with_own_tables(dev):
                                    oracle_groups(payload), D ** -0.5, D=D)
     diff, cos = max_abs_cos(out[0].permute(1, 0, 2).float().cpu().numpy(), ref)
     assert diff <= MAX_ABS and cos >= MIN_COS, (diff, cos)
+
+
+def _split_groups(payload, parts):
+    """The payload's reader group 1 split into `parts` groups of its heads."""
+    g = payload["groups"][1]
+    n = len(g["heads"])
+    cuts = [round(i * n / parts) for i in range(parts + 1)]
+    split = [{k: v[a:b] for k, v in g.items()} for a, b in zip(cuts[:-1], cuts[1:])]
+    return dict(payload, groups=[payload["groups"][0]] + split)
+
+
+@pytest.mark.parametrize("parts", [1, 3])
+def test_fast_out_camera_equals_separate_apply(dev, parts):
+    """o_camera: the call's P on the merged output gives the bits of
+    nkv_camera_apply on the output of the call without it -- on the one
+    staged launch (2 groups, P in its combine) and on the per-group path
+    (4 groups, one partition more than one launch holds)."""
+    sc = Scenario(H=5, D=128, N=300, Q=96, Nc=32, rK=128, rV=128, G=32, C=8, seed=4 + parts)
+    P = _mats(6, 3).contiguous()
+    P_T = P.transpose(-1, -2).contiguous()
+    P_inv = torch.linalg.inv(P).contiguous()
+    tpf = 60
+    qf = torch.tensor([4, 5], dtype=torch.int32, device=dev)
+    cam_k = ops.Camera(P_inv.to(dev), torch.tensor([0, 1, 2, 3, 0], dtype=torch.int32,
+                                                   device=dev), tpf)
+    cam_q = ops.Camera(P_T.to(dev), qf, 48)
+    cam_o = ops.Camera(P.to(dev), qf, 48)
+    payload = _split_groups(synth.make_readers(sc.shape, sc.layer, full_heads=(0,), d=32), parts)
+    reader = codec_native.ReaderLayer(payload, dev)
+    assert len(reader.groups) == 1 + parts
+    key, value = sc.codecs(dev)
+    protect = torch.arange(sc.N, device=dev) >= 240
+    pr = torch.nonzero(protect).flatten().to(torch.int32)
+    lr = torch.nonzero(~protect).flatten().to(torch.int32)
+    q_pre = sc.q.to(dev)
+    q = ops.camera_apply(q_pre, cam_q)
+    args = (q, sc.k_cur.to(dev), sc.v_cur.to(dev), key, value, pr, lr,
+            [g.tensors(camera=True) for g in reader.groups])
+    kw = dict(q_pre=q_pre, camera=cam_k, q_camera=cam_q)
+    raw, lse = ops.fast_attend(*args, **kw)
+    fused, lse_f = ops.fast_attend(*args, **kw, out_camera=cam_o)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, ops.camera_apply(raw, cam_o))
+    assert torch.equal(lse, lse_f)
+    assert not torch.equal(fused, raw)

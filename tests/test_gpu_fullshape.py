@@ -6,14 +6,15 @@ transform -> SDPA (max-abs 2e-2, cosine 0.9995, |dlse| < 2e-3), with
 BASELINE's queries and with queries 16 times larger (peaked attention, where
 the bar is shown to reject an oracle missing either transform).  The RoPE
 frames are bench.py's (30 x 52 tokens at temporal positions 0, 1, ...); the
-camera frames hold 1,560 rows each, four matrix sets in rotation."""
+camera frames hold 1,560 rows each, four matrix sets in rotation.  Config 3
+(NanoKV-Fast) runs at its full shape with both transforms likewise, below."""
 import numpy as np
 import pytest
 import torch
 
 import oracle.oracle as orc
 from nanokv_amd import ops, synth
-from tests._helpers import max_abs_cos, u16
+from tests._helpers import max_abs_cos, oracle_groups, u16
 
 pytestmark = pytest.mark.gpu
 
@@ -100,3 +101,116 @@ def test_cfg1_full_shape(dev, cfg1, with_rope, with_camera, q_scale):
         if with_camera:
             wrong, _ = orc.decode_attend(*args, **kw, key_freqs=freqs)
             assert not _bar(got, wrong)[0], "bar does not detect a missing camera"
+
+
+# ---------------------------------------------------------------- config 3
+# NanoKV-Fast at config 3's shape with read-time RoPE and the camera, as
+# bench.py --config 3 --rope --camera runs it: the last two frames
+# protected, six identity heads and eighteen 32-wide readers; the queries
+# and current keys form the chunk after the history (frame 8: RoPE at
+# temporal position 8, camera set 8 % 4).  The native partition takes the
+# queries rotated then times P^T, the groups project the untransformed
+# queries; P goes on the output after the call.  Heads 0 (identity group)
+# and 11, 23 (readers) are checked against the oracle's fast_attend, before
+# and after P.
+FAST_HEADS = [0, 11, 23]
+
+
+@pytest.fixture(scope="module")
+def cfg3(dev):
+    from nanokv_amd import codec_native
+    sh = synth.CONFIGS[3]
+    assert (sh.H, sh.N, sh.Q, sh.Nc, sh.rK, sh.rV, sh.C) == (24, 12480, 1560, 1560, 384, 384, 256)
+    lay = synth.make_layer(sh, seed=6, device=dev)
+    codecs, refs = [], []
+    for kind, cent, enc, dec in (("k", lay.centers_k, lay.w_enc_k, lay.w_dec_k),
+                                 ("v", lay.centers_v, lay.w_enc_v, lay.w_dec_v)):
+        rows = synth.history_rows(sh, cent, sh.N, seed=21 + (kind == "v"), device=dev)
+        e = ops.encode(rows, enc, centers=cent, group=sh.G, scale_dtype=sh.scale_dtype)
+        del rows
+        codecs.append(ops.Codec(packed=e["packed"][None], scales=e["scales"][None], w_dec=dec,
+                                group=sh.G, ids=e["ids"][None], centers=cent[None]))
+        refs.append({"packed": e["packed"].cpu().numpy(), "scales": u16(e["scales"]),
+                     "w_dec_bf16": u16(dec), "group": sh.G, "scale_dtype": "fp16",
+                     "ids": e["ids"].cpu().numpy().astype(np.int64), "centers_bf16": u16(cent)})
+    payload = synth.make_readers(sh, lay)
+    reader = codec_native.ReaderLayer(payload, dev)
+    protect = synth.fast_protect_mask(sh, device=dev)
+    pr = torch.nonzero(protect).flatten().to(torch.int32)
+    lr = torch.nonzero(~protect).flatten().to(torch.int32)
+    q_pre = synth.queries(sh, seed=23, device=dev)
+    kc = synth.history_rows(sh, lay.centers_k, sh.Nc, seed=24, device=dev)
+    vc = synth.history_rows(sh, lay.centers_v, sh.Nc, seed=25, device=dev)
+    kc = kc.reshape(1, sh.Nc, sh.H, sh.D).to(torch.bfloat16)
+    vc = vc.reshape(1, sh.Nc, sh.H, sh.D).to(torch.bfloat16)
+    return sh, codecs, refs, payload, reader, pr, lr, q_pre, kc, vc
+
+
+@pytest.mark.parametrize("q_scale", [1, 16])
+def test_cfg3_fast_rope_camera_full_shape(dev, cfg3, q_scale):
+    sh, codecs, refs, payload, reader, pr, lr, q_pre, kc, vc = cfg3
+    frames = -(-sh.N // TPF)
+    assert frames == 8 and sh.Q == TPF
+    q_pre = (q_pre.float() * q_scale).to(torch.bfloat16)
+    bands = ops.rope_bands(sh.D)
+    rope = ops.Rope.from_bands(bands, range(frames), GH, GW, dev)
+    q_rope = ops.Rope.from_bands(bands, [frames], GH, GW, dev)
+    # PRoPE's own matrices (rotations, translations, focal lengths): the
+    # outputs keep the magnitude of the values
+    P, P_T, P_inv = synth.camera_matrices(4, seed=7)
+    hist_set = np.arange(frames) % 4
+    qset = torch.tensor([frames % 4], dtype=torch.int32, device=dev)
+    cam_k = ops.Camera(P_inv.to(dev), torch.from_numpy(hist_set.astype(np.int32)).to(dev), TPF)
+    cam_q = ops.Camera(P_T.to(dev), qset, TPF)
+    cam_o = ops.Camera(P.to(dev), qset, TPF)
+    cam_c = ops.Camera(P_inv.to(dev), qset, TPF)
+    q = ops.camera_apply(ops.rope_apply(q_pre, q_rope), cam_q)
+    kcur = ops.camera_apply(ops.rope_apply(kc, q_rope), cam_c)
+    vcur = ops.camera_apply(vc, cam_c)
+    groups = [grp.tensors(rope=True, camera=True) for grp in reader.groups]
+    raw, lse = ops.fast_attend(q, kcur, vcur, codecs[0], codecs[1], pr, lr, groups, rope=rope,
+                               q_pre=q_pre, q_rope=q_rope, camera=cam_k, q_camera=cam_q)
+    out = ops.camera_apply(raw, cam_o)
+    # P inside the call (in its combine) gives the same bits
+    fused, _ = ops.fast_attend(q, kcur, vcur, codecs[0], codecs[1], pr, lr, groups, rope=rope,
+                               q_pre=q_pre, q_rope=q_rope, camera=cam_k, q_camera=cam_q,
+                               out_camera=cam_o)
+    torch.cuda.synchronize()
+    assert torch.equal(fused, out)
+    got_raw = raw[0][:, FAST_HEADS].float().cpu().numpy()
+    got = out[0][:, FAST_HEADS].float().cpu().numpy()
+
+    def freqs(r, grid_w, n):
+        t, h, w = (torch.view_as_complex(x.cpu()).numpy() for x in (r.cs_t, r.cs_h, r.cs_w))
+        return orc.kv_freqs((t, h, w), r.frame_pos.cpu().numpy(), GH, grid_w)[:n]
+
+    key_freqs, q_freqs = freqs(rope, GW, sh.N), freqs(q_rope, GW, sh.Q)
+    rows = np.arange(sh.N) // TPF
+    key_cam = P_inv[0].numpy()[hist_set[rows]]
+    q_cam = np.broadcast_to(P_T[0].numpy()[frames % 4], (sh.Q, 4, 4, 4))
+    out_cam = np.broadcast_to(P[0].numpy()[frames % 4], (sh.Q, 4, 4, 4))
+    args = (u16(q[0]), u16(kcur[0]), u16(vcur[0]), refs[0], refs[1], pr.cpu().numpy(),
+            lr.cpu().numpy(), oracle_groups(payload), sh.D ** -0.5)
+    kw = dict(heads=FAST_HEADS, D=sh.D, q_pre_bf16=u16(q_pre[0]), q_freqs=q_freqs, q_cam=q_cam)
+    # the call's output, before P: the oracle's merge of the partitions
+    # without their output transform (P is the same for both partitions of
+    # a query row, so it commutes with the LSE merge)
+    ref_raw, ref_lse = orc.fast_attend(*args, **kw, key_freqs=key_freqs, key_cam=key_cam)
+    ok, why = _bar(got_raw, ref_raw)
+    assert ok, why
+    assert np.abs(lse[0][FAST_HEADS].cpu().numpy() - ref_lse).max() < 2e-3
+    # after the caller's P: the reference rounds P o of each partition to
+    # bf16 before the merge, this path rounds the merged output and then
+    # P out, so the two may differ by a bf16 step of the value (0.125 at
+    # |x| >= 16, where peaked outputs reach): max-abs 2e-2 + 2^-7 |ref|
+    ref, _ = orc.fast_attend(*args, **kw, key_freqs=key_freqs, key_cam=key_cam, out_cam=out_cam)
+    excess = np.abs(got - ref) - (2e-2 + 2.0 ** -7 * np.abs(ref))
+    diff, cos = max_abs_cos(got, ref)
+    assert excess.max() <= 0 and cos >= 0.9995, (diff, cos, excess.max())
+    if q_scale > 1:
+        # peaked attention: an oracle that leaves the history's RoPE or
+        # camera out does not meet the bar
+        wrong, _ = orc.fast_attend(*args, **kw, key_cam=key_cam)
+        assert not _bar(got_raw, wrong)[0], "bar does not detect a missing RoPE"
+        wrong, _ = orc.fast_attend(*args, **kw, key_freqs=key_freqs)
+        assert not _bar(got_raw, wrong)[0], "bar does not detect a missing camera"

@@ -79,6 +79,9 @@ def test_v_images_at_the_128_wide_stride_are_caught(dk):
 
 
 def test_unstaged_partitions_are_refused():
-    # a 32-wide reader with the camera runs the key-chunk kernel, not the staged plan
-    rc, err, _ = _check([(1, 4, 32, 64, 512, 0, 128, 128, 1)])
+    # a 32-wide reader with ranks above the resident decoder's 384 runs the
+    # key-chunk kernel, not the staged plan; with the camera and ranks up to
+    # 384 it is staged
+    rc, err, _ = _check([(1, 4, 32, 64, 512, 0, 448, 128, 1)])
     assert rc == _lib.NKV_ERR_INVALID and "not staged" in err
+    assert _check([(1, 4, 32, 64, 512, 0, 384, 128, 1)])[0] == _lib.NKV_OK
