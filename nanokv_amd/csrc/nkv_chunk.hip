@@ -1375,6 +1375,18 @@ __device__ __forceinline__ void tile_xform(TXformSmem& sm, const ChunkParams& p,
     };
     uint32_t kx[TX_GROUP];
     if (rope || kcam) load_group(0, kx);
+    // V^T: wave v takes blocks j = 4 v .. 4 v + 4 (sub-frames 0 .. 3), rows
+    // 8 j .. 8 j + 8 at key columns 2 lane, 2 lane + 1, each block's rows
+    // loaded one block ahead (the first with K's); the finite columns of
+    // keys past the last row are never attended
+    const int lane = t & 63, v = t >> 6;
+    uint32_t* vw = reinterpret_cast<uint32_t*>(img + TF::K_IMG) + lane;
+    auto load_v = [&](int jj, uint32_t (&vx)[8]) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) vx[e] = vw[(8 * (4 * v + jj) + e) * (FT_ROW / 2)];
+    };
+    uint32_t vx[8];
+    if (cam) load_v(0, vx);
     // each key's tables, once (keys past the last row take key 0's)
     if (t < FT_T) {
         const int64_t row = history_row(p, tok0 + (t < valid ? t : 0));
@@ -1436,20 +1448,14 @@ __device__ __forceinline__ void tile_xform(TXformSmem& sm, const ChunkParams& p,
         }
     }
     if (cam) {
-        // wave v takes blocks j = 4 v .. 4 v + 4 (sub-frames 0 .. 3) of V^T:
-        // rows 8 j .. 8 j + 8 at key columns 2 lane, 2 lane + 1; the finite
-        // columns of keys past the last row are never attended
-        const int lane = t & 63, v = t >> 6;
-        uint32_t* vw = reinterpret_cast<uint32_t*>(img + TF::K_IMG) + lane;
         const double* mk[2];
 #pragma unroll
         for (int c = 0; c < 2; ++c) mk[c] = sm.mats[vt_col(2 * lane + c)];
-#pragma unroll 1
+#pragma unroll
         for (int jj = 0; jj < 4; ++jj) {
             const int j = 4 * v + jj;
-            uint32_t vx[8];
-#pragma unroll
-            for (int e = 0; e < 8; ++e) vx[e] = vw[(8 * j + e) * (FT_ROW / 2)];
+            uint32_t vn[8];
+            if (jj < 3) load_v(jj + 1, vn);
 #pragma unroll
             for (int c = 0; c < 2; ++c) {
                 const int sh = 16 * c;
@@ -1470,6 +1476,10 @@ __device__ __forceinline__ void tile_xform(TXformSmem& sm, const ChunkParams& p,
             }
 #pragma unroll
             for (int e = 0; e < 8; ++e) vw[(8 * j + e) * (FT_ROW / 2)] = vx[e];
+            if (jj < 3) {
+#pragma unroll
+                for (int e = 0; e < 8; ++e) vx[e] = vn[e];
+            }
         }
     }
 }

@@ -217,47 +217,68 @@ __global__ void __launch_bounds__(256) group_merge_kernel(
     if (lse_out && part == 0) lse_out[((int64_t)b * H + h) * Q + q] = l;
 }
 
-// The reader queries' read-time transforms in one pass, q_low [B, Q, nh, d]
-// bf16 written in place, or from the layer's queries src[b, t, heads[i]]
-// (an identity q_reduce, d == D) when src is given: RoPE rotates pair p of
-// head i by original pair pos.pairs[i * d/2 + p] (null: p) at the position of
-// query t (rope_selected, CN/core.py:75-91), then the camera multiplies the
-// two 4-vectors of 8-dim block j -- its dims {0, 2, 4, 6} and {1, 3, 5, 7} --
-// by sub-frame cams[i * d/8 + j] (null: j % 4) of query t's matrices
-// (camera_selected, CN/core.py:110-137).  One thread per (b, t, i, block):
-// one 16-byte load and store.
-__global__ void __launch_bounds__(256) query_low_kernel(uint16_t* q_low, const uint16_t* src,
-                                                        int64_t s_b, int64_t s_t, int64_t s_h,
-                                                        const int32_t* heads, int H, int B,
-                                                        int64_t Q, int nh, int d, RopeDev pos,
-                                                        CameraDev cam, const int32_t* cams) {
-    const int nbk = d / 8;
-    const int64_t tid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (tid >= (int64_t)B * Q * nh * nbk) return;
+// The reader queries' read-time transforms in one pass over up to QL_MAX
+// reader groups: q_low [B, Q, nh, d] bf16 of each group written in place, or
+// from the layer's queries src[b, t, heads[i]] (an identity q_reduce, d ==
+// D) when the group's src is given.  RoPE rotates pair p of head i by
+// original pair pairs[i * d/2 + p] (null: p) at the position of query t
+// (rope_selected, CN/core.py:75-91), then the camera multiplies the two
+// 4-vectors of 8-dim block j -- its dims {0, 2, 4, 6} and {1, 3, 5, 7} -- by
+// sub-frame cams[i * d/8 + j] (null: j % 4) of query t's matrices
+// (camera_selected, CN/core.py:110-137).  One thread per (group, b, t, i,
+// block): one 16-byte load and store.
+constexpr int QL_MAX = 8;
+struct QueryLowGroup {
+    uint16_t* q_low;
+    const uint16_t* src;
+    const int32_t* heads;
+    const int32_t* pairs;
+    const int32_t* cams;
+    int nh, d;
+};
+struct QueryLowBatch {
+    QueryLowGroup g[QL_MAX];
+    int64_t first[QL_MAX + 1];  // first thread of each group
+    int n, H, B;
+    int64_t Q, s_b, s_t, s_h;
+    RopeDev pos;
+    CameraDev cam;
+};
+
+__global__ void __launch_bounds__(256) query_low_kernel(QueryLowBatch P) {
+    const int64_t gt = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (gt >= P.first[P.n]) return;
+    int gi = 0;
+#pragma unroll
+    for (int i = 1; i < QL_MAX; ++i)
+        if (i < P.n && gt >= P.first[i]) gi = i;
+    const QueryLowGroup& G = P.g[gi];
+    const int64_t tid = gt - P.first[gi];
+    const int nbk = G.d / 8;
     const int j = (int)(tid % nbk);
     const int64_t row = tid / nbk;  // (b, t, i)
-    const int i = (int)(row % nh);
-    const int64_t t = (row / nh) % Q;
-    const int b = (int)(row / ((int64_t)nh * Q));
-    uint16_t* dst = q_low + row * d + 8 * j;
+    const int i = (int)(row % G.nh);
+    const int64_t t = (row / G.nh) % P.Q;
+    const int b = (int)(row / ((int64_t)G.nh * P.Q));
+    uint16_t* dst = G.q_low + row * G.d + 8 * j;
     const uint16_t* from = dst;
-    if (src) {
-        const int hq = min(max(ldg(heads + i), 0), H - 1);
-        from = src + b * s_b + t * s_t + hq * s_h + 8 * j;
+    if (G.src) {
+        const int hq = min(max(ldg(G.heads + i), 0), P.H - 1);
+        from = G.src + b * P.s_b + t * P.s_t + hq * P.s_h + 8 * j;
     }
     u32x4 v = ldg(reinterpret_cast<const u32x4*>(from));
-    if (rope_on(pos)) {
-        const RopeRows rr = rope_rows(pos, t);
+    if (rope_on(P.pos)) {
+        const RopeRows rr = rope_rows(P.pos, t);
 #pragma unroll
         for (int w = 0; w < 4; ++w) {
-            const int pj = pos.pairs ? ldg(pos.pairs + (int64_t)i * (d / 2) + 4 * j + w) : 4 * j + w;
-            const f64x2 cs = ldg(reinterpret_cast<const f64x2*>(rope_entry(pos, rr, pj)));
+            const int pj = G.pairs ? ldg(G.pairs + (int64_t)i * (G.d / 2) + 4 * j + w) : 4 * j + w;
+            const f64x2 cs = ldg(reinterpret_cast<const f64x2*>(rope_entry(P.pos, rr, pj)));
             v[w] = rope_pair(v[w], cs.x, cs.y);
         }
     }
-    if (cam.mats) {
-        const int sub = cams ? (ldg(cams + (int64_t)i * nbk + j) & 3) : (j & 3);
-        const float* M = camera_mats(cam, b, t) + 16 * sub;
+    if (P.cam.mats) {
+        const int sub = G.cams ? (ldg(G.cams + (int64_t)i * nbk + j) & 3) : (j & 3);
+        const float* M = camera_mats(P.cam, b, t) + 16 * sub;
         float x0[4], x1[4], y0[4], y1[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -700,8 +721,9 @@ int reader_tables(hipStream_t s, const nkv_fast_args* f, int g, unsigned char* w
     const int nh = G.num_heads, dd = G.d;
     int rc = NKV_OK;
     // q_low [B, Q, nh, d] from the pre-RoPE, pre-camera queries when
-    // given, then rotated / transformed on its retained pairs and blocks;
-    // an identity q_reduce takes them through the head map in the same pass
+    // given, then rotated / transformed on its retained pairs and blocks by
+    // query_transforms (an identity q_reduce takes them through the head map
+    // in that pass)
     uint16_t* q_low = reinterpret_cast<uint16_t*>(ws + L.q_low[g]);
     const bool pre = reader_q_pre(f);
     const uint16_t* qsrc = reinterpret_cast<const uint16_t*>(pre ? f->q_pre : a.q);
@@ -713,19 +735,6 @@ int reader_tables(hipStream_t s, const nkv_fast_args* f, int g, unsigned char* w
                                    G.q_reduce, D, dd, a.B, nh, a.Q, q_low, a.Q * nh * dd, dd,
                                    (int64_t)nh * dd);
         if (rc) return rc;
-    }
-    if (!id.q && xform) {
-        RopeDev qp{};
-        if (a.rope) {
-            qp = qrope;
-            qp.pairs = G.rope_pairs;
-        }
-        const CameraDev qc = a.camera ? qcam : CameraDev{};
-        const int64_t threads = (int64_t)a.B * a.Q * nh * (dd / 8);
-        query_low_kernel<<<dim3((unsigned)cdiv(threads, 256)), 256, 0, s>>>(
-            q_low, G.q_reduce ? nullptr : qsrc, qs_b, qs_t, qs_h, G.heads, a.H, a.B, a.Q, nh, dd,
-            qp, qc, a.camera ? G.cam_blocks : nullptr);
-        NKV_LAUNCH_CHECK();
     }
     for (int cc = 0; cc < 2 && f->n_low > 0; ++cc) {
         if (cc ? id.v : id.k) continue;
@@ -752,6 +761,49 @@ int reader_tables(hipStream_t s, const nkv_fast_args* f, int g, unsigned char* w
         }
     }
     return NKV_OK;
+}
+
+// The reader queries' RoPE and camera for every group that needs them, in
+// launches of up to QL_MAX groups (after reader_tables has projected them).
+int query_transforms(hipStream_t s, const nkv_fast_args* f, unsigned char* ws,
+                     const FastLayout& L, const RopeDev& qrope, const CameraDev& qcam) {
+    const nkv_attend_args& a = f->attend;
+    if (!a.rope && !a.camera) return NKV_OK;
+    const bool pre = reader_q_pre(f);
+    QueryLowBatch P{};
+    P.H = a.H;
+    P.B = a.B;
+    P.Q = a.Q;
+    P.s_b = pre ? f->qp_sb : a.q_sb;
+    P.s_t = pre ? f->qp_st : a.q_st;
+    P.s_h = pre ? f->qp_sh : a.q_sh;
+    if (a.rope) P.pos = qrope;
+    if (a.camera) P.cam = qcam;
+    auto flush = [&]() -> int {
+        if (P.n == 0) return NKV_OK;
+        query_low_kernel<<<dim3((unsigned)cdiv(P.first[P.n], 256)), 256, 0, s>>>(P);
+        NKV_LAUNCH_CHECK();
+        P.n = 0;
+        return NKV_OK;
+    };
+    for (int g = 0; g < f->num_groups; ++g) {
+        const nkv_reader_group& G = f->groups[g];
+        if (reader_ident(f, G, L.multi).q) continue;
+        QueryLowGroup& q = P.g[P.n];
+        q.q_low = reinterpret_cast<uint16_t*>(ws + L.q_low[g]);
+        q.src = G.q_reduce ? nullptr : reinterpret_cast<const uint16_t*>(pre ? f->q_pre : a.q);
+        q.heads = G.heads;
+        q.pairs = a.rope ? G.rope_pairs : nullptr;
+        q.cams = a.camera ? G.cam_blocks : nullptr;
+        q.nh = G.num_heads;
+        q.d = G.d;
+        P.first[P.n + 1] = P.first[P.n] + (int64_t)a.B * a.Q * G.num_heads * (G.d / 8);
+        if (++P.n == QL_MAX) {
+            int rc = flush();
+            if (rc) return rc;
+        }
+    }
+    return flush();
 }
 
 }  // namespace
@@ -797,6 +849,8 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
             rc = reader_tables(s, f, g, ws, L, qrope, qcam);
             if (rc) return rc;
         }
+        rc = query_transforms(s, f, ws, L, qrope, qcam);
+        if (rc) return rc;
         ChunkLaunchDesc d[NKV_MAX_PARTS];
         const int32_t* heads[NKV_MAX_PARTS];
         const int n = multi_descs(f, ws, L, d, heads);
@@ -822,12 +876,17 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
     // no low rows: the native partition is the whole attention
     if (f->n_low == 0) return finish();
 
-    // 2-3. reader groups
+    // 2-3. reader groups: every group's tables and queries, then each
+    // group's launch and merge
+    for (int g = 0; g < f->num_groups; ++g) {
+        rc = reader_tables(s, f, g, ws, L, qrope, qcam);
+        if (rc) return rc;
+    }
+    rc = query_transforms(s, f, ws, L, qrope, qcam);
+    if (rc) return rc;
     for (int g = 0; g < f->num_groups; ++g) {
         const nkv_reader_group& G = f->groups[g];
         const int nh = G.num_heads, D = a.D;
-        rc = reader_tables(s, f, g, ws, L, qrope, qcam);
-        if (rc) return rc;
         ChunkLaunchDesc ld = low_desc(f, g, ws, L);
         add_transforms(f, &G, ld);
         rc = chunk_launch(s, ld, ws + L.partials, part_bytes);
