@@ -367,6 +367,8 @@ int nkv_decode(void* stream, const nkv_decode_args* args);
  *   k_cur   [B, Nc, H, D] (k_sb/k_st/k_sh), v_cur likewise (v_*)
  *   out     [B, Q, H, D] bf16 (o_sb/o_st/o_sh)
  *   lse     [B, H, Q] fp32 natural-log row log-sum-exp, or NULL
+ * q, out, k_cur and v_cur are read and written as 16-byte pieces: they must be
+ * 16-byte aligned with strides divisible by 8 (NKV_ERR_INVALID otherwise).
  * key/value codecs decode to HD = H * D columns; head h reads columns
  * [h*D, (h+1)*D).  An empty key set gives out = 0 and lse = -inf
  * (attention_lse, CN/core.py:48-49).  D must be 128.

@@ -508,7 +508,8 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
                            camera: Optional[ops.Camera] = None,
                            q_camera: Optional[ops.Camera] = None,
                            visibility: Optional[ops.Visibility] = None,
-                           value_mean_correction: bool = False):
+                           value_mean_correction: bool = False,
+                           out_camera: Optional[ops.Camera] = None):
     """NanoKV-Fast history attention of q [B, H, Q, D]: the protected history
     tokens (bool mask [N] over the cache) and the current chunk are attended
     at full width by every head (mg35.py:192-303), the low history tokens
@@ -516,8 +517,8 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     group (mg35.py:315-347), and the two are merged by LSE (CN:33-42, 308).
     Everything runs in one nkv_fast_attend call: every partition's history
     tiles are decoded once into the call's workspace (the staged schedule)
-    or into LDS (the key-chunk kernel, reader groups with the camera); no
-    K/V tensor is produced.
+    or into LDS (the key-chunk kernel, reader ranks above 384); no K/V tensor
+    is produced.
     Scale: native_dim ** -0.5 (CN:287).
     RoPE (mg35.py:207-214, 305-336): rope = kv_rope(...) or an ops.RopeTable
     of the cached rows; q is then the rotated query, q_pre [B, H, Q, D] the
@@ -525,8 +526,9 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
     the current chunk's queries (query t at row t).
     Camera (mg35.py:253-257, 310-346): camera = kv_camera(P_inv, ...) of the
     cached rows and q_camera the P^T of the query rows; q, k_cur and v_cur are
-    then already transformed, q_pre is not, and the caller applies P to the
-    output.  visibility: which current keys each query sees.
+    then already transformed, q_pre is not; out_camera, P of the query rows,
+    goes on the merged output inside the call (None: the caller applies P).
+    visibility: which current keys each query sees.
     value_mean_correction: LingBot's first-moment correction of the low
     values of groups with a low-rank value lift (value_mean_shift)."""
     device = q.device
@@ -563,6 +565,6 @@ def fast_history_attention(q: torch.Tensor, cache_k: Any, cache_v: Any,
                                return_lse=return_lse, rope=rope, q_pre=qp, q_rope=q_rope,
                                camera=camera, q_camera=q_camera,
                                visibility=visibility if kc is not None else None,
-                               low_shift=shift)
+                               low_shift=shift, out_camera=out_camera)
     out = out.permute(0, 2, 1, 3)
     return (out, lse) if return_lse else out
