@@ -244,7 +244,7 @@ def rollout(args, device) -> dict:
     projection with a residual, and the commit of the chunk's K and V to the
     layer's cache.  Compressed: history in the INT4 codec (config-1 codec:
     r=384, group-32 fp16 scales, 256 centers), fused nkv_attend, commit =
-    nkv_encode of the chunk into a ring slot.  Uncompressed: bf16 K/V ring of
+    one nkv_encode_batch of the chunk's bf16 K and V into a ring slot.  Uncompressed: bf16 K/V ring of
     17 frames (history plus the chunk), nkv_attend over uncompressed keys, and
     (unless --no-sdpa) torch's flash attention over the same ring."""
     import torch
@@ -305,7 +305,7 @@ def rollout(args, device) -> dict:
                               group=sh.G, ids=e["ids"][None], centers=cent[None])
             rings.append((e, enc, cent, codec))
         comp.append(rings)
-    coeff = torch.empty(T, sh.rK, device=device, dtype=torch.float32)
+    coeffs = [torch.empty(T, sh.rK, device=device, dtype=torch.float32) for _ in range(2)]
     obuf = torch.empty(1, T, H, D, device=device, dtype=bf16)
     q0 = h0.view(1, T, H, D)
     ws = torch.empty(max(ops.attend_workspace_size(q0, N, T, comp[0][0][3], comp[0][1][3]), 1),
@@ -325,11 +325,14 @@ def rollout(args, device) -> dict:
             marks.append(("attend", b, ev()))
             b = ev()
         sl = slice(slot * T, (slot + 1) * T)
-        for (e, enc, cent, codec), x in ((rk, k), (rv, v)):
-            ops.encode(x.reshape(T, HD).float(), enc, centers=cent, group=sh.G,
-                       scale_dtype=sh.scale_dtype,
-                       out={"packed": e["packed"][sl], "scales": e["scales"][sl],
-                            "ids": e["ids"][sl], "coeff": coeff})
+        # K and V in one batched encode, read as bf16 straight from the
+        # projection's output (strided views of qkv)
+        ops.encode_batch([{"x": qkv[:, i * HD:(i + 1) * HD], "w_enc": enc, "centers": cent,
+                           "out": {"packed": e["packed"][sl], "scales": e["scales"][sl],
+                                   "ids": e["ids"][sl], "coeff": c}}
+                          for i, (e, enc, cent, codec), c in ((1, rk, coeffs[0]),
+                                                              (2, rv, coeffs[1]))],
+                         group=sh.G, scale_dtype=sh.scale_dtype)
         if marks is not None:
             marks.append(("encode", b, ev()))
         return h + obuf.view(T, HD) @ w_o[li].T

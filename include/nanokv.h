@@ -313,9 +313,25 @@ typedef struct nkv_encode_args {
     float* coeff;                 /* out [rows, r] fp32 */
     uint8_t* packed;              /* out [rows, r/2] */
     uint16_t* scales;             /* out [rows, r/group] */
+    /* bf16 rows in place of x (read as the reference's value.float(), which
+     * is exact), or NULL; needs HD % 256 == 0, HD <= 8192, at most 256
+     * centers to search and 16-byte aligned rows. */
+    const uint16_t* x_bf16;
+    int64_t x_stride;             /* elements between rows of x / x_bf16; 0 = HD */
 } nkv_encode_args;
 
 int nkv_encode(void* stream, const nkv_encode_args* args);
+
+/*
+ * n (1..8) independent encodes of one shape in one launch per stage (the
+ * K and V of a layer, batch items): every problem has its own rows, inputs,
+ * operator, centers, mean and outputs, and all share HD, r, group,
+ * scale_dtype, quant_mode, the center count and id type, ids_in, the input
+ * dtype and whether a mean is given.  Each problem's results are those of
+ * nkv_encode on it.  No counterpart in the reference (encode_tensor, MG:
+ * 333-365, encodes one tensor per call).
+ */
+int nkv_encode_batch(void* stream, const nkv_encode_args* args, int n);
 
 /*
  * Per-chunk C64 center fit (semantic_residual, MG:301-330), per batch item:

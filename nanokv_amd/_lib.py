@@ -31,7 +31,7 @@ NKV_SCHEDULE_KEY_CHUNKS = 2
 # Every symbol include/nanokv.h declares (checked by tests/test_abi.py).
 EXPORTED = (
     "nkv_abi_version", "nkv_last_error", "nkv_quant_pack", "nkv_unpack", "nkv_assign",
-    "nkv_encode", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
+    "nkv_encode", "nkv_encode_batch", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
     "nkv_fast_attend_workspace_size", "nkv_fast_attend", "nkv_rope_apply", "nkv_int8_pack",
     "nkv_int8_dequant", "nkv_c64_fit_workspace_size", "nkv_c64_fit", "nkv_camera_apply",
     "nkv_attend_static", "nkv_lift_lse_combine", "nkv_finish",
@@ -65,6 +65,7 @@ class NkvEncodeArgs(Structure):
         ("id_bytes", c_int), ("ids_in", c_int),
         ("x", c_void_p), ("centers", c_void_p), ("mean", c_void_p), ("w_enc", c_void_p),
         ("ids", c_void_p), ("coeff", c_void_p), ("packed", c_void_p), ("scales", c_void_p),
+        ("x_bf16", c_void_p), ("x_stride", c_int64),
     ]
 
 
@@ -193,6 +194,8 @@ def _declare(lib: ctypes.CDLL) -> None:
                                c_int]
     lib.nkv_encode.restype = c_int
     lib.nkv_encode.argtypes = [c_void_p, POINTER(NkvEncodeArgs)]
+    lib.nkv_encode_batch.restype = c_int
+    lib.nkv_encode_batch.argtypes = [c_void_p, POINTER(NkvEncodeArgs), c_int]
     lib.nkv_decode.restype = c_int
     lib.nkv_decode.argtypes = [c_void_p, POINTER(NkvDecodeArgs)]
     lib.nkv_attend_workspace_size.restype = c_size_t

@@ -15,13 +15,11 @@ namespace nkv {
 // arithmetic as in HY kv_codecs.py:244-255; bf16 arithmetic as MG deploys
 // it) and _pack_int4 MG:282-292.
 template <int QUANT_MODE>
-__global__ void __launch_bounds__(256) quant_pack_kernel(const float* __restrict__ coeff,
-                                                         int64_t rows, int r, int group,
-                                                         int scale_dtype,
-                                                         uint8_t* __restrict__ packed,
-                                                         uint16_t* __restrict__ scales) {
+__device__ __forceinline__ void quant_pack_group(const float* __restrict__ coeff, int64_t rows,
+                                                 int r, int group, int scale_dtype,
+                                                 uint8_t* __restrict__ packed,
+                                                 uint16_t* __restrict__ scales, int64_t gid) {
     const int ngroups = r / group;
-    const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (gid >= rows * ngroups) return;
     const int64_t row = gid / ngroups;
     const int g = (int)(gid - row * ngroups);
@@ -65,6 +63,16 @@ __global__ void __launch_bounds__(256) quant_pack_kernel(const float* __restrict
         }
         *reinterpret_cast<uint32_t*>(out + j / 2) = word;
     }
+}
+
+template <int QUANT_MODE>
+__global__ void __launch_bounds__(256) quant_pack_kernel(const float* __restrict__ coeff,
+                                                         int64_t rows, int r, int group,
+                                                         int scale_dtype,
+                                                         uint8_t* __restrict__ packed,
+                                                         uint16_t* __restrict__ scales) {
+    quant_pack_group<QUANT_MODE>(coeff, rows, r, group, scale_dtype, packed, scales,
+                                 (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
 // ============================================================ unpack
@@ -371,10 +379,77 @@ __global__ void __launch_bounds__(256) assign_mfma_kernel(const float* __restric
 constexpr int AB_ROWS = 32, AB_KC = 128, AB_SEG = 256, AB_MAXC = 256, AB_WAVES = 8, AB_MAXK = 16384;
 constexpr float AB_KAPPA = 2.5e-4f;
 
-template <int ID_BYTES>
-__global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(
-    const float* __restrict__ x, const uint16_t* __restrict__ centers, int64_t rows, int C, int HD,
-    void* __restrict__ ids) {
+// ------------------------------------------------ batched encode problems
+// One launch per encode stage serves up to ENC_MAXB independent problems of
+// one shape (K and V of a layer, batch items): problem blockIdx.y (search,
+// quantiser) or blockIdx.z (projection).  A problem's rows are fp32 (x) or
+// bf16 (xb, read as the reference's value.float(): exact), row stride ldx.
+constexpr int ENC_MAXB = 8;
+struct EncProb {
+    const float* x;
+    const uint16_t* xb;
+    int64_t ldx;
+    const uint16_t* centers;
+    void* ids;
+    const float* mean;
+    const uint16_t* w_enc;
+    float* coeff;
+    uint8_t* packed;
+    uint16_t* scales;
+    int64_t M;
+};
+struct EncBatch {
+    EncProb p[ENC_MAXB];
+    int n, K, r, num_centers, id_bytes;
+    // center id of row m of problem p (clamped into the table)
+    __device__ __forceinline__ int id_of(const EncProb& q, int64_t m) const {
+        int v;
+        if (id_bytes == 1) v = reinterpret_cast<const uint8_t*>(q.ids)[m];
+        else if (id_bytes == 2) v = reinterpret_cast<const uint16_t*>(q.ids)[m];
+        else v = reinterpret_cast<const int32_t*>(q.ids)[m];
+        return min(max(v, 0), num_centers - 1);
+    }
+};
+
+// Eight consecutive input values of one row (16-byte loads), held raw until
+// they are used.
+template <bool XB>
+struct X8 {
+    u32x4 w[XB ? 1 : 2];
+    __device__ __forceinline__ void load(const EncProb& q, int64_t m, int k) {
+        if constexpr (XB) {
+            w[0] = *reinterpret_cast<const u32x4*>(q.xb + m * q.ldx + k);
+        } else {
+            const float* r = q.x + m * q.ldx + k;
+            w[0] = *reinterpret_cast<const u32x4*>(r);
+            w[1] = *reinterpret_cast<const u32x4*>(r + 4);
+        }
+    }
+    __device__ __forceinline__ float operator[](int e) const {
+        if constexpr (XB)
+            return __uint_as_float((e & 1) ? (w[0][e >> 1] & 0xffff0000u) : (w[0][e >> 1] << 16));
+        else
+            return __uint_as_float(w[e >> 2][e & 3]);
+    }
+};
+
+// The quantiser over every problem of a batch (problem blockIdx.y).
+template <int QUANT_MODE>
+__global__ void __launch_bounds__(256) quant_pack_batch_kernel(EncBatch B, int group,
+                                                               int scale_dtype) {
+    const EncProb& P = B.p[blockIdx.y];
+    quant_pack_group<QUANT_MODE>(P.coeff, P.M, B.r, group, scale_dtype, P.packed, P.scales,
+                                 (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+}
+
+template <int ID_BYTES, bool XB>
+__global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(EncBatch B) {
+    const EncProb& P = B.p[blockIdx.y];
+    const int64_t rows = P.M;
+    const int C = B.num_centers, HD = B.K;
+    const uint16_t* __restrict__ centers = P.centers;
+    void* __restrict__ ids = P.ids;
+    if ((int64_t)blockIdx.x * AB_ROWS >= rows) return;
     __shared__ __align__(16) uint16_t xs[2][AB_ROWS][AB_KC + 8];
     __shared__ float xn[AB_ROWS];
     __shared__ float red[AB_WAVES][AB_ROWS];
@@ -388,7 +463,6 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(
     // fill: thread t splits row t/16, k columns 8*(t%16) .. +8 of each chunk
     const int frow = t >> 4, fk = 8 * (t & 15);
     const int64_t fr = min(row0 + frow, rows - 1);
-    const float* xrow = x + fr * HD + fk;
     const bool frow_ok = row0 + frow < rows;
     // this lane's center column
     const int col = 32 * wave + l32;
@@ -398,26 +472,18 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(
     double cn = 0.0;
     float xsq = 0.0f;
     u32x4 bcur[8], bnxt[8];
-    f32x4 xcur[2], xnxt[2];
-    auto fetch = [&](int kc, u32x4 (&b)[8], f32x4 (&xv)[2]) {
+    X8<XB> xcur, xnxt;
+    auto fetch = [&](int kc, u32x4 (&b)[8], X8<XB>& xv) {
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) b[ks] = *reinterpret_cast<const u32x4*>(crow + kc + 16 * ks);
-        xv[0] = *reinterpret_cast<const f32x4*>(xrow + kc);
-        xv[1] = *reinterpret_cast<const f32x4*>(xrow + kc + 4);
+        xv.load(P, fr, kc + fk);
     };
-    fetch(0, bcur, xcur);
-    __syncthreads();
-    for (int kc = 0; kc < HD; kc += AB_KC) {
-        // the next chunk's operands (the last chunk reloads itself), issued
-        // before this chunk's work and kept there (the fence stops the
-        // scheduler from sinking the loads next to their use)
-        const int kn = kc + AB_KC < HD ? kc + AB_KC : kc;
-        fetch(kn, bnxt, xnxt);
-        __builtin_amdgcn_sched_barrier(0);
+    // one chunk: split x into hi / lo bf16 through LDS, then the MFMAs of
+    // both passes and the column norms
+    auto body = [&](int kc, const u32x4 (&bq)[8], const X8<XB>& xq) {
         {
             // split this thread's 8 values into hi / lo bf16
-            const float v[8] = {xcur[0][0], xcur[0][1], xcur[0][2], xcur[0][3],
-                                xcur[1][0], xcur[1][1], xcur[1][2], xcur[1][3]};
+            const float v[8] = {xq[0], xq[1], xq[2], xq[3], xq[4], xq[5], xq[6], xq[7]};
             u32x4 hi, lo;
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
@@ -435,12 +501,12 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(
         for (int ks = 0; ks < 8; ++ks) {
             const bf16x8 ah = *reinterpret_cast<const bf16x8*>(&xs[0][l32][16 * ks + 8 * hf]);
             const bf16x8 al = *reinterpret_cast<const bf16x8*>(&xs[1][l32][16 * ks + 8 * hf]);
-            const bf16x8 b = as_bf16x8(bcur[ks]);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, b, acc, 0, 0, 0);
-            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, b, acc, 0, 0, 0);
+            const bf16x8 bb = as_bf16x8(bq[ks]);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(ah, bb, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(al, bb, acc, 0, 0, 0);
             // (the words go through named scalars: indexing the vector inside
             // the bit_cast was lowered to word 0 four times)
-            const uint32_t w4[4] = {bcur[ks].x, bcur[ks].y, bcur[ks].z, bcur[ks].w};
+            const uint32_t w4[4] = {bq[ks].x, bq[ks].y, bq[ks].z, bq[ks].w};
 #pragma unroll
             for (int e = 0; e < 4; ++e) {
                 const bf16x2 wv = __builtin_bit_cast(bf16x2, w4[e]);
@@ -456,10 +522,19 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(
             cseg = 0.0f;
         }
         __syncthreads();
+    };
+    // the next chunk's operands (the last chunk reloads itself), issued
+    // before this chunk's work and kept there (the fence stops the scheduler
+    // from sinking the loads next to their use)
+    fetch(0, bcur, xcur);
+    __syncthreads();
+    for (int kc = 0; kc < HD; kc += AB_KC) {
+        fetch(kc + AB_KC < HD ? kc + AB_KC : kc, bnxt, xnxt);
+        __builtin_amdgcn_sched_barrier(0);
+        body(kc, bcur, xcur);
 #pragma unroll
         for (int ks = 0; ks < 8; ++ks) bcur[ks] = bnxt[ks];
-        xcur[0] = xnxt[0];
-        xcur[1] = xnxt[1];
+        xcur = xnxt;
     }
     // ||x||^2 per row (16 threads per row), ||c||^2 per column (two k halves)
     atomicAdd(&xn[frow], frow_ok ? xsq : 0.0f);
@@ -509,7 +584,6 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(
         // (no candidate only for non-finite rows: index 0 then)
         int best = cnt[r] == 0 ? 0 : first[r];
         if (cnt[r] > 1) {
-            const float* xr = x + gr * HD;
             double bd = 0.0;
             best = -1;
             for (int w = 0; w < AB_MAXC / 32; ++w) {
@@ -522,10 +596,10 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(
                     // 8 consecutive values per lane and step (HD % 256 == 0)
                     for (int k = 8 * lane; k < HD; k += 512) {
                         const u32x4 cw = *reinterpret_cast<const u32x4*>(cr + k);
-                        const f32x4 x0 = *reinterpret_cast<const f32x4*>(xr + k);
-                        const f32x4 x1 = *reinterpret_cast<const f32x4*>(xr + k + 4);
+                        X8<XB> x8;
+                        x8.load(P, gr, k);
                         const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
-                        const float xv[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+                        const float xv[8] = {x8[0], x8[1], x8[2], x8[3], x8[4], x8[5], x8[6], x8[7]};
 #pragma unroll
                         for (int e = 0; e < 8; ++e) {
                             const uint32_t hb = (e & 1) ? (w4[e >> 1] & 0xffff0000u) : (w4[e >> 1] << 16);
@@ -707,40 +781,43 @@ __global__ void __launch_bounds__(256) encode_gemm_kernel(EncodeA al,
 // order (deterministic).  Needs HD % 256 == 0 and HD <= EP_MAXK.
 constexpr int EP_ROWS = 32, EP_TILES = 3, EP_SPLIT = 4, EP_MAXK = 8192;
 
-__global__ void __launch_bounds__(256) encode_proj_kernel(EncodeA al,
-                                                          const uint16_t* __restrict__ w_enc,
-                                                          int r, float* __restrict__ coeff) {
+template <bool XB, int SPLIT>
+__global__ void __launch_bounds__(64 * SPLIT) encode_proj_kernel(EncBatch B) {
     __shared__ float mean_s[EP_MAXK];
-    __shared__ float part[EP_SPLIT - 1][EP_TILES][16][64];
+    __shared__ float part[SPLIT - 1][EP_TILES][16][64];
+    const EncProb& P = B.p[blockIdx.z];
+    const int r = B.r;
+    float* __restrict__ coeff = P.coeff;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hf = lane >> 5, l32 = lane & 31;
     const int64_t m0 = (int64_t)blockIdx.x * EP_ROWS;
+    if (m0 >= P.M) return;
     const int n0 = blockIdx.y * (EP_TILES * 32);
-    const int K = al.K, KW = K / EP_SPLIT, kbeg = wave * KW;
-    if (al.mean) {
-        for (int k = t; k < K; k += 256) mean_s[k] = al.mean[k];
+    const int K = B.K, KW = K / SPLIT, kbeg = wave * KW;
+    if (P.mean) {
+        for (int k = t; k < K; k += 64 * SPLIT) mean_s[k] = P.mean[k];
         __syncthreads();
     }
     const int64_t m = m0 + l32;
-    const bool row_ok = m < al.M;
-    const float* xrow = al.x + (row_ok ? m : 0) * (int64_t)K + kbeg + 8 * hf;
+    const bool row_ok = m < P.M;
+    const int64_t xr = row_ok ? m : 0;
+    const int xk = kbeg + 8 * hf;
     const uint16_t* crow =
-        al.centers ? al.centers + (int64_t)(row_ok ? al.id_of(m) : 0) * K + kbeg + 8 * hf : nullptr;
+        P.centers ? P.centers + (int64_t)(row_ok ? B.id_of(P, m) : 0) * K + kbeg + 8 * hf : nullptr;
     const uint16_t* wrow[EP_TILES];
 #pragma unroll
     for (int j = 0; j < EP_TILES; ++j)
-        wrow[j] = w_enc + (int64_t)min(n0 + 32 * j + l32, r - 1) * K + kbeg + 8 * hf;
+        wrow[j] = P.w_enc + (int64_t)min(n0 + 32 * j + l32, r - 1) * K + kbeg + 8 * hf;
     // raw operands of one 64-wide k step: four 16-wide MFMA sub-steps
     struct Raw {
-        f32x4 x[4][2];
+        X8<XB> x[4];
         u32x4 c[4];
         u32x4 w[EP_TILES][4];
     };
     auto fetch = [&](int k0, Raw& rw) {
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
-            rw.x[sub][0] = *reinterpret_cast<const f32x4*>(xrow + k0 + 16 * sub);
-            rw.x[sub][1] = *reinterpret_cast<const f32x4*>(xrow + k0 + 16 * sub + 4);
+            rw.x[sub].load(P, xr, xk + k0 + 16 * sub);
             if (crow) rw.c[sub] = *reinterpret_cast<const u32x4*>(crow + k0 + 16 * sub);
 #pragma unroll
             for (int j = 0; j < EP_TILES; ++j)
@@ -756,8 +833,8 @@ __global__ void __launch_bounds__(256) encode_proj_kernel(EncodeA al,
         if (k0 + 64 < KW) fetch(k0 + 64, nxt);
 #pragma unroll
         for (int sub = 0; sub < 4; ++sub) {
-            float v[8] = {cur.x[sub][0][0], cur.x[sub][0][1], cur.x[sub][0][2], cur.x[sub][0][3],
-                          cur.x[sub][1][0], cur.x[sub][1][1], cur.x[sub][1][2], cur.x[sub][1][3]};
+            float v[8] = {cur.x[sub][0], cur.x[sub][1], cur.x[sub][2], cur.x[sub][3],
+                          cur.x[sub][4], cur.x[sub][5], cur.x[sub][6], cur.x[sub][7]};
             if (crow) {
 #pragma unroll
                 for (int e = 0; e < 4; ++e) {
@@ -765,7 +842,7 @@ __global__ void __launch_bounds__(256) encode_proj_kernel(EncodeA al,
                     v[2 * e + 1] = v[2 * e + 1] - __uint_as_float(cur.c[sub][e] & 0xffff0000u);
                 }
             }
-            if (al.mean) {
+            if (P.mean) {
                 const int kk = kbeg + k0 + 16 * sub + 8 * hf;
 #pragma unroll
                 for (int e = 0; e < 8; ++e) v[e] = v[e] - mean_s[kk + e];
@@ -796,9 +873,9 @@ __global__ void __launch_bounds__(256) encode_proj_kernel(EncodeA al,
         for (int i = 0; i < 16; ++i) {
             float sum = acc[j][i];
 #pragma unroll
-            for (int w = 0; w < EP_SPLIT - 1; ++w) sum += part[w][j][i][lane];
+            for (int w = 0; w < SPLIT - 1; ++w) sum += part[w][j][i][lane];
             const int64_t mm = m0 + 8 * (i / 4) + 4 * hf + (i % 4);
-            if (n < r && mm < al.M) coeff[mm * r + n] = sum;
+            if (n < r && mm < P.M) coeff[mm * r + n] = sum;
         }
     }
 }
@@ -1105,21 +1182,43 @@ static int launch_assign_f32(hipStream_t s, const float* x, const float* centers
     return NKV_OK;
 }
 
+// The exact bf16-MFMA nearest-center search over every problem of a batch
+// (C <= AB_MAXC, HD % AB_SEG == 0, HD <= AB_MAXK, 16-byte aligned rows).
+static int launch_assign_batch(hipStream_t s, const EncBatch& B, bool xb) {
+    int64_t rows = 0;
+    for (int i = 0; i < B.n; ++i) rows = std::max(rows, B.p[i].M);
+    if (rows <= 0) return NKV_OK;
+    const dim3 grid((unsigned)cdiv(rows, AB_ROWS), (unsigned)B.n);
+    const unsigned threads = 64 * AB_WAVES;
+    if (xb) {
+        if (B.id_bytes == 1) assign_bf16_kernel<1, true><<<grid, threads, 0, s>>>(B);
+        else if (B.id_bytes == 2) assign_bf16_kernel<2, true><<<grid, threads, 0, s>>>(B);
+        else assign_bf16_kernel<4, true><<<grid, threads, 0, s>>>(B);
+    } else {
+        if (B.id_bytes == 1) assign_bf16_kernel<1, false><<<grid, threads, 0, s>>>(B);
+        else if (B.id_bytes == 2) assign_bf16_kernel<2, false><<<grid, threads, 0, s>>>(B);
+        else assign_bf16_kernel<4, false><<<grid, threads, 0, s>>>(B);
+    }
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
 static int launch_assign(hipStream_t s, const float* x, const uint16_t* centers, int64_t rows,
                          int C, int HD, void* ids, int id_bytes) {
     if (rows <= 0) return NKV_OK;
     if (C <= AB_MAXC && HD > 0 && HD % AB_SEG == 0 && HD <= AB_MAXK && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(centers) % 16 == 0) {
-        dim3 grid((unsigned)cdiv(rows, AB_ROWS));
-        const unsigned threads = 64 * AB_WAVES;
-        if (id_bytes == 1)
-            assign_bf16_kernel<1><<<grid, threads, 0, s>>>(x, centers, rows, C, HD, ids);
-        else if (id_bytes == 2)
-            assign_bf16_kernel<2><<<grid, threads, 0, s>>>(x, centers, rows, C, HD, ids);
-        else
-            assign_bf16_kernel<4><<<grid, threads, 0, s>>>(x, centers, rows, C, HD, ids);
-        NKV_LAUNCH_CHECK();
-        return NKV_OK;
+        EncBatch B{};
+        B.n = 1;
+        B.K = HD;
+        B.num_centers = C;
+        B.id_bytes = id_bytes;
+        B.p[0].x = x;
+        B.p[0].ldx = HD;
+        B.p[0].centers = centers;
+        B.p[0].ids = ids;
+        B.p[0].M = rows;
+        return launch_assign_batch(s, B, false);
     }
     if (HD > 0 && HD % 16 == 0 && reinterpret_cast<uintptr_t>(x) % 16 == 0 &&
         reinterpret_cast<uintptr_t>(centers) % 8 == 0) {
@@ -1220,8 +1319,11 @@ extern "C" int nkv_assign(void* stream, const float* x, const uint16_t* centers,
     return launch_assign((hipStream_t)stream, x, centers, rows, C, HD, ids, id_bytes);
 }
 
-extern "C" int nkv_encode(void* stream, const nkv_encode_args* a) {
-    clear_error();
+namespace {
+
+// Checks of one encode problem; the batch's shape and settings are those of
+// its first problem.
+int check_encode(const nkv_encode_args* a, const nkv_encode_args* first) {
     NKV_REQUIRE(a, NKV_ERR_INVALID, "null args");
     NKV_REQUIRE(a->rows >= 0, NKV_ERR_INVALID, "rows must be >= 0");
     NKV_REQUIRE(a->HD > 0 && a->HD % 32 == 0, NKV_ERR_INVALID, "HD must be a multiple of 32");
@@ -1234,34 +1336,130 @@ extern "C" int nkv_encode(void* stream, const nkv_encode_args* a) {
         if (rc) return rc;
         NKV_REQUIRE(a->ids, NKV_ERR_INVALID, "ids required with centers");
     }
+    NKV_REQUIRE(!(a->x && a->x_bf16), NKV_ERR_INVALID, "give x or x_bf16, not both");
+    NKV_REQUIRE(a->x_stride == 0 || a->x_stride >= a->HD, NKV_ERR_INVALID,
+                "x_stride must be 0 or at least HD");
+    if (first != a) {
+        NKV_REQUIRE(a->HD == first->HD && a->r == first->r && a->group == first->group &&
+                        a->scale_dtype == first->scale_dtype &&
+                        a->quant_mode == first->quant_mode &&
+                        (a->centers != nullptr) == (first->centers != nullptr) &&
+                        a->num_centers == first->num_centers && a->id_bytes == first->id_bytes &&
+                        a->ids_in == first->ids_in &&
+                        (a->x_bf16 != nullptr) == (first->x_bf16 != nullptr) &&
+                        (a->mean != nullptr) == (first->mean != nullptr),
+                    NKV_ERR_INVALID,
+                    "the problems of one encode batch must share HD, r, group, scale and quant "
+                    "settings, center count and id type, and the input dtype");
+    }
     if (a->rows == 0) return NKV_OK;
-    NKV_REQUIRE(a->x && a->w_enc && a->coeff && a->packed && a->scales, NKV_ERR_INVALID,
-                "null pointer");
-    hipStream_t s = (hipStream_t)stream;
-    if (a->centers && !a->ids_in) {
-        rc = launch_assign(s, a->x, a->centers, a->rows, a->num_centers, a->HD, a->ids,
-                           a->id_bytes);
+    NKV_REQUIRE((a->x || a->x_bf16) && a->w_enc && a->coeff && a->packed && a->scales,
+                NKV_ERR_INVALID, "null pointer");
+    return NKV_OK;
+}
+
+int encode_batch(hipStream_t s, const nkv_encode_args* a, int n) {
+    NKV_REQUIRE(a && n >= 1 && n <= ENC_MAXB, NKV_ERR_INVALID, "1..8 encode problems");
+    for (int i = 0; i < n; ++i) {
+        int rc = check_encode(a + i, a);
         if (rc) return rc;
     }
-    EncodeA al;
-    al.x = a->x;
-    al.centers = a->centers;
-    al.ids = a->ids;
-    al.id_bytes = a->id_bytes;
-    al.num_centers = a->num_centers;
-    al.mean = a->mean;
-    al.M = a->rows;
-    al.K = a->HD;
-    if (a->HD % (EP_SPLIT * 64) == 0 && a->HD <= EP_MAXK) {
-        dim3 grid((unsigned)cdiv(a->rows, EP_ROWS), (unsigned)cdiv(a->r, EP_TILES * 32));
-        encode_proj_kernel<<<grid, 256, 0, s>>>(al, a->w_enc, a->r, a->coeff);
-    } else {
-        dim3 grid((unsigned)cdiv(a->rows, GT_M), (unsigned)cdiv(a->r, GT_N));
-        encode_gemm_kernel<<<grid, 256, 0, s>>>(al, a->w_enc, a->r, a->coeff);
+    const int HD = a->HD, r = a->r;
+    const bool xb = a->x_bf16 != nullptr;
+    EncBatch B{};
+    B.n = n;
+    B.K = HD;
+    B.r = r;
+    B.num_centers = a->num_centers;
+    B.id_bytes = a->id_bytes;
+    bool aligned = true;
+    int64_t rows = 0;
+    for (int i = 0; i < n; ++i) {
+        const nkv_encode_args& q = a[i];
+        EncProb& P = B.p[i];
+        P.x = q.x;
+        P.xb = q.x_bf16;
+        P.ldx = q.x_stride ? q.x_stride : HD;
+        P.centers = q.centers;
+        P.ids = q.ids;
+        P.mean = q.mean;
+        P.w_enc = q.w_enc;
+        P.coeff = q.coeff;
+        P.packed = q.packed;
+        P.scales = q.scales;
+        P.M = q.rows;
+        rows = std::max(rows, q.rows);
+        const uintptr_t xp = reinterpret_cast<uintptr_t>(xb ? (const void*)q.x_bf16 : (const void*)q.x);
+        aligned = aligned && xp % 16 == 0 && (P.ldx * (xb ? 2 : 4)) % 16 == 0 &&
+                  (!q.centers || reinterpret_cast<uintptr_t>(q.centers) % 16 == 0);
     }
+    if (rows == 0) return NKV_OK;
+    // the batched kernels: the exact bf16-MFMA search (C <= 256) and the
+    // K-split projection; a bf16 input takes only those
+    const bool fast_search = a->num_centers <= AB_MAXC && HD % AB_SEG == 0 && HD <= AB_MAXK;
+    const bool fast_proj = HD % (EP_SPLIT * 64) == 0 && HD <= EP_MAXK;
+    const bool search = a->centers && !a->ids_in;
+    NKV_REQUIRE(!xb || (aligned && fast_proj && (!search || fast_search)), NKV_ERR_UNSUPPORTED,
+                "a bf16 input needs HD % 256 == 0, HD <= 8192, at most 256 centers to search, and "
+                "16-byte aligned rows");
+    int rc = NKV_OK;
+    if (search) {
+        if (fast_search && aligned) {
+            rc = launch_assign_batch(s, B, xb);
+        } else {
+            for (int i = 0; i < n && !rc; ++i) {
+                NKV_REQUIRE(B.p[i].ldx == HD, NKV_ERR_UNSUPPORTED,
+                            "a strided fp32 input needs HD % 256 == 0, at most 256 centers and "
+                            "16-byte aligned rows");
+                rc = launch_assign(s, B.p[i].x, B.p[i].centers, B.p[i].M, B.num_centers, HD,
+                                   B.p[i].ids, B.id_bytes);
+            }
+        }
+        if (rc) return rc;
+    }
+    if (fast_proj && aligned) {
+        const dim3 grid((unsigned)cdiv(rows, EP_ROWS), (unsigned)cdiv(r, EP_TILES * 32), (unsigned)n);
+        if (xb) encode_proj_kernel<true, EP_SPLIT><<<grid, 64 * EP_SPLIT, 0, s>>>(B);
+        else encode_proj_kernel<false, EP_SPLIT><<<grid, 64 * EP_SPLIT, 0, s>>>(B);
+        NKV_LAUNCH_CHECK();
+    } else {
+        for (int i = 0; i < n; ++i) {
+            if (B.p[i].M == 0) continue;
+            NKV_REQUIRE(B.p[i].ldx == HD, NKV_ERR_UNSUPPORTED,
+                        "a strided fp32 input needs HD % 256 == 0 and 16-byte aligned rows");
+            EncodeA al;
+            al.x = B.p[i].x;
+            al.centers = B.p[i].centers;
+            al.ids = B.p[i].ids;
+            al.id_bytes = B.id_bytes;
+            al.num_centers = B.num_centers;
+            al.mean = B.p[i].mean;
+            al.M = B.p[i].M;
+            al.K = HD;
+            dim3 grid((unsigned)cdiv(al.M, GT_M), (unsigned)cdiv(r, GT_N));
+            encode_gemm_kernel<<<grid, 256, 0, s>>>(al, B.p[i].w_enc, r, B.p[i].coeff);
+            NKV_LAUNCH_CHECK();
+        }
+    }
+    const dim3 qgrid((unsigned)cdiv(rows * (r / a->group), 256), (unsigned)n);
+    if (a->quant_mode == NKV_QUANT_BF16)
+        quant_pack_batch_kernel<NKV_QUANT_BF16><<<qgrid, 256, 0, s>>>(B, a->group, a->scale_dtype);
+    else
+        quant_pack_batch_kernel<NKV_QUANT_FP32><<<qgrid, 256, 0, s>>>(B, a->group, a->scale_dtype);
     NKV_LAUNCH_CHECK();
-    return nkv_quant_pack(stream, a->coeff, a->rows, a->r, a->group, a->scale_dtype,
-                          a->quant_mode, a->packed, a->scales);
+    return NKV_OK;
+}
+
+}  // namespace
+
+extern "C" int nkv_encode(void* stream, const nkv_encode_args* a) {
+    clear_error();
+    return encode_batch((hipStream_t)stream, a, 1);
+}
+
+extern "C" int nkv_encode_batch(void* stream, const nkv_encode_args* args, int n) {
+    clear_error();
+    return encode_batch((hipStream_t)stream, args, n);
 }
 
 extern "C" int nkv_decode(void* stream, const nkv_decode_args* a) {

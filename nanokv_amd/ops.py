@@ -135,23 +135,21 @@ def assign(x: torch.Tensor, centers: torch.Tensor,
     return ids
 
 
-def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tensor] = None,
-           mean: Optional[torch.Tensor] = None, group: int = 32,
-           scale_dtype: torch.dtype = torch.bfloat16, quant_mode: str = "fp32",
-           id_dtype: Optional[torch.dtype] = None, out: Optional[dict] = None,
-           ids: Optional[torch.Tensor] = None) -> dict:
-    """Encode fp32 rows [rows, HD] with given centers (see nkv_encode).
-
-    out: optional preallocated outputs {"packed", "scales", "ids", "coeff"}
-    (contiguous, shaped like the returned ones; "ids" only with centers), so
-    that a chunk can be encoded straight into a slot of a larger cache.
-    ids: each row's center, given (no nearest-center search), e.g. the
-    labels of a C64 fit; returned as the payload's ids."""
+def _encode_args(x: torch.Tensor, w_enc: torch.Tensor, centers, mean, group, scale_dtype,
+                 quant_mode, id_dtype, out, ids):
+    """nkv_encode_args of one encode problem and its output tensors."""
     device = _require_gpu(x, w_enc, centers, mean)
-    _contig(x, torch.float32, "x")
-    _contig(w_enc, torch.bfloat16, "w_enc")
+    if x.dtype not in (torch.float32, torch.bfloat16) or x.dim() < 1 or x.stride(-1) != 1:
+        raise ValueError("x must be fp32 or bf16 rows [..., HD] with contiguous HD")
     hd = int(x.shape[-1])
-    rows = x.numel() // hd
+    if x.dim() == 2:
+        stride = int(x.stride(0)) if x.shape[0] > 1 else hd
+    elif x.is_contiguous():
+        stride = hd
+    else:
+        raise ValueError("x must be contiguous, or a 2-D view [rows, HD] with a row stride")
+    rows = x.numel() // hd if hd else 0
+    _contig(w_enc, torch.bfloat16, "w_enc")
     r = int(w_enc.shape[0])
     if w_enc.shape[1] != hd:
         raise ValueError("w_enc must be [r, HD]")
@@ -159,6 +157,7 @@ def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tens
     args.rows, args.HD, args.r, args.group = rows, hd, r, group
     args.scale_dtype = _SCALE_CODES[scale_dtype]
     args.quant_mode = _QUANT_CODES[quant_mode]
+    args.x_stride = stride
     lead = tuple(x.shape[:-1])
 
     def _out(name, shape, dtype):
@@ -195,10 +194,50 @@ def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tens
     coeff = _out("coeff", (*lead, r), torch.float32)
     packed = _out("packed", (*lead, r // 2), torch.uint8)
     scales = _out("scales", (*lead, r // group), scale_dtype)
-    args.x, args.w_enc = x.data_ptr(), w_enc.data_ptr()
+    if x.dtype == torch.bfloat16:
+        args.x_bf16 = x.data_ptr()
+    else:
+        args.x = x.data_ptr()
+    args.w_enc = w_enc.data_ptr()
     args.coeff, args.packed, args.scales = coeff.data_ptr(), packed.data_ptr(), scales.data_ptr()
+    return args, {"packed": packed, "scales": scales, "ids": ids, "coeff": coeff}, device
+
+
+def encode(x: torch.Tensor, w_enc: torch.Tensor, *, centers: Optional[torch.Tensor] = None,
+           mean: Optional[torch.Tensor] = None, group: int = 32,
+           scale_dtype: torch.dtype = torch.bfloat16, quant_mode: str = "fp32",
+           id_dtype: Optional[torch.dtype] = None, out: Optional[dict] = None,
+           ids: Optional[torch.Tensor] = None) -> dict:
+    """Encode rows [rows, HD] with given centers (see nkv_encode).
+
+    x: fp32, or bf16 (read as value.float(), exact; needs HD % 256 == 0 and
+    at most 256 centers to search); a 2-D x may be a view with a row stride.
+    out: optional preallocated outputs {"packed", "scales", "ids", "coeff"}
+    (contiguous, shaped like the returned ones; "ids" only with centers), so
+    that a chunk can be encoded straight into a slot of a larger cache.
+    ids: each row's center, given (no nearest-center search), e.g. the
+    labels of a C64 fit; returned as the payload's ids."""
+    args, res, device = _encode_args(x, w_enc, centers, mean, group, scale_dtype, quant_mode,
+                                     id_dtype, out, ids)
     check("nkv_encode", lib().nkv_encode(_stream(device), byref(args)))
-    return {"packed": packed, "scales": scales, "ids": ids, "coeff": coeff}
+    return res
+
+
+def encode_batch(problems: list, *, group: int = 32, scale_dtype: torch.dtype = torch.bfloat16,
+                 quant_mode: str = "fp32") -> list:
+    """Up to 8 encodes of one shape in one launch per stage (nkv_encode_batch),
+    e.g. the K and V rows of a layer's chunk.  problems: dicts of encode's
+    arguments (x, w_enc, and optionally centers, mean, id_dtype, out, ids);
+    returns encode's result for each."""
+    if not 1 <= len(problems) <= 8:
+        raise ValueError("encode_batch takes 1 to 8 problems")
+    built = [_encode_args(p["x"], p["w_enc"], p.get("centers"), p.get("mean"), group,
+                          scale_dtype, quant_mode, p.get("id_dtype"), p.get("out"), p.get("ids"))
+             for p in problems]
+    arr = (NkvEncodeArgs * len(built))(*(b[0] for b in built))
+    device = built[0][2]
+    check("nkv_encode_batch", lib().nkv_encode_batch(_stream(device), arr, len(built)))
+    return [b[1] for b in built]
 
 
 # ---------------------------------------------------------------- codec view

@@ -203,6 +203,51 @@ def test_encode_into_cache_slot(dev):
         ops.encode(x, layer.w_enc_k.to(dev), **kw, out={"packed": cache["packed"][:100]})
 
 
+@pytest.mark.parametrize("with_mean", [False, True])
+def test_encode_batch_equals_single_encodes(dev, with_mean):
+    """nkv_encode_batch: three problems of one shape with their own rows
+    (ragged counts), operators, centers and means give, each, the bits of
+    nkv_encode on that problem; a bf16 input, also as a strided view, gives
+    the bits of the fp32 encode of its values (value.float() is exact)."""
+    shape = synth.Shape("t", H=4, D=128, N=0, Q=0, Nc=0, rK=384, rV=384, G=32, C=64)
+    probs, singles = [], []
+    for i, n in enumerate((300, 77, 129)):
+        layer = synth.make_layer(shape, seed=20 + i, with_mean=with_mean)
+        x = synth.history_rows(shape, layer.centers_k, n, seed=30 + i).to(dev)
+        kw = dict(w_enc=layer.w_enc_k.to(dev), centers=layer.centers_k.to(dev),
+                  mean=None if layer.mean_k is None else layer.mean_k.to(dev))
+        probs.append(dict(x=x, **kw))
+        singles.append(ops.encode(x, **kw, group=32, scale_dtype=torch.float16))
+    got = ops.encode_batch(probs, group=32, scale_dtype=torch.float16)
+    for g, r in zip(got, singles):
+        for k in ("packed", "scales", "ids", "coeff"):
+            assert torch.equal(g[k], r[k]), k
+    # bf16 rows: contiguous, and strided views of one [rows, 3 HD] buffer
+    xb = [p["x"].to(torch.bfloat16) for p in probs]
+    wide = [torch.zeros(b.shape[0], 3 * b.shape[1], dtype=torch.bfloat16, device=dev) for b in xb]
+    for w, b in zip(wide, xb):
+        w[:, 512:1024] = b
+    for inputs in (xb, [w[:, 512:1024] for w in wide]):
+        got = ops.encode_batch([dict(p, x=b) for p, b in zip(probs, inputs)], group=32,
+                               scale_dtype=torch.float16)
+        for g, p, b in zip(got, probs, xb):
+            r = ops.encode(b.float(), **{k: v for k, v in p.items() if k != "x"}, group=32,
+                           scale_dtype=torch.float16)
+            for k in ("packed", "scales", "ids", "coeff"):
+                assert torch.equal(g[k], r[k]), k
+
+
+def test_encode_batch_rejects_mixed_problems(dev):
+    shape = synth.Shape("t", H=4, D=128, N=0, Q=0, Nc=0, rK=384, rV=384, G=32, C=64)
+    layer = synth.make_layer(shape, seed=3)
+    x = synth.history_rows(shape, layer.centers_k, 40, seed=4).to(dev)
+    p = dict(x=x, w_enc=layer.w_enc_k.to(dev), centers=layer.centers_k.to(dev))
+    with pytest.raises(Exception, match="share"):
+        ops.encode_batch([p, dict(p, centers=None)], group=32)
+    with pytest.raises(Exception, match="share"):
+        ops.encode_batch([p, dict(p, x=x.to(torch.bfloat16))], group=32)
+
+
 @pytest.mark.parametrize("with_mean,id_dtype", [(False, torch.uint8), (True, torch.int16)])
 def test_decode_parity(dev, with_mean, id_dtype):
     from tests._helpers import Scenario

@@ -123,16 +123,24 @@ def test_cfg4_rollout_slice(dev):
             assert diff <= MAX_ABS and cos >= MIN_COS, (li, diff, cos)
             assert np.abs(lse[0][heads].cpu().numpy() - ref_lse).max() < 2e-3
         check()
-        # the commit: the chunk's K / V encoded into frame slot 5 of the history
+        # the commit, as bench.py --config 4 runs it: the chunk's bf16 K and V,
+        # strided views of one [T, 3 HD] projection output, encoded in one
+        # batched call into frame slot 5 of the history
         slot = slice(5 * T, 6 * T)
-        coeff = torch.empty(T, sh.rK, device=dev, dtype=torch.float32)
-        for (e, enc, cent, dec), x in zip(ring, (k, v)):
-            ops.encode(x, enc, centers=cent, group=G, scale_dtype=sh.scale_dtype,
-                       out={"packed": e["packed"][slot], "scales": e["scales"][slot],
-                            "ids": e["ids"][slot], "coeff": coeff})
-            ref = orc.encode(x.cpu().numpy(), u16(enc), u16(cent), None, G, "fp16", "fp32")
+        qkv = torch.empty(T, 3 * HD, device=dev, dtype=torch.bfloat16)
+        qkv[:, HD:2 * HD] = kb.view(T, HD)
+        qkv[:, 2 * HD:] = vb.view(T, HD)
+        views = (qkv[:, HD:2 * HD], qkv[:, 2 * HD:])
+        coeffs = [torch.empty(T, sh.rK, device=dev, dtype=torch.float32) for _ in range(2)]
+        ops.encode_batch([{"x": x, "w_enc": enc, "centers": cent,
+                           "out": {"packed": e["packed"][slot], "scales": e["scales"][slot],
+                                   "ids": e["ids"][slot], "coeff": c}}
+                          for (e, enc, cent, dec), x, c in zip(ring, views, coeffs)],
+                         group=G, scale_dtype=sh.scale_dtype)
+        for (e, enc, cent, dec), x, c in zip(ring, views, coeffs):
+            ref = orc.encode(x.float().cpu().numpy(), u16(enc), u16(cent), None, G, "fp16", "fp32")
             assert np.array_equal(e["ids"][slot].cpu().numpy().astype(np.int64), ref["ids"])
-            rp, rs, _ = orc.quant_pack(coeff.cpu().numpy(), G, "fp16", "fp32")
+            rp, rs, _ = orc.quant_pack(c.cpu().numpy(), G, "fp16", "fp32")
             assert np.array_equal(e["packed"][slot].cpu().numpy(), rp)
             assert np.array_equal(u16(e["scales"][slot]), rs)
         check()
