@@ -64,7 +64,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 5
+#define NKV_ABI_VERSION 6
 
 enum nkv_status {
     NKV_OK = 0,

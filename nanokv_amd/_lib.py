@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libnanokv_hip.so"
 
-NKV_ABI_VERSION = 5
+NKV_ABI_VERSION = 6
 NKV_OK = 0
 NKV_ERR_INVALID = -1
 NKV_ERR_UNSUPPORTED = -2
