@@ -314,8 +314,8 @@ typedef struct nkv_encode_args {
     uint8_t* packed;              /* out [rows, r/2] */
     uint16_t* scales;             /* out [rows, r/group] */
     /* bf16 rows in place of x (read as the reference's value.float(), which
-     * is exact), or NULL; needs HD % 256 == 0, HD <= 8192, at most 256
-     * centers to search and 16-byte aligned rows. */
+     * is exact), or NULL; needs HD % 256 == 0 and 16-byte aligned rows,
+     * and to search, at most 256 centers and HD <= 16384. */
     const uint16_t* x_bf16;
     int64_t x_stride;             /* elements between rows of x / x_bf16; 0 = HD */
 } nkv_encode_args;

@@ -180,22 +180,6 @@ constexpr int DS_AHEAD = 3;
 static_assert(DS_NBUF * CK_D * 64 <= CK_T * CK_KROW, "decoder staging must fit in the K region");
 static_assert(CK_T * CK_D <= CK_T * CK_KROW, "V centers are staged in the K region");
 
-#define NKV_LDS(p) ((__attribute__((address_space(3))) void*)(p))
-
-// one 16-byte-per-lane global -> LDS DMA (the 64 lanes fill 1 KB at l); a
-// function of its own so that kernel templates name no target builtin in
-// their bodies (the host pass then instantiates them for every width)
-__device__ __forceinline__ void dma16(const void* g, void* l) {
-    __builtin_amdgcn_global_load_lds(g, NKV_LDS(l), 16, 0, 0);
-}
-
-// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits [3:0] and [15:14]; the
-// other counters at their maxima, i.e. not waited on)
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-    static_assert(N >= 0 && N < 64, "vmcnt out of range");
-    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
-}
 
 // --------------------------------------------------------------- attention
 // The d walk of the score product S^T = K Q^T over a K/Q width DK: at

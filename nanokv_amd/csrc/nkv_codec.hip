@@ -401,6 +401,7 @@ struct EncProb {
 struct EncBatch {
     EncProb p[ENC_MAXB];
     int n, K, r, num_centers, id_bytes;
+    int64_t row_blocks;   // 32-row blocks of the largest problem (set per launch)
     // center id of row m of problem p (clamped into the table)
     __device__ __forceinline__ int id_of(const EncProb& q, int64_t m) const {
         int v;
@@ -433,6 +434,17 @@ struct X8 {
     }
 };
 
+// Work item of block blk when a launch's items are cut into eight equal runs,
+// one per XCD (blocks are dispatched to the XCDs round-robin): block blk runs
+// slot blk / 8 of XCD blk % 8.  Items that share operands (one problem's
+// centers, one W_enc column slice) are numbered together, so they meet in
+// one XCD's L2.  Blocks past the last item get an item >= items.
+__device__ __forceinline__ int64_t xcd_item(int64_t blk, int64_t items) {
+    const int64_t per = (items + 7) >> 3;
+    return (blk & 7) * per + (blk >> 3);
+}
+static inline unsigned xcd_grid(int64_t items) { return (unsigned)(8 * ((items + 7) >> 3)); }
+
 // The quantiser over every problem of a batch (problem blockIdx.y).
 template <int QUANT_MODE>
 __global__ void __launch_bounds__(256) quant_pack_batch_kernel(EncBatch B, int group,
@@ -442,24 +454,132 @@ __global__ void __launch_bounds__(256) quant_pack_batch_kernel(EncBatch B, int g
                                  (int64_t)blockIdx.x * blockDim.x + threadIdx.x);
 }
 
+// The search's small block state: ||x||^2 per row, the per-wave bounds U,
+// and each row's candidate count, first candidate and candidate bit set.
+struct AssignSmall {
+    float xn[AB_ROWS];
+    float red[AB_WAVES][AB_ROWS];
+    int cnt[AB_ROWS], first[AB_ROWS];
+    uint32_t cand[AB_ROWS][AB_MAXC / 32];
+};
+
+__device__ __forceinline__ void assign_small_init(AssignSmall& sm, int t) {
+    if (t < AB_ROWS) { sm.xn[t] = 0.0f; sm.cnt[t] = 0; sm.first[t] = 0x7fffffff; }
+    for (int e = t; e < AB_ROWS * AB_MAXC / 32; e += 64 * AB_WAVES) (&sm.cand[0][0])[e] = 0u;
+}
+
+// The decision after the products: tot (this lane's 16 dot products x.c,
+// rows 8(i/4) + 4hf + i%4 of the block, center col), cnf = ||c||^2, and
+// sm.xn complete.  Rows with one candidate are decided; the others compare
+// their candidates exactly in fp64 (one wave per row, lanes split HD).
+template <int ID_BYTES, bool XB>
+__device__ __forceinline__ void assign_finish(const EncBatch& B, const EncProb& P, AssignSmall& sm,
+                                              const f32x16& tot, float cnf, int col, int64_t row0) {
+    const int64_t rows = P.M;
+    const int C = B.num_centers, HD = B.K;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int hf = lane >> 5, l32 = lane & 31;
+    float dt[16], ee[16];
+    {
+        const float cnorm = sqrtf(cnf) * 1.001f;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+            const int r = 8 * (i / 4) + 4 * hf + (i % 4);
+            const float xnorm = sqrtf(sm.xn[r]) * 1.001f;
+            dt[i] = col < C ? cnf - 2.0f * tot[i] : INFINITY;
+            ee[i] = AB_KAPPA * (xnorm * cnorm + cnf * 1.001f);
+        }
+    }
+    // U = min over the row's columns of dt + E: a half-wave holds a row's 32 columns
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        float u = dt[i] + ee[i];
+#pragma unroll
+        for (int off = 1; off < 32; off <<= 1) u = fminf(u, __shfl_xor(u, off));
+        if (l32 == 0) sm.red[wave][8 * (i / 4) + 4 * hf + (i % 4)] = u;
+    }
+    __syncthreads();
+    // candidates: dt - E <= U
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int r = 8 * (i / 4) + 4 * hf + (i % 4);
+        float U = sm.red[0][r];
+#pragma unroll
+        for (int w = 1; w < AB_WAVES; ++w) U = fminf(U, sm.red[w][r]);
+        if (col < C && dt[i] - ee[i] <= U) {
+            atomicAdd(&sm.cnt[r], 1);
+            atomicMin(&sm.first[r], col);
+            atomicOr(&sm.cand[r][col >> 5], 1u << (col & 31));
+        }
+    }
+    __syncthreads();
+    for (int r = wave; r < AB_ROWS; r += AB_WAVES) {
+        const int64_t gr = row0 + r;
+        if (gr >= rows) continue;
+        // (no candidate only for non-finite rows: index 0 then)
+        int best = sm.cnt[r] == 0 ? 0 : sm.first[r];
+        if (sm.cnt[r] > 1) {
+            double bd = 0.0;
+            best = -1;
+            for (int w = 0; w < AB_MAXC / 32; ++w) {
+                uint32_t bits = sm.cand[r][w];
+                while (bits) {
+                    const int c = 32 * w + __builtin_ctz(bits);
+                    bits &= bits - 1;
+                    const uint16_t* cr = P.centers + (int64_t)c * HD;
+                    double cc = 0.0, xc = 0.0;
+                    // 8 consecutive values per lane and step (HD % 256 == 0), four
+                    // steps' loads issued together, summed in ascending k
+                    for (int k = 8 * lane; k < HD; k += 4 * 512) {
+                        u32x4 cw[4];
+                        X8<XB> x8[4];
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            if (k + 512 * u < HD) {
+                                cw[u] = *reinterpret_cast<const u32x4*>(cr + k + 512 * u);
+                                x8[u].load(P, gr, k + 512 * u);
+                            }
+                        }
+#pragma unroll
+                        for (int u = 0; u < 4; ++u) {
+                            if (k + 512 * u >= HD) break;
+                            const uint32_t w4[4] = {cw[u].x, cw[u].y, cw[u].z, cw[u].w};
+#pragma unroll
+                            for (int e = 0; e < 8; ++e) {
+                                const uint32_t hb = (e & 1) ? (w4[e >> 1] & 0xffff0000u) : (w4[e >> 1] << 16);
+                                const double cv = (double)__uint_as_float(hb);
+                                cc = fma(cv, cv, cc);
+                                xc = fma((double)x8[u][e], cv, xc);
+                            }
+                        }
+                    }
+#pragma unroll
+                    for (int off = 1; off < 64; off <<= 1) {
+                        cc += __shfl_xor(cc, off);
+                        xc += __shfl_xor(xc, off);
+                    }
+                    const double d = cc - 2.0 * xc;
+                    if (best < 0 || d < bd) { bd = d; best = c; }  // ascending c: first index on ties
+                }
+            }
+        }
+        if (lane == 0) store_id<ID_BYTES>(P.ids, gr, best);
+    }
+}
+
 template <int ID_BYTES, bool XB>
 __global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(EncBatch B) {
     const EncProb& P = B.p[blockIdx.y];
     const int64_t rows = P.M;
     const int C = B.num_centers, HD = B.K;
     const uint16_t* __restrict__ centers = P.centers;
-    void* __restrict__ ids = P.ids;
     if ((int64_t)blockIdx.x * AB_ROWS >= rows) return;
     __shared__ __align__(16) uint16_t xs[2][AB_ROWS][AB_KC + 8];
-    __shared__ float xn[AB_ROWS];
-    __shared__ float red[AB_WAVES][AB_ROWS];
-    __shared__ int cnt[AB_ROWS], first[AB_ROWS];
-    __shared__ uint32_t cand[AB_ROWS][AB_MAXC / 32];
+    __shared__ AssignSmall sm;
     const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
     const int hf = lane >> 5, l32 = lane & 31;
     const int64_t row0 = (int64_t)blockIdx.x * AB_ROWS;
-    if (t < AB_ROWS) { xn[t] = 0.0f; cnt[t] = 0; first[t] = 0x7fffffff; }
-    for (int e = t; e < AB_ROWS * AB_MAXC / 32; e += 64 * AB_WAVES) (&cand[0][0])[e] = 0u;
+    assign_small_init(sm, t);
     // fill: thread t splits row t/16, k columns 8*(t%16) .. +8 of each chunk
     const int frow = t >> 4, fk = 8 * (t & 15);
     const int64_t fr = min(row0 + frow, rows - 1);
@@ -537,89 +657,141 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(EncBatch B) 
         xcur = xnxt;
     }
     // ||x||^2 per row (16 threads per row), ||c||^2 per column (two k halves)
-    atomicAdd(&xn[frow], frow_ok ? xsq : 0.0f);
+    atomicAdd(&sm.xn[frow], frow_ok ? xsq : 0.0f);
     cn += __shfl_xor(cn, 32);
     const float cnf = (float)cn;
     __syncthreads();
-    // tot element i: row 8(i/4) + 4hf + i%4, column col
-    float dt[16], ee[16];
-    {
-        const float cnorm = sqrtf(cnf) * 1.001f;
+    assign_finish<ID_BYTES, XB>(B, P, sm, tot, cnf, col, row0);
+}
+
+// The same search for bf16 rows.  A bf16 x is its own hi part (lo = 0), so
+// one MFMA pass gives the products the two-pass form gives, bit for bit.
+// Both operands go global -> LDS by 1 KB DMA pieces in 64-wide k stages,
+// three stages ahead, into a ring of AD_NST buffers (no register staging, so
+// no wait in the loop covers more than the stage it needs): the 256 center
+// rows and the block's 32 input rows, each as [row][8 chunks of 16 bytes]
+// with chunk c of row q at slot c ^ (q % 8).  One barrier per stage, then 4
+// MFMAs per wave; wave 0 also sums ||x||^2 of its fragments.  The old form
+// read every center fragment straight from L2 (32 rows per load
+// instruction) and waited on it at every chunk.
+constexpr int AD_KS = 64, AD_NST = 4;
+constexpr int AD_CPIECES = AB_MAXC / 8, AD_PIECES = AD_CPIECES + AB_ROWS / 8;
+constexpr int AD_STAGE = AD_PIECES * 1024;
+constexpr int AD_QLO = AD_PIECES / AB_WAVES, AD_NHI = AD_PIECES % AB_WAVES;
+constexpr int AD_QMAX = AD_QLO + (AD_NHI ? 1 : 0);
+constexpr int AD_SMEM = AD_NST * AD_STAGE;
+static_assert(AD_SMEM + (int)sizeof(AssignSmall) <= 160 * 1024, "LDS budget");
+static_assert(AB_SEG % AD_KS == 0, "segments are whole stages");
+
+template <int ID_BYTES>
+__global__ void __launch_bounds__(64 * AB_WAVES) assign_dma_kernel(EncBatch B) {
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    __shared__ AssignSmall sm;
+    // items: (problem, row block), row block fastest
+    const int64_t item = xcd_item(blockIdx.x, B.n * B.row_blocks);
+    if (item >= B.n * B.row_blocks) return;
+    const EncProb& P = B.p[item / B.row_blocks];
+    const int64_t rows = P.M;
+    const int C = B.num_centers, HD = B.K, S = HD / AD_KS;
+    const int64_t row0 = (item % B.row_blocks) * AB_ROWS;
+    if (row0 >= rows) return;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
+    const int hf = lane >> 5, l32 = lane & 31;
+    assign_small_init(sm, t);
+    // this wave's pieces e = wave + AB_WAVES i: center rows 8e .. +8 (the
+    // last row past C), then input rows 8(e - AD_CPIECES) .. +8 (the last row
+    // past the end); lane L brings chunk (L % 8) ^ (L / 8) of its row
+    const uint16_t* src[AD_QMAX];
+    int64_t ldr[AD_QMAX];
 #pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            const int r = 8 * (i / 4) + 4 * hf + (i % 4);
-            const float xnorm = sqrtf(xn[r]) * 1.001f;
-            dt[i] = col < C ? cnf - 2.0f * tot[i] : INFINITY;
-            ee[i] = AB_KAPPA * (xnorm * cnorm + cnf * 1.001f);
+    for (int i = 0; i < AD_QMAX; ++i) {
+        const int e = wave + AB_WAVES * i;
+        const int ch = 8 * ((lane & 7) ^ (lane >> 3));
+        if (e < AD_CPIECES) {
+            src[i] = P.centers + (int64_t)min(8 * e + (lane >> 3), C - 1) * HD + ch;
+        } else {
+            const int64_t m = min(row0 + 8 * (e - AD_CPIECES) + (lane >> 3), rows - 1);
+            src[i] = P.xb + m * P.ldx + ch;
         }
+        ldr[i] = 0;
     }
-    // U = min over the row's columns of dt + E: a half-wave holds a row's 32 columns
+    (void)ldr;
+    auto issue = [&](int stg) {
+        unsigned char* dst = smem_raw + (stg % AD_NST) * AD_STAGE;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        float u = dt[i] + ee[i];
+        for (int i = 0; i < AD_QMAX; ++i)
+            if (i < AD_QLO || wave < AD_NHI)
+                dma16(src[i] + stg * AD_KS, dst + 1024 * (wave + AB_WAVES * i));
+    };
+    const int col = 32 * wave + l32;
+    f32x16 acc = {}, tot = {};
+    float cseg = 0.0f, xsq = 0.0f;
+    double cn = 0.0;
+    const int xrow_b = (AB_MAXC + l32) * 128, crow_b = col * 128;
 #pragma unroll
-        for (int off = 1; off < 32; off <<= 1) u = fminf(u, __shfl_xor(u, off));
-        if (l32 == 0) red[wave][8 * (i / 4) + 4 * hf + (i % 4)] = u;
-    }
-    __syncthreads();
-    // candidates: dt - E <= U
-#pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int r = 8 * (i / 4) + 4 * hf + (i % 4);
-        float U = red[0][r];
-#pragma unroll
-        for (int w = 1; w < AB_WAVES; ++w) U = fminf(U, red[w][r]);
-        if (col < C && dt[i] - ee[i] <= U) {
-            atomicAdd(&cnt[r], 1);
-            atomicMin(&first[r], col);
-            atomicOr(&cand[r][col >> 5], 1u << (col & 31));
+    for (int j = 0; j < AD_NST - 1; ++j)
+        if (j < S) issue(j);
+    for (int it = 0; it < S; ++it) {
+        const int later = min(AD_NST - 2, S - 1 - it);
+        static_assert(AD_NST - 2 == 2, "wait counts assume two later stages");
+        if (wave < AD_NHI) {
+            if (later >= 2) wait_vmcnt<2 * (AD_QLO + 1)>();
+            else if (later == 1) wait_vmcnt<AD_QLO + 1>();
+            else wait_vmcnt<0>();
+        } else {
+            if (later >= 2) wait_vmcnt<2 * AD_QLO>();
+            else if (later == 1) wait_vmcnt<AD_QLO>();
+            else wait_vmcnt<0>();
         }
-    }
-    __syncthreads();
-    // rows with one candidate are decided; the others compare their
-    // candidates exactly in fp64 (one wave per row, lanes split HD)
-    for (int r = wave; r < AB_ROWS; r += AB_WAVES) {
-        const int64_t gr = row0 + r;
-        if (gr >= rows) continue;
-        // (no candidate only for non-finite rows: index 0 then)
-        int best = cnt[r] == 0 ? 0 : first[r];
-        if (cnt[r] > 1) {
-            double bd = 0.0;
-            best = -1;
-            for (int w = 0; w < AB_MAXC / 32; ++w) {
-                uint32_t bits = cand[r][w];
-                while (bits) {
-                    const int c = 32 * w + __builtin_ctz(bits);
-                    bits &= bits - 1;
-                    const uint16_t* cr = centers + (int64_t)c * HD;
-                    double cc = 0.0, xc = 0.0;
-                    // 8 consecutive values per lane and step (HD % 256 == 0)
-                    for (int k = 8 * lane; k < HD; k += 512) {
-                        const u32x4 cw = *reinterpret_cast<const u32x4*>(cr + k);
-                        X8<XB> x8;
-                        x8.load(P, gr, k);
-                        const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
-                        const float xv[8] = {x8[0], x8[1], x8[2], x8[3], x8[4], x8[5], x8[6], x8[7]};
+        lds_barrier();
+        if (it + AD_NST - 1 < S) issue(it + AD_NST - 1);
+        const unsigned char* sb = smem_raw + (it % AD_NST) * AD_STAGE;
+        bf16x8 af[AD_KS / 16], cf[AD_KS / 16];
 #pragma unroll
-                        for (int e = 0; e < 8; ++e) {
-                            const uint32_t hb = (e & 1) ? (w4[e >> 1] & 0xffff0000u) : (w4[e >> 1] << 16);
-                            const double cv = (double)__uint_as_float(hb);
-                            cc = fma(cv, cv, cc);
-                            xc = fma((double)xv[e], cv, xc);
-                        }
-                    }
+        for (int k16 = 0; k16 < AD_KS / 16; ++k16) {
+            const int slot = 16 * ((2 * k16 + hf) ^ (l32 & 7));
+            af[k16] = lds_b128(reinterpret_cast<const uint16_t*>(sb + xrow_b + slot));
+            cf[k16] = lds_b128(reinterpret_cast<const uint16_t*>(sb + crow_b + slot));
+        }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-                    for (int off = 1; off < 64; off <<= 1) {
-                        cc += __shfl_xor(cc, off);
-                        xc += __shfl_xor(xc, off);
-                    }
-                    const double d = cc - 2.0 * xc;
-                    if (best < 0 || d < bd) { bd = d; best = c; }  // ascending c: first index on ties
+        for (int k16 = 0; k16 < AD_KS / 16; ++k16) {
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[k16], cf[k16], acc, 0, 0, 0);
+            const u32x4 cw = __builtin_bit_cast(u32x4, cf[k16]);
+            const uint32_t w4[4] = {cw.x, cw.y, cw.z, cw.w};
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const bf16x2 wv = __builtin_bit_cast(bf16x2, w4[e]);
+                cseg = __builtin_amdgcn_fdot2_f32_bf16(wv, wv, cseg, false);
+            }
+            if (wave == 0) {
+                const u32x4 xw = __builtin_bit_cast(u32x4, af[k16]);
+                const uint32_t x4[4] = {xw.x, xw.y, xw.z, xw.w};
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    const bf16x2 xv = __builtin_bit_cast(bf16x2, x4[e]);
+                    xsq = __builtin_amdgcn_fdot2_f32_bf16(xv, xv, xsq, false);
                 }
             }
         }
-        if (lane == 0) store_id<ID_BYTES>(ids, gr, best);
+        if (((it + 1) * AD_KS) % AB_SEG == 0 || it + 1 == S) {
+            // end of a segment: fold it into the second accumulators
+#pragma unroll
+            for (int i = 0; i < 16; ++i) tot[i] += acc[i];
+            acc = f32x16{};
+            cn += (double)cseg;
+            cseg = 0.0f;
+        }
     }
+    // ||x||^2 per row (wave 0: two k halves), ||c||^2 per column (two k halves)
+    if (wave == 0) {
+        const float xs2 = xsq + __shfl_xor(xsq, 32);
+        if (hf == 0 && row0 + l32 < rows) sm.xn[l32] = xs2;
+    }
+    cn += __shfl_xor(cn, 32);
+    __syncthreads();
+    assign_finish<ID_BYTES, true>(B, P, sm, tot, (float)cn, col, row0);
 }
 
 // ============================================================ MFMA GEMM core
@@ -771,114 +943,201 @@ __global__ void __launch_bounds__(256) encode_gemm_kernel(EncodeA al,
 }
 
 // Encoder projection coeff[M, r] = bf16(x - center[id] - mean) W_enc^T, fp32
-// accumulation.  The chain of dependent k steps, not the MFMA work, bounds a
-// projection of a few thousand rows (each step waits on L2/HBM), so a block
-// owns 32 rows x 96 coefficient columns (three 32-wide tiles) and its four
-// waves split K in quarters: every wave builds its own residual A fragments
-// in registers (x and the center row from L2, the mean from LDS) and reads
-// its W_enc fragments, one 64-wide k step ahead of the MFMAs, with no block
-// barrier in the loop.  The four partial sums are added through LDS in wave
-// order (deterministic).  Needs HD % 256 == 0 and HD <= EP_MAXK.
-constexpr int EP_ROWS = 32, EP_TILES = 3, EP_SPLIT = 4, EP_MAXK = 8192;
+// accumulation (MG nanokv_codec.py:344-347: the residual minus the mean, in
+// bf16, through the bf16 operator).  A block of six waves owns 32 rows x 192
+// coefficient columns (wave w: columns 32w .. 32w + 32) and walks K in
+// 64-wide stages.  Every operand goes global -> LDS by 1 KB DMA pieces (no
+// register staging, so no wait in the loop covers more than the stage it
+// needs), two stages ahead, into a ring of EP_NST stage buffers:
+//   [W_enc 192 rows x 128 B][inputs 32 rows][center values 32 rows][mean]
+// (the mean piece holds the stage's 64 means four times).  Iteration i: wait
+// for stage i, barrier, issue stage i + 2, then waves 0-3 turn stage i into
+// the bf16 residual image (one 16-byte unit of one row per thread) while
+// every wave runs the 4 MFMAs of stage i - 1 on the previous image.  W and
+// the residual image are [row][8 chunks of 16 bytes] with chunk c of row q at
+// slot c ^ (q % 8), so the operand reads (32 rows at one chunk) are free of
+// bank conflicts.  Needs K % 64 == 0 and 16-byte aligned rows.
+constexpr int EP_ROWS = 32, EP_WAVES = 6, EP_COLS = 32 * EP_WAVES, EP_NST = 4, EP_KS = 64;
+constexpr int EP_WPIECES = EP_COLS / 8;   // W rows per 1 KB piece: 8
 
-template <bool XB, int SPLIT>
-__global__ void __launch_bounds__(64 * SPLIT) encode_proj_kernel(EncBatch B) {
-    __shared__ float mean_s[EP_MAXK];
-    __shared__ float part[SPLIT - 1][EP_TILES][16][64];
-    const EncProb& P = B.p[blockIdx.z];
-    const int r = B.r;
-    float* __restrict__ coeff = P.coeff;
-    const int t = threadIdx.x, lane = t & 63, wave = t >> 6;
+template <bool XB>
+struct EncProjFmt {
+    static constexpr int XPIECES = XB ? 4 : 8;                       // 32 input rows
+    static constexpr int X0 = EP_WPIECES, C0 = X0 + XPIECES, M0 = C0 + 4;
+    static constexpr int PIECES = M0 + 1;
+    static constexpr int STAGE = PIECES * 1024;                      // bytes
+    static constexpr int AIMG = EP_ROWS * EP_KS * 2;                 // residual image bytes
+    static constexpr int SMEM = EP_NST * STAGE + 2 * AIMG;
+    // pieces per wave and stage: the first PIECES % EP_WAVES waves take one more
+    static constexpr int QLO = PIECES / EP_WAVES, NHI = PIECES % EP_WAVES;
+    static constexpr int QMAX = QLO + (NHI ? 1 : 0);
+};
+
+template <bool XB>
+__global__ void __launch_bounds__(64 * EP_WAVES) encode_proj_kernel(EncBatch B) {
+    using F = EncProjFmt<XB>;
+    extern __shared__ __align__(16) unsigned char smem_raw[];
+    // items: (problem, column slice, row block), row block fastest
+    const int ncb = (B.r + EP_COLS - 1) / EP_COLS;
+    const int64_t item = xcd_item(blockIdx.x, B.n * ncb * B.row_blocks);
+    if (item >= B.n * ncb * B.row_blocks) return;
+    const int64_t rest = item / B.row_blocks;
+    const EncProb& P = B.p[rest / ncb];
+    const int r = B.r, K = B.K, S = K / EP_KS;
+    const int t = threadIdx.x, lane = t & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int hf = lane >> 5, l32 = lane & 31;
-    const int64_t m0 = (int64_t)blockIdx.x * EP_ROWS;
+    const int64_t m0 = (item % B.row_blocks) * EP_ROWS;
     if (m0 >= P.M) return;
-    const int n0 = blockIdx.y * (EP_TILES * 32);
-    const int K = B.K, KW = K / SPLIT, kbeg = wave * KW;
-    if (P.mean) {
-        for (int k = t; k < K; k += 64 * SPLIT) mean_s[k] = P.mean[k];
-        __syncthreads();
-    }
-    const int64_t m = m0 + l32;
-    const bool row_ok = m < P.M;
-    const int64_t xr = row_ok ? m : 0;
-    const int xk = kbeg + 8 * hf;
-    const uint16_t* crow =
-        P.centers ? P.centers + (int64_t)(row_ok ? B.id_of(P, m) : 0) * K + kbeg + 8 * hf : nullptr;
-    const uint16_t* wrow[EP_TILES];
+    const int n0 = (int)(rest % ncb) * EP_COLS;
+    // this wave's pieces e = wave + EP_WAVES i: per lane a source address
+    // and the bytes it advances per stage.  Rows past the end read the last
+    // row; absent centers or mean read W_enc (any readable bytes; unused).
+    const unsigned char* src[F::QMAX];
+    int64_t adv[F::QMAX];
+    auto xrow = [&](int q) { return min(m0 + q, P.M - 1); };
 #pragma unroll
-    for (int j = 0; j < EP_TILES; ++j)
-        wrow[j] = P.w_enc + (int64_t)min(n0 + 32 * j + l32, r - 1) * K + kbeg + 8 * hf;
-    // raw operands of one 64-wide k step: four 16-wide MFMA sub-steps
-    struct Raw {
-        X8<XB> x[4];
-        u32x4 c[4];
-        u32x4 w[EP_TILES][4];
-    };
-    auto fetch = [&](int k0, Raw& rw) {
-#pragma unroll
-        for (int sub = 0; sub < 4; ++sub) {
-            rw.x[sub].load(P, xr, xk + k0 + 16 * sub);
-            if (crow) rw.c[sub] = *reinterpret_cast<const u32x4*>(crow + k0 + 16 * sub);
-#pragma unroll
-            for (int j = 0; j < EP_TILES; ++j)
-                rw.w[j][sub] = *reinterpret_cast<const u32x4*>(wrow[j] + k0 + 16 * sub);
-        }
-    };
-    f32x16 acc[EP_TILES];
-#pragma unroll
-    for (int j = 0; j < EP_TILES; ++j) acc[j] = f32x16{};
-    Raw cur, nxt;
-    fetch(0, cur);
-    for (int k0 = 0; k0 < KW; k0 += 64) {
-        if (k0 + 64 < KW) fetch(k0 + 64, nxt);
-#pragma unroll
-        for (int sub = 0; sub < 4; ++sub) {
-            float v[8] = {cur.x[sub][0], cur.x[sub][1], cur.x[sub][2], cur.x[sub][3],
-                          cur.x[sub][4], cur.x[sub][5], cur.x[sub][6], cur.x[sub][7]};
-            if (crow) {
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    v[2 * e] = v[2 * e] - __uint_as_float(cur.c[sub][e] << 16);
-                    v[2 * e + 1] = v[2 * e + 1] - __uint_as_float(cur.c[sub][e] & 0xffff0000u);
-                }
+    for (int i = 0; i < F::QMAX; ++i) {
+        const int e = wave + EP_WAVES * i;
+        const unsigned char* sp = reinterpret_cast<const unsigned char*>(P.w_enc);
+        int64_t st = 0;
+        if (e < F::X0) {
+            const int row = min(n0 + 8 * e + (lane >> 3), r - 1);
+            sp = reinterpret_cast<const unsigned char*>(P.w_enc + (int64_t)row * K +
+                                                        8 * ((lane & 7) ^ (lane >> 3)));
+            st = 2 * EP_KS;
+        } else if (e < F::C0) {
+            if constexpr (XB) {
+                const int64_t m = xrow(8 * (e - F::X0) + (lane >> 3));
+                sp = reinterpret_cast<const unsigned char*>(P.xb + m * P.ldx + 8 * (lane & 7));
+                st = 2 * EP_KS;
+            } else {
+                const int64_t m = xrow(4 * (e - F::X0) + (lane >> 4));
+                sp = reinterpret_cast<const unsigned char*>(P.x + m * P.ldx + 4 * (lane & 15));
+                st = 4 * EP_KS;
             }
+        } else if (e < F::M0) {
+            if (P.centers) {
+                const int64_t m = xrow(8 * (e - F::C0) + (lane >> 3));
+                sp = reinterpret_cast<const unsigned char*>(P.centers + (int64_t)B.id_of(P, m) * K +
+                                                            8 * (lane & 7));
+                st = 2 * EP_KS;
+            }
+        } else if (e == F::M0) {
             if (P.mean) {
-                const int kk = kbeg + k0 + 16 * sub + 8 * hf;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) v[e] = v[e] - mean_s[kk + e];
+                sp = reinterpret_cast<const unsigned char*>(P.mean + 4 * (lane & 15));
+                st = 4 * EP_KS;
             }
-            u32x4 a;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) a[e] = row_ok ? pack_bf16x2(v[2 * e], v[2 * e + 1]) : 0u;
-#pragma unroll
-            for (int j = 0; j < EP_TILES; ++j)
-                acc[j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(as_bf16x8(a), as_bf16x8(cur.w[j][sub]),
-                                                                 acc[j], 0, 0, 0);
         }
-        if (k0 + 64 < KW) cur = nxt;
+        src[i] = sp;
+        adv[i] = st;
     }
-    // sum the K quarters in wave order
-    if (wave > 0) {
+    auto issue = [&](int stg) {
+        unsigned char* dst = smem_raw + (stg % EP_NST) * F::STAGE;
 #pragma unroll
-        for (int j = 0; j < EP_TILES; ++j)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) part[wave - 1][j][i][lane] = acc[j][i];
-    }
-    __syncthreads();
-    if (wave > 0) return;
-#pragma unroll
-    for (int j = 0; j < EP_TILES; ++j) {
-        const int n = n0 + 32 * j + l32;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-            float sum = acc[j][i];
-#pragma unroll
-            for (int w = 0; w < SPLIT - 1; ++w) sum += part[w][j][i][lane];
-            const int64_t mm = m0 + 8 * (i / 4) + 4 * hf + (i % 4);
-            if (n < r && mm < P.M) coeff[mm * r + n] = sum;
+        for (int i = 0; i < F::QMAX; ++i) {
+            const int e = wave + EP_WAVES * i;
+            if (i < F::QLO || wave < F::NHI) dma16(src[i] + stg * adv[i], dst + 1024 * e);
         }
+    };
+    unsigned char* aimg = smem_raw + EP_NST * F::STAGE;
+    const bool prod = wave < 4;
+    const int arow = (t >> 3) & 31, ach = t & 7;
+    const bool arow_ok = m0 + arow < P.M;
+    // stage stg (landed) -> residual image stg % 2; absent centers or mean
+    // subtract zeros (x - 0 = x exactly), so every read is unconditional
+    const bool has_c = P.centers != nullptr, has_m = P.mean != nullptr;
+    auto prep = [&](int stg) {
+        const unsigned char* sb = smem_raw + (stg % EP_NST) * F::STAGE;
+        const u32x4 c = *reinterpret_cast<const u32x4*>(sb + 1024 * F::C0 + arow * 128 + 16 * ach);
+        const f32x4* mp = reinterpret_cast<const f32x4*>(sb + 1024 * F::M0 + 32 * ach);
+        const f32x4 u0 = mp[0], u1 = mp[1];
+        float xv[8];
+        if constexpr (XB) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(sb + 1024 * F::X0 + arow * 128 + 16 * ach);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                xv[2 * e] = __uint_as_float(w[e] << 16);
+                xv[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+            }
+        } else {
+            const f32x4* xp = reinterpret_cast<const f32x4*>(sb + 1024 * F::X0 + arow * 256 + 32 * ach);
+            const f32x4 a0 = xp[0], a1 = xp[1];
+#pragma unroll
+            for (int e = 0; e < 4; ++e) { xv[e] = a0[e]; xv[4 + e] = a1[e]; }
+        }
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const uint32_t cw = (e & 1) ? (c[e >> 1] & 0xffff0000u) : (c[e >> 1] << 16);
+            const float cv = has_c ? __uint_as_float(cw) : 0.0f;
+            const float mv = has_m ? (e < 4 ? u0[e] : u1[e - 4]) : 0.0f;
+            xv[e] = (xv[e] - cv) - mv;
+        }
+        u32x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o[e] = arow_ok ? pack_bf16x2(xv[2 * e], xv[2 * e + 1]) : 0u;
+        *reinterpret_cast<u32x4*>(aimg + (stg & 1) * F::AIMG + arow * 128 + 16 * (ach ^ (arow & 7))) = o;
+    };
+    const bool cols = n0 + 32 * wave < r;
+    f32x16 acc = {};
+    const int slot_row = l32 * 128, wrow = (32 * wave + l32) * 128;
+    auto compute = [&](int stg) {
+        const unsigned char* ar = aimg + (stg & 1) * F::AIMG + slot_row;
+        const unsigned char* wr = smem_raw + (stg % EP_NST) * F::STAGE + wrow;
+        bf16x8 af[EP_KS / 16], wf[EP_KS / 16];
+#pragma unroll
+        for (int k16 = 0; k16 < EP_KS / 16; ++k16) {
+            const int slot = 16 * ((2 * k16 + hf) ^ (l32 & 7));
+            af[k16] = lds_b128(reinterpret_cast<const uint16_t*>(ar + slot));
+            wf[k16] = lds_b128(reinterpret_cast<const uint16_t*>(wr + slot));
+        }
+        // all eight reads in flight before the first product
+        __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+        for (int k16 = 0; k16 < EP_KS / 16; ++k16)
+            acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[k16], wf[k16], acc, 0, 0, 0);
+    };
+    issue(0);
+    if (S > 1) issue(1);
+    for (int it = 0; it <= S; ++it) {
+        if (it < S) {
+            // stage it landed; stage it + 1 (issued after it) may stay in flight
+            if (it + 1 < S) {
+                if (wave < F::NHI) wait_vmcnt<F::QLO + 1>();
+                else wait_vmcnt<F::QLO>();
+            } else {
+                wait_vmcnt<0>();
+            }
+        }
+        lds_barrier();
+        if (it + 2 < S) issue(it + 2);
+        if (it < S && prod) prep(it);
+        if (it > 0 && cols) compute(it - 1);
+    }
+    if (!cols) return;
+    const int n = n0 + 32 * wave + l32;
+    if (n >= r) return;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+        const int64_t mm = m0 + 8 * (i / 4) + 4 * hf + (i % 4);
+        if (mm < P.M) P.coeff[mm * r + n] = acc[i];
     }
 }
+
+// Dynamic LDS of the projection kernels (above 64 KB), set once per process.
+static int encode_proj_smem() {
+    static const int rc = [] {
+        const hipError_t e0 = hipFuncSetAttribute((const void*)encode_proj_kernel<true>,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  EncProjFmt<true>::SMEM);
+        const hipError_t e1 = hipFuncSetAttribute((const void*)encode_proj_kernel<false>,
+                                                  hipFuncAttributeMaxDynamicSharedMemorySize,
+                                                  EncProjFmt<false>::SMEM);
+        return e0 == hipSuccess && e1 == hipSuccess ? (int)NKV_OK : (int)NKV_ERR_HIP;
+    }();
+    return rc;
+}
+static_assert(EncProjFmt<false>::SMEM <= 160 * 1024, "LDS budget");
 
 struct DecodeEpi {
     const uint16_t* centers;   // [C, HD] for this batch item, or NULL
@@ -1184,16 +1443,27 @@ static int launch_assign_f32(hipStream_t s, const float* x, const float* centers
 
 // The exact bf16-MFMA nearest-center search over every problem of a batch
 // (C <= AB_MAXC, HD % AB_SEG == 0, HD <= AB_MAXK, 16-byte aligned rows).
-static int launch_assign_batch(hipStream_t s, const EncBatch& B, bool xb) {
+static int launch_assign_batch(hipStream_t s, EncBatch B, bool xb) {
     int64_t rows = 0;
     for (int i = 0; i < B.n; ++i) rows = std::max(rows, B.p[i].M);
     if (rows <= 0) return NKV_OK;
+    B.row_blocks = cdiv(rows, AB_ROWS);
     const dim3 grid((unsigned)cdiv(rows, AB_ROWS), (unsigned)B.n);
     const unsigned threads = 64 * AB_WAVES;
     if (xb) {
-        if (B.id_bytes == 1) assign_bf16_kernel<1, true><<<grid, threads, 0, s>>>(B);
-        else if (B.id_bytes == 2) assign_bf16_kernel<2, true><<<grid, threads, 0, s>>>(B);
-        else assign_bf16_kernel<4, true><<<grid, threads, 0, s>>>(B);
+        static const hipError_t attr = [] {
+            hipError_t e = hipSuccess;
+            for (const void* f : {(const void*)assign_dma_kernel<1>, (const void*)assign_dma_kernel<2>,
+                                  (const void*)assign_dma_kernel<4>})
+                if (e == hipSuccess)
+                    e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, AD_SMEM);
+            return e;
+        }();
+        NKV_REQUIRE(attr == hipSuccess, NKV_ERR_HIP, "hipFuncSetAttribute failed for the search kernels");
+        const unsigned g1 = xcd_grid(B.n * B.row_blocks);
+        if (B.id_bytes == 1) assign_dma_kernel<1><<<g1, threads, AD_SMEM, s>>>(B);
+        else if (B.id_bytes == 2) assign_dma_kernel<2><<<g1, threads, AD_SMEM, s>>>(B);
+        else assign_dma_kernel<4><<<g1, threads, AD_SMEM, s>>>(B);
     } else {
         if (B.id_bytes == 1) assign_bf16_kernel<1, false><<<grid, threads, 0, s>>>(B);
         else if (B.id_bytes == 2) assign_bf16_kernel<2, false><<<grid, threads, 0, s>>>(B);
@@ -1395,13 +1665,13 @@ int encode_batch(hipStream_t s, const nkv_encode_args* a, int n) {
     }
     if (rows == 0) return NKV_OK;
     // the batched kernels: the exact bf16-MFMA search (C <= 256) and the
-    // K-split projection; a bf16 input takes only those
+    // staged projection; a bf16 input takes only those
     const bool fast_search = a->num_centers <= AB_MAXC && HD % AB_SEG == 0 && HD <= AB_MAXK;
-    const bool fast_proj = HD % (EP_SPLIT * 64) == 0 && HD <= EP_MAXK;
+    const bool fast_proj = HD % 256 == 0;
     const bool search = a->centers && !a->ids_in;
     NKV_REQUIRE(!xb || (aligned && fast_proj && (!search || fast_search)), NKV_ERR_UNSUPPORTED,
-                "a bf16 input needs HD % 256 == 0, HD <= 8192, at most 256 centers to search, and "
-                "16-byte aligned rows");
+                "a bf16 input needs HD % 256 == 0, 16-byte aligned rows and, to search, at most 256 "
+                "centers and HD <= 16384");
     int rc = NKV_OK;
     if (search) {
         if (fast_search && aligned) {
@@ -1418,9 +1688,12 @@ int encode_batch(hipStream_t s, const nkv_encode_args* a, int n) {
         if (rc) return rc;
     }
     if (fast_proj && aligned) {
-        const dim3 grid((unsigned)cdiv(rows, EP_ROWS), (unsigned)cdiv(r, EP_TILES * 32), (unsigned)n);
-        if (xb) encode_proj_kernel<true, EP_SPLIT><<<grid, 64 * EP_SPLIT, 0, s>>>(B);
-        else encode_proj_kernel<false, EP_SPLIT><<<grid, 64 * EP_SPLIT, 0, s>>>(B);
+        NKV_REQUIRE(encode_proj_smem() == NKV_OK, NKV_ERR_HIP,
+                    "hipFuncSetAttribute failed for the projection kernels");
+        B.row_blocks = cdiv(rows, EP_ROWS);
+        const unsigned grid = xcd_grid(n * cdiv(r, EP_COLS) * B.row_blocks);
+        if (xb) encode_proj_kernel<true><<<grid, 64 * EP_WAVES, EncProjFmt<true>::SMEM, s>>>(B);
+        else encode_proj_kernel<false><<<grid, 64 * EP_WAVES, EncProjFmt<false>::SMEM, s>>>(B);
         NKV_LAUNCH_CHECK();
     } else {
         for (int i = 0; i < n; ++i) {

@@ -129,6 +129,29 @@ __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) {
     return r;
 }
 
+#define NKV_LDS(p) ((__attribute__((address_space(3))) void*)(p))
+
+// one 16-byte-per-lane global -> LDS DMA (the 64 lanes fill 1 KB at l); a
+// function of its own so that kernel templates name no target builtin in
+// their bodies (the host pass then instantiates them for every width)
+__device__ __forceinline__ void dma16(const void* g, void* l) {
+    __builtin_amdgcn_global_load_lds(g, NKV_LDS(l), 16, 0, 0);
+}
+
+// s_waitcnt vmcnt(N) (gfx9 encoding: vmcnt in bits [3:0] and [15:14]; the
+// other counters at their maxima, i.e. not waited on)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+    static_assert(N >= 0 && N < 64, "vmcnt out of range");
+    __builtin_amdgcn_s_waitcnt((N & 15) | ((N >> 4) << 14) | (7 << 4) | (15 << 8));
+}
+
+// s_waitcnt lgkmcnt(0) and s_barrier, with the compiler keeping memory
+// accesses on their side of it (in-flight DMAs are not waited for)
+__device__ __forceinline__ void lds_barrier() {
+    asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
 __device__ __forceinline__ bf16x8 lds_b128(const uint16_t* p) {
     return *reinterpret_cast<const bf16x8*>(p);
 }

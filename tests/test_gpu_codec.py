@@ -170,6 +170,41 @@ def test_assign_near_ties_exact(dev, id_dtype):
     assert np.array_equal(ref[:64], np.minimum(a, b).numpy())
 
 
+@pytest.mark.parametrize("C,HD,id_dtype", [(24, 256, torch.uint8), (256, 512, torch.uint8),
+                                            (200, 768, torch.int32)])
+def test_assign_bf16_rows_near_ties_exact(dev, C, HD, id_dtype):
+    """The search over bf16 rows (nkv_encode with x_bf16, one MFMA pass):
+    rows on the exact midpoint of two small-integer centers tie (the first
+    index wins); rows moved one bf16 step of one coordinate off a midpoint
+    differ by far less than the search's error bound, so both go through the
+    exact fp64 re-evaluation; the ids equal oracle.assign on x.float()."""
+    g = torch.Generator().manual_seed(32 + C)
+    centers = torch.randint(-8, 9, (C, HD), generator=g).to(torch.bfloat16)
+    cf = centers.float()
+    n = 96
+    a = torch.randint(0, C, (n,), generator=g)
+    b = (a + 1 + torch.randint(0, C - 1, (n,), generator=g)) % C
+    mid = 0.5 * (cf[a] + cf[b])                      # half-integers: exact in bf16
+    j = (cf[b] - cf[a]).abs().argmax(1)              # a coordinate where a and b differ
+    step = torch.zeros(n, HD)
+    step[torch.arange(n), j] = torch.sign(cf[b] - cf[a])[torch.arange(n), j] * 2.0 ** -6
+    x = torch.cat([mid, mid + step, mid - step,
+                   cf[a] + torch.randint(-1, 2, (n, HD), generator=g)]).to(torch.bfloat16)
+    assert torch.equal(x.float().to(torch.bfloat16), x)
+    w_enc = (torch.randn(64, HD, generator=g) / HD ** 0.5).to(torch.bfloat16)
+    got = ops.encode(x.to(dev), w_enc.to(dev), centers=centers.to(dev), group=32,
+                     id_dtype=id_dtype)
+    ids = got["ids"].cpu().to(torch.int64).numpy()
+    ref = orc.assign(x.float().numpy(), u16(centers))
+    assert np.array_equal(ids, ref)
+    assert np.array_equal(ref[:n], np.minimum(a, b).numpy())
+    assert np.array_equal(ref[n:2 * n], b.numpy()) and np.array_equal(ref[2 * n:3 * n], a.numpy())
+    # the same rows as fp32 take the two-pass search: same ids
+    got32 = ops.encode(x.float().to(dev), w_enc.to(dev), centers=centers.to(dev), group=32,
+                       id_dtype=id_dtype)
+    assert torch.equal(got32["ids"], got["ids"])
+
+
 def test_assign_rows_not_multiple_of_16(dev):
     # HD = 72: the fp64 VALU search (the MFMA search needs HD % 16 == 0)
     g = torch.Generator().manual_seed(21)
