@@ -402,6 +402,9 @@ struct EncBatch {
     EncProb p[ENC_MAXB];
     int n, K, r, num_centers, id_bytes;
     int64_t row_blocks;   // 32-row blocks of the largest problem (set per launch)
+    // the quantiser run inside the projection: group size (0: separate
+    // launch), scale dtype and NKV_QUANT_* mode
+    int qgroup, scale_dtype, quant_mode;
     // center id of row m of problem p (clamped into the table)
     __device__ __forceinline__ int id_of(const EncProb& q, int64_t m) const {
         int v;
@@ -1114,13 +1117,25 @@ __global__ void __launch_bounds__(64 * EP_WAVES) encode_proj_kernel(EncBatch B) 
         if (it < S && prod) prep(it);
         if (it > 0 && cols) compute(it - 1);
     }
-    if (!cols) return;
     const int n = n0 + 32 * wave + l32;
-    if (n >= r) return;
+    if (cols && n < r) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-        const int64_t mm = m0 + 8 * (i / 4) + 4 * hf + (i % 4);
-        if (mm < P.M) P.coeff[mm * r + n] = acc[i];
+        for (int i = 0; i < 16; ++i) {
+            const int64_t mm = m0 + 8 * (i / 4) + 4 * hf + (i % 4);
+            if (mm < P.M) P.coeff[mm * r + n] = acc[i];
+        }
+    }
+    if (B.qgroup == 0) return;
+    // the quantiser on the block's whole groups (the columns of a block hold
+    // whole groups): the coefficients just stored, read back after the barrier
+    __syncthreads();
+    const int G = B.qgroup, ngroups = r / G, gpb = (min(r - n0, EP_COLS)) / G;
+    for (int it = t; it < EP_ROWS * gpb; it += 64 * EP_WAVES) {
+        const int64_t gid = (m0 + it / gpb) * ngroups + n0 / G + it % gpb;
+        if (B.quant_mode == NKV_QUANT_BF16)
+            quant_pack_group<NKV_QUANT_BF16>(P.coeff, P.M, r, G, B.scale_dtype, P.packed, P.scales, gid);
+        else
+            quant_pack_group<NKV_QUANT_FP32>(P.coeff, P.M, r, G, B.scale_dtype, P.packed, P.scales, gid);
     }
 }
 
@@ -1691,10 +1706,15 @@ int encode_batch(hipStream_t s, const nkv_encode_args* a, int n) {
         NKV_REQUIRE(encode_proj_smem() == NKV_OK, NKV_ERR_HIP,
                     "hipFuncSetAttribute failed for the projection kernels");
         B.row_blocks = cdiv(rows, EP_ROWS);
+        // groups that do not straddle column blocks are quantised in the same launch
+        B.qgroup = EP_COLS % a->group == 0 ? a->group : 0;
+        B.scale_dtype = a->scale_dtype;
+        B.quant_mode = a->quant_mode;
         const unsigned grid = xcd_grid(n * cdiv(r, EP_COLS) * B.row_blocks);
         if (xb) encode_proj_kernel<true><<<grid, 64 * EP_WAVES, EncProjFmt<true>::SMEM, s>>>(B);
         else encode_proj_kernel<false><<<grid, 64 * EP_WAVES, EncProjFmt<false>::SMEM, s>>>(B);
         NKV_LAUNCH_CHECK();
+        if (B.qgroup) return NKV_OK;
     } else {
         for (int i = 0; i < n; ++i) {
             if (B.p[i].M == 0) continue;
