@@ -387,7 +387,11 @@ int nkv_decode(void* stream, const nkv_decode_args* args);
  * 16-byte aligned with strides divisible by 8 (NKV_ERR_INVALID otherwise).
  * key/value codecs decode to HD = H * D columns; head h reads columns
  * [h*D, (h+1)*D).  An empty key set gives out = 0 and lse = -inf
- * (attention_lse, CN/core.py:48-49).  D must be 128.
+ * (attention_lse, CN/core.py:48-49).  D = 128, or D < 128 with D % 8 == 0:
+ * narrower heads (BASELINE config 0 has D = 64) run the D = 128 kernels on
+ * operands padded with zero columns inside the workspace (exact: the zero
+ * columns add nothing to q.k and give zero output columns), without RoPE,
+ * the camera or segmented codecs.
  * rope (host pointer, NULL = none): history keys are rotated after decode at
  * the positions of their codec rows (see nkv_rope); q and k_cur are taken as
  * already rotated.  RoPE runs on the KEY_CHUNKS schedule (AUTO picks it).

@@ -833,19 +833,284 @@ int resolve_schedule(const nkv_attend_args* a, int* schedule) {
 
 }  // namespace
 
+// ------------------------------------------------- heads narrower than 128
+// A head width D < 128 (D % 8 == 0; BASELINE config 0 has D = 64) runs
+// through the D = 128 kernels on operands padded with zero columns to 128 per
+// head.  The zero dimensions add nothing to q.k, and the padded decoder rows,
+// centers and mean make every padded history row exactly the decoded row
+// followed by zeros (bf16(bf16(0 + 0) + 0) = 0), so the first D columns of
+// the output are the attention at width D (the caller's softmax_scale is
+// used as given).  The padded q, current K/V, output, decoder weights,
+// centers and means sit at the front of the caller's workspace; the rest is
+// the D = 128 call's workspace.  RoPE, the camera and segmented codecs keep
+// their D = 128 requirement.
+namespace {
+
+// [rows = B*T, H, D] strided bf16 -> [rows, H, 128] contiguous, one 16-byte
+// unit per thread, zero units past D
+__global__ void __launch_bounds__(256) pad_heads_kernel(const uint16_t* __restrict__ src,
+                                                        int64_t sb, int64_t st, int64_t sh,
+                                                        int64_t T, int H, int D, int64_t rows,
+                                                        uint16_t* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= rows * H * (AT_D / 8)) return;
+    const int c = (int)(i % (AT_D / 8));
+    const int64_t rh = i / (AT_D / 8);
+    const int h = (int)(rh % H);
+    const int64_t row = rh / H;
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (c < D / 8)
+        v = *reinterpret_cast<const u32x4*>(src + (row / T) * sb + (row % T) * st + h * sh + 8 * c);
+    *reinterpret_cast<u32x4*>(dst + 8 * i) = v;
+}
+
+// the reverse: the first D columns of [rows, H, 128] into the strided output
+__global__ void __launch_bounds__(256) unpad_heads_kernel(const uint16_t* __restrict__ src,
+                                                          int64_t T, int H, int D, int64_t rows,
+                                                          uint16_t* __restrict__ dst, int64_t sb,
+                                                          int64_t st, int64_t sh) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    const int per = D / 8;
+    if (i >= rows * H * per) return;
+    const int c = (int)(i % per);
+    const int64_t rh = i / per;
+    const int h = (int)(rh % H);
+    const int64_t row = rh / H;
+    *reinterpret_cast<u32x4*>(dst + (row / T) * sb + (row % T) * st + h * sh + 8 * c) =
+        *reinterpret_cast<const u32x4*>(src + (rh * AT_D + 8 * c));
+}
+
+// [A, D, W] -> [A, 128, W] of 16-bit elements, zero rows past D (decoder
+// rows [H, D, r], center tables [C*H, D, 1], fp32 means as [H, D, 2])
+__global__ void __launch_bounds__(256) pad_rows_kernel(const uint16_t* __restrict__ src, int64_t A,
+                                                       int D, int64_t W, uint16_t* __restrict__ dst) {
+    const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+    if (i >= A * AT_D * W) return;
+    const int64_t w = i % W, rest = i / W;
+    const int d = (int)(rest % AT_D);
+    const int64_t a = rest / AT_D;
+    dst[i] = d < D ? src[(a * D + d) * W + w] : (uint16_t)0;
+}
+
+constexpr size_t kNarrowAlign = 256;
+inline size_t narrow_round(size_t x) { return (x + kNarrowAlign - 1) & ~(kNarrowAlign - 1); }
+
+// byte offsets of the padded operands in the workspace; inner = the D = 128
+// call's workspace start
+struct NarrowLayout {
+    size_t q, o, kc, vc, w[2], c[2], m[2], inner;
+};
+
+int narrow_check(const nkv_attend_args* a) {
+    NKV_REQUIRE(a, NKV_ERR_INVALID, "null args");
+    NKV_REQUIRE(a->D > 0 && a->D < AT_D && a->D % 8 == 0, NKV_ERR_UNSUPPORTED,
+                "fused attend supports D == 128, or D < 128 with D % 8 == 0");
+    NKV_REQUIRE(!a->rope && !a->camera, NKV_ERR_UNSUPPORTED,
+                "read-time RoPE and the camera need D == 128");
+    NKV_REQUIRE(a->N == 0 || (a->key.n_segments == 0 && a->value.n_segments == 0),
+                NKV_ERR_UNSUPPORTED, "segmented codecs need D == 128");
+    return NKV_OK;
+}
+
+int center_tables(const nkv_attend_args* a, const nkv_codec& c) {
+    return c.centers_batch_stride ? a->B : 1;
+}
+
+NarrowLayout narrow_layout(const nkv_attend_args* a) {
+    NarrowLayout L{};
+    size_t off = 0;
+    auto take = [&](size_t bytes) {
+        const size_t o = off;
+        off = narrow_round(off + bytes);
+        return o;
+    };
+    const size_t row = (size_t)a->H * AT_D * sizeof(uint16_t);
+    L.q = take((size_t)a->B * a->Q * row);
+    L.o = take((size_t)a->B * a->Q * row);
+    L.kc = take((size_t)a->B * a->Nc * row);
+    L.vc = take((size_t)a->B * a->Nc * row);
+    for (int i = 0; i < 2; ++i) {
+        const nkv_codec& c = i ? a->value : a->key;
+        if (a->N == 0) continue;
+        L.w[i] = take(row * c.r);
+        if (c.centers) L.c[i] = take((size_t)center_tables(a, c) * c.num_centers * row);
+        if (c.mean) L.m[i] = take((size_t)a->H * AT_D * sizeof(float));
+    }
+    L.inner = off;
+    return L;
+}
+
+// The D = 128 arguments over the padded operands at base (base may be a
+// placeholder when only the workspace size is wanted: nothing is read).
+nkv_attend_args narrow_args(const nkv_attend_args* a, const NarrowLayout& L, unsigned char* base) {
+    nkv_attend_args n = *a;
+    n.D = AT_D;
+    const int64_t hd = (int64_t)a->H * AT_D;
+    n.q = reinterpret_cast<const uint16_t*>(base + L.q);
+    n.q_sb = a->Q * hd, n.q_st = hd, n.q_sh = AT_D;
+    n.out = reinterpret_cast<uint16_t*>(base + L.o);
+    n.o_sb = a->Q * hd, n.o_st = hd, n.o_sh = AT_D;
+    if (a->Nc > 0) {
+        n.k_cur = reinterpret_cast<const uint16_t*>(base + L.kc);
+        n.v_cur = reinterpret_cast<const uint16_t*>(base + L.vc);
+        n.k_sb = n.v_sb = a->Nc * hd;
+        n.k_st = n.v_st = hd;
+        n.k_sh = n.v_sh = AT_D;
+    }
+    if (a->N > 0) {
+        for (int i = 0; i < 2; ++i) {
+            nkv_codec& c = i ? n.value : n.key;
+            c.w_dec = reinterpret_cast<const uint16_t*>(base + L.w[i]);
+            if (c.centers) {
+                c.centers = reinterpret_cast<const uint16_t*>(base + L.c[i]);
+                if (c.centers_batch_stride) c.centers_batch_stride = (int64_t)c.num_centers * hd;
+            }
+            if (c.mean) c.mean = reinterpret_cast<const float*>(base + L.m[i]);
+        }
+    }
+    return n;
+}
+
+// a non-null, aligned stand-in base for the size query
+unsigned char* narrow_placeholder() { return reinterpret_cast<unsigned char*>((uintptr_t)1 << 12); }
+
+int inner_workspace(const nkv_attend_args* a, size_t* need);
+
+// workspace bytes of a call at any supported D
+int attend_need(const nkv_attend_args* a, size_t* need) {
+    if (a && a->D != AT_D) {
+        int rc = narrow_check(a);
+        if (rc) return rc;
+        const NarrowLayout L = narrow_layout(a);
+        const nkv_attend_args n = narrow_args(a, L, narrow_placeholder());
+        size_t inner = 0;
+        rc = inner_workspace(&n, &inner);
+        if (rc) return rc;
+        *need = L.inner + inner;
+        return NKV_OK;
+    }
+    return inner_workspace(a, need);
+}
+
+int inner_workspace(const nkv_attend_args* a, size_t* need) {
+    AttendPlan pl;
+    int rc = plan_attend(a, &pl);
+    if (rc) return rc;
+    int sch;
+    rc = resolve_schedule(a, &sch);
+    if (rc) return rc;
+    if (sch == NKV_SCHEDULE_KEY_CHUNKS) {
+        rc = chunk_check(a);
+        if (rc) return rc;
+        *need = chunk_workspace_bytes(a);
+    } else {
+        *need = workspace_bytes_for(a, pl);
+    }
+    return NKV_OK;
+}
+
+int attend_d128(hipStream_t s, const nkv_attend_args* a, void* workspace, size_t workspace_bytes);
+
+int attend_narrow(hipStream_t s, const nkv_attend_args* a, void* workspace, size_t workspace_bytes) {
+    int rc = narrow_check(a);
+    if (rc) return rc;
+    NKV_REQUIRE(a->B >= 1 && a->H >= 1, NKV_ERR_INVALID, "B and H must be >= 1");
+    NKV_REQUIRE(a->Q >= 0 && a->N >= 0 && a->Nc >= 0, NKV_ERR_INVALID, "negative length");
+    if (a->Q > 0) {
+        NKV_REQUIRE(a->q && a->out, NKV_ERR_INVALID, "q and out required");
+        NKV_REQUIRE(rows16(a->q, a->q_sb, a->q_st, a->q_sh) &&
+                        rows16(a->out, a->o_sb, a->o_st, a->o_sh),
+                    NKV_ERR_INVALID, "q and out must be 16-byte aligned with strides divisible by 8");
+    }
+    if (a->Nc > 0) {
+        NKV_REQUIRE(a->k_cur && a->v_cur, NKV_ERR_INVALID, "current K/V missing");
+        NKV_REQUIRE(rows16(a->k_cur, a->k_sb, a->k_st, a->k_sh) &&
+                        rows16(a->v_cur, a->v_sb, a->v_st, a->v_sh),
+                    NKV_ERR_INVALID,
+                    "k_cur and v_cur must be 16-byte aligned with strides divisible by 8");
+    }
+    if (a->N > 0) {
+        for (const nkv_codec* c : {&a->key, &a->value}) {
+            rc = check_attend_codec(*c, a->N, a->H * a->D, "");
+            if (rc) return rc;
+        }
+    }
+    size_t need = 0;
+    rc = attend_need(a, &need);
+    if (rc) return rc;
+    if (a->Q == 0) return NKV_OK;
+    NKV_REQUIRE(workspace && workspace_bytes >= need, NKV_ERR_WORKSPACE,
+                "workspace missing or smaller than nkv_attend_workspace_size()");
+    unsigned char* base = reinterpret_cast<unsigned char*>(workspace);
+    const NarrowLayout L = narrow_layout(a);
+    const nkv_attend_args n = narrow_args(a, L, base);
+    const int D = a->D;
+    auto blocks = [](int64_t work) { return dim3((unsigned)cdiv(work, 256)); };
+    const int64_t qrows = (int64_t)a->B * a->Q;
+    pad_heads_kernel<<<blocks(qrows * a->H * (AT_D / 8)), 256, 0, s>>>(
+        a->q, a->q_sb, a->q_st, a->q_sh, a->Q, a->H, D, qrows, const_cast<uint16_t*>(n.q));
+    NKV_LAUNCH_CHECK();
+    if (a->Nc > 0) {
+        const int64_t crows = (int64_t)a->B * a->Nc;
+        pad_heads_kernel<<<blocks(crows * a->H * (AT_D / 8)), 256, 0, s>>>(
+            a->k_cur, a->k_sb, a->k_st, a->k_sh, a->Nc, a->H, D, crows, const_cast<uint16_t*>(n.k_cur));
+        NKV_LAUNCH_CHECK();
+        pad_heads_kernel<<<blocks(crows * a->H * (AT_D / 8)), 256, 0, s>>>(
+            a->v_cur, a->v_sb, a->v_st, a->v_sh, a->Nc, a->H, D, crows, const_cast<uint16_t*>(n.v_cur));
+        NKV_LAUNCH_CHECK();
+    }
+    if (a->N > 0) {
+        for (int i = 0; i < 2; ++i) {
+            const nkv_codec& c = i ? a->value : a->key;
+            const nkv_codec& cn = i ? n.value : n.key;
+            pad_rows_kernel<<<blocks((int64_t)a->H * AT_D * c.r), 256, 0, s>>>(
+                c.w_dec, a->H, D, c.r, const_cast<uint16_t*>(cn.w_dec));
+            NKV_LAUNCH_CHECK();
+            if (c.centers) {
+                const int tables = center_tables(a, c);
+                const int64_t A = (int64_t)c.num_centers * a->H;
+                for (int t = 0; t < tables; ++t) {
+                    pad_rows_kernel<<<blocks(A * AT_D), 256, 0, s>>>(
+                        c.centers + t * c.centers_batch_stride, A, D, 1,
+                        const_cast<uint16_t*>(cn.centers) + (int64_t)t * A * AT_D);
+                    NKV_LAUNCH_CHECK();
+                }
+            }
+            if (c.mean) {
+                pad_rows_kernel<<<blocks((int64_t)a->H * AT_D * 2), 256, 0, s>>>(
+                    reinterpret_cast<const uint16_t*>(c.mean), a->H, D, 2,
+                    reinterpret_cast<uint16_t*>(const_cast<float*>(cn.mean)));
+                NKV_LAUNCH_CHECK();
+            }
+        }
+    }
+    rc = attend_d128(s, &n, base + L.inner, workspace_bytes - L.inner);
+    if (rc) return rc;
+    unpad_heads_kernel<<<blocks(qrows * a->H * (D / 8)), 256, 0, s>>>(
+        n.out, a->Q, a->H, D, qrows, a->out, a->o_sb, a->o_st, a->o_sh);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
+}
+
+}  // namespace
+
 extern "C" size_t nkv_attend_workspace_size(const nkv_attend_args* a) {
     clear_error();
-    AttendPlan pl;
-    if (plan_attend(a, &pl)) return 0;
-    int sch;
-    if (resolve_schedule(a, &sch)) return 0;
-    if (sch == NKV_SCHEDULE_KEY_CHUNKS) return chunk_check(a) ? 0 : chunk_workspace_bytes(a);
-    return workspace_bytes_for(a, pl);
+    size_t need = 0;
+    return attend_need(a, &need) ? 0 : need;
 }
 
 extern "C" int nkv_attend(void* stream, const nkv_attend_args* a, void* workspace,
                           size_t workspace_bytes) {
     clear_error();
+    hipStream_t s = (hipStream_t)stream;
+    if (a && a->D != AT_D) return attend_narrow(s, a, workspace, workspace_bytes);
+    return attend_d128(s, a, workspace, workspace_bytes);
+}
+
+namespace {
+
+int attend_d128(hipStream_t s, const nkv_attend_args* a, void* workspace, size_t workspace_bytes) {
     AttendPlan pl;
     int rc = plan_attend(a, &pl);
     if (rc) return rc;
@@ -853,7 +1118,6 @@ extern "C" int nkv_attend(void* stream, const nkv_attend_args* a, void* workspac
     rc = resolve_schedule(a, &sch);
     if (rc) return rc;
     if (a->Q == 0) return NKV_OK;
-    hipStream_t s = (hipStream_t)stream;
     if (sch == NKV_SCHEDULE_KEY_CHUNKS) return chunk_attend_launch(s, a, workspace, workspace_bytes);
     const size_t need = workspace_bytes_for(a, pl);
     NKV_REQUIRE(need == 0 || (workspace && workspace_bytes >= need), NKV_ERR_WORKSPACE,
@@ -924,6 +1188,8 @@ extern "C" int nkv_attend(void* stream, const nkv_attend_args* a, void* workspac
     return NKV_OK;
 }
 
+}  // namespace
+
 // ------------------------------------------------- allocation-free nkv_attend
 // The scratch of nkv_attend_static: one array per GPU in the code object, so
 // a call allocates nothing.  In host code the name `scratch` is only a
@@ -961,20 +1227,9 @@ int scratch_address(int dev, void** ptr) {
 
 extern "C" int nkv_attend_static(void* stream, const nkv_attend_args* a) {
     clear_error();
-    AttendPlan pl;
-    int rc = plan_attend(a, &pl);
+    size_t need = 0;
+    int rc = attend_need(a, &need);
     if (rc) return rc;
-    int sch;
-    rc = resolve_schedule(a, &sch);
-    if (rc) return rc;
-    size_t need;
-    if (sch == NKV_SCHEDULE_KEY_CHUNKS) {
-        rc = chunk_check(a);
-        if (rc) return rc;
-        need = chunk_workspace_bytes(a);
-    } else {
-        need = workspace_bytes_for(a, pl);
-    }
     NKV_REQUIRE(need <= (size_t)NKV_STATIC_SCRATCH_BYTES, NKV_ERR_WORKSPACE,
                 "the call needs " + std::to_string(need) + " bytes of scratch; "
                 "nkv_attend_static holds " + std::to_string((size_t)NKV_STATIC_SCRATCH_BYTES) +

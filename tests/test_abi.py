@@ -45,9 +45,13 @@ def test_invalid_arguments_are_rejected_before_any_launch():
 def test_attend_rejects_unsupported_shapes():
     lib = _lib.lib()
     args = _lib.NkvAttendArgs()
-    args.B, args.H, args.D, args.Q = 1, 2, 64, 8
+    args.B, args.H, args.D, args.Q = 1, 2, 256, 8
     assert lib.nkv_attend_workspace_size(ctypes.byref(args)) == 0
     assert b"D == 128" in lib.nkv_last_error()
+    args.D = 60   # narrower heads need D % 8 == 0
+    assert lib.nkv_attend_workspace_size(ctypes.byref(args)) == 0
+    assert b"D % 8" in lib.nkv_last_error()
+    args.D = 256
     rc = lib.nkv_attend(None, ctypes.byref(args), None, 0)
     assert rc == _lib.NKV_ERR_UNSUPPORTED
     args.D = 128

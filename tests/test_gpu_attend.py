@@ -37,6 +37,29 @@ SCHEDULES = ["query_tiles", "key_chunks"]
 
 
 @pytest.mark.parametrize("schedule", SCHEDULES)
+@pytest.mark.parametrize("D,B,with_mean", [(64, 1, False), (64, 2, True), (32, 1, True)])
+def test_attend_narrow_heads(dev, D, B, with_mean, schedule):
+    """Heads narrower than 128 (BASELINE config 0 has D = 64) run through the
+    D = 128 kernels on zero-padded operands: the same bar against the
+    oracle's decode-then-SDPA at width D, on both schedules, with a mean,
+    two batch items and a strided query / output."""
+    sc = Scenario(B=B, H=3, D=D, N=300, Q=70, Nc=40, rK=64, rV=128, G=32, C=8,
+                  with_mean=with_mean, seed=D + B)
+    _check(sc, dev, schedule=schedule)
+    # q and out as column slices of wider buffers (16-byte aligned rows)
+    key, value = sc.codecs(dev)
+    wide_q = torch.zeros(B, sc.Q, sc.H, 2 * D, dtype=torch.bfloat16, device=dev)
+    wide_q[..., D:] = sc.q.to(dev)
+    wide_o = torch.full((B, sc.Q, sc.H, 2 * D), 7.0, dtype=torch.bfloat16, device=dev)
+    out, _ = ops.attend(wide_q[..., D:], sc.k_cur.to(dev), sc.v_cur.to(dev), key, value,
+                        out=wide_o[..., :D], schedule=schedule)
+    ref, _ = ops.attend(sc.q.to(dev), sc.k_cur.to(dev), sc.v_cur.to(dev), key, value,
+                        schedule=schedule)
+    assert torch.equal(wide_o[..., :D], ref)
+    assert bool((wide_o[..., D:] == 7.0).all())
+
+
+@pytest.mark.parametrize("schedule", SCHEDULES)
 @pytest.mark.parametrize("N,Nc,Q", [(200, 64, 100), (257, 37, 300), (64, 0, 1), (0, 100, 33),
                                     (1000, 130, 513)])
 def test_attend_shapes(dev, N, Nc, Q, schedule):

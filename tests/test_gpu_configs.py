@@ -1,7 +1,8 @@
 """GPU parity at BASELINE's other configurations, encoded on the GPU and
 checked against the oracle on the same bits:
   cfg0  the encoder at HD = 512, r = 64, 16 centers, per-32 fp16 scales
-        (orthonormal 512 x 64 codec), and its decode;
+        (orthonormal 512 x 64 codec), its decode, and the whole layer's
+        attention at D = 64;
   cfg2  N = 49,920, Q = Nc = 780, 1,024 centers with 16-bit ids, rK = 384 /
         rV = 256: bit-exact assignment at C = 1,024 and the full fused call on
         a head subset;
@@ -49,6 +50,36 @@ def test_cfg0_encoder_and_decode(dev):
         want = orc.decode(**_oracle_codec(e, dec, cent, sh.G))
         diff = np.abs(orc.bf16_to_f32(u16(got)) - orc.bf16_to_f32(want)).max()
         assert diff <= 3 * 2 ** -7 * max(1.0, float(np.abs(orc.bf16_to_f32(want)).max())), kind
+
+
+def test_cfg0_layer_on_the_gpu(dev):
+    """Config 0's whole layer on the GPU at D = 64: the history (2,048 rows of
+    K and V) encoded by nkv_encode, then one nkv_attend of 256 queries over it
+    and 256 current keys, against the oracle's decode-then-SDPA on the same
+    payload (the GPU's codes and scales)."""
+    sh = synth.CONFIGS[0]
+    assert (sh.H, sh.D, sh.N, sh.Q, sh.Nc) == (8, 64, 2048, 256, 256)
+    lay = synth.make_layer(sh, seed=0, device=dev, orthonormal_codec=True)
+    codecs, payload = [], []
+    for kind, cent, enc, dec in (("k", lay.centers_k, lay.w_enc_k, lay.w_dec_k),
+                                 ("v", lay.centers_v, lay.w_enc_v, lay.w_dec_v)):
+        rows = synth.history_rows(sh, cent, sh.N, seed=1 + (kind == "v"), device=dev)
+        e = ops.encode(rows, enc, centers=cent, group=sh.G, scale_dtype=sh.scale_dtype)
+        codecs.append(ops.Codec(packed=e["packed"][None], scales=e["scales"][None], w_dec=dec,
+                                group=sh.G, ids=e["ids"][None], centers=cent[None]))
+        payload.append(_oracle_codec(e, dec, cent, sh.G))
+    g = torch.Generator(device=dev).manual_seed(5)
+    q = (torch.randn(1, sh.Q, sh.H, sh.D, generator=g, device=dev) / sh.D ** 0.5).to(torch.bfloat16)
+    kc = synth.history_rows(sh, lay.centers_k, sh.Nc, seed=7, device=dev)
+    vc = synth.history_rows(sh, lay.centers_v, sh.Nc, seed=8, device=dev)
+    kc = kc.view(1, sh.Nc, sh.H, sh.D).to(torch.bfloat16)
+    vc = vc.view(1, sh.Nc, sh.H, sh.D).to(torch.bfloat16)
+    out, lse = ops.attend(q, kc, vc, codecs[0], codecs[1])
+    ref, ref_lse = orc.decode_attend(u16(q[0]), u16(kc[0]), u16(vc[0]), payload[0], payload[1],
+                                     sh.D ** -0.5, D=sh.D)
+    diff, cos = max_abs_cos(out[0].float().cpu().numpy(), ref)
+    assert diff <= MAX_ABS and cos >= MIN_COS, (diff, cos)
+    assert np.abs(lse[0].cpu().numpy() - ref_lse).max() < 2e-3
 
 
 def test_cfg2_assign_1024_centers_bit_exact(dev):
