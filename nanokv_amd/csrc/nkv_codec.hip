@@ -669,22 +669,28 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_bf16_kernel(EncBatch B) 
 
 // The same search for bf16 rows.  A bf16 x is its own hi part (lo = 0), so
 // one MFMA pass gives the products the two-pass form gives, bit for bit.
-// Both operands go global -> LDS by 1 KB DMA pieces in 64-wide k stages,
-// three stages ahead, into a ring of AD_NST buffers (no register staging, so
-// no wait in the loop covers more than the stage it needs): the 256 center
-// rows and the block's 32 input rows, each as [row][8 chunks of 16 bytes]
-// with chunk c of row q at slot c ^ (q % 8).  One barrier per stage, then 4
-// MFMAs per wave; wave 0 also sums ||x||^2 of its fragments.  The old form
-// read every center fragment straight from L2 (32 rows per load
-// instruction) and waited on it at every chunk.
-constexpr int AD_KS = 64, AD_NST = 4;
-constexpr int AD_CPIECES = AB_MAXC / 8, AD_PIECES = AD_CPIECES + AB_ROWS / 8;
+// Both operands go global -> LDS by 1 KB DMA pieces in 128-wide k stages
+// (72 KB: the 256 center rows and the block's 32 input rows, each as
+// [row][16 chunks of 16 bytes] with chunk c of row q at slot c ^ (q % 8)),
+// double-buffered: after the barrier of stage i the next stage is issued and
+// stage i's 8 MFMAs per wave run under it; wave 0 also sums ||x||^2 of its
+// fragments.  A block's stream is bound by a fixed cost per barrier plus one
+// per 1 KB piece, so few large stages stream faster than many small ones (on
+// the box 32 KB stages reached about 100 GB/s per CU, 8 KB stages 38 GB/s,
+// whatever the number in flight).  The old form read every center fragment
+// straight from L2 (32 rows per load instruction) and waited on it at every
+// chunk.
+constexpr int AD_KS = 128, AD_NST = 2;
+constexpr int AD_CPR = AD_KS / 8;                 // 16-byte chunks per row
+constexpr int AD_RPP = 1024 / (AD_KS * 2);        // rows per 1 KB piece
+constexpr int AD_CPIECES = AB_MAXC / AD_RPP, AD_PIECES = AD_CPIECES + AB_ROWS / AD_RPP;
 constexpr int AD_STAGE = AD_PIECES * 1024;
 constexpr int AD_QLO = AD_PIECES / AB_WAVES, AD_NHI = AD_PIECES % AB_WAVES;
 constexpr int AD_QMAX = AD_QLO + (AD_NHI ? 1 : 0);
 constexpr int AD_SMEM = AD_NST * AD_STAGE;
 static_assert(AD_SMEM + (int)sizeof(AssignSmall) <= 160 * 1024, "LDS budget");
 static_assert(AB_SEG % AD_KS == 0, "segments are whole stages");
+static_assert(AD_NST == 2, "the loop issues one stage ahead");
 
 template <int ID_BYTES>
 __global__ void __launch_bounds__(64 * AB_WAVES) assign_dma_kernel(EncBatch B) {
@@ -702,24 +708,22 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_dma_kernel(EncBatch B) {
     const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
     const int hf = lane >> 5, l32 = lane & 31;
     assign_small_init(sm, t);
-    // this wave's pieces e = wave + AB_WAVES i: center rows 8e .. +8 (the
-    // last row past C), then input rows 8(e - AD_CPIECES) .. +8 (the last row
-    // past the end); lane L brings chunk (L % 8) ^ (L / 8) of its row
+    // this wave's pieces e = wave + AB_WAVES i: center rows AD_RPP e .. (the
+    // last row past C), then input rows (the last row past the end); lane L
+    // brings slot L % AD_CPR of its row, logical chunk (L % AD_CPR) ^ (row % 8)
     const uint16_t* src[AD_QMAX];
-    int64_t ldr[AD_QMAX];
 #pragma unroll
     for (int i = 0; i < AD_QMAX; ++i) {
         const int e = wave + AB_WAVES * i;
-        const int ch = 8 * ((lane & 7) ^ (lane >> 3));
+        const int q = AD_RPP * e + lane / AD_CPR;          // row of the stage image
+        const int ch = 8 * ((lane % AD_CPR) ^ (q & 7));
         if (e < AD_CPIECES) {
-            src[i] = P.centers + (int64_t)min(8 * e + (lane >> 3), C - 1) * HD + ch;
+            src[i] = P.centers + (int64_t)min(q, C - 1) * HD + ch;
         } else {
-            const int64_t m = min(row0 + 8 * (e - AD_CPIECES) + (lane >> 3), rows - 1);
+            const int64_t m = min(row0 + (q - AB_MAXC), rows - 1);
             src[i] = P.xb + m * P.ldx + ch;
         }
-        ldr[i] = 0;
     }
-    (void)ldr;
     auto issue = [&](int stg) {
         unsigned char* dst = smem_raw + (stg % AD_NST) * AD_STAGE;
 #pragma unroll
@@ -731,24 +735,14 @@ __global__ void __launch_bounds__(64 * AB_WAVES) assign_dma_kernel(EncBatch B) {
     f32x16 acc = {}, tot = {};
     float cseg = 0.0f, xsq = 0.0f;
     double cn = 0.0;
-    const int xrow_b = (AB_MAXC + l32) * 128, crow_b = col * 128;
-#pragma unroll
-    for (int j = 0; j < AD_NST - 1; ++j)
-        if (j < S) issue(j);
+    const int xrow_b = (AB_MAXC + l32) * (AD_KS * 2), crow_b = col * (AD_KS * 2);
+    issue(0);
     for (int it = 0; it < S; ++it) {
-        const int later = min(AD_NST - 2, S - 1 - it);
-        static_assert(AD_NST - 2 == 2, "wait counts assume two later stages");
-        if (wave < AD_NHI) {
-            if (later >= 2) wait_vmcnt<2 * (AD_QLO + 1)>();
-            else if (later == 1) wait_vmcnt<AD_QLO + 1>();
-            else wait_vmcnt<0>();
-        } else {
-            if (later >= 2) wait_vmcnt<2 * AD_QLO>();
-            else if (later == 1) wait_vmcnt<AD_QLO>();
-            else wait_vmcnt<0>();
-        }
+        // stage it landed (nothing later is in flight yet), then the buffer
+        // of stage it - 1 is free for stage it + 1
+        wait_vmcnt<0>();
         lds_barrier();
-        if (it + AD_NST - 1 < S) issue(it + AD_NST - 1);
+        if (it + 1 < S) issue(it + 1);
         const unsigned char* sb = smem_raw + (it % AD_NST) * AD_STAGE;
         bf16x8 af[AD_KS / 16], cf[AD_KS / 16];
 #pragma unroll
@@ -949,28 +943,33 @@ __global__ void __launch_bounds__(256) encode_gemm_kernel(EncodeA al,
 // accumulation (MG nanokv_codec.py:344-347: the residual minus the mean, in
 // bf16, through the bf16 operator).  A block of six waves owns 32 rows x 192
 // coefficient columns (wave w: columns 32w .. 32w + 32) and walks K in
-// 64-wide stages.  Every operand goes global -> LDS by 1 KB DMA pieces (no
-// register staging, so no wait in the loop covers more than the stage it
-// needs), two stages ahead, into a ring of EP_NST stage buffers:
-//   [W_enc 192 rows x 128 B][inputs 32 rows][center values 32 rows][mean]
-// (the mean piece holds the stage's 64 means four times).  Iteration i: wait
-// for stage i, barrier, issue stage i + 2, then waves 0-3 turn stage i into
-// the bf16 residual image (one 16-byte unit of one row per thread) while
-// every wave runs the 4 MFMAs of stage i - 1 on the previous image.  W and
-// the residual image are [row][8 chunks of 16 bytes] with chunk c of row q at
-// slot c ^ (q % 8), so the operand reads (32 rows at one chunk) are free of
-// bank conflicts.  Needs K % 64 == 0 and 16-byte aligned rows.
-constexpr int EP_ROWS = 32, EP_WAVES = 6, EP_COLS = 32 * EP_WAVES, EP_NST = 4, EP_KS = 64;
-constexpr int EP_WPIECES = EP_COLS / 8;   // W rows per 1 KB piece: 8
+// 128-wide stages.  Every operand goes global -> LDS by 1 KB DMA pieces,
+// double-buffered (no register staging, so no wait covers more than the
+// stage it needs):
+//   [W_enc 192 rows x 256 B][inputs 32 rows][center values 32 rows][mean]
+// (the mean piece holds the stage's 128 means twice).  Stage i: wait, barrier,
+// issue stage i + 1, waves 0-3 turn stage i into the bf16 residual image (two
+// 16-byte units of one row per thread), barrier, 8 MFMAs per wave.  A block's
+// stream is bound by a fixed cost per barrier plus one per piece, so few
+// large stages stream faster than many small ones (64-wide stages four deep
+// took 34.5-39.6 us for a 1,560-row K+V chunk).  W and the residual image are
+// [row][16 chunks of 16 bytes] with chunk c of row q at slot c ^ (q % 8), so
+// the operand reads (32 rows at one chunk) are free of bank conflicts.  Needs
+// K % 128 == 0 and 16-byte aligned rows.
+constexpr int EP_ROWS = 32, EP_WAVES = 6, EP_COLS = 32 * EP_WAVES, EP_KS = 128;
+constexpr int EP_CPR = EP_KS / 8;                  // 16-byte chunks per bf16 row
+constexpr int EP_RPP = 1024 / (EP_KS * 2);         // bf16 rows per 1 KB piece
+constexpr int EP_WPIECES = EP_COLS / EP_RPP;
 
 template <bool XB>
 struct EncProjFmt {
-    static constexpr int XPIECES = XB ? 4 : 8;                       // 32 input rows
-    static constexpr int X0 = EP_WPIECES, C0 = X0 + XPIECES, M0 = C0 + 4;
+    static constexpr int XROW = EP_KS * (XB ? 2 : 4);               // input bytes per row
+    static constexpr int XPIECES = EP_ROWS * XROW / 1024;
+    static constexpr int X0 = EP_WPIECES, C0 = X0 + XPIECES, M0 = C0 + EP_ROWS / EP_RPP;
     static constexpr int PIECES = M0 + 1;
     static constexpr int STAGE = PIECES * 1024;                      // bytes
     static constexpr int AIMG = EP_ROWS * EP_KS * 2;                 // residual image bytes
-    static constexpr int SMEM = EP_NST * STAGE + 2 * AIMG;
+    static constexpr int SMEM = 2 * STAGE + AIMG;
     // pieces per wave and stage: the first PIECES % EP_WAVES waves take one more
     static constexpr int QLO = PIECES / EP_WAVES, NHI = PIECES % EP_WAVES;
     static constexpr int QMAX = QLO + (NHI ? 1 : 0);
@@ -1005,30 +1004,29 @@ __global__ void __launch_bounds__(64 * EP_WAVES) encode_proj_kernel(EncBatch B) 
         const unsigned char* sp = reinterpret_cast<const unsigned char*>(P.w_enc);
         int64_t st = 0;
         if (e < F::X0) {
-            const int row = min(n0 + 8 * e + (lane >> 3), r - 1);
+            // W row n0 + q, slot lane % EP_CPR holds chunk slot ^ (q % 8)
+            const int q = EP_RPP * e + lane / EP_CPR;
+            const int row = min(n0 + q, r - 1);
             sp = reinterpret_cast<const unsigned char*>(P.w_enc + (int64_t)row * K +
-                                                        8 * ((lane & 7) ^ (lane >> 3)));
+                                                        8 * ((lane % EP_CPR) ^ (q & 7)));
             st = 2 * EP_KS;
         } else if (e < F::C0) {
-            if constexpr (XB) {
-                const int64_t m = xrow(8 * (e - F::X0) + (lane >> 3));
-                sp = reinterpret_cast<const unsigned char*>(P.xb + m * P.ldx + 8 * (lane & 7));
-                st = 2 * EP_KS;
-            } else {
-                const int64_t m = xrow(4 * (e - F::X0) + (lane >> 4));
-                sp = reinterpret_cast<const unsigned char*>(P.x + m * P.ldx + 4 * (lane & 15));
-                st = 4 * EP_KS;
-            }
+            constexpr int CPRX = F::XROW / 16, RPPX = 1024 / F::XROW;
+            const int64_t m = xrow(RPPX * (e - F::X0) + lane / CPRX);
+            const int off = 16 * (lane % CPRX);
+            sp = XB ? reinterpret_cast<const unsigned char*>(P.xb + m * P.ldx) + off
+                    : reinterpret_cast<const unsigned char*>(P.x + m * P.ldx) + off;
+            st = F::XROW;
         } else if (e < F::M0) {
             if (P.centers) {
-                const int64_t m = xrow(8 * (e - F::C0) + (lane >> 3));
+                const int64_t m = xrow(EP_RPP * (e - F::C0) + lane / EP_CPR);
                 sp = reinterpret_cast<const unsigned char*>(P.centers + (int64_t)B.id_of(P, m) * K +
-                                                            8 * (lane & 7));
+                                                            8 * (lane % EP_CPR));
                 st = 2 * EP_KS;
             }
         } else if (e == F::M0) {
             if (P.mean) {
-                sp = reinterpret_cast<const unsigned char*>(P.mean + 4 * (lane & 15));
+                sp = reinterpret_cast<const unsigned char*>(P.mean + 4 * (lane % (EP_KS / 4)));
                 st = 4 * EP_KS;
             }
         }
@@ -1036,86 +1034,83 @@ __global__ void __launch_bounds__(64 * EP_WAVES) encode_proj_kernel(EncBatch B) 
         adv[i] = st;
     }
     auto issue = [&](int stg) {
-        unsigned char* dst = smem_raw + (stg % EP_NST) * F::STAGE;
+        unsigned char* dst = smem_raw + (stg & 1) * F::STAGE;
 #pragma unroll
         for (int i = 0; i < F::QMAX; ++i) {
             const int e = wave + EP_WAVES * i;
             if (i < F::QLO || wave < F::NHI) dma16(src[i] + stg * adv[i], dst + 1024 * e);
         }
     };
-    unsigned char* aimg = smem_raw + EP_NST * F::STAGE;
+    unsigned char* aimg = smem_raw + 2 * F::STAGE;
     const bool prod = wave < 4;
-    const int arow = (t >> 3) & 31, ach = t & 7;
-    const bool arow_ok = m0 + arow < P.M;
-    // stage stg (landed) -> residual image stg % 2; absent centers or mean
+    // stage stg (landed) -> the residual image; absent centers or mean
     // subtract zeros (x - 0 = x exactly), so every read is unconditional
     const bool has_c = P.centers != nullptr, has_m = P.mean != nullptr;
     auto prep = [&](int stg) {
-        const unsigned char* sb = smem_raw + (stg % EP_NST) * F::STAGE;
-        const u32x4 c = *reinterpret_cast<const u32x4*>(sb + 1024 * F::C0 + arow * 128 + 16 * ach);
-        const f32x4* mp = reinterpret_cast<const f32x4*>(sb + 1024 * F::M0 + 32 * ach);
-        const f32x4 u0 = mp[0], u1 = mp[1];
-        float xv[8];
-        if constexpr (XB) {
-            const u32x4 w = *reinterpret_cast<const u32x4*>(sb + 1024 * F::X0 + arow * 128 + 16 * ach);
+        const unsigned char* sb = smem_raw + (stg & 1) * F::STAGE;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) {
-                xv[2 * e] = __uint_as_float(w[e] << 16);
-                xv[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+        for (int u = 0; u < 2; ++u) {
+            const int unit = t + 256 * u;                       // of 32 rows x 16 chunks
+            const int arow = unit / EP_CPR, ach = unit % EP_CPR;
+            const u32x4 c = *reinterpret_cast<const u32x4*>(sb + 1024 * F::C0 + arow * (EP_KS * 2) + 16 * ach);
+            const f32x4* mp = reinterpret_cast<const f32x4*>(sb + 1024 * F::M0 + 32 * ach);
+            const f32x4 u0 = mp[0], u1 = mp[1];
+            float xv[8];
+            if constexpr (XB) {
+                const u32x4 w = *reinterpret_cast<const u32x4*>(sb + 1024 * F::X0 + arow * F::XROW + 16 * ach);
+#pragma unroll
+                for (int e = 0; e < 4; ++e) {
+                    xv[2 * e] = __uint_as_float(w[e] << 16);
+                    xv[2 * e + 1] = __uint_as_float(w[e] & 0xffff0000u);
+                }
+            } else {
+                const f32x4* xp = reinterpret_cast<const f32x4*>(sb + 1024 * F::X0 + arow * F::XROW + 32 * ach);
+                const f32x4 a0 = xp[0], a1 = xp[1];
+#pragma unroll
+                for (int e = 0; e < 4; ++e) { xv[e] = a0[e]; xv[4 + e] = a1[e]; }
             }
-        } else {
-            const f32x4* xp = reinterpret_cast<const f32x4*>(sb + 1024 * F::X0 + arow * 256 + 32 * ach);
-            const f32x4 a0 = xp[0], a1 = xp[1];
 #pragma unroll
-            for (int e = 0; e < 4; ++e) { xv[e] = a0[e]; xv[4 + e] = a1[e]; }
+            for (int e = 0; e < 8; ++e) {
+                const uint32_t cw = (e & 1) ? (c[e >> 1] & 0xffff0000u) : (c[e >> 1] << 16);
+                const float cv = has_c ? __uint_as_float(cw) : 0.0f;
+                const float mv = has_m ? (e < 4 ? u0[e] : u1[e - 4]) : 0.0f;
+                xv[e] = (xv[e] - cv) - mv;
+            }
+            const bool ok = m0 + arow < P.M;
+            u32x4 o;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o[e] = ok ? pack_bf16x2(xv[2 * e], xv[2 * e + 1]) : 0u;
+            *reinterpret_cast<u32x4*>(aimg + arow * (EP_KS * 2) + 16 * (ach ^ (arow & 7))) = o;
         }
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const uint32_t cw = (e & 1) ? (c[e >> 1] & 0xffff0000u) : (c[e >> 1] << 16);
-            const float cv = has_c ? __uint_as_float(cw) : 0.0f;
-            const float mv = has_m ? (e < 4 ? u0[e] : u1[e - 4]) : 0.0f;
-            xv[e] = (xv[e] - cv) - mv;
-        }
-        u32x4 o;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) o[e] = arow_ok ? pack_bf16x2(xv[2 * e], xv[2 * e + 1]) : 0u;
-        *reinterpret_cast<u32x4*>(aimg + (stg & 1) * F::AIMG + arow * 128 + 16 * (ach ^ (arow & 7))) = o;
     };
     const bool cols = n0 + 32 * wave < r;
     f32x16 acc = {};
-    const int slot_row = l32 * 128, wrow = (32 * wave + l32) * 128;
+    const int arow_b = l32 * (EP_KS * 2), wrow_b = (32 * wave + l32) * (EP_KS * 2);
     auto compute = [&](int stg) {
-        const unsigned char* ar = aimg + (stg & 1) * F::AIMG + slot_row;
-        const unsigned char* wr = smem_raw + (stg % EP_NST) * F::STAGE + wrow;
+        const unsigned char* wr = smem_raw + (stg & 1) * F::STAGE + wrow_b;
         bf16x8 af[EP_KS / 16], wf[EP_KS / 16];
 #pragma unroll
         for (int k16 = 0; k16 < EP_KS / 16; ++k16) {
             const int slot = 16 * ((2 * k16 + hf) ^ (l32 & 7));
-            af[k16] = lds_b128(reinterpret_cast<const uint16_t*>(ar + slot));
+            af[k16] = lds_b128(reinterpret_cast<const uint16_t*>(aimg + arow_b + slot));
             wf[k16] = lds_b128(reinterpret_cast<const uint16_t*>(wr + slot));
         }
-        // all eight reads in flight before the first product
+        // all reads in flight before the first product
         __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
         for (int k16 = 0; k16 < EP_KS / 16; ++k16)
             acc = __builtin_amdgcn_mfma_f32_32x32x16_bf16(af[k16], wf[k16], acc, 0, 0, 0);
     };
     issue(0);
-    if (S > 1) issue(1);
-    for (int it = 0; it <= S; ++it) {
-        if (it < S) {
-            // stage it landed; stage it + 1 (issued after it) may stay in flight
-            if (it + 1 < S) {
-                if (wave < F::NHI) wait_vmcnt<F::QLO + 1>();
-                else wait_vmcnt<F::QLO>();
-            } else {
-                wait_vmcnt<0>();
-            }
-        }
+    for (int it = 0; it < S; ++it) {
+        // stage it landed (nothing later is in flight yet); after the barrier
+        // every wave is past stage it - 1, whose buffer takes stage it + 1
+        wait_vmcnt<0>();
         lds_barrier();
-        if (it + 2 < S) issue(it + 2);
-        if (it < S && prod) prep(it);
-        if (it > 0 && cols) compute(it - 1);
+        if (it + 1 < S) issue(it + 1);
+        if (prod) prep(it);
+        lds_barrier();
+        if (cols) compute(it);
     }
     const int n = n0 + 32 * wave + l32;
     if (cols && n < r) {
@@ -1683,6 +1678,7 @@ int encode_batch(hipStream_t s, const nkv_encode_args* a, int n) {
     // staged projection; a bf16 input takes only those
     const bool fast_search = a->num_centers <= AB_MAXC && HD % AB_SEG == 0 && HD <= AB_MAXK;
     const bool fast_proj = HD % 256 == 0;
+    static_assert(256 % EP_KS == 0, "the staged projection needs HD % EP_KS == 0");
     const bool search = a->centers && !a->ids_in;
     NKV_REQUIRE(!xb || (aligned && fast_proj && (!search || fast_search)), NKV_ERR_UNSUPPORTED,
                 "a bf16 input needs HD % 256 == 0, 16-byte aligned rows and, to search, at most 256 "
