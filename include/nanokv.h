@@ -64,7 +64,7 @@
 extern "C" {
 #endif
 
-#define NKV_ABI_VERSION 6
+#define NKV_ABI_VERSION 7
 
 enum nkv_status {
     NKV_OK = 0,
@@ -580,6 +580,43 @@ size_t nkv_fast_attend_workspace_size(const nkv_fast_args* args);
 
 int nkv_fast_attend(void* stream, const nkv_fast_args* args, void* workspace,
                     size_t workspace_bytes);
+
+/*
+ * Rows of a [B, S, H, D] bf16 tensor read through a reader group, for MG's
+ * low_native extension (mg35.py:241-249, 324-336): the mosaic / current
+ * tokens moved into the low partition, keys and values projected from their
+ * pre-RoPE rows by the group's affine (einsum('bhnd,hde->bhne'), bf16), and
+ * the group query.  For head i of the group (original head heads[i]):
+ *   y = bf16(x[b, s, heads[i], :] . w[i])          w [nh, D, E] bf16 (NULL:
+ *                                                  the identity, E = D)
+ *   y rotated on its pairs at the position of row s (rope, NULL = none;
+ *   pairs [nh, E/2]: original pair of reader pair j, NULL = pair j), the
+ *   arithmetic of nkv_rope_apply (rope_selected, CN/core.py:75-91)
+ *   y multiplied on its 8-dim blocks by the camera of row s (camera, FULL
+ *   layout, NULL = none; blocks [nh, E/8]: sub-frame of reader block j,
+ *   NULL = j % 4), the arithmetic of the reader queries of nkv_fast_attend
+ *   (camera_selected, CN/core.py:110-137)
+ * out [B, S, nh, out_width] bf16 (contiguous), columns E .. out_width - 1
+ * zero, so that a reader key or query of width E < 128 can be attended by
+ * nkv_attend at width 128 (the zero columns add nothing to q.k).  E and
+ * out_width are multiples of 8, E <= out_width, D <= 512.  No counterpart
+ * as one function in the reference.
+ */
+typedef struct nkv_reader_rows_args {
+    int B, H, D, E, nh, out_width;
+    int64_t S;
+    const uint16_t* x;
+    int64_t x_sb, x_st, x_sh;
+    const int32_t* heads;         /* [nh] device */
+    const uint16_t* w;            /* [nh, D, E] bf16 device, or NULL */
+    const nkv_rope* rope;         /* host pointer or NULL */
+    const int32_t* pairs;         /* [nh, E/2] device or NULL */
+    const nkv_camera* camera;     /* host pointer or NULL */
+    const int32_t* blocks;        /* [nh, E/8] device or NULL */
+    uint16_t* out;
+} nkv_reader_rows_args;
+
+int nkv_reader_rows(void* stream, const nkv_reader_rows_args* args);
 
 /*
  * Log-sum-exp merge of two attention partitions (CN/core.py:33-42):

@@ -13,7 +13,7 @@ from pathlib import Path
 
 LIB_PATH = Path(__file__).resolve().parent / "libnanokv_hip.so"
 
-NKV_ABI_VERSION = 6
+NKV_ABI_VERSION = 7
 NKV_OK = 0
 NKV_ERR_INVALID = -1
 NKV_ERR_UNSUPPORTED = -2
@@ -34,7 +34,7 @@ EXPORTED = (
     "nkv_encode", "nkv_encode_batch", "nkv_decode", "nkv_attend_workspace_size", "nkv_attend", "nkv_lse_merge",
     "nkv_fast_attend_workspace_size", "nkv_fast_attend", "nkv_rope_apply", "nkv_int8_pack",
     "nkv_int8_dequant", "nkv_c64_fit_workspace_size", "nkv_c64_fit", "nkv_camera_apply",
-    "nkv_attend_static", "nkv_lift_lse_combine", "nkv_finish",
+    "nkv_attend_static", "nkv_lift_lse_combine", "nkv_finish", "nkv_reader_rows",
 )
 NKV_STATIC_SCRATCH_BYTES = 64 << 20
 
@@ -134,6 +134,18 @@ class NkvFastArgs(Structure):
     ]
 
 
+class NkvReaderRowsArgs(Structure):
+    _fields_ = [
+        ("B", c_int), ("H", c_int), ("D", c_int), ("E", c_int), ("nh", c_int),
+        ("out_width", c_int), ("S", c_int64),
+        ("x", c_void_p), ("x_sb", c_int64), ("x_st", c_int64), ("x_sh", c_int64),
+        ("heads", c_void_p), ("w", c_void_p),
+        ("rope", POINTER(NkvRope)), ("pairs", c_void_p),
+        ("camera", POINTER(NkvCamera)), ("blocks", c_void_p),
+        ("out", c_void_p),
+    ]
+
+
 class NkvLiftCombineArgs(Structure):
     _fields_ = [
         ("B", c_int), ("H", c_int), ("Q", c_int), ("low_dim", c_int),
@@ -208,6 +220,8 @@ def _declare(lib: ctypes.CDLL) -> None:
     lib.nkv_fast_attend_workspace_size.argtypes = [POINTER(NkvFastArgs)]
     lib.nkv_fast_attend.restype = c_int
     lib.nkv_fast_attend.argtypes = [c_void_p, POINTER(NkvFastArgs), c_void_p, c_size_t]
+    lib.nkv_reader_rows.restype = c_int
+    lib.nkv_reader_rows.argtypes = [c_void_p, POINTER(NkvReaderRowsArgs)]
     lib.nkv_c64_fit_workspace_size.restype = c_size_t
     lib.nkv_c64_fit_workspace_size.argtypes = [c_int, c_int64, c_int]
     lib.nkv_c64_fit.restype = c_int

@@ -235,6 +235,7 @@ struct QueryLowGroup {
     const int32_t* pairs;
     const int32_t* cams;
     int nh, d;
+    int ostride;   // elements per q_low row (>= d; the columns past d are zeroed)
 };
 struct QueryLowBatch {
     QueryLowGroup g[QL_MAX];
@@ -254,13 +255,17 @@ __global__ void __launch_bounds__(256) query_low_kernel(QueryLowBatch P) {
         if (i < P.n && gt >= P.first[i]) gi = i;
     const QueryLowGroup& G = P.g[gi];
     const int64_t tid = gt - P.first[gi];
-    const int nbk = G.d / 8;
-    const int j = (int)(tid % nbk);
-    const int64_t row = tid / nbk;  // (b, t, i)
+    const int nbk = G.d / 8, nunit = G.ostride / 8;
+    const int j = (int)(tid % nunit);
+    const int64_t row = tid / nunit;  // (b, t, i)
     const int i = (int)(row % G.nh);
     const int64_t t = (row / G.nh) % P.Q;
     const int b = (int)(row / ((int64_t)G.nh * P.Q));
-    uint16_t* dst = G.q_low + row * G.d + 8 * j;
+    uint16_t* dst = G.q_low + row * G.ostride + 8 * j;
+    if (j >= nbk) {
+        *reinterpret_cast<u32x4*>(dst) = u32x4{0u, 0u, 0u, 0u};
+        return;
+    }
     const uint16_t* from = dst;
     if (G.src) {
         const int hq = min(max(ldg(G.heads + i), 0), P.H - 1);
@@ -797,6 +802,7 @@ int query_transforms(hipStream_t s, const nkv_fast_args* f, unsigned char* ws,
         q.cams = a.camera ? G.cam_blocks : nullptr;
         q.nh = G.num_heads;
         q.d = G.d;
+        q.ostride = G.d;
         P.first[P.n + 1] = P.first[P.n] + (int64_t)a.B * a.Q * G.num_heads * (G.d / 8);
         if (++P.n == QL_MAX) {
             int rc = flush();
@@ -900,4 +906,63 @@ extern "C" int nkv_fast_attend(void* stream, const nkv_fast_args* f, void* works
         NKV_LAUNCH_CHECK();
     }
     return finish();
+}
+
+extern "C" int nkv_reader_rows(void* stream, const nkv_reader_rows_args* a) {
+    clear_error();
+    NKV_REQUIRE(a, NKV_ERR_INVALID, "null args");
+    NKV_REQUIRE(a->B >= 1 && a->H >= 1 && a->nh >= 1 && a->S >= 0, NKV_ERR_INVALID,
+                "B, H and nh must be >= 1 and S >= 0");
+    NKV_REQUIRE(a->D > 0 && a->D % 8 == 0 && a->D <= 512, NKV_ERR_INVALID,
+                "D must be a positive multiple of 8 (at most 512)");
+    NKV_REQUIRE(a->E > 0 && a->E % 8 == 0 && a->out_width >= a->E && a->out_width % 8 == 0,
+                NKV_ERR_INVALID, "E and out_width must be multiples of 8 with E <= out_width");
+    NKV_REQUIRE(a->w || a->E == a->D, NKV_ERR_INVALID, "without w the rows keep their width (E == D)");
+    if (a->S == 0) return NKV_OK;
+    NKV_REQUIRE(a->x && a->heads && a->out, NKV_ERR_INVALID, "x, heads and out are required");
+    NKV_REQUIRE(rows16(a->x, a->x_sb, a->x_st, a->x_sh) &&
+                    reinterpret_cast<uintptr_t>(a->out) % 16 == 0,
+                NKV_ERR_INVALID, "x rows and out must be 16-byte aligned (strides divisible by 8)");
+    hipStream_t s = (hipStream_t)stream;
+    QueryLowBatch P{};
+    P.H = a->H;
+    P.B = a->B;
+    P.Q = a->S;
+    P.s_b = a->x_sb;
+    P.s_t = a->x_st;
+    P.s_h = a->x_sh;
+    if (a->rope) {
+        int rc = rope_from_abi(a->rope, a->D, &P.pos);
+        if (rc) return rc;
+    }
+    if (a->camera) {
+        NKV_REQUIRE(a->camera->layout == NKV_CAMERA_FULL, NKV_ERR_UNSUPPORTED,
+                    "reader rows take the camera on their 8-dim blocks (the FULL layout)");
+        int rc = camera_from_abi(a->camera, a->D, a->B, &P.cam);
+        if (rc) return rc;
+    }
+    if (a->w) {
+        // y = bf16(x[b, s, heads[i]] . w[i]) into out [B, S, nh, out_width]
+        const int64_t W = a->out_width;
+        int rc = project<false, false>(s, a->x, a->x_sb, a->x_st, a->x_sh, nullptr, 0, a->heads, a->H,
+                                       a->w, a->D, a->E, a->B, a->nh, a->S, a->out,
+                                       a->S * a->nh * W, W, a->nh * W);
+        if (rc) return rc;
+        if (!a->rope && !a->camera && a->out_width == a->E) return NKV_OK;
+    }
+    // RoPE, camera, the identity copy through the head map and the zero columns
+    QueryLowGroup& g = P.g[0];
+    g.q_low = a->out;
+    g.src = a->w ? nullptr : a->x;
+    g.heads = a->heads;
+    g.pairs = a->rope ? a->pairs : nullptr;
+    g.cams = a->camera ? a->blocks : nullptr;
+    g.nh = a->nh;
+    g.d = a->E;
+    g.ostride = a->out_width;
+    P.n = 1;
+    P.first[1] = (int64_t)a->B * a->S * a->nh * (a->out_width / 8);
+    query_low_kernel<<<dim3((unsigned)cdiv(P.first[1], 256)), 256, 0, s>>>(P);
+    NKV_LAUNCH_CHECK();
+    return NKV_OK;
 }

@@ -163,6 +163,62 @@ def _rope_table(freqs, disable_t_pairs: int, device) -> ops.RopeTable:
     return ops.RopeTable.from_freqs(f, device)
 
 
+def _native_low_segment(out, lse, groups, qp, all_k_pre, v_raw, native_low, low_keep, freqs_cur,
+                        t_pairs, disable_native_rope, camera_info, mosaic_frames, cur_frames,
+                        mosaic_tokens, q_rope, q_cam, out_cam, B, H, D):
+    """The low_native segment (MG35:241-249, 324-347), merged last into each
+    reader group's heads of out [B, Sq, H, D] (lse [B, H, Sq]): the moved
+    tokens' pre-RoPE keys and values read through the group's k_affine /
+    v_affine (the value lift folded in, as for the codec rows), rotated on
+    the reader pairs at their own positions and multiplied by their frames'
+    P^-1; the group query (q_reduce, RoPE, P^T) attends them at width 128 with
+    its reader columns zero-padded (nkv_reader_rows, then nkv_attend: the
+    zero columns add nothing to q.k); P of the query rows on the output; LSE
+    merge."""
+    device = out.device
+    Sk = int(native_low.numel())
+    sel = torch.nonzero(native_low).flatten().to(device)
+    k_low = all_k_pre.view(B, Sk, H, D).index_select(1, sel)
+    v_low = v_raw.view(B, Sk, H, D).index_select(1, sel)
+    low_rope = None
+    if not disable_native_rope:
+        low_rope = _rope_table(torch.as_tensor(freqs_cur).index_select(0, sel.cpu()), t_pairs,
+                               device)
+    low_cam = None
+    if camera_info is not None:
+        P_inv = camera_info[1][2]
+        # all_current_frames of MG35:245
+        tok_frames = (_expand_frames(list(mosaic_frames), mosaic_tokens)
+                      + _expand_frames(list(cur_frames), Sk - mosaic_tokens))
+        frames_low = [tok_frames[i] for i in sel.tolist()]
+        low_cam = ops.Camera(P_inv.to(device=device, dtype=torch.float32).contiguous(),
+                             torch.as_tensor(frames_low, dtype=torch.int32, device=device), 1,
+                             "full")
+    vis = None if low_keep is None else ops.Visibility.from_bool(low_keep, device)
+    out = out.clone()
+    lse = lse.clone()
+    for g in groups:
+        heads = g.heads.long()
+        q_g = ops.reader_rows(qp.to(torch.bfloat16), g.heads, g.q_reduce, rope=q_rope,
+                              pairs=g.rope_pairs if q_rope is not None else None, camera=q_cam,
+                              blocks=g.cam_blocks if q_cam is not None else None, out_width=D)
+        k_g = ops.reader_rows(k_low, g.heads, g.k_affine, rope=low_rope,
+                              pairs=g.rope_pairs if low_rope is not None else None,
+                              camera=low_cam, blocks=g.cam_blocks if low_cam is not None else None,
+                              out_width=D)
+        v_g = ops.reader_rows(v_low, g.heads, g.v_affine, camera=low_cam, out_width=D)
+        o_g, l_g = ops.attend(q_g, k_g, v_g, None, None, softmax_scale=D ** -0.5,
+                              visibility=vis)
+        if out_cam is not None:
+            o_g = ops.camera_apply(o_g, out_cam)
+        a = out.index_select(2, heads).contiguous()
+        la = lse.index_select(1, heads).transpose(1, 2).contiguous()
+        m, lm = ops.lse_merge(a, la, o_g.contiguous(), l_g.transpose(1, 2).contiguous())
+        out.index_copy_(2, heads, m)
+        lse.index_copy_(1, heads, lm.transpose(1, 2).contiguous())
+    return out
+
+
 # ---------------------------------------------------------------- the hook
 @torch.no_grad()
 def maybe_attention(self_attn, q_pre, q_native, k_native, v_raw, cur_k_pre, freqs_cur,
@@ -198,23 +254,30 @@ def maybe_attention(self_attn, q_pre, q_native, k_native, v_raw, cur_k_pre, freq
     recent = int(policy.get("recent_native_frames", 0))
     stride = int(policy.get("anchor_stride", 0))
     sink = int(policy.get("sink_native_frames", 0))
+    # low_native: the separately calibrated extension that reads mosaic and /
+    # or current tokens through the readers instead of natively
+    # (MG35:171-175, 241-249, 324-347)
     low_native = policy.get("low_native", "none")
+    Sk = int(k_native.shape[1])
+    native_low = torch.zeros(Sk, dtype=torch.bool)
     if cache_tokens and low_native != "none":
-        # the separately calibrated extension that reads mosaic / current
-        # tokens through the readers (MG35:171-175, 241-249, 324-328)
-        raise NotImplementedError(f"low_native={low_native!r} is not built; the deployed "
-                                  "policy keeps current and mosaic tokens native")
+        if low_native in ("all", "mosaic"):
+            native_low[:mosaic_tokens] = True
+        if low_native in ("all", "current"):
+            native_low[mosaic_tokens:] = True
     r = route(frames, chunk_ids, cache_read_chunk_id, cache_tokens, recent, stride, sink,
               bool(policy.get("native_history", False)))
     # no old low-dimensional history: the native path is cheaper and
     # numerically authoritative (MG35:187-190)
-    if r["low_count"] == 0:
+    if r["low_count"] == 0 and not bool(native_low.any()):
         return None
+    if bool(native_low.any()) and all_k_pre is None:
+        raise ValueError("low_native needs all_k_pre, the pre-RoPE keys of the mosaic and "
+                         "current tokens")
 
     device = q_pre.device
     B, D, H = int(q_pre.shape[0]), reader.native_dim, num_heads
     Sq = int(q_native.shape[1]) - mosaic_tokens
-    Sk = int(k_native.shape[1])
     q = q_native[:, mosaic_tokens:].reshape(B, Sq, H, D)
     qp = q_pre[:, mosaic_tokens:].reshape(B, Sq, H, D)
     kc = k_native.reshape(B, Sk, H, D)
@@ -250,17 +313,30 @@ def maybe_attention(self_attn, q_pre, q_native, k_native, v_raw, cur_k_pre, freq
 
     keep = visibility_keep(Sq, mosaic_tokens, Sk - mosaic_tokens, list(cur_frames), hole_keep,
                            cur_cache_chunk_ids)
+    low_keep = None
+    if bool(native_low.any()):
+        # the native partition keeps the other tokens; the moved tokens keep
+        # their visibility in their own segment (MG35:284-286)
+        full = torch.ones(Sq, Sk, dtype=torch.bool) if keep is None else keep.cpu()
+        low_keep = full[:, native_low]
+        low_keep = None if bool(low_keep.all()) else low_keep
+        keep = full & ~native_low[None, :]
     vis = None if keep is None else ops.Visibility.from_bool(keep, device)
 
     key, value = nanokv_codec.history_codecs(cache["k"], cache["v"], device)
     protect_rows = torch.nonzero(r["protect"]).flatten().to(torch.int32).to(device)
     low_rows = torch.nonzero(r["low"]).flatten().to(torch.int32).to(device)
     groups = [g.tensors(rope=kv_rope is not None, camera=use_camera) for g in reader.groups]
-    out, _ = ops.fast_attend(q.to(torch.bfloat16), kc.to(torch.bfloat16), vc.to(torch.bfloat16),
-                             key, value, protect_rows, low_rows, groups,
-                             softmax_scale=reader.native_dim ** -0.5, return_lse=False,
-                             rope=kv_rope, q_pre=qp.to(torch.bfloat16), q_rope=q_rope,
-                             camera=kv_cam, q_camera=q_cam, visibility=vis, out_camera=out_cam)
+    out, lse = ops.fast_attend(q.to(torch.bfloat16), kc.to(torch.bfloat16), vc.to(torch.bfloat16),
+                               key, value, protect_rows, low_rows, groups,
+                               softmax_scale=reader.native_dim ** -0.5, return_lse=True,
+                               rope=kv_rope, q_pre=qp.to(torch.bfloat16), q_rope=q_rope,
+                               camera=kv_cam, q_camera=q_cam, visibility=vis, out_camera=out_cam)
+    if bool(native_low.any()):
+        out = _native_low_segment(out, lse, groups, qp, all_k_pre, v_raw, native_low,
+                                  low_keep, freqs_cur, t_pairs, disable_native_rope, camera_info,
+                                  mosaic_frames, cur_frames, mosaic_tokens, q_rope, q_cam,
+                                  out_cam, B, H, D)
     result = torch.zeros_like(q_native)
     result[:, mosaic_tokens:] = out.reshape(B, Sq, H * D).to(q_native.dtype)
     if write_cache and cache is not None:

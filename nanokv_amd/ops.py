@@ -19,7 +19,8 @@ from . import _lib
 from ._lib import (NKV_DTYPE_BF16, NKV_DTYPE_FP16, NKV_QUANT_BF16, NKV_QUANT_FP32,
                    NKV_SCHEDULE_AUTO, NKV_SCHEDULE_KEY_CHUNKS, NKV_SCHEDULE_QUERY_TILES,
                    NkvAttendArgs, NkvCodec, NkvDecodeArgs, NkvEncodeArgs, NkvFastArgs,
-                   NkvCamera, NkvFinishArgs, NkvLiftCombineArgs, NkvReaderGroup, NkvRope,
+                   NkvCamera, NkvFinishArgs, NkvLiftCombineArgs, NkvReaderGroup,
+                   NkvReaderRowsArgs, NkvRope,
                    NkvSegment, check, lib)
 
 _SCALE_CODES = {torch.bfloat16: NKV_DTYPE_BF16, torch.float16: NKV_DTYPE_FP16}
@@ -812,6 +813,58 @@ def camera_apply(x: torch.Tensor, camera: Camera, rows: Optional[torch.Tensor] =
     check("nkv_camera_apply", lib().nkv_camera_apply(
         _stream(device), byref(c), B, S, H, D, x.data_ptr(), x.stride(0), x.stride(1),
         x.stride(2), _ptr(rows), out.data_ptr(), out.stride(0), out.stride(1), out.stride(2)))
+    return out
+
+
+def reader_rows(x: torch.Tensor, heads: torch.Tensor, w: Optional[torch.Tensor] = None, *,
+                rope=None, pairs: Optional[torch.Tensor] = None,
+                camera: Optional[Camera] = None, blocks: Optional[torch.Tensor] = None,
+                out_width: Optional[int] = None) -> torch.Tensor:
+    """Rows of x [B, S, H, D] bf16 read through a reader group
+    (nkv_reader_rows): bf16(x[:, :, heads[i]] . w[i]) (w [nh, D, E] bf16;
+    None: the rows themselves), rotated on the retained pairs (pairs [nh,
+    E/2] int32) at row s of rope, multiplied on the 8-dim blocks (blocks
+    [nh, E/8] int32 sub-frames) by row s's camera; returns [B, S, nh,
+    out_width] bf16 whose columns past E are zero.  MG's low_native segment
+    (mg35.py:241-249, 324-336) and the group query of that segment."""
+    device = _require_gpu(x, heads, w, pairs, blocks)
+    if x.dtype != torch.bfloat16 or x.dim() != 4 or x.stride(3) != 1:
+        raise ValueError("x must be bf16 [B, S, H, D] with contiguous D")
+    B, S, H, D = (int(v) for v in x.shape)
+    _contig(heads, torch.int32, "heads")
+    nh = int(heads.numel())
+    E = D
+    if w is not None:
+        _contig(w, torch.bfloat16, "w")
+        if w.dim() != 3 or tuple(w.shape[:2]) != (nh, D):
+            raise ValueError("w must be bf16 [nh, D, E]")
+        E = int(w.shape[2])
+    W = E if out_width is None else int(out_width)
+    out = torch.empty((B, S, nh, W), device=device, dtype=torch.bfloat16)
+    a = NkvReaderRowsArgs()
+    a.B, a.H, a.D, a.E, a.nh, a.out_width, a.S = B, H, D, E, nh, W, S
+    a.x, a.x_sb, a.x_st, a.x_sh = x.data_ptr(), x.stride(0), x.stride(1), x.stride(2)
+    a.heads, a.w, a.out = heads.data_ptr(), _ptr(w), out.data_ptr()
+    keep = []
+    if rope is not None:
+        rs = rope.struct()
+        keep.append(rs)
+        a.rope = ctypes.pointer(rs)
+        if pairs is not None:
+            _contig(pairs, torch.int32, "pairs")
+            if tuple(pairs.shape) != (nh, E // 2):
+                raise ValueError("pairs must be int32 [nh, E/2]")
+            a.pairs = pairs.data_ptr()
+    if camera is not None:
+        cs = camera.struct()
+        keep.append(cs)
+        a.camera = ctypes.pointer(cs)
+        if blocks is not None:
+            _contig(blocks, torch.int32, "blocks")
+            if tuple(blocks.shape) != (nh, E // 8):
+                raise ValueError("blocks must be int32 [nh, E/8]")
+            a.blocks = blocks.data_ptr()
+    check("nkv_reader_rows", lib().nkv_reader_rows(_stream(device), byref(a)))
     return out
 
 

@@ -691,7 +691,7 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
                 groups: Sequence[dict], scale: float, heads: Optional[Sequence[int]] = None,
                 D: int = 128, dtype=np.float64, key_freqs: Optional[np.ndarray] = None,
                 q_pre_bf16=None, q_freqs: Optional[np.ndarray] = None, cur_mask=None,
-                key_cam=None, q_cam=None, out_cam=None, low_shift=None):
+                key_cam=None, q_cam=None, out_cam=None, low_shift=None, native_low=None):
     """NanoKV-Fast for one batch item: hybrid_attention (CN/core.py:278-310)
     with maybe_attention's partitions (CN/mg35.py:192-348), identity lift.
 
@@ -721,7 +721,17 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
     each low output before its lift.  q_bf16, k_cur and v_cur are taken as
     already transformed; a group's query comes from q_pre_bf16 when given.
     low_shift [H, D]: LingBot's value-mean correction (codec_native_attention.py
-    :779-785), added to each head's lifted low output before the merge."""
+    :779-785), added to each head's lifted low output before the merge.
+    native_low: MG's low_native segment (CN/mg35.py:241-249, 324-347), a
+    dict of k_pre_bf16 / v_pre_bf16 [n, H, D] (the pre-RoPE keys and the
+    values of the mosaic / current tokens moved into the low partition),
+    freqs [n, D/2] (their RoPE, used when key_freqs is given), cam [n, 4, 4,
+    4] (their P^-1, used when key_cam is given) and mask [Q, n] bool or
+    None; each group head reads them through k_affine / v_affine (bf16
+    einsums), rotates and transforms them as the codec low rows, attends them
+    with its group query and merges the result last, after the codec low
+    rows.  The caller removes these tokens from the native partition
+    (cur_mask)."""
     q = bf16_to_f32(q_bf16)
     Qn, H = q.shape[0], q.shape[1]
     heads = list(range(H)) if heads is None else list(heads)
@@ -758,7 +768,7 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
         if out_cam is not None:
             on = bf16_to_f32(camera_apply(f32_to_bf16(on)[:, None, :], out_cam, "full")[:, 0])
         grp = [(g, list(g["heads"]).index(h)) for g in groups if h in list(g["heads"])]
-        if grp and low.size:
+        if grp and (low.size or native_low is not None):
             g, i = grp[0]
             qh = q[:, h] if q_pre_bf16 is None else bf16_to_f32(q_pre_bf16)[:, h]
             if g.get("q_reduce") is not None:
@@ -773,6 +783,28 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
             vcb = g.get("v_cam_blocks")
             if q_cam is not None:
                 qh = bf16_to_f32(camera_blocks_apply(f32_to_bf16(qh), q_cam, kcams))
+            vd = int(np.asarray(g["v_read"][i]).shape[0])
+            vcams = np.arange(vd // 8) % 4 if vcb is None else np.asarray(vcb[i])
+            pairs = None
+            if key_freqs is not None:
+                rp = g.get("rope_pairs")
+                pairs = np.arange(qh.shape[1] // 2) if rp is None else np.asarray(rp[i])
+
+            def finish_segment(on, ln, ol, ll):
+                # P, the lift and the merge of one low segment (mg35.py:343-347)
+                ol = bf16_to_f32(f32_to_bf16(ol[0].astype(np.float32)))
+                if out_cam is not None:
+                    ol = bf16_to_f32(camera_blocks_apply(f32_to_bf16(ol), out_cam, vcams))
+                if g.get("lift") is not None:
+                    # lift_output (CN/core.py:202-204), applied before the merge (mg35.py:347)
+                    lf = bf16_to_f32(g["lift"][i]).astype(dtype)
+                    ol = bf16_to_f32(f32_to_bf16((ol.astype(dtype) @ lf).astype(np.float32)))
+                if low_shift is not None:
+                    ol = ol + np.asarray(low_shift, np.float64)[h]
+                mo, ml = merge(on, ln, ol, ll[0])
+                return bf16_to_f32(f32_to_bf16(np.asarray(mo, np.float32))), ml
+
+        if grp and low.size:
             kt, kb = reader_tables(key.get("centers_bf16"), key.get("mean"), h,
                                    None if g.get("k_affine") is None else g["k_affine"][i], D, dtype)
             vt, vb = reader_tables(value.get("centers_bf16"), value.get("mean"), h,
@@ -788,17 +820,26 @@ def fast_attend(q_bf16, k_cur_bf16, v_cur_bf16, key: dict, value: dict, protect_
             kl = bf16_to_f32(kl)
             vl = bf16_to_f32(vl)
             ol, ll = attention(qh[None], kl[None], vl[None], scale, dtype)
-            ol = bf16_to_f32(f32_to_bf16(ol[0].astype(np.float32)))
-            if out_cam is not None:
-                ol = bf16_to_f32(camera_blocks_apply(f32_to_bf16(ol), out_cam, vcams))
-            if g.get("lift") is not None:
-                # lift_output (CN/core.py:202-204), applied before the merge (mg35.py:347)
-                lf = bf16_to_f32(g["lift"][i]).astype(dtype)
-                ol = bf16_to_f32(f32_to_bf16((ol.astype(dtype) @ lf).astype(np.float32)))
-            if low_shift is not None:
-                ol = ol + np.asarray(low_shift, np.float64)[h]
-            mo, ml = merge(on, ln, ol, ll[0])
-            on, ln = bf16_to_f32(f32_to_bf16(np.asarray(mo, np.float32))), ml
+            on, ln = finish_segment(on, ln, ol, ll)
+        if grp and native_low is not None:
+            # the mosaic / current tokens read through the group's affine maps
+            # (mg35.py:324-328), then RoPE and the camera as the low rows
+            nl = native_low
+            kp = bf16_to_f32(np.asarray(nl["k_pre_bf16"]))[:, h].astype(dtype)
+            vp = bf16_to_f32(np.asarray(nl["v_pre_bf16"]))[:, h].astype(dtype)
+            ka, va = g.get("k_affine"), g.get("v_affine")
+            kk = f32_to_bf16((kp @ bf16_to_f32(ka[i]).astype(dtype)).astype(np.float32)) \
+                if ka is not None else f32_to_bf16(kp.astype(np.float32))
+            vv = f32_to_bf16((vp @ bf16_to_f32(va[i]).astype(dtype)).astype(np.float32)) \
+                if va is not None else f32_to_bf16(vp.astype(np.float32))
+            if key_freqs is not None:
+                kk = rope_apply(kk[:, None, :], np.asarray(nl["freqs"])[:, pairs])[:, 0]
+            if key_cam is not None:
+                kk = camera_blocks_apply(kk, np.asarray(nl["cam"]), kcams)
+                vv = camera_blocks_apply(vv, np.asarray(nl["cam"]), vcams)
+            ol, ll = attention(qh[None], bf16_to_f32(kk)[None], bf16_to_f32(vv)[None], scale,
+                               dtype, mask=nl.get("mask"))
+            on, ln = finish_segment(on, ln, ol, ll)
         outs.append(on)
         lses.append(ln)
     return np.stack(outs, 1), np.stack(lses, 0)

@@ -68,6 +68,7 @@ STRUCTS = {
     "nkv_decode_args": _lib.NkvDecodeArgs, "nkv_attend_args": _lib.NkvAttendArgs,
     "nkv_reader_group": _lib.NkvReaderGroup, "nkv_fast_args": _lib.NkvFastArgs,
     "nkv_lift_combine_args": _lib.NkvLiftCombineArgs, "nkv_finish_args": _lib.NkvFinishArgs,
+    "nkv_reader_rows_args": _lib.NkvReaderRowsArgs,
 }
 
 

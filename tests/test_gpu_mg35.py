@@ -69,7 +69,23 @@ def _freqs(positions):
 
 @pytest.mark.parametrize("camera,disable_t", [(False, False), (True, False), (True, True)])
 def test_maybe_attention_against_oracle(dev, tmp_path, monkeypatch, camera, disable_t):
-    policy = {"recent_native_frames": 2, "anchor_stride": 2, "sink_native_frames": 1}
+    _hook_case(dev, tmp_path, monkeypatch, camera, disable_t, "none")
+
+
+@pytest.mark.parametrize("low_native,camera,disable_t", [("all", True, False), ("mosaic", False, False),
+                                                         ("current", True, True)])
+def test_maybe_attention_low_native(dev, tmp_path, monkeypatch, low_native, camera, disable_t):
+    """MG's low_native extension (MG35:171-175, 241-249, 324-347): the mosaic
+    and / or current tokens leave the native partition and are read by each
+    reader group through its affine maps, with their own RoPE, P^-1 and
+    visibility, merged after the codec low rows; against the oracle's
+    native_low segment."""
+    _hook_case(dev, tmp_path, monkeypatch, camera, disable_t, low_native)
+
+
+def _hook_case(dev, tmp_path, monkeypatch, camera, disable_t, low_native):
+    policy = {"recent_native_frames": 2, "anchor_stride": 2, "sink_native_frames": 1,
+              "low_native": low_native}
     sh, lay, payload = _setup(dev, tmp_path, monkeypatch, policy)
     g = torch.Generator().manual_seed(11)
     # history: 7 frames committed in 4 chunks (4 segments), chunk ids per frame
@@ -117,7 +133,7 @@ def test_maybe_attention_against_oracle(dev, tmp_path, monkeypatch, camera, disa
         cur_positions=None, mosaic_frames=mosaic_frames, cache=cache,
         cache_freqs=torch.from_numpy(cache_freqs)[:, None], cache_frames=cache["frames"],
         cache_read_chunk_id=0, cur_cache_chunk_ids=[-1, 0], write_cache=False,
-        hole_keep=hole_keep.to(dev), a1_pass=None)
+        hole_keep=hole_keep.to(dev), a1_pass=None, all_k_pre=k_pre.to(dev))
     assert out is not None and out.shape == (1, M + S, H * D)
     assert bool((out[:, :M] == 0).all())
     # ---- oracle, in the reference's order
@@ -147,13 +163,31 @@ def test_maybe_attention_against_oracle(dev, tmp_path, monkeypatch, camera, disa
         vc = orc.camera_apply(vc, P_inv[0].numpy()[rows_c], "full")
         kw = dict(key_cam=P_inv[0].numpy()[rows_k], q_cam=P_T[0].numpy()[rows_q],
                   out_cam=P[0].numpy()[rows_q])
+    # low_native: the moved tokens leave the native partition's visibility
+    moved = np.zeros(M + S, bool)
+    if low_native in ("all", "mosaic"):
+        moved[:M] = True
+    if low_native in ("all", "current"):
+        moved[M:] = True
+    if moved.any():
+        lf = freqs_cur[moved].copy()
+        if disable_t:
+            lf[:, :22] = 1
+        lm = keep[:, moved]
+        kw["native_low"] = {
+            "k_pre_bf16": u16(k_pre[0].view(M + S, H, D))[moved],
+            "v_pre_bf16": u16(v_raw[0].view(M + S, H, D))[moved],
+            "freqs": lf,
+            "cam": P_inv[0].numpy()[rows_c][moved] if camera else None,
+            "mask": None if lm.all() else lm}
+        keep = keep & ~moved[None, :]
     ref, _ = orc.fast_attend(qn, kc, vc, oracle_codec(key, 0, sname), oracle_codec(value, 0, sname),
                              prot, low, oracle_groups(payload), D ** -0.5, D=D, key_freqs=kf,
                              q_pre_bf16=u16(q_pre[0, M:].view(S, H, D)), q_freqs=qf,
                              cur_mask=keep, **kw)
     got = out[0, M:].view(S, H, D).float().cpu().numpy()
     diff, cos = max_abs_cos(got, ref)
-    assert diff <= MAX_ABS and cos >= MIN_COS, (camera, disable_t, diff, cos)
+    assert diff <= MAX_ABS and cos >= MIN_COS, (camera, disable_t, low_native, diff, cos)
 
 
 def test_maybe_attention_returns_none_and_commits(dev, tmp_path, monkeypatch):
