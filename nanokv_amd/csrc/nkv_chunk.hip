@@ -124,8 +124,8 @@ struct ChunkParams {
 // attention partitions (the native partition and the reader groups of a
 // NanoKV-Fast call, or one nkv_attend call), each with its own ChunkParams
 // and K/Q width.  Blocks [seg_first[s], seg_first[s + 1]) run segment s: work
-// seg_kind[s] of partition seg_part[s] (seg_ranges[s]: tile ranges per head
-// of a decode segment).
+// seg_kind[s] of partition seg_part[s] (seg_ranges[s]: the block count of a
+// decode segment, one range of its history tiles per block).
 constexpr int MP_SEGS = 4 * NKV_MAX_PARTS;
 enum : int { SEG_K = 0, SEG_V = 1, SEG_CUR = 2, SEG_FLASH = 3, SEG_XFORM = 4, SEG_TABLE = 5 };
 struct MultiParams {
@@ -908,64 +908,16 @@ __global__ void __launch_bounds__(C8_THREADS, 1) stage8_kernel(ChunkParams p) {
 }
 
 // ------------------------------------------------------------ current tiles
-// A current-key tile (the uncompressed keys of the chunk being attended),
-// built by CT_THREADS threads: thread t brings keys 4 (t % 32) .. +4,
-// columns 16 (t / 32) .. +16 of K and V (every load before any store); K
-// rows go straight into the image, V through LDS into V^T column order (one
-// 8-byte write of four keys per column).  Keys past the end are zero.  A
-// thread group with live == false (no such tile) only joins the barrier.
-constexpr int CT_THREADS = 256;
-struct CTileSmem {
-    uint16_t vt[FT_IMG];  // [128 d][128] in V^T column order
-};
-
-__device__ __forceinline__ void ctile_tile(const ChunkParams& p, int bh, int ct, bool live,
-                                           CTileSmem& sm, int t) {
-    const int b = bh / p.H, h = bh % p.H;
-    const int64_t key0 = (int64_t)ct * FT_T;
-    const int valid = live ? (int)min((int64_t)FT_T, p.Nc - key0) : 0;
-    uint16_t* img = p.tiles + ((int64_t)bh * p.ntiles + p.ntiles_hist + ct) * FT_TILE;
-    const int k0 = 4 * (t & 31), d0 = 16 * (t >> 5);
-    u32x4 kv[4][2], vv[4][2];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-        const bool ok = k0 + e < valid;
-        const int64_t tok = key0 + (ok ? k0 + e : 0);
-        const uint16_t* ks = p.k_cur + (int64_t)b * p.k_sb + tok * p.k_st + (int64_t)h * p.k_sh + d0;
-        const uint16_t* vs = p.v_cur + (int64_t)b * p.v_sb + tok * p.v_st + (int64_t)h * p.v_sh + d0;
-#pragma unroll
-        for (int x = 0; x < 2; ++x) {
-            kv[e][x] = ok ? *reinterpret_cast<const u32x4*>(ks + 8 * x) : u32x4{0, 0, 0, 0};
-            vv[e][x] = ok ? *reinterpret_cast<const u32x4*>(vs + 8 * x) : u32x4{0, 0, 0, 0};
-        }
-    }
-    if (live) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e)
-#pragma unroll
-            for (int x = 0; x < 2; ++x)
-                *reinterpret_cast<u32x4*>(img + (k0 + e) * FT_ROW + d0 + 8 * x) = kv[e][x];
-    }
-    const int col = vt_col(k0);
-#pragma unroll
-    for (int dd = 0; dd < 16; ++dd) {
-        const int x = dd >> 3, w = (dd & 7) >> 1, sh = 16 * (dd & 1);
-        auto val = [&](int e) { return (vv[e][x][w] >> sh) & 0xffffu; };
-        *reinterpret_cast<u32x2*>(sm.vt + (d0 + dd) * FT_ROW + col) =
-            u32x2{val(0) | (val(1) << 16), val(2) | (val(3) << 16)};
-    }
-    __syncthreads();
-    if (live)
-        for (int i = t; i < CK_D * (FT_ROW / 8); i += CT_THREADS)
-            *reinterpret_cast<u32x4*>(img + FT_IMG + 8 * i) = *reinterpret_cast<const u32x4*>(sm.vt + 8 * i);
-}
+// Current-key tiles (the uncompressed keys of the chunk being attended) are
+// built by the current-key blocks of drtile_kernel (ctile_batch).
 
 // ------------------------------------------------ decode GEMM, resident decoder
 // For codec ranks up to DR_MAXQ * 64 the history tiles come from drtile_kernel:
-// one block of eight waves per (b*h, codec, range of tiles) loads the head's
-// decoder rows into LDS once and keeps them for the whole range, so each
-// decoder element is read from L2 once per block rather than once per 256-key
-// chunk.  The block decodes two tiles at a time: wave w takes keys
+// a block of eight waves decoding a piece of one head's tiles (a range of
+// tiles, see drtile_pieces) loads the head's decoder rows into LDS once and
+// keeps them for the whole piece, so each decoder element is read from L2
+// once per piece rather than once per 256-key chunk.  The block decodes two
+// tiles at a time: wave w takes keys
 // 32 (w % 4) .. +32 of tile 2 i + w / 4 at all 128 columns, so each unpacked
 // INT4 code feeds four MFMAs, and stores its part of the image from
 // registers (each 128-byte line of a K row is written by one wave, each line
@@ -1239,12 +1191,105 @@ __device__ __forceinline__ void camera_table_entry(const CameraDev& c, int batch
     const_cast<double*>(c.m64)[i] = (double)bf16_round(ldg(c.mats + b * c.mats_bs + r));
 }
 
-// Blocks of a decode segment: b*h fastest -- with B*H a multiple of 8 every
-// range of one head's codec runs on one XCD (blockIdx % 8) and shares its
-// decoder rows in L2 -- then its seg_ranges tile ranges.  A current-key
-// segment: b*h fastest, then pairs of current tiles, one per 256 threads.
-// KQ: decoder slices of the launch's decode segments.
-static_assert(2 * sizeof(CTileSmem) <= sizeof(DResSmem), "current tiles share the decode LDS");
+// Range j of nb equal ranges of the partition's B*H*T history tiles
+// (head-major), one head piece of at most DR_MAXT tiles at a time.
+template <int CODEC, int KQ, int DK>
+__device__ __forceinline__ void drtile_pieces(DResSmem& sm, const ChunkParams& p, int64_t j, int nb,
+                                              int wave, int lane) {
+    const int T = (int)cdiv(p.n_rows, FT_T);
+    const int64_t M = (int64_t)p.B * p.H * T, start = j * M / nb, end = (j + 1) * M / nb;
+    for (int64_t pos = start; pos < end;) {
+        const int hb = (int)(pos / T), ta = (int)(pos - (int64_t)hb * T);
+        const int tb = (int)min((int64_t)min(T, ta + DR_MAXT), ta + (end - pos));
+        if (pos > start) __syncthreads();  // the previous piece's LDS reads are done
+        drtile_range<CODEC, KQ, DK>(sm, p, hb, ta, tb, wave, lane);
+        pos += tb - ta;
+    }
+}
+
+// Current tiles x0, x0 + stride, .. (up to CJ_BATCH of them below `jobs`;
+// tile x is current tile x % nct of head x / nct) by the DR_THREADS threads
+// of a current-key block, every K and V load of the batch issued before the
+// first store, each load instruction reading four whole 256-byte rows: K
+// rows straight into the image (16-byte piece t + DR_THREADS e of a tile is
+// column block piece % 16 of key piece / 16), V through LDS into V^T column
+// order (thread t: columns 8 (t % 16) .. +8 of keys 4 (t / 16) .. +4, one
+// 8-byte write of four keys per column).  The LDS V^T rows hold their
+// 16-byte chunk c at chunk c ^ ((row / 8) % 16), so that the 16 rows one
+// such write instruction touches per key group fall in distinct banks.
+// Keys past the end are zero.
+constexpr int CJ_PIECES = FT_T * CK_D / 8 / DR_THREADS;  // 16-byte pieces per thread and tile
+constexpr int CJ_BATCH = 4;
+static_assert(CJ_PIECES == 4 && DR_THREADS == 512, "current tile batches");
+static_assert(CJ_BATCH * FT_IMG * sizeof(uint16_t) <= sizeof(DResSmem), "V^T images in the decode LDS");
+
+__device__ __forceinline__ void ctile_batch(const ChunkParams& p, int x0, int stride, int jobs,
+                                            int nct, uint16_t* vt, int t) {
+    const int k0 = 4 * (t >> 4), d0 = 8 * (t & 15);
+    u32x4 kv[CJ_BATCH][CJ_PIECES], vv[CJ_BATCH][4];
+    int64_t img0[CJ_BATCH];  // element offset of each tile's image (32-bit division only)
+#pragma unroll
+    for (int m = 0; m < CJ_BATCH; ++m) {
+        const int x = x0 + m * stride, bh = x / nct, ct = x - bh * nct;
+        const int b = bh / p.H, h = bh - b * p.H;
+        img0[m] = ((int64_t)bh * p.ntiles + p.ntiles_hist + ct) * FT_TILE;
+        const int64_t key0 = (int64_t)ct * FT_T;
+        const int valid = x < jobs ? (int)min((int64_t)FT_T, p.Nc - key0) : 0;
+        const uint16_t* ks = p.k_cur + (int64_t)b * p.k_sb + (int64_t)h * p.k_sh;
+        const uint16_t* vs = p.v_cur + (int64_t)b * p.v_sb + (int64_t)h * p.v_sh + d0;
+#pragma unroll
+        for (int e = 0; e < CJ_PIECES; ++e) {
+            const int i = t + DR_THREADS * e, key = i >> 4, c = i & 15;
+            kv[m][e] = key < valid ? ldg(reinterpret_cast<const u32x4*>(ks + (key0 + key) * p.k_st + 8 * c))
+                                   : u32x4{0, 0, 0, 0};
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            vv[m][e] = k0 + e < valid ? ldg(reinterpret_cast<const u32x4*>(vs + (key0 + k0 + e) * p.v_st))
+                                      : u32x4{0, 0, 0, 0};
+    }
+    // V^T column of key k0 (its four keys are adjacent there), then its
+    // 16-byte chunk swizzled per row group
+    const int col = vt_col(k0), vch = col >> 3, vin = col & 7;
+#pragma unroll
+    for (int m = 0; m < CJ_BATCH; ++m) {
+        if (x0 + m * stride < jobs) {
+            uint16_t* img = p.tiles + img0[m];
+#pragma unroll
+            for (int e = 0; e < CJ_PIECES; ++e) {
+                const int i = t + DR_THREADS * e;
+                *reinterpret_cast<u32x4*>(img + (i >> 4) * FT_ROW + 8 * (i & 15)) = kv[m][e];
+            }
+        }
+#pragma unroll
+        for (int dd = 0; dd < 8; ++dd) {
+            const int w = dd >> 1, sh = 16 * (dd & 1);
+            auto val = [&](int e) { return (vv[m][e][w] >> sh) & 0xffffu; };
+            const int row = d0 + dd;
+            *reinterpret_cast<u32x2*>(vt + m * FT_IMG + row * FT_ROW + 8 * (vch ^ ((row >> 3) & 15)) + vin) =
+                u32x2{val(0) | (val(1) << 16), val(2) | (val(3) << 16)};
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int m = 0; m < CJ_BATCH; ++m) {
+        if (x0 + m * stride >= jobs) break;
+        uint16_t* img = p.tiles + img0[m] + FT_IMG;
+#pragma unroll
+        for (int e = 0; e < CJ_PIECES; ++e) {
+            const int i = t + DR_THREADS * e, row = i >> 4, c = i & 15;
+            *reinterpret_cast<u32x4*>(img + 8 * i) = *reinterpret_cast<const u32x4*>(
+                vt + m * FT_IMG + row * FT_ROW + 8 * (c ^ ((row >> 3) & 15)));
+        }
+    }
+    __syncthreads();  // the LDS images are read before the next batch rewrites them
+}
+
+// Blocks of a decode segment: seg_ranges equal ranges of the segment's
+// history tiles (see the kernel body).  Blocks of a current-key segment:
+// seg_ranges blocks, block c building the partition's current tiles c,
+// c + seg_ranges, .. in batches.  KQ: decoder slices of the launch's decode
+// segments.
 template <int KQ>
 __global__ void __launch_bounds__(DR_THREADS, 1) drtile_kernel(MultiParams P) {
     extern __shared__ __align__(16) unsigned char smem_raw[];
@@ -1255,30 +1300,32 @@ __global__ void __launch_bounds__(DR_THREADS, 1) drtile_kernel(MultiParams P) {
     const ChunkParams& p = P.part[pi];
     const int64_t local = (int64_t)blockIdx.x - P.seg_first[sg];
     const int BH = p.B * p.H;
-    const int bh = (int)(local % BH), rg = (int)(local / BH);
     if (kind == SEG_TABLE) {
         camera_table_entry(p.cam, camera_batches(p.cam, p.B), local * DR_THREADS + threadIdx.x);
         return;
     }
     if (kind == SEG_CUR) {
-        CTileSmem* ct = reinterpret_cast<CTileSmem*>(smem_raw);
-        const int half = threadIdx.x / CT_THREADS, c = 2 * rg + half;
-        ctile_tile(p, bh, c, c < p.ntiles - p.ntiles_hist, ct[half], threadIdx.x % CT_THREADS);
+        // (B*H*nct < 2^31: checked on the host)
+        const int ncur = P.seg_ranges[sg], nct = p.ntiles - p.ntiles_hist, jobs = BH * nct;
+        for (int x0 = (int)local; x0 < jobs; x0 += CJ_BATCH * ncur)
+            ctile_batch(p, x0, ncur, jobs, nct, reinterpret_cast<uint16_t*>(smem_raw), threadIdx.x);
         return;
     }
+    // a decode segment of nb blocks (a multiple of 8): range j of the
+    // segment's B*H*T history tiles, head-major -- ranges j .. of one XCD
+    // adjacent, so that they share decoder rows in its L2 -- one head piece
+    // at a time
     DResSmem& sm = *reinterpret_cast<DResSmem*>(smem_raw);
-    const int ranges = P.seg_ranges[sg];
-    const int T = (int)cdiv(p.n_rows, FT_T);
-    const int ta = (int)((int64_t)rg * T / ranges), tb = (int)((int64_t)(rg + 1) * T / ranges);
-    if (ta >= tb) return;
+    const int nb = P.seg_ranges[sg];
+    const int64_t j = nb % 8 == 0 ? (local & 7) * (nb >> 3) + (local >> 3) : local;
     if (kind == SEG_K) {
-        if (dk == 32) drtile_range<0, KQ, 32>(sm, p, bh, ta, tb, wave, lane);
-        else if (dk == 64) drtile_range<0, KQ, 64>(sm, p, bh, ta, tb, wave, lane);
-        else drtile_range<0, KQ, 128>(sm, p, bh, ta, tb, wave, lane);
+        if (dk == 32) drtile_pieces<0, KQ, 32>(sm, p, j, nb, wave, lane);
+        else if (dk == 64) drtile_pieces<0, KQ, 64>(sm, p, j, nb, wave, lane);
+        else drtile_pieces<0, KQ, 128>(sm, p, j, nb, wave, lane);
     } else {
-        if (dk == 32) drtile_range<1, KQ, 32>(sm, p, bh, ta, tb, wave, lane);
-        else if (dk == 64) drtile_range<1, KQ, 64>(sm, p, bh, ta, tb, wave, lane);
-        else drtile_range<1, KQ, 128>(sm, p, bh, ta, tb, wave, lane);
+        if (dk == 32) drtile_pieces<1, KQ, 32>(sm, p, j, nb, wave, lane);
+        else if (dk == 64) drtile_pieces<1, KQ, 64>(sm, p, j, nb, wave, lane);
+        else drtile_pieces<1, KQ, 128>(sm, p, j, nb, wave, lane);
     }
 }
 
@@ -2135,8 +2182,18 @@ bool use_staged(const ChunkLaunchDesc& d) {
 // plus a fixed cost per block (the decode's: the decoder rows and the
 // range's center rows, ~8 us).
 double flash_tile_cost(int dk) { return dk == 32 ? 0.7 : dk == 64 ? 0.82 : 1.0; }
-double decode_tile_cost(int w) { return w == 32 ? 0.5 : w == 64 ? 0.7 : 1.0; }
-constexpr double FLASH_BLOCK_COST = 1.0, DECODE_BLOCK_COST = 1.6, CTILE_BLOCK_COST = 0.5;
+// Modelled costs in units of one 128-wide K tile's decode (about 4.4 us of
+// a decode block at cfg1): a V tile (the centers' loads and adds in the
+// accumulator layout) 1.1; a decode block's start (the decoder rows of all
+// blocks load at once) DECODE_BLOCK_COST, and each further head piece of it
+// (its decoder rows, bias and center references again) DECODE_PIECE_COST;
+// one batch of CJ_BATCH current tiles of a current-key block
+// CTILE_BATCH_COST (about 12 us).
+double decode_tile_cost(int w, int cc) {
+    return cc ? 1.1 : w == 32 ? 0.5 : w == 64 ? 0.7 : 1.0;
+}
+constexpr double FLASH_BLOCK_COST = 1.0, DECODE_BLOCK_COST = 2.0, DECODE_PIECE_COST = 0.75,
+                 CTILE_BATCH_COST = 2.7;
 constexpr double FLASH_TILE_US = 4.4;
 // each split's partials are written by the flash kernel and read back by the
 // combine at about 4 TB/s
@@ -2175,7 +2232,8 @@ double lpt_makespan(std::vector<std::pair<double, int64_t>> groups) {
 struct MultiPlan {
     int n;
     FlashPlan f[NKV_MAX_PARTS];
-    int ranges[NKV_MAX_PARTS][2];  // decode tile ranges per head of K and V (0: none)
+    int dblocks[NKV_MAX_PARTS][2];  // decode blocks of K and V (0: no history)
+    int cblocks[NKV_MAX_PARTS];     // current-key blocks (0: no current keys)
     size_t tiles_off[NKV_MAX_PARTS], part_off[NKV_MAX_PARTS];
     // each camera partition's fp64 matrix table (after every tile and
     // partial area, which end at areas_end)
@@ -2233,56 +2291,91 @@ void plan_flash(const ChunkLaunchDesc* d, int n, MultiPlan& P) {
     for (int i = 0; i < n; ++i) P.f[i].splits = best_sp[i];
 }
 
-// Decode ranges: candidate block costs from 1 .. 32 ranges above the least
-// each (partition, codec) needs (DR_MAXT tiles per range), the current-key
-// blocks placed after the decode blocks.  cfg1 (98 tiles of each codec, 24
-// heads): 5 ranges per head and codec, 240 blocks in one round.
+// Decode blocks: each (partition, codec) segment's B*H*T history tiles in nb
+// equal ranges (nb a multiple of 8, no range above DR_MAXT tiles); a block
+// pays a head piece per head its range touches, B*H / nb more than one on
+// average.
+// Current-key blocks: a pool of them builds every partition's current tiles
+// in batches (each partition's share in proportion to its tiles), sized to
+// the CUs the decode blocks leave free or to one batch per block.  Candidate
+// per-block decode costs come from every segment's choices of nb (up to two
+// rounds of the CUs); the plan with the least modelled makespan (fewest
+// blocks on ties) wins.  cfg1 (24 heads, 98 history and 13 current tiles per
+// head): 112 K and 128 V blocks, 16 current-key blocks of 5 batches.
 void plan_decode(const ChunkLaunchDesc* d, int n, MultiPlan& P) {
     struct Seg {
         int i, cc;
-        int64_t T, bh;
+        int64_t bh, nmin, nmax;
         double w;
     };
+    auto round8 = [](int64_t x) { return 8 * cdiv(x, 8); };
     std::vector<Seg> segs;
-    std::vector<std::pair<double, int64_t>> cur;
+    int64_t jobs[NKV_MAX_PARTS] = {}, all_jobs = 0;
     for (int i = 0; i < n; ++i) {
-        P.ranges[i][0] = P.ranges[i][1] = 0;
+        P.dblocks[i][0] = P.dblocks[i][1] = 0;
+        P.cblocks[i] = 0;
         const int64_t bh = (int64_t)d[i].B * d[i].H;
+        jobs[i] = bh * (P.f[i].ntiles - P.f[i].ntiles_hist);
+        all_jobs += jobs[i];
         if (d[i].n_rows > 0) {
-            const int64_t T = cdiv(d[i].n_rows, FT_T);
+            const int64_t M = bh * cdiv(d[i].n_rows, FT_T);
+            const int64_t nmin = round8(cdiv(M, DR_MAXT));
+            const int64_t nmax = std::max(nmin, round8(std::min(M, (int64_t)2 * FT_CUS)));
             for (int cc = 0; cc < 2; ++cc)
-                segs.push_back({i, cc, T, bh, T * decode_tile_cost(cc ? CK_D : d[i].dk)});
+                segs.push_back({i, cc, bh, nmin, nmax, M * decode_tile_cost(d[i].dk, cc)});
         }
-        const int64_t nct = P.f[i].ntiles - P.f[i].ntiles_hist;
-        if (nct > 0) cur.push_back({CTILE_BLOCK_COST, bh * cdiv(nct, 2)});
     }
-    if (segs.empty()) return;
+    // the current-key pool of `pool` blocks over the partitions
+    auto share = [&](int64_t pool, int64_t (&c)[NKV_MAX_PARTS]) {
+        for (int i = 0; i < n; ++i)
+            c[i] = jobs[i] ? std::min(jobs[i], std::max((int64_t)1, pool * jobs[i] / all_jobs)) : 0;
+    };
+    auto add_cur = [&](std::vector<std::pair<double, int64_t>>& groups, const int64_t (&c)[NKV_MAX_PARTS]) {
+        int64_t blocks = 0;
+        for (int i = 0; i < n; ++i)
+            if (c[i]) {
+                groups.push_back({(double)cdiv(cdiv(jobs[i], c[i]), CJ_BATCH) * CTILE_BATCH_COST, c[i]});
+                blocks += c[i];
+            }
+        return blocks;
+    };
+    auto block_cost = [](const Seg& g, int64_t nb) {
+        return g.w / nb + DECODE_BLOCK_COST + DECODE_PIECE_COST * (double)g.bh / nb;
+    };
     std::vector<double> cand;
-    for (const Seg& g : segs) {
-        const int64_t rmin = cdiv(g.T, DR_MAXT);
-        for (int64_t r = rmin; r <= std::min(g.T, rmin + 31); ++r) cand.push_back(g.w / r);
-    }
+    for (const Seg& g : segs)
+        for (int64_t nb = g.nmin; nb <= g.nmax; nb += 8) cand.push_back(g.w / nb);
+    if (cand.empty()) cand.push_back(1.0);  // current keys only
     double best = 1e300;
     int64_t best_blocks = 0;
-    std::vector<int64_t> best_r(segs.size());
-    std::vector<int64_t> r(segs.size());
+    std::vector<int64_t> best_nb(segs.size()), nb(segs.size());
+    int64_t best_c[NKV_MAX_PARTS] = {};
     for (const double c : cand) {
-        std::vector<std::pair<double, int64_t>> groups = cur;
-        int64_t blocks = 0;
+        std::vector<std::pair<double, int64_t>> dec;
+        int64_t dblocks = 0;
         for (size_t k = 0; k < segs.size(); ++k) {
             const Seg& g = segs[k];
-            r[k] = std::min(g.T, std::max(cdiv(g.T, DR_MAXT), (int64_t)std::ceil(g.w / c - 1e-9)));
-            groups.push_back({g.w / r[k] + DECODE_BLOCK_COST, g.bh * r[k]});
-            blocks += g.bh * r[k];
+            nb[k] = std::min(g.nmax, std::max(g.nmin, round8((int64_t)std::ceil(g.w / c - 1e-9))));
+            dec.push_back({block_cost(g, nb[k]), nb[k]});
+            dblocks += nb[k];
         }
-        const double t = lpt_makespan(groups);
-        if (t < best - 1e-6 || (t < best + 1e-6 && blocks < best_blocks)) {
-            best = t;
-            best_blocks = blocks;
-            best_r = r;
+        const int64_t pools[2] = {std::max((int64_t)8, FT_CUS - dblocks), cdiv(all_jobs, CJ_BATCH)};
+        for (int q = 0; q < (all_jobs ? 2 : 1); ++q) {
+            int64_t cb[NKV_MAX_PARTS];
+            share(pools[q], cb);
+            std::vector<std::pair<double, int64_t>> groups = dec;
+            const int64_t blocks = dblocks + add_cur(groups, cb);
+            const double t = lpt_makespan(groups);
+            if (t < best - 1e-6 || (t < best + 1e-6 && blocks < best_blocks)) {
+                best = t;
+                best_blocks = blocks;
+                best_nb = nb;
+                for (int i = 0; i < n; ++i) best_c[i] = cb[i];
+            }
         }
     }
-    for (size_t k = 0; k < segs.size(); ++k) P.ranges[segs[k].i][segs[k].cc] = (int)best_r[k];
+    for (size_t k = 0; k < segs.size(); ++k) P.dblocks[segs[k].i][segs[k].cc] = (int)best_nb[k];
+    for (int i = 0; i < n; ++i) P.cblocks[i] = (int)best_c[i];
 }
 
 // The byte extents the staged kernels write in a plan's workspace, checked
@@ -2479,15 +2572,16 @@ int staged_run(hipStream_t s, const ChunkLaunchDesc* d, const ChunkParams* ps, i
                 const int64_t bh = (int64_t)d[i].B * d[i].H;
                 const int64_t T = cdiv(d[i].n_rows, FT_T);
                 for (int cc = 0; cc < 2; ++cc) {
-                    const int r = P.ranges[i][cc];
-                    if (r == 0 || (qk != qv && cc != pass)) continue;
-                    const double w = decode_tile_cost(cc ? CK_D : d[i].dk);
-                    segs.push_back({(double)T / r * w + DECODE_BLOCK_COST, i, cc ? SEG_V : SEG_K, r,
-                                    bh * r});
+                    const int nb = P.dblocks[i][cc];
+                    if (nb == 0 || (qk != qv && cc != pass)) continue;
+                    // ordered by block cost, before the current-key and
+                    // table segments (cost 0), so each starts at a
+                    // multiple of 8
+                    segs.push_back({(double)bh * T / nb * decode_tile_cost(d[i].dk, cc) + DECODE_BLOCK_COST,
+                                    i, cc ? SEG_V : SEG_K, nb, nb});
                 }
-                const int64_t nct = P.f[i].ntiles - P.f[i].ntiles_hist;
-                if (pass == 0 && nct > 0)
-                    segs.push_back({CTILE_BLOCK_COST, i, SEG_CUR, 0, bh * cdiv(nct, 2)});
+                if (pass == 0 && P.cblocks[i] > 0)
+                    segs.push_back({0.0, i, SEG_CUR, P.cblocks[i], P.cblocks[i]});
                 if (pass == 0 && table[i]) {
                     const CameraDev& c = M.part[i].cam;
                     const int64_t elems = (int64_t)camera_batches(c, d[i].B) * c.n_mats * 64;
@@ -2611,6 +2705,9 @@ int check_desc(const ChunkLaunchDesc& d) {
                 "bad launch shape");
     NKV_REQUIRE(d.Nc == 0 || (d.dk == CK_D && d.k_cur && d.v_cur), NKV_ERR_INVALID,
                 "current keys need k_cur/v_cur and a 128-wide launch");
+    // the current-key blocks index B*H*(current tiles) in 32 bits
+    NKV_REQUIRE((int64_t)d.B * d.H * 2 * chunk_count(d.Nc) < ((int64_t)1 << 29), NKV_ERR_UNSUPPORTED,
+                "B*H*ceil(Nc/256) must stay below 2^28");
     NKV_REQUIRE(!d.cur_mask || (d.n_groups >= 1 && d.mask_words >= cdiv(d.Nc, 32)),
                 NKV_ERR_INVALID, "the current-key mask needs n_groups >= 1 and "
                 "cur_mask_words >= ceil(Nc / 32)");

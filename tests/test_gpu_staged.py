@@ -72,9 +72,18 @@ def test_staged_ranks_at_resident_limit(dev):
 
 def test_staged_multi_tile_ranges(dev):
     """Blocks of the resident-decoder kernel that decode several pairs of
-    tiles, with odd tile counts per block (63 tiles over 8 ranges per head
-    and codec), and a ragged last tile."""
+    tiles: 16 heads of 63 tiles in equal ranges per codec, so that ranges of
+    odd tile counts cross head boundaries, and a ragged last tile."""
     _check(Scenario(H=16, N=8000, Q=1024, Nc=40, rK=384, rV=384, G=32, C=16, seed=16), dev)
+
+
+def test_staged_ranges_across_heads_and_current_batches(dev):
+    """Two batch items of 3 heads with 37 history tiles each (ranges of one
+    or two tiles, some across a head boundary) and 6 current tiles per head,
+    built by the current-key blocks in batches of 4 with a partial last
+    batch."""
+    _check(Scenario(B=2, H=3, N=37 * 128 - 5, Q=1030, Nc=700, rK=384, rV=384, G=32, C=16,
+                    seed=17), dev)
 
 
 @pytest.mark.parametrize("rows", ["scattered", "empty"])
