@@ -2346,26 +2346,30 @@ void plan_decode(const ChunkLaunchDesc* d, int n, MultiPlan& P) {
     for (const Seg& g : segs)
         for (int64_t nb = g.nmin; nb <= g.nmax; nb += 8) cand.push_back(g.w / nb);
     if (cand.empty()) cand.push_back(1.0);  // current keys only
+    // K and V decode in separate launches when their ranks differ (the
+    // current keys with K): the makespans add
+    const bool split = (d[0].key.r >> 6) != (d[0].value.r >> 6);
     double best = 1e300;
     int64_t best_blocks = 0;
     std::vector<int64_t> best_nb(segs.size()), nb(segs.size());
     int64_t best_c[NKV_MAX_PARTS] = {};
     for (const double c : cand) {
-        std::vector<std::pair<double, int64_t>> dec;
-        int64_t dblocks = 0;
+        std::vector<std::pair<double, int64_t>> dec[2];
+        int64_t dblocks = 0, first_launch = 0;
         for (size_t k = 0; k < segs.size(); ++k) {
             const Seg& g = segs[k];
             nb[k] = std::min(g.nmax, std::max(g.nmin, round8((int64_t)std::ceil(g.w / c - 1e-9))));
-            dec.push_back({block_cost(g, nb[k]), nb[k]});
+            dec[split ? g.cc : 0].push_back({block_cost(g, nb[k]), nb[k]});
             dblocks += nb[k];
+            if (!split || g.cc == 0) first_launch += nb[k];
         }
-        const int64_t pools[2] = {std::max((int64_t)8, FT_CUS - dblocks), cdiv(all_jobs, CJ_BATCH)};
+        const int64_t pools[2] = {std::max((int64_t)8, FT_CUS - first_launch), cdiv(all_jobs, CJ_BATCH)};
         for (int q = 0; q < (all_jobs ? 2 : 1); ++q) {
             int64_t cb[NKV_MAX_PARTS];
             share(pools[q], cb);
-            std::vector<std::pair<double, int64_t>> groups = dec;
+            std::vector<std::pair<double, int64_t>> groups = dec[0];
             const int64_t blocks = dblocks + add_cur(groups, cb);
-            const double t = lpt_makespan(groups);
+            const double t = lpt_makespan(groups) + (split ? lpt_makespan(dec[1]) : 0.0);
             if (t < best - 1e-6 || (t < best + 1e-6 && blocks < best_blocks)) {
                 best = t;
                 best_blocks = blocks;
