@@ -1837,6 +1837,45 @@ __device__ __forceinline__ void combine_partials(CombineAcc& A, const uint16_t* 
     // no chunks (no keys at all): nothing to read, and the workspace may be
     // null; the loads must not be issued ahead of this test
     if (NC <= 0) return;
+    // fold slot i's chunk in (live: a chunk of this call, not a reload)
+    auto fold = [&](int i, bool live) {
+        const float mc = __uint_as_float(mlb[i][0]);
+        // a chunk with no valid key for this query has m = -inf and O = 0
+        const bool up = live && mc > A.M;
+        if (__any(up)) {
+            const float f = up ? exp2f(A.M - mc) : 1.0f;  // M = -inf gives 0
+            A.L *= f;
+            A.Lx *= f;
+#pragma unroll
+            for (int e = 0; e < 8 * CB_ROWS; ++e) A.acc[e] *= f;
+        }
+        A.M = up ? mc : A.M;
+        const float wt = !live || mc == -INFINITY ? 0.0f : exp2f(mc - A.M);
+        const float wl = wt * __uint_as_float(mlb[i][1]);
+        A.L += wl;
+        if (track) A.Lx += wl;
+#pragma unroll
+        for (int st = 0; st < CB_ROWS; ++st)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                A.acc[8 * st + 2 * e] += wt * __uint_as_float(buf[i][st][e] << 16);
+                A.acc[8 * st + 2 * e + 1] += wt * __uint_as_float(buf[i][st][e] & 0xffff0000u);
+            }
+    };
+    // up to CB_AHEAD chunks (the staged schedule's key splits): each loaded
+    // once, all in flight before the first is folded in, and no reloads
+    // that the wave would have to wait for before it ends
+    auto fixed = [&](auto n) {
+        constexpr int NF = decltype(n)::value;
+#pragma unroll
+        for (int i = 0; i < NF; ++i) issue(i, i);
+#pragma unroll
+        for (int i = 0; i < NF; ++i) fold(i, true);
+    };
+    if (NC == 1) return fixed(std::integral_constant<int, 1>{});
+    if (NC == 2) return fixed(std::integral_constant<int, 2>{});
+    if (NC == 3) return fixed(std::integral_constant<int, 3>{});
+    if (NC == 4) return fixed(std::integral_constant<int, 4>{});
 #pragma unroll
     for (int i = 0; i < CB_AHEAD; ++i) issue(i, i);
     for (int cc0 = 0; cc0 < NC; cc0 += CB_AHEAD) {
@@ -1845,29 +1884,7 @@ __device__ __forceinline__ void combine_partials(CombineAcc& A, const uint16_t* 
             // Slots past the last chunk hold a reloaded copy of it and get
             // weight 0.  No branch skips them, so the compiler's wait for
             // slot i leaves the other slots' loads in flight.
-            const bool live = cc0 + i < NC;
-            const float mc = __uint_as_float(mlb[i][0]);
-            // a chunk with no valid key for this query has m = -inf and O = 0
-            const bool up = live && mc > A.M;
-            if (__any(up)) {
-                const float f = up ? exp2f(A.M - mc) : 1.0f;  // M = -inf gives 0
-                A.L *= f;
-                A.Lx *= f;
-#pragma unroll
-                for (int e = 0; e < 8 * CB_ROWS; ++e) A.acc[e] *= f;
-            }
-            A.M = up ? mc : A.M;
-            const float wt = !live || mc == -INFINITY ? 0.0f : exp2f(mc - A.M);
-            const float wl = wt * __uint_as_float(mlb[i][1]);
-            A.L += wl;
-            if (track) A.Lx += wl;
-#pragma unroll
-            for (int st = 0; st < CB_ROWS; ++st)
-#pragma unroll
-                for (int e = 0; e < 4; ++e) {
-                    A.acc[8 * st + 2 * e] += wt * __uint_as_float(buf[i][st][e] << 16);
-                    A.acc[8 * st + 2 * e + 1] += wt * __uint_as_float(buf[i][st][e] & 0xffff0000u);
-                }
+            fold(i, cc0 + i < NC);
             issue(cc0 + i + CB_AHEAD, i);
         }
     }
