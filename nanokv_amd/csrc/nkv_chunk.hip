@@ -60,10 +60,10 @@
 
 namespace nkv {
 
-// Partials are written non-temporally: they are read once, by the combine,
-// after the chunk kernel has written all of them (hundreds of MB at long
-// histories), so caching them only evicts the codec tables and decoded tiles
-// that the running blocks re-read.  Plain stores measured 7 % slower over
+// The key-chunk kernel's partials are written non-temporally: they are read
+// once, by the combine, after the chunk kernel has written all of them
+// (hundreds of MB at long histories), so caching them only evicts the codec
+// tables and decoded tiles that the running blocks re-read.  Plain stores measured 7 % slower over
 // the whole call at 1,560 queries x 14,040 keys (0.580 vs 0.540 ms), and
 // head-group launches sized for the partials to stay in the MALL slower
 // still (0.547-0.573 ms; at 50,700 keys 1.55 vs 1.02 ms).
@@ -220,6 +220,10 @@ __device__ __forceinline__ void load_q_block(bf16x8 (&qf)[NF], const ChunkParams
 // 1 KB * (k/4) + 16 B * lane + 4 B * (k%4): every store instruction writes
 // 1 KB contiguous.  Query columns past Q hold finite values that the combine
 // ignores; both half-waves store the same (m, l) of their query.
+// NT: non-temporal stores (the key-chunk kernel's partials, see NT_STORE);
+// the staged flash kernel's few partials (30 MB at cfg1) are stored plainly,
+// which its combine reads about 1 us faster.
+template <bool NT>
 __device__ __forceinline__ void store_partial_piece(const ChunkParams& p, int64_t blk,
                                                     const f32x16 (&o)[4], int st, int lane) {
     uint16_t* dst = p.part_o + blk * 4096 + lane * 8;
@@ -227,23 +231,27 @@ __device__ __forceinline__ void store_partial_piece(const ChunkParams& p, int64_
     u32x4 w;
 #pragma unroll
     for (int e = 0; e < 4; ++e) w[e] = pack_bf16x2(o[db][i0 + 2 * e], o[db][i0 + 2 * e + 1]);
-    NT_STORE(w, reinterpret_cast<u32x4*>(dst + 512 * st));
+    if (NT) NT_STORE(w, reinterpret_cast<u32x4*>(dst + 512 * st));
+    else *reinterpret_cast<u32x4*>(dst + 512 * st) = w;
 }
 
+template <bool NT>
 __device__ __forceinline__ void store_partial_ml(const ChunkParams& p, int64_t bh, int chunk,
                                                  int64_t qcol, float m, float lt) {
     const int64_t idx = (bh * p.nch_total + chunk) * ((int64_t)p.qblocks * 32) + qcol;
-    NT_STORE((u32x2{__float_as_uint(m), __float_as_uint(lt)}),
-             reinterpret_cast<u32x2*>(p.part_ml + 2 * idx));
+    const u32x2 v{__float_as_uint(m), __float_as_uint(lt)};
+    if (NT) NT_STORE(v, reinterpret_cast<u32x2*>(p.part_ml + 2 * idx));
+    else *reinterpret_cast<u32x2*>(p.part_ml + 2 * idx) = v;
 }
 
+template <bool NT = true>
 __device__ __forceinline__ void store_partial(const ChunkParams& p, int64_t bh, int chunk,
                                               int64_t qblk0, const f32x16 (&o)[4], float m,
                                               float lt, int lane) {
     const int64_t blk = ((int64_t)bh * p.nch_total + chunk) * p.qblocks + (qblk0 >> 5);
 #pragma unroll
-    for (int st = 0; st < 8; ++st) store_partial_piece(p, blk, o, st, lane);
-    store_partial_ml(p, bh, chunk, qblk0 + (lane & 31), m, lt);
+    for (int st = 0; st < 8; ++st) store_partial_piece<NT>(p, blk, o, st, lane);
+    store_partial_ml<NT>(p, bh, chunk, qblk0 + (lane & 31), m, lt);
 }
 
 // ======================================================= 8-wave key-chunk kernel
@@ -1772,7 +1780,7 @@ __device__ __forceinline__ void flash_block(const ChunkParams& p, int64_t blk, u
         }
     }
     if (pend) softmax_pv(s);
-    if (active) store_partial(p, bh, split, q0, o, m, halfwave_sum(l), lane);
+    if (active) store_partial<false>(p, bh, split, q0, o, m, halfwave_sum(l), lane);
 }
 
 // The flash segments of a multi-partition launch.  Only a 128-wide
