@@ -2442,6 +2442,23 @@ bool plan_extents_ok(const MultiPlan& P, const ChunkLaunchDesc* d, int n, int v_
         }
         if (f.ntiles > f.ntiles_hist && d[i].dk != CK_D)
             return fail("current tiles at a width other than 128", tiles_end, tiles_end);
+        // the decode launch's blocks: equal ranges of at most DR_MAXT tiles
+        // per codec (a multiple of 8 blocks), and current-key blocks whenever
+        // there are current tiles
+        if (staged_gemm(d[i])) {
+            auto bad = [&](const std::string& what) {
+                if (msg) *msg = "partition " + std::to_string(i) + ": " + what;
+                return false;
+            };
+            for (int cc = 0; cc < 2 && hist > 0; ++cc) {
+                const int nb = P.dblocks[i][cc];
+                if (nb <= 0 || nb % 8 || cdiv((int64_t)bh * hist, nb) > DR_MAXT)
+                    return bad("decode blocks " + std::to_string(nb) + " for " +
+                               std::to_string((int64_t)bh * hist) + " tiles");
+            }
+            if (f.ntiles > f.ntiles_hist && P.cblocks[i] <= 0)
+                return bad("current tiles without current-key blocks");
+        }
         const size_t rows = bh * f.splits * cdiv(d[i].Q, 32) * 32;
         const size_t part_end = P.part_off[i] + rows * PARTIAL_ROW_BYTES;
         const size_t lim = i + 1 < n ? P.tiles_off[i + 1] : P.areas_end;
@@ -2450,13 +2467,14 @@ bool plan_extents_ok(const MultiPlan& P, const ChunkLaunchDesc* d, int n, int v_
     return true;
 }
 
-// The plan depends on the partitions' shapes alone; the last one is kept
-// (a layer loop repeats the same shapes).
+// The plan depends on the partitions' shapes and codec ranks alone; the last
+// one is kept (a layer loop repeats the same shapes).
 MultiPlan multi_plan(const ChunkLaunchDesc* d, int n) {
     std::vector<int64_t> key{n};
     for (int i = 0; i < n; ++i)
         for (int64_t v : {(int64_t)d[i].B, (int64_t)d[i].H, (int64_t)d[i].dk, d[i].Q, d[i].n_rows,
-                          d[i].Nc, (int64_t)staged_gemm(d[i]), cam_table_bytes(d[i])})
+                          d[i].Nc, (int64_t)staged_gemm(d[i]), cam_table_bytes(d[i]),
+                          (int64_t)d[i].key.r, (int64_t)d[i].value.r})
             key.push_back(v);
     thread_local std::vector<int64_t> last_key;
     thread_local MultiPlan last;

@@ -9,6 +9,9 @@ partition's last V^T image and its partials end inside its slice.  The same
 check runs inside every staged call before any launch.  A decode that wrote
 the V^T images of a 32- or 64-wide partition at the 128-wide tile stride
 (a layout mistake that once faulted a GPU run) is caught here, on the CPU.
+The same check holds the decode launch's block plan to what the kernel
+assumes: per codec a multiple of 8 blocks with ranges of at most 24 tiles,
+and current-key blocks whenever a partition has current tiles.
 """
 import ctypes
 
@@ -85,3 +88,18 @@ def test_unstaged_partitions_are_refused():
     rc, err, _ = _check([(1, 4, 32, 64, 512, 0, 448, 128, 1)])
     assert rc == _lib.NKV_ERR_INVALID and "not staged" in err
     assert _check([(1, 4, 32, 64, 512, 0, 384, 128, 1)])[0] == _lib.NKV_OK
+
+
+@pytest.mark.parametrize("B,H,n_rows,Nc,rK,rV", [
+    (1, 24, 12480, 1560, 384, 384),    # cfg1
+    (1, 24, 49920, 780, 384, 256),     # cfg2: K and V in two launches
+    (1, 1, 1, 1, 64, 64),              # one tile of each
+    (3, 5, 128 * 37 - 5, 700, 384, 384),
+    (2, 64, 300, 5000, 128, 128),      # more current than history tiles
+    (1, 8, 2_000_000, 0, 384, 384),    # ranges pinned at 24 tiles
+    (1, 24, 0, 1560, 384, 384),        # current keys only
+    (4, 40, 12480, 1560, 192, 320),
+])
+def test_decode_block_plan(B, H, n_rows, Nc, rK, rV):
+    rc, err, _ = _check([(B, H, 128, 1024, n_rows, Nc, rK, rV, 0)])
+    assert rc == _lib.NKV_OK, err
